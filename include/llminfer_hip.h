@@ -1,0 +1,203 @@
+/*
+ * llminfer HIP backend: C ABI of the attention / linear-attention hot path.
+ *
+ * Drop-in replacement, on AMD Instinct MI355X (gfx950), for the Metal
+ * dispatches the reference's lowering emits for three GraphIR ops:
+ *
+ *   KvAppend    -> cacheAppend x2           lib/Backend/Metal/MetalExecutionPlan.cpp:516-523
+ *   CausalGqa   -> gqaFlashAttention (T>1)  lib/Backend/Metal/MetalExecutionPlan.cpp:528-534
+ *                  gqaScores/gqaSoftmax/gqaValue (T==1)  :536-548
+ *   DeltaUpdate -> graphDeltaUpdate         lib/Backend/Metal/MetalExecutionPlan.cpp:663-676
+ *
+ * The parameter structs are byte-identical to the reference's kernel
+ * parameter structs (all fields 32-bit unsigned), so a lowering that fills
+ * them for Metal fills them for this backend unchanged.
+ *
+ * Conventions (mirroring lib/Backend/Metal/MetalExecutionPlan.h:36-39 and
+ * include/llminfer/Support/Result.h:12-59):
+ *   - Every pointer is a device pointer owned by the caller and borrowed for
+ *     the duration of the call. Work is enqueued on `stream` (a hipStream_t,
+ *     NULL = the default stream) in order; nothing synchronises the host.
+ *   - Return value 0 (LLMI_HIP_OK) means enqueued. A nonzero status before
+ *     any launch (INVALID_ARGUMENT, UNSUPPORTED, WORKSPACE) leaves every
+ *     buffer untouched ("submitted = false"); LLMI_HIP_LAUNCH_FAILED means a
+ *     launch was attempted, so state buffers may be partially written and a
+ *     session must become invalid until reset (MetalExecutor.mm:283-298).
+ *   - llmi_hip_last_error() returns a per-thread message for the last
+ *     nonzero status.
+ *   - Calls that share a workspace must not overlap (same stream is fine).
+ */
+#ifndef LLMINFER_HIP_H
+#define LLMINFER_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#if defined(__GNUC__)
+#define LLMI_HIP_API __attribute__((visibility("default")))
+#else
+#define LLMI_HIP_API
+#endif
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* lib/Backend/Metal/Kernels/ReferenceParams.h:49-51 */
+typedef struct CacheParams {
+  unsigned count, offset;
+} CacheParams;
+
+/* lib/Backend/Metal/Kernels/ReferenceParams.h:53-55 */
+typedef struct GqaParams {
+  unsigned tokens, queryHeads, kvHeads, headDim, past;
+} GqaParams;
+
+/* lib/Backend/Metal/Kernels/GraphParams.h:50-52 */
+typedef struct GraphDeltaParams {
+  unsigned tokens, keyHeads, keyDim, valueHeads, valueDim;
+} GraphDeltaParams;
+
+enum llmi_hip_status {
+  LLMI_HIP_OK = 0,
+  LLMI_HIP_INVALID_ARGUMENT = 1, /* bad shape/pointer; nothing launched */
+  LLMI_HIP_UNSUPPORTED = 2,      /* valid op, no kernel for it; nothing launched */
+  LLMI_HIP_WORKSPACE = 3,        /* workspace missing or too small; nothing launched */
+  LLMI_HIP_LAUNCH_FAILED = 4,    /* a launch failed; buffers may be partially written */
+  LLMI_HIP_NO_DEVICE = 5         /* no usable gfx950 device; nothing launched */
+};
+
+enum llmi_hip_op {
+  LLMI_HIP_OP_KV_APPEND = 0,
+  LLMI_HIP_OP_CAUSAL_GQA = 1,
+  LLMI_HIP_OP_DELTA_UPDATE = 2
+};
+
+/* ---------------------------------------------------------------- KvAppend
+ * cacheAppend (lib/Backend/Metal/Kernels/Reference.metal:295-301):
+ * cache[p.offset + i] = src[i] for i < p.count, fp16 elements. The
+ * reference issues it once for K and once for V with
+ * offset = past * kvHeads * headDim (MetalExecutionPlan.cpp:516-523). */
+LLMI_HIP_API int llmi_hip_cache_append(const uint16_t *src, uint16_t *cache, CacheParams p,
+                          void *stream);
+
+/* Both halves of KvAppend in one launch: k_src -> k_cache and
+ * v_src -> v_cache with the same CacheParams. Same result as two
+ * llmi_hip_cache_append calls. */
+LLMI_HIP_API int llmi_hip_kv_append(const uint16_t *k_src, const uint16_t *v_src,
+                       uint16_t *k_cache, uint16_t *v_cache, CacheParams p,
+                       void *stream);
+
+/* --------------------------------------------------------------- CausalGqa
+ * Replaces gqaFlashAttention (FlashAttention.metal:1-83) for T > 1 and the
+ * 3-pass gqaScores/gqaSoftmax/gqaValue (Reference.metal:303-323,
+ * Graph.metal:172-230) for T == 1. Semantics of the op contract
+ * (lib/GraphIR/Graph.cpp:248-279):
+ *   q        [T][Hq][d] fp16, dense
+ *   k_cache  [cap][Hkv][d] fp16, rows [0, P+T) already appended
+ *   v_cache  same layout
+ *   out      [T][Hq][d] fp16
+ *   O[t,h] = softmax_j(q[t,h] . k[j,h/(Hq/Hkv)] / sqrt(d)) v[j,...], j <= P+t
+ * Softmax and accumulation are fp32; the output is rounded to fp16 once.
+ * `workspace` must hold llmi_hip_gqa_workspace_bytes(p) bytes and be
+ * prepared once with llmi_hip_workspace_init (the kernels leave it ready
+ * for the next call). */
+LLMI_HIP_API int llmi_hip_causal_gqa(const uint16_t *q, const uint16_t *k_cache,
+                        const uint16_t *v_cache, uint16_t *out, GqaParams p,
+                        void *workspace, size_t workspace_bytes, void *stream);
+
+LLMI_HIP_API size_t llmi_hip_gqa_workspace_bytes(GqaParams p);
+
+/* ------------------------------------------------------------- DeltaUpdate
+ * Replaces graphDeltaUpdate (Graph.metal:146-170 with updateDeltaColumn,
+ * Reference.metal:182-197): the gated delta rule over T tokens, per value
+ * head h (key head h / (Hv/Hk)) and state column j:
+ *   S <- decay_t * S ; delta = beta_t (v_tj - k_t . S[:,j])
+ *   S[:,j] += k_t delta ; out_tj = fp16(q_t . S[:,j])
+ * Operand contract (lib/GraphIR/Graph.cpp:226-246):
+ *   q, k   [T][Hk*dk] fp32 (q already L2-normalised and scaled, k normalised)
+ *   v      [T][Hv*dv] fp16
+ *   beta   [T][Hv] fp32      decay [T][Hv] fp32, LINEAR decay in [0, 1]
+ *   state  [Hv][dk][dv] fp32, read and written in place
+ *   out    [T][Hv*dv] fp16
+ * T == 1 runs the recurrent decode step; T > 1 runs the chunk-wise form. */
+LLMI_HIP_API int llmi_hip_delta_update(const float *q, const float *k, const uint16_t *v,
+                          const float *beta, const float *decay, float *state,
+                          uint16_t *out, GraphDeltaParams p, void *workspace,
+                          size_t workspace_bytes, void *stream);
+
+LLMI_HIP_API size_t llmi_hip_delta_workspace_bytes(GraphDeltaParams p);
+
+/* ----------------------------------------------------------------- helpers */
+
+/* Zero a workspace before its first use (enqueued on `stream`). */
+LLMI_HIP_API int llmi_hip_workspace_init(void *workspace, size_t bytes, void *stream);
+
+/* Plan-record support (MetalSession.h:11-16, tools/run/Main.cpp:244-255):
+ * the number of kernel launches an op lowers to and the name of launch
+ * `index`. `params` points to the op's parameter struct. NULL / 0 on a
+ * parameter set the backend rejects. */
+LLMI_HIP_API unsigned llmi_hip_dispatch_count(int op, const void *params);
+LLMI_HIP_API const char *llmi_hip_kernel_name(int op, const void *params, unsigned index);
+
+LLMI_HIP_API const char *llmi_hip_status_string(int status);
+LLMI_HIP_API const char *llmi_hip_last_error(void);
+
+/* Library version and the gfx target its kernels were built for. */
+LLMI_HIP_API const char *llmi_hip_build_info(void);
+
+/* -------------------------------------------------------------- session
+ * A host-side mirror of MetalSession's state ownership and step contract
+ * (include/llminfer/Backend/Metal/MetalSession.h:28-50,
+ * lib/Backend/Metal/MetalExecutor.mm:56-118, 255-298) for one hybrid layer
+ * pair: one GQA layer (its K/V caches) and one DeltaNet layer (its fp32
+ * recurrent state). The session allocates and owns the device state,
+ * validates before launching, advances `past` only on success, becomes
+ * invalid after a failure that happened after a launch, and zeroes state on
+ * reset. Calls on one session must be serialised. */
+typedef struct llmi_hip_session llmi_hip_session;
+
+typedef struct llmi_hip_session_config {
+  unsigned capacity;   /* KV cache rows */
+  unsigned queryHeads, kvHeads, headDim;
+  unsigned keyHeads, keyDim, valueHeads, valueDim;
+} llmi_hip_session_config;
+
+/* A plan record: MetalDispatchInfo{opIndex, kernel} (MetalSession.h:11-16). */
+typedef struct llmi_hip_dispatch {
+  size_t op_index;
+  const char *kernel;
+} llmi_hip_dispatch;
+
+LLMI_HIP_API int llmi_hip_session_open(const llmi_hip_session_config *config,
+                          void *stream, llmi_hip_session **out);
+LLMI_HIP_API void llmi_hip_session_close(llmi_hip_session *s);
+LLMI_HIP_API void llmi_hip_session_reset(llmi_hip_session *s);
+LLMI_HIP_API unsigned llmi_hip_session_past(const llmi_hip_session *s);
+LLMI_HIP_API int llmi_hip_session_invalid(const llmi_hip_session *s);
+
+/* Device pointers of the session-owned state (for inspection and tests). */
+LLMI_HIP_API uint16_t *llmi_hip_session_key_cache(llmi_hip_session *s);
+LLMI_HIP_API uint16_t *llmi_hip_session_value_cache(llmi_hip_session *s);
+LLMI_HIP_API float *llmi_hip_session_recurrent_state(llmi_hip_session *s);
+
+/* One step of T tokens through both layers, in graph order: DeltaUpdate
+ * (op 0), KvAppend (op 1), CausalGqa (op 2) -- the order the builder emits
+ * them for a DeltaNet layer followed by a GQA layer. All operands are
+ * device pointers with the op contracts above; outputs are written to
+ * delta_out [T][Hv*dv] and gqa_out [T][Hq][d]. Validation failures return
+ * nonzero before any launch. If `records` is non-NULL, up to `cap` plan
+ * records are written and *count receives the total. The step waits for
+ * the GPU once at the end (one host sync per step, MetalContext.mm:141-151). */
+LLMI_HIP_API int llmi_hip_session_step(llmi_hip_session *s, unsigned tokens,
+                          const float *dq, const float *dk, const uint16_t *dv,
+                          const float *beta, const float *decay,
+                          uint16_t *delta_out, const uint16_t *q,
+                          const uint16_t *k, const uint16_t *v,
+                          uint16_t *gqa_out, llmi_hip_dispatch *records,
+                          size_t cap, size_t *count);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

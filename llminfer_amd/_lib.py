@@ -1,0 +1,116 @@
+"""ctypes bindings of libllminfer_hip.so (declarations: include/llminfer_hip.h).
+
+The library is loaded from llminfer_amd/lib/ only. There is no fallback: if it
+is missing, importing the backend raises, so no caller can silently run a
+CPU path in its place.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent / "lib" / "libllminfer_hip.so"
+
+OK = 0
+INVALID_ARGUMENT = 1
+UNSUPPORTED = 2
+WORKSPACE = 3
+LAUNCH_FAILED = 4
+NO_DEVICE = 5
+
+OP_KV_APPEND = 0
+OP_CAUSAL_GQA = 1
+OP_DELTA_UPDATE = 2
+
+
+class CacheParams(C.Structure):
+    _fields_ = [("count", C.c_uint), ("offset", C.c_uint)]
+
+
+class GqaParams(C.Structure):
+    _fields_ = [("tokens", C.c_uint), ("queryHeads", C.c_uint),
+                ("kvHeads", C.c_uint), ("headDim", C.c_uint), ("past", C.c_uint)]
+
+
+class GraphDeltaParams(C.Structure):
+    _fields_ = [("tokens", C.c_uint), ("keyHeads", C.c_uint), ("keyDim", C.c_uint),
+                ("valueHeads", C.c_uint), ("valueDim", C.c_uint)]
+
+
+class SessionConfig(C.Structure):
+    _fields_ = [("capacity", C.c_uint), ("queryHeads", C.c_uint),
+                ("kvHeads", C.c_uint), ("headDim", C.c_uint),
+                ("keyHeads", C.c_uint), ("keyDim", C.c_uint),
+                ("valueHeads", C.c_uint), ("valueDim", C.c_uint)]
+
+
+class Dispatch(C.Structure):
+    _fields_ = [("op_index", C.c_size_t), ("kernel", C.c_char_p)]
+
+
+class HipError(RuntimeError):
+    """A nonzero llmi_hip status, with the library's message."""
+
+    def __init__(self, status: int, message: str):
+        super().__init__(f"{message} (status {status})")
+        self.status = status
+
+
+_P = C.c_void_p
+_SZ = C.c_size_t
+
+# name -> (restype, argtypes). Every function declared in include/llminfer_hip.h.
+SIGNATURES = {
+    "llmi_hip_cache_append": (C.c_int, [_P, _P, CacheParams, _P]),
+    "llmi_hip_kv_append": (C.c_int, [_P, _P, _P, _P, CacheParams, _P]),
+    "llmi_hip_causal_gqa": (C.c_int, [_P, _P, _P, _P, GqaParams, _P, _SZ, _P]),
+    "llmi_hip_gqa_workspace_bytes": (_SZ, [GqaParams]),
+    "llmi_hip_delta_update": (C.c_int, [_P, _P, _P, _P, _P, _P, _P,
+                                        GraphDeltaParams, _P, _SZ, _P]),
+    "llmi_hip_delta_workspace_bytes": (_SZ, [GraphDeltaParams]),
+    "llmi_hip_workspace_init": (C.c_int, [_P, _SZ, _P]),
+    "llmi_hip_dispatch_count": (C.c_uint, [C.c_int, _P]),
+    "llmi_hip_kernel_name": (C.c_char_p, [C.c_int, _P, C.c_uint]),
+    "llmi_hip_status_string": (C.c_char_p, [C.c_int]),
+    "llmi_hip_last_error": (C.c_char_p, []),
+    "llmi_hip_build_info": (C.c_char_p, []),
+    "llmi_hip_session_open": (C.c_int, [C.POINTER(SessionConfig), _P, C.POINTER(_P)]),
+    "llmi_hip_session_close": (None, [_P]),
+    "llmi_hip_session_reset": (None, [_P]),
+    "llmi_hip_session_past": (C.c_uint, [_P]),
+    "llmi_hip_session_invalid": (C.c_int, [_P]),
+    "llmi_hip_session_key_cache": (_P, [_P]),
+    "llmi_hip_session_value_cache": (_P, [_P]),
+    "llmi_hip_session_recurrent_state": (_P, [_P]),
+    "llmi_hip_session_step": (C.c_int, [_P, C.c_uint, _P, _P, _P, _P, _P, _P,
+                                        _P, _P, _P, _P, C.POINTER(Dispatch), _SZ,
+                                        C.POINTER(_SZ)]),
+}
+
+_lib = None
+
+
+def load() -> C.CDLL:
+    """Load the backend library (once). Raises if it was not built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not LIB_PATH.exists():
+        raise RuntimeError(
+            f"{LIB_PATH} is missing: build it with `python -m llminfer_amd.build` "
+            "(there is no non-HIP fallback)")
+    lib = C.CDLL(str(LIB_PATH))
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(lib, name, None)
+        if fn is None:
+            continue  # reported by the export test, not at load time
+        fn.restype = res
+        fn.argtypes = args
+    _lib = lib
+    return lib
+
+
+def check(status: int) -> None:
+    if status != OK:
+        lib = load()
+        raise HipError(status, lib.llmi_hip_last_error().decode())

@@ -1,0 +1,296 @@
+// C ABI of the HIP backend: validation, kernel selection, workspace sizing
+// and status reporting. Declarations and contracts: include/llminfer_hip.h.
+#include "llminfer_hip.h"
+#include "capi_internal.hpp"
+#include "kernels.hpp"
+
+#include <hip/hip_runtime.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+namespace llmi {
+
+namespace {
+thread_local char g_error[512] = "";
+} // namespace
+
+int fail(int status, const char *fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_error, sizeof g_error, fmt, ap);
+  va_end(ap);
+  return status;
+}
+
+int launched(hipError_t err, const char *what) {
+  if (err == hipSuccess)
+    return LLMI_HIP_OK;
+  return fail(LLMI_HIP_LAUNCH_FAILED, "%s: %s", what, hipGetErrorString(err));
+}
+
+// Mirrors the reference lowering's 32-bit element-index limit
+// (lib/Backend/Metal/MetalExecutionPlan.cpp:32-40).
+static bool fits32(uint64_t a, uint64_t b, uint64_t c) {
+  uint64_t ab = a * b;
+  if (a && ab / a != b)
+    return false;
+  uint64_t abc = ab * c;
+  if (ab && abc / ab != c)
+    return false;
+  return abc <= 0xffffffffull;
+}
+
+int check_gqa(const GqaParams &p) {
+  if (p.tokens == 0 || p.queryHeads == 0 || p.kvHeads == 0 || p.headDim == 0)
+    return fail(LLMI_HIP_INVALID_ARGUMENT,
+                "CausalGqa: tokens, heads and head_dim must be positive");
+  if (p.queryHeads % p.kvHeads)
+    return fail(LLMI_HIP_INVALID_ARGUMENT,
+                "CausalGqa: query heads %u not a multiple of KV heads %u",
+                p.queryHeads, p.kvHeads);
+  uint64_t rows = (uint64_t)p.past + p.tokens;
+  if (!fits32(p.tokens, p.queryHeads, p.headDim) ||
+      !fits32(rows, p.kvHeads, p.headDim))
+    return fail(LLMI_HIP_INVALID_ARGUMENT,
+                "CausalGqa: tensor exceeds the 32-bit index range");
+  return LLMI_HIP_OK;
+}
+
+int check_delta(const GraphDeltaParams &p) {
+  if (!p.tokens || !p.keyHeads || !p.keyDim || !p.valueHeads || !p.valueDim)
+    return fail(LLMI_HIP_INVALID_ARGUMENT,
+                "DeltaUpdate: every dimension must be positive");
+  if (p.valueHeads % p.keyHeads)
+    return fail(LLMI_HIP_INVALID_ARGUMENT,
+                "DeltaUpdate: value heads %u not a multiple of key heads %u",
+                p.valueHeads, p.keyHeads);
+  if (!fits32(p.tokens, p.keyHeads, p.keyDim) ||
+      !fits32(p.tokens, p.valueHeads, p.valueDim) ||
+      !fits32(p.valueHeads, p.keyDim, p.valueDim))
+    return fail(LLMI_HIP_INVALID_ARGUMENT,
+                "DeltaUpdate: tensor exceeds the 32-bit index range");
+  return LLMI_HIP_OK;
+}
+
+GqaKernel select_gqa(const GqaParams &p) {
+  GqaShape s{p.tokens, p.queryHeads, p.kvHeads, p.headDim, p.past};
+  if (p.tokens == 1 && decode_supported(s))
+    return GqaKernel::Decode;
+  if (p.tokens > 1 && prefill_supported(s))
+    return GqaKernel::Prefill;
+  if (generic_supported(s))
+    return GqaKernel::Generic;
+  return GqaKernel::None;
+}
+
+DeltaKernel select_delta(const GraphDeltaParams &p) {
+  DeltaShape s{p.tokens, p.keyHeads, p.keyDim, p.valueHeads, p.valueDim};
+  if (p.tokens > 1 && delta_chunked_supported(s))
+    return DeltaKernel::Chunked;
+  if (delta_recurrent_supported(s))
+    return DeltaKernel::Recurrent;
+  return DeltaKernel::Generic;
+}
+
+} // namespace llmi
+
+using namespace llmi;
+
+extern "C" {
+
+int llmi_hip_cache_append(const uint16_t *src, uint16_t *cache, CacheParams p,
+                          void *stream) {
+  if (p.count && (!src || !cache))
+    return fail(LLMI_HIP_INVALID_ARGUMENT, "cacheAppend: null buffer");
+  if ((uint64_t)p.offset + p.count > 0xffffffffull)
+    return fail(LLMI_HIP_INVALID_ARGUMENT,
+                "cacheAppend: offset + count exceeds the 32-bit index range");
+  return launched(launch_cache_append(src, cache, p.count, p.offset,
+                                      static_cast<hipStream_t>(stream)),
+                  "cacheAppend");
+}
+
+int llmi_hip_kv_append(const uint16_t *k_src, const uint16_t *v_src,
+                       uint16_t *k_cache, uint16_t *v_cache, CacheParams p,
+                       void *stream) {
+  if (p.count && (!k_src || !v_src || !k_cache || !v_cache))
+    return fail(LLMI_HIP_INVALID_ARGUMENT, "KvAppend: null buffer");
+  if ((uint64_t)p.offset + p.count > 0xffffffffull)
+    return fail(LLMI_HIP_INVALID_ARGUMENT,
+                "KvAppend: offset + count exceeds the 32-bit index range");
+  return launched(launch_kv_append(k_src, v_src, k_cache, v_cache, p.count,
+                                   p.offset, static_cast<hipStream_t>(stream)),
+                  "kvAppend");
+}
+
+size_t llmi_hip_gqa_workspace_bytes(GqaParams p) {
+  if (check_gqa(p) != LLMI_HIP_OK)
+    return 0;
+  if (select_gqa(p) == GqaKernel::Decode)
+    return decode_workspace_bytes(
+        {p.tokens, p.queryHeads, p.kvHeads, p.headDim, p.past});
+  return 0;
+}
+
+int llmi_hip_causal_gqa(const uint16_t *q, const uint16_t *k_cache,
+                        const uint16_t *v_cache, uint16_t *out, GqaParams p,
+                        void *workspace, size_t workspace_bytes, void *stream) {
+  if (int st = check_gqa(p))
+    return st;
+  if (!q || !k_cache || !v_cache || !out)
+    return fail(LLMI_HIP_INVALID_ARGUMENT, "CausalGqa: null buffer");
+  GqaShape s{p.tokens, p.queryHeads, p.kvHeads, p.headDim, p.past};
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  switch (select_gqa(p)) {
+  case GqaKernel::Decode: {
+    size_t need = decode_workspace_bytes(s);
+    if (!workspace || workspace_bytes < need)
+      return fail(LLMI_HIP_WORKSPACE,
+                  "CausalGqa: decode needs a %zu-byte workspace, got %zu",
+                  need, workspace ? workspace_bytes : (size_t)0);
+    return launched(launch_gqa_decode(q, k_cache, v_cache, out, workspace, s, st),
+                    "gqaDecodeSplitK");
+  }
+  case GqaKernel::Prefill:
+    return launched(launch_gqa_prefill(q, k_cache, v_cache, out, s, st),
+                    "gqaPrefillMfma");
+  case GqaKernel::Generic:
+    return launched(launch_gqa_generic(q, k_cache, v_cache, out, s, st),
+                    "gqaGeneric");
+  case GqaKernel::None:
+    break;
+  }
+  return fail(LLMI_HIP_UNSUPPORTED, "CausalGqa: head_dim %u is not supported",
+              p.headDim);
+}
+
+size_t llmi_hip_delta_workspace_bytes(GraphDeltaParams p) {
+  if (check_delta(p) != LLMI_HIP_OK)
+    return 0;
+  if (select_delta(p) == DeltaKernel::Chunked)
+    return delta_chunked_workspace_bytes(
+        {p.tokens, p.keyHeads, p.keyDim, p.valueHeads, p.valueDim});
+  return 0;
+}
+
+int llmi_hip_delta_update(const float *q, const float *k, const uint16_t *v,
+                          const float *beta, const float *decay, float *state,
+                          uint16_t *out, GraphDeltaParams p, void *workspace,
+                          size_t workspace_bytes, void *stream) {
+  if (int st = check_delta(p))
+    return st;
+  if (!q || !k || !v || !beta || !decay || !state || !out)
+    return fail(LLMI_HIP_INVALID_ARGUMENT, "DeltaUpdate: null buffer");
+  DeltaShape s{p.tokens, p.keyHeads, p.keyDim, p.valueHeads, p.valueDim};
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  switch (select_delta(p)) {
+  case DeltaKernel::Chunked: {
+    size_t need = delta_chunked_workspace_bytes(s);
+    if (need && (!workspace || workspace_bytes < need))
+      return fail(LLMI_HIP_WORKSPACE,
+                  "DeltaUpdate: chunked form needs a %zu-byte workspace", need);
+    return launched(launch_delta_chunked(q, k, v, beta, decay, state, out,
+                                         workspace, s, st),
+                    "deltaChunkedWy");
+  }
+  case DeltaKernel::Recurrent:
+    return launched(
+        launch_delta_recurrent(q, k, v, beta, decay, state, out, s, st),
+        "deltaRecurrent");
+  case DeltaKernel::Generic:
+    return launched(launch_delta_generic(q, k, v, beta, decay, state, out, s, st),
+                    "deltaGeneric");
+  }
+  return fail(LLMI_HIP_UNSUPPORTED, "DeltaUpdate: unsupported shape");
+}
+
+int llmi_hip_workspace_init(void *workspace, size_t bytes, void *stream) {
+  if (!bytes)
+    return LLMI_HIP_OK;
+  if (!workspace)
+    return fail(LLMI_HIP_INVALID_ARGUMENT, "workspace_init: null workspace");
+  return launched(hipMemsetAsync(workspace, 0, bytes,
+                                 static_cast<hipStream_t>(stream)),
+                  "workspace_init");
+}
+
+unsigned llmi_hip_dispatch_count(int op, const void *params) {
+  if (!params)
+    return 0;
+  switch (op) {
+  case LLMI_HIP_OP_KV_APPEND:
+    return 1;
+  case LLMI_HIP_OP_CAUSAL_GQA: {
+    const GqaParams &p = *static_cast<const GqaParams *>(params);
+    if (check_gqa(p) || select_gqa(p) == GqaKernel::None)
+      return 0;
+    return 1;
+  }
+  case LLMI_HIP_OP_DELTA_UPDATE: {
+    const GraphDeltaParams &p = *static_cast<const GraphDeltaParams *>(params);
+    if (check_delta(p))
+      return 0;
+    return select_delta(p) == DeltaKernel::Chunked ? delta_chunked_dispatches() : 1;
+  }
+  }
+  return 0;
+}
+
+const char *llmi_hip_kernel_name(int op, const void *params, unsigned index) {
+  if (index >= llmi_hip_dispatch_count(op, params))
+    return nullptr;
+  switch (op) {
+  case LLMI_HIP_OP_KV_APPEND:
+    return "kvAppend";
+  case LLMI_HIP_OP_CAUSAL_GQA:
+    switch (select_gqa(*static_cast<const GqaParams *>(params))) {
+    case GqaKernel::Decode:
+      return "gqaDecodeSplitK";
+    case GqaKernel::Prefill:
+      return "gqaPrefillMfma";
+    case GqaKernel::Generic:
+      return "gqaGeneric";
+    case GqaKernel::None:
+      return nullptr;
+    }
+    return nullptr;
+  case LLMI_HIP_OP_DELTA_UPDATE:
+    switch (select_delta(*static_cast<const GraphDeltaParams *>(params))) {
+    case DeltaKernel::Chunked:
+      return delta_chunked_kernel_name(index);
+    case DeltaKernel::Recurrent:
+      return "deltaRecurrent";
+    case DeltaKernel::Generic:
+      return "deltaGeneric";
+    }
+    return nullptr;
+  }
+  return nullptr;
+}
+
+const char *llmi_hip_status_string(int status) {
+  switch (status) {
+  case LLMI_HIP_OK:
+    return "ok";
+  case LLMI_HIP_INVALID_ARGUMENT:
+    return "invalid argument";
+  case LLMI_HIP_UNSUPPORTED:
+    return "unsupported";
+  case LLMI_HIP_WORKSPACE:
+    return "workspace missing or too small";
+  case LLMI_HIP_LAUNCH_FAILED:
+    return "launch failed";
+  case LLMI_HIP_NO_DEVICE:
+    return "no device";
+  }
+  return "unknown status";
+}
+
+const char *llmi_hip_last_error(void) { return g_error; }
+
+const char *llmi_hip_build_info(void) {
+  return "llminfer-hip 0.1 gfx950";
+}
+
+} // extern "C"

@@ -1,0 +1,65 @@
+// Shared device helpers for the gfx950 kernels of the attention hot path.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace llmi {
+
+typedef _Float16 half_t;
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef float float4_t __attribute__((ext_vector_type(4)));
+typedef float float16_t __attribute__((ext_vector_type(16)));
+typedef uint32_t uint4_t __attribute__((ext_vector_type(4)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+
+// DPP lane permutations on one 16-lane row (gfx9 encodings).
+enum : int {
+  kDppXor1 = 0xB1,        // quad_perm [1,0,3,2]
+  kDppXor2 = 0x4E,        // quad_perm [2,3,0,1]
+  kDppRowHalfMirror = 0x141,
+  kDppRowMirror = 0x140,
+};
+
+template <int Ctrl> __device__ __forceinline__ float dpp(float x) {
+  return __int_as_float(
+      __builtin_amdgcn_update_dpp(0, __float_as_int(x), Ctrl, 0xF, 0xF, false));
+}
+
+// Sum over aligned groups of N lanes (N in {1,2,4,8,16}); every lane of a
+// group receives the group's total. After xor1/xor2 each quad holds its sum;
+// the half-row mirror pairs quad q with quad 1-q inside each 8-lane half, the
+// row mirror pairs the two halves of a 16-lane row.
+template <int N> __device__ __forceinline__ float group_sum(float x) {
+  if constexpr (N >= 2)
+    x += dpp<kDppXor1>(x);
+  if constexpr (N >= 4)
+    x += dpp<kDppXor2>(x);
+  if constexpr (N >= 8)
+    x += dpp<kDppRowHalfMirror>(x);
+  if constexpr (N >= 16)
+    x += dpp<kDppRowMirror>(x);
+  return x;
+}
+
+__device__ __forceinline__ float fast_exp2(float x) {
+  return __builtin_amdgcn_exp2f(x);
+}
+
+// fp32 dot of 8 fp16 pairs, accumulated in fp32 (v_dot2_f32_f16).
+__device__ __forceinline__ float dot8(half8_t a, half8_t b, float acc) {
+  acc = __builtin_amdgcn_fdot2(half2_t{a[0], a[1]}, half2_t{b[0], b[1]}, acc, false);
+  acc = __builtin_amdgcn_fdot2(half2_t{a[2], a[3]}, half2_t{b[2], b[3]}, acc, false);
+  acc = __builtin_amdgcn_fdot2(half2_t{a[4], a[5]}, half2_t{b[4], b[5]}, acc, false);
+  acc = __builtin_amdgcn_fdot2(half2_t{a[6], a[7]}, half2_t{b[6], b[7]}, acc, false);
+  return acc;
+}
+
+__device__ __forceinline__ half8_t load8(const half_t *p) {
+  return *reinterpret_cast<const half8_t *>(p);
+}
+
+} // namespace llmi

@@ -1,0 +1,76 @@
+// Launch functions of the gfx950 kernels. Each returns the hipError_t of
+// its launch(es); shape checks happen in capi.cpp before any of these runs.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace llmi {
+
+// Every workspace starts with this many bytes of completion tickets. They
+// must be zero before a workspace is first used, and every kernel that takes
+// a ticket returns it to zero, so the header stays zero between calls.
+constexpr size_t kWorkspaceTicketBytes = 4096;
+
+// ---------------------------------------------------------------- KvAppend
+hipError_t launch_cache_append(const uint16_t *src, uint16_t *cache,
+                               unsigned count, unsigned offset,
+                               hipStream_t stream);
+hipError_t launch_kv_append(const uint16_t *ksrc, const uint16_t *vsrc,
+                            uint16_t *kcache, uint16_t *vcache, unsigned count,
+                            unsigned offset, hipStream_t stream);
+
+// ----------------------------------------------------------------- GQA
+struct GqaShape {
+  unsigned T, Hq, Hkv, D, P;
+};
+
+// Split-K decode (any T, fast for small T). Workspace layout is owned by
+// gqa_decode.hip; decode_workspace_bytes sizes it.
+bool decode_supported(const GqaShape &s);
+size_t decode_workspace_bytes(const GqaShape &s);
+hipError_t launch_gqa_decode(const uint16_t *q, const uint16_t *k,
+                             const uint16_t *v, uint16_t *out, void *ws,
+                             const GqaShape &s, hipStream_t stream);
+
+// MFMA flash prefill.
+bool prefill_supported(const GqaShape &s);
+hipError_t launch_gqa_prefill(const uint16_t *q, const uint16_t *k,
+                              const uint16_t *v, uint16_t *out,
+                              const GqaShape &s, hipStream_t stream);
+
+// Generic fallback for any head_dim <= 512 and any GQA ratio.
+bool generic_supported(const GqaShape &s);
+hipError_t launch_gqa_generic(const uint16_t *q, const uint16_t *k,
+                              const uint16_t *v, uint16_t *out,
+                              const GqaShape &s, hipStream_t stream);
+
+// ------------------------------------------------------------- DeltaNet
+struct DeltaShape {
+  unsigned T, Hk, Dk, Hv, Dv;
+};
+
+bool delta_recurrent_supported(const DeltaShape &s);
+hipError_t launch_delta_recurrent(const float *q, const float *k,
+                                  const uint16_t *v, const float *beta,
+                                  const float *decay, float *state,
+                                  uint16_t *out, const DeltaShape &s,
+                                  hipStream_t stream);
+
+// Any-shape fallback, one thread per state column.
+hipError_t launch_delta_generic(const float *q, const float *k,
+                                const uint16_t *v, const float *beta,
+                                const float *decay, float *state,
+                                uint16_t *out, const DeltaShape &s,
+                                hipStream_t stream);
+
+bool delta_chunked_supported(const DeltaShape &s);
+size_t delta_chunked_workspace_bytes(const DeltaShape &s);
+hipError_t launch_delta_chunked(const float *q, const float *k,
+                                const uint16_t *v, const float *beta,
+                                const float *decay, float *state,
+                                uint16_t *out, void *ws, const DeltaShape &s,
+                                hipStream_t stream);
+
+} // namespace llmi

@@ -1,0 +1,148 @@
+"""Torch-tensor front end of the HIP backend (device memory and streams only).
+
+Each function checks dtypes/layouts on the host, fills the reference's
+parameter struct and calls the C ABI on torch's current HIP stream. The math
+runs in the gfx950 kernels of libllminfer_hip.so; there is no other path.
+
+Layouts follow the reference's op contracts (lib/GraphIR/Graph.cpp:226-279):
+  q [T, Hq, d] fp16; caches [capacity, Hkv, d] fp16; out [T, Hq, d] fp16
+  DeltaNet q, k [T, Hk*dk] fp32; v [T, Hv*dv] fp16; beta, decay [T, Hv] fp32;
+  state [Hv, dk, dv] fp32 (in place); out [T, Hv*dv] fp16
+"""
+from __future__ import annotations
+
+import ctypes as C
+
+import torch
+
+from . import _lib
+
+_workspaces: dict[int, torch.Tensor] = {}
+
+
+def _ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def _stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _require(t: torch.Tensor, dtype: torch.dtype, name: str) -> None:
+    if not t.is_cuda:
+        raise ValueError(f"{name} must be a device tensor")
+    if t.dtype != dtype:
+        raise ValueError(f"{name} must be {dtype}, got {t.dtype}")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+
+
+def workspace(nbytes: int, device: torch.device | None = None) -> torch.Tensor:
+    """A zero-initialised workspace of at least nbytes, reused per device.
+
+    The kernels leave their tickets at zero after every call, so one
+    allocation serves all later calls on the same stream.
+    """
+    dev = torch.device("cuda", torch.cuda.current_device()) if device is None else device
+    key = dev.index if dev.index is not None else torch.cuda.current_device()
+    ws = _workspaces.get(key)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=dev)
+        _workspaces[key] = ws
+    return ws
+
+
+def cache_append(src: torch.Tensor, cache: torch.Tensor, offset: int) -> None:
+    """cache.view(-1)[offset : offset + src.numel()] = src (cacheAppend)."""
+    _require(src, torch.float16, "src")
+    _require(cache, torch.float16, "cache")
+    if offset + src.numel() > cache.numel():
+        raise ValueError("append exceeds the cache")
+    lib = _lib.load()
+    _lib.check(lib.llmi_hip_cache_append(_ptr(src), _ptr(cache),
+                                         _lib.CacheParams(src.numel(), offset), _stream()))
+
+
+def kv_append(k: torch.Tensor, v: torch.Tensor, k_cache: torch.Tensor,
+              v_cache: torch.Tensor, past: int) -> None:
+    """KvAppend: rows [past, past+T) of both caches <- k, v ([T, Hkv, d])."""
+    for t, n in ((k, "k"), (v, "v"), (k_cache, "k_cache"), (v_cache, "v_cache")):
+        _require(t, torch.float16, n)
+    if k.shape != v.shape or k.dim() != 3 or k_cache.shape != v_cache.shape \
+            or k.shape[1:] != k_cache.shape[1:]:
+        raise ValueError("new keys and values must match the cache layout")
+    T, hkv, d = k.shape
+    if past + T > k_cache.shape[0]:
+        raise ValueError("append exceeds the cache capacity")
+    lib = _lib.load()
+    p = _lib.CacheParams(T * hkv * d, past * hkv * d)
+    _lib.check(lib.llmi_hip_kv_append(_ptr(k), _ptr(v), _ptr(k_cache), _ptr(v_cache),
+                                      p, _stream()))
+
+
+def gqa_params(q: torch.Tensor, k_cache: torch.Tensor, past: int) -> _lib.GqaParams:
+    T, hq, d = q.shape
+    return _lib.GqaParams(T, hq, k_cache.shape[1], d, past)
+
+
+def causal_gqa(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+               past: int, out: torch.Tensor | None = None) -> torch.Tensor:
+    """CausalGqa over cache rows [0, past+T) (the step's rows already appended)."""
+    _require(q, torch.float16, "q")
+    _require(k_cache, torch.float16, "k_cache")
+    _require(v_cache, torch.float16, "v_cache")
+    if q.dim() != 3 or k_cache.dim() != 3 or k_cache.shape != v_cache.shape \
+            or q.shape[2] != k_cache.shape[2]:
+        raise ValueError("invalid attention head shape")
+    if past + q.shape[0] > k_cache.shape[0]:
+        raise ValueError("past + tokens exceeds the cache capacity")
+    if out is None:
+        out = torch.empty_like(q)
+    _require(out, torch.float16, "out")
+    lib = _lib.load()
+    p = gqa_params(q, k_cache, past)
+    need = lib.llmi_hip_gqa_workspace_bytes(p)
+    ws = workspace(need, q.device) if need else None
+    _lib.check(lib.llmi_hip_causal_gqa(_ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(out),
+                                       p, _ptr(ws), ws.numel() if ws is not None else 0,
+                                       _stream()))
+    return out
+
+
+def delta_params(q: torch.Tensor, v: torch.Tensor, state: torch.Tensor) -> _lib.GraphDeltaParams:
+    hv, dk, dv = state.shape
+    return _lib.GraphDeltaParams(q.shape[0], q.shape[1] // dk, dk, hv, dv)
+
+
+def delta_update(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, beta: torch.Tensor,
+                 decay: torch.Tensor, state: torch.Tensor,
+                 out: torch.Tensor | None = None) -> torch.Tensor:
+    """DeltaUpdate: gated delta rule over T tokens, state updated in place."""
+    for t, n, dt in ((q, "q", torch.float32), (k, "k", torch.float32),
+                     (v, "v", torch.float16), (beta, "beta", torch.float32),
+                     (decay, "decay", torch.float32), (state, "state", torch.float32)):
+        _require(t, dt, n)
+    T = q.shape[0]
+    hv, dk, dv = state.shape
+    if q.dim() != 2 or k.shape != q.shape or q.shape[1] % dk or \
+            hv % (q.shape[1] // dk) or v.shape != (T, hv * dv) or \
+            beta.shape != (T, hv) or decay.shape != beta.shape:
+        raise ValueError("DeltaUpdate operand shapes do not match its recurrent state")
+    if out is None:
+        out = torch.empty_like(v)
+    _require(out, torch.float16, "out")
+    lib = _lib.load()
+    p = delta_params(q, v, state)
+    need = lib.llmi_hip_delta_workspace_bytes(p)
+    ws = workspace(need, q.device) if need else None
+    _lib.check(lib.llmi_hip_delta_update(_ptr(q), _ptr(k), _ptr(v), _ptr(beta), _ptr(decay),
+                                         _ptr(state), _ptr(out), p, _ptr(ws),
+                                         ws.numel() if ws is not None else 0, _stream()))
+    return out
+
+
+def kernel_names(op: int, params) -> list[str]:
+    lib = _lib.load()
+    ref = C.byref(params)
+    n = lib.llmi_hip_dispatch_count(op, ref)
+    return [lib.llmi_hip_kernel_name(op, ref, i).decode() for i in range(n)]

@@ -1,0 +1,276 @@
+"""numpy front end of the C oracle (oracle.c). TEST INFRASTRUCTURE ONLY.
+
+Imported by tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg as
+the checker / CPU baseline; the product package never imports it. Every
+function forwards to the C restatement documented in oracle.h, which cites
+the reference file:line it follows.
+
+Synthetic inputs (seeded, reproducible on any host):
+  make_gqa_inputs    q [T,Hq,d], caches [cap,Hkv,d] with rows [0,P+T) filled
+  make_delta_inputs  the DeltaUpdate operands as the reference graph produces
+                     them: L2-normalised fp32 q (x 1/sqrt(dk)) and k, fp16 v,
+                     beta = fp16(sigmoid(b)), decay = exp(-softplus(a)).
+"""
+from __future__ import annotations
+
+import ctypes as C
+import subprocess
+from dataclasses import dataclass
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+LIB_PATH = HERE / "liboracle.so"
+REF_PATH = HERE / "_ref" / "libllmiref.so"
+
+_lib = None
+
+_u16p = np.ctypeslib.ndpointer(np.uint16, flags="C_CONTIGUOUS")
+_f32p = np.ctypeslib.ndpointer(np.float32, flags="C_CONTIGUOUS")
+_f64p = np.ctypeslib.ndpointer(np.float64, flags="C_CONTIGUOUS")
+_u32 = C.c_uint32
+_u64 = C.c_uint64
+
+
+class Cost(C.Structure):
+    _fields_ = [("fp_macs", _u64), ("scalar_ops", _u64), ("exp", _u64),
+                ("read_bytes", _u64), ("write_bytes", _u64)]
+
+
+def build() -> Path:
+    """Compile liboracle.so with the committed Makefile (always rebuilds)."""
+    subprocess.run(["make", "-s", "-B", "-C", str(HERE), "liboracle.so"], check=True)
+    return LIB_PATH
+
+
+def lib() -> C.CDLL:
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            build()
+        L = C.CDLL(str(LIB_PATH))
+        L.orc_f32_to_f16.restype = C.c_uint16
+        L.orc_f32_to_f16.argtypes = [C.c_float]
+        L.orc_f16_to_f32.restype = C.c_float
+        L.orc_f16_to_f32.argtypes = [C.c_uint16]
+        L.orc_f32_to_f16_n.argtypes = [_f32p, _u16p, C.c_size_t]
+        L.orc_f16_to_f32_n.argtypes = [_u16p, _f32p, C.c_size_t]
+        L.orc_fill_normal_f32.argtypes = [_u64, _u64, C.c_size_t, C.c_double, C.c_double, _f32p]
+        L.orc_fill_normal_f16.argtypes = [_u64, _u64, C.c_size_t, C.c_double, C.c_double, _u16p]
+        L.orc_fill_lcg_f16.argtypes = [C.POINTER(_u32), C.c_size_t, _u16p]
+        L.orc_gqa_dense_f64.argtypes = [_u16p, _u16p, _u16p, _f64p] + [_u32] * 5
+        L.orc_gqa_eager_f16.argtypes = [_u16p, _u16p, _u16p, _u16p] + [_u32] * 5
+        L.orc_gqa_f32.argtypes = [_u16p, _u16p, _u16p, _u16p] + [_u32] * 5 + [C.c_int]
+        L.orc_kv_append.argtypes = [_u16p, _u16p] + [_u32] * 4
+        L.orc_delta_recurrent_f64.argtypes = [_f32p, _f32p, _u16p, _f32p, _f32p, _f32p,
+                                              _f64p, C.c_void_p] + [_u32] * 5
+        L.orc_delta_recurrent_f32.argtypes = [_f32p, _f32p, _u16p, _f32p, _f32p, _f32p,
+                                              _u16p] + [_u32] * 5 + [C.c_int]
+        L.orc_delta_chunked_f64.argtypes = [_f32p, _f32p, _u16p, _f32p, _f32p, _f32p,
+                                            _f64p, C.c_void_p] + [_u32] * 6
+        L.orc_delta_gates.argtypes = [_u16p, _u16p, _f32p, _f32p, _f32p, _f32p, _u32, _u32]
+        L.orc_l2norm_f32.argtypes = [_u16p, _f32p, _u32, _u32, C.c_float, C.c_float]
+        for name, n in (("orc_cost_kv_append", 3), ("orc_cost_causal_gqa", 5),
+                        ("orc_cost_delta_update", 5)):
+            fn = getattr(L, name)
+            fn.restype = C.c_int
+            fn.argtypes = [_u64] * n + [C.POINTER(Cost)]
+        L.orc_cpu_count.restype = C.c_int
+        _lib = L
+    return _lib
+
+
+# ------------------------------------------------------------------ fp16
+
+def f32_to_f16(x) -> np.ndarray:
+    a = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty(a.shape, np.uint16)
+    lib().orc_f32_to_f16_n(a.reshape(-1), out.reshape(-1), a.size)
+    return out
+
+
+def f16_to_f32(bits) -> np.ndarray:
+    a = np.ascontiguousarray(bits, dtype=np.uint16)
+    out = np.empty(a.shape, np.float32)
+    lib().orc_f16_to_f32_n(a.reshape(-1), out.reshape(-1), a.size)
+    return out
+
+
+# ------------------------------------------------------------------- RNG
+
+def normal_f16(seed: int, stream: int, shape, mean=0.0, std=1.0) -> np.ndarray:
+    out = np.empty(shape, np.uint16)
+    lib().orc_fill_normal_f16(seed, stream, out.size, mean, std, out.reshape(-1))
+    return out
+
+
+def normal_f32(seed: int, stream: int, shape, mean=0.0, std=1.0) -> np.ndarray:
+    out = np.empty(shape, np.float32)
+    lib().orc_fill_normal_f32(seed, stream, out.size, mean, std, out.reshape(-1))
+    return out
+
+
+def lcg_f16(state: int, n: int) -> tuple[np.ndarray, int]:
+    s = _u32(state)
+    out = np.empty(n, np.uint16)
+    lib().orc_fill_lcg_f16(C.byref(s), n, out)
+    return out, s.value
+
+
+# ------------------------------------------------------------------- GQA
+
+def gqa_dense_f64(q, kc, vc, past: int) -> np.ndarray:
+    T, hq, d = q.shape
+    hkv = kc.shape[1]
+    assert kc.shape[0] >= past + T and vc.shape == kc.shape
+    out = np.empty((T, hq, d), np.float64)
+    lib().orc_gqa_dense_f64(np.ascontiguousarray(q), np.ascontiguousarray(kc),
+                            np.ascontiguousarray(vc), out, T, hq, hkv, d, past)
+    return out
+
+
+def gqa_eager_f16(q, kc, vc, past: int) -> np.ndarray:
+    T, hq, d = q.shape
+    out = np.empty((T, hq, d), np.uint16)
+    lib().orc_gqa_eager_f16(np.ascontiguousarray(q), np.ascontiguousarray(kc),
+                            np.ascontiguousarray(vc), out, T, hq, kc.shape[1], d, past)
+    return out
+
+
+def gqa_f32(q, kc, vc, past: int, threads: int = 0) -> np.ndarray:
+    T, hq, d = q.shape
+    out = np.empty((T, hq, d), np.uint16)
+    lib().orc_gqa_f32(np.ascontiguousarray(q), np.ascontiguousarray(kc),
+                      np.ascontiguousarray(vc), out, T, hq, kc.shape[1], d, past, threads)
+    return out
+
+
+def kv_append(src, cache, past: int) -> None:
+    T, hkv, d = src.shape
+    lib().orc_kv_append(np.ascontiguousarray(src), cache, T, hkv, d, past)
+
+
+@dataclass
+class GqaInputs:
+    q: np.ndarray         # [T, Hq, d] fp16 bits
+    k_new: np.ndarray     # [T, Hkv, d]
+    v_new: np.ndarray
+    k_cache: np.ndarray   # [cap, Hkv, d], rows [0, P) past, [P, P+T) = k_new
+    v_cache: np.ndarray
+    past: int
+
+
+def make_gqa_inputs(seed: int, T: int, hq: int, hkv: int, d: int, past: int,
+                    capacity: int | None = None) -> GqaInputs:
+    cap = capacity if capacity is not None else past + T
+    q = normal_f16(seed, 1, (T, hq, d))
+    k_new = normal_f16(seed, 2, (T, hkv, d))
+    v_new = normal_f16(seed, 3, (T, hkv, d))
+    kc = np.zeros((cap, hkv, d), np.uint16)
+    vc = np.zeros((cap, hkv, d), np.uint16)
+    if past:
+        kc[:past] = normal_f16(seed, 4, (past, hkv, d))
+        vc[:past] = normal_f16(seed, 5, (past, hkv, d))
+    kc[past:past + T] = k_new
+    vc[past:past + T] = v_new
+    return GqaInputs(q, k_new, v_new, kc, vc, past)
+
+
+# -------------------------------------------------------------- DeltaNet
+
+def delta_recurrent_f64(q, k, v, beta, decay, state):
+    T = q.shape[0]
+    hv, dk, dv = state.shape
+    hk = q.shape[1] // dk
+    out = np.empty((T, hv * dv), np.float64)
+    st = np.empty(state.shape, np.float64)
+    lib().orc_delta_recurrent_f64(q, k, v, beta, decay, np.ascontiguousarray(state), st,
+                                  out.ctypes.data, T, hk, dk, hv, dv)
+    return out, st
+
+
+def delta_recurrent_f32(q, k, v, beta, decay, state, threads: int = 0):
+    """Returns (out fp16 bits, new state); `state` is not modified."""
+    T = q.shape[0]
+    hv, dk, dv = state.shape
+    hk = q.shape[1] // dk
+    out = np.empty((T, hv * dv), np.uint16)
+    st = np.array(state, np.float32, copy=True)
+    lib().orc_delta_recurrent_f32(q, k, v, beta, decay, st, out, T, hk, dk, hv, dv, threads)
+    return out, st
+
+
+def delta_chunked_f64(q, k, v, beta, decay, state, chunk: int = 64):
+    T = q.shape[0]
+    hv, dk, dv = state.shape
+    hk = q.shape[1] // dk
+    out = np.empty((T, hv * dv), np.float64)
+    st = np.empty(state.shape, np.float64)
+    lib().orc_delta_chunked_f64(q, k, v, beta, decay, np.ascontiguousarray(state), st,
+                                out.ctypes.data, T, hk, dk, hv, dv, chunk)
+    return out, st
+
+
+def delta_gates(a, b, a_log, dt_bias):
+    T, hv = a.shape
+    beta = np.empty((T, hv), np.float32)
+    decay = np.empty((T, hv), np.float32)
+    lib().orc_delta_gates(np.ascontiguousarray(a), np.ascontiguousarray(b),
+                          np.ascontiguousarray(a_log, np.float32),
+                          np.ascontiguousarray(dt_bias, np.float32), beta, decay, T, hv)
+    return beta, decay
+
+
+def l2norm_f32(x, width: int, eps: float = 1e-6, scale: float = 1.0) -> np.ndarray:
+    a = np.ascontiguousarray(x, np.uint16)
+    out = np.empty(a.shape, np.float32)
+    lib().orc_l2norm_f32(a.reshape(-1), out.reshape(-1), a.size // width, width, eps, scale)
+    return out
+
+
+@dataclass
+class DeltaInputs:
+    q: np.ndarray      # [T, Hk*dk] fp32
+    k: np.ndarray      # [T, Hk*dk] fp32
+    v: np.ndarray      # [T, Hv*dv] fp16 bits
+    beta: np.ndarray   # [T, Hv] fp32
+    decay: np.ndarray  # [T, Hv] fp32 (linear)
+    state: np.ndarray  # [Hv, dk, dv] fp32
+
+
+def make_delta_inputs(seed: int, T: int, hk: int, dk: int, hv: int, dv: int,
+                      state_std: float = 0.0) -> DeltaInputs:
+    """cfg4/cfg5 DeltaNet operands, produced the way the reference graph does:
+    L2Norm(q, eps 1e-6, scale 1/sqrt(dk)) and L2Norm(k) (Qwen35ModelBuilder.cpp:
+    155-156, Graph.metal:96-109), gates via deltaGates with A_log = 0 and
+    dt_bias = 0 (Graph.metal:131-144)."""
+    qh = normal_f16(seed, 11, (T, hk * dk))
+    kh = normal_f16(seed, 12, (T, hk * dk))
+    v = normal_f16(seed, 13, (T, hv * dv))
+    a = normal_f16(seed, 14, (T, hv))
+    b = normal_f16(seed, 15, (T, hv))
+    q = l2norm_f32(qh, dk, 1e-6, float(1.0 / np.sqrt(np.float32(dk))))
+    k = l2norm_f32(kh, dk, 1e-6, 1.0)
+    beta, decay = delta_gates(a, b, np.zeros(hv, np.float32), np.zeros(hv, np.float32))
+    if state_std:
+        state = normal_f32(seed, 16, (hv, dk, dv), 0.0, state_std)
+    else:
+        state = np.zeros((hv, dk, dv), np.float32)
+    return DeltaInputs(q, k, v, beta, decay, state)
+
+
+# ------------------------------------------------------------------ cost
+
+def cost(kind: str, *dims: int) -> Cost:
+    c = Cost()
+    fn = {"kv_append": lib().orc_cost_kv_append,
+          "causal_gqa": lib().orc_cost_causal_gqa,
+          "delta_update": lib().orc_cost_delta_update}[kind]
+    if fn(*dims, C.byref(c)) != 0:
+        raise OverflowError(f"{kind} cost overflow")
+    return c
+
+
+def cpu_count() -> int:
+    return lib().orc_cpu_count()

@@ -1,0 +1,152 @@
+/*
+ * CPU oracle for the llminfer attention hot path.
+ *
+ * TEST INFRASTRUCTURE ONLY. This library is the parity checker and the CPU
+ * baseline that bench.py times next to the GPU. Only tests/, the smoke()
+ * entry of __graft_entry__.py and bench.py's cpu_baseline leg may load it.
+ * The product path (llminfer_amd, libllminfer_hip.so) never links or calls it.
+ *
+ * Every function restates the reference's arithmetic from its source (cited
+ * per function as /root/reference relative path:line). The reference's GPU
+ * kernels are Metal shaders that cannot run here, so these are restatements,
+ * not builds. The pins that check each function are listed in tests/
+ * (test_oracle_*.py); a function without a pin says so below.
+ *
+ * Layouts (identical to the reference's buffers):
+ *   q          [T][Hq][d]        fp16 bits (uint16)
+ *   k/v cache  [cap][Hkv][d]     fp16 bits, rows [0, P+T) valid
+ *   out        [T][Hq][d]
+ *   delta q,k  [T][Hk*dk]        fp32
+ *   delta v    [T][Hv*dv]        fp16 bits
+ *   beta,decay [T][Hv]           fp32 (decay is LINEAR, not log)
+ *   state      [Hv][dk][dv]      fp32, updated in place
+ *   delta out  [T][Hv*dv]        fp16 bits
+ */
+#ifndef LLMI_ORACLE_H
+#define LLMI_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* fp16 <-> fp32, round-to-nearest-even with subnormals.
+ * Follows lib/ModelFormat/Quantization.cpp:25-55. */
+uint16_t orc_f32_to_f16(float value);
+float orc_f16_to_f32(uint16_t bits);
+void orc_f32_to_f16_n(const float *in, uint16_t *out, size_t n);
+void orc_f16_to_f32_n(const uint16_t *in, float *out, size_t n);
+
+/* Seeded synthetic inputs. Counter-based SplitMix64 -> Box-Muller in double,
+ * rounded to fp32 then (for the _f16 variant) fp16 RNE. Sample i of
+ * (seed, stream) depends only on (seed, stream, i). */
+void orc_fill_normal_f32(uint64_t seed, uint64_t stream, size_t n, double mean,
+                         double stddev, float *out);
+void orc_fill_normal_f16(uint64_t seed, uint64_t stream, size_t n, double mean,
+                         double stddev, uint16_t *out);
+
+/* The LCG fixture generator of tests/FlashAttentionTest.mm:28-36:
+ * state = state*1664525 + 1013904223; value = (int(state>>24) - 128) / 64.
+ * *state carries over between calls, as the reference fills q, k, v in turn. */
+void orc_fill_lcg_f16(uint32_t *state, size_t n, uint16_t *out);
+
+/* Dense causal GQA in double precision.
+ * Restates tests/FlashAttentionTest.mm:53-86: query row (t, h) sees keys
+ * [0, P + t]; KV head = h / (Hq / Hkv); scores scaled by 1/sqrt(d). */
+void orc_gqa_dense_f64(const uint16_t *q, const uint16_t *k_cache,
+                       const uint16_t *v_cache, double *out, uint32_t T,
+                       uint32_t Hq, uint32_t Hkv, uint32_t d, uint32_t P);
+
+/* Eager 3-pass GQA with the fp16 rounding points of the reference decode
+ * path: score = fp16(fp16(q.k) * rsqrt(d)) (Reference.metal:303-323),
+ * probabilities rounded to fp16 (Graph.metal:172-210), fp32 PV accumulate
+ * rounded to fp16 (Graph.metal:212-230). */
+void orc_gqa_eager_f16(const uint16_t *q, const uint16_t *k_cache,
+                       const uint16_t *v_cache, uint16_t *out, uint32_t T,
+                       uint32_t Hq, uint32_t Hkv, uint32_t d, uint32_t P);
+
+/* fp32 causal GQA with a per-row max/sum softmax and fp16 output: the
+ * semantics of the fused flash kernel (FlashAttention.metal:14-82: fp32
+ * scores, fp32 softmax, fp32 accumulate, one fp16 rounding at the end).
+ * Multi-threaded over query rows with `threads` workers (0 = all CPUs in the
+ * affinity mask). This is the CPU baseline that bench.py times. */
+void orc_gqa_f32(const uint16_t *q, const uint16_t *k_cache,
+                 const uint16_t *v_cache, uint16_t *out, uint32_t T,
+                 uint32_t Hq, uint32_t Hkv, uint32_t d, uint32_t P,
+                 int threads);
+
+/* KvAppend: copy T new rows into cache rows [P, P+T). Reference.metal:295-301
+ * with the offset of MetalExecutionPlan.cpp:516-523. */
+void orc_kv_append(const uint16_t *src, uint16_t *cache, uint32_t T,
+                   uint32_t Hkv, uint32_t d, uint32_t P);
+
+/* Gated delta rule, token recurrence, double accumulation in a double state.
+ * Restates Reference.metal:182-197 (updateDeltaColumn) with the layouts and
+ * key-head map of Graph.metal:146-170: for value head h and column j,
+ *   pred = sum_i decay*S[i][j]*k_i ; delta = beta*(v_j - pred)
+ *   S[i][j] = decay*S[i][j] + k_i*delta ; y_j = sum_i S[i][j]*q_i.
+ * state_in is read, state_out written (may alias). out may be NULL. */
+void orc_delta_recurrent_f64(const float *q, const float *k, const uint16_t *v,
+                             const float *beta, const float *decay,
+                             const float *state_in, double *state_out,
+                             double *out, uint32_t T, uint32_t Hk, uint32_t dk,
+                             uint32_t Hv, uint32_t dv);
+
+/* The same recurrence in fp32 with fp16 outputs, operation for operation as
+ * updateDeltaColumn (fma order included). Multi-threaded over value columns.
+ * This is the DeltaNet CPU baseline. state is updated in place. */
+void orc_delta_recurrent_f32(const float *q, const float *k, const uint16_t *v,
+                             const float *beta, const float *decay,
+                             float *state, uint16_t *out, uint32_t T,
+                             uint32_t Hk, uint32_t dk, uint32_t Hv, uint32_t dv,
+                             int threads);
+
+/* Chunk-wise (WY / UT-transform) form of the same recurrence, in double.
+ * Published method: Yang, Kautz, Hatamizadeh, "Gated Delta Networks"
+ * (arXiv:2412.06464) and Yang et al. "Parallelizing Linear Transformers with
+ * the Delta Rule over Sequence Length" (arXiv:2406.06484). For each chunk of
+ * C tokens with cumulative log decay g:
+ *   A[t][s] = beta_t exp(g_t-g_s) k_t.k_s (s<t);  Tm = (I+A)^-1
+ *   W = Tm diag(beta exp(g)) K ;  U' = Tm diag(beta) V ;  U = U' - W S
+ *   Y = diag(exp(g)) Q S + M U,  M[t][s] = exp(g_t-g_s) q_t.k_s (s<=t)
+ *   S <- exp(g_C) S + K^T diag(exp(g_C-g)) U
+ * Only differences g_t - g_s with s <= t are exponentiated. */
+void orc_delta_chunked_f64(const float *q, const float *k, const uint16_t *v,
+                           const float *beta, const float *decay,
+                           const float *state_in, double *state_out,
+                           double *out, uint32_t T, uint32_t Hk, uint32_t dk,
+                           uint32_t Hv, uint32_t dv, uint32_t chunk);
+
+/* DeltaNet gate numerics of Graph.metal:131-144 with Reference.metal:4-12:
+ * beta = fp16(logistic(b)) stored as f32; decay = exp(-exp(A_log[h]) *
+ * stableSoftplus(a + dt_bias[h])). a, b are fp16 bits [T][Hv]. */
+void orc_delta_gates(const uint16_t *a, const uint16_t *b, const float *a_log,
+                     const float *dt_bias, float *beta, float *decay,
+                     uint32_t T, uint32_t Hv);
+
+/* Grouped L2 norm of Graph.metal:96-109 (l2NormF32): per row of `width`,
+ * out = x * rsqrt(sum(x^2) + eps) * scale, fp16 in, fp32 out. */
+void orc_l2norm_f32(const uint16_t *in, float *out, uint32_t rows,
+                    uint32_t width, float eps, float scale);
+
+/* Cost model of lib/GraphIR/Cost.cpp:180-201 (MACs) and :56-94 (bytes) for
+ * the three hot ops. Returns 0 on success, -1 on overflow. */
+typedef struct {
+  uint64_t fp_macs, scalar_ops, exp;
+  uint64_t read_bytes, write_bytes;
+} orc_cost;
+int orc_cost_kv_append(uint64_t T, uint64_t Hkv, uint64_t d, orc_cost *c);
+int orc_cost_causal_gqa(uint64_t T, uint64_t P, uint64_t Hq, uint64_t Hkv,
+                        uint64_t d, orc_cost *c);
+int orc_cost_delta_update(uint64_t T, uint64_t Hk, uint64_t dk, uint64_t Hv,
+                          uint64_t dv, orc_cost *c);
+
+/* Number of CPUs in this process's affinity mask. */
+int orc_cpu_count(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif
