@@ -1,0 +1,641 @@
+#!/usr/bin/env python3
+"""Benchmark of the llminfer attention hot path on one MI355X (gfx950).
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--only-headline]
+                    [--cpu-seconds S] [--no-cpu]
+
+Prints ONE JSON line. The headline workload is the GQA single-token decode
+of the reference's decode path (KvAppend + CausalGqa, T=1, 4096 past rows,
+capacity 8192, 16 query / 4 KV heads, head_dim 256, fp16): one "step" is one
+attention layer's decode -- the KvAppend launch plus the split-K CausalGqa
+launch -- over inputs already resident in HBM. `value` is GPU microseconds
+per layer step (time-like, lower is better). The K/V caches rotate over 32
+independent sets (1.07 GB) so that every step reads its 16.8 MB of K/V from
+HBM rather than from the 256 MB Infinity Cache.
+
+Timing. Warmup W steps, synchronize, then a spin kernel holds the GPU while
+the host enqueues all K steps, so the GPU runs them back to back and the
+measurement is device time, not Python launch latency. Start/end HIP events
+bracket exactly the K steps (ms_per_step), and an event pair on the same
+stream brackets every launch of the dominant kernel (roofline.achieved).
+
+`roofline`: algorithmic bytes of one decode launch (K and V rows [0, P+1)
+plus q and out, the reference cost model's traffic for CausalGqa,
+lib/GraphIR/Cost.cpp:56-94) / its average event-timed duration, against
+MI355X's 8 TB/s. `traffic` is the HBM bytes per launch from rocprofv3
+FETCH_SIZE + WRITE_SIZE, read from profiles/traffic.json when that summary
+exists for this kernel and workload.
+
+`cpu_baseline`: the C oracle (oracle/liboracle.so, the same CPU restatement
+the parity tests use) timed on this host's cores on the same inputs; it also
+reports the GPU-vs-CPU max-abs output difference of the same step.
+
+`configs`: the other BASELINE configurations measured the same way (prefill
+128, chunked prefill 2048+2048, DeltaNet prefill 1024, hybrid 32K decode),
+each with its roofline fraction and a bounded CPU sample.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import platform
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+if str(ROOT) not in sys.path:
+    sys.path.insert(0, str(ROOT))
+
+METRIC = ("attn µs/layer + % HBM roofline (decode) / % MFMA peak (prefill), 1 GPU")
+HBM_PEAK_GBS = 8000.0       # MI355X HBM3E, GB/s
+MFMA_F16_PEAK_TFS = 2500.0  # MI355X dense fp16 MFMA, TFLOP/s
+CPU_THREAD_CAP = 16         # the GPU box's CPU share per GPU
+
+
+# --------------------------------------------------------------- helpers
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def gqa_flops(T: int, P: int, hq: int, d: int) -> int:
+    """2 x MACs of lib/GraphIR/Cost.cpp:188-201."""
+    return 4 * hq * d * (T * P + T * (T + 1) // 2)
+
+
+def gqa_bytes(T: int, P: int, hq: int, hkv: int, d: int) -> int:
+    """q + visible K and V rows + out, fp16 (Cost.cpp:56-94 traffic)."""
+    return 2 * (2 * T * hq * d + 2 * (P + T) * hkv * d)
+
+
+def delta_flops(T: int, hv: int, dk: int, dv: int) -> int:
+    """2 x MACs of Cost.cpp:180-187 (3 T Hv dk dv MACs)."""
+    return 6 * T * hv * dk * dv
+
+
+def delta_bytes(T: int, hk: int, dk: int, hv: int, dv: int) -> int:
+    """f32 q, k; fp16 v; f32 beta, decay; f32 state in and out; fp16 out."""
+    return (8 * T * hk * dk + 2 * T * hv * dv + 8 * T * hv
+            + 8 * hv * dk * dv + 2 * T * hv * dv)
+
+
+def cpu_threads() -> int:
+    import oracle
+    return max(1, min(CPU_THREAD_CAP, oracle.cpu_count()))
+
+
+def cpu_model() -> str:
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or "unknown"
+
+
+def host_u16(t):
+    import numpy as np
+    import torch
+    return t.detach().contiguous().cpu().view(torch.int16).numpy().view(np.uint16)
+
+
+def host_f32(t):
+    import numpy as np
+    return t.detach().contiguous().cpu().numpy().astype(np.float32, copy=False)
+
+
+def time_cpu(fn, budget_s: float, min_runs: int = 1) -> tuple[float, int]:
+    """Mean seconds per fn() call, repeating until budget_s is spent."""
+    runs, t0 = 0, time.perf_counter()
+    while True:
+        fn()
+        runs += 1
+        el = time.perf_counter() - t0
+        if runs >= min_runs and el >= budget_s:
+            return el / runs, runs
+        if runs >= 10000:
+            return el / runs, runs
+
+
+# ------------------------------------------------------------- workloads
+
+class Workload:
+    """A repeatable step on resident device inputs.
+
+    launch(i, marks) enqueues step i; marks maps a kernel label to an
+    (event_a, event_b) pair to record around that launch, or is empty.
+    """
+    name = ""
+    tokens = 1
+    dominant = ""
+    bound = "hbm"
+
+    def launch(self, i: int, marks: dict) -> None:
+        raise NotImplementedError
+
+    def work(self, i: int) -> int:  # algorithmic bytes or flops of the dominant launch
+        raise NotImplementedError
+
+    def config(self) -> dict:
+        raise NotImplementedError
+
+    def cpu(self, budget_s: float) -> dict:
+        raise NotImplementedError
+
+
+def _randn16(gen, shape, dev):
+    import torch
+    return torch.randn(shape, generator=gen, device=dev, dtype=torch.float32).half()
+
+
+class GqaDecode(Workload):
+    """configs[1] (and the GQA half of configs[4]): KvAppend + split-K decode."""
+    bound = "hbm"
+    dominant = "gqaDecodeSplitK"
+
+    def __init__(self, dev, seed=2, past=4096, cap=8192, sets=32, hq=16, hkv=4, d=256):
+        import torch
+        from llminfer_amd import ops
+        self.P, self.cap, self.sets, self.hq, self.hkv, self.d = past, cap, sets, hq, hkv, d
+        self.name = f"gqa_decode_{past // 1024}k"
+        g = torch.Generator(device=dev).manual_seed(seed)
+        self.kc = [_randn16(g, (cap, hkv, d), dev) for _ in range(sets)]
+        self.vc = [_randn16(g, (cap, hkv, d), dev) for _ in range(sets)]
+        self.q = _randn16(g, (1, hq, d), dev)
+        self.kn = _randn16(g, (1, hkv, d), dev)
+        self.vn = _randn16(g, (1, hkv, d), dev)
+        self.out = torch.empty_like(self.q)
+        self.app = [ops.bind_kv_append(self.kn, self.vn, self.kc[s], self.vc[s], past)
+                    for s in range(sets)]
+        self.att = [ops.bind_causal_gqa(self.q, self.kc[s], self.vc[s], self.out, past)
+                    for s in range(sets)]
+        assert self.att[0].what == self.dominant, self.att[0].what
+
+    def launch(self, i, marks):
+        s = i % self.sets
+        self.app[s]()
+        m = marks.get("gqa")
+        if m:
+            m[0].record()
+        self.att[s]()
+        if m:
+            m[1].record()
+
+    def work(self, i):
+        return gqa_bytes(1, self.P, self.hq, self.hkv, self.d)
+
+    def config(self):
+        return {"workload": self.name, "tokens": 1, "past": self.P, "capacity": self.cap,
+                "query_heads": self.hq, "kv_heads": self.hkv, "head_dim": self.d,
+                "kv_sets": self.sets,
+                "kv_bytes_resident": 2 * self.sets * self.cap * self.hkv * self.d * 2,
+                "cache_state": "cold: K/V rotate over independent sets larger than the MALL"}
+
+    def cpu(self, budget_s):
+        import numpy as np
+        import oracle
+        import torch
+        s = 0
+        torch.cuda.synchronize()
+        kc, vc, q = host_u16(self.kc[s]), host_u16(self.vc[s]), host_u16(self.q)
+        kn, vn = host_u16(self.kn), host_u16(self.vn)
+        # Re-run the GPU step on set 0 so `out` belongs to these inputs.
+        self.app[s]()
+        self.att[s]()
+        torch.cuda.synchronize()
+        gpu_out = oracle.f16_to_f32(host_u16(self.out))
+        thr = cpu_threads()
+
+        def step(threads):
+            oracle.kv_append(kn, kc, self.P)
+            oracle.kv_append(vn, vc, self.P)
+            return oracle.gqa_f32(q, kc, vc, self.P, threads)
+
+        want = step(thr)
+        err = float(np.max(np.abs(gpu_out - oracle.f16_to_f32(want))))
+        sec, runs = time_cpu(lambda: step(thr), budget_s)
+        sec1, runs1 = time_cpu(lambda: step(1), budget_s / 4)
+        return {"value": sec * 1e6, "unit": "µs/layer", "cores": thr, "kind": "port",
+                "sample": f"the full step (KvAppend + CausalGqa, P={self.P}, 16/4 heads, d=256) "
+                          f"on one cache set, {runs} runs, fp32 online softmax "
+                          "(oracle orc_gqa_f32)",
+                "single_thread_value": sec1 * 1e6, "single_thread_runs": runs1,
+                "cpu_model": cpu_model(), "gpu_vs_cpu_max_abs": err}
+
+
+class GqaPrefill(Workload):
+    """configs[0] (T=128, P=0) and configs[2] (T=2048 after P=2048)."""
+    bound = "mfma"
+    dominant = "gqaPrefillMfma"
+
+    def __init__(self, dev, T, P, cap, seed, hq=16, hkv=4, d=256):
+        import torch
+        from llminfer_amd import ops
+        self.T, self.P, self.cap, self.hq, self.hkv, self.d = T, P, cap, hq, hkv, d
+        self.name = f"gqa_prefill_{T}_past{P}"
+        self.tokens = T
+        g = torch.Generator(device=dev).manual_seed(seed)
+        self.kc = _randn16(g, (cap, hkv, d), dev)
+        self.vc = _randn16(g, (cap, hkv, d), dev)
+        self.q = _randn16(g, (T, hq, d), dev)
+        self.kn = _randn16(g, (T, hkv, d), dev)
+        self.vn = _randn16(g, (T, hkv, d), dev)
+        self.out = torch.empty_like(self.q)
+        self.app = ops.bind_kv_append(self.kn, self.vn, self.kc, self.vc, P)
+        self.att = ops.bind_causal_gqa(self.q, self.kc, self.vc, self.out, P)
+        assert self.att.what == self.dominant, self.att.what
+
+    def launch(self, i, marks):
+        self.app()
+        m = marks.get("gqa")
+        if m:
+            m[0].record()
+        self.att()
+        if m:
+            m[1].record()
+
+    def work(self, i):
+        return gqa_flops(self.T, self.P, self.hq, self.d)
+
+    def config(self):
+        return {"workload": self.name, "tokens": self.T, "past": self.P, "capacity": self.cap,
+                "query_heads": self.hq, "kv_heads": self.hkv, "head_dim": self.d}
+
+    def cpu(self, budget_s):
+        import numpy as np
+        import oracle
+        import torch
+        torch.cuda.synchronize()
+        self.app()
+        self.att()
+        torch.cuda.synchronize()
+        kc, vc, q = host_u16(self.kc), host_u16(self.vc), host_u16(self.q)
+        gpu_out = oracle.f16_to_f32(host_u16(self.out))
+        thr = cpu_threads()
+        # Sample: a contiguous block of query rows centred on T/2, whose mean
+        # visible length equals the whole chunk's (P + T/2); scaled by T/rows.
+        rows = min(self.T, 64)
+        t0 = (self.T - rows) // 2
+        qs = np.ascontiguousarray(q[t0:t0 + rows])
+        want = oracle.gqa_f32(qs, kc, vc, self.P + t0, thr)
+        err = float(np.max(np.abs(gpu_out[t0:t0 + rows] - oracle.f16_to_f32(want))))
+        sec, runs = time_cpu(lambda: oracle.gqa_f32(qs, kc, vc, self.P + t0, thr), budget_s)
+        scale = self.T / rows
+        return {"value": sec * scale * 1e6, "unit": "µs/layer", "cores": thr,
+                "kind": "port",
+                "sample": f"{rows} query rows [{t0}, {t0 + rows}) of {self.T} "
+                          f"(mean visible length = the chunk's), x{scale:g}, {runs} runs",
+                "gpu_vs_cpu_max_abs": err}
+
+
+def _delta_inputs(g, dev, T, hk, dk, hv, dv):
+    """DeltaUpdate operands as the reference graph produces them: L2-normalised
+    fp32 q (x 1/sqrt(dk)) and k from fp16 N(0,1) (Graph.metal:96-109), fp16 v,
+    beta = fp16(sigmoid(N(0,1))), decay = exp(-softplus(N(0,1)))."""
+    import torch
+    qh = _randn16(g, (T, hk, dk), dev).float()
+    kh = _randn16(g, (T, hk, dk), dev).float()
+    q = qh * (torch.rsqrt((qh * qh).sum(-1, keepdim=True) + 1e-6) / math.sqrt(dk))
+    k = kh * torch.rsqrt((kh * kh).sum(-1, keepdim=True) + 1e-6)
+    v = _randn16(g, (T, hv * dv), dev)
+    beta = torch.sigmoid(_randn16(g, (T, hv), dev).float()).half().float()
+    decay = torch.exp(-torch.nn.functional.softplus(_randn16(g, (T, hv), dev).float()))
+    return (q.reshape(T, hk * dk).contiguous(), k.reshape(T, hk * dk).contiguous(),
+            v, beta.contiguous(), decay.contiguous())
+
+
+class DeltaPrefill(Workload):
+    """DeltaUpdate over 1024 tokens from a zero state."""
+    bound = "hbm"
+
+    def __init__(self, dev, T=1024, hk=16, dk=128, hv=32, dv=128, seed=4):
+        import torch
+        from llminfer_amd import ops
+        self.T, self.hk, self.dk, self.hv, self.dv = T, hk, dk, hv, dv
+        self.name = f"delta_prefill_{T}"
+        self.tokens = T
+        g = torch.Generator(device=dev).manual_seed(seed)
+        self.q, self.k, self.v, self.beta, self.decay = _delta_inputs(g, dev, T, hk, dk, hv, dv)
+        self.state0 = torch.zeros((hv, dk, dv), dtype=torch.float32, device=dev)
+        self.state = self.state0.clone()
+        self.out = torch.empty_like(self.v)
+        self.op = ops.bind_delta_update(self.q, self.k, self.v, self.beta, self.decay,
+                                        self.state, self.out)
+        self.dominant = self.op.what
+
+    def launch(self, i, marks):
+        m = marks.get("delta")
+        if m:
+            m[0].record()
+        self.op()
+        if m:
+            m[1].record()
+
+    def work(self, i):
+        return delta_bytes(self.T, self.hk, self.dk, self.hv, self.dv)
+
+    def config(self):
+        return {"workload": self.name, "tokens": self.T, "key_heads": self.hk,
+                "key_dim": self.dk, "value_heads": self.hv, "value_dim": self.dv}
+
+    def cpu(self, budget_s):
+        import numpy as np
+        import oracle
+        import torch
+        torch.cuda.synchronize()
+        self.state.copy_(self.state0)
+        self.op()
+        torch.cuda.synchronize()
+        q, k, beta, decay = (host_f32(t) for t in (self.q, self.k, self.beta, self.decay))
+        v = host_u16(self.v)
+        s0 = host_f32(self.state0)
+        gpu_out = oracle.f16_to_f32(host_u16(self.out))
+        gpu_state = host_f32(self.state)
+        thr = cpu_threads()
+        want, wstate = oracle.delta_recurrent_f32(q, k, v, beta, decay, s0, thr)
+        err = float(np.max(np.abs(gpu_out - oracle.f16_to_f32(want))))
+        serr = float(np.max(np.abs(gpu_state - wstate)) / max(1e-30, np.max(np.abs(wstate))))
+        sec, runs = time_cpu(lambda: oracle.delta_recurrent_f32(q, k, v, beta, decay, s0, thr),
+                             budget_s)
+        return {"value": sec * 1e6, "unit": "µs/layer", "cores": thr, "kind": "port",
+                "sample": f"the full {self.T}-token DeltaUpdate, {runs} runs, fp32 "
+                          "recurrence (oracle orc_delta_recurrent_f32)",
+                "gpu_vs_cpu_max_abs": err, "gpu_vs_cpu_state_rel": serr}
+
+
+class HybridDecode(Workload):
+    """DeltaNet decode step + KvAppend + GQA decode at 32K context,
+    32 positions per layer; `layers` independent layer pairs rotate so that
+    the 134 MB of K/V a decode reads come from HBM."""
+    bound = "hbm"
+    dominant = "gqaDecodeSplitK"
+
+    def __init__(self, dev, past=32768, positions=32, layers=4, seed=5,
+                 hq=16, hkv=4, d=256, hk=16, dk=128, hv=32, dv=128):
+        import torch
+        from llminfer_amd import ops
+        self.P0, self.n, self.L = past, positions, layers
+        self.cap = past + positions
+        self.hq, self.hkv, self.d = hq, hkv, d
+        self.dshape = (hk, dk, hv, dv)
+        self.name = f"hybrid_decode_{past // 1024}k"
+        g = torch.Generator(device=dev).manual_seed(seed)
+        self.kc = [_randn16(g, (self.cap, hkv, d), dev) for _ in range(layers)]
+        self.vc = [_randn16(g, (self.cap, hkv, d), dev) for _ in range(layers)]
+        self.state = [torch.randn((hv, dk, dv), generator=g, device=dev) * 0.1
+                      for _ in range(layers)]
+        self.inp = []
+        for j in range(positions):
+            dq, dkk, dvv, b, a = _delta_inputs(g, dev, 1, hk, dk, hv, dv)
+            self.inp.append(dict(dq=dq, dk=dkk, dv=dvv, beta=b, decay=a,
+                                 q=_randn16(g, (1, hq, d), dev),
+                                 kn=_randn16(g, (1, hkv, d), dev),
+                                 vn=_randn16(g, (1, hkv, d), dev)))
+        self.dout = torch.empty((1, hv * dv), dtype=torch.float16, device=dev)
+        self.gout = torch.empty((1, hq, d), dtype=torch.float16, device=dev)
+        self.ops = {}
+        for l in range(layers):
+            for j in range(positions):
+                x = self.inp[j]
+                P = past + j
+                self.ops[l, j] = (
+                    ops.bind_delta_update(x["dq"], x["dk"], x["dv"], x["beta"], x["decay"],
+                                          self.state[l], self.dout),
+                    ops.bind_kv_append(x["kn"], x["vn"], self.kc[l], self.vc[l], P),
+                    ops.bind_causal_gqa(x["q"], self.kc[l], self.vc[l], self.gout, P))
+        assert self.ops[0, 0][2].what == self.dominant
+        self.tokens = 1
+
+    def pos(self, i):
+        return i % self.L, (i // self.L) % self.n
+
+    def launch(self, i, marks):
+        delta, app, att = self.ops[self.pos(i)]
+        m = marks.get("delta")
+        if m:
+            m[0].record()
+        delta()
+        if m:
+            m[1].record()
+        app()
+        m = marks.get("gqa")
+        if m:
+            m[0].record()
+        att()
+        if m:
+            m[1].record()
+
+    def work(self, i):
+        _, j = self.pos(i)
+        return gqa_bytes(1, self.P0 + j, self.hq, self.hkv, self.d)
+
+    def config(self):
+        return {"workload": self.name, "past": self.P0, "positions": self.n,
+                "layers": self.L, "capacity": self.cap}
+
+    def cpu(self, budget_s):
+        import numpy as np
+        import oracle
+        import torch
+        hk, dk, hv, dv = self.dshape
+        thr = cpu_threads()
+        torch.cuda.synchronize()
+        kc, vc = host_u16(self.kc[0]), host_u16(self.vc[0])
+        st = host_f32(self.state[0])
+        xs = [{k: (host_u16(v) if v.dtype == torch.float16 else host_f32(v))
+               for k, v in x.items()} for x in self.inp]
+
+        def run(n):
+            s = st
+            for j in range(n):
+                x = xs[j]
+                _, s = oracle.delta_recurrent_f32(x["dq"], x["dk"], x["dv"], x["beta"],
+                                                  x["decay"], s, thr)
+                oracle.kv_append(x["kn"], kc, self.P0 + j)
+                oracle.kv_append(x["vn"], vc, self.P0 + j)
+                oracle.gqa_f32(x["q"], kc, vc, self.P0 + j, thr)
+        sec, runs = time_cpu(lambda: run(self.n), budget_s)
+        return {"value": sec / self.n * 1e6, "unit": "µs/layer-pair", "cores": thr,
+                "kind": "port",
+                "sample": f"{self.n} hybrid steps (DeltaNet decode + KvAppend + GQA decode "
+                          f"at P={self.P0}..{self.P0 + self.n - 1}) of one layer pair, "
+                          f"{runs} runs"}
+
+
+# ---------------------------------------------------------------- timing
+
+def sleep_cycles_per_ms() -> float:
+    import torch
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda._sleep(1000)  # load the kernel
+    torch.cuda.synchronize()
+    n = 1 << 22
+    a.record()
+    torch.cuda._sleep(n)
+    b.record()
+    b.synchronize()
+    ms = a.elapsed_time(b)
+    return n / max(ms, 1e-3)
+
+
+def run_timed(w: Workload, steps: int, warmup: int, labels: list[str], cyc_per_ms: float):
+    """Returns (ms_per_step, {label: [kernel ms per launch]}, host enqueue ms)."""
+    import torch
+    for i in range(warmup):
+        w.launch(i, {})
+    torch.cuda.synchronize()
+    # Host enqueue cost per step, to size the hold-off spin.
+    t0 = time.perf_counter()
+    for i in range(min(8, max(1, warmup))):
+        w.launch(i, {})
+    host_ms = (time.perf_counter() - t0) * 1e3 / min(8, max(1, warmup))
+    torch.cuda.synchronize()
+
+    ev = {l: [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+              for _ in range(steps)] for l in labels}
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    hold_ms = min(4000.0, 2.0 + 1.5 * host_ms * steps * (1 + 0.5 * len(labels)))
+    torch.cuda.synchronize()
+    torch.cuda._sleep(int(hold_ms * cyc_per_ms))
+    start.record()
+    for i in range(steps):
+        w.launch(warmup + i, {l: ev[l][i] for l in labels})
+    end.record()
+    torch.cuda.synchronize()
+    total = start.elapsed_time(end)
+    per = {l: [a.elapsed_time(b) for a, b in ev[l]] for l in labels}
+    return total / steps, per, host_ms
+
+
+def roofline(w: Workload, kern_ms: list[float], warmup: int, traffic) -> dict:
+    import statistics
+    avg_s = statistics.fmean(kern_ms) * 1e-3
+    work = statistics.fmean(w.work(warmup + i) for i in range(len(kern_ms)))
+    if w.bound == "hbm":
+        achieved, peak, unit = work / avg_s / 1e9, HBM_PEAK_GBS, "GB/s"
+    else:
+        achieved, peak, unit = work / avg_s / 1e12, MFMA_F16_PEAK_TFS, "TFLOP/s"
+    return {"bound": w.bound, "achieved": round(achieved, 2), "peak": peak, "unit": unit,
+            "frac": round(achieved / peak, 4), "traffic": traffic,
+            "kernel": w.dominant, "kernel_us_avg": round(avg_s * 1e6, 3),
+            "kernel_us_p50": round(sorted(kern_ms)[len(kern_ms) // 2] * 1e3, 3),
+            "work_per_launch": int(work),
+            "work_unit": "bytes" if w.bound == "hbm" else "flop"}
+
+
+def load_traffic(workload: str):
+    """HBM bytes per launch from the committed rocprofv3 --pmc summary."""
+    path = ROOT / "profiles" / "traffic.json"
+    try:
+        data = json.loads(path.read_text())
+    except (OSError, ValueError):
+        return None
+    entry = data.get(workload)
+    return entry.get("bytes_per_launch") if isinstance(entry, dict) else None
+
+
+# ------------------------------------------------------------------ main
+
+def main(argv=None) -> int:
+    ap = argparse.ArgumentParser(description="llminfer attention hot path benchmark")
+    ap.add_argument("--gpus", type=int, default=int(os.environ.get("WORLD_SIZE", "1")))
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--only-headline", action="store_true",
+                    help="skip the other BASELINE configurations")
+    ap.add_argument("--cpu-seconds", type=float, default=8.0,
+                    help="CPU-baseline time budget of the headline (others get half)")
+    ap.add_argument("--no-cpu", action="store_true", help="skip every CPU baseline")
+    args = ap.parse_args(argv)
+
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only: --gpus {args.gpus} is not supported "
+              "(this build's hot path runs on a single MI355X; see the sharding notes "
+              "in the design document)", file=sys.stderr)
+        return 2
+
+    import torch
+    from llminfer_amd import _lib
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU (no HIP device visible)", file=sys.stderr)
+        return 1
+    _lib.load()  # raises if the HIP library is missing; there is no fallback
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    cyc = sleep_cycles_per_ms()
+    log(f"device {torch.cuda.get_device_name(dev)}; spin {cyc:.0f} cycles/ms")
+
+    # ---- headline: configs[1]
+    w = GqaDecode(dev)
+    log(f"headline {w.name}: warmup {args.warmup}, steps {args.steps}")
+    ms, per, host_ms = run_timed(w, args.steps, args.warmup, ["gqa"], cyc)
+    rl = roofline(w, per["gqa"], args.warmup, load_traffic(w.name))
+    log(f"headline {ms * 1e3:.2f} us/step, kernel {rl['kernel_us_avg']} us, "
+        f"{rl['achieved']} GB/s ({rl['frac']:.1%})")
+    result = {
+        "metric": METRIC, "value": round(ms * 1e3, 3), "unit": "µs/layer",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms, 6), "higher_is_better": False, "scaling": "weak",
+        "vs_baseline": None, "dtype": "f16", "data": "synthetic",
+        "config": w.config(), "tokens_per_s": round(1e3 / ms, 1),
+        "host_enqueue_ms_per_step": round(host_ms, 4),
+        "roofline": rl,
+    }
+    if not args.no_cpu:
+        log("cpu baseline (headline)")
+        result["cpu_baseline"] = w.cpu(args.cpu_seconds)
+    del w
+    torch.cuda.empty_cache()
+
+    # ---- the other configurations
+    if not args.only_headline:
+        extra = {}
+        steps = max(10, min(args.steps, 50))
+        builders = [
+            ("cfg0_gqa_prefill_128", lambda: GqaPrefill(dev, 128, 0, 128, seed=1), ["gqa"]),
+            ("cfg2_gqa_chunked_prefill", lambda: GqaPrefill(dev, 2048, 2048, 4096, seed=3),
+             ["gqa"]),
+            ("cfg3_delta_prefill_1024", lambda: DeltaPrefill(dev), ["delta"]),
+            ("cfg4_hybrid_decode_32k", lambda: HybridDecode(dev), ["gqa", "delta"]),
+        ]
+        for key, make, labels in builders:
+            x = make()
+            log(f"{key}: {x.name}")
+            n = steps if key != "cfg4_hybrid_decode_32k" else max(steps, 128)
+            ms_x, per_x, _ = run_timed(x, n, min(args.warmup, 10), labels, cyc)
+            entry = {"config": x.config(), "us_per_step": round(ms_x * 1e3, 3),
+                     "tokens_per_s": round(x.tokens * 1e3 / ms_x, 1), "steps": n,
+                     "roofline": roofline(x, per_x[labels[0]], min(args.warmup, 10),
+                                          load_traffic(x.name))}
+            if x.bound == "mfma":
+                entry["hbm_frac"] = None
+            if isinstance(x, DeltaPrefill):
+                kern_s = entry["roofline"]["kernel_us_avg"] * 1e-6
+                entry["mfma_frac_recurrent_flops"] = round(
+                    delta_flops(x.T, x.hv, x.dk, x.dv) / kern_s / 1e12 / MFMA_F16_PEAK_TFS, 5)
+            if isinstance(x, HybridDecode):
+                import statistics
+                entry["delta_kernel_us_avg"] = round(statistics.fmean(per_x["delta"]) * 1e3, 3)
+                hk, dk, hv, dv = x.dshape
+                entry["delta_hbm_frac"] = round(
+                    delta_bytes(1, hk, dk, hv, dv) / (entry["delta_kernel_us_avg"] * 1e-6)
+                    / 1e9 / HBM_PEAK_GBS, 4)
+            if not args.no_cpu:
+                entry["cpu_baseline"] = x.cpu(args.cpu_seconds / 2)
+            log(f"{key}: {entry['us_per_step']} us/step, kernel "
+                f"{entry['roofline']['kernel_us_avg']} us, frac {entry['roofline']['frac']}")
+            extra[key] = entry
+            del x
+            torch.cuda.empty_cache()
+        result["configs"] = extra
+
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

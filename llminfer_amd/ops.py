@@ -141,6 +141,84 @@ def delta_update(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, beta: torch.
     return out
 
 
+class Bound:
+    """One C-ABI call with every argument converted once, for hot loops.
+
+    `bind_*` validate like the functions above and return a Bound whose
+    call() re-issues the launch on the same buffers with no per-call host
+    work beyond the ctypes call itself. Buffers must stay alive and keep
+    their shapes while the Bound is used.
+    """
+
+    def __init__(self, fn, args, what: str):
+        self._fn = fn
+        self._args = args
+        self.what = what
+
+    def __call__(self) -> None:
+        st = self._fn(*self._args)
+        if st != _lib.OK:
+            _lib.check(st)
+
+
+def bind_kv_append(k: torch.Tensor, v: torch.Tensor, k_cache: torch.Tensor,
+                   v_cache: torch.Tensor, past: int) -> Bound:
+    for t, n in ((k, "k"), (v, "v"), (k_cache, "k_cache"), (v_cache, "v_cache")):
+        _require(t, torch.float16, n)
+    T, hkv, d = k.shape
+    if v.shape != k.shape or k_cache.shape != v_cache.shape or \
+            k_cache.shape[1:] != k.shape[1:] or past + T > k_cache.shape[0]:
+        raise ValueError("KvAppend operands do not match the cache")
+    lib = _lib.load()
+    args = (_ptr(k), _ptr(v), _ptr(k_cache), _ptr(v_cache),
+            _lib.CacheParams(T * hkv * d, past * hkv * d), _stream())
+    return Bound(lib.llmi_hip_kv_append, args, "kvAppend")
+
+
+def bind_causal_gqa(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                    out: torch.Tensor, past: int) -> Bound:
+    for t, n in ((q, "q"), (k_cache, "k_cache"), (v_cache, "v_cache"), (out, "out")):
+        _require(t, torch.float16, n)
+    if q.dim() != 3 or k_cache.shape != v_cache.shape or out.shape != q.shape or \
+            q.shape[2] != k_cache.shape[2] or past + q.shape[0] > k_cache.shape[0]:
+        raise ValueError("CausalGqa operands do not match the cache")
+    lib = _lib.load()
+    p = gqa_params(q, k_cache, past)
+    need = lib.llmi_hip_gqa_workspace_bytes(p)
+    ws = workspace(need, q.device) if need else None
+    args = (_ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(out), p, _ptr(ws),
+            ws.numel() if ws is not None else 0, _stream())
+    b = Bound(lib.llmi_hip_causal_gqa, args, kernel_names(_lib.OP_CAUSAL_GQA, p)[0])
+    b._keep = ws
+    return b
+
+
+def bind_delta_update(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                      beta: torch.Tensor, decay: torch.Tensor, state: torch.Tensor,
+                      out: torch.Tensor) -> Bound:
+    for t, n, dt in ((q, "q", torch.float32), (k, "k", torch.float32),
+                     (v, "v", torch.float16), (beta, "beta", torch.float32),
+                     (decay, "decay", torch.float32), (state, "state", torch.float32),
+                     (out, "out", torch.float16)):
+        _require(t, dt, n)
+    T = q.shape[0]
+    hv, dk, dv = state.shape
+    if q.dim() != 2 or k.shape != q.shape or q.shape[1] % dk or \
+            hv % (q.shape[1] // dk) or v.shape != (T, hv * dv) or \
+            beta.shape != (T, hv) or decay.shape != beta.shape or out.shape != v.shape:
+        raise ValueError("DeltaUpdate operand shapes do not match its recurrent state")
+    lib = _lib.load()
+    p = delta_params(q, v, state)
+    need = lib.llmi_hip_delta_workspace_bytes(p)
+    ws = workspace(need, q.device) if need else None
+    args = (_ptr(q), _ptr(k), _ptr(v), _ptr(beta), _ptr(decay), _ptr(state), _ptr(out),
+            p, _ptr(ws), ws.numel() if ws is not None else 0, _stream())
+    names = kernel_names(_lib.OP_DELTA_UPDATE, p)
+    b = Bound(lib.llmi_hip_delta_update, args, "+".join(names))
+    b._keep = ws
+    return b
+
+
 def kernel_names(op: int, params) -> list[str]:
     lib = _lib.load()
     ref = C.byref(params)

@@ -1,0 +1,136 @@
+"""The C-ABI library loads and exports what include/*.h declares; host-side
+validation and plan records work without a GPU (no kernel is launched: every
+call below is rejected, or only sizes/names something, before any launch)."""
+import ctypes as C
+import re
+from pathlib import Path
+
+import pytest
+
+from llminfer_amd import _lib
+
+ROOT = Path(__file__).resolve().parent.parent
+
+
+def declared_functions() -> set[str]:
+    names = set()
+    for h in (ROOT / "include").glob("*.h"):
+        text = re.sub(r"/\*.*?\*/", "", h.read_text(), flags=re.S)
+        for m in re.finditer(r"LLMI_HIP_API\s+[^;{]*?\b(llmi_hip_\w+)\s*\(", text):
+            names.add(m.group(1))
+    return names
+
+
+def test_header_declares_the_boundary():
+    names = declared_functions()
+    for n in ("llmi_hip_kv_append", "llmi_hip_causal_gqa", "llmi_hip_delta_update",
+              "llmi_hip_session_step", "llmi_hip_kernel_name"):
+        assert n in names
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    missing = [n for n in sorted(declared_functions()) if not hasattr(lib, n)]
+    assert not missing, f"declared but not exported: {missing}"
+
+
+def test_bindings_cover_every_declared_symbol():
+    assert declared_functions() == set(_lib.SIGNATURES)
+
+
+def test_param_structs_match_reference_layout():
+    # All fields 32-bit unsigned, in the reference's order
+    # (ReferenceParams.h:49-55, GraphParams.h:50-52).
+    assert C.sizeof(_lib.CacheParams) == 8
+    assert C.sizeof(_lib.GqaParams) == 20
+    assert C.sizeof(_lib.GraphDeltaParams) == 20
+    assert [f[0] for f in _lib.GqaParams._fields_] == \
+        ["tokens", "queryHeads", "kvHeads", "headDim", "past"]
+    assert [f[0] for f in _lib.GraphDeltaParams._fields_] == \
+        ["tokens", "keyHeads", "keyDim", "valueHeads", "valueDim"]
+
+
+def test_invalid_gqa_rejected_before_launch():
+    lib = _lib.load()
+    bad = [_lib.GqaParams(0, 16, 4, 256, 0),     # no tokens
+           _lib.GqaParams(1, 15, 4, 256, 0),     # Hq % Hkv != 0
+           _lib.GqaParams(1, 16, 0, 256, 0),
+           _lib.GqaParams(1 << 20, 1 << 10, 4, 256, 0)]  # beyond 32-bit indices
+    for p in bad:
+        st = lib.llmi_hip_causal_gqa(1, 1, 1, 1, p, None, 0, None)
+        assert st == _lib.INVALID_ARGUMENT, p
+        assert lib.llmi_hip_last_error()
+        assert lib.llmi_hip_gqa_workspace_bytes(p) == 0
+        assert lib.llmi_hip_dispatch_count(_lib.OP_CAUSAL_GQA, C.byref(p)) == 0
+    # null buffers
+    p = _lib.GqaParams(1, 16, 4, 256, 10)
+    assert lib.llmi_hip_causal_gqa(None, 1, 1, 1, p, None, 0, None) == _lib.INVALID_ARGUMENT
+
+
+def test_decode_requires_workspace():
+    lib = _lib.load()
+    p = _lib.GqaParams(1, 16, 4, 256, 4096)
+    need = lib.llmi_hip_gqa_workspace_bytes(p)
+    assert need > 4096
+    st = lib.llmi_hip_causal_gqa(1, 1, 1, 1, p, None, 0, None)
+    assert st == _lib.WORKSPACE
+    st = lib.llmi_hip_causal_gqa(1, 1, 1, 1, p, 1, need - 1, None)
+    assert st == _lib.WORKSPACE
+
+
+def test_invalid_delta_rejected_before_launch():
+    lib = _lib.load()
+    for p in (_lib.GraphDeltaParams(0, 16, 128, 32, 128),
+              _lib.GraphDeltaParams(4, 16, 128, 24, 128),   # Hv % Hk != 0
+              _lib.GraphDeltaParams(4, 0, 128, 32, 128)):
+        st = lib.llmi_hip_delta_update(1, 1, 1, 1, 1, 1, 1, p, None, 0, None)
+        assert st == _lib.INVALID_ARGUMENT
+
+
+def test_append_rejects_index_overflow():
+    lib = _lib.load()
+    st = lib.llmi_hip_kv_append(1, 1, 1, 1, _lib.CacheParams(16, 0xFFFFFFF8), None)
+    assert st == _lib.INVALID_ARGUMENT
+    assert lib.llmi_hip_cache_append(None, 1, _lib.CacheParams(4, 0), None) == \
+        _lib.INVALID_ARGUMENT
+
+
+@pytest.mark.parametrize("T,P,names", [
+    (1, 4096, ["gqaDecodeSplitK"]),
+    (1, 0, ["gqaDecodeSplitK"]),
+    (2, 0, ["gqaPrefillMfma"]),
+    (2048, 2048, ["gqaPrefillMfma"]),
+])
+def test_plan_records_gqa(T, P, names):
+    from llminfer_amd import ops
+    assert ops.kernel_names(_lib.OP_CAUSAL_GQA, _lib.GqaParams(T, 16, 4, 256, P)) == names
+
+
+def test_plan_records_generic_shapes():
+    from llminfer_amd import ops
+    # The reference kernel test's head_dim 12 (FlashAttentionTest.mm:108).
+    assert ops.kernel_names(_lib.OP_CAUSAL_GQA, _lib.GqaParams(19, 4, 2, 12, 0)) == \
+        ["gqaGeneric"]
+    assert ops.kernel_names(_lib.OP_DELTA_UPDATE, _lib.GraphDeltaParams(3, 2, 7, 4, 5)) == \
+        ["deltaGeneric"]
+    assert ops.kernel_names(_lib.OP_KV_APPEND, _lib.CacheParams(8, 0)) == ["kvAppend"]
+
+
+def test_status_strings():
+    lib = _lib.load()
+    for st in range(6):
+        assert lib.llmi_hip_status_string(st)
+    assert lib.llmi_hip_status_string(99) == b"unknown status"
+    assert b"gfx950" in lib.llmi_hip_build_info()
+
+
+def test_session_open_validates_config():
+    lib = _lib.load()
+    h = C.c_void_p()
+    bad = _lib.SessionConfig(0, 16, 4, 256, 16, 128, 32, 128)
+    assert lib.llmi_hip_session_open(C.byref(bad), None, C.byref(h)) == _lib.INVALID_ARGUMENT
+    bad = _lib.SessionConfig(64, 16, 5, 256, 16, 128, 32, 128)
+    assert lib.llmi_hip_session_open(C.byref(bad), None, C.byref(h)) == _lib.INVALID_ARGUMENT
+    assert h.value is None
+    assert lib.llmi_hip_session_step(None, 1, *([None] * 10), None, 0, None) == \
+        _lib.INVALID_ARGUMENT
