@@ -7,8 +7,9 @@
 Prints ONE JSON line. The headline workload is the GQA single-token decode
 of the reference's decode path (KvAppend + CausalGqa, T=1, 4096 past rows,
 capacity 8192, 16 query / 4 KV heads, head_dim 256, fp16): one "step" is one
-attention layer's decode -- the KvAppend launch plus the split-K CausalGqa
-launch -- over inputs already resident in HBM. `value` is GPU microseconds
+attention layer's decode -- KvAppend + CausalGqa, which the backend runs as
+one split-K launch that also appends the new row -- over inputs already
+resident in HBM. `value` is GPU microseconds
 per layer step (time-like, lower is better). The K/V caches rotate over 32
 independent sets (1.07 GB) so that every step reads its 16.8 MB of K/V from
 HBM rather than from the 256 MB Infinity Cache.
@@ -20,10 +21,10 @@ bracket exactly the K steps (ms_per_step), and an event pair on the same
 stream brackets every launch of the dominant kernel (roofline.achieved).
 
 `roofline`: algorithmic bytes of one decode launch (K and V rows [0, P+1)
-plus q and out, the reference cost model's traffic for CausalGqa,
-lib/GraphIR/Cost.cpp:56-94) / its average event-timed duration, against
-MI355X's 8 TB/s. `traffic` is the HBM bytes per launch from rocprofv3
-FETCH_SIZE + WRITE_SIZE, read from profiles/traffic.json when that summary
+plus q and out -- the reference cost model's traffic for CausalGqa,
+lib/GraphIR/Cost.cpp:56-94 -- plus the 4 KB KvAppend cache write the launch
+performs) / its average event-timed duration, against MI355X's 8 TB/s.
+`traffic` is the HBM bytes per launch from rocprofv3 FETCH_SIZE + WRITE_SIZE, read from profiles/traffic.json when that summary
 exists for this kernel and workload.
 
 `cpu_baseline`: the C oracle (oracle/liboracle.so, the same CPU restatement
@@ -69,6 +70,12 @@ def gqa_flops(T: int, P: int, hq: int, d: int) -> int:
 def gqa_bytes(T: int, P: int, hq: int, hkv: int, d: int) -> int:
     """q + visible K and V rows + out, fp16 (Cost.cpp:56-94 traffic)."""
     return 2 * (2 * T * hq * d + 2 * (P + T) * hkv * d)
+
+
+def append_bytes(T: int, hkv: int, d: int) -> int:
+    """KvAppend's cache write (its reads are the new K/V rows the attention
+    reads anyway)."""
+    return 2 * T * hkv * d * 2
 
 
 def delta_flops(T: int, hv: int, dk: int, dv: int) -> int:
@@ -169,15 +176,14 @@ class GqaDecode(Workload):
         self.kn = _randn16(g, (1, hkv, d), dev)
         self.vn = _randn16(g, (1, hkv, d), dev)
         self.out = torch.empty_like(self.q)
-        self.app = [ops.bind_kv_append(self.kn, self.vn, self.kc[s], self.vc[s], past)
+        # KvAppend + CausalGqa as one fused launch (the append rides along).
+        self.att = [ops.bind_kv_append_causal_gqa(self.q, self.kn, self.vn, self.kc[s],
+                                                  self.vc[s], self.out, past)
                     for s in range(sets)]
-        self.att = [ops.bind_causal_gqa(self.q, self.kc[s], self.vc[s], self.out, past)
-                    for s in range(sets)]
-        assert self.att[0].what == self.dominant, self.att[0].what
+        assert self.att[0].what.split("+")[0] == self.dominant, self.att[0].what
 
     def launch(self, i, marks):
         s = i % self.sets
-        self.app[s]()
         m = marks.get("gqa")
         if m:
             m[0].record()
@@ -186,7 +192,7 @@ class GqaDecode(Workload):
             m[1].record()
 
     def work(self, i):
-        return gqa_bytes(1, self.P, self.hq, self.hkv, self.d)
+        return gqa_bytes(1, self.P, self.hq, self.hkv, self.d) + append_bytes(1, self.hkv, self.d)
 
     def config(self):
         return {"workload": self.name, "tokens": 1, "past": self.P, "capacity": self.cap,
@@ -204,7 +210,6 @@ class GqaDecode(Workload):
         kc, vc, q = host_u16(self.kc[s]), host_u16(self.vc[s]), host_u16(self.q)
         kn, vn = host_u16(self.kn), host_u16(self.vn)
         # Re-run the GPU step on set 0 so `out` belongs to these inputs.
-        self.app[s]()
         self.att[s]()
         torch.cuda.synchronize()
         gpu_out = oracle.f16_to_f32(host_u16(self.out))
@@ -405,23 +410,22 @@ class HybridDecode(Workload):
                 self.ops[l, j] = (
                     ops.bind_delta_update(x["dq"], x["dk"], x["dv"], x["beta"], x["decay"],
                                           self.state[l], self.dout),
-                    ops.bind_kv_append(x["kn"], x["vn"], self.kc[l], self.vc[l], P),
-                    ops.bind_causal_gqa(x["q"], self.kc[l], self.vc[l], self.gout, P))
-        assert self.ops[0, 0][2].what == self.dominant
+                    ops.bind_kv_append_causal_gqa(x["q"], x["kn"], x["vn"], self.kc[l],
+                                                  self.vc[l], self.gout, P))
+        assert self.ops[0, 0][1].what.split("+")[0] == self.dominant
         self.tokens = 1
 
     def pos(self, i):
         return i % self.L, (i // self.L) % self.n
 
     def launch(self, i, marks):
-        delta, app, att = self.ops[self.pos(i)]
+        delta, att = self.ops[self.pos(i)]
         m = marks.get("delta")
         if m:
             m[0].record()
         delta()
         if m:
             m[1].record()
-        app()
         m = marks.get("gqa")
         if m:
             m[0].record()
@@ -431,7 +435,8 @@ class HybridDecode(Workload):
 
     def work(self, i):
         _, j = self.pos(i)
-        return gqa_bytes(1, self.P0 + j, self.hq, self.hkv, self.d)
+        return gqa_bytes(1, self.P0 + j, self.hq, self.hkv, self.d) + \
+            append_bytes(1, self.hkv, self.d)
 
     def config(self):
         return {"workload": self.name, "past": self.P0, "positions": self.n,
@@ -483,32 +488,47 @@ def sleep_cycles_per_ms() -> float:
 
 
 def run_timed(w: Workload, steps: int, warmup: int, labels: list[str], cyc_per_ms: float):
-    """Returns (ms_per_step, {label: [kernel ms per launch]}, host enqueue ms)."""
+    """Returns (ms_per_step, {label: [kernel ms per launch]}, host enqueue ms/step).
+
+    A spin kernel holds the GPU while the host enqueues the K steps (with
+    their event records), so the events time the GPU, not Python. If the
+    host still fell behind the GPU (its enqueue outlasted the hold), the
+    measurement is repeated with a longer hold.
+    """
     import torch
     for i in range(warmup):
         w.launch(i, {})
     torch.cuda.synchronize()
-    # Host enqueue cost per step, to size the hold-off spin.
+    # Host enqueue cost per step, event records included.
+    probe = {l: (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+             for l in labels}
+    n = min(8, max(1, warmup))
     t0 = time.perf_counter()
-    for i in range(min(8, max(1, warmup))):
-        w.launch(i, {})
-    host_ms = (time.perf_counter() - t0) * 1e3 / min(8, max(1, warmup))
+    for i in range(n):
+        w.launch(i, probe)
+    host_ms = (time.perf_counter() - t0) * 1e3 / n
     torch.cuda.synchronize()
 
-    ev = {l: [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-              for _ in range(steps)] for l in labels}
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    hold_ms = min(4000.0, 2.0 + 1.5 * host_ms * steps * (1 + 0.5 * len(labels)))
-    torch.cuda.synchronize()
-    torch.cuda._sleep(int(hold_ms * cyc_per_ms))
-    start.record()
-    for i in range(steps):
-        w.launch(warmup + i, {l: ev[l][i] for l in labels})
-    end.record()
-    torch.cuda.synchronize()
+    hold_ms = 10.0 + 3.0 * host_ms * steps
+    for _attempt in range(4):
+        ev = {l: [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+                  for _ in range(steps)] for l in labels}
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        torch.cuda._sleep(int(min(hold_ms, 8000.0) * cyc_per_ms))
+        t0 = time.perf_counter()
+        start.record()
+        for i in range(steps):
+            w.launch(warmup + i, {l: ev[l][i] for l in labels})
+        end.record()
+        enq_ms = (time.perf_counter() - t0) * 1e3
+        torch.cuda.synchronize()
+        if enq_ms < 0.8 * hold_ms or hold_ms >= 8000.0:
+            break
+        hold_ms = 2.0 * enq_ms + 10.0
     total = start.elapsed_time(end)
     per = {l: [a.elapsed_time(b) for a, b in ev[l]] for l in labels}
-    return total / steps, per, host_ms
+    return total / steps, per, enq_ms / steps
 
 
 def roofline(w: Workload, kern_ms: list[float], warmup: int, traffic) -> dict:

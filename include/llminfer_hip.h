@@ -70,7 +70,8 @@ enum llmi_hip_status {
 enum llmi_hip_op {
   LLMI_HIP_OP_KV_APPEND = 0,
   LLMI_HIP_OP_CAUSAL_GQA = 1,
-  LLMI_HIP_OP_DELTA_UPDATE = 2
+  LLMI_HIP_OP_DELTA_UPDATE = 2,
+  LLMI_HIP_OP_KV_APPEND_CAUSAL_GQA = 3 /* the fused pair; params: GqaParams */
 };
 
 /* ---------------------------------------------------------------- KvAppend
@@ -99,14 +100,29 @@ LLMI_HIP_API int llmi_hip_kv_append(const uint16_t *k_src, const uint16_t *v_src
  *   out      [T][Hq][d] fp16
  *   O[t,h] = softmax_j(q[t,h] . k[j,h/(Hq/Hkv)] / sqrt(d)) v[j,...], j <= P+t
  * Softmax and accumulation are fp32; the output is rounded to fp16 once.
- * `workspace` must hold llmi_hip_gqa_workspace_bytes(p) bytes and be
- * prepared once with llmi_hip_workspace_init (the kernels leave it ready
- * for the next call). */
+ * `workspace` must hold llmi_hip_gqa_workspace_bytes(p) bytes (0 = none
+ * needed): the split-K decode's per-split partials, written and read
+ * within the call, so its contents between calls do not matter. */
 LLMI_HIP_API int llmi_hip_causal_gqa(const uint16_t *q, const uint16_t *k_cache,
                         const uint16_t *v_cache, uint16_t *out, GqaParams p,
                         void *workspace, size_t workspace_bytes, void *stream);
 
 LLMI_HIP_API size_t llmi_hip_gqa_workspace_bytes(GqaParams p);
+
+/* KvAppend followed by CausalGqa on the same step, in one call: the T new
+ * rows k_new/v_new [T][Hkv][d] are written to cache rows [P, P+T) exactly as
+ * llmi_hip_kv_append would, and the attention sees them -- the effect of the
+ * two ops in graph order (lib/GraphIR/Graph.cpp:248-279; the reference
+ * lowers them as two dispatch groups, MetalExecutionPlan.cpp:516-548). For
+ * T == 1 it is one launch (the decode kernel reads the new row from
+ * k_new/v_new and stores it while it attends); for T > 1 it is the append
+ * launch followed by the prefill launch. Workspace as for
+ * llmi_hip_causal_gqa (llmi_hip_gqa_workspace_bytes of the same params). */
+LLMI_HIP_API int llmi_hip_kv_append_causal_gqa(const uint16_t *q, const uint16_t *k_new,
+                                  const uint16_t *v_new, uint16_t *k_cache,
+                                  uint16_t *v_cache, uint16_t *out, GqaParams p,
+                                  void *workspace, size_t workspace_bytes,
+                                  void *stream);
 
 /* ------------------------------------------------------------- DeltaUpdate
  * Replaces graphDeltaUpdate (Graph.metal:146-170 with updateDeltaColumn,
@@ -130,7 +146,9 @@ LLMI_HIP_API size_t llmi_hip_delta_workspace_bytes(GraphDeltaParams p);
 
 /* ----------------------------------------------------------------- helpers */
 
-/* Zero a workspace before its first use (enqueued on `stream`). */
+/* Zero a workspace (enqueued on `stream`). No kernel of this library needs
+ * a zeroed workspace; provided for callers that want deterministic
+ * contents. */
 LLMI_HIP_API int llmi_hip_workspace_init(void *workspace, size_t bytes, void *stream);
 
 /* Plan-record support (MetalSession.h:11-16, tools/run/Main.cpp:244-255):
@@ -163,10 +181,14 @@ typedef struct llmi_hip_session_config {
   unsigned keyHeads, keyDim, valueHeads, valueDim;
 } llmi_hip_session_config;
 
-/* A plan record: MetalDispatchInfo{opIndex, kernel} (MetalSession.h:11-16). */
+/* A plan record: MetalDispatchInfo{opIndex, kernel, fusedOpIndex}
+ * (MetalSession.h:11-16). fused_op_index is LLMI_HIP_NO_FUSED_OP unless
+ * the launch also performs another op of the step (the fused KvAppend). */
+#define LLMI_HIP_NO_FUSED_OP ((size_t)-1)
 typedef struct llmi_hip_dispatch {
   size_t op_index;
   const char *kernel;
+  size_t fused_op_index;
 } llmi_hip_dispatch;
 
 LLMI_HIP_API int llmi_hip_session_open(const llmi_hip_session_config *config,
@@ -187,8 +209,10 @@ LLMI_HIP_API float *llmi_hip_session_recurrent_state(llmi_hip_session *s);
  * device pointers with the op contracts above; outputs are written to
  * delta_out [T][Hv*dv] and gqa_out [T][Hq][d]. Validation failures return
  * nonzero before any launch. If `records` is non-NULL, up to `cap` plan
- * records are written and *count receives the total. The step waits for
- * the GPU once at the end (one host sync per step, MetalContext.mm:141-151). */
+ * records are written and *count receives the total; for T == 1 KvAppend
+ * runs inside the attention launch, recorded as {op 2, fused_op_index 1}.
+ * The step waits for the GPU once at the end (one host sync per step,
+ * MetalContext.mm:141-151). */
 LLMI_HIP_API int llmi_hip_session_step(llmi_hip_session *s, unsigned tokens,
                           const float *dq, const float *dk, const uint16_t *dv,
                           const float *beta, const float *decay,

@@ -21,6 +21,7 @@ NO_DEVICE = 5
 OP_KV_APPEND = 0
 OP_CAUSAL_GQA = 1
 OP_DELTA_UPDATE = 2
+OP_KV_APPEND_CAUSAL_GQA = 3
 
 
 class CacheParams(C.Structure):
@@ -44,8 +45,12 @@ class SessionConfig(C.Structure):
                 ("valueHeads", C.c_uint), ("valueDim", C.c_uint)]
 
 
+NO_FUSED_OP = (1 << (8 * C.sizeof(C.c_size_t))) - 1
+
+
 class Dispatch(C.Structure):
-    _fields_ = [("op_index", C.c_size_t), ("kernel", C.c_char_p)]
+    _fields_ = [("op_index", C.c_size_t), ("kernel", C.c_char_p),
+                ("fused_op_index", C.c_size_t)]
 
 
 class HipError(RuntimeError):
@@ -65,6 +70,8 @@ SIGNATURES = {
     "llmi_hip_kv_append": (C.c_int, [_P, _P, _P, _P, CacheParams, _P]),
     "llmi_hip_causal_gqa": (C.c_int, [_P, _P, _P, _P, GqaParams, _P, _SZ, _P]),
     "llmi_hip_gqa_workspace_bytes": (_SZ, [GqaParams]),
+    "llmi_hip_kv_append_causal_gqa": (C.c_int, [_P, _P, _P, _P, _P, _P, GqaParams, _P, _SZ,
+                                                _P]),
     "llmi_hip_delta_update": (C.c_int, [_P, _P, _P, _P, _P, _P, _P,
                                         GraphDeltaParams, _P, _SZ, _P]),
     "llmi_hip_delta_workspace_bytes": (_SZ, [GraphDeltaParams]),

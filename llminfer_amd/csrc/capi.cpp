@@ -133,36 +133,78 @@ size_t llmi_hip_gqa_workspace_bytes(GqaParams p) {
   return 0;
 }
 
-int llmi_hip_causal_gqa(const uint16_t *q, const uint16_t *k_cache,
-                        const uint16_t *v_cache, uint16_t *out, GqaParams p,
-                        void *workspace, size_t workspace_bytes, void *stream) {
+} // extern "C"
+
+namespace llmi {
+namespace {
+
+// CausalGqa with an optional fused KvAppend (k_new/v_new non-null).
+int run_gqa(const uint16_t *q, const uint16_t *k_new, const uint16_t *v_new,
+            uint16_t *k_cache, uint16_t *v_cache, uint16_t *out,
+            const GqaParams &p, void *workspace, size_t workspace_bytes,
+            void *stream) {
   if (int st = check_gqa(p))
     return st;
   if (!q || !k_cache || !v_cache || !out)
     return fail(LLMI_HIP_INVALID_ARGUMENT, "CausalGqa: null buffer");
+  const bool fused = k_new || v_new;
+  if (fused && (!k_new || !v_new))
+    return fail(LLMI_HIP_INVALID_ARGUMENT, "KvAppend: null buffer");
   GqaShape s{p.tokens, p.queryHeads, p.kvHeads, p.headDim, p.past};
   hipStream_t st = static_cast<hipStream_t>(stream);
-  switch (select_gqa(p)) {
-  case GqaKernel::Decode: {
+  GqaKernel kind = select_gqa(p);
+  if (kind == GqaKernel::None)
+    return fail(LLMI_HIP_UNSUPPORTED, "CausalGqa: head_dim %u is not supported",
+                p.headDim);
+  if (kind == GqaKernel::Decode) {
     size_t need = decode_workspace_bytes(s);
-    if (!workspace || workspace_bytes < need)
+    if (need && (!workspace || workspace_bytes < need))
       return fail(LLMI_HIP_WORKSPACE,
                   "CausalGqa: decode needs a %zu-byte workspace, got %zu",
                   need, workspace ? workspace_bytes : (size_t)0);
-    return launched(launch_gqa_decode(q, k_cache, v_cache, out, workspace, s, st),
+    return launched(launch_gqa_decode(q, k_cache, v_cache, k_new, v_new, out,
+                                      workspace, s, st),
                     "gqaDecodeSplitK");
   }
-  case GqaKernel::Prefill:
+  if (fused) {
+    unsigned row = p.kvHeads * p.headDim;
+    int r = launched(launch_kv_append(k_new, v_new, k_cache, v_cache,
+                                      p.tokens * row, p.past * row, st),
+                     "kvAppend");
+    if (r != LLMI_HIP_OK)
+      return r;
+  }
+  if (kind == GqaKernel::Prefill)
     return launched(launch_gqa_prefill(q, k_cache, v_cache, out, s, st),
                     "gqaPrefillMfma");
-  case GqaKernel::Generic:
-    return launched(launch_gqa_generic(q, k_cache, v_cache, out, s, st),
-                    "gqaGeneric");
-  case GqaKernel::None:
-    break;
-  }
-  return fail(LLMI_HIP_UNSUPPORTED, "CausalGqa: head_dim %u is not supported",
-              p.headDim);
+  return launched(launch_gqa_generic(q, k_cache, v_cache, out, s, st),
+                  "gqaGeneric");
+}
+
+} // namespace
+} // namespace llmi
+
+extern "C" {
+
+int llmi_hip_causal_gqa(const uint16_t *q, const uint16_t *k_cache,
+                        const uint16_t *v_cache, uint16_t *out, GqaParams p,
+                        void *workspace, size_t workspace_bytes, void *stream) {
+  // The caches are only read on this path; the kernels take them non-const
+  // because the fused variant writes the new rows.
+  return run_gqa(q, nullptr, nullptr, const_cast<uint16_t *>(k_cache),
+                 const_cast<uint16_t *>(v_cache), out, p, workspace,
+                 workspace_bytes, stream);
+}
+
+int llmi_hip_kv_append_causal_gqa(const uint16_t *q, const uint16_t *k_new,
+                                  const uint16_t *v_new, uint16_t *k_cache,
+                                  uint16_t *v_cache, uint16_t *out, GqaParams p,
+                                  void *workspace, size_t workspace_bytes,
+                                  void *stream) {
+  if (!k_new || !v_new)
+    return fail(LLMI_HIP_INVALID_ARGUMENT, "KvAppend: null buffer");
+  return run_gqa(q, k_new, v_new, k_cache, v_cache, out, p, workspace,
+                 workspace_bytes, stream);
 }
 
 size_t llmi_hip_delta_workspace_bytes(GraphDeltaParams p) {
@@ -225,7 +267,22 @@ unsigned llmi_hip_dispatch_count(int op, const void *params) {
     const GqaParams &p = *static_cast<const GqaParams *>(params);
     if (check_gqa(p) || select_gqa(p) == GqaKernel::None)
       return 0;
+    if (select_gqa(p) == GqaKernel::Decode)
+      return decode_launches({p.tokens, p.queryHeads, p.kvHeads, p.headDim, p.past});
     return 1;
+  }
+  case LLMI_HIP_OP_KV_APPEND_CAUSAL_GQA: {
+    const GqaParams &p = *static_cast<const GqaParams *>(params);
+    if (check_gqa(p))
+      return 0;
+    switch (select_gqa(p)) {
+    case GqaKernel::Decode:
+      return decode_launches({p.tokens, p.queryHeads, p.kvHeads, p.headDim, p.past});
+    case GqaKernel::None:
+      return 0;
+    default:
+      return 2;
+    }
   }
   case LLMI_HIP_OP_DELTA_UPDATE: {
     const GraphDeltaParams &p = *static_cast<const GraphDeltaParams *>(params);
@@ -243,10 +300,15 @@ const char *llmi_hip_kernel_name(int op, const void *params, unsigned index) {
   switch (op) {
   case LLMI_HIP_OP_KV_APPEND:
     return "kvAppend";
+  case LLMI_HIP_OP_KV_APPEND_CAUSAL_GQA:
+    if (select_gqa(*static_cast<const GqaParams *>(params)) != GqaKernel::Decode)
+      return index == 0 ? "kvAppend"
+                        : llmi_hip_kernel_name(LLMI_HIP_OP_CAUSAL_GQA, params, 0);
+    return llmi_hip_kernel_name(LLMI_HIP_OP_CAUSAL_GQA, params, index);
   case LLMI_HIP_OP_CAUSAL_GQA:
     switch (select_gqa(*static_cast<const GqaParams *>(params))) {
     case GqaKernel::Decode:
-      return "gqaDecodeSplitK";
+      return index == 0 ? "gqaDecodeSplitK" : "gqaDecodeMerge";
     case GqaKernel::Prefill:
       return "gqaPrefillMfma";
     case GqaKernel::Generic:

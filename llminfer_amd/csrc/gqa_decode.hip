@@ -4,9 +4,9 @@
 // gqaValue (Reference.metal:303-323, Graph.metal:172-230) with one pass over
 // K and V. It is an HBM-bandwidth problem (4 FLOP/byte), so no MFMA:
 //
-//  * grid = (split, kv head, token). A workgroup streams one key range of
-//    one KV head and serves all G = Hq/Hkv query heads of the group, so each
-//    K/V byte leaves HBM once.
+//  * grid = (split, kv head, token). A workgroup of W waves streams one key
+//    range of one KV head and serves all G = Hq/Hkv query heads of the
+//    group, so each K/V byte leaves HBM once.
 //  * D/16 lanes share one key row: each lane holds 16 channels as two 16-byte
 //    loads, so one wave instruction reads whole 256-byte row segments.
 //  * q.k is v_dot2_f32_f16 on packed fp16 pairs, reduced over the lanes of a
@@ -14,81 +14,116 @@
 //    accumulator are fp32, with exp2 on log2e-prescaled scores.
 //  * each lane group runs its own online softmax over its keys; groups,
 //    waves and finally splits are merged with the usual (m, l, o) rescale.
-//  * the split merge happens in the same launch: every workgroup writes its
-//    (m, l, o) partial to the workspace, and the last one to arrive for a
-//    (token, kv head) -- found with a device-scope atomic ticket after a
-//    release fence -- merges all partials and writes the fp16 output. It
-//    then resets the ticket to zero, so the workspace is ready for the next
-//    call without a memset.
+//  * a one-split launch writes the output directly. Otherwise every
+//    workgroup writes its (m, l, o) partial to the workspace and a second,
+//    small launch merges them: workgroup (head, token, kv head), one thread
+//    per channel, every partial load in flight at once. (Merging inside the
+//    split kernel's last-arriving workgroup was measured slower on MI355X:
+//    the partial stores then need agent-scope release -- a whole-L2
+//    writeback per workgroup, which serialises -- and the single merging
+//    workgroup reads all partials through one CU.)
+//  * optionally (k_new/v_new non-null) the launch also performs the step's
+//    KvAppend: keys [P, P+T) are read from the new rows rather than the
+//    cache, and the workgroups of the last token write them into the cache
+//    rows [P, P+T) -- the same bytes cacheAppend (Reference.metal:295-301)
+//    writes, without a second launch.
 #include "hip_common.hpp"
 #include "kernels.hpp"
 
 #include <algorithm>
 #include <math.h>
-
-#ifndef LLMI_DECODE_MAX_SPLITS
-#define LLMI_DECODE_MAX_SPLITS 64
-#endif
-#ifndef LLMI_DECODE_TARGET_WGS
-#define LLMI_DECODE_TARGET_WGS 512
-#endif
+#include <stdlib.h>
 
 namespace llmi {
 namespace {
 
-constexpr int kWaves = 4;
-constexpr int kThreads = 64 * kWaves;
-constexpr int kSlots = 4; // keys per lane group per iteration
-constexpr unsigned kMaxSplits = LLMI_DECODE_MAX_SPLITS;
+constexpr int kSlots = 4;          // keys per lane group per iteration
+constexpr unsigned kResidentWaves = 256 * 8; // MI355X: 256 CUs x 8 waves
+constexpr unsigned kMaxSplits = 128;
 
 template <int D> struct DecodeGeom {
   static constexpr int LPK = D / 16;            // lanes per key row
   static constexpr int KPR = 64 / LPK;          // key rows per wave instruction
   static constexpr int WaveTile = KPR * kSlots; // keys per wave iteration
-  static constexpr int Tile = WaveTile * kWaves;
 };
 
 struct Plan {
-  unsigned splits, keysPerSplit;
+  unsigned waves, splits, keysPerSplit;
 };
 
-unsigned tile_for(unsigned D) {
+unsigned wave_tile(unsigned D) {
   switch (D) {
   case 64:
-    return DecodeGeom<64>::Tile;
+    return DecodeGeom<64>::WaveTile;
   case 128:
-    return DecodeGeom<128>::Tile;
+    return DecodeGeom<128>::WaveTile;
   default:
-    return DecodeGeom<256>::Tile;
+    return DecodeGeom<256>::WaveTile;
   }
 }
 
+// Tuning knobs, read once. LLMI_DECODE_TARGET_WGS: resident 8-wave
+// workgroups to plan for (default 256: one per CU of MI355X);
+// LLMI_DECODE_WAVES: waves per workgroup, 4 or 8 (default: chosen per shape).
+unsigned env_or(const char *name, unsigned dflt) {
+  const char *v = getenv(name);
+  if (!v || !*v)
+    return dflt;
+  long x = strtol(v, nullptr, 10);
+  return x > 0 ? (unsigned)x : dflt;
+}
+
+unsigned target_wgs() {
+  static const unsigned v = env_or("LLMI_DECODE_TARGET_WGS", kResidentWaves / 8);
+  return v;
+}
+
+unsigned forced_waves() {
+  static const unsigned v = env_or("LLMI_DECODE_WAVES", 0);
+  return v == 4 || v == 8 ? v : 0;
+}
+
+// The kernel holds ~200 VGPRs, so a CU keeps 2 waves per SIMD resident:
+// 256 CUs x 8 waves over the GPU. The plan gives every wave the fewest
+// 16-key wave tiles for which the whole grid is resident in one round, in
+// 8-wave workgroups (measured faster than 4-wave ones at 4K and 32K: fewer
+// partials to merge, and two threads per merged column).
+
 Plan plan_for(const GqaShape &s) {
-  unsigned tile = tile_for(s.D);
-  unsigned visible = s.P + s.T;
-  unsigned tiles = (visible + tile - 1) / tile;
-  unsigned rows = s.T * s.Hkv;
-  unsigned want = std::max(1u, (unsigned)LLMI_DECODE_TARGET_WGS / std::max(1u, rows));
-  unsigned splits = std::min({want, tiles, kMaxSplits});
-  unsigned perSplit = (tiles + splits - 1) / splits;
-  splits = (tiles + perSplit - 1) / perSplit;
-  return {splits, perSplit * tile};
+  const unsigned G = s.Hq / s.Hkv;
+  const unsigned wt = wave_tile(s.D);
+  const unsigned visible = s.P + s.T;
+  const unsigned rows = s.T * s.Hkv;
+  const unsigned budget = target_wgs() * 8; // resident waves to fill
+  const uint64_t waveTiles = (uint64_t)rows * ((visible + wt - 1) / wt);
+  unsigned iters = (unsigned)std::max<uint64_t>(1, (waveTiles + budget - 1) / budget);
+  unsigned waves = 8;
+  if (forced_waves())
+    waves = forced_waves();
+  if (G * s.D > 1024u || G > 4) // merge: a float4 column per thread, a wave per head
+    waves = 8;
+  unsigned kps = wt * waves * iters;
+  unsigned splits = (visible + kps - 1) / kps;
+  if (splits > kMaxSplits) { // very long contexts: more iterations per wave
+    kps = (visible + kMaxSplits - 1) / kMaxSplits;
+    kps = (kps + wt * waves - 1) / (wt * waves) * (wt * waves);
+    splits = (visible + kps - 1) / kps;
+  }
+  return {waves, splits, kps};
 }
 
 struct WsLayout {
-  size_t counters, ml, o, total;
+  size_t ml, o, total;
 };
 
-// Tickets live in the fixed workspace header (kWorkspaceTicketBytes), which
-// every kernel that uses tickets leaves zeroed; partials follow it.
+// Partials of a multi-split launch: (m, l) pairs, then o vectors.
 WsLayout layout_for(const GqaShape &s, const Plan &p) {
   unsigned G = s.Hq / s.Hkv;
   size_t rows = (size_t)s.T * s.Hkv;
   WsLayout w;
-  w.counters = 0;
-  w.ml = kWorkspaceTicketBytes;
-  w.o = w.ml + ((rows * p.splits * G * 2 * 4 + 255) / 256) * 256;
-  w.total = w.o + rows * p.splits * G * s.D * 4;
+  w.ml = 0;
+  w.o = ((rows * p.splits * G * 2 * 4 + 255) / 256) * 256;
+  w.total = p.splits > 1 ? w.o + rows * p.splits * G * s.D * 4 : 0;
   return w;
 }
 
@@ -96,22 +131,97 @@ __device__ __forceinline__ float rescale(float m, float M) {
   return m == -INFINITY ? 0.0f : fast_exp2(m - M);
 }
 
-template <int D, int G>
-__global__ __launch_bounds__(kThreads) void gqa_decode_kernel(
-    const half_t *__restrict__ q, const half_t *__restrict__ kc,
-    const half_t *__restrict__ vc, half_t *__restrict__ out,
-    unsigned *__restrict__ tickets, float *__restrict__ wml,
+// Max / sum over the 64 lanes of a wave, the result in every lane.
+__device__ __forceinline__ float wave_max(float x) {
+  x = fmaxf(x, row_ror<1>(x));
+  x = fmaxf(x, row_ror<2>(x));
+  x = fmaxf(x, row_ror<4>(x));
+  x = fmaxf(x, row_ror<8>(x));
+  LanePair p = pair16(x);
+  x = fmaxf(p.a, p.b);
+  p = pair32(x);
+  return fmaxf(p.a, p.b);
+}
+
+__device__ __forceinline__ float wave_sum(float x) {
+  x += row_ror<1>(x);
+  x += row_ror<2>(x);
+  x += row_ror<4>(x);
+  x += row_ror<8>(x);
+  LanePair p = pair16(x);
+  x = p.a + p.b;
+  p = pair32(x);
+  return p.a + p.b;
+}
+
+// Combine (m, l, o) with the lane N places further along the 16-lane row.
+// After the N = LPK, 2*LPK, ... < 16 steps every lane holds its row's total.
+template <int N, int G>
+__device__ __forceinline__ void merge_rotated(float (&m)[G], float (&l)[G],
+                                              float (&o)[G][16]) {
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    const float m2 = row_ror<N>(m[g]), l2 = row_ror<N>(l[g]);
+    const float M = fmaxf(m[g], m2);
+    const float a1 = rescale(m[g], M), a2 = rescale(m2, M);
+    l[g] = l[g] * a1 + l2 * a2;
+#pragma unroll
+    for (int x = 0; x < 16; ++x)
+      o[g][x] = o[g][x] * a1 + row_ror<N>(o[g][x]) * a2;
+    m[g] = M;
+  }
+}
+
+// Combine the two members of a lane pair; both partners compute the same.
+template <int G, typename Pair>
+__device__ __forceinline__ void merge_pair(LanePair mp, LanePair lp, float (&o)[16],
+                                           float &m, float &l, Pair pair) {
+  const float M = fmaxf(mp.a, mp.b);
+  const float a1 = rescale(mp.a, M), a2 = rescale(mp.b, M);
+  l = lp.a * a1 + lp.b * a2;
+#pragma unroll
+  for (int x = 0; x < 16; ++x) {
+    LanePair op = pair(o[x]);
+    o[x] = op.a * a1 + op.b * a2;
+  }
+  m = M;
+}
+
+template <int D, int G, int W>
+__global__ __launch_bounds__(64 * W) void gqa_decode_kernel(
+    const half_t *__restrict__ q, half_t *kc, half_t *vc,
+    const half_t *__restrict__ knew, const half_t *__restrict__ vnew,
+    half_t *__restrict__ out, float *__restrict__ wml,
     float *__restrict__ wo, unsigned Hq, unsigned Hkv, unsigned P,
-    unsigned keysPerSplit, unsigned splits, float scoreScale) {
+    unsigned T, unsigned keysPerSplit, unsigned splits, float scoreScale) {
   using Geo = DecodeGeom<D>;
   constexpr int LPK = Geo::LPK, KPR = Geo::KPR;
+  constexpr int NT = 64 * W;
+  constexpr int Tile = Geo::WaveTile * W;
+  constexpr int F4 = G * D / 4; // float4 columns of one (m, l, o) partial
   const unsigned split = blockIdx.x, kvh = blockIdx.y, t = blockIdx.z;
-  const unsigned lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+  const unsigned tid = threadIdx.x;
+  const unsigned lane = tid & 63u, wave = tid >> 6;
   const unsigned slice = lane % LPK, kg = lane / LPK;
   const unsigned visible = P + t + 1;
   const unsigned begin = split * keysPerSplit;
   const unsigned end = min(begin + keysPerSplit, visible);
   const size_t rowStride = (size_t)Hkv * D;
+  const bool fused = knew != nullptr;
+
+  // Fused KvAppend: the last token's workgroups own the new rows of their
+  // key range and copy them into the cache (nothing in this launch reads
+  // those cache rows: new keys are taken from k_new/v_new below).
+  if (fused && t == T - 1) {
+    const unsigned r0 = max(begin, P), r1 = end;
+    for (unsigned i = tid; i < (r1 > r0 ? r1 - r0 : 0u) * (D / 8); i += NT) {
+      const unsigned r = r0 + i / (D / 8), c = (i % (D / 8)) * 8;
+      const size_t src = (size_t)(r - P) * rowStride + (size_t)kvh * D + c;
+      const size_t dst = (size_t)r * rowStride + (size_t)kvh * D + c;
+      *reinterpret_cast<half8_t *>(kc + dst) = load8(knew + src);
+      *reinterpret_cast<half8_t *>(vc + dst) = load8(vnew + src);
+    }
+  }
 
   // Channels of this lane: [j*D/2 + slice*8, +8) for j = 0, 1.
   half8_t qv[G][2];
@@ -131,20 +241,23 @@ __global__ __launch_bounds__(kThreads) void gqa_decode_kernel(
       o[g][x] = 0.0f;
   }
 
-  const half_t *kbase = kc + (size_t)kvh * D + slice * 8;
-  const half_t *vbase = vc + (size_t)kvh * D + slice * 8;
-  for (unsigned base = begin; base < end; base += Geo::Tile) {
+  const size_t chan = (size_t)kvh * D + slice * 8;
+  for (unsigned base = begin; base < end; base += Tile) {
     const unsigned first = base + wave * Geo::WaveTile + kg;
     half8_t kx[kSlots][2], vx[kSlots][2];
 #pragma unroll
     for (int n = 0; n < kSlots; ++n) {
       unsigned key = first + n * KPR;
-      bool ok = key < end;
-      size_t off = (size_t)(ok ? key : begin) * rowStride;
+      key = key < end ? key : begin;
+      const bool isNew = fused && key >= P;
+      const half_t *kp = (isNew ? knew + (size_t)(key - P) * rowStride
+                                : kc + (size_t)key * rowStride) + chan;
+      const half_t *vp = (isNew ? vnew + (size_t)(key - P) * rowStride
+                                : vc + (size_t)key * rowStride) + chan;
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
-        kx[n][j] = load8(kbase + off + j * (D / 2));
-        vx[n][j] = load8(vbase + off + j * (D / 2));
+        kx[n][j] = load8(kp + j * (D / 2));
+        vx[n][j] = load8(vp + j * (D / 2));
       }
     }
     float sc[kSlots][G];
@@ -191,28 +304,23 @@ __global__ __launch_bounds__(kThreads) void gqa_decode_kernel(
     }
   }
 
-  // Merge the KPR lane groups of the wave (lanes kg*LPK + slice).
+  // Merge the KPR lane groups of the wave (lanes kg*LPK + slice) with VALU
+  // lane exchanges only: DPP row rotations for groups narrower than a row,
+  // then the gfx950 row-pair and half-wave swaps. (Cross-lane reads through
+  // the LDS unit cost a dependent round trip each; this chain has none.)
+  if constexpr (LPK <= 4)
+    merge_rotated<4, G>(m, l, o);
+  if constexpr (LPK <= 8)
+    merge_rotated<8, G>(m, l, o);
 #pragma unroll
-  for (int stride = LPK; stride < 64; stride <<= 1) {
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      float m2 = __shfl_xor(m[g], stride);
-      float l2 = __shfl_xor(l[g], stride);
-      float M = fmaxf(m[g], m2);
-      float a1 = rescale(m[g], M), a2 = rescale(m2, M);
-      l[g] = l[g] * a1 + l2 * a2;
-#pragma unroll
-      for (int x = 0; x < 16; ++x) {
-        float o2 = __shfl_xor(o[g][x], stride);
-        o[g][x] = o[g][x] * a1 + o2 * a2;
-      }
-      m[g] = M;
-    }
+  for (int g = 0; g < G; ++g) {
+    merge_pair<G>(pair16(m[g]), pair16(l[g]), o[g], m[g], l[g], pair16);
+    merge_pair<G>(pair32(m[g]), pair32(l[g]), o[g], m[g], l[g], pair32);
   }
 
-  // Merge the waves through LDS, then write this split's partial.
-  __shared__ float sM[kWaves][G], sL[kWaves][G];
-  __shared__ float sO[kWaves][G][D];
+  // Merge the waves through LDS.
+  __shared__ float sM[W][G], sL[W][G];
+  __shared__ __attribute__((aligned(16))) float sO[W][G][D];
   if (lane == 0)
 #pragma unroll
     for (int g = 0; g < G; ++g) {
@@ -230,106 +338,174 @@ __global__ __launch_bounds__(kThreads) void gqa_decode_kernel(
   __syncthreads();
 
   const size_t row = (size_t)t * Hkv + kvh;
+  half_t *orow = out + ((size_t)t * Hq + kvh * G) * D;
+
+  if (splits == 1) {
+    for (unsigned i = tid; i < (unsigned)F4; i += NT) {
+      const unsigned g = i * 4 / D, x = i * 4 % D;
+      float M = sM[0][g];
+#pragma unroll
+      for (int w = 1; w < W; ++w)
+        M = fmaxf(M, sM[w][g]);
+      float L = 0.0f, acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int w = 0; w < W; ++w) {
+        float a = rescale(sM[w][g], M);
+        L += sL[w][g] * a;
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          acc[e] += sO[w][g][x + e] * a;
+      }
+      const float inv = 1.0f / L;
+      half4_t hv{(half_t)(acc[0] * inv), (half_t)(acc[1] * inv),
+                 (half_t)(acc[2] * inv), (half_t)(acc[3] * inv)};
+      *reinterpret_cast<half4_t *>(orow + g * D + x) = hv;
+    }
+    return;
+  }
+
+  // Write this split's partial; the merge launch reads it.
   float *po = wo + (row * splits + split) * (size_t)(G * D);
   float *pml = wml + (row * splits + split) * (size_t)(G * 2);
-  for (unsigned i = threadIdx.x; i < (unsigned)(G * D); i += kThreads) {
-    unsigned g = i / D, x = i % D;
+  for (unsigned i = tid; i < (unsigned)F4; i += NT) {
+    const unsigned g = i * 4 / D, x = i * 4 % D;
     float M = sM[0][g];
 #pragma unroll
-    for (int w = 1; w < kWaves; ++w)
+    for (int w = 1; w < W; ++w)
       M = fmaxf(M, sM[w][g]);
-    float acc = 0.0f;
+    float4_t acc{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-    for (int w = 0; w < kWaves; ++w)
-      acc += sO[w][g][x] * rescale(sM[w][g], M);
-    po[i] = acc;
+    for (int w = 0; w < W; ++w) {
+      float a = rescale(sM[w][g], M);
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        acc[e] += sO[w][g][x + e] * a;
+    }
+    *reinterpret_cast<float4_t *>(po + i * 4) = acc;
   }
-  if (threadIdx.x < (unsigned)G) {
-    unsigned g = threadIdx.x;
+  if (tid < (unsigned)G) {
+    const unsigned g = tid;
     float M = sM[0][g];
-    for (int w = 1; w < kWaves; ++w)
+    for (int w = 1; w < W; ++w)
       M = fmaxf(M, sM[w][g]);
     float L = 0.0f;
-    for (int w = 0; w < kWaves; ++w)
+    for (int w = 0; w < W; ++w)
       L += sL[w][g] * rescale(sM[w][g], M);
     pml[g * 2 + 0] = M;
     pml[g * 2 + 1] = L;
   }
-
-  // Release this partial, take a ticket; the last arrival merges.
-  __threadfence();
-  __shared__ unsigned sTicket;
-  __syncthreads();
-  if (threadIdx.x == 0)
-    sTicket = atomicAdd(&tickets[row], 1u);
-  __syncthreads();
-  if (sTicket != splits - 1)
-    return;
-  __threadfence(); // acquire: see every other split's partial
-
-  __shared__ float sScale[kMaxSplits][G];
-  __shared__ float sInvL[G];
-  const float *rowMl = wml + row * splits * (size_t)(G * 2);
-  if (threadIdx.x < (unsigned)G) {
-    unsigned g = threadIdx.x;
-    float M = -INFINITY;
-    for (unsigned s = 0; s < splits; ++s)
-      M = fmaxf(M, rowMl[s * G * 2 + g * 2]);
-    float L = 0.0f;
-    for (unsigned s = 0; s < splits; ++s) {
-      float a = rescale(rowMl[s * G * 2 + g * 2], M);
-      sScale[s][g] = a;
-      L += a * rowMl[s * G * 2 + g * 2 + 1];
-    }
-    sInvL[g] = 1.0f / L;
-  }
-  __syncthreads();
-  const float *rowO = wo + row * splits * (size_t)(G * D);
-  for (unsigned i = threadIdx.x; i < (unsigned)(G * D); i += kThreads) {
-    unsigned g = i / D, x = i % D;
-    float acc = 0.0f;
-    for (unsigned s = 0; s < splits; ++s)
-      acc += rowO[(size_t)s * G * D + i] * sScale[s][g];
-    out[((size_t)t * Hq + kvh * G + g) * D + x] = (half_t)(acc * sInvL[g]);
-  }
-  if (threadIdx.x == 0)
-    tickets[row] = 0u; // ready for the next call
 }
 
+// Second-launch merge: workgroup (g, row) combines the splits of query
+// head g of one (token, kv head) row; thread x owns channel x.
 template <int D, int G>
-hipError_t launch_dg(const GqaShape &s, const uint16_t *q, const uint16_t *k,
-                     const uint16_t *v, uint16_t *out, void *ws,
-                     hipStream_t stream) {
-  Plan p = plan_for(s);
+__global__ __launch_bounds__(D) void gqa_decode_merge_kernel(
+    const float *__restrict__ wml, const float *__restrict__ wo,
+    half_t *__restrict__ out, unsigned Hq, unsigned Hkv, unsigned splits) {
+  static_assert(D % 64 == 0, "whole waves");
+  const unsigned g = blockIdx.x, row = blockIdx.y, x = threadIdx.x;
+  const unsigned lane = x & 63u, wave = x >> 6;
+  const float *col = wo + (size_t)row * splits * G * D + (size_t)g * D + x;
+  const float *rowMl = wml + (size_t)row * splits * G * 2;
+  constexpr int PER = 32;
+  float v[PER];
+  auto load_round = [&](unsigned s0) {
+#pragma unroll
+    for (int u = 0; u < PER; ++u) {
+      const unsigned s = s0 + u;
+      v[u] = s < splits ? col[(size_t)s * G * D] : 0.0f;
+    }
+  };
+  load_round(0);
+  __shared__ float sW[kMaxSplits];
+  if (wave == 0) {
+    float ms[2], ls[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const unsigned s = lane + 64u * h;
+      ms[h] = s < splits ? rowMl[(s * G + g) * 2 + 0] : -INFINITY;
+      ls[h] = s < splits ? rowMl[(s * G + g) * 2 + 1] : 0.0f;
+    }
+    const float M = wave_max(fmaxf(ms[0], ms[1]));
+    const float L = wave_sum(ls[0] * rescale(ms[0], M) + ls[1] * rescale(ms[1], M));
+    const float invL = 1.0f / L;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const unsigned s = lane + 64u * h;
+      if (s < splits)
+        sW[s] = rescale(ms[h], M) * invL;
+    }
+  }
+  __syncthreads();
+  float acc = 0.0f;
+  for (unsigned s0 = 0;;) {
+#pragma unroll
+    for (int u = 0; u < PER; ++u)
+      acc = fmaf(v[u], s0 + u < splits ? sW[s0 + u] : 0.0f, acc);
+    s0 += PER;
+    if (s0 >= splits)
+      break;
+    load_round(s0);
+  }
+  const unsigned t = row / Hkv, kvh = row % Hkv;
+  out[((size_t)t * Hq + kvh * G + g) * D + x] = (half_t)acc;
+}
+
+template <int D, int G, int W>
+hipError_t launch_dgw(const GqaShape &s, const Plan &p, const uint16_t *q,
+                      uint16_t *k, uint16_t *v, const uint16_t *knew,
+                      const uint16_t *vnew, uint16_t *out, void *ws,
+                      hipStream_t stream) {
   WsLayout w = layout_for(s, p);
   char *base = static_cast<char *>(ws);
   float scale = kLog2e / sqrtf((float)D);
-  hipLaunchKernelGGL((gqa_decode_kernel<D, G>), dim3(p.splits, s.Hkv, s.T),
-                     dim3(kThreads), 0, stream,
+  hipLaunchKernelGGL((gqa_decode_kernel<D, G, W>), dim3(p.splits, s.Hkv, s.T),
+                     dim3(64 * W), 0, stream,
                      reinterpret_cast<const half_t *>(q),
-                     reinterpret_cast<const half_t *>(k),
-                     reinterpret_cast<const half_t *>(v),
+                     reinterpret_cast<half_t *>(k), reinterpret_cast<half_t *>(v),
+                     reinterpret_cast<const half_t *>(knew),
+                     reinterpret_cast<const half_t *>(vnew),
                      reinterpret_cast<half_t *>(out),
-                     reinterpret_cast<unsigned *>(base + w.counters),
-                     reinterpret_cast<float *>(base + w.ml),
-                     reinterpret_cast<float *>(base + w.o), s.Hq, s.Hkv, s.P,
-                     p.keysPerSplit, p.splits, scale);
+                     reinterpret_cast<float *>(base ? base + w.ml : nullptr),
+                     reinterpret_cast<float *>(base ? base + w.o : nullptr), s.Hq,
+                     s.Hkv, s.P, s.T, p.keysPerSplit, p.splits, scale);
+  if (p.splits > 1) {
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess)
+      return e;
+    hipLaunchKernelGGL((gqa_decode_merge_kernel<D, G>), dim3(G, s.T * s.Hkv),
+                       dim3(D), 0, stream, reinterpret_cast<float *>(base + w.ml),
+                       reinterpret_cast<float *>(base + w.o),
+                       reinterpret_cast<half_t *>(out), s.Hq, s.Hkv, p.splits);
+  }
   return hipGetLastError();
 }
 
+template <int D, int G>
+hipError_t launch_dg(const GqaShape &s, const uint16_t *q, uint16_t *k,
+                     uint16_t *v, const uint16_t *knew, const uint16_t *vnew,
+                     uint16_t *out, void *ws, hipStream_t stream) {
+  Plan p = plan_for(s);
+  if constexpr (G * D <= 1024 && G <= 4) {
+    if (p.waves == 4)
+      return launch_dgw<D, G, 4>(s, p, q, k, v, knew, vnew, out, ws, stream);
+  }
+  return launch_dgw<D, G, 8>(s, p, q, k, v, knew, vnew, out, ws, stream);
+}
+
 template <int D>
-hipError_t launch_d(const GqaShape &s, const uint16_t *q, const uint16_t *k,
-                    const uint16_t *v, uint16_t *out, void *ws,
-                    hipStream_t stream) {
+hipError_t launch_d(const GqaShape &s, const uint16_t *q, uint16_t *k,
+                    uint16_t *v, const uint16_t *knew, const uint16_t *vnew,
+                    uint16_t *out, void *ws, hipStream_t stream) {
   switch (s.Hq / s.Hkv) {
   case 1:
-    return launch_dg<D, 1>(s, q, k, v, out, ws, stream);
+    return launch_dg<D, 1>(s, q, k, v, knew, vnew, out, ws, stream);
   case 2:
-    return launch_dg<D, 2>(s, q, k, v, out, ws, stream);
+    return launch_dg<D, 2>(s, q, k, v, knew, vnew, out, ws, stream);
   case 4:
-    return launch_dg<D, 4>(s, q, k, v, out, ws, stream);
+    return launch_dg<D, 4>(s, q, k, v, knew, vnew, out, ws, stream);
   case 8:
-    return launch_dg<D, 8>(s, q, k, v, out, ws, stream);
+    return launch_dg<D, 8>(s, q, k, v, knew, vnew, out, ws, stream);
   }
   return hipErrorInvalidValue;
 }
@@ -340,24 +516,28 @@ bool decode_supported(const GqaShape &s) {
   unsigned G = s.Hkv ? s.Hq / s.Hkv : 0;
   bool dOk = s.D == 64 || s.D == 128 || s.D == 256;
   bool gOk = G == 1 || G == 2 || G == 4 || G == 8;
-  return dOk && gOk && s.T >= 1 && s.T <= 64 &&
-         (size_t)s.T * s.Hkv * 4 <= kWorkspaceTicketBytes;
+  return dOk && gOk && s.T >= 1 && s.T <= 64;
 }
 
 size_t decode_workspace_bytes(const GqaShape &s) {
   return layout_for(s, plan_for(s)).total;
 }
 
-hipError_t launch_gqa_decode(const uint16_t *q, const uint16_t *k,
-                             const uint16_t *v, uint16_t *out, void *ws,
-                             const GqaShape &s, hipStream_t stream) {
+unsigned decode_splits(const GqaShape &s) { return plan_for(s).splits; }
+
+unsigned decode_launches(const GqaShape &s) { return plan_for(s).splits > 1 ? 2 : 1; }
+
+hipError_t launch_gqa_decode(const uint16_t *q, uint16_t *k, uint16_t *v,
+                             const uint16_t *knew, const uint16_t *vnew,
+                             uint16_t *out, void *ws, const GqaShape &s,
+                             hipStream_t stream) {
   switch (s.D) {
   case 64:
-    return launch_d<64>(s, q, k, v, out, ws, stream);
+    return launch_d<64>(s, q, k, v, knew, vnew, out, ws, stream);
   case 128:
-    return launch_d<128>(s, q, k, v, out, ws, stream);
+    return launch_d<128>(s, q, k, v, knew, vnew, out, ws, stream);
   case 256:
-    return launch_d<256>(s, q, k, v, out, ws, stream);
+    return launch_d<256>(s, q, k, v, knew, vnew, out, ws, stream);
   }
   return hipErrorInvalidValue;
 }

@@ -45,6 +45,31 @@ template <int N> __device__ __forceinline__ float group_sum(float x) {
   return x;
 }
 
+// DPP rotate right by N lanes inside each 16-lane row (row_ror:N, 1..15).
+template <int N> __device__ __forceinline__ float row_ror(float x) {
+  static_assert(N >= 1 && N <= 15, "row_ror takes 1..15");
+  return __int_as_float(
+      __builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x120 + N, 0xF, 0xF, false));
+}
+
+// gfx950 row-pair exchange. With both operands equal to x, the two results
+// hold x of the even and of the odd 16-lane row of each row pair (stride
+// 16), or of the low and the high 32 lanes (stride 32), in every lane: a
+// symmetric pair, so a combine of the two is identical in both partners.
+struct LanePair {
+  float a, b;
+};
+__device__ __forceinline__ LanePair pair16(float x) {
+  auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x),
+                                            false, false);
+  return {__uint_as_float(r[0]), __uint_as_float(r[1])};
+}
+__device__ __forceinline__ LanePair pair32(float x) {
+  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x),
+                                            false, false);
+  return {__uint_as_float(r[0]), __uint_as_float(r[1])};
+}
+
 __device__ __forceinline__ float fast_exp2(float x) {
   return __builtin_amdgcn_exp2f(x);
 }

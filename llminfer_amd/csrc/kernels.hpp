@@ -8,11 +8,6 @@
 
 namespace llmi {
 
-// Every workspace starts with this many bytes of completion tickets. They
-// must be zero before a workspace is first used, and every kernel that takes
-// a ticket returns it to zero, so the header stays zero between calls.
-constexpr size_t kWorkspaceTicketBytes = 4096;
-
 // ---------------------------------------------------------------- KvAppend
 hipError_t launch_cache_append(const uint16_t *src, uint16_t *cache,
                                unsigned count, unsigned offset,
@@ -26,13 +21,19 @@ struct GqaShape {
   unsigned T, Hq, Hkv, D, P;
 };
 
-// Split-K decode (any T, fast for small T). Workspace layout is owned by
-// gqa_decode.hip; decode_workspace_bytes sizes it.
+// Split-K decode (T <= 64). Workspace layout is owned by gqa_decode.hip;
+// decode_workspace_bytes sizes it (0 when the launch needs no split merge).
+// With knew/vnew non-null the launch also appends those T rows to the
+// caches at row P (fused KvAppend); with them null the rows must already be
+// in the caches.
 bool decode_supported(const GqaShape &s);
 size_t decode_workspace_bytes(const GqaShape &s);
-hipError_t launch_gqa_decode(const uint16_t *q, const uint16_t *k,
-                             const uint16_t *v, uint16_t *out, void *ws,
-                             const GqaShape &s, hipStream_t stream);
+unsigned decode_splits(const GqaShape &s);
+unsigned decode_launches(const GqaShape &s); // 1, or 2 with a merge launch
+hipError_t launch_gqa_decode(const uint16_t *q, uint16_t *k, uint16_t *v,
+                             const uint16_t *knew, const uint16_t *vnew,
+                             uint16_t *out, void *ws, const GqaShape &s,
+                             hipStream_t stream);
 
 // MFMA flash prefill.
 bool prefill_supported(const GqaShape &s);

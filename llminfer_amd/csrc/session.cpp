@@ -105,7 +105,7 @@ hipError_t zero_state(llmi_hip_session *s) {
 
 // Grow the workspace to `need` bytes before any launch of a step. The
 // previous step ended with a stream synchronisation, so nothing in flight
-// uses the old allocation. A new workspace is zeroed (ticket header).
+// uses the old allocation.
 int ensure_workspace(llmi_hip_session *s, size_t need) {
   if (need <= s->wsBytes)
     return LLMI_HIP_OK;
@@ -113,11 +113,6 @@ int ensure_workspace(llmi_hip_session *s, size_t need) {
   if (hipMalloc(&ws, need) != hipSuccess)
     return fail(LLMI_HIP_WORKSPACE, "session: cannot allocate a %zu-byte workspace",
                 need);
-  if (hipMemsetAsync(ws, 0, need, s->stream) != hipSuccess ||
-      hipStreamSynchronize(s->stream) != hipSuccess) {
-    (void)hipFree(ws);
-    return fail(LLMI_HIP_WORKSPACE, "session: cannot clear the workspace");
-  }
   if (s->ws)
     (void)hipFree(s->ws);
   s->ws = ws;
@@ -126,9 +121,9 @@ int ensure_workspace(llmi_hip_session *s, size_t need) {
 }
 
 void record(llmi_hip_dispatch *records, size_t cap, size_t &n, size_t op,
-            const char *kernel) {
+            const char *kernel, size_t fused = LLMI_HIP_NO_FUSED_OP) {
   if (records && n < cap)
-    records[n] = llmi_hip_dispatch{op, kernel};
+    records[n] = llmi_hip_dispatch{op, kernel, fused};
   ++n;
 }
 
@@ -252,14 +247,26 @@ int llmi_hip_session_step(llmi_hip_session *s, unsigned tokens, const float *dq,
     return st;
 
   // Plan records, in graph order: DeltaUpdate (op 0), KvAppend (op 1),
-  // CausalGqa (op 2), as MetalDispatchInfo{opIndex, kernel}.
+  // CausalGqa (op 2), as MetalDispatchInfo{opIndex, kernel, fusedOpIndex}.
+  // KvAppend and CausalGqa run through the fused entry point: one decode
+  // launch that also appends ({op 2, fused 1}), or append then prefill.
   size_t n = 0;
   for (unsigned i = 0, m = llmi_hip_dispatch_count(LLMI_HIP_OP_DELTA_UPDATE, &dp); i < m; ++i)
     record(records, cap, n, 0, llmi_hip_kernel_name(LLMI_HIP_OP_DELTA_UPDATE, &dp, i));
-  CacheParams cp{tokens * c.kvHeads * c.headDim, s->past * c.kvHeads * c.headDim};
-  record(records, cap, n, 1, llmi_hip_kernel_name(LLMI_HIP_OP_KV_APPEND, &cp, 0));
-  for (unsigned i = 0, m = llmi_hip_dispatch_count(LLMI_HIP_OP_CAUSAL_GQA, &gp); i < m; ++i)
-    record(records, cap, n, 2, llmi_hip_kernel_name(LLMI_HIP_OP_CAUSAL_GQA, &gp, i));
+  const unsigned pairLaunches =
+      llmi_hip_dispatch_count(LLMI_HIP_OP_KV_APPEND_CAUSAL_GQA, &gp);
+  if (select_gqa(gp) == GqaKernel::Decode) {
+    record(records, cap, n, 2,
+           llmi_hip_kernel_name(LLMI_HIP_OP_KV_APPEND_CAUSAL_GQA, &gp, 0), 1);
+    for (unsigned i = 1; i < pairLaunches; ++i)
+      record(records, cap, n, 2,
+             llmi_hip_kernel_name(LLMI_HIP_OP_KV_APPEND_CAUSAL_GQA, &gp, i));
+  } else {
+    record(records, cap, n, 1,
+           llmi_hip_kernel_name(LLMI_HIP_OP_KV_APPEND_CAUSAL_GQA, &gp, 0));
+    record(records, cap, n, 2,
+           llmi_hip_kernel_name(LLMI_HIP_OP_KV_APPEND_CAUSAL_GQA, &gp, 1));
+  }
   if (count)
     *count = n;
 
@@ -267,10 +274,8 @@ int llmi_hip_session_step(llmi_hip_session *s, unsigned tokens, const float *dq,
   int st = llmi_hip_delta_update(dq, dk, dv, beta, decay, s->state, delta_out, dp,
                                  s->ws, s->wsBytes, s->stream);
   if (st == LLMI_HIP_OK)
-    st = llmi_hip_kv_append(k, v, s->kcache, s->vcache, cp, s->stream);
-  if (st == LLMI_HIP_OK)
-    st = llmi_hip_causal_gqa(q, s->kcache, s->vcache, gqa_out, gp, s->ws,
-                             s->wsBytes, s->stream);
+    st = llmi_hip_kv_append_causal_gqa(q, k, v, s->kcache, s->vcache, gqa_out, gp,
+                                       s->ws, s->wsBytes, s->stream);
   if (st == LLMI_HIP_OK) {
     hipError_t e = hipStreamSynchronize(s->stream);
     if (e != hipSuccess)

@@ -38,11 +38,8 @@ def _require(t: torch.Tensor, dtype: torch.dtype, name: str) -> None:
 
 
 def workspace(nbytes: int, device: torch.device | None = None) -> torch.Tensor:
-    """A zero-initialised workspace of at least nbytes, reused per device.
-
-    The kernels leave their tickets at zero after every call, so one
-    allocation serves all later calls on the same stream.
-    """
+    """A workspace of at least nbytes, reused per device (calls on one
+    stream are ordered, so they can share it)."""
     dev = torch.device("cuda", torch.cuda.current_device()) if device is None else device
     key = dev.index if dev.index is not None else torch.cuda.current_device()
     ws = _workspaces.get(key)
@@ -106,6 +103,32 @@ def causal_gqa(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
     _lib.check(lib.llmi_hip_causal_gqa(_ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(out),
                                        p, _ptr(ws), ws.numel() if ws is not None else 0,
                                        _stream()))
+    return out
+
+
+def kv_append_causal_gqa(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                         k_cache: torch.Tensor, v_cache: torch.Tensor, past: int,
+                         out: torch.Tensor | None = None) -> torch.Tensor:
+    """KvAppend(k, v) at row `past` then CausalGqa(q), in one call (one launch
+    for T == 1: the decode kernel appends while it attends)."""
+    for t, n in ((q, "q"), (k, "k"), (v, "v"), (k_cache, "k_cache"), (v_cache, "v_cache")):
+        _require(t, torch.float16, n)
+    if q.dim() != 3 or k.dim() != 3 or k.shape != v.shape or k_cache.shape != v_cache.shape \
+            or k.shape[1:] != k_cache.shape[1:] or q.shape[0] != k.shape[0] \
+            or q.shape[2] != k_cache.shape[2]:
+        raise ValueError("KvAppend/CausalGqa operands do not match the cache layout")
+    if past + q.shape[0] > k_cache.shape[0]:
+        raise ValueError("past + tokens exceeds the cache capacity")
+    if out is None:
+        out = torch.empty_like(q)
+    _require(out, torch.float16, "out")
+    lib = _lib.load()
+    p = gqa_params(q, k_cache, past)
+    need = lib.llmi_hip_gqa_workspace_bytes(p)
+    ws = workspace(need, q.device) if need else None
+    _lib.check(lib.llmi_hip_kv_append_causal_gqa(
+        _ptr(q), _ptr(k), _ptr(v), _ptr(k_cache), _ptr(v_cache), _ptr(out), p, _ptr(ws),
+        ws.numel() if ws is not None else 0, _stream()))
     return out
 
 
@@ -189,6 +212,28 @@ def bind_causal_gqa(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tenso
     args = (_ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(out), p, _ptr(ws),
             ws.numel() if ws is not None else 0, _stream())
     b = Bound(lib.llmi_hip_causal_gqa, args, kernel_names(_lib.OP_CAUSAL_GQA, p)[0])
+    b._keep = ws
+    return b
+
+
+def bind_kv_append_causal_gqa(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                              k_cache: torch.Tensor, v_cache: torch.Tensor,
+                              out: torch.Tensor, past: int) -> Bound:
+    for t, n in ((q, "q"), (k, "k"), (v, "v"), (k_cache, "k_cache"), (v_cache, "v_cache"),
+                 (out, "out")):
+        _require(t, torch.float16, n)
+    if q.dim() != 3 or k.shape != v.shape or k_cache.shape != v_cache.shape or \
+            k.shape[1:] != k_cache.shape[1:] or q.shape[0] != k.shape[0] or \
+            out.shape != q.shape or past + q.shape[0] > k_cache.shape[0]:
+        raise ValueError("KvAppend/CausalGqa operands do not match the cache")
+    lib = _lib.load()
+    p = gqa_params(q, k_cache, past)
+    need = lib.llmi_hip_gqa_workspace_bytes(p)
+    ws = workspace(need, q.device) if need else None
+    args = (_ptr(q), _ptr(k), _ptr(v), _ptr(k_cache), _ptr(v_cache), _ptr(out), p, _ptr(ws),
+            ws.numel() if ws is not None else 0, _stream())
+    names = kernel_names(_lib.OP_KV_APPEND_CAUSAL_GQA, p)
+    b = Bound(lib.llmi_hip_kv_append_causal_gqa, args, "+".join(names))
     b._keep = ws
     return b
 

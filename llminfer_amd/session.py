@@ -122,8 +122,12 @@ class HipSession:
             self._h, T, dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), beta.data_ptr(),
             decay.data_ptr(), delta_out.data_ptr(), q.data_ptr(), k.data_ptr(),
             v.data_ptr(), gqa_out.data_ptr(), recs, len(recs), C.byref(n)))
-        plan = [{"op_index": int(recs[i].op_index), "kernel": recs[i].kernel.decode()}
-                for i in range(min(n.value, len(recs)))]
+        plan = []
+        for i in range(min(n.value, len(recs))):
+            rec = {"op_index": int(recs[i].op_index), "kernel": recs[i].kernel.decode()}
+            if recs[i].fused_op_index != _lib.NO_FUSED_OP:
+                rec["fused_op_index"] = int(recs[i].fused_op_index)
+            plan.append(rec)
         return StepResult(self.past, delta_out, gqa_out, plan)
 
 

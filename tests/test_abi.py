@@ -96,14 +96,20 @@ def test_append_rejects_index_overflow():
 
 
 @pytest.mark.parametrize("T,P,names", [
-    (1, 4096, ["gqaDecodeSplitK"]),
+    (1, 4096, ["gqaDecodeSplitK", "gqaDecodeMerge"]),
     (1, 0, ["gqaDecodeSplitK"]),
     (2, 0, ["gqaPrefillMfma"]),
     (2048, 2048, ["gqaPrefillMfma"]),
 ])
 def test_plan_records_gqa(T, P, names):
     from llminfer_amd import ops
-    assert ops.kernel_names(_lib.OP_CAUSAL_GQA, _lib.GqaParams(T, 16, 4, 256, P)) == names
+    got = ops.kernel_names(_lib.OP_CAUSAL_GQA, _lib.GqaParams(T, 16, 4, 256, P))
+    # The split-K decode merges its splits in a second launch or inside its
+    # last workgroup, depending on the build's merge mode; one split needs no merge.
+    if names[-1] == "gqaDecodeMerge":
+        assert got in (names, names[:1])
+    else:
+        assert got == names
 
 
 def test_plan_records_generic_shapes():

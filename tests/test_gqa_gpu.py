@@ -12,7 +12,7 @@ import torch
 
 import oracle
 from llminfer_amd import _lib, ops
-from tests.conftest import torch_to_u16, u16_to_torch
+from tests.conftest import p_rounding_bound, torch_to_u16, u16_to_torch
 
 pytestmark = pytest.mark.gpu
 TOL = 2e-3
@@ -43,7 +43,7 @@ def test_decode_parity(gpu, shape, past):
     x = oracle.make_gqa_inputs(100 + past, 1, hq, hkv, d, past, capacity=past + 9)
     _check(_run(x, gpu), oracle.gqa_dense_f64(x.q, x.k_cache, x.v_cache, past))
     names = ops.kernel_names(_lib.OP_CAUSAL_GQA, _lib.GqaParams(1, hq, hkv, d, past))
-    assert names == ["gqaDecodeSplitK"]
+    assert names in (["gqaDecodeSplitK"], ["gqaDecodeSplitK", "gqaDecodeMerge"])
 
 
 def test_decode_cfg2_with_append(gpu):
@@ -108,23 +108,6 @@ def test_prefill_cfg3_sampled_rows(gpu):
         _check(got[t], want)
 
 
-def _p_rounding_bound(q, k, v, P):
-    """First-order bound of rounding every softmax weight to fp16 before the
-    PV product: |dO| <= u * sum_j p_j |v_j| / l with u = 2^-11 (fp16 unit
-    roundoff). Zero for kernels that keep P in fp32."""
-    qf, kf, vf = (oracle.f16_to_f32(a).astype(np.float64) for a in (q, k, v))
-    T, hq, d = q.shape
-    g = hq // k.shape[1]
-    bound = np.zeros((T, hq, d))
-    for t in range(T):
-        for h in range(hq):
-            n = P + t + 1
-            s = kf[:n, h // g] @ qf[t, h] / np.sqrt(d)
-            p = np.exp(s - s.max())
-            bound[t, h] = 2.0 ** -11 * (p @ np.abs(vf[:n, h // g])) / p.sum()
-    return bound
-
-
 @pytest.mark.parametrize("case", [(19, 4, 2, 12, 0), (7, 4, 2, 256, 33)])
 def test_reference_kernel_cases(gpu, case):
     """tests/FlashAttentionTest.mm:108-109 with its LCG inputs. Its tolerance
@@ -144,9 +127,51 @@ def test_reference_kernel_cases(gpu, case):
     got = oracle.f16_to_f32(torch_to_u16(out)).astype(np.float64)
     want = oracle.gqa_dense_f64(q, k, v, P)
     kernel = ops.kernel_names(_lib.OP_CAUSAL_GQA, _lib.GqaParams(T, hq, hkv, d, P))[0]
-    extra = _p_rounding_bound(q, k, v, P) if kernel == "gqaPrefillMfma" else 0.0
+    extra = p_rounding_bound(q, k, v, P) if kernel == "gqaPrefillMfma" else 0.0
     assert np.all(np.abs(got - want) <= 2e-4 + 5e-4 * np.abs(want) + extra)
     assert np.max(np.abs(got - want)) <= TOL
+
+
+@pytest.mark.parametrize("T,past", [(1, 0), (1, 4096), (1, 33), (3, 100), (64, 640),
+                                    (65, 17), (200, 300)])
+def test_fused_append_attention(gpu, T, past):
+    """llmi_hip_kv_append_causal_gqa: the cache rows it writes are the bytes
+    KvAppend writes, and the attention equals the oracle on the appended
+    cache (one decode launch for T == 1, append + prefill for T > 1, the
+    reference's kernel choice: MetalExecutionPlan.cpp:528-548)."""
+    print(f"fused append+attention T={T} past={past}", flush=True)
+    x = oracle.make_gqa_inputs(300 + T + past, T, 16, 4, 256, past, capacity=past + T + 5)
+    kc = u16_to_torch(x.k_cache, gpu)
+    vc = u16_to_torch(x.v_cache, gpu)
+    kc[past:] = 0
+    vc[past:] = 0
+    out = ops.kv_append_causal_gqa(u16_to_torch(x.q, gpu), u16_to_torch(x.k_new, gpu),
+                                   u16_to_torch(x.v_new, gpu), kc, vc, past)
+    torch.cuda.synchronize()
+    assert np.array_equal(torch_to_u16(kc), x.k_cache)
+    assert np.array_equal(torch_to_u16(vc), x.v_cache)
+    got = oracle.f16_to_f32(torch_to_u16(out)).astype(np.float64)
+    _check(got, oracle.gqa_dense_f64(x.q, x.k_cache, x.v_cache, past))
+    names = ops.kernel_names(_lib.OP_KV_APPEND_CAUSAL_GQA,
+                             _lib.GqaParams(T, 16, 4, 256, past))
+    if T == 1:
+        assert names in (["gqaDecodeSplitK"], ["gqaDecodeSplitK", "gqaDecodeMerge"])
+    else:
+        assert names == ["kvAppend", "gqaPrefillMfma"]
+    # The unfused call on the same (now appended) cache gives the same bits.
+    if T == 1:
+        ref = ops.causal_gqa(u16_to_torch(x.q, gpu), kc, vc, past)
+        torch.cuda.synchronize()
+        assert torch.equal(ref, out)
+
+
+@pytest.mark.parametrize("P", [0, 1, 255, 4096, 32768])
+def test_decode_split_counts(gpu, P):
+    """Decode over the split plans the launcher picks (1 split at small P,
+    up to the maximum at 32K), all against the dense oracle."""
+    print(f"decode split plan P={P}", flush=True)
+    x = oracle.make_gqa_inputs(900 + P, 1, 16, 4, 256, P)
+    _check(_run(x, gpu), oracle.gqa_dense_f64(x.q, x.k_cache, x.v_cache, P))
 
 
 def test_cache_append_bit_exact(gpu):
