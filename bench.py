@@ -17,8 +17,13 @@ HBM rather than from the 256 MB Infinity Cache.
 Timing. Warmup W steps, synchronize, then a spin kernel holds the GPU while
 the host enqueues all K steps, so the GPU runs them back to back and the
 measurement is device time, not Python launch latency. Start/end HIP events
-bracket exactly the K steps (ms_per_step), and an event pair on the same
-stream brackets every launch of the dominant kernel (roofline.achieved).
+on the launch stream bracket exactly the K steps (ms_per_step). The headline
+step is one op -- the fused append+attention call -- so the same time is
+the op's time per call for the roofline; the kernels it launches and their
+rocprofv3 durations are listed in profiles/. (Events around every single
+launch were avoided: each pair adds several microseconds to a kernel of
+ten.) For the other configurations the dominant op is also timed in its own
+back-to-back loop the same way.
 
 `roofline`: algorithmic bytes of one decode launch (K and V rows [0, P+1)
 plus q and out -- the reference cost model's traffic for CausalGqa,
@@ -133,15 +138,25 @@ def time_cpu(fn, budget_s: float, min_runs: int = 1) -> tuple[float, int]:
 class Workload:
     """A repeatable step on resident device inputs.
 
-    launch(i, marks) enqueues step i; marks maps a kernel label to an
-    (event_a, event_b) pair to record around that launch, or is empty.
+    op(label, i) enqueues one op of step i (one C-ABI call: one or two
+    launches); launch(i) enqueues the whole step, its ops in graph order.
+    `dominant` labels the op the roofline is computed for.
     """
     name = ""
     tokens = 1
-    dominant = ""
+    dominant = "gqa"
+    labels: tuple = ("gqa",)
     bound = "hbm"
 
-    def launch(self, i: int, marks: dict) -> None:
+    def op(self, label: str, i: int) -> None:
+        raise NotImplementedError
+
+    def launch(self, i: int) -> None:
+        for label in self.labels:
+            self.op(label, i)
+
+    def kernels(self) -> str:
+        """Kernel names of the dominant op (plan-record names)."""
         raise NotImplementedError
 
     def work(self, i: int) -> int:  # algorithmic bytes or flops of the dominant launch
@@ -162,7 +177,6 @@ def _randn16(gen, shape, dev):
 class GqaDecode(Workload):
     """configs[1] (and the GQA half of configs[4]): KvAppend + split-K decode."""
     bound = "hbm"
-    dominant = "gqaDecodeSplitK"
 
     def __init__(self, dev, seed=2, past=4096, cap=8192, sets=32, hq=16, hkv=4, d=256):
         import torch
@@ -180,16 +194,12 @@ class GqaDecode(Workload):
         self.att = [ops.bind_kv_append_causal_gqa(self.q, self.kn, self.vn, self.kc[s],
                                                   self.vc[s], self.out, past)
                     for s in range(sets)]
-        assert self.att[0].what.split("+")[0] == self.dominant, self.att[0].what
 
-    def launch(self, i, marks):
-        s = i % self.sets
-        m = marks.get("gqa")
-        if m:
-            m[0].record()
-        self.att[s]()
-        if m:
-            m[1].record()
+    def op(self, label, i):
+        self.att[i % self.sets]()
+
+    def kernels(self):
+        return self.att[0].what
 
     def work(self, i):
         return gqa_bytes(1, self.P, self.hq, self.hkv, self.d) + append_bytes(1, self.hkv, self.d)
@@ -235,7 +245,7 @@ class GqaDecode(Workload):
 class GqaPrefill(Workload):
     """configs[0] (T=128, P=0) and configs[2] (T=2048 after P=2048)."""
     bound = "mfma"
-    dominant = "gqaPrefillMfma"
+    labels = ("append", "gqa")
 
     def __init__(self, dev, T, P, cap, seed, hq=16, hkv=4, d=256):
         import torch
@@ -252,16 +262,12 @@ class GqaPrefill(Workload):
         self.out = torch.empty_like(self.q)
         self.app = ops.bind_kv_append(self.kn, self.vn, self.kc, self.vc, P)
         self.att = ops.bind_causal_gqa(self.q, self.kc, self.vc, self.out, P)
-        assert self.att.what == self.dominant, self.att.what
 
-    def launch(self, i, marks):
-        self.app()
-        m = marks.get("gqa")
-        if m:
-            m[0].record()
-        self.att()
-        if m:
-            m[1].record()
+    def op(self, label, i):
+        (self.app if label == "append" else self.att)()
+
+    def kernels(self):
+        return self.att.what
 
     def work(self, i):
         return gqa_flops(self.T, self.P, self.hq, self.d)
@@ -316,6 +322,8 @@ def _delta_inputs(g, dev, T, hk, dk, hv, dv):
 class DeltaPrefill(Workload):
     """DeltaUpdate over 1024 tokens from a zero state."""
     bound = "hbm"
+    dominant = "delta"
+    labels = ("delta",)
 
     def __init__(self, dev, T=1024, hk=16, dk=128, hv=32, dv=128, seed=4):
         import torch
@@ -328,17 +336,14 @@ class DeltaPrefill(Workload):
         self.state0 = torch.zeros((hv, dk, dv), dtype=torch.float32, device=dev)
         self.state = self.state0.clone()
         self.out = torch.empty_like(self.v)
-        self.op = ops.bind_delta_update(self.q, self.k, self.v, self.beta, self.decay,
-                                        self.state, self.out)
-        self.dominant = self.op.what
+        self.upd = ops.bind_delta_update(self.q, self.k, self.v, self.beta, self.decay,
+                                         self.state, self.out)
 
-    def launch(self, i, marks):
-        m = marks.get("delta")
-        if m:
-            m[0].record()
-        self.op()
-        if m:
-            m[1].record()
+    def op(self, label, i):
+        self.upd()
+
+    def kernels(self):
+        return self.upd.what
 
     def work(self, i):
         return delta_bytes(self.T, self.hk, self.dk, self.hv, self.dv)
@@ -353,7 +358,7 @@ class DeltaPrefill(Workload):
         import torch
         torch.cuda.synchronize()
         self.state.copy_(self.state0)
-        self.op()
+        self.upd()
         torch.cuda.synchronize()
         q, k, beta, decay = (host_f32(t) for t in (self.q, self.k, self.beta, self.decay))
         v = host_u16(self.v)
@@ -377,7 +382,7 @@ class HybridDecode(Workload):
     32 positions per layer; `layers` independent layer pairs rotate so that
     the 134 MB of K/V a decode reads come from HBM."""
     bound = "hbm"
-    dominant = "gqaDecodeSplitK"
+    labels = ("delta", "gqa")
 
     def __init__(self, dev, past=32768, positions=32, layers=4, seed=5,
                  hq=16, hkv=4, d=256, hk=16, dk=128, hv=32, dv=128):
@@ -412,26 +417,17 @@ class HybridDecode(Workload):
                                           self.state[l], self.dout),
                     ops.bind_kv_append_causal_gqa(x["q"], x["kn"], x["vn"], self.kc[l],
                                                   self.vc[l], self.gout, P))
-        assert self.ops[0, 0][1].what.split("+")[0] == self.dominant
         self.tokens = 1
 
     def pos(self, i):
         return i % self.L, (i // self.L) % self.n
 
-    def launch(self, i, marks):
+    def op(self, label, i):
         delta, att = self.ops[self.pos(i)]
-        m = marks.get("delta")
-        if m:
-            m[0].record()
-        delta()
-        if m:
-            m[1].record()
-        m = marks.get("gqa")
-        if m:
-            m[0].record()
-        att()
-        if m:
-            m[1].record()
+        (delta if label == "delta" else att)()
+
+    def kernels(self):
+        return self.ops[0, 0][1].what
 
     def work(self, i):
         _, j = self.pos(i)
@@ -487,62 +483,55 @@ def sleep_cycles_per_ms() -> float:
     return n / max(ms, 1e-3)
 
 
-def run_timed(w: Workload, steps: int, warmup: int, labels: list[str], cyc_per_ms: float):
-    """Returns (ms_per_step, {label: [kernel ms per launch]}, host enqueue ms/step).
+def run_timed(fn, steps: int, warmup: int, cyc_per_ms: float) -> tuple[float, float]:
+    """(ms per call, host enqueue ms per call) of fn(i), i = warmup .. warmup+steps-1.
 
-    A spin kernel holds the GPU while the host enqueues the K steps (with
-    their event records), so the events time the GPU, not Python. If the
-    host still fell behind the GPU (its enqueue outlasted the hold), the
-    measurement is repeated with a longer hold.
+    A spin kernel holds the GPU while the host enqueues the K calls, so the
+    two events that bracket exactly those K calls time the GPU running them
+    back to back, not Python. If the host still fell behind (its enqueue
+    outlasted the hold), the measurement is repeated with a longer hold.
     """
     import torch
     for i in range(warmup):
-        w.launch(i, {})
+        fn(i)
     torch.cuda.synchronize()
-    # Host enqueue cost per step, event records included.
-    probe = {l: (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-             for l in labels}
     n = min(8, max(1, warmup))
     t0 = time.perf_counter()
     for i in range(n):
-        w.launch(i, probe)
+        fn(i)
     host_ms = (time.perf_counter() - t0) * 1e3 / n
     torch.cuda.synchronize()
 
     hold_ms = 10.0 + 3.0 * host_ms * steps
     for _attempt in range(4):
-        ev = {l: [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-                  for _ in range(steps)] for l in labels}
         start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         torch.cuda.synchronize()
         torch.cuda._sleep(int(min(hold_ms, 8000.0) * cyc_per_ms))
         t0 = time.perf_counter()
         start.record()
         for i in range(steps):
-            w.launch(warmup + i, {l: ev[l][i] for l in labels})
+            fn(warmup + i)
         end.record()
         enq_ms = (time.perf_counter() - t0) * 1e3
         torch.cuda.synchronize()
         if enq_ms < 0.8 * hold_ms or hold_ms >= 8000.0:
             break
         hold_ms = 2.0 * enq_ms + 10.0
-    total = start.elapsed_time(end)
-    per = {l: [a.elapsed_time(b) for a, b in ev[l]] for l in labels}
-    return total / steps, per, enq_ms / steps
+    return start.elapsed_time(end) / steps, enq_ms / steps
 
 
-def roofline(w: Workload, kern_ms: list[float], warmup: int, traffic) -> dict:
+def roofline(w: Workload, op_ms: float, steps: int, warmup: int, traffic) -> dict:
+    """Roofline of the dominant op from its back-to-back time per call."""
     import statistics
-    avg_s = statistics.fmean(kern_ms) * 1e-3
-    work = statistics.fmean(w.work(warmup + i) for i in range(len(kern_ms)))
+    avg_s = op_ms * 1e-3
+    work = statistics.fmean(w.work(warmup + i) for i in range(steps))
     if w.bound == "hbm":
         achieved, peak, unit = work / avg_s / 1e9, HBM_PEAK_GBS, "GB/s"
     else:
         achieved, peak, unit = work / avg_s / 1e12, MFMA_F16_PEAK_TFS, "TFLOP/s"
     return {"bound": w.bound, "achieved": round(achieved, 2), "peak": peak, "unit": unit,
             "frac": round(achieved / peak, 4), "traffic": traffic,
-            "kernel": w.dominant, "kernel_us_avg": round(avg_s * 1e6, 3),
-            "kernel_us_p50": round(sorted(kern_ms)[len(kern_ms) // 2] * 1e3, 3),
+            "kernel": w.kernels(), "kernel_us_avg": round(avg_s * 1e6, 3),
             "work_per_launch": int(work),
             "work_unit": "bytes" if w.bound == "hbm" else "flop"}
 
@@ -592,8 +581,10 @@ def main(argv=None) -> int:
     # ---- headline: configs[1]
     w = GqaDecode(dev)
     log(f"headline {w.name}: warmup {args.warmup}, steps {args.steps}")
-    ms, per, host_ms = run_timed(w, args.steps, args.warmup, ["gqa"], cyc)
-    rl = roofline(w, per["gqa"], args.warmup, load_traffic(w.name))
+    ms, host_ms = run_timed(w.launch, args.steps, args.warmup, cyc)
+    # The headline step is the dominant op alone (one fused append+attention
+    # call), so its back-to-back time is the op's time.
+    rl = roofline(w, ms, args.steps, args.warmup, load_traffic(w.name))
     log(f"headline {ms * 1e3:.2f} us/step, kernel {rl['kernel_us_avg']} us, "
         f"{rl['achieved']} GB/s ({rl['frac']:.1%})")
     result = {
@@ -616,21 +607,22 @@ def main(argv=None) -> int:
         extra = {}
         steps = max(10, min(args.steps, 50))
         builders = [
-            ("cfg0_gqa_prefill_128", lambda: GqaPrefill(dev, 128, 0, 128, seed=1), ["gqa"]),
-            ("cfg2_gqa_chunked_prefill", lambda: GqaPrefill(dev, 2048, 2048, 4096, seed=3),
-             ["gqa"]),
-            ("cfg3_delta_prefill_1024", lambda: DeltaPrefill(dev), ["delta"]),
-            ("cfg4_hybrid_decode_32k", lambda: HybridDecode(dev), ["gqa", "delta"]),
+            ("cfg0_gqa_prefill_128", lambda: GqaPrefill(dev, 128, 0, 128, seed=1)),
+            ("cfg2_gqa_chunked_prefill", lambda: GqaPrefill(dev, 2048, 2048, 4096, seed=3)),
+            ("cfg3_delta_prefill_1024", lambda: DeltaPrefill(dev)),
+            ("cfg4_hybrid_decode_32k", lambda: HybridDecode(dev)),
         ]
-        for key, make, labels in builders:
+        for key, make in builders:
             x = make()
             log(f"{key}: {x.name}")
             n = steps if key != "cfg4_hybrid_decode_32k" else max(steps, 128)
-            ms_x, per_x, _ = run_timed(x, n, min(args.warmup, 10), labels, cyc)
+            wu = min(args.warmup, 10)
+            ms_x, _ = run_timed(x.launch, n, wu, cyc)
+            op_ms = {l: run_timed(lambda i, l=l: x.op(l, i), n, wu, cyc)[0] for l in x.labels}
             entry = {"config": x.config(), "us_per_step": round(ms_x * 1e3, 3),
                      "tokens_per_s": round(x.tokens * 1e3 / ms_x, 1), "steps": n,
-                     "roofline": roofline(x, per_x[labels[0]], min(args.warmup, 10),
-                                          load_traffic(x.name))}
+                     "op_us": {l: round(v * 1e3, 3) for l, v in op_ms.items()},
+                     "roofline": roofline(x, op_ms[x.dominant], n, wu, load_traffic(x.name))}
             if x.bound == "mfma":
                 entry["hbm_frac"] = None
             if isinstance(x, DeltaPrefill):
@@ -638,12 +630,10 @@ def main(argv=None) -> int:
                 entry["mfma_frac_recurrent_flops"] = round(
                     delta_flops(x.T, x.hv, x.dk, x.dv) / kern_s / 1e12 / MFMA_F16_PEAK_TFS, 5)
             if isinstance(x, HybridDecode):
-                import statistics
-                entry["delta_kernel_us_avg"] = round(statistics.fmean(per_x["delta"]) * 1e3, 3)
                 hk, dk, hv, dv = x.dshape
                 entry["delta_hbm_frac"] = round(
-                    delta_bytes(1, hk, dk, hv, dv) / (entry["delta_kernel_us_avg"] * 1e-6)
-                    / 1e9 / HBM_PEAK_GBS, 4)
+                    delta_bytes(1, hk, dk, hv, dv) / (op_ms["delta"] * 1e-3) / 1e9
+                    / HBM_PEAK_GBS, 4)
             if not args.no_cpu:
                 entry["cpu_baseline"] = x.cpu(args.cpu_seconds / 2)
             log(f"{key}: {entry['us_per_step']} us/step, kernel "

@@ -1,27 +1,447 @@
-// Gated delta rule, chunk-wise (WY) prefill. Not yet enabled: the C ABI
-// routes T > 1 to the register-resident recurrent kernel until this path
-// passes its parity tests.
+// Gated delta rule, chunk-wise (WY / UT-transform) form: the DeltaNet
+// prefill.
+//
+// Same result as the token recurrence of graphDeltaUpdate / updateDeltaColumn
+// (Graph.metal:146-170, Reference.metal:182-197), which walks the tokens one
+// by one. The published chunk algorithm (Yang, Kautz, Hatamizadeh, "Gated
+// Delta Networks", arXiv:2412.06464; Yang et al., "Parallelizing Linear
+// Transformers with the Delta Rule over Sequence Length", arXiv:2406.06484)
+// splits the tokens into chunks of C = 64. With g the cumulative log decay
+// inside a chunk, per chunk and value head:
+//
+//   A[t][s] = beta_t e^(g_t - g_s) k_t.k_s  (s < t),  T = (I + A)^-1
+//   M[t][s] = e^(g_t - g_s) q_t.k_s        (s <= t)
+//   X = diag(beta) V - diag(beta e^g) K S    U = T X
+//   Y = diag(e^g) Q S + M U                  S <- e^(g_C) S + K^T diag(e^(g_C - g)) U
+//
+// Two launches:
+//
+//  * deltaChunkPrep, grid (chunk, key head): everything that does not depend
+//    on the state, for every chunk at once -- the Gram matrices K K^T and
+//    Q K^T on fp16 MFMA (v_mfma_f32_32x32x16_f16), then per value head the
+//    decay weighting, T by forward substitution in fp32 (one lane per column
+//    of T) and M. Written to the workspace: T, M, g, beta per (chunk, head).
+//
+//  * deltaChunkScan, grid (value head, 32-column dv tile): walks the chunks
+//    in order with the state tile S [dk x 32] resident in MFMA accumulators.
+//    Every product that involves the state (K S, Q S, T X, M U, K^T Z) runs
+//    on fp16 MFMA in a split form: x = hi + lo 2^-11 with hi = fp16(x),
+//    lo = fp16((x - hi) 2^11), a.b ~ ah.bh + (ah.bl + al.bh) 2^-11, the
+//    cross terms in a second fp32 accumulator -- 22 significant bits per
+//    operand. A plain fp16 product leaves the fp32
+//    state ~8e-4 relative off the recurrence after 1024 tokens; the split
+//    form ~1e-5 (measured on the cfg4 shapes), well inside the 1e-3 bound.
+//    The Gram matrices only feed T and M and stay plain fp16.
+//
+// Decays are linear at the op boundary (Graph.metal:143). The cumulative
+// log decay is summed, and differenced, in double: log(0) is clamped to -1e4
+// (e^-1e4 = 0), and in fp32 a difference of two sums near -1e4 would keep
+// only ~1e-3 absolute precision. Only non-positive differences are
+// exponentiated; the scan receives the weights e^(g_t) and e^(g_C - g_t)
+// ready-made.
 #include "hip_common.hpp"
 #include "kernels.hpp"
 
-namespace llmi {
-
-bool delta_chunked_supported(const DeltaShape &) { return false; }
-
-size_t delta_chunked_workspace_bytes(const DeltaShape &) { return 0; }
-
-hipError_t launch_delta_chunked(const float *, const float *, const uint16_t *,
-                                const float *, const float *, float *,
-                                uint16_t *, void *, const DeltaShape &,
-                                hipStream_t) {
-  return hipErrorNotSupported;
-}
-
-} // namespace llmi
-
 #include "capi_internal.hpp"
 
+#include <math.h>
+
 namespace llmi {
-unsigned delta_chunked_dispatches() { return 1; }
-const char *delta_chunked_kernel_name(unsigned) { return "deltaChunkedWy"; }
+namespace {
+
+constexpr int C = 64;        // chunk length
+constexpr int DK = 128;      // key dimension handled by these kernels
+constexpr int DT = 32;       // dv columns per scan workgroup
+constexpr int KST = DK + 8;  // fp16 stride of [token][dk] rows
+constexpr int CST = C + 8;   // fp16 stride of [*][token] rows
+constexpr int kMaxRatio = 4; // value heads per key head handled by one prep workgroup
+
+// Workspace record per (chunk, value head): T [C][C], M [C][C], then per
+// token e^(g_t), e^(g_C - g_t) and beta_t.
+constexpr size_t kPrepFloats = 2 * C * C + 3 * C;
+constexpr size_t kRecEg = 2 * C * C, kRecEz = kRecEg + C, kRecBeta = kRecEz + C;
+
+// --------------------------------------------------------------- prep
+
+__global__ __launch_bounds__(256, 1) void delta_prep_kernel(
+    const float *__restrict__ q, const float *__restrict__ k,
+    const float *__restrict__ beta, const float *__restrict__ decay,
+    float *__restrict__ prep, unsigned T, unsigned Hk, unsigned Hv) {
+  const unsigned c = blockIdx.x, kh = blockIdx.y;
+  const unsigned R = Hv / Hk;
+  const unsigned t0 = c * C, n = min((unsigned)C, T - t0);
+  const unsigned tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+  const unsigned r = lane & 31u, hh = lane >> 5;
+
+  __shared__ __attribute__((aligned(16))) half_t sK[C * KST], sQ[C * KST];
+  __shared__ __attribute__((aligned(16))) float sKK[C * C], sQK[C * C];
+  __shared__ __attribute__((aligned(16))) float sA[kMaxRatio][C * C];
+  __shared__ double sG[kMaxRatio][C];
+  __shared__ float sB[kMaxRatio][C];
+
+  // Keys and queries of the chunk as fp16 (rows past the end are zero).
+  for (unsigned i = tid; i < C * DK / 4; i += 256) {
+    const unsigned t = i / (DK / 4), d4 = (i % (DK / 4)) * 4;
+    float4_t kv{0.0f, 0.0f, 0.0f, 0.0f}, qv{0.0f, 0.0f, 0.0f, 0.0f};
+    if (t < n) {
+      const size_t off = ((size_t)(t0 + t) * Hk + kh) * DK + d4;
+      kv = *reinterpret_cast<const float4_t *>(k + off);
+      qv = *reinterpret_cast<const float4_t *>(q + off);
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      sK[t * KST + d4 + e] = (half_t)kv[e];
+      sQ[t * KST + d4 + e] = (half_t)qv[e];
+    }
+  }
+  // Cumulative log decay and beta of each value head of this key head:
+  // wave w scans head w (padding tokens: decay 1, beta 0).
+  if (wave < R) {
+    const unsigned h = kh * R + wave, t = lane;
+    const float a = t < n ? decay[(size_t)(t0 + t) * Hv + h] : 1.0f;
+    const float b = t < n ? beta[(size_t)(t0 + t) * Hv + h] : 0.0f;
+    double g = a > 0.0f ? (double)logf(a) : -1.0e4;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const double up = __shfl_up(g, off);
+      if (lane >= (unsigned)off)
+        g += up;
+    }
+    sG[wave][t] = g;
+    sB[wave][t] = b;
+  }
+  __syncthreads();
+
+  // K K^T and Q K^T, four 32x32 tiles each; wave w takes tiles w and w + 4.
+#pragma unroll
+  for (int rep = 0; rep < 2; ++rep) {
+    const int tile = wave + 4 * rep;
+    const half_t *a = tile < 4 ? sK : sQ;
+    const int mt = (tile % 4) / 2, nt = tile % 2;
+    float16_t acc = float16_t{0};
+#pragma unroll
+    for (int ks = 0; ks < DK / 16; ++ks)
+      acc = mfma32x32x16(load8(a + (32 * mt + r) * KST + 16 * ks + 8 * hh),
+                         load8(sK + (32 * nt + r) * KST + 16 * ks + 8 * hh), acc);
+    float *dst = tile < 4 ? sKK : sQK;
+#pragma unroll
+    for (int v = 0; v < 16; ++v)
+      dst[(32 * mt + mfma_c_row(v, hh)) * C + 32 * nt + r] = acc[v];
+  }
+  __syncthreads();
+
+  // Decay weighting: A (to LDS) and M, g, beta (to the workspace).
+  for (unsigned hr = 0; hr < R; ++hr) {
+    float *rec = prep + ((size_t)c * Hv + kh * R + hr) * kPrepFloats;
+    for (unsigned i = tid; i < C * C; i += 256) {
+      const unsigned t = i / C, s = i % C;
+      const float e = s <= t ? expf((float)(sG[hr][t] - sG[hr][s])) : 0.0f;
+      sA[hr][i] = s < t ? sB[hr][t] * e * sKK[i] : 0.0f;
+      rec[C * C + i] = e * sQK[i];
+    }
+    if (tid < C) {
+      rec[kRecEg + tid] = expf((float)sG[hr][tid]);
+      rec[kRecEz + tid] = expf((float)(sG[hr][C - 1] - sG[hr][tid]));
+      rec[kRecBeta + tid] = sB[hr][tid];
+    }
+  }
+  __syncthreads();
+
+  // T = (I + A)^-1 by forward substitution: lane j of wave w owns column j
+  // of value head w's T, T[t][j] = delta_tj - sum_{s<t} A[t][s] T[s][j].
+  if (wave < R) {
+    const float *A = sA[wave];
+    const unsigned j = lane;
+    float col[C];
+#pragma unroll
+    for (int t = 0; t < C; ++t) {
+      float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int s = 0; s < t; ++s)
+        acc[s & 3] = fmaf(A[t * C + s], col[s], acc[s & 3]);
+      const float sum = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+      col[t] = (unsigned)t == j ? 1.0f : ((unsigned)t > j ? -sum : 0.0f);
+    }
+    float *rec = prep + ((size_t)c * Hv + kh * R + wave) * kPrepFloats;
+#pragma unroll
+    for (int t = 0; t < C; ++t)
+      rec[t * C + j] = col[t];
+  }
+}
+
+// --------------------------------------------------------------- scan
+
+// Split a float4 into hi/lo fp16 and store them at dst_hi/dst_lo (4 halves).
+__device__ __forceinline__ void store_split4(half_t *hi, half_t *lo, float4_t x) {
+  half4_t h, l;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    half_t a, b;
+    split_f16(x[e], a, b);
+    h[e] = a;
+    l[e] = b;
+  }
+  *reinterpret_cast<half4_t *>(hi) = h;
+  *reinterpret_cast<half4_t *>(lo) = l;
+}
+
+// One 32x32x16 step of a split product: acc += ah.bh and
+// cross += ah.bl + al.bh (the scaled remainders; the lo.lo term is dropped).
+struct SplitAcc {
+  float16_t acc, cross;
+};
+__device__ __forceinline__ void mfma_split(const half_t *ah, const half_t *al,
+                                           const half_t *bh, const half_t *bl,
+                                           SplitAcc &p) {
+  const half8_t a = load8(ah), b = load8(bh);
+  p.acc = mfma32x32x16(a, b, p.acc);
+  p.cross = mfma32x32x16(a, load8(bl), p.cross);
+  p.cross = mfma32x32x16(load8(al), b, p.cross);
+}
+__device__ __forceinline__ float split_value(const SplitAcc &p, int v) {
+  return p.acc[v] + p.cross[v] * kSplitUnscale;
+}
+
+// Write a C-layout 32x32 tile transposed, as hi/lo fp16, to dst[col][row]
+// (row stride `stride` halves): lane (r, h) holds column r and rows
+// 8q + 4h + [0, 4) of register group q, i.e. four consecutive rows.
+__device__ __forceinline__ void store_tile_T(half_t *dh, half_t *dl, int stride,
+                                             int row0, unsigned r, unsigned hh,
+                                             const float (&x)[16]) {
+#pragma unroll
+  for (int qd = 0; qd < 4; ++qd) {
+    const int row = row0 + 8 * qd + 4 * (int)hh;
+    store_split4(dh + r * stride + row, dl + r * stride + row,
+                 float4_t{x[4 * qd], x[4 * qd + 1], x[4 * qd + 2], x[4 * qd + 3]});
+  }
+}
+
+__global__ __launch_bounds__(256, 1) void delta_scan_kernel(
+    const float *__restrict__ q, const float *__restrict__ k,
+    const half_t *__restrict__ v, float *__restrict__ state,
+    half_t *__restrict__ out, const float *__restrict__ prep, unsigned T,
+    unsigned Hk, unsigned Hv, unsigned DV) {
+  const unsigned tilesPerHead = DV / DT;
+  const unsigned h = blockIdx.x / tilesPerHead, jt = blockIdx.x % tilesPerHead;
+  const unsigned kh = h / (Hv / Hk), j0 = jt * DT;
+  const unsigned tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+  const unsigned r = lane & 31u, hh = lane >> 5;
+  const unsigned chunks = (T + C - 1) / C;
+  const size_t vwidth = (size_t)Hv * DV;
+
+  // K token-major, Q token-major (its space later holds K dk-major), T, M,
+  // the state transposed S^T [j][d], X^T (later Z^T) and U^T, all hi/lo.
+  constexpr int kQKT = (C * KST > DK * CST) ? C * KST : DK * CST;
+  __shared__ __attribute__((aligned(16))) half_t sKh[C * KST], sKl[C * KST];
+  __shared__ __attribute__((aligned(16))) half_t sQh[kQKT], sQl[kQKT];
+  __shared__ __attribute__((aligned(16))) half_t sTh[C * CST], sTl[C * CST];
+  __shared__ __attribute__((aligned(16))) half_t sMh[C * CST], sMl[C * CST];
+  __shared__ __attribute__((aligned(16))) half_t sSh[DT * KST], sSl[DT * KST];
+  __shared__ __attribute__((aligned(16))) half_t sXh[DT * CST], sXl[DT * CST];
+  __shared__ __attribute__((aligned(16))) half_t sUh[DT * CST], sUl[DT * CST];
+  __shared__ float sV[C * DT];
+  __shared__ float sEg[C], sEz[C], sB[C];
+  half_t *const sKTh = sQh, *const sKTl = sQl; // [dk][token]
+
+  // The state tile: wave w holds rows d in [32w, 32w + 32), column r.
+  float S[16];
+  float *stile = state + (size_t)h * DK * DV + j0 + r;
+#pragma unroll
+  for (int x = 0; x < 16; ++x)
+    S[x] = stile[(size_t)(32 * wave + mfma_c_row(x, hh)) * DV];
+  store_tile_T(sSh, sSl, KST, 32 * wave, r, hh, S);
+
+  for (unsigned c = 0; c < chunks; ++c) {
+    const unsigned t0 = c * C, n = min((unsigned)C, T - t0);
+    const float *rec = prep + ((size_t)c * Hv + h) * kPrepFloats;
+
+    // 1. Stage the chunk: K and Q split (K kept in registers for K^T), T
+    //    and M split, V tile, g and beta.
+    float4_t kreg[C * DK / 4 / 256];
+#pragma unroll
+    for (int it = 0; it < C * DK / 4 / 256; ++it) {
+      const unsigned i = tid + 256 * it, t = i / (DK / 4), d4 = (i % (DK / 4)) * 4;
+      float4_t kv{0.0f, 0.0f, 0.0f, 0.0f}, qv{0.0f, 0.0f, 0.0f, 0.0f};
+      if (t < n) {
+        const size_t off = ((size_t)(t0 + t) * Hk + kh) * DK + d4;
+        kv = *reinterpret_cast<const float4_t *>(k + off);
+        qv = *reinterpret_cast<const float4_t *>(q + off);
+      }
+      kreg[it] = kv;
+      store_split4(sKh + t * KST + d4, sKl + t * KST + d4, kv);
+      store_split4(sQh + t * KST + d4, sQl + t * KST + d4, qv);
+    }
+#pragma unroll
+    for (int it = 0; it < C * C / 4 / 256; ++it) {
+      const unsigned i = tid + 256 * it, t = i / (C / 4), s4 = (i % (C / 4)) * 4;
+      store_split4(sTh + t * CST + s4, sTl + t * CST + s4,
+                   *reinterpret_cast<const float4_t *>(rec + t * C + s4));
+      store_split4(sMh + t * CST + s4, sMl + t * CST + s4,
+                   *reinterpret_cast<const float4_t *>(rec + C * C + t * C + s4));
+    }
+    {
+      const unsigned t = tid / (DT / 8), jj = (tid % (DT / 8)) * 8;
+      half8_t vv{0, 0, 0, 0, 0, 0, 0, 0};
+      if (t < n)
+        vv = load8(v + (size_t)(t0 + t) * vwidth + (size_t)h * DV + j0 + jj);
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        sV[t * DT + jj + e] = (float)vv[e];
+    }
+    if (tid < C) {
+      sEg[tid] = rec[kRecEg + tid];
+      sEz[tid] = rec[kRecEz + tid];
+      sB[tid] = rec[kRecBeta + tid];
+    }
+    __syncthreads();
+
+    // 2. Waves 0-1: K S, waves 2-3: Q S (row tile mt of the chunk).
+    const int mt = wave & 1;
+    float16_t acc;
+    {
+      SplitAcc p{float16_t{0}, float16_t{0}};
+      const half_t *ah = wave < 2 ? sKh : sQh, *al = wave < 2 ? sKl : sQl;
+#pragma unroll
+      for (int ks = 0; ks < DK / 16; ++ks) {
+        const int ko = 16 * ks + 8 * hh;
+        mfma_split(ah + (32 * mt + r) * KST + ko, al + (32 * mt + r) * KST + ko,
+                   sSh + r * KST + ko, sSl + r * KST + ko, p);
+      }
+#pragma unroll
+      for (int x = 0; x < 16; ++x)
+        acc[x] = split_value(p, x);
+    }
+    // 3. X = beta (V - e^g K S) -> X^T; Q S -> e^g Q S (kept in acc).
+    float x16[16];
+#pragma unroll
+    for (int x = 0; x < 16; ++x) {
+      const int t = 32 * mt + mfma_c_row(x, hh);
+      if (wave < 2)
+        x16[x] = sB[t] * (sV[t * DT + r] - sEg[t] * acc[x]);
+      else
+        acc[x] *= sEg[t];
+    }
+    if (wave < 2)
+      store_tile_T(sXh, sXl, CST, 32 * mt, r, hh, x16);
+    __syncthreads();
+
+    // 4. K dk-major into Q's space (Q is no longer read).
+#pragma unroll
+    for (int it = 0; it < C * DK / 4 / 256; ++it) {
+      const unsigned i = tid + 256 * it, t = i / (DK / 4), d4 = (i % (DK / 4)) * 4;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        half_t a, b;
+        split_f16(kreg[it][e], a, b);
+        sKTh[(d4 + e) * CST + t] = a;
+        sKTl[(d4 + e) * CST + t] = b;
+      }
+    }
+    // 5. Waves 0-1: U = T X.
+    float u[16];
+    if (wave < 2) {
+      SplitAcc p{float16_t{0}, float16_t{0}};
+#pragma unroll
+      for (int ks = 0; ks < C / 16; ++ks) {
+        const int ko = 16 * ks + 8 * hh;
+        mfma_split(sTh + (32 * mt + r) * CST + ko, sTl + (32 * mt + r) * CST + ko,
+                   sXh + r * CST + ko, sXl + r * CST + ko, p);
+      }
+#pragma unroll
+      for (int x = 0; x < 16; ++x)
+        u[x] = split_value(p, x);
+    }
+    __syncthreads();
+    // 6. U^T, and Z^T = (e^(g_C - g) U)^T into X's space.
+    if (wave < 2) {
+      float zz[16];
+#pragma unroll
+      for (int x = 0; x < 16; ++x) {
+        const int t = 32 * mt + mfma_c_row(x, hh);
+        zz[x] = sEz[t] * u[x];
+      }
+      store_tile_T(sUh, sUl, CST, 32 * mt, r, hh, u);
+      store_tile_T(sXh, sXl, CST, 32 * mt, r, hh, zz);
+    }
+    __syncthreads();
+
+    // 7. Waves 2-3: Y = e^g Q S + M U -> out.
+    if (wave >= 2) {
+      SplitAcc p{acc, float16_t{0}};
+#pragma unroll
+      for (int ks = 0; ks < C / 16; ++ks) {
+        const int ko = 16 * ks + 8 * hh;
+        mfma_split(sMh + (32 * mt + r) * CST + ko, sMl + (32 * mt + r) * CST + ko,
+                   sUh + r * CST + ko, sUl + r * CST + ko, p);
+      }
+#pragma unroll
+      for (int x = 0; x < 16; ++x) {
+        const unsigned t = 32 * mt + mfma_c_row(x, hh);
+        if (t < n)
+          out[(size_t)(t0 + t) * vwidth + (size_t)h * DV + j0 + r] =
+              (half_t)split_value(p, x);
+      }
+    }
+    // 8. S <- e^(g_C) S + K^T Z (wave w: rows d in [32w, 32w + 32)).
+    {
+      const float eC = sEg[C - 1];
+      SplitAcc p{float16_t{0}, float16_t{0}};
+#pragma unroll
+      for (int x = 0; x < 16; ++x)
+        p.acc[x] = S[x] * eC;
+#pragma unroll
+      for (int ks = 0; ks < C / 16; ++ks) {
+        const int ko = 16 * ks + 8 * hh;
+        mfma_split(sKTh + (32 * wave + r) * CST + ko, sKTl + (32 * wave + r) * CST + ko,
+                   sXh + r * CST + ko, sXl + r * CST + ko, p);
+      }
+#pragma unroll
+      for (int x = 0; x < 16; ++x)
+        S[x] = split_value(p, x);
+    }
+    // 9. S^T for the next chunk (nothing reads S^T after step 2).
+    store_tile_T(sSh, sSl, KST, 32 * wave, r, hh, S);
+    __syncthreads();
+  }
+
+#pragma unroll
+  for (int x = 0; x < 16; ++x)
+    stile[(size_t)(32 * wave + mfma_c_row(x, hh)) * DV] = S[x];
+}
+
+} // namespace
+
+bool delta_chunked_supported(const DeltaShape &s) {
+  return s.Dk == DK && s.Dv % DT == 0 && s.Hk >= 1 && s.Hv % s.Hk == 0 &&
+         s.Hv / s.Hk <= (unsigned)kMaxRatio && s.T >= 32;
+}
+
+size_t delta_chunked_workspace_bytes(const DeltaShape &s) {
+  const size_t chunks = (s.T + C - 1) / C;
+  return chunks * s.Hv * kPrepFloats * sizeof(float);
+}
+
+hipError_t launch_delta_chunked(const float *q, const float *k, const uint16_t *v,
+                                const float *beta, const float *decay, float *state,
+                                uint16_t *out, void *ws, const DeltaShape &s,
+                                hipStream_t stream) {
+  const unsigned chunks = (s.T + C - 1) / C;
+  float *prep = static_cast<float *>(ws);
+  hipLaunchKernelGGL(delta_prep_kernel, dim3(chunks, s.Hk), dim3(256), 0, stream, q, k,
+                     beta, decay, prep, s.T, s.Hk, s.Hv);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess)
+    return e;
+  hipLaunchKernelGGL(delta_scan_kernel, dim3(s.Hv * (s.Dv / DT)), dim3(256), 0, stream,
+                     q, k, reinterpret_cast<const half_t *>(v), state,
+                     reinterpret_cast<half_t *>(out), prep, s.T, s.Hk, s.Hv, s.Dv);
+  return hipGetLastError();
+}
+
+unsigned delta_chunked_dispatches() { return 2; }
+
+const char *delta_chunked_kernel_name(unsigned index) {
+  return index == 0 ? "deltaChunkPrep" : "deltaChunkScan";
+}
+
 } // namespace llmi

@@ -83,6 +83,30 @@ __device__ __forceinline__ float dot8(half8_t a, half8_t b, float acc) {
   return acc;
 }
 
+// v_mfma_f32_32x32x16_f16. Operand layouts (lane l, r = l % 32, h = l / 32):
+//   A (32 x 16): lane holds A[r][8h .. 8h+7]
+//   B (16 x 32): lane holds B[8h .. 8h+7][r]
+//   C (32 x 32): lane register v holds C[8(v/4) + 4h + v%4][r]
+__device__ __forceinline__ float16_t mfma32x32x16(half8_t a, half8_t b, float16_t c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
+// Row of the C layout that register v of lane-half h holds.
+__device__ __forceinline__ int mfma_c_row(int v, int h) { return 8 * (v / 4) + 4 * h + (v % 4); }
+
+// x = hi + lo * 2^-11 with hi = fp16(x), lo = fp16((x - hi) * 2^11): 22
+// significant bits. No part is ever an fp16 subnormal, which MFMA may flush
+// to zero: the remainder is stored scaled by 2^11 (|x - hi| <= 2^-11 |x|
+// would be subnormal for |x| < 2^-3), and below the smallest normal fp16
+// (2^-14) hi is 0 and the whole value goes to the scaled remainder.
+constexpr float kSplitScale = 2048.0f;
+constexpr float kSplitUnscale = 1.0f / 2048.0f;
+constexpr float kF16MinNormal = 6.103515625e-05f; // 2^-14
+__device__ __forceinline__ void split_f16(float x, half_t &hi, half_t &lo) {
+  hi = fabsf(x) >= kF16MinNormal ? (half_t)x : (half_t)0.0f;
+  lo = (half_t)((x - (float)hi) * kSplitScale);
+}
+
 __device__ __forceinline__ half8_t load8(const half_t *p) {
   return *reinterpret_cast<const half8_t *>(p);
 }

@@ -36,6 +36,7 @@ def _check(x, got_out, got_state):
     assert np.all(np.isfinite(got_out)) and np.all(np.isfinite(got_state))
     oerr = np.max(np.abs(got_out - want_out))
     serr = np.max(np.abs(got_state - want_state)) / max(np.max(np.abs(want_state)), 1e-30)
+    print(f"  out max-abs {oerr:.3g}  state rel {serr:.3g}", flush=True)
     assert oerr <= OUT_TOL, f"out max abs err {oerr:.3g}"
     assert serr <= STATE_TOL, f"state rel err {serr:.3g}"
     return oerr, serr
@@ -50,11 +51,48 @@ def test_decode_step_cfg5_shape(gpu, state_std):
     assert names == ["deltaRecurrent"]
 
 
-@pytest.mark.parametrize("T", [2, 17, 64, 65, 200])
+@pytest.mark.parametrize("T", [2, 17, 31, 32, 64, 65, 127, 200, 1000])
 def test_prefill_small(gpu, T):
     print(f"delta prefill T={T}", flush=True)
     x = oracle.make_delta_inputs(40 + T, T, 16, 128, 32, 128, 0.1)
     _check(x, *_run(x, gpu))
+    names = ops.kernel_names(_lib.OP_DELTA_UPDATE, _lib.GraphDeltaParams(T, 16, 128, 32, 128))
+    assert names == (["deltaChunkPrep", "deltaChunkScan"] if T >= 32 else ["deltaRecurrent"])
+
+
+@pytest.mark.parametrize("T", [40, 130])
+def test_chunked_zero_decay_and_beta(gpu, T):
+    """Tokens whose decay is 0 (the chunk form clamps log 0) or whose beta is
+    0 (pure decay), in and across chunks."""
+    print(f"delta zero decay/beta T={T}", flush=True)
+    x = oracle.make_delta_inputs(70 + T, T, 16, 128, 32, 128, 0.1)
+    x.decay[5, :] = 0.0
+    x.decay[T - 3, 3] = 0.0
+    x.beta[7, :] = 0.0
+    x.beta[T // 2, 1:9] = 0.0
+    x.decay[T // 2 + 1, :] = 1.0
+    _check(x, *_run(x, gpu))
+
+
+def test_chunked_partition_invariance(gpu):
+    """Chunk boundaries are an implementation detail: 300 tokens in one call,
+    in calls that split chunks (100 + 200) and token by token agree."""
+    print("delta chunk partition", flush=True)
+    T = 300
+    x = oracle.make_delta_inputs(31, T, 16, 128, 32, 128, 0.1)
+    q, k, v, beta, decay, state = _dev(x, gpu)
+    res = []
+    for cuts in ([0, T], [0, 100, T], [0, 37, 101, 299, T]):
+        st = state.clone()
+        outs = [ops.delta_update(q[a:b], k[a:b], v[a:b], beta[a:b], decay[a:b], st)
+                for a, b in zip(cuts, cuts[1:])]
+        torch.cuda.synchronize()
+        res.append((torch.cat(outs).float().cpu().numpy(), st.cpu().numpy()))
+    for o, st in res:
+        _check(x, o.astype(np.float64), st)
+    for o, st in res[1:]:
+        assert np.max(np.abs(o - res[0][0])) <= 1e-3
+        assert np.max(np.abs(st - res[0][1])) / np.max(np.abs(res[0][1])) <= 1e-4
 
 
 def test_prefill_cfg4(gpu):
@@ -77,7 +115,8 @@ def test_other_shapes(gpu, shape):
 
 def test_token_by_token_equals_one_chunk(gpu):
     """Partition invariance (MetalReferenceTest.py:289-295): one call over T
-    tokens and T single-token calls give the same output and state."""
+    tokens (the chunk-wise form) and T single-token calls (the recurrence)
+    give the same output and state, to the split-fp16 MFMA products' error."""
     print("delta partition invariance", flush=True)
     T = 48
     x = oracle.make_delta_inputs(12, T, 16, 128, 32, 128, 0.1)
@@ -93,4 +132,4 @@ def test_token_by_token_equals_one_chunk(gpu):
     b = torch.cat(parts).float().cpu().numpy()
     assert np.max(np.abs(a - b)) <= 1e-3
     rel = (s1 - s2).abs().max().item() / s1.abs().max().item()
-    assert rel <= 1e-5
+    assert rel <= 1e-4
