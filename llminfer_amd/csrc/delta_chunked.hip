@@ -19,8 +19,9 @@
 //  * deltaChunkPrep, grid (chunk, key head): everything that does not depend
 //    on the state, for every chunk at once -- the Gram matrices K K^T and
 //    Q K^T on fp16 MFMA (v_mfma_f32_32x32x16_f16), then per value head the
-//    decay weighting, T by forward substitution in fp32 (one lane per column
-//    of T) and M. Written to the workspace: T, M, g, beta per (chunk, head).
+//    decay weighting, M, and T by forward substitution in fp32 (one lane
+//    per column of T). Written to the workspace: T, M and the token weights
+//    per (chunk, value head).
 //
 //  * deltaChunkScan, grid (value head, 32-column dv tile): walks the chunks
 //    in order with the state tile S [dk x 32] resident in MFMA accumulators.
@@ -88,14 +89,17 @@ __global__ __launch_bounds__(256, 1) void delta_prep_kernel(
       kv = *reinterpret_cast<const float4_t *>(k + off);
       qv = *reinterpret_cast<const float4_t *>(q + off);
     }
+    half4_t kh4, qh4;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      sK[t * KST + d4 + e] = (half_t)kv[e];
-      sQ[t * KST + d4 + e] = (half_t)qv[e];
+      kh4[e] = (half_t)kv[e];
+      qh4[e] = (half_t)qv[e];
     }
+    *reinterpret_cast<half4_t *>(sK + t * KST + d4) = kh4;
+    *reinterpret_cast<half4_t *>(sQ + t * KST + d4) = qh4;
   }
-  // Cumulative log decay and beta of each value head of this key head:
-  // wave w scans head w (padding tokens: decay 1, beta 0).
+  // Cumulative log decay (double) and beta of each value head of this key
+  // head: wave w scans head w (padding tokens: decay 1, beta 0).
   if (wave < R) {
     const unsigned h = kh * R + wave, t = lane;
     const float a = t < n ? decay[(size_t)(t0 + t) * Hv + h] : 1.0f;
@@ -130,19 +134,25 @@ __global__ __launch_bounds__(256, 1) void delta_prep_kernel(
   }
   __syncthreads();
 
-  // Decay weighting: A (to LDS) and M, g, beta (to the workspace).
-  for (unsigned hr = 0; hr < R; ++hr) {
-    float *rec = prep + ((size_t)c * Hv + kh * R + hr) * kPrepFloats;
-    for (unsigned i = tid; i < C * C; i += 256) {
-      const unsigned t = i / C, s = i % C;
-      const float e = s <= t ? expf((float)(sG[hr][t] - sG[hr][s])) : 0.0f;
-      sA[hr][i] = s < t ? sB[hr][t] * e * sKK[i] : 0.0f;
-      rec[C * C + i] = e * sQK[i];
-    }
-    if (tid < C) {
-      rec[kRecEg + tid] = expf((float)sG[hr][tid]);
-      rec[kRecEz + tid] = expf((float)(sG[hr][C - 1] - sG[hr][tid]));
-      rec[kRecBeta + tid] = sB[hr][tid];
+  // Decay weighting. Thread (row group tq, column s) covers rows tq + 4i:
+  // A (to LDS), M, e^(g_t), e^(g_C - g_t), beta (to the workspace).
+  {
+    const unsigned s = tid % C, tq = tid / C;
+    for (unsigned hr = 0; hr < R; ++hr) {
+      float *rec = prep + ((size_t)c * Hv + kh * R + hr) * kPrepFloats;
+      const double gs = sG[hr][s];
+#pragma unroll
+      for (int i = 0; i < C / 4; ++i) {
+        const unsigned t = tq + 4 * i, idx = t * C + s;
+        const float e = s <= t ? expf((float)(sG[hr][t] - gs)) : 0.0f;
+        sA[hr][idx] = s < t ? sB[hr][t] * e * sKK[idx] : 0.0f;
+        rec[C * C + idx] = e * sQK[idx];
+      }
+      if (tid < C) {
+        rec[kRecEg + tid] = expf((float)sG[hr][tid]);
+        rec[kRecEz + tid] = expf((float)(sG[hr][C - 1] - sG[hr][tid]));
+        rec[kRecBeta + tid] = sB[hr][tid];
+      }
     }
   }
   __syncthreads();
@@ -157,8 +167,8 @@ __global__ __launch_bounds__(256, 1) void delta_prep_kernel(
     for (int t = 0; t < C; ++t) {
       float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-      for (int s = 0; s < t; ++s)
-        acc[s & 3] = fmaf(A[t * C + s], col[s], acc[s & 3]);
+      for (int u = 0; u < t; ++u)
+        acc[u & 3] = fmaf(A[t * C + u], col[u], acc[u & 3]);
       const float sum = (acc[0] + acc[1]) + (acc[2] + acc[3]);
       col[t] = (unsigned)t == j ? 1.0f : ((unsigned)t > j ? -sum : 0.0f);
     }
@@ -198,6 +208,13 @@ __device__ __forceinline__ void mfma_split(const half_t *ah, const half_t *al,
   p.cross = mfma32x32x16(a, load8(bl), p.cross);
   p.cross = mfma32x32x16(load8(al), b, p.cross);
 }
+__device__ __forceinline__ void mfma_split_a(half8_t ah, half8_t al, const half_t *bh,
+                                             const half_t *bl, SplitAcc &p) {
+  const half8_t b = load8(bh);
+  p.acc = mfma32x32x16(ah, b, p.acc);
+  p.cross = mfma32x32x16(ah, load8(bl), p.cross);
+  p.cross = mfma32x32x16(al, b, p.cross);
+}
 __device__ __forceinline__ float split_value(const SplitAcc &p, int v) {
   return p.acc[v] + p.cross[v] * kSplitUnscale;
 }
@@ -216,6 +233,51 @@ __device__ __forceinline__ void store_tile_T(half_t *dh, half_t *dl, int stride,
   }
 }
 
+// One chunk's scan inputs as this thread loads them: its share of K and Q
+// (token-major float4s), of T and M, of the V tile, and (threads < C) the
+// token weights. Loaded one chunk ahead so that the global latency hides
+// behind the previous chunk's products.
+constexpr int kKQPer = C * DK / 4 / 256; // float4s of K (and of Q) per thread
+constexpr int kTMPer = C * C / 4 / 256;  // float4s of T (and of M) per thread
+struct ChunkRegs {
+  float4_t k[kKQPer], q[kKQPer], t[kTMPer], m[kTMPer];
+  half8_t v;
+  float eg, ez, b;
+};
+
+__device__ __forceinline__ void load_chunk(ChunkRegs &cr, const float *__restrict__ q,
+                                           const float *__restrict__ k,
+                                           const half_t *__restrict__ v,
+                                           const float *__restrict__ rec, unsigned t0,
+                                           unsigned n, unsigned kh, unsigned Hk,
+                                           size_t vcol, size_t vwidth, unsigned tid) {
+#pragma unroll
+  for (int it = 0; it < kKQPer; ++it) {
+    const unsigned i = tid + 256 * it, t = i / (DK / 4), d4 = (i % (DK / 4)) * 4;
+    cr.k[it] = cr.q[it] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    if (t < n) {
+      const size_t off = ((size_t)(t0 + t) * Hk + kh) * DK + d4;
+      cr.k[it] = *reinterpret_cast<const float4_t *>(k + off);
+      cr.q[it] = *reinterpret_cast<const float4_t *>(q + off);
+    }
+  }
+#pragma unroll
+  for (int it = 0; it < kTMPer; ++it) {
+    const unsigned i = tid + 256 * it, t = i / (C / 4), s4 = (i % (C / 4)) * 4;
+    cr.t[it] = *reinterpret_cast<const float4_t *>(rec + t * C + s4);
+    cr.m[it] = *reinterpret_cast<const float4_t *>(rec + C * C + t * C + s4);
+  }
+  const unsigned t = tid / (DT / 8), jj = (tid % (DT / 8)) * 8;
+  cr.v = half8_t{0, 0, 0, 0, 0, 0, 0, 0};
+  if (t < n)
+    cr.v = load8(v + (size_t)(t0 + t) * vwidth + vcol + jj);
+  if (tid < C) {
+    cr.eg = rec[kRecEg + tid];
+    cr.ez = rec[kRecEz + tid];
+    cr.b = rec[kRecBeta + tid];
+  }
+}
+
 __global__ __launch_bounds__(256, 1) void delta_scan_kernel(
     const float *__restrict__ q, const float *__restrict__ k,
     const half_t *__restrict__ v, float *__restrict__ state,
@@ -229,11 +291,10 @@ __global__ __launch_bounds__(256, 1) void delta_scan_kernel(
   const unsigned chunks = (T + C - 1) / C;
   const size_t vwidth = (size_t)Hv * DV;
 
-  // K token-major, Q token-major (its space later holds K dk-major), T, M,
-  // the state transposed S^T [j][d], X^T (later Z^T) and U^T, all hi/lo.
-  constexpr int kQKT = (C * KST > DK * CST) ? C * KST : DK * CST;
+  // K and Q token-major, T, M, the state transposed S^T [j][d], X^T (later
+  // Z^T) and U^T, all hi/lo.
   __shared__ __attribute__((aligned(16))) half_t sKh[C * KST], sKl[C * KST];
-  __shared__ __attribute__((aligned(16))) half_t sQh[kQKT], sQl[kQKT];
+  __shared__ __attribute__((aligned(16))) half_t sQh[C * KST], sQl[C * KST];
   __shared__ __attribute__((aligned(16))) half_t sTh[C * CST], sTl[C * CST];
   __shared__ __attribute__((aligned(16))) half_t sMh[C * CST], sMl[C * CST];
   __shared__ __attribute__((aligned(16))) half_t sSh[DT * KST], sSl[DT * KST];
@@ -241,7 +302,6 @@ __global__ __launch_bounds__(256, 1) void delta_scan_kernel(
   __shared__ __attribute__((aligned(16))) half_t sUh[DT * CST], sUl[DT * CST];
   __shared__ float sV[C * DT];
   __shared__ float sEg[C], sEz[C], sB[C];
-  half_t *const sKTh = sQh, *const sKTl = sQl; // [dk][token]
 
   // The state tile: wave w holds rows d in [32w, 32w + 32), column r.
   float S[16];
@@ -251,47 +311,37 @@ __global__ __launch_bounds__(256, 1) void delta_scan_kernel(
     S[x] = stile[(size_t)(32 * wave + mfma_c_row(x, hh)) * DV];
   store_tile_T(sSh, sSl, KST, 32 * wave, r, hh, S);
 
+  const size_t vcol = (size_t)h * DV + j0;
+  auto rec_of = [&](unsigned c) { return prep + ((size_t)c * Hv + h) * kPrepFloats; };
+  ChunkRegs cr;
+  load_chunk(cr, q, k, v, rec_of(0), 0, min((unsigned)C, T), kh, Hk, vcol, vwidth, tid);
+
   for (unsigned c = 0; c < chunks; ++c) {
     const unsigned t0 = c * C, n = min((unsigned)C, T - t0);
-    const float *rec = prep + ((size_t)c * Hv + h) * kPrepFloats;
 
-    // 1. Stage the chunk: K and Q split (K kept in registers for K^T), T
-    //    and M split, V tile, g and beta.
-    float4_t kreg[C * DK / 4 / 256];
+    // 1. Stage the chunk from registers: K, Q, T, M split; V; weights.
 #pragma unroll
-    for (int it = 0; it < C * DK / 4 / 256; ++it) {
+    for (int it = 0; it < kKQPer; ++it) {
       const unsigned i = tid + 256 * it, t = i / (DK / 4), d4 = (i % (DK / 4)) * 4;
-      float4_t kv{0.0f, 0.0f, 0.0f, 0.0f}, qv{0.0f, 0.0f, 0.0f, 0.0f};
-      if (t < n) {
-        const size_t off = ((size_t)(t0 + t) * Hk + kh) * DK + d4;
-        kv = *reinterpret_cast<const float4_t *>(k + off);
-        qv = *reinterpret_cast<const float4_t *>(q + off);
-      }
-      kreg[it] = kv;
-      store_split4(sKh + t * KST + d4, sKl + t * KST + d4, kv);
-      store_split4(sQh + t * KST + d4, sQl + t * KST + d4, qv);
+      store_split4(sKh + t * KST + d4, sKl + t * KST + d4, cr.k[it]);
+      store_split4(sQh + t * KST + d4, sQl + t * KST + d4, cr.q[it]);
     }
 #pragma unroll
-    for (int it = 0; it < C * C / 4 / 256; ++it) {
+    for (int it = 0; it < kTMPer; ++it) {
       const unsigned i = tid + 256 * it, t = i / (C / 4), s4 = (i % (C / 4)) * 4;
-      store_split4(sTh + t * CST + s4, sTl + t * CST + s4,
-                   *reinterpret_cast<const float4_t *>(rec + t * C + s4));
-      store_split4(sMh + t * CST + s4, sMl + t * CST + s4,
-                   *reinterpret_cast<const float4_t *>(rec + C * C + t * C + s4));
+      store_split4(sTh + t * CST + s4, sTl + t * CST + s4, cr.t[it]);
+      store_split4(sMh + t * CST + s4, sMl + t * CST + s4, cr.m[it]);
     }
     {
       const unsigned t = tid / (DT / 8), jj = (tid % (DT / 8)) * 8;
-      half8_t vv{0, 0, 0, 0, 0, 0, 0, 0};
-      if (t < n)
-        vv = load8(v + (size_t)(t0 + t) * vwidth + (size_t)h * DV + j0 + jj);
 #pragma unroll
       for (int e = 0; e < 8; ++e)
-        sV[t * DT + jj + e] = (float)vv[e];
+        sV[t * DT + jj + e] = (float)cr.v[e];
     }
     if (tid < C) {
-      sEg[tid] = rec[kRecEg + tid];
-      sEz[tid] = rec[kRecEz + tid];
-      sB[tid] = rec[kRecBeta + tid];
+      sEg[tid] = cr.eg;
+      sEz[tid] = cr.ez;
+      sB[tid] = cr.b;
     }
     __syncthreads();
 
@@ -325,18 +375,10 @@ __global__ __launch_bounds__(256, 1) void delta_scan_kernel(
       store_tile_T(sXh, sXl, CST, 32 * mt, r, hh, x16);
     __syncthreads();
 
-    // 4. K dk-major into Q's space (Q is no longer read).
-#pragma unroll
-    for (int it = 0; it < C * DK / 4 / 256; ++it) {
-      const unsigned i = tid + 256 * it, t = i / (DK / 4), d4 = (i % (DK / 4)) * 4;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        half_t a, b;
-        split_f16(kreg[it][e], a, b);
-        sKTh[(d4 + e) * CST + t] = a;
-        sKTl[(d4 + e) * CST + t] = b;
-      }
-    }
+    // 4. Fetch the next chunk while this one finishes.
+    if (c + 1 < chunks)
+      load_chunk(cr, q, k, v, rec_of(c + 1), t0 + C, min((unsigned)C, T - t0 - C), kh, Hk,
+                 vcol, vwidth, tid);
     // 5. Waves 0-1: U = T X.
     float u[16];
     if (wave < 2) {
@@ -382,7 +424,8 @@ __global__ __launch_bounds__(256, 1) void delta_scan_kernel(
               (half_t)split_value(p, x);
       }
     }
-    // 8. S <- e^(g_C) S + K^T Z (wave w: rows d in [32w, 32w + 32)).
+    // 8. S <- e^(g_C) S + K^T Z (wave w: rows d in [32w, 32w + 32)); the
+    //    K^T operand is gathered from the token-major K tile.
     {
       const float eC = sEg[C - 1];
       SplitAcc p{float16_t{0}, float16_t{0}};
@@ -392,8 +435,13 @@ __global__ __launch_bounds__(256, 1) void delta_scan_kernel(
 #pragma unroll
       for (int ks = 0; ks < C / 16; ++ks) {
         const int ko = 16 * ks + 8 * hh;
-        mfma_split(sKTh + (32 * wave + r) * CST + ko, sKTl + (32 * wave + r) * CST + ko,
-                   sXh + r * CST + ko, sXl + r * CST + ko, p);
+        half8_t ah, al;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          ah[e] = sKh[(ko + e) * KST + 32 * wave + r];
+          al[e] = sKl[(ko + e) * KST + 32 * wave + r];
+        }
+        mfma_split_a(ah, al, sXh + r * CST + ko, sXl + r * CST + ko, p);
       }
 #pragma unroll
       for (int x = 0; x < 16; ++x)
