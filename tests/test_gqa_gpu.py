@@ -108,6 +108,30 @@ def test_prefill_cfg3_sampled_rows(gpu):
         _check(got[t], want)
 
 
+@pytest.mark.parametrize("growth,qscale", [(2.0, 1.0), (0.0, 4.0), (6.0, 2.0)])
+def test_prefill_moving_reference(gpu, growth, qscale):
+    """Scores that keep growing along the keys (key rows scaled up with their
+    position) move each row's softmax reference many times over the tiles;
+    a wide score range puts most probabilities many binades below the row
+    maximum."""
+    T, P = 200, 700
+    print(f"prefill growth={growth} qscale={qscale}", flush=True)
+    x = oracle.make_gqa_inputs(55, T, 16, 4, 256, P)
+    pos = np.arange(P + T, dtype=np.float32)[:, None, None]
+    x.k_cache = oracle.f32_to_f16(oracle.f16_to_f32(x.k_cache) * (1.0 + growth * pos / (P + T)))
+    x.q = oracle.f32_to_f16(oracle.f16_to_f32(x.q) * qscale)
+    got = _run(x, gpu)
+    want = oracle.gqa_dense_f64(x.q, x.k_cache, x.v_cache, P)
+    # A sharp softmax puts the output at the mercy of the few largest
+    # weights, each rounded to fp16 before the PV product: the bar is the
+    # north-star tolerance on top of that first-order rounding bound.
+    bound = p_rounding_bound(x.q, x.k_cache, x.v_cache, P)
+    assert np.all(np.isfinite(got))
+    excess = np.max(np.abs(got - want) - bound)
+    print(f"  max abs err {np.max(np.abs(got - want)):.3g}, beyond P rounding {excess:.3g}")
+    assert excess <= TOL
+
+
 @pytest.mark.parametrize("case", [(19, 4, 2, 12, 0), (7, 4, 2, 256, 33)])
 def test_reference_kernel_cases(gpu, case):
     """tests/FlashAttentionTest.mm:108-109 with its LCG inputs. Its tolerance
