@@ -53,19 +53,26 @@ __device__ __forceinline__ void load_lds16(__amdgpu_buffer_rsrc_t rsrc, char *ds
   __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_void_t *)dst, 16, voffset, 0, 0, 0);
 }
 
+// Hides a value's known bit range from the compiler, so that adding a
+// constant to it stays an add (folded into the LDS instruction's offset
+// field) instead of becoming an OR of disjoint bits computed on the VALU.
+__device__ __forceinline__ void opaque(unsigned &x) { asm volatile("" : "+v"(x)); }
+
 __device__ __forceinline__ void wait_loads() {
   __builtin_amdgcn_s_waitcnt(0x0F70); // vmcnt(0)
 }
 
 // ds_read_b64_tr_b16: in each 16-lane group, lane j receives element j % 4 of
 // the 8-byte chunks addressed by lanes j/4, 4 + j/4, 8 + j/4, 12 + j/4.
-__device__ __forceinline__ half4_t read_tr(const char *p) {
-  return __builtin_bit_cast(half4_t, __builtin_amdgcn_ds_read_tr16_b64_v4f16((lds_fp16x4_t *)p));
+__device__ __forceinline__ half4_t read_tr(const char *base, unsigned off) {
+  typedef __attribute__((address_space(3))) char lds_char_t;
+  return __builtin_bit_cast(half4_t, __builtin_amdgcn_ds_read_tr16_b64_v4f16(
+                                         (lds_fp16x4_t *)((lds_char_t *)base + off)));
 }
 
 template <int D, int HW>
 __global__ __attribute__((amdgpu_flat_work_group_size(64 * HW, 64 * HW),
-                          amdgpu_waves_per_eu(D == 128 ? 2 : 1, D == 128 ? 2 : 1)))
+                          amdgpu_waves_per_eu(HW > 4 ? 2 : 1, HW > 4 ? 2 : 1)))
 void gqa_prefill_kernel(const half_t *__restrict__ q, const half_t *__restrict__ kc,
                         const half_t *__restrict__ vc, half_t *__restrict__ out,
                         unsigned T, unsigned Hq, unsigned Hkv, unsigned P,
@@ -78,9 +85,16 @@ void gqa_prefill_kernel(const half_t *__restrict__ q, const half_t *__restrict__
   constexpr int CPR = D / 8;         // 16-byte chunks per row
   constexpr int RPI = 64 / CPR;      // rows per 1-KB load
   static_assert(NIW >= 1 && TILEB % (1024 * HW) == 0, "tile/waves");
+  // V is staged transposed (V^T rows of BN keys, padded) when one pass of
+  // the workgroup's threads covers the tile in (8-key run, 8-channel) units;
+  // smaller workgroups read V with the transposing LDS read instead.
+  constexpr int VUNITS = (BN / 8) * (D / 8);
+  constexpr bool kStagedV = VUNITS <= 64 * HW;
+  constexpr int VTROW = 2 * BN;       // bytes per V^T row (8 chunks of 16 B)
+  constexpr int VBUF = kStagedV ? D * VTROW : TILEB;
 
   __shared__ __attribute__((aligned(1024))) char sK0[TILEB], sK1[TILEB];
-  __shared__ __attribute__((aligned(1024))) char sV0[TILEB], sV1[TILEB];
+  __shared__ __attribute__((aligned(1024))) char sV0[VBUF], sV1[VBUF];
 
   // Workgroup -> (head group, token block). Each XCD (workgroups are dealt
   // round-robin over 8) serves as few head groups as possible, so its L2
@@ -114,32 +128,93 @@ void gqa_prefill_kernel(const half_t *__restrict__ q, const half_t *__restrict__
   const char *kbase = reinterpret_cast<const char *>(kc) + (size_t)kvh * D * 2;
   const char *vbase = reinterpret_cast<const char *>(vc) + (size_t)kvh * D * 2;
 
-  // Per-lane source offsets of this wave's loads (constant over tiles):
-  // load n writes rows [n*RPI, n*RPI + RPI) of the tile.
-  unsigned koff[NIW], voff[NIW];
+  // Load i of this wave writes tile rows (wave + HW i) RPI + [0, RPI). The
+  // swizzle repeats every 8 rows (K) or 4 rows (V), so the lane offsets
+  // repeat every PK / PV loads up to a uniform row shift, added per load.
+  constexpr int STEP = HW * RPI;
+  constexpr int PK = STEP >= 8 ? 1 : 8 / STEP, PV = STEP >= 4 ? 1 : 4 / STEP;
+  unsigned koff[PK], voff[PV];
 #pragma unroll
-  for (int i = 0; i < NIW; ++i) {
-    const unsigned row = (wave + HW * i) * RPI + lane / CPR, slot = lane % CPR;
-    koff[i] = row * (unsigned)rowBytes + 16 * (slot ^ (row & 7));
-    voff[i] = row * (unsigned)rowBytes + 16 * (slot ^ ((row & 3) << 1));
+  for (int p = 0; p < PK; ++p) {
+    const unsigned row = wave * RPI + lane / CPR + STEP * p, slot = lane % CPR;
+    koff[p] = row * (unsigned)rowBytes + 16 * (slot ^ (row & 7));
   }
-  auto rsrc = [&](const char *base, unsigned tile) {
+#pragma unroll
+  for (int p = 0; p < PV; ++p) {
+    const unsigned row = wave * RPI + lane / CPR + STEP * p, slot = lane % CPR;
+    voff[p] = row * (unsigned)rowBytes + 16 * (slot ^ ((row & 3) << 1));
+  }
+  // One descriptor per tile over its rows below kend (none for a tile past
+  // the end, whose loads then do nothing).
+  auto tile_rsrc = [&](const char *base, unsigned tile) {
     const unsigned first = tile * BN;
-    const unsigned rows = min((unsigned)BN, kend - first);
+    const unsigned rows = kend > first ? min((unsigned)BN, kend - first) : 0u;
     return __builtin_amdgcn_make_buffer_rsrc((void *)(base + (size_t)first * rowBytes),
                                              (short)0, (int)(rows * rowBytes), kBufferWord3);
   };
-  auto issue_k = [&](unsigned tile, char *dst) {
-    const __amdgpu_buffer_rsrc_t rs = rsrc(kbase, tile);
+  // A tile's loads go out in NPART parts spread over the score MFMAs, so the
+  // vector memory pipeline takes them while the matrix cores work.
+  constexpr int NPART = 4;
+  auto issue = [&](__amdgpu_buffer_rsrc_t rs, const unsigned *off, int period, char *dst,
+                   int part) {
 #pragma unroll
     for (int i = 0; i < NIW; ++i)
-      load_lds16(rs, dst + 1024 * (wave + HW * i), koff[i]);
+      if (i * NPART / NIW == part)
+        load_lds16(rs, dst + 1024 * (wave + HW * i),
+                   off[i % period] + (unsigned)(STEP * (i - i % period)) * (unsigned)rowBytes);
+  };
+  auto issue_k = [&](unsigned tile, char *dst) {
+    const __amdgpu_buffer_rsrc_t rs = tile_rsrc(kbase, tile);
+#pragma unroll
+    for (int part = 0; part < NPART; ++part)
+      issue(rs, koff, PK, dst, part);
   };
   auto issue_v = [&](unsigned tile, char *dst) {
-    const __amdgpu_buffer_rsrc_t rs = rsrc(vbase, tile);
+    const __amdgpu_buffer_rsrc_t rs = tile_rsrc(vbase, tile);
 #pragma unroll
-    for (int i = 0; i < NIW; ++i)
-      load_lds16(rs, dst + 1024 * (wave + HW * i), voff[i]);
+    for (int part = 0; part < NPART; ++part)
+      issue(rs, voff, PV, dst, part);
+  };
+
+  // Staged V: thread t owns unit t = (run, 8-channel block cb). A run is the
+  // 8 keys 16G + 4hh + {0..3} and 16G + 8 + 4hh + {0..3} of a 16-key group
+  // G; V^T stores them at key positions 16G + 8hh + [0, 8), i.e. bits 2 and
+  // 3 of the key index swapped within each group, which is exactly the key
+  // order the probability operand holds (lane half hi, slots e: key
+  // 16G + 8(e/4) + 4hi + e%4). So one 16-byte read gives an MFMA operand.
+  // The 16-byte chunk c of V^T row j sits at c ^ ((j / 8) % 8): the eight
+  // threads writing rows 8 cb + ch for consecutive cb hit distinct banks.
+  const unsigned vunit = threadIdx.x, vcb = vunit % (D / 8), vrun = vunit / (D / 8);
+  const unsigned vG = vrun / 2, vhh = vrun % 2;
+  const bool vowner = VUNITS == 64 * HW || vunit < (unsigned)VUNITS;
+  const unsigned vsrc = (16 * vG + 4 * vhh) * (unsigned)rowBytes + 16 * vcb;
+  const unsigned vdst = (8 * vcb) * VTROW + 16 * ((2 * vG + vhh) ^ (vcb % 8));
+  half8_t vst[8];
+  auto load_v_part = [&](__amdgpu_buffer_rsrc_t rs, int part) {
+    if (vowner) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        if (e * NPART / 8 == part)
+          vst[e] = __builtin_bit_cast(
+              half8_t,
+              __builtin_amdgcn_raw_buffer_load_b128(
+                  rs, vsrc, (unsigned)((e % 4) + 8 * (e / 4)) * (unsigned)rowBytes, 0));
+    }
+  };
+  auto load_v = [&](unsigned tile) {
+    const __amdgpu_buffer_rsrc_t rs = tile_rsrc(vbase, tile);
+#pragma unroll
+    for (int part = 0; part < NPART; ++part)
+      load_v_part(rs, part);
+  };
+  auto store_vt = [&](char *dst) {
+    if (vowner) {
+#pragma unroll
+      for (int ch = 0; ch < 8; ++ch)
+        *reinterpret_cast<half8_t *>(dst + vdst + ch * VTROW) =
+            half8_t{vst[0][ch], vst[1][ch], vst[2][ch], vst[3][ch],
+                    vst[4][ch], vst[5][ch], vst[6][ch], vst[7][ch]};
+    }
   };
 
   // Operand read offsets. K (A of S^T, row 32kt + r, chunk 2s + hi): the
@@ -148,13 +223,36 @@ void gqa_prefill_kernel(const half_t *__restrict__ q, const half_t *__restrict__
   // addresses row k0 + j/4, channels 16g + 4(j%4) .. +3 of an output tile.
   unsigned kread[4];
 #pragma unroll
-  for (int b = 0; b < 4; ++b)
+  for (int b = 0; b < 4; ++b) {
     kread[b] = r * ROWB + 16 * ((2 * b + hi) ^ (r & 7));
+    opaque(kread[b]);
+  }
   const unsigned j16 = lane % 16, g = (lane / 16) % 2;
   const unsigned vx = 2 * (j16 / 4), vb = (j16 % 4) / 2;
   const unsigned vrow = (4 * hi + j16 / 4) * ROWB + 8 * (j16 % 2);
   const unsigned vread[2] = {vrow + 16 * ((2 * g + vb) ^ vx),
                              vrow + 16 * ((4 + 2 * g + vb) ^ vx)};
+  // Staged V^T: lane reads row 32 dt + r, key positions 16 G + 8 hi + [0, 8),
+  // i.e. chunk (2G + hi) ^ ((4 dt + r / 8) % 8): one offset per (dt % 2, G).
+  unsigned vtread[2][4];
+#pragma unroll
+  for (int dp = 0; dp < 2; ++dp)
+#pragma unroll
+    for (int G = 0; G < 4; ++G) {
+      vtread[dp][G] = r * VTROW + 16 * ((2 * G + hi) ^ ((4 * dp + r / 8) % 8));
+      opaque(vtread[dp][G]);
+    }
+  // PV operand of a tile: output tile dt, 16-key group G = 2 kt + m.
+  auto vop = [&](const char *sv, int dt, int kt, int m) {
+    if constexpr (kStagedV) {
+      return load8(reinterpret_cast<const half_t *>(sv + vtread[dt % 2][2 * kt + m] +
+                                                    32 * dt * VTROW));
+    } else {
+      const unsigned o = vread[dt % 2] + 128 * (dt / 2) + ROWB * (32 * kt + 16 * m);
+      const half4_t lo = read_tr(sv, o), up = read_tr(sv, o + 8 * ROWB);
+      return half8_t{lo[0], lo[1], lo[2], lo[3], up[0], up[1], up[2], up[3]};
+    }
+  };
 
   // Q^T as the MFMA B operand: lane holds query row r, channels
   // 16 s + 8 hi + [0, 8). Rows past T use zeros (their output is dropped).
@@ -168,146 +266,228 @@ void gqa_prefill_kernel(const half_t *__restrict__ q, const half_t *__restrict__
 #pragma unroll
   for (int i = 0; i < DT; ++i)
     oacc[i] = float16_t{0};
-  float mRef = -INFINITY, lRun = 0.0f;
-  half8_t pb[2][2]; // P^T B operands of the previous tile, [32-key half][16-key step]
+  // l (the softmax denominator) is accumulated by the MFMA as ones x P^T,
+  // from the same fp16 probabilities that multiply V: every register of
+  // lacc holds the row sum of the lane's query.
+  float mRef = -INFINITY;
+  float16_t lacc = float16_t{0};
+  const half8_t ones{1, 1, 1, 1, 1, 1, 1, 1};
+  half8_t pb[2][2]; // P^T B operands, [32-key half][16-key step]
 
-  // The two 32-key halves are independent accumulation chains; alternating
-  // them keeps the MFMA pipe full.
-  auto scores = [&](const char *sk, float16_t (&sacc)[2]) {
-    sacc[0] = float16_t{0};
-    sacc[1] = float16_t{0};
+  auto pv = [&](const char *svl) {
 #pragma unroll
-    for (int s = 0; s < KS; ++s)
+    for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-      for (int kt = 0; kt < 2; ++kt)
-        sacc[kt] = mfma32x32x16(load8(reinterpret_cast<const half_t *>(
-                                    sk + kread[s % 4] + 128 * (s / 4) + 32 * ROWB * kt)),
-                                qb[s], sacc[kt]);
+      for (int m = 0; m < 2; ++m) {
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt)
+          oacc[dt] = mfma32x32x16(vop(svl, dt, kt, m), pb[kt][m], oacc[dt]);
+        lacc = mfma32x32x16(ones, pb[kt][m], lacc);
+      }
   };
-  auto pv = [&](const char *sv) {
-#pragma unroll
-    for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-      for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-        for (int m = 0; m < 2; ++m) {
-          const char *p = sv + vread[dt % 2] + 128 * (dt / 2) + ROWB * (32 * kt + 16 * m);
-          half4_t lo = read_tr(p), up = read_tr(p + 8 * ROWB);
-          half8_t a{lo[0], lo[1], lo[2], lo[3], up[0], up[1], up[2], up[3]};
-          oacc[dt] = mfma32x32x16(a, pb[kt][m], oacc[dt]);
-        }
-  };
-  // Softmax of one tile: masks, moves the reference if needed, writes the
-  // fp16 probabilities into pb and returns the rescale factor of O.
-  auto softmax = [&](const float16_t (&sacc)[2], unsigned base, bool masked, bool &raised) {
-    float sv[2][16];
+  // Causal mask as the scores' initial accumulator: -inf where key > P + tq
+  // (a finite K row plus -inf stays -inf), 0 elsewhere.
+  auto mask_init = [&](unsigned base, float16_t (&init)[2]) {
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
       for (int v = 0; v < 16; ++v)
-        sv[kt][v] = sacc[kt][v];
-    if (masked) {
-#pragma unroll
-      for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-        for (int v = 0; v < 16; ++v) {
-          const unsigned key = base + 32 * kt + mfma_c_row(v, hi);
-          if (key > P + tq)
-            sv[kt][v] = -INFINITY;
-        }
-    }
-    float mx = -INFINITY;
-#pragma unroll
-    for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-      for (int v = 0; v < 16; ++v)
-        mx = fmaxf(mx, sv[kt][v]);
+        init[kt][v] = base + 32 * kt + mfma_c_row(v, hi) > P + tq ? -INFINITY : 0.0f;
+  };
+  // Softmax, first half: the tile's row maximum decides whether the
+  // reference moves (then O must be rescaled by the returned factor, which
+  // the caller does when any row of the wave moved); l follows at once.
+  auto reference = [&](float mx, bool &raised) {
     const LanePair pr = pair32(mx);
     const float tm = fmaxf(pr.a, pr.b) * c;
     const bool need = tm - mRef > kRaise;
     const float mNew = need ? tm - kHeadroom : mRef;
     const float alpha = fast_exp2(mRef - mNew);
-    const float negm = -mNew;
-    float psum = 0.0f;
-#pragma unroll
-    for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-      for (int m = 0; m < 2; ++m)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const float p = fast_exp2(fmaf(sv[kt][8 * m + e], c, negm));
-          psum += p;
-          pb[kt][m][e] = (half_t)p;
-        }
-    lRun = lRun * alpha + psum;
     mRef = mNew;
     raised = __builtin_amdgcn_ballot_w64(need) != 0;
     return alpha;
   };
+  // Softmax, second half: the fp16 probabilities of scores sp against the
+  // current reference, as PV operand pb, and their sum into l.
+  auto prob = [&](const float (&sp)[32], int j, float negm) {
+    const int kt = j / 16, m = (j / 8) % 2, e = j % 8;
+    pb[kt][m][e] = (half_t)fast_exp2(fmaf(sp[16 * kt + 8 * m + e], c, negm));
+  };
 
-  // V buffers start zeroed: rows past the block's last key are never
-  // written by the range-checked loads, and a probability of 0 must not
-  // meet a non-finite leftover.
+  // Phase A of step i: the score MFMAs of tile i, each K operand read three
+  // k-steps ahead, with the probabilities of tile i-1 (scores sp) computed
+  // on the VALU in between.
+  auto phase_a = [&](const char *sk, const float16_t *init, const float (&sp)[32],
+                     float16_t (&sacc)[2], auto &&feed) {
+    constexpr int PER = 32 / KS; // probabilities per k-step
+    auto kld = [&](int st, int kt) {
+      return load8(reinterpret_cast<const half_t *>(sk + kread[st % 4] + 128 * (st / 4) +
+                                                    32 * ROWB * kt));
+    };
+    const float negm = -mRef;
+    constexpr int AHEAD = 3;
+    half8_t ka[AHEAD + 1][2];
+#pragma unroll
+    for (int st = 0; st < AHEAD; ++st) {
+      ka[st][0] = kld(st, 0);
+      ka[st][1] = kld(st, 1);
+    }
+    sacc[0] = init ? init[0] : float16_t{0};
+    sacc[1] = init ? init[1] : float16_t{0};
+#pragma unroll
+    for (int st = 0; st < KS; ++st) {
+      if (st + AHEAD < KS) {
+        ka[(st + AHEAD) % (AHEAD + 1)][0] = kld(st + AHEAD, 0);
+        ka[(st + AHEAD) % (AHEAD + 1)][1] = kld(st + AHEAD, 1);
+      }
+      sacc[0] = mfma32x32x16(ka[st % (AHEAD + 1)][0], qb[st], sacc[0]);
+      sacc[1] = mfma32x32x16(ka[st % (AHEAD + 1)][1], qb[st], sacc[1]);
+#pragma unroll
+      for (int u = 0; u < PER; ++u)
+        prob(sp, st * PER + u, negm);
+      if (st % (KS / NPART) == 0)
+        feed(st / (KS / NPART));
+    }
+  };
+  // Phase B of step i: the PV MFMAs of tile i-1, each V^T operand read two
+  // MFMAs ahead, with the row maximum of tile i taken in between.
+  auto phase_b = [&](const char *svl, const float16_t (&sacc)[2], float (&sv)[32],
+                     bool &raised) {
+    constexpr int NPV = 4 * DT, PER = 32 / NPV;
+    // Consecutive MFMAs go to different output tiles (independent chains).
+    auto vld = [&](int n) { return vop(svl, n % DT, n / (2 * DT), (n / DT) % 2); };
+    half8_t va[3];
+    va[0] = vld(0);
+    va[1] = vld(1);
+    float mx = -INFINITY;
+#pragma unroll
+    for (int n = 0; n < NPV; ++n) {
+      if (n + 2 < NPV)
+        va[(n + 2) % 3] = vld(n + 2);
+      const int dt = n % DT, kt = n / (2 * DT), m = (n / DT) % 2;
+      oacc[dt] = mfma32x32x16(va[n % 3], pb[kt][m], oacc[dt]);
+      if (dt == DT - 1)
+        lacc = mfma32x32x16(ones, pb[kt][m], lacc);
+#pragma unroll
+      for (int u = 0; u < PER; ++u) {
+        const int j = n * PER + u;
+        sv[j] = sacc[j / 16][j % 16];
+        mx = fmaxf(mx, sv[j]);
+      }
+    }
+    return reference(mx, raised);
+  };
+
+  // Buffers start zeroed: rows past the block's last key may keep what was
+  // there before, which must be finite (a probability of 0 times V, and the
+  // -inf mask plus a K dot product, must stay exact).
   {
     const uint4_t z{0, 0, 0, 0};
     for (unsigned i = threadIdx.x * 16; i < (unsigned)TILEB; i += 64 * HW * 16) {
+      *reinterpret_cast<uint4_t *>(sK0 + i) = z;
+      *reinterpret_cast<uint4_t *>(sK1 + i) = z;
+    }
+    for (unsigned i = threadIdx.x * 16; i < (unsigned)VBUF; i += 64 * HW * 16) {
       *reinterpret_cast<uint4_t *>(sV0 + i) = z;
       *reinterpret_cast<uint4_t *>(sV1 + i) = z;
     }
   }
   __syncthreads();
   issue_k(0, sK0);
-  issue_v(0, sV0);
+  if constexpr (kStagedV)
+    load_v(0);
+  else
+    issue_v(0, sV0);
   wait_loads();
   __syncthreads();
   if (tiles > 1)
     issue_k(1, sK1);
+
+  // Tile 0: scores and reference only (O is still zero).
+  float sv[32]; // scores of the last tile, raw (masked keys -inf)
   {
-    float16_t sacc[2];
+    float16_t init[2], sacc[2];
+    const bool masked = BN > P + t0 + 1;
+    if (masked)
+      mask_init(0, init);
+    const float zero[32] = {};
+    phase_a(sK0, masked ? init : nullptr, zero, sacc, [](int) {});
+    float mx = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < 32; ++j) {
+      sv[j] = sacc[j / 16][j % 16];
+      mx = fmaxf(mx, sv[j]);
+    }
     bool raised;
-    scores(sK0, sacc);
-    softmax(sacc, 0, BN > P + t0 + 1, raised); // O is still zero: nothing to rescale
+    reference(mx, raised);
   }
 
-  // Step i: scores of tile i, PV of tile i-1, softmax of tile i, with the
-  // loads of K(i+1) and V(i) in flight. Buffers are named statically (the
-  // steady-state loop runs in pairs) so the compiler can tell the loads in
-  // flight from the LDS reads and need not wait for them.
-  auto step = [&](unsigned i, const char *kcur, const char *vprev, char *knext, char *vdst) {
+  // Step i: phase A (scores of tile i, probabilities of tile i-1), phase B
+  // (PV of tile i-1, row maximum of tile i), with the loads of K(i+1) and
+  // V(i) in flight. Buffers are named statically so the compiler can tell
+  // the loads in flight from the LDS reads and need not wait for them;
+  // tiles below the block's first query (the steady state, run in pairs)
+  // skip the mask.
+  auto step = [&](unsigned i, bool masked, const char *kcur, char *vprev, char *knext,
+                  char *vdst) {
     wait_loads();
+    if constexpr (kStagedV)
+      store_vt(vprev); // V(i-1), loaded during the previous step
     __syncthreads();
-    if (i + 1 < tiles)
-      issue_k(i + 1, knext);
-    issue_v(i, vdst);
-    float16_t sacc[2];
+    // K(i+1) (none past the last tile) and V(i), spread over phase A.
+    const __amdgpu_buffer_rsrc_t krs = tile_rsrc(kbase, i + 1), vrs = tile_rsrc(vbase, i);
+    auto feed = [&](int part) {
+      issue(krs, koff, PK, knext, part);
+      if constexpr (kStagedV)
+        load_v_part(vrs, part);
+      else
+        issue(vrs, voff, PV, vdst, part);
+    };
+    float16_t init[2], sacc[2];
+    if (masked)
+      mask_init(i * BN, init);
     bool raised;
-    scores(kcur, sacc);
-    pv(vprev);
-    const float alpha = softmax(sacc, i * BN, i * BN + BN > P + t0 + 1, raised);
+    phase_a(kcur, masked ? init : nullptr, sv, sacc, feed);
+    const float alpha = phase_b(vprev, sacc, sv, raised);
     if (raised) {
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt)
         oacc[dt] *= alpha;
+      lacc *= alpha;
     }
   };
+  // Tiles [1, iu) lie wholly below the block's first query.
+  const unsigned iu = max(1u, min(tiles, (P + t0 + 1) / BN));
   unsigned i = 1;
-  for (; i + 1 < tiles; i += 2) {
-    step(i, sK1, sV0, sK0, sV1);
-    step(i + 1, sK0, sV1, sK1, sV0);
+  for (; i + 1 < iu; i += 2) {
+    step(i, false, sK1, sV0, sK0, sV1);
+    step(i + 1, false, sK0, sV1, sK1, sV0);
   }
-  if (i < tiles) // i == tiles - 1, odd
-    step(i, sK1, sV0, sK0, sV1);
+  // The rest (at most three tiles) with the mask, which is all-pass on an
+  // unmasked tile.
+  for (; i < tiles; i += 2) {
+    step(i, true, sK1, sV0, sK0, sV1);
+    if (i + 1 < tiles)
+      step(i + 1, true, sK0, sV1, sK1, sV0);
+  }
+  {
+    const float negm = -mRef;
+#pragma unroll
+    for (int j = 0; j < 32; ++j)
+      prob(sv, j, negm);
+  }
   wait_loads();
+  if constexpr (kStagedV)
+    store_vt((tiles - 1) % 2 == 0 ? sV0 : sV1);
   __syncthreads();
   if ((tiles - 1) % 2 == 0)
     pv(sV0);
   else
     pv(sV1);
 
-  const LanePair lp = pair32(lRun);
   if (!rowValid)
     return;
-  const float inv = 1.0f / (lp.a + lp.b);
+  const float inv = 1.0f / lacc[0];
   half_t *orow = out + ((size_t)tq * Hq + h) * D;
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt)
