@@ -17,7 +17,7 @@ import torch
 
 from . import _lib
 
-_workspaces: dict[int, torch.Tensor] = {}
+_workspaces: dict[tuple[int, str], torch.Tensor] = {}
 
 
 def _ptr(t: torch.Tensor | None) -> int | None:
@@ -37,11 +37,12 @@ def _require(t: torch.Tensor, dtype: torch.dtype, name: str) -> None:
         raise ValueError(f"{name} must be contiguous")
 
 
-def workspace(nbytes: int, device: torch.device | None = None) -> torch.Tensor:
-    """A workspace of at least nbytes, reused per device (calls on one
-    stream are ordered, so they can share it)."""
+def workspace(nbytes: int, device: torch.device | None = None, kind: str = "gqa") -> torch.Tensor:
+    """A workspace of at least nbytes, reused per (device, kind): calls on
+    one stream are ordered, so they can share it (its contents between calls
+    do not matter)."""
     dev = torch.device("cuda", torch.cuda.current_device()) if device is None else device
-    key = dev.index if dev.index is not None else torch.cuda.current_device()
+    key = (dev.index if dev.index is not None else torch.cuda.current_device(), kind)
     ws = _workspaces.get(key)
     if ws is None or ws.numel() < nbytes:
         ws = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=dev)
@@ -157,7 +158,7 @@ def delta_update(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, beta: torch.
     lib = _lib.load()
     p = delta_params(q, v, state)
     need = lib.llmi_hip_delta_workspace_bytes(p)
-    ws = workspace(need, q.device) if need else None
+    ws = workspace(need, q.device, "delta") if need else None
     _lib.check(lib.llmi_hip_delta_update(_ptr(q), _ptr(k), _ptr(v), _ptr(beta), _ptr(decay),
                                          _ptr(state), _ptr(out), p, _ptr(ws),
                                          ws.numel() if ws is not None else 0, _stream()))
@@ -255,7 +256,7 @@ def bind_delta_update(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     lib = _lib.load()
     p = delta_params(q, v, state)
     need = lib.llmi_hip_delta_workspace_bytes(p)
-    ws = workspace(need, q.device) if need else None
+    ws = workspace(need, q.device, "delta") if need else None
     args = (_ptr(q), _ptr(k), _ptr(v), _ptr(beta), _ptr(decay), _ptr(state), _ptr(out),
             p, _ptr(ws), ws.numel() if ws is not None else 0, _stream())
     names = kernel_names(_lib.OP_DELTA_UPDATE, p)

@@ -65,12 +65,35 @@ def test_decode_cfg2_with_append(gpu):
 
 
 def test_decode_workspace_reuse(gpu):
-    """Two decode calls in a row share the workspace; the second (with a
-    different split count) must not see the first call's tickets."""
+    """Decode calls in a row share the workspace; each (with a different
+    split count) must see only its own partials."""
     print("decode workspace reuse", flush=True)
     for P in (5000, 700, 33, 5000):
         x = oracle.make_gqa_inputs(7 + P, 1, 16, 4, 256, P)
         _check(_run(x, gpu), oracle.gqa_dense_f64(x.q, x.k_cache, x.v_cache, P))
+
+
+@pytest.mark.parametrize("P", [4096, 32768])
+def test_decode_ignores_workspace_contents(gpu, P):
+    """The workspace holds nothing between calls: one filled with NaN
+    patterns gives the same, correct result on every call."""
+    print(f"decode poisoned workspace P={P}", flush=True)
+    lib = _lib.load()
+    x = oracle.make_gqa_inputs(17 + P, 1, 16, 4, 256, P)
+    p = _lib.GqaParams(1, 16, 4, 256, P)
+    need = lib.llmi_hip_gqa_workspace_bytes(p)
+    assert need > 0
+    ws = torch.full((need,), 0xFF, dtype=torch.uint8, device=gpu)
+    q, kc, vc = (u16_to_torch(a, gpu) for a in (x.q, x.k_cache, x.v_cache))
+    want = oracle.gqa_dense_f64(x.q, x.k_cache, x.v_cache, P)
+    for _ in range(2):
+        out = torch.empty_like(q)
+        _lib.check(lib.llmi_hip_causal_gqa(q.data_ptr(), kc.data_ptr(), vc.data_ptr(),
+                                           out.data_ptr(), p, ws.data_ptr(), need,
+                                           torch.cuda.current_stream().cuda_stream))
+        torch.cuda.synchronize()
+        _check(oracle.f16_to_f32(torch_to_u16(out)).astype(np.float64), want)
+        ws.fill_(0xFF)
 
 
 @pytest.mark.parametrize("shape", [(16, 4, 256), (16, 4, 128), (4, 2, 256), (8, 1, 128),
