@@ -20,8 +20,10 @@
 //    on the state, for every chunk at once -- the Gram matrices K K^T and
 //    Q K^T on fp16 MFMA (v_mfma_f32_32x32x16_f16), then per value head the
 //    decay weighting, M, and T by forward substitution in fp32 (one lane
-//    per column of T). Written to the workspace: T, M and the token weights
-//    per (chunk, value head).
+//    per column of T). Written to the workspace, already split into the
+//    hi/lo fp16 pairs the scan's products take: K and Q per (chunk, key
+//    head); T, M and the token weights per (chunk, value head). The scan's
+//    per-chunk staging is then plain 16-byte copies.
 //
 //  * deltaChunkScan, grid (value head, 32-column dv tile): walks the chunks
 //    in order with the state tile S [dk x 32] resident in MFMA accumulators.
@@ -57,19 +59,46 @@ constexpr int KST = DK + 8;  // fp16 stride of [token][dk] rows
 constexpr int CST = C + 8;   // fp16 stride of [*][token] rows
 constexpr int kMaxRatio = 4; // value heads per key head handled by one prep workgroup
 
-// Workspace record per (chunk, value head): T [C][C], M [C][C], then per
-// token e^(g_t), e^(g_C - g_t) and beta_t.
-constexpr size_t kPrepFloats = 2 * C * C + 3 * C;
-constexpr size_t kRecEg = 2 * C * C, kRecEz = kRecEg + C, kRecBeta = kRecEz + C;
+// Workspace. Per (chunk, value head) a record of T and M as hi/lo fp16
+// [C][C] each (Th, Tl, Mh, Ml), then per token e^(g_t), e^(g_C - g_t) and
+// beta_t (fp32). After all records, per (chunk, key head): K and Q of the
+// chunk as hi/lo fp16 [C][DK] (Kh, Kl, Qh, Ql; rows past T are zero).
+constexpr size_t kRecHalves = 4 * C * C;
+constexpr size_t kRecBytes = kRecHalves * 2 + 3 * C * 4;
+constexpr size_t kRecEg = 0, kRecEz = C, kRecBeta = 2 * C; // floats after the halves
+constexpr size_t kKQHalves = 4 * C * DK;
+
+__device__ __forceinline__ half_t *rec_halves(void *ws, size_t c, size_t Hv, size_t h) {
+  return reinterpret_cast<half_t *>(static_cast<char *>(ws) + (c * Hv + h) * kRecBytes);
+}
+__device__ __forceinline__ float *rec_weights(void *ws, size_t c, size_t Hv, size_t h) {
+  return reinterpret_cast<float *>(rec_halves(ws, c, Hv, h) + kRecHalves);
+}
+__device__ __forceinline__ half_t *kq_halves(void *ws, size_t chunks, size_t Hv, size_t c,
+                                             size_t Hk, size_t kh) {
+  return reinterpret_cast<half_t *>(static_cast<char *>(ws) + chunks * Hv * kRecBytes) +
+         (c * Hk + kh) * kKQHalves;
+}
+
+// Split four floats into hi/lo fp16.
+__device__ __forceinline__ void split4(float4_t x, half4_t &hi, half4_t &lo) {
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    half_t a, b;
+    split_f16(x[e], a, b);
+    hi[e] = a;
+    lo[e] = b;
+  }
+}
 
 // --------------------------------------------------------------- prep
 
 __global__ __launch_bounds__(256, 1) void delta_prep_kernel(
     const float *__restrict__ q, const float *__restrict__ k,
     const float *__restrict__ beta, const float *__restrict__ decay,
-    float *__restrict__ prep, unsigned T, unsigned Hk, unsigned Hv) {
+    void *__restrict__ ws, unsigned T, unsigned Hk, unsigned Hv) {
   const unsigned c = blockIdx.x, kh = blockIdx.y;
-  const unsigned R = Hv / Hk;
+  const unsigned R = Hv / Hk, chunks = (T + C - 1) / C;
   const unsigned t0 = c * C, n = min((unsigned)C, T - t0);
   const unsigned tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
   const unsigned r = lane & 31u, hh = lane >> 5;
@@ -80,7 +109,10 @@ __global__ __launch_bounds__(256, 1) void delta_prep_kernel(
   __shared__ double sG[kMaxRatio][C];
   __shared__ float sB[kMaxRatio][C];
 
-  // Keys and queries of the chunk as fp16 (rows past the end are zero).
+  // Keys and queries of the chunk as fp16 (rows past the end are zero):
+  // the hi halves to LDS for the Gram matrices, hi and lo to the workspace
+  // for the scan.
+  half_t *kq = kq_halves(ws, chunks, Hv, c, Hk, kh);
   for (unsigned i = tid; i < C * DK / 4; i += 256) {
     const unsigned t = i / (DK / 4), d4 = (i % (DK / 4)) * 4;
     float4_t kv{0.0f, 0.0f, 0.0f, 0.0f}, qv{0.0f, 0.0f, 0.0f, 0.0f};
@@ -89,14 +121,15 @@ __global__ __launch_bounds__(256, 1) void delta_prep_kernel(
       kv = *reinterpret_cast<const float4_t *>(k + off);
       qv = *reinterpret_cast<const float4_t *>(q + off);
     }
-    half4_t kh4, qh4;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      kh4[e] = (half_t)kv[e];
-      qh4[e] = (half_t)qv[e];
-    }
-    *reinterpret_cast<half4_t *>(sK + t * KST + d4) = kh4;
-    *reinterpret_cast<half4_t *>(sQ + t * KST + d4) = qh4;
+    half4_t khi, klo, qhi, qlo;
+    split4(kv, khi, klo);
+    split4(qv, qhi, qlo);
+    *reinterpret_cast<half4_t *>(sK + t * KST + d4) = khi;
+    *reinterpret_cast<half4_t *>(sQ + t * KST + d4) = qhi;
+    *reinterpret_cast<half4_t *>(kq + 4 * i) = khi;
+    *reinterpret_cast<half4_t *>(kq + C * DK + 4 * i) = klo;
+    *reinterpret_cast<half4_t *>(kq + 2 * C * DK + 4 * i) = qhi;
+    *reinterpret_cast<half4_t *>(kq + 3 * C * DK + 4 * i) = qlo;
   }
   // Cumulative log decay (double) and beta of each value head of this key
   // head: wave w scans head w (padding tokens: decay 1, beta 0).
@@ -135,23 +168,24 @@ __global__ __launch_bounds__(256, 1) void delta_prep_kernel(
   __syncthreads();
 
   // Decay weighting. Thread (row group tq, column s) covers rows tq + 4i:
-  // A (to LDS), M, e^(g_t), e^(g_C - g_t), beta (to the workspace).
+  // A (to LDS), M (hi/lo), e^(g_t), e^(g_C - g_t), beta (to the workspace).
   {
     const unsigned s = tid % C, tq = tid / C;
     for (unsigned hr = 0; hr < R; ++hr) {
-      float *rec = prep + ((size_t)c * Hv + kh * R + hr) * kPrepFloats;
+      half_t *rh = rec_halves(ws, c, Hv, kh * R + hr);
+      float *rw = rec_weights(ws, c, Hv, kh * R + hr);
       const double gs = sG[hr][s];
 #pragma unroll
       for (int i = 0; i < C / 4; ++i) {
         const unsigned t = tq + 4 * i, idx = t * C + s;
         const float e = s <= t ? expf((float)(sG[hr][t] - gs)) : 0.0f;
         sA[hr][idx] = s < t ? sB[hr][t] * e * sKK[idx] : 0.0f;
-        rec[C * C + idx] = e * sQK[idx];
+        split_f16(e * sQK[idx], rh[2 * C * C + idx], rh[3 * C * C + idx]);
       }
       if (tid < C) {
-        rec[kRecEg + tid] = expf((float)sG[hr][tid]);
-        rec[kRecEz + tid] = expf((float)(sG[hr][C - 1] - sG[hr][tid]));
-        rec[kRecBeta + tid] = sB[hr][tid];
+        rw[kRecEg + tid] = expf((float)sG[hr][tid]);
+        rw[kRecEz + tid] = expf((float)(sG[hr][C - 1] - sG[hr][tid]));
+        rw[kRecBeta + tid] = sB[hr][tid];
       }
     }
   }
@@ -172,25 +206,19 @@ __global__ __launch_bounds__(256, 1) void delta_prep_kernel(
       const float sum = (acc[0] + acc[1]) + (acc[2] + acc[3]);
       col[t] = (unsigned)t == j ? 1.0f : ((unsigned)t > j ? -sum : 0.0f);
     }
-    float *rec = prep + ((size_t)c * Hv + kh * R + wave) * kPrepFloats;
+    half_t *rh = rec_halves(ws, c, Hv, kh * R + wave);
 #pragma unroll
     for (int t = 0; t < C; ++t)
-      rec[t * C + j] = col[t];
+      split_f16(col[t], rh[t * C + j], rh[C * C + t * C + j]);
   }
 }
 
 // --------------------------------------------------------------- scan
 
-// Split a float4 into hi/lo fp16 and store them at dst_hi/dst_lo (4 halves).
+// Split a float4 into hi/lo fp16 and store them at hi/lo (4 halves each).
 __device__ __forceinline__ void store_split4(half_t *hi, half_t *lo, float4_t x) {
   half4_t h, l;
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    half_t a, b;
-    split_f16(x[e], a, b);
-    h[e] = a;
-    l[e] = b;
-  }
+  split4(x, h, l);
   *reinterpret_cast<half4_t *>(hi) = h;
   *reinterpret_cast<half4_t *>(lo) = l;
 }
@@ -233,58 +261,57 @@ __device__ __forceinline__ void store_tile_T(half_t *dh, half_t *dl, int stride,
   }
 }
 
-// One chunk's scan inputs as this thread loads them: its share of K and Q
-// (token-major float4s), of T and M, of the V tile, and (threads < C) the
-// token weights. Loaded one chunk ahead so that the global latency hides
-// behind the previous chunk's products.
-constexpr int kKQPer = C * DK / 4 / 256; // float4s of K (and of Q) per thread
-constexpr int kTMPer = C * C / 4 / 256;  // float4s of T (and of M) per thread
+// One chunk's scan inputs as this thread loads them: its share of the
+// pre-split K, Q (8 halves of a token row each), T and M, of the V tile,
+// and (threads < C) the token weights. Loaded one chunk ahead so that the
+// global latency hides behind the previous chunk's products.
+constexpr int kKQPer = C * DK / 8 / 256; // half8s of each of Kh, Kl, Qh, Ql per thread
+constexpr int kTMPer = C * C / 8 / 256;  // half8s of each of Th, Tl, Mh, Ml per thread
 struct ChunkRegs {
-  float4_t k[kKQPer], q[kKQPer], t[kTMPer], m[kTMPer];
+  half8_t kq[4][kKQPer], tm[4][kTMPer];
   half8_t v;
   float eg, ez, b;
 };
 
-__device__ __forceinline__ void load_chunk(ChunkRegs &cr, const float *__restrict__ q,
-                                           const float *__restrict__ k,
-                                           const half_t *__restrict__ v,
-                                           const float *__restrict__ rec, unsigned t0,
-                                           unsigned n, unsigned kh, unsigned Hk,
-                                           size_t vcol, size_t vwidth, unsigned tid) {
+__device__ __forceinline__ void load_chunk(ChunkRegs &cr, const half_t *__restrict__ kq,
+                                           const half_t *__restrict__ rec,
+                                           const half_t *__restrict__ v, unsigned t0,
+                                           unsigned n, size_t vcol, size_t vwidth,
+                                           unsigned tid) {
 #pragma unroll
-  for (int it = 0; it < kKQPer; ++it) {
-    const unsigned i = tid + 256 * it, t = i / (DK / 4), d4 = (i % (DK / 4)) * 4;
-    cr.k[it] = cr.q[it] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
-    if (t < n) {
-      const size_t off = ((size_t)(t0 + t) * Hk + kh) * DK + d4;
-      cr.k[it] = *reinterpret_cast<const float4_t *>(k + off);
-      cr.q[it] = *reinterpret_cast<const float4_t *>(q + off);
-    }
-  }
+  for (int a = 0; a < 4; ++a)
 #pragma unroll
-  for (int it = 0; it < kTMPer; ++it) {
-    const unsigned i = tid + 256 * it, t = i / (C / 4), s4 = (i % (C / 4)) * 4;
-    cr.t[it] = *reinterpret_cast<const float4_t *>(rec + t * C + s4);
-    cr.m[it] = *reinterpret_cast<const float4_t *>(rec + C * C + t * C + s4);
-  }
+    for (int it = 0; it < kKQPer; ++it)
+      cr.kq[a][it] = load8(kq + a * C * DK + 8 * (tid + 256 * it));
+#pragma unroll
+  for (int a = 0; a < 4; ++a)
+#pragma unroll
+    for (int it = 0; it < kTMPer; ++it)
+      cr.tm[a][it] = load8(rec + a * C * C + 8 * (tid + 256 * it));
   const unsigned t = tid / (DT / 8), jj = (tid % (DT / 8)) * 8;
   cr.v = half8_t{0, 0, 0, 0, 0, 0, 0, 0};
   if (t < n)
     cr.v = load8(v + (size_t)(t0 + t) * vwidth + vcol + jj);
   if (tid < C) {
-    cr.eg = rec[kRecEg + tid];
-    cr.ez = rec[kRecEz + tid];
-    cr.b = rec[kRecBeta + tid];
+    const float *w = reinterpret_cast<const float *>(rec + kRecHalves);
+    cr.eg = w[kRecEg + tid];
+    cr.ez = w[kRecEz + tid];
+    cr.b = w[kRecBeta + tid];
   }
 }
 
 __global__ __launch_bounds__(256, 1) void delta_scan_kernel(
-    const float *__restrict__ q, const float *__restrict__ k,
-    const half_t *__restrict__ v, float *__restrict__ state,
-    half_t *__restrict__ out, const float *__restrict__ prep, unsigned T,
-    unsigned Hk, unsigned Hv, unsigned DV) {
+    const half_t *__restrict__ v, float *__restrict__ state, half_t *__restrict__ out,
+    void *__restrict__ ws, unsigned T, unsigned Hk, unsigned Hv, unsigned DV) {
+  // Workgroups are dealt to the 8 XCDs round-robin by block index. Order
+  // the (value head, column tile) pairs key head by key head and give each
+  // XCD a contiguous run of them, so that the workgroups reading one key
+  // head's K and Q share an L2 (exactly so when Hk is a multiple of 8).
   const unsigned tilesPerHead = DV / DT;
-  const unsigned h = blockIdx.x / tilesPerHead, jt = blockIdx.x % tilesPerHead;
+  const unsigned nblocks = gridDim.x;
+  const unsigned L = nblocks % 8 == 0 ? (blockIdx.x % 8) * (nblocks / 8) + blockIdx.x / 8
+                                      : blockIdx.x;
+  const unsigned h = L / tilesPerHead, jt = L % tilesPerHead;
   const unsigned kh = h / (Hv / Hk), j0 = jt * DT;
   const unsigned tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
   const unsigned r = lane & 31u, hh = lane >> 5;
@@ -312,25 +339,30 @@ __global__ __launch_bounds__(256, 1) void delta_scan_kernel(
   store_tile_T(sSh, sSl, KST, 32 * wave, r, hh, S);
 
   const size_t vcol = (size_t)h * DV + j0;
-  auto rec_of = [&](unsigned c) { return prep + ((size_t)c * Hv + h) * kPrepFloats; };
+  auto kq_of = [&](unsigned c) { return kq_halves(ws, chunks, Hv, c, Hk, kh); };
+  auto rec_of = [&](unsigned c) { return rec_halves(ws, c, Hv, h); };
   ChunkRegs cr;
-  load_chunk(cr, q, k, v, rec_of(0), 0, min((unsigned)C, T), kh, Hk, vcol, vwidth, tid);
+  load_chunk(cr, kq_of(0), rec_of(0), v, 0, min((unsigned)C, T), vcol, vwidth, tid);
 
   for (unsigned c = 0; c < chunks; ++c) {
     const unsigned t0 = c * C, n = min((unsigned)C, T - t0);
 
-    // 1. Stage the chunk from registers: K, Q, T, M split; V; weights.
+    // 1. Stage the chunk from registers: K, Q, T, M (hi/lo); V; weights.
 #pragma unroll
     for (int it = 0; it < kKQPer; ++it) {
-      const unsigned i = tid + 256 * it, t = i / (DK / 4), d4 = (i % (DK / 4)) * 4;
-      store_split4(sKh + t * KST + d4, sKl + t * KST + d4, cr.k[it]);
-      store_split4(sQh + t * KST + d4, sQl + t * KST + d4, cr.q[it]);
+      const unsigned i = tid + 256 * it, t = i / (DK / 8), d8 = (i % (DK / 8)) * 8;
+      half_t *const dst[4] = {sKh, sKl, sQh, sQl};
+#pragma unroll
+      for (int a = 0; a < 4; ++a)
+        *reinterpret_cast<half8_t *>(dst[a] + t * KST + d8) = cr.kq[a][it];
     }
 #pragma unroll
     for (int it = 0; it < kTMPer; ++it) {
-      const unsigned i = tid + 256 * it, t = i / (C / 4), s4 = (i % (C / 4)) * 4;
-      store_split4(sTh + t * CST + s4, sTl + t * CST + s4, cr.t[it]);
-      store_split4(sMh + t * CST + s4, sMl + t * CST + s4, cr.m[it]);
+      const unsigned i = tid + 256 * it, t = i / (C / 8), s8 = (i % (C / 8)) * 8;
+      half_t *const dst[4] = {sTh, sTl, sMh, sMl};
+#pragma unroll
+      for (int a = 0; a < 4; ++a)
+        *reinterpret_cast<half8_t *>(dst[a] + t * CST + s8) = cr.tm[a][it];
     }
     {
       const unsigned t = tid / (DT / 8), jj = (tid % (DT / 8)) * 8;
@@ -377,7 +409,7 @@ __global__ __launch_bounds__(256, 1) void delta_scan_kernel(
 
     // 4. Fetch the next chunk while this one finishes.
     if (c + 1 < chunks)
-      load_chunk(cr, q, k, v, rec_of(c + 1), t0 + C, min((unsigned)C, T - t0 - C), kh, Hk,
+      load_chunk(cr, kq_of(c + 1), rec_of(c + 1), v, t0 + C, min((unsigned)C, T - t0 - C),
                  vcol, vwidth, tid);
     // 5. Waves 0-1: U = T X.
     float u[16];
@@ -466,7 +498,7 @@ bool delta_chunked_supported(const DeltaShape &s) {
 
 size_t delta_chunked_workspace_bytes(const DeltaShape &s) {
   const size_t chunks = (s.T + C - 1) / C;
-  return chunks * s.Hv * kPrepFloats * sizeof(float);
+  return chunks * s.Hv * kRecBytes + chunks * s.Hk * kKQHalves * sizeof(half_t);
 }
 
 hipError_t launch_delta_chunked(const float *q, const float *k, const uint16_t *v,
@@ -474,15 +506,14 @@ hipError_t launch_delta_chunked(const float *q, const float *k, const uint16_t *
                                 uint16_t *out, void *ws, const DeltaShape &s,
                                 hipStream_t stream) {
   const unsigned chunks = (s.T + C - 1) / C;
-  float *prep = static_cast<float *>(ws);
   hipLaunchKernelGGL(delta_prep_kernel, dim3(chunks, s.Hk), dim3(256), 0, stream, q, k,
-                     beta, decay, prep, s.T, s.Hk, s.Hv);
+                     beta, decay, ws, s.T, s.Hk, s.Hv);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess)
     return e;
   hipLaunchKernelGGL(delta_scan_kernel, dim3(s.Hv * (s.Dv / DT)), dim3(256), 0, stream,
-                     q, k, reinterpret_cast<const half_t *>(v), state,
-                     reinterpret_cast<half_t *>(out), prep, s.T, s.Hk, s.Hv, s.Dv);
+                     reinterpret_cast<const half_t *>(v), state,
+                     reinterpret_cast<half_t *>(out), ws, s.T, s.Hk, s.Hv, s.Dv);
   return hipGetLastError();
 }
 
