@@ -1,25 +1,38 @@
-// Causal GQA decode: split-K over the KV cache, one kernel.
+// Causal GQA decode: split-K over the KV cache.
 //
 // Replaces the reference's three decode dispatches gqaScores -> gqaSoftmax ->
 // gqaValue (Reference.metal:303-323, Graph.metal:172-230) with one pass over
 // K and V. It is an HBM-bandwidth problem (4 FLOP/byte), so no MFMA:
 //
-//  * grid = (split, kv head, token). A workgroup of W waves streams one key
+//  * grid = (split, kv head, token). A workgroup of 4 waves streams one key
 //    range of one KV head and serves all G = Hq/Hkv query heads of the
 //    group, so each K/V byte leaves HBM once.
 //  * D/16 lanes share one key row: each lane holds 16 channels as two 16-byte
 //    loads, so one wave instruction reads whole 256-byte row segments.
 //  * q.k is v_dot2_f32_f16 on packed fp16 pairs, reduced over the lanes of a
-//    key with DPP row permutes; softmax state (max, sum) and the output
-//    accumulator are fp32, with exp2 on log2e-prescaled scores.
+//    key with DPP row permutes; softmax state (reference, sum) and the
+//    output accumulator are fp32, with exp2 on log2e-prescaled scores.
+//  * On MI355X this loop is VALU-bound before it is HBM-bound: a wave64 VALU
+//    instruction occupies its 16-lane SIMD for 4 cycles, and with G = 4 every
+//    key costs ~30 wave instructions (measured: with the K/V reads served
+//    from L2 the loop alone takes 16 us at 32K). So the per-key arithmetic
+//    is trimmed: the probabilities are packed to fp16 pairs and P.V is
+//    v_dot2_f32_f16 over two keys at once (the sum l is taken from the same
+//    rounded values, so numerator and denominator agree), and the softmax
+//    reference is lazy -- it moves only when a score exceeds it by more than
+//    2^8, so the rescale of the accumulators is almost never executed.
+//  * One wave per SIMD (4-wave workgroups, ~256 VGPRs) with the K/V loads of
+//    the next three sets in flight while one set is scored. (With two waves
+//    per SIMD the older wave wins most VALU issue slots: per-wave timestamps
+//    showed the second wave of every SIMD finishing ~8 us after the first.)
 //  * each lane group runs its own online softmax over its keys; groups,
 //    waves and finally splits are merged with the usual (m, l, o) rescale.
 //  * a one-split launch writes the output directly. Otherwise every
 //    workgroup writes its (m, l, o) partial to the workspace and a second,
-//    small launch merges them: workgroup (head, token, kv head), one thread
-//    per channel, every partial load in flight at once. (Merging inside the
-//    split kernel's last-arriving workgroup was measured slower on MI355X:
-//    the partial stores then need agent-scope release -- a whole-L2
+//    small launch merges them: one 64-thread workgroup per 64 output channels
+//    of a query head, all of its partial loads in flight at once. (Merging
+//    inside the split kernel's last-arriving workgroup was measured slower on
+//    MI355X: the partial stores then need agent-scope release -- a whole-L2
 //    writeback per workgroup, which serialises -- and the single merging
 //    workgroup reads all partials through one CU.)
 //  * optionally (k_new/v_new non-null) the launch also performs the step's
@@ -37,18 +50,23 @@
 namespace llmi {
 namespace {
 
-constexpr int kSlots = 4;          // keys per lane group per iteration
-constexpr unsigned kResidentWaves = 256 * 8; // MI355X: 256 CUs x 8 waves
+constexpr int kSlots = 2;         // keys per lane group in one loaded set
+constexpr int kWaves = 4;         // waves per workgroup, one per SIMD
 constexpr unsigned kMaxSplits = 128;
+constexpr float kHeadroom = 8.0f; // log2 units a score may exceed the reference
+
+// Sets in flight per wave: the loads of kRing - 1 sets overlap the scoring of
+// one. Eight query heads per KV head need twice the accumulators, so less.
+template <int G> constexpr int ring_depth() { return G <= 4 ? 4 : 2; }
 
 template <int D> struct DecodeGeom {
   static constexpr int LPK = D / 16;            // lanes per key row
   static constexpr int KPR = 64 / LPK;          // key rows per wave instruction
-  static constexpr int WaveTile = KPR * kSlots; // keys per wave iteration
+  static constexpr int WaveTile = KPR * kSlots; // keys per wave and set
 };
 
 struct Plan {
-  unsigned waves, splits, keysPerSplit;
+  unsigned splits, keysPerSplit;
 };
 
 unsigned wave_tile(unsigned D) {
@@ -62,9 +80,8 @@ unsigned wave_tile(unsigned D) {
   }
 }
 
-// Tuning knobs, read once. LLMI_DECODE_TARGET_WGS: resident 8-wave
-// workgroups to plan for (default 256: one per CU of MI355X);
-// LLMI_DECODE_WAVES: waves per workgroup, 4 or 8 (default: chosen per shape).
+// Tuning knob, read once. LLMI_DECODE_TARGET_WGS: resident workgroups to
+// plan for (default 256: one per CU of MI355X).
 unsigned env_or(const char *name, unsigned dflt) {
   const char *v = getenv(name);
   if (!v || !*v)
@@ -74,42 +91,29 @@ unsigned env_or(const char *name, unsigned dflt) {
 }
 
 unsigned target_wgs() {
-  static const unsigned v = env_or("LLMI_DECODE_TARGET_WGS", kResidentWaves / 8);
+  static const unsigned v = env_or("LLMI_DECODE_TARGET_WGS", 256);
   return v;
 }
 
-unsigned forced_waves() {
-  static const unsigned v = env_or("LLMI_DECODE_WAVES", 0);
-  return v == 4 || v == 8 ? v : 0;
-}
-
-// The kernel holds ~200 VGPRs, so a CU keeps 2 waves per SIMD resident:
-// 256 CUs x 8 waves over the GPU. The plan gives every wave the fewest
-// 16-key wave tiles for which the whole grid is resident in one round, in
-// 8-wave workgroups (measured faster than 4-wave ones at 4K and 32K: fewer
-// partials to merge, and two threads per merged column).
-
+// The kernel holds ~256 VGPRs, so a CU keeps one 4-wave workgroup resident.
+// The plan gives every wave the fewest sets for which the whole grid is
+// resident in one round.
 Plan plan_for(const GqaShape &s) {
-  const unsigned G = s.Hq / s.Hkv;
   const unsigned wt = wave_tile(s.D);
   const unsigned visible = s.P + s.T;
   const unsigned rows = s.T * s.Hkv;
-  const unsigned budget = target_wgs() * 8; // resident waves to fill
+  const unsigned budget = target_wgs() * kWaves; // resident waves to fill
   const uint64_t waveTiles = (uint64_t)rows * ((visible + wt - 1) / wt);
-  unsigned iters = (unsigned)std::max<uint64_t>(1, (waveTiles + budget - 1) / budget);
-  unsigned waves = 8;
-  if (forced_waves())
-    waves = forced_waves();
-  if (G * s.D > 1024u || G > 4) // merge: a float4 column per thread, a wave per head
-    waves = 8;
-  unsigned kps = wt * waves * iters;
+  const unsigned iters =
+      (unsigned)std::max<uint64_t>(1, (waveTiles + budget - 1) / budget);
+  unsigned kps = wt * kWaves * iters;
   unsigned splits = (visible + kps - 1) / kps;
-  if (splits > kMaxSplits) { // very long contexts: more iterations per wave
+  if (splits > kMaxSplits) { // very long contexts: more sets per wave
     kps = (visible + kMaxSplits - 1) / kMaxSplits;
-    kps = (kps + wt * waves - 1) / (wt * waves) * (wt * waves);
+    kps = (kps + wt * kWaves - 1) / (wt * kWaves) * (wt * kWaves);
     splits = (visible + kps - 1) / kps;
   }
-  return {waves, splits, kps};
+  return {splits, kps};
 }
 
 struct WsLayout {
@@ -187,8 +191,8 @@ __device__ __forceinline__ void merge_pair(LanePair mp, LanePair lp, float (&o)[
   m = M;
 }
 
-template <int D, int G, int W>
-__global__ __launch_bounds__(64 * W) void gqa_decode_kernel(
+template <int D, int G>
+__global__ __launch_bounds__(64 * kWaves) void gqa_decode_kernel(
     const half_t *__restrict__ q, half_t *kc, half_t *vc,
     const half_t *__restrict__ knew, const half_t *__restrict__ vnew,
     half_t *__restrict__ out, float *__restrict__ wml,
@@ -196,7 +200,7 @@ __global__ __launch_bounds__(64 * W) void gqa_decode_kernel(
     unsigned T, unsigned keysPerSplit, unsigned splits, float scoreScale) {
   using Geo = DecodeGeom<D>;
   constexpr int LPK = Geo::LPK, KPR = Geo::KPR;
-  constexpr int NT = 64 * W;
+  constexpr int W = kWaves, NT = 64 * W;
   constexpr int Tile = Geo::WaveTile * W;
   constexpr int F4 = G * D / 4; // float4 columns of one (m, l, o) partial
   const unsigned split = blockIdx.x, kvh = blockIdx.y, t = blockIdx.z;
@@ -242,13 +246,18 @@ __global__ __launch_bounds__(64 * W) void gqa_decode_kernel(
   }
 
   const size_t chan = (size_t)kvh * D + slice * 8;
-  for (unsigned base = begin; base < end; base += Tile) {
+
+  // One set: kSlots keys of each lane group (KPR * kSlots keys per wave,
+  // Tile per workgroup). Keys past the range are clamped to the last key
+  // of the range (an L2 hit) and masked out of the softmax.
+  struct KvSet {
+    half8_t k[kSlots][2], v[kSlots][2];
+  };
+  auto load_set = [&](KvSet &st, unsigned base) {
     const unsigned first = base + wave * Geo::WaveTile + kg;
-    half8_t kx[kSlots][2], vx[kSlots][2];
 #pragma unroll
     for (int n = 0; n < kSlots; ++n) {
-      unsigned key = first + n * KPR;
-      key = key < end ? key : begin;
+      const unsigned key = min(first + n * KPR, end - 1);
       const bool isNew = fused && key >= P;
       const half_t *kp = (isNew ? knew + (size_t)(key - P) * rowStride
                                 : kc + (size_t)key * rowStride) + chan;
@@ -256,52 +265,108 @@ __global__ __launch_bounds__(64 * W) void gqa_decode_kernel(
                                 : vc + (size_t)key * rowStride) + chan;
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
-        kx[n][j] = load8(kp + j * (D / 2));
-        vx[n][j] = load8(vp + j * (D / 2));
+        st.k[n][j] = load8(kp + j * (D / 2));
+        st.v[n][j] = load8(vp + j * (D / 2));
       }
     }
+  };
+
+  // Score one set and fold it into (m, l, o). m is a lazy reference: the
+  // probabilities are 2^(s - m), at most 2^kHeadroom, and m (with l and o)
+  // is rescaled only when some lane's score exceeds it by more than that --
+  // a wave-uniform branch that random-access workloads take a handful of
+  // times per wave.
+  auto consume_set = [&](const KvSet &st, unsigned base) {
+    const unsigned first = base + wave * Geo::WaveTile + kg;
     float sc[kSlots][G];
 #pragma unroll
     for (int n = 0; n < kSlots; ++n) {
-      bool ok = first + n * KPR < end;
+      const bool ok = first + n * KPR < end;
 #pragma unroll
       for (int g = 0; g < G; ++g) {
-        float acc = dot8(qv[g][0], kx[n][0], 0.0f);
-        acc = dot8(qv[g][1], kx[n][1], acc);
+        float acc = dot8(qv[g][0], st.k[n][0], 0.0f);
+        acc = dot8(qv[g][1], st.k[n][1], acc);
         acc = group_sum<LPK>(acc);
         sc[n][g] = ok ? acc * scoreScale : -INFINITY;
       }
     }
+    float tmax[G];
+    bool raise = false;
 #pragma unroll
     for (int g = 0; g < G; ++g) {
-      float tileMax = sc[0][g];
+      tmax[g] = sc[0][g];
 #pragma unroll
       for (int n = 1; n < kSlots; ++n)
-        tileMax = fmaxf(tileMax, sc[n][g]);
-      float mNew = fmaxf(m[g], tileMax);
-      if (mNew == -INFINITY)
-        continue; // nothing visible yet for this lane group
-      float alpha = rescale(m[g], mNew);
-      float p[kSlots];
-      float psum = 0.0f;
-#pragma unroll
-      for (int n = 0; n < kSlots; ++n) {
-        p[n] = rescale(sc[n][g], mNew);
-        psum += p[n];
-      }
-      l[g] = l[g] * alpha + psum;
-      m[g] = mNew;
-#pragma unroll
-      for (int j = 0; j < 2; ++j)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          float acc = o[g][j * 8 + e] * alpha;
-#pragma unroll
-          for (int n = 0; n < kSlots; ++n)
-            acc = fmaf(p[n], (float)vx[n][j][e], acc);
-          o[g][j * 8 + e] = acc;
-        }
+        tmax[g] = fmaxf(tmax[g], sc[n][g]);
+      raise |= tmax[g] > m[g] + kHeadroom;
     }
+    if (__builtin_amdgcn_ballot_w64(raise)) {
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        const float mNew = fmaxf(m[g], tmax[g]);
+        const float alpha = rescale(m[g], mNew);
+        l[g] *= alpha;
+#pragma unroll
+        for (int x = 0; x < 16; ++x)
+          o[g][x] *= alpha;
+        m[g] = mNew;
+      }
+    }
+    // P.V two keys at a time: p of keys (2i, 2i+1) as an fp16 pair against
+    // the two keys' values of one channel, gathered by a byte permute.
+    const half2_t ones{(half_t)1.0f, (half_t)1.0f};
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const float negm = m[g] == -INFINITY ? 0.0f : -m[g]; // nothing seen yet: p = 0
+#pragma unroll
+      for (int i = 0; i < kSlots / 2; ++i) {
+        const half2_t pp = __builtin_bit_cast(
+            half2_t, __builtin_amdgcn_cvt_pkrtz(fast_exp2(sc[2 * i][g] + negm),
+                                                fast_exp2(sc[2 * i + 1][g] + negm)));
+        l[g] = __builtin_amdgcn_fdot2(pp, ones, l[g], false);
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const uint4_t a = __builtin_bit_cast(uint4_t, st.v[2 * i][j]);
+          const uint4_t b = __builtin_bit_cast(uint4_t, st.v[2 * i + 1][j]);
+#pragma unroll
+          for (int w = 0; w < 4; ++w) {
+            const half2_t lo =
+                __builtin_bit_cast(half2_t, __builtin_amdgcn_perm(b[w], a[w], 0x05040100u));
+            const half2_t hi =
+                __builtin_bit_cast(half2_t, __builtin_amdgcn_perm(b[w], a[w], 0x07060302u));
+            float &o0 = o[g][j * 8 + 2 * w], &o1 = o[g][j * 8 + 2 * w + 1];
+            o0 = __builtin_amdgcn_fdot2(pp, lo, o0, false);
+            o1 = __builtin_amdgcn_fdot2(pp, hi, o1, false);
+          }
+        }
+      }
+    }
+  };
+
+  // A ring of R sets: set i + R - 1 is requested before set i is scored. The
+  // loop body covers R sets with compile-time buffer indices, and every path
+  // into its header has the same loads outstanding, which keeps the
+  // compiler's wait counts partial.
+  if (begin < end) {
+    constexpr int R = ring_depth<G>();
+    const unsigned sets = (end - begin + Tile - 1) / Tile;
+    KvSet buf[R];
+#pragma unroll
+    for (int r = 0; r < R - 1; ++r)
+      load_set(buf[r], begin + r * Tile);
+    unsigned base = begin, i = 0;
+    for (; i + R <= sets; i += R) {
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        load_set(buf[(r + R - 1) % R], base + (r + R - 1) * Tile);
+        consume_set(buf[r], base + r * Tile);
+      }
+      base += R * Tile;
+    }
+#pragma unroll
+    for (int r = 0; r < R - 1; ++r)
+      if (i + r < sets)
+        consume_set(buf[r], base + r * Tile);
   }
 
   // Merge the KPR lane groups of the wave (lanes kg*LPK + slice) with VALU
@@ -396,71 +461,59 @@ __global__ __launch_bounds__(64 * W) void gqa_decode_kernel(
   }
 }
 
-// Second-launch merge: workgroup (g, row) combines the splits of query
-// head g of one (token, kv head) row; thread x owns channel x.
+// Second-launch merge: workgroup (channel block, g, row) combines the
+// splits of 64 output channels of query head g of one (token, kv head) row;
+// each thread loads its channel of every partial at once.
 template <int D, int G>
-__global__ __launch_bounds__(D) void gqa_decode_merge_kernel(
+__global__ __launch_bounds__(64) void gqa_decode_merge_kernel(
     const float *__restrict__ wml, const float *__restrict__ wo,
     half_t *__restrict__ out, unsigned Hq, unsigned Hkv, unsigned splits) {
   static_assert(D % 64 == 0, "whole waves");
-  const unsigned g = blockIdx.x, row = blockIdx.y, x = threadIdx.x;
-  const unsigned lane = x & 63u, wave = x >> 6;
+  const unsigned lane = threadIdx.x, g = blockIdx.y, row = blockIdx.z;
+  const unsigned x = blockIdx.x * 64 + lane;
   const float *col = wo + (size_t)row * splits * G * D + (size_t)g * D + x;
   const float *rowMl = wml + (size_t)row * splits * G * 2;
-  constexpr int PER = 32;
+  constexpr int PER = 64;
   float v[PER];
-  auto load_round = [&](unsigned s0) {
 #pragma unroll
-    for (int u = 0; u < PER; ++u) {
-      const unsigned s = s0 + u;
-      v[u] = s < splits ? col[(size_t)s * G * D] : 0.0f;
-    }
-  };
-  load_round(0);
-  __shared__ float sW[kMaxSplits];
-  if (wave == 0) {
-    float ms[2], ls[2];
+  for (int u = 0; u < PER; ++u)
+    v[u] = (unsigned)u < splits ? col[(size_t)u * G * D] : 0.0f;
+  float ms[2], ls[2];
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const unsigned s = lane + 64u * h;
-      ms[h] = s < splits ? rowMl[(s * G + g) * 2 + 0] : -INFINITY;
-      ls[h] = s < splits ? rowMl[(s * G + g) * 2 + 1] : 0.0f;
-    }
-    const float M = wave_max(fmaxf(ms[0], ms[1]));
-    const float L = wave_sum(ls[0] * rescale(ms[0], M) + ls[1] * rescale(ms[1], M));
-    const float invL = 1.0f / L;
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const unsigned s = lane + 64u * h;
-      if (s < splits)
-        sW[s] = rescale(ms[h], M) * invL;
-    }
+  for (int h = 0; h < 2; ++h) {
+    const unsigned s = lane + 64u * h;
+    ms[h] = s < splits ? rowMl[(s * G + g) * 2 + 0] : -INFINITY;
+    ls[h] = s < splits ? rowMl[(s * G + g) * 2 + 1] : 0.0f;
   }
+  const float M = wave_max(fmaxf(ms[0], ms[1]));
+  const float L = wave_sum(ls[0] * rescale(ms[0], M) + ls[1] * rescale(ms[1], M));
+  const float invL = 1.0f / L;
+  static_assert(kMaxSplits == 128, "two weights per lane");
+  __shared__ float sW[kMaxSplits];
+#pragma unroll
+  for (int h = 0; h < 2; ++h)
+    sW[lane + 64 * h] = rescale(ms[h], M) * invL;
   __syncthreads();
   float acc = 0.0f;
-  for (unsigned s0 = 0;;) {
 #pragma unroll
-    for (int u = 0; u < PER; ++u)
-      acc = fmaf(v[u], s0 + u < splits ? sW[s0 + u] : 0.0f, acc);
-    s0 += PER;
-    if (s0 >= splits)
-      break;
-    load_round(s0);
-  }
+  for (int u = 0; u < PER; ++u)
+    acc = fmaf(v[u], sW[u], acc);
+  for (unsigned s = PER; s < splits; ++s)
+    acc = fmaf(col[(size_t)s * G * D], sW[s], acc);
   const unsigned t = row / Hkv, kvh = row % Hkv;
   out[((size_t)t * Hq + kvh * G + g) * D + x] = (half_t)acc;
 }
 
-template <int D, int G, int W>
-hipError_t launch_dgw(const GqaShape &s, const Plan &p, const uint16_t *q,
-                      uint16_t *k, uint16_t *v, const uint16_t *knew,
-                      const uint16_t *vnew, uint16_t *out, void *ws,
-                      hipStream_t stream) {
-  WsLayout w = layout_for(s, p);
+template <int D, int G>
+hipError_t launch_dg(const GqaShape &s, const uint16_t *q, uint16_t *k,
+                     uint16_t *v, const uint16_t *knew, const uint16_t *vnew,
+                     uint16_t *out, void *ws, hipStream_t stream) {
+  const Plan p = plan_for(s);
+  const WsLayout w = layout_for(s, p);
   char *base = static_cast<char *>(ws);
-  float scale = kLog2e / sqrtf((float)D);
-  hipLaunchKernelGGL((gqa_decode_kernel<D, G, W>), dim3(p.splits, s.Hkv, s.T),
-                     dim3(64 * W), 0, stream,
+  const float scale = kLog2e / sqrtf((float)D);
+  hipLaunchKernelGGL((gqa_decode_kernel<D, G>), dim3(p.splits, s.Hkv, s.T),
+                     dim3(64 * kWaves), 0, stream,
                      reinterpret_cast<const half_t *>(q),
                      reinterpret_cast<half_t *>(k), reinterpret_cast<half_t *>(v),
                      reinterpret_cast<const half_t *>(knew),
@@ -473,24 +526,12 @@ hipError_t launch_dgw(const GqaShape &s, const Plan &p, const uint16_t *q,
     hipError_t e = hipGetLastError();
     if (e != hipSuccess)
       return e;
-    hipLaunchKernelGGL((gqa_decode_merge_kernel<D, G>), dim3(G, s.T * s.Hkv),
-                       dim3(D), 0, stream, reinterpret_cast<float *>(base + w.ml),
+    hipLaunchKernelGGL((gqa_decode_merge_kernel<D, G>), dim3(D / 64, G, s.T * s.Hkv),
+                       dim3(64), 0, stream, reinterpret_cast<float *>(base + w.ml),
                        reinterpret_cast<float *>(base + w.o),
                        reinterpret_cast<half_t *>(out), s.Hq, s.Hkv, p.splits);
   }
   return hipGetLastError();
-}
-
-template <int D, int G>
-hipError_t launch_dg(const GqaShape &s, const uint16_t *q, uint16_t *k,
-                     uint16_t *v, const uint16_t *knew, const uint16_t *vnew,
-                     uint16_t *out, void *ws, hipStream_t stream) {
-  Plan p = plan_for(s);
-  if constexpr (G * D <= 1024 && G <= 4) {
-    if (p.waves == 4)
-      return launch_dgw<D, G, 4>(s, p, q, k, v, knew, vnew, out, ws, stream);
-  }
-  return launch_dgw<D, G, 8>(s, p, q, k, v, knew, vnew, out, ws, stream);
 }
 
 template <int D>
