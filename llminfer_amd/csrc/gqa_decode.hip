@@ -158,39 +158,6 @@ __device__ __forceinline__ float wave_sum(float x) {
   return p.a + p.b;
 }
 
-// Combine (m, l, o) with the lane N places further along the 16-lane row.
-// After the N = LPK, 2*LPK, ... < 16 steps every lane holds its row's total.
-template <int N, int G>
-__device__ __forceinline__ void merge_rotated(float (&m)[G], float (&l)[G],
-                                              float (&o)[G][16]) {
-#pragma unroll
-  for (int g = 0; g < G; ++g) {
-    const float m2 = row_ror<N>(m[g]), l2 = row_ror<N>(l[g]);
-    const float M = fmaxf(m[g], m2);
-    const float a1 = rescale(m[g], M), a2 = rescale(m2, M);
-    l[g] = l[g] * a1 + l2 * a2;
-#pragma unroll
-    for (int x = 0; x < 16; ++x)
-      o[g][x] = o[g][x] * a1 + row_ror<N>(o[g][x]) * a2;
-    m[g] = M;
-  }
-}
-
-// Combine the two members of a lane pair; both partners compute the same.
-template <int G, typename Pair>
-__device__ __forceinline__ void merge_pair(LanePair mp, LanePair lp, float (&o)[16],
-                                           float &m, float &l, Pair pair) {
-  const float M = fmaxf(mp.a, mp.b);
-  const float a1 = rescale(mp.a, M), a2 = rescale(mp.b, M);
-  l = lp.a * a1 + lp.b * a2;
-#pragma unroll
-  for (int x = 0; x < 16; ++x) {
-    LanePair op = pair(o[x]);
-    o[x] = op.a * a1 + op.b * a2;
-  }
-  m = M;
-}
-
 template <int D, int G>
 __global__ __launch_bounds__(64 * kWaves) void gqa_decode_kernel(
     const half_t *__restrict__ q, half_t *kc, half_t *vc,
@@ -271,11 +238,11 @@ __global__ __launch_bounds__(64 * kWaves) void gqa_decode_kernel(
     }
   };
 
-  // Score one set and fold it into (m, l, o). m is a lazy reference: the
-  // probabilities are 2^(s - m), at most 2^kHeadroom, and m (with l and o)
-  // is rescaled only when some lane's score exceeds it by more than that --
-  // a wave-uniform branch that random-access workloads take a handful of
-  // times per wave.
+  // Score one set and fold it into (m, l, o). m is a lazy reference, the
+  // same in every lane of the wave: the probabilities are 2^(s - m), at most
+  // 2^kHeadroom, and m (with l and o) is raised only when some score exceeds
+  // it by more than that -- a wave-uniform branch taken a handful of times
+  // per wave.
   auto consume_set = [&](const KvSet &st, unsigned base) {
     const unsigned first = base + wave * Geo::WaveTile + kg;
     float sc[kSlots][G];
@@ -303,7 +270,7 @@ __global__ __launch_bounds__(64 * kWaves) void gqa_decode_kernel(
     if (__builtin_amdgcn_ballot_w64(raise)) {
 #pragma unroll
       for (int g = 0; g < G; ++g) {
-        const float mNew = fmaxf(m[g], tmax[g]);
+        const float mNew = wave_max(fmaxf(m[g], tmax[g])); // one m per wave
         const float alpha = rescale(m[g], mNew);
         l[g] *= alpha;
 #pragma unroll
@@ -369,95 +336,104 @@ __global__ __launch_bounds__(64 * kWaves) void gqa_decode_kernel(
         consume_set(buf[r], base + r * Tile);
   }
 
-  // Merge the KPR lane groups of the wave (lanes kg*LPK + slice) with VALU
-  // lane exchanges only: DPP row rotations for groups narrower than a row,
-  // then the gfx950 row-pair and half-wave swaps. (Cross-lane reads through
-  // the LDS unit cost a dependent round trip each; this chain has none.)
-  if constexpr (LPK <= 4)
-    merge_rotated<4, G>(m, l, o);
-  if constexpr (LPK <= 8)
-    merge_rotated<8, G>(m, l, o);
+  // Combine. m is wave-uniform, so the lane groups of a wave add up plainly:
+  // inside each 16-lane row by DPP rotations, and for G*D > 1024 the two
+  // row pairs by the gfx950 half-wave swap. The kRows row partials of every
+  // wave then meet in LDS, where each thread combines one float4 column
+  // across waves with the (m, l) rescale.
+  constexpr int kRows = G * D <= 1024 ? 4 : 2;
+  auto fold = [](float &x) {
+    if constexpr (LPK <= 4)
+      x += row_ror<4>(x);
+    if constexpr (LPK <= 8)
+      x += row_ror<8>(x);
+    if constexpr (kRows == 2) {
+      const LanePair p = pair32(x);
+      x = p.a + p.b;
+    }
+  };
 #pragma unroll
   for (int g = 0; g < G; ++g) {
-    merge_pair<G>(pair16(m[g]), pair16(l[g]), o[g], m[g], l[g], pair16);
-    merge_pair<G>(pair32(m[g]), pair32(l[g]), o[g], m[g], l[g], pair32);
+    fold(l[g]);
+#pragma unroll
+    for (int x = 0; x < 16; ++x)
+      fold(o[g][x]);
   }
 
-  // Merge the waves through LDS.
-  __shared__ float sM[W][G], sL[W][G];
-  __shared__ __attribute__((aligned(16))) float sO[W][G][D];
+  __shared__ float sM[W][G], sL[W][kRows][G];
+  __shared__ __attribute__((aligned(16))) float sO[W][kRows][G][D];
+  const unsigned rowi = lane / 16;
   if (lane == 0)
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
-      sM[wave][g] = m[g];
-      sL[wave][g] = l[g];
-    }
-  if (kg == 0)
-#pragma unroll
     for (int g = 0; g < G; ++g)
+      sM[wave][g] = m[g];
+  if (lane % 16 < (unsigned)LPK && rowi < (unsigned)kRows) {
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      if (slice == 0)
+        sL[wave][rowi][g] = l[g];
 #pragma unroll
       for (int j = 0; j < 2; ++j)
 #pragma unroll
-        for (int e = 0; e < 8; ++e)
-          sO[wave][g][j * (D / 2) + slice * 8 + e] = o[g][j * 8 + e];
+        for (int h = 0; h < 2; ++h)
+          *reinterpret_cast<float4_t *>(&sO[wave][rowi][g][j * (D / 2) + slice * 8 + 4 * h]) =
+              float4_t{o[g][j * 8 + 4 * h], o[g][j * 8 + 4 * h + 1], o[g][j * 8 + 4 * h + 2],
+                       o[g][j * 8 + 4 * h + 3]};
+    }
+  }
   __syncthreads();
 
-  const size_t row = (size_t)t * Hkv + kvh;
-  half_t *orow = out + ((size_t)t * Hq + kvh * G) * D;
-
-  if (splits == 1) {
-    for (unsigned i = tid; i < (unsigned)F4; i += NT) {
-      const unsigned g = i * 4 / D, x = i * 4 % D;
-      float M = sM[0][g];
+  // Column i: head g, channels [x, x + 4). Returns sum_w a_w o_w and L.
+  auto combine = [&](unsigned i, float &M, float &L) {
+    const unsigned g = i * 4 / D, x = i * 4 % D;
+    M = sM[0][g];
 #pragma unroll
-      for (int w = 1; w < W; ++w)
-        M = fmaxf(M, sM[w][g]);
-      float L = 0.0f, acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int w = 1; w < W; ++w)
+      M = fmaxf(M, sM[w][g]);
+    L = 0.0f;
+    float4_t acc{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-      for (int w = 0; w < W; ++w) {
-        float a = rescale(sM[w][g], M);
-        L += sL[w][g] * a;
+    for (int w = 0; w < W; ++w) {
+      const float a = rescale(sM[w][g], M);
+#pragma unroll
+      for (int r = 0; r < kRows; ++r) {
+        L = fmaf(sL[w][r][g], a, L);
+        const float4_t v = *reinterpret_cast<const float4_t *>(&sO[w][r][g][x]);
 #pragma unroll
         for (int e = 0; e < 4; ++e)
-          acc[e] += sO[w][g][x + e] * a;
+          acc[e] = fmaf(v[e], a, acc[e]);
       }
+    }
+    return acc;
+  };
+
+  if (splits == 1) {
+    half_t *orow = out + ((size_t)t * Hq + kvh * G) * D;
+    for (unsigned i = tid; i < (unsigned)F4; i += NT) {
+      float M, L;
+      const float4_t acc = combine(i, M, L);
       const float inv = 1.0f / L;
-      half4_t hv{(half_t)(acc[0] * inv), (half_t)(acc[1] * inv),
-                 (half_t)(acc[2] * inv), (half_t)(acc[3] * inv)};
-      *reinterpret_cast<half4_t *>(orow + g * D + x) = hv;
+      const unsigned g = i * 4 / D, x = i * 4 % D;
+      *reinterpret_cast<half4_t *>(orow + g * D + x) =
+          half4_t{(half_t)(acc[0] * inv), (half_t)(acc[1] * inv), (half_t)(acc[2] * inv),
+                  (half_t)(acc[3] * inv)};
     }
     return;
   }
 
   // Write this split's partial; the merge launch reads it.
+  const size_t row = (size_t)t * Hkv + kvh;
   float *po = wo + (row * splits + split) * (size_t)(G * D);
   float *pml = wml + (row * splits + split) * (size_t)(G * 2);
   for (unsigned i = tid; i < (unsigned)F4; i += NT) {
-    const unsigned g = i * 4 / D, x = i * 4 % D;
-    float M = sM[0][g];
-#pragma unroll
-    for (int w = 1; w < W; ++w)
-      M = fmaxf(M, sM[w][g]);
-    float4_t acc{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-    for (int w = 0; w < W; ++w) {
-      float a = rescale(sM[w][g], M);
-#pragma unroll
-      for (int e = 0; e < 4; ++e)
-        acc[e] += sO[w][g][x + e] * a;
-    }
+    float M, L;
+    const float4_t acc = combine(i, M, L);
     *reinterpret_cast<float4_t *>(po + i * 4) = acc;
-  }
-  if (tid < (unsigned)G) {
-    const unsigned g = tid;
-    float M = sM[0][g];
-    for (int w = 1; w < W; ++w)
-      M = fmaxf(M, sM[w][g]);
-    float L = 0.0f;
-    for (int w = 0; w < W; ++w)
-      L += sL[w][g] * rescale(sM[w][g], M);
-    pml[g * 2 + 0] = M;
-    pml[g * 2 + 1] = L;
+    if (i * 4 % D == 0) {
+      const unsigned g = i * 4 / D;
+      pml[g * 2 + 0] = M;
+      pml[g * 2 + 1] = L;
+    }
   }
 }
 
