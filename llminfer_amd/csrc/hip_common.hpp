@@ -111,4 +111,9 @@ __device__ __forceinline__ half8_t load8(const half_t *p) {
   return *reinterpret_cast<const half8_t *>(p);
 }
 
+// 16-byte load marked non-temporal: for data read once (streamed K/V).
+__device__ __forceinline__ half8_t load8_stream(const half_t *p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const half8_t *>(p));
+}
+
 } // namespace llmi
