@@ -451,17 +451,21 @@ __global__ __launch_bounds__(64) void gqa_decode_merge_kernel(
   const unsigned x = blockIdx.x * 64 + lane;
   const float *col = wo + (size_t)row * splits * G * D + (size_t)g * D + x;
   const float *rowMl = wml + (size_t)row * splits * G * 2;
+  // Indices past the last split are clamped (valid addresses, zero weight),
+  // so the loads carry no branches and all go out at once.
   constexpr int PER = 64;
+  const unsigned last = splits - 1;
   float v[PER];
 #pragma unroll
   for (int u = 0; u < PER; ++u)
-    v[u] = (unsigned)u < splits ? col[(size_t)u * G * D] : 0.0f;
+    v[u] = col[(size_t)min((unsigned)u, last) * G * D];
   float ms[2], ls[2];
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
-    const unsigned s = lane + 64u * h;
-    ms[h] = s < splits ? rowMl[(s * G + g) * 2 + 0] : -INFINITY;
-    ls[h] = s < splits ? rowMl[(s * G + g) * 2 + 1] : 0.0f;
+    const unsigned s = lane + 64u * h, sc = min(s, last);
+    const float m = rowMl[(sc * G + g) * 2 + 0], l = rowMl[(sc * G + g) * 2 + 1];
+    ms[h] = s < splits ? m : -INFINITY;
+    ls[h] = s < splits ? l : 0.0f;
   }
   const float M = wave_max(fmaxf(ms[0], ms[1]));
   const float L = wave_sum(ls[0] * rescale(ms[0], M) + ls[1] * rescale(ms[1], M));
@@ -470,14 +474,20 @@ __global__ __launch_bounds__(64) void gqa_decode_merge_kernel(
   __shared__ float sW[kMaxSplits];
 #pragma unroll
   for (int h = 0; h < 2; ++h)
-    sW[lane + 64 * h] = rescale(ms[h], M) * invL;
+    sW[lane + 64 * h] = rescale(ms[h], M) * invL; // 0 past the last split
   __syncthreads();
   float acc = 0.0f;
 #pragma unroll
   for (int u = 0; u < PER; ++u)
     acc = fmaf(v[u], sW[u], acc);
-  for (unsigned s = PER; s < splits; ++s)
-    acc = fmaf(col[(size_t)s * G * D], sW[s], acc);
+  if (splits > PER) {
+#pragma unroll
+    for (int u = 0; u < PER; ++u)
+      v[u] = col[(size_t)min((unsigned)(PER + u), last) * G * D];
+#pragma unroll
+    for (int u = 0; u < PER; ++u)
+      acc = fmaf(v[u], sW[PER + u], acc);
+  }
   const unsigned t = row / Hkv, kvh = row % Hkv;
   out[((size_t)t * Hq + kvh * G + g) * D + x] = (half_t)acc;
 }
