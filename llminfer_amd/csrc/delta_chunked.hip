@@ -223,6 +223,16 @@ __device__ __forceinline__ void store_split4(half_t *hi, half_t *lo, float4_t x)
   *reinterpret_cast<half4_t *>(lo) = l;
 }
 
+// ds_read_b64_tr_b16: in each 16-lane group, lane j receives element j % 4 of
+// the 8-byte chunks addressed by lanes j/4, 4 + j/4, 8 + j/4, 12 + j/4.
+__device__ __forceinline__ half4_t read_tr(const half_t *base, unsigned byteOff) {
+  typedef __attribute__((address_space(3))) char lds_char_t;
+  typedef __fp16 fp16x4_t __attribute__((__vector_size__(4 * sizeof(__fp16))));
+  return __builtin_bit_cast(
+      half4_t, __builtin_amdgcn_ds_read_tr16_b64_v4f16(
+                   (__attribute__((address_space(3))) fp16x4_t *)((lds_char_t *)base + byteOff)));
+}
+
 // One 32x32x16 step of a split product: acc += ah.bh and
 // cross += ah.bl + al.bh (the scaled remainders; the lo.lo term is dropped).
 struct SplitAcc {
@@ -377,8 +387,20 @@ __global__ __launch_bounds__(256, 1) void delta_scan_kernel(
     }
     __syncthreads();
 
-    // 2. Waves 0-1: K S, waves 2-3: Q S (row tile mt of the chunk).
+    // 2. Waves 0-1: K S, waves 2-3: Q S (row tile mt of the chunk). The
+    //    per-token scalars of this lane's 16 rows are read first, so their
+    //    LDS latency hides behind the products.
     const int mt = wave & 1;
+    float tEg[16], tB[16], tV[16];
+#pragma unroll
+    for (int x = 0; x < 16; ++x) {
+      const int t = 32 * mt + mfma_c_row(x, hh);
+      tEg[x] = sEg[t];
+      if (wave < 2) {
+        tB[x] = sB[t];
+        tV[x] = sV[t * DT + r];
+      }
+    }
     float16_t acc;
     {
       SplitAcc p{float16_t{0}, float16_t{0}};
@@ -397,11 +419,10 @@ __global__ __launch_bounds__(256, 1) void delta_scan_kernel(
     float x16[16];
 #pragma unroll
     for (int x = 0; x < 16; ++x) {
-      const int t = 32 * mt + mfma_c_row(x, hh);
       if (wave < 2)
-        x16[x] = sB[t] * (sV[t * DT + r] - sEg[t] * acc[x]);
+        x16[x] = tB[x] * (tV[x] - tEg[x] * acc[x]);
       else
-        acc[x] *= sEg[t];
+        acc[x] *= tEg[x];
     }
     if (wave < 2)
       store_tile_T(sXh, sXl, CST, 32 * mt, r, hh, x16);
@@ -456,23 +477,27 @@ __global__ __launch_bounds__(256, 1) void delta_scan_kernel(
               (half_t)split_value(p, x);
       }
     }
-    // 8. S <- e^(g_C) S + K^T Z (wave w: rows d in [32w, 32w + 32)); the
-    //    K^T operand is gathered from the token-major K tile.
+    // 8. S <- e^(g_C) S + K^T Z (wave w: rows d in [32w, 32w + 32)). The
+    //    K^T operand (channel d, tokens 16 ks + 8 hh .. +8) comes from the
+    //    token-major K tile through transposing reads: lane L of a 16-lane
+    //    group addresses token row ko + L/4 (+ 4), channels d0 + 4 (L%4),
+    //    and receives 4 tokens of channel d0 + L.
     {
       const float eC = sEg[C - 1];
       SplitAcc p{float16_t{0}, float16_t{0}};
 #pragma unroll
       for (int x = 0; x < 16; ++x)
         p.acc[x] = S[x] * eC;
+      const unsigned L = lane % 16;
+      const unsigned d0 = 32 * wave + 16 * ((lane % 32) / 16);
 #pragma unroll
       for (int ks = 0; ks < C / 16; ++ks) {
-        const int ko = 16 * ks + 8 * hh;
-        half8_t ah, al;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          ah[e] = sKh[(ko + e) * KST + 32 * wave + r];
-          al[e] = sKl[(ko + e) * KST + 32 * wave + r];
-        }
+        const unsigned ko = 16 * ks + 8 * hh;
+        const unsigned off = ((ko + L / 4) * KST + d0 + 4 * (L % 4)) * 2;
+        const half4_t h0 = read_tr(sKh, off), h1 = read_tr(sKh, off + 4 * KST * 2);
+        const half4_t l0 = read_tr(sKl, off), l1 = read_tr(sKl, off + 4 * KST * 2);
+        const half8_t ah{h0[0], h0[1], h0[2], h0[3], h1[0], h1[1], h1[2], h1[3]};
+        const half8_t al{l0[0], l0[1], l0[2], l0[3], l1[0], l1[1], l1[2], l1[3]};
         mfma_split_a(ah, al, sXh + r * CST + ko, sXl + r * CST + ko, p);
       }
 #pragma unroll
