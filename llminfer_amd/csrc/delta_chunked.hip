@@ -11,37 +11,53 @@
 //
 //   A[t][s] = beta_t e^(g_t - g_s) k_t.k_s  (s < t),  T = (I + A)^-1
 //   M[t][s] = e^(g_t - g_s) q_t.k_s        (s <= t)
-//   X = diag(beta) V - diag(beta e^g) K S    U = T X
+//   U = T diag(beta) (V - diag(e^g) K S)
 //   Y = diag(e^g) Q S + M U                  S <- e^(g_C) S + K^T diag(e^(g_C - g)) U
+//
+// Everything that does not involve the state S is moved out of the serial
+// chain over the chunks. With W = T diag(beta e^g) K and U0 = T diag(beta) V:
+//
+//   Z  = diag(e^(g_C - g)) U = Z0 + Wn S      Wn = -diag(e^(g_C - g)) W
+//                                             Z0 = diag(e^(g_C - g)) U0
+//   Y  = Y0 + Q' S                            Q' = diag(e^g) Q - (M T diag(beta e^g)) K
+//                                             Y0 = M U0
+//   S <- e^(g_C) S + K^T Z
+//
+// so that a chunk costs the serial chain only two products (Wn S, then
+// K^T Z) plus Q' S beside them.
 //
 // Two launches:
 //
-//  * deltaChunkPrep, grid (chunk, key head): everything that does not depend
-//    on the state, for every chunk at once -- the Gram matrices K K^T and
-//    Q K^T on fp16 MFMA (v_mfma_f32_32x32x16_f16), then per value head the
-//    decay weighting, M, and T by forward substitution in fp32 (one lane
-//    per column of T). Written to the workspace, already split into the
-//    hi/lo fp16 pairs the scan's products take: K and Q per (chunk, key
-//    head); T, M and the token weights per (chunk, value head). The scan's
-//    per-chunk staging is then plain 16-byte copies.
+//  * deltaChunkPrep, grid (chunk, key head), 256 threads: every chunk at
+//    once. The Gram matrices K K^T and Q K^T on fp16 MFMA; per value head the
+//    decay weighting, T by blocked forward substitution in fp32, and the
+//    products Wn, Q', Z0, Y0 on fp16 MFMA in split form. The results go to
+//    the workspace already in the register order of the scan's MFMA operands.
 //
-//  * deltaChunkScan, grid (value head, 32-column dv tile): walks the chunks
-//    in order with the state tile S [dk x 32] resident in MFMA accumulators.
-//    Every product that involves the state (K S, Q S, T X, M U, K^T Z) runs
-//    on fp16 MFMA in a split form: x = hi + lo 2^-11 with hi = fp16(x),
-//    lo = fp16((x - hi) 2^11), a.b ~ ah.bh + (ah.bl + al.bh) 2^-11, the
-//    cross terms in a second fp32 accumulator -- 22 significant bits per
-//    operand. A plain fp16 product leaves the fp32
-//    state ~8e-4 relative off the recurrence after 1024 tokens; the split
-//    form ~1e-5 (measured on the cfg4 shapes), well inside the 1e-3 bound.
-//    The Gram matrices only feed T and M and stay plain fp16.
+//  * deltaChunkScan, grid (value head, 16-column dv slice), ONE wave per
+//    workgroup: walks the chunks in order with its state slice S [dk x 16]
+//    in registers. Every product runs on v_mfma_f32_16x16x32_f16, with the
+//    state (and Z) as the B operand straight from the C-layout registers of
+//    the product that made it: the k index of an operand block is permuted
+//    (sigma below) so that the 8 halves a lane supplies are the 8 rows it
+//    holds in two consecutive 16-row C tiles; the A operands (Wn, Q', K^T)
+//    were written by the prep with the same permutation. No LDS round trip,
+//    no barrier. The A operands of the next chunk stream HBM/L2 -> LDS
+//    (buffer_load ... lds) while the current chunk computes; each wave reads
+//    them from LDS with one 16-byte read per lane and block.
+//
+// Split form: x = hi + lo 2^-11 with hi = fp16(x), lo = fp16((x - hi) 2^11),
+// a.b ~ ah.bh + (ah.bl + al.bh) 2^-11, the cross terms in a second fp32
+// accumulator -- 22 significant bits per operand. A plain fp16 product
+// leaves the fp32 state ~8e-4 relative off the recurrence after 1024 tokens;
+// the split form ~1e-5, well inside the 1e-3 bound. The Gram matrices only
+// feed T and M and stay plain fp16.
 //
 // Decays are linear at the op boundary (Graph.metal:143). The cumulative
 // log decay is summed, and differenced, in double: log(0) is clamped to -1e4
 // (e^-1e4 = 0), and in fp32 a difference of two sums near -1e4 would keep
 // only ~1e-3 absolute precision. Only non-positive differences are
-// exponentiated; the scan receives the weights e^(g_t) and e^(g_C - g_t)
-// ready-made.
+// exponentiated.
 #include "hip_common.hpp"
 #include "kernels.hpp"
 
@@ -52,32 +68,57 @@
 namespace llmi {
 namespace {
 
-constexpr int C = 64;        // chunk length
-constexpr int DK = 128;      // key dimension handled by these kernels
-constexpr int DT = 32;       // dv columns per scan workgroup
-constexpr int KST = DK + 8;  // fp16 stride of [token][dk] rows
-constexpr int CST = C + 8;   // fp16 stride of [*][token] rows
-constexpr int kMaxRatio = 4; // value heads per key head handled by one prep workgroup
+constexpr int C = 64;       // chunk length
+constexpr int DK = 128;     // key dimension handled by these kernels
+constexpr int KS = DK + 8;  // fp16 stride of [token][dk] rows in LDS (and of V rows)
+constexpr int CS = C + 8;   // fp16 stride of [*][token] rows in LDS
+constexpr int FS = C + 1;   // fp32 stride of the prep's A and T^T rows
+constexpr int VB = 128;     // dv columns of V the prep stages at a time
 
-// Workspace. Per (chunk, value head) a record of T and M as hi/lo fp16
-// [C][C] each (Th, Tl, Mh, Ml), then per token e^(g_t), e^(g_C - g_t) and
-// beta_t (fp32). After all records, per (chunk, key head): K and Q of the
-// chunk as hi/lo fp16 [C][DK] (Kh, Kl, Qh, Ql; rows past T are zero).
-constexpr size_t kRecHalves = 4 * C * C;
-constexpr size_t kRecBytes = kRecHalves * 2 + 3 * C * 4;
-constexpr size_t kRecEg = 0, kRecEz = C, kRecBeta = 2 * C; // floats after the halves
-constexpr size_t kKQHalves = 4 * C * DK;
+// MFMA operand blocks (v_mfma_f32_16x16x32_f16) in register order: lane l
+// holds 8 halves at halves [8 l, 8 l + 8) of the block.
+//
+// Permuted k: in a 32-wide k block, element e of lane l (g = l / 16) stands
+// for k = sigma(g, e) = 4g + e (e < 4) or 16 + 4g + (e - 4) (e >= 4) -- the
+// rows a lane holds in the C layout of the two 16-row tiles of that block
+// (register r of tile m holds row 16m + 4g + r). A product whose k is
+// permuted the same way in both operands is unchanged.
+//
+// A piece is the operand of one scan product for one chunk: 16 blocks of hi
+// halves, then 16 blocks of lo halves. Wn and Q' pieces: block 4m + kb
+// holds rows t of tile m against permuted k = d in block kb. K^T piece:
+// block 2i + kb holds rows d of tile i against permuted k = t in block kb.
+constexpr int kBlk = 64 * 8;
+constexpr int kPieceBlocks = 16;
+constexpr int kPieceHalves = 2 * kPieceBlocks * kBlk;
+constexpr int kPieceBytes = kPieceHalves * 2;      // 32 KiB
+constexpr int kPieceLoads = kPieceBytes / 1024;    // 16-byte-per-lane loads of a piece
+constexpr int kBufferWord3 = 0x00020000;           // gfx9 raw buffer descriptor, dword 3
+typedef __attribute__((address_space(3))) void lds_void_t;
 
-__device__ __forceinline__ half_t *rec_halves(void *ws, size_t c, size_t Hv, size_t h) {
-  return reinterpret_cast<half_t *>(static_cast<char *>(ws) + (c * Hv + h) * kRecBytes);
+// Workspace. Per (chunk, value head) a record: the Wn piece, the Q' piece,
+// then Z0 and Y0 as fp32 in C-layout register order, per 16-column slice js
+// and 16-row tile m a 64-lane block of float4 (block 4 js + m), then 64
+// floats of scalars (e^(g_C) first). After all records, per (chunk, key
+// head) the K^T piece.
+constexpr int kScalarBytes = 256;
+__host__ __device__ inline size_t rec_bytes(unsigned DV) {
+  return 2 * (size_t)kPieceBytes + 2 * (size_t)C * DV * sizeof(float) + kScalarBytes;
 }
-__device__ __forceinline__ float *rec_weights(void *ws, size_t c, size_t Hv, size_t h) {
-  return reinterpret_cast<float *>(rec_halves(ws, c, Hv, h) + kRecHalves);
+__host__ __device__ inline size_t rec_scalars(unsigned DV) {
+  return 2 * (size_t)kPieceBytes + 2 * (size_t)C * DV * sizeof(float);
 }
-__device__ __forceinline__ half_t *kq_halves(void *ws, size_t chunks, size_t Hv, size_t c,
-                                             size_t Hk, size_t kh) {
-  return reinterpret_cast<half_t *>(static_cast<char *>(ws) + chunks * Hv * kRecBytes) +
-         (c * Hk + kh) * kKQHalves;
+__device__ __forceinline__ char *rec_ptr(void *ws, size_t recB, size_t Hv, size_t c,
+                                         size_t h) {
+  return static_cast<char *>(ws) + (c * Hv + h) * recB;
+}
+__device__ __forceinline__ char *kpiece_ptr(void *ws, size_t recB, size_t chunks, size_t Hv,
+                                            size_t Hk, size_t c, size_t kh) {
+  return static_cast<char *>(ws) + chunks * Hv * recB + (c * Hk + kh) * kPieceBytes;
+}
+
+__device__ __forceinline__ float4_t mfma16(half8_t a, half8_t b, float4_t c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
 // Split four floats into hi/lo fp16.
@@ -91,140 +132,31 @@ __device__ __forceinline__ void split4(float4_t x, half4_t &hi, half4_t &lo) {
   }
 }
 
-// --------------------------------------------------------------- prep
-
-__global__ __launch_bounds__(256, 1) void delta_prep_kernel(
-    const float *__restrict__ q, const float *__restrict__ k,
-    const float *__restrict__ beta, const float *__restrict__ decay,
-    void *__restrict__ ws, unsigned T, unsigned Hk, unsigned Hv) {
-  const unsigned c = blockIdx.x, kh = blockIdx.y;
-  const unsigned R = Hv / Hk, chunks = (T + C - 1) / C;
-  const unsigned t0 = c * C, n = min((unsigned)C, T - t0);
-  const unsigned tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
-  const unsigned r = lane & 31u, hh = lane >> 5;
-
-  __shared__ __attribute__((aligned(16))) half_t sK[C * KST], sQ[C * KST];
-  __shared__ __attribute__((aligned(16))) float sKK[C * C], sQK[C * C];
-  __shared__ __attribute__((aligned(16))) float sA[kMaxRatio][C * C];
-  __shared__ double sG[kMaxRatio][C];
-  __shared__ float sB[kMaxRatio][C];
-
-  // Keys and queries of the chunk as fp16 (rows past the end are zero):
-  // the hi halves to LDS for the Gram matrices, hi and lo to the workspace
-  // for the scan.
-  half_t *kq = kq_halves(ws, chunks, Hv, c, Hk, kh);
-  for (unsigned i = tid; i < C * DK / 4; i += 256) {
-    const unsigned t = i / (DK / 4), d4 = (i % (DK / 4)) * 4;
-    float4_t kv{0.0f, 0.0f, 0.0f, 0.0f}, qv{0.0f, 0.0f, 0.0f, 0.0f};
-    if (t < n) {
-      const size_t off = ((size_t)(t0 + t) * Hk + kh) * DK + d4;
-      kv = *reinterpret_cast<const float4_t *>(k + off);
-      qv = *reinterpret_cast<const float4_t *>(q + off);
-    }
-    half4_t khi, klo, qhi, qlo;
-    split4(kv, khi, klo);
-    split4(qv, qhi, qlo);
-    *reinterpret_cast<half4_t *>(sK + t * KST + d4) = khi;
-    *reinterpret_cast<half4_t *>(sQ + t * KST + d4) = qhi;
-    *reinterpret_cast<half4_t *>(kq + 4 * i) = khi;
-    *reinterpret_cast<half4_t *>(kq + C * DK + 4 * i) = klo;
-    *reinterpret_cast<half4_t *>(kq + 2 * C * DK + 4 * i) = qhi;
-    *reinterpret_cast<half4_t *>(kq + 3 * C * DK + 4 * i) = qlo;
-  }
-  // Cumulative log decay (double) and beta of each value head of this key
-  // head: wave w scans head w (padding tokens: decay 1, beta 0).
-  if (wave < R) {
-    const unsigned h = kh * R + wave, t = lane;
-    const float a = t < n ? decay[(size_t)(t0 + t) * Hv + h] : 1.0f;
-    const float b = t < n ? beta[(size_t)(t0 + t) * Hv + h] : 0.0f;
-    double g = a > 0.0f ? (double)logf(a) : -1.0e4;
+// B operand (or permuted-k A operand) of one 32-wide k block from two
+// C-layout tiles: elements 0-3 from `a`, 4-7 from `b`, split hi/lo.
+__device__ __forceinline__ void split8(float4_t a, float4_t b, half8_t &hi, half8_t &lo) {
 #pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-      const double up = __shfl_up(g, off);
-      if (lane >= (unsigned)off)
-        g += up;
-    }
-    sG[wave][t] = g;
-    sB[wave][t] = b;
-  }
-  __syncthreads();
-
-  // K K^T and Q K^T, four 32x32 tiles each; wave w takes tiles w and w + 4.
-#pragma unroll
-  for (int rep = 0; rep < 2; ++rep) {
-    const int tile = wave + 4 * rep;
-    const half_t *a = tile < 4 ? sK : sQ;
-    const int mt = (tile % 4) / 2, nt = tile % 2;
-    float16_t acc = float16_t{0};
-#pragma unroll
-    for (int ks = 0; ks < DK / 16; ++ks)
-      acc = mfma32x32x16(load8(a + (32 * mt + r) * KST + 16 * ks + 8 * hh),
-                         load8(sK + (32 * nt + r) * KST + 16 * ks + 8 * hh), acc);
-    float *dst = tile < 4 ? sKK : sQK;
-#pragma unroll
-    for (int v = 0; v < 16; ++v)
-      dst[(32 * mt + mfma_c_row(v, hh)) * C + 32 * nt + r] = acc[v];
-  }
-  __syncthreads();
-
-  // Decay weighting. Thread (row group tq, column s) covers rows tq + 4i:
-  // A (to LDS), M (hi/lo), e^(g_t), e^(g_C - g_t), beta (to the workspace).
-  {
-    const unsigned s = tid % C, tq = tid / C;
-    for (unsigned hr = 0; hr < R; ++hr) {
-      half_t *rh = rec_halves(ws, c, Hv, kh * R + hr);
-      float *rw = rec_weights(ws, c, Hv, kh * R + hr);
-      const double gs = sG[hr][s];
-#pragma unroll
-      for (int i = 0; i < C / 4; ++i) {
-        const unsigned t = tq + 4 * i, idx = t * C + s;
-        const float e = s <= t ? expf((float)(sG[hr][t] - gs)) : 0.0f;
-        sA[hr][idx] = s < t ? sB[hr][t] * e * sKK[idx] : 0.0f;
-        split_f16(e * sQK[idx], rh[2 * C * C + idx], rh[3 * C * C + idx]);
-      }
-      if (tid < C) {
-        rw[kRecEg + tid] = expf((float)sG[hr][tid]);
-        rw[kRecEz + tid] = expf((float)(sG[hr][C - 1] - sG[hr][tid]));
-        rw[kRecBeta + tid] = sB[hr][tid];
-      }
-    }
-  }
-  __syncthreads();
-
-  // T = (I + A)^-1 by forward substitution: lane j of wave w owns column j
-  // of value head w's T, T[t][j] = delta_tj - sum_{s<t} A[t][s] T[s][j].
-  if (wave < R) {
-    const float *A = sA[wave];
-    const unsigned j = lane;
-    float col[C];
-#pragma unroll
-    for (int t = 0; t < C; ++t) {
-      float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-      for (int u = 0; u < t; ++u)
-        acc[u & 3] = fmaf(A[t * C + u], col[u], acc[u & 3]);
-      const float sum = (acc[0] + acc[1]) + (acc[2] + acc[3]);
-      col[t] = (unsigned)t == j ? 1.0f : ((unsigned)t > j ? -sum : 0.0f);
-    }
-    half_t *rh = rec_halves(ws, c, Hv, kh * R + wave);
-#pragma unroll
-    for (int t = 0; t < C; ++t)
-      split_f16(col[t], rh[t * C + j], rh[C * C + t * C + j]);
+  for (int e = 0; e < 4; ++e) {
+    half_t x, y;
+    split_f16(a[e], x, y);
+    hi[e] = x;
+    lo[e] = y;
+    split_f16(b[e], x, y);
+    hi[4 + e] = x;
+    lo[4 + e] = y;
   }
 }
 
-// --------------------------------------------------------------- scan
-
-// Split a float4 into hi/lo fp16 and store them at hi/lo (4 halves each).
-__device__ __forceinline__ void store_split4(half_t *hi, half_t *lo, float4_t x) {
-  half4_t h, l;
-  split4(x, h, l);
-  *reinterpret_cast<half4_t *>(hi) = h;
-  *reinterpret_cast<half4_t *>(lo) = l;
+__device__ __forceinline__ half8_t cat8(half4_t a, half4_t b) {
+  return half8_t{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+}
+__device__ __forceinline__ half4_t load4(const half_t *p) {
+  return *reinterpret_cast<const half4_t *>(p);
 }
 
-// ds_read_b64_tr_b16: in each 16-lane group, lane j receives element j % 4 of
-// the 8-byte chunks addressed by lanes j/4, 4 + j/4, 8 + j/4, 12 + j/4.
+// ds_read_b64_tr_b16: in each 16-lane group, lane L addresses the 8 bytes at
+// row r0 + L/4, columns c0 + 4 (L%4) and receives the column c0 + L of rows
+// r0 .. r0 + 3.
 __device__ __forceinline__ half4_t read_tr(const half_t *base, unsigned byteOff) {
   typedef __attribute__((address_space(3))) char lds_char_t;
   typedef __fp16 fp16x4_t __attribute__((__vector_size__(4 * sizeof(__fp16))));
@@ -233,297 +165,644 @@ __device__ __forceinline__ half4_t read_tr(const half_t *base, unsigned byteOff)
                    (__attribute__((address_space(3))) fp16x4_t *)((lds_char_t *)base + byteOff)));
 }
 
-// One 32x32x16 step of a split product: acc += ah.bh and
-// cross += ah.bl + al.bh (the scaled remainders; the lo.lo term is dropped).
-struct SplitAcc {
-  float16_t acc, cross;
-};
-__device__ __forceinline__ void mfma_split(const half_t *ah, const half_t *al,
-                                           const half_t *bh, const half_t *bl,
-                                           SplitAcc &p) {
-  const half8_t a = load8(ah), b = load8(bh);
-  p.acc = mfma32x32x16(a, b, p.acc);
-  p.cross = mfma32x32x16(a, load8(bl), p.cross);
-  p.cross = mfma32x32x16(load8(al), b, p.cross);
-}
-__device__ __forceinline__ void mfma_split_a(half8_t ah, half8_t al, const half_t *bh,
-                                             const half_t *bl, SplitAcc &p) {
-  const half8_t b = load8(bh);
-  p.acc = mfma32x32x16(ah, b, p.acc);
-  p.cross = mfma32x32x16(ah, load8(bl), p.cross);
-  p.cross = mfma32x32x16(al, b, p.cross);
-}
-__device__ __forceinline__ float split_value(const SplitAcc &p, int v) {
-  return p.acc[v] + p.cross[v] * kSplitUnscale;
+// Operand of 8 consecutive k for one row/column, from a row-major [k][x]
+// LDS matrix with `stride` halves: lane (g, L) gets X[k0 + 8g + e][x0 + L].
+__device__ __forceinline__ half8_t read_kcol(const half_t *X, int stride, unsigned k0,
+                                             unsigned x0, unsigned g, unsigned L) {
+  const unsigned off = ((k0 + 8 * g + L / 4) * stride + x0 + 4 * (L % 4)) * 2;
+  return cat8(read_tr(X, off), read_tr(X, off + 4 * stride * 2));
 }
 
-// Write a C-layout 32x32 tile transposed, as hi/lo fp16, to dst[col][row]
-// (row stride `stride` halves): lane (r, h) holds column r and rows
-// 8q + 4h + [0, 4) of register group q, i.e. four consecutive rows.
-__device__ __forceinline__ void store_tile_T(half_t *dh, half_t *dl, int stride,
-                                             int row0, unsigned r, unsigned hh,
-                                             const float (&x)[16]) {
-#pragma unroll
-  for (int qd = 0; qd < 4; ++qd) {
-    const int row = row0 + 8 * qd + 4 * (int)hh;
-    store_split4(dh + r * stride + row, dl + r * stride + row,
-                 float4_t{x[4 * qd], x[4 * qd + 1], x[4 * qd + 2], x[4 * qd + 3]});
-  }
-}
+// --------------------------------------------------------------- prep
 
-// One chunk's scan inputs as this thread loads them: its share of the
-// pre-split K, Q (8 halves of a token row each), T and M, of the V tile,
-// and (threads < C) the token weights. Loaded one chunk ahead so that the
-// global latency hides behind the previous chunk's products.
-constexpr int kKQPer = C * DK / 8 / 256; // half8s of each of Kh, Kl, Qh, Ql per thread
-constexpr int kTMPer = C * C / 8 / 256;  // half8s of each of Th, Tl, Mh, Ml per thread
-struct ChunkRegs {
-  half8_t kq[4][kKQPer], tm[4][kTMPer];
-  half8_t v;
-  float eg, ez, b;
-};
-
-__device__ __forceinline__ void load_chunk(ChunkRegs &cr, const half_t *__restrict__ kq,
-                                           const half_t *__restrict__ rec,
-                                           const half_t *__restrict__ v, unsigned t0,
-                                           unsigned n, size_t vcol, size_t vwidth,
-                                           unsigned tid) {
-#pragma unroll
-  for (int a = 0; a < 4; ++a)
-#pragma unroll
-    for (int it = 0; it < kKQPer; ++it)
-      cr.kq[a][it] = load8(kq + a * C * DK + 8 * (tid + 256 * it));
-#pragma unroll
-  for (int a = 0; a < 4; ++a)
-#pragma unroll
-    for (int it = 0; it < kTMPer; ++it)
-      cr.tm[a][it] = load8(rec + a * C * C + 8 * (tid + 256 * it));
-  const unsigned t = tid / (DT / 8), jj = (tid % (DT / 8)) * 8;
-  cr.v = half8_t{0, 0, 0, 0, 0, 0, 0, 0};
-  if (t < n)
-    cr.v = load8(v + (size_t)(t0 + t) * vwidth + vcol + jj);
-  if (tid < C) {
-    const float *w = reinterpret_cast<const float *>(rec + kRecHalves);
-    cr.eg = w[kRecEg + tid];
-    cr.ez = w[kRecEz + tid];
-    cr.b = w[kRecBeta + tid];
-  }
-}
-
-__global__ __launch_bounds__(256, 1) void delta_scan_kernel(
-    const half_t *__restrict__ v, float *__restrict__ state, half_t *__restrict__ out,
-    void *__restrict__ ws, unsigned T, unsigned Hk, unsigned Hv, unsigned DV) {
-  // Workgroups are dealt to the 8 XCDs round-robin by block index. Order
-  // the (value head, column tile) pairs key head by key head and give each
-  // XCD a contiguous run of them, so that the workgroups reading one key
-  // head's K and Q share an L2 (exactly so when Hk is a multiple of 8).
-  const unsigned tilesPerHead = DV / DT;
-  const unsigned nblocks = gridDim.x;
-  const unsigned L = nblocks % 8 == 0 ? (blockIdx.x % 8) * (nblocks / 8) + blockIdx.x / 8
-                                      : blockIdx.x;
-  const unsigned h = L / tilesPerHead, jt = L % tilesPerHead;
-  const unsigned kh = h / (Hv / Hk), j0 = jt * DT;
+__global__ __launch_bounds__(256, 1) void delta_prep_kernel(
+    const float *__restrict__ q, const float *__restrict__ k, const half_t *__restrict__ v,
+    const float *__restrict__ beta, const float *__restrict__ decay, void *__restrict__ ws,
+    unsigned T, unsigned Hk, unsigned Hv, unsigned DV) {
+  const unsigned c = blockIdx.x, kh = blockIdx.y;
+  const unsigned R = Hv / Hk, chunks = (T + C - 1) / C;
+  const unsigned t0 = c * C, n = min((unsigned)C, T - t0);
   const unsigned tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
-  const unsigned r = lane & 31u, hh = lane >> 5;
-  const unsigned chunks = (T + C - 1) / C;
-  const size_t vwidth = (size_t)Hv * DV;
+  const unsigned g = lane >> 4, L = lane & 15u;
+  const size_t recB = rec_bytes(DV);
+  const size_t qkStride = (size_t)Hk * DK, vStride = (size_t)Hv * DV;
 
-  // K and Q token-major, T, M, the state transposed S^T [j][d], X^T (later
-  // Z^T) and U^T, all hi/lo.
-  __shared__ __attribute__((aligned(16))) half_t sKh[C * KST], sKl[C * KST];
-  __shared__ __attribute__((aligned(16))) half_t sQh[C * KST], sQl[C * KST];
-  __shared__ __attribute__((aligned(16))) half_t sTh[C * CST], sTl[C * CST];
-  __shared__ __attribute__((aligned(16))) half_t sMh[C * CST], sMl[C * CST];
-  __shared__ __attribute__((aligned(16))) half_t sSh[DT * KST], sSl[DT * KST];
-  __shared__ __attribute__((aligned(16))) half_t sXh[DT * CST], sXl[DT * CST];
-  __shared__ __attribute__((aligned(16))) half_t sUh[DT * CST], sUl[DT * CST];
-  __shared__ float sV[C * DT];
-  __shared__ float sEg[C], sEz[C], sB[C];
+  __shared__ __attribute__((aligned(16))) half_t sKh[C * KS], sKl[C * KS];
+  __shared__ __attribute__((aligned(16))) half_t sQV[C * KS]; // Q hi, later a V block
+  __shared__ __attribute__((aligned(16))) float sKK[C * C], sQK[C * C];
+  // A, T^T and the substitution's R blocks (fp32), later T_w^T and T_b^T
+  // (hi/lo fp16).
+  __shared__ __attribute__((aligned(16))) float sP[4 * C * CS / 2];
+  __shared__ __attribute__((aligned(16))) half_t sMh[C * CS], sMl[C * CS];
+  __shared__ __attribute__((aligned(16))) half_t sNh[C * CS], sNl[C * CS];
+  __shared__ double sG[C];
+  __shared__ float sB[C], sEg[C], sEz[C];
+  static_assert(2 * C * FS + 3 * 256 <= 4 * C * CS / 2, "A, T^T and R share sP");
 
-  // The state tile: wave w holds rows d in [32w, 32w + 32), column r.
-  float S[16];
-  float *stile = state + (size_t)h * DK * DV + j0 + r;
-#pragma unroll
-  for (int x = 0; x < 16; ++x)
-    S[x] = stile[(size_t)(32 * wave + mfma_c_row(x, hh)) * DV];
-  store_tile_T(sSh, sSl, KST, 32 * wave, r, hh, S);
+  float *const sA = sP, *const sTT = sP + C * FS, *const sR = sP + 2 * C * FS;
+  half_t *const sTwh = reinterpret_cast<half_t *>(sP), *const sTwl = sTwh + C * CS;
+  half_t *const sTbh = sTwl + C * CS, *const sTbl = sTbh + C * CS;
 
-  const size_t vcol = (size_t)h * DV + j0;
-  auto kq_of = [&](unsigned c) { return kq_halves(ws, chunks, Hv, c, Hk, kh); };
-  auto rec_of = [&](unsigned c) { return rec_halves(ws, c, Hv, h); };
-  ChunkRegs cr;
-  load_chunk(cr, kq_of(0), rec_of(0), v, 0, min((unsigned)C, T), vcol, vwidth, tid);
+  // Keys and queries of the chunk as fp16 hi/lo (rows past the end are zero).
+  for (unsigned i = tid; i < C * DK / 4; i += 256) {
+    const unsigned t = i / (DK / 4), d4 = (i % (DK / 4)) * 4;
+    float4_t kv{0.0f, 0.0f, 0.0f, 0.0f}, qv{0.0f, 0.0f, 0.0f, 0.0f};
+    if (t < n) {
+      const size_t off = (size_t)(t0 + t) * qkStride + (size_t)kh * DK + d4;
+      kv = *reinterpret_cast<const float4_t *>(k + off);
+      qv = *reinterpret_cast<const float4_t *>(q + off);
+    }
+    half4_t khi, klo, qhi, qlo;
+    split4(kv, khi, klo);
+    split4(qv, qhi, qlo);
+    *reinterpret_cast<half4_t *>(sKh + t * KS + d4) = khi;
+    *reinterpret_cast<half4_t *>(sKl + t * KS + d4) = klo;
+    *reinterpret_cast<half4_t *>(sQV + t * KS + d4) = qhi;
+  }
+  __syncthreads();
 
-  for (unsigned c = 0; c < chunks; ++c) {
-    const unsigned t0 = c * C, n = min((unsigned)C, T - t0);
-
-    // 1. Stage the chunk from registers: K, Q, T, M (hi/lo); V; weights.
+  // The K^T piece of this (chunk, key head): block b = 2i + kb, lane (g, L)
+  // element e = K[32 kb + sigma(g, e)][16 i + L].
+  {
+    half_t *kp = reinterpret_cast<half_t *>(kpiece_ptr(ws, recB, chunks, Hv, Hk, c, kh));
 #pragma unroll
-    for (int it = 0; it < kKQPer; ++it) {
-      const unsigned i = tid + 256 * it, t = i / (DK / 8), d8 = (i % (DK / 8)) * 8;
-      half_t *const dst[4] = {sKh, sKl, sQh, sQl};
-#pragma unroll
-      for (int a = 0; a < 4; ++a)
-        *reinterpret_cast<half8_t *>(dst[a] + t * KST + d8) = cr.kq[a][it];
+    for (int bi = 0; bi < 4; ++bi) {
+      const unsigned b = 4 * wave + bi, i = b / 2, kb = b % 2;
+      const unsigned off0 = ((32 * kb + 4 * g + L / 4) * KS + 16 * i + 4 * (L % 4)) * 2;
+      const unsigned off1 = off0 + 16 * KS * 2;
+      *reinterpret_cast<half8_t *>(kp + b * kBlk + 8 * lane) =
+          cat8(read_tr(sKh, off0), read_tr(sKh, off1));
+      *reinterpret_cast<half8_t *>(kp + (kPieceBlocks + b) * kBlk + 8 * lane) =
+          cat8(read_tr(sKl, off0), read_tr(sKl, off1));
     }
-#pragma unroll
-    for (int it = 0; it < kTMPer; ++it) {
-      const unsigned i = tid + 256 * it, t = i / (C / 8), s8 = (i % (C / 8)) * 8;
-      half_t *const dst[4] = {sTh, sTl, sMh, sMl};
-#pragma unroll
-      for (int a = 0; a < 4; ++a)
-        *reinterpret_cast<half8_t *>(dst[a] + t * CST + s8) = cr.tm[a][it];
-    }
-    {
-      const unsigned t = tid / (DT / 8), jj = (tid % (DT / 8)) * 8;
-#pragma unroll
-      for (int e = 0; e < 8; ++e)
-        sV[t * DT + jj + e] = (float)cr.v[e];
-    }
-    if (tid < C) {
-      sEg[tid] = cr.eg;
-      sEz[tid] = cr.ez;
-      sB[tid] = cr.b;
-    }
-    __syncthreads();
-
-    // 2. Waves 0-1: K S, waves 2-3: Q S (row tile mt of the chunk). The
-    //    per-token scalars of this lane's 16 rows are read first, so their
-    //    LDS latency hides behind the products.
-    const int mt = wave & 1;
-    float tEg[16], tB[16], tV[16];
-#pragma unroll
-    for (int x = 0; x < 16; ++x) {
-      const int t = 32 * mt + mfma_c_row(x, hh);
-      tEg[x] = sEg[t];
-      if (wave < 2) {
-        tB[x] = sB[t];
-        tV[x] = sV[t * DT + r];
-      }
-    }
-    float16_t acc;
-    {
-      SplitAcc p{float16_t{0}, float16_t{0}};
-      const half_t *ah = wave < 2 ? sKh : sQh, *al = wave < 2 ? sKl : sQl;
-#pragma unroll
-      for (int ks = 0; ks < DK / 16; ++ks) {
-        const int ko = 16 * ks + 8 * hh;
-        mfma_split(ah + (32 * mt + r) * KST + ko, al + (32 * mt + r) * KST + ko,
-                   sSh + r * KST + ko, sSl + r * KST + ko, p);
-      }
-#pragma unroll
-      for (int x = 0; x < 16; ++x)
-        acc[x] = split_value(p, x);
-    }
-    // 3. X = beta (V - e^g K S) -> X^T; Q S -> e^g Q S (kept in acc).
-    float x16[16];
-#pragma unroll
-    for (int x = 0; x < 16; ++x) {
-      if (wave < 2)
-        x16[x] = tB[x] * (tV[x] - tEg[x] * acc[x]);
-      else
-        acc[x] *= tEg[x];
-    }
-    if (wave < 2)
-      store_tile_T(sXh, sXl, CST, 32 * mt, r, hh, x16);
-    __syncthreads();
-
-    // 4. Fetch the next chunk while this one finishes.
-    if (c + 1 < chunks)
-      load_chunk(cr, kq_of(c + 1), rec_of(c + 1), v, t0 + C, min((unsigned)C, T - t0 - C),
-                 vcol, vwidth, tid);
-    // 5. Waves 0-1: U = T X.
-    float u[16];
-    if (wave < 2) {
-      SplitAcc p{float16_t{0}, float16_t{0}};
-#pragma unroll
-      for (int ks = 0; ks < C / 16; ++ks) {
-        const int ko = 16 * ks + 8 * hh;
-        mfma_split(sTh + (32 * mt + r) * CST + ko, sTl + (32 * mt + r) * CST + ko,
-                   sXh + r * CST + ko, sXl + r * CST + ko, p);
-      }
-#pragma unroll
-      for (int x = 0; x < 16; ++x)
-        u[x] = split_value(p, x);
-    }
-    __syncthreads();
-    // 6. U^T, and Z^T = (e^(g_C - g) U)^T into X's space.
-    if (wave < 2) {
-      float zz[16];
-#pragma unroll
-      for (int x = 0; x < 16; ++x) {
-        const int t = 32 * mt + mfma_c_row(x, hh);
-        zz[x] = sEz[t] * u[x];
-      }
-      store_tile_T(sUh, sUl, CST, 32 * mt, r, hh, u);
-      store_tile_T(sXh, sXl, CST, 32 * mt, r, hh, zz);
-    }
-    __syncthreads();
-
-    // 7. Waves 2-3: Y = e^g Q S + M U -> out.
-    if (wave >= 2) {
-      SplitAcc p{acc, float16_t{0}};
-#pragma unroll
-      for (int ks = 0; ks < C / 16; ++ks) {
-        const int ko = 16 * ks + 8 * hh;
-        mfma_split(sMh + (32 * mt + r) * CST + ko, sMl + (32 * mt + r) * CST + ko,
-                   sUh + r * CST + ko, sUl + r * CST + ko, p);
-      }
-#pragma unroll
-      for (int x = 0; x < 16; ++x) {
-        const unsigned t = 32 * mt + mfma_c_row(x, hh);
-        if (t < n)
-          out[(size_t)(t0 + t) * vwidth + (size_t)h * DV + j0 + r] =
-              (half_t)split_value(p, x);
-      }
-    }
-    // 8. S <- e^(g_C) S + K^T Z (wave w: rows d in [32w, 32w + 32)). The
-    //    K^T operand (channel d, tokens 16 ks + 8 hh .. +8) comes from the
-    //    token-major K tile through transposing reads: lane L of a 16-lane
-    //    group addresses token row ko + L/4 (+ 4), channels d0 + 4 (L%4),
-    //    and receives 4 tokens of channel d0 + L.
-    {
-      const float eC = sEg[C - 1];
-      SplitAcc p{float16_t{0}, float16_t{0}};
-#pragma unroll
-      for (int x = 0; x < 16; ++x)
-        p.acc[x] = S[x] * eC;
-      const unsigned L = lane % 16;
-      const unsigned d0 = 32 * wave + 16 * ((lane % 32) / 16);
-#pragma unroll
-      for (int ks = 0; ks < C / 16; ++ks) {
-        const unsigned ko = 16 * ks + 8 * hh;
-        const unsigned off = ((ko + L / 4) * KST + d0 + 4 * (L % 4)) * 2;
-        const half4_t h0 = read_tr(sKh, off), h1 = read_tr(sKh, off + 4 * KST * 2);
-        const half4_t l0 = read_tr(sKl, off), l1 = read_tr(sKl, off + 4 * KST * 2);
-        const half8_t ah{h0[0], h0[1], h0[2], h0[3], h1[0], h1[1], h1[2], h1[3]};
-        const half8_t al{l0[0], l0[1], l0[2], l0[3], l1[0], l1[1], l1[2], l1[3]};
-        mfma_split_a(ah, al, sXh + r * CST + ko, sXl + r * CST + ko, p);
-      }
-#pragma unroll
-      for (int x = 0; x < 16; ++x)
-        S[x] = split_value(p, x);
-    }
-    // 9. S^T for the next chunk (nothing reads S^T after step 2).
-    store_tile_T(sSh, sSl, KST, 32 * wave, r, hh, S);
-    __syncthreads();
   }
 
+  // K K^T and Q K^T (fp16 hi), 16 tiles each; wave w takes tiles w + 4 rep.
 #pragma unroll
-  for (int x = 0; x < 16; ++x)
-    stile[(size_t)(32 * wave + mfma_c_row(x, hh)) * DV] = S[x];
+  for (int rep = 0; rep < 8; ++rep) {
+    const int ti = wave + 4 * rep;
+    const half_t *a = ti < 16 ? sKh : sQV;
+    const int mt = (ti % 16) / 4, nt = ti % 4;
+    float4_t acc{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int ks = 0; ks < DK / 32; ++ks)
+      acc = mfma16(load8(a + (16 * mt + L) * KS + 32 * ks + 8 * g),
+                   load8(sKh + (16 * nt + L) * KS + 32 * ks + 8 * g), acc);
+    float *dst = ti < 16 ? sKK : sQK;
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      dst[(16 * mt + 4 * g + r) * C + 16 * nt + L] = acc[r];
+  }
+  __syncthreads();
+
+  for (unsigned hr = 0; hr < R; ++hr) {
+    const unsigned h = kh * R + hr;
+    char *const rec = rec_ptr(ws, recB, Hv, c, h);
+
+    // Cumulative log decay (double) and beta (padding tokens: decay 1,
+    // beta 0), e^(g_t), e^(g_C - g_t) and e^(g_C).
+    if (wave == 0) {
+      const unsigned t = lane;
+      const float a = t < n ? decay[(size_t)(t0 + t) * Hv + h] : 1.0f;
+      const float b = t < n ? beta[(size_t)(t0 + t) * Hv + h] : 0.0f;
+      double gg = a > 0.0f ? (double)logf(a) : -1.0e4;
+#pragma unroll
+      for (int off = 1; off < 64; off <<= 1) {
+        const double up = __shfl_up(gg, off);
+        if (lane >= (unsigned)off)
+          gg += up;
+      }
+      const double gC = __shfl(gg, 63);
+      sG[t] = gg;
+      sB[t] = b;
+      sEg[t] = expf((float)gg);
+      sEz[t] = expf((float)(gC - gg));
+      if (t == 63)
+        *reinterpret_cast<float *>(rec + rec_scalars(DV)) = expf((float)gg);
+    }
+    __syncthreads();
+
+    // A (fp32) and M (hi/lo). Thread (row group tq, column s) covers rows
+    // tq + 4i.
+    {
+      const unsigned s = tid % C, tq = tid / C;
+      const double gs = sG[s];
+#pragma unroll 4
+      for (int i = 0; i < C / 4; ++i) {
+        const unsigned t = tq + 4 * i;
+        const float e = s <= t ? expf((float)(sG[t] - gs)) : 0.0f;
+        sA[t * FS + s] = s < t ? sB[t] * e * sKK[t * C + s] : 0.0f;
+        split_f16(e * sQK[t * C + s], sMh[t * CS + s], sMl[t * CS + s]);
+      }
+    }
+    __syncthreads();
+
+    // T = (I + A)^-1 by blocked forward substitution on 16x16 blocks, into
+    // sTT[s][t] = T[t][s]. Diagonal blocks first (wave w inverts block w,
+    // lane j < 16 owns its column j), then block rows i = 1..3:
+    // T_ij = -T_ii sum_{k=j}^{i-1} A_ik T_kj.
+    if (lane < 16) {
+      const unsigned j = lane, b0 = 16 * wave;
+      float col[16];
+#pragma unroll
+      for (int t = 0; t < 16; ++t) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int u = 0; u < t; ++u)
+          acc = fmaf(sA[(b0 + t) * FS + b0 + u], col[u], acc);
+        col[t] = (unsigned)t == j ? 1.0f : ((unsigned)t > j ? -acc : 0.0f);
+      }
+#pragma unroll
+      for (int t = 0; t < 16; ++t)
+        sTT[(b0 + j) * FS + b0 + t] = col[t];
+    }
+    __syncthreads();
+    for (int i = 1; i < 4; ++i) {
+      for (int o = tid; o < 256 * i; o += 256) {
+        const int jb = o / 256, s = (o / 16) % 16, t = o % 16;
+        float acc = 0.0f;
+        for (int kk = jb; kk < i; ++kk)
+#pragma unroll
+          for (int u = 0; u < 16; ++u)
+            acc = fmaf(sA[(16 * i + t) * FS + 16 * kk + u], sTT[(16 * jb + s) * FS + 16 * kk + u],
+                       acc);
+        sR[(jb * 16 + s) * 16 + t] = acc;
+      }
+      __syncthreads();
+      for (int o = tid; o < 256 * i; o += 256) {
+        const int jb = o / 256, s = (o / 16) % 16, t = o % 16;
+        float acc = 0.0f;
+        for (int u = 0; u <= t; ++u)
+          acc = fmaf(sTT[(16 * i + u) * FS + 16 * i + t], sR[(jb * 16 + s) * 16 + u], acc);
+        sTT[(16 * jb + s) * FS + 16 * i + t] = -acc;
+      }
+      __syncthreads();
+    }
+
+    // T_w^T[s][t] = beta_s e^(g_s) T[t][s] and T_b^T[s][t] = beta_s T[t][s],
+    // hi/lo, over A and T^T (read to registers first).
+    {
+      const unsigned s = tid / 4, tb = 16 * (tid % 4);
+      float tv[16];
+#pragma unroll
+      for (int x = 0; x < 16; ++x) {
+        const unsigned t = tb + x;
+        tv[x] = t >= s ? sTT[s * FS + t] : 0.0f;
+      }
+      const float bw = sB[s] * sEg[s], bb = sB[s];
+      __syncthreads();
+#pragma unroll
+      for (int x4 = 0; x4 < 4; ++x4) {
+        half4_t wh, wl, bh, bl;
+        split4(float4_t{tv[4 * x4], tv[4 * x4 + 1], tv[4 * x4 + 2], tv[4 * x4 + 3]} * bw, wh, wl);
+        split4(float4_t{tv[4 * x4], tv[4 * x4 + 1], tv[4 * x4 + 2], tv[4 * x4 + 3]} * bb, bh, bl);
+        const unsigned o = s * CS + tb + 4 * x4;
+        *reinterpret_cast<half4_t *>(sTwh + o) = wh;
+        *reinterpret_cast<half4_t *>(sTwl + o) = wl;
+        *reinterpret_cast<half4_t *>(sTbh + o) = bh;
+        *reinterpret_cast<half4_t *>(sTbl + o) = bl;
+      }
+    }
+    __syncthreads();
+
+    // N^T = T_w^T M^T (N = M T diag(beta e^g)); -N to LDS as [t][s] hi/lo.
+#pragma unroll
+    for (int rep = 0; rep < 4; ++rep) {
+      const int ti = wave + 4 * rep, st = ti / 4, tt = ti % 4;
+      float4_t acc{0.0f, 0.0f, 0.0f, 0.0f}, crs{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int ks = 0; ks < C / 32; ++ks) {
+        const int k0 = 32 * ks + 8 * g;
+        const half8_t ah = load8(sTwh + (16 * st + L) * CS + k0);
+        const half8_t al = load8(sTwl + (16 * st + L) * CS + k0);
+        const half8_t bh = load8(sMh + (16 * tt + L) * CS + k0);
+        const half8_t bl = load8(sMl + (16 * tt + L) * CS + k0);
+        acc = mfma16(ah, bh, acc);
+        crs = mfma16(ah, bl, crs);
+        crs = mfma16(al, bh, crs);
+      }
+      half4_t nh, nl;
+      split4(-(acc + crs * kSplitUnscale), nh, nl);
+      const unsigned o = (16 * tt + L) * CS + 16 * st + 4 * g;
+      *reinterpret_cast<half4_t *>(sNh + o) = nh;
+      *reinterpret_cast<half4_t *>(sNl + o) = nl;
+    }
+    __syncthreads();
+
+    // Wn and Q' pieces: W^T = K^T T_w^T and Q'^T = e^g Q^T - K^T N^T share
+    // the K^T operand. Wave w writes blocks (m, kb) = w + 4 rep; block
+    // (m, kb) is tiles d = 2 kb, 2 kb + 1 of the transposed products.
+    {
+      half_t *const wp = reinterpret_cast<half_t *>(rec);
+      half_t *const qp = reinterpret_cast<half_t *>(rec + kPieceBytes);
+#pragma unroll 1
+      for (int rep = 0; rep < 4; ++rep) {
+        const int pi = wave + 4 * rep, mt = pi / 4, kb = pi % 4;
+        const unsigned t = 16 * mt + L;
+        half8_t wh, wl, qh, ql;
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf) {
+          const int dt = 2 * kb + hf;
+          float4_t wa{0.0f, 0.0f, 0.0f, 0.0f}, wx{0.0f, 0.0f, 0.0f, 0.0f};
+          float4_t qa{0.0f, 0.0f, 0.0f, 0.0f}, qx{0.0f, 0.0f, 0.0f, 0.0f};
+          if (t < n)
+            qa = *reinterpret_cast<const float4_t *>(q + (size_t)(t0 + t) * qkStride +
+                                                     (size_t)kh * DK + 16 * dt + 4 * g) *
+                 sEg[t];
+#pragma unroll
+          for (int ks = 0; ks < C / 32; ++ks) {
+            const unsigned s0 = 32 * ks;
+            const half8_t ah = read_kcol(sKh, KS, s0, 16 * dt, g, L);
+            const half8_t al = read_kcol(sKl, KS, s0, 16 * dt, g, L);
+            const half8_t b1h = read_kcol(sTwh, CS, s0, 16 * mt, g, L);
+            const half8_t b1l = read_kcol(sTwl, CS, s0, 16 * mt, g, L);
+            const half8_t b2h = load8(sNh + t * CS + s0 + 8 * g);
+            const half8_t b2l = load8(sNl + t * CS + s0 + 8 * g);
+            wa = mfma16(ah, b1h, wa);
+            wx = mfma16(ah, b1l, wx);
+            wx = mfma16(al, b1h, wx);
+            qa = mfma16(ah, b2h, qa);
+            qx = mfma16(ah, b2l, qx);
+            qx = mfma16(al, b2h, qx);
+          }
+          const float ez = sEz[t];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            half_t a, b;
+            split_f16(-ez * (wa[r] + wx[r] * kSplitUnscale), a, b);
+            wh[4 * hf + r] = a;
+            wl[4 * hf + r] = b;
+            split_f16(qa[r] + qx[r] * kSplitUnscale, a, b);
+            qh[4 * hf + r] = a;
+            ql[4 * hf + r] = b;
+          }
+        }
+        const unsigned o = pi * kBlk + 8 * lane;
+        *reinterpret_cast<half8_t *>(wp + o) = wh;
+        *reinterpret_cast<half8_t *>(wp + kPieceBlocks * kBlk + o) = wl;
+        *reinterpret_cast<half8_t *>(qp + o) = qh;
+        *reinterpret_cast<half8_t *>(qp + kPieceBlocks * kBlk + o) = ql;
+      }
+    }
+
+    // U0 = T_b V per 16-column slice (wave w: slices w + 4 rep of each V
+    // block), then Z0 = e^(g_C - g) U0 and Y0 = M U0 with U0 as the B
+    // operand straight from its C-layout registers.
+    float4_t *const z0 = reinterpret_cast<float4_t *>(rec + 2 * kPieceBytes);
+    float4_t *const y0 = z0 + (size_t)C * DV / 4;
+    for (unsigned jb = 0; jb < DV; jb += VB) {
+      const unsigned w = min((unsigned)VB, DV - jb);
+      __syncthreads();
+      for (unsigned i = tid; i < C * w / 8; i += 256) {
+        const unsigned t = i / (w / 8), j8 = (i % (w / 8)) * 8;
+        half8_t x{0, 0, 0, 0, 0, 0, 0, 0};
+        if (t < n)
+          x = load8(v + (size_t)(t0 + t) * vStride + (size_t)h * DV + jb + j8);
+        *reinterpret_cast<half8_t *>(sQV + t * KS + j8) = x;
+      }
+      __syncthreads();
+#pragma unroll 1
+      for (unsigned jt = wave; jt < w / 16; jt += 4) {
+        const unsigned js = jb / 16 + jt;
+        float4_t u[4];
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) {
+          float4_t a{0.0f, 0.0f, 0.0f, 0.0f}, x{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+          for (int ks = 0; ks < C / 32; ++ks) {
+            const half8_t bv = read_kcol(sQV, KS, 32 * ks, 16 * jt, g, L);
+            a = mfma16(read_kcol(sTbh, CS, 32 * ks, 16 * mt, g, L), bv, a);
+            x = mfma16(read_kcol(sTbl, CS, 32 * ks, 16 * mt, g, L), bv, x);
+          }
+          u[mt] = a + x * kSplitUnscale;
+          float4_t zz;
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            zz[r] = sEz[16 * mt + 4 * g + r] * u[mt][r];
+          z0[(js * 4 + mt) * 64 + lane] = zz;
+        }
+        half8_t ubh[2], ubl[2];
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+          split8(u[2 * kb], u[2 * kb + 1], ubh[kb], ubl[kb]);
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) {
+          float4_t a{0.0f, 0.0f, 0.0f, 0.0f}, x{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+          for (int kb = 0; kb < 2; ++kb) {
+            const unsigned o = (16 * mt + L) * CS + 32 * kb + 4 * g;
+            const half8_t ah = cat8(load4(sMh + o), load4(sMh + o + 16));
+            const half8_t al = cat8(load4(sMl + o), load4(sMl + o + 16));
+            a = mfma16(ah, ubh[kb], a);
+            x = mfma16(ah, ubl[kb], x);
+            x = mfma16(al, ubh[kb], x);
+          }
+          y0[(js * 4 + mt) * 64 + lane] = a + x * kSplitUnscale;
+        }
+      }
+    }
+    __syncthreads();
+  }
+}
+
+// --------------------------------------------------------------- scan
+
+// Direct HBM/L2 -> LDS loads (buffer_load_dwordx4 ... lds), issued from
+// inline assembly so that the compiler neither waits for them nor reorders
+// LDS accesses across them ("memory" clobber): the scan orders them itself.
+// Each load moves 16 bytes per lane, lane i's bytes landing at M0 + 16 i.
+typedef __attribute__((address_space(3))) char lds_char_t;
+typedef int int4v_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ int4v_t buffer_rsrc(const void *base, unsigned bytes) {
+  const uint64_t a = reinterpret_cast<uint64_t>(base);
+  return int4v_t{__builtin_amdgcn_readfirstlane((int)(uint32_t)a),
+                 __builtin_amdgcn_readfirstlane((int)((uint32_t)(a >> 32) & 0xFFFFu)),
+                 (int)bytes, kBufferWord3};
+}
+__device__ __forceinline__ unsigned lds_addr(const void *p) {
+  return (unsigned)(uintptr_t)(const lds_char_t *)p;
+}
+// M0 is reserved to the compiler; it keeps nothing in it across these
+// statements in this file, and the clobber tells it M0 changes.
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void load_lds_1k(int4v_t rsrc, unsigned ldsDst, unsigned voff,
+                                            unsigned soff) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+               :
+               : "s"(__builtin_amdgcn_readfirstlane(ldsDst)), "v"(voff), "s"(rsrc),
+                 "s"(__builtin_amdgcn_readfirstlane(soff))
+               : "memory", "m0");
+}
+__device__ __forceinline__ void load_lds_256(int4v_t rsrc, unsigned ldsDst, unsigned voff) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dword %1, %2, 0 offen lds"
+               :
+               : "s"(__builtin_amdgcn_readfirstlane(ldsDst)), "v"(voff), "s"(rsrc)
+               : "memory", "m0");
+}
+// Wait until this wave's LDS reads have returned (before a barrier after
+// which their buffer is reloaded).
+__device__ __forceinline__ void wait_lds_reads() { __builtin_amdgcn_s_waitcnt(0xC07F); }
+// Wait until at most N of this wave's vector-memory operations are
+// outstanding (they complete in order).
+template <int N> __device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  __builtin_amdgcn_s_waitcnt(0x0F70 | (N & 15) | ((N >> 4) << 14));
+}
+// Workgroup barrier that the compiler moves no memory access across; no
+// wait attached (each wave waits for exactly what it must beforehand).
+__device__ __forceinline__ void barrier() { asm volatile("s_barrier" ::: "memory"); }
+
+// The scan workgroup: wave 0 computes; waves 1-3 load. A wave moves at most
+// ~16 bytes per cycle through direct-to-LDS loads (measured: ~38 GB/s per
+// wave whether the data sits in L2 or in HBM, scaling with the number of
+// waves), and a chunk's operands are 105 KiB: spread over three loader
+// waves they take about as long as the compute wave's products.
+constexpr int kLoaders = 3;
+constexpr int kPartLoads = (kPieceLoads + kLoaders - 1) / kLoaders; // 11 KiB of a piece per loader
+constexpr int kZYLoads = 3;   // 8 Z0/Y0 blocks and the scalars over 3 loaders
+constexpr int kWLoads = kPartLoads + kZYLoads;
+
+__global__ __launch_bounds__(64 * (1 + kLoaders), 1) void delta_scan_kernel(
+    float *__restrict__ state, half_t *__restrict__ out, const void *__restrict__ ws,
+    unsigned T, unsigned Hk, unsigned Hv, unsigned DV) {
+  // Workgroups are dealt to the 8 XCDs round-robin by block index. Give
+  // each XCD a contiguous run of (value head, slice) pairs, so that the
+  // workgroups reading one value head's Wn and Q' pieces and one key head's
+  // K^T piece share an L2.
+  const unsigned slices = DV / 16, nb = gridDim.x;
+  const unsigned Lb = nb % 8 == 0 ? (blockIdx.x % 8) * (nb / 8) + blockIdx.x / 8 : blockIdx.x;
+  const unsigned h = Lb / slices, js = Lb % slices, kh = h / (Hv / Hk);
+  const unsigned wave = threadIdx.x >> 6, lane = threadIdx.x & 63u, g = lane >> 4;
+  const unsigned chunks = (T + C - 1) / C;
+  const size_t recB = rec_bytes(DV), vStride = (size_t)Hv * DV;
+  void *const wsp = const_cast<void *>(ws);
+
+  // Wn and this slice's Z0/Y0 (+ scalars) double-buffered, K^T and Q'
+  // single. Chunk c uses buffer c % 2.
+  constexpr int PB = 2 * kPieceBlocks * 64; // half8s per piece
+  __shared__ half8_t sW0[PB], sW1[PB], sK[PB], sQ[PB];
+  __shared__ float4_t sZY0[8 * 64 + 16], sZY1[8 * 64 + 16];
+
+  auto rec = [&](unsigned c) { return rec_ptr(wsp, recB, Hv, c, h); };
+  auto kp = [&](unsigned c) { return kpiece_ptr(wsp, recB, chunks, Hv, Hk, c, kh); };
+
+  // Per chunk c, barriers A(c), B(c), C(c), then A(c + 1):
+  //   wave 0: A(c) [Wn, Z0/Y0 of c in LDS] products with Wn; B(c) [K^T of
+  //           c in LDS; Wn buffer free] products with K^T; C(c) [Q' of c in
+  //           LDS; K^T buffer free] products with Q', output rows;
+  //           A(c + 1) [Q' buffer free].
+  //   loaders: after A(c) load Q' of c; after B(c) Wn, Z0/Y0 of c + 2;
+  //           after C(c) K^T of c + 1; each waits for its own part of what
+  //           the next barrier promises before arriving there.
+  if (wave > 0) {
+    const unsigned l = __builtin_amdgcn_readfirstlane(wave - 1);
+    // Loader l's part of a piece: KiB [11 l, 11 l + 11), clamped to the
+    // piece (the last part repeats its final KiB: the same bytes again).
+    auto load_part = [&](const char *src, const half8_t *dst) {
+      const int4v_t rsrc = buffer_rsrc(src, kPieceBytes);
+#pragma unroll
+      for (int it = 0; it < kPartLoads; ++it) {
+        const unsigned kib = min(kPartLoads * l + it, (unsigned)kPieceLoads - 1);
+        load_lds_1k(rsrc, lds_addr(dst) + 1024 * kib, 16 * lane, 1024 * kib);
+      }
+    };
+    // Wn and the Z0/Y0 blocks 3l .. 3l + 2 (block 8: the scalars).
+    auto load_w = [&](unsigned c, const half8_t *dW, const float4_t *dZY) {
+      const char *r = rec(c);
+      load_part(r, dW);
+      const char *z = r + 2 * kPieceBytes + (size_t)js * 4 * 64 * sizeof(float4_t);
+      const int4v_t rz = buffer_rsrc(z, 4 * 1024), ry = buffer_rsrc(z + (size_t)C * DV * 4, 4 * 1024);
+#pragma unroll
+      for (int i = 0; i < kZYLoads; ++i) {
+        const unsigned blk = kZYLoads * l + i;
+        if (blk < 4)
+          load_lds_1k(rz, lds_addr(dZY + 64 * blk), 16 * lane, 1024 * blk);
+        else if (blk < 8)
+          load_lds_1k(ry, lds_addr(dZY + 64 * blk), 16 * lane, 1024 * (blk - 4));
+        else
+          load_lds_256(buffer_rsrc(r + rec_scalars(DV), kScalarBytes), lds_addr(dZY + 8 * 64),
+                       4 * lane);
+      }
+    };
+    const unsigned last = chunks - 1;
+    load_w(0, sW0, sZY0);
+    load_w(min(1u, last), sW1, sZY1);
+    load_part(kp(0), sK);
+    wait_vm<kWLoads + kPartLoads>();
+    for (unsigned c = 0; c < chunks; ++c) {
+      barrier(); // A(c)
+      load_part(rec(c) + kPieceBytes, sQ);
+      wait_vm<kPartLoads>(); // K^T of c
+      barrier(); // B(c)
+      if (c % 2 == 0)
+        load_w(min(c + 2, last), sW0, sZY0);
+      else
+        load_w(min(c + 2, last), sW1, sZY1);
+      wait_vm<kWLoads>(); // Q' of c
+      barrier(); // C(c)
+      load_part(kp(min(c + 1, last)), sK);
+      wait_vm<kPartLoads + kPartLoads + kWLoads + kPartLoads>(); // Wn, Z0/Y0 of c + 1
+    }
+    barrier(); // A(chunks)
+    wait_vm<0>();
+    return;
+  }
+
+  const unsigned j = 16 * js + (lane & 15u);
+  // The state slice: register r of tile i holds S[16 i + 4 g + r][j].
+  float4_t S[8];
+  float *const scol = state + (size_t)h * DK * DV + j;
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      S[i][r] = scol[(size_t)(16 * i + 4 * g + r) * DV];
+
+  auto step = [&](unsigned c, const half8_t *rW, const float4_t *rZY) {
+    const unsigned t0 = c * C, n = min((unsigned)C, T - t0);
+    barrier(); // A(c)
+    // All of a product's A blocks are read before its first MFMA (the
+    // scheduler is kept from sinking the reads next to their uses, where
+    // each would expose the LDS latency), and the MFMAs of one k block go
+    // accumulator by accumulator so that no MFMA waits on the one before.
+    half8_t A[2][kPieceBlocks];
+#pragma unroll
+    for (int b = 0; b < kPieceBlocks; ++b) {
+      A[0][b] = rW[b * 64 + lane];
+      A[1][b] = rW[(kPieceBlocks + b) * 64 + lane];
+    }
+    const float eC = rZY[8 * 64][0];
+    float4_t za[4], zx[4], ya[4], yx[4];
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      za[m] = rZY[m * 64 + lane];
+      ya[m] = rZY[(4 + m) * 64 + lane];
+      zx[m] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
+      yx[m] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+    // S as the B operand of its four 32-row k blocks.
+    half8_t bh[4], bl[4];
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb)
+      split8(S[2 * kb], S[2 * kb + 1], bh[kb], bl[kb]);
+    __builtin_amdgcn_sched_barrier(0);
+    // Z = Z0 + Wn S.
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) {
+#pragma unroll
+      for (int m = 0; m < 4; ++m)
+        za[m] = mfma16(A[0][4 * m + kb], bh[kb], za[m]);
+#pragma unroll
+      for (int m = 0; m < 4; ++m)
+        zx[m] = mfma16(A[0][4 * m + kb], bl[kb], zx[m]);
+#pragma unroll
+      for (int m = 0; m < 4; ++m)
+        zx[m] = mfma16(A[1][4 * m + kb], bh[kb], zx[m]);
+    }
+    wait_lds_reads();
+    barrier(); // B(c)
+
+    // S <- e^(g_C) S + K^T Z, Z as the B operand of its two k blocks.
+#pragma unroll
+    for (int b = 0; b < kPieceBlocks; ++b) {
+      A[0][b] = sK[b * 64 + lane];
+      A[1][b] = sK[(kPieceBlocks + b) * 64 + lane];
+    }
+    half8_t zbh[2], zbl[2];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+      split8(za[2 * kb] + zx[2 * kb] * kSplitUnscale,
+             za[2 * kb + 1] + zx[2 * kb + 1] * kSplitUnscale, zbh[kb], zbl[kb]);
+    float4_t sa[8], sx[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      sa[i] = S[i] * eC;
+      sx[i] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        sa[i] = mfma16(A[0][2 * i + kb], zbh[kb], sa[i]);
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        sx[i] = mfma16(A[0][2 * i + kb], zbl[kb], sx[i]);
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        sx[i] = mfma16(A[1][2 * i + kb], zbh[kb], sx[i]);
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      S[i] = sa[i] + sx[i] * kSplitUnscale;
+    wait_lds_reads();
+    barrier(); // C(c)
+
+    // Y = Y0 + Q' S (the state before this chunk).
+#pragma unroll
+    for (int b = 0; b < kPieceBlocks; ++b) {
+      A[0][b] = sQ[b * 64 + lane];
+      A[1][b] = sQ[(kPieceBlocks + b) * 64 + lane];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) {
+#pragma unroll
+      for (int m = 0; m < 4; ++m)
+        ya[m] = mfma16(A[0][4 * m + kb], bh[kb], ya[m]);
+#pragma unroll
+      for (int m = 0; m < 4; ++m)
+        yx[m] = mfma16(A[0][4 * m + kb], bl[kb], yx[m]);
+#pragma unroll
+      for (int m = 0; m < 4; ++m)
+        yx[m] = mfma16(A[1][4 * m + kb], bh[kb], yx[m]);
+    }
+    wait_lds_reads();
+
+    // Rows past the end of the tokens fall outside the descriptor and are
+    // dropped by the buffer stores.
+    const auto ro = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)(out + (size_t)t0 * vStride + (size_t)h * DV), (short)0,
+        (int)(((n - 1) * vStride + DV) * sizeof(half_t)), kBufferWord3);
+#pragma unroll
+    for (int m = 0; m < 4; ++m)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const unsigned t = 16 * m + 4 * g + r;
+        const half_t y = (half_t)(ya[m][r] + yx[m][r] * kSplitUnscale);
+        __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(unsigned short, y), ro,
+                                              (unsigned)((t * vStride + j) * sizeof(half_t)),
+                                              0, 0);
+      }
+  };
+
+  unsigned c = 0;
+  for (; c + 1 < chunks; c += 2) {
+    step(c, sW0, sZY0);
+    step(c + 1, sW1, sZY1);
+  }
+  if (c < chunks)
+    step(c, sW0, sZY0);
+  barrier(); // A(chunks)
+
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      scol[(size_t)(16 * i + 4 * g + r) * DV] = S[i][r];
 }
 
 } // namespace
 
 bool delta_chunked_supported(const DeltaShape &s) {
-  return s.Dk == DK && s.Dv % DT == 0 && s.Hk >= 1 && s.Hv % s.Hk == 0 &&
-         s.Hv / s.Hk <= (unsigned)kMaxRatio && s.T >= 32;
+  return s.Dk == DK && s.Dv % 16 == 0 && s.Dv >= 16 && s.Hk >= 1 && s.Hv % s.Hk == 0 &&
+         s.T >= 32;
 }
 
 size_t delta_chunked_workspace_bytes(const DeltaShape &s) {
   const size_t chunks = (s.T + C - 1) / C;
-  return chunks * s.Hv * kRecBytes + chunks * s.Hk * kKQHalves * sizeof(half_t);
+  return chunks * (s.Hv * rec_bytes(s.Dv) + s.Hk * (size_t)kPieceBytes);
 }
 
 hipError_t launch_delta_chunked(const float *q, const float *k, const uint16_t *v,
@@ -532,12 +811,13 @@ hipError_t launch_delta_chunked(const float *q, const float *k, const uint16_t *
                                 hipStream_t stream) {
   const unsigned chunks = (s.T + C - 1) / C;
   hipLaunchKernelGGL(delta_prep_kernel, dim3(chunks, s.Hk), dim3(256), 0, stream, q, k,
-                     beta, decay, ws, s.T, s.Hk, s.Hv);
+                     reinterpret_cast<const half_t *>(v), beta, decay, ws, s.T, s.Hk, s.Hv,
+                     s.Dv);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess)
     return e;
-  hipLaunchKernelGGL(delta_scan_kernel, dim3(s.Hv * (s.Dv / DT)), dim3(256), 0, stream,
-                     reinterpret_cast<const half_t *>(v), state,
+  hipLaunchKernelGGL(delta_scan_kernel, dim3(s.Hv * (s.Dv / 16)), dim3(64 * (1 + kLoaders)), 0,
+                     stream, state,
                      reinterpret_cast<half_t *>(out), ws, s.T, s.Hk, s.Hv, s.Dv);
   return hipGetLastError();
 }

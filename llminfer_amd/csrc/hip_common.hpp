@@ -95,15 +95,14 @@ __device__ __forceinline__ float16_t mfma32x32x16(half8_t a, half8_t b, float16_
 __device__ __forceinline__ int mfma_c_row(int v, int h) { return 8 * (v / 4) + 4 * h + (v % 4); }
 
 // x = hi + lo * 2^-11 with hi = fp16(x), lo = fp16((x - hi) * 2^11): 22
-// significant bits. No part is ever an fp16 subnormal, which MFMA may flush
-// to zero: the remainder is stored scaled by 2^11 (|x - hi| <= 2^-11 |x|
-// would be subnormal for |x| < 2^-3), and below the smallest normal fp16
-// (2^-14) hi is 0 and the whole value goes to the scaled remainder.
+// significant bits. The remainder is stored scaled by 2^11 so that it stays
+// a normal fp16 for |x| >= 2^-3 (unscaled it would be subnormal there);
+// fp16 subnormals that remain (|x| < 2^-14) are kept by the conversions and
+// by v_mfma_f32_*_f16 on gfx950, which does not flush fp16 inputs.
 constexpr float kSplitScale = 2048.0f;
 constexpr float kSplitUnscale = 1.0f / 2048.0f;
-constexpr float kF16MinNormal = 6.103515625e-05f; // 2^-14
 __device__ __forceinline__ void split_f16(float x, half_t &hi, half_t &lo) {
-  hi = fabsf(x) >= kF16MinNormal ? (half_t)x : (half_t)0.0f;
+  hi = (half_t)x;
   lo = (half_t)((x - (float)hi) * kSplitScale);
 }
 
