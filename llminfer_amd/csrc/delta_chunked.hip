@@ -175,6 +175,15 @@ __device__ __forceinline__ half8_t read_kcol(const half_t *X, int stride, unsign
 
 // --------------------------------------------------------------- prep
 
+__device__ __forceinline__ float4_t mfma16k16(half4_t a, half4_t b, float4_t c) {
+  return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
+}
+// Four floats at p, p + stride, ... split into hi/lo fp16.
+__device__ __forceinline__ void load_split4(const float *p, int stride, half4_t &hi,
+                                            half4_t &lo) {
+  split4(float4_t{p[0], p[stride], p[2 * stride], p[3 * stride]}, hi, lo);
+}
+
 __global__ __launch_bounds__(256, 1) void delta_prep_kernel(
     const float *__restrict__ q, const float *__restrict__ k, const half_t *__restrict__ v,
     const float *__restrict__ beta, const float *__restrict__ decay, void *__restrict__ ws,
@@ -189,35 +198,86 @@ __global__ __launch_bounds__(256, 1) void delta_prep_kernel(
 
   __shared__ __attribute__((aligned(16))) half_t sKh[C * KS], sKl[C * KS];
   __shared__ __attribute__((aligned(16))) half_t sQV[C * KS]; // Q hi, later a V block
-  __shared__ __attribute__((aligned(16))) float sKK[C * C], sQK[C * C];
-  // A, T^T and the substitution's R blocks (fp32), later T_w^T and T_b^T
-  // (hi/lo fp16).
-  __shared__ __attribute__((aligned(16))) float sP[4 * C * CS / 2];
+  __shared__ float sA[C * FS], sTT[C * FS];                   // A and T^T (fp32)
+  __shared__ __attribute__((aligned(16))) half_t sTwh[C * CS], sTwl[C * CS];
+  __shared__ __attribute__((aligned(16))) half_t sTbh[C * CS], sTbl[C * CS];
   __shared__ __attribute__((aligned(16))) half_t sMh[C * CS], sMl[C * CS];
   __shared__ __attribute__((aligned(16))) half_t sNh[C * CS], sNl[C * CS];
   __shared__ double sG[C];
   __shared__ float sB[C], sEg[C], sEz[C];
-  static_assert(2 * C * FS + 3 * 256 <= 4 * C * CS / 2, "A, T^T and R share sP");
 
-  float *const sA = sP, *const sTT = sP + C * FS, *const sR = sP + 2 * C * FS;
-  half_t *const sTwh = reinterpret_cast<half_t *>(sP), *const sTwl = sTwh + C * CS;
-  half_t *const sTbh = sTwl + C * CS, *const sTbl = sTbh + C * CS;
-
-  // Keys and queries of the chunk as fp16 hi/lo (rows past the end are zero).
-  for (unsigned i = tid; i < C * DK / 4; i += 256) {
-    const unsigned t = i / (DK / 4), d4 = (i % (DK / 4)) * 4;
-    float4_t kv{0.0f, 0.0f, 0.0f, 0.0f}, qv{0.0f, 0.0f, 0.0f, 0.0f};
-    if (t < n) {
-      const size_t off = (size_t)(t0 + t) * qkStride + (size_t)kh * DK + d4;
-      kv = *reinterpret_cast<const float4_t *>(k + off);
-      qv = *reinterpret_cast<const float4_t *>(q + off);
+  // Loads that later phases need, issued up front so that their latency
+  // hides behind the K/Q split and the Gram products: the fp32 queries of
+  // the Q' initial values (wave w: d tiles 2w, 2w + 1, all t), the gates
+  // of the first value head (wave 0) and its first block of V.
+  float4_t qinit[2][4];
+#pragma unroll
+  for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) {
+      const unsigned t = 16 * mt + L;
+      qinit[hf][mt] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
+      if (t < n)
+        qinit[hf][mt] = *reinterpret_cast<const float4_t *>(
+            q + (size_t)(t0 + t) * qkStride + (size_t)kh * DK + 16 * (2 * wave + hf) + 4 * g);
     }
-    half4_t khi, klo, qhi, qlo;
-    split4(kv, khi, klo);
-    split4(qv, qhi, qlo);
-    *reinterpret_cast<half4_t *>(sKh + t * KS + d4) = khi;
-    *reinterpret_cast<half4_t *>(sKl + t * KS + d4) = klo;
-    *reinterpret_cast<half4_t *>(sQV + t * KS + d4) = qhi;
+  float gateA = 1.0f, gateB = 0.0f;
+  auto load_gates = [&](unsigned h) {
+    if (wave == 0 && lane < n) {
+      gateA = decay[(size_t)(t0 + lane) * Hv + h];
+      gateB = beta[(size_t)(t0 + lane) * Hv + h];
+    }
+  };
+  load_gates(kh * R);
+  // V rows of one head's dv block [jb, jb + w): thread tid holds items
+  // tid + 256 i (8 halves each), w <= VB.
+  constexpr int kVItems = C * VB / 8 / 256;
+  half8_t vreg[kVItems];
+  auto fetch_v = [&](unsigned h, unsigned jb, unsigned w) {
+#pragma unroll
+    for (int it = 0; it < kVItems; ++it) {
+      const unsigned i = tid + 256 * it, t = i / (w / 8), j8 = (i % (w / 8)) * 8;
+      vreg[it] = half8_t{0, 0, 0, 0, 0, 0, 0, 0};
+      if (i < C * w / 8 && t < n)
+        vreg[it] = load8(v + (size_t)(t0 + t) * vStride + (size_t)h * DV + jb + j8);
+    }
+  };
+  auto store_v = [&](unsigned w) {
+#pragma unroll
+    for (int it = 0; it < kVItems; ++it) {
+      const unsigned i = tid + 256 * it, t = i / (w / 8), j8 = (i % (w / 8)) * 8;
+      if (i < C * w / 8)
+        *reinterpret_cast<half8_t *>(sQV + t * KS + j8) = vreg[it];
+    }
+  };
+  const unsigned w0 = min((unsigned)VB, DV);
+  fetch_v(kh * R, 0, w0);
+
+  // Keys and queries of the chunk as fp16 hi/lo (rows past the end are
+  // zero); every load is issued before the first store.
+  {
+    constexpr int NI = C * DK / 4 / 256;
+    float4_t kv[NI], qv[NI];
+#pragma unroll
+    for (int it = 0; it < NI; ++it) {
+      const unsigned i = tid + 256 * it, t = i / (DK / 4), d4 = (i % (DK / 4)) * 4;
+      kv[it] = qv[it] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
+      if (t < n) {
+        const size_t off = (size_t)(t0 + t) * qkStride + (size_t)kh * DK + d4;
+        kv[it] = *reinterpret_cast<const float4_t *>(k + off);
+        qv[it] = *reinterpret_cast<const float4_t *>(q + off);
+      }
+    }
+#pragma unroll
+    for (int it = 0; it < NI; ++it) {
+      const unsigned i = tid + 256 * it, t = i / (DK / 4), d4 = (i % (DK / 4)) * 4;
+      half4_t khi, klo, qhi, qlo;
+      split4(kv[it], khi, klo);
+      split4(qv[it], qhi, qlo);
+      *reinterpret_cast<half4_t *>(sKh + t * KS + d4) = khi;
+      *reinterpret_cast<half4_t *>(sKl + t * KS + d4) = klo;
+      *reinterpret_cast<half4_t *>(sQV + t * KS + d4) = qhi;
+    }
   }
   __syncthreads();
 
@@ -237,34 +297,32 @@ __global__ __launch_bounds__(256, 1) void delta_prep_kernel(
     }
   }
 
-  // K K^T and Q K^T (fp16 hi), 16 tiles each; wave w takes tiles w + 4 rep.
+  // K K^T and Q K^T (fp16 hi) stay in registers: wave w holds the tiles of
+  // key columns s in [16 w, 16 w + 16) for the four row tiles (register r
+  // of tile mt: t = 16 mt + 4 g + r, s = 16 w + L).
+  float4_t kk[4], qk[4];
 #pragma unroll
-  for (int rep = 0; rep < 8; ++rep) {
-    const int ti = wave + 4 * rep;
-    const half_t *a = ti < 16 ? sKh : sQV;
-    const int mt = (ti % 16) / 4, nt = ti % 4;
-    float4_t acc{0.0f, 0.0f, 0.0f, 0.0f};
+  for (int mt = 0; mt < 4; ++mt) {
+    kk[mt] = qk[mt] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-    for (int ks = 0; ks < DK / 32; ++ks)
-      acc = mfma16(load8(a + (16 * mt + L) * KS + 32 * ks + 8 * g),
-                   load8(sKh + (16 * nt + L) * KS + 32 * ks + 8 * g), acc);
-    float *dst = ti < 16 ? sKK : sQK;
-#pragma unroll
-    for (int r = 0; r < 4; ++r)
-      dst[(16 * mt + 4 * g + r) * C + 16 * nt + L] = acc[r];
+    for (int ks = 0; ks < DK / 32; ++ks) {
+      const half8_t b = load8(sKh + (16 * wave + L) * KS + 32 * ks + 8 * g);
+      kk[mt] = mfma16(load8(sKh + (16 * mt + L) * KS + 32 * ks + 8 * g), b, kk[mt]);
+      qk[mt] = mfma16(load8(sQV + (16 * mt + L) * KS + 32 * ks + 8 * g), b, qk[mt]);
+    }
   }
-  __syncthreads();
 
   for (unsigned hr = 0; hr < R; ++hr) {
     const unsigned h = kh * R + hr;
     char *const rec = rec_ptr(ws, recB, Hv, c, h);
+    __syncthreads(); // the previous head is done with every LDS buffer
 
     // Cumulative log decay (double) and beta (padding tokens: decay 1,
-    // beta 0), e^(g_t), e^(g_C - g_t) and e^(g_C).
+    // beta 0), e^(g_t), e^(g_C - g_t) and e^(g_C); V of the head's first
+    // dv block.
     if (wave == 0) {
       const unsigned t = lane;
-      const float a = t < n ? decay[(size_t)(t0 + t) * Hv + h] : 1.0f;
-      const float b = t < n ? beta[(size_t)(t0 + t) * Hv + h] : 0.0f;
+      const float a = gateA, b = gateB;
       double gg = a > 0.0f ? (double)logf(a) : -1.0e4;
 #pragma unroll
       for (int off = 1; off < 64; off <<= 1) {
@@ -280,27 +338,41 @@ __global__ __launch_bounds__(256, 1) void delta_prep_kernel(
       if (t == 63)
         *reinterpret_cast<float *>(rec + rec_scalars(DV)) = expf((float)gg);
     }
-    __syncthreads();
-
-    // A (fp32) and M (hi/lo). Thread (row group tq, column s) covers rows
-    // tq + 4i.
-    {
-      const unsigned s = tid % C, tq = tid / C;
-      const double gs = sG[s];
-#pragma unroll 4
-      for (int i = 0; i < C / 4; ++i) {
-        const unsigned t = tq + 4 * i;
-        const float e = s <= t ? expf((float)(sG[t] - gs)) : 0.0f;
-        sA[t * FS + s] = s < t ? sB[t] * e * sKK[t * C + s] : 0.0f;
-        split_f16(e * sQK[t * C + s], sMh[t * CS + s], sMl[t * CS + s]);
-      }
+    store_v(w0);
+    // The next head's gates and first V block, in flight during this head
+    // (with DV > VB the V registers carry this head's further blocks, and
+    // the next head's first block is fetched after them).
+    if (hr + 1 < R) {
+      load_gates(h + 1);
+      if (DV <= VB)
+        fetch_v(h + 1, 0, w0);
     }
     __syncthreads();
 
-    // T = (I + A)^-1 by blocked forward substitution on 16x16 blocks, into
-    // sTT[s][t] = T[t][s]. Diagonal blocks first (wave w inverts block w,
-    // lane j < 16 owns its column j), then block rows i = 1..3:
-    // T_ij = -T_ii sum_{k=j}^{i-1} A_ik T_kj.
+    // A (fp32) and M (hi/lo) from the Gram registers:
+    // A[t][s] = beta_t e^(g_t - g_s) k_t.k_s (s < t), M[t][s] = e^(g_t - g_s)
+    // q_t.k_s (s <= t), zero above.
+    {
+      const unsigned s = 16 * wave + L;
+      const double gs = sG[s];
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const unsigned t = 16 * mt + 4 * g + r;
+          const float e =
+              s <= t ? __builtin_amdgcn_exp2f((float)(sG[t] - gs) * kLog2e) : 0.0f;
+          sA[t * FS + s] = s < t ? sB[t] * e * kk[mt][r] : 0.0f;
+          split_f16(e * qk[mt][r], sMh[t * CS + s], sMl[t * CS + s]);
+        }
+    }
+    __syncthreads();
+
+    // T = (I + A)^-1 into sTT[s][t] = T[t][s], on 16x16 blocks. The
+    // diagonal blocks D_i = (I + A_ii)^-1 by forward substitution (wave i,
+    // lane j < 16 owns column j); then block rows i = 1..3 on MFMA
+    // (v_mfma_f32_16x16x16_f16, split form), whose C layout is also its B
+    // layout: T_ij = -D_i sum_{k=j}^{i-1} A_ik T_kj, wave j computing T_ij.
     if (lane < 16) {
       const unsigned j = lane, b0 = 16 * wave;
       float col[16];
@@ -317,45 +389,51 @@ __global__ __launch_bounds__(256, 1) void delta_prep_kernel(
         sTT[(b0 + j) * FS + b0 + t] = col[t];
     }
     __syncthreads();
-    for (int i = 1; i < 4; ++i) {
-      for (int o = tid; o < 256 * i; o += 256) {
-        const int jb = o / 256, s = (o / 16) % 16, t = o % 16;
-        float acc = 0.0f;
-        for (int kk = jb; kk < i; ++kk)
+    for (unsigned i = 1; i < 4; ++i) {
+      if (wave < i) {
+        const unsigned jb = wave;
+        float4_t p{0.0f, 0.0f, 0.0f, 0.0f}, px{0.0f, 0.0f, 0.0f, 0.0f};
+        for (unsigned kq = jb; kq < i; ++kq) {
+          half4_t ah, al, bh, bl;
+          // A_ik[L][4g + e] and T_kj[4g + e][L] = sTT[16j + L][16k + 4g + e].
+          load_split4(sA + (16 * i + L) * FS + 16 * kq + 4 * g, 1, ah, al);
+          load_split4(sTT + (16 * jb + L) * FS + 16 * kq + 4 * g, 1, bh, bl);
+          p = mfma16k16(ah, bh, p);
+          px = mfma16k16(ah, bl, px);
+          px = mfma16k16(al, bh, px);
+        }
+        half4_t bh, bl, dh, dl;
+        split4(p + px * kSplitUnscale, bh, bl);
+        // D_i[L][4g + e] = sTT[16i + 4g + e][16i + L].
+        load_split4(sTT + (16 * i + 4 * g) * FS + 16 * i + L, FS, dh, dl);
+        float4_t tt{0.0f, 0.0f, 0.0f, 0.0f}, tx{0.0f, 0.0f, 0.0f, 0.0f};
+        tt = mfma16k16(dh, bh, tt);
+        tx = mfma16k16(dh, bl, tx);
+        tx = mfma16k16(dl, bh, tx);
+        const float4_t res = -(tt + tx * kSplitUnscale);
 #pragma unroll
-          for (int u = 0; u < 16; ++u)
-            acc = fmaf(sA[(16 * i + t) * FS + 16 * kk + u], sTT[(16 * jb + s) * FS + 16 * kk + u],
-                       acc);
-        sR[(jb * 16 + s) * 16 + t] = acc;
-      }
-      __syncthreads();
-      for (int o = tid; o < 256 * i; o += 256) {
-        const int jb = o / 256, s = (o / 16) % 16, t = o % 16;
-        float acc = 0.0f;
-        for (int u = 0; u <= t; ++u)
-          acc = fmaf(sTT[(16 * i + u) * FS + 16 * i + t], sR[(jb * 16 + s) * 16 + u], acc);
-        sTT[(16 * jb + s) * FS + 16 * i + t] = -acc;
+        for (int r = 0; r < 4; ++r)
+          sTT[(16 * jb + L) * FS + 16 * i + 4 * g + r] = res[r];
       }
       __syncthreads();
     }
 
     // T_w^T[s][t] = beta_s e^(g_s) T[t][s] and T_b^T[s][t] = beta_s T[t][s],
-    // hi/lo, over A and T^T (read to registers first).
+    // hi/lo.
     {
       const unsigned s = tid / 4, tb = 16 * (tid % 4);
-      float tv[16];
-#pragma unroll
-      for (int x = 0; x < 16; ++x) {
-        const unsigned t = tb + x;
-        tv[x] = t >= s ? sTT[s * FS + t] : 0.0f;
-      }
       const float bw = sB[s] * sEg[s], bb = sB[s];
-      __syncthreads();
 #pragma unroll
       for (int x4 = 0; x4 < 4; ++x4) {
+        float4_t tv;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const unsigned t = tb + 4 * x4 + e;
+          tv[e] = t >= s ? sTT[s * FS + t] : 0.0f;
+        }
         half4_t wh, wl, bh, bl;
-        split4(float4_t{tv[4 * x4], tv[4 * x4 + 1], tv[4 * x4 + 2], tv[4 * x4 + 3]} * bw, wh, wl);
-        split4(float4_t{tv[4 * x4], tv[4 * x4 + 1], tv[4 * x4 + 2], tv[4 * x4 + 3]} * bb, bh, bl);
+        split4(tv * bw, wh, wl);
+        split4(tv * bb, bh, bl);
         const unsigned o = s * CS + tb + 4 * x4;
         *reinterpret_cast<half4_t *>(sTwh + o) = wh;
         *reinterpret_cast<half4_t *>(sTwl + o) = wl;
@@ -366,78 +444,96 @@ __global__ __launch_bounds__(256, 1) void delta_prep_kernel(
     __syncthreads();
 
     // N^T = T_w^T M^T (N = M T diag(beta e^g)); -N to LDS as [t][s] hi/lo.
+    // Wave w: s rows [16 w, 16 w + 16), all four t tiles.
+    {
+      half8_t ah[2], al[2];
 #pragma unroll
-    for (int rep = 0; rep < 4; ++rep) {
-      const int ti = wave + 4 * rep, st = ti / 4, tt = ti % 4;
-      float4_t acc{0.0f, 0.0f, 0.0f, 0.0f}, crs{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-      for (int ks = 0; ks < C / 32; ++ks) {
-        const int k0 = 32 * ks + 8 * g;
-        const half8_t ah = load8(sTwh + (16 * st + L) * CS + k0);
-        const half8_t al = load8(sTwl + (16 * st + L) * CS + k0);
-        const half8_t bh = load8(sMh + (16 * tt + L) * CS + k0);
-        const half8_t bl = load8(sMl + (16 * tt + L) * CS + k0);
-        acc = mfma16(ah, bh, acc);
-        crs = mfma16(ah, bl, crs);
-        crs = mfma16(al, bh, crs);
+      for (int ks = 0; ks < 2; ++ks) {
+        ah[ks] = load8(sTwh + (16 * wave + L) * CS + 32 * ks + 8 * g);
+        al[ks] = load8(sTwl + (16 * wave + L) * CS + 32 * ks + 8 * g);
       }
-      half4_t nh, nl;
-      split4(-(acc + crs * kSplitUnscale), nh, nl);
-      const unsigned o = (16 * tt + L) * CS + 16 * st + 4 * g;
-      *reinterpret_cast<half4_t *>(sNh + o) = nh;
-      *reinterpret_cast<half4_t *>(sNl + o) = nl;
+      float4_t acc[4], crs[4];
+#pragma unroll
+      for (int tt = 0; tt < 4; ++tt) {
+        acc[tt] = crs[tt] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+          const half8_t bh = load8(sMh + (16 * tt + L) * CS + 32 * ks + 8 * g);
+          const half8_t bl = load8(sMl + (16 * tt + L) * CS + 32 * ks + 8 * g);
+          acc[tt] = mfma16(ah[ks], bh, acc[tt]);
+          crs[tt] = mfma16(ah[ks], bl, crs[tt]);
+          crs[tt] = mfma16(al[ks], bh, crs[tt]);
+        }
+      }
+#pragma unroll
+      for (int tt = 0; tt < 4; ++tt) {
+        half4_t nh, nl;
+        split4(-(acc[tt] + crs[tt] * kSplitUnscale), nh, nl);
+        const unsigned o = (16 * tt + L) * CS + 16 * wave + 4 * g;
+        *reinterpret_cast<half4_t *>(sNh + o) = nh;
+        *reinterpret_cast<half4_t *>(sNl + o) = nl;
+      }
     }
     __syncthreads();
 
     // Wn and Q' pieces: W^T = K^T T_w^T and Q'^T = e^g Q^T - K^T N^T share
-    // the K^T operand. Wave w writes blocks (m, kb) = w + 4 rep; block
-    // (m, kb) is tiles d = 2 kb, 2 kb + 1 of the transposed products.
+    // the K^T operand. Wave w writes the blocks (m, kb = w): tiles d = 2w,
+    // 2w + 1 of the transposed products against the four t tiles m.
     {
       half_t *const wp = reinterpret_cast<half_t *>(rec);
       half_t *const qp = reinterpret_cast<half_t *>(rec + kPieceBytes);
-#pragma unroll 1
-      for (int rep = 0; rep < 4; ++rep) {
-        const int pi = wave + 4 * rep, mt = pi / 4, kb = pi % 4;
+      half8_t kah[2][2], kal[2][2]; // [d tile][ks]
+#pragma unroll
+      for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+          kah[hf][ks] = read_kcol(sKh, KS, 32 * ks, 16 * (2 * wave + hf), g, L);
+          kal[hf][ks] = read_kcol(sKl, KS, 32 * ks, 16 * (2 * wave + hf), g, L);
+        }
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt) {
         const unsigned t = 16 * mt + L;
-        half8_t wh, wl, qh, ql;
+        half8_t b1h[2], b1l[2], b2h[2], b2l[2];
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+          b1h[ks] = read_kcol(sTwh, CS, 32 * ks, 16 * mt, g, L);
+          b1l[ks] = read_kcol(sTwl, CS, 32 * ks, 16 * mt, g, L);
+          b2h[ks] = load8(sNh + t * CS + 32 * ks + 8 * g);
+          b2l[ks] = load8(sNl + t * CS + 32 * ks + 8 * g);
+        }
+        float4_t wa[2], wx[2], qa[2], qx[2];
 #pragma unroll
         for (int hf = 0; hf < 2; ++hf) {
-          const int dt = 2 * kb + hf;
-          float4_t wa{0.0f, 0.0f, 0.0f, 0.0f}, wx{0.0f, 0.0f, 0.0f, 0.0f};
-          float4_t qa{0.0f, 0.0f, 0.0f, 0.0f}, qx{0.0f, 0.0f, 0.0f, 0.0f};
-          if (t < n)
-            qa = *reinterpret_cast<const float4_t *>(q + (size_t)(t0 + t) * qkStride +
-                                                     (size_t)kh * DK + 16 * dt + 4 * g) *
-                 sEg[t];
+          wa[hf] = wx[hf] = qx[hf] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
+          qa[hf] = wx[hf];
+          qa[hf] = qinit[hf][mt] * sEg[t];
+        }
 #pragma unroll
-          for (int ks = 0; ks < C / 32; ++ks) {
-            const unsigned s0 = 32 * ks;
-            const half8_t ah = read_kcol(sKh, KS, s0, 16 * dt, g, L);
-            const half8_t al = read_kcol(sKl, KS, s0, 16 * dt, g, L);
-            const half8_t b1h = read_kcol(sTwh, CS, s0, 16 * mt, g, L);
-            const half8_t b1l = read_kcol(sTwl, CS, s0, 16 * mt, g, L);
-            const half8_t b2h = load8(sNh + t * CS + s0 + 8 * g);
-            const half8_t b2l = load8(sNl + t * CS + s0 + 8 * g);
-            wa = mfma16(ah, b1h, wa);
-            wx = mfma16(ah, b1l, wx);
-            wx = mfma16(al, b1h, wx);
-            qa = mfma16(ah, b2h, qa);
-            qx = mfma16(ah, b2l, qx);
-            qx = mfma16(al, b2h, qx);
+        for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+          for (int hf = 0; hf < 2; ++hf) {
+            wa[hf] = mfma16(kah[hf][ks], b1h[ks], wa[hf]);
+            qa[hf] = mfma16(kah[hf][ks], b2h[ks], qa[hf]);
+            wx[hf] = mfma16(kah[hf][ks], b1l[ks], wx[hf]);
+            qx[hf] = mfma16(kah[hf][ks], b2l[ks], qx[hf]);
+            wx[hf] = mfma16(kal[hf][ks], b1h[ks], wx[hf]);
+            qx[hf] = mfma16(kal[hf][ks], b2h[ks], qx[hf]);
           }
-          const float ez = sEz[t];
+        const float ez = sEz[t];
+        half8_t wh, wl, qh, ql;
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf)
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
             half_t a, b;
-            split_f16(-ez * (wa[r] + wx[r] * kSplitUnscale), a, b);
+            split_f16(-ez * (wa[hf][r] + wx[hf][r] * kSplitUnscale), a, b);
             wh[4 * hf + r] = a;
             wl[4 * hf + r] = b;
-            split_f16(qa[r] + qx[r] * kSplitUnscale, a, b);
+            split_f16(qa[hf][r] + qx[hf][r] * kSplitUnscale, a, b);
             qh[4 * hf + r] = a;
             ql[4 * hf + r] = b;
           }
-        }
-        const unsigned o = pi * kBlk + 8 * lane;
+        const unsigned o = (4 * mt + wave) * kBlk + 8 * lane;
         *reinterpret_cast<half8_t *>(wp + o) = wh;
         *reinterpret_cast<half8_t *>(wp + kPieceBlocks * kBlk + o) = wl;
         *reinterpret_cast<half8_t *>(qp + o) = qh;
@@ -447,61 +543,87 @@ __global__ __launch_bounds__(256, 1) void delta_prep_kernel(
 
     // U0 = T_b V per 16-column slice (wave w: slices w + 4 rep of each V
     // block), then Z0 = e^(g_C - g) U0 and Y0 = M U0 with U0 as the B
-    // operand straight from its C-layout registers.
-    float4_t *const z0 = reinterpret_cast<float4_t *>(rec + 2 * kPieceBytes);
-    float4_t *const y0 = z0 + (size_t)C * DV / 4;
-    for (unsigned jb = 0; jb < DV; jb += VB) {
-      const unsigned w = min((unsigned)VB, DV - jb);
-      __syncthreads();
-      for (unsigned i = tid; i < C * w / 8; i += 256) {
-        const unsigned t = i / (w / 8), j8 = (i % (w / 8)) * 8;
-        half8_t x{0, 0, 0, 0, 0, 0, 0, 0};
-        if (t < n)
-          x = load8(v + (size_t)(t0 + t) * vStride + (size_t)h * DV + jb + j8);
-        *reinterpret_cast<half8_t *>(sQV + t * KS + j8) = x;
-      }
-      __syncthreads();
-#pragma unroll 1
-      for (unsigned jt = wave; jt < w / 16; jt += 4) {
-        const unsigned js = jb / 16 + jt;
-        float4_t u[4];
+    // operand straight from its C-layout registers. The T_b and M operands
+    // are read once per wave.
+    {
+      half8_t tbh[4][2], tbl[4][2], mah[4][2], mal[4][2];
 #pragma unroll
-        for (int mt = 0; mt < 4; ++mt) {
-          float4_t a{0.0f, 0.0f, 0.0f, 0.0f}, x{0.0f, 0.0f, 0.0f, 0.0f};
+      for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
-          for (int ks = 0; ks < C / 32; ++ks) {
-            const half8_t bv = read_kcol(sQV, KS, 32 * ks, 16 * jt, g, L);
-            a = mfma16(read_kcol(sTbh, CS, 32 * ks, 16 * mt, g, L), bv, a);
-            x = mfma16(read_kcol(sTbl, CS, 32 * ks, 16 * mt, g, L), bv, x);
-          }
-          u[mt] = a + x * kSplitUnscale;
-          float4_t zz;
-#pragma unroll
-          for (int r = 0; r < 4; ++r)
-            zz[r] = sEz[16 * mt + 4 * g + r] * u[mt][r];
-          z0[(js * 4 + mt) * 64 + lane] = zz;
+        for (int ks = 0; ks < 2; ++ks) {
+          tbh[mt][ks] = read_kcol(sTbh, CS, 32 * ks, 16 * mt, g, L);
+          tbl[mt][ks] = read_kcol(sTbl, CS, 32 * ks, 16 * mt, g, L);
+          const unsigned o = (16 * mt + L) * CS + 32 * ks + 4 * g;
+          mah[mt][ks] = cat8(load4(sMh + o), load4(sMh + o + 16));
+          mal[mt][ks] = cat8(load4(sMl + o), load4(sMl + o + 16));
         }
-        half8_t ubh[2], ubl[2];
+      float ezr[4][4];
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
-          split8(u[2 * kb], u[2 * kb + 1], ubh[kb], ubl[kb]);
+      for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
-        for (int mt = 0; mt < 4; ++mt) {
-          float4_t a{0.0f, 0.0f, 0.0f, 0.0f}, x{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int r = 0; r < 4; ++r)
+          ezr[mt][r] = sEz[16 * mt + 4 * g + r];
+      float4_t *const z0 = reinterpret_cast<float4_t *>(rec + 2 * kPieceBytes);
+      float4_t *const y0 = z0 + (size_t)C * DV / 4;
+      for (unsigned jb = 0; jb < DV; jb += VB) {
+        const unsigned w = min((unsigned)VB, DV - jb);
+        if (jb > 0) {
+          // Further dv blocks (DV > VB) are fetched here, in turn.
+          fetch_v(h, jb, w);
+          __syncthreads();
+          store_v(w);
+          __syncthreads();
+        }
+#pragma unroll 1
+        for (unsigned jt = wave; jt < w / 16; jt += 4) {
+          const unsigned js = jb / 16 + jt;
+          half8_t bv[2];
 #pragma unroll
-          for (int kb = 0; kb < 2; ++kb) {
-            const unsigned o = (16 * mt + L) * CS + 32 * kb + 4 * g;
-            const half8_t ah = cat8(load4(sMh + o), load4(sMh + o + 16));
-            const half8_t al = cat8(load4(sMl + o), load4(sMl + o + 16));
-            a = mfma16(ah, ubh[kb], a);
-            x = mfma16(ah, ubl[kb], x);
-            x = mfma16(al, ubh[kb], x);
+          for (int ks = 0; ks < 2; ++ks)
+            bv[ks] = read_kcol(sQV, KS, 32 * ks, 16 * jt, g, L);
+          float4_t ua[4], ux[4];
+#pragma unroll
+          for (int mt = 0; mt < 4; ++mt) {
+            ua[mt] = ux[mt] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks) {
+              ua[mt] = mfma16(tbh[mt][ks], bv[ks], ua[mt]);
+              ux[mt] = mfma16(tbl[mt][ks], bv[ks], ux[mt]);
+            }
           }
-          y0[(js * 4 + mt) * 64 + lane] = a + x * kSplitUnscale;
+          float4_t u[4];
+#pragma unroll
+          for (int mt = 0; mt < 4; ++mt) {
+            u[mt] = ua[mt] + ux[mt] * kSplitUnscale;
+            float4_t zz;
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+              zz[r] = ezr[mt][r] * u[mt][r];
+            z0[(js * 4 + mt) * 64 + lane] = zz;
+          }
+          half8_t ubh[2], ubl[2];
+#pragma unroll
+          for (int kb = 0; kb < 2; ++kb)
+            split8(u[2 * kb], u[2 * kb + 1], ubh[kb], ubl[kb]);
+          float4_t ya[4], yx[4];
+#pragma unroll
+          for (int mt = 0; mt < 4; ++mt) {
+            ya[mt] = yx[mt] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb) {
+              ya[mt] = mfma16(mah[mt][kb], ubh[kb], ya[mt]);
+              yx[mt] = mfma16(mah[mt][kb], ubl[kb], yx[mt]);
+              yx[mt] = mfma16(mal[mt][kb], ubh[kb], yx[mt]);
+            }
+          }
+#pragma unroll
+          for (int mt = 0; mt < 4; ++mt)
+            y0[(js * 4 + mt) * 64 + lane] = ya[mt] + yx[mt] * kSplitUnscale;
         }
       }
     }
-    __syncthreads();
+    if (hr + 1 < R && DV > VB)
+      fetch_v(h + 1, 0, w0);
   }
 }
 
