@@ -215,11 +215,10 @@ __global__ __launch_bounds__(256, 1) void delta_prep_kernel(
   for (int hf = 0; hf < 2; ++hf)
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt) {
-      const unsigned t = 16 * mt + L;
-      qinit[hf][mt] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
-      if (t < n)
-        qinit[hf][mt] = *reinterpret_cast<const float4_t *>(
-            q + (size_t)(t0 + t) * qkStride + (size_t)kh * DK + 16 * (2 * wave + hf) + 4 * g);
+      const unsigned t = 16 * mt + L, tc = min(t, n - 1); // rows past the end read row n-1
+      const float4_t x = *reinterpret_cast<const float4_t *>(
+          q + (size_t)(t0 + tc) * qkStride + (size_t)kh * DK + 16 * (2 * wave + hf) + 4 * g);
+      qinit[hf][mt] = t < n ? x : float4_t{0.0f, 0.0f, 0.0f, 0.0f};
     }
   float gateA = 1.0f, gateB = 0.0f;
   auto load_gates = [&](unsigned h) {
@@ -237,9 +236,10 @@ __global__ __launch_bounds__(256, 1) void delta_prep_kernel(
 #pragma unroll
     for (int it = 0; it < kVItems; ++it) {
       const unsigned i = tid + 256 * it, t = i / (w / 8), j8 = (i % (w / 8)) * 8;
-      vreg[it] = half8_t{0, 0, 0, 0, 0, 0, 0, 0};
-      if (i < C * w / 8 && t < n)
-        vreg[it] = load8(v + (size_t)(t0 + t) * vStride + (size_t)h * DV + jb + j8);
+      const unsigned tc = min(t, n - 1); // rows past the end (or items past w) read row n-1
+      const half8_t x =
+          load8(v + (size_t)(t0 + tc) * vStride + (size_t)h * DV + jb + (i < C * w / 8 ? j8 : 0));
+      vreg[it] = t < n ? x : half8_t{0, 0, 0, 0, 0, 0, 0, 0};
     }
   };
   auto store_v = [&](unsigned w) {
@@ -261,19 +261,17 @@ __global__ __launch_bounds__(256, 1) void delta_prep_kernel(
 #pragma unroll
     for (int it = 0; it < NI; ++it) {
       const unsigned i = tid + 256 * it, t = i / (DK / 4), d4 = (i % (DK / 4)) * 4;
-      kv[it] = qv[it] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
-      if (t < n) {
-        const size_t off = (size_t)(t0 + t) * qkStride + (size_t)kh * DK + d4;
-        kv[it] = *reinterpret_cast<const float4_t *>(k + off);
-        qv[it] = *reinterpret_cast<const float4_t *>(q + off);
-      }
+      const size_t off = (size_t)(t0 + min(t, n - 1)) * qkStride + (size_t)kh * DK + d4;
+      kv[it] = *reinterpret_cast<const float4_t *>(k + off);
+      qv[it] = *reinterpret_cast<const float4_t *>(q + off);
     }
 #pragma unroll
     for (int it = 0; it < NI; ++it) {
       const unsigned i = tid + 256 * it, t = i / (DK / 4), d4 = (i % (DK / 4)) * 4;
+      const float4_t zero{0.0f, 0.0f, 0.0f, 0.0f};
       half4_t khi, klo, qhi, qlo;
-      split4(kv[it], khi, klo);
-      split4(qv[it], qhi, qlo);
+      split4(t < n ? kv[it] : zero, khi, klo);
+      split4(t < n ? qv[it] : zero, qhi, qlo);
       *reinterpret_cast<half4_t *>(sKh + t * KS + d4) = khi;
       *reinterpret_cast<half4_t *>(sKl + t * KS + d4) = klo;
       *reinterpret_cast<half4_t *>(sQV + t * KS + d4) = qhi;
@@ -352,6 +350,7 @@ __global__ __launch_bounds__(256, 1) void delta_prep_kernel(
     // A (fp32) and M (hi/lo) from the Gram registers:
     // A[t][s] = beta_t e^(g_t - g_s) k_t.k_s (s < t), M[t][s] = e^(g_t - g_s)
     // q_t.k_s (s <= t), zero above.
+    // Branch-free: every operand is read, the masks are selects.
     {
       const unsigned s = 16 * wave + L;
       const double gs = sG[s];
@@ -360,9 +359,10 @@ __global__ __launch_bounds__(256, 1) void delta_prep_kernel(
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const unsigned t = 16 * mt + 4 * g + r;
-          const float e =
-              s <= t ? __builtin_amdgcn_exp2f((float)(sG[t] - gs) * kLog2e) : 0.0f;
-          sA[t * FS + s] = s < t ? sB[t] * e * kk[mt][r] : 0.0f;
+          const float d = fminf((float)(sG[t] - gs), 0.0f);
+          const float e = s <= t ? __builtin_amdgcn_exp2f(d * kLog2e) : 0.0f;
+          const float a = sB[t] * e * kk[mt][r];
+          sA[t * FS + s] = s < t ? a : 0.0f;
           split_f16(e * qk[mt][r], sMh[t * CS + s], sMl[t * CS + s]);
         }
     }
@@ -429,7 +429,8 @@ __global__ __launch_bounds__(256, 1) void delta_prep_kernel(
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const unsigned t = tb + 4 * x4 + e;
-          tv[e] = t >= s ? sTT[s * FS + t] : 0.0f;
+          const float x = sTT[s * FS + t]; // read always: the select below is branch-free
+          tv[e] = t >= s ? x : 0.0f;
         }
         half4_t wh, wl, bh, bl;
         split4(tv * bw, wh, wl);
@@ -675,104 +676,174 @@ template <int N> __device__ __forceinline__ void wait_vm() {
 // wait attached (each wave waits for exactly what it must beforehand).
 __device__ __forceinline__ void barrier() { asm volatile("s_barrier" ::: "memory"); }
 
-// The scan workgroup: wave 0 computes; waves 1-3 load. A wave moves at most
-// ~16 bytes per cycle through direct-to-LDS loads (measured: ~38 GB/s per
-// wave whether the data sits in L2 or in HBM, scaling with the number of
-// waves), and a chunk's operands are 105 KiB: spread over three loader
-// waves they take about as long as the compute wave's products.
-constexpr int kLoaders = 3;
-constexpr int kPartLoads = (kPieceLoads + kLoaders - 1) / kLoaders; // 11 KiB of a piece per loader
-constexpr int kZYLoads = 3;   // 8 Z0/Y0 blocks and the scalars over 3 loaders
-constexpr int kWLoads = kPartLoads + kZYLoads;
+// The scan workgroup, 4 waves on the 4 SIMDs of one CU:
+//   wave 0 (chain): the state recursion Z = Z0 + Wn S, S <- e^(g_C) S + K^T Z;
+//   wave 1 (output): Y = Y0 + Q' S from the split S that wave 0 leaves in
+//           LDS, with Q' and Y0 loaded straight into its registers;
+//   waves 2-3 (loaders): the Wn, K^T pieces and Z0 (+ scalars) of the next
+//           chunk, direct to LDS, double-buffered.
+// A wave moves at most ~16 bytes per cycle through direct-to-LDS loads
+// (measured: ~38 GB/s per wave whether the data sits in L2 or in HBM,
+// scaling with the number of waves), so the chain wave issues none.
+constexpr int kLoaders = 2;
+constexpr int kPartLoads = kPieceLoads / kLoaders;  // 16 KiB of a piece per loader
+constexpr int kZLoads = 4 / kLoaders + 1;            // Z0 blocks + the scalars
+constexpr int kWLoads = kPartLoads + kZLoads;
 
-__global__ __launch_bounds__(64 * (1 + kLoaders), 1) void delta_scan_kernel(
+__global__ __launch_bounds__(256, 1) void delta_scan_kernel(
     float *__restrict__ state, half_t *__restrict__ out, const void *__restrict__ ws,
     unsigned T, unsigned Hk, unsigned Hv, unsigned DV) {
   // Workgroups are dealt to the 8 XCDs round-robin by block index. Give
   // each XCD a contiguous run of (value head, slice) pairs, so that the
-  // workgroups reading one value head's Wn and Q' pieces and one key head's
-  // K^T piece share an L2.
+  // workgroups reading one value head's pieces and one key head's K^T piece
+  // share an L2.
   const unsigned slices = DV / 16, nb = gridDim.x;
   const unsigned Lb = nb % 8 == 0 ? (blockIdx.x % 8) * (nb / 8) + blockIdx.x / 8 : blockIdx.x;
   const unsigned h = Lb / slices, js = Lb % slices, kh = h / (Hv / Hk);
-  const unsigned wave = threadIdx.x >> 6, lane = threadIdx.x & 63u, g = lane >> 4;
-  const unsigned chunks = (T + C - 1) / C;
+  const unsigned wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const unsigned lane = threadIdx.x & 63u, g = lane >> 4;
+  const unsigned chunks = (T + C - 1) / C, last = chunks - 1;
   const size_t recB = rec_bytes(DV), vStride = (size_t)Hv * DV;
   void *const wsp = const_cast<void *>(ws);
 
-  // Wn and this slice's Z0/Y0 (+ scalars) double-buffered, K^T and Q'
-  // single. Chunk c uses buffer c % 2.
+  // Chunk c uses buffer c % 2 of Wn, K^T and Z0; sS holds the split S of
+  // the current chunk for wave 1.
   constexpr int PB = 2 * kPieceBlocks * 64; // half8s per piece
-  __shared__ half8_t sW0[PB], sW1[PB], sK[PB], sQ[PB];
-  __shared__ float4_t sZY0[8 * 64 + 16], sZY1[8 * 64 + 16];
+  __shared__ half8_t sW0[PB], sW1[PB], sK0[PB], sK1[PB];
+  __shared__ float4_t sZ0[4 * 64 + 16], sZ1[4 * 64 + 16]; // Z0 blocks, scalars
+  __shared__ half8_t sS[8 * 64];                           // bh[4], bl[4]
 
   auto rec = [&](unsigned c) { return rec_ptr(wsp, recB, Hv, c, h); };
   auto kp = [&](unsigned c) { return kpiece_ptr(wsp, recB, chunks, Hv, Hk, c, kh); };
+  const unsigned j = 16 * js + (lane & 15u);
 
-  // Per chunk c, barriers A(c), B(c), C(c), then A(c + 1):
-  //   wave 0: A(c) [Wn, Z0/Y0 of c in LDS] products with Wn; B(c) [K^T of
-  //           c in LDS; Wn buffer free] products with K^T; C(c) [Q' of c in
-  //           LDS; K^T buffer free] products with Q', output rows;
-  //           A(c + 1) [Q' buffer free].
-  //   loaders: after A(c) load Q' of c; after B(c) Wn, Z0/Y0 of c + 2;
-  //           after C(c) K^T of c + 1; each waits for its own part of what
-  //           the next barrier promises before arriving there.
-  if (wave > 0) {
-    const unsigned l = __builtin_amdgcn_readfirstlane(wave - 1);
-    // Loader l's part of a piece: KiB [11 l, 11 l + 11), clamped to the
-    // piece (the last part repeats its final KiB: the same bytes again).
+  // Per chunk c, barriers A(c) then B(c):
+  //   A(c): Wn, Z0 of c landed (buffer c % 2); wave 1 has read the previous
+  //         split S; the buffers of chunk c - 1 are free.
+  //   B(c): K^T of c landed; wave 0 has written this chunk's split S.
+  if (wave >= 2) {
+    const unsigned l = wave - 2;
     auto load_part = [&](const char *src, const half8_t *dst) {
       const int4v_t rsrc = buffer_rsrc(src, kPieceBytes);
 #pragma unroll
       for (int it = 0; it < kPartLoads; ++it) {
-        const unsigned kib = min(kPartLoads * l + it, (unsigned)kPieceLoads - 1);
+        const unsigned kib = kPartLoads * l + it;
         load_lds_1k(rsrc, lds_addr(dst) + 1024 * kib, 16 * lane, 1024 * kib);
       }
     };
-    // Wn and the Z0/Y0 blocks 3l .. 3l + 2 (block 8: the scalars).
-    auto load_w = [&](unsigned c, const half8_t *dW, const float4_t *dZY) {
+    auto load_w = [&](unsigned c, const half8_t *dW, const float4_t *dZ) {
       const char *r = rec(c);
       load_part(r, dW);
       const char *z = r + 2 * kPieceBytes + (size_t)js * 4 * 64 * sizeof(float4_t);
-      const int4v_t rz = buffer_rsrc(z, 4 * 1024), ry = buffer_rsrc(z + (size_t)C * DV * 4, 4 * 1024);
+      const int4v_t rz = buffer_rsrc(z, 4 * 1024);
 #pragma unroll
-      for (int i = 0; i < kZYLoads; ++i) {
-        const unsigned blk = kZYLoads * l + i;
-        if (blk < 4)
-          load_lds_1k(rz, lds_addr(dZY + 64 * blk), 16 * lane, 1024 * blk);
-        else if (blk < 8)
-          load_lds_1k(ry, lds_addr(dZY + 64 * blk), 16 * lane, 1024 * (blk - 4));
-        else
-          load_lds_256(buffer_rsrc(r + rec_scalars(DV), kScalarBytes), lds_addr(dZY + 8 * 64),
-                       4 * lane);
+      for (int i = 0; i < kZLoads - 1; ++i) {
+        const unsigned blk = (kZLoads - 1) * l + i;
+        load_lds_1k(rz, lds_addr(dZ + 64 * blk), 16 * lane, 1024 * blk);
       }
+      load_lds_256(buffer_rsrc(r + rec_scalars(DV), kScalarBytes), lds_addr(dZ + 4 * 64),
+                   4 * lane);
     };
-    const unsigned last = chunks - 1;
-    load_w(0, sW0, sZY0);
-    load_w(min(1u, last), sW1, sZY1);
-    load_part(kp(0), sK);
-    wait_vm<kWLoads + kPartLoads>();
+    load_w(0, sW0, sZ0);
+    load_part(kp(0), sK0);
+    wait_vm<kPartLoads>(); // Wn, Z0 of 0
     for (unsigned c = 0; c < chunks; ++c) {
       barrier(); // A(c)
-      load_part(rec(c) + kPieceBytes, sQ);
-      wait_vm<kPartLoads>(); // K^T of c
+      const unsigned cn = min(c + 1, last);
+      if (c % 2 == 0) {
+        load_w(cn, sW1, sZ1);
+        load_part(kp(cn), sK1);
+      } else {
+        load_w(cn, sW0, sZ0);
+        load_part(kp(cn), sK0);
+      }
+      wait_vm<kWLoads + kPartLoads>(); // K^T of c
       barrier(); // B(c)
-      if (c % 2 == 0)
-        load_w(min(c + 2, last), sW0, sZY0);
-      else
-        load_w(min(c + 2, last), sW1, sZY1);
-      wait_vm<kWLoads>(); // Q' of c
-      barrier(); // C(c)
-      load_part(kp(min(c + 1, last)), sK);
-      wait_vm<kPartLoads + kPartLoads + kWLoads + kPartLoads>(); // Wn, Z0/Y0 of c + 1
+      wait_vm<kPartLoads>(); // Wn, Z0 of c + 1
     }
-    barrier(); // A(chunks)
     wait_vm<0>();
     return;
   }
 
-  const unsigned j = 16 * js + (lane & 15u);
-  // The state slice: register r of tile i holds S[16 i + 4 g + r][j].
+  if (wave == 1) {
+    // Q' (32 blocks) and Y0 (4 blocks) of a chunk, into registers.
+    struct QY {
+      half8_t q[2][kPieceBlocks];
+      float4_t y[4];
+    };
+    auto load_qy = [&](unsigned c, QY &d) {
+      const char *r = rec(c);
+      const half8_t *qp = reinterpret_cast<const half8_t *>(r + kPieceBytes) + lane;
+#pragma unroll
+      for (int b = 0; b < kPieceBlocks; ++b) {
+        d.q[0][b] = qp[b * 64];
+        d.q[1][b] = qp[(kPieceBlocks + b) * 64];
+      }
+      const float4_t *yp = reinterpret_cast<const float4_t *>(r + 2 * kPieceBytes) +
+                           (size_t)C * DV / 4 + js * 4 * 64 + lane;
+#pragma unroll
+      for (int m = 0; m < 4; ++m)
+        d.y[m] = yp[m * 64];
+    };
+    auto ystep = [&](unsigned c, const QY &cur, QY &nxt) {
+      const unsigned t0 = c * C, n = min((unsigned)C, T - t0);
+      barrier(); // A(c)
+      barrier(); // B(c)
+      half8_t bh[4], bl[4];
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb) {
+        bh[kb] = sS[kb * 64 + lane];
+        bl[kb] = sS[(4 + kb) * 64 + lane];
+      }
+      wait_lds_reads();
+      load_qy(min(c + 1, last), nxt);
+      float4_t ya[4], yx[4];
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        ya[m] = cur.y[m];
+        yx[m] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
+      }
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb) {
+#pragma unroll
+        for (int m = 0; m < 4; ++m)
+          ya[m] = mfma16(cur.q[0][4 * m + kb], bh[kb], ya[m]);
+#pragma unroll
+        for (int m = 0; m < 4; ++m)
+          yx[m] = mfma16(cur.q[0][4 * m + kb], bl[kb], yx[m]);
+#pragma unroll
+        for (int m = 0; m < 4; ++m)
+          yx[m] = mfma16(cur.q[1][4 * m + kb], bh[kb], yx[m]);
+      }
+      // Rows past the end of the tokens fall outside the descriptor and
+      // are dropped by the buffer stores.
+      const auto ro = __builtin_amdgcn_make_buffer_rsrc(
+          (void *)(out + (size_t)t0 * vStride + (size_t)h * DV), (short)0,
+          (int)(((n - 1) * vStride + DV) * sizeof(half_t)), kBufferWord3);
+#pragma unroll
+      for (int m = 0; m < 4; ++m)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const unsigned t = 16 * m + 4 * g + r;
+          const half_t y = (half_t)(ya[m][r] + yx[m][r] * kSplitUnscale);
+          __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(unsigned short, y), ro,
+                                                (unsigned)((t * vStride + j) * sizeof(half_t)),
+                                                0, 0);
+        }
+    };
+    QY qa, qb;
+    load_qy(0, qa);
+    unsigned c = 0;
+    for (; c + 1 < chunks; c += 2) {
+      ystep(c, qa, qb);
+      ystep(c + 1, qb, qa);
+    }
+    if (c < chunks)
+      ystep(c, qa, qb);
+    return;
+  }
+
+  // Wave 0: the state slice, register r of tile i holding S[16 i + 4 g + r][j].
   float4_t S[8];
   float *const scol = state + (size_t)h * DK * DV + j;
 #pragma unroll
@@ -781,33 +852,35 @@ __global__ __launch_bounds__(64 * (1 + kLoaders), 1) void delta_scan_kernel(
     for (int r = 0; r < 4; ++r)
       S[i][r] = scol[(size_t)(16 * i + 4 * g + r) * DV];
 
-  auto step = [&](unsigned c, const half8_t *rW, const float4_t *rZY) {
-    const unsigned t0 = c * C, n = min((unsigned)C, T - t0);
+  auto step = [&](unsigned c, const half8_t *rW, const float4_t *rZ, const half8_t *rK) {
     barrier(); // A(c)
     // All of a product's A blocks are read before its first MFMA (the
     // scheduler is kept from sinking the reads next to their uses, where
     // each would expose the LDS latency), and the MFMAs of one k block go
-    // accumulator by accumulator so that no MFMA waits on the one before.
+    // accumulator by accumulator so that no MFMA waits on the one before
+    // (a dependent 16x16x32 MFMA waits ~44 cycles, an independent one
+    // issues every ~18).
     half8_t A[2][kPieceBlocks];
 #pragma unroll
     for (int b = 0; b < kPieceBlocks; ++b) {
       A[0][b] = rW[b * 64 + lane];
       A[1][b] = rW[(kPieceBlocks + b) * 64 + lane];
     }
-    const float eC = rZY[8 * 64][0];
-    float4_t za[4], zx[4], ya[4], yx[4];
+    const float eC = rZ[4 * 64][0];
+    float4_t za[4], zx[4];
 #pragma unroll
     for (int m = 0; m < 4; ++m) {
-      za[m] = rZY[m * 64 + lane];
-      ya[m] = rZY[(4 + m) * 64 + lane];
+      za[m] = rZ[m * 64 + lane];
       zx[m] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
-      yx[m] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
     }
-    // S as the B operand of its four 32-row k blocks.
+    // S as the B operand of its four 32-row k blocks, also left for wave 1.
     half8_t bh[4], bl[4];
 #pragma unroll
-    for (int kb = 0; kb < 4; ++kb)
+    for (int kb = 0; kb < 4; ++kb) {
       split8(S[2 * kb], S[2 * kb + 1], bh[kb], bl[kb]);
+      sS[kb * 64 + lane] = bh[kb];
+      sS[(4 + kb) * 64 + lane] = bl[kb];
+    }
     __builtin_amdgcn_sched_barrier(0);
     // Z = Z0 + Wn S.
 #pragma unroll
@@ -828,8 +901,8 @@ __global__ __launch_bounds__(64 * (1 + kLoaders), 1) void delta_scan_kernel(
     // S <- e^(g_C) S + K^T Z, Z as the B operand of its two k blocks.
 #pragma unroll
     for (int b = 0; b < kPieceBlocks; ++b) {
-      A[0][b] = sK[b * 64 + lane];
-      A[1][b] = sK[(kPieceBlocks + b) * 64 + lane];
+      A[0][b] = rK[b * 64 + lane];
+      A[1][b] = rK[(kPieceBlocks + b) * 64 + lane];
     }
     half8_t zbh[2], zbl[2];
 #pragma unroll
@@ -859,54 +932,15 @@ __global__ __launch_bounds__(64 * (1 + kLoaders), 1) void delta_scan_kernel(
     for (int i = 0; i < 8; ++i)
       S[i] = sa[i] + sx[i] * kSplitUnscale;
     wait_lds_reads();
-    barrier(); // C(c)
-
-    // Y = Y0 + Q' S (the state before this chunk).
-#pragma unroll
-    for (int b = 0; b < kPieceBlocks; ++b) {
-      A[0][b] = sQ[b * 64 + lane];
-      A[1][b] = sQ[(kPieceBlocks + b) * 64 + lane];
-    }
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int kb = 0; kb < 4; ++kb) {
-#pragma unroll
-      for (int m = 0; m < 4; ++m)
-        ya[m] = mfma16(A[0][4 * m + kb], bh[kb], ya[m]);
-#pragma unroll
-      for (int m = 0; m < 4; ++m)
-        yx[m] = mfma16(A[0][4 * m + kb], bl[kb], yx[m]);
-#pragma unroll
-      for (int m = 0; m < 4; ++m)
-        yx[m] = mfma16(A[1][4 * m + kb], bh[kb], yx[m]);
-    }
-    wait_lds_reads();
-
-    // Rows past the end of the tokens fall outside the descriptor and are
-    // dropped by the buffer stores.
-    const auto ro = __builtin_amdgcn_make_buffer_rsrc(
-        (void *)(out + (size_t)t0 * vStride + (size_t)h * DV), (short)0,
-        (int)(((n - 1) * vStride + DV) * sizeof(half_t)), kBufferWord3);
-#pragma unroll
-    for (int m = 0; m < 4; ++m)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const unsigned t = 16 * m + 4 * g + r;
-        const half_t y = (half_t)(ya[m][r] + yx[m][r] * kSplitUnscale);
-        __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(unsigned short, y), ro,
-                                              (unsigned)((t * vStride + j) * sizeof(half_t)),
-                                              0, 0);
-      }
   };
 
   unsigned c = 0;
   for (; c + 1 < chunks; c += 2) {
-    step(c, sW0, sZY0);
-    step(c + 1, sW1, sZY1);
+    step(c, sW0, sZ0, sK0);
+    step(c + 1, sW1, sZ1, sK1);
   }
   if (c < chunks)
-    step(c, sW0, sZY0);
-  barrier(); // A(chunks)
+    step(c, sW0, sZ0, sK0);
 
 #pragma unroll
   for (int i = 0; i < 8; ++i)
@@ -938,8 +972,7 @@ hipError_t launch_delta_chunked(const float *q, const float *k, const uint16_t *
   hipError_t e = hipGetLastError();
   if (e != hipSuccess)
     return e;
-  hipLaunchKernelGGL(delta_scan_kernel, dim3(s.Hv * (s.Dv / 16)), dim3(64 * (1 + kLoaders)), 0,
-                     stream, state,
+  hipLaunchKernelGGL(delta_scan_kernel, dim3(s.Hv * (s.Dv / 16)), dim3(256), 0, stream, state,
                      reinterpret_cast<half_t *>(out), ws, s.T, s.Hk, s.Hv, s.Dv);
   return hipGetLastError();
 }
