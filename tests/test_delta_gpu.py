@@ -103,10 +103,13 @@ def test_prefill_cfg4(gpu):
 
 
 @pytest.mark.parametrize("shape", [(5, 2, 7, 4, 5), (3, 1, 4, 2, 4), (9, 2, 64, 4, 16),
-                                   (33, 4, 128, 4, 32)])
+                                   (33, 4, 128, 4, 32), (150, 2, 128, 8, 48),
+                                   (100, 1, 128, 2, 256), (70, 2, 128, 4, 144)])
 def test_other_shapes(gpu, shape):
     """Reference test-model shapes (MetalReferenceTest.py:37-40,
-    ConverterTest.py:43-46) and other head splits."""
+    ConverterTest.py:43-46) and other head splits; the last three take the
+    chunk-wise kernels with 4 value heads per key head, with dv = 256 (two
+    staged dv blocks) and with dv = 144 (a partial second block)."""
     T, hk, dk, hv, dv = shape
     print(f"delta shape {shape}", flush=True)
     x = oracle.make_delta_inputs(9, T, hk, dk, hv, dv, 0.2)
