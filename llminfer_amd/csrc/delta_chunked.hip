@@ -29,22 +29,24 @@
 // Two launches:
 //
 //  * deltaChunkPrep, grid (chunk, key head), 256 threads: every chunk at
-//    once. The Gram matrices K K^T and Q K^T on fp16 MFMA; per value head the
-//    decay weighting, T by blocked forward substitution in fp32, and the
-//    products Wn, Q', Z0, Y0 on fp16 MFMA in split form. The results go to
+//    once. The Gram matrices K K^T and Q K^T on fp16 MFMA (kept in
+//    registers); per value head the decay weighting, T by blocked
+//    substitution (diagonal blocks in fp32, off-diagonal blocks on MFMA), and
+//    the products Wn, Q', Z0, Y0 on fp16 MFMA in split form. The results go to
 //    the workspace already in the register order of the scan's MFMA operands.
 //
-//  * deltaChunkScan, grid (value head, 16-column dv slice), ONE wave per
-//    workgroup: walks the chunks in order with its state slice S [dk x 16]
-//    in registers. Every product runs on v_mfma_f32_16x16x32_f16, with the
-//    state (and Z) as the B operand straight from the C-layout registers of
-//    the product that made it: the k index of an operand block is permuted
-//    (sigma below) so that the 8 halves a lane supplies are the 8 rows it
-//    holds in two consecutive 16-row C tiles; the A operands (Wn, Q', K^T)
-//    were written by the prep with the same permutation. No LDS round trip,
-//    no barrier. The A operands of the next chunk stream HBM/L2 -> LDS
-//    (buffer_load ... lds) while the current chunk computes; each wave reads
-//    them from LDS with one 16-byte read per lane and block.
+//  * deltaChunkScan, grid (value head, 16-column dv slice), 4 waves: one
+//    walks the chunks in order with its state slice S [dk x 16] in
+//    registers, one computes the outputs, two load. Every product runs on
+//    v_mfma_f32_16x16x32_f16, with the state (and Z) as the B operand
+//    straight from the C-layout registers of the product that made it: the k
+//    index of an operand block is permuted (sigma below) so that the 8 halves
+//    a lane supplies are the 8 rows it holds in two consecutive 16-row C
+//    tiles; the A operands (Wn, Q', K^T) were written by the prep with the
+//    same permutation. No LDS round trip and no shuffle on the chain. The
+//    next chunk's Wn and K^T stream HBM/L2 -> LDS (buffer_load ... lds) while
+//    the current chunk computes; the chain wave reads them from LDS with one
+//    16-byte read per lane and block.
 //
 // Split form: x = hi + lo 2^-11 with hi = fp16(x), lo = fp16((x - hi) 2^11),
 // a.b ~ ah.bh + (ah.bl + al.bh) 2^-11, the cross terms in a second fp32
