@@ -493,54 +493,79 @@ __global__ __launch_bounds__(256, 1) void delta_prep_kernel(
           kah[hf][ks] = read_kcol(sKh, KS, 32 * ks, 16 * (2 * wave + hf), g, L);
           kal[hf][ks] = read_kcol(sKl, KS, 32 * ks, 16 * (2 * wave + hf), g, L);
         }
+      // Two t tiles at a time: their B operands read first, then 48 MFMAs
+      // over 16 independent accumulators.
 #pragma unroll
-      for (int mt = 0; mt < 4; ++mt) {
-        const unsigned t = 16 * mt + L;
-        half8_t b1h[2], b1l[2], b2h[2], b2l[2];
+      for (int mp = 0; mp < 2; ++mp) {
+        half8_t b1h[2][2], b1l[2][2], b2h[2][2], b2l[2][2]; // [tile of the pair][ks]
 #pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
-          b1h[ks] = read_kcol(sTwh, CS, 32 * ks, 16 * mt, g, L);
-          b1l[ks] = read_kcol(sTwl, CS, 32 * ks, 16 * mt, g, L);
-          b2h[ks] = load8(sNh + t * CS + 32 * ks + 8 * g);
-          b2l[ks] = load8(sNl + t * CS + 32 * ks + 8 * g);
+        for (int u = 0; u < 2; ++u) {
+          const int mt = 2 * mp + u;
+          const unsigned t = 16 * mt + L;
+#pragma unroll
+          for (int ks = 0; ks < 2; ++ks) {
+            b1h[u][ks] = read_kcol(sTwh, CS, 32 * ks, 16 * mt, g, L);
+            b1l[u][ks] = read_kcol(sTwl, CS, 32 * ks, 16 * mt, g, L);
+            b2h[u][ks] = load8(sNh + t * CS + 32 * ks + 8 * g);
+            b2l[u][ks] = load8(sNl + t * CS + 32 * ks + 8 * g);
+          }
         }
-        float4_t wa[2], wx[2], qa[2], qx[2];
+        float4_t wa[2][2], wx[2][2], qa[2][2], qx[2][2]; // [tile of the pair][d tile]
 #pragma unroll
-        for (int hf = 0; hf < 2; ++hf) {
-          wa[hf] = wx[hf] = qx[hf] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
-          qa[hf] = wx[hf];
-          qa[hf] = qinit[hf][mt] * sEg[t];
-        }
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks)
+        for (int u = 0; u < 2; ++u)
 #pragma unroll
           for (int hf = 0; hf < 2; ++hf) {
-            wa[hf] = mfma16(kah[hf][ks], b1h[ks], wa[hf]);
-            qa[hf] = mfma16(kah[hf][ks], b2h[ks], qa[hf]);
-            wx[hf] = mfma16(kah[hf][ks], b1l[ks], wx[hf]);
-            qx[hf] = mfma16(kah[hf][ks], b2l[ks], qx[hf]);
-            wx[hf] = mfma16(kal[hf][ks], b1h[ks], wx[hf]);
-            qx[hf] = mfma16(kal[hf][ks], b2h[ks], qx[hf]);
+            wa[u][hf] = wx[u][hf] = qx[u][hf] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
+            qa[u][hf] = qinit[hf][2 * mp + u] * sEg[16 * (2 * mp + u) + L];
           }
-        const float ez = sEz[t];
-        half8_t wh, wl, qh, ql;
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int hf = 0; hf < 2; ++hf)
+        for (int ks = 0; ks < 2; ++ks) {
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            half_t a, b;
-            split_f16(-ez * (wa[hf][r] + wx[hf][r] * kSplitUnscale), a, b);
-            wh[4 * hf + r] = a;
-            wl[4 * hf + r] = b;
-            split_f16(qa[hf][r] + qx[hf][r] * kSplitUnscale, a, b);
-            qh[4 * hf + r] = a;
-            ql[4 * hf + r] = b;
-          }
-        const unsigned o = (4 * mt + wave) * kBlk + 8 * lane;
-        *reinterpret_cast<half8_t *>(wp + o) = wh;
-        *reinterpret_cast<half8_t *>(wp + kPieceBlocks * kBlk + o) = wl;
-        *reinterpret_cast<half8_t *>(qp + o) = qh;
-        *reinterpret_cast<half8_t *>(qp + kPieceBlocks * kBlk + o) = ql;
+          for (int u = 0; u < 2; ++u)
+#pragma unroll
+            for (int hf = 0; hf < 2; ++hf) {
+              wa[u][hf] = mfma16(kah[hf][ks], b1h[u][ks], wa[u][hf]);
+              qa[u][hf] = mfma16(kah[hf][ks], b2h[u][ks], qa[u][hf]);
+            }
+#pragma unroll
+          for (int u = 0; u < 2; ++u)
+#pragma unroll
+            for (int hf = 0; hf < 2; ++hf) {
+              wx[u][hf] = mfma16(kah[hf][ks], b1l[u][ks], wx[u][hf]);
+              qx[u][hf] = mfma16(kah[hf][ks], b2l[u][ks], qx[u][hf]);
+            }
+#pragma unroll
+          for (int u = 0; u < 2; ++u)
+#pragma unroll
+            for (int hf = 0; hf < 2; ++hf) {
+              wx[u][hf] = mfma16(kal[hf][ks], b1h[u][ks], wx[u][hf]);
+              qx[u][hf] = mfma16(kal[hf][ks], b2h[u][ks], qx[u][hf]);
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          const int mt = 2 * mp + u;
+          const float ez = sEz[16 * mt + L];
+          half8_t wh, wl, qh, ql;
+#pragma unroll
+          for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              half_t a, b;
+              split_f16(-ez * (wa[u][hf][r] + wx[u][hf][r] * kSplitUnscale), a, b);
+              wh[4 * hf + r] = a;
+              wl[4 * hf + r] = b;
+              split_f16(qa[u][hf][r] + qx[u][hf][r] * kSplitUnscale, a, b);
+              qh[4 * hf + r] = a;
+              ql[4 * hf + r] = b;
+            }
+          const unsigned o = (4 * mt + wave) * kBlk + 8 * lane;
+          *reinterpret_cast<half8_t *>(wp + o) = wh;
+          *reinterpret_cast<half8_t *>(wp + kPieceBlocks * kBlk + o) = wl;
+          *reinterpret_cast<half8_t *>(qp + o) = qh;
+          *reinterpret_cast<half8_t *>(qp + kPieceBlocks * kBlk + o) = ql;
+        }
       }
     }
 
