@@ -58,6 +58,29 @@ typedef struct GraphDeltaParams {
   unsigned tokens, keyHeads, keyDim, valueHeads, valueDim;
 } GraphDeltaParams;
 
+/* lib/Backend/Metal/Kernels/ReferenceParams.h:23-26 */
+typedef struct RowParams {
+  unsigned rows, width;
+  float epsilon;
+} RowParams;
+
+/* lib/Backend/Metal/Kernels/ReferenceParams.h:28-30 */
+typedef struct ElementParams {
+  unsigned count;
+} ElementParams;
+
+/* lib/Backend/Metal/Kernels/ReferenceParams.h:44-47 */
+typedef struct RopeParams {
+  unsigned tokens, heads, headDim, rotaryDim, headStride, past, outputStart;
+  float epsilon, theta;
+} RopeParams;
+
+/* lib/Backend/Metal/Kernels/GraphParams.h:35-38 */
+typedef struct PartialRopeParams {
+  unsigned rows, heads, width, rotaryWidth, past;
+  float theta;
+} PartialRopeParams;
+
 enum llmi_hip_status {
   LLMI_HIP_OK = 0,
   LLMI_HIP_INVALID_ARGUMENT = 1, /* bad shape/pointer; nothing launched */
@@ -71,7 +94,11 @@ enum llmi_hip_op {
   LLMI_HIP_OP_KV_APPEND = 0,
   LLMI_HIP_OP_CAUSAL_GQA = 1,
   LLMI_HIP_OP_DELTA_UPDATE = 2,
-  LLMI_HIP_OP_KV_APPEND_CAUSAL_GQA = 3 /* the fused pair; params: GqaParams */
+  LLMI_HIP_OP_KV_APPEND_CAUSAL_GQA = 3, /* the fused pair; params: GqaParams */
+  LLMI_HIP_OP_NORM_ROPE = 4,            /* params: RopeParams */
+  LLMI_HIP_OP_RMS_NORM = 5,             /* params: RowParams */
+  LLMI_HIP_OP_PARTIAL_ROPE = 6,         /* params: PartialRopeParams */
+  LLMI_HIP_OP_SIGMOID_MUL = 7           /* params: ElementParams */
 };
 
 /* ---------------------------------------------------------------- KvAppend
@@ -88,6 +115,43 @@ LLMI_HIP_API int llmi_hip_cache_append(const uint16_t *src, uint16_t *cache, Cac
 LLMI_HIP_API int llmi_hip_kv_append(const uint16_t *k_src, const uint16_t *v_src,
                        uint16_t *k_cache, uint16_t *v_cache, CacheParams p,
                        void *stream);
+
+/* ------------------------------------------------- norms, rope, the gate
+ * The row work on either side of CausalGqa in the attention block
+ * (Qwen35ModelBuilder.cpp:175-197; MetalReferenceGraph.mm:307-330). Results
+ * equal the reference kernels' expressions evaluated in IEEE fp32 in their
+ * order (sequential fma sum of squares; 1/sqrt for rsqrt; pow, cos, sin and
+ * exp correctly rounded to fp32), bit for bit. fp16 buffers; weights fp32.
+ *
+ * normRope (Reference.metal:271-293, dispatched by
+ * MetalReferenceGraph.mm:315-326): for row r < tokens * heads, the headDim
+ * halves at input + r * headStride are RMS-normalised with (1 + weight),
+ * rounded to fp16, and pairs (i, i + rotaryDim/2), i < rotaryDim/2, are
+ * rotated by (past + r / heads) / theta^(2i / rotaryDim); the row is
+ * written at output + (outputStart * heads + r) * headDim. With
+ * outputStart = past and output = the key cache this is the K path with its
+ * cache append. output may equal input when headStride == headDim and
+ * outputStart == 0 (each row is read before it is written); other overlaps
+ * are undefined. rotaryDim must be even and <= headDim. */
+LLMI_HIP_API int llmi_hip_norm_rope(const uint16_t *input, const float *weight,
+                                    uint16_t *output, RopeParams p, void *stream);
+
+/* rmsNorm (Reference.metal:105-117; MetalExecutionPlan.cpp:579-596):
+ * output[r][i] = fp16(input[r][i] * rsqrt(mean(input[r]^2) + eps) *
+ * (1 + weight[i])), rows x width, dense. In place allowed. */
+LLMI_HIP_API int llmi_hip_rms_norm(const uint16_t *input, const float *weight,
+                                   uint16_t *output, RowParams p, void *stream);
+
+/* partialRope (Graph.metal:111-129; MetalExecutionPlan.cpp:628-637): rows of
+ * width halves, dense; the first rotaryWidth dims rotated as in normRope at
+ * position past + row / heads, the rest copied. In place allowed. */
+LLMI_HIP_API int llmi_hip_partial_rope(const uint16_t *input, uint16_t *output,
+                                       PartialRopeParams p, void *stream);
+
+/* sigmoidMul (Graph.metal:78-85; MetalExecutionPlan.cpp:609-620):
+ * output[i] = fp16(fp16(1 / (1 + exp(-gate[i]))) * input[i]), i < count. */
+LLMI_HIP_API int llmi_hip_sigmoid_mul(const uint16_t *gate, const uint16_t *input,
+                                      uint16_t *output, ElementParams p, void *stream);
 
 /* --------------------------------------------------------------- CausalGqa
  * Replaces gqaFlashAttention (FlashAttention.metal:1-83) for T > 1 and the

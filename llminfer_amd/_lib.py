@@ -22,10 +22,33 @@ OP_KV_APPEND = 0
 OP_CAUSAL_GQA = 1
 OP_DELTA_UPDATE = 2
 OP_KV_APPEND_CAUSAL_GQA = 3
+OP_NORM_ROPE = 4
+OP_RMS_NORM = 5
+OP_PARTIAL_ROPE = 6
+OP_SIGMOID_MUL = 7
 
 
 class CacheParams(C.Structure):
     _fields_ = [("count", C.c_uint), ("offset", C.c_uint)]
+
+
+class RowParams(C.Structure):
+    _fields_ = [("rows", C.c_uint), ("width", C.c_uint), ("epsilon", C.c_float)]
+
+
+class ElementParams(C.Structure):
+    _fields_ = [("count", C.c_uint)]
+
+
+class RopeParams(C.Structure):
+    _fields_ = [(n, C.c_uint) for n in ("tokens", "heads", "headDim", "rotaryDim",
+                                        "headStride", "past", "outputStart")] + \
+               [("epsilon", C.c_float), ("theta", C.c_float)]
+
+
+class PartialRopeParams(C.Structure):
+    _fields_ = [(n, C.c_uint) for n in ("rows", "heads", "width", "rotaryWidth", "past")] + \
+               [("theta", C.c_float)]
 
 
 class GqaParams(C.Structure):
@@ -67,6 +90,10 @@ _SZ = C.c_size_t
 # name -> (restype, argtypes). Every function declared in include/llminfer_hip.h.
 SIGNATURES = {
     "llmi_hip_cache_append": (C.c_int, [_P, _P, CacheParams, _P]),
+    "llmi_hip_norm_rope": (C.c_int, [_P, _P, _P, RopeParams, _P]),
+    "llmi_hip_rms_norm": (C.c_int, [_P, _P, _P, RowParams, _P]),
+    "llmi_hip_partial_rope": (C.c_int, [_P, _P, PartialRopeParams, _P]),
+    "llmi_hip_sigmoid_mul": (C.c_int, [_P, _P, _P, ElementParams, _P]),
     "llmi_hip_kv_append": (C.c_int, [_P, _P, _P, _P, CacheParams, _P]),
     "llmi_hip_causal_gqa": (C.c_int, [_P, _P, _P, _P, GqaParams, _P, _SZ, _P]),
     "llmi_hip_gqa_workspace_bytes": (_SZ, [GqaParams]),

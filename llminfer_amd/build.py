@@ -32,6 +32,13 @@ COMMON = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}",
           "-fvisibility=hidden"]
 
 
+# Per-file additions. norm_rope.hip reproduces the reference's fp16 rounding
+# points bit for bit, which needs every fp32 product rounded on its own: under
+# the default -ffp-contract=fast the backend folds a product and the fp16
+# conversion or add after it into one fused instruction.
+FILE_FLAGS = {"norm_rope.hip": ["-ffp-contract=off"]}
+
+
 def hipcc() -> str:
     for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
         if cand and Path(cand).exists():
@@ -45,7 +52,8 @@ def sources() -> list[Path]:
 
 def _compile(src: Path) -> Path:
     obj = BUILD / (src.stem + ".o")
-    cmd = [hipcc(), *COMMON, *DEVICE_FLAGS, "-c", str(src), "-o", str(obj)]
+    cmd = [hipcc(), *COMMON, *DEVICE_FLAGS, *FILE_FLAGS.get(src.name, []), "-c", str(src),
+           "-o", str(obj)]
     if src.suffix == ".cpp":
         cmd[1:1] = ["-x", "hip"]
     proc = subprocess.run(cmd, capture_output=True, text=True)

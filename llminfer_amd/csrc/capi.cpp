@@ -97,7 +97,98 @@ DeltaKernel select_delta(const GraphDeltaParams &p) {
 
 using namespace llmi;
 
+// normRope / rmsNorm / partialRope as one row shape. Rows per tile (one
+// wave each): enough tiles for about two waves per SIMD (2048 on 256 CUs),
+// but at least 8 rows, since the sequential sum costs the same per tile
+// whatever its row count.
+RopeShape rope_shape(unsigned rows, unsigned heads, unsigned D, unsigned rot,
+                     unsigned stride, unsigned past, unsigned out_row0, float eps,
+                     float theta, bool norm) {
+  unsigned rw = (rows + 2047) / 2048;
+  rw = rw < 8 ? 8 : rw > 64 ? 64 : rw;
+  return RopeShape{rows, heads, D, rot, stride, past, out_row0, eps, theta, norm, rw};
+}
+
+int check_rope(const char *what, uint64_t rows, unsigned heads, unsigned D,
+               unsigned rot, uint64_t in_extent, uint64_t out_rows) {
+  if (rows && heads == 0)
+    return fail(LLMI_HIP_INVALID_ARGUMENT, "%s: heads == 0", what);
+  if (rot % 2 || rot > D)
+    return fail(LLMI_HIP_INVALID_ARGUMENT,
+                "%s: rotary width %u must be even and <= width %u", what, rot, D);
+  if (!fits32(rows, in_extent, 1) || !fits32(out_rows, D, 1))
+    return fail(LLMI_HIP_INVALID_ARGUMENT, "%s: exceeds the 32-bit index range", what);
+  return LLMI_HIP_OK;
+}
+
+int rope_kernel_name_index(const RopeShape &s) {
+  return norm_rope_tiled(s, nullptr, nullptr) ? 0 : 1;
+}
+
 extern "C" {
+
+int llmi_hip_norm_rope(const uint16_t *input, const float *weight, uint16_t *output,
+                       RopeParams p, void *stream) {
+  uint64_t rows = (uint64_t)p.tokens * p.heads;
+  if (rows == 0 || p.headDim == 0)
+    return LLMI_HIP_OK;
+  if (!input || !weight || !output)
+    return fail(LLMI_HIP_INVALID_ARGUMENT, "normRope: null buffer");
+  if (int st = check_rope("normRope", rows, p.heads, p.headDim, p.rotaryDim,
+                          p.headStride > p.headDim ? p.headStride : p.headDim,
+                          ((uint64_t)p.outputStart + p.tokens) * p.heads))
+    return st;
+  if ((uint64_t)p.past + p.tokens > 0xffffffffull)
+    return fail(LLMI_HIP_INVALID_ARGUMENT, "normRope: past + tokens overflows");
+  RopeShape s = rope_shape((unsigned)rows, p.heads, p.headDim, p.rotaryDim, p.headStride,
+                           p.past, p.outputStart * p.heads, p.epsilon, p.theta, true);
+  return launched(launch_norm_rope(input, weight, output, s,
+                                   static_cast<hipStream_t>(stream)),
+                  "normRope");
+}
+
+int llmi_hip_rms_norm(const uint16_t *input, const float *weight, uint16_t *output,
+                      RowParams p, void *stream) {
+  if (p.rows == 0 || p.width == 0)
+    return LLMI_HIP_OK;
+  if (!input || !weight || !output)
+    return fail(LLMI_HIP_INVALID_ARGUMENT, "rmsNorm: null buffer");
+  if (int st = check_rope("rmsNorm", p.rows, 1, p.width, 0, p.width, p.rows))
+    return st;
+  RopeShape s = rope_shape(p.rows, 1, p.width, 0, p.width, 0, 0, p.epsilon, 0.0f, true);
+  return launched(launch_norm_rope(input, weight, output, s,
+                                   static_cast<hipStream_t>(stream)),
+                  "rmsNorm");
+}
+
+int llmi_hip_partial_rope(const uint16_t *input, uint16_t *output, PartialRopeParams p,
+                          void *stream) {
+  if (p.rows == 0 || p.width == 0)
+    return LLMI_HIP_OK;
+  if (!input || !output)
+    return fail(LLMI_HIP_INVALID_ARGUMENT, "partialRope: null buffer");
+  if (int st = check_rope("partialRope", p.rows, p.heads, p.width, p.rotaryWidth,
+                          p.width, p.rows))
+    return st;
+  if ((uint64_t)p.past + p.rows / p.heads > 0xffffffffull)
+    return fail(LLMI_HIP_INVALID_ARGUMENT, "partialRope: past + tokens overflows");
+  RopeShape s = rope_shape(p.rows, p.heads, p.width, p.rotaryWidth, p.width, p.past, 0,
+                           0.0f, p.theta, false);
+  return launched(launch_norm_rope(input, nullptr, output, s,
+                                   static_cast<hipStream_t>(stream)),
+                  "partialRope");
+}
+
+int llmi_hip_sigmoid_mul(const uint16_t *gate, const uint16_t *input, uint16_t *output,
+                         ElementParams p, void *stream) {
+  if (p.count == 0)
+    return LLMI_HIP_OK;
+  if (!gate || !input || !output)
+    return fail(LLMI_HIP_INVALID_ARGUMENT, "sigmoidMul: null buffer");
+  return launched(launch_sigmoid_mul(gate, input, output, p.count,
+                                     static_cast<hipStream_t>(stream)),
+                  "sigmoidMul");
+}
 
 int llmi_hip_cache_append(const uint16_t *src, uint16_t *cache, CacheParams p,
                           void *stream) {
@@ -290,6 +381,20 @@ unsigned llmi_hip_dispatch_count(int op, const void *params) {
       return 0;
     return select_delta(p) == DeltaKernel::Chunked ? delta_chunked_dispatches() : 1;
   }
+  case LLMI_HIP_OP_NORM_ROPE: {
+    const RopeParams &p = *static_cast<const RopeParams *>(params);
+    return p.tokens && p.heads && p.headDim ? 1 : 0;
+  }
+  case LLMI_HIP_OP_RMS_NORM: {
+    const RowParams &p = *static_cast<const RowParams *>(params);
+    return p.rows && p.width ? 1 : 0;
+  }
+  case LLMI_HIP_OP_PARTIAL_ROPE: {
+    const PartialRopeParams &p = *static_cast<const PartialRopeParams *>(params);
+    return p.rows && p.width ? 1 : 0;
+  }
+  case LLMI_HIP_OP_SIGMOID_MUL:
+    return static_cast<const ElementParams *>(params)->count ? 1 : 0;
   }
   return 0;
 }
@@ -327,6 +432,30 @@ const char *llmi_hip_kernel_name(int op, const void *params, unsigned index) {
       return "deltaGeneric";
     }
     return nullptr;
+  // The tile kernels need 16-byte aligned buffers as well; these names
+  // assume them (torch allocations are).
+  case LLMI_HIP_OP_NORM_ROPE: {
+    const RopeParams &p = *static_cast<const RopeParams *>(params);
+    RopeShape s = rope_shape(p.tokens * p.heads, p.heads, p.headDim, p.rotaryDim,
+                             p.headStride, p.past, 0, 0, 0, true);
+    return rope_kernel_name_index(s) == 0 ? "normRopeTile" : "normRopeRows";
+  }
+  case LLMI_HIP_OP_RMS_NORM: {
+    const RowParams &p = *static_cast<const RowParams *>(params);
+    RopeShape s = rope_shape(p.rows, 1, p.width, 0, p.width, 0, 0, 0, 0, true);
+    return rope_kernel_name_index(s) == 0 ? "normRopeTile" : "normRopeRows";
+  }
+  case LLMI_HIP_OP_PARTIAL_ROPE: {
+    const PartialRopeParams &p = *static_cast<const PartialRopeParams *>(params);
+    RopeShape s = rope_shape(p.rows, p.heads, p.width, p.rotaryWidth, p.width, 0, 0, 0,
+                             0, false);
+    return rope_kernel_name_index(s) == 0 ? "partialRopeTile" : "partialRopeRows";
+  }
+  case LLMI_HIP_OP_SIGMOID_MUL:
+    return sigmoid_mul_vectorised(static_cast<const ElementParams *>(params)->count,
+                                  nullptr, nullptr, nullptr)
+               ? "sigmoidMulVec"
+               : "sigmoidMulScalar";
   }
   return nullptr;
 }

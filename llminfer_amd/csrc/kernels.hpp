@@ -74,4 +74,23 @@ hipError_t launch_delta_chunked(const float *q, const float *k,
                                 uint16_t *out, void *ws, const DeltaShape &s,
                                 hipStream_t stream);
 
+// ------------------------------------------------ norm, rope and the gate
+// Rows r < rows of `D` halves at in + r * stride; output row out_row0 + r
+// (dense, D halves); position past + r / heads. norm = false is partialRope
+// (no normalisation, weight unused); rot = 0 is rmsNorm.
+struct RopeShape {
+  unsigned rows, heads, D, rot, stride, past, out_row0;
+  float eps, theta;
+  bool norm;
+  unsigned rows_per_tile; // tile rows per wave (host tuning; 1..64)
+};
+
+bool norm_rope_tiled(const RopeShape &s, const void *in, const void *out);
+hipError_t launch_norm_rope(const uint16_t *in, const float *w, uint16_t *out,
+                            const RopeShape &s, hipStream_t stream);
+
+bool sigmoid_mul_vectorised(unsigned count, const void *g, const void *x, const void *o);
+hipError_t launch_sigmoid_mul(const uint16_t *gate, const uint16_t *in, uint16_t *out,
+                              unsigned count, hipStream_t stream);
+
 } // namespace llmi

@@ -1,0 +1,379 @@
+// The attention block's row work around CausalGqa: the q/k RmsNorm fused with
+// the partial rotary embedding (normRope, Reference.metal:271-293, with
+// rmsScale :98-103 and rotatePair :262-269), its two halves on their own
+// (rmsNorm, Reference.metal:105-117; partialRope, Graph.metal:111-129), and
+// the output gate (sigmoidMul, Graph.metal:78-85).
+//
+// Results are bit for bit those of the reference's expressions, evaluated
+// with IEEE fp32 arithmetic in the reference's order:
+//  * the sum of squares is the reference's sequential fma chain, one lane per
+//    row (the rows are staged through LDS so that HBM reads stay coalesced);
+//  * rsqrt is 1/sqrt, both correctly rounded (the float square root is taken
+//    in double and rounded once, which is exact rounding for a float
+//    argument; HIP's __fsqrt_rn is the native, not always rounded-to-nearest
+//    instruction);
+//  * every rounding of the reference is kept. The file is compiled with
+//    -ffp-contract=off (llminfer_amd/build.py), and each product and each
+//    fp16 rounding passes through opaque(), an empty asm statement: without
+//    it the gfx950 backend selects v_fma_mixlo_f16 for an fp32 product
+//    converted to fp16 (one rounding instead of two, and +0 for a -0
+//    product) and v_fma_mix_f32 for an fp16-rounded product added to
+//    another, whatever the contraction setting.
+//  * pow, cos, sin and exp are the correctly rounded fp32 functions. cos, sin
+//    and exp are used only through their fp16 rounding, so the fast fp32
+//    library function decides whenever every value within 2^-19 relative of
+//    its result rounds to the same fp16 (its error is a few ulp, far inside
+//    that); otherwise, and always for pow, the value is evaluated in double
+//    and rounded to float once.
+//
+// normRope tile kernel: one wave per block owns `rw` consecutive rows.
+//   1. the wave loads the rows' headDim halves with 16-byte coalesced loads
+//      and stores them to LDS (row pitch headDim + 8 halves); meanwhile lanes
+//      evaluate pow(theta, 2i/rotaryDim) per pair;
+//   2. lane r sums row r sequentially from LDS; the lanes fill the
+//      (token, pair) -> (cos, sin) table of the rows' tokens and 1 + w;
+//   3. each lane takes 16-byte output chunks of consecutive columns, reads
+//      the chunk and, in the rotary part, the partner chunk (column +-
+//      rotaryDim/2) from LDS, normalises, rotates and stores 16 bytes.
+// Shapes outside the tile kernel's alignment rules (headDim, headStride or
+// rotaryDim/2 not a multiple of 8 halves, unaligned pointers, headDim > 2048)
+// run the row kernel: one thread per row, the reference's own structure,
+// with the same arithmetic.
+#include "hip_common.hpp"
+#include "kernels.hpp"
+
+
+namespace llmi {
+namespace {
+
+constexpr int kPad = 8;                 // halves of LDS padding per tile row
+constexpr unsigned kTileHalves = 16384; // rows * headDim bound of one tile
+constexpr unsigned kTileIters = kTileHalves / 8 / 64;
+
+__device__ __forceinline__ float h2f(uint16_t b) {
+  return (float)__builtin_bit_cast(half_t, b);
+}
+__device__ __forceinline__ uint16_t f2h(float x) {
+  return __builtin_bit_cast(uint16_t, (half_t)x);
+}
+// The value, hidden from the optimiser, so that the operation producing it
+// is selected as written and rounded on its own.
+__device__ __forceinline__ float opaque(float x) {
+  asm volatile("" : "+v"(x));
+  return x;
+}
+__device__ __forceinline__ float mul32(float a, float b) { return opaque(a * b); }
+__device__ __forceinline__ float round16(float x) { return opaque((float)(half_t)x); }
+
+// True when every float within 2^-19 relative of v has the same fp16
+// rounding as v (fp16 rounding is monotonic, so the two ends decide).
+__device__ __forceinline__ bool f16_settled(float v) {
+  half_t a = (half_t)__fmul_rn(v, 1.0f - 0x1p-19f);
+  half_t b = (half_t)__fmul_rn(v, 1.0f + 0x1p-19f);
+  return __builtin_bit_cast(uint16_t, a) == __builtin_bit_cast(uint16_t, b);
+}
+
+// fp16(cos(phase)), fp16(sin(phase)) of the correctly rounded fp32 values.
+__device__ __forceinline__ float2 rope_cos_sin(float phase) {
+  float s, c;
+  sincosf(phase, &s, &c);
+  if (!(f16_settled(c) && f16_settled(s))) {
+    double sd, cd;
+    sincos((double)phase, &sd, &cd);
+    c = (float)cd;
+    s = (float)sd;
+  }
+  return make_float2(round16(c), round16(s));
+}
+
+// pow(theta, 2 * pair / rotaryDim) correctly rounded to fp32.
+__device__ __forceinline__ float rope_inv_freq(float theta, unsigned pair,
+                                               unsigned rot) {
+  float e = __fdiv_rn(2.0f * (float)pair, (float)rot);
+  return (float)pow((double)theta, (double)e);
+}
+
+__device__ __forceinline__ float rms_scale_of(float sum, unsigned width, float eps) {
+  float m = __fadd_rn(__fdiv_rn(sum, (float)width), eps);
+  return __fdiv_rn(1.0f, (float)__builtin_sqrt((double)m));
+}
+
+__device__ __forceinline__ float normed(uint16_t v, float scale, float w1) {
+  return round16(mul32(mul32(h2f(v), scale), w1));
+}
+
+// rotatePair on fp16 values x, y (held in floats) and fp16 cos/sin.
+__device__ __forceinline__ uint16_t rotate_x(float x, float y, float2 cs) {
+  return f2h(opaque(round16(mul32(x, cs.x)) - round16(mul32(y, cs.y))));
+}
+__device__ __forceinline__ uint16_t rotate_y(float x, float y, float2 cs) {
+  return f2h(opaque(round16(mul32(y, cs.x)) + round16(mul32(x, cs.y))));
+}
+
+struct TileArgs {
+  unsigned rows, heads, D, rot, stride, past, out_row0, rw, maxtok;
+  float eps, theta;
+};
+
+template <bool kNorm>
+__global__ __launch_bounds__(64) void norm_rope_tile(const uint16_t *in,
+                                                     const float *__restrict__ w,
+                                                     uint16_t *out, TileArgs a) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  const unsigned lane = threadIdx.x;
+  const unsigned pitch = a.D + kPad;
+  const unsigned half = a.rot / 2;
+  uint16_t *tile = reinterpret_cast<uint16_t *>(smem);
+  float *sc = reinterpret_cast<float *>(tile + a.rw * pitch);
+  float *wt1 = sc + ((a.rw + 1) & ~1u);
+  float *invf = wt1 + (kNorm ? a.D : 0);
+  float2 *cs = reinterpret_cast<float2 *>(invf + ((half + 1) & ~1u));
+
+  const unsigned row0 = blockIdx.x * a.rw;
+  const unsigned nrows = min(a.rw, a.rows - row0);
+  const unsigned cpr = a.D / 8; // 16-byte chunks per row
+  const unsigned chunks = nrows * cpr;
+
+  // 1. coalesced loads of the tile; pow per pair while they are in flight.
+  uint4_t v[kTileIters];
+#pragma unroll
+  for (unsigned it = 0; it < kTileIters; ++it) {
+    unsigned c = it * 64 + lane;
+    unsigned r = c / cpr, col = c - r * cpr;
+    if (c < chunks)
+      v[it] = *reinterpret_cast<const uint4_t *>(
+          in + (size_t)(row0 + r) * a.stride + col * 8);
+  }
+  for (unsigned i = lane; i < half; i += 64)
+    invf[i] = rope_inv_freq(a.theta, i, a.rot);
+  if (kNorm)
+    for (unsigned i = lane; i < a.D; i += 64)
+      wt1[i] = 1.0f + w[i];
+#pragma unroll
+  for (unsigned it = 0; it < kTileIters; ++it) {
+    unsigned c = it * 64 + lane;
+    unsigned r = c / cpr, col = c - r * cpr;
+    if (c < chunks)
+      *reinterpret_cast<uint4_t *>(tile + r * pitch + col * 8) = v[it];
+  }
+  __syncthreads();
+
+  // 2. sequential sums (lane = row) and the cos/sin table.
+  if (kNorm && lane < nrows) {
+    const uint16_t *row = tile + lane * pitch;
+    float sum = 0.0f;
+    for (unsigned k = 0; k < cpr; ++k) {
+      uint4_t q = *reinterpret_cast<const uint4_t *>(row + 8 * k);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        float lo = h2f((uint16_t)(q[e] & 0xFFFFu));
+        float hi = h2f((uint16_t)(q[e] >> 16));
+        sum = __builtin_fmaf(lo, lo, sum);
+        sum = __builtin_fmaf(hi, hi, sum);
+      }
+    }
+    sc[lane] = rms_scale_of(sum, a.D, a.eps);
+  }
+  const unsigned tok0 = row0 / a.heads;
+  const unsigned ntok = (row0 + nrows - 1) / a.heads - tok0 + 1;
+  for (unsigned e = lane; e < ntok * half; e += 64) {
+    unsigned t = e / half, i = e - t * half;
+    float position = (float)(a.past + tok0 + t);
+    cs[e] = rope_cos_sin(__fdiv_rn(position, invf[i]));
+  }
+  __syncthreads();
+
+  // 3. normalise, rotate, store.
+  for (unsigned c = lane; c < chunks; c += 64) {
+    unsigned r = c / cpr, col = c - r * cpr, j0 = col * 8;
+    const uint16_t *mine = tile + r * pitch + j0;
+    uint4_t q = *reinterpret_cast<const uint4_t *>(mine);
+    float scale = kNorm ? sc[r] : 1.0f;
+    uint16_t o[8];
+    float x[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      uint16_t b = (uint16_t)(q[e / 2] >> (16 * (e & 1)));
+      x[e] = kNorm ? normed(b, scale, wt1[j0 + e]) : h2f(b);
+      o[e] = f2h(x[e]);
+    }
+    if (j0 < a.rot) {
+      bool first = j0 < half;
+      unsigned pj = first ? j0 + half : j0 - half;
+      uint4_t p = *reinterpret_cast<const uint4_t *>(tile + r * pitch + pj);
+      unsigned pair0 = first ? j0 : pj;
+      const float2 *csr = cs + ((row0 + r) / a.heads - tok0) * half + pair0;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        uint16_t b = (uint16_t)(p[e / 2] >> (16 * (e & 1)));
+        float y = kNorm ? normed(b, scale, wt1[pj + e]) : h2f(b);
+        float2 t = csr[e];
+        o[e] = first ? rotate_x(x[e], y, t) : rotate_y(y, x[e], t);
+      }
+    }
+    uint4_t st;
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      st[e] = (uint32_t)o[2 * e] | ((uint32_t)o[2 * e + 1] << 16);
+    *reinterpret_cast<uint4_t *>(out + (size_t)(a.out_row0 + row0 + r) * a.D + j0) = st;
+  }
+}
+
+// One thread per row: the reference kernel's structure, for any alignment.
+template <bool kNorm>
+__global__ __launch_bounds__(256) void norm_rope_rows(const uint16_t *in,
+                                                      const float *__restrict__ w,
+                                                      uint16_t *out, TileArgs a) {
+  unsigned row = blockIdx.x * 256 + threadIdx.x;
+  if (row >= a.rows)
+    return;
+  const uint16_t *head = in + (size_t)row * a.stride;
+  uint16_t *dst = out + (size_t)(a.out_row0 + row) * a.D;
+  float scale = 1.0f;
+  if (kNorm) {
+    float sum = 0.0f;
+    for (unsigned i = 0; i < a.D; ++i) {
+      float f = h2f(head[i]);
+      sum = __builtin_fmaf(f, f, sum);
+    }
+    scale = rms_scale_of(sum, a.D, a.eps);
+  }
+  unsigned half = a.rot / 2;
+  float position = (float)(a.past + row / a.heads);
+  for (unsigned i = 0; i < half; ++i) {
+    unsigned j = i + half;
+    float x = kNorm ? normed(head[i], scale, 1.0f + w[i]) : h2f(head[i]);
+    float y = kNorm ? normed(head[j], scale, 1.0f + w[j]) : h2f(head[j]);
+    float2 t = rope_cos_sin(__fdiv_rn(position, rope_inv_freq(a.theta, i, a.rot)));
+    uint16_t ox = rotate_x(x, y, t), oy = rotate_y(x, y, t);
+    dst[i] = ox;
+    dst[j] = oy;
+  }
+  for (unsigned i = a.rot; i < a.D; ++i)
+    dst[i] = kNorm ? f2h(normed(head[i], scale, 1.0f + w[i])) : head[i];
+}
+
+// fp16(logistic(g)) of the correctly rounded fp32 exp.
+__device__ __forceinline__ float logistic16(float g) {
+  float s = __fdiv_rn(1.0f, __fadd_rn(1.0f, expf(-g)));
+  if (!f16_settled(s))
+    s = __fdiv_rn(1.0f, __fadd_rn(1.0f, (float)exp(-(double)g)));
+  return round16(s);
+}
+
+__device__ __forceinline__ uint16_t gate_one(uint16_t g, uint16_t x) {
+  return f2h(mul32(logistic16(h2f(g)), h2f(x)));
+}
+
+__global__ __launch_bounds__(256) void sigmoid_mul_vec(const uint4_t *__restrict__ gate,
+                                                       const uint4_t *__restrict__ in,
+                                                       uint4_t *__restrict__ out,
+                                                       unsigned vectors) {
+  unsigned i = blockIdx.x * 256 + threadIdx.x;
+  if (i >= vectors)
+    return;
+  uint4_t g = __builtin_nontemporal_load(gate + i);
+  uint4_t x = __builtin_nontemporal_load(in + i);
+  uint4_t o;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    uint16_t lo = gate_one((uint16_t)(g[e] & 0xFFFFu), (uint16_t)(x[e] & 0xFFFFu));
+    uint16_t hi = gate_one((uint16_t)(g[e] >> 16), (uint16_t)(x[e] >> 16));
+    o[e] = (uint32_t)lo | ((uint32_t)hi << 16);
+  }
+  __builtin_nontemporal_store(o, out + i);
+}
+
+__global__ __launch_bounds__(256) void sigmoid_mul_scalar(const uint16_t *__restrict__ gate,
+                                                          const uint16_t *__restrict__ in,
+                                                          uint16_t *__restrict__ out,
+                                                          unsigned count) {
+  unsigned i = blockIdx.x * 256 + threadIdx.x;
+  if (i < count)
+    out[i] = gate_one(gate[i], in[i]);
+}
+
+bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// Rows per tile and the table bound for a shape the tile kernel takes.
+struct TilePlan {
+  unsigned rw, maxtok;
+  size_t lds;
+};
+
+TilePlan plan_tile(const RopeShape &s) {
+  unsigned rw = kTileHalves / s.D;
+  rw = rw > s.rows_per_tile ? s.rows_per_tile : rw;
+  rw = rw < 1 ? 1 : rw;
+  TilePlan p{};
+  const unsigned half = s.rot / 2;
+  for (;;) {
+    p.rw = rw;
+    p.maxtok = (rw - 1) / s.heads + 2;
+    if (p.maxtok > rw)
+      p.maxtok = rw;
+    size_t table = (size_t)p.maxtok * half * sizeof(float2);
+    if (rw <= 8 || table <= 16384)
+      break;
+    rw /= 2;
+  }
+  p.lds = (size_t)p.rw * (s.D + kPad) * 2 + (size_t)((p.rw + 1) & ~1u) * 4 +
+          (s.norm ? (size_t)s.D * 4 : 0) + (size_t)((half + 1) & ~1u) * 4 +
+          (size_t)p.maxtok * half * sizeof(float2);
+  return p;
+}
+
+} // namespace
+
+bool norm_rope_tiled(const RopeShape &s, const void *in, const void *out) {
+  return s.D % 8 == 0 && s.D <= 2048 && s.stride % 8 == 0 && (s.rot / 2) % 8 == 0 &&
+         aligned16(in) && aligned16(out);
+}
+
+hipError_t launch_norm_rope(const uint16_t *in, const float *w, uint16_t *out,
+                            const RopeShape &s, hipStream_t stream) {
+  if (s.rows == 0 || s.D == 0)
+    return hipSuccess;
+  TileArgs a{s.rows, s.heads, s.D, s.rot, s.stride, s.past, s.out_row0, 0, 0,
+             s.eps, s.theta};
+  if (norm_rope_tiled(s, in, out)) {
+    TilePlan p = plan_tile(s);
+    a.rw = p.rw;
+    a.maxtok = p.maxtok;
+    dim3 grid((s.rows + p.rw - 1) / p.rw);
+    if (s.norm)
+      hipLaunchKernelGGL(norm_rope_tile<true>, grid, dim3(64), p.lds, stream, in, w, out, a);
+    else
+      hipLaunchKernelGGL(norm_rope_tile<false>, grid, dim3(64), p.lds, stream, in, w, out, a);
+  } else {
+    dim3 grid((s.rows + 255) / 256);
+    if (s.norm)
+      hipLaunchKernelGGL(norm_rope_rows<true>, grid, dim3(256), 0, stream, in, w, out, a);
+    else
+      hipLaunchKernelGGL(norm_rope_rows<false>, grid, dim3(256), 0, stream, in, w, out, a);
+  }
+  return hipGetLastError();
+}
+
+bool sigmoid_mul_vectorised(unsigned count, const void *g, const void *x, const void *o) {
+  return count % 8 == 0 && aligned16(g) && aligned16(x) && aligned16(o);
+}
+
+hipError_t launch_sigmoid_mul(const uint16_t *gate, const uint16_t *in, uint16_t *out,
+                              unsigned count, hipStream_t stream) {
+  if (count == 0)
+    return hipSuccess;
+  if (sigmoid_mul_vectorised(count, gate, in, out)) {
+    unsigned vectors = count / 8;
+    hipLaunchKernelGGL(sigmoid_mul_vec, dim3((vectors + 255) / 256), dim3(256), 0, stream,
+                       reinterpret_cast<const uint4_t *>(gate),
+                       reinterpret_cast<const uint4_t *>(in),
+                       reinterpret_cast<uint4_t *>(out), vectors);
+  } else {
+    hipLaunchKernelGGL(sigmoid_mul_scalar, dim3((count + 255) / 256), dim3(256), 0, stream,
+                       gate, in, out, count);
+  }
+  return hipGetLastError();
+}
+
+} // namespace llmi

@@ -61,6 +61,64 @@ def cache_append(src: torch.Tensor, cache: torch.Tensor, offset: int) -> None:
                                          _lib.CacheParams(src.numel(), offset), _stream()))
 
 
+def norm_rope(x: torch.Tensor, weight: torch.Tensor, out: torch.Tensor, past: int,
+              rotary_dim: int, epsilon: float = 1e-6, theta: float = 1e7,
+              head_dim: int | None = None, output_start: int = 0) -> None:
+    """normRope (Reference.metal:271-293): x [T, H, stride] fp16 (the first
+    head_dim halves of each head are read; stride = 2 * head_dim for the
+    projected q with its gate), weight [head_dim] fp32, out [>= output_start
+    + T, H, head_dim] fp16, rows written from output_start (the key cache
+    with output_start = past)."""
+    _require(x, torch.float16, "x")
+    _require(weight, torch.float32, "weight")
+    _require(out, torch.float16, "out")
+    if x.dim() != 3 or out.dim() != 3 or out.shape[1] != x.shape[1]:
+        raise ValueError("x is [T, H, stride] and out [rows, H, head_dim]")
+    T, H, stride = x.shape
+    d = out.shape[2] if head_dim is None else head_dim
+    if d != out.shape[2] or d > stride or weight.numel() != d:
+        raise ValueError("head_dim must match out and weight and fit the stride")
+    if output_start + T > out.shape[0]:
+        raise ValueError("output rows exceed out")
+    p = _lib.RopeParams(T, H, d, rotary_dim, stride, past, output_start, epsilon, theta)
+    _lib.check(_lib.load().llmi_hip_norm_rope(_ptr(x), _ptr(weight), _ptr(out), p, _stream()))
+
+
+def rms_norm(x: torch.Tensor, weight: torch.Tensor, out: torch.Tensor,
+             epsilon: float = 1e-6) -> None:
+    """rmsNorm (Reference.metal:105-117) over the last dimension."""
+    for t, n in ((x, "x"), (out, "out")):
+        _require(t, torch.float16, n)
+    _require(weight, torch.float32, "weight")
+    if x.shape != out.shape or weight.numel() != x.shape[-1]:
+        raise ValueError("x, out and weight shapes disagree")
+    width = x.shape[-1]
+    p = _lib.RowParams(x.numel() // max(width, 1), width, epsilon)
+    _lib.check(_lib.load().llmi_hip_rms_norm(_ptr(x), _ptr(weight), _ptr(out), p, _stream()))
+
+
+def partial_rope(x: torch.Tensor, out: torch.Tensor, past: int, rotary_dim: int,
+                 theta: float = 1e7) -> None:
+    """partialRope (Graph.metal:111-129): x, out [T, H, width] fp16."""
+    for t, n in ((x, "x"), (out, "out")):
+        _require(t, torch.float16, n)
+    if x.shape != out.shape or x.dim() != 3:
+        raise ValueError("x and out are [T, H, width]")
+    T, H, width = x.shape
+    p = _lib.PartialRopeParams(T * H, H, width, rotary_dim, past, theta)
+    _lib.check(_lib.load().llmi_hip_partial_rope(_ptr(x), _ptr(out), p, _stream()))
+
+
+def sigmoid_mul(gate: torch.Tensor, x: torch.Tensor, out: torch.Tensor) -> None:
+    """sigmoidMul (Graph.metal:78-85): out = fp16(fp16(sigmoid(gate)) * x)."""
+    for t, n in ((gate, "gate"), (x, "x"), (out, "out")):
+        _require(t, torch.float16, n)
+    if gate.numel() != x.numel() or out.numel() != x.numel():
+        raise ValueError("gate, x and out must have the same size")
+    p = _lib.ElementParams(x.numel())
+    _lib.check(_lib.load().llmi_hip_sigmoid_mul(_ptr(gate), _ptr(x), _ptr(out), p, _stream()))
+
+
 def kv_append(k: torch.Tensor, v: torch.Tensor, k_cache: torch.Tensor,
               v_cache: torch.Tensor, past: int) -> None:
     """KvAppend: rows [past, past+T) of both caches <- k, v ([T, Hkv, d])."""

@@ -71,6 +71,8 @@ def lib() -> C.CDLL:
                                             _f64p, C.c_void_p] + [_u32] * 6
         L.orc_delta_gates.argtypes = [_u16p, _u16p, _f32p, _f32p, _f32p, _f32p, _u32, _u32]
         L.orc_l2norm_f32.argtypes = [_u16p, _f32p, _u32, _u32, C.c_float, C.c_float]
+        L.orc_norm_rope.argtypes = [_u16p, _f32p, _u16p] + [_u32] * 7 + [C.c_float, C.c_float]
+        L.orc_sigmoid_mul.argtypes = [_u16p, _u16p, _u16p, C.c_size_t]
         for name, n in (("orc_cost_kv_append", 3), ("orc_cost_causal_gqa", 5),
                         ("orc_cost_delta_update", 5)):
             fn = getattr(L, name)
@@ -220,6 +222,30 @@ def delta_gates(a, b, a_log, dt_bias):
                           np.ascontiguousarray(a_log, np.float32),
                           np.ascontiguousarray(dt_bias, np.float32), beta, decay, T, hv)
     return beta, decay
+
+
+def norm_rope(x, weight, tokens: int, heads: int, head_dim: int, rotary_dim: int,
+              head_stride: int, past: int, epsilon: float = 1e-6, theta: float = 1e7,
+              output=None, output_start: int = 0) -> np.ndarray:
+    """normRope (Reference.metal:271-293) on fp16 bits; returns the output rows
+    (a new [tokens*heads, head_dim] array, or `output` written from row
+    output_start * heads)."""
+    a = np.ascontiguousarray(x, np.uint16).reshape(-1)
+    w = np.ascontiguousarray(weight, np.float32)
+    if output is None:
+        output = np.zeros(((output_start + tokens) * heads, head_dim), np.uint16)
+    lib().orc_norm_rope(a, w, output.reshape(-1), tokens, heads, head_dim, rotary_dim,
+                        head_stride, past, output_start, epsilon, theta)
+    return output
+
+
+def sigmoid_mul(gate, x) -> np.ndarray:
+    """sigmoidMul (Graph.metal:78-85) on fp16 bits."""
+    g = np.ascontiguousarray(gate, np.uint16)
+    a = np.ascontiguousarray(x, np.uint16)
+    out = np.empty(a.shape, np.uint16)
+    lib().orc_sigmoid_mul(g.reshape(-1), a.reshape(-1), out.reshape(-1), a.size)
+    return out
 
 
 def l2norm_f32(x, width: int, eps: float = 1e-6, scale: float = 1.0) -> np.ndarray:

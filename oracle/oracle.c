@@ -651,6 +651,72 @@ void orc_l2norm_f32(const uint16_t *in, float *out, uint32_t rows,
   }
 }
 
+/* ---------------------------------------------------- norm, rope, gate */
+
+static float orc_round_f16(float x) { return orc_f16_to_f32(orc_f32_to_f16(x)); }
+
+/* rmsScale, Reference.metal:98-103: fma-accumulated sum of squares in index
+ * order, rsqrt(sum / width + eps). */
+static float orc_rms_scale(const uint16_t *x, uint32_t width, float eps) {
+  float sum = 0.0f;
+  for (uint32_t i = 0; i < width; ++i) {
+    float f = orc_f16_to_f32(x[i]);
+    sum = fmaf(f, f, sum);
+  }
+  return 1.0f / sqrtf(sum / (float)width + eps);
+}
+
+/* The fp32 pow/cos/sin/exp of the reference kernels, taken correctly
+ * rounded: evaluated in double and rounded to float once. The device kernels
+ * produce the same float (a fast fp32 evaluation with a margin test, else the
+ * same double evaluation), so results compare bit for bit. */
+static float orc_powf_cr(float x, float y) { return (float)pow((double)x, (double)y); }
+static float orc_cosf_cr(float x) { return (float)cos((double)x); }
+static float orc_sinf_cr(float x) { return (float)sin((double)x); }
+static float orc_expf_cr(float x) { return (float)exp((double)x); }
+
+/* rotatePair, Reference.metal:262-269. */
+static void orc_rotate_pair(float in_x, float in_y, float position, float theta,
+                            uint32_t pair, uint32_t rotary_width, uint16_t *out_x,
+                            uint16_t *out_y) {
+  float phase = position / orc_powf_cr(theta, 2.0f * (float)pair / (float)rotary_width);
+  float cosine = orc_round_f16(orc_cosf_cr(phase));
+  float sine = orc_round_f16(orc_sinf_cr(phase));
+  *out_x = orc_f32_to_f16(orc_round_f16(in_x * cosine) - orc_round_f16(in_y * sine));
+  *out_y = orc_f32_to_f16(orc_round_f16(in_y * cosine) + orc_round_f16(in_x * sine));
+}
+
+/* normRope, Reference.metal:271-293. */
+void orc_norm_rope(const uint16_t *input, const float *weight, uint16_t *output,
+                   uint32_t tokens, uint32_t heads, uint32_t head_dim,
+                   uint32_t rotary_dim, uint32_t head_stride, uint32_t past,
+                   uint32_t output_start, float epsilon, float theta) {
+  uint32_t rows = tokens * heads, half = rotary_dim / 2;
+  for (uint32_t row = 0; row < rows; ++row) {
+    const uint16_t *head = input + (size_t)row * head_stride;
+    uint16_t *out = output + ((size_t)output_start * heads + row) * head_dim;
+    float scale = orc_rms_scale(head, head_dim, epsilon);
+    float position = (float)(past + row / heads);
+    for (uint32_t i = 0; i < half; ++i) {
+      uint32_t j = i + half;
+      float x = orc_round_f16(orc_f16_to_f32(head[i]) * scale * (1.0f + weight[i]));
+      float y = orc_round_f16(orc_f16_to_f32(head[j]) * scale * (1.0f + weight[j]));
+      orc_rotate_pair(x, y, position, theta, i, rotary_dim, &out[i], &out[j]);
+    }
+    for (uint32_t i = rotary_dim; i < head_dim; ++i)
+      out[i] = orc_f32_to_f16(orc_f16_to_f32(head[i]) * scale * (1.0f + weight[i]));
+  }
+}
+
+/* sigmoidMul, Graph.metal:78-85 with logistic, Reference.metal:4. */
+void orc_sigmoid_mul(const uint16_t *gate, const uint16_t *input, uint16_t *output,
+                     size_t count) {
+  for (size_t i = 0; i < count; ++i) {
+    float g = orc_round_f16(1.0f / (1.0f + orc_expf_cr(-orc_f16_to_f32(gate[i]))));
+    output[i] = orc_f32_to_f16(g * orc_f16_to_f32(input[i]));
+  }
+}
+
 /* ------------------------------------------------------------------ cost */
 
 static int mul_ok(uint64_t a, uint64_t b, uint64_t *r) {

@@ -131,6 +131,27 @@ void orc_delta_gates(const uint16_t *a, const uint16_t *b, const float *a_log,
 void orc_l2norm_f32(const uint16_t *in, float *out, uint32_t rows,
                     uint32_t width, float eps, float scale);
 
+/* Fused q/k RmsNorm + PartialRoPE of the reference graph, normRope
+ * (lib/Backend/Metal/Kernels/Reference.metal:271-293 with rmsScale :98-103
+ * and rotatePair :262-269; RopeParams, ReferenceParams.h:44-47). Row r of
+ * `tokens * heads` reads `headDim` halves at input + r * headStride and
+ * writes output + (outputStart * heads + r) * headDim; position =
+ * past + r / heads. Same rounding points as the kernel: the normalised
+ * value is rounded to fp16 before the rotation, cos/sin are rounded to fp16,
+ * each product is rounded to fp16 before the sum. rsqrt is 1/sqrtf (two
+ * correctly rounded steps); pow/cos/sin are the correctly rounded fp32
+ * functions (evaluated in double, rounded once). */
+void orc_norm_rope(const uint16_t *input, const float *weight, uint16_t *output,
+                   uint32_t tokens, uint32_t heads, uint32_t head_dim,
+                   uint32_t rotary_dim, uint32_t head_stride, uint32_t past,
+                   uint32_t output_start, float epsilon, float theta);
+
+/* sigmoidMul (lib/Backend/Metal/Kernels/Graph.metal:78-85, logistic
+ * Reference.metal:4): out = fp16(fp16(1 / (1 + exp(-gate))) * input), exp
+ * correctly rounded to fp32. */
+void orc_sigmoid_mul(const uint16_t *gate, const uint16_t *input, uint16_t *output,
+                     size_t count);
+
 /* Cost model of lib/GraphIR/Cost.cpp:180-201 (MACs) and :56-94 (bytes) for
  * the three hot ops. Returns 0 on success, -1 on overflow. */
 typedef struct {

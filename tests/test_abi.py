@@ -50,6 +50,63 @@ def test_param_structs_match_reference_layout():
         ["tokens", "keyHeads", "keyDim", "valueHeads", "valueDim"]
 
 
+def test_row_param_structs_match_reference_layout():
+    # ReferenceParams.h:23-30, :44-47; GraphParams.h:35-38.
+    assert C.sizeof(_lib.RowParams) == 12
+    assert C.sizeof(_lib.ElementParams) == 4
+    assert C.sizeof(_lib.RopeParams) == 36
+    assert C.sizeof(_lib.PartialRopeParams) == 24
+    assert [f[0] for f in _lib.RopeParams._fields_] == \
+        ["tokens", "heads", "headDim", "rotaryDim", "headStride", "past", "outputStart",
+         "epsilon", "theta"]
+    assert [f[0] for f in _lib.PartialRopeParams._fields_] == \
+        ["rows", "heads", "width", "rotaryWidth", "past", "theta"]
+
+
+def test_invalid_rope_rejected_before_launch():
+    lib = _lib.load()
+    for p in (_lib.RopeParams(2, 4, 256, 63, 256, 0, 0, 1e-6, 1e7),    # odd rotary
+              _lib.RopeParams(2, 4, 64, 128, 64, 0, 0, 1e-6, 1e7),     # rotary > width
+              _lib.RopeParams(1 << 16, 16, 256, 64, 8192, 0, 0, 1e-6, 1e7)):  # > 32-bit
+        assert lib.llmi_hip_norm_rope(1, 1, 1, p, None) == _lib.INVALID_ARGUMENT
+        assert lib.llmi_hip_last_error()
+    p = _lib.RopeParams(2, 4, 256, 64, 512, 0, 0, 1e-6, 1e7)
+    assert lib.llmi_hip_norm_rope(None, 1, 1, p, None) == _lib.INVALID_ARGUMENT
+    assert lib.llmi_hip_norm_rope(1, None, 1, p, None) == _lib.INVALID_ARGUMENT
+    # empty shapes launch nothing and succeed
+    for q in (_lib.RopeParams(0, 4, 256, 64, 512, 0, 0, 1e-6, 1e7),
+              _lib.RopeParams(3, 0, 256, 64, 512, 0, 0, 1e-6, 1e7)):
+        assert lib.llmi_hip_norm_rope(None, None, None, q, None) == _lib.OK
+        assert lib.llmi_hip_dispatch_count(_lib.OP_NORM_ROPE, C.byref(q)) == 0
+    assert lib.llmi_hip_partial_rope(1, 1, _lib.PartialRopeParams(4, 0, 64, 16, 0, 1e4),
+                                     None) == _lib.INVALID_ARGUMENT
+    assert lib.llmi_hip_partial_rope(1, 1, _lib.PartialRopeParams(4, 2, 64, 15, 0, 1e4),
+                                     None) == _lib.INVALID_ARGUMENT
+    assert lib.llmi_hip_rms_norm(None, 1, 1, _lib.RowParams(4, 64, 1e-6), None) == \
+        _lib.INVALID_ARGUMENT
+    assert lib.llmi_hip_sigmoid_mul(1, None, 1, _lib.ElementParams(8), None) == \
+        _lib.INVALID_ARGUMENT
+    assert lib.llmi_hip_sigmoid_mul(None, None, None, _lib.ElementParams(0), None) == _lib.OK
+
+
+def test_plan_records_row_ops():
+    from llminfer_amd import ops
+    assert ops.kernel_names(_lib.OP_NORM_ROPE,
+                            _lib.RopeParams(2048, 16, 256, 64, 512, 0, 0, 1e-6, 1e7)) == \
+        ["normRopeTile"]
+    assert ops.kernel_names(_lib.OP_NORM_ROPE,
+                            _lib.RopeParams(3, 2, 100, 36, 100, 0, 0, 1e-6, 1e7)) == \
+        ["normRopeRows"]
+    assert ops.kernel_names(_lib.OP_RMS_NORM, _lib.RowParams(7, 4096, 1e-6)) == \
+        ["normRopeRows"]
+    assert ops.kernel_names(_lib.OP_PARTIAL_ROPE,
+                            _lib.PartialRopeParams(64, 16, 256, 64, 3, 1e7)) == \
+        ["partialRopeTile"]
+    assert ops.kernel_names(_lib.OP_SIGMOID_MUL, _lib.ElementParams(4096)) == ["sigmoidMulVec"]
+    assert ops.kernel_names(_lib.OP_SIGMOID_MUL, _lib.ElementParams(4097)) == \
+        ["sigmoidMulScalar"]
+
+
 def test_invalid_gqa_rejected_before_launch():
     lib = _lib.load()
     bad = [_lib.GqaParams(0, 16, 4, 256, 0),     # no tokens
