@@ -94,6 +94,15 @@ def delta_bytes(T: int, hk: int, dk: int, hv: int, dv: int) -> int:
             + 8 * hv * dk * dv + 2 * T * hv * dv)
 
 
+def rows_bytes(T: int, hq: int, hkv: int, d: int) -> dict:
+    """Algorithmic HBM bytes of the attention block's row ops per call: each
+    reads its fp16 input rows once and writes its output rows once (the
+    gate half of the projected q is not read; the weights are 1 KB)."""
+    return {"q_norm_rope": 2 * T * hq * d * 2 + d * 4,
+            "k_norm_rope": 2 * T * hkv * d * 2 + d * 4,
+            "gate": 3 * T * hq * d * 2}
+
+
 def cpu_threads() -> int:
     import oracle
     return max(1, min(CPU_THREAD_CAP, oracle.cpu_count()))
@@ -301,6 +310,89 @@ class GqaPrefill(Workload):
                 "sample": f"{rows} query rows [{t0}, {t0 + rows}) of {self.T} "
                           f"(mean visible length = the chunk's), x{scale:g}, {runs} runs",
                 "gpu_vs_cpu_max_abs": err}
+
+
+class AttnRows(Workload):
+    """The attention block's row work on either side of CausalGqa
+    (Qwen35ModelBuilder.cpp:175-197, lowered as MetalReferenceGraph.mm:307-330):
+    q RmsNorm + PartialRoPE from the projected q with its gate interleaved
+    (stride 2 * head_dim), k RmsNorm + PartialRoPE written straight into the
+    key cache at row `past`, and the sigmoidMul output gate. Inputs rotate
+    over independent sets larger than the MALL."""
+    bound = "hbm"
+    labels = ("q_norm_rope", "k_norm_rope", "gate")
+    dominant = "q_norm_rope"
+
+    def __init__(self, dev, T, past, sets, seed, hq=16, hkv=4, d=256, rot=64):
+        import torch
+        from llminfer_amd import ops
+        self.T, self.P, self.sets, self.hq, self.hkv, self.d, self.rot = T, past, sets, hq, hkv, d, rot
+        self.tokens = T
+        self.name = f"attn_rows_T{T}"
+        g = torch.Generator(device=dev).manual_seed(seed)
+        self.qg = [_randn16(g, (T, hq, 2 * d), dev) for _ in range(sets)]
+        self.k = [_randn16(g, (T, hkv, d), dev) for _ in range(sets)]
+        self.attn = [_randn16(g, (T, hq, d), dev) for _ in range(sets)]
+        self.qw = (0.2 * torch.randn(d, generator=g, device=dev)).float()
+        self.kw = (0.2 * torch.randn(d, generator=g, device=dev)).float()
+        self.qout = [torch.empty(T, hq, d, dtype=torch.float16, device=dev) for _ in range(sets)]
+        self.out = [torch.empty(T, hq, d, dtype=torch.float16, device=dev) for _ in range(sets)]
+        self.kc = torch.zeros(past + T, hkv, d, dtype=torch.float16, device=dev)
+        # the gate is the second half of each projected q head, made dense
+        self.gate = [x[:, :, d:].contiguous() for x in self.qg]
+        self.bound_ops = {
+            "q_norm_rope": [ops.bind_norm_rope(self.qg[s], self.qw, self.qout[s], past, rot,
+                                               head_dim=d) for s in range(sets)],
+            "k_norm_rope": [ops.bind_norm_rope(self.k[s], self.kw, self.kc, past, rot,
+                                               output_start=past) for s in range(sets)],
+            "gate": [ops.bind_sigmoid_mul(self.gate[s], self.attn[s], self.out[s])
+                     for s in range(sets)],
+        }
+        self.bytes = rows_bytes(T, hq, hkv, d)
+
+    def op(self, label, i):
+        self.bound_ops[label][i % self.sets]()
+
+    def kernels(self):
+        return self.bound_ops["q_norm_rope"][0].what
+
+    def work(self, i):
+        return self.bytes["q_norm_rope"]
+
+    def config(self):
+        return {"workload": self.name, "tokens": self.T, "past": self.P,
+                "query_heads": self.hq, "kv_heads": self.hkv, "head_dim": self.d,
+                "rotary_dim": self.rot, "theta": 1e7, "epsilon": 1e-6, "sets": self.sets,
+                "ops": "q normRope (stride 2d) + k normRope into the cache + sigmoidMul"}
+
+    def cpu(self, budget_s):
+        import numpy as np
+        import oracle
+        import torch
+        s = 0
+        T, hq, hkv, d, P, rot = self.T, self.hq, self.hkv, self.d, self.P, self.rot
+        for label in self.labels:
+            self.op(label, s)
+        torch.cuda.synchronize()
+        qg, k = host_u16(self.qg[s]).reshape(T * hq, 2 * d), host_u16(self.k[s]).reshape(T * hkv, d)
+        gate, attn = host_u16(self.gate[s]), host_u16(self.attn[s])
+        qw, kw = host_f32(self.qw), host_f32(self.kw)
+        kc = np.zeros(((P + T) * hkv, d), np.uint16)
+
+        def step():
+            q = oracle.norm_rope(qg, qw, T, hq, d, rot, 2 * d, P)
+            oracle.norm_rope(k, kw, T, hkv, d, rot, d, P, output=kc, output_start=P)
+            return q, oracle.sigmoid_mul(gate, attn)
+
+        q, o = step()
+        exact = bool(np.array_equal(q.reshape(-1), host_u16(self.qout[s]).reshape(-1))
+                     and np.array_equal(kc[P * hkv:], host_u16(self.kc[P:]).reshape(-1, d))
+                     and np.array_equal(o.reshape(-1), host_u16(self.out[s]).reshape(-1)))
+        sec, runs = time_cpu(step, budget_s)
+        return {"value": sec * 1e6, "unit": "µs/layer", "cores": 1, "kind": "port",
+                "sample": f"the three ops on one input set (T={T}, P={P}), {runs} runs, "
+                          "scalar C oracle (orc_norm_rope, orc_sigmoid_mul)",
+                "gpu_bit_exact": exact}
 
 
 def _delta_inputs(g, dev, T, hk, dk, hv, dv):
@@ -611,6 +703,8 @@ def main(argv=None) -> int:
             ("cfg2_gqa_chunked_prefill", lambda: GqaPrefill(dev, 2048, 2048, 4096, seed=3)),
             ("cfg3_delta_prefill_1024", lambda: DeltaPrefill(dev)),
             ("cfg4_hybrid_decode_32k", lambda: HybridDecode(dev)),
+            ("next_attn_rows_prefill_2048", lambda: AttnRows(dev, 2048, 2048, 6, seed=6)),
+            ("next_attn_rows_decode_4k", lambda: AttnRows(dev, 1, 4096, 64, seed=7)),
         ]
         for key, make in builders:
             x = make()
@@ -629,6 +723,12 @@ def main(argv=None) -> int:
                 kern_s = entry["roofline"]["kernel_us_avg"] * 1e-6
                 entry["mfma_frac_recurrent_flops"] = round(
                     delta_flops(x.T, x.hv, x.dk, x.dv) / kern_s / 1e12 / MFMA_F16_PEAK_TFS, 5)
+            if isinstance(x, AttnRows):
+                entry["op_roofline"] = {
+                    l: {"bytes": x.bytes[l],
+                        "achieved_GBs": round(x.bytes[l] / (op_ms[l] * 1e-3) / 1e9, 1),
+                        "frac": round(x.bytes[l] / (op_ms[l] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+                    for l in x.labels}
             if isinstance(x, HybridDecode):
                 hk, dk, hv, dv = x.dshape
                 entry["delta_hbm_frac"] = round(

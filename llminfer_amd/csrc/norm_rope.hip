@@ -23,18 +23,19 @@
 //    and exp are used only through their fp16 rounding, so the fast fp32
 //    library function decides whenever every value within 2^-19 relative of
 //    its result rounds to the same fp16 (its error is a few ulp, far inside
-//    that); otherwise, and always for pow, the value is evaluated in double
-//    and rounded to float once.
+//    that; 2^-21 for cos and sin); otherwise, and always for pow, the value
+//    is evaluated in double and rounded to float once.
 //
 // normRope tile kernel: one wave per block owns `rw` consecutive rows.
 //   1. the wave loads the rows' headDim halves with 16-byte coalesced loads
-//      and stores them to LDS (row pitch headDim + 8 halves); meanwhile lanes
-//      evaluate pow(theta, 2i/rotaryDim) per pair;
-//   2. lane r sums row r sequentially from LDS; the lanes fill the
-//      (token, pair) -> (cos, sin) table of the rows' tokens and 1 + w;
-//   3. each lane takes 16-byte output chunks of consecutive columns, reads
-//      the chunk and, in the rotary part, the partner chunk (column +-
-//      rotaryDim/2) from LDS, normalises, rotates and stores 16 bytes.
+//      and stores them to LDS (row pitch headDim + 8 halves); the inverse
+//      frequencies pow(theta, 2i/rotaryDim) come precomputed in the kernel
+//      arguments;
+//   2. the lanes fill the (token, pair) -> (cos, sin) table of the rows'
+//      tokens, and lane r sums row r sequentially from LDS;
+//   3. the rotary pairs (per item a row and 8 pairs: the chunks at columns j
+//      and j + rotaryDim/2), then the copied columns (per item one chunk),
+//      are normalised, rotated and stored with 16-byte stores.
 // Shapes outside the tile kernel's alignment rules (headDim, headStride or
 // rotaryDim/2 not a multiple of 8 halves, unaligned pointers, headDim > 2048)
 // run the row kernel: one thread per row, the reference's own structure,
@@ -42,12 +43,15 @@
 #include "hip_common.hpp"
 #include "kernels.hpp"
 
+#include <math.h>
+#include <string.h>
+
 
 namespace llmi {
 namespace {
 
 constexpr int kPad = 8;                 // halves of LDS padding per tile row
-constexpr unsigned kTileHalves = 16384; // rows * headDim bound of one tile
+constexpr unsigned kTileHalves = 8192;  // rows * headDim bound of one tile
 constexpr unsigned kTileIters = kTileHalves / 8 / 64;
 
 __device__ __forceinline__ float h2f(uint16_t b) {
@@ -65,11 +69,13 @@ __device__ __forceinline__ float opaque(float x) {
 __device__ __forceinline__ float mul32(float a, float b) { return opaque(a * b); }
 __device__ __forceinline__ float round16(float x) { return opaque((float)(half_t)x); }
 
-// True when every float within 2^-19 relative of v has the same fp16
+// True when every float within `margin` (relative) of v has the same fp16
 // rounding as v (fp16 rounding is monotonic, so the two ends decide).
+template <int kLog2Margin = 19>
 __device__ __forceinline__ bool f16_settled(float v) {
-  half_t a = (half_t)__fmul_rn(v, 1.0f - 0x1p-19f);
-  half_t b = (half_t)__fmul_rn(v, 1.0f + 0x1p-19f);
+  constexpr float m = 1.0f / (float)(1u << kLog2Margin);
+  half_t a = (half_t)__fmul_rn(v, 1.0f - m);
+  half_t b = (half_t)__fmul_rn(v, 1.0f + m);
   return __builtin_bit_cast(uint16_t, a) == __builtin_bit_cast(uint16_t, b);
 }
 
@@ -77,7 +83,8 @@ __device__ __forceinline__ bool f16_settled(float v) {
 __device__ __forceinline__ float2 rope_cos_sin(float phase) {
   float s, c;
   sincosf(phase, &s, &c);
-  if (!(f16_settled(c) && f16_settled(s))) {
+  // sincosf is within 2 ulp; 2^-21 relative is 4 to 8 ulp.
+  if (!(f16_settled<21>(c) && f16_settled<21>(s))) {
     double sd, cd;
     sincos((double)phase, &sd, &cd);
     c = (float)cd;
@@ -115,54 +122,114 @@ struct TileArgs {
   float eps, theta;
 };
 
+// pow(theta, 2i/rotaryDim) for i < rotaryDim/2, computed once on the host
+// (correctly rounded, as on the device) and passed in the kernel arguments;
+// wider rotations compute it in the kernel.
+constexpr unsigned kArgFreqs = 256;
+struct RopeFreqs {
+  float v[kArgFreqs];
+};
+
+__device__ __forceinline__ float inv_freq(const RopeFreqs &f, const TileArgs &a,
+                                          unsigned i) {
+  return a.rot / 2 <= kArgFreqs ? f.v[i] : rope_inv_freq(a.theta, i, a.rot);
+}
+
 template <bool kNorm>
 __global__ __launch_bounds__(64) void norm_rope_tile(const uint16_t *in,
                                                      const float *__restrict__ w,
-                                                     uint16_t *out, TileArgs a) {
+                                                     uint16_t *out, TileArgs a,
+                                                     RopeFreqs f) {
   extern __shared__ __align__(16) unsigned char smem[];
   const unsigned lane = threadIdx.x;
   const unsigned pitch = a.D + kPad;
   const unsigned half = a.rot / 2;
   uint16_t *tile = reinterpret_cast<uint16_t *>(smem);
   float *sc = reinterpret_cast<float *>(tile + a.rw * pitch);
-  float *wt1 = sc + ((a.rw + 1) & ~1u);
-  float *invf = wt1 + (kNorm ? a.D : 0);
-  float2 *cs = reinterpret_cast<float2 *>(invf + ((half + 1) & ~1u));
+  unsigned *rtok = reinterpret_cast<unsigned *>(sc + ((a.rw + 1) & ~1u));
+  float *wt1 = reinterpret_cast<float *>(rtok + ((a.rw + 1) & ~1u));
+  float2 *cs = reinterpret_cast<float2 *>(wt1 + (kNorm ? a.D : 0));
 
   const unsigned row0 = blockIdx.x * a.rw;
   const unsigned nrows = min(a.rw, a.rows - row0);
   const unsigned cpr = a.D / 8; // 16-byte chunks per row
-  const unsigned chunks = nrows * cpr;
+  // Lane l owns chunks l, l + 64, ... of the tile, row-major; (r, col) of
+  // the next one follows by a uniform step, without a division per chunk.
+  const unsigned step_r = 64 / cpr, step_c = 64 - step_r * cpr;
+  const unsigned lane_r = lane / cpr, lane_c = lane - lane_r * cpr;
+  auto advance = [&](unsigned &r, unsigned &col) {
+    col += step_c;
+    r += step_r;
+    if (col >= cpr) {
+      col -= cpr;
+      ++r;
+    }
+  };
 
-  // 1. coalesced loads of the tile; pow per pair while they are in flight.
+  // 1. coalesced loads of the tile, after the first inverse frequency each
+  //    lane needs for the cos/sin table (so that it is there before them).
+  const unsigned tok0 = row0 / a.heads;
+  const unsigned ntok = (row0 + nrows - 1) / a.heads - tok0 + 1;
+  const unsigned entries = ntok * half;
+  float inv0 = lane < entries ? inv_freq(f, a, lane % half) : 1.0f;
   uint4_t v[kTileIters];
+  {
+    unsigned r = lane_r, col = lane_c;
 #pragma unroll
-  for (unsigned it = 0; it < kTileIters; ++it) {
-    unsigned c = it * 64 + lane;
-    unsigned r = c / cpr, col = c - r * cpr;
-    if (c < chunks)
-      v[it] = *reinterpret_cast<const uint4_t *>(
-          in + (size_t)(row0 + r) * a.stride + col * 8);
+    for (unsigned it = 0; it < kTileIters; ++it) {
+      if (r < nrows)
+        v[it] = *reinterpret_cast<const uint4_t *>(in + (row0 + r) * a.stride + col * 8);
+      advance(r, col);
+    }
   }
-  for (unsigned i = lane; i < half; i += 64)
-    invf[i] = rope_inv_freq(a.theta, i, a.rot);
   if (kNorm)
     for (unsigned i = lane; i < a.D; i += 64)
       wt1[i] = 1.0f + w[i];
+  if (lane < nrows)
+    rtok[lane] = ((row0 + lane) / a.heads - tok0) * half;
+  {
+    unsigned r = lane_r, col = lane_c;
 #pragma unroll
-  for (unsigned it = 0; it < kTileIters; ++it) {
-    unsigned c = it * 64 + lane;
-    unsigned r = c / cpr, col = c - r * cpr;
-    if (c < chunks)
-      *reinterpret_cast<uint4_t *>(tile + r * pitch + col * 8) = v[it];
+    for (unsigned it = 0; it < kTileIters; ++it) {
+      if (r < nrows)
+        *reinterpret_cast<uint4_t *>(tile + r * pitch + col * 8) = v[it];
+      advance(r, col);
+    }
   }
   __syncthreads();
 
-  // 2. sequential sums (lane = row) and the cos/sin table.
-  if (kNorm && lane < nrows) {
-    const uint16_t *row = tile + lane * pitch;
+  // 2. the cos/sin table and the sequential sums (lane = row; every lane
+  //    runs the chain, on a valid row, so that the code stays straight and
+  //    the table's arithmetic fills the chain's latency).
+  if (lane < entries) {
+    float position = (float)(a.past + tok0 + lane / half);
+    cs[lane] = rope_cos_sin(__fdiv_rn(position, inv0));
+  }
+  for (unsigned e = lane + 64; e < entries; e += 64) {
+    unsigned t = e / half, i = e - t * half;
+    float position = (float)(a.past + tok0 + t);
+    cs[e] = rope_cos_sin(__fdiv_rn(position, inv_freq(f, a, i)));
+  }
+  if (kNorm) {
+    const uint16_t *row = tile + min(lane, nrows - 1) * pitch;
     float sum = 0.0f;
-    for (unsigned k = 0; k < cpr; ++k) {
+    unsigned k = 0;
+    for (; k + 4 <= cpr; k += 4) {
+      uint4_t q[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+        q[u] = *reinterpret_cast<const uint4_t *>(row + 8 * (k + u));
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          float lo = h2f((uint16_t)(q[u][e] & 0xFFFFu));
+          float hi = h2f((uint16_t)(q[u][e] >> 16));
+          sum = __builtin_fmaf(lo, lo, sum);
+          sum = __builtin_fmaf(hi, hi, sum);
+        }
+    }
+    for (; k < cpr; ++k) {
       uint4_t q = *reinterpret_cast<const uint4_t *>(row + 8 * k);
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
@@ -172,50 +239,80 @@ __global__ __launch_bounds__(64) void norm_rope_tile(const uint16_t *in,
         sum = __builtin_fmaf(hi, hi, sum);
       }
     }
-    sc[lane] = rms_scale_of(sum, a.D, a.eps);
-  }
-  const unsigned tok0 = row0 / a.heads;
-  const unsigned ntok = (row0 + nrows - 1) / a.heads - tok0 + 1;
-  for (unsigned e = lane; e < ntok * half; e += 64) {
-    unsigned t = e / half, i = e - t * half;
-    float position = (float)(a.past + tok0 + t);
-    cs[e] = rope_cos_sin(__fdiv_rn(position, invf[i]));
+    if (lane < nrows)
+      sc[lane] = rms_scale_of(sum, a.D, a.eps);
   }
   __syncthreads();
 
-  // 3. normalise, rotate, store.
-  for (unsigned c = lane; c < chunks; c += 64) {
-    unsigned r = c / cpr, col = c - r * cpr, j0 = col * 8;
-    const uint16_t *mine = tile + r * pitch + j0;
-    uint4_t q = *reinterpret_cast<const uint4_t *>(mine);
-    float scale = kNorm ? sc[r] : 1.0f;
-    uint16_t o[8];
-    float x[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      uint16_t b = (uint16_t)(q[e / 2] >> (16 * (e & 1)));
-      x[e] = kNorm ? normed(b, scale, wt1[j0 + e]) : h2f(b);
-      o[e] = f2h(x[e]);
-    }
-    if (j0 < a.rot) {
-      bool first = j0 < half;
-      unsigned pj = first ? j0 + half : j0 - half;
-      uint4_t p = *reinterpret_cast<const uint4_t *>(tile + r * pitch + pj);
-      unsigned pair0 = first ? j0 : pj;
-      const float2 *csr = cs + ((row0 + r) / a.heads - tok0) * half + pair0;
+  // 3. normalise, rotate, store: first the rotary pairs (an item is a row
+  //    and 8 pairs: two 16-byte chunks, columns j0 and j0 + rotaryDim/2),
+  //    then the copied columns (an item is one chunk), so that every lane
+  //    of a pass does the same kind of work.
+  const unsigned pchunks = half / 8;
+  if (pchunks) {
+    const unsigned sr = 64 / pchunks, sc_ = 64 - sr * pchunks;
+    unsigned r = lane / pchunks, k = lane - r * pchunks;
+    for (; r < nrows;) {
+      unsigned j0 = 8 * k, j1 = j0 + half;
+      const uint16_t *row = tile + r * pitch;
+      uint4_t qx = *reinterpret_cast<const uint4_t *>(row + j0);
+      uint4_t qy = *reinterpret_cast<const uint4_t *>(row + j1);
+      float scale = kNorm ? sc[r] : 1.0f;
+      const float2 *csr = cs + rtok[r] + j0;
+      uint16_t ox[8], oy[8];
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        uint16_t b = (uint16_t)(p[e / 2] >> (16 * (e & 1)));
-        float y = kNorm ? normed(b, scale, wt1[pj + e]) : h2f(b);
+        uint16_t bx = (uint16_t)(qx[e / 2] >> (16 * (e & 1)));
+        uint16_t by = (uint16_t)(qy[e / 2] >> (16 * (e & 1)));
+        float x = kNorm ? normed(bx, scale, wt1[j0 + e]) : h2f(bx);
+        float y = kNorm ? normed(by, scale, wt1[j1 + e]) : h2f(by);
         float2 t = csr[e];
-        o[e] = first ? rotate_x(x[e], y, t) : rotate_y(y, x[e], t);
+        ox[e] = rotate_x(x, y, t);
+        oy[e] = rotate_y(x, y, t);
+      }
+      uint4_t sx, sy;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        sx[e] = (uint32_t)ox[2 * e] | ((uint32_t)ox[2 * e + 1] << 16);
+        sy[e] = (uint32_t)oy[2 * e] | ((uint32_t)oy[2 * e + 1] << 16);
+      }
+      uint16_t *dst = out + (a.out_row0 + row0 + r) * a.D;
+      *reinterpret_cast<uint4_t *>(dst + j0) = sx;
+      *reinterpret_cast<uint4_t *>(dst + j1) = sy;
+      k += sc_;
+      r += sr;
+      if (k >= pchunks) {
+        k -= pchunks;
+        ++r;
       }
     }
-    uint4_t st;
+  }
+  const unsigned first = a.rot / 8, pass = cpr - first;
+  if (pass) {
+    const unsigned sr = 64 / pass, sc_ = 64 - sr * pass;
+    unsigned r = lane / pass, k = lane - r * pass;
+    for (; r < nrows;) {
+      unsigned j0 = 8 * (first + k);
+      uint4_t q = *reinterpret_cast<const uint4_t *>(tile + r * pitch + j0);
+      float scale = kNorm ? sc[r] : 1.0f;
+      uint4_t st;
 #pragma unroll
-    for (int e = 0; e < 4; ++e)
-      st[e] = (uint32_t)o[2 * e] | ((uint32_t)o[2 * e + 1] << 16);
-    *reinterpret_cast<uint4_t *>(out + (size_t)(a.out_row0 + row0 + r) * a.D + j0) = st;
+      for (int e = 0; e < 4; ++e) {
+        uint16_t lo = (uint16_t)(q[e] & 0xFFFFu), hi = (uint16_t)(q[e] >> 16);
+        if (kNorm) {
+          lo = f2h(normed(lo, scale, wt1[j0 + 2 * e]));
+          hi = f2h(normed(hi, scale, wt1[j0 + 2 * e + 1]));
+        }
+        st[e] = (uint32_t)lo | ((uint32_t)hi << 16);
+      }
+      *reinterpret_cast<uint4_t *>(out + (a.out_row0 + row0 + r) * a.D + j0) = st;
+      k += sc_;
+      r += sr;
+      if (k >= pass) {
+        k -= pass;
+        ++r;
+      }
+    }
   }
 }
 
@@ -223,7 +320,8 @@ __global__ __launch_bounds__(64) void norm_rope_tile(const uint16_t *in,
 template <bool kNorm>
 __global__ __launch_bounds__(256) void norm_rope_rows(const uint16_t *in,
                                                       const float *__restrict__ w,
-                                                      uint16_t *out, TileArgs a) {
+                                                      uint16_t *out, TileArgs a,
+                                                      RopeFreqs f) {
   unsigned row = blockIdx.x * 256 + threadIdx.x;
   if (row >= a.rows)
     return;
@@ -244,7 +342,7 @@ __global__ __launch_bounds__(256) void norm_rope_rows(const uint16_t *in,
     unsigned j = i + half;
     float x = kNorm ? normed(head[i], scale, 1.0f + w[i]) : h2f(head[i]);
     float y = kNorm ? normed(head[j], scale, 1.0f + w[j]) : h2f(head[j]);
-    float2 t = rope_cos_sin(__fdiv_rn(position, rope_inv_freq(a.theta, i, a.rot)));
+    float2 t = rope_cos_sin(__fdiv_rn(position, inv_freq(f, a, i)));
     uint16_t ox = rotate_x(x, y, t), oy = rotate_y(x, y, t);
     dst[i] = ox;
     dst[j] = oy;
@@ -253,11 +351,26 @@ __global__ __launch_bounds__(256) void norm_rope_rows(const uint16_t *in,
     dst[i] = kNorm ? f2h(normed(head[i], scale, 1.0f + w[i])) : head[i];
 }
 
+// logistic(g) = 1 / (1 + exp(-g)) with exp(-g) as 2^(-g log2 e) on the
+// hardware exp2 and the hardware reciprocal. Relative error: |g| 2^-24 from
+// the rounded argument plus about 2^-22 from the three instructions, at most
+// 1.3 * 2^-20 while the result can still round to a nonzero fp16
+// (g > -17.4), which the 2^-19 margin of f16_settled covers. Below that the
+// estimate and the exact value both round to 0, above g = 16 both to 1.
+__device__ __forceinline__ float logistic_estimate(float g) {
+  return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-g * kLog2e));
+}
+
+// The correctly rounded fp32 exp (double, rounded once), as in the oracle.
+__device__ __forceinline__ float logistic_exact(float g) {
+  return __fdiv_rn(1.0f, __fadd_rn(1.0f, (float)exp(-(double)g)));
+}
+
 // fp16(logistic(g)) of the correctly rounded fp32 exp.
 __device__ __forceinline__ float logistic16(float g) {
-  float s = __fdiv_rn(1.0f, __fadd_rn(1.0f, expf(-g)));
+  float s = logistic_estimate(g);
   if (!f16_settled(s))
-    s = __fdiv_rn(1.0f, __fadd_rn(1.0f, (float)exp(-(double)g)));
+    s = logistic_exact(g);
   return round16(s);
 }
 
@@ -265,6 +378,9 @@ __device__ __forceinline__ uint16_t gate_one(uint16_t g, uint16_t x) {
   return f2h(mul32(logistic16(h2f(g)), h2f(x)));
 }
 
+// Eight gates per lane: the estimates first, then the exact evaluation for
+// the few that need it, one per pass (a pass costs the wave one double exp,
+// so the lanes share passes instead of running one per element slot).
 __global__ __launch_bounds__(256) void sigmoid_mul_vec(const uint4_t *__restrict__ gate,
                                                        const uint4_t *__restrict__ in,
                                                        uint4_t *__restrict__ out,
@@ -272,13 +388,33 @@ __global__ __launch_bounds__(256) void sigmoid_mul_vec(const uint4_t *__restrict
   unsigned i = blockIdx.x * 256 + threadIdx.x;
   if (i >= vectors)
     return;
-  uint4_t g = __builtin_nontemporal_load(gate + i);
-  uint4_t x = __builtin_nontemporal_load(in + i);
+  uint4_t gv = __builtin_nontemporal_load(gate + i);
+  uint4_t xv = __builtin_nontemporal_load(in + i);
+  float g[8], s[8];
+  unsigned need = 0;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    g[e] = h2f((uint16_t)(gv[e / 2] >> (16 * (e & 1))));
+    s[e] = logistic_estimate(g[e]);
+    need |= f16_settled(s[e]) ? 0u : 1u << e;
+  }
+  while (need) {
+    unsigned k = __builtin_ctz(need);
+    need &= need - 1;
+    float gk = g[0];
+#pragma unroll
+    for (int e = 1; e < 8; ++e)
+      gk = k == (unsigned)e ? g[e] : gk;
+    float sk = logistic_exact(gk);
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      s[e] = k == (unsigned)e ? sk : s[e];
+  }
   uint4_t o;
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
-    uint16_t lo = gate_one((uint16_t)(g[e] & 0xFFFFu), (uint16_t)(x[e] & 0xFFFFu));
-    uint16_t hi = gate_one((uint16_t)(g[e] >> 16), (uint16_t)(x[e] >> 16));
+    uint16_t lo = f2h(mul32(round16(s[2 * e]), h2f((uint16_t)(xv[e] & 0xFFFFu))));
+    uint16_t hi = f2h(mul32(round16(s[2 * e + 1]), h2f((uint16_t)(xv[e] >> 16))));
     o[e] = (uint32_t)lo | ((uint32_t)hi << 16);
   }
   __builtin_nontemporal_store(o, out + i);
@@ -317,10 +453,26 @@ TilePlan plan_tile(const RopeShape &s) {
       break;
     rw /= 2;
   }
-  p.lds = (size_t)p.rw * (s.D + kPad) * 2 + (size_t)((p.rw + 1) & ~1u) * 4 +
-          (s.norm ? (size_t)s.D * 4 : 0) + (size_t)((half + 1) & ~1u) * 4 +
-          (size_t)p.maxtok * half * sizeof(float2);
+  p.lds = (size_t)p.rw * (s.D + kPad) * 2 + (size_t)((p.rw + 1) & ~1u) * 8 +
+          (s.norm ? (size_t)s.D * 4 : 0) + (size_t)p.maxtok * half * sizeof(float2);
   return p;
+}
+
+
+// The host's correctly rounded pow (double, rounded once), per (theta, rot),
+// kept for the next call with the same rotation.
+static const RopeFreqs &host_freqs(float theta, unsigned rot) {
+  static thread_local RopeFreqs table;
+  static thread_local float cached_theta = 0.0f;
+  static thread_local unsigned cached_rot = 0;
+  unsigned half = rot / 2;
+  if (half <= kArgFreqs && (cached_rot != rot || memcmp(&cached_theta, &theta, 4) != 0)) {
+    for (unsigned i = 0; i < half; ++i)
+      table.v[i] = (float)pow((double)theta, (double)(2.0f * (float)i / (float)rot));
+    cached_theta = theta;
+    cached_rot = rot;
+  }
+  return table;
 }
 
 } // namespace
@@ -336,21 +488,22 @@ hipError_t launch_norm_rope(const uint16_t *in, const float *w, uint16_t *out,
     return hipSuccess;
   TileArgs a{s.rows, s.heads, s.D, s.rot, s.stride, s.past, s.out_row0, 0, 0,
              s.eps, s.theta};
+  const RopeFreqs &f = host_freqs(s.theta, s.rot);
   if (norm_rope_tiled(s, in, out)) {
     TilePlan p = plan_tile(s);
     a.rw = p.rw;
     a.maxtok = p.maxtok;
     dim3 grid((s.rows + p.rw - 1) / p.rw);
     if (s.norm)
-      hipLaunchKernelGGL(norm_rope_tile<true>, grid, dim3(64), p.lds, stream, in, w, out, a);
+      hipLaunchKernelGGL(norm_rope_tile<true>, grid, dim3(64), p.lds, stream, in, w, out, a, f);
     else
-      hipLaunchKernelGGL(norm_rope_tile<false>, grid, dim3(64), p.lds, stream, in, w, out, a);
+      hipLaunchKernelGGL(norm_rope_tile<false>, grid, dim3(64), p.lds, stream, in, w, out, a, f);
   } else {
     dim3 grid((s.rows + 255) / 256);
     if (s.norm)
-      hipLaunchKernelGGL(norm_rope_rows<true>, grid, dim3(256), 0, stream, in, w, out, a);
+      hipLaunchKernelGGL(norm_rope_rows<true>, grid, dim3(256), 0, stream, in, w, out, a, f);
     else
-      hipLaunchKernelGGL(norm_rope_rows<false>, grid, dim3(256), 0, stream, in, w, out, a);
+      hipLaunchKernelGGL(norm_rope_rows<false>, grid, dim3(256), 0, stream, in, w, out, a, f);
   }
   return hipGetLastError();
 }

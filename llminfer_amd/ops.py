@@ -61,9 +61,9 @@ def cache_append(src: torch.Tensor, cache: torch.Tensor, offset: int) -> None:
                                          _lib.CacheParams(src.numel(), offset), _stream()))
 
 
-def norm_rope(x: torch.Tensor, weight: torch.Tensor, out: torch.Tensor, past: int,
-              rotary_dim: int, epsilon: float = 1e-6, theta: float = 1e7,
-              head_dim: int | None = None, output_start: int = 0) -> None:
+def bind_norm_rope(x: torch.Tensor, weight: torch.Tensor, out: torch.Tensor, past: int,
+                   rotary_dim: int, epsilon: float = 1e-6, theta: float = 1e7,
+                   head_dim: int | None = None, output_start: int = 0) -> "Bound":
     """normRope (Reference.metal:271-293): x [T, H, stride] fp16 (the first
     head_dim halves of each head are read; stride = 2 * head_dim for the
     projected q with its gate), weight [head_dim] fp32, out [>= output_start
@@ -81,7 +81,12 @@ def norm_rope(x: torch.Tensor, weight: torch.Tensor, out: torch.Tensor, past: in
     if output_start + T > out.shape[0]:
         raise ValueError("output rows exceed out")
     p = _lib.RopeParams(T, H, d, rotary_dim, stride, past, output_start, epsilon, theta)
-    _lib.check(_lib.load().llmi_hip_norm_rope(_ptr(x), _ptr(weight), _ptr(out), p, _stream()))
+    return Bound(_lib.load().llmi_hip_norm_rope, (_ptr(x), _ptr(weight), _ptr(out), p, _stream()),
+                 kernel_names(_lib.OP_NORM_ROPE, p)[0] if T * H * d else "normRope")
+
+
+def norm_rope(*args, **kwargs) -> None:
+    bind_norm_rope(*args, **kwargs)()
 
 
 def rms_norm(x: torch.Tensor, weight: torch.Tensor, out: torch.Tensor,
@@ -109,14 +114,19 @@ def partial_rope(x: torch.Tensor, out: torch.Tensor, past: int, rotary_dim: int,
     _lib.check(_lib.load().llmi_hip_partial_rope(_ptr(x), _ptr(out), p, _stream()))
 
 
-def sigmoid_mul(gate: torch.Tensor, x: torch.Tensor, out: torch.Tensor) -> None:
-    """sigmoidMul (Graph.metal:78-85): out = fp16(fp16(sigmoid(gate)) * x)."""
+def bind_sigmoid_mul(gate: torch.Tensor, x: torch.Tensor, out: torch.Tensor) -> "Bound":
     for t, n in ((gate, "gate"), (x, "x"), (out, "out")):
         _require(t, torch.float16, n)
     if gate.numel() != x.numel() or out.numel() != x.numel():
         raise ValueError("gate, x and out must have the same size")
     p = _lib.ElementParams(x.numel())
-    _lib.check(_lib.load().llmi_hip_sigmoid_mul(_ptr(gate), _ptr(x), _ptr(out), p, _stream()))
+    return Bound(_lib.load().llmi_hip_sigmoid_mul, (_ptr(gate), _ptr(x), _ptr(out), p, _stream()),
+                 kernel_names(_lib.OP_SIGMOID_MUL, p)[0] if x.numel() else "sigmoidMul")
+
+
+def sigmoid_mul(gate: torch.Tensor, x: torch.Tensor, out: torch.Tensor) -> None:
+    """sigmoidMul (Graph.metal:78-85): out = fp16(fp16(sigmoid(gate)) * x)."""
+    bind_sigmoid_mul(gate, x, out)()
 
 
 def kv_append(k: torch.Tensor, v: torch.Tensor, k_cache: torch.Tensor,
