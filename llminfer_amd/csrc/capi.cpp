@@ -99,7 +99,7 @@ using namespace llmi;
 
 // normRope / rmsNorm / partialRope as one row shape. Rows per tile (one
 // wave each): about 2048 tiles (two waves per SIMD on 256 CUs), but at least
-// 8 rows once there are that many, since the sequential sum costs a tile the
+// 8 rows once there are 4096 rows, since the sequential sum costs a tile the
 // same whatever its row count, and 2 for a decode step's few rows, where the
 // wave's latency is what counts (a sweep of 1..32 on MI355X: q 2048x16 rows
 // best at 16, k 2048x4 at 4-8, decode 16 rows at 2).
@@ -107,7 +107,7 @@ RopeShape rope_shape(unsigned rows, unsigned heads, unsigned D, unsigned rot,
                      unsigned stride, unsigned past, unsigned out_row0, float eps,
                      float theta, bool norm) {
   unsigned rw = (rows + 2047) / 2048;
-  unsigned lo = rows >= 8 * 2048 ? 8 : 2;
+  unsigned lo = rows >= 4096 ? 8 : 2;
   rw = rw < lo ? lo : rw > 64 ? 64 : rw;
   return RopeShape{rows, heads, D, rot, stride, past, out_row0, eps, theta, norm, rw};
 }
