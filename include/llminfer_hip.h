@@ -81,6 +81,17 @@ typedef struct PartialRopeParams {
   float theta;
 } PartialRopeParams;
 
+/* lib/Backend/Metal/Kernels/ReferenceParams.h:32-34 */
+typedef struct ConvParams {
+  unsigned tokens, channels, kernelSize, applySilu;
+} ConvParams;
+
+/* lib/Backend/Metal/Kernels/GraphParams.h:30-33 */
+typedef struct L2Params {
+  unsigned rows, width;
+  float epsilon, scale;
+} L2Params;
+
 enum llmi_hip_status {
   LLMI_HIP_OK = 0,
   LLMI_HIP_INVALID_ARGUMENT = 1, /* bad shape/pointer; nothing launched */
@@ -98,7 +109,10 @@ enum llmi_hip_op {
   LLMI_HIP_OP_NORM_ROPE = 4,            /* params: RopeParams */
   LLMI_HIP_OP_RMS_NORM = 5,             /* params: RowParams */
   LLMI_HIP_OP_PARTIAL_ROPE = 6,         /* params: PartialRopeParams */
-  LLMI_HIP_OP_SIGMOID_MUL = 7           /* params: ElementParams */
+  LLMI_HIP_OP_SIGMOID_MUL = 7,          /* params: ElementParams */
+  LLMI_HIP_OP_CAUSAL_CONV = 8,          /* params: ConvParams */
+  LLMI_HIP_OP_L2_NORM = 9,              /* params: L2Params */
+  LLMI_HIP_OP_DELTA_GATES = 10          /* params: RowParams (rows = tokens, width = heads) */
 };
 
 /* ---------------------------------------------------------------- KvAppend
@@ -152,6 +166,35 @@ LLMI_HIP_API int llmi_hip_partial_rope(const uint16_t *input, uint16_t *output,
  * output[i] = fp16(fp16(1 / (1 + exp(-gate[i]))) * input[i]), i < count. */
 LLMI_HIP_API int llmi_hip_sigmoid_mul(const uint16_t *gate, const uint16_t *input,
                                       uint16_t *output, ElementParams p, void *stream);
+
+/* ------------------------------------------------------ DeltaNet front end
+ * The DeltaNet layer's ops ahead of DeltaUpdate (Qwen35ModelBuilder.cpp:
+ * 146-160; lowered at MetalExecutionPlan.cpp:597-603, 639-662). Results equal
+ * the reference kernels' fp32 expressions bit for bit, with exp and log
+ * correctly rounded to fp32.
+ *
+ * causalConv (Reference.metal:137-161): input, output [tokens][channels]
+ * fp16; weight [channels][kernelSize] fp16; history [channels][kernelSize-1]
+ * fp16, read and updated in place (the last kernelSize-1 inputs of the
+ * sequence). applySilu != 0 applies fp16(silu(fp16(acc))). kernelSize 1..8;
+ * history may be null when kernelSize == 1. */
+LLMI_HIP_API int llmi_hip_causal_conv(const uint16_t *input, const uint16_t *weight,
+                                      uint16_t *history, uint16_t *output, ConvParams p,
+                                      void *stream);
+
+/* l2NormF32 (Graph.metal:96-109): output[r][i] = input[r][i] *
+ * (rsqrt(sum_i input[r][i]^2 + epsilon) * scale), fp16 in, fp32 out, rows x
+ * width dense. */
+LLMI_HIP_API int llmi_hip_l2_norm(const uint16_t *input, float *output, L2Params p,
+                                  void *stream);
+
+/* deltaGates (Graph.metal:131-144): for i < rows * width, head = i % width:
+ * beta[i] = fp16(logistic(b[i])) (as fp32), decay[i] = exp(-exp(a_log[head])
+ * * stableSoftplus(a[i] + dt_bias[head])). a, b fp16; a_log, dt_bias,
+ * beta, decay fp32. */
+LLMI_HIP_API int llmi_hip_delta_gates(const uint16_t *a, const uint16_t *b, const float *a_log,
+                                      const float *dt_bias, float *beta, float *decay,
+                                      RowParams p, void *stream);
 
 /* --------------------------------------------------------------- CausalGqa
  * Replaces gqaFlashAttention (FlashAttention.metal:1-83) for T > 1 and the

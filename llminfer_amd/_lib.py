@@ -26,6 +26,9 @@ OP_NORM_ROPE = 4
 OP_RMS_NORM = 5
 OP_PARTIAL_ROPE = 6
 OP_SIGMOID_MUL = 7
+OP_CAUSAL_CONV = 8
+OP_L2_NORM = 9
+OP_DELTA_GATES = 10
 
 
 class CacheParams(C.Structure):
@@ -49,6 +52,15 @@ class RopeParams(C.Structure):
 class PartialRopeParams(C.Structure):
     _fields_ = [(n, C.c_uint) for n in ("rows", "heads", "width", "rotaryWidth", "past")] + \
                [("theta", C.c_float)]
+
+
+class ConvParams(C.Structure):
+    _fields_ = [(n, C.c_uint) for n in ("tokens", "channels", "kernelSize", "applySilu")]
+
+
+class L2Params(C.Structure):
+    _fields_ = [("rows", C.c_uint), ("width", C.c_uint), ("epsilon", C.c_float),
+                ("scale", C.c_float)]
 
 
 class GqaParams(C.Structure):
@@ -94,6 +106,9 @@ SIGNATURES = {
     "llmi_hip_rms_norm": (C.c_int, [_P, _P, _P, RowParams, _P]),
     "llmi_hip_partial_rope": (C.c_int, [_P, _P, PartialRopeParams, _P]),
     "llmi_hip_sigmoid_mul": (C.c_int, [_P, _P, _P, ElementParams, _P]),
+    "llmi_hip_causal_conv": (C.c_int, [_P, _P, _P, _P, ConvParams, _P]),
+    "llmi_hip_l2_norm": (C.c_int, [_P, _P, L2Params, _P]),
+    "llmi_hip_delta_gates": (C.c_int, [_P, _P, _P, _P, _P, _P, RowParams, _P]),
     "llmi_hip_kv_append": (C.c_int, [_P, _P, _P, _P, CacheParams, _P]),
     "llmi_hip_causal_gqa": (C.c_int, [_P, _P, _P, _P, GqaParams, _P, _SZ, _P]),
     "llmi_hip_gqa_workspace_bytes": (_SZ, [GqaParams]),

@@ -193,6 +193,49 @@ int llmi_hip_sigmoid_mul(const uint16_t *gate, const uint16_t *input, uint16_t *
                   "sigmoidMul");
 }
 
+int llmi_hip_causal_conv(const uint16_t *input, const uint16_t *weight, uint16_t *history,
+                         uint16_t *output, ConvParams p, void *stream) {
+  if (p.tokens == 0 || p.channels == 0)
+    return LLMI_HIP_OK;
+  if (!causal_conv_supported(p.kernelSize))
+    return fail(LLMI_HIP_UNSUPPORTED, "causalConv: kernel size %u (1..8 supported)",
+                p.kernelSize);
+  if (!input || !weight || !output || (p.kernelSize > 1 && !history))
+    return fail(LLMI_HIP_INVALID_ARGUMENT, "causalConv: null buffer");
+  if (!fits32(p.tokens, p.channels, 1) || !fits32(p.channels, p.kernelSize, 1))
+    return fail(LLMI_HIP_INVALID_ARGUMENT, "causalConv: exceeds the 32-bit index range");
+  return launched(launch_causal_conv(input, weight, history, output, p.tokens, p.channels,
+                                     p.kernelSize, p.applySilu ? 1u : 0u,
+                                     static_cast<hipStream_t>(stream)),
+                  "causalConv");
+}
+
+int llmi_hip_l2_norm(const uint16_t *input, float *output, L2Params p, void *stream) {
+  if (p.rows == 0 || p.width == 0)
+    return LLMI_HIP_OK;
+  if (!input || !output)
+    return fail(LLMI_HIP_INVALID_ARGUMENT, "l2NormF32: null buffer");
+  if (!fits32(p.rows, p.width, 1))
+    return fail(LLMI_HIP_INVALID_ARGUMENT, "l2NormF32: exceeds the 32-bit index range");
+  return launched(launch_l2_norm(input, output, p.rows, p.width, p.epsilon, p.scale,
+                                 static_cast<hipStream_t>(stream)),
+                  "l2NormF32");
+}
+
+int llmi_hip_delta_gates(const uint16_t *a, const uint16_t *b, const float *a_log,
+                         const float *dt_bias, float *beta, float *decay, RowParams p,
+                         void *stream) {
+  if (p.rows == 0 || p.width == 0)
+    return LLMI_HIP_OK;
+  if (!a || !b || !a_log || !dt_bias || !beta || !decay)
+    return fail(LLMI_HIP_INVALID_ARGUMENT, "deltaGates: null buffer");
+  if (!fits32(p.rows, p.width, 1))
+    return fail(LLMI_HIP_INVALID_ARGUMENT, "deltaGates: exceeds the 32-bit index range");
+  return launched(launch_delta_gates(a, b, a_log, dt_bias, beta, decay, p.rows, p.width,
+                                     static_cast<hipStream_t>(stream)),
+                  "deltaGates");
+}
+
 int llmi_hip_cache_append(const uint16_t *src, uint16_t *cache, CacheParams p,
                           void *stream) {
   if (p.count && (!src || !cache))
@@ -398,6 +441,18 @@ unsigned llmi_hip_dispatch_count(int op, const void *params) {
   }
   case LLMI_HIP_OP_SIGMOID_MUL:
     return static_cast<const ElementParams *>(params)->count ? 1 : 0;
+  case LLMI_HIP_OP_CAUSAL_CONV: {
+    const ConvParams &p = *static_cast<const ConvParams *>(params);
+    return p.tokens && p.channels && causal_conv_supported(p.kernelSize) ? 1 : 0;
+  }
+  case LLMI_HIP_OP_L2_NORM: {
+    const L2Params &p = *static_cast<const L2Params *>(params);
+    return p.rows && p.width ? 1 : 0;
+  }
+  case LLMI_HIP_OP_DELTA_GATES: {
+    const RowParams &p = *static_cast<const RowParams *>(params);
+    return p.rows && p.width ? 1 : 0;
+  }
   }
   return 0;
 }
@@ -454,6 +509,14 @@ const char *llmi_hip_kernel_name(int op, const void *params, unsigned index) {
                              0, false);
     return rope_kernel_name_index(s) == 0 ? "partialRopeTile" : "partialRopeRows";
   }
+  case LLMI_HIP_OP_CAUSAL_CONV:
+    return "causalConv";
+  case LLMI_HIP_OP_L2_NORM:
+    return l2_norm_tiled(static_cast<const L2Params *>(params)->width, nullptr, nullptr)
+               ? "l2NormTile"
+               : "l2NormRows";
+  case LLMI_HIP_OP_DELTA_GATES:
+    return "deltaGates";
   case LLMI_HIP_OP_SIGMOID_MUL:
     return sigmoid_mul_vectorised(static_cast<const ElementParams *>(params)->count,
                                   nullptr, nullptr, nullptr)

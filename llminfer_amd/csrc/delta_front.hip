@@ -1,0 +1,236 @@
+// The DeltaNet layer's front end, ahead of DeltaUpdate: the depthwise causal
+// convolution with its history rows and SiLU (causalConv,
+// Reference.metal:137-161), the per-head L2 normalisation of q and k to fp32
+// (l2NormF32, Graph.metal:96-109) and the gates (deltaGates,
+// Graph.metal:131-144, with logistic and stableSoftplus,
+// Reference.metal:4-12). Results equal the reference's expressions in IEEE
+// fp32, in its order, bit for bit, with exp and log correctly rounded (the
+// oracle's convention; see exact_fp.hpp for how the roundings are kept).
+//
+// causalConv: the recurrence over tokens is only the sliding window of the
+// last k-1 inputs, so a thread takes one channel and a block of 16 tokens,
+// reading its window from the inputs before the block (or, for the first
+// block, from the history rows). Only the first block's thread reads the
+// history, and it writes the new history (the last k-1 positions of the
+// sequence) after reading, so no thread races it. Loads and stores are
+// coalesced across the channels of a wave.
+//
+// l2NormF32: one wave per 64 rows; the rows are staged in LDS with 16-byte
+// coalesced loads, lane r sums row r in index order (the reference's fma
+// chain), and the fp32 outputs leave as 16-byte stores. Other widths and
+// unaligned buffers take a thread per row.
+//
+// deltaGates: one thread per (token, head).
+#include "exact_fp.hpp"
+#include "hip_common.hpp"
+#include "kernels.hpp"
+
+namespace llmi {
+namespace {
+
+constexpr unsigned kConvBlock = 16; // tokens per thread
+constexpr unsigned kMaxKernel = 8;  // filter taps supported (history 7)
+
+// fp16(silu(h)) for an fp16 value h: silu(h) = h * logistic(h) in fp32.
+__device__ __forceinline__ uint16_t silu16(float h) {
+  float y = mul32(h, logistic_estimate(h));
+  if (!f16_settled(y))
+    y = mul32(h, logistic_exact(h));
+  return f2h(y);
+}
+
+__global__ __launch_bounds__(256) void causal_conv_kernel(
+    const uint16_t *__restrict__ in, const uint16_t *__restrict__ w, uint16_t *hist,
+    uint16_t *__restrict__ out, unsigned T, unsigned C, unsigned k, unsigned silu) {
+  const unsigned c = blockIdx.x * 256 + threadIdx.x;
+  if (c >= C)
+    return;
+  const unsigned hs = k - 1;
+  const unsigned t0 = blockIdx.y * kConvBlock;
+  const unsigned t1 = min(T, t0 + kConvBlock);
+  float wf[kMaxKernel];
+#pragma unroll
+  for (unsigned j = 0; j < kMaxKernel; ++j)
+    wf[j] = j < k ? h2f(w[c * k + j]) : 0.0f;
+  // window[j] = the input at position t - hs + j (negative positions are
+  // history slot hs + position)
+  uint16_t win[kMaxKernel - 1];
+  uint16_t old[kMaxKernel - 1];
+#pragma unroll
+  for (unsigned j = 0; j < kMaxKernel - 1; ++j) {
+    old[j] = (t0 == 0 && j < hs) ? hist[c * hs + j] : 0;
+    int pos = (int)t0 - (int)hs + (int)j;
+    win[j] = j < hs ? (pos < 0 ? old[j] : in[(unsigned)pos * C + c]) : 0;
+  }
+  for (unsigned t = t0; t < t1; ++t) {
+    uint16_t cur = in[t * C + c];
+    float acc = mul32(h2f(cur), wf[hs]);
+#pragma unroll
+    for (unsigned j = 0; j < kMaxKernel - 1; ++j)
+      if (j < hs)
+        acc = __builtin_fmaf(h2f(win[j]), wf[j], acc);
+    out[t * C + c] = silu ? silu16(round16(acc)) : f2h(acc);
+#pragma unroll
+    for (unsigned j = 0; j + 1 < kMaxKernel - 1; ++j)
+      if (j + 1 < hs)
+        win[j] = win[j + 1];
+    if (hs)
+      win[hs - 1] = cur;
+  }
+  if (t0 == 0) {
+    // new history: positions T - hs .. T - 1 of [old history, inputs]
+#pragma unroll
+    for (unsigned j = 0; j < kMaxKernel - 1; ++j) {
+      if (j < hs) {
+        int pos = (int)T - (int)hs + (int)j;
+        uint16_t v = 0;
+        if (pos >= 0) {
+          v = in[(unsigned)pos * C + c];
+        } else {
+#pragma unroll
+          for (unsigned m = 0; m < kMaxKernel - 1; ++m)
+            v = (int)m == (int)hs + pos ? old[m] : v;
+        }
+        hist[c * hs + j] = v;
+      }
+    }
+  }
+}
+
+__device__ __forceinline__ float l2_factor(float sum, float eps, float scale) {
+  return mul32(__fdiv_rn(1.0f, sqrt_cr(__fadd_rn(sum, eps))), scale);
+}
+
+// Rows of `width` (a multiple of 8, <= 256) halves, 64 per wave.
+__global__ __launch_bounds__(64) void l2_norm_tile(const uint16_t *__restrict__ in,
+                                                   float *__restrict__ out, unsigned rows,
+                                                   unsigned width, float eps, float scale) {
+  __shared__ __align__(16) uint16_t tile[64 * (256 + 8)];
+  __shared__ float fac[64];
+  const unsigned lane = threadIdx.x, pitch = width + 8, cpr = width / 8;
+  const unsigned row0 = blockIdx.x * 64, nrows = min(64u, rows - row0);
+  const unsigned chunks = nrows * cpr;
+  for (unsigned c = lane; c < chunks; c += 64) {
+    unsigned r = c / cpr, col = c - r * cpr;
+    *reinterpret_cast<uint4_t *>(tile + r * pitch + col * 8) =
+        *reinterpret_cast<const uint4_t *>(in + (row0 + r) * width + col * 8);
+  }
+  __syncthreads();
+  if (lane < nrows) {
+    const uint16_t *row = tile + lane * pitch;
+    float sum = 0.0f;
+    for (unsigned k = 0; k < cpr; ++k) {
+      uint4_t q = *reinterpret_cast<const uint4_t *>(row + 8 * k);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        float lo = h2f((uint16_t)(q[e] & 0xFFFFu)), hi = h2f((uint16_t)(q[e] >> 16));
+        sum = __builtin_fmaf(lo, lo, sum);
+        sum = __builtin_fmaf(hi, hi, sum);
+      }
+    }
+    fac[lane] = l2_factor(sum, eps, scale);
+  }
+  __syncthreads();
+  const unsigned quads = nrows * (width / 4), qpr = width / 4;
+  for (unsigned c = lane; c < quads; c += 64) {
+    unsigned r = c / qpr, col = c - r * qpr;
+    const uint16_t *src = tile + r * pitch + col * 4;
+    float f = fac[r];
+    float4_t o;
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      o[e] = mul32(h2f(src[e]), f);
+    *reinterpret_cast<float4_t *>(out + (row0 + r) * width + col * 4) = o;
+  }
+}
+
+__global__ __launch_bounds__(256) void l2_norm_rows(const uint16_t *__restrict__ in,
+                                                    float *__restrict__ out, unsigned rows,
+                                                    unsigned width, float eps, float scale) {
+  unsigned r = blockIdx.x * 256 + threadIdx.x;
+  if (r >= rows)
+    return;
+  const uint16_t *x = in + (size_t)r * width;
+  float sum = 0.0f;
+  for (unsigned i = 0; i < width; ++i) {
+    float f = h2f(x[i]);
+    sum = __builtin_fmaf(f, f, sum);
+  }
+  float f = l2_factor(sum, eps, scale);
+  for (unsigned i = 0; i < width; ++i)
+    out[(size_t)r * width + i] = mul32(h2f(x[i]), f);
+}
+
+__device__ __forceinline__ float exp_cr(float x) { return (float)exp((double)x); }
+__device__ __forceinline__ float log_cr(float x) { return (float)log((double)x); }
+
+// stableSoftplus (Reference.metal:8-12) with correctly rounded exp and log.
+__device__ __forceinline__ float stable_softplus(float x) {
+  float e = exp_cr(-fabsf(x));
+  float tail = e < 1e-4f ? mul32(e, __fsub_rn(1.0f, mul32(0.5f, e))) : log_cr(__fadd_rn(1.0f, e));
+  return __fadd_rn(fmaxf(x, 0.0f), tail);
+}
+
+__global__ __launch_bounds__(256) void delta_gates_kernel(
+    const uint16_t *__restrict__ a, const uint16_t *__restrict__ b,
+    const float *__restrict__ a_log, const float *__restrict__ dt_bias,
+    float *__restrict__ beta, float *__restrict__ decay, unsigned count, unsigned width) {
+  unsigned i = blockIdx.x * 256 + threadIdx.x;
+  if (i >= count)
+    return;
+  unsigned head = i % width;
+  float bf = h2f(b[i]);
+  float s = logistic_estimate(bf);
+  if (!f16_settled(s))
+    s = logistic_exact(bf);
+  beta[i] = round16(s);
+  float sp = stable_softplus(__fadd_rn(h2f(a[i]), dt_bias[head]));
+  decay[i] = exp_cr(mul32(-exp_cr(a_log[head]), sp));
+}
+
+bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+} // namespace
+
+bool causal_conv_supported(unsigned k) { return k >= 1 && k <= kMaxKernel; }
+
+hipError_t launch_causal_conv(const uint16_t *in, const uint16_t *w, uint16_t *hist,
+                              uint16_t *out, unsigned T, unsigned C, unsigned k,
+                              unsigned silu, hipStream_t stream) {
+  if (T == 0 || C == 0)
+    return hipSuccess;
+  dim3 grid((C + 255) / 256, (T + kConvBlock - 1) / kConvBlock);
+  hipLaunchKernelGGL(causal_conv_kernel, grid, dim3(256), 0, stream, in, w, hist, out, T, C,
+                     k, silu);
+  return hipGetLastError();
+}
+
+bool l2_norm_tiled(unsigned width, const void *in, const void *out) {
+  return width % 8 == 0 && width <= 256 && aligned16(in) && aligned16(out);
+}
+
+hipError_t launch_l2_norm(const uint16_t *in, float *out, unsigned rows, unsigned width,
+                          float eps, float scale, hipStream_t stream) {
+  if (rows == 0 || width == 0)
+    return hipSuccess;
+  if (l2_norm_tiled(width, in, out))
+    hipLaunchKernelGGL(l2_norm_tile, dim3((rows + 63) / 64), dim3(64), 0, stream, in, out,
+                       rows, width, eps, scale);
+  else
+    hipLaunchKernelGGL(l2_norm_rows, dim3((rows + 255) / 256), dim3(256), 0, stream, in, out,
+                       rows, width, eps, scale);
+  return hipGetLastError();
+}
+
+hipError_t launch_delta_gates(const uint16_t *a, const uint16_t *b, const float *a_log,
+                              const float *dt_bias, float *beta, float *decay,
+                              unsigned rows, unsigned width, hipStream_t stream) {
+  unsigned count = rows * width;
+  if (count == 0)
+    return hipSuccess;
+  hipLaunchKernelGGL(delta_gates_kernel, dim3((count + 255) / 256), dim3(256), 0, stream, a, b,
+                     a_log, dt_bias, beta, decay, count, width);
+  return hipGetLastError();
+}
+
+} // namespace llmi

@@ -93,4 +93,16 @@ bool sigmoid_mul_vectorised(unsigned count, const void *g, const void *x, const 
 hipError_t launch_sigmoid_mul(const uint16_t *gate, const uint16_t *in, uint16_t *out,
                               unsigned count, hipStream_t stream);
 
+// ------------------------------------------------------ DeltaNet front end
+bool causal_conv_supported(unsigned k);
+hipError_t launch_causal_conv(const uint16_t *in, const uint16_t *w, uint16_t *hist,
+                              uint16_t *out, unsigned T, unsigned C, unsigned k,
+                              unsigned silu, hipStream_t stream);
+bool l2_norm_tiled(unsigned width, const void *in, const void *out);
+hipError_t launch_l2_norm(const uint16_t *in, float *out, unsigned rows, unsigned width,
+                          float eps, float scale, hipStream_t stream);
+hipError_t launch_delta_gates(const uint16_t *a, const uint16_t *b, const float *a_log,
+                              const float *dt_bias, float *beta, float *decay,
+                              unsigned rows, unsigned width, hipStream_t stream);
+
 } // namespace llmi

@@ -40,6 +40,7 @@
 // rotaryDim/2 not a multiple of 8 halves, unaligned pointers, headDim > 2048)
 // run the row kernel: one thread per row, the reference's own structure,
 // with the same arithmetic.
+#include "exact_fp.hpp"
 #include "hip_common.hpp"
 #include "kernels.hpp"
 
@@ -53,31 +54,6 @@ namespace {
 constexpr int kPad = 8;                 // halves of LDS padding per tile row
 constexpr unsigned kTileHalves = 8192;  // rows * headDim bound of one tile
 constexpr unsigned kTileIters = kTileHalves / 8 / 64;
-
-__device__ __forceinline__ float h2f(uint16_t b) {
-  return (float)__builtin_bit_cast(half_t, b);
-}
-__device__ __forceinline__ uint16_t f2h(float x) {
-  return __builtin_bit_cast(uint16_t, (half_t)x);
-}
-// The value, hidden from the optimiser, so that the operation producing it
-// is selected as written and rounded on its own.
-__device__ __forceinline__ float opaque(float x) {
-  asm volatile("" : "+v"(x));
-  return x;
-}
-__device__ __forceinline__ float mul32(float a, float b) { return opaque(a * b); }
-__device__ __forceinline__ float round16(float x) { return opaque((float)(half_t)x); }
-
-// True when every float within `margin` (relative) of v has the same fp16
-// rounding as v (fp16 rounding is monotonic, so the two ends decide).
-template <int kLog2Margin = 19>
-__device__ __forceinline__ bool f16_settled(float v) {
-  constexpr float m = 1.0f / (float)(1u << kLog2Margin);
-  half_t a = (half_t)__fmul_rn(v, 1.0f - m);
-  half_t b = (half_t)__fmul_rn(v, 1.0f + m);
-  return __builtin_bit_cast(uint16_t, a) == __builtin_bit_cast(uint16_t, b);
-}
 
 // fp16(cos(phase)), fp16(sin(phase)) of the correctly rounded fp32 values.
 __device__ __forceinline__ float2 rope_cos_sin(float phase) {
@@ -101,8 +77,7 @@ __device__ __forceinline__ float rope_inv_freq(float theta, unsigned pair,
 }
 
 __device__ __forceinline__ float rms_scale_of(float sum, unsigned width, float eps) {
-  float m = __fadd_rn(__fdiv_rn(sum, (float)width), eps);
-  return __fdiv_rn(1.0f, (float)__builtin_sqrt((double)m));
+  return __fdiv_rn(1.0f, sqrt_cr(__fadd_rn(__fdiv_rn(sum, (float)width), eps)));
 }
 
 __device__ __forceinline__ float normed(uint16_t v, float scale, float w1) {
@@ -349,21 +324,6 @@ __global__ __launch_bounds__(256) void norm_rope_rows(const uint16_t *in,
   }
   for (unsigned i = a.rot; i < a.D; ++i)
     dst[i] = kNorm ? f2h(normed(head[i], scale, 1.0f + w[i])) : head[i];
-}
-
-// logistic(g) = 1 / (1 + exp(-g)) with exp(-g) as 2^(-g log2 e) on the
-// hardware exp2 and the hardware reciprocal. Relative error: |g| 2^-24 from
-// the rounded argument plus about 2^-22 from the three instructions, at most
-// 1.3 * 2^-20 while the result can still round to a nonzero fp16
-// (g > -17.4), which the 2^-19 margin of f16_settled covers. Below that the
-// estimate and the exact value both round to 0, above g = 16 both to 1.
-__device__ __forceinline__ float logistic_estimate(float g) {
-  return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-g * kLog2e));
-}
-
-// The correctly rounded fp32 exp (double, rounded once), as in the oracle.
-__device__ __forceinline__ float logistic_exact(float g) {
-  return __fdiv_rn(1.0f, __fadd_rn(1.0f, (float)exp(-(double)g)));
 }
 
 // fp16(logistic(g)) of the correctly rounded fp32 exp.

@@ -129,6 +129,68 @@ def sigmoid_mul(gate: torch.Tensor, x: torch.Tensor, out: torch.Tensor) -> None:
     bind_sigmoid_mul(gate, x, out)()
 
 
+def bind_causal_conv(x: torch.Tensor, weight: torch.Tensor, history: torch.Tensor | None,
+                     out: torch.Tensor, silu: bool = True) -> "Bound":
+    """causalConv (Reference.metal:137-161): x, out [T, C] fp16; weight [C, k]
+    fp16; history [C, k-1] fp16, updated in place."""
+    for t, n in ((x, "x"), (weight, "weight"), (out, "out")):
+        _require(t, torch.float16, n)
+    if x.dim() != 2 or out.shape != x.shape or weight.dim() != 2 or weight.shape[0] != x.shape[1]:
+        raise ValueError("x, out are [T, C] and weight [C, k]")
+    T, Cn = x.shape
+    k = weight.shape[1]
+    if k > 1:
+        if history is None:
+            raise ValueError("history is required for k > 1")
+        _require(history, torch.float16, "history")
+        if tuple(history.shape) != (Cn, k - 1):
+            raise ValueError("history is [C, k-1]")
+    p = _lib.ConvParams(T, Cn, k, int(silu))
+    return Bound(_lib.load().llmi_hip_causal_conv,
+                 (_ptr(x), _ptr(weight), _ptr(history), _ptr(out), p, _stream()), "causalConv")
+
+
+def causal_conv(*args, **kwargs) -> None:
+    bind_causal_conv(*args, **kwargs)()
+
+
+def bind_l2_norm(x: torch.Tensor, out: torch.Tensor, width: int, epsilon: float = 1e-6,
+                 scale: float = 1.0) -> "Bound":
+    """l2NormF32 (Graph.metal:96-109): groups of `width` fp16 values -> fp32."""
+    _require(x, torch.float16, "x")
+    _require(out, torch.float32, "out")
+    if out.numel() != x.numel() or width <= 0 or x.numel() % width:
+        raise ValueError("x and out must hold whole rows of `width`")
+    p = _lib.L2Params(x.numel() // width, width, epsilon, scale)
+    return Bound(_lib.load().llmi_hip_l2_norm, (_ptr(x), _ptr(out), p, _stream()),
+                 kernel_names(_lib.OP_L2_NORM, p)[0] if x.numel() else "l2Norm")
+
+
+def l2_norm(*args, **kwargs) -> None:
+    bind_l2_norm(*args, **kwargs)()
+
+
+def bind_delta_gates(a: torch.Tensor, b: torch.Tensor, a_log: torch.Tensor,
+                     dt_bias: torch.Tensor, beta: torch.Tensor, decay: torch.Tensor) -> "Bound":
+    """deltaGates (Graph.metal:131-144): a, b [T, Hv] fp16; a_log, dt_bias
+    [Hv] fp32; beta, decay [T, Hv] fp32."""
+    for t, n in ((a, "a"), (b, "b")):
+        _require(t, torch.float16, n)
+    for t, n in ((a_log, "a_log"), (dt_bias, "dt_bias"), (beta, "beta"), (decay, "decay")):
+        _require(t, torch.float32, n)
+    if a.dim() != 2 or b.shape != a.shape or beta.shape != a.shape or decay.shape != a.shape \
+            or a_log.numel() != a.shape[1] or dt_bias.numel() != a.shape[1]:
+        raise ValueError("gate operand shapes disagree")
+    p = _lib.RowParams(a.shape[0], a.shape[1], 0.0)
+    return Bound(_lib.load().llmi_hip_delta_gates,
+                 (_ptr(a), _ptr(b), _ptr(a_log), _ptr(dt_bias), _ptr(beta), _ptr(decay), p,
+                  _stream()), "deltaGates")
+
+
+def delta_gates(*args) -> None:
+    bind_delta_gates(*args)()
+
+
 def kv_append(k: torch.Tensor, v: torch.Tensor, k_cache: torch.Tensor,
               v_cache: torch.Tensor, past: int) -> None:
     """KvAppend: rows [past, past+T) of both caches <- k, v ([T, Hkv, d])."""

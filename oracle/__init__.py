@@ -73,6 +73,7 @@ def lib() -> C.CDLL:
         L.orc_l2norm_f32.argtypes = [_u16p, _f32p, _u32, _u32, C.c_float, C.c_float]
         L.orc_norm_rope.argtypes = [_u16p, _f32p, _u16p] + [_u32] * 7 + [C.c_float, C.c_float]
         L.orc_sigmoid_mul.argtypes = [_u16p, _u16p, _u16p, C.c_size_t]
+        L.orc_causal_conv.argtypes = [_u16p, _u16p, _u16p, _u16p] + [_u32] * 4
         for name, n in (("orc_cost_kv_append", 3), ("orc_cost_causal_gqa", 5),
                         ("orc_cost_delta_update", 5)):
             fn = getattr(L, name)
@@ -237,6 +238,19 @@ def norm_rope(x, weight, tokens: int, heads: int, head_dim: int, rotary_dim: int
     lib().orc_norm_rope(a, w, output.reshape(-1), tokens, heads, head_dim, rotary_dim,
                         head_stride, past, output_start, epsilon, theta)
     return output
+
+
+def causal_conv(x, weight, history, apply_silu: bool = True) -> np.ndarray:
+    """causalConv (Reference.metal:137-161) on fp16 bits: x [T, C], weight
+    [C, k], history [C, k-1] (updated in place); returns the output [T, C]."""
+    a = np.ascontiguousarray(x, np.uint16)
+    w = np.ascontiguousarray(weight, np.uint16)
+    assert history.dtype == np.uint16 and history.flags.c_contiguous
+    T, Cn = a.shape
+    out = np.empty_like(a)
+    lib().orc_causal_conv(a.reshape(-1), w.reshape(-1), history.reshape(-1), out.reshape(-1),
+                          T, Cn, w.shape[1], int(apply_silu))
+    return out
 
 
 def sigmoid_mul(gate, x) -> np.ndarray:

@@ -618,10 +618,21 @@ void orc_delta_chunked_f64(const float *q, const float *k, const uint16_t *v,
 }
 
 /* Reference.metal:4-12. */
-static float logistic(float x) { return 1.0f / (1.0f + expf(-x)); }
+/* The fp32 pow/cos/sin/exp/log of the reference kernels, taken correctly
+ * rounded: evaluated in double and rounded to float once. The device kernels
+ * produce the same float (a fast fp32 evaluation with a margin test, else the
+ * same double evaluation), so results compare bit for bit. */
+static float orc_powf_cr(float x, float y) { return (float)pow((double)x, (double)y); }
+static float orc_cosf_cr(float x) { return (float)cos((double)x); }
+static float orc_sinf_cr(float x) { return (float)sin((double)x); }
+static float orc_expf_cr(float x) { return (float)exp((double)x); }
+static float orc_logf_cr(float x) { return (float)log((double)x); }
+
+/* logistic and stableSoftplus, Reference.metal:4, 8-12. */
+static float logistic(float x) { return 1.0f / (1.0f + orc_expf_cr(-x)); }
 static float stable_softplus(float x) {
-  float e = expf(-fabsf(x));
-  float tail = e < 1e-4f ? e * (1.0f - 0.5f * e) : logf(1.0f + e);
+  float e = orc_expf_cr(-fabsf(x));
+  float tail = e < 1e-4f ? e * (1.0f - 0.5f * e) : orc_logf_cr(1.0f + e);
   return (x > 0.0f ? x : 0.0f) + tail;
 }
 
@@ -631,8 +642,8 @@ void orc_delta_gates(const uint16_t *a, const uint16_t *b, const float *a_log,
   for (size_t i = 0; i < (size_t)T * Hv; ++i) {
     uint32_t h = (uint32_t)(i % Hv);
     beta[i] = round_f16(logistic(orc_f16_to_f32(b[i])));
-    decay[i] = expf(-expf(a_log[h]) *
-                    stable_softplus(orc_f16_to_f32(a[i]) + dt_bias[h]));
+    decay[i] = orc_expf_cr(-orc_expf_cr(a_log[h]) *
+                           stable_softplus(orc_f16_to_f32(a[i]) + dt_bias[h]));
   }
 }
 
@@ -651,6 +662,38 @@ void orc_l2norm_f32(const uint16_t *in, float *out, uint32_t rows,
   }
 }
 
+/* causalConv, Reference.metal:137-161 (ConvParams, ReferenceParams.h:32-34):
+ * per channel, acc = x_t * w[k-1] + sum_j history_j * w[j] (fma in j order),
+ * output fp16(acc) or fp16(silu(fp16(acc))), then the k-1 history slots shift
+ * left and take x_t. Layout: input/output [tokens][channels], weight
+ * [channels][k], history [channels][k-1], all fp16; history updated in place. */
+void orc_causal_conv(const uint16_t *input, const uint16_t *weight, uint16_t *history,
+                     uint16_t *output, uint32_t tokens, uint32_t channels,
+                     uint32_t kernel_size, uint32_t apply_silu) {
+  uint32_t hs = kernel_size - 1;
+  for (uint32_t c = 0; c < channels; ++c) {
+    uint16_t *recent = history + (size_t)c * hs;
+    const uint16_t *filter = weight + (size_t)c * kernel_size;
+    for (uint32_t t = 0; t < tokens; ++t) {
+      size_t i = (size_t)t * channels + c;
+      uint16_t current = input[i];
+      float acc = orc_f16_to_f32(current) * orc_f16_to_f32(filter[hs]);
+      for (uint32_t j = 0; j < hs; ++j)
+        acc = fmaf(orc_f16_to_f32(recent[j]), orc_f16_to_f32(filter[j]), acc);
+      if (apply_silu) {
+        float h = round_f16(acc);
+        output[i] = orc_f32_to_f16(h * logistic(h));
+      } else {
+        output[i] = orc_f32_to_f16(acc);
+      }
+      for (uint32_t j = 1; j < hs; ++j)
+        recent[j - 1] = recent[j];
+      if (hs)
+        recent[hs - 1] = current;
+    }
+  }
+}
+
 /* ---------------------------------------------------- norm, rope, gate */
 
 static float orc_round_f16(float x) { return orc_f16_to_f32(orc_f32_to_f16(x)); }
@@ -666,14 +709,6 @@ static float orc_rms_scale(const uint16_t *x, uint32_t width, float eps) {
   return 1.0f / sqrtf(sum / (float)width + eps);
 }
 
-/* The fp32 pow/cos/sin/exp of the reference kernels, taken correctly
- * rounded: evaluated in double and rounded to float once. The device kernels
- * produce the same float (a fast fp32 evaluation with a margin test, else the
- * same double evaluation), so results compare bit for bit. */
-static float orc_powf_cr(float x, float y) { return (float)pow((double)x, (double)y); }
-static float orc_cosf_cr(float x) { return (float)cos((double)x); }
-static float orc_sinf_cr(float x) { return (float)sin((double)x); }
-static float orc_expf_cr(float x) { return (float)exp((double)x); }
 
 /* rotatePair, Reference.metal:262-269. */
 static void orc_rotate_pair(float in_x, float in_y, float position, float theta,

@@ -131,6 +131,15 @@ void orc_delta_gates(const uint16_t *a, const uint16_t *b, const float *a_log,
 void orc_l2norm_f32(const uint16_t *in, float *out, uint32_t rows,
                     uint32_t width, float eps, float scale);
 
+/* causalConv (lib/Backend/Metal/Kernels/Reference.metal:137-161): the
+ * DeltaNet depthwise causal convolution with its k-1 history rows (updated
+ * in place), optionally followed by SiLU (silu(x) = x * logistic(x) in fp32,
+ * exp correctly rounded). input/output [tokens][channels], weight
+ * [channels][kernel_size], history [channels][kernel_size - 1], fp16. */
+void orc_causal_conv(const uint16_t *input, const uint16_t *weight, uint16_t *history,
+                     uint16_t *output, uint32_t tokens, uint32_t channels,
+                     uint32_t kernel_size, uint32_t apply_silu);
+
 /* Fused q/k RmsNorm + PartialRoPE of the reference graph, normRope
  * (lib/Backend/Metal/Kernels/Reference.metal:271-293 with rmsScale :98-103
  * and rotatePair :262-269; RopeParams, ReferenceParams.h:44-47). Row r of

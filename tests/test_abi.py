@@ -107,6 +107,27 @@ def test_plan_records_row_ops():
         ["sigmoidMulScalar"]
 
 
+def test_delta_front_abi():
+    from llminfer_amd import ops
+    assert C.sizeof(_lib.ConvParams) == 16 and C.sizeof(_lib.L2Params) == 16
+    lib = _lib.load()
+    assert lib.llmi_hip_causal_conv(1, 1, 1, 1, _lib.ConvParams(4, 8, 9, 1), None) == \
+        _lib.UNSUPPORTED
+    assert lib.llmi_hip_causal_conv(1, 1, None, 1, _lib.ConvParams(4, 8, 4, 1), None) == \
+        _lib.INVALID_ARGUMENT
+    assert lib.llmi_hip_causal_conv(None, None, None, None, _lib.ConvParams(0, 8, 4, 1),
+                                    None) == _lib.OK
+    assert lib.llmi_hip_l2_norm(None, 1, _lib.L2Params(4, 128, 1e-6, 1.0), None) == \
+        _lib.INVALID_ARGUMENT
+    assert lib.llmi_hip_delta_gates(1, 1, 1, None, 1, 1, _lib.RowParams(4, 32, 0), None) == \
+        _lib.INVALID_ARGUMENT
+    assert ops.kernel_names(_lib.OP_CAUSAL_CONV, _lib.ConvParams(1024, 8192, 4, 1)) == \
+        ["causalConv"]
+    assert ops.kernel_names(_lib.OP_L2_NORM, _lib.L2Params(64, 128, 1e-6, 1.0)) == ["l2NormTile"]
+    assert ops.kernel_names(_lib.OP_L2_NORM, _lib.L2Params(64, 100, 1e-6, 1.0)) == ["l2NormRows"]
+    assert ops.kernel_names(_lib.OP_DELTA_GATES, _lib.RowParams(1024, 32, 0)) == ["deltaGates"]
+
+
 def test_invalid_gqa_rejected_before_launch():
     lib = _lib.load()
     bad = [_lib.GqaParams(0, 16, 4, 256, 0),     # no tokens
