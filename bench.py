@@ -395,6 +395,119 @@ class AttnRows(Workload):
                 "gpu_bit_exact": exact}
 
 
+def front_bytes(T: int, hk: int, dk: int, hv: int, dv: int, k: int = 4) -> dict:
+    """Algorithmic HBM bytes of the DeltaNet front end per call: the conv
+    reads and writes [T, C] fp16 (C = 2 hk dk + hv dv) plus its weights and
+    history; each L2 norm reads [T, hk dk] fp16 and writes it as fp32; the
+    gates read a, b fp16 and write beta, decay fp32."""
+    C = 2 * hk * dk + hv * dv
+    return {"conv": 2 * T * C * 2 + C * k * 2 + 2 * C * (k - 1) * 2,
+            "l2norm_q": T * hk * dk * 6, "l2norm_k": T * hk * dk * 6,
+            "gates": T * hv * 12 + hv * 8}
+
+
+class DeltaFront(Workload):
+    """The DeltaNet layer's front end ahead of DeltaUpdate
+    (Qwen35ModelBuilder.cpp:146-160): causalConv + SiLU over q, k, v
+    (8192 channels, 4 taps, history carried), the L2 norms of q (scaled by
+    1/sqrt(dk)) and k to fp32, and the gates. Inputs rotate over sets larger
+    than the MALL."""
+    bound = "hbm"
+    labels = ("conv", "l2norm_q", "l2norm_k", "gates")
+    dominant = "conv"
+
+    def __init__(self, dev, T, sets, seed, hk=16, dk=128, hv=32, dv=128, k=4):
+        import torch
+        from llminfer_amd import ops
+        self.T, self.sets, self.shape = T, sets, (hk, dk, hv, dv)
+        self.tokens = T
+        self.name = f"delta_front_T{T}"
+        C = 2 * hk * dk + hv * dv
+        g = torch.Generator(device=dev).manual_seed(seed)
+        self.x = [_randn16(g, (T, C), dev) for _ in range(sets)]
+        self.w = (0.5 * torch.randn(C, k, generator=g, device=dev)).half()
+        self.hist = [_randn16(g, (C, k - 1), dev) for _ in range(sets)]
+        self.y = [torch.empty(T, C, dtype=torch.float16, device=dev) for _ in range(sets)]
+        self.qn = [torch.empty(T, hk * dk, dtype=torch.float32, device=dev) for _ in range(sets)]
+        self.kn = [torch.empty(T, hk * dk, dtype=torch.float32, device=dev) for _ in range(sets)]
+        self.a = [_randn16(g, (T, hv), dev) for _ in range(sets)]
+        self.b = [_randn16(g, (T, hv), dev) for _ in range(sets)]
+        self.a_log = (0.5 * torch.randn(hv, generator=g, device=dev)).float()
+        self.dt = (0.5 * torch.randn(hv, generator=g, device=dev)).float()
+        self.beta = [torch.empty(T, hv, dtype=torch.float32, device=dev) for _ in range(sets)]
+        self.decay = [torch.empty(T, hv, dtype=torch.float32, device=dev) for _ in range(sets)]
+        q_of = lambda s: self.y[s][:, :hk * dk]
+        k_of = lambda s: self.y[s][:, hk * dk:2 * hk * dk]
+        convs = [ops.bind_causal_conv(self.x[s], self.w, self.hist[s], self.y[s], True)
+                 for s in range(sets)]
+        for c in convs:
+            c()
+        torch.cuda.synchronize()
+        # The norms take dense [T, hk*dk] inputs: copies of the conv output's
+        # q and k column blocks, made once, outside the timed region.
+        self.qin = [q_of(s).contiguous() for s in range(sets)]
+        self.kin = [k_of(s).contiguous() for s in range(sets)]
+        self.bound_ops = {
+            "conv": convs,
+            "l2norm_q": [ops.bind_l2_norm(self.qin[s], self.qn[s], dk, 1e-6, dk ** -0.5)
+                         for s in range(sets)],
+            "l2norm_k": [ops.bind_l2_norm(self.kin[s], self.kn[s], dk, 1e-6, 1.0)
+                         for s in range(sets)],
+            "gates": [ops.bind_delta_gates(self.a[s], self.b[s], self.a_log, self.dt,
+                                           self.beta[s], self.decay[s]) for s in range(sets)],
+        }
+        self.bytes = front_bytes(T, hk, dk, hv, dv, k)
+
+    def op(self, label, i):
+        self.bound_ops[label][i % self.sets]()
+
+    def kernels(self):
+        return "causalConv"
+
+    def work(self, i):
+        return self.bytes["conv"]
+
+    def config(self):
+        hk, dk, hv, dv = self.shape
+        return {"workload": self.name, "tokens": self.T, "key_heads": hk, "key_dim": dk,
+                "value_heads": hv, "value_dim": dv, "conv_channels": 2 * hk * dk + hv * dv,
+                "conv_kernel": 4, "sets": self.sets,
+                "ops": "causalConv+SiLU, l2NormF32 (q scaled 1/sqrt(dk), k), deltaGates"}
+
+    def cpu(self, budget_s):
+        import numpy as np
+        import oracle
+        import torch
+        s = 0
+        hk, dk, hv, dv = self.shape
+        x, w = host_u16(self.x[s]), host_u16(self.w)
+        h0 = host_u16(self.hist[s]).copy()
+        for label in self.labels:
+            self.op(label, s)
+        torch.cuda.synchronize()
+        qin, kin = host_u16(self.qin[s]), host_u16(self.kin[s])
+        a, b = host_u16(self.a[s]), host_u16(self.b[s])
+        a_log, dt = host_f32(self.a_log), host_f32(self.dt)
+
+        def step():
+            y = oracle.causal_conv(x, w, h0.copy(), True)
+            qn = oracle.l2norm_f32(qin, dk, 1e-6, dk ** -0.5)
+            kn = oracle.l2norm_f32(kin, dk, 1e-6, 1.0)
+            return y, qn, kn, oracle.delta_gates(a, b, a_log, dt)
+
+        y, qn, kn, (beta, decay) = step()
+        exact = bool(np.array_equal(y, host_u16(self.y[s]))
+                     and np.array_equal(qn.view(np.uint32), host_f32(self.qn[s]).view(np.uint32))
+                     and np.array_equal(kn.view(np.uint32), host_f32(self.kn[s]).view(np.uint32))
+                     and np.array_equal(beta.view(np.uint32), host_f32(self.beta[s]).view(np.uint32))
+                     and np.array_equal(decay.view(np.uint32), host_f32(self.decay[s]).view(np.uint32)))
+        sec, runs = time_cpu(step, budget_s)
+        return {"value": sec * 1e6, "unit": "µs/layer", "cores": 1, "kind": "port",
+                "sample": f"the four ops on one input set (T={self.T}), {runs} runs, scalar C "
+                          "oracle (orc_causal_conv, orc_l2norm_f32, orc_delta_gates)",
+                "gpu_bit_exact": exact}
+
+
 def _delta_inputs(g, dev, T, hk, dk, hv, dv):
     """DeltaUpdate operands as the reference graph produces them: L2-normalised
     fp32 q (x 1/sqrt(dk)) and k from fp16 N(0,1) (Graph.metal:96-109), fp16 v,
@@ -705,6 +818,8 @@ def main(argv=None) -> int:
             ("cfg4_hybrid_decode_32k", lambda: HybridDecode(dev)),
             ("next_attn_rows_prefill_2048", lambda: AttnRows(dev, 2048, 2048, 6, seed=6)),
             ("next_attn_rows_decode_4k", lambda: AttnRows(dev, 1, 4096, 64, seed=7)),
+            ("next_delta_front_1024", lambda: DeltaFront(dev, 1024, 8, seed=8)),
+            ("next_delta_front_decode", lambda: DeltaFront(dev, 1, 64, seed=9)),
         ]
         for key, make in builders:
             x = make()
@@ -723,7 +838,7 @@ def main(argv=None) -> int:
                 kern_s = entry["roofline"]["kernel_us_avg"] * 1e-6
                 entry["mfma_frac_recurrent_flops"] = round(
                     delta_flops(x.T, x.hv, x.dk, x.dv) / kern_s / 1e12 / MFMA_F16_PEAK_TFS, 5)
-            if isinstance(x, AttnRows):
+            if isinstance(x, (AttnRows, DeltaFront)):
                 entry["op_roofline"] = {
                     l: {"bytes": x.bytes[l],
                         "achieved_GBs": round(x.bytes[l] / (op_ms[l] * 1e-3) / 1e9, 1),

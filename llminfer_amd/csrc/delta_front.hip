@@ -8,14 +8,15 @@
 // oracle's convention; see exact_fp.hpp for how the roundings are kept).
 //
 // causalConv: the recurrence over tokens is only the sliding window of the
-// last k-1 inputs, so a thread takes one channel and a block of 16 tokens,
+// last k-1 inputs, so a thread takes one channel and a block of 16 tokens
+// (coalesced 2-byte loads across the wave's channels),
 // reading its window from the inputs before the block (or, for the first
 // block, from the history rows). Only the first block's thread reads the
 // history, and it writes the new history (the last k-1 positions of the
 // sequence) after reading, so no thread races it. Loads and stores are
 // coalesced across the channels of a wave.
 //
-// l2NormF32: one wave per 64 rows; the rows are staged in LDS with 16-byte
+// l2NormF32: one wave per 16 rows; the rows are staged in LDS with 16-byte
 // coalesced loads, lane r sums row r in index order (the reference's fma
 // chain), and the fp32 outputs leave as 16-byte stores. Other widths and
 // unaligned buffers take a thread per row.
@@ -30,6 +31,7 @@ namespace {
 
 constexpr unsigned kConvBlock = 16; // tokens per thread
 constexpr unsigned kMaxKernel = 8;  // filter taps supported (history 7)
+constexpr unsigned kL2Rows = 16;    // l2NormF32 rows per wave (16K rows fill 1024 waves)
 
 // fp16(silu(h)) for an fp16 value h: silu(h) = h * logistic(h) in fp32.
 __device__ __forceinline__ uint16_t silu16(float h) {
@@ -97,18 +99,72 @@ __global__ __launch_bounds__(256) void causal_conv_kernel(
   }
 }
 
+// The 4-tap case (Qwen3.5's conv) with the filter length known: a thread's
+// 16 token loads are all issued before the first output is computed (the
+// general kernel's loop waits one load latency per token), and the window
+// lives in registers with fixed indices.
+__global__ __launch_bounds__(256) void causal_conv_k4(
+    const uint16_t *__restrict__ in, const uint16_t *__restrict__ w, uint16_t *hist,
+    uint16_t *__restrict__ out, unsigned T, unsigned C, unsigned silu) {
+  constexpr unsigned hs = 3;
+  const unsigned c = blockIdx.x * 256 + threadIdx.x;
+  if (c >= C)
+    return;
+  const unsigned t0 = blockIdx.y * kConvBlock;
+  float wf[4];
+#pragma unroll
+  for (unsigned j = 0; j < 4; ++j)
+    wf[j] = h2f(w[c * 4 + j]);
+  // xs[u] = the input at position t0 - 3 + u (history for negative positions)
+  uint16_t xs[kConvBlock + hs];
+  uint16_t old[hs];
+#pragma unroll
+  for (unsigned j = 0; j < hs; ++j)
+    old[j] = t0 == 0 ? hist[c * hs + j] : 0;
+#pragma unroll
+  for (unsigned u = 0; u < kConvBlock + hs; ++u) {
+    int pos = (int)t0 - (int)hs + (int)u;
+    xs[u] = pos < 0 ? old[u] : (pos < (int)T ? in[(unsigned)pos * C + c] : 0);
+  }
+#pragma unroll
+  for (unsigned u = 0; u < kConvBlock; ++u) {
+    if (t0 + u < T) {
+      float acc = mul32(h2f(xs[u + hs]), wf[hs]);
+#pragma unroll
+      for (unsigned j = 0; j < hs; ++j)
+        acc = __builtin_fmaf(h2f(xs[u + j]), wf[j], acc);
+      out[(t0 + u) * C + c] = silu ? silu16(round16(acc)) : f2h(acc);
+    }
+  }
+  if (t0 == 0) {
+#pragma unroll
+    for (unsigned j = 0; j < hs; ++j) {
+      int pos = (int)T - (int)hs + (int)j;
+      uint16_t v = 0;
+      if (pos >= 0) {
+        v = in[(unsigned)pos * C + c];
+      } else {
+#pragma unroll
+        for (unsigned m = 0; m < hs; ++m)
+          v = (int)m == (int)hs + pos ? old[m] : v;
+      }
+      hist[c * hs + j] = v;
+    }
+  }
+}
+
 __device__ __forceinline__ float l2_factor(float sum, float eps, float scale) {
   return mul32(__fdiv_rn(1.0f, sqrt_cr(__fadd_rn(sum, eps))), scale);
 }
 
-// Rows of `width` (a multiple of 8, <= 256) halves, 64 per wave.
+// Rows of `width` (a multiple of 8, <= 256) halves, kL2Rows per wave.
 __global__ __launch_bounds__(64) void l2_norm_tile(const uint16_t *__restrict__ in,
                                                    float *__restrict__ out, unsigned rows,
                                                    unsigned width, float eps, float scale) {
-  __shared__ __align__(16) uint16_t tile[64 * (256 + 8)];
-  __shared__ float fac[64];
+  __shared__ __align__(16) uint16_t tile[kL2Rows * (256 + 8)];
+  __shared__ float fac[kL2Rows];
   const unsigned lane = threadIdx.x, pitch = width + 8, cpr = width / 8;
-  const unsigned row0 = blockIdx.x * 64, nrows = min(64u, rows - row0);
+  const unsigned row0 = blockIdx.x * kL2Rows, nrows = min(kL2Rows, rows - row0);
   const unsigned chunks = nrows * cpr;
   for (unsigned c = lane; c < chunks; c += 64) {
     unsigned r = c / cpr, col = c - r * cpr;
@@ -200,8 +256,11 @@ hipError_t launch_causal_conv(const uint16_t *in, const uint16_t *w, uint16_t *h
   if (T == 0 || C == 0)
     return hipSuccess;
   dim3 grid((C + 255) / 256, (T + kConvBlock - 1) / kConvBlock);
-  hipLaunchKernelGGL(causal_conv_kernel, grid, dim3(256), 0, stream, in, w, hist, out, T, C,
-                     k, silu);
+  if (k == 4)
+    hipLaunchKernelGGL(causal_conv_k4, grid, dim3(256), 0, stream, in, w, hist, out, T, C, silu);
+  else
+    hipLaunchKernelGGL(causal_conv_kernel, grid, dim3(256), 0, stream, in, w, hist, out, T,
+                       C, k, silu);
   return hipGetLastError();
 }
 
@@ -214,7 +273,7 @@ hipError_t launch_l2_norm(const uint16_t *in, float *out, unsigned rows, unsigne
   if (rows == 0 || width == 0)
     return hipSuccess;
   if (l2_norm_tiled(width, in, out))
-    hipLaunchKernelGGL(l2_norm_tile, dim3((rows + 63) / 64), dim3(64), 0, stream, in, out,
+    hipLaunchKernelGGL(l2_norm_tile, dim3((rows + kL2Rows - 1) / kL2Rows), dim3(64), 0, stream, in, out,
                        rows, width, eps, scale);
   else
     hipLaunchKernelGGL(l2_norm_rows, dim3((rows + 255) / 256), dim3(256), 0, stream, in, out,
