@@ -399,21 +399,24 @@ def front_bytes(T: int, hk: int, dk: int, hv: int, dv: int, k: int = 4) -> dict:
     """Algorithmic HBM bytes of the DeltaNet front end per call: the conv
     reads and writes [T, C] fp16 (C = 2 hk dk + hv dv) plus its weights and
     history; each L2 norm reads [T, hk dk] fp16 and writes it as fp32; the
-    gates read a, b fp16 and write beta, decay fp32."""
+    gates read a, b fp16 and write beta, decay fp32; the gated norm after
+    DeltaUpdate reads the output and the gate z and writes fp16."""
     C = 2 * hk * dk + hv * dv
     return {"conv": 2 * T * C * 2 + C * k * 2 + 2 * C * (k - 1) * 2,
             "l2norm_q": T * hk * dk * 6, "l2norm_k": T * hk * dk * 6,
-            "gates": T * hv * 12 + hv * 8}
+            "gates": T * hv * 12 + hv * 8,
+            "gated_norm": T * hv * dv * 6 + dv * 4}
 
 
 class DeltaFront(Workload):
     """The DeltaNet layer's front end ahead of DeltaUpdate
     (Qwen35ModelBuilder.cpp:146-160): causalConv + SiLU over q, k, v
     (8192 channels, 4 taps, history carried), the L2 norms of q (scaled by
-    1/sqrt(dk)) and k to fp32, and the gates. Inputs rotate over sets larger
-    than the MALL."""
+    1/sqrt(dk)) and k to fp32, and the gates; and the gatedRmsNorm that
+    follows DeltaUpdate (z gate through SiLU). Inputs rotate over sets
+    larger than the MALL."""
     bound = "hbm"
-    labels = ("conv", "l2norm_q", "l2norm_k", "gates")
+    labels = ("conv", "l2norm_q", "l2norm_k", "gates", "gated_norm")
     dominant = "conv"
 
     def __init__(self, dev, T, sets, seed, hk=16, dk=128, hv=32, dv=128, k=4):
@@ -435,6 +438,10 @@ class DeltaFront(Workload):
         self.a_log = (0.5 * torch.randn(hv, generator=g, device=dev)).float()
         self.dt = (0.5 * torch.randn(hv, generator=g, device=dev)).float()
         self.beta = [torch.empty(T, hv, dtype=torch.float32, device=dev) for _ in range(sets)]
+        self.mixed = [_randn16(g, (T * hv, dv), dev) for _ in range(sets)]
+        self.z = [_randn16(g, (T * hv, dv), dev) for _ in range(sets)]
+        self.nw = (1 + 0.2 * torch.randn(dv, generator=g, device=dev)).float()
+        self.gated = [torch.empty(T * hv, dv, dtype=torch.float16, device=dev) for _ in range(sets)]
         self.decay = [torch.empty(T, hv, dtype=torch.float32, device=dev) for _ in range(sets)]
         q_of = lambda s: self.y[s][:, :hk * dk]
         k_of = lambda s: self.y[s][:, hk * dk:2 * hk * dk]
@@ -455,6 +462,8 @@ class DeltaFront(Workload):
                          for s in range(sets)],
             "gates": [ops.bind_delta_gates(self.a[s], self.b[s], self.a_log, self.dt,
                                            self.beta[s], self.decay[s]) for s in range(sets)],
+            "gated_norm": [ops.bind_gated_rms_norm(self.mixed[s], self.z[s], self.nw,
+                                                   self.gated[s]) for s in range(sets)],
         }
         self.bytes = front_bytes(T, hk, dk, hv, dv, k)
 
@@ -472,7 +481,8 @@ class DeltaFront(Workload):
         return {"workload": self.name, "tokens": self.T, "key_heads": hk, "key_dim": dk,
                 "value_heads": hv, "value_dim": dv, "conv_channels": 2 * hk * dk + hv * dv,
                 "conv_kernel": 4, "sets": self.sets,
-                "ops": "causalConv+SiLU, l2NormF32 (q scaled 1/sqrt(dk), k), deltaGates"}
+                "ops": "causalConv+SiLU, l2NormF32 (q scaled 1/sqrt(dk), k), deltaGates, "
+                       "gatedRmsNorm (after DeltaUpdate)"}
 
     def cpu(self, budget_s):
         import numpy as np
@@ -489,22 +499,27 @@ class DeltaFront(Workload):
         a, b = host_u16(self.a[s]), host_u16(self.b[s])
         a_log, dt = host_f32(self.a_log), host_f32(self.dt)
 
+        mixed, z, nw = host_u16(self.mixed[s]), host_u16(self.z[s]), host_f32(self.nw)
+
         def step():
             y = oracle.causal_conv(x, w, h0.copy(), True)
             qn = oracle.l2norm_f32(qin, dk, 1e-6, dk ** -0.5)
             kn = oracle.l2norm_f32(kin, dk, 1e-6, 1.0)
-            return y, qn, kn, oracle.delta_gates(a, b, a_log, dt)
+            return (y, qn, kn, oracle.delta_gates(a, b, a_log, dt),
+                    oracle.gated_rms_norm(mixed, z, nw))
 
-        y, qn, kn, (beta, decay) = step()
+        y, qn, kn, (beta, decay), gn = step()
         exact = bool(np.array_equal(y, host_u16(self.y[s]))
                      and np.array_equal(qn.view(np.uint32), host_f32(self.qn[s]).view(np.uint32))
                      and np.array_equal(kn.view(np.uint32), host_f32(self.kn[s]).view(np.uint32))
                      and np.array_equal(beta.view(np.uint32), host_f32(self.beta[s]).view(np.uint32))
-                     and np.array_equal(decay.view(np.uint32), host_f32(self.decay[s]).view(np.uint32)))
+                     and np.array_equal(decay.view(np.uint32), host_f32(self.decay[s]).view(np.uint32))
+                     and np.array_equal(gn, host_u16(self.gated[s])))
         sec, runs = time_cpu(step, budget_s)
         return {"value": sec * 1e6, "unit": "µs/layer", "cores": 1, "kind": "port",
-                "sample": f"the four ops on one input set (T={self.T}), {runs} runs, scalar C "
-                          "oracle (orc_causal_conv, orc_l2norm_f32, orc_delta_gates)",
+                "sample": f"the five ops on one input set (T={self.T}), {runs} runs, scalar C "
+                          "oracle (orc_causal_conv, orc_l2norm_f32, orc_delta_gates, "
+                          "orc_gated_rms_norm)",
                 "gpu_bit_exact": exact}
 
 

@@ -112,7 +112,8 @@ enum llmi_hip_op {
   LLMI_HIP_OP_SIGMOID_MUL = 7,          /* params: ElementParams */
   LLMI_HIP_OP_CAUSAL_CONV = 8,          /* params: ConvParams */
   LLMI_HIP_OP_L2_NORM = 9,              /* params: L2Params */
-  LLMI_HIP_OP_DELTA_GATES = 10          /* params: RowParams (rows = tokens, width = heads) */
+  LLMI_HIP_OP_DELTA_GATES = 10,         /* params: RowParams (rows = tokens, width = heads) */
+  LLMI_HIP_OP_GATED_RMS_NORM = 11       /* params: RowParams */
 };
 
 /* ---------------------------------------------------------------- KvAppend
@@ -195,6 +196,22 @@ LLMI_HIP_API int llmi_hip_l2_norm(const uint16_t *input, float *output, L2Params
 LLMI_HIP_API int llmi_hip_delta_gates(const uint16_t *a, const uint16_t *b, const float *a_log,
                                       const float *dt_bias, float *beta, float *decay,
                                       RowParams p, void *stream);
+
+/* gatedRmsNorm (Reference.metal:228-259, dispatched at
+ * MetalReferenceGraph.mm:298-303 and MetalExecutionPlan.cpp:586-594): the
+ * DeltaNet output's norm, out[r][i] = fp16(fp16(x[r][i] * rmsScale(x[r])) *
+ * weight[i] * silu(gate[r][i])), rows x width, fp16 x, gate and out, fp32
+ * weight. width a multiple of 8 up to 256 and 16-byte aligned buffers
+ * (DeltaNet's valueDim 128); other shapes return LLMI_HIP_UNSUPPORTED. */
+LLMI_HIP_API int llmi_hip_gated_rms_norm(const uint16_t *input, const uint16_t *gate,
+                                         const float *weight, uint16_t *output, RowParams p,
+                                         void *stream);
+
+/* gatedRmsNormActivated (Reference.metal:252-259): the same with an fp32
+ * gate already activated by the projection's epilogue (no SiLU here). */
+LLMI_HIP_API int llmi_hip_gated_rms_norm_activated(const uint16_t *input, const float *gate,
+                                                   const float *weight, uint16_t *output,
+                                                   RowParams p, void *stream);
 
 /* --------------------------------------------------------------- CausalGqa
  * Replaces gqaFlashAttention (FlashAttention.metal:1-83) for T > 1 and the

@@ -29,6 +29,7 @@ OP_SIGMOID_MUL = 7
 OP_CAUSAL_CONV = 8
 OP_L2_NORM = 9
 OP_DELTA_GATES = 10
+OP_GATED_RMS_NORM = 11
 
 
 class CacheParams(C.Structure):
@@ -109,6 +110,8 @@ SIGNATURES = {
     "llmi_hip_causal_conv": (C.c_int, [_P, _P, _P, _P, ConvParams, _P]),
     "llmi_hip_l2_norm": (C.c_int, [_P, _P, L2Params, _P]),
     "llmi_hip_delta_gates": (C.c_int, [_P, _P, _P, _P, _P, _P, RowParams, _P]),
+    "llmi_hip_gated_rms_norm": (C.c_int, [_P, _P, _P, _P, RowParams, _P]),
+    "llmi_hip_gated_rms_norm_activated": (C.c_int, [_P, _P, _P, _P, RowParams, _P]),
     "llmi_hip_kv_append": (C.c_int, [_P, _P, _P, _P, CacheParams, _P]),
     "llmi_hip_causal_gqa": (C.c_int, [_P, _P, _P, _P, GqaParams, _P, _SZ, _P]),
     "llmi_hip_gqa_workspace_bytes": (_SZ, [GqaParams]),

@@ -236,6 +236,34 @@ int llmi_hip_delta_gates(const uint16_t *a, const uint16_t *b, const float *a_lo
                   "deltaGates");
 }
 
+static int gated_norm(const uint16_t *input, const void *gate, bool activated,
+                      const float *weight, uint16_t *output, RowParams p, void *stream) {
+  if (p.rows == 0 || p.width == 0)
+    return LLMI_HIP_OK;
+  if (!input || !gate || !weight || !output)
+    return fail(LLMI_HIP_INVALID_ARGUMENT, "gatedRmsNorm: null buffer");
+  if (!fits32(p.rows, p.width, 1))
+    return fail(LLMI_HIP_INVALID_ARGUMENT, "gatedRmsNorm: exceeds the 32-bit index range");
+  if (!gated_rms_norm_supported(p.width, input, gate, output))
+    return fail(LLMI_HIP_UNSUPPORTED,
+                "gatedRmsNorm: width %u (multiples of 8 up to 256, 16-byte aligned buffers)",
+                p.width);
+  return launched(launch_gated_rms_norm(input, gate, activated, weight, output, p.rows,
+                                        p.width, p.epsilon, static_cast<hipStream_t>(stream)),
+                  "gatedRmsNorm");
+}
+
+int llmi_hip_gated_rms_norm(const uint16_t *input, const uint16_t *gate, const float *weight,
+                            uint16_t *output, RowParams p, void *stream) {
+  return gated_norm(input, gate, false, weight, output, p, stream);
+}
+
+int llmi_hip_gated_rms_norm_activated(const uint16_t *input, const float *gate,
+                                      const float *weight, uint16_t *output, RowParams p,
+                                      void *stream) {
+  return gated_norm(input, gate, true, weight, output, p, stream);
+}
+
 int llmi_hip_cache_append(const uint16_t *src, uint16_t *cache, CacheParams p,
                           void *stream) {
   if (p.count && (!src || !cache))
@@ -453,6 +481,12 @@ unsigned llmi_hip_dispatch_count(int op, const void *params) {
     const RowParams &p = *static_cast<const RowParams *>(params);
     return p.rows && p.width ? 1 : 0;
   }
+  case LLMI_HIP_OP_GATED_RMS_NORM: {
+    const RowParams &p = *static_cast<const RowParams *>(params);
+    return p.rows && p.width && gated_rms_norm_supported(p.width, nullptr, nullptr, nullptr)
+               ? 1
+               : 0;
+  }
   }
   return 0;
 }
@@ -517,6 +551,8 @@ const char *llmi_hip_kernel_name(int op, const void *params, unsigned index) {
                : "l2NormRows";
   case LLMI_HIP_OP_DELTA_GATES:
     return "deltaGates";
+  case LLMI_HIP_OP_GATED_RMS_NORM:
+    return "gatedRmsNormTile";
   case LLMI_HIP_OP_SIGMOID_MUL:
     return sigmoid_mul_vectorised(static_cast<const ElementParams *>(params)->count,
                                   nullptr, nullptr, nullptr)

@@ -22,6 +22,10 @@
 // unaligned buffers take a thread per row.
 //
 // deltaGates: one thread per (token, head).
+//
+// gatedRmsNorm (the DeltaNet output's norm, Reference.metal:228-259): the
+// l2NormF32 tile structure with the rmsNorm scale, the gate applied per
+// element in the output pass.
 #include "exact_fp.hpp"
 #include "hip_common.hpp"
 #include "kernels.hpp"
@@ -217,6 +221,87 @@ __global__ __launch_bounds__(256) void l2_norm_rows(const uint16_t *__restrict__
     out[(size_t)r * width + i] = mul32(h2f(x[i]), f);
 }
 
+// gatedRmsNorm (Reference.metal:228-259): kL2Rows rows of `width` (a
+// multiple of 8, <= 256) per wave, staged in LDS like l2_norm_tile; out =
+// fp16(fp16(x * scale) * w * g) with g = silu(gate) for an fp16 gate (an
+// estimate that the margin test accepts, else exact) or the fp32 gate.
+template <bool kActivated>
+__global__ __launch_bounds__(64) void gated_rms_norm_tile(const uint16_t *__restrict__ in,
+                                                          const void *__restrict__ gate,
+                                                          const float *__restrict__ w,
+                                                          uint16_t *__restrict__ out,
+                                                          unsigned rows, unsigned width,
+                                                          float eps) {
+  __shared__ __align__(16) uint16_t tile[kL2Rows * (256 + 8)];
+  __shared__ float fac[kL2Rows];
+  const unsigned lane = threadIdx.x, pitch = width + 8, cpr = width / 8;
+  const unsigned row0 = blockIdx.x * kL2Rows, nrows = min(kL2Rows, rows - row0);
+  const unsigned chunks = nrows * cpr;
+  for (unsigned c = lane; c < chunks; c += 64) {
+    unsigned r = c / cpr, col = c - r * cpr;
+    *reinterpret_cast<uint4_t *>(tile + r * pitch + col * 8) =
+        *reinterpret_cast<const uint4_t *>(in + (row0 + r) * width + col * 8);
+  }
+  __syncthreads();
+  if (lane < nrows) {
+    const uint16_t *row = tile + lane * pitch;
+    float sum = 0.0f;
+    for (unsigned k = 0; k < cpr; ++k) {
+      uint4_t q = *reinterpret_cast<const uint4_t *>(row + 8 * k);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        float lo = h2f((uint16_t)(q[e] & 0xFFFFu)), hi = h2f((uint16_t)(q[e] >> 16));
+        sum = __builtin_fmaf(lo, lo, sum);
+        sum = __builtin_fmaf(hi, hi, sum);
+      }
+    }
+    fac[lane] = __fdiv_rn(1.0f, sqrt_cr(__fadd_rn(__fdiv_rn(sum, (float)width), eps)));
+  }
+  __syncthreads();
+  for (unsigned c = lane; c < chunks; c += 64) {
+    unsigned r = c / cpr, col = c - r * cpr;
+    const unsigned base = (row0 + r) * width + col * 8;
+    uint4_t q = *reinterpret_cast<const uint4_t *>(tile + r * pitch + col * 8);
+    float gv[8];
+    if (kActivated) {
+      const float *g = static_cast<const float *>(gate) + base;
+      float4_t g0 = *reinterpret_cast<const float4_t *>(g);
+      float4_t g1 = *reinterpret_cast<const float4_t *>(g + 4);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        gv[e] = g0[e];
+        gv[e + 4] = g1[e];
+      }
+    } else {
+      uint4_t g = *reinterpret_cast<const uint4_t *>(static_cast<const uint16_t *>(gate) + base);
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        gv[e] = h2f((uint16_t)(g[e / 2] >> (16 * (e & 1))));
+    }
+    const float f = fac[r];
+    uint4_t o;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      float norm = mul32(round16(mul32(h2f((uint16_t)(q[e / 2] >> (16 * (e & 1)))), f)),
+                         w[col * 8 + e]);
+      float y;
+      if (kActivated) {
+        y = mul32(norm, gv[e]);
+      } else {
+        y = mul32(norm, mul32(gv[e], logistic_estimate(gv[e])));
+        if (!f16_settled(y))
+          y = mul32(norm, mul32(gv[e], logistic_exact(gv[e])));
+      }
+      uint32_t b = f2h(y);
+      if (e & 1)
+        o[e / 2] |= b << 16;
+      else
+        o[e / 2] = b;
+    }
+    *reinterpret_cast<uint4_t *>(out + base) = o;
+  }
+}
+
 __device__ __forceinline__ float exp_cr(float x) { return (float)exp((double)x); }
 __device__ __forceinline__ float log_cr(float x) { return (float)log((double)x); }
 
@@ -278,6 +363,26 @@ hipError_t launch_l2_norm(const uint16_t *in, float *out, unsigned rows, unsigne
   else
     hipLaunchKernelGGL(l2_norm_rows, dim3((rows + 255) / 256), dim3(256), 0, stream, in, out,
                        rows, width, eps, scale);
+  return hipGetLastError();
+}
+
+bool gated_rms_norm_supported(unsigned width, const void *in, const void *gate,
+                              const void *out) {
+  return width % 8 == 0 && width <= 256 && aligned16(in) && aligned16(gate) && aligned16(out);
+}
+
+hipError_t launch_gated_rms_norm(const uint16_t *in, const void *gate, bool activated,
+                                 const float *w, uint16_t *out, unsigned rows, unsigned width,
+                                 float eps, hipStream_t stream) {
+  if (rows == 0 || width == 0)
+    return hipSuccess;
+  dim3 grid((rows + kL2Rows - 1) / kL2Rows);
+  if (activated)
+    hipLaunchKernelGGL(gated_rms_norm_tile<true>, grid, dim3(64), 0, stream, in, gate, w, out,
+                       rows, width, eps);
+  else
+    hipLaunchKernelGGL(gated_rms_norm_tile<false>, grid, dim3(64), 0, stream, in, gate, w, out,
+                       rows, width, eps);
   return hipGetLastError();
 }
 

@@ -101,6 +101,11 @@ hipError_t launch_causal_conv(const uint16_t *in, const uint16_t *w, uint16_t *h
 bool l2_norm_tiled(unsigned width, const void *in, const void *out);
 hipError_t launch_l2_norm(const uint16_t *in, float *out, unsigned rows, unsigned width,
                           float eps, float scale, hipStream_t stream);
+bool gated_rms_norm_supported(unsigned width, const void *in, const void *gate,
+                              const void *out);
+hipError_t launch_gated_rms_norm(const uint16_t *in, const void *gate, bool activated,
+                                 const float *w, uint16_t *out, unsigned rows, unsigned width,
+                                 float eps, hipStream_t stream);
 hipError_t launch_delta_gates(const uint16_t *a, const uint16_t *b, const float *a_log,
                               const float *dt_bias, float *beta, float *decay,
                               unsigned rows, unsigned width, hipStream_t stream);

@@ -191,6 +191,31 @@ def delta_gates(*args) -> None:
     bind_delta_gates(*args)()
 
 
+def bind_gated_rms_norm(x: torch.Tensor, gate: torch.Tensor, weight: torch.Tensor,
+                        out: torch.Tensor, epsilon: float = 1e-6) -> "Bound":
+    """gatedRmsNorm (Reference.metal:228-259) over the last dimension: gate
+    fp16 (through SiLU) or fp32 (already activated, gatedRmsNormActivated)."""
+    _require(x, torch.float16, "x")
+    _require(out, torch.float16, "out")
+    _require(weight, torch.float32, "weight")
+    if gate.dtype not in (torch.float16, torch.float32):
+        raise ValueError("gate must be float16 or float32")
+    _require(gate, gate.dtype, "gate")
+    width = x.shape[-1]
+    if gate.shape != x.shape or out.shape != x.shape or weight.numel() != width:
+        raise ValueError("x, gate, out and weight shapes disagree")
+    p = _lib.RowParams(x.numel() // max(width, 1), width, epsilon)
+    lib = _lib.load()
+    fn = lib.llmi_hip_gated_rms_norm if gate.dtype == torch.float16 \
+        else lib.llmi_hip_gated_rms_norm_activated
+    return Bound(fn, (_ptr(x), _ptr(gate), _ptr(weight), _ptr(out), p, _stream()),
+                 "gatedRmsNormTile")
+
+
+def gated_rms_norm(*args, **kwargs) -> None:
+    bind_gated_rms_norm(*args, **kwargs)()
+
+
 def kv_append(k: torch.Tensor, v: torch.Tensor, k_cache: torch.Tensor,
               v_cache: torch.Tensor, past: int) -> None:
     """KvAppend: rows [past, past+T) of both caches <- k, v ([T, Hkv, d])."""

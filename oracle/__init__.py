@@ -74,6 +74,8 @@ def lib() -> C.CDLL:
         L.orc_norm_rope.argtypes = [_u16p, _f32p, _u16p] + [_u32] * 7 + [C.c_float, C.c_float]
         L.orc_sigmoid_mul.argtypes = [_u16p, _u16p, _u16p, C.c_size_t]
         L.orc_causal_conv.argtypes = [_u16p, _u16p, _u16p, _u16p] + [_u32] * 4
+        L.orc_gated_rms_norm.argtypes = [_u16p, C.c_void_p, C.c_void_p, _f32p, _u16p,
+                                         _u32, _u32, C.c_float]
         for name, n in (("orc_cost_kv_append", 3), ("orc_cost_causal_gqa", 5),
                         ("orc_cost_delta_update", 5)):
             fn = getattr(L, name)
@@ -250,6 +252,21 @@ def causal_conv(x, weight, history, apply_silu: bool = True) -> np.ndarray:
     out = np.empty_like(a)
     lib().orc_causal_conv(a.reshape(-1), w.reshape(-1), history.reshape(-1), out.reshape(-1),
                           T, Cn, w.shape[1], int(apply_silu))
+    return out
+
+
+def gated_rms_norm(x, gate, weight, eps: float = 1e-6) -> np.ndarray:
+    """gatedRmsNorm (Reference.metal:228-259): x [rows, width] fp16 bits;
+    gate fp16 bits (through SiLU) or float32 (already activated)."""
+    a = np.ascontiguousarray(x, np.uint16)
+    w = np.ascontiguousarray(weight, np.float32)
+    g = np.ascontiguousarray(gate)
+    out = np.empty_like(a)
+    g16 = g.ctypes.data if g.dtype == np.uint16 else None
+    g32 = g.ctypes.data if g.dtype == np.float32 else None
+    assert g16 or g32, "gate must be fp16 bits or float32"
+    lib().orc_gated_rms_norm(a.reshape(-1), g16, g32, w, out.reshape(-1), a.shape[0],
+                             a.shape[1], eps)
     return out
 
 

@@ -743,6 +743,24 @@ void orc_norm_rope(const uint16_t *input, const float *weight, uint16_t *output,
   }
 }
 
+/* gatedRmsNorm / gatedRmsNormActivated, Reference.metal:228-259:
+ * out = fp16(fp16(x * rmsScale) * w[i] * g), g = silu(gate) for an fp16
+ * gate, the fp32 gate itself when activated. */
+void orc_gated_rms_norm(const uint16_t *input, const uint16_t *gate16, const float *gate32,
+                        const float *weight, uint16_t *output, uint32_t rows, uint32_t width,
+                        float eps) {
+  for (uint32_t r = 0; r < rows; ++r) {
+    size_t off = (size_t)r * width;
+    float scale = orc_rms_scale(input + off, width, eps);
+    for (uint32_t i = 0; i < width; ++i) {
+      float norm = orc_round_f16(orc_f16_to_f32(input[off + i]) * scale) * weight[i];
+      float value = gate32 ? gate32[off + i] : orc_f16_to_f32(gate16[off + i]);
+      float g = gate32 ? value : value * logistic(value);
+      output[off + i] = orc_f32_to_f16(norm * g);
+    }
+  }
+}
+
 /* sigmoidMul, Graph.metal:78-85 with logistic, Reference.metal:4. */
 void orc_sigmoid_mul(const uint16_t *gate, const uint16_t *input, uint16_t *output,
                      size_t count) {

@@ -155,6 +155,13 @@ void orc_norm_rope(const uint16_t *input, const float *weight, uint16_t *output,
                    uint32_t rotary_dim, uint32_t head_stride, uint32_t past,
                    uint32_t output_start, float epsilon, float theta);
 
+/* gatedRmsNorm (gate16, fp16 gate through SiLU) or gatedRmsNormActivated
+ * (gate32, already activated), lib/Backend/Metal/Kernels/Reference.metal:
+ * 228-259: out = fp16(fp16(x * rmsScale(x)) * weight[i] * g), rows x width. */
+void orc_gated_rms_norm(const uint16_t *input, const uint16_t *gate16, const float *gate32,
+                        const float *weight, uint16_t *output, uint32_t rows, uint32_t width,
+                        float eps);
+
 /* sigmoidMul (lib/Backend/Metal/Kernels/Graph.metal:78-85, logistic
  * Reference.metal:4): out = fp16(fp16(1 / (1 + exp(-gate))) * input), exp
  * correctly rounded to fp32. */

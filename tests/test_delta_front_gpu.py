@@ -119,3 +119,37 @@ def test_gate_beta_every_fp16_value(gpu):
     torch.cuda.synchronize()
     rb, rd = oracle.delta_gates(a, b, z, z)
     assert np.array_equal(beta.cpu().numpy().view(np.uint32), rb.view(np.uint32))
+
+
+@pytest.mark.parametrize("rows,width,activated", [(1024 * 32, 128, False), (32, 128, False),
+                                                  (1000, 128, True), (45, 256, False),
+                                                  (7, 64, True)])
+def test_gated_rms_norm(gpu, rows, width, activated):
+    rng = np.random.default_rng(rows + width)
+    x = _f16(rng, (rows, width))
+    x[0] = 0
+    w = (1 + 0.2 * rng.standard_normal(width)).astype(np.float32)
+    if activated:
+        g = (rng.standard_normal((rows, width)) * 2).astype(np.float32)
+        gt = torch.from_numpy(g).to(gpu)
+    else:
+        g = _f16(rng, (rows, width), 3.0)
+        g[1, :6] = [0x7BFF, 0xFBFF, 0x0000, 0x8000, 0xCC00, 0x4C00]
+        gt = u16_to_torch(g)
+    out = torch.empty(rows, width, dtype=torch.float16, device=gpu)
+    print(f"gatedRmsNorm rows={rows} width={width} activated={activated}", flush=True)
+    ops.gated_rms_norm(u16_to_torch(x), gt, torch.from_numpy(w).to(gpu), out)
+    torch.cuda.synchronize()
+    assert np.array_equal(torch_to_u16(out), oracle.gated_rms_norm(x, g, w))
+
+
+def test_gated_rms_norm_every_gate_value(gpu):
+    """Every finite fp16 gate value through SiLU, on rows of ones."""
+    bits = np.arange(1 << 16, dtype=np.uint32).astype(np.uint16)
+    g = bits[(bits & 0x7C00) != 0x7C00].reshape(-1, 128)
+    x = np.full(g.shape, 0x3C00, np.uint16)
+    w = np.ones(128, np.float32)
+    out = torch.empty(g.shape, dtype=torch.float16, device=gpu)
+    ops.gated_rms_norm(u16_to_torch(x), u16_to_torch(g), torch.from_numpy(w).to(gpu), out)
+    torch.cuda.synchronize()
+    assert np.array_equal(torch_to_u16(out), oracle.gated_rms_norm(x, g, w))

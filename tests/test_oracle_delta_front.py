@@ -11,6 +11,11 @@ What fixes each result:
   * kernel size 1 is an elementwise product with no history;
   * splitting the tokens over two calls, the history carried between them,
     gives the same outputs and final history as one call, bit for bit.
+
+And its gatedRmsNorm (orc_gated_rms_norm): Hugging Face's Qwen3_5RMSNormGated
+(what the reference's tests compare against) within one fp16 ulp; with an
+activated gate of 1 and unit weight it is the rmsNorm of a zero weight, bit
+for bit; a zero gate gives zeros.
 """
 import numpy as np
 import pytest
@@ -77,3 +82,42 @@ def test_split_calls_carry_the_history(split):
                             oracle.causal_conv(x[split:], w, h2, True)])
     assert np.array_equal(whole, parts)
     assert np.array_equal(h1, h2)
+
+
+def _hf_gated(x, gate, w, eps):
+    torch = pytest.importorskip("torch")
+    m = pytest.importorskip("transformers.models.qwen3_5.modeling_qwen3_5")
+    norm = m.Qwen3_5RMSNormGated(x.shape[1], eps=eps)
+    norm.load_state_dict({"weight": torch.from_numpy(w)})
+    xt = torch.from_numpy(oracle.f16_to_f32(x)).half()
+    gt = torch.from_numpy(oracle.f16_to_f32(gate)).half()
+    with torch.no_grad():
+        return norm(xt, gt).float().numpy().astype(np.float64)
+
+
+def test_gated_rms_norm_matches_huggingface():
+    """Qwen3_5RMSNormGated (the module the reference's tests compare
+    against) on the same fp16 inputs: within one fp16 ulp (its mean and
+    rsqrt differ from the sequential fma sum and 1/sqrt)."""
+    rng = np.random.default_rng(6)
+    x = oracle.f32_to_f16(rng.standard_normal((40, 128)).astype(np.float32))
+    g = oracle.f32_to_f16((rng.standard_normal((40, 128)) * 2).astype(np.float32))
+    w = (1 + 0.2 * rng.standard_normal(128)).astype(np.float32)
+    got = oracle.f16_to_f32(oracle.gated_rms_norm(x, g, w)).astype(np.float64)
+    ref = _hf_gated(x, g, w, 1e-6)
+    ulp = 2.0 ** (np.floor(np.log2(np.maximum(np.abs(ref), 2.0 ** -14))) - 10)
+    assert np.all(np.abs(got - ref) <= 1.01 * ulp)
+
+
+def test_gated_rms_norm_exact_cases():
+    rng = np.random.default_rng(7)
+    x = oracle.f32_to_f16(rng.standard_normal((9, 64)).astype(np.float32))
+    # activated gate 1 and weight 1: fp16(x * scale), which is rmsNorm with a
+    # zero weight (normRope with no rotation), bit for bit
+    one = np.ones((9, 64), np.float32)
+    got = oracle.gated_rms_norm(x, one, np.ones(64, np.float32))
+    assert np.array_equal(got, oracle.norm_rope(x, np.zeros(64, np.float32), 9, 1, 64, 0, 64, 0))
+    # gate 0: silu(0) = 0, output +-0
+    z = np.zeros((9, 64), np.uint16)
+    out = oracle.gated_rms_norm(x, z, np.ones(64, np.float32))
+    assert np.all((out & 0x7FFF) == 0)
