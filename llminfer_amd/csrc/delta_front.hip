@@ -279,25 +279,39 @@ __global__ __launch_bounds__(64) void gated_rms_norm_tile(const uint16_t *__rest
         gv[e] = h2f((uint16_t)(g[e / 2] >> (16 * (e & 1))));
     }
     const float f = fac[r];
-    uint4_t o;
+    float norm[8], y[8];
+    unsigned need = 0;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      float norm = mul32(round16(mul32(h2f((uint16_t)(q[e / 2] >> (16 * (e & 1)))), f)),
-                         w[col * 8 + e]);
-      float y;
+      norm[e] = mul32(round16(mul32(h2f((uint16_t)(q[e / 2] >> (16 * (e & 1)))), f)),
+                      w[col * 8 + e]);
       if (kActivated) {
-        y = mul32(norm, gv[e]);
+        y[e] = mul32(norm[e], gv[e]);
       } else {
-        y = mul32(norm, mul32(gv[e], logistic_estimate(gv[e])));
-        if (!f16_settled(y))
-          y = mul32(norm, mul32(gv[e], logistic_exact(gv[e])));
+        y[e] = mul32(norm[e], mul32(gv[e], logistic_estimate(gv[e])));
+        need |= f16_settled(y[e]) ? 0u : 1u << e;
       }
-      uint32_t b = f2h(y);
-      if (e & 1)
-        o[e / 2] |= b << 16;
-      else
-        o[e / 2] = b;
     }
+    // the few that the margin test rejects, one shared pass each (as in
+    // sigmoid_mul_vec)
+    while (need) {
+      unsigned k = __builtin_ctz(need);
+      need &= need - 1;
+      float gk = gv[0], nk = norm[0];
+#pragma unroll
+      for (int e = 1; e < 8; ++e) {
+        gk = k == (unsigned)e ? gv[e] : gk;
+        nk = k == (unsigned)e ? norm[e] : nk;
+      }
+      float yk = mul32(nk, mul32(gk, logistic_exact(gk)));
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        y[e] = k == (unsigned)e ? yk : y[e];
+    }
+    uint4_t o;
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      o[e] = (uint32_t)f2h(y[2 * e]) | ((uint32_t)f2h(y[2 * e + 1]) << 16);
     *reinterpret_cast<uint4_t *>(out + base) = o;
   }
 }
