@@ -6,7 +6,8 @@ reads 256 B and does 384 MACs for T=3, P=2, Hq=2, Hkv=1, d=8
 (tests/GraphIRTest.cpp:99-103); DeltaUpdate does 288 MACs for T=3, Hk=1,
 dk=dv=4, Hv=2 (tests/ConverterTest.py:171-179). Where oracle/_ref is built,
 the figures must equal the reference's estimateCost (lib/GraphIR/Cost.cpp)
-on random shapes, and the BASELINE.md table's FLOP counts are re-derived.
+on random shapes, and the published per-configuration FLOP counts of the
+benchmark configurations are re-derived.
 """
 import ctypes as C
 
@@ -26,7 +27,7 @@ def test_reference_known_answers():
 
 
 def test_baseline_table_flops():
-    # FLOPs = 2 x MACs
+    # the benchmark configurations' published FLOP counts: FLOPs = 2 x MACs
     assert 2 * oracle.cost("causal_gqa", 128, 0, 16, 4, 256).fp_macs == 135_266_304
     assert 2 * oracle.cost("causal_gqa", 1, 4096, 16, 4, 256).fp_macs == 67_125_248
     assert 2 * oracle.cost("causal_gqa", 2048, 2048, 16, 4, 256).fp_macs == 103_095_992_320
