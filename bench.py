@@ -207,6 +207,9 @@ class GqaDecode(Workload):
     def op(self, label, i):
         self.att[i % self.sets]()
 
+    def launch_warm(self, i):
+        self.att[0]()
+
     def kernels(self):
         return self.att[0].what
 
@@ -540,26 +543,39 @@ def _delta_inputs(g, dev, T, hk, dk, hv, dv):
 
 
 class DeltaPrefill(Workload):
-    """DeltaUpdate over 1024 tokens from a zero state."""
+    """DeltaUpdate over 1024 tokens from a zero state. The timed
+    calls rotate over `sets` independent operand sets (q, k, v, gates, state,
+    out: 34 MB each, 272 MB in all, past the 256 MB MALL); `warm_op` repeats
+    one set. Each timed call continues from the state its set holds (the
+    work per call does not depend on the state's values)."""
     bound = "hbm"
     dominant = "delta"
     labels = ("delta",)
+    cache_state = ("cold: 8 operand sets (272 MB) rotate past the MALL; warm: one set "
+                   "repeated")
 
-    def __init__(self, dev, T=1024, hk=16, dk=128, hv=32, dv=128, seed=4):
+    def __init__(self, dev, T=1024, hk=16, dk=128, hv=32, dv=128, seed=4, sets=8):
         import torch
         from llminfer_amd import ops
         self.T, self.hk, self.dk, self.hv, self.dv = T, hk, dk, hv, dv
         self.name = f"delta_prefill_{T}"
         self.tokens = T
+        self.sets = sets
         g = torch.Generator(device=dev).manual_seed(seed)
-        self.q, self.k, self.v, self.beta, self.decay = _delta_inputs(g, dev, T, hk, dk, hv, dv)
+        self.x = []
+        for _ in range(sets):
+            q, k, v, beta, decay = _delta_inputs(g, dev, T, hk, dk, hv, dv)
+            state = torch.zeros((hv, dk, dv), dtype=torch.float32, device=dev)
+            out = torch.empty_like(v)
+            self.x.append(dict(q=q, k=k, v=v, beta=beta, decay=decay, state=state, out=out,
+                               upd=ops.bind_delta_update(q, k, v, beta, decay, state, out)))
         self.state0 = torch.zeros((hv, dk, dv), dtype=torch.float32, device=dev)
-        self.state = self.state0.clone()
-        self.out = torch.empty_like(self.v)
-        self.upd = ops.bind_delta_update(self.q, self.k, self.v, self.beta, self.decay,
-                                         self.state, self.out)
+        self.upd = self.x[0]["upd"]
 
     def op(self, label, i):
+        self.x[i % self.sets]["upd"]()
+
+    def warm_op(self, i):
         self.upd()
 
     def kernels(self):
@@ -570,21 +586,23 @@ class DeltaPrefill(Workload):
 
     def config(self):
         return {"workload": self.name, "tokens": self.T, "key_heads": self.hk,
-                "key_dim": self.dk, "value_heads": self.hv, "value_dim": self.dv}
+                "key_dim": self.dk, "value_heads": self.hv, "value_dim": self.dv,
+                "operand_sets": self.sets, "cache_state": self.cache_state}
 
     def cpu(self, budget_s):
         import numpy as np
         import oracle
         import torch
+        x = self.x[0]
         torch.cuda.synchronize()
-        self.state.copy_(self.state0)
+        x["state"].copy_(self.state0)
         self.upd()
         torch.cuda.synchronize()
-        q, k, beta, decay = (host_f32(t) for t in (self.q, self.k, self.beta, self.decay))
-        v = host_u16(self.v)
+        q, k, beta, decay = (host_f32(x[n]) for n in ("q", "k", "beta", "decay"))
+        v = host_u16(x["v"])
         s0 = host_f32(self.state0)
-        gpu_out = oracle.f16_to_f32(host_u16(self.out))
-        gpu_state = host_f32(self.state)
+        gpu_out = oracle.f16_to_f32(host_u16(x["out"]))
+        gpu_state = host_f32(x["state"])
         thr = cpu_threads()
         want, wstate = oracle.delta_recurrent_f32(q, k, v, beta, decay, s0, thr)
         err = float(np.max(np.abs(gpu_out - oracle.f16_to_f32(want))))
@@ -670,21 +688,41 @@ class HybridDecode(Workload):
         xs = [{k: (host_u16(v) if v.dtype == torch.float16 else host_f32(v))
                for k, v in x.items()} for x in self.inp]
 
-        def run(n):
+        def run(n, outs=None):
             s = st
             for j in range(n):
                 x = xs[j]
-                _, s = oracle.delta_recurrent_f32(x["dq"], x["dk"], x["dv"], x["beta"],
-                                                  x["decay"], s, thr)
+                dout, s = oracle.delta_recurrent_f32(x["dq"], x["dk"], x["dv"], x["beta"],
+                                                     x["decay"], s, thr)
                 oracle.kv_append(x["kn"], kc, self.P0 + j)
                 oracle.kv_append(x["vn"], vc, self.P0 + j)
-                oracle.gqa_f32(x["q"], kc, vc, self.P0 + j, thr)
+                gout = oracle.gqa_f32(x["q"], kc, vc, self.P0 + j, thr)
+                if outs is not None:
+                    outs.append((dout, gout, s))
+
+        # The GPU steps of layer 0 from the state it holds now, position by
+        # position, against the oracle from the same state.
+        gpu = []
+        for j in range(self.n):
+            for fn in self.ops[0, j]:
+                fn()
+            torch.cuda.synchronize()
+            gpu.append((host_u16(self.dout), host_u16(self.gout), host_f32(self.state[0])))
+        want = []
+        run(self.n, want)
+        f = oracle.f16_to_f32
+        err_d = max(float(np.max(np.abs(f(a[0]) - f(b[0])))) for a, b in zip(gpu, want))
+        err_g = max(float(np.max(np.abs(f(a[1]) - f(b[1])))) for a, b in zip(gpu, want))
+        rel = float(np.max(np.abs(gpu[-1][2] - want[-1][2])) / np.max(np.abs(want[-1][2])))
         sec, runs = time_cpu(lambda: run(self.n), budget_s)
         return {"value": sec / self.n * 1e6, "unit": "µs/layer-pair", "cores": thr,
                 "kind": "port",
                 "sample": f"{self.n} hybrid steps (DeltaNet decode + KvAppend + GQA decode "
                           f"at P={self.P0}..{self.P0 + self.n - 1}) of one layer pair, "
-                          f"{runs} runs"}
+                          f"{runs} runs",
+                "gpu_vs_cpu_max_abs": max(err_d, err_g),
+                "gpu_vs_cpu": {"delta_out_max_abs": err_d, "gqa_out_max_abs": err_g,
+                               "final_state_rel": rel, "positions": self.n}}
 
 
 # ---------------------------------------------------------------- timing
@@ -703,14 +741,29 @@ def sleep_cycles_per_ms() -> float:
     return n / max(ms, 1e-3)
 
 
-def run_timed(fn, steps: int, warmup: int, cyc_per_ms: float) -> tuple[float, float]:
-    """(ms per call, host enqueue ms per call) of fn(i), i = warmup .. warmup+steps-1.
+class Timing(float):
+    """ms per call (the mean over the K timed calls), with the median and
+    10th percentile of the per-chunk means and the host enqueue time."""
+    median_ms: float
+    p10_ms: float
+    host_ms: float
+
+    def summary(self) -> dict:
+        return {"mean_us": round(self * 1e3, 3), "median_us": round(self.median_ms * 1e3, 3),
+                "p10_us": round(self.p10_ms * 1e3, 3)}
+
+
+def run_timed(fn, steps: int, warmup: int, cyc_per_ms: float, chunk: int = 10) -> Timing:
+    """Device time per call of fn(i), i = warmup .. warmup+steps-1.
 
     A spin kernel holds the GPU while the host enqueues the K calls, so the
-    two events that bracket exactly those K calls time the GPU running them
-    back to back, not Python. If the host still fell behind (its enqueue
+    events on the launch stream time the GPU running them back to back, not
+    Python. An event after every `chunk` calls splits the K calls into
+    back-to-back chunks; the mean is first to last event, and the median and
+    p10 are over the chunk means. If the host still fell behind (its enqueue
     outlasted the hold), the measurement is repeated with a longer hold.
     """
+    import statistics
     import torch
     for i in range(warmup):
         fn(i)
@@ -722,22 +775,33 @@ def run_timed(fn, steps: int, warmup: int, cyc_per_ms: float) -> tuple[float, fl
     host_ms = (time.perf_counter() - t0) * 1e3 / n
     torch.cuda.synchronize()
 
+    chunk = max(1, min(chunk, steps))
     hold_ms = 10.0 + 3.0 * host_ms * steps
     for _attempt in range(4):
-        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        marks = [torch.cuda.Event(enable_timing=True)]
         torch.cuda.synchronize()
         torch.cuda._sleep(int(min(hold_ms, 8000.0) * cyc_per_ms))
         t0 = time.perf_counter()
-        start.record()
+        marks[0].record()
+        counts = []
         for i in range(steps):
             fn(warmup + i)
-        end.record()
+            if (i + 1) % chunk == 0 or i + 1 == steps:
+                ev = torch.cuda.Event(enable_timing=True)
+                ev.record()
+                marks.append(ev)
+                counts.append((i + 1) - sum(counts))
         enq_ms = (time.perf_counter() - t0) * 1e3
         torch.cuda.synchronize()
         if enq_ms < 0.8 * hold_ms or hold_ms >= 8000.0:
             break
         hold_ms = 2.0 * enq_ms + 10.0
-    return start.elapsed_time(end) / steps, enq_ms / steps
+    per = sorted(marks[j].elapsed_time(marks[j + 1]) / counts[j] for j in range(len(counts)))
+    t = Timing(marks[0].elapsed_time(marks[-1]) / steps)
+    t.median_ms = statistics.median(per)
+    t.p10_ms = per[int(0.1 * (len(per) - 1))]
+    t.host_ms = enq_ms / steps
+    return t
 
 
 def roofline(w: Workload, op_ms: float, steps: int, warmup: int, traffic) -> dict:
@@ -801,7 +865,11 @@ def main(argv=None) -> int:
     # ---- headline: configs[1]
     w = GqaDecode(dev)
     log(f"headline {w.name}: warmup {args.warmup}, steps {args.steps}")
-    ms, host_ms = run_timed(w.launch, args.steps, args.warmup, cyc)
+    ms = run_timed(w.launch, args.steps, args.warmup, cyc)
+    host_ms = ms.host_ms
+    # The same step on one cache set over and over: its 16.8 MB stay in the
+    # 256 MB MALL (warm), next to the rotating sets above (cold).
+    warm = run_timed(w.launch_warm, args.steps, args.warmup, cyc)
     # The headline step is the dominant op alone (one fused append+attention
     # call), so its back-to-back time is the op's time.
     rl = roofline(w, ms, args.steps, args.warmup, load_traffic(w.name))
@@ -814,6 +882,8 @@ def main(argv=None) -> int:
         "vs_baseline": None, "dtype": "f16", "data": "synthetic",
         "config": w.config(), "tokens_per_s": round(1e3 / ms, 1),
         "host_enqueue_ms_per_step": round(host_ms, 4),
+        "timing": {"cold": ms.summary(), "warm": warm.summary(),
+                   "chunks": "median and p10 over back-to-back chunks of 10 steps"},
         "roofline": rl,
     }
     if not args.no_cpu:
@@ -841,12 +911,18 @@ def main(argv=None) -> int:
             log(f"{key}: {x.name}")
             n = steps if key != "cfg4_hybrid_decode_32k" else max(steps, 128)
             wu = min(args.warmup, 10)
-            ms_x, _ = run_timed(x.launch, n, wu, cyc)
-            op_ms = {l: run_timed(lambda i, l=l: x.op(l, i), n, wu, cyc)[0] for l in x.labels}
+            ms_x = run_timed(x.launch, n, wu, cyc)
+            op_ms = {l: run_timed(lambda i, l=l: x.op(l, i), n, wu, cyc) for l in x.labels}
             entry = {"config": x.config(), "us_per_step": round(ms_x * 1e3, 3),
                      "tokens_per_s": round(x.tokens * 1e3 / ms_x, 1), "steps": n,
                      "op_us": {l: round(v * 1e3, 3) for l, v in op_ms.items()},
+                     "timing": {"step": ms_x.summary(),
+                                "dominant_op": op_ms[x.dominant].summary()},
                      "roofline": roofline(x, op_ms[x.dominant], n, wu, load_traffic(x.name))}
+            if hasattr(x, "warm_op"):
+                warm = run_timed(x.warm_op, n, wu, cyc)
+                entry["timing"]["dominant_op_warm"] = warm.summary()
+                entry["timing"]["cache_state"] = x.cache_state
             if x.bound == "mfma":
                 entry["hbm_frac"] = None
             if isinstance(x, DeltaPrefill):

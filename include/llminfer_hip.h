@@ -305,13 +305,20 @@ typedef struct llmi_hip_session_config {
   unsigned keyHeads, keyDim, valueHeads, valueDim;
 } llmi_hip_session_config;
 
-/* A plan record: MetalDispatchInfo{opIndex, kernel, fusedOpIndex}
- * (MetalSession.h:11-16). fused_op_index is LLMI_HIP_NO_FUSED_OP unless
- * the launch also performs another op of the step (the fused KvAppend). */
-#define LLMI_HIP_NO_FUSED_OP ((size_t)-1)
+/* A plan record, laid out as MetalDispatchInfo{opIndex, kernel, epilogue,
+ * fusedOpIndex} (MetalSession.h:11-16). As in the reference, `epilogue`
+ * names a projection epilogue fused into the launch and `fused_op_index` is
+ * meaningful only when `epilogue` is non-empty (tools/run/Main.cpp:244-255
+ * prints it only then); this path has no projection epilogues, so every
+ * record carries epilogue "" and fused_op_index 0 (the reference's
+ * defaults, MetalExecutionPlan.h:31-32). A launch that performs two ops of
+ * the step -- the decode launch that also appends the new K/V row -- is
+ * recorded once under each op, in op order, so the records' op indices
+ * alone cover every op of the step (MetalReferenceTest.py:346-351). */
 typedef struct llmi_hip_dispatch {
   size_t op_index;
   const char *kernel;
+  const char *epilogue;
   size_t fused_op_index;
 } llmi_hip_dispatch;
 
@@ -327,6 +334,24 @@ LLMI_HIP_API uint16_t *llmi_hip_session_key_cache(llmi_hip_session *s);
 LLMI_HIP_API uint16_t *llmi_hip_session_value_cache(llmi_hip_session *s);
 LLMI_HIP_API float *llmi_hip_session_recurrent_state(llmi_hip_session *s);
 
+/* Declare rows [0, past) of the caches and the recurrent state as written:
+ * for a caller that filled the session-owned buffers itself through the
+ * pointers above (a restored checkpoint, or a test seeding a long context).
+ * past <= capacity; a session left invalid by a failed step must be reset
+ * first. Host only: nothing is launched. */
+LLMI_HIP_API int llmi_hip_session_restore(llmi_hip_session *s, unsigned past);
+
+/* The checks llmi_hip_session_open and llmi_hip_session_step make before
+ * any allocation or launch, for a step of `tokens` tokens at `past` in a
+ * session of `config` -- the op contracts of KvAppend, CausalGqa and
+ * DeltaUpdate (lib/GraphIR/Graph.cpp:226-279) on the shapes the session
+ * derives from its config, the step shape (0 < tokens <= capacity - past,
+ * Graph.cpp:382-387), the lowering's 32-bit element-index limit
+ * (MetalExecutionPlan.cpp:32-40) and kernel availability. Host only: needs
+ * no device. */
+LLMI_HIP_API int llmi_hip_session_check(const llmi_hip_session_config *config,
+                                        unsigned past, unsigned tokens);
+
 /* One step of T tokens through both layers, in graph order: DeltaUpdate
  * (op 0), KvAppend (op 1), CausalGqa (op 2) -- the order the builder emits
  * them for a DeltaNet layer followed by a GQA layer. All operands are
@@ -334,9 +359,9 @@ LLMI_HIP_API float *llmi_hip_session_recurrent_state(llmi_hip_session *s);
  * delta_out [T][Hv*dv] and gqa_out [T][Hq][d]. Validation failures return
  * nonzero before any launch. If `records` is non-NULL, up to `cap` plan
  * records are written and *count receives the total; for T == 1 KvAppend
- * runs inside the attention launch, recorded as {op 2, fused_op_index 1}.
- * The step waits for the GPU once at the end (one host sync per step,
- * MetalContext.mm:141-151). */
+ * runs inside the attention launch, which is recorded under op 1 and again
+ * under op 2. The step waits for the GPU once at the end (one host sync per
+ * step, MetalContext.mm:141-151). */
 LLMI_HIP_API int llmi_hip_session_step(llmi_hip_session *s, unsigned tokens,
                           const float *dq, const float *dk, const uint16_t *dv,
                           const float *beta, const float *decay,

@@ -81,12 +81,10 @@ class SessionConfig(C.Structure):
                 ("valueHeads", C.c_uint), ("valueDim", C.c_uint)]
 
 
-NO_FUSED_OP = (1 << (8 * C.sizeof(C.c_size_t))) - 1
-
-
 class Dispatch(C.Structure):
+    """MetalDispatchInfo{opIndex, kernel, epilogue, fusedOpIndex}."""
     _fields_ = [("op_index", C.c_size_t), ("kernel", C.c_char_p),
-                ("fused_op_index", C.c_size_t)]
+                ("epilogue", C.c_char_p), ("fused_op_index", C.c_size_t)]
 
 
 class HipError(RuntimeError):
@@ -130,6 +128,8 @@ SIGNATURES = {
     "llmi_hip_session_close": (None, [_P]),
     "llmi_hip_session_reset": (None, [_P]),
     "llmi_hip_session_past": (C.c_uint, [_P]),
+    "llmi_hip_session_restore": (C.c_int, [_P, C.c_uint]),
+    "llmi_hip_session_check": (C.c_int, [C.POINTER(SessionConfig), C.c_uint, C.c_uint]),
     "llmi_hip_session_invalid": (C.c_int, [_P]),
     "llmi_hip_session_key_cache": (_P, [_P]),
     "llmi_hip_session_value_cache": (_P, [_P]),

@@ -120,11 +120,33 @@ int ensure_workspace(llmi_hip_session *s, size_t need) {
   return LLMI_HIP_OK;
 }
 
+// Plan records carry no projection epilogue on this path: epilogue "" and
+// fused_op_index 0, the reference's defaults (MetalExecutionPlan.h:31-32).
 void record(llmi_hip_dispatch *records, size_t cap, size_t &n, size_t op,
-            const char *kernel, size_t fused = LLMI_HIP_NO_FUSED_OP) {
+            const char *kernel) {
   if (records && n < cap)
-    records[n] = llmi_hip_dispatch{op, kernel, fused};
+    records[n] = llmi_hip_dispatch{op, kernel, "", 0};
   ++n;
+}
+
+// Everything a step checks before it allocates or launches: the config
+// (every shape valid up to the full capacity), the step shape
+// (Graph.cpp:382-387) and the three op contracts at this step.
+int check_step(const llmi_hip_session_config &c, unsigned past, unsigned tokens) {
+  if (int st = check_config(c))
+    return st;
+  if (!tokens || past > c.capacity || tokens > c.capacity - past)
+    return fail(LLMI_HIP_INVALID_ARGUMENT,
+                "token chunk is empty or exceeds session capacity");
+  GraphDeltaParams dp{tokens, c.keyHeads, c.keyDim, c.valueHeads, c.valueDim};
+  GqaParams gp{tokens, c.queryHeads, c.kvHeads, c.headDim, past};
+  if (int st = check_delta(dp))
+    return st;
+  if (int st = check_gqa(gp))
+    return st;
+  if (select_gqa(gp) == GqaKernel::None)
+    return fail(LLMI_HIP_UNSUPPORTED, "session step: no attention kernel for this shape");
+  return LLMI_HIP_OK;
 }
 
 } // namespace
@@ -198,6 +220,26 @@ void llmi_hip_session_reset(llmi_hip_session *s) {
 
 unsigned llmi_hip_session_past(const llmi_hip_session *s) { return s ? s->past : 0; }
 
+int llmi_hip_session_restore(llmi_hip_session *s, unsigned past) {
+  if (!s)
+    return fail(LLMI_HIP_INVALID_ARGUMENT, "session: null session");
+  if (s->invalid)
+    return fail(LLMI_HIP_INVALID_ARGUMENT,
+                "session is invalid after a failed GPU step; reset it first");
+  if (past > s->cfg.capacity)
+    return fail(LLMI_HIP_INVALID_ARGUMENT, "session restore: past %u exceeds capacity %u",
+                past, s->cfg.capacity);
+  s->past = past;
+  return LLMI_HIP_OK;
+}
+
+int llmi_hip_session_check(const llmi_hip_session_config *config, unsigned past,
+                           unsigned tokens) {
+  if (!config)
+    return fail(LLMI_HIP_INVALID_ARGUMENT, "session: null config");
+  return check_step(*config, past, tokens);
+}
+
 int llmi_hip_session_invalid(const llmi_hip_session *s) { return s ? s->invalid : 1; }
 
 uint16_t *llmi_hip_session_key_cache(llmi_hip_session *s) {
@@ -224,21 +266,14 @@ int llmi_hip_session_step(llmi_hip_session *s, unsigned tokens, const float *dq,
   if (s->invalid)
     return fail(LLMI_HIP_INVALID_ARGUMENT,
                 "session is invalid after a failed GPU step");
-  if (!tokens || tokens > s->cfg.capacity - s->past)
-    return fail(LLMI_HIP_INVALID_ARGUMENT,
-                "token chunk is empty or exceeds session capacity");
+  if (int st = check_step(s->cfg, s->past, tokens))
+    return st;
   if (!dq || !dk || !dv || !beta || !decay || !delta_out || !q || !k || !v ||
       !gqa_out)
     return fail(LLMI_HIP_INVALID_ARGUMENT, "session step: null buffer");
   const llmi_hip_session_config &c = s->cfg;
   GraphDeltaParams dp{tokens, c.keyHeads, c.keyDim, c.valueHeads, c.valueDim};
   GqaParams gp{tokens, c.queryHeads, c.kvHeads, c.headDim, s->past};
-  if (int st = check_delta(dp))
-    return st;
-  if (int st = check_gqa(gp))
-    return st;
-  if (select_gqa(gp) == GqaKernel::None)
-    return fail(LLMI_HIP_UNSUPPORTED, "session step: no attention kernel for this shape");
   size_t need = llmi_hip_gqa_workspace_bytes(gp);
   size_t needDelta = llmi_hip_delta_workspace_bytes(dp);
   if (needDelta > need)
@@ -247,17 +282,18 @@ int llmi_hip_session_step(llmi_hip_session *s, unsigned tokens, const float *dq,
     return st;
 
   // Plan records, in graph order: DeltaUpdate (op 0), KvAppend (op 1),
-  // CausalGqa (op 2), as MetalDispatchInfo{opIndex, kernel, fusedOpIndex}.
-  // KvAppend and CausalGqa run through the fused entry point: one decode
-  // launch that also appends ({op 2, fused 1}), or append then prefill.
+  // CausalGqa (op 2). KvAppend and CausalGqa run through the fused entry
+  // point: one decode launch that also appends (recorded under op 1 and
+  // again under op 2), or append then prefill.
   size_t n = 0;
   for (unsigned i = 0, m = llmi_hip_dispatch_count(LLMI_HIP_OP_DELTA_UPDATE, &dp); i < m; ++i)
     record(records, cap, n, 0, llmi_hip_kernel_name(LLMI_HIP_OP_DELTA_UPDATE, &dp, i));
   const unsigned pairLaunches =
       llmi_hip_dispatch_count(LLMI_HIP_OP_KV_APPEND_CAUSAL_GQA, &gp);
   if (select_gqa(gp) == GqaKernel::Decode) {
-    record(records, cap, n, 2,
-           llmi_hip_kernel_name(LLMI_HIP_OP_KV_APPEND_CAUSAL_GQA, &gp, 0), 1);
+    const char *first = llmi_hip_kernel_name(LLMI_HIP_OP_KV_APPEND_CAUSAL_GQA, &gp, 0);
+    record(records, cap, n, 1, first);
+    record(records, cap, n, 2, first);
     for (unsigned i = 1; i < pairLaunches; ++i)
       record(records, cap, n, 2,
              llmi_hip_kernel_name(LLMI_HIP_OP_KV_APPEND_CAUSAL_GQA, &gp, i));

@@ -17,7 +17,7 @@ import torch
 
 from . import _lib
 
-_workspaces: dict[tuple[int, str], torch.Tensor] = {}
+_workspaces: dict[tuple[int, str, int], torch.Tensor] = {}
 
 
 def _ptr(t: torch.Tensor | None) -> int | None:
@@ -38,14 +38,21 @@ def _require(t: torch.Tensor, dtype: torch.dtype, name: str) -> None:
 
 
 def workspace(nbytes: int, device: torch.device | None = None, kind: str = "gqa") -> torch.Tensor:
-    """A workspace of at least nbytes, reused per (device, kind): calls on
-    one stream are ordered, so they can share it (its contents between calls
-    do not matter)."""
+    """A workspace of at least nbytes, reused per (device, kind, stream).
+    Calls on one stream are ordered, so they can share it (its contents
+    between calls do not matter); calls on different streams get different
+    buffers, so they never write the same partials. Each buffer is
+    allocated on its own stream, so when it grows torch's allocator hands
+    the old memory only to later work on that same stream, after the
+    kernels that used it."""
     dev = torch.device("cuda", torch.cuda.current_device()) if device is None else device
-    key = (dev.index if dev.index is not None else torch.cuda.current_device(), kind)
+    index = dev.index if dev.index is not None else torch.cuda.current_device()
+    stream = torch.cuda.current_stream(index)
+    key = (index, kind, stream.cuda_stream)
     ws = _workspaces.get(key)
     if ws is None or ws.numel() < nbytes:
-        ws = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=dev)
+        with torch.cuda.stream(stream):
+            ws = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=dev)
         _workspaces[key] = ws
     return ws
 

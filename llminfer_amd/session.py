@@ -11,6 +11,7 @@ the state.
     s = HipSession.open(capacity=8192)        # cfg shapes by default
     res = s.step(delta_q, delta_k, delta_v, beta, decay, q, k, v)
     res.delta_out, res.gqa_out, res.dispatches  # plan records {op_index, kernel}
+    HipSession.check(cfg, past, tokens)         # the step's checks, no device
 """
 from __future__ import annotations
 
@@ -53,6 +54,12 @@ class HipSession:
                                                  C.byref(h)))
         return cls(h.value, cfg, dev)
 
+    @staticmethod
+    def check(cfg: _lib.SessionConfig, past: int, tokens: int) -> int:
+        """The status a step of `tokens` at `past` would get from its checks
+        (llmi_hip_session_check; host only)."""
+        return _lib.load().llmi_hip_session_check(C.byref(cfg), past, tokens)
+
     def close(self) -> None:
         if self._h:
             _lib.load().llmi_hip_session_close(self._h)
@@ -80,6 +87,24 @@ class HipSession:
         ptr = getattr(_lib.load(), ptr_fn)(self._h)
         torch.cuda.synchronize(self.device)
         return torch.as_tensor(_DeviceArray(ptr, shape, dtype), device=self.device).clone()
+
+    def restore(self, past: int) -> None:
+        """Declare cache rows [0, past) and the recurrent state as written
+        through the writable views (a restored checkpoint, a seeded test)."""
+        _lib.check(_lib.load().llmi_hip_session_restore(self._h, past))
+
+    def writable_views(self) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+        """Zero-copy tensors over the session-owned K cache, V cache and
+        recurrent state, for seeding them before restore()."""
+        c = self.cfg
+        lib = _lib.load()
+        kv = (c.capacity, c.kvHeads, c.headDim)
+        mk = lambda fn, shape, dt: torch.as_tensor(
+            _DeviceArray(getattr(lib, fn)(self._h), shape, dt), device=self.device)
+        return (mk("llmi_hip_session_key_cache", kv, torch.float16),
+                mk("llmi_hip_session_value_cache", kv, torch.float16),
+                mk("llmi_hip_session_recurrent_state",
+                   (c.valueHeads, c.keyDim, c.valueDim), torch.float32))
 
     def key_cache(self) -> torch.Tensor:
         c = self.cfg
@@ -122,10 +147,13 @@ class HipSession:
             self._h, T, dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), beta.data_ptr(),
             decay.data_ptr(), delta_out.data_ptr(), q.data_ptr(), k.data_ptr(),
             v.data_ptr(), gqa_out.data_ptr(), recs, len(recs), C.byref(n)))
+        # Records as tools/run/Main.cpp:244-255 prints them: epilogue and
+        # fused_op_index only for a record with a non-empty epilogue.
         plan = []
         for i in range(min(n.value, len(recs))):
             rec = {"op_index": int(recs[i].op_index), "kernel": recs[i].kernel.decode()}
-            if recs[i].fused_op_index != _lib.NO_FUSED_OP:
+            if recs[i].epilogue:
+                rec["epilogue"] = recs[i].epilogue.decode()
                 rec["fused_op_index"] = int(recs[i].fused_op_index)
             plan.append(rec)
         return StepResult(self.past, delta_out, gqa_out, plan)

@@ -174,47 +174,55 @@ static void parallel_for(size_t tasks, int threads, task_fn fn, void *ctx) {
 
 /* ------------------------------------------------------------- GQA (f64) */
 
-void orc_gqa_dense_f64(const uint16_t *q, const uint16_t *k_cache,
-                       const uint16_t *v_cache, double *out, uint32_t T,
-                       uint32_t Hq, uint32_t Hkv, uint32_t d, uint32_t P) {
-  size_t kv_stride = (size_t)Hkv * d;
-  uint32_t group = Hq / Hkv;
+typedef struct {
+  const uint16_t *q, *k, *v;
+  double *out;
+  uint32_t T, Hq, Hkv, d, P;
+} dense_job;
+
+/* One (token, q-head) row of the dense attention; rows are independent, so
+ * the result does not depend on how they are spread over threads. */
+static void dense_row(void *ctx, size_t row) {
+  const dense_job *j = (const dense_job *)ctx;
+  uint32_t d = j->d, t = (uint32_t)(row / j->Hq), h = (uint32_t)(row % j->Hq);
+  size_t kv_stride = (size_t)j->Hkv * d;
+  size_t kv_off = (size_t)(h / (j->Hq / j->Hkv)) * d;
   double scale = 1.0 / sqrt((double)d);
-  double *p = (double *)malloc(sizeof(double) * ((size_t)P + T));
+  uint32_t visible = j->P + t + 1;
+  double *p = (double *)malloc(sizeof(double) * visible);
   double *qf = (double *)malloc(sizeof(double) * d);
-  for (uint32_t t = 0; t < T; ++t) {
-    uint32_t visible = P + t + 1;
-    for (uint32_t h = 0; h < Hq; ++h) {
-      size_t row = (size_t)t * Hq + h;
-      size_t kv_off = (size_t)(h / group) * d;
-      for (uint32_t x = 0; x < d; ++x)
-        qf[x] = orc_f16_to_f32(q[row * d + x]);
-      double mx = -INFINITY;
-      for (uint32_t j = 0; j < visible; ++j) {
-        const uint16_t *kr = k_cache + (size_t)j * kv_stride + kv_off;
-        double dot = 0.0;
-        for (uint32_t x = 0; x < d; ++x)
-          dot += qf[x] * (double)orc_f16_to_f32(kr[x]);
-        p[j] = dot * scale;
-        if (p[j] > mx)
-          mx = p[j];
-      }
-      double den = 0.0;
-      for (uint32_t j = 0; j < visible; ++j) {
-        p[j] = exp(p[j] - mx);
-        den += p[j];
-      }
-      for (uint32_t x = 0; x < d; ++x) {
-        double acc = 0.0;
-        for (uint32_t j = 0; j < visible; ++j)
-          acc += p[j] * (double)orc_f16_to_f32(
-                            v_cache[(size_t)j * kv_stride + kv_off + x]);
-        out[row * d + x] = acc / den;
-      }
-    }
+  for (uint32_t x = 0; x < d; ++x)
+    qf[x] = orc_f16_to_f32(j->q[row * d + x]);
+  double mx = -INFINITY;
+  for (uint32_t k = 0; k < visible; ++k) {
+    const uint16_t *kr = j->k + (size_t)k * kv_stride + kv_off;
+    double dot = 0.0;
+    for (uint32_t x = 0; x < d; ++x)
+      dot += qf[x] * (double)orc_f16_to_f32(kr[x]);
+    p[k] = dot * scale;
+    if (p[k] > mx)
+      mx = p[k];
+  }
+  double den = 0.0;
+  for (uint32_t k = 0; k < visible; ++k) {
+    p[k] = exp(p[k] - mx);
+    den += p[k];
+  }
+  for (uint32_t x = 0; x < d; ++x) {
+    double acc = 0.0;
+    for (uint32_t k = 0; k < visible; ++k)
+      acc += p[k] * (double)orc_f16_to_f32(j->v[(size_t)k * kv_stride + kv_off + x]);
+    j->out[row * d + x] = acc / den;
   }
   free(qf);
   free(p);
+}
+
+void orc_gqa_dense_f64(const uint16_t *q, const uint16_t *k_cache,
+                       const uint16_t *v_cache, double *out, uint32_t T,
+                       uint32_t Hq, uint32_t Hkv, uint32_t d, uint32_t P) {
+  dense_job job = {q, k_cache, v_cache, out, T, Hq, Hkv, d, P};
+  parallel_for((size_t)T * Hq, 0, dense_row, &job);
 }
 
 /* --------------------------------------------------- GQA eager fp16 path */

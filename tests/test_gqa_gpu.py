@@ -145,14 +145,14 @@ def test_prefill_moving_reference(gpu, growth, qscale):
     x.q = oracle.f32_to_f16(oracle.f16_to_f32(x.q) * qscale)
     got = _run(x, gpu)
     want = oracle.gqa_dense_f64(x.q, x.k_cache, x.v_cache, P)
-    # A sharp softmax puts the output at the mercy of the few largest
-    # weights, each rounded to fp16 before the PV product: the bar is the
-    # north-star tolerance on top of that first-order rounding bound.
+    # The north-star bar, max-abs <= 2e-3, holds outright. A sharp softmax
+    # puts the output at the mercy of the few largest weights, each rounded
+    # to fp16 before the PV product, so the error is also reported against
+    # that first-order rounding bound.
     bound = p_rounding_bound(x.q, x.k_cache, x.v_cache, P)
-    assert np.all(np.isfinite(got))
     excess = np.max(np.abs(got - want) - bound)
-    print(f"  max abs err {np.max(np.abs(got - want)):.3g}, beyond P rounding {excess:.3g}")
-    assert excess <= TOL
+    err = _check(got, want)
+    print(f"  max abs err {err:.3g}, beyond P rounding {excess:.3g}")
 
 
 @pytest.mark.parametrize("case", [(19, 4, 2, 12, 0), (7, 4, 2, 256, 33)])
@@ -179,8 +179,8 @@ def test_reference_kernel_cases(gpu, case):
     assert np.max(np.abs(got - want)) <= TOL
 
 
-@pytest.mark.parametrize("T,past", [(1, 0), (1, 4096), (1, 33), (3, 100), (64, 640),
-                                    (65, 17), (200, 300)])
+@pytest.mark.parametrize("T,past", [(1, 0), (1, 4096), (1, 33), (1, 32768), (1, 32799),
+                                    (3, 100), (64, 640), (65, 17), (200, 300)])
 def test_fused_append_attention(gpu, T, past):
     """llmi_hip_kv_append_causal_gqa: the cache rows it writes are the bytes
     KvAppend writes, and the attention equals the oracle on the appended

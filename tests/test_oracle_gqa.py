@@ -8,8 +8,18 @@ What fixes each result (no test retypes the oracle's loop):
   * causality: changing cache rows beyond P+t never changes row t;
   * the reference kernel test's own generator and cases
     (tests/FlashAttentionTest.mm:28-36, 108-109) with its tolerance
-    |a-e| <= 2e-4 + 5e-4|e| (:80-81) applied to the fp32 and eager paths.
+    |a-e| <= 2e-4 + 5e-4|e| (:80-81) applied to the fp32 and eager paths;
+  * the eager fp16 path's rounding points (gqaScores, Reference.metal:303-323;
+    gqaSoftmax/gqaValue, Graph.metal:172-230): Hugging Face's own
+    eager_attention_forward (transformers, models/qwen3_5, the attention the
+    reference's parity harness compares against) run in fp16 on the CPU, on
+    inputs whose sums are exact in fp32 in any order, so both must agree bit
+    for bit; the same inputs are checked to change when any one rounding
+    point (fp16 dot, fp16 scaled score, fp16 probability) is dropped;
+  * KvAppend (cacheAppend, Reference.metal:295-301): numpy slice assignment.
 """
+import types
+
 import numpy as np
 import pytest
 
@@ -121,3 +131,106 @@ def test_fp32_baseline_matches_dense(T, P):
     e = oracle.gqa_dense_f64(x.q, x.k_cache, x.v_cache, P)
     got = _f(oracle.gqa_f32(x.q, x.k_cache, x.v_cache, P, threads=4))
     assert np.max(np.abs(got - e)) <= 1e-3
+
+
+# ------------------------------------------------ eager fp16 rounding points
+
+def _hf_eager_f16(q, kc, vc, P):
+    """transformers' eager_attention_forward in fp16 on the CPU, with the
+    additive causal mask its models build (finfo(fp16).min where masked)."""
+    import torch
+    from transformers.models.qwen3_5.modeling_qwen3_5 import eager_attention_forward
+    T, hq, d = q.shape
+    n = P + T
+    as16 = lambda a: torch.from_numpy(np.ascontiguousarray(a).view(np.float16))
+    tq = as16(q).permute(1, 0, 2)[None]
+    tk = as16(kc[:n]).permute(1, 0, 2)[None]
+    tv = as16(vc[:n]).permute(1, 0, 2)[None]
+    mask = torch.full((T, n), torch.finfo(torch.float16).min, dtype=torch.float16)
+    for t in range(T):
+        mask[t, :P + t + 1] = 0
+    module = types.SimpleNamespace(num_key_value_groups=hq // kc.shape[1], training=False)
+    out, _ = eager_attention_forward(module, tq, tk, tv, mask[None, None], d ** -0.5)
+    return out[0].numpy().view(np.uint16)
+
+
+def _exact_sum_case(seed, T, P, hq=4, hkv=2, d=12):
+    """Scores q.k = q0 k0 + q1 k1 with dyadic operands (exact in fp32, not
+    in fp16: k1 is an odd multiple of 2^-12 next to k0 in [1.5, 3.5]); every
+    V row has two ones, so each output channel sums two probabilities
+    exactly. d = 12 makes the 1/sqrt(d) scaling inexact."""
+    rng = np.random.default_rng(seed)
+    n = P + T
+    assert n <= d
+    q = np.zeros((T, hq, d), np.float32)
+    q[:, :, 0] = rng.choice([0.75, 1.0, 1.25], (T, hq))
+    q[:, :, 1] = rng.choice([0.5, 1.0], (T, hq))
+    k = np.zeros((n, hkv, d), np.float32)
+    k[:, :, 0] = rng.integers(3, 8, (n, hkv)) * 0.5
+    k[:, :, 1] = (2 * rng.integers(0, 8, (n, hkv)) + 1) * 2.0 ** -12
+    v = np.zeros((n, hkv, d), np.float32)
+    for j in range(n):
+        v[j, :, j] = 1.0
+        v[j, :, (j + 1) % d] = 1.0
+    return oracle.f32_to_f16(q), oracle.f32_to_f16(k), oracle.f32_to_f16(v)
+
+
+def _eager_dropping(q, kc, vc, P, drop):
+    """The eager path with one rounding point left out -- only to show that
+    the cases above tell the rounding points apart."""
+    T, hq, d = q.shape
+    g = hq // kc.shape[1]
+    rnd = lambda x: _f(oracle.f32_to_f16(np.float32(x))).astype(np.float32)
+    rs = np.float32(1) / np.sqrt(np.float32(d))
+    out = np.zeros(q.shape, np.uint16)
+    for t in range(T):
+        n = P + t + 1
+        for h in range(hq):
+            dot = (_f(kc[:n, h // g]) @ _f(q[t, h])).astype(np.float32)
+            dot = dot if drop == "dot" else rnd(dot)
+            s = (dot * rs).astype(np.float32)
+            s = s if drop == "scale" else rnd(s)
+            e = np.exp((s - s.max()).astype(np.float64)).astype(np.float32)
+            p = (e / np.float32(e.astype(np.float64).sum())).astype(np.float32)
+            p = p if drop == "prob" else rnd(p)
+            out[t, h] = oracle.f32_to_f16(
+                (p.astype(np.float64) @ _f(vc[:n, h // g])).astype(np.float32))
+    return out
+
+
+@pytest.mark.parametrize("T,P", [(1, 11), (1, 6), (3, 8), (4, 0)])
+def test_eager_rounding_points_match_hf(T, P):
+    changed = {"dot": 0, "scale": 0, "prob": 0}
+    for seed in range(4):
+        q, k, v = _exact_sum_case(seed, T, P)
+        got = oracle.gqa_eager_f16(q, k, v, P)
+        assert np.array_equal(got, _hf_eager_f16(q, k, v, P)), seed
+        for drop in changed:
+            changed[drop] += int(np.sum(_eager_dropping(q, k, v, P, drop) != got))
+    # Each rounding point decides some output bits of these cases.
+    assert all(changed[d] > 0 for d in changed), changed
+
+
+def test_eager_close_to_hf_on_normal_inputs():
+    """N(0,1) decode at d=256: the summation order differs (the oracle's
+    sequential fma chain against torch's blocked sums), which moves an fp32
+    dot product across an fp16 rounding boundary now and then, so outputs
+    mostly agree bitwise and otherwise by a few fp16 ulps of |o| < 0.5."""
+    x = oracle.make_gqa_inputs(21, 1, 16, 4, 256, 300)
+    a = _f(oracle.gqa_eager_f16(x.q, x.k_cache, x.v_cache, 300))
+    b = _f(_hf_eager_f16(x.q, x.k_cache, x.v_cache, 300))
+    assert np.mean(a == b) > 0.95
+    assert np.max(np.abs(a - b)) <= 2.0 ** -12
+
+
+# ------------------------------------------------------------------ KvAppend
+
+@pytest.mark.parametrize("T,hkv,d,past,cap", [(1, 4, 256, 4096, 8192), (7, 2, 12, 0, 9),
+                                              (3, 1, 64, 5, 8)])
+def test_kv_append_is_slice_assignment(T, hkv, d, past, cap):
+    src = oracle.normal_f16(T, past, (T, hkv, d))
+    cache = oracle.normal_f16(cap, 9, (cap, hkv, d))
+    want = cache.copy()
+    want[past:past + T] = src
+    oracle.kv_append(src, cache, past)
+    assert np.array_equal(cache, want)
