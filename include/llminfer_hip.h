@@ -248,6 +248,23 @@ LLMI_HIP_API int llmi_hip_kv_append_causal_gqa(const uint16_t *q, const uint16_t
                                   void *workspace, size_t workspace_bytes,
                                   void *stream);
 
+/* The same as llmi_hip_kv_append_causal_gqa, allocating nothing and taking
+ * no workspace. It has no counterpart in the reference: it is for callers
+ * that cannot allocate device memory (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc). The split-K decode's
+ * partials go to a static device array of LLMI_HIP_NOALLOC_SCRATCH_BYTES
+ * that each device the library runs on holds until the process ends; a
+ * shape whose partials need more returns LLMI_HIP_WORKSPACE before any
+ * launch (the north-star shapes need at most 2.1 MB). Calls that overlap on
+ * one device share that array and race; calls on one stream are ordered. */
+#define LLMI_HIP_NOALLOC_SCRATCH_BYTES (8u << 20)
+LLMI_HIP_API int llmi_hip_kv_append_causal_gqa_noalloc(const uint16_t *q,
+                                                       const uint16_t *k_new,
+                                                       const uint16_t *v_new,
+                                                       uint16_t *k_cache, uint16_t *v_cache,
+                                                       uint16_t *out, GqaParams p,
+                                                       void *stream);
+
 /* ------------------------------------------------------------- DeltaUpdate
  * Replaces graphDeltaUpdate (Graph.metal:146-170 with updateDeltaColumn,
  * Reference.metal:182-197): the gated delta rule over T tokens, per value

@@ -31,6 +31,8 @@ OP_L2_NORM = 9
 OP_DELTA_GATES = 10
 OP_GATED_RMS_NORM = 11
 
+NOALLOC_SCRATCH_BYTES = 8 << 20  # LLMI_HIP_NOALLOC_SCRATCH_BYTES
+
 
 class CacheParams(C.Structure):
     _fields_ = [("count", C.c_uint), ("offset", C.c_uint)]
@@ -115,6 +117,8 @@ SIGNATURES = {
     "llmi_hip_gqa_workspace_bytes": (_SZ, [GqaParams]),
     "llmi_hip_kv_append_causal_gqa": (C.c_int, [_P, _P, _P, _P, _P, _P, GqaParams, _P, _SZ,
                                                 _P]),
+    "llmi_hip_kv_append_causal_gqa_noalloc": (C.c_int, [_P, _P, _P, _P, _P, _P, GqaParams,
+                                                        _P]),
     "llmi_hip_delta_update": (C.c_int, [_P, _P, _P, _P, _P, _P, _P,
                                         GraphDeltaParams, _P, _SZ, _P]),
     "llmi_hip_delta_workspace_bytes": (_SZ, [GraphDeltaParams]),

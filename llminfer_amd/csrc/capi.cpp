@@ -301,7 +301,6 @@ size_t llmi_hip_gqa_workspace_bytes(GqaParams p) {
 } // extern "C"
 
 namespace llmi {
-namespace {
 
 // CausalGqa with an optional fused KvAppend (k_new/v_new non-null).
 int run_gqa(const uint16_t *q, const uint16_t *k_new, const uint16_t *v_new,
@@ -346,7 +345,6 @@ int run_gqa(const uint16_t *q, const uint16_t *k_new, const uint16_t *v_new,
                   "gqaGeneric");
 }
 
-} // namespace
 } // namespace llmi
 
 extern "C" {

@@ -22,6 +22,13 @@ enum class DeltaKernel { Chunked, Recurrent, Generic };
 GqaKernel select_gqa(const GqaParams &p);
 DeltaKernel select_delta(const GraphDeltaParams &p);
 
+// CausalGqa with an optional fused KvAppend (k_new and v_new non-null):
+// validation, workspace check and the launches (capi.cpp).
+int run_gqa(const uint16_t *q, const uint16_t *k_new, const uint16_t *v_new,
+            uint16_t *k_cache, uint16_t *v_cache, uint16_t *out,
+            const GqaParams &p, void *workspace, size_t workspace_bytes,
+            void *stream);
+
 // Launch count and names of the chunked DeltaNet path (delta_chunked.hip).
 unsigned delta_chunked_dispatches();
 const char *delta_chunked_kernel_name(unsigned index);

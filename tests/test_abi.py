@@ -226,3 +226,26 @@ def test_session_open_validates_config():
     assert h.value is None
     assert lib.llmi_hip_session_step(None, 1, *([None] * 10), None, 0, None) == \
         _lib.INVALID_ARGUMENT
+
+
+def test_noalloc_rejects_partials_beyond_its_scratch():
+    """The allocation-free decode refuses, before any launch, a split plan
+    whose partials exceed its static scratch (here forced by planning for
+    far more resident workgroups than a GPU has)."""
+    import subprocess
+    import sys
+    code = (
+        "from llminfer_amd import _lib\n"
+        "lib = _lib.load()\n"
+        "p = _lib.GqaParams(1, 128, 16, 256, 32768)\n"
+        "need = lib.llmi_hip_gqa_workspace_bytes(p)\n"
+        "assert need > _lib.NOALLOC_SCRATCH_BYTES, need\n"
+        "st = lib.llmi_hip_kv_append_causal_gqa_noalloc(1, 1, 1, 1, 1, 1, p, None)\n"
+        "assert st == _lib.WORKSPACE, st\n"
+        "assert b'static scratch' in lib.llmi_hip_last_error()\n"
+        "assert lib.llmi_hip_kv_append_causal_gqa_noalloc(None, 1, 1, 1, 1, 1, p, None) == "
+        "_lib.INVALID_ARGUMENT\n")
+    env = dict(__import__("os").environ, LLMI_DECODE_TARGET_WGS="65536")
+    r = subprocess.run([sys.executable, "-c", code], cwd=str(ROOT), env=env,
+                       capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stderr
