@@ -5,43 +5,49 @@
 // whole state column in device memory and walks it twice per token. Here
 // the state lives in registers for the whole call:
 //
-//  * one wave serves 8 state columns of one value head; 8 lanes share a
-//    column and each holds 16 of its dk = 128 rows (dk = 64: 8 rows);
+//  * a workgroup of NW waves serves a slice of CW consecutive state columns
+//    of one value head; lane l of a wave holds column l % CW, and the wave's
+//    64 / CW lane groups and the NW waves split the dk rows between them
+//    (RPL rows per lane). A state load instruction therefore reads whole
+//    CW * 4-byte row segments (64 lanes over 64 / CW rows), and the grid
+//    has Hv * dv / CW workgroups;
 //  * per token the two column dot products (k.S for the prediction and q.S
-//    for the output) are partial sums over a lane's rows, finished with
-//    3 DPP row permutes over the 8 lanes of the column;
+//    for the output) are partial sums over a lane's rows; the partials of
+//    a column meet in LDS, where every lane of the column adds them in the
+//    same order, so all of them hold the same prediction;
 //  * the state is read from HBM once at the start and written once at the
 //    end, so a decode step moves exactly the 2 x Hv*dk*dv*4 state bytes plus
 //    the step's q/k/v/gates.
 //
 // Summation order inside a dot product differs from the reference's single
-// fma chain (four interleaved chains per lane plus the lane tree); the
+// fma chain (four interleaved chains per lane plus the partials in LDS); the
 // result stays within fp32 rounding of the sequential order.
 #include "hip_common.hpp"
 #include "kernels.hpp"
 
+#include <stdlib.h>
+
 namespace llmi {
 namespace {
 
-constexpr int kLanesPerCol = 8;
-constexpr int kColsPerWave = 64 / kLanesPerCol;
-
-template <int DK>
-__global__ __launch_bounds__(64) void delta_recurrent_kernel(
+template <int DK, int CW, int NW>
+__global__ __launch_bounds__(64 * NW) void delta_recurrent_kernel(
     const float *__restrict__ q, const float *__restrict__ k,
     const half_t *__restrict__ v, const float *__restrict__ beta,
     const float *__restrict__ decay, float *__restrict__ state,
     half_t *__restrict__ out, unsigned T, unsigned Hk, unsigned Hv,
     unsigned DV) {
-  constexpr int RPL = DK / kLanesPerCol; // rows per lane
-  static_assert(RPL % 4 == 0, "rows per lane must be a multiple of 4");
-  const unsigned lane = threadIdx.x;
-  const unsigned cw = lane / kLanesPerCol, rg = lane % kLanesPerCol;
-  const unsigned colsPerHead = DV / kColsPerWave;
-  const unsigned h = blockIdx.x / colsPerHead;
-  const unsigned col = (blockIdx.x % colsPerHead) * kColsPerWave + cw;
+  constexpr int RG = 64 / CW;  // row groups per wave
+  constexpr int NP = NW * RG;  // partial sums per column
+  constexpr int RPL = DK / NP; // rows per lane
+  static_assert(RPL % 4 == 0 && RPL * NP == DK, "rows per lane must be a multiple of 4");
+  const unsigned tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+  const unsigned c = lane % CW, part = wave * RG + lane / CW;
+  const unsigned slices = DV / CW;
+  const unsigned h = blockIdx.x / slices;
+  const unsigned col = (blockIdx.x % slices) * CW + c;
   const unsigned kh = h / (Hv / Hk);
-  const unsigned row0 = rg * RPL;
+  const unsigned row0 = part * RPL;
   const size_t vwidth = (size_t)Hv * DV;
 
   float S[RPL];
@@ -50,6 +56,7 @@ __global__ __launch_bounds__(64) void delta_recurrent_kernel(
   for (int m = 0; m < RPL; ++m)
     S[m] = sbase[(size_t)m * DV];
 
+  __shared__ float sPred[NP][CW], sY[NP][CW];
   for (unsigned t = 0; t < T; ++t) {
     const float *kt = k + ((size_t)t * Hk + kh) * DK + row0;
     const float *qt = q + ((size_t)t * Hk + kh) * DK + row0;
@@ -72,7 +79,12 @@ __global__ __launch_bounds__(64) void delta_recurrent_kernel(
 #pragma unroll
     for (int m = 0; m < RPL; ++m)
       p4[m % 4] = fmaf(S[m] * a, kr[m], p4[m % 4]);
-    float pred = group_sum<kLanesPerCol>((p4[0] + p4[1]) + (p4[2] + p4[3]));
+    sPred[part][c] = (p4[0] + p4[1]) + (p4[2] + p4[3]);
+    __syncthreads();
+    float pred = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NP; ++i)
+      pred += sPred[i][c];
     const float delta = (vj - pred) * b;
 
     float y4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -81,9 +93,15 @@ __global__ __launch_bounds__(64) void delta_recurrent_kernel(
       S[m] = fmaf(kr[m], delta, S[m] * a);
       y4[m % 4] = fmaf(S[m], qr[m], y4[m % 4]);
     }
-    float y = group_sum<kLanesPerCol>((y4[0] + y4[1]) + (y4[2] + y4[3]));
-    if (rg == 0)
+    sY[part][c] = (y4[0] + y4[1]) + (y4[2] + y4[3]);
+    __syncthreads();
+    if (part == 0) {
+      float y = 0.0f;
+#pragma unroll
+      for (int i = 0; i < NP; ++i)
+        y += sY[i][c];
       out[(size_t)t * vwidth + (size_t)h * DV + col] = (half_t)y;
+    }
   }
 
 #pragma unroll
@@ -139,9 +157,63 @@ hipError_t launch_delta_generic(const float *q, const float *k,
   return hipGetLastError();
 }
 
+namespace {
+
+// Column slice of a workgroup: 32 columns when dv allows, else 16.
+// LLMI_DELTA_DECODE_CW (64, 32 or 16) and LLMI_DELTA_DECODE_NW (waves per
+// workgroup: 2, 4 or 8) override the choice for tuning.
+unsigned env_or(const char *name, unsigned dflt) {
+  const char *e = getenv(name);
+  if (!e || !*e)
+    return dflt;
+  long x = strtol(e, nullptr, 10);
+  return x > 0 ? (unsigned)x : dflt;
+}
+
+unsigned slice_cols(unsigned dv) {
+  static const unsigned forced = env_or("LLMI_DELTA_DECODE_CW", 0);
+  if (forced && dv % forced == 0)
+    return forced;
+  return dv % 32 == 0 ? 32 : 16;
+}
+
+unsigned waves_per_group() {
+  static const unsigned v = env_or("LLMI_DELTA_DECODE_NW", 4);
+  return v;
+}
+
+template <int DK, int CW, int NW>
+hipError_t launch_rec(const float *q, const float *k, const uint16_t *v, const float *beta,
+                      const float *decay, float *state, uint16_t *out, const DeltaShape &s,
+                      hipStream_t stream) {
+  hipLaunchKernelGGL((delta_recurrent_kernel<DK, CW, NW>), dim3(s.Hv * (s.Dv / CW)),
+                     dim3(64 * NW), 0, stream, q, k, reinterpret_cast<const half_t *>(v),
+                     beta, decay, state, reinterpret_cast<half_t *>(out), s.T, s.Hk, s.Hv,
+                     s.Dv);
+  return hipGetLastError();
+}
+
+template <int DK, int CW>
+hipError_t launch_rec_cw(const float *q, const float *k, const uint16_t *v, const float *beta,
+                         const float *decay, float *state, uint16_t *out, const DeltaShape &s,
+                         hipStream_t stream) {
+  // Rows per lane DK / (NW * 64 / CW) must stay a multiple of 4.
+  constexpr bool ok8 = DK % (8 * (64 / CW) * 4) == 0, ok2 = DK % (2 * (64 / CW) * 4) == 0;
+  const unsigned nw = waves_per_group();
+  if constexpr (ok8)
+    if (nw == 8)
+      return launch_rec<DK, CW, 8>(q, k, v, beta, decay, state, out, s, stream);
+  if constexpr (ok2)
+    if (nw == 2)
+      return launch_rec<DK, CW, 2>(q, k, v, beta, decay, state, out, s, stream);
+  return launch_rec<DK, CW, 4>(q, k, v, beta, decay, state, out, s, stream);
+}
+
+} // namespace
+
 bool delta_recurrent_supported(const DeltaShape &s) {
-  return (s.Dk == 64 || s.Dk == 128) && s.Dv % kColsPerWave == 0 &&
-         s.Hk >= 1 && s.Hv % s.Hk == 0 && s.T >= 1;
+  return (s.Dk == 64 || s.Dk == 128) && s.Dv % 16 == 0 && s.Hk >= 1 &&
+         s.Hv % s.Hk == 0 && s.T >= 1;
 }
 
 hipError_t launch_delta_recurrent(const float *q, const float *k,
@@ -149,18 +221,19 @@ hipError_t launch_delta_recurrent(const float *q, const float *k,
                                   const float *decay, float *state,
                                   uint16_t *out, const DeltaShape &s,
                                   hipStream_t stream) {
-  dim3 grid(s.Hv * (s.Dv / kColsPerWave));
-  if (s.Dk == 64)
-    hipLaunchKernelGGL(delta_recurrent_kernel<64>, grid, dim3(64), 0, stream,
-                       q, k, reinterpret_cast<const half_t *>(v), beta, decay,
-                       state, reinterpret_cast<half_t *>(out), s.T, s.Hk, s.Hv,
-                       s.Dv);
-  else
-    hipLaunchKernelGGL(delta_recurrent_kernel<128>, grid, dim3(64), 0, stream,
-                       q, k, reinterpret_cast<const half_t *>(v), beta, decay,
-                       state, reinterpret_cast<half_t *>(out), s.T, s.Hk, s.Hv,
-                       s.Dv);
-  return hipGetLastError();
+  const unsigned cw = slice_cols(s.Dv);
+  if (s.Dk == 64) {
+    if (cw == 64)
+      return launch_rec_cw<64, 64>(q, k, v, beta, decay, state, out, s, stream);
+    if (cw == 32)
+      return launch_rec_cw<64, 32>(q, k, v, beta, decay, state, out, s, stream);
+    return launch_rec_cw<64, 16>(q, k, v, beta, decay, state, out, s, stream);
+  }
+  if (cw == 64)
+    return launch_rec_cw<128, 64>(q, k, v, beta, decay, state, out, s, stream);
+  if (cw == 32)
+    return launch_rec_cw<128, 32>(q, k, v, beta, decay, state, out, s, stream);
+  return launch_rec_cw<128, 16>(q, k, v, beta, decay, state, out, s, stream);
 }
 
 } // namespace llmi
