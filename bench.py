@@ -615,6 +615,99 @@ class DeltaPrefill(Workload):
                 "gpu_vs_cpu_max_abs": err, "gpu_vs_cpu_state_rel": serr}
 
 
+def norm_delta_bytes(T: int, hk: int, dk: int, hv: int, dv: int) -> int:
+    """The fused L2Norm -> DeltaUpdate pair: fp16 q, k instead of fp32."""
+    return delta_bytes(T, hk, dk, hv, dv) - 4 * T * hk * dk
+
+
+class DeltaNormUpdate(Workload):
+    """The L2Norm(q), L2Norm(k) -> DeltaUpdate pair of a DeltaNet layer
+    (Qwen35ModelBuilder.cpp:155-156) fused into one call
+    (llmi_hip_l2_norm_delta_update: fp16 q/k normalised in the update's own
+    loads), next to the same pair unfused (two l2NormF32 launches and
+    DeltaUpdate on fp32 q/k). Operand sets rotate past the MALL."""
+    bound = "hbm"
+    labels = ("fused", "unfused")
+    dominant = "fused"
+
+    def __init__(self, dev, T, sets, seed, hk=16, dk=128, hv=32, dv=128):
+        import numpy as np
+        import torch
+        from llminfer_amd import ops
+        self.T, self.sets, self.shape = T, sets, (hk, dk, hv, dv)
+        self.tokens = T
+        self.name = f"l2norm_delta_T{T}"
+        qs = float(np.float32(1.0) / np.sqrt(np.float32(dk)))
+        g = torch.Generator(device=dev).manual_seed(seed)
+        self.x = []
+        for _ in range(sets):
+            _, _, v, beta, decay = _delta_inputs(g, dev, T, hk, dk, hv, dv)
+            x = dict(q16=_randn16(g, (T, hk * dk), dev), k16=_randn16(g, (T, hk * dk), dev),
+                     v=v, beta=beta, decay=decay,
+                     qf=torch.empty((T, hk * dk), dtype=torch.float32, device=dev),
+                     kf=torch.empty((T, hk * dk), dtype=torch.float32, device=dev),
+                     s1=torch.randn((hv, dk, dv), generator=g, device=dev) * 0.1,
+                     o1=torch.empty_like(v), o2=torch.empty_like(v))
+            x["s2"] = x["s1"].clone()
+            x["fused"] = ops.bind_l2_norm_delta_update(x["q16"], x["k16"], v, beta, decay,
+                                                       x["s1"], x["o1"], 1e-6, qs)
+            x["unfused"] = [ops.bind_l2_norm(x["q16"], x["qf"], dk, 1e-6, qs),
+                            ops.bind_l2_norm(x["k16"], x["kf"], dk, 1e-6, 1.0),
+                            ops.bind_delta_update(x["qf"], x["kf"], v, beta, decay, x["s2"],
+                                                  x["o2"])]
+            self.x.append(x)
+        self.bytes = {"fused": norm_delta_bytes(T, hk, dk, hv, dv),
+                      "unfused": norm_delta_bytes(T, hk, dk, hv, dv)}
+
+    def op(self, label, i):
+        x = self.x[i % self.sets]
+        if label == "fused":
+            x["fused"]()
+        else:
+            for b in x["unfused"]:
+                b()
+
+    def kernels(self):
+        return self.x[0]["fused"].what
+
+    def work(self, i):
+        return self.bytes["fused"]
+
+    def config(self):
+        hk, dk, hv, dv = self.shape
+        return {"workload": self.name, "tokens": self.T, "key_heads": hk, "key_dim": dk,
+                "value_heads": hv, "value_dim": dv, "operand_sets": self.sets}
+
+    def cpu(self, budget_s):
+        import numpy as np
+        import oracle
+        import torch
+        hk, dk, hv, dv = self.shape
+        x = self.x[0]
+        torch.cuda.synchronize()
+        s0 = host_f32(x["s1"])
+        x["fused"]()
+        torch.cuda.synchronize()
+        gpu_out = oracle.f16_to_f32(host_u16(x["o1"]))
+        q16, k16, v = host_u16(x["q16"]), host_u16(x["k16"]), host_u16(x["v"])
+        beta, decay = host_f32(x["beta"]), host_f32(x["decay"])
+        qs = float(np.float32(1.0) / np.sqrt(np.float32(dk)))
+        thr = cpu_threads()
+
+        def run():
+            q = oracle.l2norm_f32(q16, dk, 1e-6, qs)
+            k = oracle.l2norm_f32(k16, dk, 1e-6, 1.0)
+            return oracle.delta_recurrent_f32(q, k, v, beta, decay, s0, thr)
+
+        want, _ = run()
+        err = float(np.max(np.abs(gpu_out - oracle.f16_to_f32(want))))
+        sec, runs = time_cpu(run, budget_s)
+        return {"value": sec * 1e6, "unit": "µs/layer", "cores": thr, "kind": "port",
+                "sample": f"L2Norm q, k + the {self.T}-token DeltaUpdate on one set, {runs} runs "
+                          "(oracle orc_l2norm_f32 + orc_delta_recurrent_f32)",
+                "gpu_vs_cpu_max_abs": err}
+
+
 class HybridDecode(Workload):
     """DeltaNet decode step + KvAppend + GQA decode at 32K context,
     32 positions per layer; `layers` independent layer pairs rotate so that
@@ -843,6 +936,9 @@ def main(argv=None) -> int:
     ap.add_argument("--cpu-seconds", type=float, default=8.0,
                     help="CPU-baseline time budget of the headline (others get half)")
     ap.add_argument("--no-cpu", action="store_true", help="skip every CPU baseline")
+    ap.add_argument("--only", default="",
+                    help="comma-separated keys of the other configurations to run "
+                         "(default: all)")
     args = ap.parse_args(argv)
 
     if args.gpus != 1:
@@ -905,8 +1001,13 @@ def main(argv=None) -> int:
             ("next_attn_rows_decode_4k", lambda: AttnRows(dev, 1, 4096, 64, seed=7)),
             ("next_delta_front_1024", lambda: DeltaFront(dev, 1024, 8, seed=8)),
             ("next_delta_front_decode", lambda: DeltaFront(dev, 1, 64, seed=9)),
+            ("next_l2norm_delta_1024", lambda: DeltaNormUpdate(dev, 1024, 8, seed=10)),
+            ("next_l2norm_delta_decode", lambda: DeltaNormUpdate(dev, 1, 128, seed=11)),
         ]
+        only = {k for k in args.only.split(",") if k}
         for key, make in builders:
+            if only and key not in only:
+                continue
             x = make()
             log(f"{key}: {x.name}")
             n = steps if key != "cfg4_hybrid_decode_32k" else max(steps, 128)
@@ -929,7 +1030,7 @@ def main(argv=None) -> int:
                 kern_s = entry["roofline"]["kernel_us_avg"] * 1e-6
                 entry["mfma_frac_recurrent_flops"] = round(
                     delta_flops(x.T, x.hv, x.dk, x.dv) / kern_s / 1e12 / MFMA_F16_PEAK_TFS, 5)
-            if isinstance(x, (AttnRows, DeltaFront)):
+            if isinstance(x, (AttnRows, DeltaFront, DeltaNormUpdate)):
                 entry["op_roofline"] = {
                     l: {"bytes": x.bytes[l],
                         "achieved_GBs": round(x.bytes[l] / (op_ms[l] * 1e-3) / 1e9, 1),

@@ -285,6 +285,25 @@ LLMI_HIP_API int llmi_hip_delta_update(const float *q, const float *k, const uin
 
 LLMI_HIP_API size_t llmi_hip_delta_workspace_bytes(GraphDeltaParams p);
 
+/* The L2Norm -> DeltaUpdate pair of a DeltaNet layer in one call
+ * (Qwen35ModelBuilder.cpp:155-156 emits L2Norm(q, eps, 1/sqrt(dk)) and
+ * L2Norm(k, eps, 1) ahead of DeltaUpdate; l2NormF32, Graph.metal:96-109):
+ * q and k are the fp16 rows [T][Hk*dk] the convolution produced, and the
+ * update kernels normalise them as they load them. Each fp32 operand
+ * element is the bits l2NormF32 would write (factor = rsqrt(sum of squares
+ * in index order + epsilon) * scale, q_scale for q and 1 for k; element =
+ * x * factor), so state and output equal llmi_hip_l2_norm on q and k
+ * followed by llmi_hip_delta_update, without the fp32 q/k round trip. Other
+ * operands, the workspace (llmi_hip_delta_workspace_bytes of the same
+ * params) and the T == 1 / T > 1 kernel choice as llmi_hip_delta_update;
+ * dk must be 64 or 128 and dv a multiple of 16 (else UNSUPPORTED). */
+LLMI_HIP_API int llmi_hip_l2_norm_delta_update(const uint16_t *q, const uint16_t *k,
+                                               const uint16_t *v, const float *beta,
+                                               const float *decay, float *state,
+                                               uint16_t *out, GraphDeltaParams p,
+                                               float epsilon, float q_scale, void *workspace,
+                                               size_t workspace_bytes, void *stream);
+
 /* ----------------------------------------------------------------- helpers */
 
 /* Zero a workspace (enqueued on `stream`). No kernel of this library needs

@@ -410,6 +410,40 @@ int llmi_hip_delta_update(const float *q, const float *k, const uint16_t *v,
   return fail(LLMI_HIP_UNSUPPORTED, "DeltaUpdate: unsupported shape");
 }
 
+int llmi_hip_l2_norm_delta_update(const uint16_t *q, const uint16_t *k, const uint16_t *v,
+                                  const float *beta, const float *decay, float *state,
+                                  uint16_t *out, GraphDeltaParams p, float epsilon,
+                                  float q_scale, void *workspace, size_t workspace_bytes,
+                                  void *stream) {
+  if (int st = check_delta(p))
+    return st;
+  if (!q || !k || !v || !beta || !decay || !state || !out)
+    return fail(LLMI_HIP_INVALID_ARGUMENT, "L2Norm+DeltaUpdate: null buffer");
+  DeltaShape s{p.tokens, p.keyHeads, p.keyDim, p.valueHeads, p.valueDim};
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  switch (select_delta(p)) {
+  case DeltaKernel::Chunked: {
+    size_t need = delta_chunked_workspace_bytes(s);
+    if (need && (!workspace || workspace_bytes < need))
+      return fail(LLMI_HIP_WORKSPACE,
+                  "L2Norm+DeltaUpdate: chunked form needs a %zu-byte workspace", need);
+    return launched(launch_delta_chunked_qk16(q, k, v, beta, decay, state, out, workspace,
+                                              epsilon, q_scale, s, st),
+                    "deltaChunkedWy");
+  }
+  case DeltaKernel::Recurrent:
+    return launched(launch_delta_recurrent_qk16(q, k, v, beta, decay, state, out, epsilon,
+                                                q_scale, s, st),
+                    "deltaRecurrent");
+  case DeltaKernel::Generic:
+    break;
+  }
+  return fail(LLMI_HIP_UNSUPPORTED,
+              "L2Norm+DeltaUpdate: dk %u, dv %u have no fused kernel (dk 64 or 128, dv a "
+              "multiple of 16)",
+              p.keyDim, p.valueDim);
+}
+
 int llmi_hip_workspace_init(void *workspace, size_t bytes, void *stream) {
   if (!bytes)
     return LLMI_HIP_OK;

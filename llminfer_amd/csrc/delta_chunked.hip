@@ -60,6 +60,7 @@
 // (e^-1e4 = 0), and in fp32 a difference of two sums near -1e4 would keep
 // only ~1e-3 absolute precision. Only non-positive differences are
 // exponentiated.
+#include "exact_fp.hpp"
 #include "hip_common.hpp"
 #include "kernels.hpp"
 
@@ -186,10 +187,17 @@ __device__ __forceinline__ void load_split4(const float *p, int stride, half4_t 
   split4(float4_t{p[0], p[stride], p[2 * stride], p[3 * stride]}, hi, lo);
 }
 
+// QK16: q and k arrive as fp16 rows and are L2-normalised here exactly as
+// l2NormF32 (Graph.metal:96-109) would: one lane per (token, q or k) row of
+// the chunk runs the reference's sequential sum of squares, and each fp32
+// element is the single product x * factor -- the bits l2NormF32 writes.
+template <bool QK16>
 __global__ __launch_bounds__(256, 1) void delta_prep_kernel(
-    const float *__restrict__ q, const float *__restrict__ k, const half_t *__restrict__ v,
+    const void *__restrict__ qp, const void *__restrict__ kp, const half_t *__restrict__ v,
     const float *__restrict__ beta, const float *__restrict__ decay, void *__restrict__ ws,
-    unsigned T, unsigned Hk, unsigned Hv, unsigned DV) {
+    unsigned T, unsigned Hk, unsigned Hv, unsigned DV, float eps, float qscale) {
+  const float *q = static_cast<const float *>(qp), *k = static_cast<const float *>(kp);
+  const half_t *q16 = static_cast<const half_t *>(qp), *k16 = static_cast<const half_t *>(kp);
   const unsigned c = blockIdx.x, kh = blockIdx.y;
   const unsigned R = Hv / Hk, chunks = (T + C - 1) / C;
   const unsigned t0 = c * C, n = min((unsigned)C, T - t0);
@@ -207,20 +215,27 @@ __global__ __launch_bounds__(256, 1) void delta_prep_kernel(
   __shared__ __attribute__((aligned(16))) half_t sNh[C * CS], sNl[C * CS];
   __shared__ double sG[C];
   __shared__ float sB[C], sEg[C], sEz[C];
+  __shared__ float sFac[QK16 ? 2 * C : 1]; // QK16: L2 factors of the k rows, then the q rows
 
   // Loads that later phases need, issued up front so that their latency
   // hides behind the K/Q split and the Gram products: the fp32 queries of
   // the Q' initial values (wave w: d tiles 2w, 2w + 1, all t), the gates
   // of the first value head (wave 0) and its first block of V.
   float4_t qinit[2][4];
+  half4_t qraw[2][4]; // QK16: the fp16 queries, normalised once the factors are known
 #pragma unroll
   for (int hf = 0; hf < 2; ++hf)
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt) {
       const unsigned t = 16 * mt + L, tc = min(t, n - 1); // rows past the end read row n-1
-      const float4_t x = *reinterpret_cast<const float4_t *>(
-          q + (size_t)(t0 + tc) * qkStride + (size_t)kh * DK + 16 * (2 * wave + hf) + 4 * g);
-      qinit[hf][mt] = t < n ? x : float4_t{0.0f, 0.0f, 0.0f, 0.0f};
+      const size_t off =
+          (size_t)(t0 + tc) * qkStride + (size_t)kh * DK + 16 * (2 * wave + hf) + 4 * g;
+      if constexpr (QK16) {
+        qraw[hf][mt] = *reinterpret_cast<const half4_t *>(q16 + off);
+      } else {
+        const float4_t x = *reinterpret_cast<const float4_t *>(q + off);
+        qinit[hf][mt] = t < n ? x : float4_t{0.0f, 0.0f, 0.0f, 0.0f};
+      }
     }
   float gateA = 1.0f, gateB = 0.0f;
   auto load_gates = [&](unsigned h) {
@@ -255,6 +270,38 @@ __global__ __launch_bounds__(256, 1) void delta_prep_kernel(
   const unsigned w0 = min((unsigned)VB, DV);
   fetch_v(kh * R, 0, w0);
 
+  // QK16: the L2 factors of the chunk's k rows (threads 0-63) and q rows
+  // (64-127), each the sequential sum over one row.
+  if constexpr (QK16) {
+    if (tid < 2 * C) {
+      const unsigned t = tid % C, isq = tid / C;
+      const uint4_t *row = reinterpret_cast<const uint4_t *>(
+          (isq ? q16 : k16) + (size_t)(t0 + min(t, n - 1)) * qkStride + (size_t)kh * DK);
+      uint4_t x[DK / 8];
+#pragma unroll
+      for (int c8 = 0; c8 < DK / 8; ++c8)
+        x[c8] = row[c8];
+      float sum = 0.0f;
+#pragma unroll
+      for (int c8 = 0; c8 < DK / 8; ++c8)
+        sum = sumsq8(x[c8], sum);
+      sFac[tid] = l2_row_factor(sum, eps, isq ? qscale : 1.0f);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt) {
+        const unsigned t = 16 * mt + L;
+        const float f = sFac[C + min(t, n - 1)];
+        float4_t x;
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          x[e] = __fmul_rn((float)qraw[hf][mt][e], f);
+        qinit[hf][mt] = t < n ? x : float4_t{0.0f, 0.0f, 0.0f, 0.0f};
+      }
+  }
+
   // Keys and queries of the chunk as fp16 hi/lo (rows past the end are
   // zero); every load is issued before the first store.
   {
@@ -263,9 +310,21 @@ __global__ __launch_bounds__(256, 1) void delta_prep_kernel(
 #pragma unroll
     for (int it = 0; it < NI; ++it) {
       const unsigned i = tid + 256 * it, t = i / (DK / 4), d4 = (i % (DK / 4)) * 4;
-      const size_t off = (size_t)(t0 + min(t, n - 1)) * qkStride + (size_t)kh * DK + d4;
-      kv[it] = *reinterpret_cast<const float4_t *>(k + off);
-      qv[it] = *reinterpret_cast<const float4_t *>(q + off);
+      const unsigned tc = min(t, n - 1);
+      const size_t off = (size_t)(t0 + tc) * qkStride + (size_t)kh * DK + d4;
+      if constexpr (QK16) {
+        const half4_t kr = *reinterpret_cast<const half4_t *>(k16 + off);
+        const half4_t qr = *reinterpret_cast<const half4_t *>(q16 + off);
+        const float fk = sFac[tc], fq = sFac[C + tc];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          kv[it][e] = __fmul_rn((float)kr[e], fk);
+          qv[it][e] = __fmul_rn((float)qr[e], fq);
+        }
+      } else {
+        kv[it] = *reinterpret_cast<const float4_t *>(k + off);
+        qv[it] = *reinterpret_cast<const float4_t *>(q + off);
+      }
     }
 #pragma unroll
     for (int it = 0; it < NI; ++it) {
@@ -988,20 +1047,38 @@ size_t delta_chunked_workspace_bytes(const DeltaShape &s) {
   return chunks * (s.Hv * rec_bytes(s.Dv) + s.Hk * (size_t)kPieceBytes);
 }
 
-hipError_t launch_delta_chunked(const float *q, const float *k, const uint16_t *v,
-                                const float *beta, const float *decay, float *state,
-                                uint16_t *out, void *ws, const DeltaShape &s,
-                                hipStream_t stream) {
+namespace {
+
+template <bool QK16>
+hipError_t launch_chunked(const void *q, const void *k, const uint16_t *v, const float *beta,
+                          const float *decay, float *state, uint16_t *out, void *ws,
+                          float eps, float qscale, const DeltaShape &s, hipStream_t stream) {
   const unsigned chunks = (s.T + C - 1) / C;
-  hipLaunchKernelGGL(delta_prep_kernel, dim3(chunks, s.Hk), dim3(256), 0, stream, q, k,
+  hipLaunchKernelGGL((delta_prep_kernel<QK16>), dim3(chunks, s.Hk), dim3(256), 0, stream, q, k,
                      reinterpret_cast<const half_t *>(v), beta, decay, ws, s.T, s.Hk, s.Hv,
-                     s.Dv);
+                     s.Dv, eps, qscale);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess)
     return e;
   hipLaunchKernelGGL(delta_scan_kernel, dim3(s.Hv * (s.Dv / 16)), dim3(256), 0, stream, state,
                      reinterpret_cast<half_t *>(out), ws, s.T, s.Hk, s.Hv, s.Dv);
   return hipGetLastError();
+}
+
+} // namespace
+
+hipError_t launch_delta_chunked(const float *q, const float *k, const uint16_t *v,
+                                const float *beta, const float *decay, float *state,
+                                uint16_t *out, void *ws, const DeltaShape &s,
+                                hipStream_t stream) {
+  return launch_chunked<false>(q, k, v, beta, decay, state, out, ws, 0.0f, 1.0f, s, stream);
+}
+
+hipError_t launch_delta_chunked_qk16(const uint16_t *q, const uint16_t *k, const uint16_t *v,
+                                     const float *beta, const float *decay, float *state,
+                                     uint16_t *out, void *ws, float eps, float qscale,
+                                     const DeltaShape &s, hipStream_t stream) {
+  return launch_chunked<true>(q, k, v, beta, decay, state, out, ws, eps, qscale, s, stream);
 }
 
 unsigned delta_chunked_dispatches() { return 2; }

@@ -158,7 +158,7 @@ __global__ __launch_bounds__(256) void causal_conv_k4(
 }
 
 __device__ __forceinline__ float l2_factor(float sum, float eps, float scale) {
-  return mul32(__fdiv_rn(1.0f, sqrt_cr(__fadd_rn(sum, eps))), scale);
+  return l2_row_factor(sum, eps, scale);
 }
 
 // Rows of `width` (a multiple of 8, <= 256) halves, kL2Rows per wave.

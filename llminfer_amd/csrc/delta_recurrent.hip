@@ -22,21 +22,30 @@
 // Summation order inside a dot product differs from the reference's single
 // fma chain (four interleaved chains per lane plus the partials in LDS); the
 // result stays within fp32 rounding of the sequential order.
+//
+// With QK16 the kernel also performs the L2 normalisations of q and k that
+// precede DeltaUpdate (l2NormF32, Graph.metal:96-109): q and k arrive as the
+// fp16 rows the convolution produced, one lane per (token, q or k) row runs
+// the reference's sequential sum of squares and forms the row factor, and
+// every fp32 element is the single product x * factor -- the bits l2NormF32
+// writes, so the update sees exactly the operands of the unfused pair.
+#include "exact_fp.hpp"
 #include "hip_common.hpp"
 #include "kernels.hpp"
 
 #include <stdlib.h>
+#include <type_traits>
 
 namespace llmi {
 namespace {
 
-template <int DK, int CW, int NW>
+template <int DK, int CW, int NW, bool QK16>
 __global__ __launch_bounds__(64 * NW) void delta_recurrent_kernel(
-    const float *__restrict__ q, const float *__restrict__ k,
+    const void *__restrict__ qp, const void *__restrict__ kp,
     const half_t *__restrict__ v, const float *__restrict__ beta,
     const float *__restrict__ decay, float *__restrict__ state,
     half_t *__restrict__ out, unsigned T, unsigned Hk, unsigned Hv,
-    unsigned DV) {
+    unsigned DV, float eps, float qscale) {
   constexpr int RG = 64 / CW;  // row groups per wave
   constexpr int NP = NW * RG;  // partial sums per column
   constexpr int RPL = DK / NP; // rows per lane
@@ -50,57 +59,122 @@ __global__ __launch_bounds__(64 * NW) void delta_recurrent_kernel(
   const unsigned row0 = part * RPL;
   const size_t vwidth = (size_t)Hv * DV;
 
+  __shared__ float sPred[NP][CW], sY[NP][CW];
+  // QK16: the L2 factors of kFacTok tokens' k and q rows at a time; thread
+  // 2i (2i + 1) sums the k (q) row of the block's token i. The rows of the
+  // first block are requested before the state, so that their sums run
+  // while the state is in flight.
+  constexpr unsigned kFacTok = 32 * NW;
+  __shared__ float sFac[QK16 ? 2 * kFacTok : 1];
+  uint4_t facRow[QK16 ? DK / 8 : 1];
+  auto fetch_fac_row = [&](unsigned tb) {
+    const unsigned tt = tb + tid / 2;
+    const uint4_t *row = reinterpret_cast<const uint4_t *>(
+        static_cast<const half_t *>((tid & 1u) ? qp : kp) + ((size_t)tt * Hk + kh) * DK);
+#pragma unroll
+    for (int c8 = 0; c8 < (QK16 ? DK / 8 : 0); ++c8)
+      facRow[c8] = row[c8];
+  };
+  if (QK16 && tid < 2 * min(kFacTok, T))
+    fetch_fac_row(0);
+
   float S[RPL];
   float *sbase = state + ((size_t)h * DK + row0) * DV + col;
 #pragma unroll
   for (int m = 0; m < RPL; ++m)
     S[m] = sbase[(size_t)m * DV];
 
-  __shared__ float sPred[NP][CW], sY[NP][CW];
-  for (unsigned t = 0; t < T; ++t) {
-    const float *kt = k + ((size_t)t * Hk + kh) * DK + row0;
-    const float *qt = q + ((size_t)t * Hk + kh) * DK + row0;
-    float kr[RPL], qr[RPL];
+  // A token's operands as loaded (fp16 q/k rows with QK16, else fp32). They
+  // are fetched one token ahead, before the barriers of the token in hand,
+  // so that no token waits for its own loads.
+  using QkRaw = typename std::conditional<QK16, half4_t, float4_t>::type;
+  struct Operands {
+    QkRaw k[RPL / 4], q[RPL / 4];
+    float a, b, vj;
+  };
+  auto fetch = [&](unsigned t, Operands &o) {
+    const size_t qk = ((size_t)t * Hk + kh) * DK + row0;
+    const QkRaw *kt = reinterpret_cast<const QkRaw *>(static_cast<const char *>(kp)) +
+                      qk / 4;
+    const QkRaw *qt = reinterpret_cast<const QkRaw *>(static_cast<const char *>(qp)) +
+                      qk / 4;
 #pragma unroll
-    for (int m = 0; m < RPL; m += 4) {
-      float4_t kv4 = *reinterpret_cast<const float4_t *>(kt + m);
-      float4_t qv4 = *reinterpret_cast<const float4_t *>(qt + m);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        kr[m + e] = kv4[e];
-        qr[m + e] = qv4[e];
+    for (int m4 = 0; m4 < RPL / 4; ++m4) {
+      o.k[m4] = kt[m4];
+      o.q[m4] = qt[m4];
+    }
+    o.a = decay[(size_t)t * Hv + h];
+    o.b = beta[(size_t)t * Hv + h];
+    o.vj = (float)v[(size_t)t * vwidth + (size_t)h * DV + col];
+  };
+  Operands cur;
+  fetch(0, cur);
+
+  for (unsigned tb = 0; tb < T; tb += QK16 ? kFacTok : T) {
+    const unsigned tn = QK16 ? min(kFacTok, T - tb) : T;
+    if constexpr (QK16) {
+      if (tb) {
+        __syncthreads(); // the previous block's factors are no longer read
+        if (tid < 2 * tn)
+          fetch_fac_row(tb);
       }
+      if (tid < 2 * tn) {
+        float sum = 0.0f;
+#pragma unroll
+        for (int c8 = 0; c8 < DK / 8; ++c8)
+          sum = sumsq8(facRow[c8], sum);
+        sFac[tid] = l2_row_factor(sum, eps, (tid & 1u) ? qscale : 1.0f);
+      }
+      __syncthreads();
     }
-    const float a = decay[(size_t)t * Hv + h];
-    const float b = beta[(size_t)t * Hv + h];
-    const float vj = (float)v[(size_t)t * vwidth + (size_t)h * DV + col];
+    for (unsigned t = tb; t < tb + tn; ++t) {
+      Operands nxt;
+      if (t + 1 < T)
+        fetch(t + 1, nxt);
+      float kr[RPL], qr[RPL];
+      const float fk = QK16 ? sFac[2 * (t - tb)] : 1.0f;
+      const float fq = QK16 ? sFac[2 * (t - tb) + 1] : 1.0f;
+#pragma unroll
+      for (int m = 0; m < RPL; ++m) {
+        if constexpr (QK16) {
+          kr[m] = __fmul_rn((float)cur.k[m / 4][m % 4], fk);
+          qr[m] = __fmul_rn((float)cur.q[m / 4][m % 4], fq);
+        } else {
+          kr[m] = cur.k[m / 4][m % 4];
+          qr[m] = cur.q[m / 4][m % 4];
+        }
+      }
+      const float a = cur.a, b = cur.b, vj = cur.vj;
 
-    float p4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+      float p4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-    for (int m = 0; m < RPL; ++m)
-      p4[m % 4] = fmaf(S[m] * a, kr[m], p4[m % 4]);
-    sPred[part][c] = (p4[0] + p4[1]) + (p4[2] + p4[3]);
-    __syncthreads();
-    float pred = 0.0f;
-#pragma unroll
-    for (int i = 0; i < NP; ++i)
-      pred += sPred[i][c];
-    const float delta = (vj - pred) * b;
-
-    float y4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-    for (int m = 0; m < RPL; ++m) {
-      S[m] = fmaf(kr[m], delta, S[m] * a);
-      y4[m % 4] = fmaf(S[m], qr[m], y4[m % 4]);
-    }
-    sY[part][c] = (y4[0] + y4[1]) + (y4[2] + y4[3]);
-    __syncthreads();
-    if (part == 0) {
-      float y = 0.0f;
+      for (int m = 0; m < RPL; ++m)
+        p4[m % 4] = fmaf(S[m] * a, kr[m], p4[m % 4]);
+      sPred[part][c] = (p4[0] + p4[1]) + (p4[2] + p4[3]);
+      __syncthreads();
+      float pred = 0.0f;
 #pragma unroll
       for (int i = 0; i < NP; ++i)
-        y += sY[i][c];
-      out[(size_t)t * vwidth + (size_t)h * DV + col] = (half_t)y;
+        pred += sPred[i][c];
+      const float delta = (vj - pred) * b;
+
+      float y4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int m = 0; m < RPL; ++m) {
+        S[m] = fmaf(kr[m], delta, S[m] * a);
+        y4[m % 4] = fmaf(S[m], qr[m], y4[m % 4]);
+      }
+      sY[part][c] = (y4[0] + y4[1]) + (y4[2] + y4[3]);
+      __syncthreads();
+      if (part == 0) {
+        float y = 0.0f;
+#pragma unroll
+        for (int i = 0; i < NP; ++i)
+          y += sY[i][c];
+        out[(size_t)t * vwidth + (size_t)h * DV + col] = (half_t)y;
+      }
+      if (t + 1 < T)
+        cur = nxt;
     }
   }
 
@@ -182,31 +256,53 @@ unsigned waves_per_group() {
   return v;
 }
 
-template <int DK, int CW, int NW>
-hipError_t launch_rec(const float *q, const float *k, const uint16_t *v, const float *beta,
-                      const float *decay, float *state, uint16_t *out, const DeltaShape &s,
-                      hipStream_t stream) {
-  hipLaunchKernelGGL((delta_recurrent_kernel<DK, CW, NW>), dim3(s.Hv * (s.Dv / CW)),
-                     dim3(64 * NW), 0, stream, q, k, reinterpret_cast<const half_t *>(v),
-                     beta, decay, state, reinterpret_cast<half_t *>(out), s.T, s.Hk, s.Hv,
-                     s.Dv);
+struct RecArgs {
+  const void *q, *k;
+  const uint16_t *v;
+  const float *beta, *decay;
+  float *state;
+  uint16_t *out;
+  float eps, qscale;
+};
+
+template <int DK, int CW, int NW, bool QK16>
+hipError_t launch_rec(const RecArgs &a, const DeltaShape &s, hipStream_t stream) {
+  hipLaunchKernelGGL((delta_recurrent_kernel<DK, CW, NW, QK16>), dim3(s.Hv * (s.Dv / CW)),
+                     dim3(64 * NW), 0, stream, a.q, a.k, reinterpret_cast<const half_t *>(a.v),
+                     a.beta, a.decay, a.state, reinterpret_cast<half_t *>(a.out), s.T, s.Hk,
+                     s.Hv, s.Dv, a.eps, a.qscale);
   return hipGetLastError();
 }
 
-template <int DK, int CW>
-hipError_t launch_rec_cw(const float *q, const float *k, const uint16_t *v, const float *beta,
-                         const float *decay, float *state, uint16_t *out, const DeltaShape &s,
-                         hipStream_t stream) {
+template <int DK, int CW, bool QK16>
+hipError_t launch_rec_cw(const RecArgs &a, const DeltaShape &s, hipStream_t stream) {
   // Rows per lane DK / (NW * 64 / CW) must stay a multiple of 4.
   constexpr bool ok8 = DK % (8 * (64 / CW) * 4) == 0, ok2 = DK % (2 * (64 / CW) * 4) == 0;
   const unsigned nw = waves_per_group();
   if constexpr (ok8)
     if (nw == 8)
-      return launch_rec<DK, CW, 8>(q, k, v, beta, decay, state, out, s, stream);
+      return launch_rec<DK, CW, 8, QK16>(a, s, stream);
   if constexpr (ok2)
     if (nw == 2)
-      return launch_rec<DK, CW, 2>(q, k, v, beta, decay, state, out, s, stream);
-  return launch_rec<DK, CW, 4>(q, k, v, beta, decay, state, out, s, stream);
+      return launch_rec<DK, CW, 2, QK16>(a, s, stream);
+  return launch_rec<DK, CW, 4, QK16>(a, s, stream);
+}
+
+template <bool QK16>
+hipError_t launch_rec_any(const RecArgs &a, const DeltaShape &s, hipStream_t stream) {
+  const unsigned cw = slice_cols(s.Dv);
+  if (s.Dk == 64) {
+    if (cw == 64)
+      return launch_rec_cw<64, 64, QK16>(a, s, stream);
+    if (cw == 32)
+      return launch_rec_cw<64, 32, QK16>(a, s, stream);
+    return launch_rec_cw<64, 16, QK16>(a, s, stream);
+  }
+  if (cw == 64)
+    return launch_rec_cw<128, 64, QK16>(a, s, stream);
+  if (cw == 32)
+    return launch_rec_cw<128, 32, QK16>(a, s, stream);
+  return launch_rec_cw<128, 16, QK16>(a, s, stream);
 }
 
 } // namespace
@@ -221,19 +317,15 @@ hipError_t launch_delta_recurrent(const float *q, const float *k,
                                   const float *decay, float *state,
                                   uint16_t *out, const DeltaShape &s,
                                   hipStream_t stream) {
-  const unsigned cw = slice_cols(s.Dv);
-  if (s.Dk == 64) {
-    if (cw == 64)
-      return launch_rec_cw<64, 64>(q, k, v, beta, decay, state, out, s, stream);
-    if (cw == 32)
-      return launch_rec_cw<64, 32>(q, k, v, beta, decay, state, out, s, stream);
-    return launch_rec_cw<64, 16>(q, k, v, beta, decay, state, out, s, stream);
-  }
-  if (cw == 64)
-    return launch_rec_cw<128, 64>(q, k, v, beta, decay, state, out, s, stream);
-  if (cw == 32)
-    return launch_rec_cw<128, 32>(q, k, v, beta, decay, state, out, s, stream);
-  return launch_rec_cw<128, 16>(q, k, v, beta, decay, state, out, s, stream);
+  return launch_rec_any<false>({q, k, v, beta, decay, state, out, 0.0f, 1.0f}, s, stream);
+}
+
+hipError_t launch_delta_recurrent_qk16(const uint16_t *q, const uint16_t *k,
+                                       const uint16_t *v, const float *beta,
+                                       const float *decay, float *state, uint16_t *out,
+                                       float eps, float qscale, const DeltaShape &s,
+                                       hipStream_t stream) {
+  return launch_rec_any<true>({q, k, v, beta, decay, state, out, eps, qscale}, s, stream);
 }
 
 } // namespace llmi

@@ -8,6 +8,8 @@
 // whatever the contraction setting.
 #pragma once
 
+#include "hip_common.hpp"
+
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -33,6 +35,26 @@ __device__ __forceinline__ float round16(float x) { return opaque((float)(_Float
 // which is exact rounding for a float argument (HIP's __fsqrt_rn is the
 // native instruction, not always rounded to nearest).
 __device__ __forceinline__ float sqrt_cr(float x) { return (float)__builtin_sqrt((double)x); }
+
+// l2NormF32's row factor rsqrt(sum + eps) * scale (Graph.metal:96-109), with
+// rsqrt as 1/sqrt, every step correctly rounded; each output element is then
+// the single fp32 product x * factor. Explicit _rn operations, so that the
+// result does not depend on the file's contraction setting.
+__device__ __forceinline__ float l2_row_factor(float sum, float eps, float scale) {
+  return __fmul_rn(__fdiv_rn(1.0f, sqrt_cr(__fadd_rn(sum, eps))), scale);
+}
+
+// The sum of squares of 8 fp16 values (as one 16-byte word) continued in
+// index order by fma, the reference's loop.
+__device__ __forceinline__ float sumsq8(uint4_t x, float sum) {
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const float lo = h2f((uint16_t)(x[e] & 0xFFFFu)), hi = h2f((uint16_t)(x[e] >> 16));
+    sum = __builtin_fmaf(lo, lo, sum);
+    sum = __builtin_fmaf(hi, hi, sum);
+  }
+  return sum;
+}
 
 // True when every float within 2^-kLog2Margin (relative) of v has the same
 // fp16 rounding as v (fp16 rounding is monotonic, so the two ends decide).

@@ -53,6 +53,18 @@ struct DeltaShape {
 };
 
 bool delta_recurrent_supported(const DeltaShape &s);
+// The same with fp16 q and k rows that the kernels L2-normalise themselves,
+// bit for bit as l2NormF32 (factor rsqrt(sum + eps) * scale; qscale for q,
+// 1 for k) before the update.
+hipError_t launch_delta_recurrent_qk16(const uint16_t *q, const uint16_t *k,
+                                       const uint16_t *v, const float *beta,
+                                       const float *decay, float *state, uint16_t *out,
+                                       float eps, float qscale, const DeltaShape &s,
+                                       hipStream_t stream);
+hipError_t launch_delta_chunked_qk16(const uint16_t *q, const uint16_t *k, const uint16_t *v,
+                                     const float *beta, const float *decay, float *state,
+                                     uint16_t *out, void *ws, float eps, float qscale,
+                                     const DeltaShape &s, hipStream_t stream);
 hipError_t launch_delta_recurrent(const float *q, const float *k,
                                   const uint16_t *v, const float *beta,
                                   const float *decay, float *state,

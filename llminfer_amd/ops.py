@@ -13,6 +13,7 @@ from __future__ import annotations
 
 import ctypes as C
 
+import numpy as np
 import torch
 
 from . import _lib
@@ -324,6 +325,50 @@ def delta_update(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, beta: torch.
     _lib.check(lib.llmi_hip_delta_update(_ptr(q), _ptr(k), _ptr(v), _ptr(beta), _ptr(decay),
                                          _ptr(state), _ptr(out), p, _ptr(ws),
                                          ws.numel() if ws is not None else 0, _stream()))
+    return out
+
+
+def bind_l2_norm_delta_update(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                              beta: torch.Tensor, decay: torch.Tensor, state: torch.Tensor,
+                              out: torch.Tensor, epsilon: float = 1e-6,
+                              q_scale: float | None = None) -> "Bound":
+    """L2Norm(q, epsilon, q_scale), L2Norm(k, epsilon, 1) and DeltaUpdate in one
+    call: q, k [T, Hk*dk] fp16 rows (l2NormF32, Graph.metal:96-109, before
+    graphDeltaUpdate). q_scale defaults to 1/sqrt(dk) as the builder emits it
+    (Qwen35ModelBuilder.cpp:155-156)."""
+    for t, n, dt in ((q, "q", torch.float16), (k, "k", torch.float16),
+                     (v, "v", torch.float16), (beta, "beta", torch.float32),
+                     (decay, "decay", torch.float32), (state, "state", torch.float32),
+                     (out, "out", torch.float16)):
+        _require(t, dt, n)
+    T = q.shape[0]
+    hv, dk, dv = state.shape
+    if q.dim() != 2 or k.shape != q.shape or q.shape[1] % dk or \
+            hv % (q.shape[1] // dk) or v.shape != (T, hv * dv) or \
+            beta.shape != (T, hv) or decay.shape != beta.shape or out.shape != v.shape:
+        raise ValueError("DeltaUpdate operand shapes do not match its recurrent state")
+    if q_scale is None:  # 1.0f / std::sqrt(float(keyDim)), both in fp32
+        q_scale = float(np.float32(1.0) / np.sqrt(np.float32(dk)))
+    lib = _lib.load()
+    p = delta_params(q, v, state)
+    need = lib.llmi_hip_delta_workspace_bytes(p)
+    ws = workspace(need, q.device, "delta") if need else None
+    args = (_ptr(q), _ptr(k), _ptr(v), _ptr(beta), _ptr(decay), _ptr(state), _ptr(out),
+            p, epsilon, q_scale, _ptr(ws), ws.numel() if ws is not None else 0, _stream())
+    names = kernel_names(_lib.OP_DELTA_UPDATE, p)
+    b = Bound(lib.llmi_hip_l2_norm_delta_update, args, "+".join(names))
+    b._keep = ws
+    return b
+
+
+def l2_norm_delta_update(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, beta: torch.Tensor,
+                         decay: torch.Tensor, state: torch.Tensor,
+                         out: torch.Tensor | None = None, epsilon: float = 1e-6,
+                         q_scale: float | None = None) -> torch.Tensor:
+    """The fused L2Norm -> DeltaUpdate pair (bind_l2_norm_delta_update)."""
+    if out is None:
+        out = torch.empty_like(v)
+    bind_l2_norm_delta_update(q, k, v, beta, decay, state, out, epsilon, q_scale)()
     return out
 
 

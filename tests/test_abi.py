@@ -249,3 +249,19 @@ def test_noalloc_rejects_partials_beyond_its_scratch():
     r = subprocess.run([sys.executable, "-c", code], cwd=str(ROOT), env=env,
                        capture_output=True, text=True, timeout=120)
     assert r.returncode == 0, r.stderr
+
+
+def test_l2_norm_delta_update_rejects_shapes_without_kernel():
+    """The fused L2Norm+DeltaUpdate has kernels for dk 64/128 only: dk = 7
+    is UNSUPPORTED before any launch; a contract violation stays
+    INVALID_ARGUMENT."""
+    lib = _lib.load()
+    p = _lib.GraphDeltaParams(4, 1, 7, 2, 5)
+    assert lib.llmi_hip_l2_norm_delta_update(1, 1, 1, 1, 1, 1, 1, p, 1e-6, 1.0, None, 0,
+                                             None) == _lib.UNSUPPORTED
+    bad = _lib.GraphDeltaParams(4, 16, 128, 24, 128)  # Hv % Hk != 0
+    assert lib.llmi_hip_l2_norm_delta_update(1, 1, 1, 1, 1, 1, 1, bad, 1e-6, 1.0, None, 0,
+                                             None) == _lib.INVALID_ARGUMENT
+    ok = _lib.GraphDeltaParams(1024, 16, 128, 32, 128)
+    assert lib.llmi_hip_l2_norm_delta_update(1, 1, 1, 1, 1, 1, 1, ok, 1e-6, 1.0, None, 0,
+                                             None) == _lib.WORKSPACE
