@@ -615,6 +615,87 @@ class DeltaPrefill(Workload):
                 "gpu_vs_cpu_max_abs": err, "gpu_vs_cpu_state_rel": serr}
 
 
+class GatedAttention(Workload):
+    """The attention block around CausalGqa fused into one call
+    (llmi_hip_gated_attention: q and k normRope, V append, attention, sigmoid
+    gate; Qwen35ModelBuilder.cpp:175-197), next to the same block as five
+    standalone calls (q normRope, k normRope into the cache, cacheAppend of
+    V, CausalGqa, sigmoidMul). Decode rotates cache sets past the MALL; the
+    roofline is the attention's (bytes at decode, FLOPs at prefill)."""
+    labels = ("fused", "unfused")
+    dominant = "fused"
+
+    def __init__(self, dev, T, past, cap, sets, seed, hq=16, hkv=4, d=256, rot=64):
+        import torch
+        from llminfer_amd import ops
+        self.T, self.P, self.sets, self.hq, self.hkv, self.d, self.rot = T, past, sets, hq, hkv, d, rot
+        self.tokens = T
+        self.bound = "hbm" if T == 1 else "mfma"
+        self.name = f"gated_attention_T{T}_past{past}"
+        g = torch.Generator(device=dev).manual_seed(seed)
+        self.qw = (0.2 * torch.randn(d, generator=g, device=dev)).float()
+        self.kw = (0.2 * torch.randn(d, generator=g, device=dev)).float()
+        self.x = []
+        for _ in range(sets):
+            x = dict(qp=_randn16(g, (T, hq, 2 * d), dev), kp=_randn16(g, (T, hkv, d), dev),
+                     vn=_randn16(g, (T, hkv, d), dev), kc=_randn16(g, (cap, hkv, d), dev),
+                     vc=_randn16(g, (cap, hkv, d), dev),
+                     out=torch.empty(T, hq, d, dtype=torch.float16, device=dev),
+                     qn=torch.empty(T, hq, d, dtype=torch.float16, device=dev),
+                     attn=torch.empty(T, hq, d, dtype=torch.float16, device=dev),
+                     out2=torch.empty(T, hq, d, dtype=torch.float16, device=dev))
+            x["gate"] = x["qp"][:, :, d:].contiguous()
+            x["fused"] = ops.bind_gated_attention(x["qp"], x["kp"], x["vn"], self.qw, self.kw,
+                                                  x["kc"], x["vc"], x["out"], past, rot)
+            x["unfused"] = [
+                ops.bind_norm_rope(x["qp"], self.qw, x["qn"], past, rot, head_dim=d),
+                ops.bind_norm_rope(x["kp"], self.kw, x["kc"], past, rot, output_start=past),
+                ops.Bound(*_append_call(x["vn"], x["vc"], past * hkv * d), "cacheAppend"),
+                ops.bind_causal_gqa(x["qn"], x["kc"], x["vc"], x["attn"], past),
+                ops.bind_sigmoid_mul(x["gate"], x["attn"], x["out2"])]
+            self.x.append(x)
+
+    def op(self, label, i):
+        x = self.x[i % self.sets]
+        if label == "fused":
+            x["fused"]()
+        else:
+            for b in x["unfused"]:
+                b()
+
+    def kernels(self):
+        return self.x[0]["fused"].what
+
+    def work(self, i):
+        if self.bound == "hbm":
+            return gqa_bytes(1, self.P, self.hq, self.hkv, self.d)
+        return gqa_flops(self.T, self.P, self.hq, self.d)
+
+    def config(self):
+        return {"workload": self.name, "tokens": self.T, "past": self.P,
+                "query_heads": self.hq, "kv_heads": self.hkv, "head_dim": self.d,
+                "rotary_dim": self.rot, "sets": self.sets}
+
+    def cpu(self, budget_s):
+        import torch
+        x = self.x[0]
+        for label in self.labels:
+            self.op(label, 0)
+        torch.cuda.synchronize()
+        return {"value": None, "unit": "µs/layer", "cores": 0, "kind": "port",
+                "sample": "none: the block's parts have their own CPU samples "
+                          "(attention legs, next_attn_rows_*)",
+                "gpu_fused_equals_unfused": bool(torch.equal(x["out"], x["out2"]))}
+
+
+def _append_call(src, cache, offset):
+    """cacheAppend as a Bound-ready (fn, args) pair."""
+    from llminfer_amd import _lib
+    return (_lib.load().llmi_hip_cache_append,
+            (src.data_ptr(), cache.data_ptr(), _lib.CacheParams(src.numel(), offset),
+             __import__("torch").cuda.current_stream().cuda_stream))
+
+
 def norm_delta_bytes(T: int, hk: int, dk: int, hv: int, dv: int) -> int:
     """The fused L2Norm -> DeltaUpdate pair: fp16 q, k instead of fp32."""
     return delta_bytes(T, hk, dk, hv, dv) - 4 * T * hk * dk
@@ -1001,6 +1082,10 @@ def main(argv=None) -> int:
             ("next_attn_rows_decode_4k", lambda: AttnRows(dev, 1, 4096, 64, seed=7)),
             ("next_delta_front_1024", lambda: DeltaFront(dev, 1024, 8, seed=8)),
             ("next_delta_front_decode", lambda: DeltaFront(dev, 1, 64, seed=9)),
+            ("next_gated_attention_prefill", lambda: GatedAttention(dev, 2048, 2048, 4096, 2,
+                                                                     seed=12)),
+            ("next_gated_attention_decode_4k", lambda: GatedAttention(dev, 1, 4096, 8192, 24,
+                                                                      seed=13)),
             ("next_l2norm_delta_1024", lambda: DeltaNormUpdate(dev, 1024, 8, seed=10)),
             ("next_l2norm_delta_decode", lambda: DeltaNormUpdate(dev, 1, 128, seed=11)),
         ]

@@ -113,7 +113,8 @@ enum llmi_hip_op {
   LLMI_HIP_OP_CAUSAL_CONV = 8,          /* params: ConvParams */
   LLMI_HIP_OP_L2_NORM = 9,              /* params: L2Params */
   LLMI_HIP_OP_DELTA_GATES = 10,         /* params: RowParams (rows = tokens, width = heads) */
-  LLMI_HIP_OP_GATED_RMS_NORM = 11       /* params: RowParams */
+  LLMI_HIP_OP_GATED_RMS_NORM = 11,      /* params: RowParams */
+  LLMI_HIP_OP_GATED_ATTENTION = 12      /* params: GqaParams */
 };
 
 /* ---------------------------------------------------------------- KvAppend
@@ -264,6 +265,35 @@ LLMI_HIP_API int llmi_hip_kv_append_causal_gqa_noalloc(const uint16_t *q,
                                                        uint16_t *k_cache, uint16_t *v_cache,
                                                        uint16_t *out, GqaParams p,
                                                        void *stream);
+
+/* The attention block of a Qwen3.5 GQA layer around CausalGqa in one call
+ * (Qwen35ModelBuilder.cpp:175-197; the reference graph's dispatches,
+ * MetalReferenceGraph.mm:307-337): q_proj [T][Hq][2d] holds per head the d
+ * query values followed by the d gate values (headStride 2d), k_proj and
+ * v_new [T][Hkv][d] the step's new keys (before their norm) and values. In
+ * order, as the reference does them:
+ *   q   = normRope(q_proj rows, q_weight)        (Reference.metal:271-293)
+ *   k_cache rows [P, P+T) = normRope(k_proj, k_weight) at positions P + t
+ *   v_cache rows [P, P+T) = v_new                (cacheAppend)
+ *   a   = CausalGqa(q, caches)                   (as llmi_hip_causal_gqa)
+ *   out = fp16(fp16(logistic(gate)) * a)         (sigmoidMul; the gate of
+ *                                                 applyGqa, Reference.metal:350-353)
+ * with rotary_dim, epsilon and theta the normRope parameters of both norms.
+ * out, k_cache and v_cache are bit-identical to llmi_hip_norm_rope (q and
+ * k), llmi_hip_cache_append, llmi_hip_causal_gqa and llmi_hip_sigmoid_mul
+ * run in that order. T == 1 is one decode launch (plus its merge) that does
+ * all of it; T > 1 normRopes K into the cache and appends V (two launches),
+ * then runs the MFMA prefill with the q normRope in its query load and the
+ * gate in its output store. Workspace: llmi_hip_gqa_workspace_bytes(p).
+ * Supported: d 128 or 256, Hq/Hkv 2 or 4 (decode) or <= 4 (prefill),
+ * rotary_dim a multiple of 16 up to d; other shapes return UNSUPPORTED. */
+LLMI_HIP_API int llmi_hip_gated_attention(const uint16_t *q_proj, const uint16_t *k_proj,
+                                          const uint16_t *v_new, const float *q_weight,
+                                          const float *k_weight, uint16_t *k_cache,
+                                          uint16_t *v_cache, uint16_t *out, GqaParams p,
+                                          unsigned rotary_dim, float epsilon, float theta,
+                                          void *workspace, size_t workspace_bytes,
+                                          void *stream);
 
 /* ------------------------------------------------------------- DeltaUpdate
  * Replaces graphDeltaUpdate (Graph.metal:146-170 with updateDeltaColumn,

@@ -30,6 +30,7 @@ OP_CAUSAL_CONV = 8
 OP_L2_NORM = 9
 OP_DELTA_GATES = 10
 OP_GATED_RMS_NORM = 11
+OP_GATED_ATTENTION = 12
 
 NOALLOC_SCRATCH_BYTES = 8 << 20  # LLMI_HIP_NOALLOC_SCRATCH_BYTES
 
@@ -119,6 +120,8 @@ SIGNATURES = {
                                                 _P]),
     "llmi_hip_kv_append_causal_gqa_noalloc": (C.c_int, [_P, _P, _P, _P, _P, _P, GqaParams,
                                                         _P]),
+    "llmi_hip_gated_attention": (C.c_int, [_P, _P, _P, _P, _P, _P, _P, _P, GqaParams,
+                                           C.c_uint, C.c_float, C.c_float, _P, _SZ, _P]),
     "llmi_hip_delta_update": (C.c_int, [_P, _P, _P, _P, _P, _P, _P,
                                         GraphDeltaParams, _P, _SZ, _P]),
     "llmi_hip_delta_workspace_bytes": (_SZ, [GraphDeltaParams]),

@@ -3,6 +3,7 @@
 #include "llminfer_hip.h"
 #include "capi_internal.hpp"
 #include "kernels.hpp"
+#include "rope_gate.hpp"
 
 #include <hip/hip_runtime.h>
 #include <stdarg.h>
@@ -370,6 +371,63 @@ int llmi_hip_kv_append_causal_gqa(const uint16_t *q, const uint16_t *k_new,
                  workspace_bytes, stream);
 }
 
+int llmi_hip_gated_attention(const uint16_t *q_proj, const uint16_t *k_proj,
+                             const uint16_t *v_new, const float *q_weight,
+                             const float *k_weight, uint16_t *k_cache, uint16_t *v_cache,
+                             uint16_t *out, GqaParams p, unsigned rotary_dim, float epsilon,
+                             float theta, void *workspace, size_t workspace_bytes,
+                             void *stream) {
+  if (int st = check_gqa(p))
+    return st;
+  if (!q_proj || !k_proj || !v_new || !q_weight || !k_weight || !k_cache || !v_cache || !out)
+    return fail(LLMI_HIP_INVALID_ARGUMENT, "gated attention: null buffer");
+  if (rotary_dim % 2 || rotary_dim > p.headDim)
+    return fail(LLMI_HIP_INVALID_ARGUMENT,
+                "gated attention: rotary width %u must be even and <= head_dim %u",
+                rotary_dim, p.headDim);
+  if (!fits32((uint64_t)p.tokens * p.queryHeads, 2 * p.headDim, 1))
+    return fail(LLMI_HIP_INVALID_ARGUMENT, "gated attention: exceeds the 32-bit index range");
+  GqaShape s{p.tokens, p.queryHeads, p.kvHeads, p.headDim, p.past};
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  GatedRows ga;
+  ga.qproj = reinterpret_cast<const _Float16 *>(q_proj);
+  ga.kproj = reinterpret_cast<const _Float16 *>(k_proj);
+  ga.vnew = reinterpret_cast<const _Float16 *>(v_new);
+  ga.qw = q_weight;
+  ga.kw = k_weight;
+  ga.rot = rotary_dim;
+  ga.eps = epsilon;
+  const unsigned half = rotary_dim / 2;
+  if (half > 256)
+    return fail(LLMI_HIP_UNSUPPORTED, "gated attention: rotary width %u", rotary_dim);
+  memcpy(ga.freqs, host_freqs(theta, rotary_dim).v, sizeof(float) * half);
+  if (decode_gated_supported(s, rotary_dim)) {
+    size_t need = decode_workspace_bytes(s);
+    if (need && (!workspace || workspace_bytes < need))
+      return fail(LLMI_HIP_WORKSPACE,
+                  "gated attention: decode needs a %zu-byte workspace, got %zu", need,
+                  workspace ? workspace_bytes : (size_t)0);
+    return launched(launch_gqa_decode_gated(k_cache, v_cache, out, workspace, s, ga, st),
+                    "gqaDecodeGated");
+  }
+  if (p.tokens > 1 && prefill_gated_supported(s, rotary_dim)) {
+    const unsigned row = p.kvHeads * p.headDim;
+    RopeShape ks = rope_shape(p.tokens * p.kvHeads, p.kvHeads, p.headDim, rotary_dim,
+                              p.headDim, p.past, p.past * p.kvHeads, epsilon, theta, true);
+    int r = launched(launch_norm_rope(k_proj, k_weight, k_cache, ks, st), "normRope");
+    if (r == LLMI_HIP_OK)
+      r = launched(launch_cache_append(v_new, v_cache, p.tokens * row, p.past * row, st),
+                   "cacheAppend");
+    if (r == LLMI_HIP_OK)
+      r = launched(launch_gqa_prefill_gated(k_cache, v_cache, out, s, ga, st),
+                   "gqaPrefillGated");
+    return r;
+  }
+  return fail(LLMI_HIP_UNSUPPORTED,
+              "gated attention: no fused kernel for T %u, heads %u/%u, head_dim %u, rotary %u",
+              p.tokens, p.queryHeads, p.kvHeads, p.headDim, rotary_dim);
+}
+
 size_t llmi_hip_delta_workspace_bytes(GraphDeltaParams p) {
   if (check_delta(p) != LLMI_HIP_OK)
     return 0;
@@ -519,6 +577,16 @@ unsigned llmi_hip_dispatch_count(int op, const void *params) {
                ? 1
                : 0;
   }
+  case LLMI_HIP_OP_GATED_ATTENTION: {
+    // Launches for a rotary width the kernels take (a multiple of 16).
+    const GqaParams &p = *static_cast<const GqaParams *>(params);
+    if (check_gqa(p))
+      return 0;
+    GqaShape s{p.tokens, p.queryHeads, p.kvHeads, p.headDim, p.past};
+    if (decode_gated_supported(s, 16))
+      return decode_launches(s);
+    return p.tokens > 1 && prefill_gated_supported(s, 16) ? 3 : 0;
+  }
   }
   return 0;
 }
@@ -590,6 +658,10 @@ const char *llmi_hip_kernel_name(int op, const void *params, unsigned index) {
                                   nullptr, nullptr, nullptr)
                ? "sigmoidMulVec"
                : "sigmoidMulScalar";
+  case LLMI_HIP_OP_GATED_ATTENTION:
+    if (static_cast<const GqaParams *>(params)->tokens == 1)
+      return index == 0 ? "gqaDecodeGated" : "gqaDecodeMergeGated";
+    return index == 0 ? "normRopeTile" : index == 1 ? "cacheAppend" : "gqaPrefillGated";
   }
   return nullptr;
 }

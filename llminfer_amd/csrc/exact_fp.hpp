@@ -29,6 +29,12 @@ __device__ __forceinline__ float opaque(float x) {
   return x;
 }
 __device__ __forceinline__ float mul32(float a, float b) { return opaque(a * b); }
+
+// fp16 of the fp32 value x, with x itself rounded to fp32 first -- the two
+// roundings of the reference's half(float expression). Without opaque() the
+// backend may fold the product or fma producing x into v_fma_mix*_f16 and
+// round once, and it decides that per instantiation.
+__device__ __forceinline__ _Float16 f16_of(float x) { return (_Float16)opaque(x); }
 __device__ __forceinline__ float round16(float x) { return opaque((float)(_Float16)x); }
 
 // Correctly rounded float square root: taken in double and rounded once,

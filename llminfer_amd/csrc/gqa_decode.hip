@@ -42,10 +42,12 @@
 //    writes, without a second launch.
 #include "hip_common.hpp"
 #include "kernels.hpp"
+#include "rope_gate.hpp"
 
 #include <algorithm>
 #include <math.h>
 #include <stdlib.h>
+#include <type_traits>
 
 namespace llmi {
 namespace {
@@ -158,13 +160,152 @@ __device__ __forceinline__ float wave_sum(float x) {
   return p.a + p.b;
 }
 
+struct NoRows {}; // the ungated kernels' (empty) row argument
+
+// LDS barrier: this wave's LDS accesses complete, then the workgroup
+// barrier. Unlike __syncthreads it does not wait for outstanding global
+// loads, so key loads issued before it stay in flight.
+__device__ __forceinline__ void lds_sync() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+// The gated decode's row work for one workgroup (kv head kvh, token 0):
+// its G query rows through normRope into qv, and -- for the owner of the
+// new key row P -- that key through normRope into the cache row P and the
+// new V row into the value cache row P, both stores complete on return.
+// Staged through LDS so that one lane per row runs the reference's
+// sequential sum of squares (rmsScale, Reference.metal:98-103).
+template <int D, int G> struct GatedStage {
+  uint4_t row, vrow; // one 16-byte chunk of a q or k row, of the v row
+};
+
 template <int D, int G>
+__device__ __forceinline__ void gated_fetch(const GatedRows &ga, unsigned P, unsigned kvh,
+                                            unsigned Hq, unsigned Hkv, bool owner,
+                                            unsigned tid, GatedStage<D, G> &st) {
+  constexpr unsigned CPR = D / 8;
+  const unsigned r = tid / CPR, col = tid % CPR;
+  if (r < (unsigned)G)
+    st.row = *reinterpret_cast<const uint4_t *>(ga.qproj + (size_t)(kvh * G + r) * 2 * D +
+                                                8 * col);
+  else if (r == (unsigned)G && owner)
+    st.row = *reinterpret_cast<const uint4_t *>(ga.kproj + (size_t)kvh * D + 8 * col);
+  if (owner && tid < CPR)
+    st.vrow = *reinterpret_cast<const uint4_t *>(ga.vnew + (size_t)kvh * D + 8 * col);
+  (void)P;
+  (void)Hq;
+  (void)Hkv;
+}
+
+template <int D, int G>
+__device__ __forceinline__ void gated_finish(const GatedRows &ga, half_t *kc, half_t *vc,
+                                             unsigned P, unsigned kvh, unsigned Hkv,
+                                             bool owner, const GatedStage<D, G> &st,
+                                             half8_t (&qv)[G][2], unsigned tid,
+                                             unsigned slice) {
+  constexpr unsigned CPR = D / 8, PITCH = D + 8;
+  __shared__ __attribute__((aligned(16))) uint16_t sRow[(G + 1) * PITCH];
+  __shared__ float sScale[G + 1];
+  __shared__ float2 sCs[D / 2];
+  const unsigned rows = owner ? G + 1 : G;
+  const size_t prow = ((size_t)P * Hkv + kvh) * D; // cache row P of this kv head
+  {
+    const unsigned r = tid / CPR, col = tid % CPR;
+    if (r < rows)
+      *reinterpret_cast<uint4_t *>(sRow + r * PITCH + 8 * col) = st.row;
+    if (owner && tid < CPR)
+      *reinterpret_cast<uint4_t *>(vc + prow + 8 * tid) = st.vrow;
+  }
+  lds_sync();
+  const unsigned half = ga.rot / 2;
+  if (tid < rows) {
+    // The sequential fma chain over the row, in index order.
+    const uint4_t *row = reinterpret_cast<const uint4_t *>(sRow + tid * PITCH);
+    float sum = 0.0f;
+    for (unsigned c8 = 0; c8 < CPR; ++c8)
+      sum = sumsq8(row[c8], sum);
+    sScale[tid] = rms_scale_of(sum, D, ga.eps);
+  }
+  if (tid >= 64 && tid - 64 < half)
+    sCs[tid - 64] = rope_cos_sin(__fdiv_rn((float)P, ga.freqs[tid - 64]));
+  lds_sync();
+  // Rotary items (a row and 8 pairs: chunks j0 and j0 + rot/2), then the
+  // copied chunks, normalised with (1 + w) and written back in place (q) or
+  // to the cache row P (the new key).
+  const unsigned pchunks = half / 8, rest = CPR - 2 * pchunks;
+  for (unsigned it = tid; it < rows * pchunks; it += 64 * kWaves) {
+    const unsigned r = it / pchunks, j0 = 8 * (it % pchunks), j1 = j0 + half;
+    uint16_t *row = sRow + r * PITCH;
+    const float *w = r < (unsigned)G ? ga.qw : ga.kw;
+    const float scale = sScale[r];
+    const uint4_t qx = *reinterpret_cast<const uint4_t *>(row + j0);
+    const uint4_t qy = *reinterpret_cast<const uint4_t *>(row + j1);
+    uint4_t sx, sy;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const uint16_t bx = (uint16_t)(qx[e / 2] >> (16 * (e & 1)));
+      const uint16_t by = (uint16_t)(qy[e / 2] >> (16 * (e & 1)));
+      const float x = normed(bx, scale, 1.0f + w[j0 + e]);
+      const float y = normed(by, scale, 1.0f + w[j1 + e]);
+      const float2 cs = sCs[j0 + e];
+      const uint32_t ox = rotate_x(x, y, cs), oy = rotate_y(x, y, cs);
+      if (e & 1) {
+        sx[e / 2] |= ox << 16;
+        sy[e / 2] |= oy << 16;
+      } else {
+        sx[e / 2] = ox;
+        sy[e / 2] = oy;
+      }
+    }
+    if (r < (unsigned)G) {
+      *reinterpret_cast<uint4_t *>(row + j0) = sx;
+      *reinterpret_cast<uint4_t *>(row + j1) = sy;
+    } else {
+      *reinterpret_cast<uint4_t *>(kc + prow + j0) = sx;
+      *reinterpret_cast<uint4_t *>(kc + prow + j1) = sy;
+    }
+  }
+  for (unsigned it = tid; it < rows * rest; it += 64 * kWaves) {
+    const unsigned r = it / rest, j0 = 8 * (2 * pchunks + it % rest);
+    uint16_t *row = sRow + r * PITCH;
+    const float *w = r < (unsigned)G ? ga.qw : ga.kw;
+    const float scale = sScale[r];
+    const uint4_t qx = *reinterpret_cast<const uint4_t *>(row + j0);
+    uint4_t sx;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const uint32_t lo = f2h(normed((uint16_t)(qx[e] & 0xFFFFu), scale, 1.0f + w[j0 + 2 * e]));
+      const uint32_t hi =
+          f2h(normed((uint16_t)(qx[e] >> 16), scale, 1.0f + w[j0 + 2 * e + 1]));
+      sx[e] = lo | (hi << 16);
+    }
+    if (r < (unsigned)G)
+      *reinterpret_cast<uint4_t *>(row + j0) = sx;
+    else
+      *reinterpret_cast<uint4_t *>(kc + prow + j0) = sx;
+  }
+  if (owner)
+    __builtin_amdgcn_s_waitcnt(0); // the cache row P is written before any key load
+  lds_sync();
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+      qv[g][j] = *reinterpret_cast<const half8_t *>(sRow + g * PITCH + j * (D / 2) + slice * 8);
+}
+
+// GATED (one token): the attention block's row work around the decode --
+// q and the new key through normRope, the new V row appended, the output
+// through the sigmoid gate -- with every result the standalone row kernels'
+// bits (rope_gate.hpp).
+template <int D, int G, bool GATED>
 __global__ __launch_bounds__(64 * kWaves) void gqa_decode_kernel(
     const half_t *__restrict__ q, half_t *kc, half_t *vc,
     const half_t *__restrict__ knew, const half_t *__restrict__ vnew,
     half_t *__restrict__ out, float *__restrict__ wml,
     float *__restrict__ wo, unsigned Hq, unsigned Hkv, unsigned P,
-    unsigned T, unsigned keysPerSplit, unsigned splits, float scoreScale) {
+    unsigned T, unsigned keysPerSplit, unsigned splits, float scoreScale,
+    typename std::conditional<GATED, GatedRows, NoRows>::type ga) {
   using Geo = DecodeGeom<D>;
   constexpr int LPK = Geo::LPK, KPR = Geo::KPR;
   constexpr int W = kWaves, NT = 64 * W;
@@ -196,11 +337,13 @@ __global__ __launch_bounds__(64 * kWaves) void gqa_decode_kernel(
 
   // Channels of this lane: [j*D/2 + slice*8, +8) for j = 0, 1.
   half8_t qv[G][2];
+  if constexpr (!GATED) {
 #pragma unroll
-  for (int g = 0; g < G; ++g)
+    for (int g = 0; g < G; ++g)
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
-      qv[g][j] = load8(q + ((size_t)t * Hq + kvh * G + g) * D + j * (D / 2) + slice * 8);
+      for (int j = 0; j < 2; ++j)
+        qv[g][j] = load8(q + ((size_t)t * Hq + kvh * G + g) * D + j * (D / 2) + slice * 8);
+  }
 
   float m[G], l[G], o[G][16];
 #pragma unroll
@@ -316,13 +459,30 @@ __global__ __launch_bounds__(64 * kWaves) void gqa_decode_kernel(
   // loop body covers R sets with compile-time buffer indices, and every path
   // into its header has the same loads outstanding, which keeps the
   // compiler's wait counts partial.
-  if (begin < end) {
-    constexpr int R = ring_depth<G>();
-    const unsigned sets = (end - begin + Tile - 1) / Tile;
-    KvSet buf[R];
+  constexpr int R = ring_depth<G>();
+  KvSet buf[R];
+  auto ring_prologue = [&]() {
 #pragma unroll
     for (int r = 0; r < R - 1; ++r)
       load_set(buf[r], begin + r * Tile);
+  };
+  // GATED: the workgroup whose keys include the new row P writes that row
+  // (normRoped K, raw V) to the cache before it loads any key; every other
+  // workgroup starts its loads first and normalises q under them.
+  const bool owner = GATED && begin <= P && P < end;
+  GatedStage<D, G> gst;
+  if constexpr (GATED)
+    gated_fetch<D, G>(ga, P, kvh, Hq, Hkv, owner, tid, gst);
+  if (begin < end && !owner)
+    ring_prologue();
+  if constexpr (GATED) {
+    gated_finish<D, G>(ga, kc, vc, P, kvh, Hkv, owner, gst, qv, tid, slice);
+    if (begin < end && owner)
+      ring_prologue();
+  }
+
+  if (begin < end) {
+    const unsigned sets = (end - begin + Tile - 1) / Tile;
     unsigned base = begin, i = 0;
     for (; i + R <= sets; i += R) {
 #pragma unroll
@@ -416,9 +576,15 @@ __global__ __launch_bounds__(64 * kWaves) void gqa_decode_kernel(
       const float4_t acc = combine(i, M, L);
       const float inv = 1.0f / L;
       const unsigned g = i * 4 / D, x = i * 4 % D;
-      *reinterpret_cast<half4_t *>(orow + g * D + x) =
-          half4_t{(half_t)(acc[0] * inv), (half_t)(acc[1] * inv), (half_t)(acc[2] * inv),
-                  (half_t)(acc[3] * inv)};
+      half4_t y{f16_of(acc[0] * inv), f16_of(acc[1] * inv), f16_of(acc[2] * inv),
+                f16_of(acc[3] * inv)};
+      if constexpr (GATED) {
+        const half_t *gr = ga.qproj + ((size_t)t * Hq + kvh * G + g) * 2 * D + D + x;
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          y[e] = __builtin_bit_cast(half_t, gate16((float)gr[e], (float)y[e]));
+      }
+      *reinterpret_cast<half4_t *>(orow + g * D + x) = y;
     }
     return;
   }
@@ -442,10 +608,11 @@ __global__ __launch_bounds__(64 * kWaves) void gqa_decode_kernel(
 // Second-launch merge: workgroup (channel block, g, row) combines the
 // splits of 64 output channels of query head g of one (token, kv head) row;
 // each thread loads its channel of every partial at once.
-template <int D, int G>
+template <int D, int G, bool GATED>
 __global__ __launch_bounds__(64) void gqa_decode_merge_kernel(
     const float *__restrict__ wml, const float *__restrict__ wo,
-    half_t *__restrict__ out, unsigned Hq, unsigned Hkv, unsigned splits) {
+    half_t *__restrict__ out, unsigned Hq, unsigned Hkv, unsigned splits,
+    const half_t *__restrict__ qproj) {
   static_assert(D % 64 == 0, "whole waves");
   const unsigned lane = threadIdx.x, g = blockIdx.y, row = blockIdx.z;
   const unsigned x = blockIdx.x * 64 + lane;
@@ -489,18 +656,24 @@ __global__ __launch_bounds__(64) void gqa_decode_merge_kernel(
       acc = fmaf(v[u], sW[PER + u], acc);
   }
   const unsigned t = row / Hkv, kvh = row % Hkv;
-  out[((size_t)t * Hq + kvh * G + g) * D + x] = (half_t)acc;
+  const half_t y = f16_of(acc);
+  if constexpr (GATED)
+    out[((size_t)t * Hq + kvh * G + g) * D + x] = __builtin_bit_cast(
+        half_t, gate16((float)qproj[((size_t)t * Hq + kvh * G + g) * 2 * D + D + x], (float)y));
+  else
+    out[((size_t)t * Hq + kvh * G + g) * D + x] = y;
 }
 
-template <int D, int G>
-hipError_t launch_dg(const GqaShape &s, const uint16_t *q, uint16_t *k,
-                     uint16_t *v, const uint16_t *knew, const uint16_t *vnew,
-                     uint16_t *out, void *ws, hipStream_t stream) {
+template <int D, int G, bool GATED, typename Rows>
+hipError_t launch_dgg(const GqaShape &s, const uint16_t *q, uint16_t *k,
+                      uint16_t *v, const uint16_t *knew, const uint16_t *vnew,
+                      uint16_t *out, void *ws, const Rows &ga, const half_t *qproj,
+                      hipStream_t stream) {
   const Plan p = plan_for(s);
   const WsLayout w = layout_for(s, p);
   char *base = static_cast<char *>(ws);
   const float scale = kLog2e / sqrtf((float)D);
-  hipLaunchKernelGGL((gqa_decode_kernel<D, G>), dim3(p.splits, s.Hkv, s.T),
+  hipLaunchKernelGGL((gqa_decode_kernel<D, G, GATED>), dim3(p.splits, s.Hkv, s.T),
                      dim3(64 * kWaves), 0, stream,
                      reinterpret_cast<const half_t *>(q),
                      reinterpret_cast<half_t *>(k), reinterpret_cast<half_t *>(v),
@@ -509,17 +682,24 @@ hipError_t launch_dg(const GqaShape &s, const uint16_t *q, uint16_t *k,
                      reinterpret_cast<half_t *>(out),
                      reinterpret_cast<float *>(base ? base + w.ml : nullptr),
                      reinterpret_cast<float *>(base ? base + w.o : nullptr), s.Hq,
-                     s.Hkv, s.P, s.T, p.keysPerSplit, p.splits, scale);
+                     s.Hkv, s.P, s.T, p.keysPerSplit, p.splits, scale, ga);
   if (p.splits > 1) {
     hipError_t e = hipGetLastError();
     if (e != hipSuccess)
       return e;
-    hipLaunchKernelGGL((gqa_decode_merge_kernel<D, G>), dim3(D / 64, G, s.T * s.Hkv),
+    hipLaunchKernelGGL((gqa_decode_merge_kernel<D, G, GATED>), dim3(D / 64, G, s.T * s.Hkv),
                        dim3(64), 0, stream, reinterpret_cast<float *>(base + w.ml),
                        reinterpret_cast<float *>(base + w.o),
-                       reinterpret_cast<half_t *>(out), s.Hq, s.Hkv, p.splits);
+                       reinterpret_cast<half_t *>(out), s.Hq, s.Hkv, p.splits, qproj);
   }
   return hipGetLastError();
+}
+
+template <int D, int G>
+hipError_t launch_dg(const GqaShape &s, const uint16_t *q, uint16_t *k,
+                     uint16_t *v, const uint16_t *knew, const uint16_t *vnew,
+                     uint16_t *out, void *ws, hipStream_t stream) {
+  return launch_dgg<D, G, false>(s, q, k, v, knew, vnew, out, ws, NoRows{}, nullptr, stream);
 }
 
 template <int D>
@@ -555,6 +735,31 @@ size_t decode_workspace_bytes(const GqaShape &s) {
 unsigned decode_splits(const GqaShape &s) { return plan_for(s).splits; }
 
 unsigned decode_launches(const GqaShape &s) { return plan_for(s).splits > 1 ? 2 : 1; }
+
+bool decode_gated_supported(const GqaShape &s, unsigned rot) {
+  const unsigned G = s.Hkv ? s.Hq / s.Hkv : 0;
+  return s.T == 1 && decode_supported(s) && (s.D == 128 || s.D == 256) &&
+         (G == 2 || G == 4) && rot % 16 == 0 && rot <= s.D;
+}
+
+hipError_t launch_gqa_decode_gated(uint16_t *k, uint16_t *v, uint16_t *out, void *ws,
+                                   const GqaShape &s, const GatedRows &ga,
+                                   hipStream_t stream) {
+  const half_t *qp = reinterpret_cast<const half_t *>(ga.qproj);
+  if (s.D == 256 && s.Hq == 4 * s.Hkv)
+    return launch_dgg<256, 4, true>(s, nullptr, k, v, nullptr, nullptr, out, ws, ga, qp,
+                                    stream);
+  if (s.D == 128 && s.Hq == 4 * s.Hkv)
+    return launch_dgg<128, 4, true>(s, nullptr, k, v, nullptr, nullptr, out, ws, ga, qp,
+                                    stream);
+  if (s.D == 256 && s.Hq == 2 * s.Hkv)
+    return launch_dgg<256, 2, true>(s, nullptr, k, v, nullptr, nullptr, out, ws, ga, qp,
+                                    stream);
+  if (s.D == 128 && s.Hq == 2 * s.Hkv)
+    return launch_dgg<128, 2, true>(s, nullptr, k, v, nullptr, nullptr, out, ws, ga, qp,
+                                    stream);
+  return hipErrorInvalidValue;
+}
 
 hipError_t launch_gqa_decode(const uint16_t *q, uint16_t *k, uint16_t *v,
                              const uint16_t *knew, const uint16_t *vnew,

@@ -30,8 +30,10 @@
 //    overlap the softmax arithmetic of tile i.
 #include "hip_common.hpp"
 #include "kernels.hpp"
+#include "rope_gate.hpp"
 
 #include <math.h>
+#include <type_traits>
 
 namespace llmi {
 namespace {
@@ -70,13 +72,21 @@ __device__ __forceinline__ half4_t read_tr(const char *base, unsigned off) {
                                          (lds_fp16x4_t *)((lds_char_t *)base + off)));
 }
 
-template <int D, int HW>
+struct NoRows {}; // the ungated kernel's (empty) row argument
+
+// GATED: the query rows come from the projected q (per head D query values,
+// then D gate values) through normRope, staged in the K/V buffers before
+// the keys need them, and the output goes through the sigmoid gate: the
+// bits of the standalone normRope and sigmoidMul (rope_gate.hpp) around the
+// same attention.
+template <int D, int HW, bool GATED>
 __global__ __attribute__((amdgpu_flat_work_group_size(64 * HW, 64 * HW),
                           amdgpu_waves_per_eu(HW > 4 ? 2 : 1, HW > 4 ? 2 : 1)))
 void gqa_prefill_kernel(const half_t *__restrict__ q, const half_t *__restrict__ kc,
                         const half_t *__restrict__ vc, half_t *__restrict__ out,
                         unsigned T, unsigned Hq, unsigned Hkv, unsigned P,
-                        unsigned groups, unsigned nb, float c) {
+                        unsigned groups, unsigned nb, float c,
+                        typename std::conditional<GATED, GatedRows, NoRows>::type ga) {
   constexpr int KS = D / 16;         // k-steps of S^T over channels
   constexpr int DT = D / 32;         // 32-channel output tiles
   constexpr int ROWB = 2 * D;        // bytes per K/V row
@@ -257,10 +267,104 @@ void gqa_prefill_kernel(const half_t *__restrict__ q, const half_t *__restrict__
   // Q^T as the MFMA B operand: lane holds query row r, channels
   // 16 s + 8 hi + [0, 8). Rows past T use zeros (their output is dropped).
   half8_t qb[KS];
+  if constexpr (GATED) {
+    // Each wave's 32 query rows through normRope in its own K/V buffer
+    // (rows of D + 8 halves, then their scales). The (1 + w) weights and the
+    // (token, pair) table of fp16 cos/sin, the same for every head of the
+    // block, are made once per workgroup after wave 0's rows. The buffers
+    // are cleared for the keys afterwards.
+    static_assert(HW <= 4, "one K/V buffer per wave");
+    constexpr unsigned PITCH = D + 8, CPR = D / 8;
+    char *buf = wave == 0 ? sK0 : wave == 1 ? sK1 : wave == 2 ? sV0 : sV1;
+    uint16_t *rows = reinterpret_cast<uint16_t *>(buf);
+    float *scl = reinterpret_cast<float *>(rows + BM * PITCH);
+    float *w1 = reinterpret_cast<float *>(sK0 + BM * PITCH * 2 + BM * 4);
+    half2_t *cs = reinterpret_cast<half2_t *>(w1 + D); // fp16 values, stored exactly
+    const unsigned half = ga.rot / 2, nrow = min((unsigned)BM, T - t0);
+    const half_t *qp = reinterpret_cast<const half_t *>(ga.qproj);
+    for (unsigned i = lane; i < nrow * CPR; i += 64) {
+      const unsigned rr = i / CPR, cc = i % CPR;
+      *reinterpret_cast<uint4_t *>(rows + rr * PITCH + 8 * cc) =
+          *reinterpret_cast<const uint4_t *>(qp + ((size_t)(t0 + rr) * Hq + h) * 2 * D + 8 * cc);
+    }
+    for (unsigned i = threadIdx.x; i < (unsigned)D; i += 64 * HW)
+      w1[i] = 1.0f + ga.qw[i];
+    for (unsigned e = threadIdx.x; e < nrow * half; e += 64 * HW) {
+      const unsigned tt = e / half, i = e % half;
+      const float2 v2 = rope_cos_sin(__fdiv_rn((float)(P + t0 + tt), ga.freqs[i]));
+      cs[e] = half2_t{(half_t)v2.x, (half_t)v2.y};
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    if (lane < nrow) {
+      // The sequential chain; its row is read eight chunks ahead.
+      const uint4_t *row = reinterpret_cast<const uint4_t *>(rows + lane * PITCH);
+      float sum = 0.0f;
+      for (unsigned c8 = 0; c8 < CPR; c8 += 8) {
+        uint4_t x[8];
 #pragma unroll
-  for (int s = 0; s < KS; ++s)
-    qb[s] = rowValid ? load8(q + ((size_t)tq * Hq + h) * D + 16 * s + 8 * hi)
-                     : half8_t{0, 0, 0, 0, 0, 0, 0, 0};
+        for (int u = 0; u < 8; ++u)
+          x[u] = row[c8 + u];
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+          sum = sumsq8(x[u], sum);
+      }
+      scl[lane] = rms_scale_of(sum, D, ga.eps);
+    }
+    __syncthreads(); // the shared tables and every row's scale are in place
+    const unsigned pchunks = half / 8, rest = CPR - 2 * pchunks;
+    for (unsigned it = lane; it < nrow * pchunks; it += 64) {
+      const unsigned rr = it / pchunks, j0 = 8 * (it % pchunks), j1 = j0 + half;
+      uint16_t *row = rows + rr * PITCH;
+      const float scale = scl[rr];
+      const uint4_t qx = *reinterpret_cast<const uint4_t *>(row + j0);
+      const uint4_t qy = *reinterpret_cast<const uint4_t *>(row + j1);
+      uint4_t sx, sy;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const uint16_t bx = (uint16_t)(qx[e / 2] >> (16 * (e & 1)));
+        const uint16_t by = (uint16_t)(qy[e / 2] >> (16 * (e & 1)));
+        const float x = normed(bx, scale, w1[j0 + e]);
+        const float y = normed(by, scale, w1[j1 + e]);
+        const half2_t c2 = cs[rr * half + j0 + e];
+        const float2 t2 = make_float2((float)c2[0], (float)c2[1]);
+        const uint32_t ox = rotate_x(x, y, t2), oy = rotate_y(x, y, t2);
+        if (e & 1) {
+          sx[e / 2] |= ox << 16;
+          sy[e / 2] |= oy << 16;
+        } else {
+          sx[e / 2] = ox;
+          sy[e / 2] = oy;
+        }
+      }
+      *reinterpret_cast<uint4_t *>(row + j0) = sx;
+      *reinterpret_cast<uint4_t *>(row + j1) = sy;
+    }
+    for (unsigned it = lane; it < nrow * rest; it += 64) {
+      const unsigned rr = it / rest, j0 = 8 * (2 * pchunks + it % rest);
+      uint16_t *row = rows + rr * PITCH;
+      const float scale = scl[rr];
+      const uint4_t qx = *reinterpret_cast<const uint4_t *>(row + j0);
+      uint4_t sx;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t lo = f2h(normed((uint16_t)(qx[e] & 0xFFFFu), scale, w1[j0 + 2 * e]));
+        const uint32_t hi = f2h(normed((uint16_t)(qx[e] >> 16), scale, w1[j0 + 2 * e + 1]));
+        sx[e] = lo | (hi << 16);
+      }
+      *reinterpret_cast<uint4_t *>(row + j0) = sx;
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+    for (int s = 0; s < KS; ++s)
+      qb[s] = rowValid ? *reinterpret_cast<const half8_t *>(rows + r * PITCH + 16 * s + 8 * hi)
+                       : half8_t{0, 0, 0, 0, 0, 0, 0, 0};
+    __syncthreads(); // every wave is done with its buffer before they are cleared
+  } else {
+#pragma unroll
+    for (int s = 0; s < KS; ++s)
+      qb[s] = rowValid ? load8(q + ((size_t)tq * Hq + h) * D + 16 * s + 8 * hi)
+                       : half8_t{0, 0, 0, 0, 0, 0, 0, 0};
+  }
 
   float16_t oacc[DT];
 #pragma unroll
@@ -490,29 +594,85 @@ void gqa_prefill_kernel(const half_t *__restrict__ q, const half_t *__restrict__
   const float inv = 1.0f / lacc[0];
   half_t *orow = out + ((size_t)tq * Hq + h) * D;
 #pragma unroll
-  for (int dt = 0; dt < DT; ++dt)
+  for (int dt = 0; dt < DT; ++dt) {
+    half4_t v[4];
 #pragma unroll
-    for (int g4 = 0; g4 < 4; ++g4) {
-      half4_t v{(half_t)(oacc[dt][4 * g4 + 0] * inv), (half_t)(oacc[dt][4 * g4 + 1] * inv),
-                (half_t)(oacc[dt][4 * g4 + 2] * inv), (half_t)(oacc[dt][4 * g4 + 3] * inv)};
-      *reinterpret_cast<half4_t *>(orow + 32 * dt + 8 * g4 + 4 * hi) = v;
+    for (int g4 = 0; g4 < 4; ++g4)
+      v[g4] = half4_t{f16_of(oacc[dt][4 * g4 + 0] * inv), f16_of(oacc[dt][4 * g4 + 1] * inv),
+                      f16_of(oacc[dt][4 * g4 + 2] * inv), f16_of(oacc[dt][4 * g4 + 3] * inv)};
+    if constexpr (GATED) {
+      // The gates of this output tile: the fast logistic first, then the
+      // exact one for the few that miss the margin test, one per pass of
+      // the wave (as the standalone gate kernel does).
+      const half_t *grow = reinterpret_cast<const half_t *>(ga.qproj) +
+                           ((size_t)tq * Hq + h) * 2 * D + D + 32 * dt + 4 * hi;
+      float g[16], sg[16];
+      unsigned need = 0;
+#pragma unroll
+      for (int g4 = 0; g4 < 4; ++g4) {
+        const half4_t gv = *reinterpret_cast<const half4_t *>(grow + 8 * g4);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          g[4 * g4 + e] = (float)gv[e];
+          sg[4 * g4 + e] = logistic_estimate(g[4 * g4 + e]);
+          need |= f16_settled(sg[4 * g4 + e]) ? 0u : 1u << (4 * g4 + e);
+        }
+      }
+      while (need) {
+        const unsigned k = __builtin_ctz(need);
+        need &= need - 1;
+        float gk = g[0];
+#pragma unroll
+        for (int e = 1; e < 16; ++e)
+          gk = k == (unsigned)e ? g[e] : gk;
+        const float sk = logistic_exact(gk);
+#pragma unroll
+        for (int e = 0; e < 16; ++e)
+          sg[e] = k == (unsigned)e ? sk : sg[e];
+      }
+#pragma unroll
+      for (int g4 = 0; g4 < 4; ++g4)
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          v[g4][e] = __builtin_bit_cast(
+              half_t, f2h(mul32(round16(sg[4 * g4 + e]), (float)v[g4][e])));
     }
+#pragma unroll
+    for (int g4 = 0; g4 < 4; ++g4)
+      *reinterpret_cast<half4_t *>(orow + 32 * dt + 8 * g4 + 4 * hi) = v[g4];
+  }
 }
 
 template <int D> constexpr unsigned heads_per_wg(unsigned G) {
   return G < (D == 256 ? 4u : 8u) ? G : (D == 256 ? 4u : 8u);
 }
 
-template <int D, int HW>
+template <int D, int HW, bool GATED = false, typename Rows = NoRows>
 hipError_t launch_dw(const GqaShape &s, const uint16_t *q, const uint16_t *k,
-                     const uint16_t *v, uint16_t *out, hipStream_t stream) {
+                     const uint16_t *v, uint16_t *out, hipStream_t stream,
+                     const Rows &rows = Rows{}) {
   const float c = kLog2e / sqrtf((float)D);
   const unsigned G = s.Hq / s.Hkv, groups = G / HW, nb = (s.T + BM - 1) / BM;
-  hipLaunchKernelGGL((gqa_prefill_kernel<D, HW>), dim3(nb * s.Hkv * groups), dim3(64 * HW), 0,
-                     stream, reinterpret_cast<const half_t *>(q),
+  hipLaunchKernelGGL((gqa_prefill_kernel<D, HW, GATED>), dim3(nb * s.Hkv * groups),
+                     dim3(64 * HW), 0, stream, reinterpret_cast<const half_t *>(q),
                      reinterpret_cast<const half_t *>(k), reinterpret_cast<const half_t *>(v),
-                     reinterpret_cast<half_t *>(out), s.T, s.Hq, s.Hkv, s.P, groups, nb, c);
+                     reinterpret_cast<half_t *>(out), s.T, s.Hq, s.Hkv, s.P, groups, nb, c,
+                     rows);
   return hipGetLastError();
+}
+
+template <int D>
+hipError_t launch_gated_d(const GqaShape &s, const uint16_t *k, const uint16_t *v,
+                          uint16_t *out, const GatedRows &ga, hipStream_t stream) {
+  switch (heads_per_wg<D>(s.Hq / s.Hkv)) {
+  case 1:
+    return launch_dw<D, 1, true>(s, nullptr, k, v, out, stream, ga);
+  case 2:
+    return launch_dw<D, 2, true>(s, nullptr, k, v, out, stream, ga);
+  case 4:
+    return launch_dw<D, 4, true>(s, nullptr, k, v, out, stream, ga);
+  }
+  return hipErrorInvalidValue;
 }
 
 template <int D>
@@ -541,6 +701,26 @@ bool prefill_supported(const GqaShape &s) {
   const uint64_t sliceBytes = (uint64_t)BN * s.Hkv * s.D * 2;
   return (s.D == 128 || s.D == 256) && (G == 1 || G == 2 || G == 4 || G == 8) &&
          s.T >= 1 && sliceBytes < (1ull << 31);
+}
+
+bool prefill_gated_supported(const GqaShape &s, unsigned rot) {
+  // One K/V buffer per wave holds the wave's rows, their scales and the
+  // cos/sin table of its 32 tokens.
+  const unsigned HW = s.D == 256 ? heads_per_wg<256>(s.Hkv ? s.Hq / s.Hkv : 0)
+                                 : heads_per_wg<128>(s.Hkv ? s.Hq / s.Hkv : 0);
+  // wave 0's buffer also holds the (1 + w) weights and the cos/sin table
+  const size_t need = (size_t)BM * (s.D + 8) * 2 + BM * 4 + (size_t)s.D * 4 +
+                      (size_t)BM * (rot / 2) * 4;
+  return prefill_supported(s) && HW <= 4 && need <= (size_t)BN * 2 * s.D &&
+         rot % 16 == 0 && rot <= s.D;
+}
+
+hipError_t launch_gqa_prefill_gated(const uint16_t *k, const uint16_t *v, uint16_t *out,
+                                    const GqaShape &s, const GatedRows &ga,
+                                    hipStream_t stream) {
+  if (s.D == 128)
+    return launch_gated_d<128>(s, k, v, out, ga, stream);
+  return launch_gated_d<256>(s, k, v, out, ga, stream);
 }
 
 hipError_t launch_gqa_prefill(const uint16_t *q, const uint16_t *k,

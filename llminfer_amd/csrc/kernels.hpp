@@ -35,8 +35,40 @@ hipError_t launch_gqa_decode(const uint16_t *q, uint16_t *k, uint16_t *v,
                              uint16_t *out, void *ws, const GqaShape &s,
                              hipStream_t stream);
 
+// The attention block's row inputs around CausalGqa for the gated forms
+// (normRope of q and k, the V append, the sigmoid output gate): the
+// projected q rows [T][Hq][2D] (per head D query values, then D gate
+// values), the new keys before their norm and the new values [T][Hkv][D],
+// the norm weights [D] (the kernels form 1 + w), the rotary width and the
+// norm epsilon, and pow(theta, 2i/rot) for i < rot/2.
+struct GatedRows {
+  const _Float16 *qproj = nullptr;
+  const _Float16 *kproj = nullptr;
+  const _Float16 *vnew = nullptr;
+  const float *qw = nullptr, *kw = nullptr;
+  unsigned rot = 0;
+  float eps = 0.0f;
+  float freqs[256] = {};
+};
+
+// The gated decode (T == 1, decode_supported, rot/2 a multiple of 8):
+// normRope of q and of the new key (written to cache row P), the new V row
+// appended, the split-K decode, and the output through the sigmoid gate --
+// the bits of the standalone normRope, cacheAppend, decode and sigmoidMul.
+bool decode_gated_supported(const GqaShape &s, unsigned rot);
+hipError_t launch_gqa_decode_gated(uint16_t *k, uint16_t *v, uint16_t *out, void *ws,
+                                   const GqaShape &s, const GatedRows &ga,
+                                   hipStream_t stream);
+
 // MFMA flash prefill.
 bool prefill_supported(const GqaShape &s);
+// The gated prefill: the query rows through normRope in the kernel, the
+// output through the sigmoid gate (the keys must already be normRoped into
+// the cache, the values appended).
+bool prefill_gated_supported(const GqaShape &s, unsigned rot);
+hipError_t launch_gqa_prefill_gated(const uint16_t *k, const uint16_t *v, uint16_t *out,
+                                    const GqaShape &s, const GatedRows &ga,
+                                    hipStream_t stream);
 hipError_t launch_gqa_prefill(const uint16_t *q, const uint16_t *k,
                               const uint16_t *v, uint16_t *out,
                               const GqaShape &s, hipStream_t stream);

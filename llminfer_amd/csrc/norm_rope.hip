@@ -43,6 +43,7 @@
 #include "exact_fp.hpp"
 #include "hip_common.hpp"
 #include "kernels.hpp"
+#include "rope_gate.hpp"
 
 #include <math.h>
 #include <string.h>
@@ -55,54 +56,9 @@ constexpr int kPad = 8;                 // halves of LDS padding per tile row
 constexpr unsigned kTileHalves = 8192;  // rows * headDim bound of one tile
 constexpr unsigned kTileIters = kTileHalves / 8 / 64;
 
-// fp16(cos(phase)), fp16(sin(phase)) of the correctly rounded fp32 values.
-__device__ __forceinline__ float2 rope_cos_sin(float phase) {
-  float s, c;
-  sincosf(phase, &s, &c);
-  // sincosf is within 2 ulp; 2^-21 relative is 4 to 8 ulp.
-  if (!(f16_settled<21>(c) && f16_settled<21>(s))) {
-    double sd, cd;
-    sincos((double)phase, &sd, &cd);
-    c = (float)cd;
-    s = (float)sd;
-  }
-  return make_float2(round16(c), round16(s));
-}
-
-// pow(theta, 2 * pair / rotaryDim) correctly rounded to fp32.
-__device__ __forceinline__ float rope_inv_freq(float theta, unsigned pair,
-                                               unsigned rot) {
-  float e = __fdiv_rn(2.0f * (float)pair, (float)rot);
-  return (float)pow((double)theta, (double)e);
-}
-
-__device__ __forceinline__ float rms_scale_of(float sum, unsigned width, float eps) {
-  return __fdiv_rn(1.0f, sqrt_cr(__fadd_rn(__fdiv_rn(sum, (float)width), eps)));
-}
-
-__device__ __forceinline__ float normed(uint16_t v, float scale, float w1) {
-  return round16(mul32(mul32(h2f(v), scale), w1));
-}
-
-// rotatePair on fp16 values x, y (held in floats) and fp16 cos/sin.
-__device__ __forceinline__ uint16_t rotate_x(float x, float y, float2 cs) {
-  return f2h(opaque(round16(mul32(x, cs.x)) - round16(mul32(y, cs.y))));
-}
-__device__ __forceinline__ uint16_t rotate_y(float x, float y, float2 cs) {
-  return f2h(opaque(round16(mul32(y, cs.x)) + round16(mul32(x, cs.y))));
-}
-
 struct TileArgs {
   unsigned rows, heads, D, rot, stride, past, out_row0, rw, maxtok;
   float eps, theta;
-};
-
-// pow(theta, 2i/rotaryDim) for i < rotaryDim/2, computed once on the host
-// (correctly rounded, as on the device) and passed in the kernel arguments;
-// wider rotations compute it in the kernel.
-constexpr unsigned kArgFreqs = 256;
-struct RopeFreqs {
-  float v[kArgFreqs];
 };
 
 __device__ __forceinline__ float inv_freq(const RopeFreqs &f, const TileArgs &a,
@@ -326,18 +282,6 @@ __global__ __launch_bounds__(256) void norm_rope_rows(const uint16_t *in,
     dst[i] = kNorm ? f2h(normed(head[i], scale, 1.0f + w[i])) : head[i];
 }
 
-// fp16(logistic(g)) of the correctly rounded fp32 exp.
-__device__ __forceinline__ float logistic16(float g) {
-  float s = logistic_estimate(g);
-  if (!f16_settled(s))
-    s = logistic_exact(g);
-  return round16(s);
-}
-
-__device__ __forceinline__ uint16_t gate_one(uint16_t g, uint16_t x) {
-  return f2h(mul32(logistic16(h2f(g)), h2f(x)));
-}
-
 // Eight gates per lane: the estimates first, then the exact evaluation for
 // the few that need it, one per pass (a pass costs the wave one double exp,
 // so the lanes share passes instead of running one per element slot).
@@ -418,22 +362,6 @@ TilePlan plan_tile(const RopeShape &s) {
   return p;
 }
 
-
-// The host's correctly rounded pow (double, rounded once), per (theta, rot),
-// kept for the next call with the same rotation.
-static const RopeFreqs &host_freqs(float theta, unsigned rot) {
-  static thread_local RopeFreqs table;
-  static thread_local float cached_theta = 0.0f;
-  static thread_local unsigned cached_rot = 0;
-  unsigned half = rot / 2;
-  if (half <= kArgFreqs && (cached_rot != rot || memcmp(&cached_theta, &theta, 4) != 0)) {
-    for (unsigned i = 0; i < half; ++i)
-      table.v[i] = (float)pow((double)theta, (double)(2.0f * (float)i / (float)rot));
-    cached_theta = theta;
-    cached_rot = rot;
-  }
-  return table;
-}
 
 } // namespace
 

@@ -328,6 +328,55 @@ def delta_update(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, beta: torch.
     return out
 
 
+def bind_gated_attention(q_proj: torch.Tensor, k_proj: torch.Tensor, v_new: torch.Tensor,
+                         q_weight: torch.Tensor, k_weight: torch.Tensor, k_cache: torch.Tensor,
+                         v_cache: torch.Tensor, out: torch.Tensor, past: int, rotary_dim: int,
+                         epsilon: float = 1e-6, theta: float = 1e7) -> "Bound":
+    """The attention block around CausalGqa in one call (llmi_hip_gated_attention):
+    q_proj [T, Hq, 2d] (per head d query then d gate values), k_proj and v_new
+    [T, Hkv, d], norm weights [d] fp32, caches [capacity, Hkv, d], out
+    [T, Hq, d]: normRope(q), normRope(k) into the cache at row past, V
+    appended, CausalGqa, sigmoid gate."""
+    for t, n in ((q_proj, "q_proj"), (k_proj, "k_proj"), (v_new, "v_new"),
+                 (k_cache, "k_cache"), (v_cache, "v_cache"), (out, "out")):
+        _require(t, torch.float16, n)
+    for t, n in ((q_weight, "q_weight"), (k_weight, "k_weight")):
+        _require(t, torch.float32, n)
+    if q_proj.dim() != 3 or k_proj.dim() != 3 or v_new.shape != k_proj.shape or \
+            k_cache.shape != v_cache.shape or k_cache.shape[1:] != k_proj.shape[1:]:
+        raise ValueError("gated attention operands disagree")
+    T, hq, d2 = q_proj.shape
+    d = d2 // 2
+    hkv = k_proj.shape[1]
+    if d2 != 2 * d or k_proj.shape[0] != T or k_proj.shape[2] != d or \
+            out.shape != (T, hq, d) or q_weight.numel() != d or k_weight.numel() != d or \
+            past + T > k_cache.shape[0]:
+        raise ValueError("gated attention shapes do not match the cache")
+    lib = _lib.load()
+    p = _lib.GqaParams(T, hq, hkv, d, past)
+    need = lib.llmi_hip_gqa_workspace_bytes(p)
+    ws = workspace(need, q_proj.device) if need else None
+    args = (_ptr(q_proj), _ptr(k_proj), _ptr(v_new), _ptr(q_weight), _ptr(k_weight),
+            _ptr(k_cache), _ptr(v_cache), _ptr(out), p, rotary_dim, epsilon, theta, _ptr(ws),
+            ws.numel() if ws is not None else 0, _stream())
+    names = kernel_names(_lib.OP_GATED_ATTENTION, p)
+    b = Bound(lib.llmi_hip_gated_attention, args, "+".join(names))
+    b._keep = ws
+    return b
+
+
+def gated_attention(q_proj, k_proj, v_new, q_weight, k_weight, k_cache, v_cache, past: int,
+                    rotary_dim: int, epsilon: float = 1e-6, theta: float = 1e7,
+                    out: torch.Tensor | None = None) -> torch.Tensor:
+    """bind_gated_attention, called once."""
+    if out is None:
+        T, hq, d2 = q_proj.shape
+        out = torch.empty((T, hq, d2 // 2), dtype=torch.float16, device=q_proj.device)
+    bind_gated_attention(q_proj, k_proj, v_new, q_weight, k_weight, k_cache, v_cache, out,
+                         past, rotary_dim, epsilon, theta)()
+    return out
+
+
 def bind_l2_norm_delta_update(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                               beta: torch.Tensor, decay: torch.Tensor, state: torch.Tensor,
                               out: torch.Tensor, epsilon: float = 1e-6,
