@@ -35,18 +35,17 @@
 //    the products Wn, Q', Z0, Y0 on fp16 MFMA in split form. The results go to
 //    the workspace already in the register order of the scan's MFMA operands.
 //
-//  * deltaChunkScan, grid (value head, 16-column dv slice), 4 waves: one
-//    walks the chunks in order with its state slice S [dk x 16] in
-//    registers, one computes the outputs, two load. Every product runs on
-//    v_mfma_f32_16x16x32_f16, with the state (and Z) as the B operand
-//    straight from the C-layout registers of the product that made it: the k
-//    index of an operand block is permuted (sigma below) so that the 8 halves
-//    a lane supplies are the 8 rows it holds in two consecutive 16-row C
-//    tiles; the A operands (Wn, Q', K^T) were written by the prep with the
-//    same permutation. No LDS round trip and no shuffle on the chain. The
-//    next chunk's Wn and K^T stream HBM/L2 -> LDS (buffer_load ... lds) while
-//    the current chunk computes; the chain wave reads them from LDS with one
-//    16-byte read per lane and block.
+//  * deltaChunkScan, grid (value head, 16-column dv slice), 4 compute waves
+//    and an L2-warming wave. Wave w keeps rows [32 w, 32 w + 32) of the
+//    state slice S [dk x 16] in registers and computes token tile w of each
+//    chunk's Z and Y; S and Z pass between the waves through LDS, two
+//    barriers per chunk. Every product runs on v_mfma_f32_16x16x32_f16,
+//    with the state (and Z) as the B operand straight from the C-layout
+//    registers of the product that made it: the k index of an operand block
+//    is permuted (sigma below) so that the 8 halves a lane supplies are the
+//    8 rows it holds in two consecutive 16-row C tiles; the A operands (Wn,
+//    Q', K^T) were written by the prep with the same permutation. Each wave
+//    loads its own operand blocks one chunk ahead into registers.
 //
 // Split form: x = hi + lo 2^-11 with hi = fp16(x), lo = fp16((x - hi) 2^11),
 // a.b ~ ah.bh + (ah.bl + al.bh) 2^-11, the cross terms in a second fp32
@@ -95,21 +94,25 @@ constexpr int kBlk = 64 * 8;
 constexpr int kPieceBlocks = 16;
 constexpr int kPieceHalves = 2 * kPieceBlocks * kBlk;
 constexpr int kPieceBytes = kPieceHalves * 2;      // 32 KiB
-constexpr int kPieceLoads = kPieceBytes / 1024;    // 16-byte-per-lane loads of a piece
 constexpr int kBufferWord3 = 0x00020000;           // gfx9 raw buffer descriptor, dword 3
 typedef __attribute__((address_space(3))) void lds_void_t;
 
-// Workspace. Per (chunk, value head) a record: the Wn piece, the Q' piece,
-// then Z0 and Y0 as fp32 in C-layout register order, per 16-column slice js
-// and 16-row tile m a 64-lane block of float4 (block 4 js + m), then 64
-// floats of scalars (e^(g_C) first). After all records, per (chunk, key
-// head) the K^T piece.
+// Workspace. Per (chunk, value head) a record: the Wn piece (hi and lo),
+// the Q' piece (plain fp16: the 16 hi blocks only, Q' feeds the outputs
+// alone), then Z0 and Y0 as fp32 in C-layout register order, per 16-column
+// slice js and 16-row tile m a 64-lane block of float4 (block 4 js + m),
+// then 64 floats of scalars (e^(g_C) first). After all records, per (chunk,
+// key head) the K^T piece.
 constexpr int kScalarBytes = 256;
-__host__ __device__ inline size_t rec_bytes(unsigned DV) {
-  return 2 * (size_t)kPieceBytes + 2 * (size_t)C * DV * sizeof(float) + kScalarBytes;
+constexpr int kQPieceBytes = kPieceBlocks * kBlk * 2; // 16 KiB
+__host__ __device__ inline size_t rec_z0(unsigned) {
+  return (size_t)kPieceBytes + kQPieceBytes;
 }
 __host__ __device__ inline size_t rec_scalars(unsigned DV) {
-  return 2 * (size_t)kPieceBytes + 2 * (size_t)C * DV * sizeof(float);
+  return rec_z0(DV) + 2 * (size_t)C * DV * sizeof(float);
+}
+__host__ __device__ inline size_t rec_bytes(unsigned DV) {
+  return rec_scalars(DV) + kScalarBytes;
 }
 __device__ __forceinline__ char *rec_ptr(void *ws, size_t recB, size_t Hv, size_t c,
                                          size_t h) {
@@ -287,7 +290,7 @@ __global__ __launch_bounds__(256, 1) void delta_prep_kernel(
         sum = sumsq8(x[c8], sum);
       sFac[tid] = l2_row_factor(sum, eps, isq ? qscale : 1.0f);
     }
-    __syncthreads();
+    lds_sync();
 #pragma unroll
     for (int hf = 0; hf < 2; ++hf)
 #pragma unroll
@@ -338,7 +341,7 @@ __global__ __launch_bounds__(256, 1) void delta_prep_kernel(
       *reinterpret_cast<half4_t *>(sQV + t * KS + d4) = qhi;
     }
   }
-  __syncthreads();
+  lds_sync();
 
   // The K^T piece of this (chunk, key head): block b = 2i + kb, lane (g, L)
   // element e = K[32 kb + sigma(g, e)][16 i + L].
@@ -374,7 +377,7 @@ __global__ __launch_bounds__(256, 1) void delta_prep_kernel(
   for (unsigned hr = 0; hr < R; ++hr) {
     const unsigned h = kh * R + hr;
     char *const rec = rec_ptr(ws, recB, Hv, c, h);
-    __syncthreads(); // the previous head is done with every LDS buffer
+    lds_sync(); // the previous head is done with every LDS buffer
 
     // Cumulative log decay (double) and beta (padding tokens: decay 1,
     // beta 0), e^(g_t), e^(g_C - g_t) and e^(g_C); V of the head's first
@@ -406,7 +409,7 @@ __global__ __launch_bounds__(256, 1) void delta_prep_kernel(
       if (DV <= VB)
         fetch_v(h + 1, 0, w0);
     }
-    __syncthreads();
+    lds_sync();
 
     // A (fp32) and M (hi/lo) from the Gram registers:
     // A[t][s] = beta_t e^(g_t - g_s) k_t.k_s (s < t), M[t][s] = e^(g_t - g_s)
@@ -427,7 +430,7 @@ __global__ __launch_bounds__(256, 1) void delta_prep_kernel(
           split_f16(e * qk[mt][r], sMh[t * CS + s], sMl[t * CS + s]);
         }
     }
-    __syncthreads();
+    lds_sync();
 
     // T = (I + A)^-1 into sTT[s][t] = T[t][s], on 16x16 blocks. The
     // diagonal blocks D_i = (I + A_ii)^-1 by forward substitution (wave i,
@@ -449,7 +452,7 @@ __global__ __launch_bounds__(256, 1) void delta_prep_kernel(
       for (int t = 0; t < 16; ++t)
         sTT[(b0 + j) * FS + b0 + t] = col[t];
     }
-    __syncthreads();
+    lds_sync();
     for (unsigned i = 1; i < 4; ++i) {
       if (wave < i) {
         const unsigned jb = wave;
@@ -476,7 +479,7 @@ __global__ __launch_bounds__(256, 1) void delta_prep_kernel(
         for (int r = 0; r < 4; ++r)
           sTT[(16 * jb + L) * FS + 16 * i + 4 * g + r] = res[r];
       }
-      __syncthreads();
+      lds_sync();
     }
 
     // T_w^T[s][t] = beta_s e^(g_s) T[t][s] and T_b^T[s][t] = beta_s T[t][s],
@@ -503,7 +506,7 @@ __global__ __launch_bounds__(256, 1) void delta_prep_kernel(
         *reinterpret_cast<half4_t *>(sTbl + o) = bl;
       }
     }
-    __syncthreads();
+    lds_sync();
 
     // N^T = T_w^T M^T (N = M T diag(beta e^g)); -N to LDS as [t][s] hi/lo.
     // Wave w: s rows [16 w, 16 w + 16), all four t tiles.
@@ -536,7 +539,7 @@ __global__ __launch_bounds__(256, 1) void delta_prep_kernel(
         *reinterpret_cast<half4_t *>(sNl + o) = nl;
       }
     }
-    __syncthreads();
+    lds_sync();
 
     // Wn and Q' pieces: W^T = K^T T_w^T and Q'^T = e^g Q^T - K^T N^T share
     // the K^T operand. Wave w writes the blocks (m, kb = w): tiles d = 2w,
@@ -606,7 +609,7 @@ __global__ __launch_bounds__(256, 1) void delta_prep_kernel(
         for (int u = 0; u < 2; ++u) {
           const int mt = 2 * mp + u;
           const float ez = sEz[16 * mt + L];
-          half8_t wh, wl, qh, ql;
+          half8_t wh, wl, qh;
 #pragma unroll
           for (int hf = 0; hf < 2; ++hf)
 #pragma unroll
@@ -615,15 +618,12 @@ __global__ __launch_bounds__(256, 1) void delta_prep_kernel(
               split_f16(-ez * (wa[u][hf][r] + wx[u][hf][r] * kSplitUnscale), a, b);
               wh[4 * hf + r] = a;
               wl[4 * hf + r] = b;
-              split_f16(qa[u][hf][r] + qx[u][hf][r] * kSplitUnscale, a, b);
-              qh[4 * hf + r] = a;
-              ql[4 * hf + r] = b;
+              qh[4 * hf + r] = (half_t)(qa[u][hf][r] + qx[u][hf][r] * kSplitUnscale);
             }
           const unsigned o = (4 * mt + wave) * kBlk + 8 * lane;
           *reinterpret_cast<half8_t *>(wp + o) = wh;
           *reinterpret_cast<half8_t *>(wp + kPieceBlocks * kBlk + o) = wl;
           *reinterpret_cast<half8_t *>(qp + o) = qh;
-          *reinterpret_cast<half8_t *>(qp + kPieceBlocks * kBlk + o) = ql;
         }
       }
     }
@@ -650,16 +650,16 @@ __global__ __launch_bounds__(256, 1) void delta_prep_kernel(
 #pragma unroll
         for (int r = 0; r < 4; ++r)
           ezr[mt][r] = sEz[16 * mt + 4 * g + r];
-      float4_t *const z0 = reinterpret_cast<float4_t *>(rec + 2 * kPieceBytes);
+      float4_t *const z0 = reinterpret_cast<float4_t *>(rec + rec_z0(DV));
       float4_t *const y0 = z0 + (size_t)C * DV / 4;
       for (unsigned jb = 0; jb < DV; jb += VB) {
         const unsigned w = min((unsigned)VB, DV - jb);
         if (jb > 0) {
           // Further dv blocks (DV > VB) are fetched here, in turn.
           fetch_v(h, jb, w);
-          __syncthreads();
+          lds_sync();
           store_v(w);
-          __syncthreads();
+          lds_sync();
         }
 #pragma unroll 1
         for (unsigned jt = wave; jt < w / 16; jt += 4) {
@@ -716,67 +716,37 @@ __global__ __launch_bounds__(256, 1) void delta_prep_kernel(
 
 // --------------------------------------------------------------- scan
 
-// Direct HBM/L2 -> LDS loads (buffer_load_dwordx4 ... lds), issued from
-// inline assembly so that the compiler neither waits for them nor reorders
-// LDS accesses across them ("memory" clobber): the scan orders them itself.
-// Each load moves 16 bytes per lane, lane i's bytes landing at M0 + 16 i.
-typedef __attribute__((address_space(3))) char lds_char_t;
-typedef int int4v_t __attribute__((ext_vector_type(4)));
+// The scan workgroup: 4 waves, one per SIMD, for one (value head, 16-column
+// dv slice). Wave w owns rows [32 w, 32 w + 32) of the slice's state (C
+// tiles 2w and 2w + 1, in its registers for the whole call) and token tile
+// w (rows [16 w, 16 w + 16)) of each chunk's Z and Y. Per chunk:
+//   1. every wave splits its state rows into the hi/lo B operand of k block
+//      w and puts it in LDS; barrier X1; every wave reads the whole split S;
+//   2. Z_w = Z0_w + sum_kb Wn[w][kb] S[kb], Y_w = Y0_w + sum_kb Q'[w][kb] S[kb];
+//   3. Z_w, split, to LDS; barrier X2; every wave reads the split Z;
+//   4. S_w <- e^(g_C) S_w + sum_kb K^T[w][kb] Z[kb] (the two C tiles of w).
+// The chain of a chunk is thus 12 + 12 MFMAs per wave instead of 48 + 48 on
+// one wave. Each wave loads exactly the operand blocks it multiplies (a
+// quarter of each piece, 88 KB per workgroup and chunk), one chunk ahead,
+// straight into its registers. A fifth wave keeps those loads L2 hits: the
+// pieces come from HBM / the MALL (the prep wrote them), ~3,500 cycles away
+// under this load against ~1,900 cycles of work per chunk, so it reads one
+// dword per 128-byte line of its workgroup's share of the record and K^T
+// piece of chunk c + kWarmAhead (the slice workgroups of a value head share
+// an XCD, and split the head's lines between them). Its loads count on its
+// own vmcnt, so the compute waves' waits never cover them. No wave issues a global store inside the
+// chunk loop -- the Y tiles go to an LDS stage that is written out every
+// kStageChunks chunks and at the end -- so a wave's only outstanding
+// vector-memory operations are those loads, which complete in order: the
+// wait for one chunk's operands then never drains the next chunk's (with a
+// store pending the compiler's wait would be vmcnt(0)).
+constexpr int kStageChunks = 32;
+constexpr int kAhead = 1;      // chunks of operands in flight in registers
+constexpr int kWarmAhead = 3;  // chunks ahead that the warming wave reads
+constexpr int kWarmSets = 8;   // its register sets (a touch is consumed kWarmSets chunks later)
+constexpr int kScanThreads = 320;
 
-__device__ __forceinline__ int4v_t buffer_rsrc(const void *base, unsigned bytes) {
-  const uint64_t a = reinterpret_cast<uint64_t>(base);
-  return int4v_t{__builtin_amdgcn_readfirstlane((int)(uint32_t)a),
-                 __builtin_amdgcn_readfirstlane((int)((uint32_t)(a >> 32) & 0xFFFFu)),
-                 (int)bytes, kBufferWord3};
-}
-__device__ __forceinline__ unsigned lds_addr(const void *p) {
-  return (unsigned)(uintptr_t)(const lds_char_t *)p;
-}
-// M0 is reserved to the compiler; it keeps nothing in it across these
-// statements in this file, and the clobber tells it M0 changes.
-#pragma clang diagnostic ignored "-Winline-asm"
-__device__ __forceinline__ void load_lds_1k(int4v_t rsrc, unsigned ldsDst, unsigned voff,
-                                            unsigned soff) {
-  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
-               :
-               : "s"(__builtin_amdgcn_readfirstlane(ldsDst)), "v"(voff), "s"(rsrc),
-                 "s"(__builtin_amdgcn_readfirstlane(soff))
-               : "memory", "m0");
-}
-__device__ __forceinline__ void load_lds_256(int4v_t rsrc, unsigned ldsDst, unsigned voff) {
-  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dword %1, %2, 0 offen lds"
-               :
-               : "s"(__builtin_amdgcn_readfirstlane(ldsDst)), "v"(voff), "s"(rsrc)
-               : "memory", "m0");
-}
-// Wait until this wave's LDS reads have returned (before a barrier after
-// which their buffer is reloaded).
-__device__ __forceinline__ void wait_lds_reads() { __builtin_amdgcn_s_waitcnt(0xC07F); }
-// Wait until at most N of this wave's vector-memory operations are
-// outstanding (they complete in order).
-template <int N> __device__ __forceinline__ void wait_vm() {
-  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
-  __builtin_amdgcn_s_waitcnt(0x0F70 | (N & 15) | ((N >> 4) << 14));
-}
-// Workgroup barrier that the compiler moves no memory access across; no
-// wait attached (each wave waits for exactly what it must beforehand).
-__device__ __forceinline__ void barrier() { asm volatile("s_barrier" ::: "memory"); }
-
-// The scan workgroup, 4 waves on the 4 SIMDs of one CU:
-//   wave 0 (chain): the state recursion Z = Z0 + Wn S, S <- e^(g_C) S + K^T Z;
-//   wave 1 (output): Y = Y0 + Q' S from the split S that wave 0 leaves in
-//           LDS, with Q' and Y0 loaded straight into its registers;
-//   waves 2-3 (loaders): the Wn, K^T pieces and Z0 (+ scalars) of the next
-//           chunk, direct to LDS, double-buffered.
-// A wave moves at most ~16 bytes per cycle through direct-to-LDS loads
-// (measured: ~38 GB/s per wave whether the data sits in L2 or in HBM,
-// scaling with the number of waves), so the chain wave issues none.
-constexpr int kLoaders = 2;
-constexpr int kPartLoads = kPieceLoads / kLoaders;  // 16 KiB of a piece per loader
-constexpr int kZLoads = 4 / kLoaders + 1;            // Z0 blocks + the scalars
-constexpr int kWLoads = kPartLoads + kZLoads;
-
-__global__ __launch_bounds__(256, 1) void delta_scan_kernel(
+__global__ __launch_bounds__(kScanThreads, 1) void delta_scan_kernel(
     float *__restrict__ state, half_t *__restrict__ out, const void *__restrict__ ws,
     unsigned T, unsigned Hk, unsigned Hv, unsigned DV) {
   // Workgroups are dealt to the 8 XCDs round-robin by block index. Give
@@ -786,253 +756,239 @@ __global__ __launch_bounds__(256, 1) void delta_scan_kernel(
   const unsigned slices = DV / 16, nb = gridDim.x;
   const unsigned Lb = nb % 8 == 0 ? (blockIdx.x % 8) * (nb / 8) + blockIdx.x / 8 : blockIdx.x;
   const unsigned h = Lb / slices, js = Lb % slices, kh = h / (Hv / Hk);
-  const unsigned wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const unsigned lane = threadIdx.x & 63u, g = lane >> 4;
+  const unsigned w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const unsigned lane = threadIdx.x & 63u, g = lane >> 4, L = lane & 15u;
   const unsigned chunks = (T + C - 1) / C, last = chunks - 1;
   const size_t recB = rec_bytes(DV), vStride = (size_t)Hv * DV;
   void *const wsp = const_cast<void *>(ws);
 
-  // Chunk c uses buffer c % 2 of Wn, K^T and Z0; sS holds the split S of
-  // the current chunk for wave 1.
-  constexpr int PB = 2 * kPieceBlocks * 64; // half8s per piece
-  __shared__ half8_t sW0[PB], sW1[PB], sK0[PB], sK1[PB];
-  __shared__ float4_t sZ0[4 * 64 + 16], sZ1[4 * 64 + 16]; // Z0 blocks, scalars
-  __shared__ half8_t sS[8 * 64];                           // bh[4], bl[4]
+  __shared__ half8_t sSx[2][4][64]; // split S: [hi, lo][k block][lane]
+  __shared__ half8_t sZx[2][2][64]; // split Z: [hi, lo][k block][lane], tile 2kb | 2kb + 1
+  __shared__ __attribute__((aligned(16))) half_t sY[kStageChunks][C][16];
 
-  auto rec = [&](unsigned c) { return rec_ptr(wsp, recB, Hv, c, h); };
-  auto kp = [&](unsigned c) { return kpiece_ptr(wsp, recB, chunks, Hv, Hk, c, kh); };
-  const unsigned j = 16 * js + (lane & 15u);
-
-  // Per chunk c, barriers A(c) then B(c):
-  //   A(c): Wn, Z0 of c landed (buffer c % 2); wave 1 has read the previous
-  //         split S; the buffers of chunk c - 1 are free.
-  //   B(c): K^T of c landed; wave 0 has written this chunk's split S.
-  if (wave >= 2) {
-    const unsigned l = wave - 2;
-    auto load_part = [&](const char *src, const half8_t *dst) {
-      const int4v_t rsrc = buffer_rsrc(src, kPieceBytes);
+  // The operand blocks of wave w for one chunk.
+  struct Ops {
+    half8_t wn[2][4]; // Wn blocks (w, kb): [hi, lo][kb]
+    half8_t kt[2][4]; // K^T blocks (tile 2w + i, kb) at 2i + kb: [hi, lo][.]
+    half8_t qp[4];    // Q' blocks (w, kb)
+    float4_t z0, y0;  // tile w of the slice's Z0 and Y0
+    float eC;         // e^(g_C)
+  };
+  // The loads of one chunk's operands in three parts, which a step spreads
+  // over its phases: issued in one burst, the 88 KB of a workgroup's loads
+  // would hold each wave at its load instructions until the CU's memory
+  // pipeline took them (~57 bytes per cycle per CU from L2, measured),
+  // while its MFMAs wait behind them.
+  auto load_wn = [&](unsigned c, Ops &d) {
+    const char *r = rec_ptr(wsp, recB, Hv, c, h);
+    const half8_t *pw = reinterpret_cast<const half8_t *>(r) + 4 * w * 64 + lane;
 #pragma unroll
-      for (int it = 0; it < kPartLoads; ++it) {
-        const unsigned kib = kPartLoads * l + it;
-        load_lds_1k(rsrc, lds_addr(dst) + 1024 * kib, 16 * lane, 1024 * kib);
-      }
-    };
-    auto load_w = [&](unsigned c, const half8_t *dW, const float4_t *dZ) {
-      const char *r = rec(c);
-      load_part(r, dW);
-      const char *z = r + 2 * kPieceBytes + (size_t)js * 4 * 64 * sizeof(float4_t);
-      const int4v_t rz = buffer_rsrc(z, 4 * 1024);
-#pragma unroll
-      for (int i = 0; i < kZLoads - 1; ++i) {
-        const unsigned blk = (kZLoads - 1) * l + i;
-        load_lds_1k(rz, lds_addr(dZ + 64 * blk), 16 * lane, 1024 * blk);
-      }
-      load_lds_256(buffer_rsrc(r + rec_scalars(DV), kScalarBytes), lds_addr(dZ + 4 * 64),
-                   4 * lane);
-    };
-    load_w(0, sW0, sZ0);
-    load_part(kp(0), sK0);
-    wait_vm<kPartLoads>(); // Wn, Z0 of 0
-    for (unsigned c = 0; c < chunks; ++c) {
-      barrier(); // A(c)
-      const unsigned cn = min(c + 1, last);
-      if (c % 2 == 0) {
-        load_w(cn, sW1, sZ1);
-        load_part(kp(cn), sK1);
-      } else {
-        load_w(cn, sW0, sZ0);
-        load_part(kp(cn), sK0);
-      }
-      wait_vm<kWLoads + kPartLoads>(); // K^T of c
-      barrier(); // B(c)
-      wait_vm<kPartLoads>(); // Wn, Z0 of c + 1
+    for (int b = 0; b < 4; ++b) {
+      d.wn[0][b] = pw[b * 64];
+      d.wn[1][b] = pw[(kPieceBlocks + b) * 64];
     }
-    wait_vm<0>();
-    return;
-  }
+  };
+  auto load_kt = [&](unsigned c, Ops &d) {
+    const half8_t *pk =
+        reinterpret_cast<const half8_t *>(kpiece_ptr(wsp, recB, chunks, Hv, Hk, c, kh)) +
+        4 * w * 64 + lane;
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      d.kt[0][b] = pk[b * 64];
+      d.kt[1][b] = pk[(kPieceBlocks + b) * 64];
+    }
+  };
+  auto load_qz = [&](unsigned c, Ops &d) {
+    const char *r = rec_ptr(wsp, recB, Hv, c, h);
+    const half8_t *pq = reinterpret_cast<const half8_t *>(r + kPieceBytes) + 4 * w * 64 + lane;
+#pragma unroll
+    for (int b = 0; b < 4; ++b)
+      d.qp[b] = pq[b * 64];
+    const float4_t *pz =
+        reinterpret_cast<const float4_t *>(r + rec_z0(DV)) + (4 * js + w) * 64 + lane;
+    d.z0 = pz[0];
+    d.y0 = pz[(size_t)C * DV / 4];
+    d.eC = *reinterpret_cast<const float *>(r + rec_scalars(DV));
+  };
+  auto load_ops = [&](unsigned c, Ops &d) {
+    load_wn(c, d);
+    load_kt(c, d);
+    load_qz(c, d);
+  };
 
-  if (wave == 1) {
-    // Q' (32 blocks) and Y0 (4 blocks) of a chunk, into registers.
-    struct QY {
-      half8_t q[2][kPieceBlocks];
-      float4_t y[4];
+  // Chunks [c0, c] of the stage to the output rows (two 16-byte stores per
+  // 16-column row; rows past the end of the tokens are skipped).
+  auto flush = [&](unsigned c) {
+    const unsigned c0 = c - c % kStageChunks, rows = (c - c0 + 1) * C;
+    for (unsigned i = threadIdx.x; i < 2 * rows; i += 256) { // waves 0-3
+      const unsigned rr = i >> 1, hf = i & 1u, t = c0 * C + rr;
+      if (t < T)
+        *reinterpret_cast<uint4_t *>(out + (size_t)t * vStride + (size_t)h * DV + 16 * js +
+                                     8 * hf) =
+            *reinterpret_cast<const uint4_t *>(&sY[rr / C][rr % C][8 * hf]);
+    }
+  };
+
+  if (w == 4) {
+    // The warming wave: this workgroup's share of a chunk is recPart bytes
+    // of each record (Wn, Q', Z0, Y0, scalars) and kPart bytes of the K^T
+    // piece; it reads one dword per line of the first 16 KiB of the former
+    // and 8 KiB of the latter (all of both at dv = 128). A touched value is
+    // consumed kWarmSets chunks later (the loop is unrolled over the register
+    // sets), long after it came, so the wave never waits on its loads.
+    const unsigned R = Hv / Hk;
+    const size_t recPart = (recB + slices - 1) / slices;
+    const size_t kShare = (size_t)R * slices;
+    const size_t kPart = ((size_t)kPieceBytes + kShare - 1) / kShare;
+    const size_t kIdx = (size_t)(h % R) * slices + js;
+    const size_t r0 = js * recPart, r1 = min(r0 + recPart, recB) - 4;
+    const size_t k0 = kIdx * kPart, k1 = min(k0 + kPart, (size_t)kPieceBytes) - 4;
+    // (The empty asm reading a register set is its consumption: the
+    // compiler waits for those loads there, in program order, and cannot
+    // hoist an arithmetic use of them ahead of the barriers.) Chunk x's
+    // touch goes to register set x % kWarmSets.
+    float4_t tv[kWarmSets];
+#pragma unroll
+    for (int u = 0; u < kWarmSets; ++u)
+      tv[u] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    auto touch = [&](unsigned c, float4_t &v) {
+      asm volatile("" ::"v"(v[0]), "v"(v[1]), "v"(v[2]));
+      const char *r = rec_ptr(wsp, recB, Hv, c, h);
+      const char *k = kpiece_ptr(wsp, recB, chunks, Hv, Hk, c, kh);
+      v[0] = *reinterpret_cast<const float *>(r + (min(r0 + 128 * lane, r1) & ~(size_t)3));
+      v[1] = *reinterpret_cast<const float *>(r + (min(r0 + 8192 + 128 * lane, r1) & ~(size_t)3));
+      v[2] = *reinterpret_cast<const float *>(k + (min(k0 + 128 * lane, k1) & ~(size_t)3));
     };
-    auto load_qy = [&](unsigned c, QY &d) {
-      const char *r = rec(c);
-      const half8_t *qp = reinterpret_cast<const half8_t *>(r + kPieceBytes) + lane;
 #pragma unroll
-      for (int b = 0; b < kPieceBlocks; ++b) {
-        d.q[0][b] = qp[b * 64];
-        d.q[1][b] = qp[(kPieceBlocks + b) * 64];
-      }
-      const float4_t *yp = reinterpret_cast<const float4_t *>(r + 2 * kPieceBytes) +
-                           (size_t)C * DV / 4 + js * 4 * 64 + lane;
-#pragma unroll
-      for (int m = 0; m < 4; ++m)
-        d.y[m] = yp[m * 64];
-    };
-    auto ystep = [&](unsigned c, const QY &cur, QY &nxt) {
-      const unsigned t0 = c * C, n = min((unsigned)C, T - t0);
-      barrier(); // A(c)
-      barrier(); // B(c)
-      half8_t bh[4], bl[4];
-#pragma unroll
-      for (int kb = 0; kb < 4; ++kb) {
-        bh[kb] = sS[kb * 64 + lane];
-        bl[kb] = sS[(4 + kb) * 64 + lane];
-      }
-      wait_lds_reads();
-      load_qy(min(c + 1, last), nxt);
-      float4_t ya[4], yx[4];
-#pragma unroll
-      for (int m = 0; m < 4; ++m) {
-        ya[m] = cur.y[m];
-        yx[m] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
-      }
-#pragma unroll
-      for (int kb = 0; kb < 4; ++kb) {
-#pragma unroll
-        for (int m = 0; m < 4; ++m)
-          ya[m] = mfma16(cur.q[0][4 * m + kb], bh[kb], ya[m]);
-#pragma unroll
-        for (int m = 0; m < 4; ++m)
-          yx[m] = mfma16(cur.q[0][4 * m + kb], bl[kb], yx[m]);
-#pragma unroll
-        for (int m = 0; m < 4; ++m)
-          yx[m] = mfma16(cur.q[1][4 * m + kb], bh[kb], yx[m]);
-      }
-      // Rows past the end of the tokens fall outside the descriptor and
-      // are dropped by the buffer stores.
-      const auto ro = __builtin_amdgcn_make_buffer_rsrc(
-          (void *)(out + (size_t)t0 * vStride + (size_t)h * DV), (short)0,
-          (int)(((n - 1) * vStride + DV) * sizeof(half_t)), kBufferWord3);
-#pragma unroll
-      for (int m = 0; m < 4; ++m)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const unsigned t = 16 * m + 4 * g + r;
-          const half_t y = (half_t)(ya[m][r] + yx[m][r] * kSplitUnscale);
-          __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(unsigned short, y), ro,
-                                                (unsigned)((t * vStride + j) * sizeof(half_t)),
-                                                0, 0);
-        }
-    };
-    QY qa, qb;
-    load_qy(0, qa);
+    for (int u = 1; u < kWarmAhead; ++u)
+      touch(min((unsigned)u, last), tv[u % kWarmSets]);
     unsigned c = 0;
-    for (; c + 1 < chunks; c += 2) {
-      ystep(c, qa, qb);
-      ystep(c + 1, qb, qa);
+    for (; c + kWarmSets <= chunks; c += kWarmSets) {
+#pragma unroll
+      for (int u = 0; u < kWarmSets; ++u) {
+        touch(min(c + u + kWarmAhead, last), tv[(u + kWarmAhead) % kWarmSets]);
+        lds_sync(); // X1
+        lds_sync(); // X2
+      }
     }
-    if (c < chunks)
-      ystep(c, qa, qb);
+    for (; c < chunks; ++c) {
+      lds_sync(); // X1
+      lds_sync(); // X2
+    }
+#pragma unroll
+    for (int u = 0; u < kWarmSets; ++u)
+      asm volatile("" ::"v"(tv[u][0]), "v"(tv[u][1]), "v"(tv[u][2]));
     return;
   }
 
-  // Wave 0: the state slice, register r of tile i holding S[16 i + 4 g + r][j].
-  float4_t S[8];
+  // State rows of wave w: register r of tile i holds S[32 w + 16 i + 4 g + r][j].
+  const unsigned j = 16 * js + L;
   float *const scol = state + (size_t)h * DK * DV + j;
+  float4_t S[2];
 #pragma unroll
-  for (int i = 0; i < 8; ++i)
+  for (int i = 0; i < 2; ++i)
 #pragma unroll
     for (int r = 0; r < 4; ++r)
-      S[i][r] = scol[(size_t)(16 * i + 4 * g + r) * DV];
+      S[i][r] = scol[(size_t)(32 * w + 16 * i + 4 * g + r) * DV];
 
-  auto step = [&](unsigned c, const half8_t *rW, const float4_t *rZ, const half8_t *rK) {
-    barrier(); // A(c)
-    // All of a product's A blocks are read before its first MFMA (the
-    // scheduler is kept from sinking the reads next to their uses, where
-    // each would expose the LDS latency), and the MFMAs of one k block go
-    // accumulator by accumulator so that no MFMA waits on the one before
-    // (a dependent 16x16x32 MFMA waits ~44 cycles, an independent one
-    // issues every ~18).
-    half8_t A[2][kPieceBlocks];
-#pragma unroll
-    for (int b = 0; b < kPieceBlocks; ++b) {
-      A[0][b] = rW[b * 64 + lane];
-      A[1][b] = rW[(kPieceBlocks + b) * 64 + lane];
+  // Chunk c multiplies `cur` and refills `dst` (the buffer of chunk c - 1)
+  // with chunk c + kAhead.
+  auto step = [&](unsigned c, const Ops &cur, Ops &dst) {
+    const unsigned cn = min(c + kAhead, last);
+    load_wn(cn, dst);
+    __builtin_amdgcn_sched_barrier(0);
+    // 1. The split S, through LDS.
+    {
+      half8_t hi, lo;
+      split8(S[0], S[1], hi, lo);
+      sSx[0][w][lane] = hi;
+      sSx[1][w][lane] = lo;
     }
-    const float eC = rZ[4 * 64][0];
-    float4_t za[4], zx[4];
-#pragma unroll
-    for (int m = 0; m < 4; ++m) {
-      za[m] = rZ[m * 64 + lane];
-      zx[m] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
-    }
-    // S as the B operand of its four 32-row k blocks, also left for wave 1.
+    lds_sync(); // X1
     half8_t bh[4], bl[4];
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb) {
-      split8(S[2 * kb], S[2 * kb + 1], bh[kb], bl[kb]);
-      sS[kb * 64 + lane] = bh[kb];
-      sS[(4 + kb) * 64 + lane] = bl[kb];
+      bh[kb] = sSx[0][kb][lane];
+      bl[kb] = sSx[1][kb][lane];
     }
     __builtin_amdgcn_sched_barrier(0);
-    // Z = Z0 + Wn S.
+    load_kt(cn, dst);
+    __builtin_amdgcn_sched_barrier(0);
+    // 2. Z_w and Y_w: five accumulators, each MFMA five issues after the
+    // one it depends on (a dependent 16x16x32 MFMA waits ~44 cycles, an
+    // independent one issues every ~18).
+    float4_t za = cur.z0, zx{0.0f, 0.0f, 0.0f, 0.0f}, zy{0.0f, 0.0f, 0.0f, 0.0f};
+    float4_t ya = cur.y0, yx{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb) {
-#pragma unroll
-      for (int m = 0; m < 4; ++m)
-        za[m] = mfma16(A[0][4 * m + kb], bh[kb], za[m]);
-#pragma unroll
-      for (int m = 0; m < 4; ++m)
-        zx[m] = mfma16(A[0][4 * m + kb], bl[kb], zx[m]);
-#pragma unroll
-      for (int m = 0; m < 4; ++m)
-        zx[m] = mfma16(A[1][4 * m + kb], bh[kb], zx[m]);
+      za = mfma16(cur.wn[0][kb], bh[kb], za);
+      ya = mfma16(cur.qp[kb], bh[kb], ya);
+      zx = mfma16(cur.wn[0][kb], bl[kb], zx);
+      yx = mfma16(cur.qp[kb], bl[kb], yx);
+      zy = mfma16(cur.wn[1][kb], bh[kb], zy);
     }
-    wait_lds_reads();
-    barrier(); // B(c)
-
-    // S <- e^(g_C) S + K^T Z, Z as the B operand of its two k blocks.
+    // 3. The split Z tile w (halves 4 (w % 2) .. of k block w / 2), and the
+    // output tile to the stage.
+    {
+      half4_t hi, lo;
+      split4(za + (zx + zy) * kSplitUnscale, hi, lo);
+      reinterpret_cast<half4_t *>(&sZx[0][w >> 1][lane])[w & 1u] = hi;
+      reinterpret_cast<half4_t *>(&sZx[1][w >> 1][lane])[w & 1u] = lo;
+      const float4_t y = ya + yx * kSplitUnscale;
+      half_t *const sy = &sY[c % kStageChunks][16 * w + 4 * g][L];
 #pragma unroll
-    for (int b = 0; b < kPieceBlocks; ++b) {
-      A[0][b] = rK[b * 64 + lane];
-      A[1][b] = rK[(kPieceBlocks + b) * 64 + lane];
+      for (int r = 0; r < 4; ++r)
+        sy[16 * r] = (half_t)y[r];
     }
-    half8_t zbh[2], zbl[2];
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
-      split8(za[2 * kb] + zx[2 * kb] * kSplitUnscale,
-             za[2 * kb + 1] + zx[2 * kb + 1] * kSplitUnscale, zbh[kb], zbl[kb]);
-    float4_t sa[8], sx[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      sa[i] = S[i] * eC;
-      sx[i] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
-    }
-    __builtin_amdgcn_sched_barrier(0);
+    lds_sync(); // X2
+    half8_t zh[2], zl[2];
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
+      zh[kb] = sZx[0][kb][lane];
+      zl[kb] = sZx[1][kb][lane];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    load_qz(cn, dst);
+    __builtin_amdgcn_sched_barrier(0);
+    // 4. S_w <- e^(g_C) S_w + K^T Z.
+    float4_t sa[2], sx[2], sy[2];
 #pragma unroll
-      for (int i = 0; i < 8; ++i)
-        sa[i] = mfma16(A[0][2 * i + kb], zbh[kb], sa[i]);
-#pragma unroll
-      for (int i = 0; i < 8; ++i)
-        sx[i] = mfma16(A[0][2 * i + kb], zbl[kb], sx[i]);
-#pragma unroll
-      for (int i = 0; i < 8; ++i)
-        sx[i] = mfma16(A[1][2 * i + kb], zbh[kb], sx[i]);
+    for (int i = 0; i < 2; ++i) {
+      sa[i] = S[i] * cur.eC;
+      sx[i] = sy[i] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
     }
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
-      S[i] = sa[i] + sx[i] * kSplitUnscale;
-    wait_lds_reads();
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        sa[i] = mfma16(cur.kt[0][2 * i + kb], zh[kb], sa[i]);
+        sx[i] = mfma16(cur.kt[0][2 * i + kb], zl[kb], sx[i]);
+        sy[i] = mfma16(cur.kt[1][2 * i + kb], zh[kb], sy[i]);
+      }
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+      S[i] = sa[i] + (sx[i] + sy[i]) * kSplitUnscale;
+    // The stage's writes of this chunk were made before X2; its reads finish
+    // before the next X1 (lds_sync waits for them), ahead of any rewrite.
+    if (c % kStageChunks == kStageChunks - 1 || c == last)
+      flush(c);
   };
 
+  Ops oa, ob;
+  load_ops(0, oa);
   unsigned c = 0;
   for (; c + 1 < chunks; c += 2) {
-    step(c, sW0, sZ0, sK0);
-    step(c + 1, sW1, sZ1, sK1);
+    step(c, oa, ob);
+    step(c + 1, ob, oa);
   }
   if (c < chunks)
-    step(c, sW0, sZ0, sK0);
+    step(c, oa, ob);
 
 #pragma unroll
-  for (int i = 0; i < 8; ++i)
+  for (int i = 0; i < 2; ++i)
 #pragma unroll
     for (int r = 0; r < 4; ++r)
-      scol[(size_t)(16 * i + 4 * g + r) * DV] = S[i][r];
+      scol[(size_t)(32 * w + 16 * i + 4 * g + r) * DV] = S[i][r];
 }
 
 } // namespace
@@ -1060,7 +1016,7 @@ hipError_t launch_chunked(const void *q, const void *k, const uint16_t *v, const
   hipError_t e = hipGetLastError();
   if (e != hipSuccess)
     return e;
-  hipLaunchKernelGGL(delta_scan_kernel, dim3(s.Hv * (s.Dv / 16)), dim3(256), 0, stream, state,
+  hipLaunchKernelGGL(delta_scan_kernel, dim3(s.Hv * (s.Dv / 16)), dim3(kScanThreads), 0, stream, state,
                      reinterpret_cast<half_t *>(out), ws, s.T, s.Hk, s.Hv, s.Dv);
   return hipGetLastError();
 }

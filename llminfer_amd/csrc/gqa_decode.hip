@@ -162,12 +162,6 @@ __device__ __forceinline__ float wave_sum(float x) {
 
 struct NoRows {}; // the ungated kernels' (empty) row argument
 
-// LDS barrier: this wave's LDS accesses complete, then the workgroup
-// barrier. Unlike __syncthreads it does not wait for outstanding global
-// loads, so key loads issued before it stay in flight.
-__device__ __forceinline__ void lds_sync() {
-  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-}
 
 // The gated decode's row work for one workgroup (kv head kvh, token 0):
 // its G query rows through normRope into qv, and -- for the owner of the

@@ -16,6 +16,16 @@ typedef uint32_t uint4_t __attribute__((ext_vector_type(4)));
 
 constexpr float kLog2e = 1.4426950408889634f;
 
+// LDS barrier: this wave's LDS accesses complete, then the workgroup
+// barrier. Unlike __syncthreads it waits for no outstanding global load or
+// store, so loads issued before it stay in flight and stores keep draining
+// behind the next phase. For barriers that order LDS traffic only: a wave
+// reading global memory that another wave of the workgroup wrote before the
+// barrier needs __syncthreads (or its own waits).
+__device__ __forceinline__ void lds_sync() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
 // DPP lane permutations on one 16-lane row (gfx9 encodings).
 enum : int {
   kDppXor1 = 0xB1,        // quad_perm [1,0,3,2]
