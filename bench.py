@@ -789,6 +789,107 @@ class DeltaNormUpdate(Workload):
                 "gpu_vs_cpu_max_abs": err}
 
 
+def norm_delta_gated_bytes(T: int, hk: int, dk: int, hv: int, dv: int) -> int:
+    """The fused L2Norm -> DeltaUpdate -> GatedRmsNorm chain: the pair's
+    bytes plus the fp16 gate z and the fp32 norm weight (the un-normalised
+    rows never leave the kernel)."""
+    return norm_delta_bytes(T, hk, dk, hv, dv) + 2 * T * hv * dv + 4 * dv
+
+
+class DeltaGatedNorm(Workload):
+    """The L2Norm -> DeltaUpdate -> GatedRmsNorm chain of a DeltaNet layer
+    (Qwen35ModelBuilder.cpp:155-166) in one call
+    (llmi_hip_l2_norm_delta_gated_norm: the chunked scan normalises the
+    head's rows at its end, the decode kernel in its workgroup), next to the
+    same chain as the fused pair plus the standalone gatedRmsNorm launch.
+    Operand sets rotate past the MALL."""
+    bound = "hbm"
+    labels = ("fused", "unfused")
+    dominant = "fused"
+
+    def __init__(self, dev, T, sets, seed, hk=16, dk=128, hv=32, dv=128):
+        import numpy as np
+        import torch
+        from llminfer_amd import ops
+        self.T, self.sets, self.shape = T, sets, (hk, dk, hv, dv)
+        self.tokens = T
+        self.name = f"l2norm_delta_gatednorm_T{T}"
+        qs = float(np.float32(1.0) / np.sqrt(np.float32(dk)))
+        g = torch.Generator(device=dev).manual_seed(seed)
+        self.weight = (torch.randn((dv,), generator=g, device=dev) * 0.2 + 1.0)
+        self.x = []
+        for _ in range(sets):
+            _, _, v, beta, decay = _delta_inputs(g, dev, T, hk, dk, hv, dv)
+            x = dict(q16=_randn16(g, (T, hk * dk), dev), k16=_randn16(g, (T, hk * dk), dev),
+                     z=_randn16(g, (T, hv * dv), dev), v=v, beta=beta, decay=decay,
+                     s1=torch.randn((hv, dk, dv), generator=g, device=dev) * 0.1,
+                     o1=torch.empty_like(v), o2=torch.empty_like(v), o3=torch.empty_like(v))
+            x["s2"] = x["s1"].clone()
+            x["fused"] = ops.bind_l2_norm_delta_gated_norm(
+                x["q16"], x["k16"], v, beta, decay, x["s1"], x["z"], self.weight, x["o1"],
+                1e-6, qs, 1e-6)
+            x["unfused"] = [ops.bind_l2_norm_delta_update(x["q16"], x["k16"], v, beta, decay,
+                                                          x["s2"], x["o2"], 1e-6, qs),
+                            ops.bind_gated_rms_norm(x["o2"].view(T * hv, dv),
+                                                    x["z"].view(T * hv, dv), self.weight,
+                                                    x["o3"].view(T * hv, dv), 1e-6)]
+            self.x.append(x)
+        self.bytes = {"fused": norm_delta_gated_bytes(T, hk, dk, hv, dv),
+                      "unfused": norm_delta_gated_bytes(T, hk, dk, hv, dv)}
+
+    def op(self, label, i):
+        x = self.x[i % self.sets]
+        if label == "fused":
+            x["fused"]()
+        else:
+            for b in x["unfused"]:
+                b()
+
+    def kernels(self):
+        return self.x[0]["fused"].what
+
+    def work(self, i):
+        return self.bytes["fused"]
+
+    def config(self):
+        hk, dk, hv, dv = self.shape
+        return {"workload": self.name, "tokens": self.T, "key_heads": hk, "key_dim": dk,
+                "value_heads": hv, "value_dim": dv, "operand_sets": self.sets}
+
+    def cpu(self, budget_s):
+        import numpy as np
+        import oracle
+        import torch
+        hk, dk, hv, dv = self.shape
+        T = self.T
+        x = self.x[0]
+        torch.cuda.synchronize()
+        s0 = host_f32(x["s1"])
+        x["fused"]()
+        torch.cuda.synchronize()
+        gpu_out = host_u16(x["o1"])
+        q16, k16, v, z = (host_u16(x[n]) for n in ("q16", "k16", "v", "z"))
+        beta, decay, w = host_f32(x["beta"]), host_f32(x["decay"]), host_f32(self.weight)
+        qs = float(np.float32(1.0) / np.sqrt(np.float32(dk)))
+        thr = cpu_threads()
+
+        def run():
+            q = oracle.l2norm_f32(q16, dk, 1e-6, qs)
+            k = oracle.l2norm_f32(k16, dk, 1e-6, 1.0)
+            y, _ = oracle.delta_recurrent_f32(q, k, v, beta, decay, s0, thr)
+            return oracle.gated_rms_norm(y.reshape(T * hv, dv), z.reshape(T * hv, dv), w)
+
+        want = run()
+        err = float(np.max(np.abs(oracle.f16_to_f32(gpu_out).reshape(-1)
+                                  - oracle.f16_to_f32(want).reshape(-1))))
+        sec, runs = time_cpu(run, budget_s)
+        return {"value": sec * 1e6, "unit": "µs/layer", "cores": thr, "kind": "port",
+                "sample": f"L2Norm q, k + the {T}-token DeltaUpdate + gatedRmsNorm on one set, "
+                          f"{runs} runs (oracle orc_l2norm_f32 + orc_delta_recurrent_f32 + "
+                          "orc_gated_rms_norm)",
+                "gpu_vs_cpu_max_abs": err}
+
+
 class HybridDecode(Workload):
     """DeltaNet decode step + KvAppend + GQA decode at 32K context,
     32 positions per layer; `layers` independent layer pairs rotate so that
@@ -1088,6 +1189,8 @@ def main(argv=None) -> int:
                                                                       seed=13)),
             ("next_l2norm_delta_1024", lambda: DeltaNormUpdate(dev, 1024, 8, seed=10)),
             ("next_l2norm_delta_decode", lambda: DeltaNormUpdate(dev, 1, 128, seed=11)),
+            ("next_l2norm_delta_gatednorm_1024", lambda: DeltaGatedNorm(dev, 1024, 8, seed=12)),
+            ("next_l2norm_delta_gatednorm_decode", lambda: DeltaGatedNorm(dev, 1, 128, seed=13)),
         ]
         only = {k for k in args.only.split(",") if k}
         for key, make in builders:

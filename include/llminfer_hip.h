@@ -334,6 +334,28 @@ LLMI_HIP_API int llmi_hip_l2_norm_delta_update(const uint16_t *q, const uint16_t
                                                float epsilon, float q_scale, void *workspace,
                                                size_t workspace_bytes, void *stream);
 
+/* The L2Norm -> DeltaUpdate -> GatedRmsNorm chain of a DeltaNet layer in
+ * one call (Qwen35ModelBuilder.cpp:155-166: the two L2Norms, DeltaUpdate,
+ * then GatedRmsNorm(mixed, z, norm.weight, epsilon); gatedRmsNorm,
+ * Reference.metal:228-259, dispatched at MetalReferenceGraph.mm:298-303).
+ * q, k, v, beta, decay, state and the workspace as
+ * llmi_hip_l2_norm_delta_update; gate is z, fp16 [T][Hv*dv]; norm_weight is
+ * fp32 [dv]; out receives the normalised rows, fp16 [T][Hv*dv], bit for
+ * bit what llmi_hip_l2_norm_delta_update followed by
+ * llmi_hip_gated_rms_norm(out, gate, norm_weight, rows T*Hv, width dv,
+ * norm_epsilon) leave there, without the round trip of the un-normalised
+ * rows. Shapes: dk 128 and T >= 32 (the chunked form, whose scan
+ * normalises the rows at its end once all Hv * dv / 16 of its workgroups
+ * have arrived: out and gate 16-byte aligned, and the grid must fit on the
+ * device at once -- 512 workgroups on MI355X), or dk 64 / 128, dv 64 / 128
+ * and T <= 32 (one workgroup per value head); others return
+ * LLMI_HIP_UNSUPPORTED. */
+LLMI_HIP_API int llmi_hip_l2_norm_delta_gated_norm(
+    const uint16_t *q, const uint16_t *k, const uint16_t *v, const float *beta,
+    const float *decay, float *state, const uint16_t *gate, const float *norm_weight,
+    uint16_t *out, GraphDeltaParams p, float qk_epsilon, float q_scale, float norm_epsilon,
+    void *workspace, size_t workspace_bytes, void *stream);
+
 /* ----------------------------------------------------------------- helpers */
 
 /* Zero a workspace (enqueued on `stream`). No kernel of this library needs

@@ -127,6 +127,9 @@ SIGNATURES = {
     "llmi_hip_delta_workspace_bytes": (_SZ, [GraphDeltaParams]),
     "llmi_hip_l2_norm_delta_update": (C.c_int, [_P, _P, _P, _P, _P, _P, _P, GraphDeltaParams,
                                                 C.c_float, C.c_float, _P, _SZ, _P]),
+    "llmi_hip_l2_norm_delta_gated_norm": (C.c_int, [_P, _P, _P, _P, _P, _P, _P, _P, _P,
+                                                    GraphDeltaParams, C.c_float, C.c_float,
+                                                    C.c_float, _P, _SZ, _P]),
     "llmi_hip_workspace_init": (C.c_int, [_P, _SZ, _P]),
     "llmi_hip_dispatch_count": (C.c_uint, [C.c_int, _P]),
     "llmi_hip_kernel_name": (C.c_char_p, [C.c_int, _P, C.c_uint]),

@@ -502,6 +502,49 @@ int llmi_hip_l2_norm_delta_update(const uint16_t *q, const uint16_t *k, const ui
               p.keyDim, p.valueDim);
 }
 
+int llmi_hip_l2_norm_delta_gated_norm(const uint16_t *q, const uint16_t *k, const uint16_t *v,
+                                      const float *beta, const float *decay, float *state,
+                                      const uint16_t *gate, const float *norm_weight,
+                                      uint16_t *out, GraphDeltaParams p, float qk_epsilon,
+                                      float q_scale, float norm_epsilon, void *workspace,
+                                      size_t workspace_bytes, void *stream) {
+  if (int st = check_delta(p))
+    return st;
+  if (!q || !k || !v || !beta || !decay || !state || !gate || !norm_weight || !out)
+    return fail(LLMI_HIP_INVALID_ARGUMENT, "L2Norm+DeltaUpdate+GatedRmsNorm: null buffer");
+  DeltaShape s{p.tokens, p.keyHeads, p.keyDim, p.valueHeads, p.valueDim};
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (select_delta(p) == DeltaKernel::Chunked) {
+    // The scan's norm reads and writes 16-byte row pieces of out and gate.
+    if ((reinterpret_cast<uintptr_t>(out) | reinterpret_cast<uintptr_t>(gate)) & 15u)
+      return fail(LLMI_HIP_UNSUPPORTED,
+                  "L2Norm+DeltaUpdate+GatedRmsNorm: out and gate must be 16-byte aligned");
+    size_t need = delta_chunked_workspace_bytes(s);
+    if (!workspace || workspace_bytes < need)
+      return fail(LLMI_HIP_WORKSPACE,
+                  "L2Norm+DeltaUpdate+GatedRmsNorm: chunked form needs a %zu-byte workspace",
+                  need);
+    if (!delta_chunked_norm_resident(s))
+      return fail(LLMI_HIP_UNSUPPORTED,
+                  "L2Norm+DeltaUpdate+GatedRmsNorm: %u x %u scan workgroups do not fit on the "
+                  "device at once",
+                  p.valueHeads, p.valueDim / 16);
+    return launched(launch_delta_chunked_gated_norm(q, k, v, beta, decay, state, gate,
+                                                    norm_weight, out, workspace, qk_epsilon,
+                                                    q_scale, norm_epsilon, s, st),
+                    "deltaChunkedWy+gatedRmsNorm");
+  }
+  if (delta_recurrent_norm_supported(s))
+    return launched(launch_delta_recurrent_gated_norm(q, k, v, beta, decay, state, gate,
+                                                      norm_weight, out, qk_epsilon, q_scale,
+                                                      norm_epsilon, s, st),
+                    "deltaRecurrent+gatedRmsNorm");
+  return fail(LLMI_HIP_UNSUPPORTED,
+              "L2Norm+DeltaUpdate+GatedRmsNorm: T %u, dk %u, dv %u have no fused kernel "
+              "(chunked: dk 128, T >= 32; recurrent: dk 64 or 128, dv 64 or 128, T <= %u)",
+              p.tokens, p.keyDim, p.valueDim, kRecNormMaxT);
+}
+
 int llmi_hip_workspace_init(void *workspace, size_t bytes, void *stream) {
   if (!bytes)
     return LLMI_HIP_OK;

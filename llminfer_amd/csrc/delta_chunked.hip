@@ -60,6 +60,7 @@
 // only ~1e-3 absolute precision. Only non-positive differences are
 // exponentiated.
 #include "exact_fp.hpp"
+#include "gated_norm.hpp"
 #include "hip_common.hpp"
 #include "kernels.hpp"
 
@@ -198,7 +199,7 @@ template <bool QK16>
 __global__ __launch_bounds__(256, 1) void delta_prep_kernel(
     const void *__restrict__ qp, const void *__restrict__ kp, const half_t *__restrict__ v,
     const float *__restrict__ beta, const float *__restrict__ decay, void *__restrict__ ws,
-    unsigned T, unsigned Hk, unsigned Hv, unsigned DV, float eps, float qscale) {
+    unsigned T, unsigned Hk, unsigned Hv, unsigned DV, float eps, float qscale, unsigned *cnt) {
   const float *q = static_cast<const float *>(qp), *k = static_cast<const float *>(kp);
   const half_t *q16 = static_cast<const half_t *>(qp), *k16 = static_cast<const half_t *>(kp);
   const unsigned c = blockIdx.x, kh = blockIdx.y;
@@ -208,6 +209,10 @@ __global__ __launch_bounds__(256, 1) void delta_prep_kernel(
   const unsigned g = lane >> 4, L = lane & 15u;
   const size_t recB = rec_bytes(DV);
   const size_t qkStride = (size_t)Hk * DK, vStride = (size_t)Hv * DV;
+  // The fused norm's per-value-head arrival records (4 words each), zeroed
+  // here (the scan runs after this launch on the same stream).
+  if (cnt && c == 0 && tid < 4 * R)
+    cnt[4 * kh * R + tid] = 0;
 
   __shared__ __attribute__((aligned(16))) half_t sKh[C * KS], sKl[C * KS];
   __shared__ __attribute__((aligned(16))) half_t sQV[C * KS]; // Q hi, later a V block
@@ -746,9 +751,23 @@ constexpr int kWarmAhead = 3;  // chunks ahead that the warming wave reads
 constexpr int kWarmSets = 8;   // its register sets (a touch is consumed kWarmSets chunks later)
 constexpr int kScanThreads = 320;
 
+// With NORM the kernel ends with gatedRmsNorm over the value head's output
+// rows (Reference.metal:228-259): once every slice workgroup of the head has
+// written its columns (a per-head arrival counter, zeroed by the prep; the
+// host launches it only when the whole grid fits on the device at once, so
+// every workgroup is resident and the wait ends; it is bounded regardless),
+// workgroup js normalises rows [js p, js p + p) of the head, p = ceil(T /
+// slices), in place: the sequential sum of squares of each row, then out =
+// fp16(fp16(x * factor) * weight * silu(gate)) per element (gated_norm.hpp,
+// the arithmetic of the standalone kernel).
+constexpr unsigned kSpinLimit = 1u << 22; // bound of the arrival wait (~0.3 s)
+constexpr unsigned kNormMaxDv = 256; // dv the fused norm supports
+
+template <bool NORM>
 __global__ __launch_bounds__(kScanThreads, 1) void delta_scan_kernel(
     float *__restrict__ state, half_t *__restrict__ out, const void *__restrict__ ws,
-    unsigned T, unsigned Hk, unsigned Hv, unsigned DV) {
+    unsigned T, unsigned Hk, unsigned Hv, unsigned DV, const half_t *__restrict__ gate,
+    const float *__restrict__ nweight, unsigned *cnt, float neps) {
   // Workgroups are dealt to the 8 XCDs round-robin by block index. Give
   // each XCD a contiguous run of (value head, slice) pairs, so that the
   // workgroups reading one value head's pieces and one key head's K^T piece
@@ -878,8 +897,7 @@ __global__ __launch_bounds__(kScanThreads, 1) void delta_scan_kernel(
 #pragma unroll
     for (int u = 0; u < kWarmSets; ++u)
       asm volatile("" ::"v"(tv[u][0]), "v"(tv[u][1]), "v"(tv[u][2]));
-    return;
-  }
+  } else {
 
   // State rows of wave w: register r of tile i holds S[32 w + 16 i + 4 g + r][j].
   const unsigned j = 16 * js + L;
@@ -989,6 +1007,106 @@ __global__ __launch_bounds__(kScanThreads, 1) void delta_scan_kernel(
 #pragma unroll
     for (int r = 0; r < 4; ++r)
       scol[(size_t)(32 * w + 16 * i + 4 * g + r) * DV] = S[i][r];
+  }
+
+  if constexpr (NORM) {
+    // Arrival. The head's 16-byte counter record holds a 64-bit arrival word
+    // -- bits 0-7 the count, 7 bits per XCD at 8 + 7 x the arrivals from
+    // that XCD -- and a second count. Every workgroup's output stores reach
+    // L2 (each wave waits for its own), then it adds 1 + 2^(8 + 7 xcd) and
+    // waits, with relaxed loads, for all slices. When they all ran on this
+    // XCD they share its L2: dropping this CU's L1 makes their rows visible.
+    // Otherwise their L2s are not coherent: every workgroup writes its L2
+    // back (a device-scope release), counts again, and acquires device-wide.
+    unsigned long long *const word = reinterpret_cast<unsigned long long *>(cnt + 4 * h);
+    unsigned *const again = cnt + 4 * h + 2;
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    __shared__ unsigned sDeviceWide;
+    if (threadIdx.x == 0) {
+      unsigned xcc;
+      asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID, 0, 4)" : "=s"(xcc));
+      __hip_atomic_fetch_add(word, 1ull + (1ull << (8 + 7 * (xcc & 7u))), __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+      unsigned long long seen = 0;
+      for (unsigned i = 0; i < kSpinLimit; ++i) {
+        seen = __hip_atomic_load(word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if ((seen & 0xFFu) >= slices)
+          break;
+        __builtin_amdgcn_s_sleep(2);
+      }
+      const unsigned here = (unsigned)(seen >> (8 + 7 * (xcc & 7u))) & 0x7Fu;
+      sDeviceWide = here != slices;
+      if (here != slices) {
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+        __hip_atomic_fetch_add(again, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        for (unsigned i = 0; i < kSpinLimit; ++i) {
+          if (__hip_atomic_load(again, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= slices)
+            break;
+          __builtin_amdgcn_s_sleep(2);
+        }
+      }
+    }
+    __syncthreads();
+    if (sDeviceWide)
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    else
+      asm volatile("buffer_inv sc0" ::: "memory");
+    const unsigned per = (T + slices - 1) / slices, r0 = min(T, js * per);
+    const unsigned nrows = min(T, r0 + per) - r0, c8n = DV / 8;
+    // The stage is free now: the weight, then the row factors.
+    float *const sWn = reinterpret_cast<float *>(&sY[0][0][0]);
+    float *const sF = sWn + DV;
+    for (unsigned jj = threadIdx.x; jj < DV; jj += kScanThreads)
+      sWn[jj] = nweight[jj];
+    half_t *const ob = out + (size_t)r0 * vStride + (size_t)h * DV;
+    const half_t *const gb = gate + (size_t)r0 * vStride + (size_t)h * DV;
+    const unsigned kRowsPass = (unsigned)(sizeof(sY) / sizeof(float)) - DV;
+    auto norm8 = [&](uint4_t x, uint4_t gv, float f, unsigned k8) {
+      return gated_norm_out8(x, gv, f, sWn + 8 * k8);
+    };
+    for (unsigned rb = 0; rb < nrows; rb += kRowsPass) {
+      const unsigned nr = min(kRowsPass, nrows - rb);
+      for (unsigned r = threadIdx.x; r < nr; r += kScanThreads) {
+        const uint4_t *row = reinterpret_cast<const uint4_t *>(ob + (size_t)(rb + r) * vStride);
+        uint4_t xr[16];
+        float sum = 0.0f;
+        for (unsigned k0 = 0; k0 < c8n; k0 += 16) {
+#pragma unroll
+          for (unsigned k8 = 0; k8 < 16; ++k8)
+            if (k0 + k8 < c8n)
+              xr[k8] = row[k0 + k8];
+#pragma unroll
+          for (unsigned k8 = 0; k8 < 16; ++k8)
+            if (k0 + k8 < c8n)
+              sum = sumsq8(xr[k8], sum);
+        }
+        sF[r] = gated_norm_factor(sum, DV, neps);
+      }
+      __syncthreads();
+      // Two 8-column pieces per thread and pass, both loaded before either
+      // is computed.
+      const unsigned items = nr * c8n;
+      for (unsigned i = threadIdx.x; i < items; i += 2 * kScanThreads) {
+        const unsigned i2 = i + kScanThreads;
+        const unsigned ra = i / c8n, ka = i % c8n, rb2 = i2 / c8n, kb = i2 % c8n;
+        uint4_t *const pa = reinterpret_cast<uint4_t *>(ob + (size_t)(rb + ra) * vStride) + ka;
+        uint4_t *const pb = reinterpret_cast<uint4_t *>(ob + (size_t)(rb + rb2) * vStride) + kb;
+        const uint4_t xa = *pa;
+        const uint4_t ga =
+            *(reinterpret_cast<const uint4_t *>(gb + (size_t)(rb + ra) * vStride) + ka);
+        uint4_t xb{0, 0, 0, 0}, gbv{0, 0, 0, 0};
+        if (i2 < items) {
+          xb = *pb;
+          gbv = *(reinterpret_cast<const uint4_t *>(gb + (size_t)(rb + rb2) * vStride) + kb);
+        }
+        *pa = norm8(xa, ga, sF[ra], ka);
+        if (i2 < items)
+          *pb = norm8(xb, gbv, sF[rb2], kb);
+      }
+      __syncthreads();
+    }
+  }
 }
 
 } // namespace
@@ -998,9 +1116,15 @@ bool delta_chunked_supported(const DeltaShape &s) {
          s.T >= 32;
 }
 
-size_t delta_chunked_workspace_bytes(const DeltaShape &s) {
+// After the records and K^T pieces: the fused norm's 16-byte per-value-head
+// arrival records (256-byte aligned).
+static size_t counters_offset(const DeltaShape &s) {
   const size_t chunks = (s.T + C - 1) / C;
   return chunks * (s.Hv * rec_bytes(s.Dv) + s.Hk * (size_t)kPieceBytes);
+}
+
+size_t delta_chunked_workspace_bytes(const DeltaShape &s) {
+  return counters_offset(s) + ((16 * (size_t)s.Hv + 255) / 256) * 256;
 }
 
 namespace {
@@ -1008,20 +1132,53 @@ namespace {
 template <bool QK16>
 hipError_t launch_chunked(const void *q, const void *k, const uint16_t *v, const float *beta,
                           const float *decay, float *state, uint16_t *out, void *ws,
-                          float eps, float qscale, const DeltaShape &s, hipStream_t stream) {
+                          float eps, float qscale, const DeltaShape &s, hipStream_t stream,
+                          const uint16_t *gate = nullptr, const float *nweight = nullptr,
+                          float neps = 0.0f) {
   const unsigned chunks = (s.T + C - 1) / C;
+  unsigned *cnt = gate ? reinterpret_cast<unsigned *>(static_cast<char *>(ws) +
+                                                      counters_offset(s))
+                       : nullptr;
   hipLaunchKernelGGL((delta_prep_kernel<QK16>), dim3(chunks, s.Hk), dim3(256), 0, stream, q, k,
                      reinterpret_cast<const half_t *>(v), beta, decay, ws, s.T, s.Hk, s.Hv,
-                     s.Dv, eps, qscale);
+                     s.Dv, eps, qscale, cnt);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess)
     return e;
-  hipLaunchKernelGGL(delta_scan_kernel, dim3(s.Hv * (s.Dv / 16)), dim3(kScanThreads), 0, stream, state,
-                     reinterpret_cast<half_t *>(out), ws, s.T, s.Hk, s.Hv, s.Dv);
+  const dim3 grid(s.Hv * (s.Dv / 16));
+  if (!gate) {
+    hipLaunchKernelGGL(delta_scan_kernel<false>, grid, dim3(kScanThreads), 0, stream, state,
+                       reinterpret_cast<half_t *>(out), ws, s.T, s.Hk, s.Hv, s.Dv,
+                       (const half_t *)nullptr, (const float *)nullptr, (unsigned *)nullptr,
+                       0.0f);
+    return hipGetLastError();
+  }
+  // The norm's arrival wait needs every slice workgroup of a value head
+  // resident at once: delta_chunked_norm_resident() checked that the whole
+  // grid fits on the device together (a cooperative launch would guarantee
+  // it too, but costs ~17 us more per call here, measured).
+  hipLaunchKernelGGL(delta_scan_kernel<true>, grid, dim3(kScanThreads), 0, stream, state,
+                     reinterpret_cast<half_t *>(out), ws, s.T, s.Hk, s.Hv, s.Dv,
+                     reinterpret_cast<const half_t *>(gate), nweight, cnt, neps);
   return hipGetLastError();
 }
 
 } // namespace
+
+bool delta_chunked_norm_resident(const DeltaShape &s) {
+  static int capacity = -1; // workgroups of the norm scan resident at once
+  if (capacity < 0) {
+    int dev = 0, cus = 0, per = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(
+            &per, reinterpret_cast<const void *>(&delta_scan_kernel<true>), kScanThreads, 0) !=
+            hipSuccess)
+      return false;
+    capacity = cus * per;
+  }
+  return s.Dv <= kNormMaxDv && (long)s.Hv * (s.Dv / 16) <= capacity;
+}
 
 hipError_t launch_delta_chunked(const float *q, const float *k, const uint16_t *v,
                                 const float *beta, const float *decay, float *state,
@@ -1035,6 +1192,16 @@ hipError_t launch_delta_chunked_qk16(const uint16_t *q, const uint16_t *k, const
                                      uint16_t *out, void *ws, float eps, float qscale,
                                      const DeltaShape &s, hipStream_t stream) {
   return launch_chunked<true>(q, k, v, beta, decay, state, out, ws, eps, qscale, s, stream);
+}
+
+hipError_t launch_delta_chunked_gated_norm(const uint16_t *q, const uint16_t *k,
+                                           const uint16_t *v, const float *beta,
+                                           const float *decay, float *state, const uint16_t *gate,
+                                           const float *nweight, uint16_t *out, void *ws,
+                                           float eps, float qscale, float neps,
+                                           const DeltaShape &s, hipStream_t stream) {
+  return launch_chunked<true>(q, k, v, beta, decay, state, out, ws, eps, qscale, s, stream, gate,
+                              nweight, neps);
 }
 
 unsigned delta_chunked_dispatches() { return 2; }

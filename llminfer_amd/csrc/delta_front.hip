@@ -27,6 +27,7 @@
 // l2NormF32 tile structure with the rmsNorm scale, the gate applied per
 // element in the output pass.
 #include "exact_fp.hpp"
+#include "gated_norm.hpp"
 #include "hip_common.hpp"
 #include "kernels.hpp"
 
@@ -255,7 +256,7 @@ __global__ __launch_bounds__(64) void gated_rms_norm_tile(const uint16_t *__rest
         sum = __builtin_fmaf(hi, hi, sum);
       }
     }
-    fac[lane] = __fdiv_rn(1.0f, sqrt_cr(__fadd_rn(__fdiv_rn(sum, (float)width), eps)));
+    fac[lane] = gated_norm_factor(sum, width, eps);
   }
   __syncthreads();
   for (unsigned c = lane; c < chunks; c += 64) {
@@ -283,12 +284,11 @@ __global__ __launch_bounds__(64) void gated_rms_norm_tile(const uint16_t *__rest
     unsigned need = 0;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      norm[e] = mul32(round16(mul32(h2f((uint16_t)(q[e / 2] >> (16 * (e & 1)))), f)),
-                      w[col * 8 + e]);
+      norm[e] = gated_norm_scaled(h2f((uint16_t)(q[e / 2] >> (16 * (e & 1)))), f, w[col * 8 + e]);
       if (kActivated) {
         y[e] = mul32(norm[e], gv[e]);
       } else {
-        y[e] = mul32(norm[e], mul32(gv[e], logistic_estimate(gv[e])));
+        y[e] = gated_norm_silu_estimate(norm[e], gv[e]);
         need |= f16_settled(y[e]) ? 0u : 1u << e;
       }
     }
@@ -303,7 +303,7 @@ __global__ __launch_bounds__(64) void gated_rms_norm_tile(const uint16_t *__rest
         gk = k == (unsigned)e ? gv[e] : gk;
         nk = k == (unsigned)e ? norm[e] : nk;
       }
-      float yk = mul32(nk, mul32(gk, logistic_exact(gk)));
+      float yk = gated_norm_silu_exact(nk, gk);
 #pragma unroll
       for (int e = 0; e < 8; ++e)
         y[e] = k == (unsigned)e ? yk : y[e];

@@ -20,8 +20,11 @@
 //    the step's q/k/v/gates.
 //
 // Summation order inside a dot product differs from the reference's single
-// fma chain (four interleaved chains per lane plus the partials in LDS); the
-// result stays within fp32 rounding of the sequential order.
+// fma chain (four interleaved chains per 16-row unit (8 at dk = 64), the 8
+// unit sums added in order through LDS); the result stays within fp32
+// rounding of the sequential order, and it does not depend on how the rows
+// are split between lanes (the one-workgroup-per-head variant below gives
+// the same bits as the default slices).
 //
 // With QK16 the kernel also performs the L2 normalisations of q and k that
 // precede DeltaUpdate (l2NormF32, Graph.metal:96-109): q and k arrive as the
@@ -30,6 +33,7 @@
 // every fp32 element is the single product x * factor -- the bits l2NormF32
 // writes, so the update sees exactly the operands of the unfused pair.
 #include "exact_fp.hpp"
+#include "gated_norm.hpp"
 #include "hip_common.hpp"
 #include "kernels.hpp"
 
@@ -39,44 +43,84 @@
 namespace llmi {
 namespace {
 
-template <int DK, int CW, int NW, bool QK16>
-__global__ __launch_bounds__(64 * NW) void delta_recurrent_kernel(
+// With NORM (and CG column groups of NW waves each, the workgroup holding
+// all CG * CW columns of a value head) the kernel ends with gatedRmsNorm
+// over the head's output rows (Reference.metal:228-259): the fp16 outputs
+// of the T <= kRecNormMaxT tokens wait in LDS, one thread per row runs the
+// row's sequential sum of squares, and every element becomes fp16(fp16(x *
+// factor) * weight * silu(gate)) (gated_norm.hpp, the standalone kernel's
+// arithmetic). The gate and weight values are requested at the start.
+template <int DK, int CW, int NW, bool QK16, int CG = 1, bool NORM = false>
+__global__ __launch_bounds__(64 * NW * CG) void delta_recurrent_kernel(
     const void *__restrict__ qp, const void *__restrict__ kp,
     const half_t *__restrict__ v, const float *__restrict__ beta,
     const float *__restrict__ decay, float *__restrict__ state,
     half_t *__restrict__ out, unsigned T, unsigned Hk, unsigned Hv,
-    unsigned DV, float eps, float qscale) {
+    unsigned DV, float eps, float qscale, const half_t *__restrict__ gate,
+    const float *__restrict__ nweight, float neps) {
   constexpr int RG = 64 / CW;  // row groups per wave
-  constexpr int NP = NW * RG;  // partial sums per column
+  constexpr int NP = NW * RG;  // lanes (row parts) per column
   constexpr int RPL = DK / NP; // rows per lane
+  // The dot products are summed in NU canonical units of UR consecutive rows
+  // (each four interleaved fma chains, then (c0 + c1) + (c2 + c3)), the
+  // units added in row order: the same bits whatever the partition, as long
+  // as NP <= 8 (a lane then holds UPL whole units).
+  constexpr int NU = NP <= 8 ? 8 : NP, UR = DK / NU, UPL = RPL / UR;
+  constexpr int kThreads = 64 * NW * CG;
   static_assert(RPL % 4 == 0 && RPL * NP == DK, "rows per lane must be a multiple of 4");
+  static_assert(UR % 4 == 0 && UR * UPL == RPL, "a lane holds whole units");
+  static_assert(!NORM || CW == 64, "the fused norm's workgroup holds 64-column groups");
   const unsigned tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
-  const unsigned c = lane % CW, part = wave * RG + lane / CW;
-  const unsigned slices = DV / CW;
+  const unsigned cg = wave / NW, wv = wave % NW;
+  const unsigned c = lane % CW, part = wv * RG + lane / CW;
+  const unsigned slices = DV / (CW * CG);
   const unsigned h = blockIdx.x / slices;
-  const unsigned col = (blockIdx.x % slices) * CW + c;
+  const unsigned col = (blockIdx.x % slices) * (CW * CG) + cg * CW + c;
   const unsigned kh = h / (Hv / Hk);
   const unsigned row0 = part * RPL;
   const size_t vwidth = (size_t)Hv * DV;
 
-  __shared__ float sPred[NP][CW], sY[NP][CW];
+  __shared__ float sPred[CG][NU][CW], sY[CG][NU][CW];
+  // NORM: the outputs x of the tokens (fp16, as the unfused kernel stores
+  // them), the row factors, and the head's gate rows and the weight, staged
+  // at the start (no register holds them across the token loop).
+  constexpr int NX = NORM ? kRecNormMaxT : 1, NC = NORM ? CW * CG : 1;
+  __shared__ __attribute__((aligned(16))) half_t sX[NX][NC], sGate[NX][NC];
+  __shared__ float sNF[NX], sW[NC];
+  if constexpr (NORM) {
+    for (unsigned i = tid; i < T * DV; i += kThreads)
+      sGate[i / DV][i % DV] = gate[(size_t)(i / DV) * vwidth + (size_t)h * DV + i % DV];
+    for (unsigned j = tid; j < DV; j += kThreads)
+      sW[j] = nweight[j];
+  }
   // QK16: the L2 factors of kFacTok tokens' k and q rows at a time; thread
   // 2i (2i + 1) sums the k (q) row of the block's token i. The rows of the
   // first block are requested before the state, so that their sums run
   // while the state is in flight.
-  constexpr unsigned kFacTok = 32 * NW;
+  // With NORM (T <= kRecNormMaxT, one block) the 2T rows are staged in LDS
+  // by all threads instead, which keeps the row out of the registers.
+  constexpr unsigned kFacTok = NORM ? kRecNormMaxT : 32 * NW * CG;
   __shared__ float sFac[QK16 ? 2 * kFacTok : 1];
-  uint4_t facRow[QK16 ? DK / 8 : 1];
+  __shared__ uint4_t sFacRows[QK16 && NORM ? 2 * kRecNormMaxT * DK / 8 : 1];
+  uint4_t facRow[QK16 && !NORM ? DK / 8 : 1];
   auto fetch_fac_row = [&](unsigned tb) {
     const unsigned tt = tb + tid / 2;
     const uint4_t *row = reinterpret_cast<const uint4_t *>(
         static_cast<const half_t *>((tid & 1u) ? qp : kp) + ((size_t)tt * Hk + kh) * DK);
 #pragma unroll
-    for (int c8 = 0; c8 < (QK16 ? DK / 8 : 0); ++c8)
+    for (int c8 = 0; c8 < (QK16 && !NORM ? DK / 8 : 0); ++c8)
       facRow[c8] = row[c8];
   };
-  if (QK16 && tid < 2 * min(kFacTok, T))
+  if constexpr (QK16 && NORM) {
+    // Row r = 2 t (+1 for q) of token t.
+    for (unsigned i = tid; i < 2 * T * (DK / 8); i += kThreads) {
+      const unsigned r = i / (DK / 8), c8 = i % (DK / 8);
+      sFacRows[i] = reinterpret_cast<const uint4_t *>(
+          static_cast<const half_t *>((r & 1u) ? qp : kp) + ((size_t)(r / 2) * Hk + kh) * DK)[c8];
+    }
+  } else if (QK16 && tid < 2 * min(kFacTok, T)) {
     fetch_fac_row(0);
+  }
 
   float S[RPL];
   float *sbase = state + ((size_t)h * DK + row0) * DV + col;
@@ -118,11 +162,13 @@ __global__ __launch_bounds__(64 * NW) void delta_recurrent_kernel(
         if (tid < 2 * tn)
           fetch_fac_row(tb);
       }
+      if constexpr (NORM)
+        __syncthreads(); // the staged rows
       if (tid < 2 * tn) {
         float sum = 0.0f;
 #pragma unroll
         for (int c8 = 0; c8 < DK / 8; ++c8)
-          sum = sumsq8(facRow[c8], sum);
+          sum = sumsq8(NORM ? sFacRows[tid * (DK / 8) + c8] : facRow[c8], sum);
         sFac[tid] = l2_row_factor(sum, eps, (tid & 1u) ? qscale : 1.0f);
       }
       __syncthreads();
@@ -146,32 +192,45 @@ __global__ __launch_bounds__(64 * NW) void delta_recurrent_kernel(
       }
       const float a = cur.a, b = cur.b, vj = cur.vj;
 
-      float p4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+      float p4[UPL][4];
+#pragma unroll
+      for (int u = 0; u < UPL; ++u)
+        p4[u][0] = p4[u][1] = p4[u][2] = p4[u][3] = 0.0f;
 #pragma unroll
       for (int m = 0; m < RPL; ++m)
-        p4[m % 4] = fmaf(S[m] * a, kr[m], p4[m % 4]);
-      sPred[part][c] = (p4[0] + p4[1]) + (p4[2] + p4[3]);
+        p4[m / UR][m % 4] = fmaf(S[m] * a, kr[m], p4[m / UR][m % 4]);
+#pragma unroll
+      for (int u = 0; u < UPL; ++u)
+        sPred[cg][part * UPL + u][c] = (p4[u][0] + p4[u][1]) + (p4[u][2] + p4[u][3]);
       __syncthreads();
       float pred = 0.0f;
 #pragma unroll
-      for (int i = 0; i < NP; ++i)
-        pred += sPred[i][c];
+      for (int i = 0; i < NU; ++i)
+        pred += sPred[cg][i][c];
       const float delta = (vj - pred) * b;
 
-      float y4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+      float y4[UPL][4];
+#pragma unroll
+      for (int u = 0; u < UPL; ++u)
+        y4[u][0] = y4[u][1] = y4[u][2] = y4[u][3] = 0.0f;
 #pragma unroll
       for (int m = 0; m < RPL; ++m) {
         S[m] = fmaf(kr[m], delta, S[m] * a);
-        y4[m % 4] = fmaf(S[m], qr[m], y4[m % 4]);
+        y4[m / UR][m % 4] = fmaf(S[m], qr[m], y4[m / UR][m % 4]);
       }
-      sY[part][c] = (y4[0] + y4[1]) + (y4[2] + y4[3]);
+#pragma unroll
+      for (int u = 0; u < UPL; ++u)
+        sY[cg][part * UPL + u][c] = (y4[u][0] + y4[u][1]) + (y4[u][2] + y4[u][3]);
       __syncthreads();
       if (part == 0) {
         float y = 0.0f;
 #pragma unroll
-        for (int i = 0; i < NP; ++i)
-          y += sY[i][c];
-        out[(size_t)t * vwidth + (size_t)h * DV + col] = (half_t)y;
+        for (int i = 0; i < NU; ++i)
+          y += sY[cg][i][c];
+        if constexpr (NORM)
+          sX[t][col] = (half_t)y;
+        else
+          out[(size_t)t * vwidth + (size_t)h * DV + col] = (half_t)y;
       }
       if (t + 1 < T)
         cur = nxt;
@@ -181,6 +240,23 @@ __global__ __launch_bounds__(64 * NW) void delta_recurrent_kernel(
 #pragma unroll
   for (int m = 0; m < RPL; ++m)
     sbase[(size_t)m * DV] = S[m];
+
+  if constexpr (NORM) {
+    __syncthreads();
+    if (tid < T) {
+      const uint4_t *row = reinterpret_cast<const uint4_t *>(&sX[tid][0]);
+      float sum = 0.0f;
+      for (unsigned k8 = 0; k8 < DV / 8; ++k8)
+        sum = sumsq8(row[k8], sum);
+      sNF[tid] = gated_norm_factor(sum, DV, neps);
+    }
+    __syncthreads();
+    for (unsigned i = tid; i < T * DV; i += kThreads) {
+      const unsigned t = i / DV, j = i % DV;
+      out[(size_t)t * vwidth + (size_t)h * DV + j] =
+          gated_norm_out((float)sX[t][j], sNF[t], sW[j], (float)sGate[t][j]);
+    }
+  }
 }
 
 // Any-shape fallback (e.g. the reference test models' dk = 7, dv = 5):
@@ -263,14 +339,18 @@ struct RecArgs {
   float *state;
   uint16_t *out;
   float eps, qscale;
+  const uint16_t *gate = nullptr;
+  const float *nweight = nullptr;
+  float neps = 0.0f;
 };
 
-template <int DK, int CW, int NW, bool QK16>
+template <int DK, int CW, int NW, bool QK16, int CG = 1, bool NORM = false>
 hipError_t launch_rec(const RecArgs &a, const DeltaShape &s, hipStream_t stream) {
-  hipLaunchKernelGGL((delta_recurrent_kernel<DK, CW, NW, QK16>), dim3(s.Hv * (s.Dv / CW)),
-                     dim3(64 * NW), 0, stream, a.q, a.k, reinterpret_cast<const half_t *>(a.v),
-                     a.beta, a.decay, a.state, reinterpret_cast<half_t *>(a.out), s.T, s.Hk,
-                     s.Hv, s.Dv, a.eps, a.qscale);
+  hipLaunchKernelGGL((delta_recurrent_kernel<DK, CW, NW, QK16, CG, NORM>),
+                     dim3(s.Hv * (s.Dv / (CW * CG))), dim3(64 * NW * CG), 0, stream, a.q, a.k,
+                     reinterpret_cast<const half_t *>(a.v), a.beta, a.decay, a.state,
+                     reinterpret_cast<half_t *>(a.out), s.T, s.Hk, s.Hv, s.Dv, a.eps, a.qscale,
+                     reinterpret_cast<const half_t *>(a.gate), a.nweight, a.neps);
   return hipGetLastError();
 }
 
@@ -306,6 +386,26 @@ hipError_t launch_rec_any(const RecArgs &a, const DeltaShape &s, hipStream_t str
 }
 
 } // namespace
+
+bool delta_recurrent_norm_supported(const DeltaShape &s) {
+  return (s.Dk == 64 || s.Dk == 128) && (s.Dv == 64 || s.Dv == 128) && s.Hk >= 1 &&
+         s.Hv % s.Hk == 0 && s.T >= 1 && s.T <= kRecNormMaxT;
+}
+
+hipError_t launch_delta_recurrent_gated_norm(const uint16_t *q, const uint16_t *k,
+                                             const uint16_t *v, const float *beta,
+                                             const float *decay, float *state,
+                                             const uint16_t *gate, const float *nweight,
+                                             uint16_t *out, float eps, float qscale,
+                                             float neps, const DeltaShape &s,
+                                             hipStream_t stream) {
+  RecArgs a{q, k, v, beta, decay, state, out, eps, qscale, gate, nweight, neps};
+  if (s.Dk == 64)
+    return s.Dv == 64 ? launch_rec<64, 64, 4, true, 1, true>(a, s, stream)
+                      : launch_rec<64, 64, 4, true, 2, true>(a, s, stream);
+  return s.Dv == 64 ? launch_rec<128, 64, 4, true, 1, true>(a, s, stream)
+                    : launch_rec<128, 64, 4, true, 2, true>(a, s, stream);
+}
 
 bool delta_recurrent_supported(const DeltaShape &s) {
   return (s.Dk == 64 || s.Dk == 128) && s.Dv % 16 == 0 && s.Hk >= 1 &&

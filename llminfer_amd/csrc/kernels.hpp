@@ -103,6 +103,29 @@ hipError_t launch_delta_recurrent(const float *q, const float *k,
                                   uint16_t *out, const DeltaShape &s,
                                   hipStream_t stream);
 
+// L2Norm -> DeltaUpdate -> gatedRmsNorm in one call (fp16 q/k, fp16 gate,
+// fp32 norm weight of dv): the recurrent form with one workgroup per value
+// head (T <= kRecNormMaxT, dv 64 or 128), and the chunked
+// form whose scan normalises the head's rows at its end.
+constexpr unsigned kRecNormMaxT = 32;
+bool delta_recurrent_norm_supported(const DeltaShape &s);
+hipError_t launch_delta_recurrent_gated_norm(const uint16_t *q, const uint16_t *k,
+                                             const uint16_t *v, const float *beta,
+                                             const float *decay, float *state,
+                                             const uint16_t *gate, const float *nweight,
+                                             uint16_t *out, float eps, float qscale,
+                                             float neps, const DeltaShape &s,
+                                             hipStream_t stream);
+// Whether the chunked form's norm scan grid fits on the device at once (its
+// per-head arrival wait needs every workgroup resident).
+bool delta_chunked_norm_resident(const DeltaShape &s);
+hipError_t launch_delta_chunked_gated_norm(const uint16_t *q, const uint16_t *k,
+                                           const uint16_t *v, const float *beta,
+                                           const float *decay, float *state, const uint16_t *gate,
+                                           const float *nweight, uint16_t *out, void *ws,
+                                           float eps, float qscale, float neps,
+                                           const DeltaShape &s, hipStream_t stream);
+
 // Any-shape fallback, one thread per state column.
 hipError_t launch_delta_generic(const float *q, const float *k,
                                 const uint16_t *v, const float *beta,

@@ -421,6 +421,45 @@ def l2_norm_delta_update(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, beta
     return out
 
 
+def bind_l2_norm_delta_gated_norm(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                                  beta: torch.Tensor, decay: torch.Tensor, state: torch.Tensor,
+                                  gate: torch.Tensor, norm_weight: torch.Tensor,
+                                  out: torch.Tensor, epsilon: float = 1e-6,
+                                  q_scale: float | None = None,
+                                  norm_epsilon: float = 1e-6) -> "Bound":
+    """L2Norm(q), L2Norm(k), DeltaUpdate and GatedRmsNorm(out, gate,
+    norm_weight, norm_epsilon) in one call (Qwen35ModelBuilder.cpp:155-166):
+    operands as bind_l2_norm_delta_update, gate fp16 like v, norm_weight fp32
+    [dv]; out receives the normalised rows."""
+    _require(gate, torch.float16, "gate")
+    _require(norm_weight, torch.float32, "norm_weight")
+    hv, dk, dv = state.shape
+    if gate.shape != v.shape or norm_weight.numel() != dv:
+        raise ValueError("gate must match v and norm_weight have dv elements")
+    inner = bind_l2_norm_delta_update(q, k, v, beta, decay, state, out, epsilon, q_scale)
+    a = inner._args
+    lib = _lib.load()
+    args = a[:6] + (_ptr(gate), _ptr(norm_weight)) + a[6:10] + (norm_epsilon,) + a[10:]
+    b = Bound(lib.llmi_hip_l2_norm_delta_gated_norm, args, inner.what + "+gatedRmsNorm")
+    b._keep = inner._keep
+    return b
+
+
+def l2_norm_delta_gated_norm(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                             beta: torch.Tensor, decay: torch.Tensor, state: torch.Tensor,
+                             gate: torch.Tensor, norm_weight: torch.Tensor,
+                             out: torch.Tensor | None = None, epsilon: float = 1e-6,
+                             q_scale: float | None = None,
+                             norm_epsilon: float = 1e-6) -> torch.Tensor:
+    """The fused L2Norm -> DeltaUpdate -> GatedRmsNorm chain
+    (bind_l2_norm_delta_gated_norm)."""
+    if out is None:
+        out = torch.empty_like(v)
+    bind_l2_norm_delta_gated_norm(q, k, v, beta, decay, state, gate, norm_weight, out,
+                                  epsilon, q_scale, norm_epsilon)()
+    return out
+
+
 class Bound:
     """One C-ABI call with every argument converted once, for hot loops.
 

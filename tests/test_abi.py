@@ -265,3 +265,27 @@ def test_l2_norm_delta_update_rejects_shapes_without_kernel():
     ok = _lib.GraphDeltaParams(1024, 16, 128, 32, 128)
     assert lib.llmi_hip_l2_norm_delta_update(1, 1, 1, 1, 1, 1, 1, ok, 1e-6, 1.0, None, 0,
                                              None) == _lib.WORKSPACE
+
+
+def test_l2_norm_delta_gated_norm_rejects_shapes_without_kernel():
+    """The fused L2Norm+DeltaUpdate+GatedRmsNorm has a chunked kernel (dk 128,
+    T >= 32) and a one-workgroup-per-head recurrent kernel (dk 64/128, dv
+    64/128, T <= 32): dk 64 at T = 64 and dv 48 at T = 5 are UNSUPPORTED
+    before any launch; the chunked form checks its workspace and the 16-byte
+    alignment of out and gate; a contract violation stays INVALID_ARGUMENT."""
+    lib = _lib.load()
+    f = lib.llmi_hip_l2_norm_delta_gated_norm
+    for T, dk, dv in ((64, 64, 64), (5, 128, 48)):
+        p = _lib.GraphDeltaParams(T, 2, dk, 4, dv)
+        assert f(16, 16, 16, 16, 16, 16, 16, 16, 16, p, 1e-6, 0.1, 1e-6, None, 0,
+                 None) == _lib.UNSUPPORTED, (T, dk, dv)
+    ok = _lib.GraphDeltaParams(1024, 16, 128, 32, 128)
+    assert f(16, 16, 16, 16, 16, 16, 16, 16, 16, ok, 1e-6, 0.1, 1e-6, None, 0,
+             None) == _lib.WORKSPACE
+    assert f(16, 16, 16, 16, 16, 16, 18, 16, 16, ok, 1e-6, 0.1, 1e-6, None, 0,
+             None) == _lib.UNSUPPORTED  # gate not 16-byte aligned
+    bad = _lib.GraphDeltaParams(4, 16, 128, 24, 128)  # Hv % Hk != 0
+    assert f(16, 16, 16, 16, 16, 16, 16, 16, 16, bad, 1e-6, 0.1, 1e-6, None, 0,
+             None) == _lib.INVALID_ARGUMENT
+    assert f(16, 16, 16, 16, 16, 16, None, 16, 16, ok, 1e-6, 0.1, 1e-6, None, 0,
+             None) == _lib.INVALID_ARGUMENT
