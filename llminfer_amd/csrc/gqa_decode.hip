@@ -29,8 +29,9 @@
 //    waves and finally splits are merged with the usual (m, l, o) rescale.
 //  * a one-split launch writes the output directly. Otherwise every
 //    workgroup writes its (m, l, o) partial to the workspace and a second,
-//    small launch merges them: one 64-thread workgroup per 64 output channels
-//    of a query head, all of its partial loads in flight at once. (Merging
+//    small launch merges them: one 64-thread workgroup per 16 output channels
+//    of a query head, four lanes per channel taking every fourth split, all
+//    of the partial loads in flight at once. (Merging
 //    inside the split kernel's last-arriving workgroup was measured slower on
 //    MI355X: the partial stores then need agent-scope release -- a whole-L2
 //    writeback per workgroup, which serialises -- and the single merging
@@ -599,27 +600,33 @@ __global__ __launch_bounds__(64 * kWaves) void gqa_decode_kernel(
   }
 }
 
-// Second-launch merge: workgroup (channel block, g, row) combines the
-// splits of 64 output channels of query head g of one (token, kv head) row;
-// each thread loads its channel of every partial at once.
+// Second-launch merge: workgroup (16-channel block, g, row) combines the
+// splits of 16 output channels of query head g of one (token, kv head) row.
+// Lane l serves channel l % 16 for the splits s = l / 16 + 4 u: every lane
+// has at most kMaxSplits / 4 loads in flight at once, and the grid has 4x
+// as many workgroups as 64-channel blocks would (each CU's share of the
+// partials arrives in fewer, shorter chains). The four quarter sums meet
+// through lane swaps, in a fixed order.
+constexpr unsigned kMergeCols = 16;
 template <int D, int G, bool GATED>
 __global__ __launch_bounds__(64) void gqa_decode_merge_kernel(
     const float *__restrict__ wml, const float *__restrict__ wo,
     half_t *__restrict__ out, unsigned Hq, unsigned Hkv, unsigned splits,
     const half_t *__restrict__ qproj) {
-  static_assert(D % 64 == 0, "whole waves");
+  static_assert(D % kMergeCols == 0, "whole channel blocks");
   const unsigned lane = threadIdx.x, g = blockIdx.y, row = blockIdx.z;
-  const unsigned x = blockIdx.x * 64 + lane;
+  const unsigned x = blockIdx.x * kMergeCols + lane % 16, quarter = lane / 16;
   const float *col = wo + (size_t)row * splits * G * D + (size_t)g * D + x;
   const float *rowMl = wml + (size_t)row * splits * G * 2;
-  // Indices past the last split are clamped (valid addresses, zero weight),
-  // so the loads carry no branches and all go out at once.
-  constexpr int PER = 64;
+  // Split indices past the last are clamped (valid addresses, zero
+  // weight), so the loads carry no branches and all go out at once.
+  constexpr int PER = kMaxSplits / 4;
   const unsigned last = splits - 1;
   float v[PER];
 #pragma unroll
   for (int u = 0; u < PER; ++u)
-    v[u] = col[(size_t)min((unsigned)u, last) * G * D];
+    if (u < 16 || splits > 64)
+      v[u] = col[(size_t)min(quarter + 4u * u, last) * G * D];
   float ms[2], ls[2];
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
@@ -640,15 +647,14 @@ __global__ __launch_bounds__(64) void gqa_decode_merge_kernel(
   float acc = 0.0f;
 #pragma unroll
   for (int u = 0; u < PER; ++u)
-    acc = fmaf(v[u], sW[u], acc);
-  if (splits > PER) {
-#pragma unroll
-    for (int u = 0; u < PER; ++u)
-      v[u] = col[(size_t)min((unsigned)(PER + u), last) * G * D];
-#pragma unroll
-    for (int u = 0; u < PER; ++u)
-      acc = fmaf(v[u], sW[PER + u], acc);
-  }
+    if (u < 16 || splits > 64)
+      acc = fmaf(v[u], sW[quarter + 4u * u], acc); // weight 0 past the last split
+  LanePair p = pair16(acc);
+  acc = p.a + p.b;
+  p = pair32(acc);
+  acc = p.a + p.b;
+  if (quarter != 0)
+    return;
   const unsigned t = row / Hkv, kvh = row % Hkv;
   const half_t y = f16_of(acc);
   if constexpr (GATED)
@@ -681,7 +687,7 @@ hipError_t launch_dgg(const GqaShape &s, const uint16_t *q, uint16_t *k,
     hipError_t e = hipGetLastError();
     if (e != hipSuccess)
       return e;
-    hipLaunchKernelGGL((gqa_decode_merge_kernel<D, G, GATED>), dim3(D / 64, G, s.T * s.Hkv),
+    hipLaunchKernelGGL((gqa_decode_merge_kernel<D, G, GATED>), dim3(D / kMergeCols, G, s.T * s.Hkv),
                        dim3(64), 0, stream, reinterpret_cast<float *>(base + w.ml),
                        reinterpret_cast<float *>(base + w.o),
                        reinterpret_cast<half_t *>(out), s.Hq, s.Hkv, p.splits, qproj);
