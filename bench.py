@@ -2,7 +2,11 @@
 """Benchmark of the llminfer attention hot path on one MI355X (gfx950).
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--only-headline]
-                    [--cpu-seconds S] [--no-cpu]
+                    [--cpu-seconds S] [--no-cpu] [--only KEY,...]
+
+`--only` runs just the named configurations (`headline` names the headline):
+a profile of one configuration then holds that configuration's launches and
+no other's. Without the headline the line carries only `configs`.
 
 Prints ONE JSON line. The headline workload is the GQA single-token decode
 of the reference's decode path (KvAppend + CausalGqa, T=1, 4096 past rows,
@@ -1106,41 +1110,9 @@ def load_traffic(workload: str):
     return entry.get("bytes_per_launch") if isinstance(entry, dict) else None
 
 
-# ------------------------------------------------------------------ main
-
-def main(argv=None) -> int:
-    ap = argparse.ArgumentParser(description="llminfer attention hot path benchmark")
-    ap.add_argument("--gpus", type=int, default=int(os.environ.get("WORLD_SIZE", "1")))
-    ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--only-headline", action="store_true",
-                    help="skip the other BASELINE configurations")
-    ap.add_argument("--cpu-seconds", type=float, default=8.0,
-                    help="CPU-baseline time budget of the headline (others get half)")
-    ap.add_argument("--no-cpu", action="store_true", help="skip every CPU baseline")
-    ap.add_argument("--only", default="",
-                    help="comma-separated keys of the other configurations to run "
-                         "(default: all)")
-    args = ap.parse_args(argv)
-
-    if args.gpus != 1:
-        print(f"bench.py measures one GPU only: --gpus {args.gpus} is not supported "
-              "(this build's hot path runs on a single MI355X; see the sharding notes "
-              "in the design document)", file=sys.stderr)
-        return 2
-
+def headline(dev, args, cyc) -> dict:
+    """The headline, configs[1]: its JSON fields."""
     import torch
-    from llminfer_amd import _lib
-    if not torch.cuda.is_available():
-        print("bench.py needs a GPU (no HIP device visible)", file=sys.stderr)
-        return 1
-    _lib.load()  # raises if the HIP library is missing; there is no fallback
-    dev = torch.device("cuda", 0)
-    torch.cuda.set_device(dev)
-    cyc = sleep_cycles_per_ms()
-    log(f"device {torch.cuda.get_device_name(dev)}; spin {cyc:.0f} cycles/ms")
-
-    # ---- headline: configs[1]
     w = GqaDecode(dev)
     log(f"headline {w.name}: warmup {args.warmup}, steps {args.steps}")
     ms = run_timed(w.launch, args.steps, args.warmup, cyc)
@@ -1169,30 +1141,75 @@ def main(argv=None) -> int:
         result["cpu_baseline"] = w.cpu(args.cpu_seconds)
     del w
     torch.cuda.empty_cache()
+    return result
+
+
+# ------------------------------------------------------------------ main
+
+def main(argv=None) -> int:
+    ap = argparse.ArgumentParser(description="llminfer attention hot path benchmark")
+    ap.add_argument("--gpus", type=int, default=int(os.environ.get("WORLD_SIZE", "1")))
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--only-headline", action="store_true",
+                    help="skip the other BASELINE configurations")
+    ap.add_argument("--cpu-seconds", type=float, default=8.0,
+                    help="CPU-baseline time budget of the headline (others get half)")
+    ap.add_argument("--no-cpu", action="store_true", help="skip every CPU baseline")
+    ap.add_argument("--only", default="",
+                    help="comma-separated keys of the configurations to run, "
+                         "'headline' for the headline (default: all)")
+    args = ap.parse_args(argv)
+
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only: --gpus {args.gpus} is not supported "
+              "(this build's hot path runs on a single MI355X; see the sharding notes "
+              "in the design document)", file=sys.stderr)
+        return 2
+
+    import torch
+    from llminfer_amd import _lib
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU (no HIP device visible)", file=sys.stderr)
+        return 1
+    _lib.load()  # raises if the HIP library is missing; there is no fallback
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    cyc = sleep_cycles_per_ms()
+    log(f"device {torch.cuda.get_device_name(dev)}; spin {cyc:.0f} cycles/ms")
+
+    only = {k for k in args.only.split(",") if k}
+    builders = [
+        ("cfg0_gqa_prefill_128", lambda: GqaPrefill(dev, 128, 0, 128, seed=1)),
+        ("cfg2_gqa_chunked_prefill", lambda: GqaPrefill(dev, 2048, 2048, 4096, seed=3)),
+        ("cfg3_delta_prefill_1024", lambda: DeltaPrefill(dev)),
+        ("cfg4_hybrid_decode_32k", lambda: HybridDecode(dev)),
+        ("next_attn_rows_prefill_2048", lambda: AttnRows(dev, 2048, 2048, 6, seed=6)),
+        ("next_attn_rows_decode_4k", lambda: AttnRows(dev, 1, 4096, 64, seed=7)),
+        ("next_delta_front_1024", lambda: DeltaFront(dev, 1024, 8, seed=8)),
+        ("next_delta_front_decode", lambda: DeltaFront(dev, 1, 64, seed=9)),
+        ("next_gated_attention_prefill", lambda: GatedAttention(dev, 2048, 2048, 4096, 2,
+                                                                 seed=12)),
+        ("next_gated_attention_decode_4k", lambda: GatedAttention(dev, 1, 4096, 8192, 24,
+                                                                  seed=13)),
+        ("next_l2norm_delta_1024", lambda: DeltaNormUpdate(dev, 1024, 8, seed=10)),
+        ("next_l2norm_delta_decode", lambda: DeltaNormUpdate(dev, 1, 128, seed=11)),
+        ("next_l2norm_delta_gatednorm_1024", lambda: DeltaGatedNorm(dev, 1024, 8, seed=12)),
+        ("next_l2norm_delta_gatednorm_decode", lambda: DeltaGatedNorm(dev, 1, 128, seed=13)),
+    ]
+    unknown = only - {k for k, _ in builders} - {"headline"}
+    if unknown:
+        print(f"unknown configuration(s): {sorted(unknown)}", file=sys.stderr)
+        return 2
+    result = {"n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "data": "synthetic"}
+    if not only or "headline" in only:
+        result = headline(dev, args, cyc)
+    only.discard("headline")
 
     # ---- the other configurations
-    if not args.only_headline:
+    if not args.only_headline and (only or not args.only):
         extra = {}
         steps = max(10, min(args.steps, 50))
-        builders = [
-            ("cfg0_gqa_prefill_128", lambda: GqaPrefill(dev, 128, 0, 128, seed=1)),
-            ("cfg2_gqa_chunked_prefill", lambda: GqaPrefill(dev, 2048, 2048, 4096, seed=3)),
-            ("cfg3_delta_prefill_1024", lambda: DeltaPrefill(dev)),
-            ("cfg4_hybrid_decode_32k", lambda: HybridDecode(dev)),
-            ("next_attn_rows_prefill_2048", lambda: AttnRows(dev, 2048, 2048, 6, seed=6)),
-            ("next_attn_rows_decode_4k", lambda: AttnRows(dev, 1, 4096, 64, seed=7)),
-            ("next_delta_front_1024", lambda: DeltaFront(dev, 1024, 8, seed=8)),
-            ("next_delta_front_decode", lambda: DeltaFront(dev, 1, 64, seed=9)),
-            ("next_gated_attention_prefill", lambda: GatedAttention(dev, 2048, 2048, 4096, 2,
-                                                                     seed=12)),
-            ("next_gated_attention_decode_4k", lambda: GatedAttention(dev, 1, 4096, 8192, 24,
-                                                                      seed=13)),
-            ("next_l2norm_delta_1024", lambda: DeltaNormUpdate(dev, 1024, 8, seed=10)),
-            ("next_l2norm_delta_decode", lambda: DeltaNormUpdate(dev, 1, 128, seed=11)),
-            ("next_l2norm_delta_gatednorm_1024", lambda: DeltaGatedNorm(dev, 1024, 8, seed=12)),
-            ("next_l2norm_delta_gatednorm_decode", lambda: DeltaGatedNorm(dev, 1, 128, seed=13)),
-        ]
-        only = {k for k in args.only.split(",") if k}
         for key, make in builders:
             if only and key not in only:
                 continue

@@ -28,11 +28,20 @@
 //    row maximum, so the MFMA sees no fp16 subnormals where they matter.
 //  * PV of tile i-1 is issued after the scores of tile i, so its MFMAs
 //    overlap the softmax arithmetic of tile i.
+//
+// At head_dim 256 with four query heads per KV head, grids of 64 workgroups
+// or more run gqa_prefill_halves_kernel instead: the single-wave kernel
+// needs ~500 registers per lane, one wave per SIMD, and a lone wave cannot
+// hide its LDS operand reads behind its MFMAs (measured on gfx950: 55-60
+// cycles per 32x32x16 MFMA with a 1 KB operand read each, against 38 with a
+// second wave on the SIMD and the reads two MFMAs ahead). The key-split
+// kernel gives each head a wave pair that splits the keys, at 248 registers.
 #include "hip_common.hpp"
 #include "kernels.hpp"
 #include "rope_gate.hpp"
 
 #include <math.h>
+#include <stdlib.h>
 #include <type_traits>
 
 namespace llmi {
@@ -70,6 +79,42 @@ __device__ __forceinline__ half4_t read_tr(const char *base, unsigned off) {
   typedef __attribute__((address_space(3))) char lds_char_t;
   return __builtin_bit_cast(half4_t, __builtin_amdgcn_ds_read_tr16_b64_v4f16(
                                          (lds_fp16x4_t *)((lds_char_t *)base + off)));
+}
+
+// The sigmoid gate of one lane's 16 outputs of a 32-channel tile (the
+// four half4 groups at g + 8 i): the fast logistic first, then the exact one
+// for the few that miss the margin test, one per pass of the wave (as the
+// standalone gate kernel does).
+__device__ __forceinline__ void gate_tile(half4_t (&v)[4], const half_t *g4p) {
+  float g[16], sg[16];
+  unsigned need = 0;
+#pragma unroll
+  for (int g4 = 0; g4 < 4; ++g4) {
+    const half4_t gv = *reinterpret_cast<const half4_t *>(g4p + 8 * g4);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      g[4 * g4 + e] = (float)gv[e];
+      sg[4 * g4 + e] = logistic_estimate(g[4 * g4 + e]);
+      need |= f16_settled(sg[4 * g4 + e]) ? 0u : 1u << (4 * g4 + e);
+    }
+  }
+  while (need) {
+    const unsigned k = __builtin_ctz(need);
+    need &= need - 1;
+    float gk = g[0];
+#pragma unroll
+    for (int e = 1; e < 16; ++e)
+      gk = k == (unsigned)e ? g[e] : gk;
+    const float sk = logistic_exact(gk);
+#pragma unroll
+    for (int e = 0; e < 16; ++e)
+      sg[e] = k == (unsigned)e ? sk : sg[e];
+  }
+#pragma unroll
+  for (int g4 = 0; g4 < 4; ++g4)
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      v[g4][e] = __builtin_bit_cast(half_t, f2h(mul32(round16(sg[4 * g4 + e]), (float)v[g4][e])));
 }
 
 struct NoRows {}; // the ungated kernel's (empty) row argument
@@ -600,43 +645,413 @@ void gqa_prefill_kernel(const half_t *__restrict__ q, const half_t *__restrict__
     for (int g4 = 0; g4 < 4; ++g4)
       v[g4] = half4_t{f16_of(oacc[dt][4 * g4 + 0] * inv), f16_of(oacc[dt][4 * g4 + 1] * inv),
                       f16_of(oacc[dt][4 * g4 + 2] * inv), f16_of(oacc[dt][4 * g4 + 3] * inv)};
-    if constexpr (GATED) {
-      // The gates of this output tile: the fast logistic first, then the
-      // exact one for the few that miss the margin test, one per pass of
-      // the wave (as the standalone gate kernel does).
-      const half_t *grow = reinterpret_cast<const half_t *>(ga.qproj) +
-                           ((size_t)tq * Hq + h) * 2 * D + D + 32 * dt + 4 * hi;
-      float g[16], sg[16];
-      unsigned need = 0;
+    if constexpr (GATED)
+      gate_tile(v, reinterpret_cast<const half_t *>(ga.qproj) + ((size_t)tq * Hq + h) * 2 * D +
+                       D + 32 * dt + 4 * hi);
 #pragma unroll
-      for (int g4 = 0; g4 < 4; ++g4) {
-        const half4_t gv = *reinterpret_cast<const half4_t *>(grow + 8 * g4);
+    for (int g4 = 0; g4 < 4; ++g4)
+      *reinterpret_cast<half4_t *>(orow + 32 * dt + 8 * g4 + 4 * hi) = v[g4];
+  }
+}
+
+// d = 256 with four query heads per workgroup: eight waves, two per SIMD.
+// Waves w and w + 4 (the same SIMD: a workgroup's waves are dealt to the
+// SIMDs in turn) serve the same query head and the block's 32 query rows
+// and split the keys by 32-key tiles, the first taking the even tiles, the
+// second the odd ones, each with its own (m, l, O). While one wave of a SIMD
+// waits on LDS operands or runs its softmax, the other keeps the matrix
+// core busy. A lane holds O^T (128 registers), Q^T (64) and one 32x32
+// score block; the row sums are fp32 sums of the fp16 probabilities that
+// multiply V (v_dot2). At the end the odd-tile wave hands its (m, l, O) to
+// its partner through LDS. One step = one barrier: the four tiles of the
+// next step (K and V of tiles 2s + 2 and 2s + 3) go HBM -> LDS as the step
+// begins. GATED as in gqa_prefill_kernel: the query rows of the four heads
+// go through normRope in LDS before the loop (the workgroup's 512 threads
+// share the rows, the scales and one cos/sin table), the output through
+// the sigmoid gate.
+template <bool GATED>
+__global__ __attribute__((amdgpu_flat_work_group_size(512, 512), amdgpu_waves_per_eu(2, 2)))
+void gqa_prefill_halves_kernel(const half_t *__restrict__ q, const half_t *__restrict__ kc,
+                               const half_t *__restrict__ vc, half_t *__restrict__ out,
+                               unsigned T, unsigned Hq, unsigned Hkv, unsigned P,
+                               unsigned groups, unsigned nb, float c,
+                               typename std::conditional<GATED, GatedRows, NoRows>::type ga) {
+  constexpr int D = 256, HW = 4, KS = D / 16, DT = D / 32;
+  constexpr int BK = 32;           // keys per tile
+  constexpr int ROWB = 2 * D;      // bytes per K/V row
+  constexpr int TILEB = BK * ROWB; // 16 KB per K or V tile
+  // [set][half]: set s % 2 holds what step s reads. Named one by one so the
+  // compiler can tell the loads in flight from the LDS reads.
+  __shared__ __attribute__((aligned(1024))) char sK00[TILEB], sK01[TILEB], sK10[TILEB],
+      sK11[TILEB];
+  __shared__ __attribute__((aligned(1024))) char sV00[TILEB], sV01[TILEB], sV10[TILEB],
+      sV11[TILEB];
+  __shared__ float sML[HW][2][64];
+  // GATED: the (1 + w) weights, then the (token, pair) table of fp16 cos/sin.
+  __shared__ float sTab[GATED ? D + BM * (D / 2) : 1];
+
+  const unsigned NH = Hkv * groups;
+  const unsigned id = blockIdx.x, xcd = id % 8, j8 = id / 8;
+  unsigned hg, tbr;
+  if (8 % NH == 0 && nb % (8 / NH) == 0) {
+    const unsigned X = 8 / NH;
+    hg = xcd / X;
+    tbr = j8 * X + xcd % X;
+  } else if (NH % 8 == 0) {
+    const unsigned per = NH / 8;
+    hg = xcd * per + j8 % per;
+    tbr = j8 / per;
+  } else {
+    hg = id % NH;
+    tbr = id / NH;
+  }
+  const unsigned tb = nb - 1 - tbr;
+  const unsigned kvh = hg / groups, grp = hg % groups;
+  const unsigned wave = __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
+  const unsigned hw = wave % HW, half = wave / HW;
+  const unsigned lane = threadIdx.x % 64, r = lane % 32, hi = lane / 32;
+  const unsigned h = (kvh * groups + grp) * HW + hw;
+  const unsigned t0 = tb * BM, tq = t0 + r;
+  const bool rowValid = tq < T;
+  const unsigned tLast = min(t0 + BM, T) - 1;
+  const unsigned kend = P + tLast + 1; // keys [0, kend) can be visible
+  const unsigned ntiles = (kend + BK - 1) / BK, steps = (ntiles + 1) / 2;
+  const unsigned ju = (P + t0 + 1) / BK; // tiles [0, ju) need no mask
+  const size_t rowBytes = (size_t)Hkv * D * 2;
+  const char *kbase = reinterpret_cast<const char *>(kc) + (size_t)kvh * D * 2;
+  const char *vbase = reinterpret_cast<const char *>(vc) + (size_t)kvh * D * 2;
+
+  // Wave w moves the 1-KB pieces w and w + 8 (tile rows 2p, 2p + 1) of each
+  // tile; the XOR swizzles (K chunk c of row j at c ^ (j % 8), V chunk c at
+  // c ^ 2(j % 4)) repeat every 16 rows, so piece w + 8 is piece w 16 rows on.
+  const unsigned prow = 2 * wave + lane / 32, slot = lane % 32;
+  const unsigned koff = prow * (unsigned)rowBytes + 16 * (slot ^ (prow & 7));
+  const unsigned voff = prow * (unsigned)rowBytes + 16 * (slot ^ ((prow & 3) << 1));
+  const unsigned pstep = 16 * (unsigned)rowBytes;
+  auto tile_rsrc = [&](const char *base, unsigned tile) {
+    const unsigned first = tile * BK;
+    const unsigned rows = kend > first ? min((unsigned)BK, kend - first) : 0u;
+    return __builtin_amdgcn_make_buffer_rsrc((void *)(base + (size_t)first * rowBytes),
+                                             (short)0, (int)(rows * rowBytes), kBufferWord3);
+  };
+  auto load_tile = [&](const char *base, unsigned tile, unsigned off, char *dst) {
+    const __amdgpu_buffer_rsrc_t rs = tile_rsrc(base, tile);
+    load_lds16(rs, dst + 1024 * wave, off);
+    load_lds16(rs, dst + 1024 * (wave + 8), off + pstep);
+  };
+
+  // Operand reads. K (A of S^T, row r, chunk 2s + hi): kread[s % 4] +
+  // 128 (s / 4). V^T through the transposing read: lane j of a 16-lane
+  // group addresses row k0 + j / 4, channels 16 g + 4 (j % 4) .. +3.
+  unsigned kread[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          g[4 * g4 + e] = (float)gv[e];
-          sg[4 * g4 + e] = logistic_estimate(g[4 * g4 + e]);
-          need |= f16_settled(sg[4 * g4 + e]) ? 0u : 1u << (4 * g4 + e);
+  for (int b = 0; b < 4; ++b) {
+    kread[b] = r * ROWB + 16 * ((2 * b + hi) ^ (r & 7));
+    opaque(kread[b]);
+  }
+  const unsigned j16 = lane % 16, g = (lane / 16) % 2;
+  const unsigned vx = 2 * (j16 / 4), vb = (j16 % 4) / 2;
+  const unsigned vrow = (4 * hi + j16 / 4) * ROWB + 8 * (j16 % 2);
+  unsigned vread[2] = {vrow + 16 * ((2 * g + vb) ^ vx), vrow + 16 * ((4 + 2 * g + vb) ^ vx)};
+  opaque(vread[0]);
+  opaque(vread[1]);
+
+  half8_t qb[KS];
+  if constexpr (GATED) {
+    // Head hh's row rr sits in buffer 2 hh + rr / 16 at (rr % 16) * PITCH
+    // (rows of D + 8 halves keep the per-row chains off one bank).
+    constexpr unsigned PITCH = D + 8, CPR = D / 8;
+    auto rowp = [&](unsigned hh, unsigned rr) {
+      const unsigned bsel = 2 * hh + rr / 16;
+      char *b = bsel == 0   ? sK00
+                : bsel == 1 ? sK01
+                : bsel == 2 ? sK10
+                : bsel == 3 ? sK11
+                : bsel == 4 ? sV00
+                : bsel == 5 ? sV01
+                : bsel == 6 ? sV10
+                            : sV11;
+      return reinterpret_cast<uint16_t *>(b) + (rr % 16) * PITCH;
+    };
+    const unsigned halfrot = ga.rot / 2, nrow = min((unsigned)BM, T - t0);
+    const unsigned hbase = (kvh * groups + grp) * HW;
+    const half_t *qp = reinterpret_cast<const half_t *>(ga.qproj);
+    for (unsigned i = threadIdx.x; i < HW * nrow * CPR; i += 512) {
+      const unsigned hh = i / (nrow * CPR), rem = i % (nrow * CPR);
+      const unsigned rr = rem / CPR, cc = rem % CPR;
+      *reinterpret_cast<uint4_t *>(rowp(hh, rr) + 8 * cc) = *reinterpret_cast<const uint4_t *>(
+          qp + ((size_t)(t0 + rr) * Hq + hbase + hh) * 2 * D + 8 * cc);
+    }
+    float *w1 = sTab;
+    half2_t *cs = reinterpret_cast<half2_t *>(sTab + D); // fp16 values, stored exactly
+    for (unsigned i = threadIdx.x; i < (unsigned)D; i += 512)
+      w1[i] = 1.0f + ga.qw[i];
+    for (unsigned e = threadIdx.x; e < nrow * halfrot; e += 512) {
+      const unsigned tt = e / halfrot, i = e % halfrot;
+      const float2 v2 = rope_cos_sin(__fdiv_rn((float)(P + t0 + tt), ga.freqs[i]));
+      cs[e] = half2_t{(half_t)v2.x, (half_t)v2.y};
+    }
+    __syncthreads();
+    if (threadIdx.x < HW * nrow) {
+      // The sequential chain of one row; its chunks are read eight ahead.
+      const unsigned hh = threadIdx.x / nrow, rr = threadIdx.x % nrow;
+      const uint4_t *row = reinterpret_cast<const uint4_t *>(rowp(hh, rr));
+      float sum = 0.0f;
+      for (unsigned c8 = 0; c8 < CPR; c8 += 8) {
+        uint4_t x[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+          x[u] = row[c8 + u];
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+          sum = sumsq8(x[u], sum);
+      }
+      sML[hh][0][rr] = rms_scale_of(sum, D, ga.eps);
+    }
+    __syncthreads();
+    const unsigned pchunks = halfrot / 8, rest = CPR - 2 * pchunks;
+    for (unsigned it = threadIdx.x; it < HW * nrow * pchunks; it += 512) {
+      const unsigned hh = it / (nrow * pchunks), rem = it % (nrow * pchunks);
+      const unsigned rr = rem / pchunks, j0 = 8 * (rem % pchunks), j1 = j0 + halfrot;
+      uint16_t *row = rowp(hh, rr);
+      const float scale = sML[hh][0][rr];
+      const uint4_t qx = *reinterpret_cast<const uint4_t *>(row + j0);
+      const uint4_t qy = *reinterpret_cast<const uint4_t *>(row + j1);
+      uint4_t sx, sy;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const uint16_t bx = (uint16_t)(qx[e / 2] >> (16 * (e & 1)));
+        const uint16_t by = (uint16_t)(qy[e / 2] >> (16 * (e & 1)));
+        const float x = normed(bx, scale, w1[j0 + e]);
+        const float y = normed(by, scale, w1[j1 + e]);
+        const half2_t c2 = cs[rr * halfrot + j0 + e];
+        const float2 t2 = make_float2((float)c2[0], (float)c2[1]);
+        const uint32_t ox = rotate_x(x, y, t2), oy = rotate_y(x, y, t2);
+        if (e & 1) {
+          sx[e / 2] |= ox << 16;
+          sy[e / 2] |= oy << 16;
+        } else {
+          sx[e / 2] = ox;
+          sy[e / 2] = oy;
         }
       }
-      while (need) {
-        const unsigned k = __builtin_ctz(need);
-        need &= need - 1;
-        float gk = g[0];
-#pragma unroll
-        for (int e = 1; e < 16; ++e)
-          gk = k == (unsigned)e ? g[e] : gk;
-        const float sk = logistic_exact(gk);
-#pragma unroll
-        for (int e = 0; e < 16; ++e)
-          sg[e] = k == (unsigned)e ? sk : sg[e];
-      }
-#pragma unroll
-      for (int g4 = 0; g4 < 4; ++g4)
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-          v[g4][e] = __builtin_bit_cast(
-              half_t, f2h(mul32(round16(sg[4 * g4 + e]), (float)v[g4][e])));
+      *reinterpret_cast<uint4_t *>(row + j0) = sx;
+      *reinterpret_cast<uint4_t *>(row + j1) = sy;
     }
+    for (unsigned it = threadIdx.x; it < HW * nrow * rest; it += 512) {
+      const unsigned hh = it / (nrow * rest), rem = it % (nrow * rest);
+      const unsigned rr = rem / rest, j0 = 8 * (2 * pchunks + rem % rest);
+      uint16_t *row = rowp(hh, rr);
+      const float scale = sML[hh][0][rr];
+      const uint4_t qx = *reinterpret_cast<const uint4_t *>(row + j0);
+      uint4_t sx;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t lo = f2h(normed((uint16_t)(qx[e] & 0xFFFFu), scale, w1[j0 + 2 * e]));
+        const uint32_t hi2 = f2h(normed((uint16_t)(qx[e] >> 16), scale, w1[j0 + 2 * e + 1]));
+        sx[e] = lo | (hi2 << 16);
+      }
+      *reinterpret_cast<uint4_t *>(row + j0) = sx;
+    }
+    __syncthreads();
+    const uint16_t *myrow = rowp(hw, r);
+#pragma unroll
+    for (int s = 0; s < KS; ++s)
+      qb[s] = rowValid ? *reinterpret_cast<const half8_t *>(myrow + 16 * s + 8 * hi)
+                       : half8_t{0, 0, 0, 0, 0, 0, 0, 0};
+    __syncthreads(); // every wave has its rows before the buffers are cleared
+  } else {
+#pragma unroll
+    for (int s = 0; s < KS; ++s)
+      qb[s] = rowValid ? load8(q + ((size_t)tq * Hq + h) * D + 16 * s + 8 * hi)
+                       : half8_t{0, 0, 0, 0, 0, 0, 0, 0};
+  }
+
+  float16_t oacc[DT];
+#pragma unroll
+  for (int i = 0; i < DT; ++i)
+    oacc[i] = float16_t{0};
+  float mRef = -INFINITY, lsum = 0.0f;
+  float16_t sacc = float16_t{0};
+  half8_t pb[2]; // P^T B operands, [16-key step]
+
+  // Scores of one tile into sacc (the causal mask as the initial
+  // accumulator where the tile reaches past the block's first query).
+  auto scores = [&](const char *kb, unsigned tile) {
+    auto kld = [&](int st) {
+      return load8(reinterpret_cast<const half_t *>(kb + kread[st % 4] + 128 * (st / 4)));
+    };
+    constexpr int KA = 2; // operand reads run KA MFMAs ahead
+    half8_t ka[KA + 1];
+#pragma unroll
+    for (int st = 0; st < KA; ++st)
+      ka[st] = kld(st);
+    if (tile >= ju) {
+#pragma unroll
+      for (int v = 0; v < 16; ++v)
+        sacc[v] = tile * BK + mfma_c_row(v, hi) > P + tq ? -INFINITY : 0.0f;
+    } else {
+      sacc = float16_t{0};
+    }
+#pragma unroll
+    for (int st = 0; st < KS; ++st) {
+      if (st + KA < KS)
+        ka[(st + KA) % (KA + 1)] = kld(st + KA);
+      sacc = mfma32x32x16(ka[st % (KA + 1)], qb[st], sacc);
+      __builtin_amdgcn_sched_barrier(0); // operand reads stay KA ahead, no further
+    }
+  };
+  // Softmax of sacc against the lazily moved reference (raised only when a
+  // probability would pass 2^15; O and l rescaled then), the fp16
+  // probabilities into pb, their sum into l.
+  auto softmax = [&]() {
+    float mx = sacc[0];
+#pragma unroll
+    for (int v = 1; v < 16; ++v)
+      mx = fmaxf(mx, sacc[v]);
+    const LanePair pr = pair32(mx);
+    const float tm = fmaxf(pr.a, pr.b) * c;
+    const bool need = tm - mRef > kRaise; // false while every key so far is masked
+    const float mNew = need ? tm - kHeadroom : mRef;
+    const float alpha = need ? fast_exp2(mRef - mNew) : 1.0f;
+    mRef = mNew;
+    if (__builtin_amdgcn_ballot_w64(need) != 0) {
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt)
+        oacc[dt] *= alpha;
+      lsum *= alpha;
+    }
+    const float negm = mRef == -INFINITY ? 0.0f : -mRef;
+#pragma unroll
+    for (int m = 0; m < 2; ++m)
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        pb[m][e] = (half_t)fast_exp2(fmaf(sacc[8 * m + e], c, negm));
+    const half2_t one2{1, 1};
+#pragma unroll
+    for (int m = 0; m < 2; ++m)
+#pragma unroll
+      for (int e = 0; e < 8; e += 2)
+        lsum = __builtin_amdgcn_fdot2(half2_t{pb[m][e], pb[m][e + 1]}, one2, lsum, false);
+  };
+  // O^T += V^T P^T for one tile: output tile dt, 16-key step m.
+  auto pv = [&](const char *vbuf) {
+    auto vld = [&](int n) {
+      const int dt = n % DT, m = n / DT;
+      const unsigned o = vread[dt % 2] + 128 * (dt / 2) + ROWB * 16 * m;
+      const half4_t lo = read_tr(vbuf, o), up = read_tr(vbuf, o + 8 * ROWB);
+      return half8_t{lo[0], lo[1], lo[2], lo[3], up[0], up[1], up[2], up[3]};
+    };
+    constexpr int VA = 2;
+    half8_t va[VA + 1];
+#pragma unroll
+    for (int n = 0; n < VA; ++n)
+      va[n] = vld(n);
+#pragma unroll
+    for (int n = 0; n < 2 * DT; ++n) {
+      if (n + VA < 2 * DT)
+        va[(n + VA) % (VA + 1)] = vld(n + VA);
+      oacc[n % DT] = mfma32x32x16(va[n % (VA + 1)], pb[n / DT], oacc[n % DT]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+
+  // LDS starts zeroed: rows past the block's last key keep whatever an
+  // earlier tile left there, which must be finite.
+  {
+    const uint4_t z{0, 0, 0, 0};
+    for (unsigned i = threadIdx.x * 16; i < (unsigned)TILEB; i += 512 * 16) {
+      *reinterpret_cast<uint4_t *>(sK00 + i) = z;
+      *reinterpret_cast<uint4_t *>(sK01 + i) = z;
+      *reinterpret_cast<uint4_t *>(sK10 + i) = z;
+      *reinterpret_cast<uint4_t *>(sK11 + i) = z;
+      *reinterpret_cast<uint4_t *>(sV00 + i) = z;
+      *reinterpret_cast<uint4_t *>(sV01 + i) = z;
+      *reinterpret_cast<uint4_t *>(sV10 + i) = z;
+      *reinterpret_cast<uint4_t *>(sV11 + i) = z;
+    }
+  }
+  __syncthreads();
+  load_tile(kbase, 0, koff, sK00);
+  load_tile(kbase, 1, koff, sK01);
+  load_tile(vbase, 0, voff, sV00);
+  load_tile(vbase, 1, voff, sV01);
+
+  // Step s: set s % 2 holds K and V of tiles 2s and 2s + 1; the other set
+  // receives those of 2s + 2 and 2s + 3, requested as the step begins. Each
+  // half runs its own loop (one barrier per step in both) over its
+  // statically named buffers.
+  auto loads = [&](unsigned s, char *nkA, char *nkB, char *nvA, char *nvB) {
+    load_tile(kbase, 2 * s + 2, koff, nkA);
+    load_tile(kbase, 2 * s + 3, koff, nkB);
+    load_tile(vbase, 2 * s + 2, voff, nvA);
+    load_tile(vbase, 2 * s + 3, voff, nvB);
+  };
+  auto run = [&](unsigned first, const char *k0, const char *v0, const char *k1,
+                 const char *v1) {
+    auto step = [&](unsigned s, const char *kc_, const char *vc_, char *nkA, char *nkB,
+                    char *nvA, char *nvB) {
+      wait_loads();
+      __syncthreads();
+      loads(s, nkA, nkB, nvA, nvB);
+      if (2 * s + first < ntiles) {
+        scores(kc_, 2 * s + first);
+        softmax();
+        pv(vc_);
+      }
+    };
+    unsigned s = 0;
+    for (; s + 1 < steps; s += 2) {
+      step(s, k0, v0, sK10, sK11, sV10, sV11);
+      step(s + 1, k1, v1, sK00, sK01, sV00, sV01);
+    }
+    if (s < steps)
+      step(s, k0, v0, sK10, sK11, sV10, sV11);
+  };
+  if (half == 0)
+    run(0, sK00, sV00, sK10, sV10);
+  else
+    run(1, sK01, sV01, sK11, sV11);
+  wait_loads();
+  __syncthreads(); // every wave is done with the K/V buffers
+
+  // The odd half's (m, l, O^T) to LDS, lane-major (conflict-free): pair hw
+  // uses two 16 KB buffers, output tiles 0-3 in the first.
+  char *ma = hw == 0 ? sK00 : hw == 1 ? sK10 : hw == 2 ? sV00 : sV10;
+  char *mb = hw == 0 ? sK01 : hw == 1 ? sK11 : hw == 2 ? sV01 : sV11;
+  if (half == 1) {
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int v = 0; v < 16; ++v)
+        reinterpret_cast<float *>(dt < 4 ? ma : mb)[((dt % 4) * 16 + v) * 64 + lane] =
+            oacc[dt][v];
+    sML[hw][0][lane] = mRef;
+    sML[hw][1][lane] = lsum;
+  }
+  __syncthreads();
+  if (half == 1 || !rowValid)
+    return;
+  const float m1 = sML[hw][0][lane], l1 = sML[hw][1][lane];
+  const float M = fmaxf(mRef, m1); // mRef is finite: key 0 is visible to every row
+  const float a0 = fast_exp2(mRef - M), a1 = fast_exp2(m1 - M);
+  const LanePair lp = pair32(lsum * a0 + l1 * a1);
+  const float inv = 1.0f / (lp.a + lp.b);
+  half_t *orow = out + ((size_t)tq * Hq + h) * D;
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) {
+    const float *o1 = reinterpret_cast<const float *>(dt < 4 ? ma : mb) + (dt % 4) * 16 * 64;
+    half4_t v[4];
+#pragma unroll
+    for (int g4 = 0; g4 < 4; ++g4)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int i = 4 * g4 + e;
+        v[g4][e] = f16_of((oacc[dt][i] * a0 + o1[i * 64 + lane] * a1) * inv);
+      }
+    if constexpr (GATED)
+      gate_tile(v, reinterpret_cast<const half_t *>(ga.qproj) + ((size_t)tq * Hq + h) * 2 * D +
+                       D + 32 * dt + 4 * hi);
 #pragma unroll
     for (int g4 = 0; g4 < 4; ++g4)
       *reinterpret_cast<half4_t *>(orow + 32 * dt + 8 * g4 + 4 * hi) = v[g4];
@@ -661,6 +1076,36 @@ hipError_t launch_dw(const GqaShape &s, const uint16_t *q, const uint16_t *k,
   return hipGetLastError();
 }
 
+template <bool GATED, typename Rows>
+hipError_t launch_halves(const GqaShape &s, const uint16_t *q, const uint16_t *k,
+                         const uint16_t *v, uint16_t *out, hipStream_t stream,
+                         const Rows &rows) {
+  const float c = kLog2e / sqrtf(256.0f);
+  const unsigned G = s.Hq / s.Hkv, groups = G / 4, nb = (s.T + BM - 1) / BM;
+  hipLaunchKernelGGL((gqa_prefill_halves_kernel<GATED>), dim3(nb * s.Hkv * groups), dim3(512),
+                     0, stream, reinterpret_cast<const half_t *>(q),
+                     reinterpret_cast<const half_t *>(k), reinterpret_cast<const half_t *>(v),
+                     reinterpret_cast<half_t *>(out), s.T, s.Hq, s.Hkv, s.P, groups, nb, c,
+                     rows);
+  return hipGetLastError();
+}
+
+// The key-split kernel once the grid has at least 64 workgroups (below
+// that, as at 128 tokens, the single-wave kernel's shorter prologue wins by
+// ~1 us). LLMI_PREFILL_HALVES=0 selects the single-wave kernel always, =1
+// the key-split one always (for A/B timing). The plain and gated launches
+// take the same choice, so the two stay bit-identical.
+bool use_halves(const GqaShape &s) {
+  static const int forced = [] {
+    const char *e = getenv("LLMI_PREFILL_HALVES");
+    return e && *e ? (*e == '0' ? 0 : 1) : -1;
+  }();
+  if (forced >= 0)
+    return forced == 1;
+  const unsigned nb = (s.T + BM - 1) / BM, groups = s.Hq / s.Hkv / 4;
+  return nb * s.Hkv * groups >= 64;
+}
+
 template <int D>
 hipError_t launch_gated_d(const GqaShape &s, const uint16_t *k, const uint16_t *v,
                           uint16_t *out, const GatedRows &ga, hipStream_t stream) {
@@ -670,6 +1115,8 @@ hipError_t launch_gated_d(const GqaShape &s, const uint16_t *k, const uint16_t *
   case 2:
     return launch_dw<D, 2, true>(s, nullptr, k, v, out, stream, ga);
   case 4:
+    if (D == 256 && use_halves(s))
+      return launch_halves<true>(s, nullptr, k, v, out, stream, ga);
     return launch_dw<D, 4, true>(s, nullptr, k, v, out, stream, ga);
   }
   return hipErrorInvalidValue;
@@ -684,6 +1131,8 @@ hipError_t launch_d(const GqaShape &s, const uint16_t *q, const uint16_t *k,
   case 2:
     return launch_dw<D, 2>(s, q, k, v, out, stream);
   case 4:
+    if (D == 256 && use_halves(s))
+      return launch_halves<false>(s, q, k, v, out, stream, NoRows{});
     return launch_dw<D, 4>(s, q, k, v, out, stream);
   case 8:
     if constexpr (D == 128)

@@ -65,7 +65,8 @@ def _run_both(gpu, x, q_proj, k_proj, qw, kw, past, rot):
     (1, 0, (16, 4, 256), 64), (1, 33, (16, 4, 256), 64), (1, 4096, (16, 4, 256), 64),
     (1, 32768, (16, 4, 256), 64), (1, 700, (8, 4, 128), 32), (1, 300, (16, 8, 256), 64),
     (40, 24, (16, 4, 256), 64), (128, 0, (16, 4, 256), 64), (2048, 2048, (16, 4, 256), 64),
-    (65, 17, (16, 4, 128), 32), (33, 100, (8, 4, 256), 128)])
+    (65, 17, (16, 4, 128), 32), (33, 100, (8, 4, 256), 128),
+    (100, 37, (64, 16, 256), 64), (130, 64, (64, 16, 256), 128)])
 def test_fused_block_equals_the_unfused_ops(gpu, T, past, shape, rot):
     hq, hkv, d = shape
     print(f"gated attention T={T} past={past} shape={shape} rot={rot}", flush=True)
@@ -81,9 +82,9 @@ def test_fused_block_equals_the_unfused_ops(gpu, T, past, shape, rot):
         assert names == ["normRopeTile", "cacheAppend", "gqaPrefillGated"]
 
 
-@pytest.mark.parametrize("T,past", [(1, 4096), (40, 24)])
-def test_fused_block_against_the_oracle(gpu, T, past):
-    hq, hkv, d, rot = 16, 4, 256, 64
+@pytest.mark.parametrize("T,past,hq,hkv", [(1, 4096, 16, 4), (40, 24, 16, 4), (100, 37, 64, 16)])
+def test_fused_block_against_the_oracle(gpu, T, past, hq, hkv):
+    d, rot = 256, 64
     print(f"gated attention vs oracle T={T} past={past}", flush=True)
     x, q_proj, k_proj, qw, kw = _case(900 + T, T, hq, hkv, d, past)
     _, out, _, (kc, vc) = _run_both(gpu, x, q_proj, k_proj, qw, kw, past, rot)

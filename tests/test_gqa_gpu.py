@@ -108,6 +108,21 @@ def test_prefill_parity(gpu, shape, T, past):
     assert names == ["gqaPrefillMfma"]
 
 
+@pytest.mark.parametrize("T,past", [(97, 0), (100, 5), (100, 77), (130, 64), (128, 300),
+                                    (160, 1)])
+def test_prefill_key_split_parity(gpu, T, past):
+    """head_dim 256 with four query heads per KV head splits each head's keys
+    over a wave pair (even and odd 32-key tiles, merged at the end) once the
+    grid has at least 64 workgroups; 64 query / 16 KV heads reach that at
+    T >= 97 with small inputs. The cases cover even and odd tile counts, a
+    half with no tile in the last step, masked and unmasked tiles and a
+    partial last query block."""
+    hq, hkv, d = 64, 16, 256
+    print(f"prefill key split T={T} past={past}", flush=True)
+    x = oracle.make_gqa_inputs(300 + T + past, T, hq, hkv, d, past)
+    _check(_run(x, gpu), oracle.gqa_dense_f64(x.q, x.k_cache, x.v_cache, past))
+
+
 def test_prefill_cfg1(gpu):
     """BASELINE cfg1: 128 tokens, past 0, 16/4 heads, head_dim 256."""
     print("prefill cfg1", flush=True)
