@@ -654,29 +654,34 @@ void gqa_prefill_kernel(const half_t *__restrict__ q, const half_t *__restrict__
   }
 }
 
-// d = 256 with four query heads per workgroup: eight waves, two per SIMD.
-// Waves w and w + 4 (the same SIMD: a workgroup's waves are dealt to the
-// SIMDs in turn) serve the same query head and the block's 32 query rows
-// and split the keys by 32-key tiles, the first taking the even tiles, the
-// second the odd ones, each with its own (m, l, O). While one wave of a SIMD
-// waits on LDS operands or runs its softmax, the other keeps the matrix
-// core busy. A lane holds O^T (128 registers), Q^T (64) and one 32x32
+// d = 256 with an even number of query heads per KV head: eight waves, two
+// per SIMD, over a pair of token blocks (nb - 1 - p and p: their key counts
+// add up to the same total for every pair, which balances the causal
+// triangle across workgroups) and two query heads. Wave w serves block
+// w / 4 (the long one first), head (w / 2) % 2 and key half w % 2: each
+// (block, head) has a wave pair that splits the keys by 32-key tiles, the
+// even tiles to one wave, the odd ones to the other, each with its own
+// (m, l, O). SIMD j (a workgroup's waves are dealt to the SIMDs in turn)
+// runs wave j of the long block and wave j of the short one: while one
+// waits on LDS operands or runs its softmax the other keeps the matrix core
+// busy, and once the short block is done the long block's wave has the
+// SIMD to itself. A lane holds O^T (128 registers), Q^T (64) and one 32x32
 // score block; the row sums are fp32 sums of the fp16 probabilities that
-// multiply V (v_dot2). At the end the odd-tile wave hands its (m, l, O) to
+// multiply V (v_dot2). At the end each odd-tile wave hands its (m, l, O) to
 // its partner through LDS. One step = one barrier: the four tiles of the
-// next step (K and V of tiles 2s + 2 and 2s + 3) go HBM -> LDS as the step
-// begins. GATED as in gqa_prefill_kernel: the query rows of the four heads
-// go through normRope in LDS before the loop (the workgroup's 512 threads
-// share the rows, the scales and one cos/sin table), the output through
-// the sigmoid gate.
+// next step (K and V of tiles 2s + 2 and 2s + 3, shared by both blocks) go
+// HBM -> LDS as the step begins. GATED as in gqa_prefill_kernel: the query
+// rows go through normRope in LDS before the loop (the workgroup's 512
+// threads share the rows, the scales and one cos/sin table per block), the
+// output through the sigmoid gate.
 template <bool GATED>
 __global__ __attribute__((amdgpu_flat_work_group_size(512, 512), amdgpu_waves_per_eu(2, 2)))
 void gqa_prefill_halves_kernel(const half_t *__restrict__ q, const half_t *__restrict__ kc,
                                const half_t *__restrict__ vc, half_t *__restrict__ out,
                                unsigned T, unsigned Hq, unsigned Hkv, unsigned P,
-                               unsigned groups, unsigned nb, float c,
+                               unsigned hpairs, unsigned nb, float c,
                                typename std::conditional<GATED, GatedRows, NoRows>::type ga) {
-  constexpr int D = 256, HW = 4, KS = D / 16, DT = D / 32;
+  constexpr int D = 256, KS = D / 16, DT = D / 32;
   constexpr int BK = 32;           // keys per tile
   constexpr int ROWB = 2 * D;      // bytes per K/V row
   constexpr int TILEB = BK * ROWB; // 16 KB per K or V tile
@@ -686,36 +691,43 @@ void gqa_prefill_halves_kernel(const half_t *__restrict__ q, const half_t *__res
       sK11[TILEB];
   __shared__ __attribute__((aligned(1024))) char sV00[TILEB], sV01[TILEB], sV10[TILEB],
       sV11[TILEB];
-  __shared__ float sML[HW][2][64];
+  __shared__ float sML[4][2][64];
   // GATED: the (1 + w) weights, then the (token, pair) table of fp16 cos/sin.
   __shared__ float sTab[GATED ? D + BM * (D / 2) : 1];
 
-  const unsigned NH = Hkv * groups;
+  // Workgroup -> (block pair, KV head, head pair): each XCD (workgroups are
+  // dealt round-robin over 8) serves as few KV heads as possible, so its L2
+  // holds their K/V.
+  const unsigned NH = Hkv * hpairs, npairs = (nb + 1) / 2;
   const unsigned id = blockIdx.x, xcd = id % 8, j8 = id / 8;
-  unsigned hg, tbr;
-  if (8 % NH == 0 && nb % (8 / NH) == 0) {
+  unsigned hg, pr;
+  if (8 % NH == 0 && npairs % (8 / NH) == 0) {
     const unsigned X = 8 / NH;
     hg = xcd / X;
-    tbr = j8 * X + xcd % X;
+    pr = j8 * X + xcd % X;
   } else if (NH % 8 == 0) {
     const unsigned per = NH / 8;
     hg = xcd * per + j8 % per;
-    tbr = j8 / per;
+    pr = j8 / per;
   } else {
     hg = id % NH;
-    tbr = id / NH;
+    pr = id / NH;
   }
-  const unsigned tb = nb - 1 - tbr;
-  const unsigned kvh = hg / groups, grp = hg % groups;
+  const unsigned kvh = hg / hpairs, hp = hg % hpairs;
+  const unsigned bL = nb - 1 - pr, bS = pr;
   const unsigned wave = __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
-  const unsigned hw = wave % HW, half = wave / HW;
+  const unsigned blk = wave / 4, hs = (wave / 2) % 2, half = wave % 2;
+  const unsigned pi = 2 * blk + hs; // (block, head) of this wave
+  const bool idle = blk == 1 && bS == bL; // nb odd: the middle block pairs with itself
   const unsigned lane = threadIdx.x % 64, r = lane % 32, hi = lane / 32;
-  const unsigned h = (kvh * groups + grp) * HW + hw;
-  const unsigned t0 = tb * BM, tq = t0 + r;
-  const bool rowValid = tq < T;
-  const unsigned tLast = min(t0 + BM, T) - 1;
-  const unsigned kend = P + tLast + 1; // keys [0, kend) can be visible
+  const unsigned h = (kvh * hpairs + hp) * 2 + hs;
+  const unsigned t0 = (blk ? bS : bL) * BM, tq = t0 + r;
+  const bool rowValid = tq < T && !idle;
+  // Keys [0, kend) can be visible to the long block; this wave's block needs
+  // its first `mine` tiles.
+  const unsigned kend = P + min(bL * BM + BM, T);
   const unsigned ntiles = (kend + BK - 1) / BK, steps = (ntiles + 1) / 2;
+  const unsigned mine = idle ? 0u : (P + min(t0 + BM, T) + BK - 1) / BK;
   const unsigned ju = (P + t0 + 1) / BK; // tiles [0, ju) need no mask
   const size_t rowBytes = (size_t)Hkv * D * 2;
   const char *kbase = reinterpret_cast<const char *>(kc) + (size_t)kvh * D * 2;
@@ -758,11 +770,12 @@ void gqa_prefill_halves_kernel(const half_t *__restrict__ q, const half_t *__res
 
   half8_t qb[KS];
   if constexpr (GATED) {
-    // Head hh's row rr sits in buffer 2 hh + rr / 16 at (rr % 16) * PITCH
-    // (rows of D + 8 halves keep the per-row chains off one bank).
+    // (block, head) pair pp's row rr sits in buffer 2 pp + rr / 16 at
+    // (rr % 16) * PITCH (rows of D + 8 halves keep the per-row chains off
+    // one bank).
     constexpr unsigned PITCH = D + 8, CPR = D / 8;
-    auto rowp = [&](unsigned hh, unsigned rr) {
-      const unsigned bsel = 2 * hh + rr / 16;
+    auto rowp = [&](unsigned pp, unsigned rr) {
+      const unsigned bsel = 2 * pp + rr / 16;
       char *b = bsel == 0   ? sK00
                 : bsel == 1 ? sK01
                 : bsel == 2 ? sK10
@@ -773,88 +786,100 @@ void gqa_prefill_halves_kernel(const half_t *__restrict__ q, const half_t *__res
                             : sV11;
       return reinterpret_cast<uint16_t *>(b) + (rr % 16) * PITCH;
     };
-    const unsigned halfrot = ga.rot / 2, nrow = min((unsigned)BM, T - t0);
-    const unsigned hbase = (kvh * groups + grp) * HW;
+    const unsigned halfrot = ga.rot / 2;
+    const unsigned nrL = min((unsigned)BM, T - bL * BM), nrS = min((unsigned)BM, T - bS * BM);
+    auto nrow = [&](unsigned pp) { return pp < 2 ? nrL : nrS; };
+    auto first_tok = [&](unsigned pp) { return (pp < 2 ? bL : bS) * BM; };
     const half_t *qp = reinterpret_cast<const half_t *>(ga.qproj);
-    for (unsigned i = threadIdx.x; i < HW * nrow * CPR; i += 512) {
-      const unsigned hh = i / (nrow * CPR), rem = i % (nrow * CPR);
+    for (unsigned i = threadIdx.x; i < 4 * BM * CPR; i += 512) {
+      const unsigned pp = i / (BM * CPR), rem = i % (BM * CPR);
       const unsigned rr = rem / CPR, cc = rem % CPR;
-      *reinterpret_cast<uint4_t *>(rowp(hh, rr) + 8 * cc) = *reinterpret_cast<const uint4_t *>(
-          qp + ((size_t)(t0 + rr) * Hq + hbase + hh) * 2 * D + 8 * cc);
+      if (rr < nrow(pp))
+        *reinterpret_cast<uint4_t *>(rowp(pp, rr) + 8 * cc) =
+            *reinterpret_cast<const uint4_t *>(
+                qp + ((size_t)(first_tok(pp) + rr) * Hq + (kvh * hpairs + hp) * 2 + pp % 2) *
+                         2 * D +
+                8 * cc);
     }
     float *w1 = sTab;
     half2_t *cs = reinterpret_cast<half2_t *>(sTab + D); // fp16 values, stored exactly
     for (unsigned i = threadIdx.x; i < (unsigned)D; i += 512)
       w1[i] = 1.0f + ga.qw[i];
-    for (unsigned e = threadIdx.x; e < nrow * halfrot; e += 512) {
-      const unsigned tt = e / halfrot, i = e % halfrot;
-      const float2 v2 = rope_cos_sin(__fdiv_rn((float)(P + t0 + tt), ga.freqs[i]));
-      cs[e] = half2_t{(half_t)v2.x, (half_t)v2.y};
-    }
     __syncthreads();
-    if (threadIdx.x < HW * nrow) {
+    if (threadIdx.x < 4 * BM) {
       // The sequential chain of one row; its chunks are read eight ahead.
-      const unsigned hh = threadIdx.x / nrow, rr = threadIdx.x % nrow;
-      const uint4_t *row = reinterpret_cast<const uint4_t *>(rowp(hh, rr));
-      float sum = 0.0f;
-      for (unsigned c8 = 0; c8 < CPR; c8 += 8) {
-        uint4_t x[8];
+      const unsigned pp = threadIdx.x / BM, rr = threadIdx.x % BM;
+      if (rr < nrow(pp)) {
+        const uint4_t *row = reinterpret_cast<const uint4_t *>(rowp(pp, rr));
+        float sum = 0.0f;
+        for (unsigned c8 = 0; c8 < CPR; c8 += 8) {
+          uint4_t x[8];
 #pragma unroll
-        for (int u = 0; u < 8; ++u)
-          x[u] = row[c8 + u];
+          for (int u = 0; u < 8; ++u)
+            x[u] = row[c8 + u];
 #pragma unroll
-        for (int u = 0; u < 8; ++u)
-          sum = sumsq8(x[u], sum);
-      }
-      sML[hh][0][rr] = rms_scale_of(sum, D, ga.eps);
-    }
-    __syncthreads();
-    const unsigned pchunks = halfrot / 8, rest = CPR - 2 * pchunks;
-    for (unsigned it = threadIdx.x; it < HW * nrow * pchunks; it += 512) {
-      const unsigned hh = it / (nrow * pchunks), rem = it % (nrow * pchunks);
-      const unsigned rr = rem / pchunks, j0 = 8 * (rem % pchunks), j1 = j0 + halfrot;
-      uint16_t *row = rowp(hh, rr);
-      const float scale = sML[hh][0][rr];
-      const uint4_t qx = *reinterpret_cast<const uint4_t *>(row + j0);
-      const uint4_t qy = *reinterpret_cast<const uint4_t *>(row + j1);
-      uint4_t sx, sy;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const uint16_t bx = (uint16_t)(qx[e / 2] >> (16 * (e & 1)));
-        const uint16_t by = (uint16_t)(qy[e / 2] >> (16 * (e & 1)));
-        const float x = normed(bx, scale, w1[j0 + e]);
-        const float y = normed(by, scale, w1[j1 + e]);
-        const half2_t c2 = cs[rr * halfrot + j0 + e];
-        const float2 t2 = make_float2((float)c2[0], (float)c2[1]);
-        const uint32_t ox = rotate_x(x, y, t2), oy = rotate_y(x, y, t2);
-        if (e & 1) {
-          sx[e / 2] |= ox << 16;
-          sy[e / 2] |= oy << 16;
-        } else {
-          sx[e / 2] = ox;
-          sy[e / 2] = oy;
+          for (int u = 0; u < 8; ++u)
+            sum = sumsq8(x[u], sum);
         }
+        sML[pp][0][rr] = rms_scale_of(sum, D, ga.eps);
       }
-      *reinterpret_cast<uint4_t *>(row + j0) = sx;
-      *reinterpret_cast<uint4_t *>(row + j1) = sy;
     }
-    for (unsigned it = threadIdx.x; it < HW * nrow * rest; it += 512) {
-      const unsigned hh = it / (nrow * rest), rem = it % (nrow * rest);
-      const unsigned rr = rem / rest, j0 = 8 * (2 * pchunks + rem % rest);
-      uint16_t *row = rowp(hh, rr);
-      const float scale = sML[hh][0][rr];
-      const uint4_t qx = *reinterpret_cast<const uint4_t *>(row + j0);
-      uint4_t sx;
+    const unsigned pchunks = halfrot / 8, rest = CPR - 2 * pchunks;
+    for (unsigned bb = 0; bb < 2; ++bb) {
+      // The cos/sin table of this block's tokens, then its two heads' rows.
+      const unsigned tok0 = bb ? bS * BM : bL * BM, nr = bb ? nrS : nrL;
+      for (unsigned e = threadIdx.x; e < nr * halfrot; e += 512) {
+        const unsigned tt = e / halfrot, i = e % halfrot;
+        const float2 v2 = rope_cos_sin(__fdiv_rn((float)(P + tok0 + tt), ga.freqs[i]));
+        cs[e] = half2_t{(half_t)v2.x, (half_t)v2.y};
+      }
+      __syncthreads(); // the table (and, the first time, every scale)
+      for (unsigned it = threadIdx.x; it < 2 * nr * pchunks; it += 512) {
+        const unsigned pp = 2 * bb + it / (nr * pchunks), rem = it % (nr * pchunks);
+        const unsigned rr = rem / pchunks, j0 = 8 * (rem % pchunks), j1 = j0 + halfrot;
+        uint16_t *row = rowp(pp, rr);
+        const float scale = sML[pp][0][rr];
+        const uint4_t qx = *reinterpret_cast<const uint4_t *>(row + j0);
+        const uint4_t qy = *reinterpret_cast<const uint4_t *>(row + j1);
+        uint4_t sx, sy;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const uint32_t lo = f2h(normed((uint16_t)(qx[e] & 0xFFFFu), scale, w1[j0 + 2 * e]));
-        const uint32_t hi2 = f2h(normed((uint16_t)(qx[e] >> 16), scale, w1[j0 + 2 * e + 1]));
-        sx[e] = lo | (hi2 << 16);
+        for (int e = 0; e < 8; ++e) {
+          const uint16_t bx = (uint16_t)(qx[e / 2] >> (16 * (e & 1)));
+          const uint16_t by = (uint16_t)(qy[e / 2] >> (16 * (e & 1)));
+          const float x = normed(bx, scale, w1[j0 + e]);
+          const float y = normed(by, scale, w1[j1 + e]);
+          const half2_t c2 = cs[rr * halfrot + j0 + e];
+          const float2 t2 = make_float2((float)c2[0], (float)c2[1]);
+          const uint32_t ox = rotate_x(x, y, t2), oy = rotate_y(x, y, t2);
+          if (e & 1) {
+            sx[e / 2] |= ox << 16;
+            sy[e / 2] |= oy << 16;
+          } else {
+            sx[e / 2] = ox;
+            sy[e / 2] = oy;
+          }
+        }
+        *reinterpret_cast<uint4_t *>(row + j0) = sx;
+        *reinterpret_cast<uint4_t *>(row + j1) = sy;
       }
-      *reinterpret_cast<uint4_t *>(row + j0) = sx;
+      for (unsigned it = threadIdx.x; it < 2 * nr * rest; it += 512) {
+        const unsigned pp = 2 * bb + it / (nr * rest), rem = it % (nr * rest);
+        const unsigned rr = rem / rest, j0 = 8 * (2 * pchunks + rem % rest);
+        uint16_t *row = rowp(pp, rr);
+        const float scale = sML[pp][0][rr];
+        const uint4_t qx = *reinterpret_cast<const uint4_t *>(row + j0);
+        uint4_t sx;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const uint32_t lo = f2h(normed((uint16_t)(qx[e] & 0xFFFFu), scale, w1[j0 + 2 * e]));
+          const uint32_t hi2 = f2h(normed((uint16_t)(qx[e] >> 16), scale, w1[j0 + 2 * e + 1]));
+          sx[e] = lo | (hi2 << 16);
+        }
+        *reinterpret_cast<uint4_t *>(row + j0) = sx;
+      }
+      __syncthreads(); // the table is free again
     }
-    __syncthreads();
-    const uint16_t *myrow = rowp(hw, r);
+    const uint16_t *myrow = rowp(pi, r);
 #pragma unroll
     for (int s = 0; s < KS; ++s)
       qb[s] = rowValid ? *reinterpret_cast<const half8_t *>(myrow + 16 * s + 8 * hi)
@@ -994,7 +1019,7 @@ void gqa_prefill_halves_kernel(const half_t *__restrict__ q, const half_t *__res
       wait_loads();
       __syncthreads();
       loads(s, nkA, nkB, nvA, nvB);
-      if (2 * s + first < ntiles) {
+      if (2 * s + first < mine) {
         scores(kc_, 2 * s + first);
         softmax();
         pv(vc_);
@@ -1015,10 +1040,10 @@ void gqa_prefill_halves_kernel(const half_t *__restrict__ q, const half_t *__res
   wait_loads();
   __syncthreads(); // every wave is done with the K/V buffers
 
-  // The odd half's (m, l, O^T) to LDS, lane-major (conflict-free): pair hw
+  // The odd half's (m, l, O^T) to LDS, lane-major (conflict-free): pair pi
   // uses two 16 KB buffers, output tiles 0-3 in the first.
-  char *ma = hw == 0 ? sK00 : hw == 1 ? sK10 : hw == 2 ? sV00 : sV10;
-  char *mb = hw == 0 ? sK01 : hw == 1 ? sK11 : hw == 2 ? sV01 : sV11;
+  char *ma = pi == 0 ? sK00 : pi == 1 ? sK10 : pi == 2 ? sV00 : sV10;
+  char *mb = pi == 0 ? sK01 : pi == 1 ? sK11 : pi == 2 ? sV01 : sV11;
   if (half == 1) {
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt)
@@ -1026,13 +1051,13 @@ void gqa_prefill_halves_kernel(const half_t *__restrict__ q, const half_t *__res
       for (int v = 0; v < 16; ++v)
         reinterpret_cast<float *>(dt < 4 ? ma : mb)[((dt % 4) * 16 + v) * 64 + lane] =
             oacc[dt][v];
-    sML[hw][0][lane] = mRef;
-    sML[hw][1][lane] = lsum;
+    sML[pi][0][lane] = mRef;
+    sML[pi][1][lane] = lsum;
   }
   __syncthreads();
   if (half == 1 || !rowValid)
     return;
-  const float m1 = sML[hw][0][lane], l1 = sML[hw][1][lane];
+  const float m1 = sML[pi][0][lane], l1 = sML[pi][1][lane];
   const float M = fmaxf(mRef, m1); // mRef is finite: key 0 is visible to every row
   const float a0 = fast_exp2(mRef - M), a1 = fast_exp2(m1 - M);
   const LanePair lp = pair32(lsum * a0 + l1 * a1);
@@ -1081,11 +1106,11 @@ hipError_t launch_halves(const GqaShape &s, const uint16_t *q, const uint16_t *k
                          const uint16_t *v, uint16_t *out, hipStream_t stream,
                          const Rows &rows) {
   const float c = kLog2e / sqrtf(256.0f);
-  const unsigned G = s.Hq / s.Hkv, groups = G / 4, nb = (s.T + BM - 1) / BM;
-  hipLaunchKernelGGL((gqa_prefill_halves_kernel<GATED>), dim3(nb * s.Hkv * groups), dim3(512),
-                     0, stream, reinterpret_cast<const half_t *>(q),
+  const unsigned G = s.Hq / s.Hkv, hpairs = G / 2, nb = (s.T + BM - 1) / BM;
+  hipLaunchKernelGGL((gqa_prefill_halves_kernel<GATED>), dim3((nb + 1) / 2 * s.Hkv * hpairs),
+                     dim3(512), 0, stream, reinterpret_cast<const half_t *>(q),
                      reinterpret_cast<const half_t *>(k), reinterpret_cast<const half_t *>(v),
-                     reinterpret_cast<half_t *>(out), s.T, s.Hq, s.Hkv, s.P, groups, nb, c,
+                     reinterpret_cast<half_t *>(out), s.T, s.Hq, s.Hkv, s.P, hpairs, nb, c,
                      rows);
   return hipGetLastError();
 }
@@ -1102,8 +1127,8 @@ bool use_halves(const GqaShape &s) {
   }();
   if (forced >= 0)
     return forced == 1;
-  const unsigned nb = (s.T + BM - 1) / BM, groups = s.Hq / s.Hkv / 4;
-  return nb * s.Hkv * groups >= 64;
+  const unsigned nb = (s.T + BM - 1) / BM, hpairs = s.Hq / s.Hkv / 2;
+  return (nb + 1) / 2 * s.Hkv * hpairs >= 64;
 }
 
 template <int D>
