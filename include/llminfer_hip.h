@@ -92,6 +92,39 @@ typedef struct L2Params {
   float epsilon, scale;
 } L2Params;
 
+/* lib/Backend/Metal/Kernels/GraphParams.h:12-14 */
+typedef struct QuantizeParams {
+  unsigned rows, width, groups;
+} QuantizeParams;
+
+/* lib/Backend/Metal/Kernels/GraphParams.h:25-28 (epilogue: LinearEpilogue
+ * below; epilogueBlock: the column block of LLMI_LINEAR_SIGMOID_COLUMNS) */
+typedef struct LinearW8Params {
+  unsigned outputWidth, firstRow, groups, rows, columns;
+  unsigned epilogue, epilogueBlock;
+} LinearW8Params;
+
+/* lib/Backend/Metal/Kernels/GraphParams.h:8-10 */
+typedef struct GroupedEmbedParams {
+  unsigned tokens, hidden, firstRow, rowCount, groups;
+} GroupedEmbedParams;
+
+/* lib/Backend/Metal/Kernels/ReferenceParams.h:4-6 */
+typedef struct EmbedParams {
+  unsigned tokens, hidden, firstRow, rowCount;
+} EmbedParams;
+
+/* LinearEpilogue, lib/Backend/Metal/Kernels/ReferenceParams.h:8-16 */
+enum llmi_linear_epilogue {
+  LLMI_LINEAR_NONE = 0,
+  LLMI_LINEAR_SILU = 1,
+  LLMI_LINEAR_SILU_MUL = 2,
+  LLMI_LINEAR_SIGMOID_COLUMNS = 3,
+  LLMI_LINEAR_SILU_F32 = 4,
+  LLMI_LINEAR_DELTA_BETA = 5,
+  LLMI_LINEAR_DELTA_DECAY = 6
+};
+
 enum llmi_hip_status {
   LLMI_HIP_OK = 0,
   LLMI_HIP_INVALID_ARGUMENT = 1, /* bad shape/pointer; nothing launched */
@@ -114,7 +147,11 @@ enum llmi_hip_op {
   LLMI_HIP_OP_L2_NORM = 9,              /* params: L2Params */
   LLMI_HIP_OP_DELTA_GATES = 10,         /* params: RowParams (rows = tokens, width = heads) */
   LLMI_HIP_OP_GATED_RMS_NORM = 11,      /* params: RowParams */
-  LLMI_HIP_OP_GATED_ATTENTION = 12      /* params: GqaParams */
+  LLMI_HIP_OP_GATED_ATTENTION = 12,     /* params: GqaParams */
+  LLMI_HIP_OP_QUANTIZE_ACTIVATION = 13, /* params: QuantizeParams */
+  LLMI_HIP_OP_LINEAR_W8A8 = 14,         /* params: LinearW8Params */
+  LLMI_HIP_OP_EMBEDDING_W8 = 15,        /* params: GroupedEmbedParams */
+  LLMI_HIP_OP_EMBEDDING = 16            /* params: EmbedParams */
 };
 
 /* ---------------------------------------------------------------- KvAppend
@@ -355,6 +392,56 @@ LLMI_HIP_API int llmi_hip_l2_norm_delta_gated_norm(
     const float *decay, float *state, const uint16_t *gate, const float *norm_weight,
     uint16_t *out, GraphDeltaParams p, float qk_epsilon, float q_scale, float norm_epsilon,
     void *workspace, size_t workspace_bytes, void *stream);
+
+/* ------------------------------------------------------- W8A8 projections
+ * The quantized projection path of the whole-graph plan (lowered at
+ * MetalExecutionPlan.cpp:464-510 for LinearW8A8, :566-580 for
+ * QuantizeActivation, :435-462 for EmbeddingGather). Integer parts are exact; the fp32 arithmetic and every fp16
+ * rounding follow the reference kernels' expressions, with exp and log
+ * correctly rounded to fp32.
+ *
+ * quantizeActivation (Graph.metal:33-68): input [rows][width] fp16 ->
+ * quantized [rows][groups * 32] int8 (groups = ceil(width / 32), the tail of
+ * the last group zero), scales [rows][groups] fp32 (max |x| / 127 of the
+ * group; 1 for an all-zero group); a group holding a non-finite value is
+ * quantized to zeros with scale 1 and ORs 1 into *invalid (may be NULL). */
+LLMI_HIP_API int llmi_hip_quantize_activation(const uint16_t *input, int8_t *quantized,
+                                              float *scales, uint32_t *invalid,
+                                              QuantizeParams p, void *stream);
+
+/* linearW8A8Gemv (rows == 1) / linearW8A8Gemm (W8A8.metal:28-113; launch
+ * shape LinearW8Launch.h:14-21) with storeLinear (Reference.metal:14-47):
+ * activation [rows][groups * 32] int8 and act_scales [rows][groups] fp32 (a
+ * quantizeActivation result); weight [columns][groups * 32] int8 and
+ * weight_scales [columns][groups] fp16 (one shard of the projection: output
+ * columns firstRow .. firstRow + columns - 1). For each (row, column): the
+ * exact int32 dot of each 32-wide group, times the activation scale, times
+ * the weight scale, summed in fp32 by 16 (one row) or 8 interleaved group
+ * lanes combined by an xor butterfly -- the reference's order -- then
+ * rounded to fp16 and passed through the epilogue into
+ * output[row * outputWidth + firstRow + column]: fp16, or fp32 for
+ * LLMI_LINEAR_SILU_F32 / DELTA_BETA / DELTA_DECAY. aux is the fp16
+ * multiplier of SILU_MUL (same index as the output) or the fp32 A_log of
+ * DELTA_DECAY (by column), bias the fp32 dt bias of DELTA_DECAY; otherwise
+ * both may be NULL. */
+LLMI_HIP_API int llmi_hip_linear_w8a8(const int8_t *activation, const float *act_scales,
+                                      const int8_t *weight, const uint16_t *weight_scales,
+                                      void *output, const void *aux, const float *bias,
+                                      LinearW8Params p, void *stream);
+
+/* embeddingW8 (Graph.metal:16-31): for token t with id in [firstRow,
+ * firstRow + rowCount), output[t][c] = fp16(weight[id - firstRow][c] *
+ * scales[id - firstRow][c / 32]), weight rows groups * 32 int8 wide, scales
+ * fp16; rows of other ids are left as they are (another shard writes them).
+ * ids uint32. */
+LLMI_HIP_API int llmi_hip_embedding_w8(const uint32_t *ids, const int8_t *weight,
+                                       const uint16_t *scales, uint16_t *output,
+                                       GroupedEmbedParams p, void *stream);
+
+/* embedding (Reference.metal:49-58): fp16 rows [rowCount][hidden], copied
+ * for ids in [firstRow, firstRow + rowCount). */
+LLMI_HIP_API int llmi_hip_embedding(const uint32_t *ids, const uint16_t *weight,
+                                    uint16_t *output, EmbedParams p, void *stream);
 
 /* ----------------------------------------------------------------- helpers */
 

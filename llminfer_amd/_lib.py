@@ -31,6 +31,14 @@ OP_L2_NORM = 9
 OP_DELTA_GATES = 10
 OP_GATED_RMS_NORM = 11
 OP_GATED_ATTENTION = 12
+OP_QUANTIZE_ACTIVATION = 13
+OP_LINEAR_W8A8 = 14
+OP_EMBEDDING_W8 = 15
+OP_EMBEDDING = 16
+
+# LinearEpilogue (ReferenceParams.h:8-16)
+LINEAR_NONE, LINEAR_SILU, LINEAR_SILU_MUL, LINEAR_SIGMOID_COLUMNS = 0, 1, 2, 3
+LINEAR_SILU_F32, LINEAR_DELTA_BETA, LINEAR_DELTA_DECAY = 4, 5, 6
 
 NOALLOC_SCRATCH_BYTES = 8 << 20  # LLMI_HIP_NOALLOC_SCRATCH_BYTES
 
@@ -65,6 +73,23 @@ class ConvParams(C.Structure):
 class L2Params(C.Structure):
     _fields_ = [("rows", C.c_uint), ("width", C.c_uint), ("epsilon", C.c_float),
                 ("scale", C.c_float)]
+
+
+class QuantizeParams(C.Structure):
+    _fields_ = [(n, C.c_uint) for n in ("rows", "width", "groups")]
+
+
+class LinearW8Params(C.Structure):
+    _fields_ = [(n, C.c_uint) for n in ("outputWidth", "firstRow", "groups", "rows", "columns",
+                                        "epilogue", "epilogueBlock")]
+
+
+class GroupedEmbedParams(C.Structure):
+    _fields_ = [(n, C.c_uint) for n in ("tokens", "hidden", "firstRow", "rowCount", "groups")]
+
+
+class EmbedParams(C.Structure):
+    _fields_ = [(n, C.c_uint) for n in ("tokens", "hidden", "firstRow", "rowCount")]
 
 
 class GqaParams(C.Structure):
@@ -130,6 +155,10 @@ SIGNATURES = {
     "llmi_hip_l2_norm_delta_gated_norm": (C.c_int, [_P, _P, _P, _P, _P, _P, _P, _P, _P,
                                                     GraphDeltaParams, C.c_float, C.c_float,
                                                     C.c_float, _P, _SZ, _P]),
+    "llmi_hip_quantize_activation": (C.c_int, [_P, _P, _P, _P, QuantizeParams, _P]),
+    "llmi_hip_linear_w8a8": (C.c_int, [_P, _P, _P, _P, _P, _P, _P, LinearW8Params, _P]),
+    "llmi_hip_embedding_w8": (C.c_int, [_P, _P, _P, _P, GroupedEmbedParams, _P]),
+    "llmi_hip_embedding": (C.c_int, [_P, _P, _P, EmbedParams, _P]),
     "llmi_hip_workspace_init": (C.c_int, [_P, _SZ, _P]),
     "llmi_hip_dispatch_count": (C.c_uint, [C.c_int, _P]),
     "llmi_hip_kernel_name": (C.c_char_p, [C.c_int, _P, C.c_uint]),

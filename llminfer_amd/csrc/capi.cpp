@@ -237,6 +237,100 @@ int llmi_hip_delta_gates(const uint16_t *a, const uint16_t *b, const float *a_lo
                   "deltaGates");
 }
 
+// ------------------------------------------------------ W8A8 projections
+
+static bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+int llmi_hip_quantize_activation(const uint16_t *input, int8_t *quantized, float *scales,
+                                 uint32_t *invalid, QuantizeParams p, void *stream) {
+  if (p.rows == 0 || p.width == 0)
+    return LLMI_HIP_OK;
+  if (!input || !quantized || !scales)
+    return fail(LLMI_HIP_INVALID_ARGUMENT, "quantizeActivation: null buffer");
+  if (p.groups != (p.width + 31) / 32)
+    return fail(LLMI_HIP_INVALID_ARGUMENT,
+                "quantizeActivation: %u groups for width %u (32-element groups: %u)",
+                p.groups, p.width, (p.width + 31) / 32);
+  if (!fits32(p.rows, p.groups, 32) || !fits32(p.rows, p.width, 1))
+    return fail(LLMI_HIP_INVALID_ARGUMENT,
+                "quantizeActivation: exceeds the 32-bit index range");
+  if (!aligned16(quantized))
+    return fail(LLMI_HIP_UNSUPPORTED, "quantizeActivation: quantized rows not 16-byte aligned");
+  return launched(launch_quantize_activation(input, quantized, scales, invalid, p.rows, p.width,
+                                             p.groups, static_cast<hipStream_t>(stream)),
+                  "quantizeActivation");
+}
+
+static int check_linear_w8(const LinearW8Params &p) {
+  if (p.epilogue > LLMI_LINEAR_DELTA_DECAY)
+    return fail(LLMI_HIP_INVALID_ARGUMENT, "linearW8A8: unknown epilogue %u", p.epilogue);
+  if (p.epilogue == LLMI_LINEAR_SIGMOID_COLUMNS && p.epilogueBlock == 0)
+    return fail(LLMI_HIP_INVALID_ARGUMENT, "linearW8A8: sigmoid columns need a block width");
+  if (p.groups == 0)
+    return fail(LLMI_HIP_INVALID_ARGUMENT, "linearW8A8: no groups");
+  if ((uint64_t)p.firstRow + p.columns > p.outputWidth)
+    return fail(LLMI_HIP_INVALID_ARGUMENT,
+                "linearW8A8: columns %u from %u past the output width %u", p.columns,
+                p.firstRow, p.outputWidth);
+  if (!fits32(p.rows, p.groups, 32) || !fits32(p.columns, p.groups, 32) ||
+      !fits32(p.rows, p.outputWidth, 1))
+    return fail(LLMI_HIP_INVALID_ARGUMENT, "linearW8A8: exceeds the 32-bit index range");
+  return LLMI_HIP_OK;
+}
+
+int llmi_hip_linear_w8a8(const int8_t *activation, const float *act_scales,
+                         const int8_t *weight, const uint16_t *weight_scales, void *output,
+                         const void *aux, const float *bias, LinearW8Params p, void *stream) {
+  if (p.rows == 0 || p.columns == 0)
+    return LLMI_HIP_OK;
+  if (int rc = check_linear_w8(p))
+    return rc;
+  if (!activation || !act_scales || !weight || !weight_scales || !output)
+    return fail(LLMI_HIP_INVALID_ARGUMENT, "linearW8A8: null buffer");
+  if (p.epilogue == LLMI_LINEAR_SILU_MUL && !aux)
+    return fail(LLMI_HIP_INVALID_ARGUMENT, "linearW8A8: SiluMul needs its multiplier (aux)");
+  if (p.epilogue == LLMI_LINEAR_DELTA_DECAY && (!aux || !bias))
+    return fail(LLMI_HIP_INVALID_ARGUMENT, "linearW8A8: the decay needs A_log (aux) and bias");
+  if (!aligned16(activation) || !aligned16(weight))
+    return fail(LLMI_HIP_UNSUPPORTED,
+                "linearW8A8: activation and weight rows must be 16-byte aligned");
+  const W8Shape s{p.outputWidth, p.firstRow, p.groups, p.rows, p.columns, p.epilogue,
+                  p.epilogueBlock};
+  return launched(launch_linear_w8a8(activation, act_scales, weight, weight_scales, output, aux,
+                                     bias, s, static_cast<hipStream_t>(stream)),
+                  linear_w8a8_kernel(p.rows));
+}
+
+int llmi_hip_embedding_w8(const uint32_t *ids, const int8_t *weight, const uint16_t *scales,
+                          uint16_t *output, GroupedEmbedParams p, void *stream) {
+  if (p.tokens == 0 || p.hidden == 0 || p.rowCount == 0)
+    return LLMI_HIP_OK;
+  if (!ids || !weight || !scales || !output)
+    return fail(LLMI_HIP_INVALID_ARGUMENT, "embeddingW8: null buffer");
+  if (p.groups < (p.hidden + 31) / 32)
+    return fail(LLMI_HIP_INVALID_ARGUMENT, "embeddingW8: %u groups for hidden %u", p.groups,
+                p.hidden);
+  if (!fits32(p.tokens, p.hidden, 1) || !fits32(p.rowCount, p.groups, 32))
+    return fail(LLMI_HIP_INVALID_ARGUMENT, "embeddingW8: exceeds the 32-bit index range");
+  return launched(launch_embedding_w8(ids, weight, scales, output, p.tokens, p.hidden,
+                                      p.firstRow, p.rowCount, p.groups,
+                                      static_cast<hipStream_t>(stream)),
+                  "embeddingW8");
+}
+
+int llmi_hip_embedding(const uint32_t *ids, const uint16_t *weight, uint16_t *output,
+                       EmbedParams p, void *stream) {
+  if (p.tokens == 0 || p.hidden == 0 || p.rowCount == 0)
+    return LLMI_HIP_OK;
+  if (!ids || !weight || !output)
+    return fail(LLMI_HIP_INVALID_ARGUMENT, "embedding: null buffer");
+  if (!fits32(p.tokens, p.hidden, 1) || !fits32(p.rowCount, p.hidden, 1))
+    return fail(LLMI_HIP_INVALID_ARGUMENT, "embedding: exceeds the 32-bit index range");
+  return launched(launch_embedding(ids, weight, output, p.tokens, p.hidden, p.firstRow,
+                                   p.rowCount, static_cast<hipStream_t>(stream)),
+                  "embedding");
+}
+
 static int gated_norm(const uint16_t *input, const void *gate, bool activated,
                       const float *weight, uint16_t *output, RowParams p, void *stream) {
   if (p.rows == 0 || p.width == 0)
@@ -610,6 +704,22 @@ unsigned llmi_hip_dispatch_count(int op, const void *params) {
     const L2Params &p = *static_cast<const L2Params *>(params);
     return p.rows && p.width ? 1 : 0;
   }
+  case LLMI_HIP_OP_QUANTIZE_ACTIVATION: {
+    const QuantizeParams &p = *static_cast<const QuantizeParams *>(params);
+    return p.rows && p.width && p.groups == (p.width + 31) / 32 ? 1 : 0;
+  }
+  case LLMI_HIP_OP_LINEAR_W8A8: {
+    const LinearW8Params &p = *static_cast<const LinearW8Params *>(params);
+    return p.rows && p.columns && check_linear_w8(p) == LLMI_HIP_OK ? 1 : 0;
+  }
+  case LLMI_HIP_OP_EMBEDDING_W8: {
+    const GroupedEmbedParams &p = *static_cast<const GroupedEmbedParams *>(params);
+    return p.tokens && p.hidden && p.rowCount && p.groups >= (p.hidden + 31) / 32 ? 1 : 0;
+  }
+  case LLMI_HIP_OP_EMBEDDING: {
+    const EmbedParams &p = *static_cast<const EmbedParams *>(params);
+    return p.tokens && p.hidden && p.rowCount ? 1 : 0;
+  }
   case LLMI_HIP_OP_DELTA_GATES: {
     const RowParams &p = *static_cast<const RowParams *>(params);
     return p.rows && p.width ? 1 : 0;
@@ -694,6 +804,14 @@ const char *llmi_hip_kernel_name(int op, const void *params, unsigned index) {
                : "l2NormRows";
   case LLMI_HIP_OP_DELTA_GATES:
     return "deltaGates";
+  case LLMI_HIP_OP_QUANTIZE_ACTIVATION:
+    return "quantizeActivation";
+  case LLMI_HIP_OP_LINEAR_W8A8:
+    return linear_w8a8_kernel(static_cast<const LinearW8Params *>(params)->rows);
+  case LLMI_HIP_OP_EMBEDDING_W8:
+    return "embeddingW8";
+  case LLMI_HIP_OP_EMBEDDING:
+    return "embedding";
   case LLMI_HIP_OP_GATED_RMS_NORM:
     return "gatedRmsNormTile";
   case LLMI_HIP_OP_SIGMOID_MUL:

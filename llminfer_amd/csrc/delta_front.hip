@@ -38,14 +38,6 @@ constexpr unsigned kConvBlock = 16; // tokens per thread
 constexpr unsigned kMaxKernel = 8;  // filter taps supported (history 7)
 constexpr unsigned kL2Rows = 16;    // l2NormF32 rows per wave (16K rows fill 1024 waves)
 
-// fp16(silu(h)) for an fp16 value h: silu(h) = h * logistic(h) in fp32.
-__device__ __forceinline__ uint16_t silu16(float h) {
-  float y = mul32(h, logistic_estimate(h));
-  if (!f16_settled(y))
-    y = mul32(h, logistic_exact(h));
-  return f2h(y);
-}
-
 __global__ __launch_bounds__(256) void causal_conv_kernel(
     const uint16_t *__restrict__ in, const uint16_t *__restrict__ w, uint16_t *hist,
     uint16_t *__restrict__ out, unsigned T, unsigned C, unsigned k, unsigned silu) {
@@ -314,16 +306,6 @@ __global__ __launch_bounds__(64) void gated_rms_norm_tile(const uint16_t *__rest
       o[e] = (uint32_t)f2h(y[2 * e]) | ((uint32_t)f2h(y[2 * e + 1]) << 16);
     *reinterpret_cast<uint4_t *>(out + base) = o;
   }
-}
-
-__device__ __forceinline__ float exp_cr(float x) { return (float)exp((double)x); }
-__device__ __forceinline__ float log_cr(float x) { return (float)log((double)x); }
-
-// stableSoftplus (Reference.metal:8-12) with correctly rounded exp and log.
-__device__ __forceinline__ float stable_softplus(float x) {
-  float e = exp_cr(-fabsf(x));
-  float tail = e < 1e-4f ? mul32(e, __fsub_rn(1.0f, mul32(0.5f, e))) : log_cr(__fadd_rn(1.0f, e));
-  return __fadd_rn(fmaxf(x, 0.0f), tail);
 }
 
 __global__ __launch_bounds__(256) void delta_gates_kernel(

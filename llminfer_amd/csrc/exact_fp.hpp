@@ -89,4 +89,22 @@ __device__ __forceinline__ float logistic_exact(float g) {
   return __fdiv_rn(1.0f, __fadd_rn(1.0f, (float)exp(-(double)g)));
 }
 
+// fp16(silu(h)) for an fp16 value h: silu(h) = h * logistic(h) in fp32.
+__device__ __forceinline__ uint16_t silu16(float h) {
+  float y = mul32(h, logistic_estimate(h));
+  if (!f16_settled(y))
+    y = mul32(h, logistic_exact(h));
+  return f2h(y);
+}
+
+__device__ __forceinline__ float exp_cr(float x) { return (float)exp((double)x); }
+__device__ __forceinline__ float log_cr(float x) { return (float)log((double)x); }
+
+// stableSoftplus (Reference.metal:8-12) with correctly rounded exp and log.
+__device__ __forceinline__ float stable_softplus(float x) {
+  float e = exp_cr(-fabsf(x));
+  float tail = e < 1e-4f ? mul32(e, __fsub_rn(1.0f, mul32(0.5f, e))) : log_cr(__fadd_rn(1.0f, e));
+  return __fadd_rn(fmaxf(x, 0.0f), tail);
+}
+
 } // namespace llmi

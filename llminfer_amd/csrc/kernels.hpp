@@ -177,4 +177,22 @@ hipError_t launch_delta_gates(const uint16_t *a, const uint16_t *b, const float 
                               const float *dt_bias, float *beta, float *decay,
                               unsigned rows, unsigned width, hipStream_t stream);
 
+// -------------------------------------------------------- W8A8 projections
+hipError_t launch_quantize_activation(const uint16_t *in, int8_t *q, float *scales,
+                                      unsigned *invalid, unsigned rows, unsigned width,
+                                      unsigned groups, hipStream_t stream);
+struct W8Shape {
+  unsigned outputWidth, firstRow, groups, rows, columns, epilogue, block;
+};
+const char *linear_w8a8_kernel(unsigned rows);
+hipError_t launch_linear_w8a8(const int8_t *act, const float *as, const int8_t *w,
+                              const uint16_t *ws, void *out, const void *aux, const float *bias,
+                              const W8Shape &s, hipStream_t stream);
+hipError_t launch_embedding_w8(const uint32_t *ids, const int8_t *w, const uint16_t *sc,
+                               uint16_t *out, unsigned tokens, unsigned hidden, unsigned first,
+                               unsigned count, unsigned groups, hipStream_t stream);
+hipError_t launch_embedding(const uint32_t *ids, const uint16_t *w, uint16_t *out,
+                            unsigned tokens, unsigned hidden, unsigned first, unsigned count,
+                            hipStream_t stream);
+
 } // namespace llmi

@@ -137,6 +137,113 @@ def sigmoid_mul(gate: torch.Tensor, x: torch.Tensor, out: torch.Tensor) -> None:
     bind_sigmoid_mul(gate, x, out)()
 
 
+# ------------------------------------------------------ W8A8 projections
+
+def bind_quantize_activation(x: torch.Tensor, q: torch.Tensor, scales: torch.Tensor,
+                             invalid: torch.Tensor | None = None) -> "Bound":
+    """quantizeActivation (Graph.metal:33-68): x [rows, width] fp16 -> q [rows,
+    groups * 32] int8, scales [rows, groups] fp32; invalid (int32, one
+    element) gets bit 0 set by a group holding a non-finite value."""
+    _require(x, torch.float16, "x")
+    _require(q, torch.int8, "q")
+    _require(scales, torch.float32, "scales")
+    if x.dim() != 2:
+        raise ValueError("x is [rows, width]")
+    rows, width = x.shape
+    groups = (width + 31) // 32
+    if tuple(q.shape) != (rows, groups * 32) or tuple(scales.shape) != (rows, groups):
+        raise ValueError("q is [rows, groups * 32] and scales [rows, groups]")
+    if invalid is not None:
+        _require(invalid, torch.int32, "invalid")
+    p = _lib.QuantizeParams(rows, width, groups)
+    return Bound(_lib.load().llmi_hip_quantize_activation,
+                 (_ptr(x), _ptr(q), _ptr(scales), _ptr(invalid), p, _stream()),
+                 "quantizeActivation")
+
+
+def quantize_activation(*args) -> None:
+    bind_quantize_activation(*args)()
+
+
+_F32_EPILOGUES = (_lib.LINEAR_SILU_F32, _lib.LINEAR_DELTA_BETA, _lib.LINEAR_DELTA_DECAY)
+
+
+def bind_linear_w8a8(q: torch.Tensor, scales: torch.Tensor, weight: torch.Tensor,
+                     weight_scales: torch.Tensor, out: torch.Tensor,
+                     epilogue: int = _lib.LINEAR_NONE, block: int = 0,
+                     aux: torch.Tensor | None = None, bias: torch.Tensor | None = None,
+                     first_row: int = 0) -> "Bound":
+    """linearW8A8Gemv / Gemm (W8A8.metal:28-113) with storeLinear
+    (Reference.metal:14-47): q [rows, groups * 32] int8, scales [rows, groups]
+    fp32, weight [columns, groups * 32] int8, weight_scales [columns, groups]
+    fp16; out [rows, width] fp16 (fp32 for the SiluF32, DeltaBeta and
+    DeltaDecay epilogues), columns first_row .. first_row + columns - 1
+    written. aux: fp16 like out (SiluMul) or fp32 A_log [width]
+    (DeltaDecay); bias: fp32 [width] (DeltaDecay)."""
+    _require(q, torch.int8, "q")
+    _require(scales, torch.float32, "scales")
+    _require(weight, torch.int8, "weight")
+    _require(weight_scales, torch.float16, "weight_scales")
+    _require(out, torch.float32 if epilogue in _F32_EPILOGUES else torch.float16, "out")
+    rows, groups = scales.shape
+    columns = weight.shape[0]
+    if tuple(q.shape) != (rows, groups * 32) or tuple(weight.shape) != (columns, groups * 32) \
+            or tuple(weight_scales.shape) != (columns, groups) or out.dim() != 2 \
+            or out.shape[0] != rows:
+        raise ValueError("q, scales, weight, weight_scales and out shapes disagree")
+    if aux is not None:
+        _require(aux, aux.dtype, "aux")
+    if bias is not None:
+        _require(bias, torch.float32, "bias")
+    p = _lib.LinearW8Params(out.shape[1], first_row, groups, rows, columns, epilogue, block)
+    return Bound(_lib.load().llmi_hip_linear_w8a8,
+                 (_ptr(q), _ptr(scales), _ptr(weight), _ptr(weight_scales), _ptr(out), _ptr(aux),
+                  _ptr(bias), p, _stream()),
+                 "linearW8A8Gemv" if rows == 1 else "linearW8A8Gemm")
+
+
+def linear_w8a8(*args, **kwargs) -> None:
+    bind_linear_w8a8(*args, **kwargs)()
+
+
+def bind_embedding_w8(ids: torch.Tensor, weight: torch.Tensor, scales: torch.Tensor,
+                      out: torch.Tensor, first_row: int = 0) -> "Bound":
+    """embeddingW8 (Graph.metal:16-31): ids int32 [tokens] (read as uint32),
+    weight [rows, groups * 32] int8, scales [rows, groups] fp16, out [tokens,
+    hidden] fp16 (rows of other shards' ids untouched)."""
+    _require(ids, torch.int32, "ids")
+    _require(weight, torch.int8, "weight")
+    _require(scales, torch.float16, "scales")
+    _require(out, torch.float16, "out")
+    rows, groups = scales.shape
+    if out.dim() != 2 or out.shape[0] != ids.numel() or tuple(weight.shape) != (rows, groups * 32):
+        raise ValueError("ids, weight, scales and out shapes disagree")
+    p = _lib.GroupedEmbedParams(ids.numel(), out.shape[1], first_row, rows, groups)
+    return Bound(_lib.load().llmi_hip_embedding_w8,
+                 (_ptr(ids), _ptr(weight), _ptr(scales), _ptr(out), p, _stream()), "embeddingW8")
+
+
+def embedding_w8(*args, **kwargs) -> None:
+    bind_embedding_w8(*args, **kwargs)()
+
+
+def bind_embedding(ids: torch.Tensor, weight: torch.Tensor, out: torch.Tensor,
+                   first_row: int = 0) -> "Bound":
+    """embedding (Reference.metal:49-58): fp16 weight rows [rows, hidden]."""
+    _require(ids, torch.int32, "ids")
+    _require(weight, torch.float16, "weight")
+    _require(out, torch.float16, "out")
+    if out.dim() != 2 or out.shape[0] != ids.numel() or weight.shape[1] != out.shape[1]:
+        raise ValueError("ids, weight and out shapes disagree")
+    p = _lib.EmbedParams(ids.numel(), out.shape[1], first_row, weight.shape[0])
+    return Bound(_lib.load().llmi_hip_embedding, (_ptr(ids), _ptr(weight), _ptr(out), p,
+                                                  _stream()), "embedding")
+
+
+def embedding(*args, **kwargs) -> None:
+    bind_embedding(*args, **kwargs)()
+
+
 def bind_causal_conv(x: torch.Tensor, weight: torch.Tensor, history: torch.Tensor | None,
                      out: torch.Tensor, silu: bool = True) -> "Bound":
     """causalConv (Reference.metal:137-161): x, out [T, C] fp16; weight [C, k]

@@ -76,6 +76,12 @@ def lib() -> C.CDLL:
         L.orc_causal_conv.argtypes = [_u16p, _u16p, _u16p, _u16p] + [_u32] * 4
         L.orc_gated_rms_norm.argtypes = [_u16p, C.c_void_p, C.c_void_p, _f32p, _u16p,
                                          _u32, _u32, C.c_float]
+        L.orc_quantize_activation.argtypes = [_u16p, C.c_void_p, _f32p, C.POINTER(_u32)] + \
+            [_u32] * 3
+        L.orc_linear_w8a8.argtypes = [C.c_void_p, _f32p, C.c_void_p, _u16p, C.c_void_p,
+                                      C.c_void_p, C.c_void_p] + [_u32] * 7
+        L.orc_embedding_w8.argtypes = [C.c_void_p, C.c_void_p, _u16p, _u16p] + [_u32] * 5
+        L.orc_embedding.argtypes = [C.c_void_p, _u16p, _u16p] + [_u32] * 4
         for name, n in (("orc_cost_kv_append", 3), ("orc_cost_causal_gqa", 5),
                         ("orc_cost_delta_update", 5)):
             fn = getattr(L, name)
@@ -277,6 +283,78 @@ def sigmoid_mul(gate, x) -> np.ndarray:
     out = np.empty(a.shape, np.uint16)
     lib().orc_sigmoid_mul(g.reshape(-1), a.reshape(-1), out.reshape(-1), a.size)
     return out
+
+
+# ------------------------------------------------------------- W8A8 path
+
+LINEAR_NONE, LINEAR_SILU, LINEAR_SILU_MUL, LINEAR_SIGMOID_COLUMNS = 0, 1, 2, 3
+LINEAR_SILU_F32, LINEAR_DELTA_BETA, LINEAR_DELTA_DECAY = 4, 5, 6
+F32_EPILOGUES = (LINEAR_SILU_F32, LINEAR_DELTA_BETA, LINEAR_DELTA_DECAY)
+
+
+def quantize_activation(x) -> tuple[np.ndarray, np.ndarray, int]:
+    """quantizeActivation (Graph.metal:33-68) on fp16 bits [rows, width]:
+    int8 [rows, groups * 32], float32 scales [rows, groups], invalid flag."""
+    a = np.ascontiguousarray(x, np.uint16)
+    rows, width = a.shape
+    groups = (width + 31) // 32
+    q = np.zeros((rows, groups * 32), np.int8)
+    sc = np.empty((rows, groups), np.float32)
+    invalid = _u32(0)
+    lib().orc_quantize_activation(a.reshape(-1), q.ctypes.data, sc.reshape(-1),
+                                  C.byref(invalid), rows, width, groups)
+    return q, sc, invalid.value
+
+
+def linear_w8a8(act, act_scales, weight, weight_scales, epilogue: int = LINEAR_NONE,
+                block: int = 0, aux=None, bias=None, output=None, first_row: int = 0,
+                output_width: int | None = None) -> np.ndarray:
+    """linearW8A8Gemv/Gemm (W8A8.metal:28-113) with storeLinear
+    (Reference.metal:14-47): act int8 [rows, groups * 32], act_scales float32
+    [rows, groups], weight int8 [columns, groups * 32], weight_scales fp16
+    bits [columns, groups]. Returns (or writes into `output`, rows x
+    output_width) fp16 bits, or float32 for the fp32 epilogues."""
+    x = np.ascontiguousarray(act, np.int8)
+    w = np.ascontiguousarray(weight, np.int8)
+    xs = np.ascontiguousarray(act_scales, np.float32)
+    ws = np.ascontiguousarray(weight_scales, np.uint16)
+    rows, columns, groups = x.shape[0], w.shape[0], xs.shape[1]
+    assert x.shape[1] == w.shape[1] == groups * 32 and ws.shape == (columns, groups)
+    width = output_width if output_width is not None else first_row + columns
+    if output is None:
+        dt = np.float32 if epilogue in F32_EPILOGUES else np.uint16
+        output = np.zeros((rows, width), dt)
+    ax = np.ascontiguousarray(aux) if aux is not None else None
+    bs = np.ascontiguousarray(bias, np.float32) if bias is not None else None
+    lib().orc_linear_w8a8(x.ctypes.data, xs.reshape(-1), w.ctypes.data, ws.reshape(-1),
+                          output.ctypes.data, ax.ctypes.data if ax is not None else None,
+                          bs.ctypes.data if bs is not None else None, width, first_row, groups,
+                          rows, columns, epilogue, block)
+    return output
+
+
+def embedding_w8(ids, weight, scales, hidden: int, first_row: int = 0, output=None):
+    """embeddingW8 (Graph.metal:16-31): ids uint32 [tokens], weight int8
+    [rows, groups * 32], scales fp16 bits [rows, groups]."""
+    i = np.ascontiguousarray(ids, np.uint32)
+    w = np.ascontiguousarray(weight, np.int8)
+    sc = np.ascontiguousarray(scales, np.uint16)
+    if output is None:
+        output = np.zeros((i.size, hidden), np.uint16)
+    lib().orc_embedding_w8(i.ctypes.data, w.ctypes.data, sc.reshape(-1), output.reshape(-1),
+                           i.size, hidden, first_row, w.shape[0], sc.shape[1])
+    return output
+
+
+def embedding(ids, weight, first_row: int = 0, output=None):
+    """embedding (Reference.metal:49-58): fp16 rows of weight [rows, hidden]."""
+    i = np.ascontiguousarray(ids, np.uint32)
+    w = np.ascontiguousarray(weight, np.uint16)
+    if output is None:
+        output = np.zeros((i.size, w.shape[1]), np.uint16)
+    lib().orc_embedding(i.ctypes.data, w.reshape(-1), output.reshape(-1), i.size, w.shape[1],
+                        first_row, w.shape[0])
+    return output
 
 
 def l2norm_f32(x, width: int, eps: float = 1e-6, scale: float = 1.0) -> np.ndarray:

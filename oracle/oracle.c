@@ -778,6 +778,155 @@ void orc_sigmoid_mul(const uint16_t *gate, const uint16_t *input, uint16_t *outp
   }
 }
 
+/* ------------------------------------------------------------- W8A8 path */
+
+/* silu, Reference.metal:6 (x * logistic(x), each step rounded to fp32). */
+static float silu(float x) { return x * logistic(x); }
+
+/* quantizeActivation, Graph.metal:33-68: per row and 32-wide group, scale =
+ * max|x| / 127 (1 for an all-zero or non-finite group), q = x / scale
+ * clamped to [-127, 127] and rounded half to even; a non-finite group sets
+ * *invalid and quantizes to zeros. Output rows are groups * 32 wide. */
+void orc_quantize_activation(const uint16_t *input, int8_t *quantized, float *scales,
+                             uint32_t *invalid, uint32_t rows, uint32_t width,
+                             uint32_t groups) {
+  for (size_t i = 0; i < (size_t)rows * groups; ++i) {
+    uint32_t row = (uint32_t)(i / groups), begin = (uint32_t)(i % groups) * 32u;
+    uint32_t length = width - begin < 32u ? width - begin : 32u;
+    const uint16_t *group = input + (size_t)row * width + begin;
+    float max_abs = 0.0f;
+    int finite = 1;
+    for (uint32_t j = 0; j < length; ++j) {
+      float value = orc_f16_to_f32(group[j]);
+      finite = finite && isfinite(value);
+      max_abs = fmaxf(max_abs, fabsf(value));
+    }
+    if (!finite)
+      *invalid |= 1u;
+    float scale = finite && max_abs > 0.0f ? max_abs / 127.0f : 1.0f;
+    scales[i] = scale;
+    for (uint32_t j = 0; j < 32; ++j) {
+      int rounded = 0;
+      if (finite && j < length) {
+        float x = orc_f16_to_f32(group[j]) / scale;
+        x = x < -127.0f ? -127.0f : (x > 127.0f ? 127.0f : x);
+        float lower = floorf(x);
+        float fraction = x - lower;
+        rounded = (int)lower;
+        if (fraction > 0.5f || (fraction == 0.5f && (rounded % 2 != 0)))
+          ++rounded;
+      }
+      quantized[i * 32 + j] = (int8_t)rounded;
+    }
+  }
+}
+
+/* storeLinear, Reference.metal:14-47: the projection rounded to fp16, then
+ * the fused epilogue of the consumer. */
+static void store_linear(void *output, const void *aux, const float *bias, size_t i,
+                         uint32_t col, uint32_t epilogue, uint32_t block,
+                         float accumulator) {
+  float projected = orc_round_f16(accumulator);
+  switch (epilogue) {
+  case ORC_LINEAR_SILU:
+    projected = orc_round_f16(silu(projected));
+    break;
+  case ORC_LINEAR_SILU_MUL:
+    projected = orc_round_f16(orc_round_f16(silu(projected)) *
+                              orc_f16_to_f32(((const uint16_t *)aux)[i]));
+    break;
+  case ORC_LINEAR_SIGMOID_COLUMNS:
+    if ((col / block) % 2 != 0)
+      projected = orc_round_f16(logistic(projected));
+    break;
+  case ORC_LINEAR_SILU_F32:
+    ((float *)output)[i] = silu(projected);
+    return;
+  case ORC_LINEAR_DELTA_BETA:
+    ((float *)output)[i] = orc_round_f16(logistic(projected));
+    return;
+  case ORC_LINEAR_DELTA_DECAY: {
+    const float *a_log = (const float *)aux;
+    ((float *)output)[i] =
+        orc_expf_cr(-orc_expf_cr(a_log[col]) * stable_softplus(projected + bias[col]));
+    return;
+  }
+  default:
+    break;
+  }
+  ((uint16_t *)output)[i] = orc_f32_to_f16(projected);
+}
+
+/* linearW8A8Gemv / linearW8A8Gemm, W8A8.metal:28-113 (dispatch by rows,
+ * LinearW8Launch.h:14-21): per output (row, column), lane l of the column's
+ * `lanes` lanes (16 for one row, else 8, GraphParams.h:17-23) sums in fp32,
+ * over groups g = l, l + lanes, ..., the exact int32 dot of the 32 int8
+ * activations and weights of group g times the activation scale times the
+ * weight scale, in that order; the lanes then combine by the xor butterfly
+ * (acc += shuffle_xor(acc, m), m = lanes / 2 ... 1) and lane 0 stores
+ * through storeLinear at row * outputWidth + firstRow + column. */
+void orc_linear_w8a8(const int8_t *act, const float *act_scales, const int8_t *weight,
+                     const uint16_t *weight_scales, void *output, const void *aux,
+                     const float *bias, uint32_t output_width, uint32_t first_row,
+                     uint32_t groups, uint32_t rows, uint32_t columns, uint32_t epilogue,
+                     uint32_t epilogue_block) {
+  const uint32_t lanes = rows == 1 ? 16u : 8u;
+  float acc[16];
+  for (uint32_t row = 0; row < rows; ++row)
+    for (uint32_t col = 0; col < columns; ++col) {
+      for (uint32_t l = 0; l < lanes; ++l) {
+        float a = 0.0f;
+        for (uint32_t g = l; g < groups; g += lanes) {
+          const int8_t *x = act + ((size_t)row * groups + g) * 32;
+          const int8_t *w = weight + ((size_t)col * groups + g) * 32;
+          int32_t dot = 0;
+          for (int j = 0; j < 32; ++j)
+            dot += (int32_t)x[j] * (int32_t)w[j];
+          float term = (float)dot * act_scales[(size_t)row * groups + g];
+          term = term * orc_f16_to_f32(weight_scales[(size_t)col * groups + g]);
+          a = a + term;
+        }
+        acc[l] = a;
+      }
+      for (uint32_t m = lanes / 2; m != 0; m >>= 1) {
+        float next[16];
+        for (uint32_t l = 0; l < lanes; ++l)
+          next[l] = acc[l] + acc[l ^ m];
+        memcpy(acc, next, sizeof(float) * lanes);
+      }
+      uint32_t column = first_row + col;
+      store_linear(output, aux, bias, (size_t)row * output_width + column, column, epilogue,
+                   epilogue_block, acc[0]);
+    }
+}
+
+/* embeddingW8, Graph.metal:16-31: out[t][c] = fp16(w[row][c] * scale[row][c /
+ * 32]) for token ids in [firstRow, firstRow + rowCount), rows `groups * 32`
+ * int8 wide; other ids leave the output row untouched. */
+void orc_embedding_w8(const uint32_t *ids, const int8_t *weight, const uint16_t *scales,
+                      uint16_t *output, uint32_t tokens, uint32_t hidden, uint32_t first_row,
+                      uint32_t row_count, uint32_t groups) {
+  for (size_t i = 0; i < (size_t)tokens * hidden; ++i) {
+    uint32_t id = ids[i / hidden];
+    if (id < first_row || id - first_row >= row_count)
+      continue;
+    size_t row = id - first_row;
+    uint32_t col = (uint32_t)(i % hidden);
+    output[i] = orc_f32_to_f16((float)weight[row * groups * 32 + col] *
+                               orc_f16_to_f32(scales[row * groups + col / 32]));
+  }
+}
+
+/* embedding, Reference.metal:49-58: fp16 rows copied for ids in range. */
+void orc_embedding(const uint32_t *ids, const uint16_t *weight, uint16_t *output,
+                   uint32_t tokens, uint32_t hidden, uint32_t first_row, uint32_t row_count) {
+  for (size_t i = 0; i < (size_t)tokens * hidden; ++i) {
+    uint32_t id = ids[i / hidden];
+    if (id >= first_row && id - first_row < row_count)
+      output[i] = weight[(size_t)(id - first_row) * hidden + i % hidden];
+  }
+}
+
 /* ------------------------------------------------------------------ cost */
 
 static int mul_ok(uint64_t a, uint64_t b, uint64_t *r) {

@@ -168,6 +168,35 @@ void orc_gated_rms_norm(const uint16_t *input, const uint16_t *gate16, const flo
 void orc_sigmoid_mul(const uint16_t *gate, const uint16_t *input, uint16_t *output,
                      size_t count);
 
+/* The W8A8 projection path (lib/Backend/Metal/Kernels/W8A8.metal,
+ * Graph.metal:16-68, storeLinear Reference.metal:14-47). Epilogue codes are
+ * LinearEpilogue of ReferenceParams.h:8-16. */
+enum {
+  ORC_LINEAR_NONE = 0,
+  ORC_LINEAR_SILU = 1,
+  ORC_LINEAR_SILU_MUL = 2,
+  ORC_LINEAR_SIGMOID_COLUMNS = 3,
+  ORC_LINEAR_SILU_F32 = 4,
+  ORC_LINEAR_DELTA_BETA = 5,
+  ORC_LINEAR_DELTA_DECAY = 6,
+};
+void orc_quantize_activation(const uint16_t *input, int8_t *quantized, float *scales,
+                             uint32_t *invalid, uint32_t rows, uint32_t width,
+                             uint32_t groups);
+/* output is fp16 (uint16_t) or, for SILU_F32 / DELTA_BETA / DELTA_DECAY,
+ * fp32; aux is the fp16 multiplier (SILU_MUL) or the fp32 A_log
+ * (DELTA_DECAY). */
+void orc_linear_w8a8(const int8_t *act, const float *act_scales, const int8_t *weight,
+                     const uint16_t *weight_scales, void *output, const void *aux,
+                     const float *bias, uint32_t output_width, uint32_t first_row,
+                     uint32_t groups, uint32_t rows, uint32_t columns, uint32_t epilogue,
+                     uint32_t epilogue_block);
+void orc_embedding_w8(const uint32_t *ids, const int8_t *weight, const uint16_t *scales,
+                      uint16_t *output, uint32_t tokens, uint32_t hidden, uint32_t first_row,
+                      uint32_t row_count, uint32_t groups);
+void orc_embedding(const uint32_t *ids, const uint16_t *weight, uint16_t *output,
+                   uint32_t tokens, uint32_t hidden, uint32_t first_row, uint32_t row_count);
+
 /* Cost model of lib/GraphIR/Cost.cpp:180-201 (MACs) and :56-94 (bytes) for
  * the three hot ops. Returns 0 on success, -1 on overflow. */
 typedef struct {

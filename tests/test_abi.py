@@ -289,3 +289,54 @@ def test_l2_norm_delta_gated_norm_rejects_shapes_without_kernel():
              None) == _lib.INVALID_ARGUMENT
     assert f(16, 16, 16, 16, 16, 16, None, 16, 16, ok, 1e-6, 0.1, 1e-6, None, 0,
              None) == _lib.INVALID_ARGUMENT
+
+
+def test_w8a8_abi():
+    """The W8A8 projection path: GraphParams.h:8-28 / ReferenceParams.h:4-6
+    layouts, validation before any launch, plan-record names
+    (LinearW8Launch.h:14-21: one row -> linearW8A8Gemv)."""
+    from llminfer_amd import ops
+    assert C.sizeof(_lib.QuantizeParams) == 12
+    assert C.sizeof(_lib.LinearW8Params) == 28
+    assert C.sizeof(_lib.GroupedEmbedParams) == 20
+    assert C.sizeof(_lib.EmbedParams) == 16
+    lib = _lib.load()
+    a16 = 16  # a 16-byte-aligned stand-in pointer; nothing is launched
+    ok = _lib.LinearW8Params(2560, 0, 80, 1, 2560, _lib.LINEAR_NONE, 0)
+    assert lib.llmi_hip_linear_w8a8(None, None, None, None, None, None, None,
+                                    _lib.LinearW8Params(2560, 0, 80, 0, 2560, 0, 0), None) == \
+        _lib.OK
+    bad = [
+        _lib.LinearW8Params(2560, 0, 80, 1, 2560, 7, 0),                   # unknown epilogue
+        _lib.LinearW8Params(2560, 0, 80, 1, 2560, _lib.LINEAR_SIGMOID_COLUMNS, 0),  # no block
+        _lib.LinearW8Params(2560, 1, 80, 1, 2560, 0, 0),                   # past the width
+        _lib.LinearW8Params(2560, 0, 0, 1, 2560, 0, 0),                    # no groups
+    ]
+    for p in bad:
+        assert lib.llmi_hip_linear_w8a8(a16, a16, a16, a16, a16, None, None, p, None) == \
+            _lib.INVALID_ARGUMENT
+    silu_mul = _lib.LinearW8Params(2560, 0, 80, 1, 2560, _lib.LINEAR_SILU_MUL, 0)
+    assert lib.llmi_hip_linear_w8a8(a16, a16, a16, a16, a16, None, None, silu_mul, None) == \
+        _lib.INVALID_ARGUMENT
+    decay = _lib.LinearW8Params(32, 0, 80, 4, 32, _lib.LINEAR_DELTA_DECAY, 0)
+    assert lib.llmi_hip_linear_w8a8(a16, a16, a16, a16, a16, a16, None, decay, None) == \
+        _lib.INVALID_ARGUMENT
+    assert lib.llmi_hip_linear_w8a8(a16 + 1, a16, a16, a16, a16, None, None, ok, None) == \
+        _lib.UNSUPPORTED
+    assert lib.llmi_hip_quantize_activation(a16, a16, a16, None,
+                                            _lib.QuantizeParams(4, 100, 3), None) == \
+        _lib.INVALID_ARGUMENT
+    assert lib.llmi_hip_embedding_w8(a16, a16, a16, a16,
+                                     _lib.GroupedEmbedParams(4, 100, 0, 10, 3), None) == \
+        _lib.INVALID_ARGUMENT
+    assert lib.llmi_hip_embedding(None, a16, a16, _lib.EmbedParams(4, 100, 0, 10), None) == \
+        _lib.INVALID_ARGUMENT
+    assert ops.kernel_names(_lib.OP_LINEAR_W8A8, ok) == ["linearW8A8Gemv"]
+    assert ops.kernel_names(_lib.OP_LINEAR_W8A8,
+                            _lib.LinearW8Params(9216, 0, 80, 64, 9216, 2, 0)) == ["linearW8A8Gemm"]
+    assert ops.kernel_names(_lib.OP_LINEAR_W8A8, bad[0]) == []
+    assert ops.kernel_names(_lib.OP_QUANTIZE_ACTIVATION, _lib.QuantizeParams(4, 100, 4)) == \
+        ["quantizeActivation"]
+    assert ops.kernel_names(_lib.OP_EMBEDDING_W8,
+                            _lib.GroupedEmbedParams(4, 100, 0, 10, 4)) == ["embeddingW8"]
+    assert ops.kernel_names(_lib.OP_EMBEDDING, _lib.EmbedParams(4, 100, 0, 10)) == ["embedding"]

@@ -1,0 +1,191 @@
+"""GPU parity of the W8A8 projection path against the CPU oracle.
+
+quantizeActivation, linearW8A8Gemv / Gemm with every storeLinear epilogue,
+embeddingW8 and embedding: the HIP kernels follow the reference kernels'
+integer and fp32 arithmetic order (Graph.metal:16-68, W8A8.metal:28-113,
+Reference.metal:14-58), so every output is compared bit for bit with
+oracle.c on the same seeded inputs. Shapes include Qwen3.5-4B's decode
+projections (hidden 2560, MLP 9216).
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from llminfer_amd import _lib, ops
+
+pytestmark = pytest.mark.gpu
+
+
+def _dev(a, gpu):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(gpu)
+
+
+def _f16(x):
+    return oracle.f32_to_f16(np.asarray(x, np.float32))
+
+
+def _u16_dev(bits, gpu):
+    return torch.from_numpy(np.ascontiguousarray(bits).view(np.int16)).to(gpu).view(torch.float16)
+
+
+def _host_u16(t):
+    return t.view(torch.int16).cpu().numpy().view(np.uint16)
+
+
+@pytest.mark.parametrize("rows,width", [(1, 2560), (1, 9216), (7, 96), (3, 70), (64, 2560),
+                                        (2, 1)])
+def test_quantize_bit_exact(gpu, rows, width):
+    print(f"quantize rows={rows} width={width}", flush=True)
+    x = _f16(np.random.default_rng(rows + width).standard_normal((rows, width)) * 4)
+    if width >= 96:
+        x[0, 32:64] = 0           # an all-zero group
+        x[-1, 1] = 0x7E00         # NaN in group 0 of the last row
+        x[0, 127 % width] = 0xFC00  # -inf
+        vals = [127, 0.5, 1.5, 2.5, -0.5, -1.5, -2.5, 126.5]
+        x[rows // 2, 64:72] = _f16(vals)  # exact ties (the group max is 127)
+        x[rows // 2, 72:96] = 0
+    q_ref, s_ref, inv_ref = oracle.quantize_activation(x)
+    groups = (width + 31) // 32
+    q = torch.empty((rows, groups * 32), dtype=torch.int8, device=gpu)
+    s = torch.empty((rows, groups), dtype=torch.float32, device=gpu)
+    inv = torch.zeros(1, dtype=torch.int32, device=gpu)
+    ops.quantize_activation(_u16_dev(x, gpu), q, s, inv)
+    torch.cuda.synchronize()
+    assert np.array_equal(q.cpu().numpy(), q_ref)
+    assert np.array_equal(s.cpu().numpy().view(np.uint32), s_ref.view(np.uint32))
+    assert int(inv.item()) == inv_ref
+
+
+def _case(seed, rows, columns, groups, spread=1.0):
+    r = np.random.default_rng(seed)
+    x16 = _f16(r.standard_normal((rows, groups * 32)) * spread)
+    xq, xs, _ = oracle.quantize_activation(x16)
+    w = r.integers(-127, 128, (columns, groups * 32), dtype=np.int8)
+    ws = _f16(r.random((columns, groups)) * 0.01 + 2e-4)
+    return xq, xs, w, ws
+
+
+def _run_linear(gpu, xq, xs, w, ws, epilogue=0, block=0, aux=None, bias=None, first_row=0,
+                width=None):
+    rows = xq.shape[0]
+    width = width if width is not None else first_row + w.shape[0]
+    f32 = epilogue in oracle.F32_EPILOGUES
+    out = torch.full((rows, width), 7.0, dtype=torch.float32 if f32 else torch.float16,
+                     device=gpu)
+    aux_d = None
+    if aux is not None:
+        aux_d = _u16_dev(aux, gpu) if aux.dtype == np.uint16 else _dev(aux, gpu)
+    bias_d = _dev(bias, gpu) if bias is not None else None
+    ops.linear_w8a8(_dev(xq, gpu), _dev(xs, gpu), _dev(w, gpu), _u16_dev(ws, gpu), out,
+                    epilogue, block, aux_d, bias_d, first_row)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy() if f32 else _host_u16(out)
+    ref_out = np.full((rows, width), 7.0, np.float32) if f32 else \
+        np.full((rows, width), 0x4700, np.uint16)
+    oracle.linear_w8a8(xq, xs, w, ws, epilogue, block, aux, bias, ref_out, first_row, width)
+    return got, ref_out
+
+
+def _same(got, want):
+    if got.dtype == np.float32:
+        return np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    return np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("rows,columns,groups", [
+    (1, 9216, 80),    # Qwen3.5-4B MLP gate/up, decode
+    (1, 2560, 288),   # MLP down, decode
+    (1, 37, 5), (1, 16, 1), (1, 33, 17),
+    (2, 40, 9), (3, 70, 12), (4, 32, 80), (5, 19, 3), (64, 256, 80)])
+def test_linear_bit_exact(gpu, rows, columns, groups):
+    print(f"linear rows={rows} columns={columns} groups={groups}", flush=True)
+    xq, xs, w, ws = _case(rows * 7 + columns + groups, rows, columns, groups)
+    got, want = _run_linear(gpu, xq, xs, w, ws)
+    assert _same(got, want)
+
+
+def test_linear_shard_writes_only_its_columns(gpu):
+    xq, xs, w, ws = _case(3, 3, 48, 7)
+    got, want = _run_linear(gpu, xq, xs, w, ws, first_row=40, width=100)
+    assert _same(got, want)
+    assert np.all(got[:, :40] == 0x4700) and np.all(got[:, 88:] == 0x4700)
+    got1, want1 = _run_linear(gpu, xq[:1], xs[:1], w, ws, first_row=52, width=100)
+    assert _same(got1, want1)
+
+
+@pytest.mark.parametrize("rows", [1, 6])
+@pytest.mark.parametrize("epilogue", [1, 2, 3, 4, 5, 6])
+def test_linear_epilogues_bit_exact(gpu, rows, epilogue):
+    print(f"linear epilogue {epilogue} rows={rows}", flush=True)
+    columns, groups = 96, 20
+    # wide activations: projections spread over the epilogues' ranges
+    xq, xs, w, ws = _case(100 + epilogue * 10 + rows, rows, columns, groups, spread=6.0)
+    r = np.random.default_rng(epilogue)
+    aux = bias = None
+    if epilogue == oracle.LINEAR_SILU_MUL:
+        aux = _f16(r.standard_normal((rows, columns)) * 2)
+    if epilogue == oracle.LINEAR_DELTA_DECAY:
+        aux = (r.standard_normal(columns) * 0.5).astype(np.float32)
+        bias = (r.standard_normal(columns) * 0.5).astype(np.float32)
+    got, want = _run_linear(gpu, xq, xs, w, ws, epilogue, 16, aux, bias)
+    assert _same(got, want)
+
+
+def test_embeddings_bit_exact(gpu):
+    r = np.random.default_rng(5)
+    rows, hidden = 300, 2560
+    groups = hidden // 32
+    w = r.integers(-127, 128, (rows, groups * 32), dtype=np.int8)
+    sc = _f16(r.random((rows, groups)) * 0.02)
+    ids = np.array([5, 299, 0, 301, 150, 5, 1000], np.uint32)   # 301, 1000: other shards
+    out = torch.full((ids.size, hidden), 3.0, dtype=torch.float16, device=gpu)
+    ops.embedding_w8(_dev(ids.view(np.int32), gpu), _dev(w, gpu), _u16_dev(sc, gpu), out)
+    want = np.full((ids.size, hidden), 0x4200, np.uint16)
+    oracle.embedding_w8(ids, w, sc, hidden, 0, want)
+    torch.cuda.synchronize()
+    assert np.array_equal(_host_u16(out), want)
+    # an odd width takes the one-element path; a shard offset
+    hid2 = 70
+    w2 = r.integers(-127, 128, (40, 96), dtype=np.int8)
+    sc2 = _f16(r.random((40, 3)) * 0.02)
+    ids2 = np.array([12, 51, 9, 30], np.uint32)
+    out2 = torch.zeros((4, hid2), dtype=torch.float16, device=gpu)
+    ops.embedding_w8(_dev(ids2.view(np.int32), gpu), _dev(w2, gpu), _u16_dev(sc2, gpu), out2,
+                     first_row=10)
+    want2 = np.zeros((4, hid2), np.uint16)
+    oracle.embedding_w8(ids2, w2, sc2, hid2, 10, want2)
+    torch.cuda.synchronize()
+    assert np.array_equal(_host_u16(out2), want2)
+    wf = _f16(r.standard_normal((rows, hidden)))
+    outf = torch.zeros((ids.size, hidden), dtype=torch.float16, device=gpu)
+    ops.embedding(_dev(ids.view(np.int32), gpu), _u16_dev(wf, gpu), outf)
+    torch.cuda.synchronize()
+    assert np.array_equal(_host_u16(outf), oracle.embedding(ids, wf))
+
+
+def test_quantize_then_project_decode_step(gpu):
+    """One decode-step projection as the plan lowers it: quantizeActivation
+    then linearW8A8Gemv with the SwiGLU epilogue (the up projection's output
+    as aux), against the oracle chain."""
+    r = np.random.default_rng(11)
+    hidden, inter = 2560, 9216
+    x = _f16(r.standard_normal((1, hidden)))
+    groups = hidden // 32
+    wg = r.integers(-127, 128, (inter, hidden), dtype=np.int8)
+    wu = r.integers(-127, 128, (inter, hidden), dtype=np.int8)
+    sg = _f16(r.random((inter, groups)) * 0.002)
+    su = _f16(r.random((inter, groups)) * 0.002)
+    q = torch.empty((1, hidden), dtype=torch.int8, device=gpu)
+    s = torch.empty((1, groups), dtype=torch.float32, device=gpu)
+    ops.quantize_activation(_u16_dev(x, gpu), q, s)
+    up = torch.empty((1, inter), dtype=torch.float16, device=gpu)
+    ops.linear_w8a8(q, s, _dev(wu, gpu), _u16_dev(su, gpu), up)
+    act = torch.empty((1, inter), dtype=torch.float16, device=gpu)
+    ops.linear_w8a8(q, s, _dev(wg, gpu), _u16_dev(sg, gpu), act, _lib.LINEAR_SILU_MUL, 0, up)
+    torch.cuda.synchronize()
+    xq, xs, _ = oracle.quantize_activation(x)
+    up_ref = oracle.linear_w8a8(xq, xs, wu, su)
+    act_ref = oracle.linear_w8a8(xq, xs, wg, sg, oracle.LINEAR_SILU_MUL, 0, up_ref)
+    assert np.array_equal(_host_u16(up), up_ref)
+    assert np.array_equal(_host_u16(act), act_ref)
