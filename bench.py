@@ -530,6 +530,128 @@ class DeltaFront(Workload):
                 "gpu_bit_exact": exact}
 
 
+def w8_bytes(rows: int, columns: int, groups: int, out_bytes: int = 2) -> int:
+    """HBM bytes of one linearW8A8 call: int8 weights and fp16 weight scales
+    (read once), int8 activations and fp32 activation scales, the output."""
+    return (columns * groups * (32 + 2) + rows * groups * (32 + 4) +
+            rows * columns * out_bytes)
+
+
+def quantize_bytes(rows: int, width: int) -> int:
+    """quantizeActivation: fp16 in, int8 and fp32 scales out."""
+    groups = (width + 31) // 32
+    return rows * width * 2 + rows * groups * (32 + 4)
+
+
+class W8A8Mlp(Workload):
+    """The SwiGLU MLP of a Qwen3.5-4B layer (hidden 2560, intermediate 9216,
+    docs/architecture.md:115) on the W8A8 path as the plan lowers it
+    (MetalExecutionPlan.cpp:464-510, 566-580): quantizeActivation of the
+    hidden rows, the up projection, the gate projection with the SwiGLU
+    epilogue (the up output as its multiplier), quantizeActivation of the
+    product, the down projection. Random int8 weights and fp16 scales of
+    those shapes (75 MB a set) rotate over sets larger than the MALL."""
+    bound = "hbm"
+    labels = ("quantize_in", "up", "gate_swiglu", "quantize_mid", "down")
+    dominant = "up"
+
+    def __init__(self, dev, T, sets, seed, hidden=2560, inter=9216):
+        import torch
+        from llminfer_amd import _lib, ops
+        self.T, self.sets, self.hidden, self.inter = T, sets, hidden, inter
+        self.tokens = T
+        self.name = f"w8a8_mlp_T{T}"
+        g = torch.Generator(device=dev).manual_seed(seed)
+        gh, gi = hidden // 32, inter // 32
+
+        def weights(cols, groups):
+            w = torch.randint(-127, 128, (cols, groups * 32), generator=g, device=dev,
+                              dtype=torch.int8)
+            sc = (torch.rand(cols, groups, generator=g, device=dev) * 2e-3 + 1e-4).half()
+            return w, sc
+
+        self.wu, self.wg, self.wd = [], [], []
+        for _ in range(sets):
+            self.wu.append(weights(inter, gh))
+            self.wg.append(weights(inter, gh))
+            self.wd.append(weights(hidden, gi))
+        self.x = [_randn16(g, (T, hidden), dev) for _ in range(sets)]
+        self.qx = [torch.empty(T, gh * 32, dtype=torch.int8, device=dev) for _ in range(sets)]
+        self.sx = [torch.empty(T, gh, dtype=torch.float32, device=dev) for _ in range(sets)]
+        self.up = [torch.empty(T, inter, dtype=torch.float16, device=dev) for _ in range(sets)]
+        self.act = [torch.empty(T, inter, dtype=torch.float16, device=dev) for _ in range(sets)]
+        self.qa = [torch.empty(T, gi * 32, dtype=torch.int8, device=dev) for _ in range(sets)]
+        self.sa = [torch.empty(T, gi, dtype=torch.float32, device=dev) for _ in range(sets)]
+        self.out = [torch.empty(T, hidden, dtype=torch.float16, device=dev) for _ in range(sets)]
+        S = range(sets)
+        self.bound_ops = {
+            "quantize_in": [ops.bind_quantize_activation(self.x[s], self.qx[s], self.sx[s])
+                            for s in S],
+            "up": [ops.bind_linear_w8a8(self.qx[s], self.sx[s], *self.wu[s], self.up[s]) for s in S],
+            "gate_swiglu": [ops.bind_linear_w8a8(self.qx[s], self.sx[s], *self.wg[s], self.act[s],
+                                                 _lib.LINEAR_SILU_MUL, 0, self.up[s]) for s in S],
+            "quantize_mid": [ops.bind_quantize_activation(self.act[s], self.qa[s], self.sa[s])
+                             for s in S],
+            "down": [ops.bind_linear_w8a8(self.qa[s], self.sa[s], *self.wd[s], self.out[s])
+                     for s in S],
+        }
+        self.bytes = {
+            "quantize_in": quantize_bytes(T, hidden),
+            "up": w8_bytes(T, inter, gh),
+            "gate_swiglu": w8_bytes(T, inter, gh) + T * inter * 2,
+            "quantize_mid": quantize_bytes(T, inter),
+            "down": w8_bytes(T, hidden, gi),
+        }
+
+    def launch(self, i):
+        for label in self.labels:
+            self.op(label, i)
+
+    def op(self, label, i):
+        self.bound_ops[label][i % self.sets]()
+
+    def kernels(self):
+        return "linearW8A8Gemv" if self.T == 1 else "linearW8A8Gemm"
+
+    def work(self, i):
+        return self.bytes["up"]
+
+    def config(self):
+        return {"workload": self.name, "tokens": self.T, "hidden": self.hidden,
+                "intermediate": self.inter, "group": 32, "sets": self.sets,
+                "ops": "quantizeActivation, linearW8A8 up, linearW8A8 gate + SwiGLU epilogue, "
+                       "quantizeActivation, linearW8A8 down"}
+
+    def cpu(self, budget_s):
+        import numpy as np
+        import oracle
+        import torch
+        s = 0
+        self.launch(s)
+        torch.cuda.synchronize()
+        x = host_u16(self.x[s])
+        wu, su = self.wu[s][0].cpu().numpy(), host_u16(self.wu[s][1])
+        wg, sg = self.wg[s][0].cpu().numpy(), host_u16(self.wg[s][1])
+        wd, sd = self.wd[s][0].cpu().numpy(), host_u16(self.wd[s][1])
+
+        def step():
+            qx, sx, _ = oracle.quantize_activation(x)
+            up = oracle.linear_w8a8(qx, sx, wu, su)
+            act = oracle.linear_w8a8(qx, sx, wg, sg, oracle.LINEAR_SILU_MUL, 0, up)
+            qa, sa, _ = oracle.quantize_activation(act)
+            return up, act, oracle.linear_w8a8(qa, sa, wd, sd)
+
+        up, act, out = step()
+        exact = bool(np.array_equal(up, host_u16(self.up[s])) and
+                     np.array_equal(act, host_u16(self.act[s])) and
+                     np.array_equal(out, host_u16(self.out[s])))
+        sec, runs = time_cpu(step, budget_s)
+        return {"value": sec * 1e6, "unit": "µs/layer", "cores": 1, "kind": "port",
+                "sample": f"the five ops on one weight set (T={self.T}), {runs} runs, scalar C "
+                          "oracle (orc_quantize_activation, orc_linear_w8a8)",
+                "gpu_bit_exact": exact}
+
+
 def _delta_inputs(g, dev, T, hk, dk, hv, dv):
     """DeltaUpdate operands as the reference graph produces them: L2-normalised
     fp32 q (x 1/sqrt(dk)) and k from fp16 N(0,1) (Graph.metal:96-109), fp16 v,
@@ -1196,6 +1318,8 @@ def main(argv=None) -> int:
         ("next_l2norm_delta_decode", lambda: DeltaNormUpdate(dev, 1, 128, seed=11)),
         ("next_l2norm_delta_gatednorm_1024", lambda: DeltaGatedNorm(dev, 1024, 8, seed=12)),
         ("next_l2norm_delta_gatednorm_decode", lambda: DeltaGatedNorm(dev, 1, 128, seed=13)),
+        ("next_w8a8_mlp_decode", lambda: W8A8Mlp(dev, 1, 4, seed=20)),
+        ("next_w8a8_mlp_prefill_128", lambda: W8A8Mlp(dev, 128, 4, seed=21)),
     ]
     unknown = only - {k for k, _ in builders} - {"headline"}
     if unknown:
@@ -1235,7 +1359,7 @@ def main(argv=None) -> int:
                 kern_s = entry["roofline"]["kernel_us_avg"] * 1e-6
                 entry["mfma_frac_recurrent_flops"] = round(
                     delta_flops(x.T, x.hv, x.dk, x.dv) / kern_s / 1e12 / MFMA_F16_PEAK_TFS, 5)
-            if isinstance(x, (AttnRows, DeltaFront, DeltaNormUpdate)):
+            if isinstance(x, (AttnRows, DeltaFront, DeltaNormUpdate, W8A8Mlp)):
                 entry["op_roofline"] = {
                     l: {"bytes": x.bytes[l],
                         "achieved_GBs": round(x.bytes[l] / (op_ms[l] * 1e-3) / 1e9, 1),

@@ -10,14 +10,14 @@
 //    a scale out). x / scale is the IEEE quotient; the reference's
 //    floor/fraction tie rule is round half to even (v_rndne_f32).
 //  * GEMV (one row, the decode step): bound by the weight stream. A
-//    256-thread workgroup serves 16 output columns with 16 lanes each, the
+//    one-wave workgroup serves 4 output columns with 16 lanes each, the
 //    reference's linearW8GemvLanes: lane l takes groups l, l + 16, ... of its
 //    column, so the 16 lanes of a column read 512 contiguous weight bytes per
-//    step and a wave streams 2 KB. Group dots run on v_dot4_i32_i8 (exact
-//    int32); each group adds (float(dot) * a) * w to the lane's fp32 sum in
-//    group order and the lanes meet by the xor butterfly, which is the
-//    reference's arithmetic order, so outputs are its bits. Four groups'
-//    loads go out before their arithmetic.
+//    step. Group dots run on v_dot4_i32_i8 (exact int32); each group adds
+//    (float(dot) * a) * w to the lane's fp32 sum in group order and the lanes
+//    meet by the xor butterfly, which is the reference's arithmetic order, so
+//    outputs are its bits. Eight groups' weight loads go out before their
+//    arithmetic.
 //  * GEMM (several rows): the reference's 8 lanes per column and 4 rows per
 //    lane; a weight group is loaded once for its four rows.
 #include "exact_fp.hpp"
@@ -152,9 +152,14 @@ struct W8Args {
   unsigned outputWidth, firstRow, groups, rows, columns, epilogue, block;
 };
 
-constexpr int kGemvLanes = 16, kGemvCols = 256 / kGemvLanes, kGemvUnroll = 4;
+// One wave per workgroup (4 columns): even the 2560-column down projection
+// spreads over 640 workgroups. A lane requests the weights of 8 of its
+// groups (256 bytes) before using any; the activations, read by every
+// column, come from L1/L2.
+constexpr int kGemvLanes = 16, kGemvThreads = 64, kGemvCols = kGemvThreads / kGemvLanes;
+constexpr int kGemvUnroll = 8;
 
-__global__ __launch_bounds__(256) void gemv_kernel(
+__global__ __launch_bounds__(kGemvThreads) void gemv_kernel(
     const int8_t *__restrict__ act, const float *__restrict__ as, const int8_t *__restrict__ w,
     const uint16_t *__restrict__ ws, void *out, const void *aux, const float *bias, W8Args p) {
   const unsigned col = blockIdx.x * kGemvCols + threadIdx.x / kGemvLanes;
@@ -165,27 +170,83 @@ __global__ __launch_bounds__(256) void gemv_kernel(
     const uint4_t *arow = reinterpret_cast<const uint4_t *>(act);
     const uint16_t *wsrow = ws + (size_t)col * p.groups;
     for (unsigned g0 = l; g0 < p.groups; g0 += kGemvLanes * kGemvUnroll) {
-      uint4_t wv[kGemvUnroll][2], av[kGemvUnroll][2];
-      float asv[kGemvUnroll], wsv[kGemvUnroll];
+      uint4_t wv[kGemvUnroll][2];
+      float wsv[kGemvUnroll];
 #pragma unroll
       for (int u = 0; u < kGemvUnroll; ++u) {
         const unsigned g = min(g0 + kGemvLanes * u, p.groups - 1); // clamped: in bounds
         wv[u][0] = __builtin_nontemporal_load(wrow + 2 * g);
         wv[u][1] = __builtin_nontemporal_load(wrow + 2 * g + 1);
-        av[u][0] = arow[2 * g];
-        av[u][1] = arow[2 * g + 1];
-        asv[u] = as[g];
         wsv[u] = h2f(wsrow[g]);
       }
 #pragma unroll
-      for (int u = 0; u < kGemvUnroll; ++u)
-        if (g0 + kGemvLanes * u < p.groups)
-          acc = add_term(acc, group_dot(av[u][0], av[u][1], wv[u][0], wv[u][1]), asv[u],
-                         wsv[u]);
+      for (int u = 0; u < kGemvUnroll; ++u) {
+        const unsigned g = g0 + kGemvLanes * u;
+        if (g < p.groups)
+          acc = add_term(acc, group_dot(arow[2 * g], arow[2 * g + 1], wv[u][0], wv[u][1]),
+                         as[g], wsv[u]);
+      }
     }
   }
   // The xor butterfly of the column's 16 lanes (every lane ends with the
   // same sum: fp32 addition is commutative).
+#pragma unroll
+  for (int m = kGemvLanes / 2; m >= 1; m /= 2)
+    acc = __fadd_rn(acc, __shfl_xor(acc, m, kGemvLanes));
+  if (l == 0 && col < p.columns) {
+    const unsigned column = p.firstRow + col;
+    store_linear(out, aux, bias, column, column, p.epilogue, p.block, acc);
+  }
+}
+
+// Long rows (more than 128 groups: 8 per lane or more): four waves share the
+// same 4 columns. Wave w computes the group terms (float(dot) * a) * w of the
+// w-th quarter of every lane's groups, all its loads issued at once, into
+// LDS; wave 0 then adds each lane's terms in group order -- the same fp32
+// sums as one lane would form -- and finishes as above.
+constexpr int kSplitWaves = 4, kSplitMaxSteps = 64; // groups per lane <= 64
+constexpr int kSplitPer = kSplitMaxSteps / kSplitWaves;
+
+__global__ __launch_bounds__(64 * kSplitWaves) void gemv_split_kernel(
+    const int8_t *__restrict__ act, const float *__restrict__ as, const int8_t *__restrict__ w,
+    const uint16_t *__restrict__ ws, void *out, const void *aux, const float *bias, W8Args p) {
+  __shared__ float sT[kSplitMaxSteps][64];
+  const unsigned wave = threadIdx.x / 64, t = threadIdx.x % 64;
+  const unsigned col = blockIdx.x * kGemvCols + t / kGemvLanes;
+  const unsigned l = t % kGemvLanes;
+  const unsigned steps = (p.groups + kGemvLanes - 1) / kGemvLanes; // a lane's steps, at most
+  const unsigned per = (steps + kSplitWaves - 1) / kSplitWaves, i0 = wave * per;
+  if (col < p.columns) {
+    const uint4_t *wrow = reinterpret_cast<const uint4_t *>(w + (size_t)col * p.groups * kGroup);
+    const uint4_t *arow = reinterpret_cast<const uint4_t *>(act);
+    const uint16_t *wsrow = ws + (size_t)col * p.groups;
+    uint4_t wv[kSplitPer][2];
+    float wsv[kSplitPer];
+#pragma unroll
+    for (int u = 0; u < kSplitPer; ++u) {
+      const unsigned g = min(l + kGemvLanes * (i0 + u), p.groups - 1); // clamped: in bounds
+      if ((unsigned)u < per) {
+        wv[u][0] = __builtin_nontemporal_load(wrow + 2 * g);
+        wv[u][1] = __builtin_nontemporal_load(wrow + 2 * g + 1);
+        wsv[u] = h2f(wsrow[g]);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kSplitPer; ++u) {
+      const unsigned g = l + kGemvLanes * (i0 + u);
+      if ((unsigned)u < per && g < p.groups)
+        sT[i0 + u][t] = __fmul_rn(
+            __fmul_rn((float)group_dot(arow[2 * g], arow[2 * g + 1], wv[u][0], wv[u][1]), as[g]),
+            wsv[u]);
+    }
+  }
+  __syncthreads();
+  if (wave != 0)
+    return;
+  float acc = 0.0f;
+  if (col < p.columns)
+    for (unsigned i = 0; l + kGemvLanes * i < p.groups; ++i)
+      acc = __fadd_rn(acc, sT[i][t]);
 #pragma unroll
   for (int m = kGemvLanes / 2; m >= 1; m /= 2)
     acc = __fadd_rn(acc, __shfl_xor(acc, m, kGemvLanes));
@@ -312,9 +373,13 @@ hipError_t launch_linear_w8a8(const int8_t *act, const float *as, const int8_t *
                               const uint16_t *ws, void *out, const void *aux, const float *bias,
                               const W8Shape &s, hipStream_t stream) {
   const W8Args a{s.outputWidth, s.firstRow, s.groups, s.rows, s.columns, s.epilogue, s.block};
-  if (s.rows == 1)
-    hipLaunchKernelGGL(gemv_kernel, dim3((s.columns + kGemvCols - 1) / kGemvCols), dim3(256),
-                       0, stream, act, as, w, ws, out, aux, bias, a);
+  const unsigned steps = (s.groups + kGemvLanes - 1) / kGemvLanes;
+  if (s.rows == 1 && steps > kGemvUnroll && steps <= kSplitMaxSteps)
+    hipLaunchKernelGGL(gemv_split_kernel, dim3((s.columns + kGemvCols - 1) / kGemvCols),
+                       dim3(64 * kSplitWaves), 0, stream, act, as, w, ws, out, aux, bias, a);
+  else if (s.rows == 1)
+    hipLaunchKernelGGL(gemv_kernel, dim3((s.columns + kGemvCols - 1) / kGemvCols),
+                       dim3(kGemvThreads), 0, stream, act, as, w, ws, out, aux, bias, a);
   else
     hipLaunchKernelGGL(gemm_kernel,
                        dim3((s.columns + kGemmCols - 1) / kGemmCols,

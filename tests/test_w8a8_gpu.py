@@ -97,6 +97,7 @@ def _same(got, want):
     (1, 9216, 80),    # Qwen3.5-4B MLP gate/up, decode
     (1, 2560, 288),   # MLP down, decode
     (1, 37, 5), (1, 16, 1), (1, 33, 17),
+    (1, 50, 150), (1, 20, 1024), (1, 12, 1030),   # four waves per column; the limit; past it
     (2, 40, 9), (3, 70, 12), (4, 32, 80), (5, 19, 3), (64, 256, 80)])
 def test_linear_bit_exact(gpu, rows, columns, groups):
     print(f"linear rows={rows} columns={columns} groups={groups}", flush=True)
@@ -114,11 +115,11 @@ def test_linear_shard_writes_only_its_columns(gpu):
     assert _same(got1, want1)
 
 
-@pytest.mark.parametrize("rows", [1, 6])
+@pytest.mark.parametrize("rows,groups", [(1, 20), (1, 160), (6, 20)])
 @pytest.mark.parametrize("epilogue", [1, 2, 3, 4, 5, 6])
-def test_linear_epilogues_bit_exact(gpu, rows, epilogue):
-    print(f"linear epilogue {epilogue} rows={rows}", flush=True)
-    columns, groups = 96, 20
+def test_linear_epilogues_bit_exact(gpu, rows, groups, epilogue):
+    print(f"linear epilogue {epilogue} rows={rows} groups={groups}", flush=True)
+    columns = 96
     # wide activations: projections spread over the epilogues' ranges
     xq, xs, w, ws = _case(100 + epilogue * 10 + rows, rows, columns, groups, spread=6.0)
     r = np.random.default_rng(epilogue)
