@@ -18,8 +18,10 @@
 //    meet by the xor butterfly, which is the reference's arithmetic order, so
 //    outputs are its bits. Eight groups' weight loads go out before their
 //    arithmetic.
-//  * GEMM (several rows): the reference's 8 lanes per column and 4 rows per
-//    lane; a weight group is loaded once for its four rows.
+//  * GEMM (several rows): the reference's 8 lanes per column. Below 16 rows,
+//    a lane holds 4 rows and a weight group is loaded once for them; from 16
+//    rows the group dots come from int8 MFMA over 32 x 32 tiles, with the 8
+//    lanes' fp32 sums kept apart and merged in the butterfly's order.
 #include "exact_fp.hpp"
 #include "hip_common.hpp"
 #include "kernels.hpp"
@@ -299,6 +301,194 @@ __global__ __launch_bounds__(256) void gemm_kernel(
   }
 }
 
+// ------------------------------------------------------------- MFMA GEMM
+
+// Many rows (prefill): the group dots come from v_mfma_i32_32x32x32_i8, one
+// instruction per 32-row x 32-column tile and group (K = 32 is exactly one
+// group, so each int32 result is the group's exact dot), and the VALU adds
+// (float(dot) * a) * w to fp32 sums. The reference's GEMM gives each output 8
+// lanes, lane l summing groups l, l + 8, ... in order before the xor
+// butterfly; here those 8 lane classes are split over the workgroup's waves
+// (wave w takes the groups g = w (mod waves), i.e. classes w and w + 4 with 4
+// waves, class w with 8), each class keeping its own fp32 sum per output, and
+// the sums meet through LDS in the butterfly's order
+// ((c0 + c4) + (c2 + c6)) + ((c1 + c5) + (c3 + c7)). So the bits are the
+// reference's. The per-element fp32 work (convert, two products, add: 4 VALU
+// operations per output and group) is the floor of the kernel.
+//
+// Staging: a step covers kPer groups per wave, i.e. (waves x kPer x 32)
+// consecutive bytes of each of the tile's 32 activation rows and 32 weight
+// rows, plus their scales. Each thread loads 16-byte chunks of each operand
+// (whole cache lines per row) kDepth - 1 steps ahead into registers and
+// writes them to the other of two LDS buffers, before the current step's
+// arithmetic (kEarly) or after it; one barrier a step. Rows are padded by 16
+// bytes so the MFMA operand reads (lane i: row i % 32) meet no bank
+// conflicts. Large grids (at least kMfmaManyTiles tiles) take 8 waves, one
+// group each a step, loads one step ahead, staged early: 71 VGPRs, so three
+// workgroups share a CU. Small grids (the 2560-column down projection) take
+// loads three steps ahead, staged late, which hides more latency inside a
+// workgroup when few workgroups share a CU.
+//
+// Operand layout: lane i supplies row (column) i % 32 of the tile and the
+// 16 bytes (i / 32) * 16 of the group for both operands; any K order shared
+// by the two operands gives the same exact integer dot. Lane i's results are
+// column i % 32 and rows 8 * (r / 4) + 4 * (i / 32) + r % 4 of register r.
+//
+// Workgroups sharing a column tile run on one XCD (blockIdx % 8 selects the
+// XCD), so each weight tile is read from HBM once and then from that XCD's L2.
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+
+constexpr unsigned kTile = 32, kMfmaMinRows = 16, kMfmaManyTiles = 512;
+
+// A step stages kWaves * kPer groups; loads run kDepth - 1 steps ahead.
+template <int kWaves, int kPer, int kDepth> struct MfmaCfg {
+  static constexpr unsigned kSpan = kWaves * kPer;             // groups per step
+  static constexpr unsigned kPitch = kSpan * kGroup + 16;      // bytes per staged row
+  static constexpr unsigned kOperand = kTile * kPitch;         // one operand tile
+  static constexpr unsigned kScales = kSpan * kTile * 4;       // [group][32] fp32
+  static constexpr unsigned kBuffer = 2 * kOperand + 2 * kScales;
+  static constexpr unsigned kSums = kWaves * kTile * kTile * 4;
+  static constexpr unsigned kBytes = 2 * kBuffer > kSums ? 2 * kBuffer : kSums;
+};
+
+template <int kWaves, int kPer, int kDepth, bool kEarly>
+__global__ __launch_bounds__(64 * kWaves) void gemm_mfma_kernel(
+    const int8_t *__restrict__ act, const float *__restrict__ as, const int8_t *__restrict__ w,
+    const uint16_t *__restrict__ ws, void *out, const void *aux, const float *bias, W8Args p,
+    unsigned rowTiles) {
+  using L = MfmaCfg<kWaves, kPer, kDepth>;
+  constexpr int kClasses = 8 / kWaves; // lane classes per wave
+  static_assert(L::kSpan % 8 == 0, "a step must hold whole sets of the 8 lane classes");
+  __shared__ __align__(16) unsigned char lds[L::kBytes];
+  const unsigned nwg = gridDim.x, b = blockIdx.x, x = b % 8;
+  const unsigned v = x * (nwg / 8) + min(x, nwg % 8) + b / 8;
+  const unsigned row0 = (v % rowTiles) * kTile, col0 = (v / rowTiles) * kTile;
+  const unsigned tid = threadIdx.x, lane = tid % 64, wave = tid / 64;
+  const size_t k = (size_t)p.groups * kGroup;
+  const unsigned nsteps = (p.groups + L::kSpan - 1) / L::kSpan;
+
+  // Staging roles: chunks schunk + 2 * kWaves * j (16 bytes each, j < kPer)
+  // of one row of each operand; kPer scales of one row (column) for the
+  // first 32 * kWaves threads.
+  const unsigned srow = tid / (2 * kWaves), schunk = tid % (2 * kWaves);
+  const int8_t *sact = act + min(row0 + srow, p.rows - 1) * k + 16 * (schunk % 2);
+  const int8_t *swt = w + min(col0 + srow, p.columns - 1) * k + 16 * (schunk % 2);
+  const bool scaler = tid < kTile * kWaves;
+  const unsigned sr = tid / kWaves, sg = tid % kWaves;
+  const float *sas = as + (size_t)min(row0 + sr, p.rows - 1) * p.groups;
+  const uint16_t *sws = ws + (size_t)min(col0 + sr, p.columns - 1) * p.groups;
+  v4i ra[kDepth][kPer], rb[kDepth][kPer];
+  float rs[kDepth][kPer];
+  uint16_t rt[kDepth][kPer];
+  auto load = [&](int slot, unsigned step) {
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+      const unsigned g = min(step * L::kSpan + schunk / 2 + kWaves * j, p.groups - 1); // clamped
+      ra[slot][j] = *reinterpret_cast<const v4i *>(sact + (size_t)g * kGroup);
+      rb[slot][j] = *reinterpret_cast<const v4i *>(swt + (size_t)g * kGroup);
+      if (scaler) {
+        const unsigned gs = min(step * L::kSpan + sg + kWaves * j, p.groups - 1);
+        rs[slot][j] = sas[gs];
+        rt[slot][j] = sws[gs];
+      }
+    }
+  };
+  auto stage = [&](int slot, unsigned buf) {
+    unsigned char *base = lds + buf * L::kBuffer;
+    float *sc = reinterpret_cast<float *>(base + 2 * L::kOperand);
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+      const unsigned at = srow * L::kPitch + 16 * (schunk + 2 * kWaves * j);
+      *reinterpret_cast<v4i *>(base + at) = ra[slot][j];
+      *reinterpret_cast<v4i *>(base + L::kOperand + at) = rb[slot][j];
+      if (scaler) {
+        sc[(sg + kWaves * j) * kTile + sr] = rs[slot][j];
+        sc[L::kSpan * kTile + (sg + kWaves * j) * kTile + sr] = h2f(rt[slot][j]);
+      }
+    }
+  };
+
+#pragma unroll
+  for (int d = 0; d < kDepth - 1; ++d)
+    if ((unsigned)d < nsteps)
+      load(d, d);
+  stage(0, 0);
+  __syncthreads();
+
+  const unsigned m = lane % kTile, h = lane / kTile;
+  const v16i zero = {};
+  float acc[kClasses][16];
+#pragma unroll
+  for (int c = 0; c < kClasses; ++c)
+#pragma unroll
+    for (int r = 0; r < 16; ++r)
+      acc[c][r] = 0.0f;
+  for (unsigned s0 = 0; s0 < nsteps; s0 += kDepth) {
+#pragma unroll
+    for (int d = 0; d < kDepth; ++d) {
+      const unsigned step = s0 + d;
+      if (step >= nsteps)
+        break;
+      if (step + kDepth - 1 < nsteps)
+        load((d + kDepth - 1) % kDepth, step + kDepth - 1);
+      // The other buffer was released by the previous step's barrier.
+      if (kEarly && step + 1 < nsteps)
+        stage((d + 1) % kDepth, (step + 1) % 2);
+      const unsigned char *base = lds + (step % 2) * L::kBuffer;
+      const float *sc = reinterpret_cast<const float *>(base + 2 * L::kOperand);
+#pragma unroll
+      for (int j = 0; j < kPer; ++j) {
+        const unsigned gl = wave + kWaves * j; // group within the step
+        if (step * L::kSpan + gl < p.groups) {
+          const unsigned off = m * L::kPitch + gl * kGroup + 16 * h;
+          const v4i a = *reinterpret_cast<const v4i *>(base + off);
+          const v4i bw = *reinterpret_cast<const v4i *>(base + L::kOperand + off);
+          const float wsv = sc[L::kSpan * kTile + gl * kTile + m];
+          const v16i dots = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, bw, zero, 0, 0, 0);
+          const float4 *sa = reinterpret_cast<const float4 *>(sc + gl * kTile + 4 * h);
+          const int c = j % kClasses;
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const float4 a4 = sa[2 * q];
+            acc[c][4 * q + 0] = add_term(acc[c][4 * q + 0], dots[4 * q + 0], a4.x, wsv);
+            acc[c][4 * q + 1] = add_term(acc[c][4 * q + 1], dots[4 * q + 1], a4.y, wsv);
+            acc[c][4 * q + 2] = add_term(acc[c][4 * q + 2], dots[4 * q + 2], a4.z, wsv);
+            acc[c][4 * q + 3] = add_term(acc[c][4 * q + 3], dots[4 * q + 3], a4.w, wsv);
+          }
+        }
+      }
+      if (!kEarly && step + 1 < nsteps)
+        stage((d + 1) % kDepth, (step + 1) % 2);
+      __syncthreads();
+    }
+  }
+
+  float *sums = reinterpret_cast<float *>(lds) + wave * kTile * kTile;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const unsigned rr = 8 * (r / 4) + 4 * h + r % 4;
+    sums[rr * kTile + m] = kClasses == 2 ? __fadd_rn(acc[0][r], acc[kClasses - 1][r]) : acc[0][r];
+  }
+  __syncthreads();
+  for (unsigned e = tid; e < kTile * kTile; e += 64 * kWaves) {
+    const unsigned row = row0 + e / kTile, col = col0 + e % kTile;
+    if (row >= p.rows || col >= p.columns)
+      continue;
+    const float *s = reinterpret_cast<const float *>(lds) + e;
+    constexpr unsigned T = kTile * kTile;
+    float total;
+    if (kWaves == 4) // wave w holds c_w + c_(w+4)
+      total = __fadd_rn(__fadd_rn(s[0], s[2 * T]), __fadd_rn(s[T], s[3 * T]));
+    else
+      total = __fadd_rn(__fadd_rn(__fadd_rn(s[0], s[4 * T]), __fadd_rn(s[2 * T], s[6 * T])),
+                        __fadd_rn(__fadd_rn(s[T], s[5 * T]), __fadd_rn(s[3 * T], s[7 * T])));
+    const unsigned column = p.firstRow + col;
+    store_linear(out, aux, bias, (size_t)row * p.outputWidth + column, column, p.epilogue,
+                 p.block, total);
+  }
+}
+
 // ------------------------------------------------------------- embeddings
 
 // embeddingW8 (Graph.metal:16-31): eight outputs per lane (they share a
@@ -380,7 +570,16 @@ hipError_t launch_linear_w8a8(const int8_t *act, const float *as, const int8_t *
   else if (s.rows == 1)
     hipLaunchKernelGGL(gemv_kernel, dim3((s.columns + kGemvCols - 1) / kGemvCols),
                        dim3(kGemvThreads), 0, stream, act, as, w, ws, out, aux, bias, a);
-  else
+  else if (s.rows >= kMfmaMinRows) {
+    const unsigned rowTiles = (s.rows + kTile - 1) / kTile;
+    const unsigned tiles = rowTiles * ((s.columns + kTile - 1) / kTile);
+    if (tiles >= kMfmaManyTiles)
+      hipLaunchKernelGGL((gemm_mfma_kernel<8, 1, 2, true>), dim3(tiles), dim3(512), 0, stream,
+                         act, as, w, ws, out, aux, bias, a, rowTiles);
+    else
+      hipLaunchKernelGGL((gemm_mfma_kernel<8, 1, 4, false>), dim3(tiles), dim3(512), 0, stream,
+                         act, as, w, ws, out, aux, bias, a, rowTiles);
+  } else
     hipLaunchKernelGGL(gemm_kernel,
                        dim3((s.columns + kGemmCols - 1) / kGemmCols,
                             (s.rows + kGemmRows - 1) / kGemmRows),

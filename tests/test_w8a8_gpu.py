@@ -98,7 +98,11 @@ def _same(got, want):
     (1, 2560, 288),   # MLP down, decode
     (1, 37, 5), (1, 16, 1), (1, 33, 17),
     (1, 50, 150), (1, 20, 1024), (1, 12, 1030),   # four waves per column; the limit; past it
-    (2, 40, 9), (3, 70, 12), (4, 32, 80), (5, 19, 3), (64, 256, 80)])
+    (2, 40, 9), (3, 70, 12), (4, 32, 80), (5, 19, 3), (15, 40, 9),
+    # the MFMA kernel (16 rows or more): eight waves per tile, four once the
+    # grid has 1024 tiles, and ragged row and column tiles
+    (16, 40, 9), (37, 70, 12), (64, 256, 80), (100, 33, 1), (33, 65, 3), (128, 96, 288),
+    (32, 32768, 2), (70, 15000, 3), (20, 40, 600)])
 def test_linear_bit_exact(gpu, rows, columns, groups):
     print(f"linear rows={rows} columns={columns} groups={groups}", flush=True)
     xq, xs, w, ws = _case(rows * 7 + columns + groups, rows, columns, groups)
@@ -113,9 +117,13 @@ def test_linear_shard_writes_only_its_columns(gpu):
     assert np.all(got[:, :40] == 0x4700) and np.all(got[:, 88:] == 0x4700)
     got1, want1 = _run_linear(gpu, xq[:1], xs[:1], w, ws, first_row=52, width=100)
     assert _same(got1, want1)
+    xq, xs, w, ws = _case(4, 40, 48, 7)
+    got2, want2 = _run_linear(gpu, xq, xs, w, ws, first_row=30, width=100)
+    assert _same(got2, want2)
+    assert np.all(got2[:, :30] == 0x4700) and np.all(got2[:, 78:] == 0x4700)
 
 
-@pytest.mark.parametrize("rows,groups", [(1, 20), (1, 160), (6, 20)])
+@pytest.mark.parametrize("rows,groups", [(1, 20), (1, 160), (6, 20), (20, 20), (40, 160)])
 @pytest.mark.parametrize("epilogue", [1, 2, 3, 4, 5, 6])
 def test_linear_epilogues_bit_exact(gpu, rows, groups, epilogue):
     print(f"linear epilogue {epilogue} rows={rows} groups={groups}", flush=True)
