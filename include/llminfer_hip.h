@@ -114,6 +114,19 @@ typedef struct EmbedParams {
   unsigned tokens, hidden, firstRow, rowCount;
 } EmbedParams;
 
+/* lib/Backend/Metal/Kernels/GraphParams.h:4-6: a view of at most three
+ * dimensions (outermost first), strides and offset in elements */
+typedef struct HalfViewParams {
+  unsigned count, offset, dims[3], strides[3];
+} HalfViewParams;
+
+/* lib/Backend/Metal/Kernels/ReferenceParams.h:18-21 (rowCount: output
+ * columns this call computes, from firstRow) */
+typedef struct LinearParams {
+  unsigned tokens, inputWidth, outputWidth, firstRow, rowCount;
+  unsigned epilogue, epilogueBlock;
+} LinearParams;
+
 /* LinearEpilogue, lib/Backend/Metal/Kernels/ReferenceParams.h:8-16 */
 enum llmi_linear_epilogue {
   LLMI_LINEAR_NONE = 0,
@@ -151,7 +164,13 @@ enum llmi_hip_op {
   LLMI_HIP_OP_QUANTIZE_ACTIVATION = 13, /* params: QuantizeParams */
   LLMI_HIP_OP_LINEAR_W8A8 = 14,         /* params: LinearW8Params */
   LLMI_HIP_OP_EMBEDDING_W8 = 15,        /* params: GroupedEmbedParams */
-  LLMI_HIP_OP_EMBEDDING = 16            /* params: EmbedParams */
+  LLMI_HIP_OP_EMBEDDING = 16,           /* params: EmbedParams */
+  LLMI_HIP_OP_RESIDUAL_ADD = 17,        /* params: ElementParams */
+  LLMI_HIP_OP_SWIGLU = 18,              /* params: ElementParams */
+  LLMI_HIP_OP_SILU = 19,                /* params: ElementParams */
+  LLMI_HIP_OP_MULTIPLY = 20,            /* params: ElementParams */
+  LLMI_HIP_OP_COPY_HALF_VIEW = 21,      /* params: HalfViewParams */
+  LLMI_HIP_OP_LINEAR_F16 = 22           /* params: LinearParams */
 };
 
 /* ---------------------------------------------------------------- KvAppend
@@ -442,6 +461,38 @@ LLMI_HIP_API int llmi_hip_embedding_w8(const uint32_t *ids, const int8_t *weight
  * for ids in [firstRow, firstRow + rowCount). */
 LLMI_HIP_API int llmi_hip_embedding(const uint32_t *ids, const uint16_t *weight,
                                     uint16_t *output, EmbedParams p, void *stream);
+
+/* -------------------------------------------- elementwise, views, linearF16
+ * The whole-graph plan's remaining ops (lowered at MetalExecutionPlan.cpp:
+ * 469-477, 604-626). Elementwise ops take count fp16 elements, dense. */
+
+/* residualAdd (Reference.metal:119-126): out[i] = fp16(a[i] + b[i]). */
+LLMI_HIP_API int llmi_hip_residual_add(const uint16_t *a, const uint16_t *b, uint16_t *out,
+                                       ElementParams p, void *stream);
+
+/* swiGlu (Reference.metal:128-135): out[i] = fp16(fp16(silu(gate[i])) * up[i]). */
+LLMI_HIP_API int llmi_hip_swiglu(const uint16_t *gate, const uint16_t *up, uint16_t *out,
+                                 ElementParams p, void *stream);
+
+/* siluF16 (Graph.metal:70-76): out[i] = fp16(silu(in[i])). In place allowed. */
+LLMI_HIP_API int llmi_hip_silu(const uint16_t *in, uint16_t *out, ElementParams p, void *stream);
+
+/* multiplyF16 (Graph.metal:87-94): out[i] = fp16(a[i] * b[i]). */
+LLMI_HIP_API int llmi_hip_multiply(const uint16_t *a, const uint16_t *b, uint16_t *out,
+                                   ElementParams p, void *stream);
+
+/* copyHalfView (Graph.metal:1-14): out[i] = src[offset + sum_d index_d(i) *
+ * strides[d]], i < count, the index taken over dims (outermost first). */
+LLMI_HIP_API int llmi_hip_copy_half_view(const uint16_t *src, uint16_t *out, HalfViewParams p,
+                                         void *stream);
+
+/* linearF16 (Reference.metal:61-103): for row < tokens, col < rowCount,
+ * acc = fma chain over k = 0 .. inputWidth-1 of input[row][k] *
+ * weight[col][k] in fp32, then storeLinear at output[row * outputWidth +
+ * firstRow + col] with the given epilogue (aux, bias as for linearW8A8). */
+LLMI_HIP_API int llmi_hip_linear_f16(const uint16_t *input, const uint16_t *weight, void *output,
+                                     const void *aux, const float *bias, LinearParams p,
+                                     void *stream);
 
 /* ----------------------------------------------------------------- helpers */
 

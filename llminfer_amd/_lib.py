@@ -35,6 +35,12 @@ OP_QUANTIZE_ACTIVATION = 13
 OP_LINEAR_W8A8 = 14
 OP_EMBEDDING_W8 = 15
 OP_EMBEDDING = 16
+OP_RESIDUAL_ADD = 17
+OP_SWIGLU = 18
+OP_SILU = 19
+OP_MULTIPLY = 20
+OP_COPY_HALF_VIEW = 21
+OP_LINEAR_F16 = 22
 
 # LinearEpilogue (ReferenceParams.h:8-16)
 LINEAR_NONE, LINEAR_SILU, LINEAR_SILU_MUL, LINEAR_SIGMOID_COLUMNS = 0, 1, 2, 3
@@ -90,6 +96,16 @@ class GroupedEmbedParams(C.Structure):
 
 class EmbedParams(C.Structure):
     _fields_ = [(n, C.c_uint) for n in ("tokens", "hidden", "firstRow", "rowCount")]
+
+
+class HalfViewParams(C.Structure):
+    _fields_ = [("count", C.c_uint), ("offset", C.c_uint), ("dims", C.c_uint * 3),
+                ("strides", C.c_uint * 3)]
+
+
+class LinearParams(C.Structure):
+    _fields_ = [(n, C.c_uint) for n in ("tokens", "inputWidth", "outputWidth", "firstRow",
+                                        "rowCount", "epilogue", "epilogueBlock")]
 
 
 class GqaParams(C.Structure):
@@ -159,6 +175,12 @@ SIGNATURES = {
     "llmi_hip_linear_w8a8": (C.c_int, [_P, _P, _P, _P, _P, _P, _P, LinearW8Params, _P]),
     "llmi_hip_embedding_w8": (C.c_int, [_P, _P, _P, _P, GroupedEmbedParams, _P]),
     "llmi_hip_embedding": (C.c_int, [_P, _P, _P, EmbedParams, _P]),
+    "llmi_hip_residual_add": (C.c_int, [_P, _P, _P, ElementParams, _P]),
+    "llmi_hip_swiglu": (C.c_int, [_P, _P, _P, ElementParams, _P]),
+    "llmi_hip_silu": (C.c_int, [_P, _P, ElementParams, _P]),
+    "llmi_hip_multiply": (C.c_int, [_P, _P, _P, ElementParams, _P]),
+    "llmi_hip_copy_half_view": (C.c_int, [_P, _P, HalfViewParams, _P]),
+    "llmi_hip_linear_f16": (C.c_int, [_P, _P, _P, _P, _P, LinearParams, _P]),
     "llmi_hip_workspace_init": (C.c_int, [_P, _SZ, _P]),
     "llmi_hip_dispatch_count": (C.c_uint, [C.c_int, _P]),
     "llmi_hip_kernel_name": (C.c_char_p, [C.c_int, _P, C.c_uint]),

@@ -32,12 +32,12 @@ COMMON = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}",
           "-fvisibility=hidden"]
 
 
-# Per-file additions. norm_rope.hip, delta_front.hip and w8a8.hip reproduce
+# Per-file additions. norm_rope.hip, delta_front.hip, w8a8.hip and graph_ops.hip reproduce
 # the reference's fp16 rounding points bit for bit, which needs every fp32 product rounded on its own: under
 # the default -ffp-contract=fast the backend folds a product and the fp16
 # conversion or add after it into one fused instruction.
 FILE_FLAGS = {"norm_rope.hip": ["-ffp-contract=off"], "delta_front.hip": ["-ffp-contract=off"],
-              "w8a8.hip": ["-ffp-contract=off"]}
+              "w8a8.hip": ["-ffp-contract=off"], "graph_ops.hip": ["-ffp-contract=off"]}
 
 
 def hipcc() -> str:

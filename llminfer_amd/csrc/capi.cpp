@@ -239,8 +239,6 @@ int llmi_hip_delta_gates(const uint16_t *a, const uint16_t *b, const float *a_lo
 
 // ------------------------------------------------------ W8A8 projections
 
-static bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
-
 int llmi_hip_quantize_activation(const uint16_t *input, int8_t *quantized, float *scales,
                                  uint32_t *invalid, QuantizeParams p, void *stream) {
   if (p.rows == 0 || p.width == 0)
@@ -329,6 +327,95 @@ int llmi_hip_embedding(const uint32_t *ids, const uint16_t *weight, uint16_t *ou
   return launched(launch_embedding(ids, weight, output, p.tokens, p.hidden, p.firstRow,
                                    p.rowCount, static_cast<hipStream_t>(stream)),
                   "embedding");
+}
+
+static int elementwise(ElementwiseKind kind, const char *name, const uint16_t *a,
+                       const uint16_t *b, uint16_t *out, ElementParams p, void *stream) {
+  if (p.count == 0)
+    return LLMI_HIP_OK;
+  if (!a || !out || (kind != ElementwiseKind::Silu && !b))
+    return fail(LLMI_HIP_INVALID_ARGUMENT, "%s: null buffer", name);
+  return launched(launch_elementwise(kind, a, b, out, p.count, static_cast<hipStream_t>(stream)),
+                  name);
+}
+
+int llmi_hip_residual_add(const uint16_t *a, const uint16_t *b, uint16_t *out, ElementParams p,
+                          void *stream) {
+  return elementwise(ElementwiseKind::Add, "residualAdd", a, b, out, p, stream);
+}
+
+int llmi_hip_swiglu(const uint16_t *gate, const uint16_t *up, uint16_t *out, ElementParams p,
+                    void *stream) {
+  return elementwise(ElementwiseKind::SwiGlu, "swiGlu", gate, up, out, p, stream);
+}
+
+int llmi_hip_silu(const uint16_t *in, uint16_t *out, ElementParams p, void *stream) {
+  return elementwise(ElementwiseKind::Silu, "siluF16", in, nullptr, out, p, stream);
+}
+
+int llmi_hip_multiply(const uint16_t *a, const uint16_t *b, uint16_t *out, ElementParams p,
+                      void *stream) {
+  return elementwise(ElementwiseKind::Multiply, "multiplyF16", a, b, out, p, stream);
+}
+
+static int check_view(const HalfViewParams &p) {
+  uint64_t last = p.offset;
+  for (int d = 0; d < 3; ++d) {
+    if (p.dims[d] == 0)
+      return fail(LLMI_HIP_INVALID_ARGUMENT, "copyHalfView: zero extent on axis %d", d);
+    last += (uint64_t)(p.dims[d] - 1) * p.strides[d];
+  }
+  if ((uint64_t)p.dims[0] * p.dims[1] * p.dims[2] != p.count)
+    return fail(LLMI_HIP_INVALID_ARGUMENT, "copyHalfView: count %u is not the view's extent",
+                p.count);
+  if (last > UINT32_MAX)
+    return fail(LLMI_HIP_INVALID_ARGUMENT, "copyHalfView: exceeds the 32-bit index range");
+  return LLMI_HIP_OK;
+}
+
+int llmi_hip_copy_half_view(const uint16_t *src, uint16_t *out, HalfViewParams p, void *stream) {
+  if (p.count == 0)
+    return LLMI_HIP_OK;
+  if (int rc = check_view(p))
+    return rc;
+  if (!src || !out)
+    return fail(LLMI_HIP_INVALID_ARGUMENT, "copyHalfView: null buffer");
+  return launched(launch_copy_half_view(src, out, p, static_cast<hipStream_t>(stream)),
+                  "copyHalfView");
+}
+
+static int check_linear_f16(const LinearParams &p) {
+  if (p.epilogue > LLMI_LINEAR_DELTA_DECAY)
+    return fail(LLMI_HIP_INVALID_ARGUMENT, "linearF16: unknown epilogue %u", p.epilogue);
+  if (p.epilogue == LLMI_LINEAR_SIGMOID_COLUMNS && p.epilogueBlock == 0)
+    return fail(LLMI_HIP_INVALID_ARGUMENT, "linearF16: sigmoid columns need a block width");
+  if (p.inputWidth == 0)
+    return fail(LLMI_HIP_INVALID_ARGUMENT, "linearF16: zero input width");
+  if ((uint64_t)p.firstRow + p.rowCount > p.outputWidth)
+    return fail(LLMI_HIP_INVALID_ARGUMENT,
+                "linearF16: columns %u from %u past the output width %u", p.rowCount,
+                p.firstRow, p.outputWidth);
+  if (!fits32(p.tokens, p.inputWidth, 1) || !fits32(p.rowCount, p.inputWidth, 1) ||
+      !fits32(p.tokens, p.outputWidth, 1))
+    return fail(LLMI_HIP_INVALID_ARGUMENT, "linearF16: exceeds the 32-bit index range");
+  return LLMI_HIP_OK;
+}
+
+int llmi_hip_linear_f16(const uint16_t *input, const uint16_t *weight, void *output,
+                        const void *aux, const float *bias, LinearParams p, void *stream) {
+  if (p.tokens == 0 || p.rowCount == 0)
+    return LLMI_HIP_OK;
+  if (int rc = check_linear_f16(p))
+    return rc;
+  if (!input || !weight || !output)
+    return fail(LLMI_HIP_INVALID_ARGUMENT, "linearF16: null buffer");
+  if (p.epilogue == LLMI_LINEAR_SILU_MUL && !aux)
+    return fail(LLMI_HIP_INVALID_ARGUMENT, "linearF16: SiluMul needs its multiplier (aux)");
+  if (p.epilogue == LLMI_LINEAR_DELTA_DECAY && (!aux || !bias))
+    return fail(LLMI_HIP_INVALID_ARGUMENT, "linearF16: the decay needs A_log (aux) and bias");
+  return launched(launch_linear_f16(input, weight, output, aux, bias, p,
+                                    static_cast<hipStream_t>(stream)),
+                  "linearF16");
 }
 
 static int gated_norm(const uint16_t *input, const void *gate, bool activated,
@@ -720,6 +807,19 @@ unsigned llmi_hip_dispatch_count(int op, const void *params) {
     const EmbedParams &p = *static_cast<const EmbedParams *>(params);
     return p.tokens && p.hidden && p.rowCount ? 1 : 0;
   }
+  case LLMI_HIP_OP_RESIDUAL_ADD:
+  case LLMI_HIP_OP_SWIGLU:
+  case LLMI_HIP_OP_SILU:
+  case LLMI_HIP_OP_MULTIPLY:
+    return static_cast<const ElementParams *>(params)->count ? 1 : 0;
+  case LLMI_HIP_OP_COPY_HALF_VIEW: {
+    const HalfViewParams &p = *static_cast<const HalfViewParams *>(params);
+    return p.count && check_view(p) == LLMI_HIP_OK ? 1 : 0;
+  }
+  case LLMI_HIP_OP_LINEAR_F16: {
+    const LinearParams &p = *static_cast<const LinearParams *>(params);
+    return p.tokens && p.rowCount && check_linear_f16(p) == LLMI_HIP_OK ? 1 : 0;
+  }
   case LLMI_HIP_OP_DELTA_GATES: {
     const RowParams &p = *static_cast<const RowParams *>(params);
     return p.rows && p.width ? 1 : 0;
@@ -812,6 +912,18 @@ const char *llmi_hip_kernel_name(int op, const void *params, unsigned index) {
     return "embeddingW8";
   case LLMI_HIP_OP_EMBEDDING:
     return "embedding";
+  case LLMI_HIP_OP_RESIDUAL_ADD:
+    return "residualAdd";
+  case LLMI_HIP_OP_SWIGLU:
+    return "swiGlu";
+  case LLMI_HIP_OP_SILU:
+    return "siluF16";
+  case LLMI_HIP_OP_MULTIPLY:
+    return "multiplyF16";
+  case LLMI_HIP_OP_COPY_HALF_VIEW:
+    return "copyHalfView";
+  case LLMI_HIP_OP_LINEAR_F16:
+    return "linearF16";
   case LLMI_HIP_OP_GATED_RMS_NORM:
     return "gatedRmsNormTile";
   case LLMI_HIP_OP_SIGMOID_MUL:

@@ -325,8 +325,6 @@ __global__ __launch_bounds__(256) void delta_gates_kernel(
   decay[i] = exp_cr(mul32(-exp_cr(a_log[head]), sp));
 }
 
-bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
-
 } // namespace
 
 bool causal_conv_supported(unsigned k) { return k >= 1 && k <= kMaxKernel; }

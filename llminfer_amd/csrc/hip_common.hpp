@@ -16,6 +16,9 @@ typedef uint32_t uint4_t __attribute__((ext_vector_type(4)));
 
 constexpr float kLog2e = 1.4426950408889634f;
 
+// Host-side check for the 16-byte vector paths.
+inline bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
 // LDS barrier: this wave's LDS accesses complete, then the workgroup
 // barrier. Unlike __syncthreads it waits for no outstanding global load or
 // store, so loads issued before it stay in flight and stores keep draining

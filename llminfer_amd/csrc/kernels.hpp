@@ -6,6 +6,8 @@
 #include <stddef.h>
 #include <stdint.h>
 
+#include "llminfer_hip.h"
+
 namespace llmi {
 
 // ---------------------------------------------------------------- KvAppend
@@ -194,5 +196,15 @@ hipError_t launch_embedding_w8(const uint32_t *ids, const int8_t *w, const uint1
 hipError_t launch_embedding(const uint32_t *ids, const uint16_t *w, uint16_t *out,
                             unsigned tokens, unsigned hidden, unsigned first, unsigned count,
                             hipStream_t stream);
+
+// residualAdd / swiGlu / siluF16 / multiplyF16, copyHalfView, linearF16
+// (graph_ops.hip).
+enum class ElementwiseKind { Add, SwiGlu, Silu, Multiply };
+hipError_t launch_elementwise(ElementwiseKind kind, const uint16_t *a, const uint16_t *b,
+                              uint16_t *out, unsigned count, hipStream_t stream);
+hipError_t launch_copy_half_view(const uint16_t *src, uint16_t *out, const HalfViewParams &p,
+                                 hipStream_t stream);
+hipError_t launch_linear_f16(const uint16_t *in, const uint16_t *w, void *out, const void *aux,
+                             const float *bias, const LinearParams &p, hipStream_t stream);
 
 } // namespace llmi

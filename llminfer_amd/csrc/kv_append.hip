@@ -33,8 +33,6 @@ __global__ __launch_bounds__(256) void kv_append_scalar(
     vc[i] = vs[i];
 }
 
-bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
-
 hipError_t launch(const uint16_t *ksrc, const uint16_t *vsrc, uint16_t *kcache,
                   uint16_t *vcache, unsigned count, unsigned offset,
                   unsigned halves, hipStream_t stream) {

@@ -333,8 +333,6 @@ __global__ __launch_bounds__(256) void sigmoid_mul_scalar(const uint16_t *__rest
     out[i] = gate_one(gate[i], in[i]);
 }
 
-bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
-
 // Rows per tile and the table bound for a shape the tile kernel takes.
 struct TilePlan {
   unsigned rw, maxtok;

@@ -25,7 +25,7 @@
 #include "exact_fp.hpp"
 #include "hip_common.hpp"
 #include "kernels.hpp"
-#include "rope_gate.hpp"
+#include "linear_store.hpp"
 
 #include "llminfer_hip.h"
 
@@ -50,41 +50,6 @@ __device__ __forceinline__ int group_dot(uint4_t a0, uint4_t a1, uint4_t w0, uin
 // operation rounded on its own.
 __device__ __forceinline__ float add_term(float acc, int dot, float a, float w) {
   return __fadd_rn(acc, __fmul_rn(__fmul_rn((float)dot, a), w));
-}
-
-// storeLinear (Reference.metal:14-47): the projection rounded to fp16, then
-// the consumer's fused epilogue.
-__device__ __forceinline__ void store_linear(void *out, const void *aux, const float *bias,
-                                             size_t i, unsigned col, unsigned epilogue,
-                                             unsigned block, float acc) {
-  const float projected = round16(acc);
-  uint16_t *o16 = static_cast<uint16_t *>(out);
-  float *o32 = static_cast<float *>(out);
-  switch (epilogue) {
-  case LLMI_LINEAR_SILU:
-    o16[i] = silu16(projected);
-    return;
-  case LLMI_LINEAR_SILU_MUL:
-    o16[i] = f2h(mul32(h2f(silu16(projected)), h2f(static_cast<const uint16_t *>(aux)[i])));
-    return;
-  case LLMI_LINEAR_SIGMOID_COLUMNS:
-    o16[i] = f2h((col / block) % 2 ? logistic16(projected) : projected);
-    return;
-  case LLMI_LINEAR_SILU_F32:
-    o32[i] = mul32(projected, logistic_exact(projected));
-    return;
-  case LLMI_LINEAR_DELTA_BETA:
-    o32[i] = logistic16(projected);
-    return;
-  case LLMI_LINEAR_DELTA_DECAY: {
-    const float *a_log = static_cast<const float *>(aux);
-    o32[i] = exp_cr(mul32(-exp_cr(a_log[col]), stable_softplus(__fadd_rn(projected, bias[col]))));
-    return;
-  }
-  default:
-    o16[i] = f2h(projected);
-    return;
-  }
 }
 
 // --------------------------------------------------------------- quantize
@@ -540,8 +505,6 @@ __global__ __launch_bounds__(256) void embedding_kernel(const uint32_t *__restri
   else
     out[i0] = w[src];
 }
-
-bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 } // namespace
 

@@ -244,6 +244,80 @@ def embedding(*args, **kwargs) -> None:
     bind_embedding(*args, **kwargs)()
 
 
+# ------------------------------------ elementwise, views, fp16 projections
+
+_ELEMENTWISE = {"add": ("llmi_hip_residual_add", "residualAdd"),
+                "swiglu": ("llmi_hip_swiglu", "swiGlu"),
+                "multiply": ("llmi_hip_multiply", "multiplyF16")}
+
+
+def bind_elementwise(kind: str, a: torch.Tensor, b: torch.Tensor | None,
+                     out: torch.Tensor) -> "Bound":
+    """residualAdd (a + b), swiGlu (fp16(silu(a)) * b), multiplyF16 (a * b)
+    or siluF16 (silu(a), kind "silu", b unused): fp16 tensors of one size
+    (Reference.metal:119-135, Graph.metal:70-95)."""
+    operands = ((a, "a"), (out, "out")) if kind == "silu" else ((a, "a"), (b, "b"), (out, "out"))
+    for t, n in operands:
+        _require(t, torch.float16, n)
+    if out.numel() != a.numel() or (kind != "silu" and b.numel() != a.numel()):
+        raise ValueError("operands and out must have the same size")
+    p = _lib.ElementParams(a.numel())
+    if kind == "silu":
+        return Bound(_lib.load().llmi_hip_silu, (_ptr(a), _ptr(out), p, _stream()), "siluF16")
+    fn, name = _ELEMENTWISE[kind]
+    return Bound(getattr(_lib.load(), fn), (_ptr(a), _ptr(b), _ptr(out), p, _stream()), name)
+
+
+def elementwise(kind: str, a: torch.Tensor, b: torch.Tensor | None, out: torch.Tensor) -> None:
+    bind_elementwise(kind, a, b, out)()
+
+
+def bind_copy_half_view(src: torch.Tensor, out: torch.Tensor, dims, strides,
+                        offset: int = 0) -> "Bound":
+    """copyHalfView (Graph.metal:1-14): out (dense, fp16) = the view of src
+    with up to 3 dims (outermost first), strides and offset in elements."""
+    _require(src, torch.float16, "src")
+    _require(out, torch.float16, "out")
+    d = [1] * (3 - len(dims)) + [int(x) for x in dims]
+    st = [0] * (3 - len(strides)) + [int(x) for x in strides]
+    count = d[0] * d[1] * d[2]
+    if out.numel() != count:
+        raise ValueError("out must hold the view's elements")
+    if offset + sum((x - 1) * y for x, y in zip(d, st)) >= src.numel():
+        raise ValueError("the view reaches past src")
+    p = _lib.HalfViewParams(count, offset, (C.c_uint * 3)(*d), (C.c_uint * 3)(*st))
+    return Bound(_lib.load().llmi_hip_copy_half_view, (_ptr(src), _ptr(out), p, _stream()),
+                 "copyHalfView")
+
+
+def copy_half_view(*args, **kwargs) -> None:
+    bind_copy_half_view(*args, **kwargs)()
+
+
+def bind_linear_f16(x: torch.Tensor, weight: torch.Tensor, out: torch.Tensor,
+                    epilogue: int = _lib.LINEAR_NONE, block: int = 0,
+                    aux: torch.Tensor | None = None, bias: torch.Tensor | None = None,
+                    first_row: int = 0) -> "Bound":
+    """linearF16 (Reference.metal:61-103) with storeLinear: x [tokens, K]
+    fp16, weight [columns, K] fp16, out [tokens, width] (fp32 for the fp32
+    epilogues), columns first_row .. first_row + columns - 1 written."""
+    _require(x, torch.float16, "x")
+    _require(weight, torch.float16, "weight")
+    _require(out, torch.float32 if epilogue in _F32_EPILOGUES else torch.float16, "out")
+    if x.dim() != 2 or weight.dim() != 2 or weight.shape[1] != x.shape[1] or out.dim() != 2 \
+            or out.shape[0] != x.shape[0]:
+        raise ValueError("x [tokens, K], weight [columns, K] and out [tokens, width] disagree")
+    tokens, k = x.shape
+    p = _lib.LinearParams(tokens, k, out.shape[1], first_row, weight.shape[0], epilogue, block)
+    return Bound(_lib.load().llmi_hip_linear_f16,
+                 (_ptr(x), _ptr(weight), _ptr(out), _ptr(aux), _ptr(bias), p, _stream()),
+                 "linearF16")
+
+
+def linear_f16(*args, **kwargs) -> None:
+    bind_linear_f16(*args, **kwargs)()
+
+
 def bind_causal_conv(x: torch.Tensor, weight: torch.Tensor, history: torch.Tensor | None,
                      out: torch.Tensor, silu: bool = True) -> "Bound":
     """causalConv (Reference.metal:137-161): x, out [T, C] fp16; weight [C, k]

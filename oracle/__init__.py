@@ -82,6 +82,11 @@ def lib() -> C.CDLL:
                                       C.c_void_p, C.c_void_p] + [_u32] * 7
         L.orc_embedding_w8.argtypes = [C.c_void_p, C.c_void_p, _u16p, _u16p] + [_u32] * 5
         L.orc_embedding.argtypes = [C.c_void_p, _u16p, _u16p] + [_u32] * 4
+        L.orc_elementwise.argtypes = [_u32, _u16p, _u16p, _u16p, C.c_size_t]
+        L.orc_copy_half_view.argtypes = [_u16p, _u16p, _u32, _u32, C.POINTER(_u32),
+                                         C.POINTER(_u32)]
+        L.orc_linear_f16.argtypes = [_u16p, _u16p, C.c_void_p, C.c_void_p, C.c_void_p] + \
+            [_u32] * 7
         for name, n in (("orc_cost_kv_append", 3), ("orc_cost_causal_gqa", 5),
                         ("orc_cost_delta_update", 5)):
             fn = getattr(L, name)
@@ -354,6 +359,58 @@ def embedding(ids, weight, first_row: int = 0, output=None):
         output = np.zeros((i.size, w.shape[1]), np.uint16)
     lib().orc_embedding(i.ctypes.data, w.reshape(-1), output.reshape(-1), i.size, w.shape[1],
                         first_row, w.shape[0])
+    return output
+
+
+ELEMENTWISE = {"add": 0, "swiglu": 1, "silu": 2, "multiply": 3}
+
+
+def elementwise(kind: str, a, b=None) -> np.ndarray:
+    """residualAdd / swiGlu / siluF16 / multiplyF16 (Reference.metal:119-135,
+    Graph.metal:70-95) on fp16 bits."""
+    x = np.ascontiguousarray(a, np.uint16)
+    y = np.ascontiguousarray(b if b is not None else a, np.uint16)
+    assert x.shape == y.shape
+    out = np.empty(x.shape, np.uint16)
+    lib().orc_elementwise(ELEMENTWISE[kind], x.reshape(-1), y.reshape(-1), out.reshape(-1),
+                          x.size)
+    return out
+
+
+def copy_half_view(src, dims, strides, offset: int = 0) -> np.ndarray:
+    """copyHalfView (Graph.metal:1-14): a dense copy of the view of fp16 bits
+    with at most 3 dims (outermost first), strides and offset in elements."""
+    s = np.ascontiguousarray(src, np.uint16).reshape(-1)
+    d = [1] * (3 - len(dims)) + list(dims)
+    st = [0] * (3 - len(strides)) + list(strides)
+    count = int(np.prod(d))
+    out = np.empty(count, np.uint16)
+    D = (C.c_uint32 * 3)(*d)
+    S = (C.c_uint32 * 3)(*st)
+    lib().orc_copy_half_view(s, out, count, offset, D, S)
+    return out.reshape(dims)
+
+
+def linear_f16(x, weight, epilogue: int = LINEAR_NONE, block: int = 0, aux=None, bias=None,
+               output=None, first_row: int = 0, output_width: int | None = None) -> np.ndarray:
+    """linearF16 (Reference.metal:61-103): x fp16 bits [tokens, K], weight
+    fp16 bits [columns, K]; one fp32 fma chain per output over k in order,
+    then storeLinear."""
+    a = np.ascontiguousarray(x, np.uint16)
+    w = np.ascontiguousarray(weight, np.uint16)
+    tokens, k = a.shape
+    columns = w.shape[0]
+    assert w.shape[1] == k
+    width = output_width if output_width is not None else first_row + columns
+    if output is None:
+        dt = np.float32 if epilogue in F32_EPILOGUES else np.uint16
+        output = np.zeros((tokens, width), dt)
+    ax = np.ascontiguousarray(aux) if aux is not None else None
+    bs = np.ascontiguousarray(bias, np.float32) if bias is not None else None
+    lib().orc_linear_f16(a.reshape(-1), w.reshape(-1), output.ctypes.data,
+                         ax.ctypes.data if ax is not None else None,
+                         bs.ctypes.data if bs is not None else None, tokens, k, width,
+                         first_row, columns, epilogue, block)
     return output
 
 

@@ -927,6 +927,65 @@ void orc_embedding(const uint32_t *ids, const uint16_t *weight, uint16_t *output
   }
 }
 
+/* ----------------------------------------- elementwise, views, linearF16 */
+
+/* residualAdd, swiGlu, siluF16, multiplyF16 (Reference.metal:119-135,
+ * Graph.metal:70-95): kind 0..3 in that order; b is unused by siluF16. */
+void orc_elementwise(uint32_t kind, const uint16_t *a, const uint16_t *b, uint16_t *out,
+                     size_t count) {
+  for (size_t i = 0; i < count; ++i) {
+    float x = orc_f16_to_f32(a[i]);
+    float r;
+    switch (kind) {
+    case 0:
+      r = x + orc_f16_to_f32(b[i]);
+      break;
+    case 1:
+      r = orc_round_f16(silu(x)) * orc_f16_to_f32(b[i]);
+      break;
+    case 2:
+      r = silu(x);
+      break;
+    default:
+      r = x * orc_f16_to_f32(b[i]);
+      break;
+    }
+    out[i] = orc_f32_to_f16(r);
+  }
+}
+
+/* copyHalfView, Graph.metal:1-14: out[i] = src[offset + sum_d index_d(i) *
+ * strides[d]] over dims (outermost first). */
+void orc_copy_half_view(const uint16_t *src, uint16_t *out, uint32_t count, uint32_t offset,
+                        const uint32_t *dims, const uint32_t *strides) {
+  for (uint32_t i = 0; i < count; ++i) {
+    uint32_t rest = i, at = offset;
+    for (int d = 2; d >= 0; --d) {
+      at += (rest % dims[d]) * strides[d];
+      rest /= dims[d];
+    }
+    out[i] = src[at];
+  }
+}
+
+/* linearF16, Reference.metal:61-103: per output (row, col), acc = fma(x[k],
+ * w[k], acc) over k = 0 .. inputWidth-1 in fp32, then storeLinear. */
+void orc_linear_f16(const uint16_t *input, const uint16_t *weight, void *output,
+                    const void *aux, const float *bias, uint32_t tokens, uint32_t input_width,
+                    uint32_t output_width, uint32_t first_row, uint32_t columns,
+                    uint32_t epilogue, uint32_t epilogue_block) {
+  for (uint32_t row = 0; row < tokens; ++row)
+    for (uint32_t col = 0; col < columns; ++col) {
+      float acc = 0.0f;
+      for (uint32_t k = 0; k < input_width; ++k)
+        acc = fmaf(orc_f16_to_f32(input[(size_t)row * input_width + k]),
+                   orc_f16_to_f32(weight[(size_t)col * input_width + k]), acc);
+      uint32_t column = first_row + col;
+      store_linear(output, aux, bias, (size_t)row * output_width + column, column, epilogue,
+                   epilogue_block, acc);
+    }
+}
+
 /* ------------------------------------------------------------------ cost */
 
 static int mul_ok(uint64_t a, uint64_t b, uint64_t *r) {

@@ -197,6 +197,17 @@ void orc_embedding_w8(const uint32_t *ids, const int8_t *weight, const uint16_t 
 void orc_embedding(const uint32_t *ids, const uint16_t *weight, uint16_t *output,
                    uint32_t tokens, uint32_t hidden, uint32_t first_row, uint32_t row_count);
 
+/* residualAdd / swiGlu / siluF16 / multiplyF16 (kind 0..3), copyHalfView and
+ * linearF16 (Reference.metal:61-135, Graph.metal:1-14, 70-95). */
+void orc_elementwise(uint32_t kind, const uint16_t *a, const uint16_t *b, uint16_t *out,
+                     size_t count);
+void orc_copy_half_view(const uint16_t *src, uint16_t *out, uint32_t count, uint32_t offset,
+                        const uint32_t *dims, const uint32_t *strides);
+void orc_linear_f16(const uint16_t *input, const uint16_t *weight, void *output,
+                    const void *aux, const float *bias, uint32_t tokens, uint32_t input_width,
+                    uint32_t output_width, uint32_t first_row, uint32_t columns,
+                    uint32_t epilogue, uint32_t epilogue_block);
+
 /* Cost model of lib/GraphIR/Cost.cpp:180-201 (MACs) and :56-94 (bytes) for
  * the three hot ops. Returns 0 on success, -1 on overflow. */
 typedef struct {
