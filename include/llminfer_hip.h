@@ -596,6 +596,131 @@ LLMI_HIP_API int llmi_hip_session_step(llmi_hip_session *s, unsigned tokens,
                           uint16_t *gqa_out, llmi_hip_dispatch *records,
                           size_t cap, size_t *count);
 
+/* ------------------------------------------------------ whole-graph plan
+ * Replaces MetalExecutionPlan::lower (lib/Backend/Metal/
+ * MetalExecutionPlan.cpp:169-760) and the executor that encodes it
+ * (MetalExecutor.mm:120-200): one step's GraphIR graph lowered to HIP
+ * dispatches over the calls above. The graph is passed flat; its enums are
+ * GraphIR's in declaration order (include/llminfer/GraphIR/Graph.h:22-88),
+ * so a reference-side adapter copies ir::Graph field by field.
+ *
+ * Lowering keeps the reference's decisions that its tooling observes:
+ * projection epilogues fused into their sole consumer (Silu, SiluMul,
+ * GatedRmsNorm's gate, DeltaGates' a and b, and the interleaved query /
+ * gate halves of SigmoidMul; MetalExecutionPlan.cpp:313-403), one record per
+ * launched kernel with its op, epilogue and fused op, non-contiguous fp16
+ * views materialised by copyHalfView. Results live in one scratch arena:
+ * each value takes the first free range that fits from its defining op to
+ * its last use. Contiguous views are addressed in place. */
+
+enum llmi_graph_element { LLMI_GRAPH_I8 = 0, LLMI_GRAPH_U32, LLMI_GRAPH_F16, LLMI_GRAPH_F32 };
+enum llmi_graph_value_kind {
+  LLMI_GRAPH_INPUT = 0, LLMI_GRAPH_WEIGHT, LLMI_GRAPH_RESULT, LLMI_GRAPH_VIEW
+};
+enum llmi_graph_state_kind {
+  LLMI_GRAPH_CONV_HISTORY = 0, LLMI_GRAPH_DELTA_RECURRENT, LLMI_GRAPH_KEY_CACHE,
+  LLMI_GRAPH_VALUE_CACHE
+};
+enum llmi_graph_op_kind {
+  LLMI_GRAPH_EMBEDDING_GATHER = 0, LLMI_GRAPH_QUANTIZE_ACTIVATION, LLMI_GRAPH_LINEAR_F16,
+  LLMI_GRAPH_LINEAR_W8A8, LLMI_GRAPH_RMS_NORM, LLMI_GRAPH_GATED_RMS_NORM, LLMI_GRAPH_L2_NORM,
+  LLMI_GRAPH_ADD, LLMI_GRAPH_SILU, LLMI_GRAPH_SILU_MUL, LLMI_GRAPH_SIGMOID_MUL,
+  LLMI_GRAPH_RESHAPE, LLMI_GRAPH_SLICE, LLMI_GRAPH_PARTIAL_ROPE, LLMI_GRAPH_CAUSAL_CONV1D,
+  LLMI_GRAPH_DELTA_GATES, LLMI_GRAPH_DELTA_UPDATE, LLMI_GRAPH_KV_APPEND, LLMI_GRAPH_CAUSAL_GQA
+};
+
+#define LLMI_GRAPH_MAX_RANK 4
+
+/* ir::ValueDesc (Graph.h:35-46): strides and view_offset in elements;
+ * view_of and defining_op -1 when absent; weight: the index of a weight
+ * value's tensor in the table given to llmi_hip_plan_lower, -1 otherwise. */
+typedef struct llmi_graph_value {
+  uint32_t element, kind, rank, reserved;
+  uint64_t shape[LLMI_GRAPH_MAX_RANK], strides[LLMI_GRAPH_MAX_RANK];
+  int64_t view_of, defining_op, weight;
+  uint64_t view_offset, group_size;
+} llmi_graph_value;
+
+/* ir::StateDesc (Graph.h:48-52). */
+typedef struct llmi_graph_state {
+  uint32_t kind, layer, element, rank;
+  uint64_t shape[LLMI_GRAPH_MAX_RANK];
+} llmi_graph_state;
+
+/* ir::Operation (Graph.h:120-126) with its attributes flattened
+ * (Graph.h:90-118): group_size (QuantizeAttr), epsilon (NormAttr),
+ * group_width / epsilon / scale (L2NormAttr), axis / begin / length
+ * (SliceAttr), rotary_width / theta (RopeAttr), state (StateAttr), keys /
+ * values (KvAttr). layer -1: none. */
+typedef struct llmi_graph_op {
+  uint32_t kind;
+  int32_t layer;
+  uint32_t input_count, output_count;
+  uint32_t inputs[5], outputs[2];
+  uint32_t state, keys, values;
+  uint64_t group_size, group_width, axis, begin, length, rotary_width;
+  float epsilon, scale, theta, reserved;
+} llmi_graph_op;
+
+/* One step's graph (ir::Graph, Graph.h:133-170). */
+typedef struct llmi_graph {
+  uint64_t tokens, past, capacity;
+  const llmi_graph_value *values;
+  size_t value_count;
+  const llmi_graph_state *states;
+  size_t state_count;
+  const llmi_graph_op *ops;
+  size_t op_count;
+  const uint32_t *outputs;
+  size_t output_count;
+} llmi_graph;
+
+/* A model tensor in device memory (ModelFile's TensorView): data, and for
+ * int8 tensors the fp16 group scales [rows][groups]. Rows of int8 tensors
+ * are padded to whole 32-wide groups. */
+typedef struct llmi_weight {
+  const void *data;
+  const uint16_t *scales;
+} llmi_weight;
+
+typedef struct llmi_hip_plan llmi_hip_plan;
+
+/* Lowers `graph` (host memory, read during the call only) over `weights`
+ * (device pointers, which must stay valid while the plan is used). Host
+ * only: launches nothing and needs no device. Fails with
+ * LLMI_HIP_INVALID_ARGUMENT for a malformed graph or a graph the plan
+ * cannot lower (a message in llmi_hip_last_error), LLMI_HIP_UNSUPPORTED for
+ * an op shape no kernel here serves. */
+LLMI_HIP_API int llmi_hip_plan_lower(const llmi_graph *graph, const llmi_weight *weights,
+                                     size_t weight_count, llmi_hip_plan **out);
+LLMI_HIP_API void llmi_hip_plan_destroy(llmi_hip_plan *plan);
+
+/* Bytes of the scratch arena llmi_hip_plan_execute needs (256-aligned). */
+LLMI_HIP_API size_t llmi_hip_plan_scratch_bytes(const llmi_hip_plan *plan);
+
+/* The logits output: rows and elements (0 when the graph has no output). */
+LLMI_HIP_API void llmi_hip_plan_logits(const llmi_hip_plan *plan, uint64_t *rows,
+                                       uint64_t *elements);
+
+/* The plan's records, one per launched kernel in launch order
+ * (MetalDispatchInfo, MetalSession.h:11-16): up to `cap` are written to
+ * `records` (may be NULL); returns the total. Kernel and epilogue names are
+ * static strings; epilogue is NULL for an unfused launch, and
+ * fused_op_index is then 0. */
+LLMI_HIP_API size_t llmi_hip_plan_dispatches(const llmi_hip_plan *plan,
+                                             llmi_hip_dispatch *records, size_t cap);
+
+/* Runs the plan on `stream`: scratch (device, llmi_hip_plan_scratch_bytes),
+ * states[i] the device buffer of graph state i (its shape, dense),
+ * token_ids (device, tokens uint32), logits (device fp16 [rows][vocab], or
+ * NULL when the graph has no output), invalid (device uint32 that each
+ * quantizeActivation ORs 1 into on a non-finite group; NULL: ignored). The
+ * launches are only enqueued: the caller synchronises. */
+LLMI_HIP_API int llmi_hip_plan_execute(const llmi_hip_plan *plan, void *scratch,
+                                       size_t scratch_bytes, void *const *states,
+                                       size_t state_count, const uint32_t *token_ids,
+                                       uint16_t *logits, uint32_t *invalid, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

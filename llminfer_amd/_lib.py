@@ -200,6 +200,13 @@ SIGNATURES = {
     "llmi_hip_session_step": (C.c_int, [_P, C.c_uint, _P, _P, _P, _P, _P, _P,
                                         _P, _P, _P, _P, C.POINTER(Dispatch), _SZ,
                                         C.POINTER(_SZ)]),
+    # whole-graph plan (structs in llminfer_amd/plan.py)
+    "llmi_hip_plan_lower": (C.c_int, [_P, _P, _SZ, _P]),
+    "llmi_hip_plan_destroy": (None, [_P]),
+    "llmi_hip_plan_scratch_bytes": (_SZ, [_P]),
+    "llmi_hip_plan_logits": (None, [_P, _P, _P]),
+    "llmi_hip_plan_dispatches": (_SZ, [_P, C.POINTER(Dispatch), _SZ]),
+    "llmi_hip_plan_execute": (C.c_int, [_P, _P, _SZ, _P, _SZ, _P, _P, _P, _P]),
 }
 
 _lib = None

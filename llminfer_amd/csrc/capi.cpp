@@ -426,10 +426,6 @@ static int gated_norm(const uint16_t *input, const void *gate, bool activated,
     return fail(LLMI_HIP_INVALID_ARGUMENT, "gatedRmsNorm: null buffer");
   if (!fits32(p.rows, p.width, 1))
     return fail(LLMI_HIP_INVALID_ARGUMENT, "gatedRmsNorm: exceeds the 32-bit index range");
-  if (!gated_rms_norm_supported(p.width, input, gate, output))
-    return fail(LLMI_HIP_UNSUPPORTED,
-                "gatedRmsNorm: width %u (multiples of 8 up to 256, 16-byte aligned buffers)",
-                p.width);
   return launched(launch_gated_rms_norm(input, gate, activated, weight, output, p.rows,
                                         p.width, p.epsilon, static_cast<hipStream_t>(stream)),
                   "gatedRmsNorm");
@@ -826,9 +822,7 @@ unsigned llmi_hip_dispatch_count(int op, const void *params) {
   }
   case LLMI_HIP_OP_GATED_RMS_NORM: {
     const RowParams &p = *static_cast<const RowParams *>(params);
-    return p.rows && p.width && gated_rms_norm_supported(p.width, nullptr, nullptr, nullptr)
-               ? 1
-               : 0;
+    return p.rows && p.width ? 1 : 0;
   }
   case LLMI_HIP_OP_GATED_ATTENTION: {
     // Launches for a rotary width the kernels take (a multiple of 16).
@@ -924,8 +918,10 @@ const char *llmi_hip_kernel_name(int op, const void *params, unsigned index) {
     return "copyHalfView";
   case LLMI_HIP_OP_LINEAR_F16:
     return "linearF16";
-  case LLMI_HIP_OP_GATED_RMS_NORM:
-    return "gatedRmsNormTile";
+  case LLMI_HIP_OP_GATED_RMS_NORM: {
+    const unsigned width = static_cast<const RowParams *>(params)->width;
+    return width % 8 == 0 && width <= 256 ? "gatedRmsNormTile" : "gatedRmsNormRows";
+  }
   case LLMI_HIP_OP_SIGMOID_MUL:
     return sigmoid_mul_vectorised(static_cast<const ElementParams *>(params)->count,
                                   nullptr, nullptr, nullptr)

@@ -214,6 +214,35 @@ __global__ __launch_bounds__(256) void l2_norm_rows(const uint16_t *__restrict__
     out[(size_t)r * width + i] = mul32(h2f(x[i]), f);
 }
 
+// gatedRmsNorm for any width: one thread per row, the tile kernel's
+// arithmetic (fma sum of squares in order, the same factor and products,
+// the exact SiLU) on one element at a time.
+template <bool kActivated>
+__global__ __launch_bounds__(256) void gated_rms_norm_rows(const uint16_t *__restrict__ in,
+                                                           const void *__restrict__ gate,
+                                                           const float *__restrict__ w,
+                                                           uint16_t *__restrict__ out,
+                                                           unsigned rows, unsigned width,
+                                                           float eps) {
+  const unsigned r = blockIdx.x * 256 + threadIdx.x;
+  if (r >= rows)
+    return;
+  const size_t base = (size_t)r * width;
+  float sum = 0.0f;
+  for (unsigned i = 0; i < width; ++i) {
+    const float f = h2f(in[base + i]);
+    sum = __builtin_fmaf(f, f, sum);
+  }
+  const float f = gated_norm_factor(sum, width, eps);
+  for (unsigned i = 0; i < width; ++i) {
+    const float norm = gated_norm_scaled(h2f(in[base + i]), f, w[i]);
+    const float y =
+        kActivated ? mul32(norm, static_cast<const float *>(gate)[base + i])
+                   : gated_norm_silu_exact(norm, h2f(static_cast<const uint16_t *>(gate)[base + i]));
+    out[base + i] = f2h(y);
+  }
+}
+
 // gatedRmsNorm (Reference.metal:228-259): kL2Rows rows of `width` (a
 // multiple of 8, <= 256) per wave, staged in LDS like l2_norm_tile; out =
 // fp16(fp16(x * scale) * w * g) with g = silu(gate) for an fp16 gate (an
@@ -360,8 +389,7 @@ hipError_t launch_l2_norm(const uint16_t *in, float *out, unsigned rows, unsigne
   return hipGetLastError();
 }
 
-bool gated_rms_norm_supported(unsigned width, const void *in, const void *gate,
-                              const void *out) {
+bool gated_rms_norm_tiled(unsigned width, const void *in, const void *gate, const void *out) {
   return width % 8 == 0 && width <= 256 && aligned16(in) && aligned16(gate) && aligned16(out);
 }
 
@@ -370,6 +398,16 @@ hipError_t launch_gated_rms_norm(const uint16_t *in, const void *gate, bool acti
                                  float eps, hipStream_t stream) {
   if (rows == 0 || width == 0)
     return hipSuccess;
+  if (!gated_rms_norm_tiled(width, in, gate, out)) {
+    const dim3 g((rows + 255) / 256);
+    if (activated)
+      hipLaunchKernelGGL(gated_rms_norm_rows<true>, g, dim3(256), 0, stream, in, gate, w, out,
+                         rows, width, eps);
+    else
+      hipLaunchKernelGGL(gated_rms_norm_rows<false>, g, dim3(256), 0, stream, in, gate, w, out,
+                         rows, width, eps);
+    return hipGetLastError();
+  }
   dim3 grid((rows + kL2Rows - 1) / kL2Rows);
   if (activated)
     hipLaunchKernelGGL(gated_rms_norm_tile<true>, grid, dim3(64), 0, stream, in, gate, w, out,

@@ -170,8 +170,9 @@ hipError_t launch_causal_conv(const uint16_t *in, const uint16_t *w, uint16_t *h
 bool l2_norm_tiled(unsigned width, const void *in, const void *out);
 hipError_t launch_l2_norm(const uint16_t *in, float *out, unsigned rows, unsigned width,
                           float eps, float scale, hipStream_t stream);
-bool gated_rms_norm_supported(unsigned width, const void *in, const void *gate,
-                              const void *out);
+// The LDS-tiled kernel (width a multiple of 8 up to 256, 16-byte aligned
+// buffers); other shapes take a thread per row.
+bool gated_rms_norm_tiled(unsigned width, const void *in, const void *gate, const void *out);
 hipError_t launch_gated_rms_norm(const uint16_t *in, const void *gate, bool activated,
                                  const float *w, uint16_t *out, unsigned rows, unsigned width,
                                  float eps, hipStream_t stream);

@@ -1,0 +1,941 @@
+// The whole-graph plan: one step's GraphIR graph lowered to HIP dispatches
+// over the per-op C ABI (capi.cpp), then run on a stream.
+//
+// Replaces MetalExecutionPlan (lib/Backend/Metal/MetalExecutionPlan.cpp:
+// 169-760). What the reference's tooling observes is kept: which projection
+// epilogue fuses into which consumer (prepareFusions, :313-403), the order
+// of the launches, and one record per launch with op index, kernel,
+// epilogue and fused op. The storage is MI355X-side: every result lives in
+// one device arena (the reference binds a Metal buffer per scratch slot),
+// placed first-fit between its defining op and its last use, offsets fixed
+// at lowering so a run is pointer arithmetic and launches; contiguous views
+// are addressed in place (the reference copies any view with an offset),
+// non-contiguous fp16 views go through copyHalfView.
+#include "capi_internal.hpp"
+#include "kernels.hpp"
+#include "llminfer_hip.h"
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstring>
+#include <string>
+#include <vector>
+
+namespace llmi {
+namespace {
+
+constexpr uint64_t kAlign = 256;
+
+enum class Space : uint8_t { None, Scratch, Weight, Scale, State, Input, Output, Invalid };
+
+// A device address resolved at run time: the base of `space` (entry `index`
+// of the weight or state table) plus `offset` bytes.
+struct Ref {
+  Space space = Space::None;
+  uint32_t index = 0;
+  uint64_t offset = 0;
+};
+
+enum class Launch : uint8_t {
+  Embedding, EmbeddingW8, Quantize, LinearW8, LinearF16, RmsNorm, GatedRmsNorm,
+  GatedRmsNormActivated, L2Norm, Elementwise, SigmoidMul, PartialRope, CausalConv, DeltaGates,
+  DeltaUpdate, KvAppend, CausalGqa, CopyView
+};
+
+struct Dispatch {
+  Launch launch;
+  ElementwiseKind elementwise = ElementwiseKind::Add;
+  Ref buf[8];
+  uint64_t workspaceBytes = 0;
+  union {
+    EmbedParams embed;
+    GroupedEmbedParams embedW8;
+    QuantizeParams quantize;
+    LinearW8Params linearW8;
+    LinearParams linear;
+    RowParams row;
+    L2Params l2;
+    ElementParams element;
+    PartialRopeParams rope;
+    ConvParams conv;
+    GraphDeltaParams delta;
+    CacheParams cache;
+    GqaParams gqa;
+    HalfViewParams view;
+  } p;
+  size_t opIndex = 0, fusedOpIndex = 0;
+  const char *epilogue = nullptr;
+  std::vector<const char *> kernels;
+};
+
+struct Fusion {
+  unsigned kind = LLMI_LINEAR_NONE;
+  size_t consumer = 0;
+  unsigned block = 0;
+  // Run at the consumer: the epilogue needs the consumer's other operands,
+  // or the consumer's output is the projection's (MetalExecutionPlan.cpp:
+  // 60-68).
+  bool deferred() const {
+    return kind == LLMI_LINEAR_SILU || kind == LLMI_LINEAR_SILU_MUL ||
+           kind == LLMI_LINEAR_DELTA_BETA || kind == LLMI_LINEAR_DELTA_DECAY;
+  }
+};
+
+const char *epilogue_name(unsigned kind) {
+  switch (kind) {
+  case LLMI_LINEAR_SILU:
+  case LLMI_LINEAR_SILU_F32:
+    return "silu";
+  case LLMI_LINEAR_SILU_MUL:
+    return "swiglu";
+  case LLMI_LINEAR_SIGMOID_COLUMNS:
+  case LLMI_LINEAR_DELTA_BETA:
+    return "sigmoid";
+  case LLMI_LINEAR_DELTA_DECAY:
+    return "softplus_decay";
+  default:
+    return nullptr;
+  }
+}
+
+uint64_t element_bytes(uint32_t e) {
+  return e == LLMI_GRAPH_I8 ? 1 : e == LLMI_GRAPH_F16 ? 2 : 4;
+}
+
+} // namespace
+} // namespace llmi
+
+struct llmi_hip_plan {
+  std::vector<llmi::Dispatch> dispatches;
+  std::vector<llmi_hip_dispatch> records;
+  std::vector<llmi_weight> weights;
+  uint64_t scratchBytes = 0;
+  uint64_t logitRows = 0, logitElements = 0;
+  uint64_t invalidOffset = 0;
+  size_t stateCount = 0;
+  bool hasOutput = false;
+};
+
+namespace llmi {
+namespace {
+
+// First-fit ranges of one arena; a range is free again once the op index
+// passes its last use.
+class Arena {
+public:
+  uint64_t allocate(uint64_t bytes, size_t lastUse) {
+    bytes = (std::max<uint64_t>(bytes, 1) + kAlign - 1) / kAlign * kAlign;
+    for (size_t i = 0; i < free_.size(); ++i) {
+      auto &f = free_[i];
+      if (f.second - f.first >= bytes) {
+        uint64_t at = f.first;
+        f.first += bytes;
+        if (f.first == f.second)
+          free_.erase(free_.begin() + i);
+        live_.push_back({at, bytes, lastUse});
+        return at;
+      }
+    }
+    uint64_t at = end_;
+    if (!free_.empty() && free_.back().second == end_) { // grow the trailing gap
+      at = free_.back().first;
+      free_.pop_back();
+    }
+    end_ = at + bytes;
+    live_.push_back({at, bytes, lastUse});
+    return at;
+  }
+
+  // Releases every range whose last use is before op `index`.
+  void release_before(size_t index) {
+    for (size_t i = 0; i < live_.size();) {
+      if (live_[i].lastUse < index) {
+        insert_free(live_[i].at, live_[i].at + live_[i].bytes);
+        live_[i] = live_.back();
+        live_.pop_back();
+      } else {
+        ++i;
+      }
+    }
+  }
+
+  uint64_t size() const { return end_; }
+
+private:
+  struct Live {
+    uint64_t at, bytes;
+    size_t lastUse;
+  };
+  void insert_free(uint64_t b, uint64_t e) {
+    auto it = std::lower_bound(free_.begin(), free_.end(), std::make_pair(b, e));
+    it = free_.insert(it, {b, e});
+    size_t i = it - free_.begin();
+    if (i + 1 < free_.size() && free_[i].second == free_[i + 1].first) {
+      free_[i].second = free_[i + 1].second;
+      free_.erase(free_.begin() + i + 1);
+    }
+    if (i > 0 && free_[i - 1].second == free_[i].first) {
+      free_[i - 1].second = free_[i].second;
+      free_.erase(free_.begin() + i);
+    }
+  }
+  std::vector<std::pair<uint64_t, uint64_t>> free_;
+  std::vector<Live> live_;
+  uint64_t end_ = 0;
+};
+
+class Lowering {
+public:
+  Lowering(const llmi_graph &g, size_t weightCount, llmi_hip_plan &plan)
+      : g_(g), weightCount_(weightCount), plan_(plan) {}
+
+  int run();
+
+private:
+  const llmi_graph_value &value(uint32_t id) const { return g_.values[id]; }
+  uint64_t count(uint32_t id) const {
+    uint64_t n = 1;
+    for (uint32_t i = 0; i < value(id).rank; ++i)
+      n *= value(id).shape[i];
+    return n;
+  }
+  uint64_t dim(uint32_t id, int axis) const {
+    const auto &v = value(id);
+    return v.shape[axis < 0 ? v.rank + axis : axis];
+  }
+  bool contiguous(uint32_t id) const {
+    const auto &v = value(id);
+    uint64_t stride = 1;
+    for (uint32_t i = v.rank; i-- > 0;) {
+      if (v.shape[i] > 1 && v.strides[i] != stride)
+        return false;
+      stride *= v.shape[i];
+    }
+    return true;
+  }
+  const llmi_graph_op &op(size_t i) const { return g_.ops[i]; }
+
+  int validate();
+  void prepare_values();
+  void prepare_fusions();
+  int lower(size_t index);
+  int dense(uint32_t id, Ref &out);
+  int linear(size_t producer, uint32_t result, int64_t aux, int64_t bias);
+  Ref temporary(uint64_t bytes) { return {Space::Scratch, 0, arena_.allocate(bytes, index_)}; }
+  Dispatch &emit(Launch launch, const char *kernel) {
+    plan_.dispatches.push_back({});
+    Dispatch &d = plan_.dispatches.back();
+    d.launch = launch;
+    d.opIndex = index_;
+    if (kernel)
+      d.kernels.push_back(kernel);
+    return d;
+  }
+
+  const llmi_graph &g_;
+  size_t weightCount_;
+  llmi_hip_plan &plan_;
+  Arena arena_;
+  size_t index_ = 0;
+  std::vector<size_t> root_, lastUse_;
+  std::vector<uint64_t> offset_; // element offset of a view in its root
+  std::vector<Ref> buffer_;      // of roots
+  std::vector<Fusion> fusion_;
+};
+
+int Lowering::validate() {
+  if (!g_.values || !g_.ops || (g_.state_count && !g_.states) ||
+      (g_.output_count && !g_.outputs))
+    return fail(LLMI_HIP_INVALID_ARGUMENT, "plan: null graph array");
+  if (!g_.tokens || g_.past > g_.capacity || g_.tokens > g_.capacity - g_.past ||
+      g_.capacity > UINT32_MAX)
+    return fail(LLMI_HIP_INVALID_ARGUMENT, "plan: invalid step (tokens %llu, past %llu, "
+                "capacity %llu)", (unsigned long long)g_.tokens,
+                (unsigned long long)g_.past, (unsigned long long)g_.capacity);
+  for (size_t i = 0; i < g_.value_count; ++i) {
+    const auto &v = g_.values[i];
+    if (v.rank == 0 || v.rank > LLMI_GRAPH_MAX_RANK || v.element > LLMI_GRAPH_F32 ||
+        v.kind > LLMI_GRAPH_VIEW)
+      return fail(LLMI_HIP_INVALID_ARGUMENT, "plan: value %zu is malformed", i);
+    if (v.kind == LLMI_GRAPH_VIEW &&
+        (v.view_of < 0 || (uint64_t)v.view_of >= i))
+      return fail(LLMI_HIP_INVALID_ARGUMENT, "plan: view %zu has no preceding base", i);
+    if (v.kind == LLMI_GRAPH_WEIGHT && (v.weight < 0 || (uint64_t)v.weight >= weightCount_))
+      return fail(LLMI_HIP_INVALID_ARGUMENT, "plan: weight value %zu has no tensor", i);
+    if (v.kind == LLMI_GRAPH_RESULT &&
+        (v.defining_op < 0 || (uint64_t)v.defining_op >= g_.op_count))
+      return fail(LLMI_HIP_INVALID_ARGUMENT, "plan: result %zu has no defining op", i);
+    uint64_t span = 1;
+    for (uint32_t d = 0; d < v.rank; ++d) {
+      if (v.shape[d] == 0 || v.shape[d] > UINT32_MAX)
+        return fail(LLMI_HIP_INVALID_ARGUMENT, "plan: value %zu has an extent out of range", i);
+      span += (v.shape[d] - 1) * v.strides[d];
+    }
+    if (span + v.view_offset > UINT32_MAX)
+      return fail(LLMI_HIP_INVALID_ARGUMENT,
+                  "plan: value %zu exceeds the 32-bit index range", i);
+  }
+  for (size_t i = 0; i < g_.op_count; ++i) {
+    const auto &o = g_.ops[i];
+    if (o.kind > LLMI_GRAPH_CAUSAL_GQA || o.input_count > 5 || o.output_count > 2)
+      return fail(LLMI_HIP_INVALID_ARGUMENT, "plan: op %zu is malformed", i);
+    for (uint32_t j = 0; j < o.input_count; ++j)
+      if (o.inputs[j] >= g_.value_count)
+        return fail(LLMI_HIP_INVALID_ARGUMENT, "plan: op %zu reads a missing value", i);
+    for (uint32_t j = 0; j < o.output_count; ++j)
+      if (o.outputs[j] >= g_.value_count || g_.values[o.outputs[j]].defining_op != (int64_t)i)
+        return fail(LLMI_HIP_INVALID_ARGUMENT, "plan: op %zu has a foreign output", i);
+    const bool stateful = o.kind == LLMI_GRAPH_CAUSAL_CONV1D ||
+                          o.kind == LLMI_GRAPH_DELTA_UPDATE;
+    const bool cache = o.kind == LLMI_GRAPH_KV_APPEND || o.kind == LLMI_GRAPH_CAUSAL_GQA;
+    if ((stateful && o.state >= g_.state_count) ||
+        (cache && (o.keys >= g_.state_count || o.values >= g_.state_count)))
+      return fail(LLMI_HIP_INVALID_ARGUMENT, "plan: op %zu names a missing state", i);
+  }
+  for (size_t i = 0; i < g_.output_count; ++i)
+    if (g_.outputs[i] >= g_.value_count)
+      return fail(LLMI_HIP_INVALID_ARGUMENT, "plan: output %zu is missing", i);
+  return LLMI_HIP_OK;
+}
+
+// Roots, view offsets and last uses (MetalExecutionPlan.cpp:255-311).
+void Lowering::prepare_values() {
+  const size_t n = g_.value_count;
+  root_.resize(n);
+  offset_.assign(n, 0);
+  lastUse_.assign(n, 0);
+  buffer_.assign(n, {});
+  for (size_t i = 0; i < n; ++i) {
+    const auto &v = g_.values[i];
+    root_[i] = i;
+    if (v.kind == LLMI_GRAPH_VIEW) {
+      root_[i] = root_[v.view_of];
+      offset_[i] = offset_[v.view_of] + v.view_offset;
+    } else if (v.kind == LLMI_GRAPH_WEIGHT) {
+      buffer_[i] = {Space::Weight, (uint32_t)v.weight, 0};
+    } else if (v.kind == LLMI_GRAPH_INPUT) {
+      buffer_[i] = {Space::Input, 0, 0};
+    }
+  }
+  for (size_t i = 0; i < g_.op_count; ++i)
+    for (uint32_t j = 0; j < op(i).input_count; ++j)
+      lastUse_[root_[op(i).inputs[j]]] = i;
+  for (size_t i = 0; i < g_.output_count; ++i)
+    lastUse_[root_[g_.outputs[i]]] = g_.op_count;
+}
+
+// Projection epilogues fused into their consumer (MetalExecutionPlan.cpp:
+// 313-403): a projection whose result has exactly one use by Silu / SiluMul
+// (the SiLU and SwiGLU epilogues), by GatedRmsNorm as its gate (the fp32
+// SiLU epilogue), the a and b projections of DeltaGates (the decay and beta
+// epilogues), and the query / gate projection of SigmoidMul when the gate is
+// the second half of every interleaved head (the sigmoid-columns epilogue).
+void Lowering::prepare_fusions() {
+  const size_t n = g_.value_count;
+  std::vector<unsigned> uses(n, 0);
+  std::vector<uint32_t> firstUse(n, 0), secondUse(n, 0);
+  auto record = [&](uint32_t id) {
+    size_t r = root_[id];
+    if (uses[r] == 0)
+      firstUse[r] = id;
+    else if (uses[r] == 1)
+      secondUse[r] = id;
+    ++uses[r];
+  };
+  for (size_t i = 0; i < g_.op_count; ++i)
+    if (op(i).kind != LLMI_GRAPH_SLICE && op(i).kind != LLMI_GRAPH_RESHAPE)
+      for (uint32_t j = 0; j < op(i).input_count; ++j)
+        record(op(i).inputs[j]);
+  for (size_t i = 0; i < g_.output_count; ++i)
+    record(g_.outputs[i]);
+
+  auto projection = [&](uint32_t id) -> int64_t {
+    int64_t p = value(id).defining_op;
+    if (p >= 0 && (op(p).kind == LLMI_GRAPH_LINEAR_F16 || op(p).kind == LLMI_GRAPH_LINEAR_W8A8))
+      return p;
+    return -1;
+  };
+  auto sole = [&](uint32_t id) -> int64_t { return uses[id] == 1 ? projection(id) : -1; };
+  fusion_.assign(g_.op_count, {});
+  auto fuse = [&](size_t producer, size_t consumer, unsigned kind, unsigned block) {
+    fusion_[producer] = {kind, consumer, block};
+    if (fusion_[producer].deferred())
+      for (uint32_t j = 0; j < op(producer).input_count; ++j) {
+        size_t r = root_[op(producer).inputs[j]];
+        lastUse_[r] = std::max(lastUse_[r], consumer);
+      }
+  };
+  for (size_t i = 0; i < g_.op_count; ++i) {
+    const auto &o = op(i);
+    switch (o.kind) {
+    case LLMI_GRAPH_SILU:
+    case LLMI_GRAPH_SILU_MUL: {
+      int64_t p = sole(o.inputs[0]);
+      if (p >= 0)
+        fuse(p, i, o.kind == LLMI_GRAPH_SILU ? LLMI_LINEAR_SILU : LLMI_LINEAR_SILU_MUL, 0);
+      break;
+    }
+    case LLMI_GRAPH_GATED_RMS_NORM: {
+      int64_t p = sole(o.inputs[1]);
+      if (p >= 0)
+        fuse(p, i, LLMI_LINEAR_SILU_F32, 0);
+      break;
+    }
+    case LLMI_GRAPH_DELTA_GATES: {
+      int64_t a = sole(o.inputs[0]), b = sole(o.inputs[1]);
+      if (a >= 0 && b >= 0) {
+        fuse(a, i, LLMI_LINEAR_DELTA_DECAY, 0);
+        fuse(b, i, LLMI_LINEAR_DELTA_BETA, 0);
+      }
+      break;
+    }
+    case LLMI_GRAPH_SIGMOID_MUL: {
+      const uint32_t gate = o.inputs[0];
+      const size_t root = root_[gate];
+      const int64_t p = projection((uint32_t)root);
+      const auto &gv = value(gate);
+      if (p < 0 || uses[root] != 2 || gv.kind != LLMI_GRAPH_VIEW || gv.defining_op < 0)
+        break;
+      const uint32_t other = firstUse[root] == gate ? secondUse[root] : firstUse[root];
+      const auto &ov = value(other);
+      if (other == gate || ov.kind != LLMI_GRAPH_VIEW || ov.view_of != gv.view_of ||
+          ov.defining_op < 0)
+        break;
+      // The packed [tokens, heads, 2 * width] reshape of the projection.
+      const uint32_t packed = (uint32_t)gv.view_of;
+      const auto &pv = value(packed);
+      if (pv.kind != LLMI_GRAPH_VIEW || (size_t)pv.view_of != root || pv.rank != 3 ||
+          !contiguous(packed))
+        break;
+      const auto &gs = op(gv.defining_op), &qs = op(ov.defining_op);
+      const uint64_t width = pv.shape[2];
+      if (gs.kind == LLMI_GRAPH_SLICE && qs.kind == LLMI_GRAPH_SLICE && gs.axis == 2 &&
+          qs.axis == 2 && gs.begin == gs.length && qs.begin == 0 && qs.length == gs.length &&
+          width == 2 * gs.length)
+        fuse(p, i, LLMI_LINEAR_SIGMOID_COLUMNS, (unsigned)gs.length);
+      break;
+    }
+    default:
+      break;
+    }
+  }
+}
+
+// The address of a value's elements, materialising a non-contiguous fp16
+// view of at most 3 dimensions (MetalExecutionPlan.cpp:405-425).
+int Lowering::dense(uint32_t id, Ref &out) {
+  const auto &v = value(id);
+  Ref base = buffer_[root_[id]];
+  if (base.space == Space::None)
+    return fail(LLMI_HIP_INVALID_ARGUMENT, "plan: value %u is read before it is written", id);
+  if (v.kind != LLMI_GRAPH_VIEW || contiguous(id)) {
+    base.offset += offset_[id] * element_bytes(v.element);
+    out = base;
+    return LLMI_HIP_OK;
+  }
+  if (v.element != LLMI_GRAPH_F16 || v.rank > 3)
+    return fail(LLMI_HIP_INVALID_ARGUMENT, "plan: cannot materialise the view %u", id);
+  Dispatch &d = emit(Launch::CopyView, "copyHalfView");
+  HalfViewParams &p = d.p.view;
+  p.count = (unsigned)count(id);
+  p.offset = (unsigned)offset_[id];
+  for (int k = 0; k < 3; ++k) {
+    p.dims[k] = 1;
+    p.strides[k] = 0;
+  }
+  for (uint32_t k = 0; k < v.rank; ++k) {
+    p.dims[3 - v.rank + k] = (unsigned)v.shape[k];
+    p.strides[3 - v.rank + k] = (unsigned)v.strides[k];
+  }
+  d.buf[0] = base;
+  out = d.buf[1] = temporary(count(id) * 2);
+  return LLMI_HIP_OK;
+}
+
+int Lowering::linear(size_t producer, uint32_t result, int64_t aux, int64_t bias) {
+  const auto &o = op(producer);
+  const Fusion &f = fusion_[producer];
+  const bool w8 = o.kind == LLMI_GRAPH_LINEAR_W8A8;
+  const uint32_t wid = o.inputs[w8 ? 2 : 1];
+  Ref in, scales, weight, outRef, auxRef, biasRef;
+  if (int rc = dense(o.inputs[0], in))
+    return rc;
+  if (w8)
+    if (int rc = dense(o.inputs[1], scales))
+      return rc;
+  if (int rc = dense(wid, weight))
+    return rc;
+  if (int rc = dense(result, outRef))
+    return rc;
+  if (aux >= 0)
+    if (int rc = dense((uint32_t)aux, auxRef))
+      return rc;
+  if (bias >= 0)
+    if (int rc = dense((uint32_t)bias, biasRef))
+      return rc;
+  const unsigned rows = (unsigned)dim(result, 0), width = (unsigned)dim(result, 1);
+  const unsigned cols = (unsigned)dim(wid, 0);
+  Dispatch &d = emit(w8 ? Launch::LinearW8 : Launch::LinearF16, nullptr);
+  d.epilogue = epilogue_name(f.kind);
+  d.fusedOpIndex = d.epilogue ? (producer == index_ ? f.consumer : producer) : 0;
+  d.buf[0] = in;
+  d.buf[1] = scales;
+  d.buf[2] = weight;
+  d.buf[3] = {Space::Scale, weight.index, 0};
+  d.buf[4] = outRef;
+  d.buf[5] = auxRef;
+  d.buf[6] = biasRef;
+  if (w8) {
+    d.p.linearW8 = {width, 0, (unsigned)dim(o.inputs[1], 1), rows, cols, f.kind, f.block};
+    if (llmi_hip_dispatch_count(LLMI_HIP_OP_LINEAR_W8A8, &d.p.linearW8) == 0)
+      return fail(LLMI_HIP_INVALID_ARGUMENT, "plan: op %zu: %s", producer, llmi_hip_last_error());
+    d.kernels.push_back(llmi_hip_kernel_name(LLMI_HIP_OP_LINEAR_W8A8, &d.p.linearW8, 0));
+  } else {
+    d.p.linear = {rows, (unsigned)dim(o.inputs[0], 1), width, 0, cols, f.kind, f.block};
+    d.kernels.push_back("linearF16");
+  }
+  return LLMI_HIP_OK;
+}
+
+int Lowering::lower(size_t i) {
+  const auto &o = op(i);
+  const uint32_t *in = o.inputs, *out = o.outputs;
+  Ref r[6];
+  auto dense_all = [&](std::initializer_list<std::pair<uint32_t, int>> ids) -> int {
+    for (auto [id, slot] : ids)
+      if (int rc = dense(id, r[slot]))
+        return rc;
+    return LLMI_HIP_OK;
+  };
+  auto state = [&](uint32_t s) { return Ref{Space::State, s, 0}; };
+  switch (o.kind) {
+  case LLMI_GRAPH_RESHAPE:
+  case LLMI_GRAPH_SLICE:
+    return LLMI_HIP_OK;
+  case LLMI_GRAPH_EMBEDDING_GATHER: {
+    if (int rc = dense_all({{in[0], 0}, {in[1], 1}, {out[0], 2}}))
+      return rc;
+    const unsigned tokens = (unsigned)g_.tokens, hidden = (unsigned)dim(out[0], 1);
+    const unsigned rows = (unsigned)dim(in[1], 0);
+    if (value(in[1]).group_size) {
+      Dispatch &d = emit(Launch::EmbeddingW8, "embeddingW8");
+      d.p.embedW8 = {tokens, hidden, 0, rows, (hidden + 31) / 32};
+      d.buf[0] = r[0], d.buf[1] = r[1], d.buf[2] = {Space::Scale, r[1].index, 0}, d.buf[3] = r[2];
+    } else {
+      Dispatch &d = emit(Launch::Embedding, "embedding");
+      d.p.embed = {tokens, hidden, 0, rows};
+      d.buf[0] = r[0], d.buf[1] = r[1], d.buf[2] = r[2];
+    }
+    return LLMI_HIP_OK;
+  }
+  case LLMI_GRAPH_LINEAR_F16:
+  case LLMI_GRAPH_LINEAR_W8A8:
+    return linear(i, out[0], -1, -1);
+  case LLMI_GRAPH_QUANTIZE_ACTIVATION: {
+    if (value(out[0]).group_size != 32)
+      return fail(LLMI_HIP_INVALID_ARGUMENT,
+                  "plan: activation quantization requires 32-element groups");
+    if (int rc = dense_all({{in[0], 0}, {out[0], 1}, {out[1], 2}}))
+      return rc;
+    Dispatch &d = emit(Launch::Quantize, "quantizeActivation");
+    d.p.quantize = {(unsigned)dim(in[0], 0), (unsigned)dim(in[0], 1), (unsigned)dim(out[1], 1)};
+    d.buf[0] = r[0], d.buf[1] = r[1], d.buf[2] = r[2], d.buf[3] = {Space::Invalid, 0, 0};
+    return LLMI_HIP_OK;
+  }
+  case LLMI_GRAPH_RMS_NORM:
+  case LLMI_GRAPH_GATED_RMS_NORM: {
+    const bool gated = o.kind == LLMI_GRAPH_GATED_RMS_NORM;
+    const uint32_t w = in[gated ? 2 : 1];
+    const unsigned width = (unsigned)dim(w, 0);
+    const RowParams p{(unsigned)(count(in[0]) / width), width, o.epsilon};
+    if (!gated) {
+      if (int rc = dense_all({{in[0], 0}, {in[1], 1}, {out[0], 2}}))
+        return rc;
+      Dispatch &d = emit(Launch::RmsNorm, nullptr);
+      d.p.row = p;
+      d.kernels.push_back(llmi_hip_kernel_name(LLMI_HIP_OP_RMS_NORM, &p, 0));
+      d.buf[0] = r[0], d.buf[1] = r[1], d.buf[2] = r[2];
+      return LLMI_HIP_OK;
+    }
+    if (int rc = dense_all({{in[0], 0}, {in[1], 1}, {in[2], 2}, {out[0], 3}}))
+      return rc;
+    const int64_t gp = value(in[1]).defining_op;
+    const bool activated = gp >= 0 && fusion_[gp].kind == LLMI_LINEAR_SILU_F32;
+    Dispatch &d = emit(activated ? Launch::GatedRmsNormActivated : Launch::GatedRmsNorm,
+                       activated ? "gatedRmsNormActivated" : "gatedRmsNorm");
+    d.p.row = p;
+    d.buf[0] = r[0], d.buf[1] = r[1], d.buf[2] = r[2], d.buf[3] = r[3];
+    return LLMI_HIP_OK;
+  }
+  case LLMI_GRAPH_L2_NORM: {
+    if (int rc = dense_all({{in[0], 0}, {out[0], 1}}))
+      return rc;
+    Dispatch &d = emit(Launch::L2Norm, "l2NormF32");
+    const unsigned width = (unsigned)o.group_width;
+    d.p.l2 = {(unsigned)(count(in[0]) / width), width, o.epsilon, o.scale};
+    d.buf[0] = r[0], d.buf[1] = r[1];
+    return LLMI_HIP_OK;
+  }
+  case LLMI_GRAPH_ADD:
+  case LLMI_GRAPH_SILU_MUL:
+  case LLMI_GRAPH_SIGMOID_MUL: {
+    const int64_t p = value(in[0]).defining_op;
+    if (o.kind == LLMI_GRAPH_SILU_MUL && p >= 0 && fusion_[p].kind == LLMI_LINEAR_SILU_MUL)
+      return linear(p, out[0], in[1], -1);
+    if (int rc = dense_all({{in[0], 0}, {in[1], 1}, {out[0], 2}}))
+      return rc;
+    const unsigned n = (unsigned)count(out[0]);
+    const int64_t gp = value(in[0]).defining_op >= 0 ? value(root_[in[0]]).defining_op : -1;
+    if (o.kind == LLMI_GRAPH_SIGMOID_MUL &&
+        !(gp >= 0 && fusion_[gp].kind == LLMI_LINEAR_SIGMOID_COLUMNS)) {
+      Dispatch &d = emit(Launch::SigmoidMul, nullptr);
+      d.p.element = {n};
+      d.kernels.push_back(llmi_hip_kernel_name(LLMI_HIP_OP_SIGMOID_MUL, &d.p.element, 0));
+      d.buf[0] = r[0], d.buf[1] = r[1], d.buf[2] = r[2];
+      return LLMI_HIP_OK;
+    }
+    const ElementwiseKind k = o.kind == LLMI_GRAPH_ADD        ? ElementwiseKind::Add
+                              : o.kind == LLMI_GRAPH_SILU_MUL ? ElementwiseKind::SwiGlu
+                                                              : ElementwiseKind::Multiply;
+    Dispatch &d = emit(Launch::Elementwise, k == ElementwiseKind::Add      ? "residualAdd"
+                                            : k == ElementwiseKind::SwiGlu ? "swiGlu"
+                                                                           : "multiplyF16");
+    d.elementwise = k;
+    d.p.element = {n};
+    d.buf[0] = r[0], d.buf[1] = r[1], d.buf[2] = r[2];
+    return LLMI_HIP_OK;
+  }
+  case LLMI_GRAPH_SILU: {
+    const int64_t p = value(in[0]).defining_op;
+    if (p >= 0 && fusion_[p].kind == LLMI_LINEAR_SILU)
+      return linear(p, out[0], -1, -1);
+    if (int rc = dense_all({{in[0], 0}, {out[0], 1}}))
+      return rc;
+    Dispatch &d = emit(Launch::Elementwise, "siluF16");
+    d.elementwise = ElementwiseKind::Silu;
+    d.p.element = {(unsigned)count(out[0])};
+    d.buf[0] = r[0], d.buf[2] = r[1];
+    return LLMI_HIP_OK;
+  }
+  case LLMI_GRAPH_PARTIAL_ROPE: {
+    if (int rc = dense_all({{in[0], 0}, {out[0], 1}}))
+      return rc;
+    Dispatch &d = emit(Launch::PartialRope, nullptr);
+    const unsigned width = (unsigned)dim(in[0], 2);
+    d.p.rope = {(unsigned)(count(in[0]) / width), (unsigned)dim(in[0], 1), width,
+                (unsigned)o.rotary_width, (unsigned)g_.past, o.theta};
+    d.kernels.push_back(llmi_hip_kernel_name(LLMI_HIP_OP_PARTIAL_ROPE, &d.p.rope, 0));
+    d.buf[0] = r[0], d.buf[1] = r[1];
+    return LLMI_HIP_OK;
+  }
+  case LLMI_GRAPH_CAUSAL_CONV1D: {
+    if (int rc = dense_all({{in[0], 0}, {in[1], 1}, {out[0], 2}}))
+      return rc;
+    Dispatch &d = emit(Launch::CausalConv, nullptr);
+    d.p.conv = {(unsigned)g_.tokens, (unsigned)dim(in[0], 1), (unsigned)dim(in[1], 2), 0};
+    d.kernels.push_back(llmi_hip_kernel_name(LLMI_HIP_OP_CAUSAL_CONV, &d.p.conv, 0));
+    d.buf[0] = r[0], d.buf[1] = r[1], d.buf[2] = state(o.state), d.buf[3] = r[2];
+    return LLMI_HIP_OK;
+  }
+  case LLMI_GRAPH_DELTA_GATES: {
+    const int64_t a = value(in[0]).defining_op;
+    if (a >= 0 && fusion_[a].kind == LLMI_LINEAR_DELTA_DECAY) {
+      if (int rc = linear(a, out[1], in[2], in[3]))
+        return rc;
+      return linear(value(in[1]).defining_op, out[0], -1, -1);
+    }
+    if (int rc = dense_all({{in[0], 0}, {in[1], 1}, {in[2], 2}, {in[3], 3}, {out[0], 4},
+                            {out[1], 5}}))
+      return rc;
+    Dispatch &d = emit(Launch::DeltaGates, nullptr);
+    d.p.row = {(unsigned)dim(in[0], 0), (unsigned)dim(in[0], 1), 0.0f};
+    d.kernels.push_back(llmi_hip_kernel_name(LLMI_HIP_OP_DELTA_GATES, &d.p.row, 0));
+    for (int k = 0; k < 6; ++k)
+      d.buf[k] = r[k];
+    return LLMI_HIP_OK;
+  }
+  case LLMI_GRAPH_DELTA_UPDATE: {
+    if (int rc = dense_all({{in[0], 0}, {in[1], 1}, {in[2], 2}, {in[3], 3}, {in[4], 4},
+                            {out[0], 5}}))
+      return rc;
+    const auto &s = g_.states[o.state];
+    GraphDeltaParams p{(unsigned)g_.tokens, (unsigned)(dim(in[0], 1) / s.shape[1]),
+                       (unsigned)s.shape[1], (unsigned)s.shape[0], (unsigned)s.shape[2]};
+    const unsigned n = llmi_hip_dispatch_count(LLMI_HIP_OP_DELTA_UPDATE, &p);
+    if (n == 0)
+      return fail(LLMI_HIP_UNSUPPORTED, "plan: op %zu: %s", i, llmi_hip_last_error());
+    const uint64_t ws = llmi_hip_delta_workspace_bytes(p);
+    Dispatch &d = emit(Launch::DeltaUpdate, nullptr);
+    d.p.delta = p;
+    for (unsigned k = 0; k < n; ++k)
+      d.kernels.push_back(llmi_hip_kernel_name(LLMI_HIP_OP_DELTA_UPDATE, &p, k));
+    for (int k = 0; k < 5; ++k)
+      d.buf[k] = r[k];
+    d.buf[5] = state(o.state);
+    d.buf[6] = r[5];
+    d.workspaceBytes = ws;
+    if (ws)
+      d.buf[7] = temporary(ws);
+    return LLMI_HIP_OK;
+  }
+  case LLMI_GRAPH_KV_APPEND: {
+    if (int rc = dense_all({{in[0], 0}, {in[1], 1}}))
+      return rc;
+    const unsigned heads = (unsigned)g_.states[o.keys].shape[1];
+    const unsigned hd = (unsigned)g_.states[o.keys].shape[2];
+    Dispatch &d = emit(Launch::KvAppend, nullptr);
+    d.p.cache = {(unsigned)count(in[0]), (unsigned)(g_.past * heads * hd)};
+    d.kernels.push_back(llmi_hip_kernel_name(LLMI_HIP_OP_KV_APPEND, &d.p.cache, 0));
+    d.buf[0] = r[0], d.buf[1] = r[1], d.buf[2] = state(o.keys), d.buf[3] = state(o.values);
+    return LLMI_HIP_OK;
+  }
+  case LLMI_GRAPH_CAUSAL_GQA: {
+    if (int rc = dense_all({{in[0], 0}, {out[0], 1}}))
+      return rc;
+    const auto &cache = g_.states[o.keys].shape;
+    GqaParams p{(unsigned)g_.tokens, (unsigned)dim(in[0], 1), (unsigned)cache[1],
+                (unsigned)cache[2], (unsigned)g_.past};
+    const unsigned n = llmi_hip_dispatch_count(LLMI_HIP_OP_CAUSAL_GQA, &p);
+    if (n == 0)
+      return fail(LLMI_HIP_UNSUPPORTED, "plan: op %zu: %s", i, llmi_hip_last_error());
+    const uint64_t ws = llmi_hip_gqa_workspace_bytes(p);
+    Dispatch &d = emit(Launch::CausalGqa, nullptr);
+    d.p.gqa = p;
+    for (unsigned k = 0; k < n; ++k)
+      d.kernels.push_back(llmi_hip_kernel_name(LLMI_HIP_OP_CAUSAL_GQA, &p, k));
+    d.buf[0] = r[0], d.buf[1] = state(o.keys), d.buf[2] = state(o.values), d.buf[3] = r[1];
+    d.workspaceBytes = ws;
+    if (ws)
+      d.buf[4] = temporary(ws);
+    return LLMI_HIP_OK;
+  }
+  default:
+    return fail(LLMI_HIP_INVALID_ARGUMENT, "plan: op %zu has an unknown kind", i);
+  }
+}
+
+int Lowering::run() {
+  if (int rc = validate())
+    return rc;
+  size_t inputs = 0;
+  for (size_t i = 0; i < g_.value_count; ++i)
+    if (g_.values[i].kind == LLMI_GRAPH_INPUT) {
+      const auto &v = g_.values[i];
+      if (++inputs > 1 || v.element != LLMI_GRAPH_U32 || v.rank != 1 || v.shape[0] != g_.tokens)
+        return fail(LLMI_HIP_INVALID_ARGUMENT, "plan: expects a single token ID input");
+    }
+  if (!inputs)
+    return fail(LLMI_HIP_INVALID_ARGUMENT, "plan: missing token ID input");
+  if (g_.output_count > 1)
+    return fail(LLMI_HIP_INVALID_ARGUMENT, "plan: expects one logits output");
+  prepare_values();
+  prepare_fusions();
+  if (g_.output_count) {
+    const uint32_t id = g_.outputs[0];
+    const auto &v = value(id);
+    if (v.element != LLMI_GRAPH_F16 || v.rank != 2 || v.kind != LLMI_GRAPH_RESULT)
+      return fail(LLMI_HIP_INVALID_ARGUMENT, "plan: expects a dense FP16 logits result");
+    buffer_[id] = {Space::Output, 0, 0};
+    plan_.hasOutput = true;
+    plan_.logitRows = v.shape[0];
+    plan_.logitElements = count(id);
+  }
+  plan_.invalidOffset = arena_.allocate(4, g_.op_count);
+  for (index_ = 0; index_ < g_.op_count; ++index_) {
+    arena_.release_before(index_);
+    const Fusion &f = fusion_[index_];
+    if (f.deferred())
+      continue; // runs at its consumer, into the consumer's output
+    const auto &o = op(index_);
+    for (uint32_t j = 0; j < o.output_count; ++j) {
+      const uint32_t id = o.outputs[j];
+      const auto &v = value(id);
+      if (v.kind == LLMI_GRAPH_VIEW || buffer_[id].space != Space::None)
+        continue;
+      const uint64_t bytes = f.kind == LLMI_LINEAR_SILU_F32 ? 4 : element_bytes(v.element);
+      buffer_[id] = {Space::Scratch, 0, arena_.allocate(v.shape[0] * v.strides[0] * bytes,
+                                                        lastUse_[id])};
+    }
+    if (int rc = lower(index_))
+      return rc;
+  }
+  plan_.scratchBytes = (arena_.size() + kAlign - 1) / kAlign * kAlign;
+  for (const auto &d : plan_.dispatches)
+    for (const char *k : d.kernels)
+      plan_.records.push_back({d.opIndex, k, d.epilogue, d.fusedOpIndex});
+  plan_.stateCount = g_.state_count;
+  return LLMI_HIP_OK;
+}
+
+struct Bases {
+  unsigned char *scratch;
+  void *const *states;
+  const llmi_weight *weights;
+  const uint32_t *tokens;
+  uint16_t *logits;
+  uint32_t *invalid;
+};
+
+void *resolve(const Bases &b, const Ref &r) {
+  unsigned char *base = nullptr;
+  switch (r.space) {
+  case Space::None:
+    return nullptr;
+  case Space::Scratch:
+    base = b.scratch;
+    break;
+  case Space::Weight:
+    base = (unsigned char *)b.weights[r.index].data;
+    break;
+  case Space::Scale:
+    base = (unsigned char *)b.weights[r.index].scales;
+    break;
+  case Space::State:
+    base = (unsigned char *)b.states[r.index];
+    break;
+  case Space::Input:
+    base = (unsigned char *)b.tokens;
+    break;
+  case Space::Output:
+    base = (unsigned char *)b.logits;
+    break;
+  case Space::Invalid:
+    return b.invalid;
+  }
+  return base ? base + r.offset : nullptr;
+}
+
+int run_dispatch(const Dispatch &d, const Bases &b, hipStream_t stream) {
+  void *x[8];
+  for (int i = 0; i < 8; ++i)
+    x[i] = resolve(b, d.buf[i]);
+  auto u16 = [&](int i) { return static_cast<uint16_t *>(x[i]); };
+  auto f32 = [&](int i) { return static_cast<float *>(x[i]); };
+  switch (d.launch) {
+  case Launch::Embedding:
+    return llmi_hip_embedding((const uint32_t *)x[0], u16(1), u16(2), d.p.embed, stream);
+  case Launch::EmbeddingW8:
+    return llmi_hip_embedding_w8((const uint32_t *)x[0], (const int8_t *)x[1], u16(2), u16(3),
+                                 d.p.embedW8, stream);
+  case Launch::Quantize:
+    return llmi_hip_quantize_activation(u16(0), (int8_t *)x[1], f32(2), (uint32_t *)x[3],
+                                        d.p.quantize, stream);
+  case Launch::LinearW8:
+    return llmi_hip_linear_w8a8((const int8_t *)x[0], f32(1), (const int8_t *)x[2], u16(3),
+                                x[4], x[5], f32(6), d.p.linearW8, stream);
+  case Launch::LinearF16:
+    return llmi_hip_linear_f16(u16(0), u16(2), x[4], x[5], f32(6), d.p.linear, stream);
+  case Launch::RmsNorm:
+    return llmi_hip_rms_norm(u16(0), f32(1), u16(2), d.p.row, stream);
+  case Launch::GatedRmsNorm:
+    return llmi_hip_gated_rms_norm(u16(0), u16(1), f32(2), u16(3), d.p.row, stream);
+  case Launch::GatedRmsNormActivated:
+    return llmi_hip_gated_rms_norm_activated(u16(0), f32(1), f32(2), u16(3), d.p.row, stream);
+  case Launch::L2Norm:
+    return llmi_hip_l2_norm(u16(0), f32(1), d.p.l2, stream);
+  case Launch::Elementwise:
+    switch (d.elementwise) {
+    case ElementwiseKind::Add:
+      return llmi_hip_residual_add(u16(0), u16(1), u16(2), d.p.element, stream);
+    case ElementwiseKind::SwiGlu:
+      return llmi_hip_swiglu(u16(0), u16(1), u16(2), d.p.element, stream);
+    case ElementwiseKind::Silu:
+      return llmi_hip_silu(u16(0), u16(2), d.p.element, stream);
+    case ElementwiseKind::Multiply:
+      return llmi_hip_multiply(u16(0), u16(1), u16(2), d.p.element, stream);
+    }
+    break;
+  case Launch::SigmoidMul:
+    return llmi_hip_sigmoid_mul(u16(0), u16(1), u16(2), d.p.element, stream);
+  case Launch::PartialRope:
+    return llmi_hip_partial_rope(u16(0), u16(1), d.p.rope, stream);
+  case Launch::CausalConv:
+    return llmi_hip_causal_conv(u16(0), u16(1), u16(2), u16(3), d.p.conv, stream);
+  case Launch::DeltaGates:
+    return llmi_hip_delta_gates(u16(0), u16(1), f32(2), f32(3), f32(4), f32(5), d.p.row,
+                                stream);
+  case Launch::DeltaUpdate:
+    return llmi_hip_delta_update(f32(0), f32(1), u16(2), f32(3), f32(4), f32(5), u16(6),
+                                 d.p.delta, x[7], d.workspaceBytes, stream);
+  case Launch::KvAppend:
+    return llmi_hip_kv_append(u16(0), u16(1), u16(2), u16(3), d.p.cache, stream);
+  case Launch::CausalGqa:
+    return llmi_hip_causal_gqa(u16(0), u16(1), u16(2), u16(3), d.p.gqa, x[4],
+                               d.workspaceBytes, stream);
+  case Launch::CopyView:
+    return llmi_hip_copy_half_view(u16(0), u16(1), d.p.view, stream);
+  }
+  return fail(LLMI_HIP_INVALID_ARGUMENT, "plan: unknown dispatch");
+}
+
+} // namespace
+} // namespace llmi
+
+using namespace llmi;
+
+int llmi_hip_plan_lower(const llmi_graph *graph, const llmi_weight *weights, size_t weight_count,
+                        llmi_hip_plan **out) {
+  if (!out)
+    return fail(LLMI_HIP_INVALID_ARGUMENT, "plan: null output");
+  *out = nullptr;
+  if (!graph || (weight_count && !weights))
+    return fail(LLMI_HIP_INVALID_ARGUMENT, "plan: null graph or weights");
+  auto *plan = new llmi_hip_plan();
+  plan->weights.assign(weights, weights + weight_count);
+  Lowering lowering(*graph, weight_count, *plan);
+  if (int rc = lowering.run()) {
+    delete plan;
+    return rc;
+  }
+  *out = plan;
+  return LLMI_HIP_OK;
+}
+
+void llmi_hip_plan_destroy(llmi_hip_plan *plan) { delete plan; }
+
+size_t llmi_hip_plan_scratch_bytes(const llmi_hip_plan *plan) {
+  return plan ? plan->scratchBytes : 0;
+}
+
+void llmi_hip_plan_logits(const llmi_hip_plan *plan, uint64_t *rows, uint64_t *elements) {
+  if (rows)
+    *rows = plan ? plan->logitRows : 0;
+  if (elements)
+    *elements = plan ? plan->logitElements : 0;
+}
+
+size_t llmi_hip_plan_dispatches(const llmi_hip_plan *plan, llmi_hip_dispatch *records,
+                                size_t cap) {
+  if (!plan)
+    return 0;
+  if (records)
+    std::memcpy(records, plan->records.data(),
+                sizeof(llmi_hip_dispatch) * std::min(cap, plan->records.size()));
+  return plan->records.size();
+}
+
+int llmi_hip_plan_execute(const llmi_hip_plan *plan, void *scratch, size_t scratch_bytes,
+                          void *const *states, size_t state_count, const uint32_t *token_ids,
+                          uint16_t *logits, uint32_t *invalid, void *stream) {
+  if (!plan)
+    return fail(LLMI_HIP_INVALID_ARGUMENT, "plan: null plan");
+  if (scratch_bytes < plan->scratchBytes || (plan->scratchBytes && !scratch))
+    return fail(LLMI_HIP_WORKSPACE, "plan: needs a %llu-byte scratch arena",
+                (unsigned long long)plan->scratchBytes);
+  if (state_count != plan->stateCount || (state_count && !states))
+    return fail(LLMI_HIP_INVALID_ARGUMENT, "plan: expects %zu state buffers",
+                plan->stateCount);
+  for (size_t i = 0; i < state_count; ++i)
+    if (!states[i])
+      return fail(LLMI_HIP_INVALID_ARGUMENT, "plan: state %zu is null", i);
+  if (!token_ids || (plan->hasOutput && !logits))
+    return fail(LLMI_HIP_INVALID_ARGUMENT, "plan: null token IDs or logits");
+  unsigned char *base = static_cast<unsigned char *>(scratch);
+  const Bases b{base, states, plan->weights.data(), token_ids, logits,
+                invalid ? invalid : reinterpret_cast<uint32_t *>(base + plan->invalidOffset)};
+  for (const auto &d : plan->dispatches)
+    if (int rc = run_dispatch(d, b, static_cast<hipStream_t>(stream)))
+      return rc;
+  return LLMI_HIP_OK;
+}

@@ -83,6 +83,7 @@ def lib() -> C.CDLL:
         L.orc_embedding_w8.argtypes = [C.c_void_p, C.c_void_p, _u16p, _u16p] + [_u32] * 5
         L.orc_embedding.argtypes = [C.c_void_p, _u16p, _u16p] + [_u32] * 4
         L.orc_elementwise.argtypes = [_u32, _u16p, _u16p, _u16p, C.c_size_t]
+        L.orc_partial_rope.argtypes = [_u16p, _u16p] + [_u32] * 5 + [C.c_float]
         L.orc_copy_half_view.argtypes = [_u16p, _u16p, _u32, _u32, C.POINTER(_u32),
                                          C.POINTER(_u32)]
         L.orc_linear_f16.argtypes = [_u16p, _u16p, C.c_void_p, C.c_void_p, C.c_void_p] + \
@@ -251,6 +252,25 @@ def norm_rope(x, weight, tokens: int, heads: int, head_dim: int, rotary_dim: int
     lib().orc_norm_rope(a, w, output.reshape(-1), tokens, heads, head_dim, rotary_dim,
                         head_stride, past, output_start, epsilon, theta)
     return output
+
+
+def rms_norm(x, weight, epsilon: float = 1e-6) -> np.ndarray:
+    """rmsNorm (Reference.metal:105-117) over the last axis: normRope with
+    no rotated dims."""
+    a = np.ascontiguousarray(x, np.uint16)
+    width = a.shape[-1]
+    rows = a.size // width
+    return norm_rope(a, weight, rows, 1, width, 0, width, 0, epsilon).reshape(a.shape)
+
+
+def partial_rope(x, rotary_dim: int, past: int, theta: float = 1e7) -> np.ndarray:
+    """partialRope (Graph.metal:111-129): x [T, H, width] fp16 bits."""
+    a = np.ascontiguousarray(x, np.uint16)
+    T, H, width = a.shape
+    out = np.empty_like(a)
+    lib().orc_partial_rope(a.reshape(-1), out.reshape(-1), T * H, H, width, rotary_dim, past,
+                           theta)
+    return out
 
 
 def causal_conv(x, weight, history, apply_silu: bool = True) -> np.ndarray:

@@ -751,6 +751,23 @@ void orc_norm_rope(const uint16_t *input, const float *weight, uint16_t *output,
   }
 }
 
+/* partialRope, Graph.metal:111-129: rotatePair on the raw fp16 halves of
+ * the first rotary_dim dims at position past + row / heads, the rest copied. */
+void orc_partial_rope(const uint16_t *input, uint16_t *output, uint32_t rows, uint32_t heads,
+                      uint32_t width, uint32_t rotary_dim, uint32_t past, float theta) {
+  uint32_t half = rotary_dim / 2;
+  for (uint32_t row = 0; row < rows; ++row) {
+    const uint16_t *in = input + (size_t)row * width;
+    uint16_t *out = output + (size_t)row * width;
+    float position = (float)(past + row / heads);
+    for (uint32_t i = 0; i < half; ++i)
+      orc_rotate_pair(orc_f16_to_f32(in[i]), orc_f16_to_f32(in[i + half]), position, theta, i,
+                      rotary_dim, &out[i], &out[i + half]);
+    for (uint32_t i = rotary_dim; i < width; ++i)
+      out[i] = in[i];
+  }
+}
+
 /* gatedRmsNorm / gatedRmsNormActivated, Reference.metal:228-259:
  * out = fp16(fp16(x * rmsScale) * w[i] * g), g = silu(gate) for an fp16
  * gate, the fp32 gate itself when activated. */

@@ -155,6 +155,11 @@ void orc_norm_rope(const uint16_t *input, const float *weight, uint16_t *output,
                    uint32_t rotary_dim, uint32_t head_stride, uint32_t past,
                    uint32_t output_start, float epsilon, float theta);
 
+/* partialRope (lib/Backend/Metal/Kernels/Graph.metal:111-129): rows of
+ * width fp16 values, rotatePair on the first rotary_dim, the rest copied. */
+void orc_partial_rope(const uint16_t *input, uint16_t *output, uint32_t rows, uint32_t heads,
+                      uint32_t width, uint32_t rotary_dim, uint32_t past, float theta);
+
 /* gatedRmsNorm (gate16, fp16 gate through SiLU) or gatedRmsNormActivated
  * (gate32, already activated), lib/Backend/Metal/Kernels/Reference.metal:
  * 228-259: out = fp16(fp16(x * rmsScale(x)) * weight[i] * g), rows x width. */

@@ -10,7 +10,13 @@
 #include "llminfer/ModelFormat/Quantization.h"
 
 #include <cstdint>
+#include <cstdio>
+#include <cstdlib>
 #include <cstring>
+#include <sstream>
+#include <optional>
+#include <string>
+#include <vector>
 
 using namespace llminfer;
 using namespace llminfer::ir;
@@ -166,5 +172,186 @@ int ref_delta_graph(uint64_t tokens, const int *ranks, const uint64_t *dims,
   cost[2] = c.logicalWriteBytes;
   cost[3] = c.scalarOps;
   return 1;
+}
+
+// Replays a graph program through the reference's Graph::create / addInput /
+// addWeight / addState / append and reports what the reference inferred, so
+// a builder of the same graph can be compared value by value. The program
+// is text, one item a line (floats as C hex floats, ids in order):
+//   step T P C
+//   input ELEM RANK d...
+//   weight ID ELEM GROUP RANK d...
+//   state KIND LAYER ELEM RANK d...
+//   op KIND LAYER NIN in... ATTR [fields]   (LAYER -1: none)
+//      ATTR: none | quant G | norm EPS | l2 W EPS SCALE | reshape RANK d... |
+//            slice AXIS BEGIN LENGTH | rope W THETA | state S | kv K V
+// The report (into out, at most cap bytes) lists, per value:
+//   value KIND ELEM RANK d... s... VIEWOF OFFSET DEFOP GROUP   (-1: none)
+// and per op: effects OP N (STATE ACCESS BEGIN LENGTH BEFORE AFTER)...
+// A rejected item ends the report with "error INDEX message" (INDEX: the
+// op's position, or -1 for a source). Returns 0, or -1 when out is too small.
+int ref_graph_replay(const char *program, char *out, size_t cap) {
+  std::istringstream in(program);
+  std::ostringstream rep;
+  std::string line;
+  std::optional<Graph> graph;
+  auto fail = [&](long index, const Error &e) {
+    rep << "error " << index << " " << e.getMessage() << "\n";
+  };
+  auto readShape = [&](std::istringstream &ls) {
+    int rank = 0;
+    ls >> rank;
+    Shape s;
+    for (int i = 0; i < rank; ++i) {
+      uint64_t d;
+      ls >> d;
+      s.push_back(d);
+    }
+    return s;
+  };
+  auto readFloat = [&](std::istringstream &ls) {
+    std::string t;
+    ls >> t;
+    return std::strtof(t.c_str(), nullptr);
+  };
+  long opIndex = 0;
+  bool failed = false;
+  while (!failed && std::getline(in, line)) {
+    std::istringstream ls(line);
+    std::string kw;
+    if (!(ls >> kw))
+      continue;
+    if (kw == "step") {
+      uint64_t t, p, c;
+      ls >> t >> p >> c;
+      auto g = Graph::create({t, p, c});
+      if (!g) {
+        fail(-1, g.getError());
+        failed = true;
+      } else {
+        graph.emplace(std::move(*g));
+      }
+    } else if (kw == "input") {
+      int e;
+      ls >> e;
+      auto r = graph->addInput({elementOf(e), readShape(ls)});
+      if (!r) {
+        fail(-1, r.getError());
+        failed = true;
+      }
+    } else if (kw == "weight") {
+      std::string id;
+      int e;
+      uint64_t group;
+      ls >> id >> e >> group;
+      auto r = graph->addWeight(id, {elementOf(e), readShape(ls)}, group);
+      if (!r) {
+        fail(-1, r.getError());
+        failed = true;
+      }
+    } else if (kw == "state") {
+      int kind, e;
+      uint32_t layer;
+      ls >> kind >> layer >> e;
+      auto r = graph->addState(static_cast<StateKind>(kind), layer,
+                               {elementOf(e), readShape(ls)});
+      if (!r) {
+        fail(-1, r.getError());
+        failed = true;
+      }
+    } else if (kw == "op") {
+      int kind, layer, n;
+      ls >> kind >> layer >> n;
+      std::vector<ValueId> ins;
+      for (int i = 0; i < n; ++i) {
+        size_t v;
+        ls >> v;
+        ins.push_back({v});
+      }
+      std::string attr;
+      ls >> attr;
+      Attributes a;
+      if (attr == "quant") {
+        uint64_t g;
+        ls >> g;
+        a = QuantizeAttr{g};
+      } else if (attr == "norm") {
+        a = NormAttr{readFloat(ls)};
+      } else if (attr == "l2") {
+        uint64_t w;
+        ls >> w;
+        float eps = readFloat(ls), scale = readFloat(ls);
+        a = L2NormAttr{w, eps, scale};
+      } else if (attr == "reshape") {
+        a = ReshapeAttr{readShape(ls)};
+      } else if (attr == "slice") {
+        size_t axis;
+        uint64_t b, l;
+        ls >> axis >> b >> l;
+        a = SliceAttr{axis, b, l};
+      } else if (attr == "rope") {
+        uint64_t w;
+        ls >> w;
+        a = RopeAttr{w, readFloat(ls)};
+      } else if (attr == "state") {
+        size_t st;
+        ls >> st;
+        a = StateAttr{{st}};
+      } else if (attr == "kv") {
+        size_t k, v;
+        ls >> k >> v;
+        a = KvAttr{{k}, {v}};
+      }
+      std::optional<uint32_t> lay;
+      if (layer >= 0)
+        lay = static_cast<uint32_t>(layer);
+      Result<Values> r = Error("unsupported operand count");
+      switch (n) {
+      case 1: r = graph->append(static_cast<OpKind>(kind), {ins[0]}, a, lay); break;
+      case 2: r = graph->append(static_cast<OpKind>(kind), {ins[0], ins[1]}, a, lay); break;
+      case 3:
+        r = graph->append(static_cast<OpKind>(kind), {ins[0], ins[1], ins[2]}, a, lay);
+        break;
+      case 4:
+        r = graph->append(static_cast<OpKind>(kind), {ins[0], ins[1], ins[2], ins[3]}, a, lay);
+        break;
+      case 5:
+        r = graph->append(static_cast<OpKind>(kind), {ins[0], ins[1], ins[2], ins[3], ins[4]},
+                          a, lay);
+        break;
+      default: break;
+      }
+      if (!r) {
+        fail(opIndex, r.getError());
+        failed = true;
+      }
+      ++opIndex;
+    }
+  }
+  if (graph) {
+    for (const auto &v : graph->getValues()) {
+      rep << "value " << static_cast<int>(v.kind) << " " << static_cast<int>(v.type.element)
+          << " " << v.type.shape.size();
+      for (auto d : v.type.shape)
+        rep << " " << d;
+      for (auto d : v.strides)
+        rep << " " << d;
+      rep << " " << (v.viewOf ? (long)v.viewOf->index : -1L) << " " << v.viewOffset << " "
+          << (v.definingOp ? (long)*v.definingOp : -1L) << " " << v.groupSize << "\n";
+    }
+    size_t i = 0;
+    for (const auto &op : graph->getOps()) {
+      rep << "effects " << i++ << " " << op.effects.size();
+      for (const auto &e : op.effects)
+        rep << " " << e.state.index << " " << static_cast<int>(e.access) << " " << e.begin
+            << " " << e.length << " " << e.versionBefore << " " << e.versionAfter;
+      rep << "\n";
+    }
+  }
+  std::string text = rep.str();
+  if (text.size() + 1 > cap)
+    return -1;
+  std::memcpy(out, text.c_str(), text.size() + 1);
+  return 0;
 }
 }

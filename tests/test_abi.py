@@ -126,14 +126,14 @@ def test_delta_front_abi():
     assert ops.kernel_names(_lib.OP_L2_NORM, _lib.L2Params(64, 128, 1e-6, 1.0)) == ["l2NormTile"]
     assert ops.kernel_names(_lib.OP_L2_NORM, _lib.L2Params(64, 100, 1e-6, 1.0)) == ["l2NormRows"]
     assert ops.kernel_names(_lib.OP_DELTA_GATES, _lib.RowParams(1024, 32, 0)) == ["deltaGates"]
-    # gatedRmsNorm: widths beyond the tile are refused before any launch
-    assert lib.llmi_hip_gated_rms_norm(16, 16, 16, 16, _lib.RowParams(4, 100, 1e-6), None) == \
-        _lib.UNSUPPORTED
+    # gatedRmsNorm: the LDS tile up to width 256 in multiples of 8, else a
+    # thread per row
     assert lib.llmi_hip_gated_rms_norm(None, 16, 16, 16, _lib.RowParams(4, 128, 1e-6), None) == \
         _lib.INVALID_ARGUMENT
     assert ops.kernel_names(_lib.OP_GATED_RMS_NORM, _lib.RowParams(32768, 128, 1e-6)) == \
         ["gatedRmsNormTile"]
-    assert ops.kernel_names(_lib.OP_GATED_RMS_NORM, _lib.RowParams(4, 100, 1e-6)) == []
+    assert ops.kernel_names(_lib.OP_GATED_RMS_NORM, _lib.RowParams(4, 100, 1e-6)) == \
+        ["gatedRmsNormRows"]
 
 
 def test_invalid_gqa_rejected_before_launch():

@@ -123,7 +123,10 @@ def test_gate_beta_every_fp16_value(gpu):
 
 @pytest.mark.parametrize("rows,width,activated", [(1024 * 32, 128, False), (32, 128, False),
                                                   (1000, 128, True), (45, 256, False),
-                                                  (7, 64, True)])
+                                                  (7, 64, True),
+                                                  # a thread per row: odd and wide widths
+                                                  (37, 5, False), (9, 5, True), (300, 100, False),
+                                                  (3, 264, True)])
 def test_gated_rms_norm(gpu, rows, width, activated):
     rng = np.random.default_rng(rows + width)
     x = _f16(rng, (rows, width))
@@ -134,7 +137,8 @@ def test_gated_rms_norm(gpu, rows, width, activated):
         gt = torch.from_numpy(g).to(gpu)
     else:
         g = _f16(rng, (rows, width), 3.0)
-        g[1, :6] = [0x7BFF, 0xFBFF, 0x0000, 0x8000, 0xCC00, 0x4C00]
+        special = [0x7BFF, 0xFBFF, 0x0000, 0x8000, 0xCC00, 0x4C00][:width]
+        g[1, :len(special)] = special
         gt = u16_to_torch(g)
     out = torch.empty(rows, width, dtype=torch.float16, device=gpu)
     print(f"gatedRmsNorm rows={rows} width={width} activated={activated}", flush=True)

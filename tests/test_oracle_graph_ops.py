@@ -105,3 +105,17 @@ def test_linear_f16_epilogue_and_shard():
     oracle.linear_f16(x, w[3:7], output=out, first_row=20, output_width=30)
     assert np.array_equal(out[:, 20:24], p[:, 3:7])
     assert np.all(out[:, :20] == 0x3C00) and np.all(out[:, 24:] == 0x3C00)
+
+
+def test_partial_rope_of_the_rms_norm_is_norm_rope():
+    """normRope (Reference.metal:271-293, pinned with the attention rows)
+    rounds the normalised value to fp16 before rotatePair, which is exactly
+    partialRope applied to rmsNorm's output."""
+    T, H, d, past = 5, 3, 24, 17
+    x = _rand16(12, (T * H, d), 3.0)
+    w = (np.random.default_rng(13).standard_normal(d) * 0.2).astype(np.float32)
+    normed = oracle.rms_norm(x, w)
+    assert np.array_equal(normed, oracle.norm_rope(x, w, T, H, d, 0, d, 0))
+    got = oracle.partial_rope(normed.reshape(T, H, d), 8, past)
+    assert np.array_equal(got.reshape(T * H, d), oracle.norm_rope(x, w, T, H, d, 8, d, past))
+    assert np.array_equal(got.reshape(T * H, d)[:, 8:], normed[:, 8:])
