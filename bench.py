@@ -652,6 +652,98 @@ class W8A8Mlp(Workload):
                 "gpu_bit_exact": exact}
 
 
+class Qwen35Model(Workload):
+    """Qwen3.5-4B with W8A8 weights (random, of the model's shapes) through
+    the whole-graph HIP plan (llminfer_amd.plan.ModelSession): the graph of
+    each step lowered once before timing, then one step a call. Decode:
+    step i runs at past = P + i after an untimed P-token prefill, one token
+    and the last row's logits; prefill: T tokens from past 0, the last
+    row's logits (the reference's llmi-benchmark: prefill then decode,
+    docs/architecture.md:145)."""
+    labels = ("step",)
+    dominant = "step"
+
+    def __init__(self, dev, T, past, plans=64, seed=30):
+        import torch
+        from llminfer_amd.graph import qwen35_4b
+        from llminfer_amd.plan import ModelSession, random_weights
+        self.c = c = qwen35_4b()
+        self.T, self.P = T, past
+        self.tokens = T
+        self.decode = T == 1
+        self.bound = "hbm" if self.decode else "mfma"
+        self.name = f"qwen35_4b_w8a8_decode_P{past}" if self.decode else \
+            f"qwen35_4b_w8a8_prefill_{T}"
+        weights = random_weights(c, True, dev, seed)
+        self.session = s = ModelSession(c, weights, past + plans + T + 8, True, dev)
+        g = torch.Generator().manual_seed(seed)
+        if self.decode and past:
+            s.step(torch.randint(0, c.vocabulary, (past,), generator=g).numpy(), "none")
+        self.plans = [s.plan(T, "last")]
+        if self.decode:
+            for i in range(1, plans):
+                s.past += 1           # the graph of the next position (no step run)
+                self.plans.append(s.plan(1, "last"))
+            s.past = past
+        self.ids = torch.randint(0, c.vocabulary, (T,), generator=g, dtype=torch.int32).to(dev)
+        self.logits = torch.empty(1, c.vocabulary, dtype=torch.float16, device=dev)
+        s.run(self.plans[-1], self.ids, self.logits)   # size the scratch arena once
+        torch.cuda.synchronize()
+
+    def op(self, label, i):
+        self.session.run(self.plans[i % len(self.plans)], self.ids, self.logits)
+
+    def kernels(self):
+        return f"whole-graph plan ({len(self.plans[0].dispatches)} launches a step)"
+
+    def weight_bytes(self):
+        from llminfer_amd.graph import EMBEDDING_ID, Element, qwen35_tensors
+        total = 0
+        for tid, (element, shape) in qwen35_tensors(self.c, True).items():
+            if tid == EMBEDDING_ID:
+                continue  # gathered rows here; the tied head below reads it whole
+            n = 1
+            for d in shape:
+                n *= d
+            total += n * (1 if element == Element.I8 else 2 if element == Element.F16 else 4)
+            if element == Element.I8:
+                total += shape[0] * ((shape[1] + 31) // 32) * 2
+        rows, width = self.c.vocabulary, self.c.hidden
+        return total + rows * width + rows * ((width + 31) // 32) * 2
+
+    def work(self, i):
+        c = self.c
+        gqa = sum(k == "gqa" for k in c.layers)
+        delta = len(c.layers) - gqa
+        if self.decode:
+            past = self.P + i % len(self.plans)
+            kv = gqa * 2 * (past + 1) * c.kv_heads * c.head_dim * 2
+            state = delta * 2 * c.value_heads * c.key_dim * c.value_dim * 4
+            return self.weight_bytes() + kv + state
+        # prefill: two flops per weight per token (the projections and the
+        # head on the last row), attention's QK and PV, the delta rule's
+        # recurrent count (4 dk dv per head and token)
+        proj = (self.weight_bytes() - c.vocabulary * c.hidden) * 2 * self.T
+        head = 2 * c.vocabulary * c.hidden
+        att = gqa * 2 * 2 * c.q_heads * c.head_dim * self.T * (self.T + 1) // 2
+        rec = delta * 4 * c.value_heads * c.key_dim * c.value_dim * self.T
+        return proj + head + att + rec
+
+    def config(self):
+        c = self.c
+        return {"workload": self.name, "model": "Qwen3.5-4B (random weights of its shapes)",
+                "precision": "W8A8", "tokens": self.T, "past": self.P,
+                "layers": len(c.layers), "vocabulary": c.vocabulary,
+                "launches_per_step": len(self.plans[0].dispatches),
+                "scratch_bytes": self.plans[0].scratch_bytes,
+                "reference_m2_tok_s": 9.82 if self.decode else 20.81}
+
+    def cpu(self, budget_s):
+        return {"value": None, "unit": "tok/s", "cores": 0, "kind": "port",
+                "sample": "not timed: the whole-model oracle (tests/graph_runner.py) runs the "
+                          "two-layer test model; per-op CPU baselines are on the other legs"}
+
+
 def _delta_inputs(g, dev, T, hk, dk, hv, dv):
     """DeltaUpdate operands as the reference graph produces them: L2-normalised
     fp32 q (x 1/sqrt(dk)) and k from fp16 N(0,1) (Graph.metal:96-109), fp16 v,
@@ -1320,6 +1412,8 @@ def main(argv=None) -> int:
         ("next_l2norm_delta_gatednorm_decode", lambda: DeltaGatedNorm(dev, 1, 128, seed=13)),
         ("next_w8a8_mlp_decode", lambda: W8A8Mlp(dev, 1, 4, seed=20)),
         ("next_w8a8_mlp_prefill_128", lambda: W8A8Mlp(dev, 128, 4, seed=21)),
+        ("next_qwen35_decode", lambda: Qwen35Model(dev, 1, 512)),
+        ("next_qwen35_prefill_512", lambda: Qwen35Model(dev, 512, 0, plans=1)),
     ]
     unknown = only - {k for k, _ in builders} - {"headline"}
     if unknown:

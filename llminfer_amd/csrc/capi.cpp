@@ -126,7 +126,13 @@ int check_rope(const char *what, uint64_t rows, unsigned heads, unsigned D,
 }
 
 int rope_kernel_name_index(const RopeShape &s) {
-  return norm_rope_tiled(s, nullptr, nullptr) ? 0 : 1;
+  return norm_rope_tiled(s, nullptr, nullptr) ? 0 : norm_rope_wide_rows(s) ? 2 : 1;
+}
+
+static const char *rope_kernel_name(const RopeShape &s, const char *tile, const char *rows,
+                                    const char *wide) {
+  const int i = rope_kernel_name_index(s);
+  return i == 0 ? tile : i == 2 ? wide : rows;
 }
 
 extern "C" {
@@ -877,18 +883,18 @@ const char *llmi_hip_kernel_name(int op, const void *params, unsigned index) {
     const RopeParams &p = *static_cast<const RopeParams *>(params);
     RopeShape s = rope_shape(p.tokens * p.heads, p.heads, p.headDim, p.rotaryDim,
                              p.headStride, p.past, 0, 0, 0, true);
-    return rope_kernel_name_index(s) == 0 ? "normRopeTile" : "normRopeRows";
+    return rope_kernel_name(s, "normRopeTile", "normRopeRows", "normRopeWide");
   }
   case LLMI_HIP_OP_RMS_NORM: {
     const RowParams &p = *static_cast<const RowParams *>(params);
     RopeShape s = rope_shape(p.rows, 1, p.width, 0, p.width, 0, 0, 0, 0, true);
-    return rope_kernel_name_index(s) == 0 ? "normRopeTile" : "normRopeRows";
+    return rope_kernel_name(s, "normRopeTile", "normRopeRows", "normRopeWide");
   }
   case LLMI_HIP_OP_PARTIAL_ROPE: {
     const PartialRopeParams &p = *static_cast<const PartialRopeParams *>(params);
     RopeShape s = rope_shape(p.rows, p.heads, p.width, p.rotaryWidth, p.width, 0, 0, 0,
                              0, false);
-    return rope_kernel_name_index(s) == 0 ? "partialRopeTile" : "partialRopeRows";
+    return rope_kernel_name(s, "partialRopeTile", "partialRopeRows", "partialRopeWide");
   }
   case LLMI_HIP_OP_CAUSAL_CONV:
     return "causalConv";

@@ -155,6 +155,8 @@ struct RopeShape {
 };
 
 bool norm_rope_tiled(const RopeShape &s, const void *in, const void *out);
+// Rows wider than the tile's limit (a workgroup per row, the row in LDS).
+bool norm_rope_wide_rows(const RopeShape &s);
 hipError_t launch_norm_rope(const uint16_t *in, const float *w, uint16_t *out,
                             const RopeShape &s, hipStream_t stream);
 

@@ -53,6 +53,8 @@ namespace llmi {
 namespace {
 
 constexpr int kPad = 8;                 // halves of LDS padding per tile row
+// Rows past the tile's width limit, up to 32K halves, take a workgroup each.
+constexpr unsigned kWideMin = 256, kWideMax = 32768;
 constexpr unsigned kTileHalves = 8192;  // rows * headDim bound of one tile
 constexpr unsigned kTileIters = kTileHalves / 8 / 64;
 
@@ -282,6 +284,57 @@ __global__ __launch_bounds__(256) void norm_rope_rows(const uint16_t *in,
     dst[i] = kNorm ? f2h(normed(head[i], scale, 1.0f + w[i])) : head[i];
 }
 
+// Rows wider than the tile (the 2560-wide hidden rows of the model's
+// RMSNorms): a workgroup per row. The row is staged in LDS by all 256
+// threads; one lane runs rmsScale's fma chain over it in order (the
+// reference's arithmetic: one sequential fp32 sum), reading 8 halves per
+// LDS load; then every thread writes its share of the outputs.
+template <bool kNorm>
+__global__ __launch_bounds__(256) void norm_rope_wide(const uint16_t *in,
+                                                      const float *__restrict__ w,
+                                                      uint16_t *out, TileArgs a, RopeFreqs f) {
+  extern __shared__ __align__(16) uint16_t srow[];
+  __shared__ float sscale;
+  const unsigned row = blockIdx.x, t = threadIdx.x;
+  const uint16_t *head = in + (size_t)row * a.stride;
+  uint16_t *dst = out + (size_t)(a.out_row0 + row) * a.D;
+  for (unsigned i = t; i < a.D; i += 256)
+    srow[i] = head[i];
+  __syncthreads();
+  if (kNorm && t == 0) {
+    float sum = 0.0f;
+    unsigned i = 0;
+    for (; i + 8 <= a.D; i += 8) {
+      const uint4_t q = *reinterpret_cast<const uint4_t *>(srow + i);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float lo = h2f((uint16_t)(q[e] & 0xFFFFu)), hi = h2f((uint16_t)(q[e] >> 16));
+        sum = __builtin_fmaf(lo, lo, sum);
+        sum = __builtin_fmaf(hi, hi, sum);
+      }
+    }
+    for (; i < a.D; ++i) {
+      const float v = h2f(srow[i]);
+      sum = __builtin_fmaf(v, v, sum);
+    }
+    sscale = rms_scale_of(sum, a.D, a.eps);
+  }
+  __syncthreads();
+  const float scale = kNorm ? sscale : 1.0f;
+  const unsigned half = a.rot / 2;
+  const float position = (float)(a.past + row / a.heads);
+  for (unsigned i = t; i < half; i += 256) {
+    const unsigned j = i + half;
+    const float x = kNorm ? normed(srow[i], scale, 1.0f + w[i]) : h2f(srow[i]);
+    const float y = kNorm ? normed(srow[j], scale, 1.0f + w[j]) : h2f(srow[j]);
+    const float2 cs = rope_cos_sin(__fdiv_rn(position, inv_freq(f, a, i)));
+    dst[i] = rotate_x(x, y, cs);
+    dst[j] = rotate_y(x, y, cs);
+  }
+  for (unsigned i = a.rot + t; i < a.D; i += 256)
+    dst[i] = kNorm ? f2h(normed(srow[i], scale, 1.0f + w[i])) : srow[i];
+}
+
 // Eight gates per lane: the estimates first, then the exact evaluation for
 // the few that need it, one per pass (a pass costs the wave one double exp,
 // so the lanes share passes instead of running one per element slot).
@@ -368,6 +421,8 @@ bool norm_rope_tiled(const RopeShape &s, const void *in, const void *out) {
          aligned16(in) && aligned16(out);
 }
 
+bool norm_rope_wide_rows(const RopeShape &s) { return s.D > kWideMin && s.D <= kWideMax; }
+
 hipError_t launch_norm_rope(const uint16_t *in, const float *w, uint16_t *out,
                             const RopeShape &s, hipStream_t stream) {
   if (s.rows == 0 || s.D == 0)
@@ -384,6 +439,14 @@ hipError_t launch_norm_rope(const uint16_t *in, const float *w, uint16_t *out,
       hipLaunchKernelGGL(norm_rope_tile<true>, grid, dim3(64), p.lds, stream, in, w, out, a, f);
     else
       hipLaunchKernelGGL(norm_rope_tile<false>, grid, dim3(64), p.lds, stream, in, w, out, a, f);
+  } else if (norm_rope_wide_rows(s)) {
+    const size_t lds = (size_t)(s.D + 8) * 2;
+    if (s.norm)
+      hipLaunchKernelGGL(norm_rope_wide<true>, dim3(s.rows), dim3(256), lds, stream, in, w, out,
+                         a, f);
+    else
+      hipLaunchKernelGGL(norm_rope_wide<false>, dim3(s.rows), dim3(256), lds, stream, in, w,
+                         out, a, f);
   } else {
     dim3 grid((s.rows + 255) / 256);
     if (s.norm)

@@ -196,3 +196,36 @@ def test_kernel_names_match_the_launch():
     assert ops.kernel_names(_lib.OP_NORM_ROPE,
                             _lib.RopeParams(1, 16, 256, 64, 512, 0, 0, 1e-6, 1e7)) == \
         ["normRopeTile"]
+
+
+@pytest.mark.parametrize("rows,width", [(1, 2560), (37, 2560), (3, 4100), (2, 257)])
+def test_rms_norm_wide_rows(gpu, rows, width):
+    """Rows past the tile's width (the model's hidden RMSNorms): a workgroup
+    per row, the same sequential sum, bit-exact; in place too."""
+    print(f"rmsNorm wide rows={rows} width={width}", flush=True)
+    x, w = _x(21 + rows, rows, width, 2.0), _w(21, width)
+    xt, wt = u16_to_torch(x), torch.from_numpy(w).to(gpu)
+    out = torch.empty_like(xt)
+    ops.rms_norm(xt, wt, out)
+    ops.rms_norm(xt, wt, xt)
+    torch.cuda.synchronize()
+    ref = oracle.norm_rope(x, w, rows, 1, width, 0, width, 0)
+    assert _same(torch_to_u16(out), ref, "wide")
+    assert np.array_equal(torch_to_u16(xt), ref)
+    assert ops.kernel_names(_lib.OP_RMS_NORM, _lib.RowParams(rows, width, 1e-6)) == \
+        ["normRopeWide"]
+
+
+def test_norm_rope_wide_heads(gpu):
+    """normRope and partialRope on heads wider than the tile (64 rotated
+    dims of 2600)."""
+    T, H, d, past = 3, 2, 2600, 9
+    x, w = _x(23, T * H, d), _w(23, d)
+    got, ref = _run_norm_rope(gpu, x, w, T, H, d, 64, d, past)
+    assert _same(got, ref, "normRope wide")
+    normed = oracle.norm_rope(x, w, T, H, d, 0, d, 0)
+    nt = u16_to_torch(normed.reshape(T, H, d))
+    rot = torch.empty_like(nt)
+    ops.partial_rope(nt, rot, past, 64)
+    torch.cuda.synchronize()
+    assert np.array_equal(torch_to_u16(rot).reshape(T * H, d), ref)
