@@ -53,8 +53,8 @@ namespace llmi {
 namespace {
 
 constexpr int kPad = 8;                 // halves of LDS padding per tile row
-// Rows past the tile's width limit, up to 32K halves, take a workgroup each.
-constexpr unsigned kWideMin = 256, kWideMax = 32768;
+// Rows past the tile's width limit, up to 16K halves, take a workgroup each.
+constexpr unsigned kWideMin = 256, kWideMax = 16384;
 constexpr unsigned kTileHalves = 8192;  // rows * headDim bound of one tile
 constexpr unsigned kTileIters = kTileHalves / 8 / 64;
 
@@ -285,37 +285,39 @@ __global__ __launch_bounds__(256) void norm_rope_rows(const uint16_t *in,
 }
 
 // Rows wider than the tile (the 2560-wide hidden rows of the model's
-// RMSNorms): a workgroup per row. The row is staged in LDS by all 256
-// threads; one lane runs rmsScale's fma chain over it in order (the
-// reference's arithmetic: one sequential fp32 sum), reading 8 halves per
-// LDS load; then every thread writes its share of the outputs.
+// RMSNorms): a workgroup per row. All 256 threads stage the row in LDS as
+// fp32 (x itself and, for the norm, nothing else: x * x is exact in fp32
+// for an fp16 x, so the chain needs only the fma); one lane then runs
+// rmsScale's fma chain in order -- the reference's one sequential fp32
+// sum, bound by one wave's VALU issue (~8 cycles an instruction, ~9 us at
+// width 2560) -- reading 4 terms per LDS load; every thread then writes its
+// share of the outputs.
 template <bool kNorm>
 __global__ __launch_bounds__(256) void norm_rope_wide(const uint16_t *in,
                                                       const float *__restrict__ w,
                                                       uint16_t *out, TileArgs a, RopeFreqs f) {
-  extern __shared__ __align__(16) uint16_t srow[];
+  extern __shared__ __align__(16) float srow[];
   __shared__ float sscale;
   const unsigned row = blockIdx.x, t = threadIdx.x;
   const uint16_t *head = in + (size_t)row * a.stride;
   uint16_t *dst = out + (size_t)(a.out_row0 + row) * a.D;
-  for (unsigned i = t; i < a.D; i += 256)
-    srow[i] = head[i];
+  const unsigned padded = (a.D + 31) / 32 * 32;
+  for (unsigned i = t; i < padded; i += 256)
+    srow[i] = i < a.D ? h2f(head[i]) : 0.0f;
   __syncthreads();
   if (kNorm && t == 0) {
+    // fma(0, 0, sum) == sum for the padding: sum starts at +0 and a sum of
+    // squares is never -0.
+    const float4 *v = reinterpret_cast<const float4 *>(srow);
+    const unsigned n = padded / 4; // a multiple of 8
     float sum = 0.0f;
-    unsigned i = 0;
-    for (; i + 8 <= a.D; i += 8) {
-      const uint4_t q = *reinterpret_cast<const uint4_t *>(srow + i);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const float lo = h2f((uint16_t)(q[e] & 0xFFFFu)), hi = h2f((uint16_t)(q[e] >> 16));
-        sum = __builtin_fmaf(lo, lo, sum);
-        sum = __builtin_fmaf(hi, hi, sum);
-      }
-    }
-    for (; i < a.D; ++i) {
-      const float v = h2f(srow[i]);
-      sum = __builtin_fmaf(v, v, sum);
+#pragma unroll 8
+    for (unsigned c = 0; c < n; ++c) {
+      const float4 q = v[c];
+      sum = __builtin_fmaf(q.x, q.x, sum);
+      sum = __builtin_fmaf(q.y, q.y, sum);
+      sum = __builtin_fmaf(q.z, q.z, sum);
+      sum = __builtin_fmaf(q.w, q.w, sum);
     }
     sscale = rms_scale_of(sum, a.D, a.eps);
   }
@@ -325,14 +327,14 @@ __global__ __launch_bounds__(256) void norm_rope_wide(const uint16_t *in,
   const float position = (float)(a.past + row / a.heads);
   for (unsigned i = t; i < half; i += 256) {
     const unsigned j = i + half;
-    const float x = kNorm ? normed(srow[i], scale, 1.0f + w[i]) : h2f(srow[i]);
-    const float y = kNorm ? normed(srow[j], scale, 1.0f + w[j]) : h2f(srow[j]);
+    const float x = kNorm ? normed_f(srow[i], scale, 1.0f + w[i]) : srow[i];
+    const float y = kNorm ? normed_f(srow[j], scale, 1.0f + w[j]) : srow[j];
     const float2 cs = rope_cos_sin(__fdiv_rn(position, inv_freq(f, a, i)));
     dst[i] = rotate_x(x, y, cs);
     dst[j] = rotate_y(x, y, cs);
   }
   for (unsigned i = a.rot + t; i < a.D; i += 256)
-    dst[i] = kNorm ? f2h(normed(srow[i], scale, 1.0f + w[i])) : srow[i];
+    dst[i] = kNorm ? f2h(normed_f(srow[i], scale, 1.0f + w[i])) : f2h(srow[i]);
 }
 
 // Eight gates per lane: the estimates first, then the exact evaluation for
@@ -440,7 +442,7 @@ hipError_t launch_norm_rope(const uint16_t *in, const float *w, uint16_t *out,
     else
       hipLaunchKernelGGL(norm_rope_tile<false>, grid, dim3(64), p.lds, stream, in, w, out, a, f);
   } else if (norm_rope_wide_rows(s)) {
-    const size_t lds = (size_t)(s.D + 8) * 2;
+    const size_t lds = (size_t)(s.D + 31) / 32 * 32 * 4;
     if (s.norm)
       hipLaunchKernelGGL(norm_rope_wide<true>, dim3(s.rows), dim3(256), lds, stream, in, w, out,
                          a, f);

@@ -43,8 +43,11 @@ __device__ __forceinline__ float rms_scale_of(float sum, unsigned width, float e
   return __fdiv_rn(1.0f, sqrt_cr(__fadd_rn(__fdiv_rn(sum, (float)width), eps)));
 }
 
+__device__ __forceinline__ float normed_f(float x, float scale, float w1) {
+  return round16(mul32(mul32(x, scale), w1));
+}
 __device__ __forceinline__ float normed(uint16_t v, float scale, float w1) {
-  return round16(mul32(mul32(h2f(v), scale), w1));
+  return normed_f(h2f(v), scale, w1);
 }
 
 // rotatePair on fp16 values x, y (held in floats) and fp16 cos/sin.
