@@ -97,7 +97,12 @@ def test_plan_records_row_ops():
     assert ops.kernel_names(_lib.OP_NORM_ROPE,
                             _lib.RopeParams(3, 2, 100, 36, 100, 0, 0, 1e-6, 1e7)) == \
         ["normRopeRows"]
+    # rows wider than the tile take a workgroup each up to 16K halves
     assert ops.kernel_names(_lib.OP_RMS_NORM, _lib.RowParams(7, 4096, 1e-6)) == \
+        ["normRopeWide"]
+    assert ops.kernel_names(_lib.OP_RMS_NORM, _lib.RowParams(7, 2560, 1e-6)) == \
+        ["normRopeWide"]
+    assert ops.kernel_names(_lib.OP_RMS_NORM, _lib.RowParams(7, 20000, 1e-6)) == \
         ["normRopeRows"]
     assert ops.kernel_names(_lib.OP_PARTIAL_ROPE,
                             _lib.PartialRopeParams(64, 16, 256, 64, 3, 1e7)) == \
