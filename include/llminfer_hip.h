@@ -170,7 +170,8 @@ enum llmi_hip_op {
   LLMI_HIP_OP_SILU = 19,                /* params: ElementParams */
   LLMI_HIP_OP_MULTIPLY = 20,            /* params: ElementParams */
   LLMI_HIP_OP_COPY_HALF_VIEW = 21,      /* params: HalfViewParams */
-  LLMI_HIP_OP_LINEAR_F16 = 22           /* params: LinearParams */
+  LLMI_HIP_OP_LINEAR_F16 = 22,          /* params: LinearParams */
+  LLMI_HIP_OP_ADD_RMS_NORM_QUANTIZE = 23 /* params: RowParams */
 };
 
 /* ---------------------------------------------------------------- KvAppend
@@ -493,6 +494,18 @@ LLMI_HIP_API int llmi_hip_copy_half_view(const uint16_t *src, uint16_t *out, Hal
 LLMI_HIP_API int llmi_hip_linear_f16(const uint16_t *input, const uint16_t *weight, void *output,
                                      const void *aux, const float *bias, LinearParams p,
                                      void *stream);
+
+/* residualAdd -> rmsNorm -> quantizeActivation of rows x width in one launch
+ * (no counterpart in the reference, which launches the three; the plan uses
+ * it where a norm's only consumer is the quantization): sum = fp16(a + b)
+ * written to sum_out, then exactly llmi_hip_rms_norm of sum and
+ * llmi_hip_quantize_activation of that into q [rows][groups * 32] (16-byte
+ * aligned), scales [rows][groups] and *invalid (may be NULL). b == NULL
+ * normalises a itself (sum_out unused). width <= 16384. */
+LLMI_HIP_API int llmi_hip_add_rms_norm_quantize(const uint16_t *a, const uint16_t *b,
+                                                uint16_t *sum_out, const float *weight,
+                                                int8_t *q, float *scales, uint32_t *invalid,
+                                                RowParams p, void *stream);
 
 /* ----------------------------------------------------------------- helpers */
 

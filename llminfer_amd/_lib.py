@@ -41,6 +41,7 @@ OP_SILU = 19
 OP_MULTIPLY = 20
 OP_COPY_HALF_VIEW = 21
 OP_LINEAR_F16 = 22
+OP_ADD_RMS_NORM_QUANTIZE = 23
 
 # LinearEpilogue (ReferenceParams.h:8-16)
 LINEAR_NONE, LINEAR_SILU, LINEAR_SILU_MUL, LINEAR_SIGMOID_COLUMNS = 0, 1, 2, 3
@@ -181,6 +182,7 @@ SIGNATURES = {
     "llmi_hip_multiply": (C.c_int, [_P, _P, _P, ElementParams, _P]),
     "llmi_hip_copy_half_view": (C.c_int, [_P, _P, HalfViewParams, _P]),
     "llmi_hip_linear_f16": (C.c_int, [_P, _P, _P, _P, _P, LinearParams, _P]),
+    "llmi_hip_add_rms_norm_quantize": (C.c_int, [_P, _P, _P, _P, _P, _P, _P, RowParams, _P]),
     "llmi_hip_workspace_init": (C.c_int, [_P, _SZ, _P]),
     "llmi_hip_dispatch_count": (C.c_uint, [C.c_int, _P]),
     "llmi_hip_kernel_name": (C.c_char_p, [C.c_int, _P, C.c_uint]),

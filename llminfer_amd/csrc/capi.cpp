@@ -364,6 +364,31 @@ int llmi_hip_multiply(const uint16_t *a, const uint16_t *b, uint16_t *out, Eleme
   return elementwise(ElementwiseKind::Multiply, "multiplyF16", a, b, out, p, stream);
 }
 
+static int check_add_norm_quantize(const RowParams &p) {
+  if (p.width > kAddNormQuantizeMax)
+    return fail(LLMI_HIP_UNSUPPORTED, "addRmsNormQuantize: width %u (at most %u)", p.width,
+                kAddNormQuantizeMax);
+  if (!fits32(p.rows, (p.width + 31) / 32 * 32, 1))
+    return fail(LLMI_HIP_INVALID_ARGUMENT, "addRmsNormQuantize: exceeds the 32-bit index range");
+  return LLMI_HIP_OK;
+}
+
+int llmi_hip_add_rms_norm_quantize(const uint16_t *a, const uint16_t *b, uint16_t *sum_out,
+                                   const float *weight, int8_t *q, float *scales,
+                                   uint32_t *invalid, RowParams p, void *stream) {
+  if (p.rows == 0 || p.width == 0)
+    return LLMI_HIP_OK;
+  if (int rc = check_add_norm_quantize(p))
+    return rc;
+  if (!a || !weight || !q || !scales || (b && !sum_out))
+    return fail(LLMI_HIP_INVALID_ARGUMENT, "addRmsNormQuantize: null buffer");
+  if (!aligned16(q))
+    return fail(LLMI_HIP_UNSUPPORTED, "addRmsNormQuantize: quantized rows not 16-byte aligned");
+  return launched(launch_add_norm_quantize(a, b, sum_out, weight, q, scales, invalid, p.rows,
+                                           p.width, p.epsilon, static_cast<hipStream_t>(stream)),
+                  b ? "addRmsNormQuantize" : "rmsNormQuantize");
+}
+
 static int check_view(const HalfViewParams &p) {
   uint64_t last = p.offset;
   for (int d = 0; d < 3; ++d) {
@@ -818,6 +843,10 @@ unsigned llmi_hip_dispatch_count(int op, const void *params) {
     const HalfViewParams &p = *static_cast<const HalfViewParams *>(params);
     return p.count && check_view(p) == LLMI_HIP_OK ? 1 : 0;
   }
+  case LLMI_HIP_OP_ADD_RMS_NORM_QUANTIZE: {
+    const RowParams &p = *static_cast<const RowParams *>(params);
+    return p.rows && p.width && check_add_norm_quantize(p) == LLMI_HIP_OK ? 1 : 0;
+  }
   case LLMI_HIP_OP_LINEAR_F16: {
     const LinearParams &p = *static_cast<const LinearParams *>(params);
     return p.tokens && p.rowCount && check_linear_f16(p) == LLMI_HIP_OK ? 1 : 0;
@@ -924,6 +953,8 @@ const char *llmi_hip_kernel_name(int op, const void *params, unsigned index) {
     return "copyHalfView";
   case LLMI_HIP_OP_LINEAR_F16:
     return "linearF16";
+  case LLMI_HIP_OP_ADD_RMS_NORM_QUANTIZE:
+    return "addRmsNormQuantize";
   case LLMI_HIP_OP_GATED_RMS_NORM: {
     const unsigned width = static_cast<const RowParams *>(params)->width;
     return width % 8 == 0 && width <= 256 ? "gatedRmsNormTile" : "gatedRmsNormRows";

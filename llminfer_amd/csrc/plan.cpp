@@ -40,7 +40,7 @@ struct Ref {
 enum class Launch : uint8_t {
   Embedding, EmbeddingW8, Quantize, LinearW8, LinearF16, RmsNorm, GatedRmsNorm,
   GatedRmsNormActivated, L2Norm, Elementwise, SigmoidMul, PartialRope, CausalConv, DeltaGates,
-  DeltaUpdate, KvAppend, CausalGqa, CopyView
+  DeltaUpdate, KvAppend, CausalGqa, CopyView, AddNormQuantize
 };
 
 struct Dispatch {
@@ -67,6 +67,7 @@ struct Dispatch {
   size_t opIndex = 0, fusedOpIndex = 0;
   const char *epilogue = nullptr;
   std::vector<const char *> kernels;
+  std::vector<size_t> ops; // a launch serving several ops: a record for each
 };
 
 struct Fusion {
@@ -219,6 +220,7 @@ private:
   int validate();
   void prepare_values();
   void prepare_fusions();
+  void prepare_norm_quantize();
   int lower(size_t index);
   int dense(uint32_t id, Ref &out);
   int linear(size_t producer, uint32_t result, int64_t aux, int64_t bias);
@@ -242,6 +244,9 @@ private:
   std::vector<uint64_t> offset_; // element offset of a view in its root
   std::vector<Ref> buffer_;      // of roots
   std::vector<Fusion> fusion_;
+  std::vector<unsigned> uses_;   // non-view uses of each root
+  std::vector<int64_t> normQuantize_, normAdd_; // by RmsNorm op: the fused ops
+  std::vector<char> skip_;       // launched by a fused launch at another op
 };
 
 int Lowering::validate() {
@@ -333,7 +338,8 @@ void Lowering::prepare_values() {
 // the second half of every interleaved head (the sigmoid-columns epilogue).
 void Lowering::prepare_fusions() {
   const size_t n = g_.value_count;
-  std::vector<unsigned> uses(n, 0);
+  std::vector<unsigned> &uses = uses_;
+  uses.assign(n, 0);
   std::vector<uint32_t> firstUse(n, 0), secondUse(n, 0);
   auto record = [&](uint32_t id) {
     size_t r = root_[id];
@@ -418,6 +424,39 @@ void Lowering::prepare_fusions() {
     }
     default:
       break;
+    }
+  }
+}
+
+// RMSNorm -> QuantizeActivation (the norm's only consumer, the next op),
+// with the Add that produced the norm's input when it is the op before:
+// one launch (llmi_hip_add_rms_norm_quantize) with the same bits, recorded
+// under each op. The Add's operands stay live until the norm's index.
+void Lowering::prepare_norm_quantize() {
+  const size_t n = g_.op_count;
+  normQuantize_.assign(n, -1);
+  normAdd_.assign(n, -1);
+  skip_.assign(n, 0);
+  for (size_t j = 0; j + 1 < n; ++j) {
+    const auto &o = op(j), &k = op(j + 1);
+    if (o.kind != LLMI_GRAPH_RMS_NORM || k.kind != LLMI_GRAPH_QUANTIZE_ACTIVATION)
+      continue;
+    const uint32_t normed = o.outputs[0], h = o.inputs[0];
+    if (k.inputs[0] != normed || uses_[normed] != 1 || value(normed).kind != LLMI_GRAPH_RESULT ||
+        value(k.outputs[0]).group_size != 32 || value(h).element != LLMI_GRAPH_F16 ||
+        !contiguous(h) || dim(o.inputs[1], 0) > kAddNormQuantizeMax ||
+        dim(h, -1) != dim(o.inputs[1], 0) || fusion_[j].kind != LLMI_LINEAR_NONE)
+      continue;
+    normQuantize_[j] = (int64_t)j + 1;
+    skip_[j + 1] = 1;
+    if (j > 0 && op(j - 1).kind == LLMI_GRAPH_ADD && op(j - 1).outputs[0] == h &&
+        value(h).kind == LLMI_GRAPH_RESULT) {
+      normAdd_[j] = (int64_t)j - 1;
+      skip_[j - 1] = 1;
+      for (uint32_t x = 0; x < op(j - 1).input_count; ++x) {
+        const size_t r = root_[op(j - 1).inputs[x]];
+        lastUse_[r] = std::max(lastUse_[r], j);
+      }
     }
   }
 }
@@ -549,6 +588,29 @@ int Lowering::lower(size_t i) {
     const uint32_t w = in[gated ? 2 : 1];
     const unsigned width = (unsigned)dim(w, 0);
     const RowParams p{(unsigned)(count(in[0]) / width), width, o.epsilon};
+    if (!gated && normQuantize_[i] >= 0) {
+      const auto &add = normAdd_[i] >= 0 ? op(normAdd_[i]) : o;
+      const auto &q = op(normQuantize_[i]);
+      if (normAdd_[i] >= 0) {
+        if (int rc = dense_all({{add.inputs[0], 0}, {add.inputs[1], 1}, {add.outputs[0], 2}}))
+          return rc;
+      } else if (int rc = dense(in[0], r[0])) {
+        return rc;
+      }
+      if (int rc = dense_all({{in[1], 3}, {q.outputs[0], 4}, {q.outputs[1], 5}}))
+        return rc;
+      Dispatch &d = emit(Launch::AddNormQuantize,
+                         normAdd_[i] >= 0 ? "addRmsNormQuantize" : "rmsNormQuantize");
+      d.p.row = p;
+      for (int k = 0; k < 6; ++k)
+        d.buf[k] = r[k];
+      d.buf[6] = {Space::Invalid, 0, 0};
+      if (normAdd_[i] >= 0)
+        d.ops.push_back((size_t)normAdd_[i]);
+      d.ops.push_back(i);
+      d.ops.push_back((size_t)normQuantize_[i]);
+      return LLMI_HIP_OK;
+    }
     if (!gated) {
       if (int rc = dense_all({{in[0], 0}, {in[1], 1}, {out[0], 2}}))
         return rc;
@@ -731,6 +793,7 @@ int Lowering::run() {
     return fail(LLMI_HIP_INVALID_ARGUMENT, "plan: expects one logits output");
   prepare_values();
   prepare_fusions();
+  prepare_norm_quantize();
   if (g_.output_count) {
     const uint32_t id = g_.outputs[0];
     const auto &v = value(id);
@@ -748,22 +811,34 @@ int Lowering::run() {
     if (f.deferred())
       continue; // runs at its consumer, into the consumer's output
     const auto &o = op(index_);
-    for (uint32_t j = 0; j < o.output_count; ++j) {
-      const uint32_t id = o.outputs[j];
-      const auto &v = value(id);
-      if (v.kind == LLMI_GRAPH_VIEW || buffer_[id].space != Space::None)
-        continue;
-      const uint64_t bytes = f.kind == LLMI_LINEAR_SILU_F32 ? 4 : element_bytes(v.element);
-      buffer_[id] = {Space::Scratch, 0, arena_.allocate(v.shape[0] * v.strides[0] * bytes,
-                                                        lastUse_[id])};
-    }
+    auto allocate = [&](const llmi_graph_op &of, bool f32) {
+      for (uint32_t j = 0; j < of.output_count; ++j) {
+        const uint32_t id = of.outputs[j];
+        const auto &v = value(id);
+        if (v.kind == LLMI_GRAPH_VIEW || buffer_[id].space != Space::None)
+          continue;
+        const uint64_t bytes = f32 ? 4 : element_bytes(v.element);
+        buffer_[id] = {Space::Scratch, 0, arena_.allocate(v.shape[0] * v.strides[0] * bytes,
+                                                          lastUse_[id])};
+      }
+    };
+    if (normQuantize_[index_] >= 0)
+      allocate(op(normQuantize_[index_]), false); // the norm itself stores nothing
+    else
+      allocate(o, f.kind == LLMI_LINEAR_SILU_F32);
+    if (skip_[index_])
+      continue;
     if (int rc = lower(index_))
       return rc;
   }
   plan_.scratchBytes = (arena_.size() + kAlign - 1) / kAlign * kAlign;
   for (const auto &d : plan_.dispatches)
-    for (const char *k : d.kernels)
-      plan_.records.push_back({d.opIndex, k, d.epilogue, d.fusedOpIndex});
+    for (const char *k : d.kernels) {
+      if (d.ops.empty())
+        plan_.records.push_back({d.opIndex, k, d.epilogue, d.fusedOpIndex});
+      for (size_t o : d.ops)
+        plan_.records.push_back({o, k, nullptr, 0});
+    }
   plan_.stateCount = g_.state_count;
   return LLMI_HIP_OK;
 }
@@ -865,6 +940,9 @@ int run_dispatch(const Dispatch &d, const Bases &b, hipStream_t stream) {
                                d.workspaceBytes, stream);
   case Launch::CopyView:
     return llmi_hip_copy_half_view(u16(0), u16(1), d.p.view, stream);
+  case Launch::AddNormQuantize:
+    return llmi_hip_add_rms_norm_quantize(u16(0), u16(1), u16(2), f32(3), (int8_t *)x[4],
+                                          f32(5), (uint32_t *)x[6], d.p.row, stream);
   }
   return fail(LLMI_HIP_INVALID_ARGUMENT, "plan: unknown dispatch");
 }

@@ -54,6 +54,41 @@ __device__ __forceinline__ float add_term(float acc, int dot, float a, float w) 
 
 // --------------------------------------------------------------- quantize
 
+// One 32-wide group (zeros past the row's end): scale = max|x| / 127 (1 for
+// an all-zero or non-finite group), q = x / scale clamped to +-127 and
+// rounded half to even (zeros for a non-finite group), written as 32 bytes
+// at dst (16-byte aligned). Returns the scale.
+__device__ __forceinline__ float quantize_group(const float *x, int8_t *dst, bool &finite) {
+  float max_abs = 0.0f;
+  finite = true;
+#pragma unroll
+  for (unsigned j = 0; j < kGroup; ++j) {
+    finite = finite && __builtin_isfinite(x[j]);
+    max_abs = fmaxf(max_abs, fabsf(x[j]));
+  }
+  const float scale = finite && max_abs > 0.0f ? __fdiv_rn(max_abs, 127.0f) : 1.0f;
+  uint4_t packed[2];
+#pragma unroll
+  for (unsigned j = 0; j < kGroup; j += 4) {
+    uint32_t word = 0;
+#pragma unroll
+    for (unsigned e = 0; e < 4; ++e) {
+      int r = 0;
+      if (finite) {
+        const float v = fminf(fmaxf(__fdiv_rn(x[j + e], scale), -127.0f), 127.0f);
+        r = (int)__builtin_rintf(v);
+      }
+      word |= ((uint32_t)r & 0xFFu) << (8 * e);
+    }
+    packed[j / 16][(j / 4) % 4] = word;
+  }
+  uint4_t *d = reinterpret_cast<uint4_t *>(dst);
+  d[0] = packed[0];
+  d[1] = packed[1];
+  return scale;
+}
+
+
 __global__ __launch_bounds__(256) void quantize_kernel(const uint16_t *__restrict__ in,
                                                        int8_t *__restrict__ q,
                                                        float *__restrict__ scales,
@@ -82,35 +117,72 @@ __global__ __launch_bounds__(256) void quantize_kernel(const uint16_t *__restric
     for (unsigned j = 0; j < kGroup; ++j)
       x[j] = j < length ? h2f(group[j]) : 0.0f;
   }
-  float max_abs = 0.0f;
-  bool finite = true;
-#pragma unroll
-  for (unsigned j = 0; j < kGroup; ++j) {
-    finite = finite && __builtin_isfinite(x[j]);
-    max_abs = fmaxf(max_abs, fabsf(x[j]));
-  }
+  bool finite;
+  scales[i] = quantize_group(x, q + (size_t)i * kGroup, finite);
   if (!finite && invalid)
     atomicOr(invalid, 1u);
-  const float scale = finite && max_abs > 0.0f ? __fdiv_rn(max_abs, 127.0f) : 1.0f;
-  scales[i] = scale;
-  uint4_t packed[2];
-#pragma unroll
-  for (unsigned j = 0; j < kGroup; j += 4) {
-    uint32_t word = 0;
-#pragma unroll
-    for (unsigned e = 0; e < 4; ++e) {
-      int r = 0;
-      if (finite) {
-        const float v = fminf(fmaxf(__fdiv_rn(x[j + e], scale), -127.0f), 127.0f);
-        r = (int)__builtin_rintf(v);
+}
+
+// residualAdd -> rmsNorm -> quantizeActivation of one row in one launch
+// (Reference.metal:105-126, Graph.metal:33-68): a workgroup per row. The
+// sum fp16(a + b) is written (it is the next residual) and staged in LDS as
+// fp32 with the row padded to whole groups by zeros; one lane runs the
+// norm's sequential fma sum; every thread then forms its groups' normalised
+// fp16 values and quantizes them with the standalone kernel's code. The
+// bits equal the three launches'. Without b the input row is normalised as
+// it is.
+template <bool kAdd>
+__global__ __launch_bounds__(256) void add_norm_quantize_kernel(
+    const uint16_t *__restrict__ a, const uint16_t *__restrict__ b, uint16_t *sum_out,
+    const float *__restrict__ w, int8_t *__restrict__ q, float *__restrict__ scales,
+    unsigned *invalid, unsigned width, unsigned groups, float eps) {
+  extern __shared__ __align__(16) float srow[];
+  __shared__ float sscale;
+  const unsigned row = blockIdx.x, t = threadIdx.x;
+  const size_t base = (size_t)row * width;
+  const unsigned padded = groups * kGroup;
+  for (unsigned i = t; i < padded; i += 256) {
+    float x = 0.0f;
+    if (i < width) {
+      uint16_t h = a[base + i];
+      if (kAdd) {
+        h = f2h(__fadd_rn(h2f(h), h2f(b[base + i])));
+        sum_out[base + i] = h;
       }
-      word |= ((uint32_t)r & 0xFFu) << (8 * e);
+      x = h2f(h);
     }
-    packed[j / 16][(j / 4) % 4] = word;
+    srow[i] = x;
   }
-  uint4_t *dst = reinterpret_cast<uint4_t *>(q + (size_t)i * kGroup);
-  dst[0] = packed[0];
-  dst[1] = packed[1];
+  __syncthreads();
+  if (t == 0) {
+    // fma(0, 0, sum) == sum for the padding (sum >= +0)
+    const float4 *v = reinterpret_cast<const float4 *>(srow);
+    float sum = 0.0f;
+#pragma unroll 8
+    for (unsigned c = 0; c < padded / 4; ++c) {
+      const float4 x4 = v[c];
+      sum = __builtin_fmaf(x4.x, x4.x, sum);
+      sum = __builtin_fmaf(x4.y, x4.y, sum);
+      sum = __builtin_fmaf(x4.z, x4.z, sum);
+      sum = __builtin_fmaf(x4.w, x4.w, sum);
+    }
+    sscale = rms_scale_of(sum, width, eps);
+  }
+  __syncthreads();
+  const float scale = sscale;
+  for (unsigned g = t; g < groups; g += 256) {
+    float y[kGroup];
+#pragma unroll
+    for (unsigned j = 0; j < kGroup; ++j) {
+      const unsigned i = g * kGroup + j;
+      y[j] = i < width ? normed_f(srow[i], scale, 1.0f + w[i]) : 0.0f;
+    }
+    bool finite;
+    scales[(size_t)row * groups + g] =
+        quantize_group(y, q + ((size_t)row * groups + g) * kGroup, finite);
+    if (!finite && invalid)
+      atomicOr(invalid, 1u);
+  }
 }
 
 // ------------------------------------------------------------------- GEMV
@@ -515,6 +587,20 @@ hipError_t launch_quantize_activation(const uint16_t *in, int8_t *q, float *scal
   const bool vec = width % kGroup == 0 && aligned16(in);
   hipLaunchKernelGGL(quantize_kernel, dim3((n + 255) / 256), dim3(256), 0, stream, in, q,
                      scales, invalid, rows, width, groups, vec);
+  return hipGetLastError();
+}
+
+hipError_t launch_add_norm_quantize(const uint16_t *a, const uint16_t *b, uint16_t *sum_out,
+                                   const float *w, int8_t *q, float *scales, unsigned *invalid,
+                                   unsigned rows, unsigned width, float eps, hipStream_t stream) {
+  const unsigned groups = (width + kGroup - 1) / kGroup;
+  const size_t lds = (size_t)groups * kGroup * sizeof(float);
+  if (b)
+    hipLaunchKernelGGL(add_norm_quantize_kernel<true>, dim3(rows), dim3(256), lds, stream, a, b,
+                       sum_out, w, q, scales, invalid, width, groups, eps);
+  else
+    hipLaunchKernelGGL(add_norm_quantize_kernel<false>, dim3(rows), dim3(256), lds, stream, a,
+                       b, sum_out, w, q, scales, invalid, width, groups, eps);
   return hipGetLastError();
 }
 

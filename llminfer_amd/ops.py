@@ -318,6 +318,39 @@ def linear_f16(*args, **kwargs) -> None:
     bind_linear_f16(*args, **kwargs)()
 
 
+def bind_add_rms_norm_quantize(a: torch.Tensor, b: torch.Tensor | None,
+                               sum_out: torch.Tensor | None, weight: torch.Tensor,
+                               q: torch.Tensor, scales: torch.Tensor,
+                               invalid: torch.Tensor | None = None,
+                               epsilon: float = 1e-6) -> "Bound":
+    """residualAdd -> rmsNorm -> quantizeActivation in one launch: a, b,
+    sum_out [rows, width] fp16 (b None: normalise a); weight [width] fp32;
+    q [rows, groups * 32] int8, scales [rows, groups] fp32."""
+    _require(a, torch.float16, "a")
+    if b is not None:
+        _require(b, torch.float16, "b")
+        _require(sum_out, torch.float16, "sum_out")
+    _require(weight, torch.float32, "weight")
+    _require(q, torch.int8, "q")
+    _require(scales, torch.float32, "scales")
+    rows, width = a.shape
+    groups = (width + 31) // 32
+    if (b is not None and (b.shape != a.shape or sum_out.shape != a.shape)) or \
+            weight.numel() != width or tuple(q.shape) != (rows, groups * 32) or \
+            tuple(scales.shape) != (rows, groups):
+        raise ValueError("a, b, sum_out [rows, width], weight [width], q, scales disagree")
+    if invalid is not None:
+        _require(invalid, torch.int32, "invalid")
+    p = _lib.RowParams(rows, width, epsilon)
+    return Bound(_lib.load().llmi_hip_add_rms_norm_quantize,
+                 (_ptr(a), _ptr(b), _ptr(sum_out), _ptr(weight), _ptr(q), _ptr(scales),
+                  _ptr(invalid), p, _stream()), "addRmsNormQuantize")
+
+
+def add_rms_norm_quantize(*args, **kwargs) -> None:
+    bind_add_rms_norm_quantize(*args, **kwargs)()
+
+
 def bind_causal_conv(x: torch.Tensor, weight: torch.Tensor, history: torch.Tensor | None,
                      out: torch.Tensor, silu: bool = True) -> "Bound":
     """causalConv (Reference.metal:137-161): x, out [T, C] fp16; weight [C, k]

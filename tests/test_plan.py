@@ -86,10 +86,21 @@ def test_lowering_matches_the_reference_predicates(w8):
 
 def test_qwen35_4b_lowers_with_the_hot_kernels():
     c = G.qwen35_4b()
-    _, decode = _lower(c, 1, 4096, 8192, "last", True)
+    g, decode = _lower(c, 1, 4096, 8192, "last", True)
     kinds = Counter(d["kernel"] for d in decode.dispatches)
     assert kinds["linearW8A8Gemv"] == 24 * 5 + 8 * 4 + 32 * 3 + 1
     assert kinds["gqaDecodeSplitK"] == 8 and kinds["deltaRecurrent"] == 24
+    # every hidden-width norm and its quantization in one launch, with the
+    # residual Add before it (all but the first layer's), each op recorded
+    # (launches: the first layer's input norm alone, 63 later norms and the
+    # final one with their Add; two or three records each)
+    assert kinds["rmsNormQuantize"] == 2 and kinds["addRmsNormQuantize"] == 64 * 3
+    assert kinds["residualAdd"] == 0
+    assert "quantizeActivation" in kinds     # the others (after GQA / gated norms, SwiGLU)
+    indices = [d["op_index"] for d in decode.dispatches]
+    assert indices == sorted(indices)
+    assert set(indices) | {d["fused_op_index"] for d in decode.dispatches if "epilogue" in d} \
+        == {i for i, op in enumerate(g.ops) if op.kind not in (G.OpKind.RESHAPE, G.OpKind.SLICE)}
     _, prefill = _lower(c, 512, 0, 8192, "last", True)
     kinds = Counter(d["kernel"] for d in prefill.dispatches)
     assert kinds["gqaPrefillMfma"] == 8

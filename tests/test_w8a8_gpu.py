@@ -198,3 +198,43 @@ def test_quantize_then_project_decode_step(gpu):
     act_ref = oracle.linear_w8a8(xq, xs, wg, sg, oracle.LINEAR_SILU_MUL, 0, up_ref)
     assert np.array_equal(_host_u16(up), up_ref)
     assert np.array_equal(_host_u16(act), act_ref)
+
+
+@pytest.mark.parametrize("rows,width,add", [(1, 2560, True), (37, 2560, True), (5, 4100, False),
+                                            (3, 33, True), (512, 2560, True), (2, 96, False)])
+def test_add_rms_norm_quantize_is_the_three_ops(gpu, rows, width, add):
+    """residualAdd -> rmsNorm -> quantizeActivation in one launch equals the
+    three launches bit for bit: the sum, the int8 rows, the scales and the
+    invalid flag."""
+    print(f"addRmsNormQuantize rows={rows} width={width} add={add}", flush=True)
+    r = np.random.default_rng(rows + width)
+    a = _f16(r.standard_normal((rows, width)) * 3)
+    b = _f16(r.standard_normal((rows, width)) * 3)
+    if rows > 2:
+        a[2, 5] = 0x7C00                      # inf: its row's groups flag invalid
+    w = (r.standard_normal(width) * 0.2).astype(np.float32)
+    groups = (width + 31) // 32
+    da, db, dw = _u16_dev(a, gpu), _u16_dev(b, gpu), _dev(w, gpu)
+    # three launches
+    s3 = torch.empty(rows, width, dtype=torch.float16, device=gpu)
+    n3 = torch.empty_like(s3)
+    q3 = torch.empty(rows, groups * 32, dtype=torch.int8, device=gpu)
+    c3 = torch.empty(rows, groups, dtype=torch.float32, device=gpu)
+    i3 = torch.zeros(1, dtype=torch.int32, device=gpu)
+    src = s3 if add else da
+    if add:
+        ops.elementwise("add", da, db, s3)
+    ops.rms_norm(src, dw, n3)
+    ops.quantize_activation(n3, q3, c3, i3)
+    # one launch
+    s1 = torch.empty_like(s3)
+    q1 = torch.empty_like(q3)
+    c1 = torch.empty_like(c3)
+    i1 = torch.zeros(1, dtype=torch.int32, device=gpu)
+    ops.add_rms_norm_quantize(da, db if add else None, s1 if add else None, dw, q1, c1, i1)
+    torch.cuda.synchronize()
+    if add:
+        assert np.array_equal(_host_u16(s1), _host_u16(s3))
+    assert torch.equal(q1, q3)
+    assert np.array_equal(c1.cpu().numpy().view(np.uint32), c3.cpu().numpy().view(np.uint32))
+    assert int(i1.item()) == int(i3.item())
