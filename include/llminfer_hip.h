@@ -501,7 +501,7 @@ LLMI_HIP_API int llmi_hip_linear_f16(const uint16_t *input, const uint16_t *weig
  * written to sum_out, then exactly llmi_hip_rms_norm of sum and
  * llmi_hip_quantize_activation of that into q [rows][groups * 32] (16-byte
  * aligned), scales [rows][groups] and *invalid (may be NULL). b == NULL
- * normalises a itself (sum_out unused). width <= 16384. */
+ * normalises a itself (sum_out unused). width <= 8192. */
 LLMI_HIP_API int llmi_hip_add_rms_norm_quantize(const uint16_t *a, const uint16_t *b,
                                                 uint16_t *sum_out, const float *weight,
                                                 int8_t *q, float *scales, uint32_t *invalid,

@@ -202,7 +202,7 @@ hipError_t launch_embedding(const uint32_t *ids, const uint16_t *w, uint16_t *ou
 
 // residualAdd -> rmsNorm -> quantizeActivation in one launch, a workgroup
 // per row of up to kAddNormQuantizeMax halves (w8a8.hip); b null: no add.
-constexpr unsigned kAddNormQuantizeMax = 16384;
+constexpr unsigned kAddNormQuantizeMax = 8192;
 hipError_t launch_add_norm_quantize(const uint16_t *a, const uint16_t *b, uint16_t *sum_out,
                                    const float *w, int8_t *q, float *scales, unsigned *invalid,
                                    unsigned rows, unsigned width, float eps, hipStream_t stream);

@@ -126,23 +126,24 @@ __global__ __launch_bounds__(256) void quantize_kernel(const uint16_t *__restric
 // residualAdd -> rmsNorm -> quantizeActivation of one row in one launch
 // (Reference.metal:105-126, Graph.metal:33-68): a workgroup per row. The
 // sum fp16(a + b) is written (it is the next residual) and staged in LDS as
-// fp32 with the row padded to whole groups by zeros; one lane runs the
-// norm's sequential fma sum; every thread then forms its groups' normalised
-// fp16 values and quantizes them with the standalone kernel's code. The
-// bits equal the three launches'. Without b the input row is normalised as
+// fp32 with the row padded to whole groups by zeros, next to 1 + w; one
+// lane runs the norm's sequential fma sum; eight lanes per group then form
+// the normalised fp16 values and quantize them with the standalone
+// kernel's expressions. The bits equal the three launches'. Without b the input row is normalised as
 // it is.
 template <bool kAdd>
 __global__ __launch_bounds__(256) void add_norm_quantize_kernel(
     const uint16_t *__restrict__ a, const uint16_t *__restrict__ b, uint16_t *sum_out,
     const float *__restrict__ w, int8_t *__restrict__ q, float *__restrict__ scales,
     unsigned *invalid, unsigned width, unsigned groups, float eps) {
-  extern __shared__ __align__(16) float srow[];
+  extern __shared__ __align__(16) float srow[]; // the row, then 1 + w, padded
   __shared__ float sscale;
   const unsigned row = blockIdx.x, t = threadIdx.x;
   const size_t base = (size_t)row * width;
   const unsigned padded = groups * kGroup;
+  float *sw = srow + padded;
   for (unsigned i = t; i < padded; i += 256) {
-    float x = 0.0f;
+    float x = 0.0f, w1 = 1.0f;
     if (i < width) {
       uint16_t h = a[base + i];
       if (kAdd) {
@@ -150,8 +151,10 @@ __global__ __launch_bounds__(256) void add_norm_quantize_kernel(
         sum_out[base + i] = h;
       }
       x = h2f(h);
+      w1 = 1.0f + w[i];
     }
     srow[i] = x;
+    sw[i] = w1;
   }
   __syncthreads();
   if (t == 0) {
@@ -169,19 +172,49 @@ __global__ __launch_bounds__(256) void add_norm_quantize_kernel(
     sscale = rms_scale_of(sum, width, eps);
   }
   __syncthreads();
+  // Eight lanes a group, four elements a lane: the group's max |y| and
+  // finiteness by lane swaps (exact in any order), then each lane
+  // quantizes its four with the standalone kernel's expressions.
   const float scale = sscale;
-  for (unsigned g = t; g < groups; g += 256) {
-    float y[kGroup];
+  const unsigned sub = t % 8;
+  for (unsigned g0 = 0; g0 < groups; g0 += 32) {
+    const unsigned g = g0 + t / 8;
+    const bool live = g < groups;
+    const unsigned i0 = (live ? g : 0) * kGroup + 4 * sub;
+    float y[4];
+    float max_abs = 0.0f;
+    bool finite = true;
 #pragma unroll
-    for (unsigned j = 0; j < kGroup; ++j) {
-      const unsigned i = g * kGroup + j;
-      y[j] = i < width ? normed_f(srow[i], scale, 1.0f + w[i]) : 0.0f;
+    for (int e = 0; e < 4; ++e) {
+      const unsigned i = i0 + e;
+      y[e] = i < width ? normed_f(srow[i], scale, sw[i]) : 0.0f;
+      finite = finite && __builtin_isfinite(y[e]);
+      max_abs = fmaxf(max_abs, fabsf(y[e]));
     }
-    bool finite;
-    scales[(size_t)row * groups + g] =
-        quantize_group(y, q + ((size_t)row * groups + g) * kGroup, finite);
-    if (!finite && invalid)
-      atomicOr(invalid, 1u);
+#pragma unroll
+    for (int m = 1; m < 8; m *= 2) {
+      max_abs = fmaxf(max_abs, __shfl_xor(max_abs, m, 8));
+      finite = __shfl_xor((int)finite, m, 8) && finite;
+    }
+    if (!live)
+      continue;
+    const float qs = finite && max_abs > 0.0f ? __fdiv_rn(max_abs, 127.0f) : 1.0f;
+    uint32_t word = 0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      int r = 0;
+      if (finite) {
+        const float v = fminf(fmaxf(__fdiv_rn(y[e], qs), -127.0f), 127.0f);
+        r = (int)__builtin_rintf(v);
+      }
+      word |= ((uint32_t)r & 0xFFu) << (8 * e);
+    }
+    reinterpret_cast<uint32_t *>(q + ((size_t)row * groups + g) * kGroup)[sub] = word;
+    if (sub == 0) {
+      scales[(size_t)row * groups + g] = qs;
+      if (!finite && invalid)
+        atomicOr(invalid, 1u);
+    }
   }
 }
 
@@ -594,7 +627,7 @@ hipError_t launch_add_norm_quantize(const uint16_t *a, const uint16_t *b, uint16
                                    const float *w, int8_t *q, float *scales, unsigned *invalid,
                                    unsigned rows, unsigned width, float eps, hipStream_t stream) {
   const unsigned groups = (width + kGroup - 1) / kGroup;
-  const size_t lds = (size_t)groups * kGroup * sizeof(float);
+  const size_t lds = 2 * (size_t)groups * kGroup * sizeof(float);
   if (b)
     hipLaunchKernelGGL(add_norm_quantize_kernel<true>, dim3(rows), dim3(256), lds, stream, a, b,
                        sum_out, w, q, scales, invalid, width, groups, eps);
