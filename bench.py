@@ -694,7 +694,7 @@ class Qwen35Model(Workload):
         self.session.run(self.plans[i % len(self.plans)], self.ids, self.logits)
 
     def kernels(self):
-        return f"whole-graph plan ({len(self.plans[0].dispatches)} launches a step)"
+        return f"whole-graph plan ({self.plans[0].launches} launches a step)"
 
     def weight_bytes(self):
         from llminfer_amd.graph import EMBEDDING_ID, Element, qwen35_tensors
@@ -734,7 +734,8 @@ class Qwen35Model(Workload):
         return {"workload": self.name, "model": "Qwen3.5-4B (random weights of its shapes)",
                 "precision": "W8A8", "tokens": self.T, "past": self.P,
                 "layers": len(c.layers), "vocabulary": c.vocabulary,
-                "launches_per_step": len(self.plans[0].dispatches),
+                "launches_per_step": self.plans[0].launches,
+                "records_per_step": len(self.plans[0].dispatches),
                 "scratch_bytes": self.plans[0].scratch_bytes,
                 "reference_m2_tok_s": 9.82 if self.decode else 20.81}
 

@@ -171,7 +171,8 @@ enum llmi_hip_op {
   LLMI_HIP_OP_MULTIPLY = 20,            /* params: ElementParams */
   LLMI_HIP_OP_COPY_HALF_VIEW = 21,      /* params: HalfViewParams */
   LLMI_HIP_OP_LINEAR_F16 = 22,          /* params: LinearParams */
-  LLMI_HIP_OP_ADD_RMS_NORM_QUANTIZE = 23 /* params: RowParams */
+  LLMI_HIP_OP_ADD_RMS_NORM_QUANTIZE = 23, /* params: RowParams */
+  LLMI_HIP_OP_ADD_RMS_NORM_LINEAR_W8A8 = 24 /* params: NormLinearParams */
 };
 
 /* ---------------------------------------------------------------- KvAppend
@@ -507,6 +508,41 @@ LLMI_HIP_API int llmi_hip_add_rms_norm_quantize(const uint16_t *a, const uint16_
                                                 int8_t *q, float *scales, uint32_t *invalid,
                                                 RowParams p, void *stream);
 
+/* The buffers of one projection of llmi_hip_add_rms_norm_linear_w8a8: those
+ * of an llmi_hip_linear_w8a8 call on the norm's quantized row. */
+typedef struct llmi_hip_norm_projection {
+  const int8_t *weight;          /* [columns][groups * 32], 16-byte aligned */
+  const uint16_t *weight_scales; /* [columns][groups] fp16 */
+  void *output;
+  const void *aux;
+  const float *bias;
+} llmi_hip_norm_projection;
+
+#define LLMI_HIP_NORM_LINEAR_MAX 4
+
+typedef struct NormLinearParams {
+  RowParams norm;   /* rows == 1, width <= 4096 */
+  unsigned count;   /* projections, 1 .. LLMI_HIP_NORM_LINEAR_MAX */
+  LinearW8Params linear[LLMI_HIP_NORM_LINEAR_MAX]; /* rows == 1, groups = ceil(width / 32) */
+} NormLinearParams;
+
+/* llmi_hip_add_rms_norm_quantize of one row followed by llmi_hip_linear_w8a8
+ * of each projection on the quantized row, in one launch (no counterpart in
+ * the reference, which launches them one by one; the plan uses it for a
+ * decode step's input norm and the projections that read its quantization).
+ * The outputs are the separate calls' bits. q and scales may be NULL (not
+ * written) when nothing else reads them. Epilogues as for
+ * llmi_hip_linear_w8a8, except that a LLMI_LINEAR_SILU_MUL multiplier
+ * (aux) must not be an output of the same call. At most 4096 workgroups of
+ * 60 columns in all (one per CU runs best: 256 on MI355X). No output may
+ * overlap a, b, sum_out, q, scales or another output: the projections run
+ * concurrently with the norm of other workgroups. */
+LLMI_HIP_API int llmi_hip_add_rms_norm_linear_w8a8(const uint16_t *a, const uint16_t *b,
+                                                   uint16_t *sum_out, const float *weight,
+                                                   int8_t *q, float *scales, uint32_t *invalid,
+                                                   const llmi_hip_norm_projection *projections,
+                                                   NormLinearParams p, void *stream);
+
 /* ----------------------------------------------------------------- helpers */
 
 /* Zero a workspace (enqueued on `stream`). No kernel of this library needs
@@ -722,6 +758,11 @@ LLMI_HIP_API void llmi_hip_plan_logits(const llmi_hip_plan *plan, uint64_t *rows
  * fused_op_index is then 0. */
 LLMI_HIP_API size_t llmi_hip_plan_dispatches(const llmi_hip_plan *plan,
                                              llmi_hip_dispatch *records, size_t cap);
+
+/* The kernel launches one llmi_hip_plan_execute issues (no counterpart in
+ * the reference: a launch that serves several ops has a record for each, so
+ * records outnumber launches). */
+LLMI_HIP_API size_t llmi_hip_plan_launches(const llmi_hip_plan *plan);
 
 /* Runs the plan on `stream`: scratch (device, llmi_hip_plan_scratch_bytes),
  * states[i] the device buffer of graph state i (its shape, dense),

@@ -42,6 +42,8 @@ OP_MULTIPLY = 20
 OP_COPY_HALF_VIEW = 21
 OP_LINEAR_F16 = 22
 OP_ADD_RMS_NORM_QUANTIZE = 23
+OP_ADD_RMS_NORM_LINEAR_W8A8 = 24
+NORM_LINEAR_MAX = 4  # LLMI_HIP_NORM_LINEAR_MAX
 
 # LinearEpilogue (ReferenceParams.h:8-16)
 LINEAR_NONE, LINEAR_SILU, LINEAR_SILU_MUL, LINEAR_SIGMOID_COLUMNS = 0, 1, 2, 3
@@ -89,6 +91,16 @@ class QuantizeParams(C.Structure):
 class LinearW8Params(C.Structure):
     _fields_ = [(n, C.c_uint) for n in ("outputWidth", "firstRow", "groups", "rows", "columns",
                                         "epilogue", "epilogueBlock")]
+
+
+class NormProjection(C.Structure):
+    _fields_ = [("weight", C.c_void_p), ("weight_scales", C.c_void_p), ("output", C.c_void_p),
+                ("aux", C.c_void_p), ("bias", C.c_void_p)]
+
+
+class NormLinearParams(C.Structure):
+    _fields_ = [("norm", RowParams), ("count", C.c_uint),
+                ("linear", LinearW8Params * NORM_LINEAR_MAX)]
 
 
 class GroupedEmbedParams(C.Structure):
@@ -183,6 +195,8 @@ SIGNATURES = {
     "llmi_hip_copy_half_view": (C.c_int, [_P, _P, HalfViewParams, _P]),
     "llmi_hip_linear_f16": (C.c_int, [_P, _P, _P, _P, _P, LinearParams, _P]),
     "llmi_hip_add_rms_norm_quantize": (C.c_int, [_P, _P, _P, _P, _P, _P, _P, RowParams, _P]),
+    "llmi_hip_add_rms_norm_linear_w8a8": (C.c_int, [_P, _P, _P, _P, _P, _P, _P, _P,
+                                                    NormLinearParams, _P]),
     "llmi_hip_workspace_init": (C.c_int, [_P, _SZ, _P]),
     "llmi_hip_dispatch_count": (C.c_uint, [C.c_int, _P]),
     "llmi_hip_kernel_name": (C.c_char_p, [C.c_int, _P, C.c_uint]),
@@ -208,6 +222,7 @@ SIGNATURES = {
     "llmi_hip_plan_scratch_bytes": (_SZ, [_P]),
     "llmi_hip_plan_logits": (None, [_P, _P, _P]),
     "llmi_hip_plan_dispatches": (_SZ, [_P, C.POINTER(Dispatch), _SZ]),
+    "llmi_hip_plan_launches": (_SZ, [_P]),
     "llmi_hip_plan_execute": (C.c_int, [_P, _P, _SZ, _P, _SZ, _P, _P, _P, _P]),
 }
 

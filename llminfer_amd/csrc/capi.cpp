@@ -389,6 +389,78 @@ int llmi_hip_add_rms_norm_quantize(const uint16_t *a, const uint16_t *b, uint16_
                   b ? "addRmsNormQuantize" : "rmsNormQuantize");
 }
 
+static int check_norm_linear(const NormLinearParams &p) {
+  const RowParams &n = p.norm;
+  if (n.rows != 1 || n.width == 0 || n.width > kNormLinearMaxWidth)
+    return fail(LLMI_HIP_UNSUPPORTED, "addRmsNormLinearW8A8: one row of at most %u (%u x %u)",
+                kNormLinearMaxWidth, n.rows, n.width);
+  if (p.count == 0 || p.count > kNormLinearMax)
+    return fail(LLMI_HIP_INVALID_ARGUMENT, "addRmsNormLinearW8A8: %u projections (1 to %u)",
+                p.count, kNormLinearMax);
+  const unsigned groups = (n.width + 31) / 32;
+  unsigned wgs = 0;
+  for (unsigned k = 0; k < p.count; ++k) {
+    const LinearW8Params &l = p.linear[k];
+    if (int rc = check_linear_w8(l))
+      return rc;
+    if (l.rows != 1 || l.groups != groups || l.columns == 0)
+      return fail(LLMI_HIP_INVALID_ARGUMENT,
+                  "addRmsNormLinearW8A8: projection %u takes %u rows of %u groups and %u "
+                  "columns (one row of %u groups, at least one column)",
+                  k, l.rows, l.groups, l.columns, groups);
+    wgs += norm_linear_workgroups(l.columns);
+  }
+  if (wgs > kNormLinearMaxWgs)
+    return fail(LLMI_HIP_UNSUPPORTED, "addRmsNormLinearW8A8: %u workgroups (at most %u)", wgs,
+                kNormLinearMaxWgs);
+  return LLMI_HIP_OK;
+}
+
+int llmi_hip_add_rms_norm_linear_w8a8(const uint16_t *a, const uint16_t *b, uint16_t *sum_out,
+                                      const float *weight, int8_t *q, float *scales,
+                                      uint32_t *invalid,
+                                      const llmi_hip_norm_projection *projections,
+                                      NormLinearParams p, void *stream) {
+  if (int rc = check_norm_linear(p))
+    return rc;
+  if (!a || !weight || !projections || (b && !sum_out))
+    return fail(LLMI_HIP_INVALID_ARGUMENT, "addRmsNormLinearW8A8: null buffer");
+  if (q && !aligned16(q))
+    return fail(LLMI_HIP_UNSUPPORTED, "addRmsNormLinearW8A8: quantized row not 16-byte aligned");
+  NormLinearProj proj[kNormLinearMax];
+  for (unsigned k = 0; k < p.count; ++k) {
+    const llmi_hip_norm_projection &x = projections[k];
+    const LinearW8Params &l = p.linear[k];
+    if (!x.weight || !x.weight_scales || !x.output)
+      return fail(LLMI_HIP_INVALID_ARGUMENT, "addRmsNormLinearW8A8: projection %u: null buffer",
+                  k);
+    if (!aligned16(x.weight))
+      return fail(LLMI_HIP_UNSUPPORTED,
+                  "addRmsNormLinearW8A8: projection %u: weight rows not 16-byte aligned", k);
+    if (l.epilogue == LLMI_LINEAR_SILU_MUL) {
+      if (!x.aux)
+        return fail(LLMI_HIP_INVALID_ARGUMENT,
+                    "addRmsNormLinearW8A8: projection %u: SiluMul needs its multiplier (aux)", k);
+      for (unsigned j = 0; j < p.count; ++j)
+        if (projections[j].output == x.aux)
+          return fail(LLMI_HIP_UNSUPPORTED,
+                      "addRmsNormLinearW8A8: projection %u: the SwiGLU multiplier is computed "
+                      "in the same call",
+                      k);
+    }
+    if (l.epilogue == LLMI_LINEAR_DELTA_DECAY && (!x.aux || !x.bias))
+      return fail(LLMI_HIP_INVALID_ARGUMENT,
+                  "addRmsNormLinearW8A8: projection %u: the decay needs A_log (aux) and bias", k);
+    proj[k] = {x.weight, x.weight_scales, x.output, x.aux, x.bias,
+               W8Shape{l.outputWidth, l.firstRow, l.groups, l.rows, l.columns, l.epilogue,
+                       l.epilogueBlock}};
+  }
+  return launched(launch_add_norm_linear(a, b, sum_out, weight, q, scales, invalid, p.norm.width,
+                                         p.norm.epsilon, proj, p.count,
+                                         static_cast<hipStream_t>(stream)),
+                  b ? "addRmsNormLinearW8A8" : "rmsNormLinearW8A8");
+}
+
 static int check_view(const HalfViewParams &p) {
   uint64_t last = p.offset;
   for (int d = 0; d < 3; ++d) {
@@ -847,6 +919,9 @@ unsigned llmi_hip_dispatch_count(int op, const void *params) {
     const RowParams &p = *static_cast<const RowParams *>(params);
     return p.rows && p.width && check_add_norm_quantize(p) == LLMI_HIP_OK ? 1 : 0;
   }
+  case LLMI_HIP_OP_ADD_RMS_NORM_LINEAR_W8A8:
+    return check_norm_linear(*static_cast<const NormLinearParams *>(params)) == LLMI_HIP_OK ? 1
+                                                                                          : 0;
   case LLMI_HIP_OP_LINEAR_F16: {
     const LinearParams &p = *static_cast<const LinearParams *>(params);
     return p.tokens && p.rowCount && check_linear_f16(p) == LLMI_HIP_OK ? 1 : 0;
@@ -955,6 +1030,8 @@ const char *llmi_hip_kernel_name(int op, const void *params, unsigned index) {
     return "linearF16";
   case LLMI_HIP_OP_ADD_RMS_NORM_QUANTIZE:
     return "addRmsNormQuantize";
+  case LLMI_HIP_OP_ADD_RMS_NORM_LINEAR_W8A8:
+    return "addRmsNormLinearW8A8";
   case LLMI_HIP_OP_GATED_RMS_NORM: {
     const unsigned width = static_cast<const RowParams *>(params)->width;
     return width % 8 == 0 && width <= 256 ? "gatedRmsNormTile" : "gatedRmsNormRows";

@@ -203,6 +203,26 @@ hipError_t launch_embedding(const uint32_t *ids, const uint16_t *w, uint16_t *ou
 // residualAdd -> rmsNorm -> quantizeActivation in one launch, a workgroup
 // per row of up to kAddNormQuantizeMax halves (w8a8.hip); b null: no add.
 constexpr unsigned kAddNormQuantizeMax = 8192;
+// The same row's norm and quantization followed by up to kNormLinearMax
+// W8A8 projections of it, rows == 1, width <= kNormLinearMaxWidth, one
+// workgroup per 60 columns of a projection (w8a8.hip).
+constexpr unsigned kNormLinearMax = LLMI_HIP_NORM_LINEAR_MAX, kNormLinearMaxWidth = 4096;
+constexpr unsigned kNormLinearCols = 60, kNormLinearMaxWgs = 4096;
+inline unsigned norm_linear_workgroups(unsigned columns) {
+  return (columns + kNormLinearCols - 1) / kNormLinearCols;
+}
+struct NormLinearProj {
+  const int8_t *w;
+  const uint16_t *ws;
+  void *out;
+  const void *aux;
+  const float *bias;
+  W8Shape shape;
+};
+hipError_t launch_add_norm_linear(const uint16_t *a, const uint16_t *b, uint16_t *sum_out,
+                                  const float *w, int8_t *q, float *scales, unsigned *invalid,
+                                  unsigned width, float eps, const NormLinearProj *proj,
+                                  unsigned count, hipStream_t stream);
 hipError_t launch_add_norm_quantize(const uint16_t *a, const uint16_t *b, uint16_t *sum_out,
                                    const float *w, int8_t *q, float *scales, unsigned *invalid,
                                    unsigned rows, unsigned width, float eps, hipStream_t stream);

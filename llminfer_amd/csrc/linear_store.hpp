@@ -10,6 +10,12 @@
 
 namespace llmi {
 
+// The SwiGLU epilogue's value: SiLU of the rounded projection times the
+// fp16 multiplier.
+__device__ __forceinline__ uint16_t silu_mul16(float projected, uint16_t multiplier) {
+  return f2h(mul32(h2f(silu16(projected)), h2f(multiplier)));
+}
+
 __device__ __forceinline__ void store_linear(void *out, const void *aux, const float *bias,
                                              size_t i, unsigned col, unsigned epilogue,
                                              unsigned block, float acc) {
@@ -21,7 +27,7 @@ __device__ __forceinline__ void store_linear(void *out, const void *aux, const f
     o16[i] = silu16(projected);
     return;
   case LLMI_LINEAR_SILU_MUL:
-    o16[i] = f2h(mul32(h2f(silu16(projected)), h2f(static_cast<const uint16_t *>(aux)[i])));
+    o16[i] = silu_mul16(projected, static_cast<const uint16_t *>(aux)[i]);
     return;
   case LLMI_LINEAR_SIGMOID_COLUMNS:
     o16[i] = f2h((col / block) % 2 ? logistic16(projected) : projected);

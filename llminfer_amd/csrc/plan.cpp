@@ -40,7 +40,14 @@ struct Ref {
 enum class Launch : uint8_t {
   Embedding, EmbeddingW8, Quantize, LinearW8, LinearF16, RmsNorm, GatedRmsNorm,
   GatedRmsNormActivated, L2Norm, Elementwise, SigmoidMul, PartialRope, CausalConv, DeltaGates,
-  DeltaUpdate, KvAppend, CausalGqa, CopyView, AddNormQuantize
+  DeltaUpdate, KvAppend, CausalGqa, CopyView, AddNormQuantize, AddNormLinear
+};
+
+// One plan record of a launch that serves several ops.
+struct Rec {
+  size_t op;
+  const char *epilogue;
+  size_t fused;
 };
 
 struct Dispatch {
@@ -63,11 +70,14 @@ struct Dispatch {
     CacheParams cache;
     GqaParams gqa;
     HalfViewParams view;
+    NormLinearParams normLinear;
   } p;
   size_t opIndex = 0, fusedOpIndex = 0;
   const char *epilogue = nullptr;
   std::vector<const char *> kernels;
   std::vector<size_t> ops; // a launch serving several ops: a record for each
+  std::vector<Rec> recs;   // ... with their epilogues (replaces ops when set)
+  Ref proj[kNormLinearMax][5]; // AddNormLinear: weight, scales, output, aux, bias
 };
 
 struct Fusion {
@@ -221,6 +231,7 @@ private:
   void prepare_values();
   void prepare_fusions();
   void prepare_norm_quantize();
+  void merge_norm_linears();
   int lower(size_t index);
   int dense(uint32_t id, Ref &out);
   int linear(size_t producer, uint32_t result, int64_t aux, int64_t bias);
@@ -449,16 +460,114 @@ void Lowering::prepare_norm_quantize() {
       continue;
     normQuantize_[j] = (int64_t)j + 1;
     skip_[j + 1] = 1;
+    // One row (decode): the projections of the quantized row may join the
+    // launch (merge_norm_linears), reading nothing the norm reads is
+    // overwritten while they run: its inputs stay live as long as the
+    // quantized row.
+    const bool oneRow = count(h) == dim(o.inputs[1], 0);
+    const size_t until = oneRow ? std::max({j, lastUse_[root_[k.outputs[0]]],
+                                            lastUse_[root_[k.outputs[1]]]})
+                                : j;
     if (j > 0 && op(j - 1).kind == LLMI_GRAPH_ADD && op(j - 1).outputs[0] == h &&
         value(h).kind == LLMI_GRAPH_RESULT) {
       normAdd_[j] = (int64_t)j - 1;
       skip_[j - 1] = 1;
       for (uint32_t x = 0; x < op(j - 1).input_count; ++x) {
         const size_t r = root_[op(j - 1).inputs[x]];
-        lastUse_[r] = std::max(lastUse_[r], j);
+        lastUse_[r] = std::max(lastUse_[r], until);
       }
+    } else {
+      lastUse_[root_[h]] = std::max(lastUse_[root_[h]], until);
     }
   }
+}
+
+// A one-row norm + quantization launch and the W8A8 projections right after
+// it that read its quantized row, merged into one launch
+// (llmi_hip_add_rms_norm_linear_w8a8) whose weight stream runs under the
+// norm's chain: at most kNormLinearMax projections, one round of
+// workgroups (one a CU), no SwiGLU projection (its multiplier would be
+// computed in the same launch), not the logits head, and no output
+// overlapping what the launch reads or another output. Every op keeps its
+// record.
+void Lowering::merge_norm_linears() {
+  constexpr unsigned kOneRound = 256;
+  auto &ds = plan_.dispatches;
+  struct Range {
+    Ref r;
+    uint64_t bytes;
+  };
+  auto overlap = [](const Range &a, const Range &b) {
+    return a.r.space == b.r.space && a.r.index == b.r.index && a.r.space != Space::None &&
+           a.r.offset < b.r.offset + b.bytes && b.r.offset < a.r.offset + a.bytes;
+  };
+  std::vector<Dispatch> out;
+  out.reserve(ds.size());
+  for (size_t i = 0; i < ds.size(); ++i) {
+    const Dispatch &d = ds[i];
+    const RowParams &row = d.p.row;
+    if (d.launch != Launch::AddNormQuantize || row.rows != 1 || row.width > kNormLinearMaxWidth) {
+      out.push_back(d);
+      continue;
+    }
+    const unsigned groups = (row.width + 31) / 32;
+    std::vector<Range> reads = {{d.buf[0], 2ull * row.width}, {d.buf[1], 2ull * row.width},
+                                {d.buf[2], 2ull * row.width}, {d.buf[4], 32ull * groups},
+                                {d.buf[5], 4ull * groups}};
+    NormLinearParams np{};
+    np.norm = row;
+    unsigned wgs = 0;
+    size_t j = i + 1;
+    for (; j < ds.size() && np.count < kNormLinearMax; ++j) {
+      const Dispatch &l = ds[j];
+      const LinearW8Params &lp = l.p.linearW8;
+      if (l.launch != Launch::LinearW8 || l.buf[0].space != d.buf[4].space ||
+          l.buf[0].offset != d.buf[4].offset || l.buf[1].offset != d.buf[5].offset ||
+          l.buf[1].space != d.buf[5].space || lp.rows != 1 || lp.groups != groups ||
+          lp.epilogue == LLMI_LINEAR_SILU_MUL || l.buf[4].space == Space::Output ||
+          wgs + norm_linear_workgroups(lp.columns) > kOneRound)
+        break; // the logits head keeps its own GEMV launch and record
+      const bool f32 = lp.epilogue == LLMI_LINEAR_SILU_F32 ||
+                       lp.epilogue == LLMI_LINEAR_DELTA_BETA ||
+                       lp.epilogue == LLMI_LINEAR_DELTA_DECAY;
+      const Range o{l.buf[4], (uint64_t)lp.outputWidth * (f32 ? 4 : 2)};
+      bool clash = false;
+      for (const Range &r : reads)
+        clash = clash || overlap(o, r);
+      if (clash)
+        break;
+      reads.push_back(o);
+      np.linear[np.count] = lp;
+      ++np.count;
+      wgs += norm_linear_workgroups(lp.columns);
+    }
+    if (np.count == 0 || llmi_hip_dispatch_count(LLMI_HIP_OP_ADD_RMS_NORM_LINEAR_W8A8, &np) == 0) {
+      out.push_back(d);
+      continue;
+    }
+    Dispatch m;
+    m.launch = Launch::AddNormLinear;
+    for (int k = 0; k < 7; ++k)
+      m.buf[k] = d.buf[k];
+    m.p.normLinear = np;
+    m.opIndex = d.opIndex;
+    m.kernels.push_back(d.buf[1].space != Space::None ? "addRmsNormLinearW8A8"
+                                                      : "rmsNormLinearW8A8");
+    for (size_t o : d.ops)
+      m.recs.push_back({o, nullptr, 0});
+    for (unsigned k = 0; k < np.count; ++k) {
+      const Dispatch &l = ds[i + 1 + k];
+      m.recs.push_back({l.opIndex, l.epilogue, l.fusedOpIndex});
+      m.proj[k][0] = l.buf[2];
+      m.proj[k][1] = l.buf[3];
+      m.proj[k][2] = l.buf[4];
+      m.proj[k][3] = l.buf[5];
+      m.proj[k][4] = l.buf[6];
+    }
+    out.push_back(std::move(m));
+    i += np.count;
+  }
+  ds.swap(out);
 }
 
 // The address of a value's elements, materialising a non-contiguous fp16
@@ -832,8 +941,14 @@ int Lowering::run() {
       return rc;
   }
   plan_.scratchBytes = (arena_.size() + kAlign - 1) / kAlign * kAlign;
+  merge_norm_linears();
   for (const auto &d : plan_.dispatches)
     for (const char *k : d.kernels) {
+      if (!d.recs.empty()) {
+        for (const Rec &r : d.recs)
+          plan_.records.push_back({r.op, k, r.epilogue, r.fused});
+        continue;
+      }
       if (d.ops.empty())
         plan_.records.push_back({d.opIndex, k, d.epilogue, d.fusedOpIndex});
       for (size_t o : d.ops)
@@ -943,6 +1058,17 @@ int run_dispatch(const Dispatch &d, const Bases &b, hipStream_t stream) {
   case Launch::AddNormQuantize:
     return llmi_hip_add_rms_norm_quantize(u16(0), u16(1), u16(2), f32(3), (int8_t *)x[4],
                                           f32(5), (uint32_t *)x[6], d.p.row, stream);
+  case Launch::AddNormLinear: {
+    llmi_hip_norm_projection proj[kNormLinearMax] = {};
+    for (unsigned k = 0; k < d.p.normLinear.count; ++k)
+      proj[k] = {static_cast<const int8_t *>(resolve(b, d.proj[k][0])),
+                 static_cast<const uint16_t *>(resolve(b, d.proj[k][1])),
+                 resolve(b, d.proj[k][2]), resolve(b, d.proj[k][3]),
+                 static_cast<const float *>(resolve(b, d.proj[k][4]))};
+    return llmi_hip_add_rms_norm_linear_w8a8(u16(0), u16(1), u16(2), f32(3), (int8_t *)x[4],
+                                             f32(5), (uint32_t *)x[6], proj, d.p.normLinear,
+                                             stream);
+  }
   }
   return fail(LLMI_HIP_INVALID_ARGUMENT, "plan: unknown dispatch");
 }
@@ -991,6 +1117,14 @@ size_t llmi_hip_plan_dispatches(const llmi_hip_plan *plan, llmi_hip_dispatch *re
     std::memcpy(records, plan->records.data(),
                 sizeof(llmi_hip_dispatch) * std::min(cap, plan->records.size()));
   return plan->records.size();
+}
+
+size_t llmi_hip_plan_launches(const llmi_hip_plan *plan) {
+  size_t n = 0;
+  if (plan)
+    for (const auto &d : plan->dispatches)
+      n += d.kernels.size();
+  return n;
 }
 
 int llmi_hip_plan_execute(const llmi_hip_plan *plan, void *scratch, size_t scratch_bytes,

@@ -123,61 +123,81 @@ __global__ __launch_bounds__(256) void quantize_kernel(const uint16_t *__restric
     atomicOr(invalid, 1u);
 }
 
-// residualAdd -> rmsNorm -> quantizeActivation of one row in one launch
-// (Reference.metal:105-126, Graph.metal:33-68): a workgroup per row. The
-// sum fp16(a + b) is written (it is the next residual) and staged in LDS as
-// fp32 with the row padded to whole groups by zeros, next to 1 + w; one
-// lane runs the norm's sequential fma sum; eight lanes per group then form
-// the normalised fp16 values and quantize them with the standalone
-// kernel's expressions. The bits equal the three launches'. Without b the input row is normalised as
-// it is.
-template <bool kAdd>
-__global__ __launch_bounds__(256) void add_norm_quantize_kernel(
-    const uint16_t *__restrict__ a, const uint16_t *__restrict__ b, uint16_t *sum_out,
-    const float *__restrict__ w, int8_t *__restrict__ q, float *__restrict__ scales,
-    unsigned *invalid, unsigned width, unsigned groups, float eps) {
-  extern __shared__ __align__(16) float srow[]; // the row, then 1 + w, padded
-  __shared__ float sscale;
-  const unsigned row = blockIdx.x, t = threadIdx.x;
-  const size_t base = (size_t)row * width;
-  const unsigned padded = groups * kGroup;
-  float *sw = srow + padded;
-  for (unsigned i = t; i < padded; i += 256) {
-    float x = 0.0f, w1 = 1.0f;
-    if (i < width) {
-      uint16_t h = a[base + i];
-      if (kAdd) {
-        h = f2h(__fadd_rn(h2f(h), h2f(b[base + i])));
-        sum_out[base + i] = h;
+// residualAdd -> rmsNorm -> quantizeActivation of a row, in three phases that
+// the fused launches below share (Reference.metal:105-126, Graph.metal:
+// 33-68).
+//
+// Phase 1: the sum fp16(a + b) (the next residual; written when sum_out is
+// given) staged in LDS as fp32, the row padded to whole groups by zeros,
+// next to 1 + w. Without b the input row is staged as it is.
+template <bool kAdd, unsigned kThreads = 256>
+__device__ __forceinline__ void stage_norm_row(const uint16_t *__restrict__ a,
+                                               const uint16_t *__restrict__ b, uint16_t *sum_out,
+                                               const float *__restrict__ w, float *srow,
+                                               float *sw, unsigned width, unsigned padded,
+                                               unsigned t) {
+  // Eight elements a lane in flight at once: one memory round trip per
+  // eight, not per element.
+  constexpr unsigned kBatch = 8;
+  for (unsigned i0 = 0; i0 < padded; i0 += kBatch * kThreads) {
+    uint16_t ha[kBatch], hb[kBatch];
+    float wi[kBatch];
+#pragma unroll
+    for (unsigned j = 0; j < kBatch; ++j) {
+      const unsigned i = i0 + j * kThreads + t;
+      const bool in = i < width;
+      ha[j] = in ? a[i] : (uint16_t)0;
+      hb[j] = in && kAdd ? b[i] : (uint16_t)0;
+      wi[j] = in ? w[i] : 0.0f;
+    }
+#pragma unroll
+    for (unsigned j = 0; j < kBatch; ++j) {
+      const unsigned i = i0 + j * kThreads + t;
+      if (i >= padded)
+        break;
+      float x = 0.0f, w1 = 1.0f;
+      if (i < width) {
+        uint16_t h = ha[j];
+        if (kAdd) {
+          h = f2h(__fadd_rn(h2f(h), h2f(hb[j])));
+          if (sum_out)
+            sum_out[i] = h;
+        }
+        x = h2f(h);
+        w1 = 1.0f + wi[j];
       }
-      x = h2f(h);
-      w1 = 1.0f + w[i];
+      srow[i] = x;
+      sw[i] = w1;
     }
-    srow[i] = x;
-    sw[i] = w1;
   }
-  __syncthreads();
-  if (t == 0) {
-    // fma(0, 0, sum) == sum for the padding (sum >= +0)
-    const float4 *v = reinterpret_cast<const float4 *>(srow);
-    float sum = 0.0f;
+}
+
+// Phase 2 (one lane): the norm's sequential fp32 fma sum over the staged row
+// (fma(0, 0, sum) == sum for the padding, sum >= +0).
+__device__ __forceinline__ float norm_row_sum(const float *srow, unsigned padded) {
+  const float4 *v = reinterpret_cast<const float4 *>(srow);
+  float sum = 0.0f;
 #pragma unroll 8
-    for (unsigned c = 0; c < padded / 4; ++c) {
-      const float4 x4 = v[c];
-      sum = __builtin_fmaf(x4.x, x4.x, sum);
-      sum = __builtin_fmaf(x4.y, x4.y, sum);
-      sum = __builtin_fmaf(x4.z, x4.z, sum);
-      sum = __builtin_fmaf(x4.w, x4.w, sum);
-    }
-    sscale = rms_scale_of(sum, width, eps);
+  for (unsigned c = 0; c < padded / 4; ++c) {
+    const float4 x4 = v[c];
+    sum = __builtin_fmaf(x4.x, x4.x, sum);
+    sum = __builtin_fmaf(x4.y, x4.y, sum);
+    sum = __builtin_fmaf(x4.z, x4.z, sum);
+    sum = __builtin_fmaf(x4.w, x4.w, sum);
   }
-  __syncthreads();
-  // Eight lanes a group, four elements a lane: the group's max |y| and
-  // finiteness by lane swaps (exact in any order), then each lane
-  // quantizes its four with the standalone kernel's expressions.
-  const float scale = sscale;
+  return sum;
+}
+
+// Phase 3: eight lanes a group, four elements a lane: the group's max |y|
+// and finiteness by lane swaps (exact in any order), then each lane
+// quantizes its four with the standalone kernel's expressions into q (a
+// word per lane) and the group's scale into scales.
+template <unsigned kThreads = 256>
+__device__ __forceinline__ void quantize_norm_row(const float *srow, const float *sw, float scale,
+                                                  unsigned width, unsigned groups, unsigned t,
+                                                  uint32_t *q, float *scales, unsigned *invalid) {
   const unsigned sub = t % 8;
-  for (unsigned g0 = 0; g0 < groups; g0 += 32) {
+  for (unsigned g0 = 0; g0 < groups; g0 += kThreads / 8) {
     const unsigned g = g0 + t / 8;
     const bool live = g < groups;
     const unsigned i0 = (live ? g : 0) * kGroup + 4 * sub;
@@ -209,13 +229,37 @@ __global__ __launch_bounds__(256) void add_norm_quantize_kernel(
       }
       word |= ((uint32_t)r & 0xFFu) << (8 * e);
     }
-    reinterpret_cast<uint32_t *>(q + ((size_t)row * groups + g) * kGroup)[sub] = word;
+    q[g * (kGroup / 4) + sub] = word;
     if (sub == 0) {
-      scales[(size_t)row * groups + g] = qs;
+      scales[g] = qs;
       if (!finite && invalid)
         atomicOr(invalid, 1u);
     }
   }
+}
+
+// The three in one launch, a workgroup per row; the bits equal the three
+// launches' (residualAdd, rmsNorm, quantizeActivation).
+template <bool kAdd>
+__global__ __launch_bounds__(256) void add_norm_quantize_kernel(
+    const uint16_t *__restrict__ a, const uint16_t *__restrict__ b, uint16_t *sum_out,
+    const float *__restrict__ w, int8_t *__restrict__ q, float *__restrict__ scales,
+    unsigned *invalid, unsigned width, unsigned groups, float eps) {
+  extern __shared__ __align__(16) float srow[]; // the row, then 1 + w, padded
+  __shared__ float sscale;
+  const unsigned row = blockIdx.x, t = threadIdx.x;
+  const size_t base = (size_t)row * width;
+  const unsigned padded = groups * kGroup;
+  float *sw = srow + padded;
+  stage_norm_row<kAdd>(a + base, kAdd ? b + base : nullptr, kAdd ? sum_out + base : nullptr, w,
+                       srow, sw, width, padded, t);
+  __syncthreads();
+  if (t == 0)
+    sscale = rms_scale_of(norm_row_sum(srow, padded), width, eps);
+  __syncthreads();
+  quantize_norm_row(srow, sw, sscale, width, groups, t,
+                    reinterpret_cast<uint32_t *>(q + (size_t)row * groups * kGroup),
+                    scales + (size_t)row * groups, invalid);
 }
 
 // ------------------------------------------------------------------- GEMV
@@ -559,6 +603,129 @@ __global__ __launch_bounds__(64 * kWaves) void gemm_mfma_kernel(
   }
 }
 
+// ------------------------------------------------- norm + projections, decode
+
+// residualAdd -> rmsNorm -> quantizeActivation of one row and up to four
+// W8A8 projections of the quantized row in one launch (the decode step's
+// input norms and the projections that read them). The norm's sequential
+// sum is one lane's latency-bound chain (~11 us at width 2560) while the
+// projections stream their weights: in each 1024-thread workgroup, wave 0
+// stages nothing but the norm (every workgroup forms the same bits) and
+// runs the chain as soon as the row is in LDS, while waves 1-15 issue their
+// weight loads (a wave issues its loads in order, so the chain wave issues
+// none: measured, issuing 160 KB of loads a CU takes ~3 us). Waves 1-15
+// serve 60 columns of one projection with the GEMV's lanes (16 a column,
+// lane l the groups l, l + 16, ...; width <= 4096 leaves at most 8 groups a
+// lane, one unrolled step) and its arithmetic, so the outputs are the
+// separate launches' bits. One workgroup a CU keeps one chain a CU (chains
+// sharing a SIMD slow each other down).
+static_assert(kNormLinearMaxWidth == kGroup * kGemvLanes * kGemvUnroll,
+              "a lane's groups fit one unrolled step");
+constexpr unsigned kNormLinearThreads = 64 + kNormLinearCols * kGemvLanes;
+static_assert(kNormLinearThreads == 1024, "the norm wave and 60 columns of 16 lanes");
+
+struct NormLinearSeg {
+  const int8_t *w;
+  const uint16_t *ws;
+  void *out;
+  const void *aux;
+  const float *bias;
+  unsigned columns, outputWidth, firstRow, epilogue, block, wgs;
+};
+
+struct NormLinearArgs {
+  NormLinearSeg seg[kNormLinearMax];
+  unsigned count, width, groups;
+  float eps;
+};
+
+template <bool kAdd>
+__global__ __launch_bounds__(kNormLinearThreads) void norm_linear_kernel(
+    const uint16_t *__restrict__ a, const uint16_t *__restrict__ b, uint16_t *sum_out,
+    const float *__restrict__ nw, int8_t *q, float *scales, unsigned *invalid,
+    NormLinearArgs p) {
+  extern __shared__ __align__(16) float srow[]; // row, 1 + w, quantized words, scales
+  __shared__ float sscale;
+  const unsigned t = threadIdx.x, padded = p.groups * kGroup;
+  float *sw = srow + padded;
+  uint32_t *sq = reinterpret_cast<uint32_t *>(sw + padded);
+  float *ss = reinterpret_cast<float *>(sq + p.groups * (kGroup / 4));
+  unsigned blk = blockIdx.x, s = 0;
+  bool found = false;
+#pragma unroll
+  for (unsigned k = 0; k < kNormLinearMax; ++k)
+    if (!found && k < p.count) {
+      if (blk < p.seg[k].wgs) {
+        s = k;
+        found = true;
+      } else {
+        blk -= p.seg[k].wgs;
+      }
+    }
+  NormLinearSeg seg = p.seg[0]; // selected with constant indices (no private copy)
+#pragma unroll
+  for (unsigned k = 1; k < kNormLinearMax; ++k)
+    if (k == s)
+      seg = p.seg[k];
+  const bool norm_wave = t < 64;
+  const unsigned col = blk * kNormLinearCols + (t - 64) / kGemvLanes, l = t % kGemvLanes;
+  const bool live = !norm_wave && col < seg.columns;
+  const unsigned cc = live ? col : 0; // clamped: in bounds
+
+  // The row, then (waves 1-15) the weights or (wave 0) the chain. The
+  // barriers order LDS only: a __syncthreads would wait for the weight
+  // stream.
+  const bool first = blockIdx.x == 0; // writes the sum, q, scales and the flag
+  stage_norm_row<kAdd, kNormLinearThreads>(a, b, first ? sum_out : nullptr, nw, srow, sw,
+                                           p.width, padded, t);
+  lds_sync();
+  uint4_t wv[kGemvUnroll][2];
+  float wsv[kGemvUnroll];
+  if (norm_wave) {
+    if (t == 0)
+      sscale = rms_scale_of(norm_row_sum(srow, padded), p.width, p.eps);
+  } else {
+    const uint4_t *wrow = reinterpret_cast<const uint4_t *>(seg.w + (size_t)cc * padded);
+    const uint16_t *wsrow = seg.ws + (size_t)cc * p.groups;
+#pragma unroll
+    for (int u = 0; u < (int)kGemvUnroll; ++u) {
+      const unsigned g = min(l + kGemvLanes * u, p.groups - 1); // clamped: in bounds
+      wv[u][0] = __builtin_nontemporal_load(wrow + 2 * g);
+      wv[u][1] = __builtin_nontemporal_load(wrow + 2 * g + 1);
+      wsv[u] = h2f(wsrow[g]);
+    }
+  }
+  lds_sync();
+  quantize_norm_row<kNormLinearThreads>(srow, sw, sscale, p.width, p.groups, t, sq, ss,
+                                        first ? invalid : nullptr);
+  lds_sync();
+  if (first && q)
+    for (unsigned i = t; i < p.groups * (kGroup / 4); i += kNormLinearThreads)
+      reinterpret_cast<uint32_t *>(q)[i] = sq[i];
+  if (first && scales)
+    for (unsigned i = t; i < p.groups; i += kNormLinearThreads)
+      scales[i] = ss[i];
+
+  if (norm_wave)
+    return;
+  const uint4_t *arow = reinterpret_cast<const uint4_t *>(sq);
+  float acc = 0.0f;
+#pragma unroll
+  for (int u = 0; u < (int)kGemvUnroll; ++u) {
+    const unsigned g = l + kGemvLanes * u;
+    if (g < p.groups)
+      acc = add_term(acc, group_dot(arow[2 * g], arow[2 * g + 1], wv[u][0], wv[u][1]), ss[g],
+                     wsv[u]);
+  }
+#pragma unroll
+  for (int m = kGemvLanes / 2; m >= 1; m /= 2)
+    acc = __fadd_rn(acc, __shfl_xor(acc, m, kGemvLanes));
+  if (l == 0 && live) {
+    const unsigned column = seg.firstRow + col;
+    store_linear(seg.out, seg.aux, seg.bias, column, column, seg.epilogue, seg.block, acc);
+  }
+}
+
 // ------------------------------------------------------------- embeddings
 
 // embeddingW8 (Graph.metal:16-31): eight outputs per lane (they share a
@@ -634,6 +801,34 @@ hipError_t launch_add_norm_quantize(const uint16_t *a, const uint16_t *b, uint16
   else
     hipLaunchKernelGGL(add_norm_quantize_kernel<false>, dim3(rows), dim3(256), lds, stream, a,
                        b, sum_out, w, q, scales, invalid, width, groups, eps);
+  return hipGetLastError();
+}
+
+hipError_t launch_add_norm_linear(const uint16_t *a, const uint16_t *b, uint16_t *sum_out,
+                                  const float *w, int8_t *q, float *scales, unsigned *invalid,
+                                  unsigned width, float eps, const NormLinearProj *proj,
+                                  unsigned count, hipStream_t stream) {
+  NormLinearArgs p{};
+  p.count = count;
+  p.width = width;
+  p.groups = (width + kGroup - 1) / kGroup;
+  p.eps = eps;
+  unsigned wgs = 0;
+  for (unsigned k = 0; k < count; ++k) {
+    const NormLinearProj &x = proj[k];
+    p.seg[k] = {x.w, x.ws, x.out, x.aux, x.bias, x.shape.columns, x.shape.outputWidth,
+                x.shape.firstRow, x.shape.epilogue, x.shape.block,
+                norm_linear_workgroups(x.shape.columns)};
+    wgs += p.seg[k].wgs;
+  }
+  const size_t lds = 2 * (size_t)p.groups * kGroup * sizeof(float) + (size_t)p.groups * kGroup +
+                     (size_t)p.groups * sizeof(float);
+  if (b)
+    hipLaunchKernelGGL(norm_linear_kernel<true>, dim3(wgs), dim3(kNormLinearThreads), lds,
+                       stream, a, b, sum_out, w, q, scales, invalid, p);
+  else
+    hipLaunchKernelGGL(norm_linear_kernel<false>, dim3(wgs), dim3(kNormLinearThreads), lds,
+                       stream, a, b, sum_out, w, q, scales, invalid, p);
   return hipGetLastError();
 }
 

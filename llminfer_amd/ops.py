@@ -351,6 +351,66 @@ def add_rms_norm_quantize(*args, **kwargs) -> None:
     bind_add_rms_norm_quantize(*args, **kwargs)()
 
 
+def bind_add_rms_norm_linear_w8a8(a: torch.Tensor, b: torch.Tensor | None,
+                                  sum_out: torch.Tensor | None, weight: torch.Tensor,
+                                  projections: list, q: torch.Tensor | None = None,
+                                  scales: torch.Tensor | None = None,
+                                  invalid: torch.Tensor | None = None,
+                                  epsilon: float = 1e-6) -> "Bound":
+    """add_rms_norm_quantize of one row, then linear_w8a8 of each projection
+    on the quantized row, in one launch. a, b, sum_out [1, width] fp16;
+    projections: up to 4 dicts with weight, weight_scales, out and optionally
+    epilogue, block, aux, bias, first_row (as for linear_w8a8; a SwiGLU
+    projection follows its multiplier's projection and takes its out as
+    aux); q, scales as for add_rms_norm_quantize or None."""
+    _require(a, torch.float16, "a")
+    if b is not None:
+        _require(b, torch.float16, "b")
+        _require(sum_out, torch.float16, "sum_out")
+    _require(weight, torch.float32, "weight")
+    rows, width = a.shape
+    groups = (width + 31) // 32
+    if (b is not None and (b.shape != a.shape or sum_out.shape != a.shape)) or \
+            weight.numel() != width:
+        raise ValueError("a, b, sum_out [1, width] and weight [width] disagree")
+    if q is not None:
+        _require(q, torch.int8, "q")
+        _require(scales, torch.float32, "scales")
+        if tuple(q.shape) != (rows, groups * 32) or tuple(scales.shape) != (rows, groups):
+            raise ValueError("q [rows, groups * 32] and scales [rows, groups] disagree")
+    if invalid is not None:
+        _require(invalid, torch.int32, "invalid")
+    if not 1 <= len(projections) <= _lib.NORM_LINEAR_MAX:
+        raise ValueError(f"1 to {_lib.NORM_LINEAR_MAX} projections")
+    bufs = (_lib.NormProjection * _lib.NORM_LINEAR_MAX)()
+    p = _lib.NormLinearParams()
+    p.norm = _lib.RowParams(rows, width, epsilon)
+    p.count = len(projections)
+    for k, x in enumerate(projections):
+        w, ws, out = x["weight"], x["weight_scales"], x["out"]
+        epilogue = x.get("epilogue", _lib.LINEAR_NONE)
+        _require(w, torch.int8, "weight")
+        _require(ws, torch.float16, "weight_scales")
+        _require(out, torch.float32 if epilogue in _F32_EPILOGUES else torch.float16, "out")
+        columns = w.shape[0]
+        if tuple(w.shape) != (columns, groups * 32) or tuple(ws.shape) != (columns, groups) \
+                or out.dim() != 2 or out.shape[0] != rows:
+            raise ValueError(f"projection {k}: weight, weight_scales and out shapes disagree")
+        aux, bias = x.get("aux"), x.get("bias")
+        bufs[k] = _lib.NormProjection(_ptr(w), _ptr(ws), _ptr(out), _ptr(aux), _ptr(bias))
+        p.linear[k] = _lib.LinearW8Params(out.shape[1], x.get("first_row", 0), groups, rows,
+                                          columns, epilogue, x.get("block", 0))
+    bound = Bound(_lib.load().llmi_hip_add_rms_norm_linear_w8a8,
+                  (_ptr(a), _ptr(b), _ptr(sum_out), _ptr(weight), _ptr(q), _ptr(scales),
+                   _ptr(invalid), C.addressof(bufs), p, _stream()), "addRmsNormLinearW8A8")
+    bound.keep = bufs  # the projection table the call points at
+    return bound
+
+
+def add_rms_norm_linear_w8a8(*args, **kwargs) -> None:
+    bind_add_rms_norm_linear_w8a8(*args, **kwargs)()
+
+
 def bind_causal_conv(x: torch.Tensor, weight: torch.Tensor, history: torch.Tensor | None,
                      out: torch.Tensor, silu: bool = True) -> "Bound":
     """causalConv (Reference.metal:137-161): x, out [T, C] fp16; weight [C, k]

@@ -125,7 +125,8 @@ class Plan:
         n = lib.llmi_hip_plan_dispatches(handle, None, 0)
         recs = (_lib.Dispatch * max(1, n))()
         lib.llmi_hip_plan_dispatches(handle, recs, n)
-        self.dispatches = []
+        self.launches = lib.llmi_hip_plan_launches(handle)  # kernel launches a step
+        self.dispatches = []  # plan records, one per op a launch serves
         for r in recs[:n]:
             d = {"op_index": r.op_index, "kernel": r.kernel.decode()}
             if r.epilogue:

@@ -345,3 +345,46 @@ def test_w8a8_abi():
     assert ops.kernel_names(_lib.OP_EMBEDDING_W8,
                             _lib.GroupedEmbedParams(4, 100, 0, 10, 4)) == ["embeddingW8"]
     assert ops.kernel_names(_lib.OP_EMBEDDING, _lib.EmbedParams(4, 100, 0, 10)) == ["embedding"]
+
+
+def test_norm_linear_abi():
+    """The decode norm + projections launch: its parameter layout, the shapes
+    it takes (one row of at most 4096, 1-4 projections of that row's
+    groups, at most 4096 workgroups of 60 columns) and the SwiGLU multiplier
+    that must not be computed in the same call, all rejected before any
+    launch."""
+    from llminfer_amd import ops
+    assert C.sizeof(_lib.NormProjection) == 40
+    assert C.sizeof(_lib.NormLinearParams) == 12 + 4 + 4 * 28
+    lib = _lib.load()
+    a16 = 16  # a 16-byte-aligned stand-in pointer; nothing is launched
+
+    def params(width, *linears, rows=1):
+        p = _lib.NormLinearParams()
+        p.norm = _lib.RowParams(rows, width, 1e-6)
+        p.count = len(linears)
+        for k, (cols, ep) in enumerate(linears):
+            p.linear[k] = _lib.LinearW8Params(cols, 0, (width + 31) // 32, 1, cols, ep, 0)
+        return p
+
+    op = _lib.OP_ADD_RMS_NORM_LINEAR_W8A8
+    good = params(2560, (8192, 0), (4096, _lib.LINEAR_SILU_F32), (32, _lib.LINEAR_DELTA_DECAY),
+                  (32, _lib.LINEAR_DELTA_BETA))
+    assert ops.kernel_names(op, good) == ["addRmsNormLinearW8A8"]
+    for bad in (params(8192, (16, 0)), params(2560, (16, 0), rows=2), params(2560),
+                params(2560, (0, 0)), params(40, (300000, 0))):
+        assert ops.kernel_names(op, bad) == []
+    wrong_groups = params(2560, (16, 0))
+    wrong_groups.linear[0].groups = 79
+    assert ops.kernel_names(op, wrong_groups) == []
+    # a SwiGLU projection whose multiplier is another projection's output
+    p = params(2560, (64, 0), (64, _lib.LINEAR_SILU_MUL))
+    bufs = (_lib.NormProjection * _lib.NORM_LINEAR_MAX)()
+    bufs[0] = _lib.NormProjection(a16, a16, 4096, None, None)
+    bufs[1] = _lib.NormProjection(a16, a16, 8192, 4096, None)
+    assert lib.llmi_hip_add_rms_norm_linear_w8a8(a16, None, None, a16, None, None, None,
+                                                 C.addressof(bufs), p, None) == _lib.UNSUPPORTED
+    bufs[1] = _lib.NormProjection(a16, a16, 8192, None, None)
+    assert lib.llmi_hip_add_rms_norm_linear_w8a8(a16, None, None, a16, None, None, None,
+                                                 C.addressof(bufs), p, None) == \
+        _lib.INVALID_ARGUMENT

@@ -88,13 +88,23 @@ def test_qwen35_4b_lowers_with_the_hot_kernels():
     c = G.qwen35_4b()
     g, decode = _lower(c, 1, 4096, 8192, "last", True)
     kinds = Counter(d["kernel"] for d in decode.dispatches)
-    assert kinds["linearW8A8Gemv"] == 24 * 5 + 8 * 4 + 32 * 3 + 1
+    # every hidden-width norm, its quantization and the residual Add before
+    # it (all but the first layer's) in one launch, and in decode the
+    # projections right after it too (DeltaNet qkv and z, attention q, k
+    # and v, the MLP's up), each op recorded: the first layer's norm with
+    # its two projections alone, 23 DeltaNet, 8 attention and 32 MLP norms
+    # with their Add (3 + 2, 3 + 3, 3 + 1 records); the final norm before
+    # the head, whose GEMV stays its own launch
+    assert kinds["rmsNormLinearW8A8"] == 2 + 2
+    assert kinds["addRmsNormLinearW8A8"] == 23 * 5 + 8 * 6 + 32 * 4
+    assert kinds["addRmsNormQuantize"] == 3 and kinds["rmsNormQuantize"] == 0
+    # the rest: DeltaNet a, b (at DeltaGates) and out; attention out; the
+    # MLP's gate (SwiGLU) and down; the head
+    assert kinds["linearW8A8Gemv"] == 24 * 3 + 8 * 1 + 32 * 2 + 1
     assert kinds["gqaDecodeSplitK"] == 8 and kinds["deltaRecurrent"] == 24
-    # every hidden-width norm and its quantization in one launch, with the
-    # residual Add before it (all but the first layer's), each op recorded
-    # (launches: the first layer's input norm alone, 63 later norms and the
-    # final one with their Add; two or three records each)
-    assert kinds["rmsNormQuantize"] == 2 and kinds["addRmsNormQuantize"] == 64 * 3
+    # a launch that serves several ops (the Adds, norms, quantizations and
+    # projections above) has a record for each: 732 records, 499 launches
+    assert len(decode.dispatches) == 732 and decode.launches == 499
     assert kinds["residualAdd"] == 0
     assert "quantizeActivation" in kinds     # the others (after GQA / gated norms, SwiGLU)
     indices = [d["op_index"] for d in decode.dispatches]
@@ -104,6 +114,10 @@ def test_qwen35_4b_lowers_with_the_hot_kernels():
     _, prefill = _lower(c, 512, 0, 8192, "last", True)
     kinds = Counter(d["kernel"] for d in prefill.dispatches)
     assert kinds["gqaPrefillMfma"] == 8
+    # several rows: the norms keep their quantization launch (the final
+    # norm takes the last row, a view, without its Add); the head stays a GEMV
+    assert kinds["rmsNormQuantize"] == 2 + 2 and kinds["addRmsNormQuantize"] == 63 * 3
+    assert "addRmsNormLinearW8A8" not in kinds and kinds["linearW8A8Gemv"] == 1
     # the MLP down projection and the head: at most a few hundred MB of scratch
     assert prefill.scratch_bytes < 512 << 20
 

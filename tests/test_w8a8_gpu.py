@@ -238,3 +238,114 @@ def test_add_rms_norm_quantize_is_the_three_ops(gpu, rows, width, add):
     assert torch.equal(q1, q3)
     assert np.array_equal(c1.cpu().numpy().view(np.uint32), c3.cpu().numpy().view(np.uint32))
     assert int(i1.item()) == int(i3.item())
+
+
+def _projection_weights(r, columns, groups, gpu):
+    w = r.integers(-127, 128, (columns, groups * 32), dtype=np.int8)
+    ws = _f16(r.uniform(0.001, 0.02, (columns, groups)))
+    return _dev(w, gpu), _u16_dev(ws, gpu)
+
+
+# (width, add, projections: (columns, epilogue, block)); the shapes of the
+# Qwen3.5-4B decode step's input norms: DeltaNet qkv / z / a / b, the MLP's
+# up + gate (SwiGLU), the attention's q (+ gate columns) / k / v.
+_NORM_LINEAR_CASES = [
+    (2560, True, [(8192, _lib.LINEAR_NONE, 0), (4096, _lib.LINEAR_SILU_F32, 0),
+                  (32, _lib.LINEAR_DELTA_DECAY, 0), (32, _lib.LINEAR_DELTA_BETA, 0)]),
+    (2560, True, [(9216, _lib.LINEAR_NONE, 0)]),
+    (2560, False, [(8192, _lib.LINEAR_SIGMOID_COLUMNS, 256), (1024, _lib.LINEAR_NONE, 0),
+                   (1024, _lib.LINEAR_NONE, 0)]),
+    (1000, True, [(100, _lib.LINEAR_SILU, 0), (37, _lib.LINEAR_NONE, 0),
+                  (37, _lib.LINEAR_SILU_MUL, 0)]),  # its multiplier computed beforehand
+    (4096, False, [(17, _lib.LINEAR_NONE, 0)]),
+    (33, True, [(16, _lib.LINEAR_DELTA_BETA, 0), (65, _lib.LINEAR_NONE, 0),
+                (129, _lib.LINEAR_SIGMOID_COLUMNS, 8)]),
+]
+
+
+@pytest.mark.parametrize("case", range(len(_NORM_LINEAR_CASES)))
+@pytest.mark.parametrize("special", [False, True])
+def test_add_rms_norm_linear_is_the_separate_ops(gpu, case, special):
+    """The norm and its projections in one launch equal add_rms_norm_quantize
+    followed by one linear_w8a8 per projection, bit for bit: the sum, the
+    quantized row, its scales, the invalid flag and every projection
+    output (special: an infinite input quantizes its group to zeros and
+    raises the flag)."""
+    width, add, projs = _NORM_LINEAR_CASES[case]
+    print(f"addRmsNormLinearW8A8 width={width} add={add} projections={projs} "
+          f"special={special}", flush=True)
+    r = np.random.default_rng(100 + case)
+    groups = (width + 31) // 32
+    a = _f16(r.standard_normal((1, width)) * 3)
+    b = _f16(r.standard_normal((1, width)) * 3)
+    if special:
+        a[0, width // 2] = 0x7C00
+    w = (r.standard_normal(width) * 0.2).astype(np.float32)
+    da, db, dw = _u16_dev(a, gpu), _u16_dev(b, gpu), _dev(w, gpu)
+    f32 = (_lib.LINEAR_SILU_F32, _lib.LINEAR_DELTA_BETA, _lib.LINEAR_DELTA_DECAY)
+    specs = []
+    for k, (columns, epilogue, block) in enumerate(projs):
+        wt, ws = _projection_weights(r, columns, groups, gpu)
+        spec = {"weight": wt, "weight_scales": ws, "epilogue": epilogue, "block": block}
+        if epilogue == _lib.LINEAR_DELTA_DECAY:
+            spec["aux"] = _dev(r.uniform(-2, 1, columns).astype(np.float32), gpu)
+            spec["bias"] = _dev(r.uniform(-1, 1, columns).astype(np.float32), gpu)
+        if epilogue == _lib.LINEAR_SILU_MUL:  # a multiplier computed before the call
+            spec["aux"] = _u16_dev(_f16(r.standard_normal((1, columns))), gpu)
+        specs.append(spec)
+
+    def outputs():
+        outs = []
+        for (columns, epilogue, _), spec in zip(projs, specs):
+            dtype = torch.float32 if epilogue in f32 else torch.float16
+            outs.append(torch.full((1, columns), -7.0, dtype=dtype, device=gpu))
+        return outs
+
+    # separate launches
+    s3 = torch.empty(1, width, dtype=torch.float16, device=gpu)
+    q3 = torch.empty(1, groups * 32, dtype=torch.int8, device=gpu)
+    c3 = torch.empty(1, groups, dtype=torch.float32, device=gpu)
+    i3 = torch.zeros(1, dtype=torch.int32, device=gpu)
+    ops.add_rms_norm_quantize(da, db if add else None, s3 if add else None, dw, q3, c3, i3)
+    o3 = outputs()
+    for k, spec in enumerate(specs):
+        ops.linear_w8a8(q3, c3, spec["weight"], spec["weight_scales"], o3[k], spec["epilogue"],
+                        spec["block"], spec.get("aux"), spec.get("bias"))
+    # one launch
+    s1 = torch.empty_like(s3)
+    q1 = torch.zeros_like(q3)
+    c1 = torch.zeros_like(c3)
+    i1 = torch.zeros(1, dtype=torch.int32, device=gpu)
+    o1 = outputs()
+    plist = [dict(spec, out=o1[k]) for k, spec in enumerate(specs)]
+    ops.add_rms_norm_linear_w8a8(da, db if add else None, s1 if add else None, dw, plist, q1, c1,
+                                 i1)
+    torch.cuda.synchronize()
+    if add:
+        assert np.array_equal(_host_u16(s1), _host_u16(s3))
+    assert torch.equal(q1, q3)
+    assert np.array_equal(c1.cpu().numpy().view(np.uint32), c3.cpu().numpy().view(np.uint32))
+    assert int(i1.item()) == int(i3.item()) == (1 if special else 0)
+    for k in range(len(projs)):
+        assert np.array_equal(o1[k].cpu().numpy().view(np.uint8),
+                              o3[k].cpu().numpy().view(np.uint8)), f"projection {k}"
+
+
+def test_add_rms_norm_linear_without_q(gpu):
+    """q and scales may be omitted; the projections are the same."""
+    print("addRmsNormLinearW8A8 without q", flush=True)
+    r = np.random.default_rng(7)
+    width, groups = 2560, 80
+    a = _u16_dev(_f16(r.standard_normal((1, width))), gpu)
+    w = _dev((r.standard_normal(width) * 0.2).astype(np.float32), gpu)
+    wt, ws = _projection_weights(r, 300, groups, gpu)
+    q = torch.empty(1, groups * 32, dtype=torch.int8, device=gpu)
+    c = torch.empty(1, groups, dtype=torch.float32, device=gpu)
+    ops.add_rms_norm_quantize(a, None, None, w, q, c)
+    want = torch.empty(1, 300, dtype=torch.float16, device=gpu)
+    ops.linear_w8a8(q, c, wt, ws, want)
+    got = torch.empty_like(want)
+    ops.add_rms_norm_linear_w8a8(a, None, None, w,
+                                 [{"weight": wt, "weight_scales": ws, "out": got}])
+    torch.cuda.synchronize()
+    assert torch.equal(got.view(torch.int16), want.view(torch.int16))
