@@ -532,8 +532,10 @@ typedef struct NormLinearParams {
  * decode step's input norm and the projections that read its quantization).
  * The outputs are the separate calls' bits. q and scales may be NULL (not
  * written) when nothing else reads them. Epilogues as for
- * llmi_hip_linear_w8a8, except that a LLMI_LINEAR_SILU_MUL multiplier
- * (aux) must not be an output of the same call. At most 4096 workgroups of
+ * llmi_hip_linear_w8a8; a LLMI_LINEAR_SILU_MUL multiplier (aux) computed
+ * in the same call must be the previous projection's output, that
+ * projection with no epilogue and the same columns, width <= 2560 (the two
+ * are computed by the same lanes). At most 4096 workgroups of
  * 60 columns in all (one per CU runs best: 256 on MI355X). No output may
  * overlap a, b, sum_out, q, scales or another output: the projections run
  * concurrently with the norm of other workgroups. */

@@ -437,15 +437,26 @@ int llmi_hip_add_rms_norm_linear_w8a8(const uint16_t *a, const uint16_t *b, uint
     if (!aligned16(x.weight))
       return fail(LLMI_HIP_UNSUPPORTED,
                   "addRmsNormLinearW8A8: projection %u: weight rows not 16-byte aligned", k);
+    bool mate = false; // computed by the lanes of projection k - 1
     if (l.epilogue == LLMI_LINEAR_SILU_MUL) {
       if (!x.aux)
         return fail(LLMI_HIP_INVALID_ARGUMENT,
                     "addRmsNormLinearW8A8: projection %u: SiluMul needs its multiplier (aux)", k);
+      mate = k > 0 && x.aux == projections[k - 1].output;
+      if (mate && (p.norm.width > kNormLinearPairedWidth ||
+                   p.linear[k - 1].epilogue != LLMI_LINEAR_NONE ||
+                   p.linear[k - 1].columns != l.columns || proj[k - 1].paired ||
+                   (k > 1 && proj[k - 2].paired)))
+        return fail(LLMI_HIP_UNSUPPORTED,
+                    "addRmsNormLinearW8A8: projection %u: a SwiGLU multiplier computed in the "
+                    "call must be the previous projection's output, with no epilogue, the same "
+                    "columns and width <= %u",
+                    k, kNormLinearPairedWidth);
       for (unsigned j = 0; j < p.count; ++j)
-        if (projections[j].output == x.aux)
+        if (j + 1 != k && projections[j].output == x.aux)
           return fail(LLMI_HIP_UNSUPPORTED,
-                      "addRmsNormLinearW8A8: projection %u: the SwiGLU multiplier is computed "
-                      "in the same call",
+                      "addRmsNormLinearW8A8: projection %u: its SwiGLU multiplier is another "
+                      "projection's output",
                       k);
     }
     if (l.epilogue == LLMI_LINEAR_DELTA_DECAY && (!x.aux || !x.bias))
@@ -453,7 +464,10 @@ int llmi_hip_add_rms_norm_linear_w8a8(const uint16_t *a, const uint16_t *b, uint
                   "addRmsNormLinearW8A8: projection %u: the decay needs A_log (aux) and bias", k);
     proj[k] = {x.weight, x.weight_scales, x.output, x.aux, x.bias,
                W8Shape{l.outputWidth, l.firstRow, l.groups, l.rows, l.columns, l.epilogue,
-                       l.epilogueBlock}};
+                       l.epilogueBlock},
+               false};
+    if (mate)
+      proj[k - 1].paired = true;
   }
   return launched(launch_add_norm_linear(a, b, sum_out, weight, q, scales, invalid, p.norm.width,
                                          p.norm.epsilon, proj, p.count,

@@ -206,7 +206,10 @@ constexpr unsigned kAddNormQuantizeMax = 8192;
 // The same row's norm and quantization followed by up to kNormLinearMax
 // W8A8 projections of it, rows == 1, width <= kNormLinearMaxWidth, one
 // workgroup per 60 columns of a projection (w8a8.hip).
+// A SwiGLU projection right after its multiplier's projection is computed
+// by the same lanes (paired) up to kNormLinearPairedWidth.
 constexpr unsigned kNormLinearMax = LLMI_HIP_NORM_LINEAR_MAX, kNormLinearMaxWidth = 4096;
+constexpr unsigned kNormLinearPairedWidth = 2560;
 constexpr unsigned kNormLinearCols = 60, kNormLinearMaxWgs = 4096;
 inline unsigned norm_linear_workgroups(unsigned columns) {
   return (columns + kNormLinearCols - 1) / kNormLinearCols;
@@ -218,6 +221,7 @@ struct NormLinearProj {
   const void *aux;
   const float *bias;
   W8Shape shape;
+  bool paired; // the next projection is this one's SwiGLU partner
 };
 hipError_t launch_add_norm_linear(const uint16_t *a, const uint16_t *b, uint16_t *sum_out,
                                   const float *w, int8_t *q, float *scales, unsigned *invalid,

@@ -486,10 +486,10 @@ void Lowering::prepare_norm_quantize() {
 // it that read its quantized row, merged into one launch
 // (llmi_hip_add_rms_norm_linear_w8a8) whose weight stream runs under the
 // norm's chain: at most kNormLinearMax projections, one round of
-// workgroups (one a CU), no SwiGLU projection (its multiplier would be
-// computed in the same launch), not the logits head, and no output
-// overlapping what the launch reads or another output. Every op keeps its
-// record.
+// workgroups (one a CU), a SwiGLU projection only right after its
+// multiplier's projection (the same lanes compute both), not the logits
+// head, and no output overlapping what the launch reads or another output.
+// Every op keeps its record.
 void Lowering::merge_norm_linears() {
   constexpr unsigned kOneRound = 256;
   auto &ds = plan_.dispatches;
@@ -517,15 +517,26 @@ void Lowering::merge_norm_linears() {
     NormLinearParams np{};
     np.norm = row;
     unsigned wgs = 0;
+    bool lastMate = false;
     size_t j = i + 1;
     for (; j < ds.size() && np.count < kNormLinearMax; ++j) {
       const Dispatch &l = ds[j];
       const LinearW8Params &lp = l.p.linearW8;
+      // A SwiGLU projection joins only as the mate of the projection just
+      // taken (its multiplier), computed by the same lanes.
+      const bool mate = lp.epilogue == LLMI_LINEAR_SILU_MUL && np.count > 0 && !lastMate &&
+                        row.width <= kNormLinearPairedWidth &&
+                        np.linear[np.count - 1].epilogue == LLMI_LINEAR_NONE &&
+                        np.linear[np.count - 1].columns == lp.columns &&
+                        l.buf[5].space == ds[j - 1].buf[4].space &&
+                        l.buf[5].index == ds[j - 1].buf[4].index &&
+                        l.buf[5].offset == ds[j - 1].buf[4].offset;
+      const unsigned more = mate ? 0 : norm_linear_workgroups(lp.columns);
       if (l.launch != Launch::LinearW8 || l.buf[0].space != d.buf[4].space ||
           l.buf[0].offset != d.buf[4].offset || l.buf[1].offset != d.buf[5].offset ||
           l.buf[1].space != d.buf[5].space || lp.rows != 1 || lp.groups != groups ||
-          lp.epilogue == LLMI_LINEAR_SILU_MUL || l.buf[4].space == Space::Output ||
-          wgs + norm_linear_workgroups(lp.columns) > kOneRound)
+          (lp.epilogue == LLMI_LINEAR_SILU_MUL && !mate) || l.buf[4].space == Space::Output ||
+          wgs + more > kOneRound)
         break; // the logits head keeps its own GEMV launch and record
       const bool f32 = lp.epilogue == LLMI_LINEAR_SILU_F32 ||
                        lp.epilogue == LLMI_LINEAR_DELTA_BETA ||
@@ -539,7 +550,8 @@ void Lowering::merge_norm_linears() {
       reads.push_back(o);
       np.linear[np.count] = lp;
       ++np.count;
-      wgs += norm_linear_workgroups(lp.columns);
+      wgs += more;
+      lastMate = mate;
     }
     if (np.count == 0 || llmi_hip_dispatch_count(LLMI_HIP_OP_ADD_RMS_NORM_LINEAR_W8A8, &np) == 0) {
       out.push_back(d);

@@ -615,14 +615,17 @@ __global__ __launch_bounds__(64 * kWaves) void gemm_mfma_kernel(
 // weight loads (a wave issues its loads in order, so the chain wave issues
 // none: measured, issuing 160 KB of loads a CU takes ~3 us). Waves 1-15
 // serve 60 columns of one projection with the GEMV's lanes (16 a column,
-// lane l the groups l, l + 16, ...; width <= 4096 leaves at most 8 groups a
-// lane, one unrolled step) and its arithmetic, so the outputs are the
-// separate launches' bits. One workgroup a CU keeps one chain a CU (chains
-// sharing a SIMD slow each other down).
-static_assert(kNormLinearMaxWidth == kGroup * kGemvLanes * kGemvUnroll,
-              "a lane's groups fit one unrolled step");
+// lane l the groups l, l + 16, ...: kLaneGroups of them, 5 up to width 2560,
+// 8 up to 4096, one unrolled step) and its arithmetic, so the outputs are
+// the separate launches' bits. A paired projection (kPaired, width <= 2560)
+// also computes the next one, a SwiGLU projection whose multiplier is this
+// one's output, in the same lanes: its weights sit beside the first's and
+// the multiplier comes from registers. One workgroup a CU keeps one chain a
+// CU (chains sharing a SIMD slow each other down).
 constexpr unsigned kNormLinearThreads = 64 + kNormLinearCols * kGemvLanes;
 static_assert(kNormLinearThreads == 1024, "the norm wave and 60 columns of 16 lanes");
+static_assert(kNormLinearMaxWidth == kGroup * kGemvLanes * 8, "8 groups a lane at most");
+static_assert(kNormLinearPairedWidth == kGroup * kGemvLanes * 5, "5 groups a lane paired");
 
 struct NormLinearSeg {
   const int8_t *w;
@@ -630,7 +633,7 @@ struct NormLinearSeg {
   void *out;
   const void *aux;
   const float *bias;
-  unsigned columns, outputWidth, firstRow, epilogue, block, wgs;
+  unsigned columns, outputWidth, firstRow, epilogue, block, wgs, paired;
 };
 
 struct NormLinearArgs {
@@ -639,7 +642,44 @@ struct NormLinearArgs {
   float eps;
 };
 
-template <bool kAdd>
+// One column's weights for a lane: its kLaneGroups groups (clamped: in
+// bounds) and their scales.
+template <int kLaneGroups>
+__device__ __forceinline__ void load_lane_weights(const NormLinearSeg &seg, unsigned cc,
+                                                  unsigned l, unsigned groups,
+                                                  uint4_t (&wv)[kLaneGroups][2],
+                                                  float (&wsv)[kLaneGroups]) {
+  const uint4_t *wrow = reinterpret_cast<const uint4_t *>(seg.w + (size_t)cc * groups * kGroup);
+  const uint16_t *wsrow = seg.ws + (size_t)cc * groups;
+#pragma unroll
+  for (int u = 0; u < kLaneGroups; ++u) {
+    const unsigned g = min(l + kGemvLanes * u, groups - 1);
+    wv[u][0] = __builtin_nontemporal_load(wrow + 2 * g);
+    wv[u][1] = __builtin_nontemporal_load(wrow + 2 * g + 1);
+    wsv[u] = h2f(wsrow[g]);
+  }
+}
+
+// The lane's fp32 sum in group order, then the column's butterfly.
+template <int kLaneGroups>
+__device__ __forceinline__ float lane_dots(const uint4_t *arow, const float *ss, unsigned l,
+                                           unsigned groups, const uint4_t (&wv)[kLaneGroups][2],
+                                           const float (&wsv)[kLaneGroups]) {
+  float acc = 0.0f;
+#pragma unroll
+  for (int u = 0; u < kLaneGroups; ++u) {
+    const unsigned g = l + kGemvLanes * u;
+    if (g < groups)
+      acc = add_term(acc, group_dot(arow[2 * g], arow[2 * g + 1], wv[u][0], wv[u][1]), ss[g],
+                     wsv[u]);
+  }
+#pragma unroll
+  for (int m = kGemvLanes / 2; m >= 1; m /= 2)
+    acc = __fadd_rn(acc, __shfl_xor(acc, m, kGemvLanes));
+  return acc;
+}
+
+template <bool kAdd, int kLaneGroups, bool kPaired>
 __global__ __launch_bounds__(kNormLinearThreads) void norm_linear_kernel(
     const uint16_t *__restrict__ a, const uint16_t *__restrict__ b, uint16_t *sum_out,
     const float *__restrict__ nw, int8_t *q, float *scales, unsigned *invalid,
@@ -662,11 +702,16 @@ __global__ __launch_bounds__(kNormLinearThreads) void norm_linear_kernel(
         blk -= p.seg[k].wgs;
       }
     }
-  NormLinearSeg seg = p.seg[0]; // selected with constant indices (no private copy)
+  // selected with constant indices (no private copy of the table)
+  NormLinearSeg seg = p.seg[0], mate = p.seg[0];
 #pragma unroll
-  for (unsigned k = 1; k < kNormLinearMax; ++k)
+  for (unsigned k = 1; k < kNormLinearMax; ++k) {
     if (k == s)
       seg = p.seg[k];
+    if (kPaired && k == s + 1)
+      mate = p.seg[k];
+  }
+  const bool paired = kPaired && seg.paired;
   const bool norm_wave = t < 64;
   const unsigned col = blk * kNormLinearCols + (t - 64) / kGemvLanes, l = t % kGemvLanes;
   const bool live = !norm_wave && col < seg.columns;
@@ -679,21 +724,16 @@ __global__ __launch_bounds__(kNormLinearThreads) void norm_linear_kernel(
   stage_norm_row<kAdd, kNormLinearThreads>(a, b, first ? sum_out : nullptr, nw, srow, sw,
                                            p.width, padded, t);
   lds_sync();
-  uint4_t wv[kGemvUnroll][2];
-  float wsv[kGemvUnroll];
+  uint4_t wv[kLaneGroups][2], mv[kPaired ? kLaneGroups : 1][2];
+  float wsv[kLaneGroups], msv[kPaired ? kLaneGroups : 1];
   if (norm_wave) {
     if (t == 0)
       sscale = rms_scale_of(norm_row_sum(srow, padded), p.width, p.eps);
   } else {
-    const uint4_t *wrow = reinterpret_cast<const uint4_t *>(seg.w + (size_t)cc * padded);
-    const uint16_t *wsrow = seg.ws + (size_t)cc * p.groups;
-#pragma unroll
-    for (int u = 0; u < (int)kGemvUnroll; ++u) {
-      const unsigned g = min(l + kGemvLanes * u, p.groups - 1); // clamped: in bounds
-      wv[u][0] = __builtin_nontemporal_load(wrow + 2 * g);
-      wv[u][1] = __builtin_nontemporal_load(wrow + 2 * g + 1);
-      wsv[u] = h2f(wsrow[g]);
-    }
+    load_lane_weights<kLaneGroups>(seg, cc, l, p.groups, wv, wsv);
+    if constexpr (kPaired)
+      if (paired)
+        load_lane_weights<kLaneGroups>(mate, cc, l, p.groups, mv, msv);
   }
   lds_sync();
   quantize_norm_row<kNormLinearThreads>(srow, sw, sscale, p.width, p.groups, t, sq, ss,
@@ -709,17 +749,21 @@ __global__ __launch_bounds__(kNormLinearThreads) void norm_linear_kernel(
   if (norm_wave)
     return;
   const uint4_t *arow = reinterpret_cast<const uint4_t *>(sq);
-  float acc = 0.0f;
-#pragma unroll
-  for (int u = 0; u < (int)kGemvUnroll; ++u) {
-    const unsigned g = l + kGemvLanes * u;
-    if (g < p.groups)
-      acc = add_term(acc, group_dot(arow[2 * g], arow[2 * g + 1], wv[u][0], wv[u][1]), ss[g],
-                     wsv[u]);
+  const float acc = lane_dots<kLaneGroups>(arow, ss, l, p.groups, wv, wsv);
+  if constexpr (kPaired) {
+    if (paired) {
+      const float macc = lane_dots<kLaneGroups>(arow, ss, l, p.groups, mv, msv);
+      if (l == 0 && live) {
+        // the first projection has no epilogue: its fp16 output is the
+        // SwiGLU multiplier
+        const float projected = round16(acc);
+        static_cast<uint16_t *>(seg.out)[seg.firstRow + col] = f2h(projected);
+        static_cast<uint16_t *>(mate.out)[mate.firstRow + col] =
+            silu_mul16(round16(macc), f2h(projected));
+      }
+      return;
+    }
   }
-#pragma unroll
-  for (int m = kGemvLanes / 2; m >= 1; m /= 2)
-    acc = __fadd_rn(acc, __shfl_xor(acc, m, kGemvLanes));
   if (l == 0 && live) {
     const unsigned column = seg.firstRow + col;
     store_linear(seg.out, seg.aux, seg.bias, column, column, seg.epilogue, seg.block, acc);
@@ -804,6 +848,16 @@ hipError_t launch_add_norm_quantize(const uint16_t *a, const uint16_t *b, uint16
   return hipGetLastError();
 }
 
+template <bool kAdd, int kLaneGroups, bool kPaired>
+static void launch_norm_linear_as(const uint16_t *a, const uint16_t *b, uint16_t *sum_out,
+                                  const float *w, int8_t *q, float *scales, unsigned *invalid,
+                                  const NormLinearArgs &p, unsigned wgs, size_t lds,
+                                  hipStream_t stream) {
+  hipLaunchKernelGGL((norm_linear_kernel<kAdd, kLaneGroups, kPaired>), dim3(wgs),
+                     dim3(kNormLinearThreads), lds, stream, a, b, sum_out, w, q, scales, invalid,
+                     p);
+}
+
 hipError_t launch_add_norm_linear(const uint16_t *a, const uint16_t *b, uint16_t *sum_out,
                                   const float *w, int8_t *q, float *scales, unsigned *invalid,
                                   unsigned width, float eps, const NormLinearProj *proj,
@@ -814,21 +868,40 @@ hipError_t launch_add_norm_linear(const uint16_t *a, const uint16_t *b, uint16_t
   p.groups = (width + kGroup - 1) / kGroup;
   p.eps = eps;
   unsigned wgs = 0;
+  bool paired = false;
   for (unsigned k = 0; k < count; ++k) {
     const NormLinearProj &x = proj[k];
+    const bool mate = k > 0 && proj[k - 1].paired;
     p.seg[k] = {x.w, x.ws, x.out, x.aux, x.bias, x.shape.columns, x.shape.outputWidth,
                 x.shape.firstRow, x.shape.epilogue, x.shape.block,
-                norm_linear_workgroups(x.shape.columns)};
+                mate ? 0u : norm_linear_workgroups(x.shape.columns), x.paired ? 1u : 0u};
     wgs += p.seg[k].wgs;
+    paired = paired || x.paired;
   }
   const size_t lds = 2 * (size_t)p.groups * kGroup * sizeof(float) + (size_t)p.groups * kGroup +
                      (size_t)p.groups * sizeof(float);
-  if (b)
-    hipLaunchKernelGGL(norm_linear_kernel<true>, dim3(wgs), dim3(kNormLinearThreads), lds,
-                       stream, a, b, sum_out, w, q, scales, invalid, p);
-  else
-    hipLaunchKernelGGL(norm_linear_kernel<false>, dim3(wgs), dim3(kNormLinearThreads), lds,
-                       stream, a, b, sum_out, w, q, scales, invalid, p);
+  const bool five = width <= kNormLinearPairedWidth;
+  if (b) {
+    if (paired)
+      launch_norm_linear_as<true, 5, true>(a, b, sum_out, w, q, scales, invalid, p, wgs, lds,
+                                           stream);
+    else if (five)
+      launch_norm_linear_as<true, 5, false>(a, b, sum_out, w, q, scales, invalid, p, wgs, lds,
+                                            stream);
+    else
+      launch_norm_linear_as<true, 8, false>(a, b, sum_out, w, q, scales, invalid, p, wgs, lds,
+                                            stream);
+  } else {
+    if (paired)
+      launch_norm_linear_as<false, 5, true>(a, b, sum_out, w, q, scales, invalid, p, wgs, lds,
+                                            stream);
+    else if (five)
+      launch_norm_linear_as<false, 5, false>(a, b, sum_out, w, q, scales, invalid, p, wgs, lds,
+                                             stream);
+    else
+      launch_norm_linear_as<false, 8, false>(a, b, sum_out, w, q, scales, invalid, p, wgs, lds,
+                                             stream);
+  }
   return hipGetLastError();
 }
 

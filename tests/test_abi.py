@@ -350,9 +350,9 @@ def test_w8a8_abi():
 def test_norm_linear_abi():
     """The decode norm + projections launch: its parameter layout, the shapes
     it takes (one row of at most 4096, 1-4 projections of that row's
-    groups, at most 4096 workgroups of 60 columns) and the SwiGLU multiplier
-    that must not be computed in the same call, all rejected before any
-    launch."""
+    groups, at most 4096 workgroups of 60 columns) and a SwiGLU multiplier
+    computed in the same call only as the previous projection's output (the
+    pair computed by the same lanes), all rejected before any launch."""
     from llminfer_amd import ops
     assert C.sizeof(_lib.NormProjection) == 40
     assert C.sizeof(_lib.NormLinearParams) == 12 + 4 + 4 * 28
@@ -377,14 +377,24 @@ def test_norm_linear_abi():
     wrong_groups = params(2560, (16, 0))
     wrong_groups.linear[0].groups = 79
     assert ops.kernel_names(op, wrong_groups) == []
-    # a SwiGLU projection whose multiplier is another projection's output
-    p = params(2560, (64, 0), (64, _lib.LINEAR_SILU_MUL))
+    # a SwiGLU projection whose multiplier is computed in the call but is not
+    # the previous projection's output, or is too wide to pair
     bufs = (_lib.NormProjection * _lib.NORM_LINEAR_MAX)()
     bufs[0] = _lib.NormProjection(a16, a16, 4096, None, None)
-    bufs[1] = _lib.NormProjection(a16, a16, 8192, 4096, None)
+    bufs[1] = _lib.NormProjection(a16, a16, 8192, None, None)
+    bufs[2] = _lib.NormProjection(a16, a16, 12288, 4096, None)
+    p = params(2560, (64, 0), (64, 0), (64, _lib.LINEAR_SILU_MUL))
     assert lib.llmi_hip_add_rms_norm_linear_w8a8(a16, None, None, a16, None, None, None,
                                                  C.addressof(bufs), p, None) == _lib.UNSUPPORTED
+    bufs[1] = _lib.NormProjection(a16, a16, 8192, 4096, None)
+    for p in (params(4096, (64, 0), (64, _lib.LINEAR_SILU_MUL)),
+              params(2560, (64, 0), (32, _lib.LINEAR_SILU_MUL)),
+              params(2560, (64, _lib.LINEAR_SILU), (64, _lib.LINEAR_SILU_MUL))):
+        assert lib.llmi_hip_add_rms_norm_linear_w8a8(a16, None, None, a16, None, None, None,
+                                                     C.addressof(bufs), p, None) == \
+            _lib.UNSUPPORTED
     bufs[1] = _lib.NormProjection(a16, a16, 8192, None, None)
+    p = params(2560, (64, 0), (64, _lib.LINEAR_SILU_MUL))
     assert lib.llmi_hip_add_rms_norm_linear_w8a8(a16, None, None, a16, None, None, None,
                                                  C.addressof(bufs), p, None) == \
         _lib.INVALID_ARGUMENT

@@ -248,18 +248,21 @@ def _projection_weights(r, columns, groups, gpu):
 
 # (width, add, projections: (columns, epilogue, block)); the shapes of the
 # Qwen3.5-4B decode step's input norms: DeltaNet qkv / z / a / b, the MLP's
-# up + gate (SwiGLU), the attention's q (+ gate columns) / k / v.
+# up + gate (SwiGLU, its multiplier up's output: computed by up's lanes),
+# the attention's q (+ gate columns) / k / v.
+_PAIRED = -1  # SwiGLU with the previous projection's output as multiplier
 _NORM_LINEAR_CASES = [
     (2560, True, [(8192, _lib.LINEAR_NONE, 0), (4096, _lib.LINEAR_SILU_F32, 0),
                   (32, _lib.LINEAR_DELTA_DECAY, 0), (32, _lib.LINEAR_DELTA_BETA, 0)]),
-    (2560, True, [(9216, _lib.LINEAR_NONE, 0)]),
+    (2560, True, [(9216, _lib.LINEAR_NONE, 0), (9216, _PAIRED, 0)]),
     (2560, False, [(8192, _lib.LINEAR_SIGMOID_COLUMNS, 256), (1024, _lib.LINEAR_NONE, 0),
                    (1024, _lib.LINEAR_NONE, 0)]),
     (1000, True, [(100, _lib.LINEAR_SILU, 0), (37, _lib.LINEAR_NONE, 0),
                   (37, _lib.LINEAR_SILU_MUL, 0)]),  # its multiplier computed beforehand
     (4096, False, [(17, _lib.LINEAR_NONE, 0)]),
     (33, True, [(16, _lib.LINEAR_DELTA_BETA, 0), (65, _lib.LINEAR_NONE, 0),
-                (129, _lib.LINEAR_SIGMOID_COLUMNS, 8)]),
+                (65, _PAIRED, 0), (129, _lib.LINEAR_SIGMOID_COLUMNS, 8)]),
+    (4000, False, [(61, _lib.LINEAR_NONE, 0), (7, _lib.LINEAR_SILU_MUL, 0)]),
 ]
 
 
@@ -283,21 +286,23 @@ def test_add_rms_norm_linear_is_the_separate_ops(gpu, case, special):
     w = (r.standard_normal(width) * 0.2).astype(np.float32)
     da, db, dw = _u16_dev(a, gpu), _u16_dev(b, gpu), _dev(w, gpu)
     f32 = (_lib.LINEAR_SILU_F32, _lib.LINEAR_DELTA_BETA, _lib.LINEAR_DELTA_DECAY)
-    specs = []
+    specs, paired = [], []
     for k, (columns, epilogue, block) in enumerate(projs):
+        paired.append(epilogue == _PAIRED)
+        epilogue = _lib.LINEAR_SILU_MUL if epilogue == _PAIRED else epilogue
         wt, ws = _projection_weights(r, columns, groups, gpu)
         spec = {"weight": wt, "weight_scales": ws, "epilogue": epilogue, "block": block}
         if epilogue == _lib.LINEAR_DELTA_DECAY:
             spec["aux"] = _dev(r.uniform(-2, 1, columns).astype(np.float32), gpu)
             spec["bias"] = _dev(r.uniform(-1, 1, columns).astype(np.float32), gpu)
-        if epilogue == _lib.LINEAR_SILU_MUL:  # a multiplier computed before the call
+        if epilogue == _lib.LINEAR_SILU_MUL and not paired[k]:  # computed before the call
             spec["aux"] = _u16_dev(_f16(r.standard_normal((1, columns))), gpu)
         specs.append(spec)
 
     def outputs():
         outs = []
-        for (columns, epilogue, _), spec in zip(projs, specs):
-            dtype = torch.float32 if epilogue in f32 else torch.float16
+        for (columns, _, _), spec in zip(projs, specs):
+            dtype = torch.float32 if spec["epilogue"] in f32 else torch.float16
             outs.append(torch.full((1, columns), -7.0, dtype=dtype, device=gpu))
         return outs
 
@@ -309,15 +314,17 @@ def test_add_rms_norm_linear_is_the_separate_ops(gpu, case, special):
     ops.add_rms_norm_quantize(da, db if add else None, s3 if add else None, dw, q3, c3, i3)
     o3 = outputs()
     for k, spec in enumerate(specs):
+        aux = o3[k - 1] if paired[k] else spec.get("aux")
         ops.linear_w8a8(q3, c3, spec["weight"], spec["weight_scales"], o3[k], spec["epilogue"],
-                        spec["block"], spec.get("aux"), spec.get("bias"))
+                        spec["block"], aux, spec.get("bias"))
     # one launch
     s1 = torch.empty_like(s3)
     q1 = torch.zeros_like(q3)
     c1 = torch.zeros_like(c3)
     i1 = torch.zeros(1, dtype=torch.int32, device=gpu)
     o1 = outputs()
-    plist = [dict(spec, out=o1[k]) for k, spec in enumerate(specs)]
+    plist = [dict(spec, out=o1[k], **({"aux": o1[k - 1]} if paired[k] else {}))
+             for k, spec in enumerate(specs)]
     ops.add_rms_norm_linear_w8a8(da, db if add else None, s1 if add else None, dw, plist, q1, c1,
                                  i1)
     torch.cuda.synchronize()
