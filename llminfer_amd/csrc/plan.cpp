@@ -232,6 +232,11 @@ private:
   void prepare_fusions();
   void prepare_norm_quantize();
   void merge_norm_linears();
+  // A one-row step's DeltaGates projections launch at their own ops.
+  bool early_gates(size_t producer) const {
+    const unsigned k = fusion_[producer].kind;
+    return g_.tokens == 1 && (k == LLMI_LINEAR_DELTA_DECAY || k == LLMI_LINEAR_DELTA_BETA);
+  }
   int lower(size_t index);
   int dense(uint32_t id, Ref &out);
   int linear(size_t producer, uint32_t result, int64_t aux, int64_t bias);
@@ -823,6 +828,8 @@ int Lowering::lower(size_t i) {
   }
   case LLMI_GRAPH_DELTA_GATES: {
     const int64_t a = value(in[0]).defining_op;
+    if (a >= 0 && early_gates((size_t)a))
+      return LLMI_HIP_OK; // both projections launched at their own ops
     if (a >= 0 && fusion_[a].kind == LLMI_LINEAR_DELTA_DECAY) {
       if (int rc = linear(a, out[1], in[2], in[3]))
         return rc;
@@ -929,9 +936,6 @@ int Lowering::run() {
   for (index_ = 0; index_ < g_.op_count; ++index_) {
     arena_.release_before(index_);
     const Fusion &f = fusion_[index_];
-    if (f.deferred())
-      continue; // runs at its consumer, into the consumer's output
-    const auto &o = op(index_);
     auto allocate = [&](const llmi_graph_op &of, bool f32) {
       for (uint32_t j = 0; j < of.output_count; ++j) {
         const uint32_t id = of.outputs[j];
@@ -943,6 +947,22 @@ int Lowering::run() {
                                                           lastUse_[id])};
       }
     };
+    if (early_gates(index_)) {
+      // DeltaGates' a / b projection of a one-row step, launched here into
+      // DeltaGates' outputs (its record: this op, fused into DeltaGates), so
+      // that it can join the norm launch before it
+      const auto &c = op(f.consumer);
+      allocate(c, false);
+      const int rc = f.kind == LLMI_LINEAR_DELTA_DECAY
+                         ? linear(index_, c.outputs[1], c.inputs[2], c.inputs[3])
+                         : linear(index_, c.outputs[0], -1, -1);
+      if (rc)
+        return rc;
+      continue;
+    }
+    if (f.deferred())
+      continue; // runs at its consumer, into the consumer's output
+    const auto &o = op(index_);
     if (normQuantize_[index_] >= 0)
       allocate(op(normQuantize_[index_]), false); // the norm itself stores nothing
     else

@@ -90,21 +90,23 @@ def test_qwen35_4b_lowers_with_the_hot_kernels():
     kinds = Counter(d["kernel"] for d in decode.dispatches)
     # every hidden-width norm, its quantization and the residual Add before
     # it (all but the first layer's) in one launch, and in decode the
-    # projections right after it too (DeltaNet qkv and z, attention q, k
-    # and v, the MLP's up and its SwiGLU gate), each op recorded: the first
-    # layer's norm with its two projections alone, 23 DeltaNet, 8 attention
-    # and 32 MLP norms with their Add (3 + 2, 3 + 3, 3 + 2 records); the
-    # final norm before the head, whose GEMV stays its own launch
-    assert kinds["rmsNormLinearW8A8"] == 2 + 2
-    assert kinds["addRmsNormLinearW8A8"] == 23 * 5 + 8 * 6 + 32 * 5
+    # projections right after it too (DeltaNet qkv, z, a and b — a and b
+    # launched at their own ops in a one-row step, recorded as fused into
+    # DeltaGates —, attention q, k and v, the MLP's up and its SwiGLU gate),
+    # each op recorded: the first layer's norm with its four projections
+    # alone, 23 DeltaNet, 8 attention and 32 MLP norms with their Add
+    # (3 + 4, 3 + 3, 3 + 2 records); the final norm before the head, whose
+    # GEMV stays its own launch
+    assert kinds["rmsNormLinearW8A8"] == 2 + 4
+    assert kinds["addRmsNormLinearW8A8"] == 23 * 7 + 8 * 6 + 32 * 5
     assert kinds["addRmsNormQuantize"] == 3 and kinds["rmsNormQuantize"] == 0
-    # the rest: DeltaNet a, b (at DeltaGates) and out; attention out; the
-    # MLP's down; the head
-    assert kinds["linearW8A8Gemv"] == 24 * 3 + 8 * 1 + 32 * 1 + 1
+    # the rest: the DeltaNet and attention out projections, the MLP's down,
+    # the head
+    assert kinds["linearW8A8Gemv"] == 24 + 8 + 32 + 1
     assert kinds["gqaDecodeSplitK"] == 8 and kinds["deltaRecurrent"] == 24
     # a launch that serves several ops (the Adds, norms, quantizations and
-    # projections above) has a record for each: 732 records, 467 launches
-    assert len(decode.dispatches) == 732 and decode.launches == 467
+    # projections above) has a record for each: 732 records, 419 launches
+    assert len(decode.dispatches) == 732 and decode.launches == 419
     assert kinds["residualAdd"] == 0
     assert "quantizeActivation" in kinds     # the others (after GQA / gated norms, SwiGLU)
     indices = [d["op_index"] for d in decode.dispatches]
