@@ -40,7 +40,7 @@ struct Ref {
 enum class Launch : uint8_t {
   Embedding, EmbeddingW8, Quantize, LinearW8, LinearF16, RmsNorm, GatedRmsNorm,
   GatedRmsNormActivated, L2Norm, Elementwise, SigmoidMul, PartialRope, CausalConv, DeltaGates,
-  DeltaUpdate, KvAppend, CausalGqa, CopyView, AddNormQuantize, AddNormLinear
+  DeltaUpdate, KvAppend, CausalGqa, CopyView, AddNormQuantize, AddNormLinear, L2DeltaUpdate
 };
 
 // One plan record of a launch that serves several ops.
@@ -77,6 +77,7 @@ struct Dispatch {
   std::vector<const char *> kernels;
   std::vector<size_t> ops; // a launch serving several ops: a record for each
   std::vector<Rec> recs;   // ... with their epilogues (replaces ops when set)
+  float epsilon = 0.0f, scale = 0.0f; // L2DeltaUpdate: the q / k norms
   Ref proj[kNormLinearMax][5]; // AddNormLinear: weight, scales, output, aux, bias
 };
 
@@ -263,6 +264,8 @@ private:
   std::vector<unsigned> uses_;   // non-view uses of each root
   std::vector<int64_t> normQuantize_, normAdd_; // by RmsNorm op: the fused ops
   std::vector<char> skip_;       // launched by a fused launch at another op
+  std::vector<std::pair<int64_t, int64_t>> l2Delta_; // by DeltaUpdate op: its q / k L2Norms
+  void prepare_l2_delta();
 };
 
 int Lowering::validate() {
@@ -484,6 +487,50 @@ void Lowering::prepare_norm_quantize() {
     } else {
       lastUse_[root_[h]] = std::max(lastUse_[root_[h]], until);
     }
+  }
+}
+
+// L2Norm(q) and L2Norm(k) whose only consumer is the DeltaUpdate of a
+// one-row step, with nothing launched between them and it, at the shapes
+// the fused kernels take (dk 64 or 128, dv a multiple of 16): the update
+// normalises the fp16 rows as it loads them (llmi_hip_l2_norm_delta_update,
+// the same bits), recorded under each of the three ops.
+void Lowering::prepare_l2_delta() {
+  l2Delta_.assign(g_.op_count, {-1, -1});
+  if (g_.tokens != 1)
+    return;
+  for (size_t u = 0; u < g_.op_count; ++u) {
+    const auto &o = op(u);
+    if (o.kind != LLMI_GRAPH_DELTA_UPDATE)
+      continue;
+    const int64_t qo = value(o.inputs[0]).defining_op, ko = value(o.inputs[1]).defining_op;
+    if (qo < 0 || ko < 0 || op(qo).kind != LLMI_GRAPH_L2_NORM ||
+        op(ko).kind != LLMI_GRAPH_L2_NORM || uses_[o.inputs[0]] != 1 ||
+        uses_[o.inputs[1]] != 1 || skip_[qo] || skip_[ko])
+      continue;
+    const auto &qn = op(qo), &kn = op(ko);
+    const uint64_t dk = g_.states[o.state].shape[1], dv = g_.states[o.state].shape[2];
+    // the shapes the fused update kernels take
+    if ((dk != 64 && dk != 128) || dv % 16 != 0)
+      continue;
+    if (qn.epsilon != kn.epsilon || kn.scale != 1.0f || qn.group_width != dk ||
+        kn.group_width != dk || value(qn.inputs[0]).element != LLMI_GRAPH_F16 ||
+        value(kn.inputs[0]).element != LLMI_GRAPH_F16 || !contiguous(qn.inputs[0]) ||
+        !contiguous(kn.inputs[0]))
+      continue;
+    bool quiet = true; // nothing launched between the norms and the update
+    for (size_t j = (size_t)std::max(qo, ko) + 1; j < u && quiet; ++j) {
+      const auto &x = op(j);
+      const int64_t a = x.kind == LLMI_GRAPH_DELTA_GATES ? value(x.inputs[0]).defining_op : -1;
+      quiet = x.kind == LLMI_GRAPH_RESHAPE || x.kind == LLMI_GRAPH_SLICE ||
+              (a >= 0 && early_gates((size_t)a));
+    }
+    if (!quiet || std::min(qo, ko) + 1 != std::max(qo, ko))
+      continue;
+    l2Delta_[u] = {qo, ko};
+    skip_[qo] = skip_[ko] = 1;
+    for (uint32_t x : {qn.inputs[0], kn.inputs[0]})
+      lastUse_[root_[x]] = std::max(lastUse_[root_[x]], u);
   }
 }
 
@@ -846,12 +893,32 @@ int Lowering::lower(size_t i) {
     return LLMI_HIP_OK;
   }
   case LLMI_GRAPH_DELTA_UPDATE: {
-    if (int rc = dense_all({{in[0], 0}, {in[1], 1}, {in[2], 2}, {in[3], 3}, {in[4], 4},
-                            {out[0], 5}}))
-      return rc;
     const auto &s = g_.states[o.state];
     GraphDeltaParams p{(unsigned)g_.tokens, (unsigned)(dim(in[0], 1) / s.shape[1]),
                        (unsigned)s.shape[1], (unsigned)s.shape[0], (unsigned)s.shape[2]};
+    if (l2Delta_[i].first >= 0) {
+      const auto &qn = op(l2Delta_[i].first), &kn = op(l2Delta_[i].second);
+      if (int rc = dense_all({{qn.inputs[0], 0}, {kn.inputs[0], 1}, {in[2], 2}, {in[3], 3},
+                              {in[4], 4}, {out[0], 5}}))
+        return rc;
+      if (llmi_hip_delta_workspace_bytes(p) != 0)
+        return fail(LLMI_HIP_UNSUPPORTED, "plan: op %zu: a one-row update with a workspace", i);
+      Dispatch &d = emit(Launch::L2DeltaUpdate, llmi_hip_kernel_name(LLMI_HIP_OP_DELTA_UPDATE,
+                                                                     &p, 0));
+      d.p.delta = p;
+      d.epsilon = qn.epsilon;
+      d.scale = qn.scale;
+      for (int k = 0; k < 5; ++k)
+        d.buf[k] = r[k];
+      d.buf[5] = state(o.state);
+      d.buf[6] = r[5];
+      d.ops = {(size_t)std::min(l2Delta_[i].first, l2Delta_[i].second),
+               (size_t)std::max(l2Delta_[i].first, l2Delta_[i].second), i};
+      return LLMI_HIP_OK;
+    }
+    if (int rc = dense_all({{in[0], 0}, {in[1], 1}, {in[2], 2}, {in[3], 3}, {in[4], 4},
+                            {out[0], 5}}))
+      return rc;
     const unsigned n = llmi_hip_dispatch_count(LLMI_HIP_OP_DELTA_UPDATE, &p);
     if (n == 0)
       return fail(LLMI_HIP_UNSUPPORTED, "plan: op %zu: %s", i, llmi_hip_last_error());
@@ -922,6 +989,7 @@ int Lowering::run() {
   prepare_values();
   prepare_fusions();
   prepare_norm_quantize();
+  prepare_l2_delta();
   if (g_.output_count) {
     const uint32_t id = g_.outputs[0];
     const auto &v = value(id);
@@ -1087,6 +1155,9 @@ int run_dispatch(const Dispatch &d, const Bases &b, hipStream_t stream) {
                                d.workspaceBytes, stream);
   case Launch::CopyView:
     return llmi_hip_copy_half_view(u16(0), u16(1), d.p.view, stream);
+  case Launch::L2DeltaUpdate:
+    return llmi_hip_l2_norm_delta_update(u16(0), u16(1), u16(2), f32(3), f32(4), f32(5), u16(6),
+                                         d.p.delta, d.epsilon, d.scale, nullptr, 0, stream);
   case Launch::AddNormQuantize:
     return llmi_hip_add_rms_norm_quantize(u16(0), u16(1), u16(2), f32(3), (int8_t *)x[4],
                                           f32(5), (uint32_t *)x[6], d.p.row, stream);

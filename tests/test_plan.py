@@ -103,10 +103,13 @@ def test_qwen35_4b_lowers_with_the_hot_kernels():
     # the rest: the DeltaNet and attention out projections, the MLP's down,
     # the head
     assert kinds["linearW8A8Gemv"] == 24 + 8 + 32 + 1
-    assert kinds["gqaDecodeSplitK"] == 8 and kinds["deltaRecurrent"] == 24
+    # the q and k L2Norms run inside the one-row DeltaUpdate's loads
+    # (llmi_hip_l2_norm_delta_update), recorded under its kernel
+    assert kinds["gqaDecodeSplitK"] == 8 and kinds["deltaRecurrent"] == 24 * 3
+    assert kinds["l2NormF32"] == 0
     # a launch that serves several ops (the Adds, norms, quantizations and
-    # projections above) has a record for each: 732 records, 419 launches
-    assert len(decode.dispatches) == 732 and decode.launches == 419
+    # projections above) has a record for each: 732 records, 371 launches
+    assert len(decode.dispatches) == 732 and decode.launches == 371
     assert kinds["residualAdd"] == 0
     assert "quantizeActivation" in kinds     # the others (after GQA / gated norms, SwiGLU)
     indices = [d["op_index"] for d in decode.dispatches]
@@ -120,6 +123,7 @@ def test_qwen35_4b_lowers_with_the_hot_kernels():
     # norm takes the last row, a view, without its Add); the head stays a GEMV
     assert kinds["rmsNormQuantize"] == 2 + 2 and kinds["addRmsNormQuantize"] == 63 * 3
     assert "addRmsNormLinearW8A8" not in kinds and kinds["linearW8A8Gemv"] == 1
+    assert kinds["l2NormF32"] == 48
     # the MLP down projection and the head: at most a few hundred MB of scratch
     assert prefill.scratch_bytes < 512 << 20
 

@@ -190,4 +190,5 @@ def test_qwen35_4b_decode_step(gpu):
     r = session.step([7], "last", trace=True)
     assert r.past == 65 and np.isfinite(r.logits).all()
     kinds = [d["kernel"] for d in r.dispatches]
-    assert kinds.count("gqaDecodeSplitK") == 8 and kinds.count("deltaRecurrent") == 24
+    # deltaRecurrent: the update and its fused q / k L2Norms, a record each
+    assert kinds.count("gqaDecodeSplitK") == 8 and kinds.count("deltaRecurrent") == 24 * 3
