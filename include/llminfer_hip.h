@@ -545,6 +545,19 @@ LLMI_HIP_API int llmi_hip_add_rms_norm_linear_w8a8(const uint16_t *a, const uint
                                                    const llmi_hip_norm_projection *projections,
                                                    NormLinearParams p, void *stream);
 
+/* llmi_hip_gated_rms_norm_activated of rows x width followed by
+ * llmi_hip_quantize_activation of its output (the flattened rows, 32-wide
+ * groups), in one launch (no counterpart in the reference, which launches
+ * the two; the plan uses it where the quantization reads the norm's output
+ * right after it). out, q, scales and *invalid receive the two launches'
+ * bits. width a multiple of 32 and at most 256; x, gate, out and q 16-byte
+ * aligned (else LLMI_HIP_UNSUPPORTED). */
+LLMI_HIP_API int llmi_hip_gated_rms_norm_activated_quantize(const uint16_t *x, const float *gate,
+                                                            const float *weight, uint16_t *out,
+                                                            int8_t *q, float *scales,
+                                                            uint32_t *invalid, RowParams p,
+                                                            void *stream);
+
 /* ----------------------------------------------------------------- helpers */
 
 /* Zero a workspace (enqueued on `stream`). No kernel of this library needs

@@ -197,6 +197,8 @@ SIGNATURES = {
     "llmi_hip_add_rms_norm_quantize": (C.c_int, [_P, _P, _P, _P, _P, _P, _P, RowParams, _P]),
     "llmi_hip_add_rms_norm_linear_w8a8": (C.c_int, [_P, _P, _P, _P, _P, _P, _P, _P,
                                                     NormLinearParams, _P]),
+    "llmi_hip_gated_rms_norm_activated_quantize": (C.c_int, [_P, _P, _P, _P, _P, _P, _P,
+                                                             RowParams, _P]),
     "llmi_hip_workspace_init": (C.c_int, [_P, _SZ, _P]),
     "llmi_hip_dispatch_count": (C.c_uint, [C.c_int, _P]),
     "llmi_hip_kernel_name": (C.c_char_p, [C.c_int, _P, C.c_uint]),

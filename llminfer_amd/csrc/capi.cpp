@@ -475,6 +475,27 @@ int llmi_hip_add_rms_norm_linear_w8a8(const uint16_t *a, const uint16_t *b, uint
                   b ? "addRmsNormLinearW8A8" : "rmsNormLinearW8A8");
 }
 
+int llmi_hip_gated_rms_norm_activated_quantize(const uint16_t *x, const float *gate,
+                                               const float *weight, uint16_t *out, int8_t *q,
+                                               float *scales, uint32_t *invalid, RowParams p,
+                                               void *stream) {
+  if (p.rows == 0 || p.width == 0)
+    return LLMI_HIP_OK;
+  if (!x || !gate || !weight || !out || !q || !scales)
+    return fail(LLMI_HIP_INVALID_ARGUMENT, "gatedRmsNormQuantize: null buffer");
+  if (!fits32(p.rows, p.width, 1))
+    return fail(LLMI_HIP_INVALID_ARGUMENT, "gatedRmsNormQuantize: exceeds the 32-bit index range");
+  if (!gated_rms_norm_quantize_supported(p.width, x, gate, out, q))
+    return fail(LLMI_HIP_UNSUPPORTED,
+                "gatedRmsNormQuantize: width %u (a multiple of 32, at most 256) or an unaligned "
+                "buffer",
+                p.width);
+  return launched(launch_gated_rms_norm_quantize(x, gate, weight, out, q, scales, invalid, p.rows,
+                                                 p.width, p.epsilon,
+                                                 static_cast<hipStream_t>(stream)),
+                  "gatedRmsNormQuantize");
+}
+
 static int check_view(const HalfViewParams &p) {
   uint64_t last = p.offset;
   for (int d = 0; d < 3; ++d) {

@@ -247,13 +247,18 @@ __global__ __launch_bounds__(256) void gated_rms_norm_rows(const uint16_t *__res
 // multiple of 8, <= 256) per wave, staged in LDS like l2_norm_tile; out =
 // fp16(fp16(x * scale) * w * g) with g = silu(gate) for an fp16 gate (an
 // estimate that the margin test accepts, else exact) or the fp32 gate.
-template <bool kActivated>
+// kQuant: the stored fp16 rows also quantized (quantizeActivation's
+// expressions over the flattened rows: 32-wide groups, four lanes' chunks
+// of eight, width a multiple of 32) into qout, scales and the invalid flag.
+template <bool kActivated, bool kQuant>
 __global__ __launch_bounds__(64) void gated_rms_norm_tile(const uint16_t *__restrict__ in,
                                                           const void *__restrict__ gate,
                                                           const float *__restrict__ w,
                                                           uint16_t *__restrict__ out,
                                                           unsigned rows, unsigned width,
-                                                          float eps) {
+                                                          float eps, int8_t *__restrict__ qout,
+                                                          float *__restrict__ scales,
+                                                          unsigned *invalid) {
   __shared__ __align__(16) uint16_t tile[kL2Rows * (256 + 8)];
   __shared__ float fac[kL2Rows];
   const unsigned lane = threadIdx.x, pitch = width + 8, cpr = width / 8;
@@ -334,6 +339,39 @@ __global__ __launch_bounds__(64) void gated_rms_norm_tile(const uint16_t *__rest
     for (int e = 0; e < 4; ++e)
       o[e] = (uint32_t)f2h(y[2 * e]) | ((uint32_t)f2h(y[2 * e + 1]) << 16);
     *reinterpret_cast<uint4_t *>(out + base) = o;
+    if constexpr (kQuant) {
+      float x[8], max_abs = 0.0f;
+      bool finite = true;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        x[e] = h2f(f2h(y[e]));
+        finite = finite && __builtin_isfinite(x[e]);
+        max_abs = fmaxf(max_abs, fabsf(x[e]));
+      }
+#pragma unroll
+      for (int m = 1; m < 4; m *= 2) {
+        max_abs = fmaxf(max_abs, __shfl_xor(max_abs, m, 4));
+        finite = __shfl_xor((int)finite, m, 4) && finite;
+      }
+      const float qs = finite && max_abs > 0.0f ? __fdiv_rn(max_abs, 127.0f) : 1.0f;
+      uint32_t words[2] = {0u, 0u};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        int r = 0;
+        if (finite) {
+          const float v = fminf(fmaxf(__fdiv_rn(x[e], qs), -127.0f), 127.0f);
+          r = (int)__builtin_rintf(v);
+        }
+        words[e / 4] |= ((uint32_t)r & 0xFFu) << (8 * (e % 4));
+      }
+      reinterpret_cast<uint32_t *>(qout + base)[0] = words[0];
+      reinterpret_cast<uint32_t *>(qout + base)[1] = words[1];
+      if ((c & 3u) == 0) {
+        scales[base / 32] = qs;
+        if (!finite && invalid)
+          atomicOr(invalid, 1u);
+      }
+    }
   }
 }
 
@@ -410,11 +448,28 @@ hipError_t launch_gated_rms_norm(const uint16_t *in, const void *gate, bool acti
   }
   dim3 grid((rows + kL2Rows - 1) / kL2Rows);
   if (activated)
-    hipLaunchKernelGGL(gated_rms_norm_tile<true>, grid, dim3(64), 0, stream, in, gate, w, out,
-                       rows, width, eps);
+    hipLaunchKernelGGL((gated_rms_norm_tile<true, false>), grid, dim3(64), 0, stream, in, gate,
+                       w, out, rows, width, eps, nullptr, nullptr, nullptr);
   else
-    hipLaunchKernelGGL(gated_rms_norm_tile<false>, grid, dim3(64), 0, stream, in, gate, w, out,
-                       rows, width, eps);
+    hipLaunchKernelGGL((gated_rms_norm_tile<false, false>), grid, dim3(64), 0, stream, in, gate,
+                       w, out, rows, width, eps, nullptr, nullptr, nullptr);
+  return hipGetLastError();
+}
+
+bool gated_rms_norm_quantize_supported(unsigned width, const void *in, const void *gate,
+                                       const void *out, const void *q) {
+  return width % 32 == 0 && gated_rms_norm_tiled(width, in, gate, out) && aligned16(q);
+}
+
+hipError_t launch_gated_rms_norm_quantize(const uint16_t *in, const float *gate, const float *w,
+                                          uint16_t *out, int8_t *q, float *scales,
+                                          unsigned *invalid, unsigned rows, unsigned width,
+                                          float eps, hipStream_t stream) {
+  if (rows == 0)
+    return hipSuccess;
+  hipLaunchKernelGGL((gated_rms_norm_tile<true, true>), dim3((rows + kL2Rows - 1) / kL2Rows),
+                     dim3(64), 0, stream, in, gate, w, out, rows, width, eps, q, scales,
+                     invalid);
   return hipGetLastError();
 }
 

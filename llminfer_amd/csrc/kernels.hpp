@@ -175,6 +175,14 @@ hipError_t launch_l2_norm(const uint16_t *in, float *out, unsigned rows, unsigne
 // The LDS-tiled kernel (width a multiple of 8 up to 256, 16-byte aligned
 // buffers); other shapes take a thread per row.
 bool gated_rms_norm_tiled(unsigned width, const void *in, const void *gate, const void *out);
+// The activated gated norm with the quantization of its rows in one launch
+// (delta_front.hip): width a multiple of 32 on the tiled path.
+bool gated_rms_norm_quantize_supported(unsigned width, const void *in, const void *gate,
+                                       const void *out, const void *q);
+hipError_t launch_gated_rms_norm_quantize(const uint16_t *in, const float *gate, const float *w,
+                                          uint16_t *out, int8_t *q, float *scales,
+                                          unsigned *invalid, unsigned rows, unsigned width,
+                                          float eps, hipStream_t stream);
 hipError_t launch_gated_rms_norm(const uint16_t *in, const void *gate, bool activated,
                                  const float *w, uint16_t *out, unsigned rows, unsigned width,
                                  float eps, hipStream_t stream);

@@ -40,7 +40,8 @@ struct Ref {
 enum class Launch : uint8_t {
   Embedding, EmbeddingW8, Quantize, LinearW8, LinearF16, RmsNorm, GatedRmsNorm,
   GatedRmsNormActivated, L2Norm, Elementwise, SigmoidMul, PartialRope, CausalConv, DeltaGates,
-  DeltaUpdate, KvAppend, CausalGqa, CopyView, AddNormQuantize, AddNormLinear, L2DeltaUpdate
+  DeltaUpdate, KvAppend, CausalGqa, CopyView, AddNormQuantize, AddNormLinear, L2DeltaUpdate,
+  GatedNormQuantize
 };
 
 // One plan record of a launch that serves several ops.
@@ -496,6 +497,16 @@ void Lowering::prepare_norm_quantize() {
 // normalises the fp16 rows as it loads them (llmi_hip_l2_norm_delta_update,
 // the same bits), recorded under each of the three ops.
 void Lowering::prepare_l2_delta() {
+  // A quantization right after the GatedRmsNorm that produced its input may
+  // launch with it (merge_norm_linears): the norm's inputs stay live until
+  // the quantization, which writes while the launch reads them.
+  for (size_t j = 1; j < g_.op_count; ++j)
+    if (op(j).kind == LLMI_GRAPH_QUANTIZE_ACTIVATION && op(j - 1).kind == LLMI_GRAPH_GATED_RMS_NORM &&
+        op(j).inputs[0] == op(j - 1).outputs[0])
+      for (uint32_t x = 0; x < op(j - 1).input_count; ++x) {
+        const size_t r = root_[op(j - 1).inputs[x]];
+        lastUse_[r] = std::max(lastUse_[r], j);
+      }
   l2Delta_.assign(g_.op_count, {-1, -1});
   if (g_.tokens != 1)
     return;
@@ -557,6 +568,34 @@ void Lowering::merge_norm_linears() {
   out.reserve(ds.size());
   for (size_t i = 0; i < ds.size(); ++i) {
     const Dispatch &d = ds[i];
+    // The activated gated norm and the quantization of its output right
+    // after it (llmi_hip_gated_rms_norm_activated_quantize).
+    if (d.launch == Launch::GatedRmsNormActivated && i + 1 < ds.size() &&
+        ds[i + 1].launch == Launch::Quantize) {
+      const Dispatch &qd = ds[i + 1];
+      const RowParams &nr = d.p.row;
+      const QuantizeParams &qp = qd.p.quantize;
+      const uint64_t n = (uint64_t)nr.rows * nr.width;
+      const Range qr{qd.buf[1], n}, sr{qd.buf[2], n / 8};
+      bool clash = false; // with the fp16 input, the fp32 gate, the weight, the fp16 output
+      const uint64_t bytes[4] = {2 * n, 4 * n, 4ull * nr.width, 2 * n};
+      for (int k = 0; k < 4; ++k)
+        clash = clash || overlap(qr, {d.buf[k], bytes[k]}) || overlap(sr, {d.buf[k], bytes[k]});
+      if (qd.buf[0].space == d.buf[3].space && qd.buf[0].index == d.buf[3].index &&
+          qd.buf[0].offset == d.buf[3].offset && nr.width % 32 == 0 && nr.width <= 256 &&
+          (uint64_t)qp.rows * qp.width == n && qp.groups * 32 == qp.width && !clash) {
+        Dispatch m = d;
+        m.launch = Launch::GatedNormQuantize;
+        m.buf[4] = qd.buf[1];
+        m.buf[5] = qd.buf[2];
+        m.buf[6] = qd.buf[3];
+        m.kernels = {"gatedRmsNormQuantize"};
+        m.recs = {{d.opIndex, nullptr, 0}, {qd.opIndex, nullptr, 0}};
+        out.push_back(std::move(m));
+        ++i;
+        continue;
+      }
+    }
     const RowParams &row = d.p.row;
     if (d.launch != Launch::AddNormQuantize || row.rows != 1 || row.width > kNormLinearMaxWidth) {
       out.push_back(d);
@@ -1155,6 +1194,10 @@ int run_dispatch(const Dispatch &d, const Bases &b, hipStream_t stream) {
                                d.workspaceBytes, stream);
   case Launch::CopyView:
     return llmi_hip_copy_half_view(u16(0), u16(1), d.p.view, stream);
+  case Launch::GatedNormQuantize:
+    return llmi_hip_gated_rms_norm_activated_quantize(u16(0), f32(1), f32(2), u16(3),
+                                                      (int8_t *)x[4], f32(5), (uint32_t *)x[6],
+                                                      d.p.row, stream);
   case Launch::L2DeltaUpdate:
     return llmi_hip_l2_norm_delta_update(u16(0), u16(1), u16(2), f32(3), f32(4), f32(5), u16(6),
                                          d.p.delta, d.epsilon, d.scale, nullptr, 0, stream);

@@ -411,6 +411,30 @@ def add_rms_norm_linear_w8a8(*args, **kwargs) -> None:
     bind_add_rms_norm_linear_w8a8(*args, **kwargs)()
 
 
+def gated_rms_norm_activated_quantize(x: torch.Tensor, gate: torch.Tensor, weight: torch.Tensor,
+                                      out: torch.Tensor, q: torch.Tensor, scales: torch.Tensor,
+                                      invalid: torch.Tensor | None = None,
+                                      epsilon: float = 1e-6) -> None:
+    """gated_rms_norm_activated of x [rows, width] (gate fp32, weight [width]
+    fp32) into out, and quantize_activation of out's flattened rows into q
+    [n * 32] int8 and scales [n] fp32, n = rows * width / 32, one launch."""
+    _require(x, torch.float16, "x")
+    _require(gate, torch.float32, "gate")
+    _require(weight, torch.float32, "weight")
+    _require(out, torch.float16, "out")
+    _require(q, torch.int8, "q")
+    _require(scales, torch.float32, "scales")
+    rows, width = x.shape
+    if gate.shape != x.shape or out.shape != x.shape or weight.numel() != width or \
+            q.numel() != rows * width or scales.numel() * 32 != rows * width:
+        raise ValueError("x, gate, out [rows, width], weight [width], q, scales disagree")
+    if invalid is not None:
+        _require(invalid, torch.int32, "invalid")
+    _lib.check(_lib.load().llmi_hip_gated_rms_norm_activated_quantize(
+        _ptr(x), _ptr(gate), _ptr(weight), _ptr(out), _ptr(q), _ptr(scales), _ptr(invalid),
+        _lib.RowParams(rows, width, epsilon), _stream()))
+
+
 def bind_causal_conv(x: torch.Tensor, weight: torch.Tensor, history: torch.Tensor | None,
                      out: torch.Tensor, silu: bool = True) -> "Bound":
     """causalConv (Reference.metal:137-161): x, out [T, C] fp16; weight [C, k]

@@ -103,13 +103,15 @@ def test_qwen35_4b_lowers_with_the_hot_kernels():
     # the rest: the DeltaNet and attention out projections, the MLP's down,
     # the head
     assert kinds["linearW8A8Gemv"] == 24 + 8 + 32 + 1
+    # each DeltaNet layer's gated norm with the quantization of its output
+    assert kinds["gatedRmsNormQuantize"] == 24 * 2 and kinds["quantizeActivation"] == 40
     # the q and k L2Norms run inside the one-row DeltaUpdate's loads
     # (llmi_hip_l2_norm_delta_update), recorded under its kernel
     assert kinds["gqaDecodeSplitK"] == 8 and kinds["deltaRecurrent"] == 24 * 3
     assert kinds["l2NormF32"] == 0
     # a launch that serves several ops (the Adds, norms, quantizations and
-    # projections above) has a record for each: 732 records, 371 launches
-    assert len(decode.dispatches) == 732 and decode.launches == 371
+    # projections above) has a record for each: 732 records, 347 launches
+    assert len(decode.dispatches) == 732 and decode.launches == 347
     assert kinds["residualAdd"] == 0
     assert "quantizeActivation" in kinds     # the others (after GQA / gated norms, SwiGLU)
     indices = [d["op_index"] for d in decode.dispatches]

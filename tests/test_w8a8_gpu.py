@@ -356,3 +356,36 @@ def test_add_rms_norm_linear_without_q(gpu):
                                  [{"weight": wt, "weight_scales": ws, "out": got}])
     torch.cuda.synchronize()
     assert torch.equal(got.view(torch.int16), want.view(torch.int16))
+
+
+@pytest.mark.parametrize("rows,width", [(32, 128), (1024 * 32, 128), (5, 256), (3, 32)])
+@pytest.mark.parametrize("special", [False, True])
+def test_gated_norm_quantize_is_the_two_ops(gpu, rows, width, special):
+    """The activated gated RMSNorm and the quantization of its output in one
+    launch equal gated_rms_norm (fp32 gate) followed by quantize_activation
+    of the flattened rows, bit for bit: the normalised rows, the int8 rows,
+    the scales and the invalid flag (special: an infinite input)."""
+    print(f"gatedRmsNormQuantize rows={rows} width={width} special={special}", flush=True)
+    r = np.random.default_rng(rows + width)
+    x = _f16(r.standard_normal((rows, width)) * 2)
+    if special:
+        x[rows // 2, width // 3] = 0x7C00
+    dx = _u16_dev(x, gpu)
+    gate = _dev((r.standard_normal((rows, width)) * 1.5).astype(np.float32), gpu)
+    w = _dev((r.standard_normal(width) * 0.2).astype(np.float32), gpu)
+    n = rows * width
+    out2 = torch.empty(rows, width, dtype=torch.float16, device=gpu)
+    q2 = torch.empty(1, n, dtype=torch.int8, device=gpu)
+    c2 = torch.empty(1, n // 32, dtype=torch.float32, device=gpu)
+    i2 = torch.zeros(1, dtype=torch.int32, device=gpu)
+    ops.gated_rms_norm(dx, gate, w, out2)
+    ops.quantize_activation(out2.view(1, n), q2, c2, i2)
+    out1 = torch.empty_like(out2)
+    q1, c1 = torch.zeros_like(q2), torch.zeros_like(c2)
+    i1 = torch.zeros(1, dtype=torch.int32, device=gpu)
+    ops.gated_rms_norm_activated_quantize(dx, gate, w, out1, q1, c1, i1)
+    torch.cuda.synchronize()
+    assert np.array_equal(_host_u16(out1), _host_u16(out2))
+    assert torch.equal(q1, q2)
+    assert np.array_equal(c1.cpu().numpy().view(np.uint32), c2.cpu().numpy().view(np.uint32))
+    assert int(i1.item()) == int(i2.item()) == (1 if special else 0)
