@@ -443,10 +443,10 @@ int llmi_hip_add_rms_norm_linear_w8a8(const uint16_t *a, const uint16_t *b, uint
         return fail(LLMI_HIP_INVALID_ARGUMENT,
                     "addRmsNormLinearW8A8: projection %u: SiluMul needs its multiplier (aux)", k);
       mate = k > 0 && x.aux == projections[k - 1].output;
+      // (projection k - 1 has no epilogue, so it is nobody's mate itself)
       if (mate && (p.norm.width > kNormLinearPairedWidth ||
                    p.linear[k - 1].epilogue != LLMI_LINEAR_NONE ||
-                   p.linear[k - 1].columns != l.columns || proj[k - 1].paired ||
-                   (k > 1 && proj[k - 2].paired)))
+                   p.linear[k - 1].columns != l.columns))
         return fail(LLMI_HIP_UNSUPPORTED,
                     "addRmsNormLinearW8A8: projection %u: a SwiGLU multiplier computed in the "
                     "call must be the previous projection's output, with no epilogue, the same "
