@@ -41,7 +41,7 @@ enum class Launch : uint8_t {
   Embedding, EmbeddingW8, Quantize, LinearW8, LinearF16, RmsNorm, GatedRmsNorm,
   GatedRmsNormActivated, L2Norm, Elementwise, SigmoidMul, PartialRope, CausalConv, DeltaGates,
   DeltaUpdate, KvAppend, CausalGqa, CopyView, AddNormQuantize, AddNormLinear, L2DeltaUpdate,
-  GatedNormQuantize
+  GatedNormQuantize, KvAppendGqa
 };
 
 // One plan record of a launch that serves several ops.
@@ -568,6 +568,39 @@ void Lowering::merge_norm_linears() {
   out.reserve(ds.size());
   for (size_t i = 0; i < ds.size(); ++i) {
     const Dispatch &d = ds[i];
+    // A one-token KvAppend and the CausalGqa right after it on the same
+    // caches: the fused decode call (llmi_hip_kv_append_causal_gqa), whose
+    // attention reads the new rows as it appends them.
+    if (d.launch == Launch::KvAppend && i + 1 < ds.size() &&
+        ds[i + 1].launch == Launch::CausalGqa) {
+      const Dispatch &c = ds[i + 1];
+      const GqaParams &gp = c.p.gqa;
+      auto same = [](const Ref &a, const Ref &b) {
+        return a.space == b.space && a.index == b.index && a.offset == b.offset;
+      };
+      const uint64_t row = 2ull * d.p.cache.count; // the new K (or V) row, fp16
+      const Range ws{c.buf[4], c.workspaceBytes};
+      const bool clash = overlap(ws, {d.buf[0], row}) || overlap(ws, {d.buf[1], row}) ||
+                         overlap(ws, {c.buf[0], 2ull * gp.queryHeads * gp.headDim}) ||
+                         overlap(ws, {c.buf[3], 2ull * gp.queryHeads * gp.headDim});
+      if (gp.tokens == 1 && same(d.buf[2], c.buf[1]) && same(d.buf[3], c.buf[2]) && !clash &&
+          llmi_hip_gqa_workspace_bytes(gp) == c.workspaceBytes &&
+          llmi_hip_dispatch_count(LLMI_HIP_OP_KV_APPEND_CAUSAL_GQA, &gp) > 0) {
+        Dispatch m = c;
+        m.launch = Launch::KvAppendGqa;
+        m.opIndex = d.opIndex;
+        m.buf[5] = d.buf[0];
+        m.buf[6] = d.buf[1];
+        m.kernels.clear();
+        for (unsigned k = 0; k < llmi_hip_dispatch_count(LLMI_HIP_OP_KV_APPEND_CAUSAL_GQA, &gp);
+             ++k)
+          m.kernels.push_back(llmi_hip_kernel_name(LLMI_HIP_OP_KV_APPEND_CAUSAL_GQA, &gp, k));
+        m.recs = {{d.opIndex, nullptr, 0}, {c.opIndex, nullptr, 0}};
+        out.push_back(std::move(m));
+        ++i;
+        continue;
+      }
+    }
     // The activated gated norm and the quantization of its output right
     // after it (llmi_hip_gated_rms_norm_activated_quantize).
     if (d.launch == Launch::GatedRmsNormActivated && i + 1 < ds.size() &&
@@ -1081,18 +1114,19 @@ int Lowering::run() {
   }
   plan_.scratchBytes = (arena_.size() + kAlign - 1) / kAlign * kAlign;
   merge_norm_linears();
-  for (const auto &d : plan_.dispatches)
+  for (const auto &d : plan_.dispatches) {
+    for (const Rec &r : d.recs) // op by op, so the records stay in op order
+      for (const char *k : d.kernels)
+        plan_.records.push_back({r.op, k, r.epilogue, r.fused});
+    if (!d.recs.empty())
+      continue;
     for (const char *k : d.kernels) {
-      if (!d.recs.empty()) {
-        for (const Rec &r : d.recs)
-          plan_.records.push_back({r.op, k, r.epilogue, r.fused});
-        continue;
-      }
       if (d.ops.empty())
         plan_.records.push_back({d.opIndex, k, d.epilogue, d.fusedOpIndex});
       for (size_t o : d.ops)
         plan_.records.push_back({o, k, nullptr, 0});
     }
+  }
   plan_.stateCount = g_.state_count;
   return LLMI_HIP_OK;
 }
@@ -1192,6 +1226,9 @@ int run_dispatch(const Dispatch &d, const Bases &b, hipStream_t stream) {
   case Launch::CausalGqa:
     return llmi_hip_causal_gqa(u16(0), u16(1), u16(2), u16(3), d.p.gqa, x[4],
                                d.workspaceBytes, stream);
+  case Launch::KvAppendGqa:
+    return llmi_hip_kv_append_causal_gqa(u16(0), u16(5), u16(6), u16(1), u16(2), u16(3),
+                                         d.p.gqa, x[4], d.workspaceBytes, stream);
   case Launch::CopyView:
     return llmi_hip_copy_half_view(u16(0), u16(1), d.p.view, stream);
   case Launch::GatedNormQuantize:

@@ -107,11 +107,15 @@ def test_qwen35_4b_lowers_with_the_hot_kernels():
     assert kinds["gatedRmsNormQuantize"] == 24 * 2 and kinds["quantizeActivation"] == 40
     # the q and k L2Norms run inside the one-row DeltaUpdate's loads
     # (llmi_hip_l2_norm_delta_update), recorded under its kernel
-    assert kinds["gqaDecodeSplitK"] == 8 and kinds["deltaRecurrent"] == 24 * 3
+    # each attention layer's KvAppend and CausalGqa in the fused decode
+    # call (llmi_hip_kv_append_causal_gqa), both ops recorded under its
+    # split and merge kernels
+    assert kinds["gqaDecodeSplitK"] == kinds["gqaDecodeMerge"] == 8 * 2
+    assert kinds["kvAppend"] == 0 and kinds["deltaRecurrent"] == 24 * 3
     assert kinds["l2NormF32"] == 0
     # a launch that serves several ops (the Adds, norms, quantizations and
-    # projections above) has a record for each: 732 records, 347 launches
-    assert len(decode.dispatches) == 732 and decode.launches == 347
+    # projections above) has a record for each: 740 records, 339 launches
+    assert len(decode.dispatches) == 740 and decode.launches == 339
     assert kinds["residualAdd"] == 0
     assert "quantizeActivation" in kinds     # the others (after GQA / gated norms, SwiGLU)
     indices = [d["op_index"] for d in decode.dispatches]

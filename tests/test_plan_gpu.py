@@ -191,4 +191,5 @@ def test_qwen35_4b_decode_step(gpu):
     assert r.past == 65 and np.isfinite(r.logits).all()
     kinds = [d["kernel"] for d in r.dispatches]
     # deltaRecurrent: the update and its fused q / k L2Norms, a record each
-    assert kinds.count("gqaDecodeSplitK") == 8 and kinds.count("deltaRecurrent") == 24 * 3
+    # gqaDecodeSplitK: KvAppend and CausalGqa in one fused call, a record each
+    assert kinds.count("gqaDecodeSplitK") == 8 * 2 and kinds.count("deltaRecurrent") == 24 * 3
