@@ -8,7 +8,11 @@
 a profile of one configuration then holds that configuration's launches and
 no other's. Without the headline the line carries only `configs`.
 
-Prints ONE JSON line. The headline workload is the GQA single-token decode
+Prints ONE compact JSON line on stdout (under 7.5 KB: the contract's fields,
+the headline's roofline and CPU baseline, and a short summary per
+configuration); the full record of every leg goes to stderr as one
+`[bench-detail] KEY {...}` line per leg, and to `--detail FILE` when given.
+The headline workload is the GQA single-token decode
 of the reference's decode path (KvAppend + CausalGqa, T=1, 4096 past rows,
 capacity 8192, 16 query / 4 KV heads, head_dim 256, fp16): one "step" is one
 attention layer's decode -- KvAppend + CausalGqa, which the backend runs as
@@ -110,6 +114,14 @@ def rows_bytes(T: int, hq: int, hkv: int, d: int) -> dict:
 def cpu_threads() -> int:
     import oracle
     return max(1, min(CPU_THREAD_CAP, oracle.cpu_count()))
+
+
+def host_cores() -> int:
+    """CPUs this process may run on (the box's share), not the thread cap."""
+    try:
+        return len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        return os.cpu_count() or 1
 
 
 def cpu_model() -> str:
@@ -1314,6 +1326,61 @@ def roofline(w: Workload, op_ms: float, steps: int, warmup: int, traffic) -> dic
             "work_unit": "bytes" if w.bound == "hbm" else "flop"}
 
 
+COMPACT_LIMIT = 7500  # bytes of the final stdout line; the driver keeps a bounded tail
+
+
+def _r(x, nd=3):
+    return None if x is None else round(float(x), nd)
+
+
+def compact(result: dict) -> dict:
+    """The final stdout line: the contract's fields, the headline's roofline and
+    CPU baseline, and a short summary per configuration. The full per-leg
+    record goes to stderr (one `[bench-detail]` line per leg) and to --detail."""
+    keep = ("metric", "value", "unit", "n_gpus", "steps", "warmup", "ms_per_step",
+            "higher_is_better", "scaling", "vs_baseline", "dtype", "data", "config",
+            "tokens_per_s")
+    out = {k: result[k] for k in keep if k in result}
+    if "timing" in result:
+        t = result["timing"]
+        out["timing"] = {"cold_median_us": t["cold"]["median_us"],
+                         "cold_p10_us": t["cold"]["p10_us"],
+                         "warm_mean_us": t["warm"]["mean_us"]}
+    if "roofline" in result:
+        rl = result["roofline"]
+        out["roofline"] = {k: rl[k] for k in ("bound", "achieved", "peak", "unit", "frac",
+                                               "traffic", "kernel", "kernel_us_avg",
+                                               "work_per_launch", "work_unit") if k in rl}
+    if "cpu_baseline" in result:
+        cb = result["cpu_baseline"]
+        out["cpu_baseline"] = {k: cb[k] for k in (
+            "value", "unit", "cores", "host_cores", "kind", "sample", "cpu_model",
+            "single_thread_value", "gpu_vs_cpu_max_abs") if k in cb}
+        if isinstance(out["cpu_baseline"].get("sample"), str):
+            out["cpu_baseline"]["sample"] = out["cpu_baseline"]["sample"][:160]
+    confs = {}
+    for key, e in result.get("configs", {}).items():
+        rl = e.get("roofline", {})
+        c = {"us": e.get("us_per_step"), "kernel_us": rl.get("kernel_us_avg"),
+             "bound": rl.get("bound"), "frac": rl.get("frac"), "kernel": rl.get("kernel")}
+        if "hbm_frac" in e and e["hbm_frac"] is not None:
+            c["hbm_frac"] = e["hbm_frac"]
+        for k in ("mfma_frac_recurrent_flops", "delta_hbm_frac", "gqa_hbm_frac"):
+            if k in e:
+                c[k] = e[k]
+        cb = e.get("cpu_baseline")
+        if cb:
+            c["cpu_us"] = _r(cb.get("value"), 1)
+            c["cpu_threads"] = cb.get("cores")
+            for k in ("gpu_vs_cpu_max_abs", "gpu_vs_cpu_state_rel", "gpu_bit_exact"):
+                if k in cb:
+                    c[k] = cb[k]
+        confs[key] = c
+    if confs:
+        out["configs"] = confs
+    return out
+
+
 def load_traffic(workload: str):
     """HBM bytes per launch from the committed rocprofv3 --pmc summary."""
     path = ROOT / "profiles" / "traffic.json"
@@ -1354,6 +1421,7 @@ def headline(dev, args, cyc) -> dict:
     if not args.no_cpu:
         log("cpu baseline (headline)")
         result["cpu_baseline"] = w.cpu(args.cpu_seconds)
+        result["cpu_baseline"]["host_cores"] = host_cores()
     del w
     torch.cuda.empty_cache()
     return result
@@ -1374,6 +1442,8 @@ def main(argv=None) -> int:
     ap.add_argument("--only", default="",
                     help="comma-separated keys of the configurations to run, "
                          "'headline' for the headline (default: all)")
+    ap.add_argument("--detail", default="",
+                    help="also write the full per-leg record as JSON to this file")
     args = ap.parse_args(argv)
 
     if args.gpus != 1:
@@ -1467,14 +1537,26 @@ def main(argv=None) -> int:
                     / HBM_PEAK_GBS, 4)
             if not args.no_cpu:
                 entry["cpu_baseline"] = x.cpu(args.cpu_seconds / 2)
+                entry["cpu_baseline"]["host_cores"] = host_cores()
             log(f"{key}: {entry['us_per_step']} us/step, kernel "
                 f"{entry['roofline']['kernel_us_avg']} us, frac {entry['roofline']['frac']}")
             extra[key] = entry
+            print(f"[bench-detail] {key} {json.dumps(entry)}", file=sys.stderr, flush=True)
             del x
             torch.cuda.empty_cache()
         result["configs"] = extra
 
-    print(json.dumps(result), flush=True)
+    if args.detail:
+        Path(args.detail).parent.mkdir(parents=True, exist_ok=True)
+        Path(args.detail).write_text(json.dumps(result, indent=1) + "\n")
+    line = json.dumps(compact(result))
+    if len(line) > COMPACT_LIMIT:  # never expected; keep the record parseable
+        log(f"compact line {len(line)} B over {COMPACT_LIMIT}: dropping per-config fields")
+        slim = compact(result)
+        slim["configs"] = {k: {"us": v.get("us"), "frac": v.get("frac")}
+                           for k, v in slim.get("configs", {}).items()}
+        line = json.dumps(slim)
+    print(line, flush=True)
     return 0
 
 

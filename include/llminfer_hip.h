@@ -414,6 +414,26 @@ LLMI_HIP_API int llmi_hip_l2_norm_delta_gated_norm(
     uint16_t *out, GraphDeltaParams p, float qk_epsilon, float q_scale, float norm_epsilon,
     void *workspace, size_t workspace_bytes, void *stream);
 
+/* After llmi_hip_l2_norm_delta_gated_norm with the same params and
+ * workspace (no counterpart in the reference, whose Metal dispatches do not
+ * wait for each other inside a launch): the chunked form's scan normalises
+ * a value head's rows only after a bounded wait for all of the head's
+ * workgroups. This call waits for `stream` and returns LLMI_HIP_OK, or
+ * LLMI_HIP_LAUNCH_FAILED if any workgroup's wait gave up (the normalised
+ * rows are then not trustworthy and a session using them must become
+ * invalid, MetalExecutor.mm:283-298). Shapes that take the recurrent form
+ * return LLMI_HIP_OK at once without waiting. */
+LLMI_HIP_API int llmi_hip_l2_norm_delta_gated_norm_status(const void *workspace,
+                                                          size_t workspace_bytes,
+                                                          GraphDeltaParams p, void *stream);
+
+/* Bound, in polls, of that arrival wait for later launches (0: every
+ * workgroup gives up at once); returns the previous bound (default 2^22,
+ * ~0.3 s). Process-wide, not thread-safe against concurrent launches. No
+ * counterpart in the reference: for tests that force the give-up from the
+ * host, so that every workgroup still exits normally. */
+LLMI_HIP_API unsigned llmi_hip_set_arrival_wait_limit(unsigned polls);
+
 /* ------------------------------------------------------- W8A8 projections
  * The quantized projection path of the whole-graph plan (lowered at
  * MetalExecutionPlan.cpp:464-510 for LinearW8A8, :566-580 for

@@ -860,6 +860,32 @@ int llmi_hip_l2_norm_delta_gated_norm(const uint16_t *q, const uint16_t *k, cons
               p.tokens, p.keyDim, p.valueDim, kRecNormMaxT);
 }
 
+int llmi_hip_l2_norm_delta_gated_norm_status(const void *workspace, size_t workspace_bytes,
+                                             GraphDeltaParams p, void *stream) {
+  if (int st = check_delta(p))
+    return st;
+  // Only the chunked form waits for other workgroups.
+  if (select_delta(p) != DeltaKernel::Chunked)
+    return LLMI_HIP_OK;
+  DeltaShape s{p.tokens, p.keyHeads, p.keyDim, p.valueHeads, p.valueDim};
+  if (!workspace || workspace_bytes < delta_chunked_workspace_bytes(s))
+    return fail(LLMI_HIP_WORKSPACE, "GatedRmsNorm status: workspace smaller than the call's");
+  bool gave_up = false;
+  if (int st = launched(delta_chunked_wait_status(workspace, s, static_cast<hipStream_t>(stream),
+                                                  &gave_up),
+                        "GatedRmsNorm status"))
+    return st;
+  if (gave_up)
+    return fail(LLMI_HIP_LAUNCH_FAILED,
+                "L2Norm+DeltaUpdate+GatedRmsNorm: the scan's arrival wait gave up; the "
+                "normalised rows are not trustworthy");
+  return LLMI_HIP_OK;
+}
+
+unsigned llmi_hip_set_arrival_wait_limit(unsigned polls) {
+  return delta_chunked_wait_limit(polls);
+}
+
 int llmi_hip_workspace_init(void *workspace, size_t bytes, void *stream) {
   if (!bytes)
     return LLMI_HIP_OK;

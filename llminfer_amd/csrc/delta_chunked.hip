@@ -51,8 +51,10 @@
 // a.b ~ ah.bh + (ah.bl + al.bh) 2^-11, the cross terms in a second fp32
 // accumulator -- 22 significant bits per operand. A plain fp16 product
 // leaves the fp32 state ~8e-4 relative off the recurrence after 1024 tokens;
-// the split form ~1e-5, well inside the 1e-3 bound. The Gram matrices only
-// feed T and M and stay plain fp16.
+// the split form ~1e-5, well inside the 1e-3 bound. The Gram matrices are
+// split too: in plain fp16 they leave the outputs of small-RMS rows a few
+// percent off (relative to the row), which the gated norm after the update
+// turns into errors of a few output ulps.
 //
 // Decays are linear at the op boundary (Graph.metal:143). The cumulative
 // log decay is summed, and differenced, in double: log(0) is clamped to -1e4
@@ -67,6 +69,8 @@
 #include "capi_internal.hpp"
 
 #include <math.h>
+
+#include <vector>
 
 namespace llmi {
 namespace {
@@ -216,7 +220,11 @@ __global__ __launch_bounds__(256, 1) void delta_prep_kernel(
 
   __shared__ __attribute__((aligned(16))) half_t sKh[C * KS], sKl[C * KS];
   __shared__ __attribute__((aligned(16))) half_t sQV[C * KS]; // Q hi, later a V block
-  __shared__ float sA[C * FS], sTT[C * FS];                   // A and T^T (fp32)
+  // A and T^T (fp32); before them, during the Gram products, Q lo
+  __shared__ __attribute__((aligned(16))) float sATT[2 * C * FS];
+  float *const sA = sATT, *const sTT = sATT + C * FS;
+  half_t *const sQl = reinterpret_cast<half_t *>(sATT);
+  static_assert(C * KS * sizeof(half_t) <= 2 * C * FS * sizeof(float), "Q lo fits");
   __shared__ __attribute__((aligned(16))) half_t sTwh[C * CS], sTwl[C * CS];
   __shared__ __attribute__((aligned(16))) half_t sTbh[C * CS], sTbl[C * CS];
   __shared__ __attribute__((aligned(16))) half_t sMh[C * CS], sMl[C * CS];
@@ -344,6 +352,7 @@ __global__ __launch_bounds__(256, 1) void delta_prep_kernel(
       *reinterpret_cast<half4_t *>(sKh + t * KS + d4) = khi;
       *reinterpret_cast<half4_t *>(sKl + t * KS + d4) = klo;
       *reinterpret_cast<half4_t *>(sQV + t * KS + d4) = qhi;
+      *reinterpret_cast<half4_t *>(sQl + t * KS + d4) = qlo;
     }
   }
   lds_sync();
@@ -364,19 +373,33 @@ __global__ __launch_bounds__(256, 1) void delta_prep_kernel(
     }
   }
 
-  // K K^T and Q K^T (fp16 hi) stay in registers: wave w holds the tiles of
-  // key columns s in [16 w, 16 w + 16) for the four row tiles (register r
-  // of tile mt: t = 16 mt + 4 g + r, s = 16 w + L).
+  // K K^T and Q K^T stay in registers: wave w holds the tiles of key
+  // columns s in [16 w, 16 w + 16) for the four row tiles (register r of
+  // tile mt: t = 16 mt + 4 g + r, s = 16 w + L). Split form: both feed M,
+  // and through M the outputs Y0 = M U0 and Q', where a row's output is
+  // often much smaller than the terms that cancel in it, so a plain fp16
+  // product (2^-11 relative per term) would show in rows of small RMS.
   float4_t kk[4], qk[4];
 #pragma unroll
   for (int mt = 0; mt < 4; ++mt) {
+    float4_t kx{0.0f, 0.0f, 0.0f, 0.0f}, qx{0.0f, 0.0f, 0.0f, 0.0f};
     kk[mt] = qk[mt] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int ks = 0; ks < DK / 32; ++ks) {
-      const half8_t b = load8(sKh + (16 * wave + L) * KS + 32 * ks + 8 * g);
-      kk[mt] = mfma16(load8(sKh + (16 * mt + L) * KS + 32 * ks + 8 * g), b, kk[mt]);
-      qk[mt] = mfma16(load8(sQV + (16 * mt + L) * KS + 32 * ks + 8 * g), b, qk[mt]);
+      const unsigned bo = (16 * wave + L) * KS + 32 * ks + 8 * g;
+      const unsigned ao = (16 * mt + L) * KS + 32 * ks + 8 * g;
+      const half8_t bh = load8(sKh + bo), bl = load8(sKl + bo);
+      const half8_t kah = load8(sKh + ao), kal = load8(sKl + ao);
+      const half8_t qah = load8(sQV + ao), qal = load8(sQl + ao);
+      kk[mt] = mfma16(kah, bh, kk[mt]);
+      qk[mt] = mfma16(qah, bh, qk[mt]);
+      kx = mfma16(kah, bl, kx);
+      qx = mfma16(qah, bl, qx);
+      kx = mfma16(kal, bh, kx);
+      qx = mfma16(qal, bh, qx);
     }
+    kk[mt] += kx * kSplitUnscale;
+    qk[mt] += qx * kSplitUnscale;
   }
 
   for (unsigned hr = 0; hr < R; ++hr) {
@@ -760,14 +783,18 @@ constexpr int kScanThreads = 320;
 // slices), in place: the sequential sum of squares of each row, then out =
 // fp16(fp16(x * factor) * weight * silu(gate)) per element (gated_norm.hpp,
 // the arithmetic of the standalone kernel).
-constexpr unsigned kSpinLimit = 1u << 22; // bound of the arrival wait (~0.3 s)
+// The wait polls at most `spin` times (delta_chunked_wait_limit(), 2^22 by
+// default: ~0.3 s). A workgroup that gives up sets the fourth word of its
+// head's counter record, which delta_chunked_wait_status() reads after the
+// call: the rows it then normalises may not all have been written.
+unsigned g_wait_limit = 1u << 22;
 constexpr unsigned kNormMaxDv = 256; // dv the fused norm supports
 
 template <bool NORM>
 __global__ __launch_bounds__(kScanThreads, 1) void delta_scan_kernel(
     float *__restrict__ state, half_t *__restrict__ out, const void *__restrict__ ws,
     unsigned T, unsigned Hk, unsigned Hv, unsigned DV, const half_t *__restrict__ gate,
-    const float *__restrict__ nweight, unsigned *cnt, float neps) {
+    const float *__restrict__ nweight, unsigned *cnt, float neps, unsigned spin) {
   // Workgroups are dealt to the 8 XCDs round-robin by block index. Give
   // each XCD a contiguous run of (value head, slice) pairs, so that the
   // workgroups reading one value head's pieces and one key head's K^T piece
@@ -1029,23 +1056,27 @@ __global__ __launch_bounds__(kScanThreads, 1) void delta_scan_kernel(
       __hip_atomic_fetch_add(word, 1ull + (1ull << (8 + 7 * (xcc & 7u))), __ATOMIC_RELAXED,
                              __HIP_MEMORY_SCOPE_AGENT);
       unsigned long long seen = 0;
-      for (unsigned i = 0; i < kSpinLimit; ++i) {
+      bool arrived = false;
+      for (unsigned i = 0; i < spin && !arrived; ++i) {
         seen = __hip_atomic_load(word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if ((seen & 0xFFu) >= slices)
-          break;
-        __builtin_amdgcn_s_sleep(2);
+        arrived = (seen & 0xFFu) >= slices;
+        if (!arrived)
+          __builtin_amdgcn_s_sleep(2);
       }
       const unsigned here = (unsigned)(seen >> (8 + 7 * (xcc & 7u))) & 0x7Fu;
       sDeviceWide = here != slices;
       if (here != slices) {
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
         __hip_atomic_fetch_add(again, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        for (unsigned i = 0; i < kSpinLimit; ++i) {
-          if (__hip_atomic_load(again, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= slices)
-            break;
-          __builtin_amdgcn_s_sleep(2);
+        arrived = false;
+        for (unsigned i = 0; i < spin && !arrived; ++i) {
+          arrived = __hip_atomic_load(again, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= slices;
+          if (!arrived)
+            __builtin_amdgcn_s_sleep(2);
         }
       }
+      if (!arrived)
+        __hip_atomic_store(cnt + 4 * h + 3, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     __syncthreads();
     if (sDeviceWide)
@@ -1150,7 +1181,7 @@ hipError_t launch_chunked(const void *q, const void *k, const uint16_t *v, const
     hipLaunchKernelGGL(delta_scan_kernel<false>, grid, dim3(kScanThreads), 0, stream, state,
                        reinterpret_cast<half_t *>(out), ws, s.T, s.Hk, s.Hv, s.Dv,
                        (const half_t *)nullptr, (const float *)nullptr, (unsigned *)nullptr,
-                       0.0f);
+                       0.0f, 0u);
     return hipGetLastError();
   }
   // The norm's arrival wait needs every slice workgroup of a value head
@@ -1159,7 +1190,7 @@ hipError_t launch_chunked(const void *q, const void *k, const uint16_t *v, const
   // it too, but costs ~17 us more per call here, measured).
   hipLaunchKernelGGL(delta_scan_kernel<true>, grid, dim3(kScanThreads), 0, stream, state,
                      reinterpret_cast<half_t *>(out), ws, s.T, s.Hk, s.Hv, s.Dv,
-                     reinterpret_cast<const half_t *>(gate), nweight, cnt, neps);
+                     reinterpret_cast<const half_t *>(gate), nweight, cnt, neps, g_wait_limit);
   return hipGetLastError();
 }
 
@@ -1202,6 +1233,27 @@ hipError_t launch_delta_chunked_gated_norm(const uint16_t *q, const uint16_t *k,
                                            const DeltaShape &s, hipStream_t stream) {
   return launch_chunked<true>(q, k, v, beta, decay, state, out, ws, eps, qscale, s, stream, gate,
                               nweight, neps);
+}
+
+unsigned delta_chunked_wait_limit(unsigned limit) {
+  const unsigned old = g_wait_limit;
+  g_wait_limit = limit;
+  return old;
+}
+
+hipError_t delta_chunked_wait_status(const void *ws, const DeltaShape &s, hipStream_t stream,
+                                     bool *gave_up) {
+  *gave_up = false;
+  std::vector<unsigned> rec(4 * (size_t)s.Hv);
+  hipError_t e = hipMemcpyAsync(rec.data(), static_cast<const char *>(ws) + counters_offset(s),
+                                rec.size() * sizeof(unsigned), hipMemcpyDeviceToHost, stream);
+  if (e == hipSuccess)
+    e = hipStreamSynchronize(stream);
+  if (e != hipSuccess)
+    return e;
+  for (size_t h = 0; h < s.Hv; ++h)
+    *gave_up = *gave_up || rec[4 * h + 3] != 0;
+  return hipSuccess;
 }
 
 unsigned delta_chunked_dispatches() { return 2; }

@@ -127,6 +127,13 @@ hipError_t launch_delta_chunked_gated_norm(const uint16_t *q, const uint16_t *k,
                                            const float *nweight, uint16_t *out, void *ws,
                                            float eps, float qscale, float neps,
                                            const DeltaShape &s, hipStream_t stream);
+// The polls the norm scan's arrival wait makes before it gives up: sets the
+// bound for later launches (0: give up at once); returns the previous bound.
+unsigned delta_chunked_wait_limit(unsigned limit);
+// After a launch_delta_chunked_gated_norm on `ws`: waits for `stream`, then
+// reports whether any workgroup's arrival wait gave up.
+hipError_t delta_chunked_wait_status(const void *ws, const DeltaShape &s, hipStream_t stream,
+                                     bool *gave_up);
 
 // Any-shape fallback, one thread per state column.
 hipError_t launch_delta_generic(const float *q, const float *k,

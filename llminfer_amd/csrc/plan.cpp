@@ -267,6 +267,7 @@ private:
   std::vector<char> skip_;       // launched by a fused launch at another op
   std::vector<std::pair<int64_t, int64_t>> l2Delta_; // by DeltaUpdate op: its q / k L2Norms
   void prepare_l2_delta();
+  void prepare_kv_decode();
 };
 
 int Lowering::validate() {
@@ -545,6 +546,29 @@ void Lowering::prepare_l2_delta() {
   }
 }
 
+// A one-token KvAppend whose next launched op is the CausalGqa on the same
+// caches runs as one fused decode call that reads the new K and V rows while
+// the attention writes its output, so the new rows stay live until the
+// attention op: its output is then never placed over them.
+void Lowering::prepare_kv_decode() {
+  if (g_.tokens != 1)
+    return;
+  for (size_t i = 0; i < g_.op_count; ++i) {
+    const auto &a = op(i);
+    if (a.kind != LLMI_GRAPH_KV_APPEND)
+      continue;
+    size_t j = i + 1;
+    while (j < g_.op_count &&
+           (op(j).kind == LLMI_GRAPH_RESHAPE || op(j).kind == LLMI_GRAPH_SLICE))
+      ++j;
+    if (j == g_.op_count || op(j).kind != LLMI_GRAPH_CAUSAL_GQA || op(j).keys != a.keys ||
+        op(j).values != a.values)
+      continue;
+    for (uint32_t k = 0; k < 2; ++k)
+      lastUse_[root_[a.inputs[k]]] = std::max(lastUse_[root_[a.inputs[k]]], j);
+  }
+}
+
 // A one-row norm + quantization launch and the W8A8 projections right after
 // it that read its quantized row, merged into one launch
 // (llmi_hip_add_rms_norm_linear_w8a8) whose weight stream runs under the
@@ -580,9 +604,11 @@ void Lowering::merge_norm_linears() {
       };
       const uint64_t row = 2ull * d.p.cache.count; // the new K (or V) row, fp16
       const Range ws{c.buf[4], c.workspaceBytes};
+      const Range o{c.buf[3], 2ull * gp.queryHeads * gp.headDim};
       const bool clash = overlap(ws, {d.buf[0], row}) || overlap(ws, {d.buf[1], row}) ||
                          overlap(ws, {c.buf[0], 2ull * gp.queryHeads * gp.headDim}) ||
-                         overlap(ws, {c.buf[3], 2ull * gp.queryHeads * gp.headDim});
+                         overlap(ws, o) || overlap(o, {d.buf[0], row}) ||
+                         overlap(o, {d.buf[1], row});
       if (gp.tokens == 1 && same(d.buf[2], c.buf[1]) && same(d.buf[3], c.buf[2]) && !clash &&
           llmi_hip_gqa_workspace_bytes(gp) == c.workspaceBytes &&
           llmi_hip_dispatch_count(LLMI_HIP_OP_KV_APPEND_CAUSAL_GQA, &gp) > 0) {
@@ -1062,6 +1088,7 @@ int Lowering::run() {
   prepare_fusions();
   prepare_norm_quantize();
   prepare_l2_delta();
+  prepare_kv_decode();
   if (g_.output_count) {
     const uint32_t id = g_.outputs[0];
     const auto &v = value(id);

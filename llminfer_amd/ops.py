@@ -740,7 +740,15 @@ def bind_l2_norm_delta_gated_norm(q: torch.Tensor, k: torch.Tensor, v: torch.Ten
     args = a[:6] + (_ptr(gate), _ptr(norm_weight)) + a[6:10] + (norm_epsilon,) + a[10:]
     b = Bound(lib.llmi_hip_l2_norm_delta_gated_norm, args, inner.what + "+gatedRmsNorm")
     b._keep = inner._keep
+    # the chunked form's bounded arrival wait: its give-up, read after a call
+    b.status_args = (a[10], a[11], a[7], a[12])
     return b
+
+
+def gated_norm_status(b: "Bound") -> None:
+    """Waits for the stream of a bind_l2_norm_delta_gated_norm call and raises
+    HipError (LAUNCH_FAILED) if the chunked scan's arrival wait gave up."""
+    _lib.check(_lib.load().llmi_hip_l2_norm_delta_gated_norm_status(*b.status_args))
 
 
 def l2_norm_delta_gated_norm(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
@@ -748,13 +756,17 @@ def l2_norm_delta_gated_norm(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                              gate: torch.Tensor, norm_weight: torch.Tensor,
                              out: torch.Tensor | None = None, epsilon: float = 1e-6,
                              q_scale: float | None = None,
-                             norm_epsilon: float = 1e-6) -> torch.Tensor:
+                             norm_epsilon: float = 1e-6, check: bool = True) -> torch.Tensor:
     """The fused L2Norm -> DeltaUpdate -> GatedRmsNorm chain
-    (bind_l2_norm_delta_gated_norm)."""
+    (bind_l2_norm_delta_gated_norm). With `check` it waits for the call and
+    raises if the chunked scan's arrival wait gave up (gated_norm_status)."""
     if out is None:
         out = torch.empty_like(v)
-    bind_l2_norm_delta_gated_norm(q, k, v, beta, decay, state, gate, norm_weight, out,
-                                  epsilon, q_scale, norm_epsilon)()
+    b = bind_l2_norm_delta_gated_norm(q, k, v, beta, decay, state, gate, norm_weight, out,
+                                      epsilon, q_scale, norm_epsilon)
+    b()
+    if check:
+        gated_norm_status(b)
     return out
 
 

@@ -296,6 +296,23 @@ def test_l2_norm_delta_gated_norm_rejects_shapes_without_kernel():
              None) == _lib.INVALID_ARGUMENT
 
 
+def test_gated_norm_status_host_paths():
+    """The status call of the fused chain: the recurrent form (T <= 32) has
+    no arrival wait and reports OK without touching the device; the chunked
+    form refuses a workspace smaller than the call's; a contract violation
+    stays INVALID_ARGUMENT. The wait bound setter returns the previous bound
+    (2^22 polls by default)."""
+    lib = _lib.load()
+    st = lib.llmi_hip_l2_norm_delta_gated_norm_status
+    assert st(None, 0, _lib.GraphDeltaParams(1, 16, 128, 32, 128), None) == _lib.OK
+    assert st(None, 0, _lib.GraphDeltaParams(1024, 16, 128, 32, 128), None) == _lib.WORKSPACE
+    assert st(None, 0, _lib.GraphDeltaParams(4, 16, 128, 24, 128), None) == \
+        _lib.INVALID_ARGUMENT
+    old = lib.llmi_hip_set_arrival_wait_limit(5)
+    assert old == 1 << 22
+    assert lib.llmi_hip_set_arrival_wait_limit(old) == 5
+
+
 def test_w8a8_abi():
     """The W8A8 projection path: GraphParams.h:8-28 / ReferenceParams.h:4-6
     layouts, validation before any launch, plan-record names

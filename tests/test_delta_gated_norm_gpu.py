@@ -81,3 +81,101 @@ def test_fused_repeats_and_reuses_counters(gpu):
         outs.append(ops.l2_norm_delta_gated_norm(q, k, v, f(d.beta), f(d.decay), st, z, wt))
     torch.cuda.synchronize()
     assert torch.equal(outs[0], outs[1]) and torch.equal(outs[1], outs[2])
+
+
+def _cfg4_chain_inputs(seed):
+    """cfg4's DeltaNet operands at the fused call's boundary: fp16 q/k rows
+    (the L2Norms run inside the call), v, beta, linear decay, zero state,
+    the fp16 gate z and the fp32 norm weight."""
+    T, hk, dk, hv, dv = 1024, 16, 128, 32, 128
+    d = oracle.make_delta_inputs(seed, T, hk, dk, hv, dv, 0.0)
+    q16 = oracle.normal_f16(seed, 11, (T, hk * dk))   # the rows make_delta_inputs normalised
+    k16 = oracle.normal_f16(seed, 12, (T, hk * dk))
+    z16 = oracle.normal_f16(seed, 23, (T, hv * dv))
+    w = oracle.normal_f32(seed, 24, (dv,), 1.0, 0.2)
+    return (T, hk, dk, hv, dv), d, q16, k16, z16, w
+
+
+def test_fused_cfg4_against_the_oracle_chain(gpu):
+    """The fused chain end to end at cfg4 size against the oracle chain
+    l2norm_f32 -> delta_recurrent_f64 -> fp16 -> gated_rms_norm
+    (Reference.metal:228-259 on Graph.metal:146-170's output).
+
+    The norm divides each 128-wide row by its RMS (median ~3.5e-3 at cfg4,
+    down to ~1e-4), so one fp16 ulp of difference in the DeltaUpdate output
+    moves a normalised output of magnitude ~8-16 by one of its own ulps
+    (2^-7). No fp16 implementation can be closer than that to the f64 chain:
+    the oracle's own fp32 chain (orc_delta_recurrent_f32) differs from the
+    f64 chain by exactly such flips. The bound is twice that spread, taken
+    on the same inputs; the DeltaUpdate output (before the norm) is held to
+    the north star's 2e-3 and the state to 1e-3 relative as well."""
+    shape, d, q16, k16, z16, w = _cfg4_chain_inputs(12)
+    T, hk, dk, hv, dv = shape
+    print(f"fused DeltaNet core vs oracle chain at cfg4 {shape}", flush=True)
+    f = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(gpu)
+    q, k, v, z = (u16_to_torch(a, gpu) for a in (q16, k16, d.v, z16))
+    st = f(d.state)
+    out = ops.l2_norm_delta_gated_norm(q, k, v, f(d.beta), f(d.decay), st, z, f(w))
+    torch.cuda.synchronize()
+    got = oracle.f16_to_f32(torch_to_u16(out)).astype(np.float64).reshape(T * hv, dv)
+    y64, s64 = oracle.delta_recurrent_f64(d.q, d.k, d.v, d.beta, d.decay, d.state)
+    y32, _ = oracle.delta_recurrent_f32(d.q, d.k, d.v, d.beta, d.decay, d.state)
+    rows = lambda y: y.reshape(T * hv, dv)
+    z2 = z16.reshape(T * hv, dv)
+    o64 = oracle.f16_to_f32(oracle.gated_rms_norm(
+        rows(oracle.f32_to_f16(y64.astype(np.float32))), z2, w)).astype(np.float64)
+    o32 = oracle.f16_to_f32(oracle.gated_rms_norm(rows(y32), z2, w)).astype(np.float64)
+    spread = float(np.max(np.abs(o32 - o64)))
+    err = float(np.max(np.abs(got - o64)))
+    e_state = float(np.max(np.abs(st.cpu().numpy() - s64)) / np.max(np.abs(s64)))
+    print(f"  out max-abs vs f64 chain {err:.4g}; f32-vs-f64 oracle spread {spread:.4g}; "
+          f"state rel {e_state:.3g}", flush=True)
+    assert spread > 0
+    assert err <= 2 * spread, (err, spread)
+    assert e_state <= 1e-3
+    # the un-normalised DeltaUpdate output of the same call, through the
+    # unfused pair (bit-identical to the fused call's, test_fused_equals_chain)
+    st2 = f(d.state)
+    y = ops.l2_norm_delta_update(q, k, v, f(d.beta), f(d.decay), st2)
+    torch.cuda.synchronize()
+    ey = float(np.max(np.abs(oracle.f16_to_f32(torch_to_u16(y)).astype(np.float64) - y64)))
+    assert ey <= 2e-3, ey
+
+
+def test_arrival_wait_give_up_is_reported(gpu):
+    """The chunked scan's bounded arrival wait, forced to give up from the
+    host (a bound of 0 polls: every workgroup stops waiting at once and
+    still exits normally), is reported by the status call as a launch
+    failure; with the bound restored the next call on the same workspace
+    (the prep re-zeroes the records) is reported clean and equals the
+    unfused chain bit for bit."""
+    from llminfer_amd import _lib
+    lib = _lib.load()
+    T, hk, dk, hv, dv = 96, 2, 128, 4, 128
+    print(f"arrival wait give-up, shape {(T, hk, dk, hv, dv)}", flush=True)
+    d = oracle.make_delta_inputs(7, T, hk, dk, hv, dv, 0.1)
+    q16 = oracle.normal_f16(7, 21, (T, hk * dk))
+    k16 = oracle.normal_f16(7, 22, (T, hk * dk))
+    z16 = oracle.normal_f16(7, 23, (T, hv * dv))
+    f = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(gpu)
+    q, k, v, z = (u16_to_torch(a, gpu) for a in (q16, k16, d.v, z16))
+    wt = f(np.ones(dv, np.float32))
+    out = torch.empty_like(v)
+    b = ops.bind_l2_norm_delta_gated_norm(q, k, v, f(d.beta), f(d.decay), f(d.state), z, wt,
+                                          out)
+    old = lib.llmi_hip_set_arrival_wait_limit(0)
+    try:
+        b()
+    finally:
+        lib.llmi_hip_set_arrival_wait_limit(old)
+    with pytest.raises(_lib.HipError) as e:
+        ops.gated_norm_status(b)
+    assert e.value.status == _lib.LAUNCH_FAILED
+    st = f(d.state)
+    out = ops.l2_norm_delta_gated_norm(q, k, v, f(d.beta), f(d.decay), st, z, wt)
+    s_ref = f(d.state)
+    x = ops.l2_norm_delta_update(q, k, v, f(d.beta), f(d.decay), s_ref)
+    ref = torch.empty_like(x)
+    ops.gated_rms_norm(x.view(T * hv, dv), z.view(T * hv, dv), wt, ref.view(T * hv, dv), 1e-6)
+    torch.cuda.synchronize()
+    assert torch.equal(st, s_ref) and torch.equal(out, ref)

@@ -134,6 +134,24 @@ def test_qwen35_4b_lowers_with_the_hot_kernels():
     assert prefill.scratch_bytes < 512 << 20
 
 
+@pytest.mark.parametrize("past", [0, 5, 31, 32, 100, 4096])
+def test_fused_decode_output_never_covers_the_new_rows(past):
+    """The fused one-token KvAppend + CausalGqa launch reads the new K / V
+    rows while it writes the attention output (in the same launch when there
+    is one split, i.e. P + 1 <= 32). The lowering keeps the new rows live
+    until the attention op, so the arena never places the output over them,
+    and it fuses only when neither the output nor the workspace overlaps the
+    new rows (a clash leaves KvAppend as its own launch). So a fused decode
+    in every attention layer at every past, with no kvAppend launch, shows
+    that no output of a fused decode covers its new rows."""
+    c = G.qwen35_4b()
+    _, decode = _lower(c, 1, past, 8192, "last", True)
+    kinds = Counter(d["kernel"] for d in decode.dispatches)
+    assert kinds["kvAppend"] == 0
+    assert kinds["gqaDecodeSplitK"] == 8 * 2
+    assert kinds["gqaDecodeMerge"] == (0 if past + 1 <= 32 else 8 * 2)
+
+
 def test_malformed_graphs_are_rejected_before_any_launch():
     c = G.tiny_qwen35()
     g = G.build_qwen35(c, 2, 0, 8, "all", True)
