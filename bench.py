@@ -692,11 +692,8 @@ class Qwen35Model(Workload):
         if self.decode and past:
             s.step(torch.randint(0, c.vocabulary, (past,), generator=g).numpy(), "none")
         self.plans = [s.plan(T, "last")]
-        if self.decode:
-            for i in range(1, plans):
-                s.past += 1           # the graph of the next position (no step run)
-                self.plans.append(s.plan(1, "last"))
-            s.past = past
+        if self.decode:   # the graphs of the next positions (no step run)
+            self.plans += [s.plan(1, "last", past=past + i) for i in range(1, plans)]
         self.ids = torch.randint(0, c.vocabulary, (T,), generator=g, dtype=torch.int32).to(dev)
         self.logits = torch.empty(1, c.vocabulary, dtype=torch.float16, device=dev)
         s.run(self.plans[-1], self.ids, self.logits)   # size the scratch arena once

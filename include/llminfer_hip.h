@@ -810,6 +810,111 @@ LLMI_HIP_API int llmi_hip_plan_execute(const llmi_hip_plan *plan, void *scratch,
                                        size_t state_count, const uint32_t *token_ids,
                                        uint16_t *logits, uint32_t *invalid, void *stream);
 
+/* ------------------------------------------------------ Qwen3.5 session
+ * The whole-model session: MetalSession (include/llminfer/Backend/Metal/
+ * MetalSession.h:26-50) and its executor (lib/Backend/Metal/
+ * MetalExecutor.mm:56-118, 212-298) over the plan above. Each step builds
+ * the graph of its shape with the op sequence of Qwen35ModelBuilder::build
+ * (lib/Models/Qwen35/Qwen35ModelBuilder.cpp:100-235), lowers it, runs it
+ * with one host synchronisation and returns the logits as floats. */
+
+/* Qwen35TextConfig's fields (lib/ModelFormat/Qwen35Schema.h:16-23); the
+ * derived widths follow from them. layer_kinds: one per layer. */
+enum llmi_qwen35_layer { LLMI_QWEN35_DELTANET = 0, LLMI_QWEN35_GQA = 1 };
+typedef struct llmi_qwen35_config {
+  uint64_t hidden, intermediate, vocabulary, max_positions;
+  uint64_t head_dim, q_heads, kv_heads, rotary_width;
+  uint64_t key_heads, value_heads, key_dim, value_dim, conv_kernel;
+  double epsilon, theta;
+  uint32_t w8;            /* 1: int8 matrices and W8A8 projections; 0: fp16 */
+  uint32_t layer_count;
+  const uint8_t *layer_kinds;
+} llmi_qwen35_config;
+
+/* LogitsMode (include/llminfer/Models/Qwen35/Qwen35ModelBuilder.h:10). */
+enum llmi_logits_mode { LLMI_LOGITS_NONE = 0, LLMI_LOGITS_LAST = 1, LLMI_LOGITS_ALL = 2 };
+
+/* The graph of one step, host only (Qwen35ModelBuilder::build): tokens new
+ * rows after past cached ones in caches of capacity rows (0: past +
+ * tokens). Weight values refer by index to llmi_qwen35_graph_tensor's ids
+ * ("embed_tokens.weight", "layers.<i>.mlp.up_proj.weight", ...; the tied
+ * head reads the embedding). */
+typedef struct llmi_qwen35_graph llmi_qwen35_graph;
+LLMI_HIP_API int llmi_qwen35_build(const llmi_qwen35_config *config, uint64_t tokens,
+                                   uint64_t past, uint64_t capacity, int logits_mode,
+                                   llmi_qwen35_graph **out);
+LLMI_HIP_API const llmi_graph *llmi_qwen35_graph_view(const llmi_qwen35_graph *graph);
+LLMI_HIP_API size_t llmi_qwen35_graph_tensor_count(const llmi_qwen35_graph *graph);
+LLMI_HIP_API const char *llmi_qwen35_graph_tensor(const llmi_qwen35_graph *graph, size_t index);
+LLMI_HIP_API void llmi_qwen35_graph_destroy(llmi_qwen35_graph *graph);
+
+/* A model tensor by id: device data and, for int8 tensors, fp16 group
+ * scales (llmi_weight). */
+typedef struct llmi_named_weight {
+  const char *name;
+  const void *data;
+  const uint16_t *scales;
+} llmi_named_weight;
+
+/* MetalStepResult (MetalSession.h:18-24) without its vectors: the logits
+ * go to the caller's buffer, the records to llmi_hip_model_dispatches. */
+typedef struct llmi_hip_model_step_result {
+  uint64_t past, logit_rows, scratch_bytes;
+  size_t dispatch_count;
+} llmi_hip_model_step_result;
+
+typedef struct llmi_hip_model llmi_hip_model;
+
+/* MetalSession::open (MetalExecutor.mm:230-253): the weights are borrowed
+ * (device pointers that must outlive the session, looked up by id; every
+ * tensor the model reads must be present); the session allocates and
+ * zeroes one device buffer per state slot of the model's graph, and runs on
+ * `stream`. 0 < capacity <= min(max_positions, 2^32 - 1). */
+LLMI_HIP_API int llmi_hip_model_open(const llmi_qwen35_config *config,
+                                     const llmi_named_weight *weights, size_t weight_count,
+                                     uint64_t capacity, void *stream, llmi_hip_model **out);
+LLMI_HIP_API void llmi_hip_model_close(llmi_hip_model *model);
+/* MetalSession::reset (MetalExecutor.mm:294-298): zero state, past 0. */
+LLMI_HIP_API void llmi_hip_model_reset(llmi_hip_model *model);
+LLMI_HIP_API uint64_t llmi_hip_model_past(const llmi_hip_model *model);
+LLMI_HIP_API int llmi_hip_model_invalid(const llmi_hip_model *model);
+LLMI_HIP_API uint64_t llmi_hip_model_vocabulary(const llmi_hip_model *model);
+
+/* MetalSession::step (MetalExecutor.mm:255-292): `count` host token IDs.
+ * Checked before any launch: the session is valid, 0 < count <= capacity -
+ * past, every ID is in the vocabulary, the step's state layout equals the
+ * session's, the logits buffer holds the step's rows x vocabulary floats.
+ * Then one graph run and one host synchronisation; past advances only on
+ * success. A failure after the launches, or a non-finite activation found
+ * by a quantization (MetalExecutor.mm:180-187), returns
+ * LLMI_HIP_LAUNCH_FAILED and leaves the session invalid until reset. */
+LLMI_HIP_API int llmi_hip_model_step(llmi_hip_model *model, const uint32_t *ids, size_t count,
+                                     int logits_mode, float *logits, size_t logits_capacity,
+                                     llmi_hip_model_step_result *result);
+/* The plan records of the last successful step (MetalStepResult's
+ * dispatches): up to `cap` written, the total returned. */
+LLMI_HIP_API size_t llmi_hip_model_dispatches(const llmi_hip_model *model,
+                                              llmi_hip_dispatch *records, size_t cap);
+/* State slot `index` in graph order: its descriptor, device buffer (dense,
+ * session-owned) and size. */
+LLMI_HIP_API size_t llmi_hip_model_state_count(const llmi_hip_model *model);
+LLMI_HIP_API int llmi_hip_model_state(const llmi_hip_model *model, size_t index,
+                                      llmi_graph_state *desc, void **device, size_t *bytes);
+/* Copies state slot `index` (all `bytes` of it) to `dst`, host or device
+ * memory, after the session's pending work; waits for the copy. */
+LLMI_HIP_API int llmi_hip_model_read_state(llmi_hip_model *model, size_t index, void *dst,
+                                           size_t bytes);
+
+/* Timing aid (no counterpart in the reference): the plan of a step of
+ * `tokens` rows at `past` (destroy with llmi_hip_plan_destroy), and its run
+ * on the session's state, scratch and stream without a synchronisation, a
+ * check or a change of past. ids: device uint32 [tokens]; logits: device
+ * fp16 [rows][vocabulary] or NULL for LLMI_LOGITS_NONE. */
+LLMI_HIP_API int llmi_hip_model_plan(const llmi_hip_model *model, uint64_t tokens, uint64_t past,
+                                     int logits_mode, llmi_hip_plan **out);
+LLMI_HIP_API int llmi_hip_model_run(llmi_hip_model *model, const llmi_hip_plan *plan,
+                                    const uint32_t *ids, uint16_t *logits);
+
 #ifdef __cplusplus
 }
 #endif

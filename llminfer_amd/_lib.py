@@ -228,6 +228,25 @@ SIGNATURES = {
     "llmi_hip_plan_dispatches": (_SZ, [_P, C.POINTER(Dispatch), _SZ]),
     "llmi_hip_plan_launches": (_SZ, [_P]),
     "llmi_hip_plan_execute": (C.c_int, [_P, _P, _SZ, _P, _SZ, _P, _P, _P, _P]),
+    # Qwen3.5 graph builder and model session (structs in llminfer_amd/plan.py)
+    "llmi_qwen35_build": (C.c_int, [_P, C.c_uint64, C.c_uint64, C.c_uint64, C.c_int, _P]),
+    "llmi_qwen35_graph_view": (_P, [_P]),
+    "llmi_qwen35_graph_tensor_count": (_SZ, [_P]),
+    "llmi_qwen35_graph_tensor": (C.c_char_p, [_P, _SZ]),
+    "llmi_qwen35_graph_destroy": (None, [_P]),
+    "llmi_hip_model_open": (C.c_int, [_P, _P, _SZ, C.c_uint64, _P, _P]),
+    "llmi_hip_model_close": (None, [_P]),
+    "llmi_hip_model_reset": (None, [_P]),
+    "llmi_hip_model_past": (C.c_uint64, [_P]),
+    "llmi_hip_model_invalid": (C.c_int, [_P]),
+    "llmi_hip_model_vocabulary": (C.c_uint64, [_P]),
+    "llmi_hip_model_step": (C.c_int, [_P, _P, _SZ, C.c_int, _P, _SZ, _P]),
+    "llmi_hip_model_dispatches": (_SZ, [_P, C.POINTER(Dispatch), _SZ]),
+    "llmi_hip_model_state_count": (_SZ, [_P]),
+    "llmi_hip_model_state": (C.c_int, [_P, _SZ, _P, _P, _P]),
+    "llmi_hip_model_read_state": (C.c_int, [_P, _SZ, _P, _SZ]),
+    "llmi_hip_model_plan": (C.c_int, [_P, C.c_uint64, C.c_uint64, C.c_int, _P]),
+    "llmi_hip_model_run": (C.c_int, [_P, _P, _P, _P]),
 }
 
 _lib = None

@@ -1,11 +1,13 @@
-"""The whole-graph HIP plan and a model session over it.
+"""Bindings of the whole-graph HIP plan and of the C++ model session.
 
 Plan lowers one step's graph (llminfer_amd.graph.Graph) through the C ABI
-(llmi_hip_plan_lower, csrc/plan.cpp) and runs it; ModelSession plays the
-part of the reference's MetalSession (include/llminfer/Backend/Metal/
-MetalSession.h:26-50, MetalExecutor.mm:212-298): it owns the model's
-device weights and the per-layer states, builds the Qwen3.5 graph of each
-step, lowers and runs it, and returns the logits with the plan records.
+(llmi_hip_plan_lower, csrc/plan.cpp) and runs it, or wraps a plan the model
+session lowered. ModelSession binds the C++ session (llmi_hip_model_*,
+csrc/model.cpp), the part of the reference's MetalSession
+(include/llminfer/Backend/Metal/MetalSession.h:26-50, MetalExecutor.mm:
+212-298): the session owns the per-layer states, builds the Qwen3.5 graph of
+each step in C++, lowers and runs it, and returns the logits with the plan
+records.
 """
 from __future__ import annotations
 
@@ -107,32 +109,24 @@ def marshal(g: Graph, weight_index: dict[str, int]):
 class Plan:
     """A lowered step: llmi_hip_plan_lower's result, owned here."""
 
-    def __init__(self, g: Graph, weight_table: list[tuple[int, int]],
-                 weight_index: dict[str, int]):
+    def __init__(self, g: Graph | None, weight_table: list[tuple[int, int]] | None = None,
+                 weight_index: dict[str, int] | None = None, handle=None):
         lib = _lib.load()
-        desc, self._keep = marshal(g, weight_index)
-        table = (WeightDesc * max(1, len(weight_table)))(
-            *[WeightDesc(d, s) for d, s in weight_table])
-        self._table = table
-        handle = C.c_void_p()
-        _check(lib.llmi_hip_plan_lower(C.byref(desc), table, len(weight_table), C.byref(handle)),
-               "plan lowering")
+        if handle is None:
+            desc, self._keep = marshal(g, weight_index)
+            table = (WeightDesc * max(1, len(weight_table)))(
+                *[WeightDesc(d, s) for d, s in weight_table])
+            self._table = table
+            handle = C.c_void_p()
+            _check(lib.llmi_hip_plan_lower(C.byref(desc), table, len(weight_table),
+                                           C.byref(handle)), "plan lowering")
         self._h = handle
         self.scratch_bytes = lib.llmi_hip_plan_scratch_bytes(handle)
         rows, elements = C.c_uint64(), C.c_uint64()
         lib.llmi_hip_plan_logits(handle, C.byref(rows), C.byref(elements))
         self.logit_rows, self.logit_elements = rows.value, elements.value
-        n = lib.llmi_hip_plan_dispatches(handle, None, 0)
-        recs = (_lib.Dispatch * max(1, n))()
-        lib.llmi_hip_plan_dispatches(handle, recs, n)
         self.launches = lib.llmi_hip_plan_launches(handle)  # kernel launches a step
-        self.dispatches = []  # plan records, one per op a launch serves
-        for r in recs[:n]:
-            d = {"op_index": r.op_index, "kernel": r.kernel.decode()}
-            if r.epilogue:
-                d["epilogue"] = r.epilogue.decode()
-                d["fused_op_index"] = r.fused_op_index
-            self.dispatches.append(d)
+        self.dispatches = records(lib.llmi_hip_plan_dispatches, handle)
         self.graph = g
 
     def execute(self, scratch: torch.Tensor, states: list[torch.Tensor], ids: torch.Tensor,
@@ -149,6 +143,22 @@ class Plan:
         if h is not None and h.value and _lib is not None and _lib._lib is not None:
             _lib._lib.llmi_hip_plan_destroy(h)
             self._h = None
+
+
+def records(query, handle) -> list[dict]:
+    """Plan records {op_index, kernel[, epilogue, fused_op_index]}
+    (tools/run/Main.cpp:244-255) from a (handle, records, cap) query."""
+    n = query(handle, None, 0)
+    recs = (_lib.Dispatch * max(1, n))()
+    query(handle, recs, n)
+    out = []
+    for r in recs[:n]:
+        d = {"op_index": r.op_index, "kernel": r.kernel.decode()}
+        if r.epilogue:
+            d["epilogue"] = r.epilogue.decode()
+            d["fused_op_index"] = r.fused_op_index
+        out.append(d)
+    return out
 
 
 _TORCH = {Element.I8: torch.int8, Element.U32: torch.int32, Element.F16: torch.float16,
@@ -191,80 +201,134 @@ def random_weights(c: Qwen35Config, w8: bool, device, seed: int = 0) -> dict:
     return out
 
 
+class Qwen35Config_C(C.Structure):
+    """llmi_qwen35_config (include/llminfer_hip.h)."""
+    _fields_ = [(n, C.c_uint64) for n in (
+        "hidden", "intermediate", "vocabulary", "max_positions", "head_dim", "q_heads",
+        "kv_heads", "rotary_width", "key_heads", "value_heads", "key_dim", "value_dim",
+        "conv_kernel")] + [("epsilon", C.c_double), ("theta", C.c_double), ("w8", C.c_uint32),
+                          ("layer_count", C.c_uint32), ("layer_kinds", C.POINTER(C.c_uint8))]
+
+
+class NamedWeight(C.Structure):
+    _fields_ = [("name", C.c_char_p), ("data", C.c_void_p), ("scales", C.c_void_p)]
+
+
+class StepResult_C(C.Structure):
+    _fields_ = [("past", C.c_uint64), ("logit_rows", C.c_uint64), ("scratch_bytes", C.c_uint64),
+                ("dispatch_count", C.c_size_t)]
+
+
+LOGITS = {"none": 0, "last": 1, "all": 2}   # LogitsMode (Qwen35ModelBuilder.h:10)
+
+
+def c_config(c: Qwen35Config, w8: bool):
+    """The C config of c, and the layer-kind array it points to (keep both)."""
+    kinds = (C.c_uint8 * len(c.layers))(*[1 if k == "gqa" else 0 for k in c.layers])
+    cfg = Qwen35Config_C(c.hidden, c.intermediate, c.vocabulary, c.max_positions, c.head_dim,
+                         c.q_heads, c.kv_heads, c.rotary_width, c.key_heads, c.value_heads,
+                         c.key_dim, c.value_dim, c.conv_kernel, c.epsilon, c.theta, int(w8),
+                         len(c.layers), kinds)
+    return cfg, kinds
+
+
 class ModelSession:
-    """One sequence through the Qwen3.5 graph on the HIP plan (MetalSession,
-    MetalExecutor.mm:212-298): states persist across steps; every step
-    builds the graph of its shape, lowers it and runs it with one host sync.
-    Calls on one session must be serialised."""
+    """One sequence through the Qwen3.5 graph: a binding of the C++ model
+    session (llmi_hip_model_*, csrc/model.cpp), which plays MetalSession
+    (MetalSession.h:26-50, MetalExecutor.mm:212-298): it owns the per-layer
+    states, builds and lowers each step's graph and runs it with one host
+    sync. The weights stay owned here (the session borrows their device
+    pointers). Calls on one session must be serialised."""
 
     def __init__(self, config: Qwen35Config, weights: dict, capacity: int, w8: bool = True,
                  device=None):
-        if not capacity or capacity > min(config.max_positions, 2 ** 32 - 1):
-            raise ValueError("Invalid session capacity")
+        lib = _lib.load()
         self.config, self.w8, self.capacity = config, w8, capacity
         self.device = torch.device(device) if device is not None else torch.device("cuda", 0)
-        names = sorted(weights)
-        self.weight_index = {n: i for i, n in enumerate(names)}
         self.weights = weights
-        self.weight_table = [(weights[n][0].data_ptr(),
-                              weights[n][1].data_ptr() if weights[n][1] is not None else 0)
-                             for n in names]
-        self.vocabulary = weights[EMBEDDING_ID][0].shape[0]
-        layout = build_qwen35(config, 1, 0, capacity, "none", w8)
-        self.states = [torch.zeros(s.shape, dtype=_TORCH[s.element], device=self.device)
-                       for s in layout.states]
-        self._layout = [(s.kind, s.layer, s.shape) for s in layout.states]
-        self.scratch = torch.empty(0, dtype=torch.uint8, device=self.device)
-        self.invalid_flag = torch.zeros(1, dtype=torch.int32, device=self.device)
-        self.past = 0
-        self.invalid = False
+        names = sorted(weights)
+        self._names = [n.encode() for n in names]
+        table = (NamedWeight * max(1, len(names)))(
+            *[NamedWeight(self._names[i], weights[n][0].data_ptr(),
+                          weights[n][1].data_ptr() if weights[n][1] is not None else None)
+              for i, n in enumerate(names)])
+        self._cfg, self._kinds = c_config(config, w8)
+        h = C.c_void_p()
+        rc = lib.llmi_hip_model_open(C.byref(self._cfg), table, len(names), capacity,
+                                     torch.cuda.current_stream(self.device).cuda_stream,
+                                     C.byref(h))
+        if rc != _lib.OK:
+            msg = lib.llmi_hip_last_error().decode()
+            raise (ValueError if rc == _lib.INVALID_ARGUMENT else _lib.HipError)(
+                *((msg,) if rc == _lib.INVALID_ARGUMENT else (rc, msg)))
+        self._h = h
+        self.vocabulary = lib.llmi_hip_model_vocabulary(h)
 
-    def plan(self, tokens: int, logits: str = "last") -> Plan:
-        g = build_qwen35(self.config, tokens, self.past, self.capacity, logits, self.w8)
-        if [(s.kind, s.layer, s.shape) for s in g.states] != self._layout:
-            raise RuntimeError("Graph state layout changed within the session")
-        return Plan(g, self.weight_table, self.weight_index)
+    @property
+    def past(self) -> int:
+        return _lib.load().llmi_hip_model_past(self._h)
+
+    @property
+    def invalid(self) -> bool:
+        return bool(_lib.load().llmi_hip_model_invalid(self._h))
+
+    @property
+    def states(self) -> list[torch.Tensor]:
+        """Copies of the session's state buffers, in graph order."""
+        lib = _lib.load()
+        out = []
+        for i in range(lib.llmi_hip_model_state_count(self._h)):
+            d, n = GraphState(), C.c_size_t()
+            _check(lib.llmi_hip_model_state(self._h, i, C.byref(d), None, C.byref(n)), "state")
+            dtype = torch.float32 if d.element == Element.F32 else torch.float16
+            t = torch.empty(tuple(d.shape[:d.rank]), dtype=dtype, device=self.device)
+            _check(lib.llmi_hip_model_read_state(self._h, i, t.data_ptr(), n.value), "state")
+            out.append(t)
+        return out
+
+    def plan(self, tokens: int, logits: str = "last", past: int | None = None) -> Plan:
+        """The lowered step of `tokens` rows at `past` (default: the session's)."""
+        h = C.c_void_p()
+        _check(_lib.load().llmi_hip_model_plan(self._h, tokens, self.past if past is None
+                                               else past, LOGITS[logits], C.byref(h)),
+               "model plan")
+        return Plan(None, handle=h)
 
     def run(self, plan: Plan, ids: torch.Tensor, logits: torch.Tensor | None) -> None:
-        """Enqueues one lowered step (no sync, no state checks): for timing."""
-        if self.scratch.numel() < plan.scratch_bytes:
-            self.scratch = torch.empty(plan.scratch_bytes, dtype=torch.uint8, device=self.device)
-        plan.execute(self.scratch, self.states, ids, logits, self.invalid_flag)
+        """Enqueues one lowered step (no sync, no checks, past unchanged): for timing."""
+        _check(_lib.load().llmi_hip_model_run(self._h, plan._h, ids.data_ptr(),
+                                              None if logits is None else logits.data_ptr()),
+               "model run")
 
     def step(self, ids, logits: str = "last", trace: bool = False) -> StepResult:
-        if self.invalid:
-            raise RuntimeError("Session is invalid after a failed GPU step")
-        ids = np.asarray(ids, np.uint32).reshape(-1)
-        if ids.size == 0 or ids.size > self.capacity - self.past:
-            raise ValueError("Token chunk is empty or exceeds session capacity")
-        if np.any(ids >= self.vocabulary):
+        lib = _lib.load()
+        ids = np.ascontiguousarray(np.asarray(ids, np.int64).reshape(-1))
+        if ids.size and (ids.min() < 0 or ids.max() >= 2 ** 32):
             raise ValueError("Token ID is outside the vocabulary")
-        plan = self.plan(ids.size, logits)
-        dev_ids = torch.from_numpy(ids.view(np.int32)).to(self.device)
-        out = None
-        if plan.logit_rows:
-            out = torch.empty(plan.logit_rows, plan.logit_elements // plan.logit_rows,
-                              dtype=torch.float16, device=self.device)
-        self.invalid_flag.zero_()
-        try:
-            self.run(plan, dev_ids, out)
-            torch.cuda.synchronize(self.device)
-        except Exception:
-            self.invalid = True
-            raise
-        if int(self.invalid_flag.item()):
-            self.invalid = True
-            raise RuntimeError("Non-finite activation during W8A8 quantization")
-        self.past += ids.size
-        return StepResult(self.past, plan.logit_rows, plan.scratch_bytes, len(plan.dispatches),
-                          out.float().cpu().numpy() if out is not None else None,
-                          plan.dispatches if trace else [])
+        ids = ids.astype(np.uint32)
+        rows = 0 if logits == "none" else (ids.size if logits == "all" else 1)
+        out = np.empty((rows, self.vocabulary), np.float32)
+        res = StepResult_C()
+        rc = lib.llmi_hip_model_step(self._h, ids.ctypes.data, ids.size, LOGITS[logits],
+                                     out.ctypes.data if rows else None, out.size,
+                                     C.byref(res))
+        if rc != _lib.OK:
+            msg = lib.llmi_hip_last_error().decode()
+            if rc == _lib.INVALID_ARGUMENT and not self.invalid:
+                raise ValueError(msg)
+            raise RuntimeError(f"{msg} (status {rc})")
+        disp = records(lib.llmi_hip_model_dispatches, self._h) if trace else []
+        return StepResult(res.past, res.logit_rows, res.scratch_bytes, res.dispatch_count,
+                          out if rows else None, disp)
 
     def reset(self) -> None:
-        for s in self.states:
-            s.zero_()
-        self.past = 0
-        self.invalid = False
+        _lib.load().llmi_hip_model_reset(self._h)
+
+    def __del__(self):
+        h = getattr(self, "_h", None)
+        if h is not None and h.value and _lib is not None and _lib._lib is not None:
+            _lib._lib.llmi_hip_model_close(h)
+            self._h = None
 
 
 __all__ = ["Plan", "ModelSession", "StepResult", "random_weights", "marshal", "OpKind",

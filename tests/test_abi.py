@@ -16,7 +16,7 @@ def declared_functions() -> set[str]:
     names = set()
     for h in (ROOT / "include").glob("*.h"):
         text = re.sub(r"/\*.*?\*/", "", h.read_text(), flags=re.S)
-        for m in re.finditer(r"LLMI_HIP_API\s+[^;{]*?\b(llmi_hip_\w+)\s*\(", text):
+        for m in re.finditer(r"LLMI_HIP_API\s+[^;{]*?\b(llmi_\w+)\s*\(", text):
             names.add(m.group(1))
     return names
 

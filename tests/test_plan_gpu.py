@@ -193,3 +193,44 @@ def test_qwen35_4b_decode_step(gpu):
     # deltaRecurrent: the update and its fused q / k L2Norms, a record each
     # gqaDecodeSplitK: KvAppend and CausalGqa in one fused call, a record each
     assert kinds.count("gqaDecodeSplitK") == 8 * 2 and kinds.count("deltaRecurrent") == 24 * 3
+
+
+def test_nonfinite_activation_invalidates_until_reset(gpu):
+    """A non-finite activation found by a quantization fails the step after
+    its launches and leaves the session invalid until reset
+    (MetalExecutor.mm:180-187, 283-298); past does not advance, and the
+    session is clean again after reset."""
+    c = G.tiny_qwen35()
+    weights = tiny_weights(c, 11)
+    dw = device_weights(weights, gpu)
+    session = ModelSession(c, dw, 8, True, gpu)
+    good = session.step(TOKENS[:2], "all").logits
+    # an infinite embedding row: its token's hidden row is non-finite
+    table, scales = dw[G.EMBEDDING_ID]
+    saved = scales[TOKENS[2]].clone()
+    scales[TOKENS[2]] = float("inf")
+    print("nonfinite activation step", flush=True)
+    with pytest.raises(RuntimeError):
+        session.step(TOKENS[2:3])
+    assert session.invalid and session.past == 2
+    with pytest.raises(RuntimeError):
+        session.step(TOKENS[3:4])        # refused before any launch
+    scales[TOKENS[2]] = saved
+    session.reset()
+    assert not session.invalid and session.past == 0
+    again = session.step(TOKENS[:2], "all").logits
+    assert np.array_equal(good.view(np.uint32), again.view(np.uint32))
+
+
+def test_session_states_read_back(gpu):
+    """The state copies the session hands out are its buffers after the
+    step: the KV cache rows of the step are written, rows past it zero."""
+    c = G.tiny_qwen35()
+    session = ModelSession(c, device_weights(tiny_weights(c, 5), gpu), 8, True, gpu)
+    session.step(TOKENS[:3], "none")
+    states = session.states
+    kinds = [s.kind for s in G.build_qwen35(c, 1, 0, 8, "none", True).states]
+    assert len(states) == len(kinds)
+    for st, kind in zip(states, kinds):
+        if kind in (G.StateKind.KEY_CACHE, G.StateKind.VALUE_CACHE):
+            assert torch.count_nonzero(st[:3]) > 0 and torch.count_nonzero(st[3:]) == 0
