@@ -749,9 +749,78 @@ class Qwen35Model(Workload):
                 "reference_m2_tok_s": 9.82 if self.decode else 20.81}
 
     def cpu(self, budget_s):
-        return {"value": None, "unit": "tok/s", "cores": 0, "kind": "port",
-                "sample": "not timed: the whole-model oracle (tests/graph_runner.py) runs the "
-                          "two-layer test model; per-op CPU baselines are on the other legs"}
+        """The whole step on the CPU oracle (oracle/graph_runner.py, scalar C,
+        one thread), from a bounded sample: one DeltaNet and one GQA layer of
+        the model's widths and the head over 8192 of its 248,320 rows, at the
+        leg's past (the caches and states hold random values: the time does
+        not depend on them); prefill runs 16 of the 512 tokens. Scaled: 24
+        DeltaNet + 8 GQA layers, the head to the full vocabulary, and for the
+        prefill the per-token work x 512/16 (the head reads one row; the
+        quadratic attention term is then undercounted, ~2 % of the step)."""
+        import dataclasses
+        import time as _time
+        import numpy as np
+        import oracle
+        from llminfer_amd.graph import (EMBEDDING_ID, Element, OpKind, build_qwen35,
+                                        qwen35_tensors)
+        from oracle.graph_runner import GraphRunner
+        c = self.c
+        sample_vocab, T = 8192, (1 if self.decode else 16)
+        cs = dataclasses.replace(c, layers=("delta", "gqa"), vocabulary=sample_vocab)
+        r = np.random.default_rng(7)
+        weights = {}
+        for tid, (element, shape) in qwen35_tensors(cs, True).items():
+            if element == Element.I8:
+                rows, width = shape
+                groups = (width + 31) // 32
+                data = np.zeros((rows, groups * 32), np.int8)
+                data[:, :width] = r.integers(-127, 128, (rows, width), dtype=np.int8)
+                scale = (0.25 if tid == EMBEDDING_ID else 0.6 / np.sqrt(width)) / 127
+                weights[tid] = (data, oracle.f32_to_f16(
+                    (r.random((rows, groups)) * 2 * scale).astype(np.float32)))
+            elif element == Element.F16:
+                weights[tid] = (oracle.f32_to_f16(
+                    (r.standard_normal(shape) * 0.12).astype(np.float32)), None)
+            else:
+                v = (r.standard_normal(shape) * 0.1).astype(np.float32)
+                weights[tid] = (v + 1 if tid.endswith("linear_attn.norm.weight") else v, None)
+        past = self.P
+        g = build_qwen35(cs, T, past, past + T, "last", True)
+        states = []
+        for st in g.states:
+            if st.element == Element.F32:
+                states.append((r.standard_normal(st.shape) * 0.1).astype(np.float32))
+            else:
+                states.append(oracle.f32_to_f16(
+                    r.standard_normal(st.shape).astype(np.float32)))
+        ids = r.integers(0, sample_vocab, T).astype(np.uint32)
+        head_op = max(i for i, op in enumerate(g.ops) if op.kind == OpKind.LINEAR_W8A8)
+        tot = {"delta": 0.0, "gqa": 0.0, "head": 0.0, "rest": 0.0}
+
+        def account(i, op, dt):
+            part = "head" if i == head_op else {0: "delta", 1: "gqa"}.get(op.layer, "rest")
+            tot[part] += dt
+
+        runs, t0 = 0, _time.perf_counter()
+        while runs == 0 or _time.perf_counter() - t0 < budget_s:
+            run = GraphRunner(g, weights, states)
+            run.op_hook = account
+            run.run(ids)
+            runs += 1
+        per = {k: v / runs for k, v in tot.items()}
+        n_gqa = sum(k == "gqa" for k in c.layers)
+        n_delta = len(c.layers) - n_gqa
+        scale_t = self.T / T
+        step_s = scale_t * (n_delta * per["delta"] + n_gqa * per["gqa"] + per["rest"]) + \
+            per["head"] * c.vocabulary / sample_vocab
+        return {"value": step_s * 1e6, "unit": "µs/step", "cores": 1, "kind": "port",
+                "tokens_per_s": round(self.T / step_s, 3),
+                "sample": f"oracle graph runner, 1 thread: one DeltaNet + one GQA layer and "
+                          f"the head over {sample_vocab} rows at T={T}, past={past}, "
+                          f"{runs} runs, scaled to {n_delta}+{n_gqa} layers, "
+                          f"{c.vocabulary} rows" + ("" if self.decode else
+                                                    f", x{self.T // T} tokens"),
+                "per_layer_us": {k: round(v * 1e6, 1) for k, v in per.items()}}
 
 
 def _delta_inputs(g, dev, T, hk, dk, hv, dv):

@@ -9,7 +9,7 @@
   swiGlu / deltaGates / sigmoidMul, an unfused siluF16 after the
   convolution, the head on linearW8A8Gemm / Gemv by row count, and fewer
   launches without logits.
-* The oracle runner (tests/graph_runner.py) executes the same graphs op by
+* The oracle runner (oracle/graph_runner.py) executes the same graphs op by
   op on the CPU oracle; its logits are pinned against HF transformers'
   Qwen3.5 decoder layers with the reference test's W8A8 projection
   (quantized_linear, MetalReferenceTest.py:88-100) over chunked steps that
