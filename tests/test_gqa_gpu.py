@@ -146,6 +146,42 @@ def test_prefill_cfg3_sampled_rows(gpu):
         _check(got[t], want)
 
 
+def _dense_f64_torch(x, gpu):
+    """Dense causal GQA in float64 on the device (torch matmul per head, all
+    operands contiguous): the same sum as oracle.gqa_dense_f64, fast enough
+    to cover every token of cfg3."""
+    T, hq, d = x.q.shape
+    hkv, past = x.k_cache.shape[1], x.past
+    to64 = lambda a: torch.from_numpy(oracle.f16_to_f32(a).astype(np.float64)).to(gpu)
+    q, kc, vc = to64(x.q), to64(x.k_cache[:past + T]), to64(x.v_cache[:past + T])
+    keys = torch.arange(past + T, device=gpu)
+    mask = keys[None, :] > (past + torch.arange(T, device=gpu))[:, None]
+    out = torch.empty(T, hq, d, dtype=torch.float64, device=gpu)
+    for h in range(hq):
+        g = h // (hq // hkv)
+        s = (q[:, h].contiguous() @ kc[:, g].contiguous().T.contiguous()) / np.sqrt(d)
+        s.masked_fill_(mask, -np.inf)
+        out[:, h] = torch.softmax(s, dim=-1) @ vc[:, g].contiguous()
+    return out.cpu().numpy()
+
+
+def test_prefill_cfg3_every_token(gpu):
+    """BASELINE cfg3 in full: every token and query head against a float64
+    dense reference computed on the device, itself checked against the
+    oracle on sampled tokens (they agree to ~1e-8, far inside the 2e-3 bar;
+    the device GEMM sums in another order)."""
+    print("prefill cfg3, every token", flush=True)
+    T, P = 2048, 2048
+    x = oracle.make_gqa_inputs(3, T, 16, 4, 256, P)
+    got = _run(x, gpu)
+    want = _dense_f64_torch(x, gpu)
+    for t in (0, 777, 2047):
+        pin = oracle.gqa_dense_f64(x.q[t:t + 1], x.k_cache, x.v_cache, P + t)[0]
+        assert np.max(np.abs(want[t] - pin)) < 1e-6
+    err = _check(got, want)
+    print(f"  max abs err over {T} tokens x 16 heads: {err:.3g}", flush=True)
+
+
 @pytest.mark.parametrize("growth,qscale", [(2.0, 1.0), (0.0, 4.0), (6.0, 2.0)])
 def test_prefill_moving_reference(gpu, growth, qscale):
     """Scores that keep growing along the keys (key rows scaled up with their

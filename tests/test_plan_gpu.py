@@ -121,7 +121,10 @@ def test_tiny_plan_matches_the_oracle(gpu):
     want, _ = run_oracle(c, weights, chunks)
     for chunk, w_ in zip(chunks, want):
         got = session.step(chunk, "all").logits
-        assert np.linalg.norm(got - w_) <= 0.02 * np.linalg.norm(w_)
+        rel = np.linalg.norm(got - w_) / np.linalg.norm(w_)
+        print(f"  tiny plan vs oracle: rel L2 {rel:.3g}, max {np.abs(got - w_).max():.3g}, "
+              f"identical {np.mean(got == w_):.3f}", flush=True)
+        assert rel <= 0.02
         assert np.abs(got - w_).max() < 0.1
 
 
@@ -163,7 +166,10 @@ def test_small_plan_on_the_hot_kernels(gpu):
     assert {"gqaDecodeSplitK", "deltaRecurrent", "linearW8A8Gemv"} <= kernels
     want, _ = run_oracle(c, weights, chunks, capacity=256)
     for p, w_ in zip(plan_logits, want):
-        assert np.linalg.norm(p - w_) <= 0.02 * np.linalg.norm(w_)
+        rel = np.linalg.norm(p - w_) / np.linalg.norm(w_)
+        print(f"  small plan vs oracle: rel L2 {rel:.3g}, max {np.abs(p - w_).max():.3g}",
+              flush=True)
+        assert rel <= 0.02
 
 
 def test_session_rejects_bad_steps_and_resets(gpu):
