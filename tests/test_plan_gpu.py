@@ -114,6 +114,8 @@ def test_tiny_plan_is_the_op_by_op_graph(gpu, w8):
 
 
 def test_tiny_plan_matches_the_oracle(gpu):
+    """The reference's tiny model through the plan against the oracle model
+    (itself pinned to HF transformers in test_plan.py), over chunked steps."""
     c = G.tiny_qwen35()
     weights = tiny_weights(c, 7)
     chunks = [TOKENS[:2], TOKENS[2:3], TOKENS[3:]]
@@ -124,8 +126,11 @@ def test_tiny_plan_matches_the_oracle(gpu):
         rel = np.linalg.norm(got - w_) / np.linalg.norm(w_)
         print(f"  tiny plan vs oracle: rel L2 {rel:.3g}, max {np.abs(got - w_).max():.3g}, "
               f"identical {np.mean(got == w_):.3f}", flush=True)
-        assert rel <= 0.02
-        assert np.abs(got - w_).max() < 0.1
+        # measured: bit-identical (the tiny model's generic attention and
+        # DeltaNet kernels round like the float64 oracle here); the bound
+        # leaves room for a single int8 rounding flip
+        assert rel <= 2e-3
+        assert np.abs(got - w_).max() < 0.02
 
 
 def _small_weights(c, seed):
@@ -166,10 +171,15 @@ def test_small_plan_on_the_hot_kernels(gpu):
     assert {"gqaDecodeSplitK", "deltaRecurrent", "linearW8A8Gemv"} <= kernels
     want, _ = run_oracle(c, weights, chunks, capacity=256)
     for p, w_ in zip(plan_logits, want):
+        # measured 0.8-1.0 % (max 0.022): the MFMA attention and chunked
+        # delta rule sum in fp32 where the oracle sums in float64, and a
+        # rounding flip ahead of an int8 quantization moves the activation by
+        # a whole step, which the later layers carry; a wrong term, sign or
+        # head order is O(1)
         rel = np.linalg.norm(p - w_) / np.linalg.norm(w_)
         print(f"  small plan vs oracle: rel L2 {rel:.3g}, max {np.abs(p - w_).max():.3g}",
               flush=True)
-        assert rel <= 0.02
+        assert rel <= 0.02 and np.abs(p - w_).max() < 0.05
 
 
 def test_session_rejects_bad_steps_and_resets(gpu):
