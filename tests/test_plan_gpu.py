@@ -197,14 +197,35 @@ def test_session_rejects_bad_steps_and_resets(gpu):
 
 
 def test_qwen35_4b_decode_step(gpu):
+    """Qwen3.5-4B (32 layers, random W8A8 weights of its shapes): a 64-token
+    prefill and a decode step through the session equal, bit for bit, the
+    same two graphs run op by op through the per-op entry points (logits and
+    every state), and the decode step's records name the fused kernels."""
     c = G.qwen35_4b()
     print("qwen3.5-4b random weights", flush=True)
     weights = random_weights(c, True, gpu, seed=1)
     session = ModelSession(c, weights, 1024, True, gpu)
-    r = session.step(list(range(100, 164)), "last")
+    prompt = list(range(100, 164))
+    r = session.step(prompt, "last")
     assert r.logits.shape == (1, c.vocabulary) and np.isfinite(r.logits).all()
+    first = r.logits
     r = session.step([7], "last", trace=True)
     assert r.past == 65 and np.isfinite(r.logits).all()
+    print("qwen3.5-4b op by op", flush=True)
+    states = None
+    want = []
+    for past, chunk in ((0, prompt), (64, [7])):
+        g = G.build_qwen35(c, len(chunk), past, 1024, "last", True)
+        if states is None:
+            states = [torch.zeros(s.shape, dtype=torch.float32 if s.element == G.Element.F32
+                                  else torch.float16, device=gpu) for s in g.states]
+        ids = torch.tensor(chunk, dtype=torch.int32, device=gpu)
+        want.append(GraphRunner(g, weights, states, "gpu").run(ids)[0].float().cpu().numpy())
+    torch.cuda.synchronize()
+    assert np.array_equal(first.view(np.uint32), want[0].view(np.uint32))
+    assert np.array_equal(r.logits.view(np.uint32), want[1].view(np.uint32))
+    for a, b in zip(session.states, states):
+        assert _same_state(a, b)
     kinds = [d["kernel"] for d in r.dispatches]
     # deltaRecurrent: the update and its fused q / k L2Norms, a record each
     # gqaDecodeSplitK: KvAppend and CausalGqa in one fused call, a record each
