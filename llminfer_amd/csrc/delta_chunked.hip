@@ -6,7 +6,7 @@
 // by one. The published chunk algorithm (Yang, Kautz, Hatamizadeh, "Gated
 // Delta Networks", arXiv:2412.06464; Yang et al., "Parallelizing Linear
 // Transformers with the Delta Rule over Sequence Length", arXiv:2406.06484)
-// splits the tokens into chunks of C = 64. With g the cumulative log decay
+// splits the tokens into chunks of C = 32. With g the cumulative log decay
 // inside a chunk, per chunk and value head:
 //
 //   A[t][s] = beta_t e^(g_t - g_s) k_t.k_s  (s < t),  T = (I + A)^-1
@@ -28,24 +28,32 @@
 //
 // Two launches:
 //
-//  * deltaChunkPrep, grid (chunk, key head), 256 threads: every chunk at
-//    once. The Gram matrices K K^T and Q K^T on fp16 MFMA (kept in
-//    registers); per value head the decay weighting, T by blocked
-//    substitution (diagonal blocks in fp32, off-diagonal blocks on MFMA), and
-//    the products Wn, Q', Z0, Y0 on fp16 MFMA in split form. The results go to
-//    the workspace already in the register order of the scan's MFMA operands.
+//  * deltaChunkPrep, grid (chunk, key head), 256 threads, two workgroups a
+//    CU (56 KB of LDS each): every chunk at once. The Gram matrices K K^T
+//    and Q K^T on fp16 MFMA (kept in registers); per value head the decay
+//    weighting, T by blocked substitution (the two 16x16 diagonal blocks in
+//    fp32, the off-diagonal block on MFMA), and the products Wn, Q', Z0, Y0
+//    on fp16 MFMA in split form. The results go to the workspace already in
+//    the register order of the scan's MFMA operands.
 //
 //  * deltaChunkScan, grid (value head, 16-column dv slice), 4 compute waves
 //    and an L2-warming wave. Wave w keeps rows [32 w, 32 w + 32) of the
-//    state slice S [dk x 16] in registers and computes token tile w of each
-//    chunk's Z and Y; S and Z pass between the waves through LDS, two
-//    barriers per chunk. Every product runs on v_mfma_f32_16x16x32_f16,
-//    with the state (and Z) as the B operand straight from the C-layout
-//    registers of the product that made it: the k index of an operand block
-//    is permuted (sigma below) so that the 8 halves a lane supplies are the
-//    8 rows it holds in two consecutive 16-row C tiles; the A operands (Wn,
-//    Q', K^T) were written by the prep with the same permutation. Each wave
-//    loads its own operand blocks one chunk ahead into registers.
+//    state slice S [dk x 16] in registers; waves 0 and 1 compute the two
+//    16-token tiles of each chunk's Z, waves 2 and 3 those of Y; S and Z
+//    pass between the waves through LDS, two barriers per chunk. Every
+//    product runs on v_mfma_f32_16x16x32_f16, with the state (and Z) as the
+//    B operand straight from the C-layout registers of the product that made
+//    it: the k index of an operand block is permuted (sigma below) so that
+//    the 8 halves a lane supplies are the 8 rows it holds in two consecutive
+//    16-row C tiles; the A operands (Wn, Q', K^T) were written by the prep
+//    with the same permutation. Each wave loads its own operand blocks one
+//    chunk ahead into registers.
+//
+// Why 32: the prep's cost per chunk is dominated by its chain of dependent
+// phases (the triangular solve, the products that follow it), which shrink
+// with the chunk, and at 32 two workgroups share a CU and hide each other's
+// latencies; the scan's chain per chunk (two barriers, two short MFMA runs)
+// costs about as much at 32 as at 64 tokens' worth of work halved.
 //
 // Split form: x = hi + lo 2^-11 with hi = fp16(x), lo = fp16((x - hi) 2^11),
 // a.b ~ ah.bh + (ah.bl + al.bh) 2^-11, the cross terms in a second fp32
@@ -75,12 +83,15 @@
 namespace llmi {
 namespace {
 
-constexpr int C = 64;       // chunk length
+constexpr int C = 32;       // chunk length
 constexpr int DK = 128;     // key dimension handled by these kernels
 constexpr int KS = DK + 8;  // fp16 stride of [token][dk] rows in LDS (and of V rows)
 constexpr int CS = C + 8;   // fp16 stride of [*][token] rows in LDS
 constexpr int FS = C + 1;   // fp32 stride of the prep's A and T^T rows
 constexpr int VB = 128;     // dv columns of V the prep stages at a time
+constexpr int TT = C / 16;  // 16-token tiles of a chunk
+constexpr int KB = DK / 32; // 32-wide blocks of the key dimension
+constexpr int DT = DK / 16; // 16-wide tiles of the key dimension
 
 // MFMA operand blocks (v_mfma_f32_16x16x32_f16) in register order: lane l
 // holds 8 halves at halves [8 l, 8 l + 8) of the block.
@@ -91,28 +102,28 @@ constexpr int VB = 128;     // dv columns of V the prep stages at a time
 // (register r of tile m holds row 16m + 4g + r). A product whose k is
 // permuted the same way in both operands is unchanged.
 //
-// A piece is the operand of one scan product for one chunk: 16 blocks of hi
-// halves, then 16 blocks of lo halves. Wn and Q' pieces: block 4m + kb
-// holds rows t of tile m against permuted k = d in block kb. K^T piece:
-// block 2i + kb holds rows d of tile i against permuted k = t in block kb.
+// The operands of the scan's products for one chunk:
+//  * Wn piece (per chunk and value head): block KB m + kb holds token rows t
+//    of tile m against permuted k = d in block kb; TT x KB blocks of hi
+//    halves, then as many of lo halves.
+//  * Q' piece: the same blocks, hi halves only (Q' feeds the outputs alone).
+//  * K^T piece (per chunk and key head): block i holds rows d of tile i
+//    against permuted k = t (the chunk's one 32-token block); DT blocks of
+//    hi halves, then DT of lo halves.
 constexpr int kBlk = 64 * 8;
-constexpr int kPieceBlocks = 16;
-constexpr int kPieceHalves = 2 * kPieceBlocks * kBlk;
-constexpr int kPieceBytes = kPieceHalves * 2;      // 32 KiB
-constexpr int kBufferWord3 = 0x00020000;           // gfx9 raw buffer descriptor, dword 3
-typedef __attribute__((address_space(3))) void lds_void_t;
+constexpr int kWnBlocks = TT * KB;
+constexpr int kWnBytes = 2 * kWnBlocks * kBlk * 2; // 16 KiB
+constexpr int kQpBytes = kWnBlocks * kBlk * 2;     // 8 KiB
+constexpr int kKtBlocks = DT;
+constexpr int kKtBytes = 2 * kKtBlocks * kBlk * 2; // 16 KiB
 
-// Workspace. Per (chunk, value head) a record: the Wn piece (hi and lo),
-// the Q' piece (plain fp16: the 16 hi blocks only, Q' feeds the outputs
-// alone), then Z0 and Y0 as fp32 in C-layout register order, per 16-column
-// slice js and 16-row tile m a 64-lane block of float4 (block 4 js + m),
-// then 64 floats of scalars (e^(g_C) first). After all records, per (chunk,
-// key head) the K^T piece.
+// Workspace. Per (chunk, value head) a record: the Wn piece, the Q' piece,
+// then Z0 and Y0 as fp32 in C-layout register order, per 16-column slice js
+// and 16-row tile m a 64-lane block of float4 (block TT js + m), then 64
+// floats of scalars (e^(g_C) first). After all records, per (chunk, key
+// head) the K^T piece.
 constexpr int kScalarBytes = 256;
-constexpr int kQPieceBytes = kPieceBlocks * kBlk * 2; // 16 KiB
-__host__ __device__ inline size_t rec_z0(unsigned) {
-  return (size_t)kPieceBytes + kQPieceBytes;
-}
+__host__ __device__ inline size_t rec_z0(unsigned) { return (size_t)kWnBytes + kQpBytes; }
 __host__ __device__ inline size_t rec_scalars(unsigned DV) {
   return rec_z0(DV) + 2 * (size_t)C * DV * sizeof(float);
 }
@@ -125,7 +136,7 @@ __device__ __forceinline__ char *rec_ptr(void *ws, size_t recB, size_t Hv, size_
 }
 __device__ __forceinline__ char *kpiece_ptr(void *ws, size_t recB, size_t chunks, size_t Hv,
                                             size_t Hk, size_t c, size_t kh) {
-  return static_cast<char *>(ws) + chunks * Hv * recB + (c * Hk + kh) * kPieceBytes;
+  return static_cast<char *>(ws) + chunks * Hv * recB + (c * Hk + kh) * kKtBytes;
 }
 
 __device__ __forceinline__ float4_t mfma16(half8_t a, half8_t b, float4_t c) {
@@ -195,12 +206,15 @@ __device__ __forceinline__ void load_split4(const float *p, int stride, half4_t 
   split4(float4_t{p[0], p[stride], p[2 * stride], p[3 * stride]}, hi, lo);
 }
 
+// One workgroup per (chunk, key head), four waves; the key head's value
+// heads in turn.
+//
 // QK16: q and k arrive as fp16 rows and are L2-normalised here exactly as
 // l2NormF32 (Graph.metal:96-109) would: one lane per (token, q or k) row of
 // the chunk runs the reference's sequential sum of squares, and each fp32
 // element is the single product x * factor -- the bits l2NormF32 writes.
 template <bool QK16>
-__global__ __launch_bounds__(256, 1) void delta_prep_kernel(
+__global__ __launch_bounds__(256, 2) void delta_prep_kernel(
     const void *__restrict__ qp, const void *__restrict__ kp, const half_t *__restrict__ v,
     const float *__restrict__ beta, const float *__restrict__ decay, void *__restrict__ ws,
     unsigned T, unsigned Hk, unsigned Hv, unsigned DV, float eps, float qscale, unsigned *cnt) {
@@ -220,29 +234,33 @@ __global__ __launch_bounds__(256, 1) void delta_prep_kernel(
 
   __shared__ __attribute__((aligned(16))) half_t sKh[C * KS], sKl[C * KS];
   __shared__ __attribute__((aligned(16))) half_t sQV[C * KS]; // Q hi, later a V block
-  // A and T^T (fp32); before them, during the Gram products, Q lo
-  __shared__ __attribute__((aligned(16))) float sATT[2 * C * FS];
+  __shared__ __attribute__((aligned(16))) float sATT[2 * C * FS]; // A, then T^T
   float *const sA = sATT, *const sTT = sATT + C * FS;
-  half_t *const sQl = reinterpret_cast<half_t *>(sATT);
-  static_assert(C * KS * sizeof(half_t) <= 2 * C * FS * sizeof(float), "Q lo fits");
-  __shared__ __attribute__((aligned(16))) half_t sTwh[C * CS], sTwl[C * CS];
-  __shared__ __attribute__((aligned(16))) half_t sTbh[C * CS], sTbl[C * CS];
-  __shared__ __attribute__((aligned(16))) half_t sMh[C * CS], sMl[C * CS];
-  __shared__ __attribute__((aligned(16))) half_t sNh[C * CS], sNl[C * CS];
-  __shared__ double sG[C];
-  __shared__ float sB[C], sEg[C], sEz[C];
+  // T_w^T, T_b^T, M and -N as hi/lo [*][token] rows; Q lo before them,
+  // during the Gram products.
+  __shared__ __attribute__((aligned(16))) half_t sTMN[8 * C * CS];
+  half_t *const sTwh = sTMN, *const sTwl = sTMN + C * CS;
+  half_t *const sTbh = sTMN + 2 * C * CS, *const sTbl = sTMN + 3 * C * CS;
+  half_t *const sMh = sTMN + 4 * C * CS, *const sMl = sTMN + 5 * C * CS;
+  half_t *const sNh = sTMN + 6 * C * CS, *const sNl = sTMN + 7 * C * CS;
+  half_t *const sQl = sTMN;
+  static_assert(C * KS <= 8 * C * CS, "Q lo fits");
+  // Per value head, double-buffered by head parity: cumulative log decay,
+  // beta, e^(g_t), e^(g_C - g_t).
+  __shared__ double sG[2][C];
+  __shared__ float sB[2][C], sEg[2][C], sEz[2][C];
   __shared__ float sFac[QK16 ? 2 * C : 1]; // QK16: L2 factors of the k rows, then the q rows
 
   // Loads that later phases need, issued up front so that their latency
   // hides behind the K/Q split and the Gram products: the fp32 queries of
   // the Q' initial values (wave w: d tiles 2w, 2w + 1, all t), the gates
   // of the first value head (wave 0) and its first block of V.
-  float4_t qinit[2][4];
-  half4_t qraw[2][4]; // QK16: the fp16 queries, normalised once the factors are known
+  float4_t qinit[2][TT];
+  half4_t qraw[2][TT]; // QK16: the fp16 queries, normalised once the factors are known
 #pragma unroll
   for (int hf = 0; hf < 2; ++hf)
 #pragma unroll
-    for (int mt = 0; mt < 4; ++mt) {
+    for (int mt = 0; mt < TT; ++mt) {
       const unsigned t = 16 * mt + L, tc = min(t, n - 1); // rows past the end read row n-1
       const size_t off =
           (size_t)(t0 + tc) * qkStride + (size_t)kh * DK + 16 * (2 * wave + hf) + 4 * g;
@@ -253,11 +271,37 @@ __global__ __launch_bounds__(256, 1) void delta_prep_kernel(
         qinit[hf][mt] = t < n ? x : float4_t{0.0f, 0.0f, 0.0f, 0.0f};
       }
     }
+  // Wave 1 prepares each value head's gates one head ahead, off the chain of
+  // dependent phases: the loads, then the cumulative log decay (double;
+  // padding tokens: decay 1, beta 0), e^(g_t), e^(g_C - g_t) and e^(g_C).
   float gateA = 1.0f, gateB = 0.0f;
   auto load_gates = [&](unsigned h) {
-    if (wave == 0 && lane < n) {
+    if (wave == 1 && lane < n) {
       gateA = decay[(size_t)(t0 + lane) * Hv + h];
       gateB = beta[(size_t)(t0 + lane) * Hv + h];
+    }
+  };
+  auto gates = [&](unsigned hr) {
+    if (wave == 1) {
+      const unsigned t = lane, pb = hr & 1u;
+      const float a = gateA, b = gateB;
+      double gg = a > 0.0f ? (double)logf(a) : -1.0e4;
+#pragma unroll
+      for (int off = 1; off < C; off <<= 1) {
+        const double up = __shfl_up(gg, off);
+        if (lane >= (unsigned)off)
+          gg += up;
+      }
+      const double gC = __shfl(gg, C - 1);
+      if (t < C) {
+        sG[pb][t] = gg;
+        sB[pb][t] = b;
+        sEg[pb][t] = expf((float)gg);
+        sEz[pb][t] = expf((float)(gC - gg));
+      }
+      if (t == C - 1)
+        *reinterpret_cast<float *>(rec_ptr(ws, recB, Hv, c, kh * R + hr) + rec_scalars(DV)) =
+            expf((float)gg);
     }
   };
   load_gates(kh * R);
@@ -286,8 +330,8 @@ __global__ __launch_bounds__(256, 1) void delta_prep_kernel(
   const unsigned w0 = min((unsigned)VB, DV);
   fetch_v(kh * R, 0, w0);
 
-  // QK16: the L2 factors of the chunk's k rows (threads 0-63) and q rows
-  // (64-127), each the sequential sum over one row.
+  // QK16: the L2 factors of the chunk's k rows (threads 0 .. C-1) and q
+  // rows (C .. 2C-1), each the sequential sum over one row.
   if constexpr (QK16) {
     if (tid < 2 * C) {
       const unsigned t = tid % C, isq = tid / C;
@@ -307,7 +351,7 @@ __global__ __launch_bounds__(256, 1) void delta_prep_kernel(
 #pragma unroll
     for (int hf = 0; hf < 2; ++hf)
 #pragma unroll
-      for (int mt = 0; mt < 4; ++mt) {
+      for (int mt = 0; mt < TT; ++mt) {
         const unsigned t = 16 * mt + L;
         const float f = sFac[C + min(t, n - 1)];
         float4_t x;
@@ -355,118 +399,97 @@ __global__ __launch_bounds__(256, 1) void delta_prep_kernel(
       *reinterpret_cast<half4_t *>(sQl + t * KS + d4) = qlo;
     }
   }
+  gates(0);
+  if (R > 1)
+    load_gates(kh * R + 1);
   lds_sync();
 
-  // The K^T piece of this (chunk, key head): block b = 2i + kb, lane (g, L)
-  // element e = K[32 kb + sigma(g, e)][16 i + L].
+  // The K^T piece of this (chunk, key head): block i (wave w writes 2w and
+  // 2w + 1), lane (g, L) element e = K[sigma(g, e)][16 i + L].
   {
-    half_t *kp = reinterpret_cast<half_t *>(kpiece_ptr(ws, recB, chunks, Hv, Hk, c, kh));
+    half_t *kt = reinterpret_cast<half_t *>(kpiece_ptr(ws, recB, chunks, Hv, Hk, c, kh));
 #pragma unroll
-    for (int bi = 0; bi < 4; ++bi) {
-      const unsigned b = 4 * wave + bi, i = b / 2, kb = b % 2;
-      const unsigned off0 = ((32 * kb + 4 * g + L / 4) * KS + 16 * i + 4 * (L % 4)) * 2;
+    for (int bi = 0; bi < 2; ++bi) {
+      const unsigned b = 2 * wave + bi;
+      const unsigned off0 = ((4 * g + L / 4) * KS + 16 * b + 4 * (L % 4)) * 2;
       const unsigned off1 = off0 + 16 * KS * 2;
-      *reinterpret_cast<half8_t *>(kp + b * kBlk + 8 * lane) =
+      *reinterpret_cast<half8_t *>(kt + b * kBlk + 8 * lane) =
           cat8(read_tr(sKh, off0), read_tr(sKh, off1));
-      *reinterpret_cast<half8_t *>(kp + (kPieceBlocks + b) * kBlk + 8 * lane) =
+      *reinterpret_cast<half8_t *>(kt + (kKtBlocks + b) * kBlk + 8 * lane) =
           cat8(read_tr(sKl, off0), read_tr(sKl, off1));
     }
   }
 
-  // K K^T and Q K^T stay in registers: wave w holds the tiles of key
-  // columns s in [16 w, 16 w + 16) for the four row tiles (register r of
-  // tile mt: t = 16 mt + 4 g + r, s = 16 w + L). Split form: both feed M,
-  // and through M the outputs Y0 = M U0 and Q', where a row's output is
-  // often much smaller than the terms that cancel in it, so a plain fp16
-  // product (2^-11 relative per term) would show in rows of small RMS.
-  float4_t kk[4], qk[4];
-#pragma unroll
-  for (int mt = 0; mt < 4; ++mt) {
+  // K K^T and Q K^T stay in registers: wave w holds the tile of rows t in
+  // tile gm = w / 2 and columns s in tile gs = w % 2 (register r: t = 16 gm
+  // + 4 g + r, s = 16 gs + L). Split form: both feed M, and through M the
+  // outputs Y0 = M U0 and Q', where a row's output is often much smaller
+  // than the terms that cancel in it, so a plain fp16 product (2^-11
+  // relative per term) would show in rows of small RMS.
+  const unsigned gm = wave >> 1, gs = wave & 1u;
+  float4_t kk{0.0f, 0.0f, 0.0f, 0.0f}, qk{0.0f, 0.0f, 0.0f, 0.0f};
+  {
     float4_t kx{0.0f, 0.0f, 0.0f, 0.0f}, qx{0.0f, 0.0f, 0.0f, 0.0f};
-    kk[mt] = qk[mt] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-    for (int ks = 0; ks < DK / 32; ++ks) {
-      const unsigned bo = (16 * wave + L) * KS + 32 * ks + 8 * g;
-      const unsigned ao = (16 * mt + L) * KS + 32 * ks + 8 * g;
+    for (int ks = 0; ks < KB; ++ks) {
+      const unsigned bo = (16 * gs + L) * KS + 32 * ks + 8 * g;
+      const unsigned ao = (16 * gm + L) * KS + 32 * ks + 8 * g;
       const half8_t bh = load8(sKh + bo), bl = load8(sKl + bo);
       const half8_t kah = load8(sKh + ao), kal = load8(sKl + ao);
       const half8_t qah = load8(sQV + ao), qal = load8(sQl + ao);
-      kk[mt] = mfma16(kah, bh, kk[mt]);
-      qk[mt] = mfma16(qah, bh, qk[mt]);
+      kk = mfma16(kah, bh, kk);
+      qk = mfma16(qah, bh, qk);
       kx = mfma16(kah, bl, kx);
       qx = mfma16(qah, bl, qx);
       kx = mfma16(kal, bh, kx);
       qx = mfma16(qal, bh, qx);
     }
-    kk[mt] += kx * kSplitUnscale;
-    qk[mt] += qx * kSplitUnscale;
+    kk += kx * kSplitUnscale;
+    qk += qx * kSplitUnscale;
   }
 
   for (unsigned hr = 0; hr < R; ++hr) {
-    const unsigned h = kh * R + hr;
+    const unsigned h = kh * R + hr, pb = hr & 1u;
     char *const rec = rec_ptr(ws, recB, Hv, c, h);
+    const double *const hG = sG[pb];
+    const float *const hB = sB[pb], *const hEg = sEg[pb], *const hEz = sEz[pb];
     lds_sync(); // the previous head is done with every LDS buffer
 
-    // Cumulative log decay (double) and beta (padding tokens: decay 1,
-    // beta 0), e^(g_t), e^(g_C - g_t) and e^(g_C); V of the head's first
-    // dv block.
-    if (wave == 0) {
-      const unsigned t = lane;
-      const float a = gateA, b = gateB;
-      double gg = a > 0.0f ? (double)logf(a) : -1.0e4;
-#pragma unroll
-      for (int off = 1; off < 64; off <<= 1) {
-        const double up = __shfl_up(gg, off);
-        if (lane >= (unsigned)off)
-          gg += up;
-      }
-      const double gC = __shfl(gg, 63);
-      sG[t] = gg;
-      sB[t] = b;
-      sEg[t] = expf((float)gg);
-      sEz[t] = expf((float)(gC - gg));
-      if (t == 63)
-        *reinterpret_cast<float *>(rec + rec_scalars(DV)) = expf((float)gg);
-    }
+    // V of the head's first dv block; the next head's first V block in
+    // flight during this head (with DV > VB the V registers carry this
+    // head's further blocks, and the next head's first block is fetched
+    // after them).
     store_v(w0);
-    // The next head's gates and first V block, in flight during this head
-    // (with DV > VB the V registers carry this head's further blocks, and
-    // the next head's first block is fetched after them).
-    if (hr + 1 < R) {
-      load_gates(h + 1);
-      if (DV <= VB)
-        fetch_v(h + 1, 0, w0);
-    }
-    lds_sync();
+    if (hr + 1 < R && DV <= VB)
+      fetch_v(h + 1, 0, w0);
 
     // A (fp32) and M (hi/lo) from the Gram registers:
     // A[t][s] = beta_t e^(g_t - g_s) k_t.k_s (s < t), M[t][s] = e^(g_t - g_s)
     // q_t.k_s (s <= t), zero above.
     // Branch-free: every operand is read, the masks are selects.
     {
-      const unsigned s = 16 * wave + L;
-      const double gs = sG[s];
+      const unsigned s = 16 * gs + L;
+      const double gsv = hG[s];
 #pragma unroll
-      for (int mt = 0; mt < 4; ++mt)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const unsigned t = 16 * mt + 4 * g + r;
-          const float d = fminf((float)(sG[t] - gs), 0.0f);
-          const float e = s <= t ? __builtin_amdgcn_exp2f(d * kLog2e) : 0.0f;
-          const float a = sB[t] * e * kk[mt][r];
-          sA[t * FS + s] = s < t ? a : 0.0f;
-          split_f16(e * qk[mt][r], sMh[t * CS + s], sMl[t * CS + s]);
-        }
+      for (int r = 0; r < 4; ++r) {
+        const unsigned t = 16 * gm + 4 * g + r;
+        const float d = fminf((float)(hG[t] - gsv), 0.0f);
+        const float e = s <= t ? __builtin_amdgcn_exp2f(d * kLog2e) : 0.0f;
+        const float a = hB[t] * e * kk[r];
+        sA[t * FS + s] = s < t ? a : 0.0f;
+        split_f16(e * qk[r], sMh[t * CS + s], sMl[t * CS + s]);
+      }
     }
-    lds_sync();
 
-    // T = (I + A)^-1 into sTT[s][t] = T[t][s], on 16x16 blocks. The
-    // diagonal blocks D_i = (I + A_ii)^-1 by forward substitution (wave i,
-    // lane j < 16 owns column j); then block rows i = 1..3 on MFMA
-    // (v_mfma_f32_16x16x16_f16, split form), whose C layout is also its B
-    // layout: T_ij = -D_i sum_{k=j}^{i-1} A_ik T_kj, wave j computing T_ij.
-    if (lane < 16) {
-      const unsigned j = lane, b0 = 16 * wave;
+    // T = (I + A)^-1 on 16x16 blocks. The diagonal blocks D_i = (I +
+    // A_ii)^-1 by forward substitution on the waves that wrote A_ii (waves 0
+    // and 3: they read only their own LDS writes, so no barrier), lane j <
+    // 16 owning column j; D_i goes to sTT[s][t] = T[t][s] for the product
+    // below, and straight into T_w^T[s][t] = beta_s e^(g_s) T[t][s] and
+    // T_b^T[s][t] = beta_s T[t][s] (hi/lo), with the zeros of T_w^T / T_b^T
+    // above the diagonal blocks (wave 3: s >= 16, t < 16).
+    if ((wave == 0 || wave == 3) && lane < 16) {
+      const unsigned j = lane, b0 = wave == 0 ? 0u : 16u;
       float col[16];
 #pragma unroll
       for (int t = 0; t < 16; ++t) {
@@ -479,180 +502,160 @@ __global__ __launch_bounds__(256, 1) void delta_prep_kernel(
 #pragma unroll
       for (int t = 0; t < 16; ++t)
         sTT[(b0 + j) * FS + b0 + t] = col[t];
-    }
-    lds_sync();
-    for (unsigned i = 1; i < 4; ++i) {
-      if (wave < i) {
-        const unsigned jb = wave;
-        float4_t p{0.0f, 0.0f, 0.0f, 0.0f}, px{0.0f, 0.0f, 0.0f, 0.0f};
-        for (unsigned kq = jb; kq < i; ++kq) {
-          half4_t ah, al, bh, bl;
-          // A_ik[L][4g + e] and T_kj[4g + e][L] = sTT[16j + L][16k + 4g + e].
-          load_split4(sA + (16 * i + L) * FS + 16 * kq + 4 * g, 1, ah, al);
-          load_split4(sTT + (16 * jb + L) * FS + 16 * kq + 4 * g, 1, bh, bl);
-          p = mfma16k16(ah, bh, p);
-          px = mfma16k16(ah, bl, px);
-          px = mfma16k16(al, bh, px);
-        }
-        half4_t bh, bl, dh, dl;
-        split4(p + px * kSplitUnscale, bh, bl);
-        // D_i[L][4g + e] = sTT[16i + 4g + e][16i + L].
-        load_split4(sTT + (16 * i + 4 * g) * FS + 16 * i + L, FS, dh, dl);
-        float4_t tt{0.0f, 0.0f, 0.0f, 0.0f}, tx{0.0f, 0.0f, 0.0f, 0.0f};
-        tt = mfma16k16(dh, bh, tt);
-        tx = mfma16k16(dh, bl, tx);
-        tx = mfma16k16(dl, bh, tx);
-        const float4_t res = -(tt + tx * kSplitUnscale);
+      const unsigned s = b0 + j;
+      const float bw = hB[s] * hEg[s], bb = hB[s];
 #pragma unroll
-        for (int r = 0; r < 4; ++r)
-          sTT[(16 * jb + L) * FS + 16 * i + 4 * g + r] = res[r];
-      }
-      lds_sync();
-    }
-
-    // T_w^T[s][t] = beta_s e^(g_s) T[t][s] and T_b^T[s][t] = beta_s T[t][s],
-    // hi/lo.
-    {
-      const unsigned s = tid / 4, tb = 16 * (tid % 4);
-      const float bw = sB[s] * sEg[s], bb = sB[s];
-#pragma unroll
-      for (int x4 = 0; x4 < 4; ++x4) {
-        float4_t tv;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const unsigned t = tb + 4 * x4 + e;
-          const float x = sTT[s * FS + t]; // read always: the select below is branch-free
-          tv[e] = t >= s ? x : 0.0f;
-        }
+      for (int q4 = 0; q4 < 4; ++q4) {
+        const float4_t tv{col[4 * q4], col[4 * q4 + 1], col[4 * q4 + 2], col[4 * q4 + 3]};
         half4_t wh, wl, bh, bl;
         split4(tv * bw, wh, wl);
         split4(tv * bb, bh, bl);
-        const unsigned o = s * CS + tb + 4 * x4;
+        const unsigned o = s * CS + b0 + 4 * q4;
         *reinterpret_cast<half4_t *>(sTwh + o) = wh;
         *reinterpret_cast<half4_t *>(sTwl + o) = wl;
         *reinterpret_cast<half4_t *>(sTbh + o) = bh;
         *reinterpret_cast<half4_t *>(sTbl + o) = bl;
+        if (b0 == 16) {
+          const half4_t z{0, 0, 0, 0};
+          const unsigned oz = s * CS + 4 * q4;
+          *reinterpret_cast<half4_t *>(sTwh + oz) = z;
+          *reinterpret_cast<half4_t *>(sTwl + oz) = z;
+          *reinterpret_cast<half4_t *>(sTbh + oz) = z;
+          *reinterpret_cast<half4_t *>(sTbl + oz) = z;
+        }
       }
+    }
+    lds_sync();
+    // The block below the diagonal, T_10 = -D_1 A_10 D_0, on MFMA
+    // (v_mfma_f32_16x16x16_f16, split form; its C layout is also its B
+    // layout), on wave 0, into T_w^T / T_b^T directly. Meanwhile wave 1
+    // prepares the next head's gates.
+    if (wave == 0) {
+      half4_t ah, al, bh, bl;
+      // A_10[L][4g + e] and D_0[4g + e][L] = sTT[L][4g + e].
+      load_split4(sA + (16 + L) * FS + 4 * g, 1, ah, al);
+      load_split4(sTT + L * FS + 4 * g, 1, bh, bl);
+      float4_t p{0.0f, 0.0f, 0.0f, 0.0f}, px{0.0f, 0.0f, 0.0f, 0.0f};
+      p = mfma16k16(ah, bh, p);
+      px = mfma16k16(ah, bl, px);
+      px = mfma16k16(al, bh, px);
+      half4_t ph, pl, dh, dl;
+      split4(p + px * kSplitUnscale, ph, pl);
+      // D_1[L][4g + e] = sTT[16 + 4g + e][16 + L].
+      load_split4(sTT + (16 + 4 * g) * FS + 16 + L, FS, dh, dl);
+      float4_t tt{0.0f, 0.0f, 0.0f, 0.0f}, tx{0.0f, 0.0f, 0.0f, 0.0f};
+      tt = mfma16k16(dh, ph, tt);
+      tx = mfma16k16(dh, pl, tx);
+      tx = mfma16k16(dl, ph, tx);
+      // Register r: T[16 + 4g + r][L], i.e. T_w^T / T_b^T row s = L at
+      // columns 16 + 4g + r.
+      const float4_t res = -(tt + tx * kSplitUnscale);
+      const float bw = hB[L] * hEg[L], bb = hB[L];
+      half4_t wh, wl, vh, vl;
+      split4(res * bw, wh, wl);
+      split4(res * bb, vh, vl);
+      const unsigned o = L * CS + 16 + 4 * g;
+      *reinterpret_cast<half4_t *>(sTwh + o) = wh;
+      *reinterpret_cast<half4_t *>(sTwl + o) = wl;
+      *reinterpret_cast<half4_t *>(sTbh + o) = vh;
+      *reinterpret_cast<half4_t *>(sTbl + o) = vl;
+    }
+    if (hr + 1 < R) {
+      gates(hr + 1);
+      if (hr + 2 < R)
+        load_gates(h + 2);
     }
     lds_sync();
 
     // N^T = T_w^T M^T (N = M T diag(beta e^g)); -N to LDS as [t][s] hi/lo.
-    // Wave w: s rows [16 w, 16 w + 16), all four t tiles.
+    // Wave w: the tile of s rows 16 (w / 2) .. and t columns 16 (w % 2) ..
     {
-      half8_t ah[2], al[2];
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
-        ah[ks] = load8(sTwh + (16 * wave + L) * CS + 32 * ks + 8 * g);
-        al[ks] = load8(sTwl + (16 * wave + L) * CS + 32 * ks + 8 * g);
-      }
-      float4_t acc[4], crs[4];
-#pragma unroll
-      for (int tt = 0; tt < 4; ++tt) {
-        acc[tt] = crs[tt] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
-          const half8_t bh = load8(sMh + (16 * tt + L) * CS + 32 * ks + 8 * g);
-          const half8_t bl = load8(sMl + (16 * tt + L) * CS + 32 * ks + 8 * g);
-          acc[tt] = mfma16(ah[ks], bh, acc[tt]);
-          crs[tt] = mfma16(ah[ks], bl, crs[tt]);
-          crs[tt] = mfma16(al[ks], bh, crs[tt]);
-        }
-      }
-#pragma unroll
-      for (int tt = 0; tt < 4; ++tt) {
-        half4_t nh, nl;
-        split4(-(acc[tt] + crs[tt] * kSplitUnscale), nh, nl);
-        const unsigned o = (16 * tt + L) * CS + 16 * wave + 4 * g;
-        *reinterpret_cast<half4_t *>(sNh + o) = nh;
-        *reinterpret_cast<half4_t *>(sNl + o) = nl;
-      }
+      const unsigned st = wave >> 1, tt = wave & 1u;
+      const half8_t ah = load8(sTwh + (16 * st + L) * CS + 8 * g);
+      const half8_t al = load8(sTwl + (16 * st + L) * CS + 8 * g);
+      const half8_t bh = load8(sMh + (16 * tt + L) * CS + 8 * g);
+      const half8_t bl = load8(sMl + (16 * tt + L) * CS + 8 * g);
+      float4_t acc{0.0f, 0.0f, 0.0f, 0.0f}, crs{0.0f, 0.0f, 0.0f, 0.0f};
+      acc = mfma16(ah, bh, acc);
+      crs = mfma16(ah, bl, crs);
+      crs = mfma16(al, bh, crs);
+      half4_t nh, nl;
+      split4(-(acc + crs * kSplitUnscale), nh, nl);
+      const unsigned o = (16 * tt + L) * CS + 16 * st + 4 * g;
+      *reinterpret_cast<half4_t *>(sNh + o) = nh;
+      *reinterpret_cast<half4_t *>(sNl + o) = nl;
     }
     lds_sync();
 
     // Wn and Q' pieces: W^T = K^T T_w^T and Q'^T = e^g Q^T - K^T N^T share
     // the K^T operand. Wave w writes the blocks (m, kb = w): tiles d = 2w,
-    // 2w + 1 of the transposed products against the four t tiles m.
+    // 2w + 1 of the transposed products against the token tiles m.
     {
       half_t *const wp = reinterpret_cast<half_t *>(rec);
-      half_t *const qp = reinterpret_cast<half_t *>(rec + kPieceBytes);
-      half8_t kah[2][2], kal[2][2]; // [d tile][ks]
+      half_t *const qp = reinterpret_cast<half_t *>(rec + kWnBytes);
+      half8_t kah[2], kal[2]; // [d tile]
 #pragma unroll
-      for (int hf = 0; hf < 2; ++hf)
+      for (int hf = 0; hf < 2; ++hf) {
+        kah[hf] = read_kcol(sKh, KS, 0, 16 * (2 * wave + hf), g, L);
+        kal[hf] = read_kcol(sKl, KS, 0, 16 * (2 * wave + hf), g, L);
+      }
+      half8_t b1h[TT], b1l[TT], b2h[TT], b2l[TT];
 #pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
-          kah[hf][ks] = read_kcol(sKh, KS, 32 * ks, 16 * (2 * wave + hf), g, L);
-          kal[hf][ks] = read_kcol(sKl, KS, 32 * ks, 16 * (2 * wave + hf), g, L);
+      for (int mt = 0; mt < TT; ++mt) {
+        const unsigned t = 16 * mt + L;
+        b1h[mt] = read_kcol(sTwh, CS, 0, 16 * mt, g, L);
+        b1l[mt] = read_kcol(sTwl, CS, 0, 16 * mt, g, L);
+        b2h[mt] = load8(sNh + t * CS + 8 * g);
+        b2l[mt] = load8(sNl + t * CS + 8 * g);
+      }
+      float4_t wa[TT][2], wx[TT][2], qa[TT][2], qx[TT][2]; // [token tile][d tile]
+#pragma unroll
+      for (int mt = 0; mt < TT; ++mt)
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf) {
+          wa[mt][hf] = wx[mt][hf] = qx[mt][hf] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
+          qa[mt][hf] = qinit[hf][mt] * hEg[16 * mt + L];
         }
-      // Two t tiles at a time: their B operands read first, then 48 MFMAs
-      // over 16 independent accumulators.
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int mp = 0; mp < 2; ++mp) {
-        half8_t b1h[2][2], b1l[2][2], b2h[2][2], b2l[2][2]; // [tile of the pair][ks]
+      for (int mt = 0; mt < TT; ++mt)
 #pragma unroll
-        for (int u = 0; u < 2; ++u) {
-          const int mt = 2 * mp + u;
-          const unsigned t = 16 * mt + L;
+        for (int hf = 0; hf < 2; ++hf) {
+          wa[mt][hf] = mfma16(kah[hf], b1h[mt], wa[mt][hf]);
+          qa[mt][hf] = mfma16(kah[hf], b2h[mt], qa[mt][hf]);
+        }
 #pragma unroll
-          for (int ks = 0; ks < 2; ++ks) {
-            b1h[u][ks] = read_kcol(sTwh, CS, 32 * ks, 16 * mt, g, L);
-            b1l[u][ks] = read_kcol(sTwl, CS, 32 * ks, 16 * mt, g, L);
-            b2h[u][ks] = load8(sNh + t * CS + 32 * ks + 8 * g);
-            b2l[u][ks] = load8(sNl + t * CS + 32 * ks + 8 * g);
+      for (int mt = 0; mt < TT; ++mt)
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf) {
+          wx[mt][hf] = mfma16(kah[hf], b1l[mt], wx[mt][hf]);
+          qx[mt][hf] = mfma16(kah[hf], b2l[mt], qx[mt][hf]);
+        }
+#pragma unroll
+      for (int mt = 0; mt < TT; ++mt)
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf) {
+          wx[mt][hf] = mfma16(kal[hf], b1h[mt], wx[mt][hf]);
+          qx[mt][hf] = mfma16(kal[hf], b2h[mt], qx[mt][hf]);
+        }
+#pragma unroll
+      for (int mt = 0; mt < TT; ++mt) {
+        const float ez = hEz[16 * mt + L];
+        half8_t wh, wl, qh;
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            half_t a, b;
+            split_f16(-ez * (wa[mt][hf][r] + wx[mt][hf][r] * kSplitUnscale), a, b);
+            wh[4 * hf + r] = a;
+            wl[4 * hf + r] = b;
+            qh[4 * hf + r] = (half_t)(qa[mt][hf][r] + qx[mt][hf][r] * kSplitUnscale);
           }
-        }
-        float4_t wa[2][2], wx[2][2], qa[2][2], qx[2][2]; // [tile of the pair][d tile]
-#pragma unroll
-        for (int u = 0; u < 2; ++u)
-#pragma unroll
-          for (int hf = 0; hf < 2; ++hf) {
-            wa[u][hf] = wx[u][hf] = qx[u][hf] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
-            qa[u][hf] = qinit[hf][2 * mp + u] * sEg[16 * (2 * mp + u) + L];
-          }
-        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
-#pragma unroll
-          for (int u = 0; u < 2; ++u)
-#pragma unroll
-            for (int hf = 0; hf < 2; ++hf) {
-              wa[u][hf] = mfma16(kah[hf][ks], b1h[u][ks], wa[u][hf]);
-              qa[u][hf] = mfma16(kah[hf][ks], b2h[u][ks], qa[u][hf]);
-            }
-#pragma unroll
-          for (int u = 0; u < 2; ++u)
-#pragma unroll
-            for (int hf = 0; hf < 2; ++hf) {
-              wx[u][hf] = mfma16(kah[hf][ks], b1l[u][ks], wx[u][hf]);
-              qx[u][hf] = mfma16(kah[hf][ks], b2l[u][ks], qx[u][hf]);
-            }
-#pragma unroll
-          for (int u = 0; u < 2; ++u)
-#pragma unroll
-            for (int hf = 0; hf < 2; ++hf) {
-              wx[u][hf] = mfma16(kal[hf][ks], b1h[u][ks], wx[u][hf]);
-              qx[u][hf] = mfma16(kal[hf][ks], b2h[u][ks], qx[u][hf]);
-            }
-        }
-#pragma unroll
-        for (int u = 0; u < 2; ++u) {
-          const int mt = 2 * mp + u;
-          const float ez = sEz[16 * mt + L];
-          half8_t wh, wl, qh;
-#pragma unroll
-          for (int hf = 0; hf < 2; ++hf)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-              half_t a, b;
-              split_f16(-ez * (wa[u][hf][r] + wx[u][hf][r] * kSplitUnscale), a, b);
-              wh[4 * hf + r] = a;
-              wl[4 * hf + r] = b;
-              qh[4 * hf + r] = (half_t)(qa[u][hf][r] + qx[u][hf][r] * kSplitUnscale);
-            }
-          const unsigned o = (4 * mt + wave) * kBlk + 8 * lane;
-          *reinterpret_cast<half8_t *>(wp + o) = wh;
-          *reinterpret_cast<half8_t *>(wp + kPieceBlocks * kBlk + o) = wl;
-          *reinterpret_cast<half8_t *>(qp + o) = qh;
-        }
+        const unsigned o = (KB * mt + wave) * kBlk + 8 * lane;
+        *reinterpret_cast<half8_t *>(wp + o) = wh;
+        *reinterpret_cast<half8_t *>(wp + kWnBlocks * kBlk + o) = wl;
+        *reinterpret_cast<half8_t *>(qp + o) = qh;
       }
     }
 
@@ -661,23 +664,21 @@ __global__ __launch_bounds__(256, 1) void delta_prep_kernel(
     // operand straight from its C-layout registers. The T_b and M operands
     // are read once per wave.
     {
-      half8_t tbh[4][2], tbl[4][2], mah[4][2], mal[4][2];
+      half8_t tbh[TT], tbl[TT], mah[TT], mal[TT];
 #pragma unroll
-      for (int mt = 0; mt < 4; ++mt)
+      for (int mt = 0; mt < TT; ++mt) {
+        tbh[mt] = read_kcol(sTbh, CS, 0, 16 * mt, g, L);
+        tbl[mt] = read_kcol(sTbl, CS, 0, 16 * mt, g, L);
+        const unsigned o = (16 * mt + L) * CS + 4 * g;
+        mah[mt] = cat8(load4(sMh + o), load4(sMh + o + 16));
+        mal[mt] = cat8(load4(sMl + o), load4(sMl + o + 16));
+      }
+      float ezr[TT][4];
 #pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
-          tbh[mt][ks] = read_kcol(sTbh, CS, 32 * ks, 16 * mt, g, L);
-          tbl[mt][ks] = read_kcol(sTbl, CS, 32 * ks, 16 * mt, g, L);
-          const unsigned o = (16 * mt + L) * CS + 32 * ks + 4 * g;
-          mah[mt][ks] = cat8(load4(sMh + o), load4(sMh + o + 16));
-          mal[mt][ks] = cat8(load4(sMl + o), load4(sMl + o + 16));
-        }
-      float ezr[4][4];
-#pragma unroll
-      for (int mt = 0; mt < 4; ++mt)
+      for (int mt = 0; mt < TT; ++mt)
 #pragma unroll
         for (int r = 0; r < 4; ++r)
-          ezr[mt][r] = sEz[16 * mt + 4 * g + r];
+          ezr[mt][r] = hEz[16 * mt + 4 * g + r];
       float4_t *const z0 = reinterpret_cast<float4_t *>(rec + rec_z0(DV));
       float4_t *const y0 = z0 + (size_t)C * DV / 4;
       for (unsigned jb = 0; jb < DV; jb += VB) {
@@ -692,48 +693,30 @@ __global__ __launch_bounds__(256, 1) void delta_prep_kernel(
 #pragma unroll 1
         for (unsigned jt = wave; jt < w / 16; jt += 4) {
           const unsigned js = jb / 16 + jt;
-          half8_t bv[2];
+          const half8_t bv = read_kcol(sQV, KS, 0, 16 * jt, g, L);
+          float4_t u[TT];
 #pragma unroll
-          for (int ks = 0; ks < 2; ++ks)
-            bv[ks] = read_kcol(sQV, KS, 32 * ks, 16 * jt, g, L);
-          float4_t ua[4], ux[4];
-#pragma unroll
-          for (int mt = 0; mt < 4; ++mt) {
-            ua[mt] = ux[mt] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-            for (int ks = 0; ks < 2; ++ks) {
-              ua[mt] = mfma16(tbh[mt][ks], bv[ks], ua[mt]);
-              ux[mt] = mfma16(tbl[mt][ks], bv[ks], ux[mt]);
-            }
-          }
-          float4_t u[4];
-#pragma unroll
-          for (int mt = 0; mt < 4; ++mt) {
-            u[mt] = ua[mt] + ux[mt] * kSplitUnscale;
+          for (int mt = 0; mt < TT; ++mt) {
+            float4_t ua{0.0f, 0.0f, 0.0f, 0.0f}, ux{0.0f, 0.0f, 0.0f, 0.0f};
+            ua = mfma16(tbh[mt], bv, ua);
+            ux = mfma16(tbl[mt], bv, ux);
+            u[mt] = ua + ux * kSplitUnscale;
             float4_t zz;
 #pragma unroll
             for (int r = 0; r < 4; ++r)
               zz[r] = ezr[mt][r] * u[mt][r];
-            z0[(js * 4 + mt) * 64 + lane] = zz;
+            z0[(js * TT + mt) * 64 + lane] = zz;
           }
-          half8_t ubh[2], ubl[2];
+          half8_t ubh, ubl;
+          split8(u[0], u[1], ubh, ubl);
 #pragma unroll
-          for (int kb = 0; kb < 2; ++kb)
-            split8(u[2 * kb], u[2 * kb + 1], ubh[kb], ubl[kb]);
-          float4_t ya[4], yx[4];
-#pragma unroll
-          for (int mt = 0; mt < 4; ++mt) {
-            ya[mt] = yx[mt] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-            for (int kb = 0; kb < 2; ++kb) {
-              ya[mt] = mfma16(mah[mt][kb], ubh[kb], ya[mt]);
-              yx[mt] = mfma16(mah[mt][kb], ubl[kb], yx[mt]);
-              yx[mt] = mfma16(mal[mt][kb], ubh[kb], yx[mt]);
-            }
+          for (int mt = 0; mt < TT; ++mt) {
+            float4_t ya{0.0f, 0.0f, 0.0f, 0.0f}, yx{0.0f, 0.0f, 0.0f, 0.0f};
+            ya = mfma16(mah[mt], ubh, ya);
+            yx = mfma16(mah[mt], ubl, yx);
+            yx = mfma16(mal[mt], ubh, yx);
+            y0[(js * TT + mt) * 64 + lane] = ya + yx * kSplitUnscale;
           }
-#pragma unroll
-          for (int mt = 0; mt < 4; ++mt)
-            y0[(js * 4 + mt) * 64 + lane] = ya[mt] + yx[mt] * kSplitUnscale;
         }
       }
     }
@@ -744,35 +727,35 @@ __global__ __launch_bounds__(256, 1) void delta_prep_kernel(
 
 // --------------------------------------------------------------- scan
 
-// The scan workgroup: 4 waves, one per SIMD, for one (value head, 16-column
-// dv slice). Wave w owns rows [32 w, 32 w + 32) of the slice's state (C
-// tiles 2w and 2w + 1, in its registers for the whole call) and token tile
-// w (rows [16 w, 16 w + 16)) of each chunk's Z and Y. Per chunk:
+// The scan workgroup: 4 compute waves, one per SIMD, for one (value head,
+// 16-column dv slice). Wave w owns rows [32 w, 32 w + 32) of the slice's
+// state (C tiles 2w and 2w + 1, in its registers for the whole call).
+// Per chunk:
 //   1. every wave splits its state rows into the hi/lo B operand of k block
 //      w and puts it in LDS; barrier X1; every wave reads the whole split S;
-//   2. Z_w = Z0_w + sum_kb Wn[w][kb] S[kb], Y_w = Y0_w + sum_kb Q'[w][kb] S[kb];
-//   3. Z_w, split, to LDS; barrier X2; every wave reads the split Z;
-//   4. S_w <- e^(g_C) S_w + sum_kb K^T[w][kb] Z[kb] (the two C tiles of w).
-// The chain of a chunk is thus 12 + 12 MFMAs per wave instead of 48 + 48 on
-// one wave. Each wave loads exactly the operand blocks it multiplies (a
-// quarter of each piece, 88 KB per workgroup and chunk), one chunk ahead,
-// straight into its registers. A fifth wave keeps those loads L2 hits: the
-// pieces come from HBM / the MALL (the prep wrote them), ~3,500 cycles away
-// under this load against ~1,900 cycles of work per chunk, so it reads one
-// dword per 128-byte line of its workgroup's share of the record and K^T
-// piece of chunk c + kWarmAhead (the slice workgroups of a value head share
-// an XCD, and split the head's lines between them). Its loads count on its
-// own vmcnt, so the compute waves' waits never cover them. No wave issues a global store inside the
-// chunk loop -- the Y tiles go to an LDS stage that is written out every
-// kStageChunks chunks and at the end -- so a wave's only outstanding
-// vector-memory operations are those loads, which complete in order: the
-// wait for one chunk's operands then never drains the next chunk's (with a
-// store pending the compiler's wait would be vmcnt(0)).
-constexpr int kStageChunks = 32;
+//   2. waves 0 and 1: Z_m = Z0_m + sum_kb Wn[m][kb] S[kb] for token tile
+//      m = w; waves 2 and 3: Y_m = Y0_m + sum_kb Q'[m][kb] S[kb], m = w - 2;
+//   3. Z_m, split, to LDS; barrier X2; every wave reads the split Z;
+//   4. S_w <- e^(g_C) S_w + K^T[w] Z (the two C tiles of w).
+// Each wave loads exactly the operand blocks it multiplies (44 KB per
+// workgroup and chunk in all), one chunk ahead, straight into its
+// registers. A fifth wave keeps those loads L2 hits: the pieces come from
+// HBM / the MALL (the prep wrote them), so it reads one dword per 128-byte
+// line of its workgroup's share of the record and K^T piece of chunk
+// c + kWarmAhead (the slice workgroups of a value head share an XCD, and
+// split the head's lines between them). Its loads count on its own vmcnt,
+// so the compute waves' waits never cover them. No wave issues a global
+// store inside the chunk loop -- the Y tiles go to an LDS stage that is
+// written out every kStageChunks chunks and at the end -- so a wave's only
+// outstanding vector-memory operations are those loads, which complete in
+// order: the wait for one chunk's operands then never drains the next
+// chunk's (with a store pending the compiler's wait would be vmcnt(0)).
+constexpr int kStageChunks = 64;
 constexpr int kAhead = 1;      // chunks of operands in flight in registers
-constexpr int kWarmAhead = 3;  // chunks ahead that the warming wave reads
+constexpr int kWarmAhead = 4;  // chunks ahead that the warming wave reads
 constexpr int kWarmSets = 8;   // its register sets (a touch is consumed kWarmSets chunks later)
 constexpr int kScanThreads = 320;
+static_assert(TT == 2, "two token tiles a chunk: two Z waves and two Y waves");
 
 // With NORM the kernel ends with gatedRmsNorm over the value head's output
 // rows (Reference.metal:228-259): once every slice workgroup of the head has
@@ -807,57 +790,62 @@ __global__ __launch_bounds__(kScanThreads, 1) void delta_scan_kernel(
   const unsigned chunks = (T + C - 1) / C, last = chunks - 1;
   const size_t recB = rec_bytes(DV), vStride = (size_t)Hv * DV;
   void *const wsp = const_cast<void *>(ws);
+  // Waves 0-1 compute Z tiles, waves 2-3 Y tiles; m is the token tile.
+  const bool zw = w < 2;
+  const unsigned m = w & 1u;
 
-  __shared__ half8_t sSx[2][4][64]; // split S: [hi, lo][k block][lane]
-  __shared__ half8_t sZx[2][2][64]; // split Z: [hi, lo][k block][lane], tile 2kb | 2kb + 1
+  __shared__ half8_t sSx[2][KB][64]; // split S: [hi, lo][k block][lane]
+  __shared__ half8_t sZx[2][64];     // split Z: [hi, lo][lane], tiles 0 | 1
   __shared__ __attribute__((aligned(16))) half_t sY[kStageChunks][C][16];
 
   // The operand blocks of wave w for one chunk.
   struct Ops {
-    half8_t wn[2][4]; // Wn blocks (w, kb): [hi, lo][kb]
-    half8_t kt[2][4]; // K^T blocks (tile 2w + i, kb) at 2i + kb: [hi, lo][.]
-    half8_t qp[4];    // Q' blocks (w, kb)
-    float4_t z0, y0;  // tile w of the slice's Z0 and Y0
+    half8_t a[2][KB]; // Z waves: Wn blocks (m, kb) [hi, lo][kb]; Y waves: Q' blocks in a[0]
+    half8_t kt[2][2]; // K^T blocks (tile 2w + i): [hi, lo][i]
+    float4_t zy;      // tile m of the slice's Z0 (Z waves) or Y0 (Y waves)
     float eC;         // e^(g_C)
   };
   // The loads of one chunk's operands in three parts, which a step spreads
-  // over its phases: issued in one burst, the 88 KB of a workgroup's loads
-  // would hold each wave at its load instructions until the CU's memory
-  // pipeline took them (~57 bytes per cycle per CU from L2, measured),
-  // while its MFMAs wait behind them.
-  auto load_wn = [&](unsigned c, Ops &d) {
+  // over its phases: issued in one burst, a workgroup's loads would hold
+  // each wave at its load instructions until the CU's memory pipeline took
+  // them (~57 bytes per cycle per CU from L2, measured), while its MFMAs
+  // wait behind them.
+  auto load_a = [&](unsigned c, Ops &d) __attribute__((always_inline)) {
+    // The hi blocks (Wn or Q') through a selected pointer, the Wn lo blocks
+    // under a branch: with stores to different fields in the two arms of one
+    // branch, the optimiser merges them into a store through a selected
+    // address, and the buffers then live in scratch memory.
     const char *r = rec_ptr(wsp, recB, Hv, c, h);
-    const half8_t *pw = reinterpret_cast<const half8_t *>(r) + 4 * w * 64 + lane;
+    const half8_t *p =
+        reinterpret_cast<const half8_t *>(r + (zw ? 0 : kWnBytes)) + KB * m * 64 + lane;
 #pragma unroll
-    for (int b = 0; b < 4; ++b) {
-      d.wn[0][b] = pw[b * 64];
-      d.wn[1][b] = pw[(kPieceBlocks + b) * 64];
+    for (int b = 0; b < KB; ++b)
+      d.a[0][b] = p[b * 64];
+    if (zw) {
+#pragma unroll
+      for (int b = 0; b < KB; ++b)
+        d.a[1][b] = p[(kWnBlocks + b) * 64];
     }
   };
-  auto load_kt = [&](unsigned c, Ops &d) {
+  auto load_kt = [&](unsigned c, Ops &d) __attribute__((always_inline)) {
     const half8_t *pk =
         reinterpret_cast<const half8_t *>(kpiece_ptr(wsp, recB, chunks, Hv, Hk, c, kh)) +
-        4 * w * 64 + lane;
+        2 * w * 64 + lane;
 #pragma unroll
-    for (int b = 0; b < 4; ++b) {
-      d.kt[0][b] = pk[b * 64];
-      d.kt[1][b] = pk[(kPieceBlocks + b) * 64];
+    for (int i = 0; i < 2; ++i) {
+      d.kt[0][i] = pk[i * 64];
+      d.kt[1][i] = pk[(kKtBlocks + i) * 64];
     }
   };
-  auto load_qz = [&](unsigned c, Ops &d) {
+  auto load_qz = [&](unsigned c, Ops &d) __attribute__((always_inline)) {
     const char *r = rec_ptr(wsp, recB, Hv, c, h);
-    const half8_t *pq = reinterpret_cast<const half8_t *>(r + kPieceBytes) + 4 * w * 64 + lane;
-#pragma unroll
-    for (int b = 0; b < 4; ++b)
-      d.qp[b] = pq[b * 64];
     const float4_t *pz =
-        reinterpret_cast<const float4_t *>(r + rec_z0(DV)) + (4 * js + w) * 64 + lane;
-    d.z0 = pz[0];
-    d.y0 = pz[(size_t)C * DV / 4];
+        reinterpret_cast<const float4_t *>(r + rec_z0(DV)) + (TT * js + m) * 64 + lane;
+    d.zy = pz[zw ? 0 : (size_t)C * DV / 4];
     d.eC = *reinterpret_cast<const float *>(r + rec_scalars(DV));
   };
-  auto load_ops = [&](unsigned c, Ops &d) {
-    load_wn(c, d);
+  auto load_ops = [&](unsigned c, Ops &d) __attribute__((always_inline)) {
+    load_a(c, d);
     load_kt(c, d);
     load_qz(c, d);
   };
@@ -885,10 +873,10 @@ __global__ __launch_bounds__(kScanThreads, 1) void delta_scan_kernel(
     const unsigned R = Hv / Hk;
     const size_t recPart = (recB + slices - 1) / slices;
     const size_t kShare = (size_t)R * slices;
-    const size_t kPart = ((size_t)kPieceBytes + kShare - 1) / kShare;
+    const size_t kPart = ((size_t)kKtBytes + kShare - 1) / kShare;
     const size_t kIdx = (size_t)(h % R) * slices + js;
     const size_t r0 = js * recPart, r1 = min(r0 + recPart, recB) - 4;
-    const size_t k0 = kIdx * kPart, k1 = min(k0 + kPart, (size_t)kPieceBytes) - 4;
+    const size_t k0 = kIdx * kPart, k1 = min(k0 + kPart, (size_t)kKtBytes) - 4;
     // (The empty asm reading a register set is its consumption: the
     // compiler waits for those loads there, in program order, and cannot
     // hoist an arithmetic use of them ahead of the barriers.) Chunk x's
@@ -938,9 +926,9 @@ __global__ __launch_bounds__(kScanThreads, 1) void delta_scan_kernel(
 
   // Chunk c multiplies `cur` and refills `dst` (the buffer of chunk c - 1)
   // with chunk c + kAhead.
-  auto step = [&](unsigned c, const Ops &cur, Ops &dst) {
+  auto step = [&](unsigned c, const Ops &cur, Ops &dst) __attribute__((always_inline)) {
     const unsigned cn = min(c + kAhead, last);
-    load_wn(cn, dst);
+    load_a(cn, dst);
     __builtin_amdgcn_sched_barrier(0);
     // 1. The split S, through LDS.
     {
@@ -950,48 +938,49 @@ __global__ __launch_bounds__(kScanThreads, 1) void delta_scan_kernel(
       sSx[1][w][lane] = lo;
     }
     lds_sync(); // X1
-    half8_t bh[4], bl[4];
+    half8_t bh[KB], bl[KB];
 #pragma unroll
-    for (int kb = 0; kb < 4; ++kb) {
+    for (int kb = 0; kb < KB; ++kb) {
       bh[kb] = sSx[0][kb][lane];
       bl[kb] = sSx[1][kb][lane];
     }
     __builtin_amdgcn_sched_barrier(0);
     load_kt(cn, dst);
     __builtin_amdgcn_sched_barrier(0);
-    // 2. Z_w and Y_w: five accumulators, each MFMA five issues after the
-    // one it depends on (a dependent 16x16x32 MFMA waits ~44 cycles, an
-    // independent one issues every ~18).
-    float4_t za = cur.z0, zx{0.0f, 0.0f, 0.0f, 0.0f}, zy{0.0f, 0.0f, 0.0f, 0.0f};
-    float4_t ya = cur.y0, yx{0.0f, 0.0f, 0.0f, 0.0f};
+    // 2. Z or Y of token tile m (each MFMA issued two or three after the
+    // one it depends on: a dependent 16x16x32 MFMA waits ~44 cycles, an
+    // independent one issues every ~18). 3. The split Z tile (halves
+    // 4 m .. 4 m + 3 of the k block), or the output tile to the stage.
+    if (zw) {
+      float4_t za = cur.zy, zx{0.0f, 0.0f, 0.0f, 0.0f}, zy{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-    for (int kb = 0; kb < 4; ++kb) {
-      za = mfma16(cur.wn[0][kb], bh[kb], za);
-      ya = mfma16(cur.qp[kb], bh[kb], ya);
-      zx = mfma16(cur.wn[0][kb], bl[kb], zx);
-      yx = mfma16(cur.qp[kb], bl[kb], yx);
-      zy = mfma16(cur.wn[1][kb], bh[kb], zy);
-    }
-    // 3. The split Z tile w (halves 4 (w % 2) .. of k block w / 2), and the
-    // output tile to the stage.
-    {
+      for (int kb = 0; kb < KB; ++kb) {
+        za = mfma16(cur.a[0][kb], bh[kb], za);
+        zx = mfma16(cur.a[0][kb], bl[kb], zx);
+        zy = mfma16(cur.a[1][kb], bh[kb], zy);
+      }
       half4_t hi, lo;
       split4(za + (zx + zy) * kSplitUnscale, hi, lo);
-      reinterpret_cast<half4_t *>(&sZx[0][w >> 1][lane])[w & 1u] = hi;
-      reinterpret_cast<half4_t *>(&sZx[1][w >> 1][lane])[w & 1u] = lo;
-      const float4_t y = ya + yx * kSplitUnscale;
-      half_t *const sy = &sY[c % kStageChunks][16 * w + 4 * g][L];
+      reinterpret_cast<half4_t *>(&sZx[0][lane])[m] = hi;
+      reinterpret_cast<half4_t *>(&sZx[1][lane])[m] = lo;
+    } else {
+      float4_t ya = cur.zy, yb{0.0f, 0.0f, 0.0f, 0.0f};
+      float4_t yx{0.0f, 0.0f, 0.0f, 0.0f}, yz{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int kb = 0; kb < KB; kb += 2) {
+        ya = mfma16(cur.a[0][kb], bh[kb], ya);
+        yb = mfma16(cur.a[0][kb + 1], bh[kb + 1], yb);
+        yx = mfma16(cur.a[0][kb], bl[kb], yx);
+        yz = mfma16(cur.a[0][kb + 1], bl[kb + 1], yz);
+      }
+      const float4_t y = (ya + yb) + (yx + yz) * kSplitUnscale;
+      half_t *const sy = &sY[c % kStageChunks][16 * m + 4 * g][L];
 #pragma unroll
       for (int r = 0; r < 4; ++r)
         sy[16 * r] = (half_t)y[r];
     }
     lds_sync(); // X2
-    half8_t zh[2], zl[2];
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-      zh[kb] = sZx[0][kb][lane];
-      zl[kb] = sZx[1][kb][lane];
-    }
+    const half8_t zh = sZx[0][lane], zl = sZx[1][lane];
     __builtin_amdgcn_sched_barrier(0);
     load_qz(cn, dst);
     __builtin_amdgcn_sched_barrier(0);
@@ -1003,13 +992,11 @@ __global__ __launch_bounds__(kScanThreads, 1) void delta_scan_kernel(
       sx[i] = sy[i] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
     }
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        sa[i] = mfma16(cur.kt[0][2 * i + kb], zh[kb], sa[i]);
-        sx[i] = mfma16(cur.kt[0][2 * i + kb], zl[kb], sx[i]);
-        sy[i] = mfma16(cur.kt[1][2 * i + kb], zh[kb], sy[i]);
-      }
+    for (int i = 0; i < 2; ++i) {
+      sa[i] = mfma16(cur.kt[0][i], zh, sa[i]);
+      sx[i] = mfma16(cur.kt[0][i], zl, sx[i]);
+      sy[i] = mfma16(cur.kt[1][i], zh, sy[i]);
+    }
 #pragma unroll
     for (int i = 0; i < 2; ++i)
       S[i] = sa[i] + (sx[i] + sy[i]) * kSplitUnscale;
@@ -1151,7 +1138,7 @@ bool delta_chunked_supported(const DeltaShape &s) {
 // arrival records (256-byte aligned).
 static size_t counters_offset(const DeltaShape &s) {
   const size_t chunks = (s.T + C - 1) / C;
-  return chunks * (s.Hv * rec_bytes(s.Dv) + s.Hk * (size_t)kPieceBytes);
+  return chunks * (s.Hv * rec_bytes(s.Dv) + s.Hk * (size_t)kKtBytes);
 }
 
 size_t delta_chunked_workspace_bytes(const DeltaShape &s) {
