@@ -984,22 +984,19 @@ __global__ __launch_bounds__(kScanThreads, 1) void delta_scan_kernel(
     __builtin_amdgcn_sched_barrier(0);
     load_qz(cn, dst);
     __builtin_amdgcn_sched_barrier(0);
-    // 4. S_w <- e^(g_C) S_w + K^T Z.
-    float4_t sa[2], sx[2], sy[2];
+    // 4. S_w <- e^(g_C) S_w + K^T Z (both cross terms in one accumulator).
+    float4_t sa[2], sx[2];
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
-      sa[i] = S[i] * cur.eC;
-      sx[i] = sy[i] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
-    }
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      sa[i] = mfma16(cur.kt[0][i], zh, sa[i]);
-      sx[i] = mfma16(cur.kt[0][i], zl, sx[i]);
-      sy[i] = mfma16(cur.kt[1][i], zh, sy[i]);
+      sa[i] = mfma16(cur.kt[0][i], zh, S[i] * cur.eC);
+      sx[i] = mfma16(cur.kt[0][i], zl, float4_t{0.0f, 0.0f, 0.0f, 0.0f});
     }
 #pragma unroll
     for (int i = 0; i < 2; ++i)
-      S[i] = sa[i] + (sx[i] + sy[i]) * kSplitUnscale;
+      sx[i] = mfma16(cur.kt[1][i], zh, sx[i]);
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+      S[i] = sa[i] + sx[i] * kSplitUnscale;
     // The stage's writes of this chunk were made before X2; its reads finish
     // before the next X1 (lds_sync waits for them), ahead of any rewrite.
     if (c % kStageChunks == kStageChunks - 1 || c == last)

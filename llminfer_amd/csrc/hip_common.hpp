@@ -114,9 +114,14 @@ __device__ __forceinline__ int mfma_c_row(int v, int h) { return 8 * (v / 4) + 4
 // by v_mfma_f32_*_f16 on gfx950, which does not flush fp16 inputs.
 constexpr float kSplitScale = 2048.0f;
 constexpr float kSplitUnscale = 1.0f / 2048.0f;
+// The remainder as one fused multiply-add on the scaled values, hi 2^11
+// subtracted from x 2^11: both are exact and so is their difference (hi is
+// x rounded to fp16), so this is (x - hi) 2^11 rounded once to fp16, the
+// same bits as the subtraction followed by the scaling, in fewer
+// instructions (the backend takes the fp16 hi as a mixed-precision operand).
 __device__ __forceinline__ void split_f16(float x, half_t &hi, half_t &lo) {
   hi = (half_t)x;
-  lo = (half_t)((x - (float)hi) * kSplitScale);
+  lo = (half_t)fmaf((float)hi, -kSplitScale, x * kSplitScale);
 }
 
 __device__ __forceinline__ half8_t load8(const half_t *p) {
