@@ -88,7 +88,6 @@ constexpr int DK = 128;     // key dimension handled by these kernels
 constexpr int KS = DK + 8;  // fp16 stride of [token][dk] rows in LDS (and of V rows)
 constexpr int CS = C + 8;   // fp16 stride of [*][token] rows in LDS
 constexpr int FS = C + 1;   // fp32 stride of the prep's A and T^T rows
-constexpr int VB = 128;     // dv columns of V the prep stages at a time
 constexpr int TT = C / 16;  // 16-token tiles of a chunk
 constexpr int KB = DK / 32; // 32-wide blocks of the key dimension
 constexpr int DT = DK / 16; // 16-wide tiles of the key dimension
@@ -110,26 +109,28 @@ constexpr int DT = DK / 16; // 16-wide tiles of the key dimension
 //  * K^T piece (per chunk and key head): block i holds rows d of tile i
 //    against permuted k = t (the chunk's one 32-token block); DT blocks of
 //    hi halves, then DT of lo halves.
+//  * T_b and M pieces (per chunk and value head), the operands of the
+//    scan's U0 = T_b V and Y0 = M U0: block TT hl + m holds rows t of tile m
+//    (hl 0: hi halves, 1: lo halves), against k = u in plain order for T_b
+//    (V is its B operand) and permuted for M (U0 in C layout is its B
+//    operand).
 constexpr int kBlk = 64 * 8;
 constexpr int kWnBlocks = TT * KB;
 constexpr int kWnBytes = 2 * kWnBlocks * kBlk * 2; // 16 KiB
 constexpr int kQpBytes = kWnBlocks * kBlk * 2;     // 8 KiB
 constexpr int kKtBlocks = DT;
 constexpr int kKtBytes = 2 * kKtBlocks * kBlk * 2; // 16 KiB
+constexpr int kTbBytes = 2 * TT * kBlk * 2;        // 4 KiB
+constexpr int kMBytes = 2 * TT * kBlk * 2;         // 4 KiB
 
-// Workspace. Per (chunk, value head) a record: the Wn piece, the Q' piece,
-// then Z0 and Y0 as fp32 in C-layout register order, per 16-column slice js
-// and 16-row tile m a 64-lane block of float4 (block TT js + m), then 64
-// floats of scalars (e^(g_C) first). After all records, per (chunk, key
-// head) the K^T piece.
+// Workspace. Per (chunk, value head) a record: the Wn, Q', T_b and M
+// pieces, then 64 floats of scalars: e^(g_C) at 0, e^(g_C - g_t) at 32 + t.
+// After all records, per (chunk, key head) the K^T piece.
 constexpr int kScalarBytes = 256;
-__host__ __device__ inline size_t rec_z0(unsigned) { return (size_t)kWnBytes + kQpBytes; }
-__host__ __device__ inline size_t rec_scalars(unsigned DV) {
-  return rec_z0(DV) + 2 * (size_t)C * DV * sizeof(float);
-}
-__host__ __device__ inline size_t rec_bytes(unsigned DV) {
-  return rec_scalars(DV) + kScalarBytes;
-}
+constexpr size_t kRecTb = (size_t)kWnBytes + kQpBytes;
+constexpr size_t kRecM = kRecTb + kTbBytes;
+constexpr size_t kRecScalars = kRecM + kMBytes;
+constexpr size_t kRecBytes = kRecScalars + kScalarBytes; // 32.25 KiB
 __device__ __forceinline__ char *rec_ptr(void *ws, size_t recB, size_t Hv, size_t c,
                                          size_t h) {
   return static_cast<char *>(ws) + (c * Hv + h) * recB;
@@ -215,8 +216,8 @@ __device__ __forceinline__ void load_split4(const float *p, int stride, half4_t 
 // element is the single product x * factor -- the bits l2NormF32 writes.
 template <bool QK16>
 __global__ __launch_bounds__(256, 2) void delta_prep_kernel(
-    const void *__restrict__ qp, const void *__restrict__ kp, const half_t *__restrict__ v,
-    const float *__restrict__ beta, const float *__restrict__ decay, void *__restrict__ ws,
+    const void *__restrict__ qp, const void *__restrict__ kp, const float *__restrict__ beta,
+    const float *__restrict__ decay, void *__restrict__ ws,
     unsigned T, unsigned Hk, unsigned Hv, unsigned DV, float eps, float qscale, unsigned *cnt) {
   const float *q = static_cast<const float *>(qp), *k = static_cast<const float *>(kp);
   const half_t *q16 = static_cast<const half_t *>(qp), *k16 = static_cast<const half_t *>(kp);
@@ -225,15 +226,15 @@ __global__ __launch_bounds__(256, 2) void delta_prep_kernel(
   const unsigned t0 = c * C, n = min((unsigned)C, T - t0);
   const unsigned tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
   const unsigned g = lane >> 4, L = lane & 15u;
-  const size_t recB = rec_bytes(DV);
-  const size_t qkStride = (size_t)Hk * DK, vStride = (size_t)Hv * DV;
+  const size_t recB = kRecBytes;
+  const size_t qkStride = (size_t)Hk * DK;
   // The fused norm's per-value-head arrival records (4 words each), zeroed
   // here (the scan runs after this launch on the same stream).
   if (cnt && c == 0 && tid < 4 * R)
     cnt[4 * kh * R + tid] = 0;
 
   __shared__ __attribute__((aligned(16))) half_t sKh[C * KS], sKl[C * KS];
-  __shared__ __attribute__((aligned(16))) half_t sQV[C * KS]; // Q hi, later a V block
+  __shared__ __attribute__((aligned(16))) half_t sQV[C * KS]; // Q hi
   __shared__ __attribute__((aligned(16))) float sATT[2 * C * FS]; // A, then T^T
   float *const sA = sATT, *const sTT = sATT + C * FS;
   // T_w^T, T_b^T, M and -N as hi/lo [*][token] rows; Q lo before them,
@@ -299,36 +300,15 @@ __global__ __launch_bounds__(256, 2) void delta_prep_kernel(
         sEg[pb][t] = expf((float)gg);
         sEz[pb][t] = expf((float)(gC - gg));
       }
+      float *const sc = reinterpret_cast<float *>(rec_ptr(ws, recB, Hv, c, kh * R + hr) +
+                                                   kRecScalars);
+      if (t < C)
+        sc[32 + t] = expf((float)(gC - gg));
       if (t == C - 1)
-        *reinterpret_cast<float *>(rec_ptr(ws, recB, Hv, c, kh * R + hr) + rec_scalars(DV)) =
-            expf((float)gg);
+        sc[0] = expf((float)gg);
     }
   };
   load_gates(kh * R);
-  // V rows of one head's dv block [jb, jb + w): thread tid holds items
-  // tid + 256 i (8 halves each), w <= VB.
-  constexpr int kVItems = C * VB / 8 / 256;
-  half8_t vreg[kVItems];
-  auto fetch_v = [&](unsigned h, unsigned jb, unsigned w) {
-#pragma unroll
-    for (int it = 0; it < kVItems; ++it) {
-      const unsigned i = tid + 256 * it, t = i / (w / 8), j8 = (i % (w / 8)) * 8;
-      const unsigned tc = min(t, n - 1); // rows past the end (or items past w) read row n-1
-      const half8_t x =
-          load8(v + (size_t)(t0 + tc) * vStride + (size_t)h * DV + jb + (i < C * w / 8 ? j8 : 0));
-      vreg[it] = t < n ? x : half8_t{0, 0, 0, 0, 0, 0, 0, 0};
-    }
-  };
-  auto store_v = [&](unsigned w) {
-#pragma unroll
-    for (int it = 0; it < kVItems; ++it) {
-      const unsigned i = tid + 256 * it, t = i / (w / 8), j8 = (i % (w / 8)) * 8;
-      if (i < C * w / 8)
-        *reinterpret_cast<half8_t *>(sQV + t * KS + j8) = vreg[it];
-    }
-  };
-  const unsigned w0 = min((unsigned)VB, DV);
-  fetch_v(kh * R, 0, w0);
 
   // QK16: the L2 factors of the chunk's k rows (threads 0 .. C-1) and q
   // rows (C .. 2C-1), each the sequential sum over one row.
@@ -454,14 +434,6 @@ __global__ __launch_bounds__(256, 2) void delta_prep_kernel(
     const double *const hG = sG[pb];
     const float *const hB = sB[pb], *const hEg = sEg[pb], *const hEz = sEz[pb];
     lds_sync(); // the previous head is done with every LDS buffer
-
-    // V of the head's first dv block; the next head's first V block in
-    // flight during this head (with DV > VB the V registers carry this
-    // head's further blocks, and the next head's first block is fetched
-    // after them).
-    store_v(w0);
-    if (hr + 1 < R && DV <= VB)
-      fetch_v(h + 1, 0, w0);
 
     // A (fp32) and M (hi/lo) from the Gram registers:
     // A[t][s] = beta_t e^(g_t - g_s) k_t.k_s (s < t), M[t][s] = e^(g_t - g_s)
@@ -659,69 +631,23 @@ __global__ __launch_bounds__(256, 2) void delta_prep_kernel(
       }
     }
 
-    // U0 = T_b V per 16-column slice (wave w: slices w + 4 rep of each V
-    // block), then Z0 = e^(g_C - g) U0 and Y0 = M U0 with U0 as the B
-    // operand straight from its C-layout registers. The T_b and M operands
-    // are read once per wave.
+    // The T_b and M pieces: wave w writes T_b tile w (w < 2) or M tile w - 2,
+    // hi and lo.
     {
-      half8_t tbh[TT], tbl[TT], mah[TT], mal[TT];
-#pragma unroll
-      for (int mt = 0; mt < TT; ++mt) {
-        tbh[mt] = read_kcol(sTbh, CS, 0, 16 * mt, g, L);
-        tbl[mt] = read_kcol(sTbl, CS, 0, 16 * mt, g, L);
+      const unsigned mt = wave & 1u;
+      half8_t hi, lo;
+      if (wave < 2) {
+        hi = read_kcol(sTbh, CS, 0, 16 * mt, g, L);
+        lo = read_kcol(sTbl, CS, 0, 16 * mt, g, L);
+      } else {
         const unsigned o = (16 * mt + L) * CS + 4 * g;
-        mah[mt] = cat8(load4(sMh + o), load4(sMh + o + 16));
-        mal[mt] = cat8(load4(sMl + o), load4(sMl + o + 16));
+        hi = cat8(load4(sMh + o), load4(sMh + o + 16));
+        lo = cat8(load4(sMl + o), load4(sMl + o + 16));
       }
-      float ezr[TT][4];
-#pragma unroll
-      for (int mt = 0; mt < TT; ++mt)
-#pragma unroll
-        for (int r = 0; r < 4; ++r)
-          ezr[mt][r] = hEz[16 * mt + 4 * g + r];
-      float4_t *const z0 = reinterpret_cast<float4_t *>(rec + rec_z0(DV));
-      float4_t *const y0 = z0 + (size_t)C * DV / 4;
-      for (unsigned jb = 0; jb < DV; jb += VB) {
-        const unsigned w = min((unsigned)VB, DV - jb);
-        if (jb > 0) {
-          // Further dv blocks (DV > VB) are fetched here, in turn.
-          fetch_v(h, jb, w);
-          lds_sync();
-          store_v(w);
-          lds_sync();
-        }
-#pragma unroll 1
-        for (unsigned jt = wave; jt < w / 16; jt += 4) {
-          const unsigned js = jb / 16 + jt;
-          const half8_t bv = read_kcol(sQV, KS, 0, 16 * jt, g, L);
-          float4_t u[TT];
-#pragma unroll
-          for (int mt = 0; mt < TT; ++mt) {
-            float4_t ua{0.0f, 0.0f, 0.0f, 0.0f}, ux{0.0f, 0.0f, 0.0f, 0.0f};
-            ua = mfma16(tbh[mt], bv, ua);
-            ux = mfma16(tbl[mt], bv, ux);
-            u[mt] = ua + ux * kSplitUnscale;
-            float4_t zz;
-#pragma unroll
-            for (int r = 0; r < 4; ++r)
-              zz[r] = ezr[mt][r] * u[mt][r];
-            z0[(js * TT + mt) * 64 + lane] = zz;
-          }
-          half8_t ubh, ubl;
-          split8(u[0], u[1], ubh, ubl);
-#pragma unroll
-          for (int mt = 0; mt < TT; ++mt) {
-            float4_t ya{0.0f, 0.0f, 0.0f, 0.0f}, yx{0.0f, 0.0f, 0.0f, 0.0f};
-            ya = mfma16(mah[mt], ubh, ya);
-            yx = mfma16(mah[mt], ubl, yx);
-            yx = mfma16(mal[mt], ubh, yx);
-            y0[(js * TT + mt) * 64 + lane] = ya + yx * kSplitUnscale;
-          }
-        }
-      }
+      half8_t *const pc = reinterpret_cast<half8_t *>(rec + (wave < 2 ? kRecTb : kRecM));
+      pc[mt * 64 + lane] = hi;
+      pc[(TT + mt) * 64 + lane] = lo;
     }
-    if (hr + 1 < R && DV > VB)
-      fetch_v(h + 1, 0, w0);
   }
 }
 
@@ -776,8 +702,9 @@ constexpr unsigned kNormMaxDv = 256; // dv the fused norm supports
 template <bool NORM>
 __global__ __launch_bounds__(kScanThreads, 1) void delta_scan_kernel(
     float *__restrict__ state, half_t *__restrict__ out, const void *__restrict__ ws,
-    unsigned T, unsigned Hk, unsigned Hv, unsigned DV, const half_t *__restrict__ gate,
-    const float *__restrict__ nweight, unsigned *cnt, float neps, unsigned spin) {
+    const half_t *__restrict__ v, unsigned T, unsigned Hk, unsigned Hv, unsigned DV,
+    const half_t *__restrict__ gate, const float *__restrict__ nweight, unsigned *cnt,
+    float neps, unsigned spin) {
   // Workgroups are dealt to the 8 XCDs round-robin by block index. Give
   // each XCD a contiguous run of (value head, slice) pairs, so that the
   // workgroups reading one value head's pieces and one key head's K^T piece
@@ -788,21 +715,26 @@ __global__ __launch_bounds__(kScanThreads, 1) void delta_scan_kernel(
   const unsigned w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const unsigned lane = threadIdx.x & 63u, g = lane >> 4, L = lane & 15u;
   const unsigned chunks = (T + C - 1) / C, last = chunks - 1;
-  const size_t recB = rec_bytes(DV), vStride = (size_t)Hv * DV;
+  const size_t recB = kRecBytes, vStride = (size_t)Hv * DV;
   void *const wsp = const_cast<void *>(ws);
-  // Waves 0-1 compute Z tiles, waves 2-3 Y tiles; m is the token tile.
-  const bool zw = w < 2;
-  const unsigned m = w & 1u;
+  // Waves 1 and 2 compute the Z tiles 0 and 1, waves 0 and 3 the Y tiles
+  // 0 and 1 (m is the token tile): wave 0 shares its SIMD with the fifth
+  // wave, and a Y wave is off the chain.
+  const bool zw = w == 1 || w == 2;
+  const unsigned m = w >> 1;
 
   __shared__ half8_t sSx[2][KB][64]; // split S: [hi, lo][k block][lane]
   __shared__ half8_t sZx[2][64];     // split Z: [hi, lo][lane], tiles 0 | 1
+  // Z0 and Y0 of the slice, from the fifth wave: [chunk parity][Z0 tile 0,
+  // Z0 tile 1, Y0 tile 0, Y0 tile 1][lane], C layout.
+  __shared__ float4_t sZY[2][2 * TT][64];
+  __shared__ __attribute__((aligned(16))) half_t sVt[C * 24]; // its V rows, 24-half stride
   __shared__ __attribute__((aligned(16))) half_t sY[kStageChunks][C][16];
 
   // The operand blocks of wave w for one chunk.
   struct Ops {
     half8_t a[2][KB]; // Z waves: Wn blocks (m, kb) [hi, lo][kb]; Y waves: Q' blocks in a[0]
     half8_t kt[2][2]; // K^T blocks (tile 2w + i): [hi, lo][i]
-    float4_t zy;      // tile m of the slice's Z0 (Z waves) or Y0 (Y waves)
     float eC;         // e^(g_C)
   };
   // The loads of one chunk's operands in three parts, which a step spreads
@@ -838,11 +770,7 @@ __global__ __launch_bounds__(kScanThreads, 1) void delta_scan_kernel(
     }
   };
   auto load_qz = [&](unsigned c, Ops &d) __attribute__((always_inline)) {
-    const char *r = rec_ptr(wsp, recB, Hv, c, h);
-    const float4_t *pz =
-        reinterpret_cast<const float4_t *>(r + rec_z0(DV)) + (TT * js + m) * 64 + lane;
-    d.zy = pz[zw ? 0 : (size_t)C * DV / 4];
-    d.eC = *reinterpret_cast<const float *>(r + rec_scalars(DV));
+    d.eC = *reinterpret_cast<const float *>(rec_ptr(wsp, recB, Hv, c, h) + kRecScalars);
   };
   auto load_ops = [&](unsigned c, Ops &d) __attribute__((always_inline)) {
     load_a(c, d);
@@ -864,12 +792,77 @@ __global__ __launch_bounds__(kScanThreads, 1) void delta_scan_kernel(
   };
 
   if (w == 4) {
-    // The warming wave: this workgroup's share of a chunk is recPart bytes
-    // of each record (Wn, Q', Z0, Y0, scalars) and kPart bytes of the K^T
-    // piece; it reads one dword per line of the first 16 KiB of the former
-    // and 8 KiB of the latter (all of both at dv = 128). A touched value is
-    // consumed kWarmSets chunks later (the loop is unrolled over the register
-    // sets), long after it came, so the wave never waits on its loads.
+    // The fifth wave. (1) Z0 and Y0 of the slice, one chunk ahead of the
+    // compute waves, into sZY: U0 = T_b V (V, 32 rows x 16 columns, staged
+    // in LDS and read transposed as the B operand), Z0 = e^(g_C - g) U0, Y0
+    // = M U0 with U0 as the B operand from its C-layout registers, in split
+    // form as the other products. Chunk x's Z0/Y0 are written during step
+    // x - 1, after that step's first barrier (the compute waves read parity
+    // x % 2 of chunk x - 2 before that step's second barrier) and before
+    // its own next barrier. (2) Warming: this workgroup's share of a chunk is
+    // recPart bytes of each record and kPart bytes of the K^T piece; it
+    // reads one dword per line of the first 16 KiB of the former and 8 KiB
+    // of the latter (all of both at dv = 128). A touched value is consumed
+    // kWarmSets chunks later (the loop is unrolled over the register sets),
+    // long after it came, so the wave never waits on its loads.
+    struct ZYOps {
+      half8_t tb[2][TT], mm[2][TT]; // T_b and M blocks: [hi, lo][tile]
+      uint4_t vr;                   // 8 halves of row lane / 2 of the slice's V
+      float4_t ez[TT];              // e^(g_C - g_t) of the lane's C-layout rows
+    };
+    auto load_zy = [&](unsigned x, ZYOps &d) __attribute__((always_inline)) {
+      const char *r = rec_ptr(wsp, recB, Hv, x, h);
+      const half8_t *pt = reinterpret_cast<const half8_t *>(r + kRecTb) + lane;
+      const half8_t *pm = reinterpret_cast<const half8_t *>(r + kRecM) + lane;
+#pragma unroll
+      for (int hl = 0; hl < 2; ++hl)
+#pragma unroll
+        for (int mt = 0; mt < TT; ++mt) {
+          d.tb[hl][mt] = pt[(TT * hl + mt) * 64];
+          d.mm[hl][mt] = pm[(TT * hl + mt) * 64];
+        }
+      const unsigned t = x * C + (lane >> 1);
+      d.vr = t < T ? *reinterpret_cast<const uint4_t *>(v + (size_t)t * vStride + (size_t)h * DV +
+                                                         16 * js + 8 * (lane & 1u))
+                   : uint4_t{0, 0, 0, 0};
+      const float4_t *pe = reinterpret_cast<const float4_t *>(r + kRecScalars) + 8 + g;
+#pragma unroll
+      for (int mt = 0; mt < TT; ++mt)
+        d.ez[mt] = pe[4 * mt];
+    };
+    // In two parts, one per barrier interval of the step before chunk x:
+    // U0 and Z0, then Y0 (U0 kept in registers between them).
+    float4_t u[TT];
+    auto compute_z0 = [&](unsigned x, const ZYOps &d) __attribute__((always_inline)) {
+      *reinterpret_cast<uint4_t *>(sVt + (lane >> 1) * 24 + 8 * (lane & 1u)) = d.vr;
+      const half8_t vb = read_kcol(sVt, 24, 0, 0, g, L); // V[8g + e][L]
+#pragma unroll
+      for (int mt = 0; mt < TT; ++mt) {
+        float4_t ua{0.0f, 0.0f, 0.0f, 0.0f}, ux{0.0f, 0.0f, 0.0f, 0.0f};
+        ua = mfma16(d.tb[0][mt], vb, ua);
+        ux = mfma16(d.tb[1][mt], vb, ux);
+        u[mt] = ua + ux * kSplitUnscale;
+        sZY[x & 1u][mt][lane] = u[mt] * d.ez[mt];
+      }
+    };
+    auto compute_y0 = [&](unsigned x, const ZYOps &d) __attribute__((always_inline)) {
+      half8_t ubh, ubl;
+      split8(u[0], u[1], ubh, ubl);
+#pragma unroll
+      for (int mt = 0; mt < TT; ++mt) {
+        float4_t ya{0.0f, 0.0f, 0.0f, 0.0f}, yx{0.0f, 0.0f, 0.0f, 0.0f};
+        ya = mfma16(d.mm[0][mt], ubh, ya);
+        yx = mfma16(d.mm[0][mt], ubl, yx);
+        yx = mfma16(d.mm[1][mt], ubh, yx);
+        sZY[x & 1u][TT + mt][lane] = ya + yx * kSplitUnscale;
+      }
+    };
+    ZYOps z0s, z1s; // chunk x's operands in set x % 2
+    load_zy(0, z0s);
+    load_zy(min(1u, last), z1s);
+    compute_z0(0, z0s);
+    compute_y0(0, z0s);
+    load_zy(min(2u, last), z0s);
     const unsigned R = Hv / Hk;
     const size_t recPart = (recB + slices - 1) / slices;
     const size_t kShare = (size_t)R * slices;
@@ -896,16 +889,47 @@ __global__ __launch_bounds__(kScanThreads, 1) void delta_scan_kernel(
 #pragma unroll
     for (int u = 1; u < kWarmAhead; ++u)
       touch(min((unsigned)u, last), tv[u % kWarmSets]);
+    // Step x, between its two barriers: chunk x + 1's U0 and Z0 from set
+    // (x + 1) % 2; after the second: its Y0, and the set then takes chunk
+    // x + 3.
+    auto next_z0 = [&](unsigned x, ZYOps &d) __attribute__((always_inline)) {
+      if (x + 1 < chunks)
+        compute_z0(x + 1, d);
+    };
+    auto next_y0 = [&](unsigned x, ZYOps &d) __attribute__((always_inline)) {
+      if (x + 1 < chunks) {
+        compute_y0(x + 1, d);
+        load_zy(min(x + 3, last), d);
+      }
+    };
+    static_assert(kWarmSets % 2 == 0, "the Z0/Y0 sets alternate inside the unrolled loop");
     unsigned c = 0;
     for (; c + kWarmSets <= chunks; c += kWarmSets) {
 #pragma unroll
-      for (int u = 0; u < kWarmSets; ++u) {
+      for (int u = 0; u < kWarmSets; u += 2) {
         touch(min(c + u + kWarmAhead, last), tv[(u + kWarmAhead) % kWarmSets]);
         lds_sync(); // X1
+        next_z0(c + u, z1s);
         lds_sync(); // X2
+        next_y0(c + u, z1s);
+        touch(min(c + u + 1 + kWarmAhead, last), tv[(u + 1 + kWarmAhead) % kWarmSets]);
+        lds_sync(); // X1
+        next_z0(c + u + 1, z0s);
+        lds_sync(); // X2
+        next_y0(c + u + 1, z0s);
       }
     }
-    for (; c < chunks; ++c) {
+    for (; c + 2 <= chunks; c += 2) {
+      lds_sync(); // X1
+      next_z0(c, z1s);
+      lds_sync(); // X2
+      next_y0(c, z1s);
+      lds_sync(); // X1
+      next_z0(c + 1, z0s);
+      lds_sync(); // X2
+      next_y0(c + 1, z0s);
+    }
+    if (c < chunks) {
       lds_sync(); // X1
       lds_sync(); // X2
     }
@@ -952,7 +976,8 @@ __global__ __launch_bounds__(kScanThreads, 1) void delta_scan_kernel(
     // independent one issues every ~18). 3. The split Z tile (halves
     // 4 m .. 4 m + 3 of the k block), or the output tile to the stage.
     if (zw) {
-      float4_t za = cur.zy, zx{0.0f, 0.0f, 0.0f, 0.0f}, zy{0.0f, 0.0f, 0.0f, 0.0f};
+      float4_t za = sZY[c & 1u][m][lane], zx{0.0f, 0.0f, 0.0f, 0.0f};
+      float4_t zy{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
       for (int kb = 0; kb < KB; ++kb) {
         za = mfma16(cur.a[0][kb], bh[kb], za);
@@ -964,7 +989,7 @@ __global__ __launch_bounds__(kScanThreads, 1) void delta_scan_kernel(
       reinterpret_cast<half4_t *>(&sZx[0][lane])[m] = hi;
       reinterpret_cast<half4_t *>(&sZx[1][lane])[m] = lo;
     } else {
-      float4_t ya = cur.zy, yb{0.0f, 0.0f, 0.0f, 0.0f};
+      float4_t ya = sZY[c & 1u][TT + m][lane], yb{0.0f, 0.0f, 0.0f, 0.0f};
       float4_t yx{0.0f, 0.0f, 0.0f, 0.0f}, yz{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
       for (int kb = 0; kb < KB; kb += 2) {
@@ -1135,7 +1160,7 @@ bool delta_chunked_supported(const DeltaShape &s) {
 // arrival records (256-byte aligned).
 static size_t counters_offset(const DeltaShape &s) {
   const size_t chunks = (s.T + C - 1) / C;
-  return chunks * (s.Hv * rec_bytes(s.Dv) + s.Hk * (size_t)kKtBytes);
+  return chunks * (s.Hv * kRecBytes + s.Hk * (size_t)kKtBytes);
 }
 
 size_t delta_chunked_workspace_bytes(const DeltaShape &s) {
@@ -1155,15 +1180,15 @@ hipError_t launch_chunked(const void *q, const void *k, const uint16_t *v, const
                                                       counters_offset(s))
                        : nullptr;
   hipLaunchKernelGGL((delta_prep_kernel<QK16>), dim3(chunks, s.Hk), dim3(256), 0, stream, q, k,
-                     reinterpret_cast<const half_t *>(v), beta, decay, ws, s.T, s.Hk, s.Hv,
-                     s.Dv, eps, qscale, cnt);
+                     beta, decay, ws, s.T, s.Hk, s.Hv, s.Dv, eps, qscale, cnt);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess)
     return e;
   const dim3 grid(s.Hv * (s.Dv / 16));
   if (!gate) {
     hipLaunchKernelGGL(delta_scan_kernel<false>, grid, dim3(kScanThreads), 0, stream, state,
-                       reinterpret_cast<half_t *>(out), ws, s.T, s.Hk, s.Hv, s.Dv,
+                       reinterpret_cast<half_t *>(out), ws, reinterpret_cast<const half_t *>(v),
+                       s.T, s.Hk, s.Hv, s.Dv,
                        (const half_t *)nullptr, (const float *)nullptr, (unsigned *)nullptr,
                        0.0f, 0u);
     return hipGetLastError();
@@ -1173,7 +1198,8 @@ hipError_t launch_chunked(const void *q, const void *k, const uint16_t *v, const
   // grid fits on the device together (a cooperative launch would guarantee
   // it too, but costs ~17 us more per call here, measured).
   hipLaunchKernelGGL(delta_scan_kernel<true>, grid, dim3(kScanThreads), 0, stream, state,
-                     reinterpret_cast<half_t *>(out), ws, s.T, s.Hk, s.Hv, s.Dv,
+                     reinterpret_cast<half_t *>(out), ws, reinterpret_cast<const half_t *>(v),
+                     s.T, s.Hk, s.Hv, s.Dv,
                      reinterpret_cast<const half_t *>(gate), nweight, cnt, neps, g_wait_limit);
   return hipGetLastError();
 }
