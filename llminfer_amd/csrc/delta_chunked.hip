@@ -32,15 +32,17 @@
 //    CU (56 KB of LDS each): every chunk at once. The Gram matrices K K^T
 //    and Q K^T on fp16 MFMA (kept in registers); per value head the decay
 //    weighting, T by blocked substitution (the two 16x16 diagonal blocks in
-//    fp32, the off-diagonal block on MFMA), and the products Wn, Q', Z0, Y0
-//    on fp16 MFMA in split form. The results go to the workspace already in
-//    the register order of the scan's MFMA operands.
+//    fp32, the off-diagonal block on MFMA), and the products Wn and Q' on
+//    fp16 MFMA in split form. The results (with T_b and M) go to the
+//    workspace already in the register order of the scan's MFMA operands.
 //
 //  * deltaChunkScan, grid (value head, 16-column dv slice), 4 compute waves
-//    and an L2-warming wave. Wave w keeps rows [32 w, 32 w + 32) of the
-//    state slice S [dk x 16] in registers; waves 0 and 1 compute the two
-//    16-token tiles of each chunk's Z, waves 2 and 3 those of Y; S and Z
-//    pass between the waves through LDS, two barriers per chunk. Every
+//    and a fifth wave. Wave w keeps rows [32 w, 32 w + 32) of the state
+//    slice S [dk x 16] in registers; waves 1 and 2 compute the two 16-token
+//    tiles of each chunk's Z, waves 0 and 3 those of Y; S and Z pass
+//    between the waves through LDS, two barriers per chunk. The fifth wave
+//    forms the slice's Z0 and Y0 from T_b, M and V a chunk ahead and keeps
+//    the other operands' lines in L2. Every
 //    product runs on v_mfma_f32_16x16x32_f16, with the state (and Z) as the
 //    B operand straight from the C-layout registers of the product that made
 //    it: the k index of an operand block is permuted (sigma below) so that
@@ -53,7 +55,7 @@
 // phases (the triangular solve, the products that follow it), which shrink
 // with the chunk, and at 32 two workgroups share a CU and hide each other's
 // latencies; the scan's chain per chunk (two barriers, two short MFMA runs)
-// costs about as much at 32 as at 64 tokens' worth of work halved.
+// costs about as much at 32 as at 64 tokens.
 //
 // Split form: x = hi + lo 2^-11 with hi = fp16(x), lo = fp16((x - hi) 2^11),
 // a.b ~ ah.bh + (ah.bl + al.bh) 2^-11, the cross terms in a second fp32
@@ -659,18 +661,19 @@ __global__ __launch_bounds__(256, 2) void delta_prep_kernel(
 // Per chunk:
 //   1. every wave splits its state rows into the hi/lo B operand of k block
 //      w and puts it in LDS; barrier X1; every wave reads the whole split S;
-//   2. waves 0 and 1: Z_m = Z0_m + sum_kb Wn[m][kb] S[kb] for token tile
-//      m = w; waves 2 and 3: Y_m = Y0_m + sum_kb Q'[m][kb] S[kb], m = w - 2;
+//   2. waves 1 and 2: Z_m = Z0_m + sum_kb Wn[m][kb] S[kb] for token tile
+//      m = w / 2; waves 0 and 3: Y_m = Y0_m + sum_kb Q'[m][kb] S[kb];
 //   3. Z_m, split, to LDS; barrier X2; every wave reads the split Z;
 //   4. S_w <- e^(g_C) S_w + K^T[w] Z (the two C tiles of w).
-// Each wave loads exactly the operand blocks it multiplies (44 KB per
-// workgroup and chunk in all), one chunk ahead, straight into its
-// registers. A fifth wave keeps those loads L2 hits: the pieces come from
-// HBM / the MALL (the prep wrote them), so it reads one dword per 128-byte
-// line of its workgroup's share of the record and K^T piece of chunk
-// c + kWarmAhead (the slice workgroups of a value head share an XCD, and
-// split the head's lines between them). Its loads count on its own vmcnt,
-// so the compute waves' waits never cover them. No wave issues a global
+// Z0 and Y0 come from LDS, where the fifth wave put them during the step
+// before. Each compute wave loads exactly the operand blocks it multiplies
+// (40 KB per workgroup and chunk in all), one chunk ahead, straight into
+// its registers. The fifth wave also keeps those loads L2 hits: the pieces
+// come from HBM / the MALL (the prep wrote them), so it reads one dword
+// per 128-byte line of its workgroup's share of the record and K^T piece
+// of chunk c + kWarmAhead (the slice workgroups of a value head share an
+// XCD, and split the head's lines between them). Its loads count on its
+// own vmcnt, so the compute waves' waits never cover them. No wave issues a global
 // store inside the chunk loop -- the Y tiles go to an LDS stage that is
 // written out every kStageChunks chunks and at the end -- so a wave's only
 // outstanding vector-memory operations are those loads, which complete in
