@@ -26,6 +26,7 @@ SHAPES = [
     # chunked (T >= 32, dk 128)
     (1024, 16, 128, 32, 128), (100, 16, 128, 32, 128), (64, 2, 128, 4, 64),
     (33, 2, 128, 4, 128), (150, 2, 128, 8, 48), (300, 1, 128, 2, 32),
+    (2100, 1, 128, 2, 32),  # past the scan's 64-chunk output stage
     # recurrent, one workgroup per value head (T <= 32)
     (1, 16, 128, 32, 128), (5, 16, 128, 32, 128), (31, 2, 128, 4, 128),
     (1, 4, 64, 8, 64), (17, 2, 64, 4, 128), (32, 2, 64, 2, 64),

@@ -102,6 +102,15 @@ def test_prefill_cfg4(gpu):
     _check(x, *_run(x, gpu))
 
 
+def test_prefill_long_stage_write_outs(gpu):
+    """2100 tokens = 66 chunks of 32: the scan writes its staged output rows
+    out after chunk 63 and again at the end (every other test ends within
+    its first 64 chunks)."""
+    print("delta prefill T=2100", flush=True)
+    x = oracle.make_delta_inputs(21, 2100, 1, 128, 2, 32, 0.1)
+    _check(x, *_run(x, gpu))
+
+
 @pytest.mark.parametrize("shape", [(5, 2, 7, 4, 5), (3, 1, 4, 2, 4), (9, 2, 64, 4, 16),
                                    (33, 4, 128, 4, 32), (150, 2, 128, 8, 48),
                                    (100, 1, 128, 2, 256), (70, 2, 128, 4, 144)])
