@@ -266,8 +266,10 @@ private:
   std::vector<int64_t> normQuantize_, normAdd_; // by RmsNorm op: the fused ops
   std::vector<char> skip_;       // launched by a fused launch at another op
   std::vector<std::pair<int64_t, int64_t>> l2Delta_; // by DeltaUpdate op: its q / k L2Norms
+  std::vector<int64_t> convSilu_; // by CausalConv1d op: the SiLU launched with it
   void prepare_l2_delta();
   void prepare_kv_decode();
+  void prepare_conv_silu();
 };
 
 int Lowering::validate() {
@@ -543,6 +545,29 @@ void Lowering::prepare_l2_delta() {
     skip_[qo] = skip_[ko] = 1;
     for (uint32_t x : {qn.inputs[0], kn.inputs[0]})
       lastUse_[root_[x]] = std::max(lastUse_[root_[x]], u);
+  }
+}
+
+// CausalConv1d -> SiLU (the convolution's only consumer, the next op): the
+// convolution kernel applies SiLU to each fp16-rounded output
+// (causalConv with applySilu, Reference.metal:137-161), the same bits as
+// siluF16 over the stored output, so one launch writes the SiLU's output
+// and is recorded under both ops. The convolution's own output is never
+// stored.
+void Lowering::prepare_conv_silu() {
+  convSilu_.assign(g_.op_count, -1);
+  for (size_t j = 0; j + 1 < g_.op_count; ++j) {
+    const auto &c = op(j), &s = op(j + 1);
+    if (c.kind != LLMI_GRAPH_CAUSAL_CONV1D || s.kind != LLMI_GRAPH_SILU || skip_[j] ||
+        skip_[j + 1] || fusion_[j + 1].kind != LLMI_LINEAR_NONE)
+      continue;
+    const uint32_t y = c.outputs[0], z = s.outputs[0];
+    if (s.inputs[0] != y || uses_[y] != 1 || value(y).kind != LLMI_GRAPH_RESULT ||
+        value(z).kind != LLMI_GRAPH_RESULT || value(y).element != LLMI_GRAPH_F16 ||
+        value(z).element != LLMI_GRAPH_F16 || count(y) != count(z))
+      continue;
+    convSilu_[j] = (int64_t)j + 1;
+    skip_[j + 1] = 1;
   }
 }
 
@@ -963,12 +988,17 @@ int Lowering::lower(size_t i) {
     return LLMI_HIP_OK;
   }
   case LLMI_GRAPH_CAUSAL_CONV1D: {
-    if (int rc = dense_all({{in[0], 0}, {in[1], 1}, {out[0], 2}}))
+    const int64_t silu = convSilu_[i];
+    if (int rc = dense_all({{in[0], 0}, {in[1], 1},
+                            {silu >= 0 ? op((size_t)silu).outputs[0] : out[0], 2}}))
       return rc;
     Dispatch &d = emit(Launch::CausalConv, nullptr);
-    d.p.conv = {(unsigned)g_.tokens, (unsigned)dim(in[0], 1), (unsigned)dim(in[1], 2), 0};
+    d.p.conv = {(unsigned)g_.tokens, (unsigned)dim(in[0], 1), (unsigned)dim(in[1], 2),
+                silu >= 0 ? 1u : 0u};
     d.kernels.push_back(llmi_hip_kernel_name(LLMI_HIP_OP_CAUSAL_CONV, &d.p.conv, 0));
     d.buf[0] = r[0], d.buf[1] = r[1], d.buf[2] = state(o.state), d.buf[3] = r[2];
+    if (silu >= 0)
+      d.recs = {{i, nullptr, 0}, {(size_t)silu, nullptr, 0}};
     return LLMI_HIP_OK;
   }
   case LLMI_GRAPH_DELTA_GATES: {
@@ -1089,6 +1119,7 @@ int Lowering::run() {
   prepare_norm_quantize();
   prepare_l2_delta();
   prepare_kv_decode();
+  prepare_conv_silu();
   if (g_.output_count) {
     const uint32_t id = g_.outputs[0];
     const auto &v = value(id);
@@ -1132,6 +1163,8 @@ int Lowering::run() {
     const auto &o = op(index_);
     if (normQuantize_[index_] >= 0)
       allocate(op(normQuantize_[index_]), false); // the norm itself stores nothing
+    else if (convSilu_[index_] >= 0)
+      allocate(op(convSilu_[index_]), false); // nor does a convolution with its SiLU
     else
       allocate(o, f.kind == LLMI_LINEAR_SILU_F32);
     if (skip_[index_])

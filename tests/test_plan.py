@@ -6,9 +6,10 @@
   order, every non-view op covered by a launch or a fused epilogue, a
   copyHalfView for the interleaved query / gate halves, the epilogue
   multiset {sigmoid x2, silu, softplus_decay, swiglu x2}, no unfused
-  swiGlu / deltaGates / sigmoidMul, an unfused siluF16 after the
-  convolution, the head on linearW8A8Gemm / Gemv by row count, and fewer
-  launches without logits.
+  swiGlu / deltaGates / sigmoidMul, and the head on linearW8A8Gemm / Gemv by row count, and fewer
+  launches without logits. Where the reference keeps an unfused siluF16
+  after the convolution, the SiLU here runs in the convolution's launch
+  (causalConv with applySilu: the same bits) and is recorded under it.
 * The oracle runner (oracle/graph_runner.py) executes the same graphs op by
   op on the CPU oracle; its logits are pinned against HF transformers'
   Qwen3.5 decoder layers with the reference test's W8A8 projection
@@ -65,12 +66,18 @@ def test_lowering_matches_the_reference_predicates(w8):
                                     if op.kind not in (G.OpKind.RESHAPE, G.OpKind.SLICE)}
     assert any(d["kernel"] == "copyHalfView" for d in lowered)
     assert lowered[-1]["kernel"] == ("linearW8A8Gemm" if w8 else "linearF16")
-    for _, p in [(g, full), *steps]:
+    for gs, p in [(g, full), *steps]:
         ds = p.dispatches
         assert sorted(d["epilogue"] for d in ds if "epilogue" in d) == [
             "sigmoid", "sigmoid", "silu", "softplus_decay", "swiglu", "swiglu"]
         assert not {"swiGlu", "deltaGates", "sigmoidMul"} & {d["kernel"] for d in ds}
-        assert any(d["kernel"] == "siluF16" for d in ds)
+        assert "siluF16" not in {d["kernel"] for d in ds}
+        conv = [i for i, op in enumerate(gs.ops) if op.kind == G.OpKind.CAUSAL_CONV1D]
+        assert conv and all(gs.ops[i + 1].kind == G.OpKind.SILU for i in conv)
+        by_op = {}
+        for d in ds:
+            by_op.setdefault(d["op_index"], []).append(d["kernel"])
+        assert all(by_op[i] == by_op[i + 1] == ["causalConv"] for i in conv)
         assert p.scratch_bytes > 0 and p.scratch_bytes % 256 == 0
     if w8:
         assert [p.dispatches[-1]["kernel"] for _, p in steps] == [
@@ -113,9 +120,12 @@ def test_qwen35_4b_lowers_with_the_hot_kernels():
     assert kinds["gqaDecodeSplitK"] == kinds["gqaDecodeMerge"] == 8 * 2
     assert kinds["kvAppend"] == 0 and kinds["deltaRecurrent"] == 24 * 3
     assert kinds["l2NormF32"] == 0
-    # a launch that serves several ops (the Adds, norms, quantizations and
-    # projections above) has a record for each: 740 records, 339 launches
-    assert len(decode.dispatches) == 740 and decode.launches == 339
+    # each DeltaNet layer's convolution with its SiLU
+    assert kinds["causalConv"] == 24 * 2 and kinds["siluF16"] == 0
+    # a launch that serves several ops (the Adds, norms, quantizations,
+    # projections and SiLUs above) has a record for each: 740 records,
+    # 315 launches
+    assert len(decode.dispatches) == 740 and decode.launches == 315
     assert kinds["residualAdd"] == 0
     assert "quantizeActivation" in kinds     # the others (after GQA / gated norms, SwiGLU)
     indices = [d["op_index"] for d in decode.dispatches]
