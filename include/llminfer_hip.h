@@ -353,6 +353,22 @@ LLMI_HIP_API int llmi_hip_gated_attention(const uint16_t *q_proj, const uint16_t
                                           void *workspace, size_t workspace_bytes,
                                           void *stream);
 
+/* The same block when the q projection has already activated its gate
+ * half: the execution plan fuses Sigmoid into that projection's epilogue
+ * (the sigmoid-columns epilogue of the interleaved query / gate halves,
+ * MetalExecutionPlan.cpp:376-404), and SigmoidMul then lowers to
+ * multiplyF16 of the stored gate and the attention output
+ * (MetalExecutionPlan.cpp:606-614). Here the gate values in q_proj are
+ * those fp16(logistic(.)) values and
+ *   out = fp16(gate * a)                         (multiplyF16, Graph.metal:87-94)
+ * Everything else, the launches, the workspace and the supported shapes are
+ * llmi_hip_gated_attention's. */
+LLMI_HIP_API int llmi_hip_gated_attention_activated(
+    const uint16_t *q_proj, const uint16_t *k_proj, const uint16_t *v_new,
+    const float *q_weight, const float *k_weight, uint16_t *k_cache, uint16_t *v_cache,
+    uint16_t *out, GqaParams p, unsigned rotary_dim, float epsilon, float theta,
+    void *workspace, size_t workspace_bytes, void *stream);
+
 /* ------------------------------------------------------------- DeltaUpdate
  * Replaces graphDeltaUpdate (Graph.metal:146-170 with updateDeltaColumn,
  * Reference.metal:182-197): the gated delta rule over T tokens, per value

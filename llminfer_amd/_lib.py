@@ -176,6 +176,9 @@ SIGNATURES = {
                                                         _P]),
     "llmi_hip_gated_attention": (C.c_int, [_P, _P, _P, _P, _P, _P, _P, _P, GqaParams,
                                            C.c_uint, C.c_float, C.c_float, _P, _SZ, _P]),
+    "llmi_hip_gated_attention_activated": (C.c_int, [_P, _P, _P, _P, _P, _P, _P, _P, GqaParams,
+                                                     C.c_uint, C.c_float, C.c_float, _P, _SZ,
+                                                     _P]),
     "llmi_hip_delta_update": (C.c_int, [_P, _P, _P, _P, _P, _P, _P,
                                         GraphDeltaParams, _P, _SZ, _P]),
     "llmi_hip_delta_workspace_bytes": (_SZ, [GraphDeltaParams]),

@@ -686,12 +686,11 @@ int llmi_hip_kv_append_causal_gqa(const uint16_t *q, const uint16_t *k_new,
                  workspace_bytes, stream);
 }
 
-int llmi_hip_gated_attention(const uint16_t *q_proj, const uint16_t *k_proj,
-                             const uint16_t *v_new, const float *q_weight,
-                             const float *k_weight, uint16_t *k_cache, uint16_t *v_cache,
-                             uint16_t *out, GqaParams p, unsigned rotary_dim, float epsilon,
-                             float theta, void *workspace, size_t workspace_bytes,
-                             void *stream) {
+static int gated_attention(const uint16_t *q_proj, const uint16_t *k_proj,
+                           const uint16_t *v_new, const float *q_weight, const float *k_weight,
+                           uint16_t *k_cache, uint16_t *v_cache, uint16_t *out, GqaParams p,
+                           unsigned rotary_dim, float epsilon, float theta, void *workspace,
+                           size_t workspace_bytes, bool activated, void *stream) {
   if (int st = check_gqa(p))
     return st;
   if (!q_proj || !k_proj || !v_new || !q_weight || !k_weight || !k_cache || !v_cache || !out)
@@ -712,6 +711,7 @@ int llmi_hip_gated_attention(const uint16_t *q_proj, const uint16_t *k_proj,
   ga.kw = k_weight;
   ga.rot = rotary_dim;
   ga.eps = epsilon;
+  ga.activated = activated ? 1u : 0u;
   const unsigned half = rotary_dim / 2;
   if (half > 256)
     return fail(LLMI_HIP_UNSUPPORTED, "gated attention: rotary width %u", rotary_dim);
@@ -741,6 +741,26 @@ int llmi_hip_gated_attention(const uint16_t *q_proj, const uint16_t *k_proj,
   return fail(LLMI_HIP_UNSUPPORTED,
               "gated attention: no fused kernel for T %u, heads %u/%u, head_dim %u, rotary %u",
               p.tokens, p.queryHeads, p.kvHeads, p.headDim, rotary_dim);
+}
+
+int llmi_hip_gated_attention(const uint16_t *q_proj, const uint16_t *k_proj,
+                             const uint16_t *v_new, const float *q_weight,
+                             const float *k_weight, uint16_t *k_cache, uint16_t *v_cache,
+                             uint16_t *out, GqaParams p, unsigned rotary_dim, float epsilon,
+                             float theta, void *workspace, size_t workspace_bytes,
+                             void *stream) {
+  return gated_attention(q_proj, k_proj, v_new, q_weight, k_weight, k_cache, v_cache, out, p,
+                         rotary_dim, epsilon, theta, workspace, workspace_bytes, false, stream);
+}
+
+int llmi_hip_gated_attention_activated(const uint16_t *q_proj, const uint16_t *k_proj,
+                                       const uint16_t *v_new, const float *q_weight,
+                                       const float *k_weight, uint16_t *k_cache,
+                                       uint16_t *v_cache, uint16_t *out, GqaParams p,
+                                       unsigned rotary_dim, float epsilon, float theta,
+                                       void *workspace, size_t workspace_bytes, void *stream) {
+  return gated_attention(q_proj, k_proj, v_new, q_weight, k_weight, k_cache, v_cache, out, p,
+                         rotary_dim, epsilon, theta, workspace, workspace_bytes, true, stream);
 }
 
 size_t llmi_hip_delta_workspace_bytes(GraphDeltaParams p) {

@@ -577,7 +577,7 @@ __global__ __launch_bounds__(64 * kWaves) void gqa_decode_kernel(
         const half_t *gr = ga.qproj + ((size_t)t * Hq + kvh * G + g) * 2 * D + D + x;
 #pragma unroll
         for (int e = 0; e < 4; ++e)
-          y[e] = __builtin_bit_cast(half_t, gate16((float)gr[e], (float)y[e]));
+          y[e] = __builtin_bit_cast(half_t, gate_out((float)gr[e], (float)y[e], ga.activated));
       }
       *reinterpret_cast<half4_t *>(orow + g * D + x) = y;
     }
@@ -612,7 +612,7 @@ template <int D, int G, bool GATED>
 __global__ __launch_bounds__(64) void gqa_decode_merge_kernel(
     const float *__restrict__ wml, const float *__restrict__ wo,
     half_t *__restrict__ out, unsigned Hq, unsigned Hkv, unsigned splits,
-    const half_t *__restrict__ qproj) {
+    const half_t *__restrict__ qproj, unsigned activated) {
   static_assert(D % kMergeCols == 0, "whole channel blocks");
   const unsigned lane = threadIdx.x, g = blockIdx.y, row = blockIdx.z;
   const unsigned x = blockIdx.x * kMergeCols + lane % 16, quarter = lane / 16;
@@ -659,10 +659,14 @@ __global__ __launch_bounds__(64) void gqa_decode_merge_kernel(
   const half_t y = f16_of(acc);
   if constexpr (GATED)
     out[((size_t)t * Hq + kvh * G + g) * D + x] = __builtin_bit_cast(
-        half_t, gate16((float)qproj[((size_t)t * Hq + kvh * G + g) * 2 * D + D + x], (float)y));
+        half_t, gate_out((float)qproj[((size_t)t * Hq + kvh * G + g) * 2 * D + D + x], (float)y,
+                         activated));
   else
     out[((size_t)t * Hq + kvh * G + g) * D + x] = y;
 }
+
+inline unsigned activation_of(const NoRows &) { return 0; }
+inline unsigned activation_of(const GatedRows &ga) { return ga.activated; }
 
 template <int D, int G, bool GATED, typename Rows>
 hipError_t launch_dgg(const GqaShape &s, const uint16_t *q, uint16_t *k,
@@ -690,7 +694,8 @@ hipError_t launch_dgg(const GqaShape &s, const uint16_t *q, uint16_t *k,
     hipLaunchKernelGGL((gqa_decode_merge_kernel<D, G, GATED>), dim3(D / kMergeCols, G, s.T * s.Hkv),
                        dim3(64), 0, stream, reinterpret_cast<float *>(base + w.ml),
                        reinterpret_cast<float *>(base + w.o),
-                       reinterpret_cast<half_t *>(out), s.Hq, s.Hkv, p.splits, qproj);
+                       reinterpret_cast<half_t *>(out), s.Hq, s.Hkv, p.splits, qproj,
+                       activation_of(ga));
   }
   return hipGetLastError();
 }

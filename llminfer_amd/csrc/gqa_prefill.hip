@@ -84,8 +84,9 @@ __device__ __forceinline__ half4_t read_tr(const char *base, unsigned off) {
 // The sigmoid gate of one lane's 16 outputs of a 32-channel tile (the
 // four half4 groups at g + 8 i): the fast logistic first, then the exact one
 // for the few that miss the margin test, one per pass of the wave (as the
-// standalone gate kernel does).
-__device__ __forceinline__ void gate_tile(half4_t (&v)[4], const half_t *g4p) {
+// standalone gate kernel does). activated: the gate values are already
+// fp16(logistic(.)), and the output is their plain product (multiplyF16).
+__device__ __forceinline__ void gate_tile(half4_t (&v)[4], const half_t *g4p, bool activated) {
   float g[16], sg[16];
   unsigned need = 0;
 #pragma unroll
@@ -94,8 +95,8 @@ __device__ __forceinline__ void gate_tile(half4_t (&v)[4], const half_t *g4p) {
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       g[4 * g4 + e] = (float)gv[e];
-      sg[4 * g4 + e] = logistic_estimate(g[4 * g4 + e]);
-      need |= f16_settled(sg[4 * g4 + e]) ? 0u : 1u << (4 * g4 + e);
+      sg[4 * g4 + e] = activated ? g[4 * g4 + e] : logistic_estimate(g[4 * g4 + e]);
+      need |= activated || f16_settled(sg[4 * g4 + e]) ? 0u : 1u << (4 * g4 + e);
     }
   }
   while (need) {
@@ -647,7 +648,7 @@ void gqa_prefill_kernel(const half_t *__restrict__ q, const half_t *__restrict__
                       f16_of(oacc[dt][4 * g4 + 2] * inv), f16_of(oacc[dt][4 * g4 + 3] * inv)};
     if constexpr (GATED)
       gate_tile(v, reinterpret_cast<const half_t *>(ga.qproj) + ((size_t)tq * Hq + h) * 2 * D +
-                       D + 32 * dt + 4 * hi);
+                       D + 32 * dt + 4 * hi, ga.activated);
 #pragma unroll
     for (int g4 = 0; g4 < 4; ++g4)
       *reinterpret_cast<half4_t *>(orow + 32 * dt + 8 * g4 + 4 * hi) = v[g4];
@@ -1076,7 +1077,7 @@ void gqa_prefill_halves_kernel(const half_t *__restrict__ q, const half_t *__res
       }
     if constexpr (GATED)
       gate_tile(v, reinterpret_cast<const half_t *>(ga.qproj) + ((size_t)tq * Hq + h) * 2 * D +
-                       D + 32 * dt + 4 * hi);
+                       D + 32 * dt + 4 * hi, ga.activated);
 #pragma unroll
     for (int g4 = 0; g4 < 4; ++g4)
       *reinterpret_cast<half4_t *>(orow + 32 * dt + 8 * g4 + 4 * hi) = v[g4];

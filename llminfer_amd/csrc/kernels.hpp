@@ -42,7 +42,9 @@ hipError_t launch_gqa_decode(const uint16_t *q, uint16_t *k, uint16_t *v,
 // projected q rows [T][Hq][2D] (per head D query values, then D gate
 // values), the new keys before their norm and the new values [T][Hkv][D],
 // the norm weights [D] (the kernels form 1 + w), the rotary width and the
-// norm epsilon, and pow(theta, 2i/rot) for i < rot/2.
+// norm epsilon, and pow(theta, 2i/rot) for i < rot/2. activated: the gate
+// values are already fp16(logistic(.)) (the q projection's sigmoid-columns
+// epilogue), so the output is fp16(gate * x) -- multiplyF16's bits.
 struct GatedRows {
   const _Float16 *qproj = nullptr;
   const _Float16 *kproj = nullptr;
@@ -50,6 +52,7 @@ struct GatedRows {
   const float *qw = nullptr, *kw = nullptr;
   unsigned rot = 0;
   float eps = 0.0f;
+  unsigned activated = 0;
   float freqs[256] = {};
 };
 

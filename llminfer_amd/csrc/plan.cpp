@@ -18,6 +18,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <array>
 #include <cstring>
 #include <string>
 #include <vector>
@@ -41,7 +42,7 @@ enum class Launch : uint8_t {
   Embedding, EmbeddingW8, Quantize, LinearW8, LinearF16, RmsNorm, GatedRmsNorm,
   GatedRmsNormActivated, L2Norm, Elementwise, SigmoidMul, PartialRope, CausalConv, DeltaGates,
   DeltaUpdate, KvAppend, CausalGqa, CopyView, AddNormQuantize, AddNormLinear, L2DeltaUpdate,
-  GatedNormQuantize, KvAppendGqa
+  GatedNormQuantize, KvAppendGqa, GatedAttention
 };
 
 // One plan record of a launch that serves several ops.
@@ -54,7 +55,7 @@ struct Rec {
 struct Dispatch {
   Launch launch;
   ElementwiseKind elementwise = ElementwiseKind::Add;
-  Ref buf[8];
+  Ref buf[9];
   uint64_t workspaceBytes = 0;
   union {
     EmbedParams embed;
@@ -79,6 +80,11 @@ struct Dispatch {
   std::vector<size_t> ops; // a launch serving several ops: a record for each
   std::vector<Rec> recs;   // ... with their epilogues (replaces ops when set)
   float epsilon = 0.0f, scale = 0.0f; // L2DeltaUpdate: the q / k norms
+  // GatedAttention: the rotation of both normRopes, and whether the gate
+  // values are already activated
+  unsigned rotary = 0;
+  float theta = 0.0f;
+  bool activated = false;
   Ref proj[kNormLinearMax][5]; // AddNormLinear: weight, scales, output, aux, bias
 };
 
@@ -240,6 +246,7 @@ private:
     return g_.tokens == 1 && (k == LLMI_LINEAR_DELTA_DECAY || k == LLMI_LINEAR_DELTA_BETA);
   }
   int lower(size_t index);
+  int gated_attention(size_t s);
   int dense(uint32_t id, Ref &out);
   int linear(size_t producer, uint32_t result, int64_t aux, int64_t bias);
   Ref temporary(uint64_t bytes) { return {Space::Scratch, 0, arena_.allocate(bytes, index_)}; }
@@ -267,9 +274,14 @@ private:
   std::vector<char> skip_;       // launched by a fused launch at another op
   std::vector<std::pair<int64_t, int64_t>> l2Delta_; // by DeltaUpdate op: its q / k L2Norms
   std::vector<int64_t> convSilu_; // by CausalConv1d op: the SiLU launched with it
+  // By SigmoidMul op of a one-row step: the attention block launched with
+  // it -- q norm, k norm, q rope, k rope, KvAppend, CausalGqa.
+  std::vector<std::array<int64_t, 6>> gated_;
+  std::vector<char> inGated_; // launched by a gated block's call; its outputs are never stored
   void prepare_l2_delta();
   void prepare_kv_decode();
   void prepare_conv_silu();
+  void prepare_gated_attention();
 };
 
 int Lowering::validate() {
@@ -568,6 +580,103 @@ void Lowering::prepare_conv_silu() {
       continue;
     convSilu_[j] = (int64_t)j + 1;
     skip_[j + 1] = 1;
+  }
+}
+
+// The attention block of a one-row step (Qwen35ModelBuilder.cpp:175-197) in
+// one call (llmi_hip_gated_attention, or its activated form when the q
+// projection's epilogue has applied the sigmoid to the gate half): RMSNorm
+// and PartialRope of the q half of the projected rows and of the new key,
+// KvAppend, CausalGqa and the SigmoidMul with the gate half -- the bits of
+// those launches in that order. Each op keeps its record; the
+// intermediate values are never stored. Taken only when nothing else is
+// launched inside the block, every intermediate has that one consumer, q
+// and the gate are the two halves of one [1][Hq][2d] row set, both norms
+// share the epsilon and both rotations the width and theta, and the fused
+// kernels take the shape. The projected rows stay live until the
+// SigmoidMul, where the call is made, so its output never covers them.
+void Lowering::prepare_gated_attention() {
+  gated_.assign(g_.op_count, {-1, -1, -1, -1, -1, -1});
+  inGated_.assign(g_.op_count, 0);
+  if (g_.tokens != 1)
+    return;
+  auto def = [&](uint32_t id) { return value(id).defining_op; };
+  auto single = [&](uint32_t id) {
+    return value(id).kind == LLMI_GRAPH_RESULT && uses_[id] == 1;
+  };
+  auto is = [&](int64_t x, uint32_t kind) { return x >= 0 && op((size_t)x).kind == kind; };
+  auto f16 = [&](uint32_t id) { return value(id).element == LLMI_GRAPH_F16; };
+  for (size_t s = 0; s < g_.op_count; ++s) {
+    const auto &sm = op(s);
+    if (sm.kind != LLMI_GRAPH_SIGMOID_MUL || skip_[s])
+      continue;
+    const uint32_t gate = sm.inputs[0], mixed = sm.inputs[1];
+    const int64_t j = def(mixed);
+    if (!is(j, LLMI_GRAPH_CAUSAL_GQA) || !single(mixed))
+      continue;
+    const auto &att = op((size_t)j);
+    const int64_t rq = def(att.inputs[0]);
+    if (!is(rq, LLMI_GRAPH_PARTIAL_ROPE) || !single(att.inputs[0]))
+      continue;
+    const int64_t nq = def(op((size_t)rq).inputs[0]);
+    if (!is(nq, LLMI_GRAPH_RMS_NORM) || !single(op((size_t)rq).inputs[0]))
+      continue;
+    int64_t a = j - 1;
+    while (is(a, LLMI_GRAPH_RESHAPE) || is(a, LLMI_GRAPH_SLICE))
+      --a;
+    if (!is(a, LLMI_GRAPH_KV_APPEND) || op((size_t)a).keys != att.keys ||
+        op((size_t)a).values != att.values)
+      continue;
+    const auto &app = op((size_t)a);
+    const int64_t rk = def(app.inputs[0]);
+    if (!is(rk, LLMI_GRAPH_PARTIAL_ROPE) || !single(app.inputs[0]))
+      continue;
+    const int64_t nk = def(op((size_t)rk).inputs[0]);
+    if (!is(nk, LLMI_GRAPH_RMS_NORM) || !single(op((size_t)rk).inputs[0]))
+      continue;
+    // q and the gate: the halves of one contiguous [1][Hq][2d] row set
+    const uint32_t qv = op((size_t)nq).inputs[0];
+    const int64_t sq = def(qv), sg = def(gate);
+    if (!is(sq, LLMI_GRAPH_SLICE) || !is(sg, LLMI_GRAPH_SLICE))
+      continue;
+    const auto &slq = op((size_t)sq), &slg = op((size_t)sg);
+    const uint32_t qg = slq.inputs[0];
+    if (value(qg).rank != 3 || !f16(qg) || !contiguous(qg) || slg.inputs[0] != qg)
+      continue;
+    const uint64_t D = dim(qg, 2) / 2;
+    if (slq.axis != 2 || slg.axis != 2 || slq.begin != 0 || slq.length != D ||
+        slg.begin != D || slg.length != D || dim(qg, 2) != 2 * D)
+      continue;
+    const uint32_t k = op((size_t)nk).inputs[0], v = app.inputs[1];
+    if (value(k).rank != 3 || value(v).rank != 3 || !f16(k) || !f16(v) || !contiguous(k) ||
+        !contiguous(v) || dim(k, 2) != D || dim(v, 2) != D || dim(v, 1) != dim(k, 1))
+      continue;
+    const auto &oq = op((size_t)rq), &ok = op((size_t)rk);
+    const uint32_t wq = op((size_t)nq).inputs[1], wk = op((size_t)nk).inputs[1];
+    if (op((size_t)nq).epsilon != op((size_t)nk).epsilon || oq.rotary_width != ok.rotary_width ||
+        oq.theta != ok.theta || oq.rotary_width % 16 != 0 || oq.rotary_width > D ||
+        value(wq).element != LLMI_GRAPH_F32 || value(wk).element != LLMI_GRAPH_F32 ||
+        count(wq) != D || count(wk) != D)
+      continue;
+    const auto &cache = g_.states[att.keys].shape;
+    GqaParams gp{1, (unsigned)dim(qg, 1), (unsigned)cache[1], (unsigned)cache[2],
+                 (unsigned)g_.past};
+    if (cache[2] != D || dim(k, 1) != cache[1] ||
+        llmi_hip_dispatch_count(LLMI_HIP_OP_GATED_ATTENTION, &gp) == 0)
+      continue;
+    const std::array<int64_t, 6> blk{nq, nk, rq, rk, a, j};
+    bool quiet = true; // nothing else launched inside the block
+    for (size_t x = (size_t)std::min(nq, nk); x < s && quiet; ++x)
+      quiet = std::find(blk.begin(), blk.end(), (int64_t)x) != blk.end()
+                  ? !skip_[x]
+                  : op(x).kind == LLMI_GRAPH_RESHAPE || op(x).kind == LLMI_GRAPH_SLICE;
+    if (!quiet)
+      continue;
+    gated_[s] = blk;
+    for (int64_t x : blk)
+      skip_[(size_t)x] = inGated_[(size_t)x] = 1;
+    for (uint32_t x : {qg, k, v})
+      lastUse_[root_[x]] = std::max(lastUse_[root_[x]], s);
   }
 }
 
@@ -935,9 +1044,12 @@ int Lowering::lower(size_t i) {
     d.buf[0] = r[0], d.buf[1] = r[1];
     return LLMI_HIP_OK;
   }
+  case LLMI_GRAPH_SIGMOID_MUL:
+    if (gated_[i][0] >= 0)
+      return gated_attention(i);
+    [[fallthrough]];
   case LLMI_GRAPH_ADD:
-  case LLMI_GRAPH_SILU_MUL:
-  case LLMI_GRAPH_SIGMOID_MUL: {
+  case LLMI_GRAPH_SILU_MUL: {
     const int64_t p = value(in[0]).defining_op;
     if (o.kind == LLMI_GRAPH_SILU_MUL && p >= 0 && fusion_[p].kind == LLMI_LINEAR_SILU_MUL)
       return linear(p, out[0], in[1], -1);
@@ -1100,6 +1212,66 @@ int Lowering::lower(size_t i) {
   }
 }
 
+// The attention block closed by SigmoidMul s (prepare_gated_attention), in
+// one llmi_hip_gated_attention(_activated) call recorded under each op.
+int Lowering::gated_attention(size_t s) {
+  const auto &blk = gated_[s];
+  const auto &sm = op(s), &nq = op((size_t)blk[0]), &nk = op((size_t)blk[1]);
+  const auto &rq = op((size_t)blk[2]), &att = op((size_t)blk[5]);
+  const uint32_t gate = sm.inputs[0];
+  const uint32_t qg = op((size_t)value(nq.inputs[0]).defining_op).inputs[0];
+  Ref r[6];
+  for (auto [id, slot] : {std::pair<uint32_t, int>{qg, 0}, {nk.inputs[0], 1},
+                          {op((size_t)blk[4]).inputs[1], 2}, {nq.inputs[1], 3},
+                          {nk.inputs[1], 4}, {sm.outputs[0], 5}})
+    if (int rc = dense(id, r[slot]))
+      return rc;
+  const auto &cache = g_.states[att.keys].shape;
+  const GqaParams p{1, (unsigned)dim(qg, 1), (unsigned)cache[1], (unsigned)cache[2],
+                    (unsigned)g_.past};
+  const unsigned n = llmi_hip_dispatch_count(LLMI_HIP_OP_GATED_ATTENTION, &p);
+  if (n == 0)
+    return fail(LLMI_HIP_UNSUPPORTED, "plan: op %zu: %s", s, llmi_hip_last_error());
+  const int64_t gp = value(root_[gate]).defining_op;
+  Dispatch &d = emit(Launch::GatedAttention, nullptr);
+  d.p.gqa = p;
+  for (unsigned k = 0; k < n; ++k)
+    d.kernels.push_back(llmi_hip_kernel_name(LLMI_HIP_OP_GATED_ATTENTION, &p, k));
+  for (int k = 0; k < 5; ++k)
+    d.buf[k] = r[k];
+  d.buf[5] = {Space::State, att.keys, 0};
+  d.buf[6] = {Space::State, att.values, 0};
+  d.buf[7] = r[5];
+  d.epsilon = nq.epsilon;
+  d.rotary = (unsigned)rq.rotary_width;
+  d.theta = rq.theta;
+  d.activated = gp >= 0 && fusion_[gp].kind == LLMI_LINEAR_SIGMOID_COLUMNS;
+  d.workspaceBytes = llmi_hip_gqa_workspace_bytes(p);
+  if (d.workspaceBytes)
+    d.buf[8] = temporary(d.workspaceBytes);
+  // The call reads the projected rows while it writes its output and
+  // workspace: the rows are live until this op, so the arena keeps them
+  // apart; checked here all the same.
+  auto overlap = [](const Ref &a, uint64_t an, const Ref &b, uint64_t bn) {
+    return a.space == b.space && a.index == b.index && a.space == Space::Scratch &&
+           a.offset < b.offset + bn && b.offset < a.offset + an;
+  };
+  const uint64_t rowsQ = 2ull * p.queryHeads * 2 * p.headDim, rowKV = 2ull * p.kvHeads * p.headDim;
+  const uint64_t outBytes = 2ull * p.queryHeads * p.headDim, ws = d.workspaceBytes;
+  const std::pair<Ref, uint64_t> reads[3] = {{r[0], rowsQ}, {r[1], rowKV}, {r[2], rowKV}};
+  for (const auto &[ref, n] : reads)
+    if (overlap(ref, n, r[5], outBytes) || (ws && overlap(ref, n, d.buf[8], ws)))
+      return fail(LLMI_HIP_INVALID_ARGUMENT, "plan: op %zu: the attention block's output "
+                  "or workspace overlaps its projected rows", s);
+  if (ws && overlap(r[5], outBytes, d.buf[8], ws))
+    return fail(LLMI_HIP_INVALID_ARGUMENT, "plan: op %zu: output overlaps the workspace", s);
+  for (int64_t x : blk)
+    d.recs.push_back({(size_t)x, nullptr, 0});
+  d.recs.push_back({s, nullptr, 0});
+  std::sort(d.recs.begin(), d.recs.end(), [](const Rec &a, const Rec &b) { return a.op < b.op; });
+  return LLMI_HIP_OK;
+}
+
 int Lowering::run() {
   if (int rc = validate())
     return rc;
@@ -1120,6 +1292,7 @@ int Lowering::run() {
   prepare_l2_delta();
   prepare_kv_decode();
   prepare_conv_silu();
+  prepare_gated_attention();
   if (g_.output_count) {
     const uint32_t id = g_.outputs[0];
     const auto &v = value(id);
@@ -1161,6 +1334,8 @@ int Lowering::run() {
     if (f.deferred())
       continue; // runs at its consumer, into the consumer's output
     const auto &o = op(index_);
+    if (inGated_[index_])
+      continue; // launched, and recorded, at the block's SigmoidMul
     if (normQuantize_[index_] >= 0)
       allocate(op(normQuantize_[index_]), false); // the norm itself stores nothing
     else if (convSilu_[index_] >= 0)
@@ -1230,8 +1405,8 @@ void *resolve(const Bases &b, const Ref &r) {
 }
 
 int run_dispatch(const Dispatch &d, const Bases &b, hipStream_t stream) {
-  void *x[8];
-  for (int i = 0; i < 8; ++i)
+  void *x[9];
+  for (int i = 0; i < 9; ++i)
     x[i] = resolve(b, d.buf[i]);
   auto u16 = [&](int i) { return static_cast<uint16_t *>(x[i]); };
   auto f32 = [&](int i) { return static_cast<float *>(x[i]); };
@@ -1291,6 +1466,10 @@ int run_dispatch(const Dispatch &d, const Bases &b, hipStream_t stream) {
                                          d.p.gqa, x[4], d.workspaceBytes, stream);
   case Launch::CopyView:
     return llmi_hip_copy_half_view(u16(0), u16(1), d.p.view, stream);
+  case Launch::GatedAttention:
+    return (d.activated ? llmi_hip_gated_attention_activated : llmi_hip_gated_attention)(
+        u16(0), u16(1), u16(2), f32(3), f32(4), u16(5), u16(6), u16(7), d.p.gqa, d.rotary,
+        d.epsilon, d.theta, x[8], d.workspaceBytes, stream);
   case Launch::GatedNormQuantize:
     return llmi_hip_gated_rms_norm_activated_quantize(u16(0), f32(1), f32(2), u16(3),
                                                       (int8_t *)x[4], f32(5), (uint32_t *)x[6],

@@ -79,6 +79,13 @@ __device__ __forceinline__ uint16_t gate16(float gate, float x) {
   return f2h(mul32(logistic16(gate), x));
 }
 
+// The output gate of the gated attention forms: fp16(fp16(logistic(gate)) *
+// x), or fp16(gate * x) when the gate values are already activated
+// (multiplyF16, the product of two fp16 values in fp32, rounded once).
+__device__ __forceinline__ uint16_t gate_out(float gate, float x, bool activated) {
+  return activated ? f2h(mul32(gate, x)) : gate16(gate, x);
+}
+
 __device__ __forceinline__ uint16_t gate_one(uint16_t g, uint16_t x) {
   return gate16(h2f(g), h2f(x));
 }

@@ -629,12 +629,15 @@ def delta_update(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, beta: torch.
 def bind_gated_attention(q_proj: torch.Tensor, k_proj: torch.Tensor, v_new: torch.Tensor,
                          q_weight: torch.Tensor, k_weight: torch.Tensor, k_cache: torch.Tensor,
                          v_cache: torch.Tensor, out: torch.Tensor, past: int, rotary_dim: int,
-                         epsilon: float = 1e-6, theta: float = 1e7) -> "Bound":
+                         epsilon: float = 1e-6, theta: float = 1e7,
+                         activated: bool = False) -> "Bound":
     """The attention block around CausalGqa in one call (llmi_hip_gated_attention):
     q_proj [T, Hq, 2d] (per head d query then d gate values), k_proj and v_new
     [T, Hkv, d], norm weights [d] fp32, caches [capacity, Hkv, d], out
     [T, Hq, d]: normRope(q), normRope(k) into the cache at row past, V
-    appended, CausalGqa, sigmoid gate."""
+    appended, CausalGqa, sigmoid gate. activated: the gate values are already
+    fp16(logistic(.)) and the output is their product with the attention
+    (llmi_hip_gated_attention_activated)."""
     for t, n in ((q_proj, "q_proj"), (k_proj, "k_proj"), (v_new, "v_new"),
                  (k_cache, "k_cache"), (v_cache, "v_cache"), (out, "out")):
         _require(t, torch.float16, n)
@@ -658,20 +661,21 @@ def bind_gated_attention(q_proj: torch.Tensor, k_proj: torch.Tensor, v_new: torc
             _ptr(k_cache), _ptr(v_cache), _ptr(out), p, rotary_dim, epsilon, theta, _ptr(ws),
             ws.numel() if ws is not None else 0, _stream())
     names = kernel_names(_lib.OP_GATED_ATTENTION, p)
-    b = Bound(lib.llmi_hip_gated_attention, args, "+".join(names))
+    fn = lib.llmi_hip_gated_attention_activated if activated else lib.llmi_hip_gated_attention
+    b = Bound(fn, args, "+".join(names))
     b._keep = ws
     return b
 
 
 def gated_attention(q_proj, k_proj, v_new, q_weight, k_weight, k_cache, v_cache, past: int,
                     rotary_dim: int, epsilon: float = 1e-6, theta: float = 1e7,
-                    out: torch.Tensor | None = None) -> torch.Tensor:
+                    out: torch.Tensor | None = None, activated: bool = False) -> torch.Tensor:
     """bind_gated_attention, called once."""
     if out is None:
         T, hq, d2 = q_proj.shape
         out = torch.empty((T, hq, d2 // 2), dtype=torch.float16, device=q_proj.device)
     bind_gated_attention(q_proj, k_proj, v_new, q_weight, k_weight, k_cache, v_cache, out,
-                         past, rotary_dim, epsilon, theta)()
+                         past, rotary_dim, epsilon, theta, activated)()
     return out
 
 

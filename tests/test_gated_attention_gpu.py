@@ -98,3 +98,47 @@ def test_fused_block_against_the_oracle(gpu, T, past, hq, hkv):
     want = attn / (1.0 + np.exp(-gate))
     got = oracle.f16_to_f32(torch_to_u16(out)).astype(np.float64)
     assert np.max(np.abs(got - want)) <= 2e-3
+
+
+@pytest.mark.parametrize("T,past,shape,rot", [
+    (1, 0, (16, 4, 256), 64), (1, 33, (16, 4, 256), 64), (1, 512, (16, 4, 256), 64),
+    (1, 4096, (16, 4, 256), 64), (1, 700, (8, 4, 128), 32), (40, 24, (16, 4, 256), 64),
+    (65, 17, (16, 4, 128), 32)])
+def test_activated_block_equals_the_unfused_ops(gpu, T, past, shape, rot):
+    """llmi_hip_gated_attention_activated: the gate half of q_proj already
+    holds fp16(logistic(gate)) (here made by sigmoidMul against ones, the
+    values the q projection's sigmoid-columns epilogue stores); the output
+    must equal multiplyF16(gate, attention) after the same unfused normRope,
+    append and attention, bit for bit, with the caches."""
+    hq, hkv, d = shape
+    print(f"activated gated attention T={T} past={past} shape={shape} rot={rot}", flush=True)
+    x, q_proj, k_proj, qw, kw = _case(700 + T + past, T, hq, hkv, d, past)
+    f32 = lambda a: torch.from_numpy(a).to(gpu)
+    qp = u16_to_torch(q_proj, gpu)
+    act = torch.empty((T, hq, d), dtype=torch.float16, device=gpu)
+    ops.sigmoid_mul(qp[:, :, d:].contiguous(), torch.ones_like(act), act)
+    qp[:, :, d:] = act
+    kp, vn = u16_to_torch(k_proj, gpu), u16_to_torch(x.v_new, gpu)
+    base_k, base_v = u16_to_torch(x.k_cache, gpu), u16_to_torch(x.v_cache, gpu)
+    base_k[past:] = 0
+    base_v[past:] = 0
+    kc, vc = base_k.clone(), base_v.clone()
+    qn = torch.empty((T, hq, d), dtype=torch.float16, device=gpu)
+    ops.norm_rope(qp, f32(qw), qn, past, rot, EPS, THETA, head_dim=d)
+    ops.norm_rope(kp, f32(kw), kc, past, rot, EPS, THETA, output_start=past)
+    ops.cache_append(vn, vc, past * hkv * d)
+    attn = ops.causal_gqa(qn, kc, vc, past)
+    ref = torch.empty_like(attn)
+    ops.elementwise("multiply", act, attn, ref)
+    kc2, vc2 = base_k.clone(), base_v.clone()
+    out = ops.gated_attention(qp, kp, vn, f32(qw), f32(kw), kc2, vc2, past, rot, EPS, THETA,
+                              activated=True)
+    torch.cuda.synchronize()
+    assert torch.equal(kc, kc2), "key cache differs"
+    assert torch.equal(vc, vc2), "value cache differs"
+    assert torch.equal(ref, out), "output differs from multiplyF16 after the unfused ops"
+    # the plain call on the same rows applies the logistic again: different
+    plain = ops.gated_attention(qp, kp, vn, f32(qw), f32(kw), base_k.clone(), base_v.clone(),
+                                past, rot, EPS, THETA)
+    torch.cuda.synchronize()
+    assert not torch.equal(plain, out)

@@ -6,10 +6,12 @@
   order, every non-view op covered by a launch or a fused epilogue, a
   copyHalfView for the interleaved query / gate halves, the epilogue
   multiset {sigmoid x2, silu, softplus_decay, swiglu x2}, no unfused
-  swiGlu / deltaGates / sigmoidMul, and the head on linearW8A8Gemm / Gemv by row count, and fewer
-  launches without logits. Where the reference keeps an unfused siluF16
-  after the convolution, the SiLU here runs in the convolution's launch
-  (causalConv with applySilu: the same bits) and is recorded under it.
+  swiGlu / deltaGates / sigmoidMul, the head on linearW8A8Gemm / Gemv by
+  row count, and fewer launches without logits. Where the reference keeps
+  an unfused siluF16 after the convolution, the SiLU here runs in the
+  convolution's launch (causalConv with applySilu: the same bits) and is
+  recorded under it. Qwen3.5-4B's one-row attention blocks lower to one
+  gated-attention call each, recorded under every op of the block.
 * The oracle runner (oracle/graph_runner.py) executes the same graphs op by
   op on the CPU oracle; its logits are pinned against HF transformers'
   Qwen3.5 decoder layers with the reference test's W8A8 projection
@@ -19,6 +21,7 @@
 """
 import ctypes as C
 from collections import Counter
+from dataclasses import replace
 from functools import partial
 
 import numpy as np
@@ -114,18 +117,21 @@ def test_qwen35_4b_lowers_with_the_hot_kernels():
     assert kinds["gatedRmsNormQuantize"] == 24 * 2 and kinds["quantizeActivation"] == 40
     # the q and k L2Norms run inside the one-row DeltaUpdate's loads
     # (llmi_hip_l2_norm_delta_update), recorded under its kernel
-    # each attention layer's KvAppend and CausalGqa in the fused decode
-    # call (llmi_hip_kv_append_causal_gqa), both ops recorded under its
-    # split and merge kernels
-    assert kinds["gqaDecodeSplitK"] == kinds["gqaDecodeMerge"] == 8 * 2
-    assert kinds["kvAppend"] == 0 and kinds["deltaRecurrent"] == 24 * 3
+    # each attention layer's block -- the q and k RMSNorms and PartialRopes,
+    # KvAppend, CausalGqa and the SigmoidMul with the gate the q projection
+    # activated -- in one call (llmi_hip_gated_attention_activated), its
+    # seven ops recorded under its split and merge kernels
+    assert kinds["gqaDecodeGated"] == kinds["gqaDecodeMergeGated"] == 8 * 7
+    assert not {"gqaDecodeSplitK", "kvAppend", "normRopeTile", "partialRopeTile",
+                "copyHalfView", "multiplyF16"} & set(kinds)
+    assert kinds["deltaRecurrent"] == 24 * 3
     assert kinds["l2NormF32"] == 0
     # each DeltaNet layer's convolution with its SiLU
     assert kinds["causalConv"] == 24 * 2 and kinds["siluF16"] == 0
     # a launch that serves several ops (the Adds, norms, quantizations,
-    # projections and SiLUs above) has a record for each: 740 records,
-    # 315 launches
-    assert len(decode.dispatches) == 740 and decode.launches == 315
+    # projections, SiLUs and attention blocks above) has a record for each:
+    # 764 records, 259 launches
+    assert len(decode.dispatches) == 764 and decode.launches == 259
     assert kinds["residualAdd"] == 0
     assert "quantizeActivation" in kinds     # the others (after GQA / gated norms, SwiGLU)
     indices = [d["op_index"] for d in decode.dispatches]
@@ -153,13 +159,32 @@ def test_fused_decode_output_never_covers_the_new_rows(past):
     and it fuses only when neither the output nor the workspace overlaps the
     new rows (a clash leaves KvAppend as its own launch). So a fused decode
     in every attention layer at every past, with no kvAppend launch, shows
-    that no output of a fused decode covers its new rows."""
-    c = G.qwen35_4b()
+    that no output of a fused decode covers its new rows. (Qwen3.5-4B with a
+    40-wide rotation, which the whole-block call does not take, so that the
+    plan uses this pair.)"""
+    c = replace(G.qwen35_4b(), rotary_width=40)
     _, decode = _lower(c, 1, past, 8192, "last", True)
     kinds = Counter(d["kernel"] for d in decode.dispatches)
     assert kinds["kvAppend"] == 0
     assert kinds["gqaDecodeSplitK"] == 8 * 2
     assert kinds["gqaDecodeMerge"] == (0 if past + 1 <= 32 else 8 * 2)
+
+
+@pytest.mark.parametrize("past", [0, 5, 31, 32, 100, 4096])
+def test_gated_block_output_never_covers_its_rows(past):
+    """The one-row attention block call reads the projected q / gate rows,
+    the new key and value rows while it writes its output (in the split
+    launch itself when there is one split). The lowering keeps those rows
+    live until the block's SigmoidMul, where the call is made, and refuses
+    to lower (an error, not a silent overlap) if the output or the workspace
+    covered them; so the block in all 8 attention layers at every past shows
+    that they never do."""
+    c = G.qwen35_4b()
+    _, decode = _lower(c, 1, past, 8192, "last", True)
+    kinds = Counter(d["kernel"] for d in decode.dispatches)
+    assert kinds["gqaDecodeGated"] == 8 * 7
+    assert kinds["gqaDecodeMergeGated"] == (0 if past + 1 <= 32 else 8 * 7)
+    assert "kvAppend" not in kinds and "gqaDecodeSplitK" not in kinds
 
 
 def test_malformed_graphs_are_rejected_before_any_launch():

@@ -168,7 +168,9 @@ def test_small_plan_on_the_hot_kernels(gpu):
     for a, b in zip(session.states, states):
         assert _same_state(a, b)
     kernels = {d["kernel"] for d in session.plan(1, "last").dispatches}
-    assert {"gqaDecodeSplitK", "deltaRecurrent", "linearW8A8Gemv"} <= kernels
+    # the one-row attention block in one call (llmi_hip_gated_attention_activated)
+    assert {"gqaDecodeGated", "deltaRecurrent", "linearW8A8Gemv"} <= kernels
+    assert "gqaDecodeSplitK" not in kernels
     want, _ = run_oracle(c, weights, chunks, capacity=256)
     for p, w_ in zip(plan_logits, want):
         # measured 0.8-1.0 % (max 0.022): the MFMA attention and chunked
@@ -228,8 +230,9 @@ def test_qwen35_4b_decode_step(gpu):
         assert _same_state(a, b)
     kinds = [d["kernel"] for d in r.dispatches]
     # deltaRecurrent: the update and its fused q / k L2Norms, a record each
-    # gqaDecodeSplitK: KvAppend and CausalGqa in one fused call, a record each
-    assert kinds.count("gqaDecodeSplitK") == 8 * 2 and kinds.count("deltaRecurrent") == 24 * 3
+    # gqaDecodeGated: the attention block's seven ops (q / k RMSNorm and
+    # PartialRope, KvAppend, CausalGqa, SigmoidMul) in one call, a record each
+    assert kinds.count("gqaDecodeGated") == 8 * 7 and kinds.count("deltaRecurrent") == 24 * 3
 
 
 def test_nonfinite_activation_invalidates_until_reset(gpu):
