@@ -11,7 +11,10 @@ output and cache bits, at the decode (one launch + merge) and prefill
 (K normRope + append, then the MFMA prefill with q normRope in its load and
 the gate in its store) shapes. Two cases are also checked end to end against
 the oracle: oracle normRope and sigmoidMul around the double-precision
-attention, within the north-star 2e-3.
+attention, within the north-star 2e-3. The activated form
+(llmi_hip_gated_attention_activated: the gate half already holds
+fp16(logistic(.)), as the q projection's sigmoid-columns epilogue leaves it)
+must equal the same unfused ops with multiplyF16 in place of sigmoidMul.
 """
 import numpy as np
 import pytest
