@@ -464,14 +464,20 @@ __global__ __launch_bounds__(256, 2) void delta_prep_kernel(
     // above the diagonal blocks (wave 3: s >= 16, t < 16).
     if ((wave == 0 || wave == 3) && lane < 16) {
       const unsigned j = lane, b0 = wave == 0 ? 0u : 16u;
-      float col[16];
+      // Column-oriented: once col[u] is known it enters every later row's
+      // sum. Each row's fma chain still runs over u in increasing order
+      // (the bits of the row-by-row form), but the rows' chains are
+      // independent, and the A values can be read well ahead of their use.
+      float col[16], acc[16];
 #pragma unroll
-      for (int t = 0; t < 16; ++t) {
-        float acc = 0.0f;
+      for (int t = 0; t < 16; ++t)
+        acc[t] = 0.0f;
 #pragma unroll
-        for (int u = 0; u < t; ++u)
-          acc = fmaf(sA[(b0 + t) * FS + b0 + u], col[u], acc);
-        col[t] = (unsigned)t == j ? 1.0f : ((unsigned)t > j ? -acc : 0.0f);
+      for (int u = 0; u < 16; ++u) {
+        col[u] = (unsigned)u == j ? 1.0f : ((unsigned)u > j ? -acc[u] : 0.0f);
+#pragma unroll
+        for (int t = u + 1; t < 16; ++t)
+          acc[t] = fmaf(sA[(b0 + t) * FS + b0 + u], col[u], acc[t]);
       }
 #pragma unroll
       for (int t = 0; t < 16; ++t)
