@@ -443,6 +443,27 @@ LLMI_HIP_API int llmi_hip_l2_norm_delta_gated_norm_status(const void *workspace,
                                                           size_t workspace_bytes,
                                                           GraphDeltaParams p, void *stream);
 
+/* The same chain with the W8A8 model's tail (Qwen35ModelBuilder.cpp:
+ * 155-166, then project(prepare(gated)): the out projection's
+ * QuantizeActivation of the normalised rows), for a one-workgroup-per-head
+ * step: gate is z as the fp32 SiLU epilogue of its projection left it
+ * (llmi_hip_gated_rms_norm_activated), fp32 [T][Hv*dv]; out, quantized,
+ * scales and *invalid receive, bit for bit, what
+ * llmi_hip_l2_norm_delta_update followed by
+ * llmi_hip_gated_rms_norm_activated_quantize(rows T*Hv, width dv,
+ * norm_epsilon) leave there (its quantization: the flattened rows in
+ * 32-wide groups). No counterpart in the reference, which launches them
+ * one by one; the plan uses it for a decode step's DeltaNet tail. q, k, v,
+ * beta, decay and state as llmi_hip_l2_norm_delta_update. dk 64 or 128, dv
+ * 64 or 128, T <= 32, out and quantized 16-byte aligned (else
+ * LLMI_HIP_UNSUPPORTED); no workspace. No output may overlap an input:
+ * each workgroup writes its head's rows while others still read. */
+LLMI_HIP_API int llmi_hip_l2_norm_delta_gated_norm_activated_quantize(
+    const uint16_t *q, const uint16_t *k, const uint16_t *v, const float *beta,
+    const float *decay, float *state, const float *gate, const float *norm_weight,
+    uint16_t *out, int8_t *quantized, float *scales, uint32_t *invalid, GraphDeltaParams p,
+    float qk_epsilon, float q_scale, float norm_epsilon, void *stream);
+
 /* Bound, in polls, of that arrival wait for later launches (0: every
  * workgroup gives up at once); returns the previous bound (default 2^22,
  * ~0.3 s). Process-wide, not thread-safe against concurrent launches. No

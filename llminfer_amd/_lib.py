@@ -188,6 +188,9 @@ SIGNATURES = {
                                                     GraphDeltaParams, C.c_float, C.c_float,
                                                     C.c_float, _P, _SZ, _P]),
     "llmi_hip_l2_norm_delta_gated_norm_status": (C.c_int, [_P, _SZ, GraphDeltaParams, _P]),
+    "llmi_hip_l2_norm_delta_gated_norm_activated_quantize": (
+        C.c_int, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, GraphDeltaParams, C.c_float,
+                  C.c_float, C.c_float, _P]),
     "llmi_hip_set_arrival_wait_limit": (C.c_uint, [C.c_uint]),
     "llmi_hip_quantize_activation": (C.c_int, [_P, _P, _P, _P, QuantizeParams, _P]),
     "llmi_hip_linear_w8a8": (C.c_int, [_P, _P, _P, _P, _P, _P, _P, LinearW8Params, _P]),

@@ -902,6 +902,35 @@ int llmi_hip_l2_norm_delta_gated_norm_status(const void *workspace, size_t works
   return LLMI_HIP_OK;
 }
 
+int llmi_hip_l2_norm_delta_gated_norm_activated_quantize(
+    const uint16_t *q, const uint16_t *k, const uint16_t *v, const float *beta,
+    const float *decay, float *state, const float *gate, const float *norm_weight,
+    uint16_t *out, int8_t *quantized, float *scales, uint32_t *invalid, GraphDeltaParams p,
+    float qk_epsilon, float q_scale, float norm_epsilon, void *stream) {
+  if (int st = check_delta(p))
+    return st;
+  if (!q || !k || !v || !beta || !decay || !state || !gate || !norm_weight || !out ||
+      !quantized || !scales)
+    return fail(LLMI_HIP_INVALID_ARGUMENT,
+                "L2Norm+DeltaUpdate+GatedRmsNormQuantize: null buffer");
+  DeltaShape s{p.tokens, p.keyHeads, p.keyDim, p.valueHeads, p.valueDim};
+  if (!delta_recurrent_norm_supported(s))
+    return fail(LLMI_HIP_UNSUPPORTED,
+                "L2Norm+DeltaUpdate+GatedRmsNormQuantize: T %u, dk %u, dv %u have no fused "
+                "kernel (dk 64 or 128, dv 64 or 128, T <= %u)",
+                p.tokens, p.keyDim, p.valueDim, kRecNormMaxT);
+  // The norm writes 16-byte pieces of out and 8-byte pieces of quantized.
+  if (!aligned16(out) || !aligned16(quantized))
+    return fail(LLMI_HIP_UNSUPPORTED,
+                "L2Norm+DeltaUpdate+GatedRmsNormQuantize: out and quantized must be 16-byte "
+                "aligned");
+  return launched(launch_delta_recurrent_gated_norm_quantize(
+                      q, k, v, beta, decay, state, gate, norm_weight, out, quantized, scales,
+                      invalid, qk_epsilon, q_scale, norm_epsilon, s,
+                      static_cast<hipStream_t>(stream)),
+                  "deltaRecurrent+gatedRmsNormQuantize");
+}
+
 unsigned llmi_hip_set_arrival_wait_limit(unsigned polls) {
   return delta_chunked_wait_limit(polls);
 }

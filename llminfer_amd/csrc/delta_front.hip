@@ -339,39 +339,8 @@ __global__ __launch_bounds__(64) void gated_rms_norm_tile(const uint16_t *__rest
     for (int e = 0; e < 4; ++e)
       o[e] = (uint32_t)f2h(y[2 * e]) | ((uint32_t)f2h(y[2 * e + 1]) << 16);
     *reinterpret_cast<uint4_t *>(out + base) = o;
-    if constexpr (kQuant) {
-      float x[8], max_abs = 0.0f;
-      bool finite = true;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        x[e] = h2f(f2h(y[e]));
-        finite = finite && __builtin_isfinite(x[e]);
-        max_abs = fmaxf(max_abs, fabsf(x[e]));
-      }
-#pragma unroll
-      for (int m = 1; m < 4; m *= 2) {
-        max_abs = fmaxf(max_abs, __shfl_xor(max_abs, m, 4));
-        finite = __shfl_xor((int)finite, m, 4) && finite;
-      }
-      const float qs = finite && max_abs > 0.0f ? __fdiv_rn(max_abs, 127.0f) : 1.0f;
-      uint32_t words[2] = {0u, 0u};
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        int r = 0;
-        if (finite) {
-          const float v = fminf(fmaxf(__fdiv_rn(x[e], qs), -127.0f), 127.0f);
-          r = (int)__builtin_rintf(v);
-        }
-        words[e / 4] |= ((uint32_t)r & 0xFFu) << (8 * (e % 4));
-      }
-      reinterpret_cast<uint32_t *>(qout + base)[0] = words[0];
-      reinterpret_cast<uint32_t *>(qout + base)[1] = words[1];
-      if ((c & 3u) == 0) {
-        scales[base / 32] = qs;
-        if (!finite && invalid)
-          atomicOr(invalid, 1u);
-      }
-    }
+    if constexpr (kQuant)
+      quantize_chunk8(y, qout + base, scales + base / 32, invalid, (c & 3u) == 0);
   }
 }
 

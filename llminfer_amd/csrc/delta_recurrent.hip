@@ -50,14 +50,20 @@ namespace {
 // row's sequential sum of squares, and every element becomes fp16(fp16(x *
 // factor) * weight * silu(gate)) (gated_norm.hpp, the standalone kernel's
 // arithmetic). The gate and weight values are requested at the start.
-template <int DK, int CW, int NW, bool QK16, int CG = 1, bool NORM = false>
+// With ACTQ the gate is the fp32 activated one (gatedRmsNorm with the
+// projection's SiLU epilogue: fp16(fp16(x * factor) * weight * gate)) and
+// the normalised rows are also quantized (quantizeActivation over the
+// flattened [T][Hv*dv] rows: a head's row is dv / 32 whole groups), the
+// bits of the standalone gated_rms_norm_tile<true, true>.
+template <int DK, int CW, int NW, bool QK16, int CG = 1, bool NORM = false, bool ACTQ = false>
 __global__ __launch_bounds__(64 * NW * CG) void delta_recurrent_kernel(
     const void *__restrict__ qp, const void *__restrict__ kp,
     const half_t *__restrict__ v, const float *__restrict__ beta,
     const float *__restrict__ decay, float *__restrict__ state,
     half_t *__restrict__ out, unsigned T, unsigned Hk, unsigned Hv,
-    unsigned DV, float eps, float qscale, const half_t *__restrict__ gate,
-    const float *__restrict__ nweight, float neps) {
+    unsigned DV, float eps, float qscale, const void *__restrict__ gate,
+    const float *__restrict__ nweight, float neps, int8_t *__restrict__ qout,
+    float *__restrict__ scales, unsigned *invalid) {
   constexpr int RG = 64 / CW;  // row groups per wave
   constexpr int NP = NW * RG;  // lanes (row parts) per column
   constexpr int RPL = DK / NP; // rows per lane
@@ -70,6 +76,7 @@ __global__ __launch_bounds__(64 * NW * CG) void delta_recurrent_kernel(
   static_assert(RPL % 4 == 0 && RPL * NP == DK, "rows per lane must be a multiple of 4");
   static_assert(UR % 4 == 0 && UR * UPL == RPL, "a lane holds whole units");
   static_assert(!NORM || CW == 64, "the fused norm's workgroup holds 64-column groups");
+  static_assert(!ACTQ || NORM, "the quantization follows the fused norm");
   const unsigned tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
   const unsigned cg = wave / NW, wv = wave % NW;
   const unsigned c = lane % CW, part = wv * RG + lane / CW;
@@ -85,11 +92,14 @@ __global__ __launch_bounds__(64 * NW * CG) void delta_recurrent_kernel(
   // them), the row factors, and the head's gate rows and the weight, staged
   // at the start (no register holds them across the token loop).
   constexpr int NX = NORM ? kRecNormMaxT : 1, NC = NORM ? CW * CG : 1;
-  __shared__ __attribute__((aligned(16))) half_t sX[NX][NC], sGate[NX][NC];
+  using GateT = typename std::conditional<ACTQ, float, half_t>::type;
+  __shared__ __attribute__((aligned(16))) half_t sX[NX][NC];
+  __shared__ __attribute__((aligned(16))) GateT sGate[NX][NC];
   __shared__ float sNF[NX], sW[NC];
   if constexpr (NORM) {
     for (unsigned i = tid; i < T * DV; i += kThreads)
-      sGate[i / DV][i % DV] = gate[(size_t)(i / DV) * vwidth + (size_t)h * DV + i % DV];
+      sGate[i / DV][i % DV] = static_cast<const GateT *>(
+          gate)[(size_t)(i / DV) * vwidth + (size_t)h * DV + i % DV];
     for (unsigned j = tid; j < DV; j += kThreads)
       sW[j] = nweight[j];
   }
@@ -251,10 +261,30 @@ __global__ __launch_bounds__(64 * NW * CG) void delta_recurrent_kernel(
       sNF[tid] = gated_norm_factor(sum, DV, neps);
     }
     __syncthreads();
-    for (unsigned i = tid; i < T * DV; i += kThreads) {
-      const unsigned t = i / DV, j = i % DV;
-      out[(size_t)t * vwidth + (size_t)h * DV + j] =
-          gated_norm_out((float)sX[t][j], sNF[t], sW[j], (float)sGate[t][j]);
+    if constexpr (ACTQ) {
+      // Chunks of eight: the four chunks of a 32-wide group are handled by
+      // four consecutive lanes (dv / 8 is a multiple of 4).
+      for (unsigned c8 = tid; c8 < T * (DV / 8); c8 += kThreads) {
+        const unsigned t = c8 / (DV / 8), j0 = c8 % (DV / 8) * 8;
+        const size_t base = (size_t)t * vwidth + (size_t)h * DV + j0;
+        float y[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          y[e] = mul32(gated_norm_scaled((float)sX[t][j0 + e], sNF[t], sW[j0 + e]),
+                       sGate[t][j0 + e]);
+        uint4_t o;
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          o[e] = (uint32_t)f2h(y[2 * e]) | ((uint32_t)f2h(y[2 * e + 1]) << 16);
+        *reinterpret_cast<uint4_t *>(out + base) = o;
+        quantize_chunk8(y, qout + base, scales + base / 32, invalid, (c8 & 3u) == 0);
+      }
+    } else {
+      for (unsigned i = tid; i < T * DV; i += kThreads) {
+        const unsigned t = i / DV, j = i % DV;
+        out[(size_t)t * vwidth + (size_t)h * DV + j] =
+            gated_norm_out((float)sX[t][j], sNF[t], sW[j], (float)sGate[t][j]);
+      }
     }
   }
 }
@@ -339,18 +369,21 @@ struct RecArgs {
   float *state;
   uint16_t *out;
   float eps, qscale;
-  const uint16_t *gate = nullptr;
+  const void *gate = nullptr;
   const float *nweight = nullptr;
   float neps = 0.0f;
+  int8_t *qout = nullptr;
+  float *scales = nullptr;
+  unsigned *invalid = nullptr;
 };
 
-template <int DK, int CW, int NW, bool QK16, int CG = 1, bool NORM = false>
+template <int DK, int CW, int NW, bool QK16, int CG = 1, bool NORM = false, bool ACTQ = false>
 hipError_t launch_rec(const RecArgs &a, const DeltaShape &s, hipStream_t stream) {
-  hipLaunchKernelGGL((delta_recurrent_kernel<DK, CW, NW, QK16, CG, NORM>),
+  hipLaunchKernelGGL((delta_recurrent_kernel<DK, CW, NW, QK16, CG, NORM, ACTQ>),
                      dim3(s.Hv * (s.Dv / (CW * CG))), dim3(64 * NW * CG), 0, stream, a.q, a.k,
                      reinterpret_cast<const half_t *>(a.v), a.beta, a.decay, a.state,
                      reinterpret_cast<half_t *>(a.out), s.T, s.Hk, s.Hv, s.Dv, a.eps, a.qscale,
-                     reinterpret_cast<const half_t *>(a.gate), a.nweight, a.neps);
+                     a.gate, a.nweight, a.neps, a.qout, a.scales, a.invalid);
   return hipGetLastError();
 }
 
@@ -405,6 +438,20 @@ hipError_t launch_delta_recurrent_gated_norm(const uint16_t *q, const uint16_t *
                       : launch_rec<64, 64, 4, true, 2, true>(a, s, stream);
   return s.Dv == 64 ? launch_rec<128, 64, 4, true, 1, true>(a, s, stream)
                     : launch_rec<128, 64, 4, true, 2, true>(a, s, stream);
+}
+
+hipError_t launch_delta_recurrent_gated_norm_quantize(
+    const uint16_t *q, const uint16_t *k, const uint16_t *v, const float *beta,
+    const float *decay, float *state, const float *gate, const float *nweight, uint16_t *out,
+    int8_t *qout, float *scales, unsigned *invalid, float eps, float qscale, float neps,
+    const DeltaShape &s, hipStream_t stream) {
+  RecArgs a{q, k, v, beta, decay, state, out, eps, qscale, gate, nweight, neps,
+            qout, scales, invalid};
+  if (s.Dk == 64)
+    return s.Dv == 64 ? launch_rec<64, 64, 4, true, 1, true, true>(a, s, stream)
+                      : launch_rec<64, 64, 4, true, 2, true, true>(a, s, stream);
+  return s.Dv == 64 ? launch_rec<128, 64, 4, true, 1, true, true>(a, s, stream)
+                    : launch_rec<128, 64, 4, true, 2, true, true>(a, s, stream);
 }
 
 bool delta_recurrent_supported(const DeltaShape &s) {

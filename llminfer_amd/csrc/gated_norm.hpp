@@ -77,4 +77,45 @@ __device__ __forceinline__ uint4_t gated_norm_out8(uint4_t x, uint4_t gv, float 
   return o;
 }
 
+// quantizeActivation's expressions for the fp16 rounding of eight fp32
+// values y, chunk (lane & 3) of a 32-wide group held by four consecutive
+// lanes, all four active: scale = max|x| / 127 over the group (1 for an
+// all-zero or non-finite group), q = rint(clamp(x / scale, +-127)) (zeros
+// for a non-finite group), written as 8 bytes at q; the group's first lane
+// (first) writes *scale and raises *invalid for a non-finite group.
+__device__ __forceinline__ void quantize_chunk8(const float *y, int8_t *q, float *scale,
+                                                unsigned *invalid, bool first) {
+  float x[8], max_abs = 0.0f;
+  bool finite = true;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    x[e] = h2f(f2h(y[e]));
+    finite = finite && __builtin_isfinite(x[e]);
+    max_abs = fmaxf(max_abs, fabsf(x[e]));
+  }
+#pragma unroll
+  for (int m = 1; m < 4; m *= 2) {
+    max_abs = fmaxf(max_abs, __shfl_xor(max_abs, m, 4));
+    finite = __shfl_xor((int)finite, m, 4) && finite;
+  }
+  const float qs = finite && max_abs > 0.0f ? __fdiv_rn(max_abs, 127.0f) : 1.0f;
+  uint32_t words[2] = {0u, 0u};
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    int r = 0;
+    if (finite) {
+      const float v = fminf(fmaxf(__fdiv_rn(x[e], qs), -127.0f), 127.0f);
+      r = (int)__builtin_rintf(v);
+    }
+    words[e / 4] |= ((uint32_t)r & 0xFFu) << (8 * (e % 4));
+  }
+  reinterpret_cast<uint32_t *>(q)[0] = words[0];
+  reinterpret_cast<uint32_t *>(q)[1] = words[1];
+  if (first) {
+    *scale = qs;
+    if (!finite && invalid)
+      atomicOr(invalid, 1u);
+  }
+}
+
 } // namespace llmi

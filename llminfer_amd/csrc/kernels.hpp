@@ -121,6 +121,13 @@ hipError_t launch_delta_recurrent_gated_norm(const uint16_t *q, const uint16_t *
                                              uint16_t *out, float eps, float qscale,
                                              float neps, const DeltaShape &s,
                                              hipStream_t stream);
+// The same with the fp32 activated gate, the normalised rows also quantized
+// (32-wide groups of the flattened rows) into qout, scales and *invalid.
+hipError_t launch_delta_recurrent_gated_norm_quantize(
+    const uint16_t *q, const uint16_t *k, const uint16_t *v, const float *beta,
+    const float *decay, float *state, const float *gate, const float *nweight, uint16_t *out,
+    int8_t *qout, float *scales, unsigned *invalid, float eps, float qscale, float neps,
+    const DeltaShape &s, hipStream_t stream);
 // Whether the chunked form's norm scan grid fits on the device at once (its
 // per-head arrival wait needs every workgroup resident).
 bool delta_chunked_norm_resident(const DeltaShape &s);

@@ -42,7 +42,7 @@ enum class Launch : uint8_t {
   Embedding, EmbeddingW8, Quantize, LinearW8, LinearF16, RmsNorm, GatedRmsNorm,
   GatedRmsNormActivated, L2Norm, Elementwise, SigmoidMul, PartialRope, CausalConv, DeltaGates,
   DeltaUpdate, KvAppend, CausalGqa, CopyView, AddNormQuantize, AddNormLinear, L2DeltaUpdate,
-  GatedNormQuantize, KvAppendGqa, GatedAttention
+  GatedNormQuantize, KvAppendGqa, GatedAttention, L2DeltaNormQuantize
 };
 
 // One plan record of a launch that serves several ops.
@@ -55,7 +55,7 @@ struct Rec {
 struct Dispatch {
   Launch launch;
   ElementwiseKind elementwise = ElementwiseKind::Add;
-  Ref buf[9];
+  Ref buf[12];
   uint64_t workspaceBytes = 0;
   union {
     EmbedParams embed;
@@ -79,7 +79,9 @@ struct Dispatch {
   std::vector<const char *> kernels;
   std::vector<size_t> ops; // a launch serving several ops: a record for each
   std::vector<Rec> recs;   // ... with their epilogues (replaces ops when set)
-  float epsilon = 0.0f, scale = 0.0f; // L2DeltaUpdate: the q / k norms
+  // L2DeltaUpdate: the q / k norms; L2DeltaNormQuantize: also the gated
+  // norm's epsilon
+  float epsilon = 0.0f, scale = 0.0f, normEpsilon = 0.0f;
   // GatedAttention: the rotation of both normRopes, and whether the gate
   // values are already activated
   unsigned rotary = 0;
@@ -279,6 +281,7 @@ private:
   std::vector<std::array<int64_t, 6>> gated_;
   std::vector<char> inGated_; // launched by a gated block's call; its outputs are never stored
   void prepare_l2_delta();
+  bool merge_delta_norm(Dispatch &u, const Dispatch &n) const;
   void prepare_kv_decode();
   void prepare_conv_silu();
   void prepare_gated_attention();
@@ -555,9 +558,79 @@ void Lowering::prepare_l2_delta() {
       continue;
     l2Delta_[u] = {qo, ko};
     skip_[qo] = skip_[ko] = 1;
-    for (uint32_t x : {qn.inputs[0], kn.inputs[0]})
-      lastUse_[root_[x]] = std::max(lastUse_[root_[x]], u);
+    // With the gated norm of the update's output and its quantization right
+    // after, the three may launch as one (merge_delta_norm), which writes
+    // the norm's outputs while other workgroups still read the update's
+    // operands: those then stay live until the quantization.
+    size_t until = u;
+    if (u + 2 < g_.op_count && op(u + 1).kind == LLMI_GRAPH_GATED_RMS_NORM &&
+        op(u + 1).inputs[0] == o.outputs[0] &&
+        op(u + 2).kind == LLMI_GRAPH_QUANTIZE_ACTIVATION &&
+        op(u + 2).inputs[0] == op(u + 1).outputs[0])
+      until = u + 2;
+    for (uint32_t x : {qn.inputs[0], kn.inputs[0], o.inputs[2], o.inputs[3], o.inputs[4]})
+      lastUse_[root_[x]] = std::max(lastUse_[root_[x]], until);
   }
+}
+
+// A one-row L2DeltaUpdate launch (u) and the activated gated norm +
+// quantization launch right after it (n) that reads its output, merged
+// into one (llmi_hip_l2_norm_delta_gated_norm_activated_quantize, the same
+// bits; the update's output is never stored): taken when nothing else reads
+// that output, at the shapes of the one-workgroup-per-head kernel, and when
+// no output of the merged launch overlaps what it reads or another output.
+// Every op keeps its record.
+bool Lowering::merge_delta_norm(Dispatch &u, const Dispatch &n) const {
+  if (u.launch != Launch::L2DeltaUpdate || n.launch != Launch::GatedNormQuantize ||
+      u.ops.size() != 3 || n.recs.size() != 2)
+    return false;
+  const GraphDeltaParams &p = u.p.delta;
+  const RowParams &r = n.p.row;
+  const uint32_t y = op(u.ops[2]).outputs[0];
+  if (op(n.recs[0].op).inputs[0] != y || uses_[y] != 1 ||
+      value(y).kind != LLMI_GRAPH_RESULT || p.tokens > kRecNormMaxT ||
+      (p.keyDim != 64 && p.keyDim != 128) || (p.valueDim != 64 && p.valueDim != 128) ||
+      r.rows != p.tokens * p.valueHeads || r.width != p.valueDim)
+    return false;
+  struct Range {
+    Ref r;
+    uint64_t bytes;
+  };
+  auto overlap = [](const Range &a, const Range &b) {
+    return a.r.space == b.r.space && a.r.index == b.r.index && a.r.space != Space::None &&
+           a.r.offset < b.r.offset + b.bytes && b.r.offset < a.r.offset + a.bytes;
+  };
+  const uint64_t qk = 2ull * p.tokens * p.keyHeads * p.keyDim,
+                 nv = (uint64_t)p.tokens * p.valueHeads * p.valueDim,
+                 gates = 4ull * p.tokens * p.valueHeads;
+  const Range reads[] = {{u.buf[0], qk},     {u.buf[1], qk},      {u.buf[2], 2 * nv},
+                         {u.buf[3], gates},  {u.buf[4], gates},   {n.buf[1], 4 * nv},
+                         {n.buf[2], 4ull * p.valueDim}};
+  const Range writes[] = {{n.buf[3], 2 * nv}, {n.buf[4], nv}, {n.buf[5], nv / 8},
+                          {n.buf[6], 4}};
+  for (size_t a = 0; a < 4; ++a) {
+    for (const Range &x : reads)
+      if (overlap(writes[a], x))
+        return false;
+    for (size_t b = a + 1; b < 4; ++b)
+      if (overlap(writes[a], writes[b]))
+        return false;
+  }
+  u.launch = Launch::L2DeltaNormQuantize;
+  // q, k, v, beta, decay and state stay; the update's output gives way to
+  // the invalid flag, then the gate, the weight and the norm's outputs.
+  u.buf[6] = n.buf[6];
+  for (int k = 0; k < 5; ++k)
+    u.buf[7 + k] = n.buf[1 + k];
+  u.normEpsilon = r.epsilon;
+  u.kernels = {"deltaRecurrentNormQuantize"};
+  u.recs.clear();
+  for (size_t o : u.ops)
+    u.recs.push_back({o, nullptr, 0});
+  for (const Rec &x : n.recs)
+    u.recs.push_back(x);
+  u.ops.clear();
+  return true;
 }
 
 // CausalConv1d -> SiLU (the convolution's only consumer, the next op): the
@@ -784,6 +857,10 @@ void Lowering::merge_norm_linears() {
         m.buf[6] = qd.buf[3];
         m.kernels = {"gatedRmsNormQuantize"};
         m.recs = {{d.opIndex, nullptr, 0}, {qd.opIndex, nullptr, 0}};
+        if (!out.empty() && merge_delta_norm(out.back(), m)) {
+          ++i;
+          continue;
+        }
         out.push_back(std::move(m));
         ++i;
         continue;
@@ -1405,8 +1482,8 @@ void *resolve(const Bases &b, const Ref &r) {
 }
 
 int run_dispatch(const Dispatch &d, const Bases &b, hipStream_t stream) {
-  void *x[9];
-  for (int i = 0; i < 9; ++i)
+  void *x[12];
+  for (int i = 0; i < 12; ++i)
     x[i] = resolve(b, d.buf[i]);
   auto u16 = [&](int i) { return static_cast<uint16_t *>(x[i]); };
   auto f32 = [&](int i) { return static_cast<float *>(x[i]); };
@@ -1477,6 +1554,10 @@ int run_dispatch(const Dispatch &d, const Bases &b, hipStream_t stream) {
   case Launch::L2DeltaUpdate:
     return llmi_hip_l2_norm_delta_update(u16(0), u16(1), u16(2), f32(3), f32(4), f32(5), u16(6),
                                          d.p.delta, d.epsilon, d.scale, nullptr, 0, stream);
+  case Launch::L2DeltaNormQuantize:
+    return llmi_hip_l2_norm_delta_gated_norm_activated_quantize(
+        u16(0), u16(1), u16(2), f32(3), f32(4), f32(5), f32(7), f32(8), u16(9), (int8_t *)x[10],
+        f32(11), (uint32_t *)x[6], d.p.delta, d.epsilon, d.scale, d.normEpsilon, stream);
   case Launch::AddNormQuantize:
     return llmi_hip_add_rms_norm_quantize(u16(0), u16(1), u16(2), f32(3), (int8_t *)x[4],
                                           f32(5), (uint32_t *)x[6], d.p.row, stream);

@@ -774,6 +774,50 @@ def l2_norm_delta_gated_norm(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     return out
 
 
+def bind_l2_norm_delta_gated_norm_activated_quantize(
+        q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, beta: torch.Tensor,
+        decay: torch.Tensor, state: torch.Tensor, gate: torch.Tensor, norm_weight: torch.Tensor,
+        out: torch.Tensor, quantized: torch.Tensor, scales: torch.Tensor,
+        invalid: torch.Tensor | None = None, epsilon: float = 1e-6,
+        q_scale: float | None = None, norm_epsilon: float = 1e-6) -> "Bound":
+    """The W8A8 DeltaNet tail in one call: L2Norm(q), L2Norm(k), DeltaUpdate,
+    GatedRmsNorm with the fp32 activated gate (gatedRmsNormActivated) and the
+    QuantizeActivation of its rows (Qwen35ModelBuilder.cpp:155-166, then the
+    out projection's prepare): operands as bind_l2_norm_delta_update, gate
+    fp32 like v, norm_weight fp32 [dv]; out the normalised rows (fp16),
+    quantized int8 [T*Hv*dv], scales fp32 [T*Hv*dv/32]. T <= 32."""
+    _require(gate, torch.float32, "gate")
+    _require(norm_weight, torch.float32, "norm_weight")
+    _require(quantized, torch.int8, "quantized")
+    _require(scales, torch.float32, "scales")
+    if invalid is not None:
+        _require(invalid, torch.int32, "invalid")
+    hv, dk, dv = state.shape
+    if gate.shape != v.shape or norm_weight.numel() != dv or quantized.numel() != v.numel() or \
+            scales.numel() * 32 != v.numel():
+        raise ValueError("gate must match v, norm_weight have dv elements, quantized and "
+                         "scales cover v's elements in 32-wide groups")
+    inner = bind_l2_norm_delta_update(q, k, v, beta, decay, state, out, epsilon, q_scale)
+    a = inner._args
+    lib = _lib.load()
+    args = a[:6] + (_ptr(gate), _ptr(norm_weight), a[6], _ptr(quantized), _ptr(scales),
+                    _ptr(invalid), a[7], a[8], a[9], norm_epsilon, a[12])
+    return Bound(lib.llmi_hip_l2_norm_delta_gated_norm_activated_quantize, args,
+                 inner.what + "+gatedRmsNormQuantize")
+
+
+def l2_norm_delta_gated_norm_activated_quantize(q, k, v, beta, decay, state, gate, norm_weight,
+                                                out, quantized, scales, invalid=None,
+                                                epsilon: float = 1e-6,
+                                                q_scale: float | None = None,
+                                                norm_epsilon: float = 1e-6) -> None:
+    """bind_l2_norm_delta_gated_norm_activated_quantize, called once."""
+    bind_l2_norm_delta_gated_norm_activated_quantize(q, k, v, beta, decay, state, gate,
+                                                     norm_weight, out, quantized, scales,
+                                                     invalid, epsilon, q_scale,
+                                                     norm_epsilon)()
+
+
 class Bound:
     """One C-ABI call with every argument converted once, for hot loops.
 

@@ -296,6 +296,26 @@ def test_l2_norm_delta_gated_norm_rejects_shapes_without_kernel():
              None) == _lib.INVALID_ARGUMENT
 
 
+def test_delta_norm_quantize_rejects_shapes_without_kernel():
+    """The W8A8 DeltaNet tail in one call has only the one-workgroup-per-head
+    kernel: T 33, dk 96 and dv 48 are UNSUPPORTED before any launch, and so
+    are an out or quantized row that is not 16-byte aligned; a contract
+    violation (Hv % Hk, a null buffer) stays INVALID_ARGUMENT."""
+    lib = _lib.load()
+    f = lib.llmi_hip_l2_norm_delta_gated_norm_activated_quantize
+    ptrs = [16] * 12
+    call = lambda p, ptrs=ptrs: f(*ptrs, p, 1e-6, 0.1, 1e-6, None)
+    for T, dk, dv in ((33, 128, 128), (4, 96, 128), (5, 128, 48)):
+        assert call(_lib.GraphDeltaParams(T, 2, dk, 4, dv)) == _lib.UNSUPPORTED, (T, dk, dv)
+    ok = _lib.GraphDeltaParams(1, 16, 128, 32, 128)
+    for at in (8, 9):  # out, quantized
+        assert call(ok, [18 if i == at else 16 for i in range(12)]) == _lib.UNSUPPORTED, at
+    assert call(_lib.GraphDeltaParams(1, 16, 128, 24, 128)) == _lib.INVALID_ARGUMENT
+    for at in range(11):  # every buffer but the optional invalid flag
+        assert call(ok, [None if i == at else 16 for i in range(12)]) == \
+            _lib.INVALID_ARGUMENT, at
+
+
 def test_gated_norm_status_host_paths():
     """The status call of the fused chain: the recurrent form (T <= 32) has
     no arrival wait and reports OK without touching the device; the chunked

@@ -84,6 +84,61 @@ def test_fused_repeats_and_reuses_counters(gpu):
     assert torch.equal(outs[0], outs[1]) and torch.equal(outs[1], outs[2])
 
 
+RECURRENT = [s for s in SHAPES if s[0] <= 32]
+
+
+@pytest.mark.parametrize("special", [False, True])
+@pytest.mark.parametrize("shape", RECURRENT)
+def test_activated_quantize_equals_chain(gpu, shape, special):
+    """The W8A8 model's DeltaNet tail in one call
+    (llmi_hip_l2_norm_delta_gated_norm_activated_quantize) against its
+    launches one by one -- llmi_hip_l2_norm_delta_update, then
+    llmi_hip_gated_rms_norm_activated_quantize over rows of dv (fp32 gate;
+    bit-exact with gated_rms_norm + quantize_activation, test_w8a8_gpu.py)
+    --: the same state, normalised rows, int8 rows, scales and invalid flag
+    bit for bit (special: an infinite gate value, whose group is reported
+    and zeroed)."""
+    T, hk, dk, hv, dv = shape
+    print(f"l2norm+delta+gatednorm+quantize shape {shape} special {special}", flush=True)
+    seed = 190 + T + dv
+    d = oracle.make_delta_inputs(seed, T, hk, dk, hv, dv, 0.1)
+    q16 = oracle.normal_f16(seed, 21, (T, hk * dk))
+    k16 = oracle.normal_f16(seed, 22, (T, hk * dk))
+    g = oracle.normal_f32(seed, 23, (T, hv * dv), 0.0, 1.5)
+    if special:
+        g[T // 2, (hv * dv) // 3] = np.inf
+    w = oracle.normal_f32(seed, 24, (dv,), 1.0, 0.2)
+    f = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(gpu)
+    q, k, v = (u16_to_torch(a, gpu) for a in (q16, k16, d.v))
+    beta, decay, gate, wt = f(d.beta), f(d.decay), f(g), f(w)
+    n = T * hv * dv
+    # one by one
+    s_ref = f(d.state)
+    x = ops.l2_norm_delta_update(q, k, v, beta, decay, s_ref)
+    ref = torch.empty_like(x)
+    q_ref = torch.empty(n, dtype=torch.int8, device=gpu)
+    c_ref = torch.empty(n // 32, dtype=torch.float32, device=gpu)
+    i_ref = torch.zeros(1, dtype=torch.int32, device=gpu)
+    ops.gated_rms_norm_activated_quantize(x.view(T * hv, dv), gate.view(T * hv, dv), wt,
+                                          ref.view(T * hv, dv), q_ref, c_ref, i_ref)
+    # fused
+    s_fused = f(d.state)
+    out = torch.empty_like(x)
+    q_got, c_got = torch.zeros_like(q_ref), torch.zeros_like(c_ref)
+    i_got = torch.zeros(1, dtype=torch.int32, device=gpu)
+    ops.l2_norm_delta_gated_norm_activated_quantize(q, k, v, beta, decay, s_fused, gate, wt,
+                                                    out, q_got, c_got, i_got)
+    torch.cuda.synchronize()
+    assert torch.equal(s_ref, s_fused), "states differ from the unfused chain"
+    got, want = torch_to_u16(out), torch_to_u16(ref)
+    bad = np.flatnonzero(got.reshape(-1) != want.reshape(-1))
+    assert bad.size == 0, f"{bad.size} outputs differ from the unfused chain, first at {bad[:4]}"
+    assert torch.equal(q_got, q_ref)
+    assert np.array_equal(c_got.cpu().numpy().view(np.uint32),
+                          c_ref.cpu().numpy().view(np.uint32))
+    assert int(i_got.item()) == int(i_ref.item()) == (1 if special else 0)
+
+
 def _cfg4_chain_inputs(seed):
     """cfg4's DeltaNet operands at the fused call's boundary: fp16 q/k rows
     (the L2Norms run inside the call), v, beta, linear decay, zero state,

@@ -113,10 +113,13 @@ def test_qwen35_4b_lowers_with_the_hot_kernels():
     # the rest: the DeltaNet and attention out projections, the MLP's down,
     # the head
     assert kinds["linearW8A8Gemv"] == 24 + 8 + 32 + 1
-    # each DeltaNet layer's gated norm with the quantization of its output
-    assert kinds["gatedRmsNormQuantize"] == 24 * 2 and kinds["quantizeActivation"] == 40
-    # the q and k L2Norms run inside the one-row DeltaUpdate's loads
-    # (llmi_hip_l2_norm_delta_update), recorded under its kernel
+    # each DeltaNet layer's tail in one call
+    # (llmi_hip_l2_norm_delta_gated_norm_activated_quantize): the q and k
+    # L2Norms run inside the one-row DeltaUpdate's loads, and the gated norm
+    # of its output and the quantization of the norm's rows at its end; the
+    # five ops recorded under its kernel
+    assert kinds["deltaRecurrentNormQuantize"] == 24 * 5
+    assert kinds["gatedRmsNormQuantize"] == 0 and kinds["quantizeActivation"] == 40
     # each attention layer's block -- the q and k RMSNorms and PartialRopes,
     # KvAppend, CausalGqa and the SigmoidMul with the gate the q projection
     # activated -- in one call (llmi_hip_gated_attention_activated), its
@@ -124,14 +127,13 @@ def test_qwen35_4b_lowers_with_the_hot_kernels():
     assert kinds["gqaDecodeGated"] == kinds["gqaDecodeMergeGated"] == 8 * 7
     assert not {"gqaDecodeSplitK", "kvAppend", "normRopeTile", "partialRopeTile",
                 "copyHalfView", "multiplyF16"} & set(kinds)
-    assert kinds["deltaRecurrent"] == 24 * 3
-    assert kinds["l2NormF32"] == 0
+    assert kinds["deltaRecurrent"] == 0 and kinds["l2NormF32"] == 0
     # each DeltaNet layer's convolution with its SiLU
     assert kinds["causalConv"] == 24 * 2 and kinds["siluF16"] == 0
     # a launch that serves several ops (the Adds, norms, quantizations,
     # projections, SiLUs and attention blocks above) has a record for each:
-    # 764 records, 259 launches
-    assert len(decode.dispatches) == 764 and decode.launches == 259
+    # 764 records, 235 launches
+    assert len(decode.dispatches) == 764 and decode.launches == 235
     assert kinds["residualAdd"] == 0
     assert "quantizeActivation" in kinds     # the others (after GQA / gated norms, SwiGLU)
     indices = [d["op_index"] for d in decode.dispatches]
@@ -146,6 +148,9 @@ def test_qwen35_4b_lowers_with_the_hot_kernels():
     assert kinds["rmsNormQuantize"] == 2 + 2 and kinds["addRmsNormQuantize"] == 63 * 3
     assert "addRmsNormLinearW8A8" not in kinds and kinds["linearW8A8Gemv"] == 1
     assert kinds["l2NormF32"] == 48
+    # several rows: the chunked DeltaUpdate, then the gated norm with its
+    # quantization
+    assert kinds["gatedRmsNormQuantize"] == 24 * 2
     # the MLP down projection and the head: at most a few hundred MB of scratch
     assert prefill.scratch_bytes < 512 << 20
 

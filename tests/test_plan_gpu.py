@@ -168,8 +168,9 @@ def test_small_plan_on_the_hot_kernels(gpu):
     for a, b in zip(session.states, states):
         assert _same_state(a, b)
     kernels = {d["kernel"] for d in session.plan(1, "last").dispatches}
-    # the one-row attention block in one call (llmi_hip_gated_attention_activated)
-    assert {"gqaDecodeGated", "deltaRecurrent", "linearW8A8Gemv"} <= kernels
+    # the one-row attention block in one call (llmi_hip_gated_attention_activated),
+    # and the DeltaNet tail (llmi_hip_l2_norm_delta_gated_norm_activated_quantize)
+    assert {"gqaDecodeGated", "deltaRecurrentNormQuantize", "linearW8A8Gemv"} <= kernels
     assert "gqaDecodeSplitK" not in kernels
     want, _ = run_oracle(c, weights, chunks, capacity=256)
     for p, w_ in zip(plan_logits, want):
@@ -229,10 +230,13 @@ def test_qwen35_4b_decode_step(gpu):
     for a, b in zip(session.states, states):
         assert _same_state(a, b)
     kinds = [d["kernel"] for d in r.dispatches]
-    # deltaRecurrent: the update and its fused q / k L2Norms, a record each
+    # deltaRecurrentNormQuantize: the update, its fused q / k L2Norms, the
+    # gated norm of its output and the quantization of the norm's rows, a
+    # record each
     # gqaDecodeGated: the attention block's seven ops (q / k RMSNorm and
     # PartialRope, KvAppend, CausalGqa, SigmoidMul) in one call, a record each
-    assert kinds.count("gqaDecodeGated") == 8 * 7 and kinds.count("deltaRecurrent") == 24 * 3
+    assert kinds.count("gqaDecodeGated") == 8 * 7
+    assert kinds.count("deltaRecurrentNormQuantize") == 24 * 5
 
 
 def test_nonfinite_activation_invalidates_until_reset(gpu):
