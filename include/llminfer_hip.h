@@ -566,13 +566,21 @@ LLMI_HIP_API int llmi_hip_add_rms_norm_quantize(const uint16_t *a, const uint16_
                                                 RowParams p, void *stream);
 
 /* The buffers of one projection of llmi_hip_add_rms_norm_linear_w8a8: those
- * of an llmi_hip_linear_w8a8 call on the norm's quantized row. */
+ * of an llmi_hip_linear_w8a8 call on the norm's quantized row. With
+ * conv_weight set, the projection's fp16 row (no epilogue) is not stored:
+ * it passes through the one-token causalConv of a kernel-4 convolution
+ * with SiLU (causalConv with applySilu, Reference.metal:137-161, T = 1):
+ * output receives, bit for bit, what llmi_hip_causal_conv (silu on) of the
+ * projected row leaves there, and conv_history [columns][3] fp16 is
+ * updated in place as it updates it. */
 typedef struct llmi_hip_norm_projection {
   const int8_t *weight;          /* [columns][groups * 32], 16-byte aligned */
   const uint16_t *weight_scales; /* [columns][groups] fp16 */
   void *output;
   const void *aux;
   const float *bias;
+  const uint16_t *conv_weight;   /* NULL, or [columns][4] fp16 */
+  uint16_t *conv_history;        /* with conv_weight: [columns][3] fp16 */
 } llmi_hip_norm_projection;
 
 #define LLMI_HIP_NORM_LINEAR_MAX 4
@@ -592,10 +600,12 @@ typedef struct NormLinearParams {
  * llmi_hip_linear_w8a8; a LLMI_LINEAR_SILU_MUL multiplier (aux) computed
  * in the same call must be the previous projection's output, that
  * projection with no epilogue and the same columns, width <= 2560 (the two
- * are computed by the same lanes). At most 4096 workgroups of
- * 60 columns in all (one per CU runs best: 256 on MI355X). No output may
- * overlap a, b, sum_out, q, scales or another output: the projections run
- * concurrently with the norm of other workgroups. */
+ * are computed by the same lanes). A projection with a convolution
+ * (conv_weight) has no epilogue, computes all of its output row (first row
+ * 0, columns == output width) and is no SwiGLU multiplier. At most 4096
+ * workgroups of 60 columns in all (one per CU runs best: 256 on MI355X).
+ * No output may overlap a, b, sum_out, q, scales or another output: the
+ * projections run concurrently with the norm of other workgroups. */
 LLMI_HIP_API int llmi_hip_add_rms_norm_linear_w8a8(const uint16_t *a, const uint16_t *b,
                                                    uint16_t *sum_out, const float *weight,
                                                    int8_t *q, float *scales, uint32_t *invalid,

@@ -95,7 +95,8 @@ class LinearW8Params(C.Structure):
 
 class NormProjection(C.Structure):
     _fields_ = [("weight", C.c_void_p), ("weight_scales", C.c_void_p), ("output", C.c_void_p),
-                ("aux", C.c_void_p), ("bias", C.c_void_p)]
+                ("aux", C.c_void_p), ("bias", C.c_void_p), ("conv_weight", C.c_void_p),
+                ("conv_history", C.c_void_p)]
 
 
 class NormLinearParams(C.Structure):

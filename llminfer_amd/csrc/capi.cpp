@@ -462,12 +462,29 @@ int llmi_hip_add_rms_norm_linear_w8a8(const uint16_t *a, const uint16_t *b, uint
     if (l.epilogue == LLMI_LINEAR_DELTA_DECAY && (!x.aux || !x.bias))
       return fail(LLMI_HIP_INVALID_ARGUMENT,
                   "addRmsNormLinearW8A8: projection %u: the decay needs A_log (aux) and bias", k);
+    if (!x.conv_weight != !x.conv_history)
+      return fail(LLMI_HIP_INVALID_ARGUMENT,
+                  "addRmsNormLinearW8A8: projection %u: a convolution needs its weight and its "
+                  "history",
+                  k);
+    if (x.conv_weight && (l.epilogue != LLMI_LINEAR_NONE || l.firstRow != 0 ||
+                          l.columns != l.outputWidth))
+      return fail(LLMI_HIP_UNSUPPORTED,
+                  "addRmsNormLinearW8A8: projection %u: a convolution takes the whole row of a "
+                  "projection with no epilogue",
+                  k);
     proj[k] = {x.weight, x.weight_scales, x.output, x.aux, x.bias,
                W8Shape{l.outputWidth, l.firstRow, l.groups, l.rows, l.columns, l.epilogue,
                        l.epilogueBlock},
-               false};
-    if (mate)
+               false, x.conv_weight, x.conv_history};
+    if (mate) {
+      if (proj[k - 1].cw)
+        return fail(LLMI_HIP_UNSUPPORTED,
+                    "addRmsNormLinearW8A8: projection %u: a SwiGLU multiplier has no "
+                    "convolution",
+                    k);
       proj[k - 1].paired = true;
+    }
   }
   return launched(launch_add_norm_linear(a, b, sum_out, weight, q, scales, invalid, p.norm.width,
                                          p.norm.epsilon, proj, p.count,

@@ -35,7 +35,7 @@ __device__ __forceinline__ float mul32(float a, float b) { return opaque(a * b);
 // backend may fold the product or fma producing x into v_fma_mix*_f16 and
 // round once, and it decides that per instantiation.
 __device__ __forceinline__ _Float16 f16_of(float x) { return (_Float16)opaque(x); }
-__device__ __forceinline__ float round16(float x) { return opaque((float)(_Float16)x); }
+__device__ __forceinline__ float round16(float x) { return opaque((float)f16_of(x)); }
 
 // Correctly rounded float square root: taken in double and rounded once,
 // which is exact rounding for a float argument (HIP's __fsqrt_rn is the

@@ -247,6 +247,9 @@ struct NormLinearProj {
   const float *bias;
   W8Shape shape;
   bool paired; // the next projection is this one's SwiGLU partner
+  // the one-token kernel-4 convolution + SiLU the row passes through
+  const uint16_t *cw = nullptr;
+  uint16_t *ch = nullptr;
 };
 hipError_t launch_add_norm_linear(const uint16_t *a, const uint16_t *b, uint16_t *sum_out,
                                   const float *w, int8_t *q, float *scales, unsigned *invalid,

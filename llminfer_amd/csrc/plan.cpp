@@ -87,7 +87,9 @@ struct Dispatch {
   unsigned rotary = 0;
   float theta = 0.0f;
   bool activated = false;
-  Ref proj[kNormLinearMax][5]; // AddNormLinear: weight, scales, output, aux, bias
+  // AddNormLinear: weight, scales, output, aux, bias, and the convolution
+  // weight and history of a projection with the convolution epilogue
+  Ref proj[kNormLinearMax][7];
 };
 
 struct Fusion {
@@ -653,6 +655,25 @@ void Lowering::prepare_conv_silu() {
       continue;
     convSilu_[j] = (int64_t)j + 1;
     skip_[j + 1] = 1;
+    // In a one-row step the convolution may run as the epilogue of the
+    // projection whose row it reads, inside the norm + projections launch
+    // (merge_norm_linears): it writes its output while other workgroups
+    // still read the norm's operands and the first one writes the
+    // quantized row, so those stay live until the convolution.
+    const int64_t p = value(c.inputs[0]).defining_op;
+    if (g_.tokens != 1 || p < 0 || op(p).kind != LLMI_GRAPH_LINEAR_W8A8)
+      continue;
+    const int64_t qo = value(op(p).inputs[0]).defining_op;
+    if (qo < 1 || normQuantize_[qo - 1] != qo)
+      continue;
+    std::vector<uint32_t> live(op(qo - 1).inputs, op(qo - 1).inputs + op(qo - 1).input_count);
+    live.insert(live.end(), op(qo).outputs, op(qo).outputs + op(qo).output_count);
+    if (normAdd_[qo - 1] >= 0) {
+      const auto &a = op(normAdd_[qo - 1]);
+      live.insert(live.end(), a.inputs, a.inputs + a.input_count);
+    }
+    for (uint32_t x : live)
+      lastUse_[root_[x]] = std::max(lastUse_[root_[x]], j);
   }
 }
 
@@ -937,8 +958,46 @@ void Lowering::merge_norm_linears() {
       m.proj[k][3] = l.buf[5];
       m.proj[k][4] = l.buf[6];
     }
+    // The one-token convolution with its SiLU right after, over the whole
+    // row of a projection that nothing else reads (no epilogue, no SwiGLU
+    // multiplier): that projection's convolution epilogue, which stores
+    // the convolution's output instead of the row; the convolution's
+    // records join.
+    size_t taken = np.count;
+    if (i + 1 + np.count < ds.size() && ds[i + 1 + np.count].launch == Launch::CausalConv) {
+      const Dispatch &c = ds[i + 1 + np.count];
+      const ConvParams &cp = c.p.conv;
+      for (unsigned k = 0; k < np.count; ++k) {
+        const LinearW8Params &lp = np.linear[k];
+        const uint32_t y = op(ds[i + 1 + k].opIndex).outputs[0];
+        const bool multiplier = k + 1 < np.count &&
+                                np.linear[k + 1].epilogue == LLMI_LINEAR_SILU_MUL;
+        if (cp.tokens != 1 || cp.kernelSize != 4 || !cp.applySilu ||
+            lp.epilogue != LLMI_LINEAR_NONE || lp.firstRow != 0 ||
+            lp.columns != lp.outputWidth || cp.channels != lp.columns || multiplier ||
+            root_[op(c.opIndex).inputs[0]] != root_[y] || uses_[root_[y]] != 1 ||
+            c.buf[0].space != m.proj[k][2].space || c.buf[0].index != m.proj[k][2].index ||
+            c.buf[0].offset != m.proj[k][2].offset)
+          continue;
+        const Range o{c.buf[3], 2ull * lp.columns};
+        bool clash = false;
+        for (const Range &r : reads)
+          clash = clash || overlap(o, r);
+        if (clash)
+          break;
+        m.proj[k][2] = c.buf[3];
+        m.proj[k][5] = c.buf[1];
+        m.proj[k][6] = c.buf[2];
+        if (c.recs.empty())
+          m.recs.push_back({c.opIndex, nullptr, 0});
+        for (const Rec &x : c.recs)
+          m.recs.push_back(x);
+        ++taken;
+        break;
+      }
+    }
     out.push_back(std::move(m));
-    i += np.count;
+    i += taken;
   }
   ds.swap(out);
 }
@@ -1567,7 +1626,9 @@ int run_dispatch(const Dispatch &d, const Bases &b, hipStream_t stream) {
       proj[k] = {static_cast<const int8_t *>(resolve(b, d.proj[k][0])),
                  static_cast<const uint16_t *>(resolve(b, d.proj[k][1])),
                  resolve(b, d.proj[k][2]), resolve(b, d.proj[k][3]),
-                 static_cast<const float *>(resolve(b, d.proj[k][4]))};
+                 static_cast<const float *>(resolve(b, d.proj[k][4])),
+                 static_cast<const uint16_t *>(resolve(b, d.proj[k][5])),
+                 static_cast<uint16_t *>(resolve(b, d.proj[k][6]))};
     return llmi_hip_add_rms_norm_linear_w8a8(u16(0), u16(1), u16(2), f32(3), (int8_t *)x[4],
                                              f32(5), (uint32_t *)x[6], proj, d.p.normLinear,
                                              stream);

@@ -634,7 +634,28 @@ struct NormLinearSeg {
   const void *aux;
   const float *bias;
   unsigned columns, outputWidth, firstRow, epilogue, block, wgs, paired;
+  const uint16_t *cw; // the one-token convolution + SiLU, or null
+  uint16_t *ch;
 };
+
+// causalConv with applySilu (Reference.metal:137-161) of one token for
+// channel c, whose input is the projection's fp32 sum: the input is its
+// fp16 rounding, the window the channel's three history values and the
+// input, the sum the product of the newest term followed by the fmas of
+// the older ones (causal_conv_k4's order), and the history shifts by one.
+__device__ __forceinline__ void store_conv_silu(uint16_t *out, const uint16_t *cw, uint16_t *ch,
+                                                unsigned c, float acc) {
+  const float x = round16(acc);
+  const uint16_t h0 = ch[3 * c], h1 = ch[3 * c + 1], h2 = ch[3 * c + 2];
+  float y = mul32(x, h2f(cw[4 * c + 3]));
+  y = __builtin_fmaf(h2f(h0), h2f(cw[4 * c]), y);
+  y = __builtin_fmaf(h2f(h1), h2f(cw[4 * c + 1]), y);
+  y = __builtin_fmaf(h2f(h2), h2f(cw[4 * c + 2]), y);
+  out[c] = silu16(round16(y));
+  ch[3 * c] = h1;
+  ch[3 * c + 1] = h2;
+  ch[3 * c + 2] = f2h(x);
+}
 
 struct NormLinearArgs {
   NormLinearSeg seg[kNormLinearMax];
@@ -766,7 +787,10 @@ __global__ __launch_bounds__(kNormLinearThreads) void norm_linear_kernel(
   }
   if (l == 0 && live) {
     const unsigned column = seg.firstRow + col;
-    store_linear(seg.out, seg.aux, seg.bias, column, column, seg.epilogue, seg.block, acc);
+    if (seg.cw)
+      store_conv_silu(static_cast<uint16_t *>(seg.out), seg.cw, seg.ch, column, acc);
+    else
+      store_linear(seg.out, seg.aux, seg.bias, column, column, seg.epilogue, seg.block, acc);
   }
 }
 
@@ -874,7 +898,8 @@ hipError_t launch_add_norm_linear(const uint16_t *a, const uint16_t *b, uint16_t
     const bool mate = k > 0 && proj[k - 1].paired;
     p.seg[k] = {x.w, x.ws, x.out, x.aux, x.bias, x.shape.columns, x.shape.outputWidth,
                 x.shape.firstRow, x.shape.epilogue, x.shape.block,
-                mate ? 0u : norm_linear_workgroups(x.shape.columns), x.paired ? 1u : 0u};
+                mate ? 0u : norm_linear_workgroups(x.shape.columns), x.paired ? 1u : 0u,
+                x.cw, x.ch};
     wgs += p.seg[k].wgs;
     paired = paired || x.paired;
   }

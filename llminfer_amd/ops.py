@@ -362,7 +362,10 @@ def bind_add_rms_norm_linear_w8a8(a: torch.Tensor, b: torch.Tensor | None,
     projections: up to 4 dicts with weight, weight_scales, out and optionally
     epilogue, block, aux, bias, first_row (as for linear_w8a8; a SwiGLU
     projection follows its multiplier's projection and takes its out as
-    aux); q, scales as for add_rms_norm_quantize or None."""
+    aux) and conv_weight [columns, 4], conv_history [columns, 3] (fp16: the
+    row then passes through the one-token causal_conv with SiLU, history
+    updated, as causal_conv leaves it); q, scales as for
+    add_rms_norm_quantize or None."""
     _require(a, torch.float16, "a")
     if b is not None:
         _require(b, torch.float16, "b")
@@ -397,7 +400,16 @@ def bind_add_rms_norm_linear_w8a8(a: torch.Tensor, b: torch.Tensor | None,
                 or out.dim() != 2 or out.shape[0] != rows:
             raise ValueError(f"projection {k}: weight, weight_scales and out shapes disagree")
         aux, bias = x.get("aux"), x.get("bias")
-        bufs[k] = _lib.NormProjection(_ptr(w), _ptr(ws), _ptr(out), _ptr(aux), _ptr(bias))
+        cw, ch = x.get("conv_weight"), x.get("conv_history")
+        if cw is not None:
+            _require(cw, torch.float16, "conv_weight")
+            _require(ch, torch.float16, "conv_history")
+            if tuple(cw.shape) != (columns, 4) or tuple(ch.shape) != (columns, 3) or \
+                    tuple(out.shape) != (1, columns):
+                raise ValueError(f"projection {k}: conv_weight [columns, 4], conv_history "
+                                 "[columns, 3] and out [1, columns] disagree")
+        bufs[k] = _lib.NormProjection(_ptr(w), _ptr(ws), _ptr(out), _ptr(aux), _ptr(bias),
+                                      _ptr(cw), _ptr(ch))
         p.linear[k] = _lib.LinearW8Params(out.shape[1], x.get("first_row", 0), groups, rows,
                                           columns, epilogue, x.get("block", 0))
     bound = Bound(_lib.load().llmi_hip_add_rms_norm_linear_w8a8,

@@ -389,9 +389,11 @@ def test_norm_linear_abi():
     it takes (one row of at most 4096, 1-4 projections of that row's
     groups, at most 4096 workgroups of 60 columns) and a SwiGLU multiplier
     computed in the same call only as the previous projection's output (the
-    pair computed by the same lanes), all rejected before any launch."""
+    pair computed by the same lanes), a convolution epilogue only on the
+    whole row of a projection with no epilogue that is no multiplier, all
+    rejected before any launch."""
     from llminfer_amd import ops
-    assert C.sizeof(_lib.NormProjection) == 40
+    assert C.sizeof(_lib.NormProjection) == 56
     assert C.sizeof(_lib.NormLinearParams) == 12 + 4 + 4 * 28
     lib = _lib.load()
     a16 = 16  # a 16-byte-aligned stand-in pointer; nothing is launched
@@ -435,3 +437,17 @@ def test_norm_linear_abi():
     assert lib.llmi_hip_add_rms_norm_linear_w8a8(a16, None, None, a16, None, None, None,
                                                  C.addressof(bufs), p, None) == \
         _lib.INVALID_ARGUMENT
+    # the convolution epilogue: weight and history together, on the whole
+    # row of a projection with no epilogue that is no SwiGLU multiplier
+    call = lambda p: lib.llmi_hip_add_rms_norm_linear_w8a8(
+        a16, None, None, a16, None, None, None, C.addressof(bufs), p, None)
+    bufs[0] = _lib.NormProjection(a16, a16, 4096, None, None, a16, None)
+    assert call(params(2560, (64, 0))) == _lib.INVALID_ARGUMENT
+    bufs[0] = _lib.NormProjection(a16, a16, 4096, None, None, a16, 8192)
+    assert call(params(2560, (64, _lib.LINEAR_SILU))) == _lib.UNSUPPORTED
+    split = params(2560, (64, 0))
+    split.linear[0].firstRow = 32
+    split.linear[0].columns = 32
+    assert call(split) == _lib.UNSUPPORTED
+    bufs[1] = _lib.NormProjection(a16, a16, 12288, 4096, None)
+    assert call(params(2560, (64, 0), (64, _lib.LINEAR_SILU_MUL))) == _lib.UNSUPPORTED

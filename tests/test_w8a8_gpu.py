@@ -338,6 +338,58 @@ def test_add_rms_norm_linear_is_the_separate_ops(gpu, case, special):
                               o3[k].cpu().numpy().view(np.uint8)), f"projection {k}"
 
 
+@pytest.mark.parametrize("width,columns,second", [(2560, 8192, 4096), (1000, 300, 0),
+                                                  (4096, 65, 64)])
+def test_add_rms_norm_linear_conv_is_the_separate_ops(gpu, width, columns, second):
+    """A projection with the convolution epilogue equals linear_w8a8 of the
+    quantized row followed by causal_conv (one token, kernel 4, SiLU) of its
+    output, bit for bit: the convolution's output and its updated history,
+    twice in a row (the second call convolving over the first's history);
+    a projection beside it keeps its own output (second: its columns, 0
+    for none)."""
+    print(f"addRmsNormLinearW8A8 conv width={width} columns={columns} second={second}",
+          flush=True)
+    r = np.random.default_rng(width + columns)
+    groups = (width + 31) // 32
+    w = _dev((r.standard_normal(width) * 0.2).astype(np.float32), gpu)
+    wt, ws = _projection_weights(r, columns, groups, gpu)
+    cw = _u16_dev(_f16(r.standard_normal((columns, 4)) * 0.5), gpu)
+    hist0 = _f16(r.standard_normal((columns, 3)))
+    h_ref, h_got = _u16_dev(hist0, gpu), _u16_dev(hist0, gpu)
+    extra = _projection_weights(r, second, groups, gpu) if second else None
+    for step in range(2):
+        a = _u16_dev(_f16(r.standard_normal((1, width)) * 3), gpu)
+        b = _u16_dev(_f16(r.standard_normal((1, width)) * 3), gpu)
+        # separate launches
+        s3 = torch.empty(1, width, dtype=torch.float16, device=gpu)
+        q3 = torch.empty(1, groups * 32, dtype=torch.int8, device=gpu)
+        c3 = torch.empty(1, groups, dtype=torch.float32, device=gpu)
+        ops.add_rms_norm_quantize(a, b, s3, w, q3, c3)
+        x = torch.empty(1, columns, dtype=torch.float16, device=gpu)
+        ops.linear_w8a8(q3, c3, wt, ws, x)
+        want = torch.empty_like(x)
+        ops.causal_conv(x, cw, h_ref, want, silu=True)
+        if second:
+            want2 = torch.empty(1, second, dtype=torch.float16, device=gpu)
+            ops.linear_w8a8(q3, c3, extra[0], extra[1], want2)
+        # one launch
+        s1 = torch.empty_like(s3)
+        got = torch.full_like(x, -7.0)
+        plist = [{"weight": wt, "weight_scales": ws, "out": got, "conv_weight": cw,
+                  "conv_history": h_got}]
+        if second:
+            got2 = torch.full_like(want2, -7.0)
+            plist.append({"weight": extra[0], "weight_scales": extra[1], "out": got2})
+        ops.add_rms_norm_linear_w8a8(a, b, s1, w, plist)
+        torch.cuda.synchronize()
+        g, e = _host_u16(got).reshape(-1), _host_u16(want).reshape(-1)
+        assert np.array_equal(g, e), f"step {step}"
+        assert np.array_equal(_host_u16(h_got), _host_u16(h_ref)), f"history, step {step}"
+        assert np.array_equal(_host_u16(s1), _host_u16(s3))
+        if second:
+            assert np.array_equal(_host_u16(got2), _host_u16(want2))
+
+
 def test_add_rms_norm_linear_without_q(gpu):
     """q and scales may be omitted; the projections are the same."""
     print("addRmsNormLinearW8A8 without q", flush=True)
