@@ -286,6 +286,7 @@ private:
   bool merge_delta_norm(Dispatch &u, const Dispatch &n) const;
   void prepare_kv_decode();
   void prepare_conv_silu();
+  void keep_norm_operands(int64_t projection, size_t until);
   void prepare_gated_attention();
 };
 
@@ -656,25 +657,31 @@ void Lowering::prepare_conv_silu() {
     convSilu_[j] = (int64_t)j + 1;
     skip_[j + 1] = 1;
     // In a one-row step the convolution may run as the epilogue of the
-    // projection whose row it reads, inside the norm + projections launch
-    // (merge_norm_linears): it writes its output while other workgroups
-    // still read the norm's operands and the first one writes the
-    // quantized row, so those stay live until the convolution.
-    const int64_t p = value(c.inputs[0]).defining_op;
-    if (g_.tokens != 1 || p < 0 || op(p).kind != LLMI_GRAPH_LINEAR_W8A8)
-      continue;
-    const int64_t qo = value(op(p).inputs[0]).defining_op;
-    if (qo < 1 || normQuantize_[qo - 1] != qo)
-      continue;
-    std::vector<uint32_t> live(op(qo - 1).inputs, op(qo - 1).inputs + op(qo - 1).input_count);
-    live.insert(live.end(), op(qo).outputs, op(qo).outputs + op(qo).output_count);
-    if (normAdd_[qo - 1] >= 0) {
-      const auto &a = op(normAdd_[qo - 1]);
-      live.insert(live.end(), a.inputs, a.inputs + a.input_count);
-    }
-    for (uint32_t x : live)
-      lastUse_[root_[x]] = std::max(lastUse_[root_[x]], j);
+    // projection whose row it reads, inside the norm + projections launch.
+    keep_norm_operands(value(c.inputs[0]).defining_op, j);
   }
+}
+
+// A launch that the norm + projections call of a one-row step may take
+// over (merge_norm_linears: a convolution epilogue) writes at op `until`
+// while other workgroups still read the norm's operands and the first one
+// writes the norm's quantized row: when projection p reads such a norm's
+// quantization, those stay live until `until`, so the arena places nothing
+// of that op over them.
+void Lowering::keep_norm_operands(int64_t p, size_t until) {
+  if (g_.tokens != 1 || p < 0 || op(p).kind != LLMI_GRAPH_LINEAR_W8A8)
+    return;
+  const int64_t qo = value(op(p).inputs[0]).defining_op;
+  if (qo < 1 || normQuantize_[qo - 1] != qo)
+    return;
+  std::vector<uint32_t> live(op(qo - 1).inputs, op(qo - 1).inputs + op(qo - 1).input_count);
+  live.insert(live.end(), op(qo).outputs, op(qo).outputs + op(qo).output_count);
+  if (normAdd_[qo - 1] >= 0) {
+    const auto &a = op(normAdd_[qo - 1]);
+    live.insert(live.end(), a.inputs, a.inputs + a.input_count);
+  }
+  for (uint32_t x : live)
+    lastUse_[root_[x]] = std::max(lastUse_[root_[x]], until);
 }
 
 // The attention block of a one-row step (Qwen35ModelBuilder.cpp:175-197) in

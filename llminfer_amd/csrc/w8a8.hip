@@ -661,15 +661,18 @@ struct NormLinearArgs {
   NormLinearSeg seg[kNormLinearMax];
   unsigned count, width, groups;
   float eps;
+  unsigned cols; // columns a workgroup (a multiple of 4, at most 60)
 };
 
 // One column's weights for a lane: its kLaneGroups groups (clamped: in
-// bounds) and their scales.
+// bounds) and their scales, kept as loaded (fp16 bits): converted where the
+// dots use them, so that nothing before then waits for the loads (the norm
+// wave issues its own before its chain).
 template <int kLaneGroups>
 __device__ __forceinline__ void load_lane_weights(const NormLinearSeg &seg, unsigned cc,
                                                   unsigned l, unsigned groups,
                                                   uint4_t (&wv)[kLaneGroups][2],
-                                                  float (&wsv)[kLaneGroups]) {
+                                                  uint16_t (&wsv)[kLaneGroups]) {
   const uint4_t *wrow = reinterpret_cast<const uint4_t *>(seg.w + (size_t)cc * groups * kGroup);
   const uint16_t *wsrow = seg.ws + (size_t)cc * groups;
 #pragma unroll
@@ -677,7 +680,7 @@ __device__ __forceinline__ void load_lane_weights(const NormLinearSeg &seg, unsi
     const unsigned g = min(l + kGemvLanes * u, groups - 1);
     wv[u][0] = __builtin_nontemporal_load(wrow + 2 * g);
     wv[u][1] = __builtin_nontemporal_load(wrow + 2 * g + 1);
-    wsv[u] = h2f(wsrow[g]);
+    wsv[u] = wsrow[g];
   }
 }
 
@@ -685,14 +688,20 @@ __device__ __forceinline__ void load_lane_weights(const NormLinearSeg &seg, unsi
 template <int kLaneGroups>
 __device__ __forceinline__ float lane_dots(const uint4_t *arow, const float *ss, unsigned l,
                                            unsigned groups, const uint4_t (&wv)[kLaneGroups][2],
-                                           const float (&wsv)[kLaneGroups]) {
+                                           const uint16_t (&wsv)[kLaneGroups]) {
   float acc = 0.0f;
 #pragma unroll
   for (int u = 0; u < kLaneGroups; ++u) {
     const unsigned g = l + kGemvLanes * u;
+    // pinned here (volatile asm keeps its place after the workgroup's
+    // barriers): the backend otherwise converts the loaded scale right
+    // after its load, which makes the norm wave wait for its weights
+    // before its chain
+    uint32_t bits = wsv[u];
+    asm volatile("" : "+v"(bits));
     if (g < groups)
       acc = add_term(acc, group_dot(arow[2 * g], arow[2 * g + 1], wv[u][0], wv[u][1]), ss[g],
-                     wsv[u]);
+                     h2f((uint16_t)bits));
   }
 #pragma unroll
   for (int m = kGemvLanes / 2; m >= 1; m /= 2)
@@ -734,8 +743,13 @@ __global__ __launch_bounds__(kNormLinearThreads) void norm_linear_kernel(
   }
   const bool paired = kPaired && seg.paired;
   const bool norm_wave = t < 64;
-  const unsigned col = blk * kNormLinearCols + (t - 64) / kGemvLanes, l = t % kGemvLanes;
-  const bool live = !norm_wave && col < seg.columns;
+  // waves 1-15 serve four columns each, as many as the launch gives a
+  // workgroup; the others only help stage and quantize the row
+  const unsigned lane_col = (t - 64) / kGemvLanes; // (wraps for the norm wave)
+  const unsigned col = blk * p.cols + lane_col;
+  const unsigned l = t % kGemvLanes;
+  const bool serves = !norm_wave && lane_col < p.cols; // a wave with columns
+  const bool live = serves && col < seg.columns;
   const unsigned cc = live ? col : 0; // clamped: in bounds
 
   // The row, then (waves 1-15) the weights or (wave 0) the chain. The
@@ -746,16 +760,15 @@ __global__ __launch_bounds__(kNormLinearThreads) void norm_linear_kernel(
                                            p.width, padded, t);
   lds_sync();
   uint4_t wv[kLaneGroups][2], mv[kPaired ? kLaneGroups : 1][2];
-  float wsv[kLaneGroups], msv[kPaired ? kLaneGroups : 1];
-  if (norm_wave) {
-    if (t == 0)
-      sscale = rms_scale_of(norm_row_sum(srow, padded), p.width, p.eps);
-  } else {
+  uint16_t wsv[kLaneGroups], msv[kPaired ? kLaneGroups : 1];
+  if (serves) {
     load_lane_weights<kLaneGroups>(seg, cc, l, p.groups, wv, wsv);
     if constexpr (kPaired)
       if (paired)
         load_lane_weights<kLaneGroups>(mate, cc, l, p.groups, mv, msv);
   }
+  if (norm_wave && t == 0)
+    sscale = rms_scale_of(norm_row_sum(srow, padded), p.width, p.eps);
   lds_sync();
   quantize_norm_row<kNormLinearThreads>(srow, sw, sscale, p.width, p.groups, t, sq, ss,
                                         first ? invalid : nullptr);
@@ -767,7 +780,7 @@ __global__ __launch_bounds__(kNormLinearThreads) void norm_linear_kernel(
     for (unsigned i = t; i < p.groups; i += kNormLinearThreads)
       scales[i] = ss[i];
 
-  if (norm_wave)
+  if (!serves)
     return;
   const uint4_t *arow = reinterpret_cast<const uint4_t *>(sq);
   const float acc = lane_dots<kLaneGroups>(arow, ss, l, p.groups, wv, wsv);
@@ -872,6 +885,22 @@ hipError_t launch_add_norm_quantize(const uint16_t *a, const uint16_t *b, uint16
   return hipGetLastError();
 }
 
+// Compute units of the current device (256 on MI355X), read once a device.
+static unsigned device_cus() {
+  static int cus[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64)
+    return 256;
+  if (cus[dev] <= 0) {
+    int c = 0;
+    cus[dev] = hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) ==
+                           hipSuccess && c > 0
+                   ? c
+                   : 256;
+  }
+  return (unsigned)cus[dev];
+}
+
 template <bool kAdd, int kLaneGroups, bool kPaired>
 static void launch_norm_linear_as(const uint16_t *a, const uint16_t *b, uint16_t *sum_out,
                                   const float *w, int8_t *q, float *scales, unsigned *invalid,
@@ -893,12 +922,29 @@ hipError_t launch_add_norm_linear(const uint16_t *a, const uint16_t *b, uint16_t
   p.eps = eps;
   unsigned wgs = 0;
   bool paired = false;
+  // The fewest columns a workgroup (a multiple of 4) that still fit the
+  // launch in one workgroup a CU: each workgroup's weight stream is then
+  // the shortest, with every CU streaming (at 60 columns the MLP's 9216
+  // fill 154 CUs, whose streams outlast the norm's chain).
+  unsigned perWg = kNormLinearCols;
+  const unsigned cus = device_cus();
+  for (unsigned c = 4; c < kNormLinearCols; c += 4) {
+    unsigned n = 0;
+    for (unsigned k = 0; k < count; ++k)
+      if (!(k > 0 && proj[k - 1].paired))
+        n += (proj[k].shape.columns + c - 1) / c;
+    if (n <= cus) {
+      perWg = c;
+      break;
+    }
+  }
+  p.cols = perWg;
   for (unsigned k = 0; k < count; ++k) {
     const NormLinearProj &x = proj[k];
     const bool mate = k > 0 && proj[k - 1].paired;
     p.seg[k] = {x.w, x.ws, x.out, x.aux, x.bias, x.shape.columns, x.shape.outputWidth,
                 x.shape.firstRow, x.shape.epilogue, x.shape.block,
-                mate ? 0u : norm_linear_workgroups(x.shape.columns), x.paired ? 1u : 0u,
+                mate ? 0u : (x.shape.columns + perWg - 1) / perWg, x.paired ? 1u : 0u,
                 x.cw, x.ch};
     wgs += p.seg[k].wgs;
     paired = paired || x.paired;
