@@ -317,44 +317,74 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(
 
 // Long rows (more than 128 groups: 8 per lane or more): four waves share the
 // same 4 columns. Wave w computes the group terms (float(dot) * a) * w of the
-// w-th quarter of every lane's groups, all its loads issued at once, into
-// LDS; wave 0 then adds each lane's terms in group order -- the same fp32
-// sums as one lane would form -- and finishes as above.
+// w-th quarter of every lane's groups (kPer steps of 16 groups), all its
+// loads issued at once, into LDS; wave 0 then adds each lane's terms in
+// group order -- the same fp32 sums as one lane would form -- and finishes
+// as above. The workgroup's threads first request the activation row and
+// its scales, then the weights, and stage the row in LDS once its loads
+// (the oldest) are back: read from memory in the dot loop, each step's
+// activations waited for the whole weight stream before them and for one
+// another. kPer is a template parameter so that every load count is fixed
+// and the waits count only what they need.
 constexpr int kSplitWaves = 4, kSplitMaxSteps = 64; // groups per lane <= 64
 constexpr int kSplitPer = kSplitMaxSteps / kSplitWaves;
 
+template <int kPer>
 __global__ __launch_bounds__(64 * kSplitWaves) void gemv_split_kernel(
     const int8_t *__restrict__ act, const float *__restrict__ as, const int8_t *__restrict__ w,
     const uint16_t *__restrict__ ws, void *out, const void *aux, const float *bias, W8Args p) {
-  __shared__ float sT[kSplitMaxSteps][64];
-  const unsigned wave = threadIdx.x / 64, t = threadIdx.x % 64;
+  constexpr unsigned kThreads = 64 * kSplitWaves, kGroups = kSplitWaves * kPer * kGemvLanes;
+  constexpr int kA = (2 * kGroups + kThreads - 1) / kThreads, kS = (kGroups + kThreads - 1) / kThreads;
+  __shared__ float sT[kSplitWaves * kPer][64];
+  __shared__ uint4_t sAct[2 * kGroups];
+  __shared__ float sAs[kGroups];
+  const unsigned tid = threadIdx.x, wave = tid / 64, t = tid % 64;
   const unsigned col = blockIdx.x * kGemvCols + t / kGemvLanes;
   const unsigned l = t % kGemvLanes;
-  const unsigned steps = (p.groups + kGemvLanes - 1) / kGemvLanes; // a lane's steps, at most
-  const unsigned per = (steps + kSplitWaves - 1) / kSplitWaves, i0 = wave * per;
-  if (col < p.columns) {
-    const uint4_t *wrow = reinterpret_cast<const uint4_t *>(w + (size_t)col * p.groups * kGroup);
-    const uint4_t *arow = reinterpret_cast<const uint4_t *>(act);
-    const uint16_t *wsrow = ws + (size_t)col * p.groups;
-    uint4_t wv[kSplitPer][2];
-    float wsv[kSplitPer];
+  const unsigned i0 = wave * kPer;
+  const unsigned nA = 2 * p.groups; // 16-byte pieces of the row
+  const uint4_t *arow = reinterpret_cast<const uint4_t *>(act);
+  uint4_t aReg[kA];
+  float sReg[kS];
 #pragma unroll
-    for (int u = 0; u < kSplitPer; ++u) {
-      const unsigned g = min(l + kGemvLanes * (i0 + u), p.groups - 1); // clamped: in bounds
-      if ((unsigned)u < per) {
-        wv[u][0] = __builtin_nontemporal_load(wrow + 2 * g);
-        wv[u][1] = __builtin_nontemporal_load(wrow + 2 * g + 1);
-        wsv[u] = h2f(wsrow[g]);
-      }
-    }
+  for (int k = 0; k < kA; ++k)
+    aReg[k] = arow[min(tid + k * kThreads, nA - 1)]; // clamped: in bounds
 #pragma unroll
-    for (int u = 0; u < kSplitPer; ++u) {
-      const unsigned g = l + kGemvLanes * (i0 + u);
-      if ((unsigned)u < per && g < p.groups)
-        sT[i0 + u][t] = __fmul_rn(
-            __fmul_rn((float)group_dot(arow[2 * g], arow[2 * g + 1], wv[u][0], wv[u][1]), as[g]),
-            wsv[u]);
-    }
+  for (int k = 0; k < kS; ++k)
+    sReg[k] = as[min(tid + k * kThreads, p.groups - 1)];
+  asm volatile("" ::: "memory"); // (keeps these loads ahead of the weights')
+  // The weights (a column past the end reads the last one and stores
+  // nothing); the scales stay fp16 bits, one a register, until the
+  // products, so that nothing waits for them here.
+  const bool live = col < p.columns;
+  const unsigned cc = live ? col : p.columns - 1;
+  const uint4_t *wrow = reinterpret_cast<const uint4_t *>(w + (size_t)cc * p.groups * kGroup);
+  const uint16_t *wsrow = ws + (size_t)cc * p.groups;
+  uint4_t wv[kPer][2];
+  uint32_t wsv[kPer];
+#pragma unroll
+  for (int u = 0; u < kPer; ++u) {
+    const unsigned g = min(l + kGemvLanes * (i0 + u), p.groups - 1); // clamped: in bounds
+    wv[u][0] = __builtin_nontemporal_load(wrow + 2 * g);
+    wv[u][1] = __builtin_nontemporal_load(wrow + 2 * g + 1);
+    wsv[u] = wsrow[g];
+  }
+#pragma unroll
+  for (int k = 0; k < kA; ++k)
+    if (tid + k * kThreads < nA)
+      sAct[tid + k * kThreads] = aReg[k];
+#pragma unroll
+  for (int k = 0; k < kS; ++k)
+    if (tid + k * kThreads < p.groups)
+      sAs[tid + k * kThreads] = sReg[k];
+  lds_sync(); // LDS only: the weights stay in flight
+#pragma unroll
+  for (int u = 0; u < kPer; ++u) {
+    const unsigned g = l + kGemvLanes * (i0 + u);
+    if (live && g < p.groups)
+      sT[i0 + u][t] = __fmul_rn(
+          __fmul_rn((float)group_dot(sAct[2 * g], sAct[2 * g + 1], wv[u][0], wv[u][1]), sAs[g]),
+          h2f((uint16_t)wsv[u]));
   }
   __syncthreads();
   if (wave != 0)
@@ -980,14 +1010,34 @@ const char *linear_w8a8_kernel(unsigned rows) {
   return rows == 1 ? "linearW8A8Gemv" : "linearW8A8Gemm";
 }
 
+// The split GEMV for kPer steps a wave (3 .. kSplitPer).
+template <int kPer>
+static void launch_gemv_split_as(dim3 grid, hipStream_t stream, const int8_t *act, const float *as,
+                                 const int8_t *w, const uint16_t *ws, void *out, const void *aux,
+                                 const float *bias, const W8Args &a) {
+  hipLaunchKernelGGL(gemv_split_kernel<kPer>, grid, dim3(64 * kSplitWaves), 0, stream, act, as, w,
+                     ws, out, aux, bias, a);
+}
+
+template <int kPer = kSplitPer>
+static void launch_gemv_split(unsigned per, dim3 grid, hipStream_t stream, const int8_t *act,
+                              const float *as, const int8_t *w, const uint16_t *ws, void *out,
+                              const void *aux, const float *bias, const W8Args &a) {
+  if constexpr (kPer > 3)
+    if (per < (unsigned)kPer)
+      return launch_gemv_split<kPer - 1>(per, grid, stream, act, as, w, ws, out, aux, bias, a);
+  launch_gemv_split_as<kPer>(grid, stream, act, as, w, ws, out, aux, bias, a);
+}
+
 hipError_t launch_linear_w8a8(const int8_t *act, const float *as, const int8_t *w,
                               const uint16_t *ws, void *out, const void *aux, const float *bias,
                               const W8Shape &s, hipStream_t stream) {
   const W8Args a{s.outputWidth, s.firstRow, s.groups, s.rows, s.columns, s.epilogue, s.block};
   const unsigned steps = (s.groups + kGemvLanes - 1) / kGemvLanes;
   if (s.rows == 1 && steps > kGemvUnroll && steps <= kSplitMaxSteps)
-    hipLaunchKernelGGL(gemv_split_kernel, dim3((s.columns + kGemvCols - 1) / kGemvCols),
-                       dim3(64 * kSplitWaves), 0, stream, act, as, w, ws, out, aux, bias, a);
+    launch_gemv_split((steps + kSplitWaves - 1) / kSplitWaves,
+                      dim3((s.columns + kGemvCols - 1) / kGemvCols), stream, act, as, w, ws, out,
+                      aux, bias, a);
   else if (s.rows == 1)
     hipLaunchKernelGGL(gemv_kernel, dim3((s.columns + kGemvCols - 1) / kGemvCols),
                        dim3(kGemvThreads), 0, stream, act, as, w, ws, out, aux, bias, a);
