@@ -23,6 +23,7 @@
 //    rows the group dots come from int8 MFMA over 32 x 32 tiles, with the 8
 //    lanes' fp32 sums kept apart and merged in the butterfly's order.
 #include "exact_fp.hpp"
+#include "gated_norm.hpp"
 #include "hip_common.hpp"
 #include "kernels.hpp"
 #include "linear_store.hpp"
@@ -88,6 +89,27 @@ __device__ __forceinline__ float quantize_group(const float *x, int8_t *dst, boo
   return scale;
 }
 
+
+// Rows of whole 32-wide groups from 16-byte-aligned input: a lane per chunk
+// of eight values, four lanes a group (quantize_chunk8, the expressions
+// above): a group's 32 divides spread over its four lanes instead of one
+// lane's sequence.
+__global__ __launch_bounds__(256) void quantize_chunks_kernel(const uint16_t *__restrict__ in,
+                                                              int8_t *__restrict__ q,
+                                                              float *__restrict__ scales,
+                                                              unsigned *invalid, unsigned chunks) {
+  const unsigned c = blockIdx.x * 256 + threadIdx.x;
+  if (c >= chunks) // (chunks is a multiple of 4: a group's lanes leave together)
+    return;
+  const uint4_t v = reinterpret_cast<const uint4_t *>(in)[c];
+  float y[8];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    y[2 * e] = h2f((uint16_t)(v[e] & 0xFFFFu));
+    y[2 * e + 1] = h2f((uint16_t)(v[e] >> 16));
+  }
+  quantize_chunk8(y, q + 8 * (size_t)c, scales + c / 4, invalid, (c & 3u) == 0);
+}
 
 __global__ __launch_bounds__(256) void quantize_kernel(const uint16_t *__restrict__ in,
                                                        int8_t *__restrict__ q,
@@ -896,8 +918,14 @@ hipError_t launch_quantize_activation(const uint16_t *in, int8_t *q, float *scal
                                       unsigned groups, hipStream_t stream) {
   const unsigned n = rows * groups;
   const bool vec = width % kGroup == 0 && aligned16(in);
-  hipLaunchKernelGGL(quantize_kernel, dim3((n + 255) / 256), dim3(256), 0, stream, in, q,
-                     scales, invalid, rows, width, groups, vec);
+  if (vec) {
+    const unsigned chunks = n * (kGroup / 8);
+    hipLaunchKernelGGL(quantize_chunks_kernel, dim3((chunks + 255) / 256), dim3(256), 0, stream,
+                       in, q, scales, invalid, chunks);
+  } else {
+    hipLaunchKernelGGL(quantize_kernel, dim3((n + 255) / 256), dim3(256), 0, stream, in, q,
+                       scales, invalid, rows, width, groups, vec);
+  }
   return hipGetLastError();
 }
 
