@@ -337,7 +337,7 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(
   }
 }
 
-// Long rows (more than 128 groups: 8 per lane or more): four waves share the
+// Long rows (more than 112 groups: 8 steps a lane or more): four waves share the
 // same 4 columns. Wave w computes the group terms (float(dot) * a) * w of the
 // w-th quarter of every lane's groups (kPer steps of 16 groups), all its
 // loads issued at once, into LDS; wave 0 then adds each lane's terms in
@@ -1038,7 +1038,7 @@ const char *linear_w8a8_kernel(unsigned rows) {
   return rows == 1 ? "linearW8A8Gemv" : "linearW8A8Gemm";
 }
 
-// The split GEMV for kPer steps a wave (3 .. kSplitPer).
+// The split GEMV for kPer steps a wave (2 .. kSplitPer).
 template <int kPer>
 static void launch_gemv_split_as(dim3 grid, hipStream_t stream, const int8_t *act, const float *as,
                                  const int8_t *w, const uint16_t *ws, void *out, const void *aux,
@@ -1051,7 +1051,7 @@ template <int kPer = kSplitPer>
 static void launch_gemv_split(unsigned per, dim3 grid, hipStream_t stream, const int8_t *act,
                               const float *as, const int8_t *w, const uint16_t *ws, void *out,
                               const void *aux, const float *bias, const W8Args &a) {
-  if constexpr (kPer > 3)
+  if constexpr (kPer > 2)
     if (per < (unsigned)kPer)
       return launch_gemv_split<kPer - 1>(per, grid, stream, act, as, w, ws, out, aux, bias, a);
   launch_gemv_split_as<kPer>(grid, stream, act, as, w, ws, out, aux, bias, a);
@@ -1062,7 +1062,7 @@ hipError_t launch_linear_w8a8(const int8_t *act, const float *as, const int8_t *
                               const W8Shape &s, hipStream_t stream) {
   const W8Args a{s.outputWidth, s.firstRow, s.groups, s.rows, s.columns, s.epilogue, s.block};
   const unsigned steps = (s.groups + kGemvLanes - 1) / kGemvLanes;
-  if (s.rows == 1 && steps > kGemvUnroll && steps <= kSplitMaxSteps)
+  if (s.rows == 1 && steps >= kGemvUnroll && steps <= kSplitMaxSteps)
     launch_gemv_split((steps + kSplitWaves - 1) / kSplitWaves,
                       dim3((s.columns + kGemvCols - 1) / kGemvCols), stream, act, as, w, ws, out,
                       aux, bias, a);

@@ -96,6 +96,7 @@ def _same(got, want):
 @pytest.mark.parametrize("rows,columns,groups", [
     (1, 9216, 80),    # Qwen3.5-4B MLP gate/up, decode
     (1, 2560, 288),   # MLP down, decode
+    (1, 2560, 128), (1, 40, 113),  # out projections: 8 steps a lane, the split kernel's 2 a wave
     (1, 37, 5), (1, 16, 1), (1, 33, 17),
     (1, 50, 150), (1, 20, 1024), (1, 12, 1030),   # four waves per column; the limit; past it
     (2, 40, 9), (3, 70, 12), (4, 32, 80), (5, 19, 3), (15, 40, 9),
