@@ -198,6 +198,24 @@ def test_gated_block_output_never_covers_its_rows(past):
     assert "kvAppend" not in kinds and "gqaDecodeSplitK" not in kinds
 
 
+@pytest.mark.parametrize("past", [0, 5, 31, 32, 100, 4096])
+def test_delta_tail_and_conv_launches_never_cover_what_they_read(past):
+    """The DeltaNet tail in one launch (llmi_hip_l2_norm_delta_gated_norm_
+    activated_quantize) writes the normalised and quantized rows while other
+    workgroups still read q, k, v and the gates, and the qkv projection's
+    convolution epilogue writes its output while other workgroups still read
+    the norm's operands. The lowering keeps those operands live until the
+    last op of each merged launch and merges only when no output overlaps
+    what the launch reads; so both merges in all 24 DeltaNet layers at every
+    past show that no such output covers them."""
+    c = G.qwen35_4b()
+    _, decode = _lower(c, 1, past, 8192, "last", True)
+    kinds = Counter(d["kernel"] for d in decode.dispatches)
+    assert kinds["deltaRecurrentNormQuantize"] == 24 * 5
+    assert kinds["causalConv"] == 0 and kinds["deltaRecurrent"] == 0
+    assert kinds["rmsNormLinearW8A8"] + kinds["addRmsNormLinearW8A8"] == 8 + 415
+
+
 def test_malformed_graphs_are_rejected_before_any_launch():
     c = G.tiny_qwen35()
     g = G.build_qwen35(c, 2, 0, 8, "all", True)
