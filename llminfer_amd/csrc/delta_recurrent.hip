@@ -88,6 +88,18 @@ __global__ __launch_bounds__(64 * NW * CG) void delta_recurrent_kernel(
   const size_t vwidth = (size_t)Hv * DV;
 
   __shared__ float sPred[CG][NU][CW], sY[CG][NU][CW];
+  // With NORM the state is requested first: the largest read, in flight
+  // while the operands below are staged (requested after them, it was
+  // waited behind their staging, ~1.6 us into the kernel).
+  float S[RPL];
+  float *sbase = state + ((size_t)h * DK + row0) * DV + col;
+  auto load_state = [&] {
+#pragma unroll
+    for (int m = 0; m < RPL; ++m)
+      S[m] = sbase[(size_t)m * DV];
+  };
+  if constexpr (NORM)
+    load_state();
   // NORM: the outputs x of the tokens (fp16, as the unfused kernel stores
   // them), the row factors, and the head's gate rows and the weight, staged
   // at the start (no register holds them across the token loop).
@@ -132,11 +144,8 @@ __global__ __launch_bounds__(64 * NW * CG) void delta_recurrent_kernel(
     fetch_fac_row(0);
   }
 
-  float S[RPL];
-  float *sbase = state + ((size_t)h * DK + row0) * DV + col;
-#pragma unroll
-  for (int m = 0; m < RPL; ++m)
-    S[m] = sbase[(size_t)m * DV];
+  if constexpr (!NORM)
+    load_state();
 
   // A token's operands as loaded (fp16 q/k rows with QK16, else fp32). They
   // are fetched one token ahead, before the barriers of the token in hand,
